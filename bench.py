@@ -1,0 +1,274 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized decode hot path on one MI355X.
+
+Workload (batch 1): one decode pass through the Q8_0 projections of a layer --
+quantize x[2048] -> q/gate 2048->4096 and kv 2048->512 GEMVs -> quantize a[4096] -> o 4096->2048 GEMV -- with
+weights seeded on the device and rotated over enough distinct copies (>= 570 MB) that no launch reads weights from
+the 256 MB MALL. A step is one such pass; steps are recorded once into a HIP graph and replayed.
+
+value  = algorithmic bytes of a pass (weights + activations + outputs) / measured time per pass, in GB/s.
+roofline = config C0 (one 4096x4096 Q8_0 GEMV, 17,858,560 algorithmic bytes), the dominant kernel, timed with HIP
+           events over back-to-back launches on the device stream, against 8 TB/s.
+cpu_baseline = the reference's CPU MatVec (cpu::MatVec, built from its sources into oracle/_ref) on the same three
+           projections, all hardware threads, on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "halo-flash_amd"))
+
+HBM_PEAK_GBS = 8000.0
+C0_BYTES = 4096 * 128 * 34 + 4096 * 4 + 4096 * 4  # 17,858,560
+C1_SHAPES = [(4096, 2048), (512, 2048), (2048, 4096)]  # fused q/gate, kv, o
+MIN_ROTATION_BYTES = 600 << 20
+
+
+def q8_bytes(rows, cols):
+    return rows * (cols // 32) * 34
+
+
+def c1_pass_bytes(m: int) -> int:
+    """Algorithmic bytes of one C1 pass: every weight byte once, fp32 inputs and outputs per token."""
+    w = sum(q8_bytes(r, c) for r, c in C1_SHAPES)
+    act = m * (2048 * 4 + 4096 * 4)  # x (read by the quantizer) and a
+    out = m * (4096 + 512 + 2048) * 4
+    return w + act + out
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def run_gpu(args):
+    import halo_amd as H
+
+    dev = H.Device()
+    try:
+        res = {}
+        # ---------------- C1 pass at M=1 (the bench value) and the M sweep ----------------
+        per_copy = sum(q8_bytes(r, c) for r, c in C1_SHAPES)
+        copies = max(2, -(-MIN_ROTATION_BYTES // per_copy))
+        log(f"[bench] C1: {copies} weight copies ({copies * per_copy / 2**20:.0f} MiB)")
+        sets = []
+        for i in range(copies):
+            sets.append([H.Q8Weights(dev, r, c).synth(dev, seed=1000 * i + j) for j, (r, c) in enumerate(C1_SHAPES)])
+        mmax = 16
+        x = dev.array((mmax, 2048), np.float32)
+        a = dev.array((mmax, 4096), np.float32)
+        dev.op("synth_f32", x.ptr, mmax * 2048, 7, 1.0)
+        dev.op("synth_f32", a.ptr, mmax * 4096, 8, 1.0)
+        xq, xs = dev.array((mmax, 2048), np.int8), dev.array((mmax, 64), np.float32)
+        aq, as_ = dev.array((mmax, 4096), np.int8), dev.array((mmax, 128), np.float32)
+        yqg, ykv, yo = (dev.array((mmax, 4096), np.float32), dev.array((mmax, 512), np.float32),
+                        dev.array((mmax, 2048), np.float32))
+        dev.sync()
+
+        def c1_pass(ws, m):
+            dev.op("quantize_q8", x.ptr, xq.ptr, xs.ptr, m, 2048)
+            dev.op("matvec_q8a8", ctypes.byref(ws[0].desc), xq.ptr, xs.ptr, yqg.ptr, m, 4096)
+            dev.op("matvec_q8a8", ctypes.byref(ws[1].desc), xq.ptr, xs.ptr, ykv.ptr, m, 512)
+            dev.op("quantize_q8", a.ptr, aq.ptr, as_.ptr, m, 4096)
+            dev.op("matvec_q8a8", ctypes.byref(ws[2].desc), aq.ptr, as_.ptr, yo.ptr, m, 2048)
+
+        # correctness spot check of copy 0 against the oracle before timing anything
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle_py as O
+
+        c1_pass(sets[0], 1)
+        qs, d = sets[0][2].host()
+        a_host = a.download()[0]
+        aq_h, as_h = O.quantize(a_host)
+        want, mag = O.gemv_q8a8(qs, d, aq_h, as_h)
+        got = yo.download()[0]
+        assert np.all(np.abs(got - want) <= 1e-5 * mag + 1e-6), "bench spot check failed"
+
+        def graph_for(m):
+            dev.begin_capture()
+            for ws in sets:
+                c1_pass(ws, m)
+            return dev.end_capture()
+
+        sweep = {}
+        for m in (1, 2, 4, 8, 16):
+            g = graph_for(m)
+            reps = 1 if m > 1 else max(1, args.warmup // copies)
+            for _ in range(reps):
+                dev.launch_graph(g)
+            dev.sync()
+            if m == 1:
+                nrep = max(1, -(-args.steps // copies))
+                dev.timer_start()
+                for _ in range(nrep):
+                    dev.launch_graph(g)
+                ms = dev.timer_stop()
+                steps = nrep * copies
+                res["steps_timed"] = steps
+                res["ms_per_step"] = ms / steps
+                res["value"] = c1_pass_bytes(1) / (ms / steps * 1e-3) / 1e9
+            else:
+                nrep = max(1, -(-200 // copies))
+                dev.timer_start()
+                for _ in range(nrep):
+                    dev.launch_graph(g)
+                ms = dev.timer_stop()
+                steps = nrep * copies
+            sweep[str(m)] = {"us_per_pass": round(ms / steps * 1e3, 3),
+                             "GBps": round(c1_pass_bytes(m) / (ms / steps * 1e-3) / 1e9, 1)}
+            dev.free_graph(g)
+        res["c1_sweep"] = sweep
+        log(f"[bench] C1 sweep {sweep}")
+        del sets
+
+        # ---------------- C0: the dominant kernel, back-to-back over rotated copies ----------------
+        c0_copies = max(2, -(-MIN_ROTATION_BYTES // q8_bytes(4096, 4096)))
+        ws0 = [H.Q8Weights(dev, 4096, 4096).synth(dev, seed=50000 + i) for i in range(c0_copies)]
+        x0 = dev.array(4096, np.float32)
+        dev.op("synth_f32", x0.ptr, 4096, 9, 1.0)
+        x0q, x0s, y0 = dev.array(4096, np.int8), dev.array(128, np.float32), dev.array(4096, np.float32)
+        dev.op("quantize_q8", x0.ptr, x0q.ptr, x0s.ptr, 1, 4096)
+        dev.sync()
+        tilings = [(64, 1, 4), (64, 2, 4), (64, 1, 2), (64, 1, 1), (32, 1, 4), (64, 4, 4)] if args.sweep else [None]
+        c0 = {}
+        for t in tilings:
+            dev.begin_capture()
+            for w in ws0:
+                if t is None:
+                    dev.op("matvec_q8a8", ctypes.byref(w.desc), x0q.ptr, x0s.ptr, y0.ptr, 1, 4096)
+                else:
+                    dev.op("matvec_q8a8_tiled", ctypes.byref(w.desc), x0q.ptr, x0s.ptr, y0.ptr, 1, 4096, *t)
+            g = dev.end_capture()
+            dev.launch_graph(g)
+            dev.sync()
+            nrep = max(1, -(-max(args.steps, 2000) // c0_copies))
+            dev.timer_start()
+            for _ in range(nrep):
+                dev.launch_graph(g)
+            ms = dev.timer_stop()
+            us = ms * 1e3 / (nrep * c0_copies)
+            c0[str(t)] = {"us_per_gemv": round(us, 3), "GBps": round(C0_BYTES / (us * 1e-6) / 1e9, 1)}
+            dev.free_graph(g)
+        log(f"[bench] C0 {c0}")
+        best = c0[str(tilings[0])]
+        res["roofline"] = {
+            "bound": "hbm",
+            "kernel": "halo_gemv_q8a8_l64_r1_b1 (C0 4096x4096 Q8_0 GEMV)",
+            "achieved": best["GBps"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(best["GBps"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "us_per_launch": best["us_per_gemv"],
+            "algorithmic_bytes_per_launch": C0_BYTES,
+        }
+        if args.sweep:
+            res["c0_tilings"] = c0
+        return res
+    finally:
+        dev.close()
+
+
+def cpu_baseline(budget_s: float):
+    """The reference's cpu::MatVec (fp32 activations, dequantize-row, double accumulate, row split over
+    std::thread::hardware_concurrency() threads) over the three C1 projections."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle_py as O
+
+    rng = np.random.default_rng(0)
+    mats = []
+    for r, c in C1_SHAPES:
+        qs, d = O.synth_q8(rng, r, c)
+        raw = np.zeros(r * (c // 32) * 34, np.uint8)
+        O.oracle().or_pack_q8_0(qs, d, raw, r, c, c)
+        mats.append((raw, qs, d, r, c))
+    x = {2048: rng.normal(0, 1, 2048).astype(np.float32), 4096: rng.normal(0, 1, 4096).astype(np.float32)}
+    if O.has_ref():
+        R = O.ref()
+        kind, threads = "reference", int(R.ref_hw_threads())
+
+        def one():
+            for raw, qs, d, r, c in mats:
+                y = np.empty(r, np.float32)
+                R.ref_matvec_q8_0(raw, r, c, x[c], y)
+    else:
+        o = O.oracle()
+        kind, threads = "port", os.cpu_count() or 1
+
+        def one():
+            for raw, qs, d, r, c in mats:
+                y = np.empty(r, np.float32)
+                o.or_matvec_q8_0_f32x(qs, d, r, c, c, x[c], y, threads)
+    one()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 10:
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 2000:
+            break
+    med = float(np.median(times))
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except AttributeError:
+        aff = os.cpu_count()
+    return {
+        "value": round(c1_pass_bytes(1) / med / 1e9, 2),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": kind,
+        "sample": (f"C1 M=1 pass (3 Q8_0 projections, fp32 x), median of {len(times)} passes "
+                   f"({med * 1e3:.2f} ms/pass), {threads} threads on {aff} available cpus"),
+    }
+
+
+def main():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=4000)
+    p.add_argument("--warmup", type=int, default=400)
+    p.add_argument("--sweep", action="store_true", help="also time alternative C0 GEMV tilings")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--no-cpu", action="store_true")
+    args = p.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the path is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    res = run_gpu(args)
+    line = {
+        "metric": "Q8_0 GEMV achieved HBM GB/s; decode tokens/s at 1 and 4 sessions",
+        "value": round(res["value"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": res["steps_timed"],
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (device-seeded Q8_0 weights, N(0,1) activations)",
+        "config": {"workload": "C1 Q8_0 projections 2048->4096, 2048->512, 4096->2048 at M=1 (batch 1)",
+                   "bytes_per_step": c1_pass_bytes(1), "rotated_weight_copies_MiB": 600},
+        "roofline": res["roofline"],
+        "c1_sweep": res["c1_sweep"],
+    }
+    if "c0_tilings" in res:
+        line["c0_tilings"] = res["c0_tilings"]
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

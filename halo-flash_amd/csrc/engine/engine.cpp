@@ -1,0 +1,140 @@
+// halo_engine: code-object load, kernel lookup and the Q8_0 projection dispatch.
+//
+// Reference: FlashNextGpu::Init (src/engine/flash_next_gpu.cpp:256-327) loads the code object and repacks Q8_0
+// weights; FlashNextGpu::MatVec (212-254) picks the GEMV variant and grid per matrix.
+#include "engine.hpp"
+
+using namespace halo::engine;
+
+extern "C" {
+
+int halo_engine_create(halo_device* dev, halo_engine** out, char* err, size_t errlen) {
+  if (dev == nullptr || out == nullptr) return SetErr(err, errlen, "null argument"), -1;
+  *out = nullptr;
+  std::size_t bytes = 0;
+  const std::uint8_t* code = halo_core_code_object(&bytes);
+  if (halo_load_module(dev, code, bytes, err, errlen) != 0) return -1;
+  auto* eng = new halo_engine();
+  eng->dev = dev;
+  *out = eng;
+  return 0;
+}
+
+void halo_engine_destroy(halo_engine* eng) { delete eng; }
+
+halo_device* halo_engine_device(halo_engine* eng) { return eng ? eng->dev : nullptr; }
+
+int halo_engine_launch(halo_engine* eng, const char* kernel, halo_dim3 grid, halo_dim3 block, const halo_arg* args,
+                       size_t nargs, char* err, size_t errlen) {
+  if (eng == nullptr) return SetErr(err, errlen, "null engine"), -1;
+  auto it = eng->ids.find(kernel);
+  halo_kernel_id id;
+  if (it == eng->ids.end()) {
+    id = halo_kernel(eng->dev, kernel, err, errlen);
+    if (id < 0) return -1;
+    eng->ids.emplace(kernel, id);
+  } else {
+    id = it->second;
+  }
+  return halo_launch(eng->dev, id, grid, block, args, nargs, err, errlen);
+}
+
+int halo_op_repack_q8_0(halo_engine* eng, const void* raw, int8_t* qs, uint16_t* d, uint32_t rows, uint32_t cols,
+                        uint32_t qstride, char* err, size_t errlen) {
+  if (cols % 32 != 0 || qstride < cols || qstride % 16 != 0)
+    return SetErr(err, errlen, "repack: cols %u must be a multiple of 32, qstride %u >= cols and a multiple of 16",
+                  cols, qstride),
+           -1;
+  const std::uint64_t blocks = static_cast<std::uint64_t>(rows) * (cols / 32);
+  const std::uint32_t grid = static_cast<std::uint32_t>(std::min<std::uint64_t>(CeilDiv(blocks, 256), 8192));
+  const halo_arg a[] = {Ptr(raw), Ptr(qs), Ptr(d), U32(rows), U32(cols), U32(qstride)};
+  return Launch(eng, "halo_repack_q8_0", D3(grid ? grid : 1), D3(256), a, err, errlen);
+}
+
+int halo_op_quantize_q8(halo_engine* eng, const float* x, int8_t* xq, float* xs, uint32_t tokens, uint32_t cols,
+                        char* err, size_t errlen) {
+  if (cols % 32 != 0 || tokens == 0) return SetErr(err, errlen, "quantize: cols %% 32 != 0 or no tokens"), -1;
+  const halo_arg a[] = {Ptr(x), Ptr(xq), Ptr(xs), U32(cols)};
+  return Launch(eng, "halo_quantize_q8_rows", D3(tokens), D3(256), a, err, errlen);
+}
+
+static int CheckMatrix(const halo_q8_matrix* w, char* err, size_t errlen) {
+  if (w == nullptr || w->qs == nullptr || w->d == nullptr) return SetErr(err, errlen, "null matrix"), -1;
+  if (w->rows == 0 || w->cols == 0 || w->cols % 32 != 0 || w->qstride < w->cols || w->qstride % 16 != 0)
+    return SetErr(err, errlen, "bad Q8_0 matrix %ux%u qstride %u", w->rows, w->cols, w->qstride), -1;
+  return 0;
+}
+
+int halo_op_matvec_q8a8_tiled(halo_engine* eng, const halo_q8_matrix* w, const int8_t* xq, const float* xs,
+                              float* y, uint32_t m, uint32_t ystride, uint32_t lpr, uint32_t rpl, uint32_t waves,
+                              char* err, size_t errlen) {
+  if (CheckMatrix(w, err, errlen) != 0) return -1;
+  if (!(m == 1 || m == 2 || m == 4 || m == 8)) return SetErr(err, errlen, "tiled GEMV takes m in {1,2,4,8}"), -1;
+  if (!(lpr == 16 || lpr == 32 || lpr == 64) || !(rpl == 1 || rpl == 2 || rpl == 4) || waves < 1 || waves > 4)
+    return SetErr(err, errlen, "bad tiling lpr=%u r=%u waves=%u", lpr, rpl, waves), -1;
+  if (m > 1 && ystride < w->rows) return SetErr(err, errlen, "ystride %u < rows %u", ystride, w->rows), -1;
+  char name[64];
+  std::snprintf(name, sizeof name, "halo_gemv_q8a8_l%u_r%u_b%u", lpr, rpl, m);
+  const std::uint32_t rows_per_block = waves * rpl * (64 / lpr);
+  const halo_arg a[] = {Ptr(w->qs), Ptr(w->d), Ptr(xq), Ptr(xs), Ptr(y),
+                        U32(w->rows), U32(w->cols), U32(w->qstride), U32(m > 1 ? ystride : w->rows)};
+  return Launch(eng, name, D3(CeilDiv(w->rows, rows_per_block)), D3(64 * waves), a, err, errlen);
+}
+
+int halo_op_matvec_q8a8(halo_engine* eng, const halo_q8_matrix* w, const int8_t* xq, const float* xs, float* y,
+                        uint32_t m, uint32_t ystride, char* err, size_t errlen) {
+  if (CheckMatrix(w, err, errlen) != 0) return -1;
+  if (m == 0) return SetErr(err, errlen, "m == 0"), -1;
+  if (m > 1 && ystride < w->rows) return SetErr(err, errlen, "ystride %u < rows %u", ystride, w->rows), -1;
+  // Tiling: a row is covered by as many lanes as its 16-byte pieces allow (up to a wave); more activation columns
+  // reuse each weight load over more rows per lane group.
+  const std::uint32_t lpr = w->cols >= 1024 ? 64 : (w->cols >= 512 ? 32 : 16);
+  std::uint32_t done = 0;
+  while (done < m) {
+    const std::uint32_t left = m - done;
+    const std::uint32_t nb = left >= 8 ? 8 : (left >= 4 ? 4 : (left >= 2 ? 2 : 1));
+    const std::uint32_t rpl = nb >= 4 ? 2 : 1;
+    const std::size_t nblk = w->cols / 32;
+    if (halo_op_matvec_q8a8_tiled(eng, w, xq + static_cast<std::size_t>(done) * w->cols, xs + done * nblk,
+                                  y + static_cast<std::size_t>(done) * (m > 1 ? ystride : 0), nb,
+                                  m > 1 ? ystride : w->rows, lpr, rpl, 4, err, errlen) != 0)
+      return -1;
+    done += nb;
+  }
+  return 0;
+}
+
+int halo_op_matvec_q8_f32x(halo_engine* eng, const halo_q8_matrix* w, const float* x, float* y, char* err,
+                           size_t errlen) {
+  if (CheckMatrix(w, err, errlen) != 0) return -1;
+  const bool r4 = w->rows >= 2048;
+  const halo_arg a[] = {Ptr(w->qs), Ptr(w->d), Ptr(x), Ptr(y), U32(w->rows), U32(w->cols), U32(w->qstride)};
+  return Launch(eng, r4 ? "halo_gemv_q8r_r4" : "halo_gemv_q8r_r2", D3(CeilDiv(w->rows, r4 ? 32 : 16)), D3(256), a,
+                err, errlen);
+}
+
+int halo_op_q8_half_dots(halo_engine* eng, const halo_q8_matrix* w, const int8_t* xq, int32_t* isum, char* err,
+                         size_t errlen) {
+  if (CheckMatrix(w, err, errlen) != 0) return -1;
+  const std::uint64_t n = static_cast<std::uint64_t>(w->rows) * (w->cols / 16);
+  const halo_arg a[] = {Ptr(w->qs), Ptr(xq), Ptr(isum), U32(w->rows), U32(w->cols), U32(w->qstride)};
+  return Launch(eng, "halo_q8_half_dots", D3(static_cast<std::uint32_t>(std::min<std::uint64_t>(CeilDiv(n, 256), 8192))),
+                D3(256), a, err, errlen);
+}
+
+int halo_op_synth_q8(halo_engine* eng, int8_t* qs, uint16_t* d, uint32_t rows, uint32_t cols, uint32_t qstride,
+                     uint64_t seed, float sigma, char* err, size_t errlen) {
+  if (cols % 32 != 0 || qstride < cols || qstride % 16 != 0) return SetErr(err, errlen, "synth: bad shape"), -1;
+  const std::uint64_t n = static_cast<std::uint64_t>(rows) * (cols / 16);
+  const halo_arg a[] = {Ptr(qs), Ptr(d), U32(rows), U32(cols), U32(qstride), Val(seed), Val(sigma)};
+  return Launch(eng, "halo_synth_q8", D3(static_cast<std::uint32_t>(std::min<std::uint64_t>(CeilDiv(n, 256), 65536))),
+                D3(256), a, err, errlen);
+}
+
+int halo_op_synth_f32(halo_engine* eng, float* x, uint64_t n, uint64_t seed, float sigma, char* err, size_t errlen) {
+  const halo_arg a[] = {Ptr(x), Val(n), Val(seed), Val(sigma)};
+  return Launch(eng, "halo_synth_f32", D3(static_cast<std::uint32_t>(std::min<std::uint64_t>(CeilDiv(n, 256), 65536))),
+                D3(256), a, err, errlen);
+}
+
+}  // extern "C"

@@ -1,0 +1,60 @@
+// Internal C++ side of halo_engine: kernel-id cache, argument packing and shared launch helpers.
+#pragma once
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <type_traits>
+#include <unordered_map>
+
+#include "halo_ops.h"
+#include "halo_rt.h"
+
+struct halo_engine {
+  halo_device* dev = nullptr;
+  std::unordered_map<std::string, halo_kernel_id> ids;
+};
+
+namespace halo::engine {
+
+inline void SetErr(char* err, std::size_t errlen, const char* fmt, ...) {
+  if (err == nullptr || errlen == 0) return;
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(err, errlen, fmt, ap);
+  va_end(ap);
+}
+
+// Kernel argument builders (the reference's Arg::Buf / Arg::Val, src/rt/device.hpp:35-59).
+inline halo_arg Ptr(const void* p) {
+  halo_arg a{};
+  a.kind = HALO_ARG_BUFFER;
+  a.buffer.device = const_cast<void*>(p);
+  a.buffer.bytes = 0;
+  return a;
+}
+template <typename T>
+inline halo_arg Val(T v) {
+  static_assert(sizeof(T) <= 8 && std::is_trivially_copyable_v<T>);
+  halo_arg a{};
+  a.kind = HALO_ARG_SCALAR;
+  a.size = sizeof(T);
+  std::memcpy(a.bytes, &v, sizeof(T));
+  return a;
+}
+inline halo_arg U32(std::uint32_t v) { return Val(v); }
+
+inline halo_dim3 D3(std::uint32_t x, std::uint32_t y = 1, std::uint32_t z = 1) { return halo_dim3{x, y, z}; }
+
+inline std::uint32_t CeilDiv(std::uint64_t a, std::uint64_t b) { return static_cast<std::uint32_t>((a + b - 1) / b); }
+
+// Launch by name through the device layer.
+template <std::size_t N>
+inline int Launch(halo_engine* eng, const char* name, halo_dim3 grid, halo_dim3 block, const halo_arg (&args)[N],
+                  char* err, std::size_t errlen) {
+  return halo_engine_launch(eng, name, grid, block, args, N, err, errlen);
+}
+
+}  // namespace halo::engine

@@ -1,0 +1,2 @@
+// The gfx950 code object: every kernel the device layer can look up by name.
+#include "q8.hip"

@@ -1,0 +1,377 @@
+// Q8_0 repack, activation quantizer and the decode GEMV family (gfx950, wave64).
+//
+// Weight layout in HBM (reference src/kernels/core.hip:2116-2124): a Q8_0 matrix [rows][cols] is repacked once at
+// load into int8 rows `qs` (row stride `qstride` bytes, a multiple of 16) and fp16 scales `d` [rows][cols / 32].
+// Activations are quantized per 32 values to int8 `xq` with an fp32 scale `xs` (amax / 127, round half to even).
+//
+// The GEMV streams weights with one 16-byte load per lane per row: a row is covered by LPR lanes (LPR * 16 bytes
+// per instruction), a wave covers 64 / LPR rows per pass and R passes, so a wave owns R * 64 / LPR rows and keeps
+// R * U 16-byte loads per lane in flight (U column steps issued before any arithmetic). The integer part of every
+// 16-value half block is an exact v_dot4_i32_i8 chain; the epilogue per half block is acc += s_w * (s_x * isum).
+#include "common.h"
+
+using halo::Dot16;
+using halo::F16;
+using halo::kWave;
+
+// ---- repack ------------------------------------------------------------------------------------------------
+// reference src/kernels/core.hip:2126-2138. Grid-stride over 34-byte blocks; a thread copies one block.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_repack_q8_0(const std::uint8_t* raw, std::int8_t* qs, std::uint16_t* d, std::uint32_t rows,
+                     std::uint32_t cols, std::uint32_t qstride) {
+  const std::uint32_t blocks = cols / 32;
+  const std::uint64_t total = static_cast<std::uint64_t>(rows) * blocks;
+  for (std::uint64_t b = blockIdx.x * static_cast<std::uint64_t>(blockDim.x) + threadIdx.x; b < total;
+       b += static_cast<std::uint64_t>(gridDim.x) * blockDim.x) {
+    const std::uint64_t r = b / blocks, k = b % blocks;
+    const std::uint8_t* src = raw + (r * blocks + k) * 34;
+    d[r * blocks + k] = static_cast<std::uint16_t>(src[0] | (src[1] << 8));
+    // 34-byte blocks are only 2-byte aligned: read halves, write 16-byte vectors.
+    std::uint16_t h[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) h[i] = reinterpret_cast<const std::uint16_t*>(src + 2)[i];
+    int4 lo, hi;
+    lo.x = h[0] | (h[1] << 16);
+    lo.y = h[2] | (h[3] << 16);
+    lo.z = h[4] | (h[5] << 16);
+    lo.w = h[6] | (h[7] << 16);
+    hi.x = h[8] | (h[9] << 16);
+    hi.y = h[10] | (h[11] << 16);
+    hi.z = h[12] | (h[13] << 16);
+    hi.w = h[14] | (h[15] << 16);
+    int4* dst = reinterpret_cast<int4*>(qs + r * qstride + k * 32);
+    dst[0] = lo;
+    dst[1] = hi;
+  }
+}
+
+// ---- activation quantizer -----------------------------------------------------------------------------------
+namespace {
+// One 32-value block per half wave. Division is IEEE (the code object is built with correctly rounded fp32
+// divide); rintf is round-half-to-even.
+__device__ __forceinline__ void QuantizeBlock32(const float* x, std::int8_t* xq, float* xs, std::uint32_t blk) {
+  const std::uint32_t lane = threadIdx.x % 32;
+  const float v = x[blk * 32 + lane];
+  const float amax = halo::GroupMax<32>(fabsf(v));
+  const float scale = amax / 127.0f;
+  const int q = scale > 0.0f ? static_cast<int>(rintf(v / scale)) : 0;
+  xq[blk * 32 + lane] = static_cast<std::int8_t>(q);
+  if (lane == 0) xs[blk] = scale;
+}
+}  // namespace
+
+// reference src/kernels/core.hip:3089-3101. grid (T), any multiple of 64 threads; x [T][cols] -> xq [T][cols],
+// xd [T][cols / 32].
+extern "C" __global__ void __launch_bounds__(256)
+    halo_quantize_q8_rows(const float* x, std::int8_t* xq, float* xd, std::uint32_t cols) {
+  const std::size_t t = blockIdx.x;
+  for (std::uint32_t blk = threadIdx.x / 32; blk < cols / 32; blk += blockDim.x / 32)
+    QuantizeBlock32(x + t * cols, xq + t * cols, xd + t * (cols / 32), blk);
+}
+
+// reference src/kernels/batch_decode.hip:201-222. Grid (ceil(cols / 256), B), 256 threads: x column b at
+// x + b * xstride -> xq + b * cols, xs + b * cols / 32; with xq2 the residual x - q * s is quantized again.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_q8x_cols(const float* x, std::uint32_t xstride, std::uint32_t cols, std::int8_t* xq, float* xs,
+                  std::int8_t* xq2, float* xs2) {
+  const std::uint32_t b = blockIdx.y, lane = threadIdx.x % 32, nblk = cols / 32;
+  const std::uint32_t blk = blockIdx.x * (blockDim.x / 32) + threadIdx.x / 32;
+  if (blk >= nblk) return;  // whole half waves exit together
+  const float v = x[static_cast<std::size_t>(b) * xstride + blk * 32 + lane];
+  const float amax = halo::GroupMax<32>(fabsf(v));
+  const float scale = amax / 127.0f;
+  const int qv = scale > 0.0f ? static_cast<int>(rintf(v / scale)) : 0;
+  xq[static_cast<std::size_t>(b) * cols + blk * 32 + lane] = static_cast<std::int8_t>(qv);
+  if (lane == 0) xs[static_cast<std::size_t>(b) * nblk + blk] = scale;
+  if (!xq2) return;
+  const float r = v - static_cast<float>(qv) * scale;
+  const float rmax = halo::GroupMax<32>(fabsf(r));
+  const float s2 = rmax / 127.0f;
+  const int q2 = s2 > 0.0f ? static_cast<int>(rintf(r / s2)) : 0;
+  xq2[static_cast<std::size_t>(b) * cols + blk * 32 + lane] = static_cast<std::int8_t>(q2);
+  if (lane == 0) xs2[static_cast<std::size_t>(b) * nblk + blk] = s2;
+}
+
+// ---- int8-activation GEMV ------------------------------------------------------------------------------------
+namespace {
+
+constexpr int kInFlight = 4;  // column steps whose loads are issued before their arithmetic
+
+// Rows r(k) = base + k * P + lane / LPR (P = 64 / LPR), columns [k0, k1) of NB activation columns. Returns the
+// per-row sums reduced over the LPR lanes (valid in every lane).
+template <int LPR, int R, int NB, bool kResid>
+__device__ __forceinline__ void Q8A8Rows(const std::int8_t* __restrict__ qs, const std::uint16_t* __restrict__ d,
+                                         const std::int8_t* __restrict__ xq, const float* __restrict__ xs,
+                                         const std::int8_t* __restrict__ xq2, const float* __restrict__ xs2,
+                                         std::uint32_t base, std::uint32_t rows, std::uint32_t cols,
+                                         std::uint32_t qstride, std::uint32_t k0, std::uint32_t k1,
+                                         float (&out)[NB][R]) {
+  constexpr int P = kWave / LPR;
+  constexpr std::uint32_t kStep = LPR * 16;
+  const std::uint32_t lane = threadIdx.x % kWave, nblk = cols / 32;
+  const std::uint32_t sub = lane / LPR;
+  const std::int8_t* rowp[R];
+  const std::uint16_t* dp[R];
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const std::uint32_t r = min(base + k * P + sub, rows - 1);
+    rowp[k] = qs + static_cast<std::size_t>(r) * qstride;
+    dp[k] = d + static_cast<std::size_t>(r) * nblk;
+  }
+  float acc[NB][R];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int k = 0; k < R; ++k) acc[b][k] = 0.0f;
+
+  for (std::uint32_t c0 = k0 + (lane % LPR) * 16; c0 < k1; c0 += kInFlight * kStep) {
+    int4 q[kInFlight][R];
+    float s[kInFlight][R];
+    int4 xv[kInFlight][NB];
+    float sx[kInFlight][NB];
+    int4 rv[kInFlight][kResid ? NB : 1];
+    float sr[kInFlight][kResid ? NB : 1];
+#pragma unroll
+    for (int u = 0; u < kInFlight; ++u) {
+      const std::uint32_t c = c0 + u * kStep;
+      const bool ok = c < k1;
+      const std::uint32_t cc = ok ? c : k0 + (lane % LPR) * 16;
+#pragma unroll
+      for (int k = 0; k < R; ++k) {
+        q[u][k] = *reinterpret_cast<const int4*>(rowp[k] + cc);
+        s[u][k] = ok ? F16(dp[k][cc / 32]) : 0.0f;
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        xv[u][b] = *reinterpret_cast<const int4*>(xq + static_cast<std::size_t>(b) * cols + cc);
+        sx[u][b] = xs[static_cast<std::size_t>(b) * nblk + cc / 32];
+        if constexpr (kResid) {
+          rv[u][b] = *reinterpret_cast<const int4*>(xq2 + static_cast<std::size_t>(b) * cols + cc);
+          sr[u][b] = xs2[static_cast<std::size_t>(b) * nblk + cc / 32];
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kInFlight; ++u)
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+          float part = sx[u][b] * static_cast<float>(Dot16(q[u][k], xv[u][b]));
+          if constexpr (kResid) part += sr[u][b] * static_cast<float>(Dot16(q[u][k], rv[u][b]));
+          acc[b][k] += s[u][k] * part;
+        }
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int k = 0; k < R; ++k) out[b][k] = halo::GroupSum<LPR>(acc[b][k]);
+}
+
+template <int LPR, int R, int NB, bool kResid>
+__device__ __forceinline__ void StoreRows(float* y, std::uint32_t ystride, std::uint32_t base, std::uint32_t rows,
+                                         const float (&out)[NB][R]) {
+  constexpr int P = kWave / LPR;
+  const std::uint32_t lane = threadIdx.x % kWave;
+  if (lane % LPR != 0) return;
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const std::uint32_t r = base + k * P + lane / LPR;
+    if (r < rows)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) y[static_cast<std::size_t>(b) * ystride + r] = out[b][k];
+  }
+}
+
+// Reference-convention batched int8 GEMV (src/kernels/batch_decode.hip:273-298): a 256-thread block covers 8 * R
+// rows (4 waves x 2 rows per pass x R), blockIdx.x = row block * groups + column group, blockIdx.y = split-K part
+// over [part * chunk, (part + 1) * chunk) written to y plane part (offset part * rows).
+template <int R, int NB, bool kResid>
+__device__ __forceinline__ void GemvQ8rI8B(const std::int8_t* qs, const std::uint16_t* d, const std::int8_t* xq,
+                                           const float* xs, const std::int8_t* xq2, const float* xs2, float* y,
+                                           std::uint32_t rows, std::uint32_t cols, std::uint32_t qstride,
+                                           std::uint32_t ystride, std::uint32_t groups, std::uint32_t chunk) {
+  const std::uint32_t k0 = blockIdx.y * chunk;
+  const std::uint32_t k1 = min(cols, k0 + chunk);
+  y += static_cast<std::size_t>(blockIdx.y) * rows;
+  const std::uint32_t bx = blockIdx.x / groups, g = blockIdx.x % groups;
+  xq += static_cast<std::size_t>(g) * NB * cols;
+  xs += static_cast<std::size_t>(g) * NB * (cols / 32);
+  if constexpr (kResid) {
+    xq2 += static_cast<std::size_t>(g) * NB * cols;
+    xs2 += static_cast<std::size_t>(g) * NB * (cols / 32);
+  }
+  y += static_cast<std::size_t>(g) * NB * ystride;
+  const std::uint32_t base = (bx * (blockDim.x / kWave) + threadIdx.x / kWave) * (2 * R);
+  if (base >= rows) return;
+  float out[NB][R];
+  Q8A8Rows<32, R, NB, kResid>(qs, d, xq, xs, xq2, xs2, base, rows, cols, qstride, k0, k1, out);
+  StoreRows<32, R, NB, kResid>(y, ystride, base, rows, out);
+}
+
+}  // namespace
+
+#define HALO_GEMV_I8_REF(NB, R, SUF, RES)                                                                        \
+  extern "C" __global__ void __launch_bounds__(256) halo_gemv_q8r_i8##SUF##_r##R##_b##NB(                       \
+      const std::int8_t* qs, const std::uint16_t* d, const std::int8_t* xq, const float* xs,                    \
+      const std::int8_t* xq2, const float* xs2, float* y, std::uint32_t rows, std::uint32_t cols,               \
+      std::uint32_t qstride, std::uint32_t ystride, std::uint32_t groups, std::uint32_t chunk) {                \
+    GemvQ8rI8B<R, NB, RES>(qs, d, xq, xs, xq2, xs2, y, rows, cols, qstride, ystride, groups, chunk);            \
+  }
+#define HALO_GEMV_I8_REF_NB(NB)                                                                                   \
+  HALO_GEMV_I8_REF(NB, 1, , false) HALO_GEMV_I8_REF(NB, 2, , false) HALO_GEMV_I8_REF(NB, 4, , false)             \
+  HALO_GEMV_I8_REF(NB, 1, x, true) HALO_GEMV_I8_REF(NB, 2, x, true) HALO_GEMV_I8_REF(NB, 4, x, true)
+HALO_GEMV_I8_REF_NB(1)
+HALO_GEMV_I8_REF_NB(2)
+HALO_GEMV_I8_REF_NB(3)
+HALO_GEMV_I8_REF_NB(4)
+HALO_GEMV_I8_REF_NB(5)
+HALO_GEMV_I8_REF_NB(6)
+HALO_GEMV_I8_REF_NB(7)
+HALO_GEMV_I8_REF_NB(8)
+#undef HALO_GEMV_I8_REF_NB
+#undef HALO_GEMV_I8_REF
+
+// MI355X-native int8-activation GEMV (new name, no reference counterpart): blockDim.x / 64 waves per block, each
+// wave owns R * 64 / LPR consecutive-pass rows; grid.x = ceil(rows / (waves * R * 64 / LPR)). No split-K: the
+// dispatcher picks LPR and the block size so that the grid has >= 4 waves per CU.
+//   y[b * ystride + r] = sum over 32-blocks of d[r] * xs[b] * isum, b < NB.
+#define HALO_GEMV_Q8A8(LPR, R, NB)                                                                                \
+  extern "C" __global__ void __launch_bounds__(256) halo_gemv_q8a8_l##LPR##_r##R##_b##NB(                       \
+      const std::int8_t* qs, const std::uint16_t* d, const std::int8_t* xq, const float* xs, float* y,          \
+      std::uint32_t rows, std::uint32_t cols, std::uint32_t qstride, std::uint32_t ystride) {                   \
+    constexpr std::uint32_t kRowsPerWave = R * (kWave / LPR);                                                   \
+    const std::uint32_t base = (blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave) * kRowsPerWave;       \
+    if (base >= rows) return;                                                                                    \
+    float out[NB][R];                                                                                            \
+    Q8A8Rows<LPR, R, NB, false>(qs, d, xq, xs, nullptr, nullptr, base, rows, cols, qstride, 0, cols, out);     \
+    StoreRows<LPR, R, NB, false>(y, ystride, base, rows, out);                                                  \
+  }
+#define HALO_GEMV_Q8A8_R(LPR, NB) HALO_GEMV_Q8A8(LPR, 1, NB) HALO_GEMV_Q8A8(LPR, 2, NB) HALO_GEMV_Q8A8(LPR, 4, NB)
+#define HALO_GEMV_Q8A8_NB(LPR) \
+  HALO_GEMV_Q8A8_R(LPR, 1) HALO_GEMV_Q8A8_R(LPR, 2) HALO_GEMV_Q8A8_R(LPR, 4) HALO_GEMV_Q8A8_R(LPR, 8)
+HALO_GEMV_Q8A8_NB(64)
+HALO_GEMV_Q8A8_NB(32)
+HALO_GEMV_Q8A8_NB(16)
+#undef HALO_GEMV_Q8A8_NB
+#undef HALO_GEMV_Q8A8_R
+#undef HALO_GEMV_Q8A8
+
+// Exact integer half-block dots for parity checks: isum[r][c / 16] = sum of 16 int8 products, computed by the
+// same 16-byte loads and v_dot4 chain as the GEMV. Grid-stride over (row, 16-column piece).
+extern "C" __global__ void __launch_bounds__(256)
+    halo_q8_half_dots(const std::int8_t* qs, const std::int8_t* xq, std::int32_t* isum, std::uint32_t rows,
+                      std::uint32_t cols, std::uint32_t qstride) {
+  const std::uint32_t pieces = cols / 16;
+  const std::uint64_t total = static_cast<std::uint64_t>(rows) * pieces;
+  for (std::uint64_t i = blockIdx.x * static_cast<std::uint64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<std::uint64_t>(gridDim.x) * blockDim.x) {
+    const std::uint64_t r = i / pieces, p = i % pieces;
+    const int4 q = *reinterpret_cast<const int4*>(qs + r * qstride + p * 16);
+    const int4 x = *reinterpret_cast<const int4*>(xq + p * 16);
+    isum[i] = Dot16(q, x);
+  }
+}
+
+// ---- fp32-activation GEMV (reference names) -----------------------------------------------------------------
+// reference src/kernels/core.hip:2147-2188, 2388-2443: y[r] = sum_b F16(d) * sum_i q * x with fp32 x. Wave64: a
+// 256-thread block covers the reference's rows per block (8 * R); x is read through the vector cache.
+namespace {
+template <int R>
+__device__ __forceinline__ void GemvQ8rF32(const std::int8_t* __restrict__ qs, const std::uint16_t* __restrict__ d,
+                                           const float* __restrict__ x, float* __restrict__ y, std::uint32_t rows,
+                                           std::uint32_t cols, std::uint32_t qstride) {
+  constexpr int LPR = 32, P = 2;
+  const std::uint32_t base = (blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave) * (P * R);
+  if (base >= rows) return;
+  const std::uint32_t lane = threadIdx.x % kWave, nblk = cols / 32, sub = lane / LPR;
+  float acc[R];
+#pragma unroll
+  for (int k = 0; k < R; ++k) acc[k] = 0.0f;
+  for (std::uint32_t c = (lane % LPR) * 16; c < cols; c += LPR * 16) {
+    const float4* xp = reinterpret_cast<const float4*>(x + c);
+    float xr[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 v = xp[i];
+      xr[4 * i] = v.x;
+      xr[4 * i + 1] = v.y;
+      xr[4 * i + 2] = v.z;
+      xr[4 * i + 3] = v.w;
+    }
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      const std::uint32_t r = min(base + k * P + sub, rows - 1);
+      const int4 q = *reinterpret_cast<const int4*>(qs + static_cast<std::size_t>(r) * qstride + c);
+      const float s = F16(d[static_cast<std::size_t>(r) * nblk + c / 32]);
+      const std::int8_t* v = reinterpret_cast<const std::int8_t*>(&q);
+      float part = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) part += static_cast<float>(v[i]) * xr[i];
+      acc[k] += s * part;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const float a = halo::GroupSum<LPR>(acc[k]);
+    const std::uint32_t r = base + k * P + sub;
+    if (lane % LPR == 0 && r < rows) y[r] = a;
+  }
+}
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(256)
+    halo_gemv_q8r(const std::int8_t* qs, const std::uint16_t* d, const float* x, float* y, std::uint32_t rows,
+                  std::uint32_t cols, std::uint32_t qstride) {
+  GemvQ8rF32<1>(qs, d, x, y, rows, cols, qstride);
+}
+extern "C" __global__ void __launch_bounds__(256)
+    halo_gemv_q8r_r2(const std::int8_t* qs, const std::uint16_t* d, const float* x, float* y, std::uint32_t rows,
+                     std::uint32_t cols, std::uint32_t qstride) {
+  GemvQ8rF32<2>(qs, d, x, y, rows, cols, qstride);
+}
+extern "C" __global__ void __launch_bounds__(256)
+    halo_gemv_q8r_r4(const std::int8_t* qs, const std::uint16_t* d, const float* x, float* y, std::uint32_t rows,
+                     std::uint32_t cols, std::uint32_t qstride) {
+  GemvQ8rF32<4>(qs, d, x, y, rows, cols, qstride);
+}
+
+// ---- synthetic tensors ------------------------------------------------------------------------------------------
+// Seeded Q8_0 weights generated in place (no host copy of multi-GB models): q uniform in [-127, 127] from a
+// counter hash of (seed, row, column), d = fp16(|N(0, sigma)| / 127) from a hash of (seed, row, block).
+extern "C" __global__ void __launch_bounds__(256)
+    halo_synth_q8(std::int8_t* qs, std::uint16_t* d, std::uint32_t rows, std::uint32_t cols, std::uint32_t qstride,
+                  std::uint64_t seed, float sigma) {
+  const std::uint32_t pieces = cols / 16, nblk = cols / 32;
+  const std::uint64_t total = static_cast<std::uint64_t>(rows) * pieces;
+  for (std::uint64_t i = blockIdx.x * static_cast<std::uint64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<std::uint64_t>(gridDim.x) * blockDim.x) {
+    const std::uint64_t r = i / pieces, p = i % pieces;
+    const std::uint64_t key = halo::Mix64(seed ^ (r * 0x100000001B3ull)) + p;
+    int w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const std::uint64_t h = halo::Mix64(key * 4 + j);
+      std::uint32_t word = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int v = static_cast<int>(((h >> (16 * b)) & 0xFFFF) % 255u) - 127;
+        word |= (static_cast<std::uint32_t>(v) & 0xFFu) << (8 * b);
+      }
+      w[j] = static_cast<int>(word);
+    }
+    *reinterpret_cast<int4*>(qs + r * qstride + p * 16) = make_int4(w[0], w[1], w[2], w[3]);
+    if (p % 2 == 0) {
+      const float n = halo::Normal(halo::Mix64(seed + 0x5851F42D4C957F2Dull) ^ (r * nblk + p / 2));
+      d[r * nblk + p / 2] = halo::ToF16Bits(fabsf(n) * sigma / 127.0f);
+    }
+  }
+}
+
+// fp32 N(0, sigma) or bf16 tensors from a counter hash.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_synth_f32(float* x, std::uint64_t n, std::uint64_t seed, float sigma) {
+  for (std::uint64_t i = blockIdx.x * static_cast<std::uint64_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<std::uint64_t>(gridDim.x) * blockDim.x)
+    x[i] = sigma * halo::Normal(halo::Mix64(seed) ^ i);
+}

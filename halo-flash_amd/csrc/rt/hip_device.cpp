@@ -1,0 +1,272 @@
+// HIP implementation of the device C ABI (include/halo_rt.h) for MI355X (gfx950).
+//
+// Mirrors the reference's HipDevice (src/rt/hip_device.cpp): one non-blocking stream per device, code objects
+// loaded with hipModuleLoadData, kernels resolved by name with hipModuleGetFunction, kernargs packed in declaration
+// order (pointer = buffer address + offset, scalar = its bytes) and launched with hipModuleLaunchKernel, stream
+// capture into an instantiated hipGraphExec.
+#include "halo_rt.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+struct halo_device {
+  hipStream_t stream = nullptr;
+  hipModule_t module = nullptr;
+  std::vector<std::uint8_t> image;
+  std::vector<hipFunction_t> functions;
+  std::vector<std::string> names;
+  bool capturing = false;
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+};
+
+namespace {
+
+void SetErr(char* err, std::size_t errlen, const char* fmt, ...) {
+  if (err == nullptr || errlen == 0) return;
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(err, errlen, fmt, ap);
+  va_end(ap);
+}
+
+bool Ok(hipError_t e, const char* what, char* err, std::size_t errlen) {
+  if (e == hipSuccess) return true;
+  SetErr(err, errlen, "%s: %s", what, hipGetErrorString(e));
+  return false;
+}
+
+bool NotCapturing(halo_device* dev, const char* what, char* err, std::size_t errlen) {
+  if (!dev->capturing) return true;
+  SetErr(err, errlen, "%s is not capturable", what);
+  return false;
+}
+
+bool InRange(const halo_buffer* b, std::size_t offset, std::size_t bytes, char* err, std::size_t errlen) {
+  if (b == nullptr || b->device == nullptr) {
+    SetErr(err, errlen, "null buffer");
+    return false;
+  }
+  if (offset > b->bytes || bytes > b->bytes - offset) {
+    SetErr(err, errlen, "range [%zu, %zu) outside a buffer of %zu bytes", offset, offset + bytes, b->bytes);
+    return false;
+  }
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int halo_device_create(int backend, halo_device** out, char* err, size_t errlen) {
+  if (out == nullptr) return SetErr(err, errlen, "null out"), -1;
+  *out = nullptr;
+  if (backend != HALO_BACKEND_HIP) return SetErr(err, errlen, "unsupported backend %d", backend), -1;
+  int n = 0;
+  if (!Ok(hipGetDeviceCount(&n), "hipGetDeviceCount", err, errlen)) return -1;
+  if (n == 0) return SetErr(err, errlen, "no HIP device"), -1;
+  auto* dev = new halo_device();
+  if (!Ok(hipSetDevice(0), "hipSetDevice", err, errlen) ||
+      !Ok(hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking), "hipStreamCreate", err, errlen) ||
+      !Ok(hipEventCreate(&dev->t0), "hipEventCreate", err, errlen) ||
+      !Ok(hipEventCreate(&dev->t1), "hipEventCreate", err, errlen)) {
+    halo_device_destroy(dev);
+    return -1;
+  }
+  *out = dev;
+  return 0;
+}
+
+void halo_device_destroy(halo_device* dev) {
+  if (dev == nullptr) return;
+  if (dev->stream) (void)hipStreamSynchronize(dev->stream);
+  if (dev->module) (void)hipModuleUnload(dev->module);
+  if (dev->t0) (void)hipEventDestroy(dev->t0);
+  if (dev->t1) (void)hipEventDestroy(dev->t1);
+  if (dev->stream) (void)hipStreamDestroy(dev->stream);
+  delete dev;
+}
+
+int halo_alloc(halo_device* dev, size_t bytes, halo_buffer* out, char* err, size_t errlen) {
+  if (dev == nullptr || out == nullptr) return SetErr(err, errlen, "null argument"), -1;
+  *out = halo_buffer{};
+  if (!NotCapturing(dev, "Alloc", err, errlen)) return -1;
+  void* p = nullptr;
+  if (!Ok(hipMalloc(&p, bytes ? bytes : 1), "hipMalloc", err, errlen)) return -1;
+  out->device = p;
+  out->bytes = bytes;
+  return 0;
+}
+
+void halo_free(halo_device* dev, halo_buffer* buf) {
+  (void)dev;
+  if (buf == nullptr || buf->device == nullptr) return;
+  (void)hipFree(buf->device);
+  *buf = halo_buffer{};
+}
+
+int halo_upload(halo_device* dev, const halo_buffer* dst, size_t offset, const void* src, size_t bytes, char* err,
+                size_t errlen) {
+  if (!NotCapturing(dev, "Upload", err, errlen) || !InRange(dst, offset, bytes, err, errlen)) return -1;
+  if (bytes == 0) return 0;
+  if (!Ok(hipMemcpyAsync(static_cast<char*>(dst->device) + offset, src, bytes, hipMemcpyHostToDevice, dev->stream),
+          "hipMemcpyAsync(HtoD)", err, errlen))
+    return -1;
+  return Ok(hipStreamSynchronize(dev->stream), "hipStreamSynchronize", err, errlen) ? 0 : -1;
+}
+
+int halo_upload_async(halo_device* dev, const halo_buffer* dst, size_t offset, const void* src, size_t bytes,
+                      char* err, size_t errlen) {
+  if (!NotCapturing(dev, "UploadAsync", err, errlen) || !InRange(dst, offset, bytes, err, errlen)) return -1;
+  if (bytes == 0) return 0;
+  return Ok(hipMemcpyAsync(static_cast<char*>(dst->device) + offset, src, bytes, hipMemcpyHostToDevice,
+                           dev->stream),
+            "hipMemcpyAsync(HtoD)", err, errlen)
+             ? 0
+             : -1;
+}
+
+int halo_download(halo_device* dev, const halo_buffer* src, size_t offset, void* dst, size_t bytes, char* err,
+                  size_t errlen) {
+  if (!NotCapturing(dev, "Download", err, errlen) || !InRange(src, offset, bytes, err, errlen)) return -1;
+  if (bytes == 0) return Ok(hipStreamSynchronize(dev->stream), "hipStreamSynchronize", err, errlen) ? 0 : -1;
+  if (!Ok(hipMemcpyAsync(dst, static_cast<const char*>(src->device) + offset, bytes, hipMemcpyDeviceToHost,
+                         dev->stream),
+          "hipMemcpyAsync(DtoH)", err, errlen))
+    return -1;
+  return Ok(hipStreamSynchronize(dev->stream), "hipStreamSynchronize", err, errlen) ? 0 : -1;
+}
+
+int halo_fill(halo_device* dev, const halo_buffer* dst, uint8_t value, char* err, size_t errlen) {
+  // Memset nodes are kept out of captured graphs: fills run eagerly only.
+  if (!NotCapturing(dev, "Fill", err, errlen) || !InRange(dst, 0, dst ? dst->bytes : 0, err, errlen)) return -1;
+  return Ok(hipMemsetAsync(dst->device, value, dst->bytes, dev->stream), "hipMemsetAsync", err, errlen) ? 0 : -1;
+}
+
+void* halo_alloc_host(halo_device* dev, size_t bytes, char* err, size_t errlen) {
+  (void)dev;
+  void* p = nullptr;
+  if (!Ok(hipHostMalloc(&p, bytes ? bytes : 1, hipHostMallocDefault), "hipHostMalloc", err, errlen)) return nullptr;
+  return p;
+}
+
+void halo_free_host(halo_device* dev, void* p) {
+  (void)dev;
+  if (p) (void)hipHostFree(p);
+}
+
+size_t halo_available_bytes(halo_device* dev) {
+  (void)dev;
+  std::size_t free_b = 0, total = 0;
+  if (hipMemGetInfo(&free_b, &total) != hipSuccess) return SIZE_MAX;
+  return free_b;
+}
+
+int halo_load_module(halo_device* dev, const uint8_t* code, size_t bytes, char* err, size_t errlen) {
+  if (dev == nullptr || code == nullptr || bytes == 0) return SetErr(err, errlen, "empty code object"), -1;
+  if (dev->module) return SetErr(err, errlen, "a module is already loaded"), -1;
+  dev->image.assign(code, code + bytes);
+  return Ok(hipModuleLoadData(&dev->module, dev->image.data()), "hipModuleLoadData", err, errlen) ? 0 : -1;
+}
+
+halo_kernel_id halo_kernel(halo_device* dev, const char* name, char* err, size_t errlen) {
+  if (dev == nullptr || dev->module == nullptr) return SetErr(err, errlen, "no module loaded"), -1;
+  for (std::size_t i = 0; i < dev->names.size(); ++i)
+    if (dev->names[i] == name) return static_cast<halo_kernel_id>(i);
+  hipFunction_t f = nullptr;
+  if (!Ok(hipModuleGetFunction(&f, dev->module, name), name, err, errlen)) return -1;
+  dev->functions.push_back(f);
+  dev->names.emplace_back(name);
+  return static_cast<halo_kernel_id>(dev->functions.size() - 1);
+}
+
+int halo_launch(halo_device* dev, halo_kernel_id kernel, halo_dim3 grid, halo_dim3 block, const halo_arg* args,
+                size_t nargs, char* err, size_t errlen) {
+  if (dev == nullptr || kernel < 0 || static_cast<std::size_t>(kernel) >= dev->functions.size())
+    return SetErr(err, errlen, "bad kernel id %d", kernel), -1;
+  if (grid.x == 0 || grid.y == 0 || grid.z == 0 || block.x == 0 || block.y == 0 || block.z == 0 ||
+      block.x * block.y * block.z > 1024)
+    return SetErr(err, errlen, "bad launch shape (%u,%u,%u)x(%u,%u,%u) for %s", grid.x, grid.y, grid.z, block.x,
+                  block.y, block.z, dev->names[kernel].c_str()),
+           -1;
+  std::uint64_t storage[32];
+  void* params[32];
+  if (nargs > 32) return SetErr(err, errlen, "too many kernel arguments"), -1;
+  for (std::size_t i = 0; i < nargs; ++i) {
+    storage[i] = 0;
+    if (args[i].kind == HALO_ARG_BUFFER) {
+      void* p = args[i].buffer.device ? static_cast<char*>(args[i].buffer.device) + args[i].offset : nullptr;
+      std::memcpy(&storage[i], &p, sizeof(p));
+    } else {
+      if (args[i].size == 0 || args[i].size > 8) return SetErr(err, errlen, "bad scalar size"), -1;
+      std::memcpy(&storage[i], args[i].bytes, args[i].size);
+    }
+    params[i] = &storage[i];
+  }
+  if (!Ok(hipModuleLaunchKernel(dev->functions[kernel], grid.x, grid.y, grid.z, block.x, block.y, block.z, 0,
+                                dev->stream, params, nullptr),
+          "hipModuleLaunchKernel", err, errlen)) {
+    std::string m = err ? std::string(err) : std::string();
+    SetErr(err, errlen, "%s (launching %s)", m.c_str(), dev->names[kernel].c_str());
+    return -1;
+  }
+  return 0;
+}
+
+int halo_synchronize(halo_device* dev, char* err, size_t errlen) {
+  if (!NotCapturing(dev, "Synchronize", err, errlen)) return -1;
+  return Ok(hipStreamSynchronize(dev->stream), "hipStreamSynchronize", err, errlen) ? 0 : -1;
+}
+
+int halo_begin_capture(halo_device* dev, char* err, size_t errlen) {
+  if (dev->capturing) return SetErr(err, errlen, "already capturing"), -1;
+  if (!Ok(hipStreamBeginCapture(dev->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture", err, errlen))
+    return -1;
+  dev->capturing = true;
+  return 0;
+}
+
+int halo_end_capture(halo_device* dev, halo_graph* out, char* err, size_t errlen) {
+  if (!dev->capturing) return SetErr(err, errlen, "not capturing"), -1;
+  dev->capturing = false;
+  hipGraph_t g = nullptr;
+  if (!Ok(hipStreamEndCapture(dev->stream, &g), "hipStreamEndCapture", err, errlen)) return -1;
+  hipGraphExec_t exec = nullptr;
+  const bool ok = Ok(hipGraphInstantiate(&exec, g, nullptr, nullptr, 0), "hipGraphInstantiate", err, errlen);
+  (void)hipGraphDestroy(g);
+  if (!ok) return -1;
+  out->exec = exec;
+  return 0;
+}
+
+int halo_launch_graph(halo_device* dev, const halo_graph* graph, char* err, size_t errlen) {
+  if (graph == nullptr || graph->exec == nullptr) return SetErr(err, errlen, "null graph"), -1;
+  return Ok(hipGraphLaunch(static_cast<hipGraphExec_t>(graph->exec), dev->stream), "hipGraphLaunch", err, errlen)
+             ? 0
+             : -1;
+}
+
+void halo_free_graph(halo_device* dev, halo_graph* graph) {
+  (void)dev;
+  if (graph && graph->exec) (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph->exec));
+  if (graph) graph->exec = nullptr;
+}
+
+int halo_timer_start(halo_device* dev, char* err, size_t errlen) {
+  return Ok(hipEventRecord(dev->t0, dev->stream), "hipEventRecord", err, errlen) ? 0 : -1;
+}
+
+int halo_timer_stop(halo_device* dev, float* ms, char* err, size_t errlen) {
+  if (!Ok(hipEventRecord(dev->t1, dev->stream), "hipEventRecord", err, errlen) ||
+      !Ok(hipEventSynchronize(dev->t1), "hipEventSynchronize", err, errlen))
+    return -1;
+  return Ok(hipEventElapsedTime(ms, dev->t0, dev->t1), "hipEventElapsedTime", err, errlen) ? 0 : -1;
+}
+
+void* halo_device_stream(halo_device* dev) { return dev ? static_cast<void*>(dev->stream) : nullptr; }
+
+}  // extern "C"

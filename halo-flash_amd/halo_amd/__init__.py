@@ -1,0 +1,297 @@
+"""ctypes binding of libhalo_flash_amd.so (include/halo_rt.h, include/halo_ops.h).
+
+This is a thin harness for tests and the benchmark: every operation goes through the C ABI into the HIP library.
+There is no CPU fallback: if the library is missing, importing the binding raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import numpy as np
+
+PKG_DIR = Path(__file__).resolve().parent.parent  # halo-flash_amd/
+LIB_PATH = PKG_DIR / "libhalo_flash_amd.so"
+
+
+class HaloError(RuntimeError):
+    pass
+
+
+class Buffer(C.Structure):
+    _fields_ = [("device", C.c_void_p), ("bytes", C.c_size_t), ("handle", C.c_void_p)]
+
+
+class Arg(C.Structure):
+    _fields_ = [
+        ("kind", C.c_uint8),
+        ("size", C.c_uint8),
+        ("pad", C.c_uint8 * 6),
+        ("buffer", Buffer),
+        ("offset", C.c_size_t),
+        ("bytes", C.c_uint8 * 8),
+    ]
+
+
+class Dim3(C.Structure):
+    _fields_ = [("x", C.c_uint32), ("y", C.c_uint32), ("z", C.c_uint32)]
+
+
+class Graph(C.Structure):
+    _fields_ = [("exec", C.c_void_p)]
+
+
+class Q8Matrix(C.Structure):
+    _fields_ = [
+        ("qs", C.c_void_p),
+        ("d", C.c_void_p),
+        ("rows", C.c_uint32),
+        ("cols", C.c_uint32),
+        ("qstride", C.c_uint32),
+        ("pad", C.c_uint32),
+    ]
+
+
+ERRLEN = 1024
+_VP, _SZ, _U32, _U64, _F32, _I32 = C.c_void_p, C.c_size_t, C.c_uint32, C.c_uint64, C.c_float, C.c_int32
+_ERR = [C.c_char_p, _SZ]
+
+# name -> (restype, argtypes without the trailing err/errlen, has_err)
+_SIGS = {
+    "halo_device_create": (C.c_int, [C.c_int, C.POINTER(_VP)], True),
+    "halo_device_destroy": (None, [_VP], False),
+    "halo_alloc": (C.c_int, [_VP, _SZ, C.POINTER(Buffer)], True),
+    "halo_free": (None, [_VP, C.POINTER(Buffer)], False),
+    "halo_upload": (C.c_int, [_VP, C.POINTER(Buffer), _SZ, _VP, _SZ], True),
+    "halo_upload_async": (C.c_int, [_VP, C.POINTER(Buffer), _SZ, _VP, _SZ], True),
+    "halo_download": (C.c_int, [_VP, C.POINTER(Buffer), _SZ, _VP, _SZ], True),
+    "halo_fill": (C.c_int, [_VP, C.POINTER(Buffer), C.c_uint8], True),
+    "halo_alloc_host": (_VP, [_VP, _SZ], True),
+    "halo_free_host": (None, [_VP, _VP], False),
+    "halo_available_bytes": (_SZ, [_VP], False),
+    "halo_core_code_object": (C.POINTER(C.c_uint8), [C.POINTER(_SZ)], False),
+    "halo_load_module": (C.c_int, [_VP, _VP, _SZ], True),
+    "halo_kernel": (_I32, [_VP, C.c_char_p], True),
+    "halo_launch": (C.c_int, [_VP, _I32, Dim3, Dim3, C.POINTER(Arg), _SZ], True),
+    "halo_synchronize": (C.c_int, [_VP], True),
+    "halo_begin_capture": (C.c_int, [_VP], True),
+    "halo_end_capture": (C.c_int, [_VP, C.POINTER(Graph)], True),
+    "halo_launch_graph": (C.c_int, [_VP, C.POINTER(Graph)], True),
+    "halo_free_graph": (None, [_VP, C.POINTER(Graph)], False),
+    "halo_timer_start": (C.c_int, [_VP], True),
+    "halo_timer_stop": (C.c_int, [_VP, C.POINTER(_F32)], True),
+    "halo_device_stream": (_VP, [_VP], False),
+    "halo_engine_create": (C.c_int, [_VP, C.POINTER(_VP)], True),
+    "halo_engine_destroy": (None, [_VP], False),
+    "halo_engine_device": (_VP, [_VP], False),
+    "halo_engine_launch": (C.c_int, [_VP, C.c_char_p, Dim3, Dim3, C.POINTER(Arg), _SZ], True),
+    "halo_op_repack_q8_0": (C.c_int, [_VP, _VP, _VP, _VP, _U32, _U32, _U32], True),
+    "halo_op_quantize_q8": (C.c_int, [_VP, _VP, _VP, _VP, _U32, _U32], True),
+    "halo_op_matvec_q8a8": (C.c_int, [_VP, C.POINTER(Q8Matrix), _VP, _VP, _VP, _U32, _U32], True),
+    "halo_op_matvec_q8a8_tiled": (
+        C.c_int, [_VP, C.POINTER(Q8Matrix), _VP, _VP, _VP, _U32, _U32, _U32, _U32, _U32], True),
+    "halo_op_matvec_q8_f32x": (C.c_int, [_VP, C.POINTER(Q8Matrix), _VP, _VP], True),
+    "halo_op_q8_half_dots": (C.c_int, [_VP, C.POINTER(Q8Matrix), _VP, _VP], True),
+    "halo_op_synth_q8": (C.c_int, [_VP, _VP, _VP, _U32, _U32, _U32, _U64, _F32], True),
+    "halo_op_synth_f32": (C.c_int, [_VP, _VP, _U64, _U64, _F32], True),
+}
+
+_lib = None
+
+
+def declared_symbols() -> list[str]:
+    """Every function the public headers declare (parsed from include/*.h)."""
+    import re
+
+    names = []
+    for h in sorted((PKG_DIR.parent / "include").glob("*.h")):
+        text = h.read_text()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"^[A-Za-z_][\w\s\*]*?\b(halo_\w+)\s*\(", text, flags=re.M):
+            names.append(m.group(1))
+    return sorted(set(names))
+
+
+def lib() -> C.CDLL:
+    """Loads the HIP library (raises if it was not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise HaloError(f"{LIB_PATH} is not built (run __graft_entry__.build())")
+    L = C.CDLL(str(LIB_PATH))
+    for name, (res, args, has_err) in _SIGS.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args + (_ERR if has_err else [])
+    _lib = L
+    return L
+
+
+def _call(name, *args):
+    f = getattr(lib(), name)
+    err = C.create_string_buffer(ERRLEN)
+    rc = f(*args, err, ERRLEN)
+    if rc not in (0, None) and not (isinstance(rc, int) and rc >= 0 and name == "halo_kernel"):
+        raise HaloError(f"{name}: {err.value.decode(errors='replace')}")
+    if name == "halo_kernel" and rc < 0:
+        raise HaloError(f"{name}: {err.value.decode(errors='replace')}")
+    return rc
+
+
+def _scalar_arg(v, ctype) -> Arg:
+    a = Arg()
+    a.kind = 1
+    raw = bytes(ctype(v))
+    a.size = len(raw)
+    for i, b in enumerate(raw):
+        a.bytes[i] = b
+    return a
+
+
+class DeviceArray:
+    """A device allocation with a numpy dtype/shape for uploads and downloads."""
+
+    def __init__(self, dev: "Device", shape, dtype):
+        self.dev = dev
+        self.shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        self.buf = Buffer()
+        _call("halo_alloc", dev.handle, self.nbytes, C.byref(self.buf))
+
+    @property
+    def ptr(self) -> int:
+        return int(self.buf.device)
+
+    def upload(self, host: np.ndarray):
+        host = np.ascontiguousarray(host, dtype=self.dtype)
+        if host.nbytes != self.nbytes:
+            raise HaloError(f"upload of {host.nbytes} bytes into {self.nbytes}")
+        _call("halo_upload", self.dev.handle, C.byref(self.buf), 0, host.ctypes.data, host.nbytes)
+        return self
+
+    def download(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        _call("halo_download", self.dev.handle, C.byref(self.buf), 0, out.ctypes.data, out.nbytes)
+        return out
+
+    def fill(self, value: int = 0):
+        _call("halo_fill", self.dev.handle, C.byref(self.buf), value)
+        return self
+
+    def free(self):
+        if self.buf.device:
+            lib().halo_free(self.dev.handle, C.byref(self.buf))
+
+    def __del__(self):
+        try:
+            if self.dev.handle and self.buf.device:
+                self.free()
+        except Exception:
+            pass
+
+
+class Device:
+    """halo_device + halo_engine (one HIP device, one stream, the embedded gfx950 code object)."""
+
+    def __init__(self):
+        h = C.c_void_p()
+        _call("halo_device_create", 0, C.byref(h))
+        self.handle = h
+        e = C.c_void_p()
+        _call("halo_engine_create", self.handle, C.byref(e))
+        self.eng = e
+
+    def close(self):
+        if self.eng:
+            lib().halo_engine_destroy(self.eng)
+            self.eng = None
+        if self.handle:
+            lib().halo_device_destroy(self.handle)
+            self.handle = None
+
+    def array(self, shape, dtype) -> DeviceArray:
+        return DeviceArray(self, shape, dtype)
+
+    def to_device(self, host: np.ndarray) -> DeviceArray:
+        host = np.ascontiguousarray(host)
+        return DeviceArray(self, host.shape, host.dtype).upload(host)
+
+    def sync(self):
+        _call("halo_synchronize", self.handle)
+
+    def launch(self, kernel: str, grid, block, args):
+        """Launch by name; args are DeviceArray / ('u32', v) / ('u64', v) / ('f32', v) / ('ptr', int)."""
+        n = len(args)
+        arr = (Arg * n)()
+        for i, a in enumerate(args):
+            if isinstance(a, DeviceArray):
+                arr[i].kind = 0
+                arr[i].buffer = a.buf
+            elif a is None:
+                arr[i].kind = 0
+            else:
+                kind, v = a
+                if kind == "ptr":
+                    arr[i].kind = 0
+                    arr[i].buffer.device = v
+                else:
+                    ct = {"u32": C.c_uint32, "i32": C.c_int32, "u64": C.c_uint64, "f32": C.c_float}[kind]
+                    arr[i] = _scalar_arg(v, ct)
+        g = Dim3(*(tuple(grid) + (1,) * (3 - len(grid))))
+        b = Dim3(*(tuple(block) + (1,) * (3 - len(block))))
+        _call("halo_engine_launch", self.eng, kernel.encode(), g, b, arr, n)
+
+    def op(self, name: str, *args):
+        return _call("halo_op_" + name, self.eng, *args)
+
+    def timer_start(self):
+        _call("halo_timer_start", self.handle)
+
+    def timer_stop(self) -> float:
+        ms = C.c_float()
+        _call("halo_timer_stop", self.handle, C.byref(ms))
+        return float(ms.value)
+
+    def begin_capture(self):
+        _call("halo_begin_capture", self.handle)
+
+    def end_capture(self) -> Graph:
+        g = Graph()
+        _call("halo_end_capture", self.handle, C.byref(g))
+        return g
+
+    def launch_graph(self, g: Graph):
+        _call("halo_launch_graph", self.handle, C.byref(g))
+
+    def free_graph(self, g: Graph):
+        lib().halo_free_graph(self.handle, C.byref(g))
+
+
+class Q8Weights:
+    """A repacked Q8_0 matrix on the device (qs [rows][qstride] int8 + d [rows][cols/32] fp16 bits)."""
+
+    def __init__(self, dev: Device, rows: int, cols: int, qstride: int | None = None):
+        self.rows, self.cols = rows, cols
+        self.qstride = qstride or ((cols + 15) // 16 * 16)
+        self.qs = dev.array((rows, self.qstride), np.int8)
+        self.d = dev.array((rows, cols // 32), np.uint16)
+        self.desc = Q8Matrix(self.qs.ptr, self.d.ptr, rows, cols, self.qstride, 0)
+
+    @classmethod
+    def from_host(cls, dev: Device, qs: np.ndarray, d: np.ndarray):
+        w = cls(dev, qs.shape[0], qs.shape[1])
+        q = np.zeros((w.rows, w.qstride), np.int8)
+        q[:, : w.cols] = qs
+        w.qs.upload(q)
+        w.d.upload(d.astype(np.uint16))
+        return w
+
+    def synth(self, dev: Device, seed: int, sigma: float = 0.02):
+        dev.op("synth_q8", self.qs.ptr, self.d.ptr, self.rows, self.cols, self.qstride, seed, sigma)
+        return self
+
+    def host(self):
+        return self.qs.download()[:, : self.cols], self.d.download()

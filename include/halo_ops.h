@@ -1,0 +1,80 @@
+/* halo-flash MI355X operators: the engine-side dispatch of the hot path, as a C ABI.
+ *
+ * The reference's engine (src/engine/flash_next_gpu.cpp, batch_decode.cpp, prefill_chunk.cpp) decides which
+ * kernel and grid run each operator and launches them by name through rt::Device. halo_engine is that dispatch
+ * layer for gfx950: it owns the loaded code object and resolves kernels once; each halo_op_* call enqueues the
+ * launches of one operator on the device stream (no synchronization, no allocation unless stated). All tensor
+ * arguments are device addresses. Functions return 0 / -1 with a message in err, as halo_rt.h.
+ */
+#ifndef HALO_OPS_H_
+#define HALO_OPS_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "halo_rt.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct halo_engine halo_engine;
+
+/* A repacked Q8_0 matrix in device memory: int8 qs[rows][qstride] + fp16 d[rows][cols/32]
+ * (reference src/kernels/core.hip:2116-2124; FlashNextGpu::RepackQ8, src/engine/flash_next_gpu.cpp:414-432). */
+typedef struct halo_q8_matrix {
+  const int8_t* qs;
+  const uint16_t* d;
+  uint32_t rows, cols, qstride;
+  uint32_t pad;
+} halo_q8_matrix;
+
+/* FlashNextGpu::Init's LoadModule(CoreHsaco()) (src/engine/flash_next_gpu.cpp:273) plus kernel lookup. */
+int halo_engine_create(halo_device* dev, halo_engine** out, char* err, size_t errlen);
+void halo_engine_destroy(halo_engine* eng);
+halo_device* halo_engine_device(halo_engine* eng);
+/* Launches a kernel of the loaded code object by name (the engine's Launch(name, ...),
+ * src/engine/flash_next_gpu.cpp:125-158). */
+int halo_engine_launch(halo_engine* eng, const char* kernel, halo_dim3 grid, halo_dim3 block, const halo_arg* args,
+                       size_t nargs, char* err, size_t errlen);
+
+/* RepackQ8 (src/engine/flash_next_gpu.cpp:414-432): raw GGUF 34-byte blocks -> qs/d. */
+int halo_op_repack_q8_0(halo_engine* eng, const void* raw, int8_t* qs, uint16_t* d, uint32_t rows, uint32_t cols,
+                        uint32_t qstride, char* err, size_t errlen);
+
+/* Activation quantizer (halo_quantize_q8_rows, src/kernels/core.hip:3089-3101): x [T][cols] fp32 ->
+ * xq [T][cols] int8, xs [T][cols/32] fp32. */
+int halo_op_quantize_q8(halo_engine* eng, const float* x, int8_t* xq, float* xs, uint32_t tokens, uint32_t cols,
+                        char* err, size_t errlen);
+
+/* Q8_0 x int8-activation projection for M tokens (FlashNextGpu::MatVec + the batched int8 GEMV,
+ * src/engine/flash_next_gpu.cpp:212-254, src/kernels/batch_decode.hip:226-345):
+ *   y[t * ystride + r] = sum_b d[r][b] * xs[t][b] * isum(r, b, t),   t < M.
+ * M <= 8 streams the weights once per launch with v_dot4; larger M runs 16-token MFMA int8 tiles. */
+int halo_op_matvec_q8a8(halo_engine* eng, const halo_q8_matrix* w, const int8_t* xq, const float* xs, float* y,
+                        uint32_t m, uint32_t ystride, char* err, size_t errlen);
+/* The same with an explicit GEMV tiling (lanes per row 16/32/64, rows per lane group 1/2/4, waves per block) for
+ * tuning sweeps; m <= 8. */
+int halo_op_matvec_q8a8_tiled(halo_engine* eng, const halo_q8_matrix* w, const int8_t* xq, const float* xs,
+                              float* y, uint32_t m, uint32_t ystride, uint32_t lanes_per_row, uint32_t rows_per_lane,
+                              uint32_t waves, char* err, size_t errlen);
+
+/* fp32-activation Q8_0 GEMV (halo_gemv_q8r_r2 / _r4 as FlashNextGpu::MatVec picks them: r2 below 2048 rows). */
+int halo_op_matvec_q8_f32x(halo_engine* eng, const halo_q8_matrix* w, const float* x, float* y, char* err,
+                           size_t errlen);
+
+/* Exact int32 half-block dots isum[r][c/16] (parity instrumentation; same loads and dot chain as the GEMV). */
+int halo_op_q8_half_dots(halo_engine* eng, const halo_q8_matrix* w, const int8_t* xq, int32_t* isum, char* err,
+                         size_t errlen);
+
+/* Seeded synthetic tensors generated on the device: Q8_0 with q ~ U{-127..127}, d = fp16(|N(0, sigma)|/127);
+ * fp32 ~ N(0, sigma). */
+int halo_op_synth_q8(halo_engine* eng, int8_t* qs, uint16_t* d, uint32_t rows, uint32_t cols, uint32_t qstride,
+                     uint64_t seed, float sigma, char* err, size_t errlen);
+int halo_op_synth_f32(halo_engine* eng, float* x, uint64_t n, uint64_t seed, float sigma, char* err, size_t errlen);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HALO_OPS_H_ */

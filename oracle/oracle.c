@@ -1,0 +1,408 @@
+/* CPU oracle for the quantized decode / ragged-prefill hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker the HIP path is compared against. Only tests/, smoke() and bench.py's
+ * cpu_baseline leg load it. Each function cites the reference (casselc/halo-flash) file:line it restates.
+ *
+ * Parity pins (what checks each function independently of this file):
+ *   fp16/bf16 decode, Q8_0 dequant   -- tests/golden/quant_q8_0_f16_bf16.tsv (gguf-py outputs) + oracle/_ref
+ *   quantizer, block dots, gemv_q8a8 -- closed forms, brute force over edge blocks, oracle/_ref dot product
+ *   matvec_q8_0_f32x, route_topk, rmsnorm, l2norm, rope, silu -- oracle/_ref (the reference's own cpu_ops.cpp)
+ *   moe_token                        -- composition of the above, re-derived in numpy in tests
+ *   gdn_step                         -- closed-form invariants (zero state, beta=0 decay-only, delta rule fixes
+ *                                      S k = v when beta=1 and |k|=1), numpy restatement on tiny sizes
+ *   attention_head                   -- one position returns v; equal keys average v; numpy softmax
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* reference: src/core/quant.cpp:13-39 (IEEE binary16 -> binary32, subnormals exact). */
+float or_fp16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t exp = (h >> 10) & 0x1Fu;
+  const uint32_t mant = h & 0x3FFu;
+  uint32_t bits;
+  if (exp == 0) {
+    if (mant == 0) {
+      bits = sign;
+    } else {
+      /* value = mant * 2^-24: exact in fp32 */
+      float f = (float)mant * 5.9604644775390625e-8f;
+      return (h & 0x8000u) ? -f : f;
+    }
+  } else if (exp == 31) {
+    bits = sign | 0x7F800000u | (mant << 13);
+  } else {
+    bits = sign | ((exp + 112u) << 23) | (mant << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+uint16_t or_f32_to_fp16(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+  const uint32_t ax = x & 0x7FFFFFFFu;
+  if (ax >= 0x7F800000u) return (uint16_t)(sign | 0x7C00u | (ax > 0x7F800000u ? 0x200u : 0u));
+  if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u); /* rounds to >= 65520 -> inf */
+  if (ax < 0x38800000u) {
+    /* subnormal half (or zero): value / 2^-24 rounded to nearest even */
+    float a;
+    memcpy(&a, &ax, 4);
+    const float scaled = a * 16777216.0f; /* exact: power of two */
+    const float r = nearbyintf(scaled);   /* default rounding mode is RNE */
+    return (uint16_t)(sign | (uint16_t)r);
+  }
+  /* normal: drop 13 mantissa bits with RNE */
+  const uint32_t lsb = (ax >> 13) & 1u;
+  const uint32_t rounded = ax + 0xFFFu + lsb;
+  return (uint16_t)(sign | (uint16_t)((rounded - 0x38000000u) >> 13));
+}
+
+float or_bf16_to_f32(uint16_t h) {
+  const uint32_t bits = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+uint16_t or_f32_to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+/* reference: src/core/quant.cpp:411-421 (value = fp16(d) * q), block layout src/core/quant.hpp:58-61. */
+void or_dequant_q8_0(const uint8_t* blocks, float* out, size_t k) {
+  for (size_t b = 0; b < k / 32; ++b) {
+    const uint8_t* blk = blocks + b * 34;
+    const float d = or_fp16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+    for (int i = 0; i < 32; ++i) out[b * 32 + i] = d * (float)(int8_t)blk[2 + i];
+  }
+}
+
+/* reference: src/kernels/core.hip:2126-2138 (halo_repack_q8_0): int8 rows at stride qstride + fp16 scale array. */
+void or_repack_q8_0(const uint8_t* raw, int8_t* qs, uint16_t* d, uint32_t rows, uint32_t cols, uint32_t qstride) {
+  const uint32_t nb = cols / 32;
+  for (uint32_t r = 0; r < rows; ++r)
+    for (uint32_t b = 0; b < nb; ++b) {
+      const uint8_t* src = raw + ((size_t)r * nb + b) * 34;
+      d[(size_t)r * nb + b] = (uint16_t)(src[0] | (src[1] << 8));
+      memcpy(qs + (size_t)r * qstride + (size_t)b * 32, src + 2, 32);
+    }
+}
+
+void or_pack_q8_0(const int8_t* qs, const uint16_t* d, uint8_t* raw, uint32_t rows, uint32_t cols, uint32_t qstride) {
+  const uint32_t nb = cols / 32;
+  for (uint32_t r = 0; r < rows; ++r)
+    for (uint32_t b = 0; b < nb; ++b) {
+      uint8_t* dst = raw + ((size_t)r * nb + b) * 34;
+      const uint16_t s = d[(size_t)r * nb + b];
+      dst[0] = (uint8_t)(s & 0xFF);
+      dst[1] = (uint8_t)(s >> 8);
+      memcpy(dst + 2, qs + (size_t)r * qstride + (size_t)b * 32, 32);
+    }
+}
+
+/* reference: src/kernels/core.hip:3089-3101 (halo_quantize_q8_rows), host pin tests/gpu/quant_gpu_test.cpp:980-986
+ * and src/model/reference.cpp:58-66: scale = amax / 127.0f in fp32, q = nearbyint(x / scale) (round half to even,
+ * correctly rounded fp32 division), an all-zero block gives scale 0 and q 0. */
+void or_quantize_q8_act(const float* x, int8_t* xq, float* xs, size_t n) {
+  for (size_t b = 0; b < n / 32; ++b) {
+    float amax = 0.0f;
+    for (int i = 0; i < 32; ++i) {
+      const float a = fabsf(x[b * 32 + i]);
+      if (a > amax) amax = a;
+    }
+    const float scale = amax / 127.0f;
+    xs[b] = scale;
+    for (int i = 0; i < 32; ++i) {
+      const float t = x[b * 32 + i] / scale;
+      xq[b * 32 + i] = (int8_t)(scale > 0.0f ? (int)nearbyintf(t) : 0);
+    }
+  }
+}
+
+/* Exact integer block sums: reference src/kernels/batch_decode.hip:249-252 (sudot4 chain over 16 values, two halves
+ * per block) and tests/gpu/quant_gpu_test.cpp:987-1002 (host sums in `long`). |isum| <= 32*127*128 fits int32. */
+void or_q8_block_dots(const int8_t* qs, uint32_t rows, uint32_t cols, uint32_t qstride, const int8_t* xq,
+                      int32_t* isum) {
+  const uint32_t nb = cols / 32;
+  for (uint32_t r = 0; r < rows; ++r) {
+    const int8_t* w = qs + (size_t)r * qstride;
+    for (uint32_t b = 0; b < nb; ++b) {
+      int32_t s = 0;
+      for (int i = 0; i < 32; ++i) s += (int32_t)w[b * 32 + i] * (int32_t)xq[b * 32 + i];
+      isum[(size_t)r * nb + b] = s;
+    }
+  }
+}
+
+/* reference: tests/gpu/quant_gpu_test.cpp:987-1002 (sum over blocks of dw * sx * dot in double) and the kernel's
+ * epilogue src/kernels/batch_decode.hip:253-265 (acc += s_w * (s_x * isum)). */
+void or_gemv_q8a8(const int8_t* qs, const uint16_t* d, uint32_t rows, uint32_t cols, uint32_t qstride,
+                  const int8_t* xq, const float* xs, float* y) {
+  const uint32_t nb = cols / 32;
+  for (uint32_t r = 0; r < rows; ++r) {
+    const int8_t* w = qs + (size_t)r * qstride;
+    double acc = 0.0;
+    for (uint32_t b = 0; b < nb; ++b) {
+      int32_t s = 0;
+      for (int i = 0; i < 32; ++i) s += (int32_t)w[b * 32 + i] * (int32_t)xq[b * 32 + i];
+      acc += (double)or_fp16_to_f32(d[(size_t)r * nb + b]) * (double)xs[b] * (double)s;
+    }
+    y[r] = (float)acc;
+  }
+}
+
+void or_gemv_q8a8_mag(const int8_t* qs, const uint16_t* d, uint32_t rows, uint32_t cols, uint32_t qstride,
+                      const int8_t* xq, const float* xs, double* mag) {
+  const uint32_t nb = cols / 32;
+  for (uint32_t r = 0; r < rows; ++r) {
+    const int8_t* w = qs + (size_t)r * qstride;
+    double acc = 0.0;
+    for (uint32_t b = 0; b < nb; ++b) {
+      int32_t s = 0;
+      for (int i = 0; i < 32; ++i) s += (int32_t)w[b * 32 + i] * (int32_t)xq[b * 32 + i];
+      acc += fabs((double)or_fp16_to_f32(d[(size_t)r * nb + b]) * (double)xs[b] * (double)s);
+    }
+    mag[r] = acc;
+  }
+}
+
+/* reference: src/model/cpu_ops.cpp:108-132 (cpu::MatVec: dequantize each row to fp32, accumulate w*x in double,
+ * cast to float; rows split into ceil(rows/threads) chunks, one std::thread each). */
+struct mv_job {
+  const int8_t* qs;
+  const uint16_t* d;
+  uint32_t cols, qstride, r0, r1;
+  const float* x;
+  float* y;
+};
+
+static void* mv_work(void* p) {
+  const struct mv_job* j = (const struct mv_job*)p;
+  const uint32_t nb = j->cols / 32;
+  float* w = (float*)malloc(sizeof(float) * j->cols);
+  for (uint32_t r = j->r0; r < j->r1; ++r) {
+    const int8_t* q = j->qs + (size_t)r * j->qstride;
+    for (uint32_t b = 0; b < nb; ++b) {
+      const float s = or_fp16_to_f32(j->d[(size_t)r * nb + b]);
+      for (int i = 0; i < 32; ++i) w[b * 32 + i] = s * (float)q[b * 32 + i];
+    }
+    double acc = 0.0;
+    for (uint32_t i = 0; i < j->cols; ++i) acc += (double)w[i] * (double)j->x[i];
+    j->y[r] = (float)acc;
+  }
+  free(w);
+  return NULL;
+}
+
+void or_matvec_q8_0_f32x(const int8_t* qs, const uint16_t* d, uint32_t rows, uint32_t cols, uint32_t qstride,
+                         const float* x, float* y, int threads) {
+  if (threads < 1) threads = 1;
+  if (threads == 1 || rows < 2u * (uint32_t)threads) {
+    struct mv_job j = {qs, d, cols, qstride, 0, rows, x, y};
+    mv_work(&j);
+    return;
+  }
+  const uint32_t chunk = (rows + (uint32_t)threads - 1) / (uint32_t)threads;
+  pthread_t* th = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)threads);
+  struct mv_job* jobs = (struct mv_job*)malloc(sizeof(struct mv_job) * (size_t)threads);
+  int n = 0;
+  for (uint32_t b = 0; b < rows; b += chunk, ++n) {
+    jobs[n] = (struct mv_job){qs, d, cols, qstride, b, b + chunk < rows ? b + chunk : rows, x, y};
+    pthread_create(&th[n], NULL, mv_work, &jobs[n]);
+  }
+  for (int i = 0; i < n; ++i) pthread_join(th[i], NULL);
+  free(th);
+  free(jobs);
+}
+
+void or_matvec_f32(const float* w, uint32_t rows, uint32_t cols, const float* x, float* y) {
+  for (uint32_t r = 0; r < rows; ++r) {
+    double acc = 0.0;
+    for (uint32_t i = 0; i < cols; ++i) acc += (double)w[(size_t)r * cols + i] * (double)x[i];
+    y[r] = (float)acc;
+  }
+}
+
+/* reference: src/model/cpu_ops.cpp:158-166 */
+float or_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+float or_silu(float x) { return x * or_sigmoid(x); }
+float or_softplus(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+
+/* reference: src/model/cpu_ops.cpp:134-145 (sum of squares in double, scale computed in fp32). */
+void or_rmsnorm(float* x, size_t n, const float* w, float eps) {
+  double ss = 0.0;
+  for (size_t i = 0; i < n; ++i) ss += (double)x[i] * (double)x[i];
+  const float scale = 1.0f / sqrtf((float)(ss / (double)n) + eps);
+  for (size_t i = 0; i < n; ++i) x[i] = x[i] * scale * (w ? w[i] : 1.0f);
+}
+
+/* reference: src/model/cpu_ops.cpp:147-156 */
+void or_l2norm(float* x, size_t n, float eps) {
+  double ss = 0.0;
+  for (size_t i = 0; i < n; ++i) ss += (double)x[i] * (double)x[i];
+  const float scale = 1.0f / sqrtf((float)ss + eps);
+  for (size_t i = 0; i < n; ++i) x[i] *= scale;
+}
+
+/* reference: src/model/cpu_ops.cpp:168-185 (NEOX pairs (i, i + rotary/2), freq = theta^(-2i/rotary)). */
+void or_rope_neox(float* x, uint32_t heads, uint32_t head_dim, uint32_t rotary_dim, uint32_t pos, float theta) {
+  const uint32_t half = rotary_dim / 2;
+  for (uint32_t h = 0; h < heads; ++h) {
+    float* v = x + (size_t)h * head_dim;
+    for (uint32_t i = 0; i < half; ++i) {
+      const float freq = powf(theta, -2.0f * (float)i / (float)rotary_dim);
+      const float angle = (float)pos * freq;
+      const float c = cosf(angle), s = sinf(angle);
+      const float a = v[i], b = v[i + half];
+      v[i] = a * c - b * s;
+      v[i + half] = a * s + b * c;
+    }
+  }
+}
+
+/* reference: src/model/cpu_ops.cpp:187-207 (softmax with a double denominator, k largest probabilities with ties to
+ * the lower id, renormalized by max(sum, 2^-14)). Selection by repeated arg-max, which orders exactly as the
+ * reference's partial_sort comparator. */
+void or_route_topk(const float* logits, uint32_t n, uint32_t k, uint32_t* ids, float* weights) {
+  float mx = logits[0];
+  for (uint32_t i = 1; i < n; ++i)
+    if (logits[i] > mx) mx = logits[i];
+  float* prob = (float*)malloc(sizeof(float) * n);
+  unsigned char* taken = (unsigned char*)calloc(n, 1);
+  double den = 0.0;
+  for (uint32_t i = 0; i < n; ++i) {
+    prob[i] = expf(logits[i] - mx);
+    den += prob[i];
+  }
+  for (uint32_t i = 0; i < n; ++i) prob[i] = (float)(prob[i] / den);
+  float sum = 0.0f;
+  for (uint32_t s = 0; s < k; ++s) {
+    uint32_t best = n;
+    for (uint32_t i = 0; i < n; ++i)
+      if (!taken[i] && (best == n || prob[i] > prob[best])) best = i;
+    taken[best] = 1;
+    ids[s] = best;
+    sum += prob[best];
+  }
+  if (sum < 6.103515625e-5f) sum = 6.103515625e-5f;
+  for (uint32_t s = 0; s < k; ++s) weights[s] = prob[ids[s]] / sum;
+  free(prob);
+  free(taken);
+}
+
+/* reference: src/model/reference.cpp:530-578 (ReferenceModel::Moe): route, per slot SiLU(gate) * up, down, weighted
+ * sum in slot order, then the shared expert scaled by sigmoid(shared gate logit). Expert projections take the input
+ * quantized per 32 values (the int8-activation decode path, src/kernels/batch_decode.hip:226-270). */
+void or_moe_token(const float* x, uint32_t hidden, uint32_t ff, uint32_t n_experts, uint32_t k,
+                  const float* router, const int8_t* gu_q, const uint16_t* gu_d, const int8_t* dn_q,
+                  const uint16_t* dn_d, const int8_t* sgu_q, const uint16_t* sgu_d, const int8_t* sdn_q,
+                  const uint16_t* sdn_d, uint32_t sff, const float* sgate, float* out, uint32_t* ids, float* weights) {
+  float* logits = (float*)malloc(sizeof(float) * n_experts);
+  or_matvec_f32(router, n_experts, hidden, x, logits);
+  or_route_topk(logits, n_experts, k, ids, weights);
+  const uint32_t maxff = ff > sff ? ff : sff;
+  int8_t* xq = (int8_t*)malloc(hidden);
+  float* xs = (float*)malloc(sizeof(float) * (hidden / 32));
+  float* gu = (float*)malloc(sizeof(float) * 2 * maxff);
+  float* h = (float*)malloc(sizeof(float) * maxff);
+  int8_t* hq = (int8_t*)malloc(maxff);
+  float* hs = (float*)malloc(sizeof(float) * (maxff / 32));
+  float* down = (float*)malloc(sizeof(float) * hidden);
+  or_quantize_q8_act(x, xq, xs, hidden);
+  for (uint32_t i = 0; i < hidden; ++i) out[i] = 0.0f;
+  for (uint32_t s = 0; s <= k; ++s) {
+    const int shared = s == k;
+    const uint32_t f = shared ? sff : ff;
+    const int8_t* gq = shared ? sgu_q : gu_q + (size_t)ids[s] * 2 * ff * hidden;
+    const uint16_t* gd = shared ? sgu_d : gu_d + (size_t)ids[s] * 2 * ff * (hidden / 32);
+    const int8_t* dq = shared ? sdn_q : dn_q + (size_t)ids[s] * hidden * ff;
+    const uint16_t* dd = shared ? sdn_d : dn_d + (size_t)ids[s] * hidden * (ff / 32);
+    or_gemv_q8a8(gq, gd, 2 * f, hidden, hidden, xq, xs, gu);
+    for (uint32_t j = 0; j < f; ++j) h[j] = or_silu(gu[j]) * gu[f + j];
+    or_quantize_q8_act(h, hq, hs, f);
+    or_gemv_q8a8(dq, dd, hidden, f, f, hq, hs, down);
+    float wgt;
+    if (shared) {
+      double g = 0.0;
+      for (uint32_t i = 0; i < hidden; ++i) g += (double)sgate[i] * (double)x[i];
+      wgt = or_sigmoid((float)g);
+    } else {
+      wgt = weights[s];
+    }
+    for (uint32_t i = 0; i < hidden; ++i) out[i] += wgt * down[i];
+  }
+  free(logits);
+  free(xq);
+  free(xs);
+  free(gu);
+  free(h);
+  free(hq);
+  free(hs);
+  free(down);
+}
+
+/* reference: src/model/reference.cpp:329-364 (ReferenceModel::LinearAttention, one value head):
+ *   S <- decay * S; u = S k; delta = (v - u) * beta; S <- S + delta k^T; o = (S q) / sqrt(d)
+ * with S[j][i] (j value, i key), dot products in double. The layer's decay = exp(a * softplus(alpha + dt)) is
+ * passed here as its logarithm g. */
+void or_gdn_step(float* S, uint32_t d, const float* q, const float* k, const float* v, float g, float beta, float* o) {
+  const float decay = expf(g);
+  const float q_scale = 1.0f / sqrtf((float)d);
+  float* u = (float*)malloc(sizeof(float) * d);
+  for (uint32_t j = 0; j < d; ++j) {
+    float* row = S + (size_t)j * d;
+    double acc = 0.0;
+    for (uint32_t i = 0; i < d; ++i) {
+      row[i] *= decay;
+      acc += (double)row[i] * k[i];
+    }
+    u[j] = (float)acc;
+  }
+  for (uint32_t j = 0; j < d; ++j) {
+    const float delta = (v[j] - u[j]) * beta;
+    float* row = S + (size_t)j * d;
+    double acc = 0.0;
+    for (uint32_t i = 0; i < d; ++i) {
+      row[i] += delta * k[i];
+      acc += (double)row[i] * q[i];
+    }
+    o[j] = (float)acc * q_scale;
+  }
+  free(u);
+}
+
+/* reference: src/model/reference.cpp:492-521 (dense branch: scores in double rounded to fp32, scaled by 1/sqrt(hd),
+ * max-subtracted exp, double denominator, p = score/denom in fp32, o += p * v). */
+void or_attention_head(const float* q, const float* k, const float* v, uint32_t n, uint32_t hd, size_t kv_stride,
+                       float* o) {
+  const float scale = 1.0f / sqrtf((float)hd);
+  float* sc = (float*)malloc(sizeof(float) * (n ? n : 1));
+  float mx = -INFINITY;
+  for (uint32_t j = 0; j < n; ++j) {
+    double dot = 0.0;
+    for (uint32_t i = 0; i < hd; ++i) dot += (double)q[i] * k[(size_t)j * kv_stride + i];
+    sc[j] = (float)dot * scale;
+    if (sc[j] > mx) mx = sc[j];
+  }
+  double den = 0.0;
+  for (uint32_t j = 0; j < n; ++j) {
+    sc[j] = expf(sc[j] - mx);
+    den += sc[j];
+  }
+  for (uint32_t i = 0; i < hd; ++i) o[i] = 0.0f;
+  for (uint32_t j = 0; j < n; ++j) {
+    const float p = (float)(sc[j] / den);
+    for (uint32_t i = 0; i < hd; ++i) o[i] += p * v[(size_t)j * kv_stride + i];
+  }
+  free(sc);
+}

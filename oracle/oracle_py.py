@@ -1,0 +1,142 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so) and of the reference build (oracle/_ref/libhaloref.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, as the
+checker. The product library never loads it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ORACLE_SO = HERE / "liboracle.so"
+REF_SO = HERE / "_ref" / "libhaloref.so"
+
+_VP, _SZ, _U32, _U64, _F32 = C.c_void_p, C.c_size_t, C.c_uint32, C.c_uint64, C.c_float
+_PF = np.ctypeslib.ndpointer(np.float32, flags="C")
+_PD = np.ctypeslib.ndpointer(np.float64, flags="C")
+_PI8 = np.ctypeslib.ndpointer(np.int8, flags="C")
+_PU8 = np.ctypeslib.ndpointer(np.uint8, flags="C")
+_PU16 = np.ctypeslib.ndpointer(np.uint16, flags="C")
+_PI32 = np.ctypeslib.ndpointer(np.int32, flags="C")
+_PU32 = np.ctypeslib.ndpointer(np.uint32, flags="C")
+
+_ORACLE_SIGS = {
+    "or_fp16_to_f32": (_F32, [C.c_uint16]),
+    "or_f32_to_fp16": (C.c_uint16, [_F32]),
+    "or_bf16_to_f32": (_F32, [C.c_uint16]),
+    "or_f32_to_bf16": (C.c_uint16, [_F32]),
+    "or_dequant_q8_0": (None, [_PU8, _PF, _SZ]),
+    "or_repack_q8_0": (None, [_PU8, _PI8, _PU16, _U32, _U32, _U32]),
+    "or_pack_q8_0": (None, [_PI8, _PU16, _PU8, _U32, _U32, _U32]),
+    "or_quantize_q8_act": (None, [_PF, _PI8, _PF, _SZ]),
+    "or_q8_block_dots": (None, [_PI8, _U32, _U32, _U32, _PI8, _PI32]),
+    "or_gemv_q8a8": (None, [_PI8, _PU16, _U32, _U32, _U32, _PI8, _PF, _PF]),
+    "or_gemv_q8a8_mag": (None, [_PI8, _PU16, _U32, _U32, _U32, _PI8, _PF, _PD]),
+    "or_matvec_q8_0_f32x": (None, [_PI8, _PU16, _U32, _U32, _U32, _PF, _PF, C.c_int]),
+    "or_matvec_f32": (None, [_PF, _U32, _U32, _PF, _PF]),
+    "or_sigmoid": (_F32, [_F32]),
+    "or_silu": (_F32, [_F32]),
+    "or_softplus": (_F32, [_F32]),
+    "or_rmsnorm": (None, [_PF, _SZ, _VP, _F32]),
+    "or_l2norm": (None, [_PF, _SZ, _F32]),
+    "or_rope_neox": (None, [_PF, _U32, _U32, _U32, _U32, _F32]),
+    "or_route_topk": (None, [_PF, _U32, _U32, _PU32, _PF]),
+    "or_moe_token": (None, [_PF, _U32, _U32, _U32, _U32, _PF, _PI8, _PU16, _PI8, _PU16, _PI8, _PU16, _PI8,
+                            _PU16, _U32, _PF, _PF, _PU32, _PF]),
+    "or_gdn_step": (None, [_PF, _U32, _PF, _PF, _PF, _F32, _F32, _PF]),
+    "or_attention_head": (None, [_PF, _PF, _PF, _U32, _U32, _SZ, _PF]),
+}
+
+_REF_SIGS = {
+    "ref_fp16_to_f32": (_F32, [C.c_uint16]),
+    "ref_dequant_q8_0": (None, [_PU8, _PF, _SZ]),
+    "ref_dot_q8_0": (_F32, [_PU8, _PF, _SZ]),
+    "ref_matvec_q8_0": (None, [_PU8, _U64, _U64, _PF, _PF]),
+    "ref_matvec_f32": (None, [_PF, _U64, _U64, _PF, _PF]),
+    "ref_route_topk": (None, [_PF, _U32, _U32, _PU32, _PF]),
+    "ref_rmsnorm": (None, [_PF, _SZ, _VP, _F32]),
+    "ref_l2norm": (None, [_PF, _SZ, _F32]),
+    "ref_rope": (None, [_PF, _U32, _U32, _U32, _U32, _F32]),
+    "ref_silu": (_F32, [_F32]),
+    "ref_sigmoid": (_F32, [_F32]),
+    "ref_softplus": (_F32, [_F32]),
+    "ref_hw_threads": (C.c_uint, []),
+}
+
+_libs: dict[str, C.CDLL] = {}
+
+
+def _load(path: Path, sigs) -> C.CDLL:
+    key = str(path)
+    if key not in _libs:
+        L = C.CDLL(key)
+        for n, (r, a) in sigs.items():
+            f = getattr(L, n)
+            f.restype, f.argtypes = r, a
+        _libs[key] = L
+    return _libs[key]
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+
+
+def oracle() -> C.CDLL:
+    if not ORACLE_SO.exists():
+        build()
+    return _load(ORACLE_SO, _ORACLE_SIGS)
+
+
+def has_ref() -> bool:
+    return REF_SO.exists()
+
+
+def ref() -> C.CDLL:
+    return _load(REF_SO, _REF_SIGS)
+
+
+# ---- numpy conveniences -------------------------------------------------------------------------------------------
+
+def quantize(x: np.ndarray):
+    x = np.ascontiguousarray(x, np.float32)
+    xq = np.empty(x.shape, np.int8)
+    xs = np.empty(x.shape[:-1] + (x.shape[-1] // 32,), np.float32)
+    oracle().or_quantize_q8_act(x.reshape(-1), xq.reshape(-1), xs.reshape(-1), x.size)
+    return xq, xs
+
+
+def gemv_q8a8(qs, d, xq, xs):
+    """y[t][r] for t tokens (xq [T][cols] or [cols])."""
+    qs = np.ascontiguousarray(qs, np.int8)
+    d = np.ascontiguousarray(d, np.uint16)
+    rows, cols = qs.shape
+    xq2 = np.atleast_2d(xq)
+    xs2 = np.atleast_2d(xs)
+    y = np.empty((xq2.shape[0], rows), np.float32)
+    mag = np.empty((xq2.shape[0], rows), np.float64)
+    for t in range(xq2.shape[0]):
+        oracle().or_gemv_q8a8(qs, d, rows, cols, cols, np.ascontiguousarray(xq2[t]), np.ascontiguousarray(xs2[t]), y[t])
+        oracle().or_gemv_q8a8_mag(qs, d, rows, cols, cols, np.ascontiguousarray(xq2[t]),
+                                  np.ascontiguousarray(xs2[t]), mag[t])
+    if np.ndim(xq) == 1:
+        return y[0], mag[0]
+    return y, mag
+
+
+def block_dots(qs, xq):
+    qs = np.ascontiguousarray(qs, np.int8)
+    rows, cols = qs.shape
+    out = np.empty((rows, cols // 32), np.int32)
+    oracle().or_q8_block_dots(qs, rows, cols, cols, np.ascontiguousarray(xq, np.int8), out)
+    return out
+
+
+def synth_q8(rng: np.random.Generator, rows: int, cols: int, sigma: float = 0.02):
+    """BASELINE's Q8_0 distribution: q ~ U{-127..127}, d = fp16(|N(0, sigma)| / 127)."""
+    qs = rng.integers(-127, 128, size=(rows, cols), dtype=np.int8)
+    d = (np.abs(rng.normal(0.0, sigma, size=(rows, cols // 32))) / 127.0).astype(np.float16).view(np.uint16)
+    return qs, d

@@ -1,0 +1,62 @@
+// C entry points over the reference's own CPU code (casselc/halo-flash src/core/quant.cpp,
+// src/model/cpu_ops.cpp), compiled from the sources where they lie by oracle/Makefile into oracle/_ref/.
+// TEST INFRASTRUCTURE ONLY: used to validate the C restatement in oracle.c and, in bench.py's cpu_baseline leg,
+// as the timed reference CPU path. Nothing here is linked into the product library.
+#include <cstdint>
+#include <cstring>
+#include <span>
+#include <thread>
+
+#include "core/quant.hpp"
+#include "model/cpu_ops.hpp"
+#include "model/weights.hpp"
+
+using halo::core::GgmlType;
+using halo::model::TensorRef;
+
+extern "C" {
+
+float ref_fp16_to_f32(std::uint16_t h) { return halo::quant::Fp16ToFloat(h); }
+
+void ref_dequant_q8_0(const void* blocks, float* out, std::size_t k) { halo::quant::DequantizeQ8_0(blocks, out, k); }
+
+float ref_dot_q8_0(const void* blocks, const float* x, std::size_t k) {
+  return halo::quant::DotProductQ8_0(blocks, std::span<const float>(x, k), k);
+}
+
+// cpu::MatVec over a raw GGUF Q8_0 matrix (rows x cols, 34-byte blocks); threads as the reference picks them.
+void ref_matvec_q8_0(const void* raw, std::uint64_t rows, std::uint64_t cols, const float* x, float* y) {
+  TensorRef t;
+  t.data = raw;
+  t.type = GgmlType::kQ8_0;
+  t.rows = rows;
+  t.cols = cols;
+  halo::model::cpu::MatVec(t, 0, std::span<const float>(x, cols), std::span<float>(y, rows));
+}
+
+void ref_matvec_f32(const float* w, std::uint64_t rows, std::uint64_t cols, const float* x, float* y) {
+  TensorRef t;
+  t.data = w;
+  t.type = GgmlType::kF32;
+  t.rows = rows;
+  t.cols = cols;
+  halo::model::cpu::MatVec(t, 0, std::span<const float>(x, cols), std::span<float>(y, rows));
+}
+
+void ref_route_topk(const float* logits, std::uint32_t n, std::uint32_t k, std::uint32_t* ids, float* w) {
+  halo::model::cpu::RouteTopK(std::span<const float>(logits, n), std::span<std::uint32_t>(ids, k),
+                              std::span<float>(w, k));
+}
+
+void ref_rmsnorm(float* x, std::size_t n, const float* w, float eps) {
+  halo::model::cpu::RmsNorm(std::span<float>(x, n), w, eps);
+}
+void ref_l2norm(float* x, std::size_t n, float eps) { halo::model::cpu::L2Norm(std::span<float>(x, n), eps); }
+void ref_rope(float* x, std::uint32_t heads, std::uint32_t hd, std::uint32_t rot, std::uint32_t pos, float theta) {
+  halo::model::cpu::Rope(x, heads, hd, rot, pos, theta);
+}
+float ref_silu(float x) { return halo::model::cpu::Silu(x); }
+float ref_sigmoid(float x) { return halo::model::cpu::Sigmoid(x); }
+float ref_softplus(float x) { return halo::model::cpu::Softplus(x); }
+unsigned ref_hw_threads() { return std::thread::hardware_concurrency(); }
+}

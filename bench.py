@@ -55,6 +55,10 @@ def run_gpu(args):
     dev = H.Device()
     try:
         res = {}
+        if args.mode == "c0":
+            return run_c0(args, dev, H, res)
+        if args.mode == "membw":
+            return run_membw(args, dev, H, res)
         # ---------------- C1 pass at M=1 (the bench value) and the M sweep ----------------
         per_copy = sum(q8_bytes(r, c) for r, c in C1_SHAPES)
         copies = max(2, -(-MIN_ROTATION_BYTES // per_copy))
@@ -128,7 +132,46 @@ def run_gpu(args):
         res["c1_sweep"] = sweep
         log(f"[bench] C1 sweep {sweep}")
         del sets
+        return run_c0(args, dev, H, res)
+    finally:
+        dev.close()
 
+
+def run_membw(args, dev, H, res):
+    """Streaming-read yardstick: one launch reads one buffer of the given size; buffers rotate over >= 600 MB."""
+    out = {}
+    sink = dev.array(4, np.int32)
+    pool = dev.array(MIN_ROTATION_BYTES + (256 << 20), np.uint8)  # one allocation, carved by offset
+    for size in (17858560, 4 << 20, 64 << 20, 256 << 20):
+        n16 = size // 16
+        nbuf = max(2, -(-MIN_ROTATION_BYTES // size))
+        step = (size + 4095) // 4096 * 4096
+        ptrs = [pool.ptr + i * step for i in range(nbuf)]
+        for grid in (1024, 2048, 4096, 8192):
+            if grid * 256 > n16:
+                continue
+            log(f"[bench] membw size {size} grid {grid} buffers {nbuf}")
+            dev.begin_capture()
+            for p_ in ptrs:
+                dev.launch("halo_stream_read", (grid,), (256,), [("ptr", p_), ("u64", n16), sink])
+            g = dev.end_capture()
+            dev.launch_graph(g)
+            dev.sync()
+            nrep = max(1, 2000 // nbuf)
+            dev.timer_start()
+            for _ in range(nrep):
+                dev.launch_graph(g)
+            ms = dev.timer_stop()
+            us = ms * 1e3 / (nrep * nbuf)
+            out[f"{size}B_grid{grid}"] = {"us": round(us, 3), "GBps": round(size / us / 1e3, 1)}
+            dev.free_graph(g)
+    log(f"[bench] membw {out}")
+    res["membw"] = out
+    res["roofline"] = None
+    return res
+
+
+def run_c0(args, dev, H, res):
         # ---------------- C0: the dominant kernel, back-to-back over rotated copies ----------------
         c0_copies = max(2, -(-MIN_ROTATION_BYTES // q8_bytes(4096, 4096)))
         ws0 = [H.Q8Weights(dev, 4096, 4096).synth(dev, seed=50000 + i) for i in range(c0_copies)]
@@ -137,12 +180,16 @@ def run_gpu(args):
         x0q, x0s, y0 = dev.array(4096, np.int8), dev.array(128, np.float32), dev.array(4096, np.float32)
         dev.op("quantize_q8", x0.ptr, x0q.ptr, x0s.ptr, 1, 4096)
         dev.sync()
-        tilings = [(64, 1, 4), (64, 2, 4), (64, 1, 2), (64, 1, 1), (32, 1, 4), (64, 4, 4)] if args.sweep else [None]
+        tilings = [(64, 1, 4), (64, 2, 4), (64, 1, 2), (64, 1, 1), (32, 1, 4), "nt"] if args.sweep else [None]
         c0 = {}
         for t in tilings:
             dev.begin_capture()
             for w in ws0:
-                if t is None:
+                if t == "nt":
+                    dev.launch("halo_gemv_q8a8nt_l64_r1_b1", (1024,), (256,),
+                               [("ptr", w.qs.ptr), ("ptr", w.d.ptr), x0q, x0s, y0, ("u32", 4096), ("u32", 4096),
+                                ("u32", w.qstride), ("u32", 4096)])
+                elif t is None:
                     dev.op("matvec_q8a8", ctypes.byref(w.desc), x0q.ptr, x0s.ptr, y0.ptr, 1, 4096)
                 else:
                     dev.op("matvec_q8a8_tiled", ctypes.byref(w.desc), x0q.ptr, x0s.ptr, y0.ptr, 1, 4096, *t)
@@ -173,8 +220,6 @@ def run_gpu(args):
         if args.sweep:
             res["c0_tilings"] = c0
         return res
-    finally:
-        dev.close()
 
 
 def cpu_baseline(budget_s: float):
@@ -239,12 +284,17 @@ def main():
     p.add_argument("--sweep", action="store_true", help="also time alternative C0 GEMV tilings")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--mode", choices=["all", "c0", "membw"], default="all",
+                   help="c0: only the C0 GEMV loop (for profiling one kernel shape)")
     args = p.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
               "(the path is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
         sys.exit(2)
     res = run_gpu(args)
+    if args.mode in ("c0", "membw"):
+        print(json.dumps({k: res.get(k) for k in ("roofline", "c0_tilings", "membw")}), flush=True)
+        return
     line = {
         "metric": "Q8_0 GEMV achieved HBM GB/s; decode tokens/s at 1 and 4 sessions",
         "value": round(res["value"], 1),

@@ -4,7 +4,44 @@
 // weights; FlashNextGpu::MatVec (212-254) picks the GEMV variant and grid per matrix.
 #include "engine.hpp"
 
+#include <elf.h>
+
+#include <vector>
+
 using namespace halo::engine;
+
+namespace {
+
+// Names of every kernel in an AMDGPU code object: the symbols with a ".kd" (kernel descriptor) suffix.
+std::vector<std::string> KernelNames(const std::uint8_t* code, std::size_t bytes) {
+  std::vector<std::string> out;
+  if (bytes < sizeof(Elf64_Ehdr)) return out;
+  Elf64_Ehdr eh;
+  std::memcpy(&eh, code, sizeof eh);
+  if (std::memcmp(eh.e_ident, ELFMAG, SELFMAG) != 0 || eh.e_shoff == 0) return out;
+  for (unsigned i = 0; i < eh.e_shnum; ++i) {
+    Elf64_Shdr sh;
+    std::memcpy(&sh, code + eh.e_shoff + i * sizeof(Elf64_Shdr), sizeof sh);
+    if (sh.sh_type != SHT_SYMTAB && sh.sh_type != SHT_DYNSYM) continue;
+    Elf64_Shdr strh;
+    std::memcpy(&strh, code + eh.e_shoff + sh.sh_link * sizeof(Elf64_Shdr), sizeof strh);
+    const char* strtab = reinterpret_cast<const char*>(code + strh.sh_offset);
+    for (std::size_t off = 0; off + sizeof(Elf64_Sym) <= sh.sh_size; off += sizeof(Elf64_Sym)) {
+      Elf64_Sym sym;
+      std::memcpy(&sym, code + sh.sh_offset + off, sizeof sym);
+      std::string name(strtab + sym.st_name);
+      if (name.size() > 3 && name.compare(name.size() - 3, 3, ".kd") == 0) {
+        name.resize(name.size() - 3);
+        bool seen = false;
+        for (const auto& n : out) seen = seen || n == name;
+        if (!seen) out.push_back(name);
+      }
+    }
+  }
+  return out;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -16,6 +53,19 @@ int halo_engine_create(halo_device* dev, halo_engine** out, char* err, size_t er
   if (halo_load_module(dev, code, bytes, err, errlen) != 0) return -1;
   auto* eng = new halo_engine();
   eng->dev = dev;
+  // Resolve every kernel now: lookups are not allowed while a graph is being captured.
+  for (const auto& name : KernelNames(code, bytes)) {
+    const halo_kernel_id id = halo_kernel(dev, name.c_str(), err, errlen);
+    if (id < 0) {
+      delete eng;
+      return -1;
+    }
+    eng->ids.emplace(name, id);
+  }
+  if (eng->ids.empty()) {
+    delete eng;
+    return SetErr(err, errlen, "the code object lists no kernels"), -1;
+  }
   *out = eng;
   return 0;
 }

@@ -1,0 +1,124 @@
+// MoE decode dispatch (FlashNextGpu::Moe, src/engine/flash_next_gpu.cpp:697-845, and the session-union path of
+// StepBatch, src/engine/batch_decode.cpp): four launches over device-resident routing, no host round trip.
+#include "engine.hpp"
+
+using namespace halo::engine;
+
+namespace {
+
+constexpr std::uint32_t kMaxTokens = 16;
+
+std::size_t Align(std::size_t v) { return (v + 255) / 256 * 256; }
+
+std::uint32_t MaxU(const halo_moe_weights* w, std::uint32_t T) {
+  return std::min<std::uint32_t>(T * w->n_used, w->n_experts);
+}
+
+int Check(const halo_moe_weights* w, std::uint32_t T, char* err, std::size_t errlen) {
+  if (w == nullptr || w->router == nullptr || w->gate.qs == nullptr || w->up.qs == nullptr || w->down.qs == nullptr)
+    return SetErr(err, errlen, "moe: missing tensors"), -1;
+  if (T == 0 || T > kMaxTokens) return SetErr(err, errlen, "moe decode takes 1..%u tokens, got %u", kMaxTokens, T), -1;
+  const std::uint32_t H = w->hidden, F = w->ff, SF = w->shared_ff;
+  if (w->n_experts == 0 || w->n_experts > 1024 || w->n_used == 0 || w->n_used > 32 || w->n_used > w->n_experts)
+    return SetErr(err, errlen, "moe: %u experts / %u used unsupported", w->n_experts, w->n_used), -1;
+  if (H % 1024 != 0 || H > 4096 || H % 32 != 0) return SetErr(err, errlen, "moe: hidden %u must be 1024..4096 step 1024", H), -1;
+  if (F % 32 != 0 || F == 0 || F > 512) return SetErr(err, errlen, "moe: expert ff %u must be a multiple of 32, <= 512", F), -1;
+  const bool shared = w->shared_gate_proj.qs != nullptr;
+  if (shared && (SF % 32 != 0 || SF == 0 || SF > 512 || w->shared_up.qs == nullptr || w->shared_down.qs == nullptr))
+    return SetErr(err, errlen, "moe: shared ff %u must be a multiple of 32, <= 512", SF), -1;
+  auto dense = [](const halo_q8_matrix& m, std::uint32_t rows, std::uint32_t cols) {
+    return m.rows == rows && m.cols == cols && m.qstride == cols;
+  };
+  if (!dense(w->gate, w->n_experts * F, H) || !dense(w->up, w->n_experts * F, H) ||
+      !dense(w->down, w->n_experts * H, F))
+    return SetErr(err, errlen, "moe: expert tensors must be stacked [E*ff][H] / [E*H][ff] with qstride == cols"), -1;
+  if (shared && (!dense(w->shared_gate_proj, SF, H) || !dense(w->shared_up, SF, H) || !dense(w->shared_down, H, SF)))
+    return SetErr(err, errlen, "moe: shared expert tensors must be [sff][H] / [H][sff] with qstride == cols"), -1;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int halo_op_moe_views(const halo_moe_weights* w, uint32_t T, void* ws, halo_moe_views* v, char* err, size_t errlen) {
+  if (Check(w, T, err, errlen) != 0) return -1;
+  const std::uint32_t E = w->n_experts, k = w->n_used, H = w->hidden;
+  const std::uint32_t hstride = std::max(w->ff, w->shared_ff ? w->shared_ff : w->ff);
+  const std::uint32_t maxu = MaxU(w, T);
+  const std::uintptr_t base = reinterpret_cast<std::uintptr_t>(ws);
+  std::size_t o = 0;
+  auto take = [&](std::size_t bytes) {
+    const std::uintptr_t r = base + o;
+    o += Align(bytes);
+    return reinterpret_cast<char*>(r);
+  };
+  v->logits = reinterpret_cast<float*>(take(sizeof(float) * T * E));
+  v->shared_logit = reinterpret_cast<float*>(take(sizeof(float) * T));
+  v->xq = reinterpret_cast<int8_t*>(take(static_cast<std::size_t>(T) * H));
+  v->xs = reinterpret_cast<float*>(take(sizeof(float) * T * (H / 32)));
+  v->ids = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * T * k));
+  v->weights = reinterpret_cast<float*>(take(sizeof(float) * T * k));
+  v->route = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * 4));
+  v->expert = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * maxu));
+  v->pair_begin = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * (maxu + 1)));
+  v->pair_token = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * T * k));
+  v->pair_of = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * T * k));
+  v->hq = reinterpret_cast<int8_t*>(take(static_cast<std::size_t>(T) * (k + 1) * hstride));
+  v->hs = reinterpret_cast<float*>(take(sizeof(float) * T * (k + 1) * (hstride / 32)));
+  v->hstride = hstride;
+  v->max_u = maxu;
+  v->bytes = o;
+  return 0;
+}
+
+size_t halo_op_moe_workspace_bytes(const halo_moe_weights* w, uint32_t T) {
+  halo_moe_views v;
+  if (halo_op_moe_views(w, T, nullptr, &v, nullptr, 0) != 0) return 0;
+  return v.bytes;
+}
+
+int halo_op_moe_decode(halo_engine* eng, const halo_moe_weights* w, const float* x, float* out, uint32_t T, void* ws,
+                       size_t ws_bytes, char* err, size_t errlen) {
+  halo_moe_views v;
+  if (halo_op_moe_views(w, T, ws, &v, err, errlen) != 0) return -1;
+  if (ws == nullptr || ws_bytes < halo_op_moe_workspace_bytes(w, T))
+    return SetErr(err, errlen, "moe: workspace of %zu bytes < %zu", ws_bytes, halo_op_moe_workspace_bytes(w, T)), -1;
+  const std::uint32_t E = w->n_experts, k = w->n_used, H = w->hidden, F = w->ff;
+  const bool shared = w->shared_gate_proj.qs != nullptr;
+  const std::uint32_t SF = shared ? w->shared_ff : 0;
+  // 1. router logits + shared gate logit + x quantized
+  {
+    const std::uint32_t qblocks = CeilDiv(static_cast<std::uint64_t>(T) * (H / 32), 8);
+    const halo_arg a[] = {Ptr(w->router), Ptr(shared ? w->shared_gate : nullptr), Ptr(x), Ptr(v.logits),
+                          Ptr(v.shared_logit), Ptr(v.xq), Ptr(v.xs), U32(E), U32(H), U32(T)};
+    if (Launch(eng, "halo_moe_router", D3(E + 1 + qblocks), D3(256), a, err, errlen) != 0) return -1;
+  }
+  // 2. softmax / top-k / union of experts
+  {
+    const halo_arg a[] = {Ptr(v.logits), Ptr(v.ids), Ptr(v.weights), Ptr(v.route), Ptr(v.expert),
+                          Ptr(v.pair_begin), Ptr(v.pair_token), Ptr(v.pair_of), U32(T), U32(E), U32(k)};
+    if (Launch(eng, "halo_moe_route", D3(1), D3(1024), a, err, errlen) != 0) return -1;
+  }
+  // 3. grouped gate/up + SwiGLU + quantized h
+  {
+    const halo_arg a[] = {Ptr(w->gate.qs), Ptr(w->gate.d), Ptr(w->up.qs), Ptr(w->up.d),
+                          Ptr(shared ? w->shared_gate_proj.qs : nullptr), Ptr(shared ? w->shared_gate_proj.d : nullptr),
+                          Ptr(shared ? w->shared_up.qs : nullptr), Ptr(shared ? w->shared_up.d : nullptr),
+                          Ptr(v.xq), Ptr(v.xs), Ptr(v.route), Ptr(v.expert), Ptr(v.pair_begin), Ptr(v.pair_token),
+                          Ptr(v.hq), Ptr(v.hs), U32(T), U32(H), U32(F), U32(SF), U32(k), U32(v.max_u),
+                          U32(v.hstride)};
+    if (Launch(eng, "halo_moe_gate_up_q8", D3(v.max_u + 1, v.hstride / 32), D3(512), a, err, errlen) != 0) return -1;
+  }
+  // 4. down + routed combine + shared expert
+  {
+    const halo_arg a[] = {Ptr(w->down.qs), Ptr(w->down.d), Ptr(shared ? w->shared_down.qs : nullptr),
+                          Ptr(shared ? w->shared_down.d : nullptr), Ptr(v.hq), Ptr(v.hs), Ptr(v.ids),
+                          Ptr(v.weights), Ptr(v.pair_of), Ptr(v.shared_logit), Ptr(out), U32(T), U32(H), U32(F),
+                          U32(SF), U32(k), U32(v.hstride)};
+    if (Launch(eng, "halo_moe_down_q8", D3(CeilDiv(H, 8)), D3(256), a, err, errlen) != 0) return -1;
+  }
+  return 0;
+}
+
+}  // extern "C"

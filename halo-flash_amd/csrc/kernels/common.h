@@ -12,6 +12,8 @@ namespace halo {
 
 constexpr int kWave = 64;
 
+typedef int V4i __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ float F16(std::uint16_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }

@@ -1,2 +1,3 @@
 // The gfx950 code object: every kernel the device layer can look up by name.
 #include "q8.hip"
+#include "moe.hip"

@@ -84,7 +84,12 @@ extern "C" __global__ void __launch_bounds__(256)
   xq[static_cast<std::size_t>(b) * cols + blk * 32 + lane] = static_cast<std::int8_t>(qv);
   if (lane == 0) xs[static_cast<std::size_t>(b) * nblk + blk] = scale;
   if (!xq2) return;
-  const float r = v - static_cast<float>(qv) * scale;
+  // r = v - q * s with the product rounded first (no fused multiply-add), as the residual is defined.
+  float r;
+  {
+#pragma clang fp contract(off)
+    r = v - static_cast<float>(qv) * scale;
+  }
   const float rmax = halo::GroupMax<32>(fabsf(r));
   const float s2 = rmax / 127.0f;
   const int q2 = s2 > 0.0f ? static_cast<int>(rintf(r / s2)) : 0;
@@ -99,7 +104,7 @@ constexpr int kInFlight = 4;  // column steps whose loads are issued before thei
 
 // Rows r(k) = base + k * P + lane / LPR (P = 64 / LPR), columns [k0, k1) of NB activation columns. Returns the
 // per-row sums reduced over the LPR lanes (valid in every lane).
-template <int LPR, int R, int NB, bool kResid>
+template <int LPR, int R, int NB, bool kResid, bool kNT = false>
 __device__ __forceinline__ void Q8A8Rows(const std::int8_t* __restrict__ qs, const std::uint16_t* __restrict__ d,
                                          const std::int8_t* __restrict__ xq, const float* __restrict__ xs,
                                          const std::int8_t* __restrict__ xq2, const float* __restrict__ xs2,
@@ -138,7 +143,10 @@ __device__ __forceinline__ void Q8A8Rows(const std::int8_t* __restrict__ qs, con
       const std::uint32_t cc = ok ? c : k0 + (lane % LPR) * 16;
 #pragma unroll
       for (int k = 0; k < R; ++k) {
-        q[u][k] = *reinterpret_cast<const int4*>(rowp[k] + cc);
+        if constexpr (kNT)
+          q[u][k] = __builtin_bit_cast(int4, __builtin_nontemporal_load(reinterpret_cast<const halo::V4i*>(rowp[k] + cc)));
+        else
+          q[u][k] = *reinterpret_cast<const int4*>(rowp[k] + cc);
         s[u][k] = ok ? F16(dp[k][cc / 32]) : 0.0f;
       }
 #pragma unroll
@@ -244,7 +252,7 @@ HALO_GEMV_I8_REF_NB(8)
     const std::uint32_t base = (blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave) * kRowsPerWave;       \
     if (base >= rows) return;                                                                                    \
     float out[NB][R];                                                                                            \
-    Q8A8Rows<LPR, R, NB, false>(qs, d, xq, xs, nullptr, nullptr, base, rows, cols, qstride, 0, cols, out);     \
+    Q8A8Rows<LPR, R, NB, false, true>(qs, d, xq, xs, nullptr, nullptr, base, rows, cols, qstride, 0, cols, out); \
     StoreRows<LPR, R, NB, false>(y, ystride, base, rows, out);                                                  \
   }
 #define HALO_GEMV_Q8A8_R(LPR, NB) HALO_GEMV_Q8A8(LPR, 1, NB) HALO_GEMV_Q8A8(LPR, 2, NB) HALO_GEMV_Q8A8(LPR, 4, NB)
@@ -256,6 +264,17 @@ HALO_GEMV_Q8A8_NB(16)
 #undef HALO_GEMV_Q8A8_NB
 #undef HALO_GEMV_Q8A8_R
 #undef HALO_GEMV_Q8A8
+
+// Variant with non-temporal weight loads (streamed once; kept out of the caches' reuse sets).
+extern "C" __global__ void __launch_bounds__(256) halo_gemv_q8a8nt_l64_r1_b1(
+    const std::int8_t* qs, const std::uint16_t* d, const std::int8_t* xq, const float* xs, float* y,
+    std::uint32_t rows, std::uint32_t cols, std::uint32_t qstride, std::uint32_t ystride) {
+  const std::uint32_t base = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (base >= rows) return;
+  float out[1][1];
+  Q8A8Rows<64, 1, 1, false, true>(qs, d, xq, xs, nullptr, nullptr, base, rows, cols, qstride, 0, cols, out);
+  StoreRows<64, 1, 1, false>(y, ystride, base, rows, out);
+}
 
 // Exact integer half-block dots for parity checks: isum[r][c / 16] = sum of 16 int8 products, computed by the
 // same 16-byte loads and v_dot4 chain as the GEMV. Grid-stride over (row, 16-column piece).
@@ -374,4 +393,33 @@ extern "C" __global__ void __launch_bounds__(256)
   for (std::uint64_t i = blockIdx.x * static_cast<std::uint64_t>(blockDim.x) + threadIdx.x; i < n;
        i += static_cast<std::uint64_t>(gridDim.x) * blockDim.x)
     x[i] = sigma * halo::Normal(halo::Mix64(seed) ^ i);
+}
+
+// ---- bandwidth references ----------------------------------------------------------------------------------
+// Plain streaming read and copy of n 16-byte vectors, the yardsticks the GEMV is compared against (and the
+// calibration kernels for hardware byte counters). Each lane handles kPer vectors spaced a grid apart.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_stream_read(const int4* __restrict__ src, std::uint64_t n, int* __restrict__ sink) {
+  constexpr int kPer = 4;
+  const std::uint64_t stride = static_cast<std::uint64_t>(gridDim.x) * blockDim.x;
+  const std::uint64_t i0 = blockIdx.x * static_cast<std::uint64_t>(blockDim.x) + threadIdx.x;
+  int acc = 0;
+  for (std::uint64_t base = i0; base < n; base += kPer * stride) {
+    int4 v[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const std::uint64_t i = base + u * stride;
+      v[u] = i < n ? src[i] : make_int4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  if (acc == 0x7F3A5C11) sink[0] = acc;  // keeps the loads; practically never taken
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    halo_stream_copy(const int4* __restrict__ src, int4* __restrict__ dst, std::uint64_t n) {
+  const std::uint64_t stride = static_cast<std::uint64_t>(gridDim.x) * blockDim.x;
+  for (std::uint64_t i = blockIdx.x * static_cast<std::uint64_t>(blockDim.x) + threadIdx.x; i < n; i += stride)
+    dst[i] = src[i];
 }

@@ -53,6 +53,31 @@ class Q8Matrix(C.Structure):
     ]
 
 
+class MoeWeights(C.Structure):
+    _fields_ = [
+        ("router", C.c_void_p),
+        ("shared_gate", C.c_void_p),
+        ("gate", Q8Matrix),
+        ("up", Q8Matrix),
+        ("down", Q8Matrix),
+        ("shared_gate_proj", Q8Matrix),
+        ("shared_up", Q8Matrix),
+        ("shared_down", Q8Matrix),
+        ("n_experts", C.c_uint32),
+        ("n_used", C.c_uint32),
+        ("hidden", C.c_uint32),
+        ("ff", C.c_uint32),
+        ("shared_ff", C.c_uint32),
+        ("pad", C.c_uint32),
+    ]
+
+
+class MoeViews(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("logits", "shared_logit", "xq", "xs", "ids", "weights", "route", "expert",
+                                          "pair_begin", "pair_token", "pair_of", "hq", "hs")] + [
+        ("hstride", C.c_uint32), ("max_u", C.c_uint32), ("bytes", C.c_size_t)]
+
+
 ERRLEN = 1024
 _VP, _SZ, _U32, _U64, _F32, _I32 = C.c_void_p, C.c_size_t, C.c_uint32, C.c_uint64, C.c_float, C.c_int32
 _ERR = [C.c_char_p, _SZ]
@@ -95,6 +120,9 @@ _SIGS = {
     "halo_op_q8_half_dots": (C.c_int, [_VP, C.POINTER(Q8Matrix), _VP, _VP], True),
     "halo_op_synth_q8": (C.c_int, [_VP, _VP, _VP, _U32, _U32, _U32, _U64, _F32], True),
     "halo_op_synth_f32": (C.c_int, [_VP, _VP, _U64, _U64, _F32], True),
+    "halo_op_moe_workspace_bytes": (_SZ, [C.POINTER(MoeWeights), _U32], False),
+    "halo_op_moe_views": (C.c_int, [C.POINTER(MoeWeights), _U32, _VP, C.POINTER(MoeViews)], True),
+    "halo_op_moe_decode": (C.c_int, [_VP, C.POINTER(MoeWeights), _VP, _VP, _U32, _VP, _SZ], True),
 }
 
 _lib = None
@@ -171,6 +199,13 @@ class DeviceArray:
             raise HaloError(f"upload of {host.nbytes} bytes into {self.nbytes}")
         _call("halo_upload", self.dev.handle, C.byref(self.buf), 0, host.ctypes.data, host.nbytes)
         return self
+
+    def download_range(self, offset: int, count: int, dtype=None) -> np.ndarray:
+        """Download `count` elements of `dtype` (default: the array's) starting at byte `offset`."""
+        dt = np.dtype(dtype or self.dtype)
+        out = np.empty(count, dt)
+        _call("halo_download", self.dev.handle, C.byref(self.buf), offset, out.ctypes.data, out.nbytes)
+        return out
 
     def download(self) -> np.ndarray:
         out = np.empty(self.shape, self.dtype)
@@ -295,3 +330,52 @@ class Q8Weights:
 
     def host(self):
         return self.qs.download()[:, : self.cols], self.d.download()
+
+    def host_rows(self, r0: int, n: int):
+        """Rows [r0, r0 + n) as (qs, d) host arrays."""
+        q = self.qs.download_range(r0 * self.qstride, n * self.qstride).reshape(n, self.qstride)[:, : self.cols]
+        d = self.d.download_range(r0 * (self.cols // 32) * 2, n * (self.cols // 32)).reshape(n, self.cols // 32)
+        return q, d
+
+
+class MoeLayer:
+    """Seeded synthetic MoE layer on the device (BASELINE config C2 shapes by default)."""
+
+    def __init__(self, dev: Device, n_experts=512, n_used=10, hidden=2048, ff=512, shared_ff=512, seed=0,
+                 shared=True):
+        self.dev = dev
+        self.E, self.k, self.H, self.F, self.SF = n_experts, n_used, hidden, ff, shared_ff
+        self.router = dev.array((n_experts, hidden), np.float32)
+        dev.op("synth_f32", self.router.ptr, n_experts * hidden, seed + 1, 0.02)
+        self.gate = Q8Weights(dev, n_experts * ff, hidden).synth(dev, seed + 2)
+        self.up = Q8Weights(dev, n_experts * ff, hidden).synth(dev, seed + 3)
+        self.down = Q8Weights(dev, n_experts * hidden, ff).synth(dev, seed + 4)
+        w = MoeWeights()
+        w.router = self.router.ptr
+        w.gate, w.up, w.down = self.gate.desc, self.up.desc, self.down.desc
+        w.n_experts, w.n_used, w.hidden, w.ff = n_experts, n_used, hidden, ff
+        self.shared = shared
+        if shared:
+            self.sgate = dev.array(hidden, np.float32)
+            dev.op("synth_f32", self.sgate.ptr, hidden, seed + 5, 0.02)
+            self.sg = Q8Weights(dev, shared_ff, hidden).synth(dev, seed + 6)
+            self.su = Q8Weights(dev, shared_ff, hidden).synth(dev, seed + 7)
+            self.sd = Q8Weights(dev, hidden, shared_ff).synth(dev, seed + 8)
+            w.shared_gate = self.sgate.ptr
+            w.shared_gate_proj, w.shared_up, w.shared_down = self.sg.desc, self.su.desc, self.sd.desc
+            w.shared_ff = shared_ff
+        self.w = w
+
+    def workspace(self, tokens: int):
+        n = lib().halo_op_moe_workspace_bytes(C.byref(self.w), tokens)
+        if n == 0:
+            raise HaloError("moe: unsupported shape")
+        return self.dev.array(n, np.uint8)
+
+    def views(self, tokens: int, ws: DeviceArray) -> MoeViews:
+        v = MoeViews()
+        _call("halo_op_moe_views", C.byref(self.w), tokens, ws.ptr, C.byref(v))
+        return v
+
+    def forward(self, x: DeviceArray, out: DeviceArray, tokens: int, ws: DeviceArray):
+        self.dev.op("moe_decode", C.byref(self.w), x.ptr, out.ptr, tokens, ws.ptr, ws.nbytes)

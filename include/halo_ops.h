@@ -73,6 +73,49 @@ int halo_op_synth_q8(halo_engine* eng, int8_t* qs, uint16_t* d, uint32_t rows, u
                      uint64_t seed, float sigma, char* err, size_t errlen);
 int halo_op_synth_f32(halo_engine* eng, float* x, uint64_t n, uint64_t seed, float sigma, char* err, size_t errlen);
 
+/* ---- MoE decode layer ----------------------------------------------------------------------------------------
+ * ReferenceModel::Moe (src/model/reference.cpp:530-578) / FlashNextGpu::Moe (src/engine/flash_next_gpu.cpp:697-845)
+ * for T <= 16 tokens: router (fp32) -> softmax/top-k -> union of experts over tokens -> grouped gate/up + SwiGLU
+ * -> down with the routed combine in slot order + the shared expert scaled by sigmoid(shared gate logit).
+ * Expert tensors are stacked repacked Q8_0 with qstride == cols: gate/up rows = n_experts * ff (cols hidden),
+ * down rows = n_experts * hidden (cols ff). The shared expert is absent when shared_gate_proj.qs is NULL. */
+typedef struct halo_moe_weights {
+  const float* router;      /* [n_experts][hidden] */
+  const float* shared_gate; /* [hidden] scalar-gate row, or NULL */
+  halo_q8_matrix gate, up, down;
+  halo_q8_matrix shared_gate_proj, shared_up, shared_down;
+  uint32_t n_experts, n_used, hidden, ff, shared_ff;
+  uint32_t pad;
+} halo_moe_weights;
+
+/* Device workspace the layer needs for `tokens` tokens (routing tables, quantized activations, h). */
+size_t halo_op_moe_workspace_bytes(const halo_moe_weights* w, uint32_t tokens);
+
+/* out [T][hidden] = MoE(x [T][hidden]); 4 launches, no allocation, no host round trip (routing stays on the
+ * device). `ws` holds halo_op_moe_workspace_bytes; its layout is returned through halo_moe_views for
+ * inspection. */
+typedef struct halo_moe_views {
+  float* logits;          /* [T][n_experts] */
+  float* shared_logit;    /* [T] */
+  int8_t* xq;             /* [T][hidden] */
+  float* xs;              /* [T][hidden/32] */
+  uint32_t* ids;          /* [T][n_used] */
+  float* weights;         /* [T][n_used] */
+  uint32_t* route;        /* [1]: U, the number of distinct routed experts */
+  uint32_t* expert;       /* [max U] ascending expert ids */
+  uint32_t* pair_begin;   /* [max U + 1] */
+  uint32_t* pair_token;   /* [T * n_used] */
+  uint32_t* pair_of;      /* [T][n_used] */
+  int8_t* hq;             /* [T * (n_used + 1)][hstride] */
+  float* hs;              /* [T * (n_used + 1)][hstride / 32] */
+  uint32_t hstride, max_u;
+  size_t bytes;           /* workspace bytes the views span */
+} halo_moe_views;
+int halo_op_moe_views(const halo_moe_weights* w, uint32_t tokens, void* ws, halo_moe_views* out, char* err,
+                      size_t errlen);
+int halo_op_moe_decode(halo_engine* eng, const halo_moe_weights* w, const float* x, float* out, uint32_t tokens,
+                       void* ws, size_t ws_bytes, char* err, size_t errlen);
+
 #ifdef __cplusplus
 }
 #endif

@@ -59,6 +59,8 @@ def run_gpu(args):
             return run_c0(args, dev, H, res)
         if args.mode == "membw":
             return run_membw(args, dev, H, res)
+        if args.mode == "moe":
+            return run_moe(args, dev, H, res)
         # ---------------- C1 pass at M=1 (the bench value) and the M sweep ----------------
         per_copy = sum(q8_bytes(r, c) for r, c in C1_SHAPES)
         copies = max(2, -(-MIN_ROTATION_BYTES // per_copy))
@@ -135,6 +137,80 @@ def run_gpu(args):
         return run_c0(args, dev, H, res)
     finally:
         dev.close()
+
+
+def moe_bytes(E, H_, F, SF, U, T):
+    """Algorithmic bytes of one MoE decode call: router (fp32) + shared gate row + shared expert + U routed
+    experts (Q8_0, 34 bytes per 32 weights), fp32 activations in and out."""
+    q8 = lambda r, c: r * (c // 32) * 34
+    expert = 2 * q8(F, H_) + q8(H_, F)
+    shared = 2 * q8(SF, H_) + q8(H_, SF)
+    return E * H_ * 4 + H_ * 4 + shared + U * expert + 2 * T * H_ * 4
+
+
+def run_moe(args, dev, H, res):
+    """C2: one MoE layer decode at T tokens. The 512-expert pool (1.7 GB) is shared; router, shared gate and
+    shared expert are rotated over copies (> 256 MB), and each call routes a different x, so expert weights come
+    from HBM."""
+    import ctypes as C
+
+    base = H.MoeLayer(dev, seed=77)
+    ncopy = 40
+    copies = []
+    for i in range(ncopy):
+        r = dev.array((base.E, base.H), np.float32)
+        dev.op("synth_f32", r.ptr, base.E * base.H, 1000 + i, 0.02)
+        sgv = dev.array(base.H, np.float32)
+        dev.op("synth_f32", sgv.ptr, base.H, 2000 + i, 0.02)
+        sg = H.Q8Weights(dev, base.SF, base.H).synth(dev, 3000 + i)
+        su = H.Q8Weights(dev, base.SF, base.H).synth(dev, 4000 + i)
+        sd = H.Q8Weights(dev, base.H, base.SF).synth(dev, 5000 + i)
+        w = H.MoeWeights()
+        C.memmove(C.byref(w), C.byref(base.w), C.sizeof(w))
+        w.router, w.shared_gate = r.ptr, sgv.ptr
+        w.shared_gate_proj, w.shared_up, w.shared_down = sg.desc, su.desc, sd.desc
+        copies.append((w, [r, sgv, sg, su, sd]))
+    out = {}
+    for T in (1, 4, 16):
+        xs = [dev.array((T, base.H), np.float32) for _ in range(ncopy)]
+        for i, x in enumerate(xs):
+            dev.op("synth_f32", x.ptr, T * base.H, 9000 + 100 * T + i, 1.0)
+        y = dev.array((T, base.H), np.float32)
+        wsb = H.lib().halo_op_moe_workspace_bytes(C.byref(base.w), T)
+        wss = [dev.array(wsb, np.uint8) for _ in range(ncopy)]
+        dev.sync()
+        if args.eager:  # per-kernel durations under a profiler that cannot trace graph launches
+            for _ in range(5):
+                for (w, _), x, ws in zip(copies, xs, wss):
+                    dev.op("moe_decode", C.byref(w), x.ptr, y.ptr, T, ws.ptr, ws.nbytes)
+            dev.sync()
+            continue
+        dev.begin_capture()
+        for (w, _), x, ws in zip(copies, xs, wss):
+            dev.op("moe_decode", C.byref(w), x.ptr, y.ptr, T, ws.ptr, ws.nbytes)
+        g = dev.end_capture()
+        dev.launch_graph(g)
+        dev.sync()
+        nrep = max(1, 2000 // ncopy // max(1, T // 4))
+        dev.timer_start()
+        for _ in range(nrep):
+            dev.launch_graph(g)
+        ms = dev.timer_stop()
+        us = ms * 1e3 / (nrep * ncopy)
+        dev.free_graph(g)
+        Us = []
+        for (w, _), ws in zip(copies, wss):
+            v = H.MoeViews()
+            H._call("halo_op_moe_views", C.byref(w), T, ws.ptr, C.byref(v))
+            ids = ws.download_range(v.ids - ws.ptr, T * base.k, np.uint32)
+            Us.append(len(set(ids.tolist())))
+        nbytes = float(np.mean([moe_bytes(base.E, base.H, base.F, base.SF, u, T) for u in Us]))
+        out[f"T{T}"] = {"us_per_layer": round(us, 3), "mean_U": round(float(np.mean(Us)), 2),
+                        "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        log(f"[bench] moe T={T}: {out[f'T{T}']}")
+    res["moe"] = out
+    res["roofline"] = None
+    return res
 
 
 def run_membw(args, dev, H, res):
@@ -284,7 +360,8 @@ def main():
     p.add_argument("--sweep", action="store_true", help="also time alternative C0 GEMV tilings")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--mode", choices=["all", "c0", "membw"], default="all",
+    p.add_argument("--eager", action="store_true", help="launch without graphs (for profiling kernel durations)")
+    p.add_argument("--mode", choices=["all", "c0", "membw", "moe"], default="all",
                    help="c0: only the C0 GEMV loop (for profiling one kernel shape)")
     args = p.parse_args()
     if args.gpus != 1:
@@ -292,8 +369,8 @@ def main():
               "(the path is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
         sys.exit(2)
     res = run_gpu(args)
-    if args.mode in ("c0", "membw"):
-        print(json.dumps({k: res.get(k) for k in ("roofline", "c0_tilings", "membw")}), flush=True)
+    if args.mode in ("c0", "membw", "moe"):
+        print(json.dumps({k: res.get(k) for k in ("roofline", "c0_tilings", "membw", "moe")}), flush=True)
         return
     line = {
         "metric": "Q8_0 GEMV achieved HBM GB/s; decode tokens/s at 1 and 4 sessions",

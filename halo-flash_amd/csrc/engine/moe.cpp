@@ -1,5 +1,6 @@
 // MoE decode dispatch (FlashNextGpu::Moe, src/engine/flash_next_gpu.cpp:697-845, and the session-union path of
 // StepBatch, src/engine/batch_decode.cpp): four launches over device-resident routing, no host round trip.
+// Workspace: logits, shared logit, quantized x, ids/weights, quantized h (rows t*k+s routed, T*k+t shared).
 #include "engine.hpp"
 
 using namespace halo::engine;
@@ -10,16 +11,12 @@ constexpr std::uint32_t kMaxTokens = 16;
 
 std::size_t Align(std::size_t v) { return (v + 255) / 256 * 256; }
 
-std::uint32_t MaxU(const halo_moe_weights* w, std::uint32_t T) {
-  return std::min<std::uint32_t>(T * w->n_used, w->n_experts);
-}
-
 int Check(const halo_moe_weights* w, std::uint32_t T, char* err, std::size_t errlen) {
   if (w == nullptr || w->router == nullptr || w->gate.qs == nullptr || w->up.qs == nullptr || w->down.qs == nullptr)
     return SetErr(err, errlen, "moe: missing tensors"), -1;
   if (T == 0 || T > kMaxTokens) return SetErr(err, errlen, "moe decode takes 1..%u tokens, got %u", kMaxTokens, T), -1;
   const std::uint32_t H = w->hidden, F = w->ff, SF = w->shared_ff;
-  if (w->n_experts == 0 || w->n_experts > 1024 || w->n_used == 0 || w->n_used > 32 || w->n_used > w->n_experts)
+  if (w->n_experts == 0 || w->n_experts > 1024 || w->n_used == 0 || w->n_used > 15 || w->n_used > w->n_experts)
     return SetErr(err, errlen, "moe: %u experts / %u used unsupported", w->n_experts, w->n_used), -1;
   if (H % 1024 != 0 || H > 4096 || H % 32 != 0) return SetErr(err, errlen, "moe: hidden %u must be 1024..4096 step 1024", H), -1;
   if (F % 32 != 0 || F == 0 || F > 512) return SetErr(err, errlen, "moe: expert ff %u must be a multiple of 32, <= 512", F), -1;
@@ -45,7 +42,6 @@ int halo_op_moe_views(const halo_moe_weights* w, uint32_t T, void* ws, halo_moe_
   if (Check(w, T, err, errlen) != 0) return -1;
   const std::uint32_t E = w->n_experts, k = w->n_used, H = w->hidden;
   const std::uint32_t hstride = std::max(w->ff, w->shared_ff ? w->shared_ff : w->ff);
-  const std::uint32_t maxu = MaxU(w, T);
   const std::uintptr_t base = reinterpret_cast<std::uintptr_t>(ws);
   std::size_t o = 0;
   auto take = [&](std::size_t bytes) {
@@ -59,15 +55,9 @@ int halo_op_moe_views(const halo_moe_weights* w, uint32_t T, void* ws, halo_moe_
   v->xs = reinterpret_cast<float*>(take(sizeof(float) * T * (H / 32)));
   v->ids = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * T * k));
   v->weights = reinterpret_cast<float*>(take(sizeof(float) * T * k));
-  v->route = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * 4));
-  v->expert = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * maxu));
-  v->pair_begin = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * (maxu + 1)));
-  v->pair_token = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * T * k));
-  v->pair_of = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * T * k));
   v->hq = reinterpret_cast<int8_t*>(take(static_cast<std::size_t>(T) * (k + 1) * hstride));
   v->hs = reinterpret_cast<float*>(take(sizeof(float) * T * (k + 1) * (hstride / 32)));
   v->hstride = hstride;
-  v->max_u = maxu;
   v->bytes = o;
   return 0;
 }
@@ -82,8 +72,8 @@ int halo_op_moe_decode(halo_engine* eng, const halo_moe_weights* w, const float*
                        size_t ws_bytes, char* err, size_t errlen) {
   halo_moe_views v;
   if (halo_op_moe_views(w, T, ws, &v, err, errlen) != 0) return -1;
-  if (ws == nullptr || ws_bytes < halo_op_moe_workspace_bytes(w, T))
-    return SetErr(err, errlen, "moe: workspace of %zu bytes < %zu", ws_bytes, halo_op_moe_workspace_bytes(w, T)), -1;
+  if (ws == nullptr || ws_bytes < v.bytes)
+    return SetErr(err, errlen, "moe: workspace of %zu bytes < %zu", ws_bytes, v.bytes), -1;
   const std::uint32_t E = w->n_experts, k = w->n_used, H = w->hidden, F = w->ff;
   const bool shared = w->shared_gate_proj.qs != nullptr;
   const std::uint32_t SF = shared ? w->shared_ff : 0;
@@ -94,29 +84,28 @@ int halo_op_moe_decode(halo_engine* eng, const halo_moe_weights* w, const float*
                           Ptr(v.shared_logit), Ptr(v.xq), Ptr(v.xs), U32(E), U32(H), U32(T)};
     if (Launch(eng, "halo_moe_router", D3(E + 1 + qblocks), D3(256), a, err, errlen) != 0) return -1;
   }
-  // 2. softmax / top-k / union of experts
+  // 2. softmax / top-k, one block per token
   {
-    const halo_arg a[] = {Ptr(v.logits), Ptr(v.ids), Ptr(v.weights), Ptr(v.route), Ptr(v.expert),
-                          Ptr(v.pair_begin), Ptr(v.pair_token), Ptr(v.pair_of), U32(T), U32(E), U32(k)};
-    if (Launch(eng, "halo_moe_route", D3(1), D3(1024), a, err, errlen) != 0) return -1;
+    const halo_arg a[] = {Ptr(v.logits), Ptr(v.ids), Ptr(v.weights), U32(E), U32(k)};
+    if (Launch(eng, "halo_moe_topk", D3(T), D3(CeilDiv(E, 64) * 64), a, err, errlen) != 0) return -1;
   }
-  // 3. grouped gate/up + SwiGLU + quantized h
+  // 3. gate/up over the union of experts + SwiGLU + quantized h
   {
     const halo_arg a[] = {Ptr(w->gate.qs), Ptr(w->gate.d), Ptr(w->up.qs), Ptr(w->up.d),
                           Ptr(shared ? w->shared_gate_proj.qs : nullptr), Ptr(shared ? w->shared_gate_proj.d : nullptr),
                           Ptr(shared ? w->shared_up.qs : nullptr), Ptr(shared ? w->shared_up.d : nullptr),
-                          Ptr(v.xq), Ptr(v.xs), Ptr(v.route), Ptr(v.expert), Ptr(v.pair_begin), Ptr(v.pair_token),
-                          Ptr(v.hq), Ptr(v.hs), U32(T), U32(H), U32(F), U32(SF), U32(k), U32(v.max_u),
+                          Ptr(v.xq), Ptr(v.xs), Ptr(v.ids), Ptr(v.hq), Ptr(v.hs), U32(T), U32(F), U32(SF), U32(k),
                           U32(v.hstride)};
-    if (Launch(eng, "halo_moe_gate_up_q8", D3(v.max_u + 1, v.hstride / 32), D3(512), a, err, errlen) != 0) return -1;
+    const char* name = H == 1024 ? "halo_moe_gate_up_q8_s1" : H == 2048 ? "halo_moe_gate_up_q8_s2" : "halo_moe_gate_up_q8_s4";
+    if (H == 3072) return SetErr(err, errlen, "moe: hidden 3072 has no gate/up instance"), -1;
+    if (Launch(eng, name, D3(T * k + 1, v.hstride / 32), D3(512), a, err, errlen) != 0) return -1;
   }
   // 4. down + routed combine + shared expert
   {
     const halo_arg a[] = {Ptr(w->down.qs), Ptr(w->down.d), Ptr(shared ? w->shared_down.qs : nullptr),
-                          Ptr(shared ? w->shared_down.d : nullptr), Ptr(v.hq), Ptr(v.hs), Ptr(v.ids),
-                          Ptr(v.weights), Ptr(v.pair_of), Ptr(v.shared_logit), Ptr(out), U32(T), U32(H), U32(F),
-                          U32(SF), U32(k), U32(v.hstride)};
-    if (Launch(eng, "halo_moe_down_q8", D3(CeilDiv(H, 8)), D3(256), a, err, errlen) != 0) return -1;
+                          Ptr(shared ? w->shared_down.d : nullptr), Ptr(v.hq), Ptr(v.hs), Ptr(v.ids), Ptr(v.weights),
+                          Ptr(v.shared_logit), Ptr(out), U32(T), U32(H), U32(F), U32(SF), U32(k), U32(v.hstride)};
+    if (Launch(eng, "halo_moe_down_q8", D3(CeilDiv(H, 8), T), D3(64 * (k + 1)), a, err, errlen) != 0) return -1;
   }
   return 0;
 }

@@ -26,24 +26,64 @@ __device__ __forceinline__ std::uint16_t ToBf16Bits(float v) {
   return static_cast<std::uint16_t>((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 
-// Sum / max over groups of `kWidth` consecutive lanes (kWidth a power of two <= 64); every lane gets the result.
+// Cross-lane data movement within 16-lane rows uses DPP (a VALU operand modifier, a few cycles) instead of the
+// LDS permute unit; the four row results are combined with v_readlane. Control: quad_perm [1,0,3,2] = 0xB1,
+// quad_perm [2,3,0,1] = 0x4E, row_half_mirror = 0x141, row_mirror = 0x140.
+template <int kCtrl>
+__device__ __forceinline__ float Dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, false));
+}
+template <int kCtrl>
+__device__ __forceinline__ int DppI(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, kCtrl, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float ReadLane(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+// Sum / max over groups of `kWidth` consecutive lanes (kWidth in {16, 32, 64}); every lane of the group gets the
+// result. Each group must be entirely active (whole rows of 16 for widths 16 and 32 use only their own lanes).
 template <int kWidth = kWave>
 __device__ __forceinline__ float GroupSum(float v) {
-#pragma unroll
-  for (int o = kWidth / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
+  static_assert(kWidth == 16 || kWidth == 32 || kWidth == 64, "group width");
+  v += Dpp<0xB1>(v);
+  v += Dpp<0x4E>(v);
+  v += Dpp<0x141>(v);
+  v += Dpp<0x140>(v);
+  if constexpr (kWidth == 16) {
+    return v;
+  } else if constexpr (kWidth == 32) {
+    const float lo = ReadLane(v, 0) + ReadLane(v, 16), hi = ReadLane(v, 32) + ReadLane(v, 48);
+    return (threadIdx.x & 32) ? hi : lo;
+  } else {
+    return (ReadLane(v, 0) + ReadLane(v, 16)) + (ReadLane(v, 32) + ReadLane(v, 48));
+  }
 }
 template <int kWidth = kWave>
 __device__ __forceinline__ float GroupMax(float v) {
-#pragma unroll
-  for (int o = kWidth / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
+  static_assert(kWidth == 16 || kWidth == 32 || kWidth == 64, "group width");
+  v = fmaxf(v, Dpp<0xB1>(v));
+  v = fmaxf(v, Dpp<0x4E>(v));
+  v = fmaxf(v, Dpp<0x141>(v));
+  v = fmaxf(v, Dpp<0x140>(v));
+  if constexpr (kWidth == 16) {
+    return v;
+  } else if constexpr (kWidth == 32) {
+    const float lo = fmaxf(ReadLane(v, 0), ReadLane(v, 16)), hi = fmaxf(ReadLane(v, 32), ReadLane(v, 48));
+    return (threadIdx.x & 32) ? hi : lo;
+  } else {
+    return fmaxf(fmaxf(ReadLane(v, 0), ReadLane(v, 16)), fmaxf(ReadLane(v, 32), ReadLane(v, 48)));
+  }
 }
 template <int kWidth = kWave>
 __device__ __forceinline__ int GroupSumI(int v) {
-#pragma unroll
-  for (int o = kWidth / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
+  static_assert(kWidth == 64, "group width");
+  v += DppI<0xB1>(v);
+  v += DppI<0x4E>(v);
+  v += DppI<0x141>(v);
+  v += DppI<0x140>(v);
+  return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+         (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
 }
 
 // Block-wide reductions; `scratch` holds one float per wave. Every thread of the block must call them.

@@ -7,13 +7,12 @@
 //
 // Launches (all take device buffers only, so one captured graph replays for any routing):
 //   1. halo_moe_router     logits[t][e] = W_r[e] . x[t] (fp32), shared-gate logit, x quantized per 32 (int8).
-//   2. halo_moe_route      one wave per token: softmax, top-k (ties -> lower id), renormalized weights; then the
-//                          union U of experts over tokens (ascending id) with each expert's (token, slot) pairs.
-//   3. halo_moe_gate_up_q8 block (active expert u, 32 ff rows): gate and up rows streamed once for all of the
-//                          expert's pairs, h = SiLU(g) * u, quantized per 32 into hq[pair]. The shared expert is
-//                          the extra u = maxU, with pairs T*k + t.
-//   4. halo_moe_down_q8    a wave owns 2 output rows for every token: sum over slots in slot order of
-//                          w[t][s] * (W_d[e][r] . h[pair]), then + sigmoid(shared gate) * (W_sd[r] . h_shared).
+//   2. halo_moe_topk       one block per token: softmax, top-k (ties -> lower id), renormalized weights.
+//   3. halo_moe_gate_up_q8 block (routed pair, 32 ff rows): the first token that selected an expert computes it for
+//                          every token that selected it (the union of experts: weights streamed once), h =
+//                          SiLU(g) * u quantized per 32. One more block column is the shared expert.
+//   4. halo_moe_down_q8    block (8 output rows, token): one wave per slot streams 4 KB of its expert; the
+//                          slots are combined in slot order in LDS, then + sigmoid(shared gate) * shared.
 #include "common.h"
 
 using halo::Dot16;
@@ -77,13 +76,36 @@ extern "C" __global__ void __launch_bounds__(256)
 }
 
 namespace {
-// Softmax over E logits and top-k of the probabilities for one token, one wave. Returns (in lane 0's registers
-// and written to ids/weights) the k ids in descending probability, ties to the lower id, and the weights
-// renormalized by max(sum, 2^-14) (src/model/cpu_ops.cpp:187-207; sum accumulated in slot order).
+// Softmax over E logits and top-k of the probabilities for one token, one wave (src/model/cpu_ops.cpp:187-207):
+// the k ids in descending probability (ties to the lower id) and the weights renormalized by max(sum, 2^-14),
+// the sum accumulated in slot order. Selection: tau = the k-th largest of the 64 lane maxima bounds the k-th
+// largest probability from below, so the top k are among the candidates p >= tau (at most a few per selected
+// lane); each candidate's rank among the candidates, by (probability desc, id asc), is its slot. Results go to
+// lds_ids / lds_w (k entries) and, when non-null, to ids / weights in global memory.
 constexpr int kMaxPerLane = 16;  // E <= 1024
+constexpr int kCandMax = 256;
+
+struct TopKScratch {
+  float lanemax[kWave];
+  float cp[kCandMax];
+  std::uint32_t ci[kCandMax];
+  float tau;
+  float sum;
+};
+
+// Orders this wave's LDS accesses: everything before is visible to every lane after.
+__device__ __forceinline__ void WaveSync() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ std::uint32_t LanesBelow(std::uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<std::uint32_t>(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo(static_cast<std::uint32_t>(mask), 0u));
+}
 
 __device__ void WaveTopK(const float* logits, std::uint32_t E, std::uint32_t k, std::uint32_t* ids, float* weights,
-                         std::uint32_t* lds_ids) {
+                         std::uint32_t* lds_ids, float* lds_w, TopKScratch& sc) {
   const std::uint32_t lane = threadIdx.x % kWave;
   float p[kMaxPerLane];
   float mx = -INFINITY;
@@ -102,187 +124,321 @@ __device__ void WaveTopK(const float* logits, std::uint32_t E, std::uint32_t k, 
     den += p[i];
   }
   den = halo::GroupSum(den);
-  std::uint32_t taken = 0;
+  float lm = -1.0f;
 #pragma unroll
   for (int i = 0; i < kMaxPerLane; ++i) {
     const std::uint32_t e = lane + kWave * i;
     p[i] = e < E ? p[i] / den : -1.0f;
+    lm = fmaxf(lm, p[i]);
   }
-  float sum = 0.0f;
-  for (std::uint32_t s = 0; s < k; ++s) {
-    float v = -2.0f;
-    std::uint32_t at = 0xFFFFFFFFu;
+  // tau: the k-th largest lane maximum (every probability is >= 0, so tau = -1 admits all when k > 64)
+  sc.lanemax[lane] = lm;
+  if (lane == 0) sc.tau = -1.0f;
+  WaveSync();
+  std::uint32_t r = 0;
+  for (std::uint32_t j = 0; j < kWave; ++j) {
+    const float mj = sc.lanemax[j];
+    r += (mj > lm) || (mj == lm && j < lane);
+  }
+  WaveSync();
+  if (k <= kWave && r == k - 1) sc.tau = lm;
+  WaveSync();
+  const float tau = sc.tau;
+  // candidates p >= tau, compacted in (i, lane) order
+  std::uint32_t n = 0;
 #pragma unroll
-    for (int i = 0; i < kMaxPerLane; ++i)
-      if (!((taken >> i) & 1u) && p[i] > v) {  // ascending i: the first maximum has the lowest id in this lane
-        v = p[i];
-        at = lane + kWave * i;
+  for (int i = 0; i < kMaxPerLane; ++i) {
+    const std::uint32_t e = lane + kWave * i;
+    const bool f = e < E && p[i] >= tau;
+    const std::uint64_t m = __ballot(f);
+    const std::uint32_t pos = n + LanesBelow(m);
+    if (f && pos < kCandMax) {
+      sc.cp[pos] = p[i];
+      sc.ci[pos] = e;
+    }
+    n += static_cast<std::uint32_t>(__builtin_popcountll(m));
+  }
+  WaveSync();
+  if (n <= kCandMax) {
+    for (std::uint32_t c = lane; c < n; c += kWave) {
+      const float pc = sc.cp[c];
+      const std::uint32_t ic = sc.ci[c];
+      std::uint32_t rank = 0;
+      for (std::uint32_t j = 0; j < n; ++j) {
+        const float pj = sc.cp[j];
+        rank += (pj > pc) || (pj == pc && sc.ci[j] < ic);
       }
-#pragma unroll
-    for (int o = kWave / 2; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(v, o, kWave);
-      const std::uint32_t oi = __shfl_xor(at, o, kWave);
-      if (ov > v || (ov == v && oi < at)) {
-        v = ov;
-        at = oi;
+      if (rank < k) {
+        lds_ids[rank] = ic;
+        lds_w[rank] = pc;
       }
     }
-    if (at % kWave == lane) taken |= 1u << (at / kWave);
-    sum += v;  // every lane holds the same v: slot-order sum
-    if (lane == 0) {
-      ids[s] = at;
-      weights[s] = v;
-      lds_ids[s] = at;
+  } else {
+    // more candidates than the scratch holds (massive ties): repeated arg-max
+    std::uint32_t taken = 0;
+    for (std::uint32_t s = 0; s < k; ++s) {
+      float v = -2.0f;
+      std::uint32_t at = 0xFFFFFFFFu;
+#pragma unroll
+      for (int i = 0; i < kMaxPerLane; ++i)
+        if (!((taken >> i) & 1u) && p[i] > v) {
+          v = p[i];
+          at = lane + kWave * i;
+        }
+#pragma unroll
+      for (int o = kWave / 2; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(v, o, kWave);
+        const std::uint32_t oi = __shfl_xor(at, o, kWave);
+        if (ov > v || (ov == v && oi < at)) {
+          v = ov;
+          at = oi;
+        }
+      }
+      if (at % kWave == lane) taken |= 1u << (at / kWave);
+      if (lane == 0) {
+        lds_ids[s] = at;
+        lds_w[s] = v;
+      }
     }
   }
-  sum = fmaxf(sum, 6.103515625e-5f);
-  if (lane == 0)
-    for (std::uint32_t s = 0; s < k; ++s) weights[s] = weights[s] / sum;
+  WaveSync();
+  if (lane == 0) {
+    float sum = 0.0f;
+    for (std::uint32_t s = 0; s < k; ++s) sum += lds_w[s];
+    sc.sum = fmaxf(sum, 6.103515625e-5f);
+  }
+  WaveSync();
+  const float sum = sc.sum;
+  for (std::uint32_t s = lane; s < k; s += kWave) {
+    const float w = lds_w[s] / sum;
+    lds_w[s] = w;
+    if (ids != nullptr) {
+      ids[s] = lds_ids[s];
+      weights[s] = w;
+    }
+  }
+  WaveSync();
 }
 }  // namespace
 
-// One block of 1024 threads. logits [T][E] -> ids [T][k], weights [T][k]; the union of experts:
-//   route[0] = U, expert[u] (ascending id), pair_begin[u] (U + 1 entries; pairs of expert u are
-//   [pair_begin[u], pair_begin[u+1]) in ascending token order), pair_token[p], pair_of[t][s] = p.
+namespace {
+// Block-wide max / sum over blockDim.x threads (a multiple of 64, <= 1024); red holds 16 floats.
+__device__ __forceinline__ float BlockMax16(float v, float* red) {
+  v = halo::GroupMax(v);
+  const std::uint32_t wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
+  if (threadIdx.x % kWave == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+  for (std::uint32_t w = 1; w < waves; ++w) r = fmaxf(r, red[w]);
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ float BlockSum16(float v, float* red) {
+  v = halo::GroupSum(v);
+  const std::uint32_t wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
+  if (threadIdx.x % kWave == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+  for (std::uint32_t w = 1; w < waves; ++w) r += red[w];
+  __syncthreads();
+  return r;
+}
+}  // namespace
+
+// Routing of T tokens, one block per token, one thread per expert (blockDim.x = E rounded up to 64, <= 1024):
+// softmax over the E logits, top-k by probability (ties to the lower id), weights renormalized by max(sum, 2^-14)
+// with the sum in slot order (src/model/cpu_ops.cpp:187-207). Selection: groups of 8 consecutive experts; tau,
+// the k-th largest group maximum, bounds the k-th largest probability from below, so the top k are among the
+// candidates p >= tau; a candidate's rank among the candidates by (probability desc, id asc) is its slot.
+//   logits [T][E] -> ids [T][k], weights [T][k]
 extern "C" __global__ void __launch_bounds__(1024)
-    halo_moe_route(const float* __restrict__ logits, std::uint32_t* __restrict__ ids, float* __restrict__ weights,
-                   std::uint32_t* __restrict__ route, std::uint32_t* __restrict__ expert,
-                   std::uint32_t* __restrict__ pair_begin, std::uint32_t* __restrict__ pair_token,
-                   std::uint32_t* __restrict__ pair_of, std::uint32_t T, std::uint32_t E, std::uint32_t k) {
-  __shared__ std::uint32_t sel[kMoeMaxT * 32];
-  __shared__ std::uint32_t ubeg[1024];
-  __shared__ std::uint32_t wtot[2][16];
-  const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  if (wave < T)
-    WaveTopK(logits + static_cast<std::size_t>(wave) * E, E, k, ids + wave * k, weights + wave * k, sel + wave * k);
+    halo_moe_topk(const float* __restrict__ logits, std::uint32_t* __restrict__ ids, float* __restrict__ weights,
+                  std::uint32_t E, std::uint32_t k) {
+  constexpr int kCand = 256;
+  __shared__ float red[16];
+  __shared__ float gmax[128];
+  __shared__ float cp[kCand];
+  __shared__ std::uint32_t ci[kCand];
+  __shared__ float selp[32];
+  __shared__ std::uint32_t seli[32];
+  __shared__ float pall[1024];
+  __shared__ float tau_s;
+  __shared__ std::uint32_t ncand;
+  const std::uint32_t t = blockIdx.x, e = threadIdx.x;
+  const bool valid = e < E;
+  const float l = valid ? logits[static_cast<std::size_t>(t) * E + e] : -INFINITY;
+  if (e == 0) {
+    tau_s = -1.0f;
+    ncand = 0;
+  }
+  const float mx = BlockMax16(l, red);
+  const float ex = valid ? expf(l - mx) : 0.0f;
+  const float den = BlockSum16(ex, red);
+  const float p = valid ? ex / den : -1.0f;
+  pall[e] = p;
+  // group-of-8 maxima
+  float g = fmaxf(p, halo::Dpp<0xB1>(p));
+  g = fmaxf(g, halo::Dpp<0x4E>(g));
+  g = fmaxf(g, halo::Dpp<0x141>(g));
+  const std::uint32_t G = (E + 7) / 8;
+  if (e % 8 == 0 && e / 8 < G) gmax[e / 8] = g;
   __syncthreads();
-  // per expert: number of pairs; exclusive scans of (active, count) over experts
-  const std::uint32_t e = threadIdx.x;
-  std::uint32_t cnt = 0;
-  if (e < E)
-    for (std::uint32_t i = 0; i < T * k; ++i) cnt += sel[i] == e;
-  std::uint32_t a = cnt > 0, c = cnt;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {  // inclusive wave scan
-    const std::uint32_t ao = __shfl_up(a, o, kWave), co = __shfl_up(c, o, kWave);
-    if (lane >= static_cast<std::uint32_t>(o)) {
-      a += ao;
-      c += co;
+  if (k <= G && e < G) {
+    const float mine = gmax[e];
+    std::uint32_t r = 0;
+    for (std::uint32_t j = 0; j < G; ++j) {
+      const float gj = gmax[j];
+      r += (gj > mine) || (gj == mine && j < e);
+    }
+    if (r == k - 1) tau_s = mine;
+  }
+  __syncthreads();
+  const float tau = tau_s;
+  const bool cand = valid && p >= tau;
+  if (cand) {
+    const std::uint32_t pos = atomicAdd(&ncand, 1u);
+    if (pos < kCand) {
+      cp[pos] = p;
+      ci[pos] = e;
     }
   }
-  if (lane == kWave - 1) {
-    wtot[0][wave] = a;
-    wtot[1][wave] = c;
-  }
   __syncthreads();
-  std::uint32_t abase = 0, cbase = 0;
-  for (std::uint32_t w = 0; w < wave; ++w) {
-    abase += wtot[0][w];
-    cbase += wtot[1][w];
-  }
-  const std::uint32_t aex = abase + a - (cnt > 0), cex = cbase + c - cnt;
-  if (e < E) {
-    ubeg[e] = cex;
-    if (cnt > 0) {
-      expert[aex] = e;
-      pair_begin[aex] = cex;
+  const std::uint32_t n = ncand;
+  if (n <= kCand) {
+    if (cand) {
+      std::uint32_t r = 0;
+      for (std::uint32_t j = 0; j < n; ++j) {
+        const float pj = cp[j];
+        r += (pj > p) || (pj == p && ci[j] < e);
+      }
+      if (r < k) {
+        selp[r] = p;
+        seli[r] = e;
+      }
+    }
+  } else if (cand) {
+    // more candidates than the scratch holds (massive ties): rank against every expert
+    std::uint32_t r = 0;
+    for (std::uint32_t j = 0; j < E; ++j) {
+      const float pj = pall[j];
+      r += (pj > p) || (pj == p && j < e);
+    }
+    if (r < k) {
+      selp[r] = p;
+      seli[r] = e;
     }
   }
-  if (threadIdx.x == blockDim.x - 1) {
-    std::uint32_t U = 0;
-    for (std::uint32_t w = 0; w < blockDim.x / kWave; ++w) U += wtot[0][w];
-    route[0] = U;
-    pair_begin[U] = T * k;
+  __syncthreads();
+  if (e == 0) {
+    float sum = 0.0f;
+    for (std::uint32_t s = 0; s < k; ++s) sum += selp[s];
+    red[0] = fmaxf(sum, 6.103515625e-5f);
   }
   __syncthreads();
-  if (threadIdx.x < T * k) {
-    const std::uint32_t t = threadIdx.x / k, ex = sel[threadIdx.x];
-    std::uint32_t pos = 0;
-    for (std::uint32_t i = 0; i < t * k; ++i) pos += sel[i] == ex;  // earlier tokens routed to the same expert
-    const std::uint32_t p = ubeg[ex] + pos;
-    pair_token[p] = t;
-    pair_of[threadIdx.x] = p;
+  if (e < k) {
+    ids[static_cast<std::size_t>(t) * k + e] = seli[e];
+    weights[static_cast<std::size_t>(t) * k + e] = selp[e] / red[0];
   }
 }
 
 namespace {
 constexpr int kGuRowsPerWave = 4;  // 4 ff rows of gate and 4 of up
-constexpr int kGuMaxSteps = 4;     // H <= 4096 (1024 columns per step with 64 lanes x 16 bytes)
 }  // namespace
 
-// grid (maxU + 1, ceil(max(ff, sff) / 32)), block 512 (8 waves x 4 ff rows = 32). Gate/up [E][ff][H] repacked
-// Q8_0 (row stride qstride = H); shared gate/up [sff][H]. hq [T * (k + 1)][max ff] int8, hs [.][max ff / 32].
-extern "C" __global__ void __launch_bounds__(512) halo_moe_gate_up_q8(
+// grid (T * k + 1, ceil(max(ff, sff) / 32)), block 512 (8 waves x 4 ff rows = 32). Block x < T * k is routed
+// pair x (token x / k, slot x % k); the block of the first token that selected an expert computes that expert
+// for every token that selected it (weights streamed once), the others exit: the union of experts over tokens
+// without a separate bucketing pass. Block x = T * k is the shared expert for all tokens. kSteps = H / 1024.
+// Gate/up [E][ff][H] repacked Q8_0 (row stride H), shared gate/up [sff][H]. h = SiLU(gate) * up, quantized per 32:
+// hq [T * k + T][hstride] int8 (row t * k + s for routed pairs, T * k + t for the shared expert),
+// hs [.][hstride / 32].
+template <int kSteps>
+__device__ __forceinline__ void MoeGateUp(
     const std::int8_t* __restrict__ gq, const std::uint16_t* __restrict__ gd, const std::int8_t* __restrict__ uq,
     const std::uint16_t* __restrict__ ud, const std::int8_t* __restrict__ sgq, const std::uint16_t* __restrict__ sgd,
     const std::int8_t* __restrict__ suq, const std::uint16_t* __restrict__ sud, const std::int8_t* __restrict__ xq,
-    const float* __restrict__ xs, const std::uint32_t* __restrict__ route, const std::uint32_t* __restrict__ expert,
-    const std::uint32_t* __restrict__ pair_begin, const std::uint32_t* __restrict__ pair_token,
-    std::int8_t* __restrict__ hq, float* __restrict__ hs, std::uint32_t T, std::uint32_t H, std::uint32_t ff,
-    std::uint32_t sff, std::uint32_t k, std::uint32_t maxU, std::uint32_t hstride) {
-  const std::uint32_t ux = blockIdx.x, jb = blockIdx.y;
-  const bool shared = ux == maxU;
-  std::uint32_t pb, pe, f;
+    const float* __restrict__ xs, const std::uint32_t* __restrict__ ids, std::int8_t* __restrict__ hq,
+    float* __restrict__ hs, std::uint32_t T, std::uint32_t ff, std::uint32_t sff, std::uint32_t k,
+    std::uint32_t hstride) {
+  constexpr std::uint32_t H = kSteps * kWave * 16;
+  constexpr std::uint32_t nblk = H / 32;
+  const std::uint32_t px = blockIdx.x, jb = blockIdx.y;
+  const bool shared = px == T * k;
+  __shared__ std::uint32_t rows_s[kMoeMaxT];  // hq row of each pair, ascending token
+  __shared__ std::uint32_t tokmask;
+  __shared__ std::uint32_t owner;
+  __shared__ float hbuf[kMoeMaxT][32];
+  std::uint32_t np, f;
   const std::int8_t *q0, *q1;
   const std::uint16_t *d0, *d1;
-  const std::uint32_t nblk = H / 32;
   if (shared) {
-    if (sgq == nullptr) return;
-    pb = T * k;
-    pe = T * k + T;
+    if (sgq == nullptr || jb * 32 >= sff) return;
+    np = T;
     f = sff;
     q0 = sgq;
     d0 = sgd;
     q1 = suq;
     d1 = sud;
+    if (threadIdx.x < T) rows_s[threadIdx.x] = T * k + threadIdx.x;
   } else {
-    if (ux >= route[0]) return;
-    const std::size_t e = expert[ux];
-    pb = pair_begin[ux];
-    pe = pair_begin[ux + 1];
+    if (jb * 32 >= ff) return;
+    const std::uint32_t e = ids[px], t = px / k;
+    if (threadIdx.x == 0) {
+      tokmask = 0;
+      owner = 1;
+    }
+    __syncthreads();
+    for (std::uint32_t i = threadIdx.x; i < T * k; i += blockDim.x)
+      if (ids[i] == e) {
+        if (i / k < t) owner = 0;
+        atomicOr(&tokmask, 1u << (i / k));
+      }
+    __syncthreads();
+    if (!owner) return;
+    const std::uint32_t m = tokmask;
+    np = static_cast<std::uint32_t>(__builtin_popcount(m));
+    for (std::uint32_t i = threadIdx.x; i < T * k; i += blockDim.x)
+      if (ids[i] == e) rows_s[__builtin_popcount(m & ((1u << (i / k)) - 1u))] = i;
     f = ff;
-    q0 = gq + e * ff * H;
-    d0 = gd + e * ff * nblk;
-    q1 = uq + e * ff * H;
-    d1 = ud + e * ff * nblk;
+    q0 = gq + static_cast<std::size_t>(e) * ff * H;
+    d0 = gd + static_cast<std::size_t>(e) * ff * nblk;
+    q1 = uq + static_cast<std::size_t>(e) * ff * H;
+    d1 = ud + static_cast<std::size_t>(e) * ff * nblk;
   }
-  if (jb * 32 >= f) return;
-  __shared__ float hbuf[kMoeMaxT][32];
   const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const std::uint32_t j0 = jb * 32 + wave * kGuRowsPerWave;
-  const std::uint32_t steps = H / (kWave * 16);
   // weights: rows j0..j0+3 of gate (r < 4) and up (r >= 4), all column steps, loaded once
-  int4 w[2 * kGuRowsPerWave][kGuMaxSteps];
-  float sw[2 * kGuRowsPerWave][kGuMaxSteps];
+  int4 w[2 * kGuRowsPerWave][kSteps];
+  float sw[2 * kGuRowsPerWave][kSteps];
 #pragma unroll
   for (int r = 0; r < 2 * kGuRowsPerWave; ++r) {
     const std::int8_t* base = (r < kGuRowsPerWave ? q0 : q1) + static_cast<std::size_t>(j0 + r % kGuRowsPerWave) * H;
     const std::uint16_t* dbase =
         (r < kGuRowsPerWave ? d0 : d1) + static_cast<std::size_t>(j0 + r % kGuRowsPerWave) * nblk;
 #pragma unroll
-    for (int st = 0; st < kGuMaxSteps; ++st)
-      if (st < static_cast<int>(steps)) {
-        const std::uint32_t c = st * kWave * 16 + lane * 16;
-        w[r][st] = __builtin_bit_cast(int4, __builtin_nontemporal_load(reinterpret_cast<const halo::V4i*>(base + c)));
-        sw[r][st] = F16(dbase[c / 32]);
-      }
+    for (int st = 0; st < kSteps; ++st) {
+      const std::uint32_t c = st * kWave * 16 + lane * 16;
+      w[r][st] = __builtin_bit_cast(int4, __builtin_nontemporal_load(reinterpret_cast<const halo::V4i*>(base + c)));
+      sw[r][st] = F16(dbase[c / 32]);
+    }
   }
-  for (std::uint32_t p = pb; p < pe; ++p) {
-    const std::uint32_t t = shared ? p - T * k : pair_token[p];
-    const std::int8_t* xt = xq + static_cast<std::size_t>(t) * H;
-    const float* st_ = xs + static_cast<std::size_t>(t) * nblk;
+  __syncthreads();  // rows_s
+  for (std::uint32_t lp = 0; lp < np; ++lp) {
+    const std::uint32_t row = rows_s[lp];
+    const std::uint32_t tok = shared ? row - T * k : row / k;
+    const std::int8_t* xt = xq + static_cast<std::size_t>(tok) * H;
+    const float* st_ = xs + static_cast<std::size_t>(tok) * nblk;
     float acc[2 * kGuRowsPerWave];
 #pragma unroll
     for (int r = 0; r < 2 * kGuRowsPerWave; ++r) acc[r] = 0.0f;
 #pragma unroll
-    for (int st = 0; st < kGuMaxSteps; ++st)
-      if (st < static_cast<int>(steps)) {
-        const std::uint32_t c = st * kWave * 16 + lane * 16;
-        const int4 xv = *reinterpret_cast<const int4*>(xt + c);
-        const float sx = st_[c / 32];
+    for (int st = 0; st < kSteps; ++st) {
+      const std::uint32_t c = st * kWave * 16 + lane * 16;
+      const int4 xv = *reinterpret_cast<const int4*>(xt + c);
+      const float sx = st_[c / 32];
 #pragma unroll
-        for (int r = 0; r < 2 * kGuRowsPerWave; ++r) acc[r] += sw[r][st] * (sx * static_cast<float>(Dot16(w[r][st], xv)));
-      }
+      for (int r = 0; r < 2 * kGuRowsPerWave; ++r) acc[r] += sw[r][st] * (sx * static_cast<float>(Dot16(w[r][st], xv)));
+    }
 #pragma unroll
     for (int r = 0; r < 2 * kGuRowsPerWave; ++r) acc[r] = halo::GroupSum(acc[r]);
     if (lane < kGuRowsPerWave) {
@@ -293,74 +449,88 @@ extern "C" __global__ void __launch_bounds__(512) halo_moe_gate_up_q8(
           g = acc[r];
           u = acc[kGuRowsPerWave + r];
         }
-      hbuf[p - pb][wave * kGuRowsPerWave + lane] = halo::Silu(g) * u;
+      hbuf[lp][wave * kGuRowsPerWave + lane] = halo::Silu(g) * u;
     }
   }
   __syncthreads();
   // quantize h per 32 values: one half wave per pair
   const std::uint32_t hw = threadIdx.x / 32, hl = threadIdx.x % 32;
-  for (std::uint32_t lp = hw; lp < pe - pb; lp += blockDim.x / 32) {
+  for (std::uint32_t lp = hw; lp < np; lp += blockDim.x / 32) {
     const float v = hbuf[lp][hl];
     const float amax = halo::GroupMax<32>(fabsf(v));
     const float scale = amax / 127.0f;
     const int q = scale > 0.0f ? static_cast<int>(rintf(v / scale)) : 0;
-    const std::uint32_t p = pb + lp;
-    hq[static_cast<std::size_t>(p) * hstride + jb * 32 + hl] = static_cast<std::int8_t>(q);
-    if (hl == 0) hs[static_cast<std::size_t>(p) * (hstride / 32) + jb] = scale;
+    const std::uint32_t row = rows_s[lp];
+    hq[static_cast<std::size_t>(row) * hstride + jb * 32 + hl] = static_cast<std::int8_t>(q);
+    if (hl == 0) hs[static_cast<std::size_t>(row) * (hstride / 32) + jb] = scale;
   }
 }
 
-// grid ceil(H / 8), block 256 (4 waves x 2 rows; a row is 32 lanes x 16 bytes, ff <= 512 per step). Down
-// [E][H][ff] repacked (qstride ff), shared down [H][sff]. out [T][H].
-extern "C" __global__ void __launch_bounds__(256) halo_moe_down_q8(
+#define HALO_MOE_GATE_UP(S)                                                                                        \
+  extern "C" __global__ void __launch_bounds__(512) halo_moe_gate_up_q8_s##S(                                     \
+      const std::int8_t* gq, const std::uint16_t* gd, const std::int8_t* uq, const std::uint16_t* ud,             \
+      const std::int8_t* sgq, const std::uint16_t* sgd, const std::int8_t* suq, const std::uint16_t* sud,         \
+      const std::int8_t* xq, const float* xs, const std::uint32_t* ids, std::int8_t* hq, float* hs,               \
+      std::uint32_t T, std::uint32_t ff, std::uint32_t sff, std::uint32_t k, std::uint32_t hstride) {             \
+    MoeGateUp<S>(gq, gd, uq, ud, sgq, sgd, suq, sud, xq, xs, ids, hq, hs, T, ff, sff, k, hstride);                 \
+  }
+HALO_MOE_GATE_UP(1)
+HALO_MOE_GATE_UP(2)
+HALO_MOE_GATE_UP(4)
+#undef HALO_MOE_GATE_UP
+
+namespace {
+constexpr int kDownRows = 8;  // output rows per block: 4 passes x 2 rows (a row is 32 lanes x 16 bytes)
+}
+
+// grid (ceil(H / 8), T), block 64 * (k + 1) (<= 1024): wave s < k streams 8 rows of expert ids[t][s]'s down matrix
+// (4 KB contiguous), wave k the shared expert's; the block combines in slot order through LDS:
+//   out[t][r] = sum over s < k, in order, of weights[t][s] * (W_d[ids[t][s]][r] . h[t * k + s]),
+//               then + sigmoid(sgl[t]) * (W_sd[r] . h[T * k + t]).
+// Down [E][H][ff] repacked (row stride ff), shared down [H][sff]; ff, sff <= 512.
+extern "C" __global__ void __launch_bounds__(1024) halo_moe_down_q8(
     const std::int8_t* __restrict__ dq, const std::uint16_t* __restrict__ dd, const std::int8_t* __restrict__ sdq,
     const std::uint16_t* __restrict__ sdd, const std::int8_t* __restrict__ hq, const float* __restrict__ hs,
-    const std::uint32_t* __restrict__ ids, const float* __restrict__ weights, const std::uint32_t* __restrict__ pair_of,
-    const float* __restrict__ sgl, float* __restrict__ out, std::uint32_t T, std::uint32_t H, std::uint32_t ff,
-    std::uint32_t sff, std::uint32_t k, std::uint32_t hstride) {
-  constexpr int LPR = 32;
-  const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, sub = lane / LPR, l = lane % LPR;
-  const std::uint32_t r = (blockIdx.x * (blockDim.x / kWave) + wave) * 2 + sub;
-  const bool live = r < H;
-  const std::uint32_t rr = live ? r : H - 1;
-  for (std::uint32_t t = 0; t < T; ++t) {
-    float acc = 0.0f;
-    for (std::uint32_t s0 = 0; s0 <= k; s0 += 4) {
-      // up to 4 slots' loads in flight; slot k is the shared expert
-      float part[4];
+    const std::uint32_t* __restrict__ ids, const float* __restrict__ weights, const float* __restrict__ sgl,
+    float* __restrict__ out, std::uint32_t T, std::uint32_t H, std::uint32_t ff, std::uint32_t sff, std::uint32_t k,
+    std::uint32_t hstride) {
+  __shared__ float part[33][kDownRows];
+  const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, sub = lane / 32, l = lane % 32;
+  const std::uint32_t t = blockIdx.y, r0 = blockIdx.x * kDownRows;
+  const bool shared = wave == k;
+  if (wave < k || (shared && sdq != nullptr)) {
+    const std::uint32_t f = shared ? sff : ff;
+    const std::size_t e = shared ? 0 : ids[t * k + wave];
+    const std::uint32_t hrow = shared ? T * k + t : t * k + wave;
+    const std::int8_t* base = shared ? sdq : dq + e * H * f;
+    const std::uint16_t* dbase = shared ? sdd : dd + e * H * (f / 32);
+    const std::uint32_t c = l * 16;
+    const bool in = c < f;
+    int4 q[kDownRows / 2];
+    float sw[kDownRows / 2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const std::uint32_t s = s0 + i;
-        part[i] = 0.0f;
-        if (s > k) continue;
-        const bool sh = s == k;
-        if (sh && sdq == nullptr) continue;
-        const std::uint32_t f = sh ? sff : ff;
-        const std::size_t e = sh ? 0 : ids[t * k + s];
-        const std::uint32_t p = sh ? T * k + t : pair_of[t * k + s];
-        const std::int8_t* row = (sh ? sdq : dq + e * H * f) + static_cast<std::size_t>(rr) * f;
-        const std::uint16_t* drow = (sh ? sdd : dd + e * H * (f / 32)) + static_cast<std::size_t>(rr) * (f / 32);
-        float a = 0.0f;
-        for (std::uint32_t c = l * 16; c < f; c += LPR * 16) {
-          const int4 q = __builtin_bit_cast(int4, __builtin_nontemporal_load(reinterpret_cast<const halo::V4i*>(row + c)));
-          const int4 hv = *reinterpret_cast<const int4*>(hq + static_cast<std::size_t>(p) * hstride + c);
-          a += F16(drow[c / 32]) * (hs[static_cast<std::size_t>(p) * (hstride / 32) + c / 32] *
-                                    static_cast<float>(Dot16(q, hv)));
-        }
-        part[i] = a;
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const std::uint32_t s = s0 + i;
-        if (s > k) break;
-        const float v = halo::GroupSum<LPR>(part[i]);
-        if (s < k)
-          acc += weights[t * k + s] * v;
-        else if (sdq != nullptr)
-          acc += halo::Sigmoid(sgl[t]) * v;
-      }
+    for (int p = 0; p < kDownRows / 2; ++p) {
+      const std::uint32_t r = min(r0 + 2 * p + sub, H - 1);
+      q[p] = in ? __builtin_bit_cast(int4, __builtin_nontemporal_load(
+                                              reinterpret_cast<const halo::V4i*>(base + static_cast<std::size_t>(r) * f + c)))
+                : make_int4(0, 0, 0, 0);
+      sw[p] = in ? F16(dbase[static_cast<std::size_t>(r) * (f / 32) + c / 32]) : 0.0f;
     }
-    if (live && l == 0) out[static_cast<std::size_t>(t) * H + r] = acc;
+    const int4 hv = in ? *reinterpret_cast<const int4*>(hq + static_cast<std::size_t>(hrow) * hstride + c)
+                       : make_int4(0, 0, 0, 0);
+    const float sh = in ? hs[static_cast<std::size_t>(hrow) * (hstride / 32) + c / 32] : 0.0f;
+#pragma unroll
+    for (int p = 0; p < kDownRows / 2; ++p) {
+      const float v = halo::GroupSum<32>(sw[p] * (sh * static_cast<float>(Dot16(q[p], hv))));
+      if (l == 0) part[wave][2 * p + sub] = v;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < kDownRows && r0 + threadIdx.x < H) {
+    float acc = 0.0f;
+    for (std::uint32_t s = 0; s < k; ++s) acc += weights[t * k + s] * part[s][threadIdx.x];
+    if (sdq != nullptr) acc += halo::Sigmoid(sgl[t]) * part[k][threadIdx.x];
+    out[static_cast<std::size_t>(t) * H + r0 + threadIdx.x] = acc;
   }
 }
 
@@ -369,11 +539,15 @@ extern "C" __global__ void __launch_bounds__(256) halo_moe_down_q8(
 extern "C" __global__ void __launch_bounds__(64)
     halo_router_topk(const float* logits, std::uint32_t* ids, float* weights, std::uint32_t n, std::uint32_t k) {
   __shared__ std::uint32_t scratch[64];
-  WaveTopK(logits, n, k, ids, weights, scratch);
+  __shared__ float wscratch[64];
+  __shared__ TopKScratch sc;
+  WaveTopK(logits, n, k, ids, weights, scratch, wscratch, sc);
 }
 extern "C" __global__ void __launch_bounds__(64)
     halo_router_topk_rows(const float* logits, std::uint32_t* ids, float* weights, std::uint32_t n, std::uint32_t k) {
   __shared__ std::uint32_t scratch[64];
+  __shared__ float wscratch[64];
+  __shared__ TopKScratch sc;
   const std::size_t t = blockIdx.x;
-  WaveTopK(logits + t * n, n, k, ids + t * k, weights + t * k, scratch);
+  WaveTopK(logits + t * n, n, k, ids + t * k, weights + t * k, scratch, wscratch, sc);
 }

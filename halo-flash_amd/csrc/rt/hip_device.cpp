@@ -21,6 +21,8 @@ struct halo_device {
   std::vector<hipFunction_t> functions;
   std::vector<std::string> names;
   bool capturing = false;
+  std::size_t captured = 0;          // launches recorded since BeginCapture
+  std::vector<void*> deferred_free;  // Free() calls made while capturing, released at EndCapture
   hipEvent_t t0 = nullptr, t1 = nullptr;
 };
 
@@ -103,9 +105,12 @@ int halo_alloc(halo_device* dev, size_t bytes, halo_buffer* out, char* err, size
 }
 
 void halo_free(halo_device* dev, halo_buffer* buf) {
-  (void)dev;
   if (buf == nullptr || buf->device == nullptr) return;
-  (void)hipFree(buf->device);
+  // hipFree is not capturable (it would invalidate the capture): a free requested mid-capture is deferred.
+  if (dev != nullptr && dev->capturing)
+    dev->deferred_free.push_back(buf->device);
+  else
+    (void)hipFree(buf->device);
   *buf = halo_buffer{};
 }
 
@@ -207,13 +212,22 @@ int halo_launch(halo_device* dev, halo_kernel_id kernel, halo_dim3 grid, halo_di
     }
     params[i] = &storage[i];
   }
+  if (dev->capturing) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(dev->stream, &st) == hipSuccess && st != hipStreamCaptureStatusActive)
+      return SetErr(err, errlen, "capture is no longer active (status %d) before launch %zu (%s)", static_cast<int>(st),
+                    dev->captured, dev->names[kernel].c_str()),
+             -1;
+  }
   if (!Ok(hipModuleLaunchKernel(dev->functions[kernel], grid.x, grid.y, grid.z, block.x, block.y, block.z, 0,
                                 dev->stream, params, nullptr),
           "hipModuleLaunchKernel", err, errlen)) {
     std::string m = err ? std::string(err) : std::string();
-    SetErr(err, errlen, "%s (launching %s)", m.c_str(), dev->names[kernel].c_str());
+    SetErr(err, errlen, "%s (launching %s, launch %zu of the capture)", m.c_str(), dev->names[kernel].c_str(),
+           dev->captured);
     return -1;
   }
+  if (dev->capturing) ++dev->captured;
   return 0;
 }
 
@@ -224,6 +238,10 @@ int halo_synchronize(halo_device* dev, char* err, size_t errlen) {
 
 int halo_begin_capture(halo_device* dev, char* err, size_t errlen) {
   if (dev->capturing) return SetErr(err, errlen, "already capturing"), -1;
+  // Drain all device work first (allocations and copies the runtime may still be completing on other queues), so
+  // that nothing outside the capturing stream is pending when capture starts.
+  if (!Ok(hipDeviceSynchronize(), "hipDeviceSynchronize", err, errlen)) return -1;
+  dev->captured = 0;
   if (!Ok(hipStreamBeginCapture(dev->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture", err, errlen))
     return -1;
   dev->capturing = true;
@@ -234,7 +252,10 @@ int halo_end_capture(halo_device* dev, halo_graph* out, char* err, size_t errlen
   if (!dev->capturing) return SetErr(err, errlen, "not capturing"), -1;
   dev->capturing = false;
   hipGraph_t g = nullptr;
-  if (!Ok(hipStreamEndCapture(dev->stream, &g), "hipStreamEndCapture", err, errlen)) return -1;
+  const hipError_t end = hipStreamEndCapture(dev->stream, &g);
+  for (void* p : dev->deferred_free) (void)hipFree(p);
+  dev->deferred_free.clear();
+  if (!Ok(end, "hipStreamEndCapture", err, errlen)) return -1;
   hipGraphExec_t exec = nullptr;
   const bool ok = Ok(hipGraphInstantiate(&exec, g, nullptr, nullptr, 0), "hipGraphInstantiate", err, errlen);
   (void)hipGraphDestroy(g);

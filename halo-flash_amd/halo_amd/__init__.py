@@ -73,9 +73,8 @@ class MoeWeights(C.Structure):
 
 
 class MoeViews(C.Structure):
-    _fields_ = [(n, C.c_void_p) for n in ("logits", "shared_logit", "xq", "xs", "ids", "weights", "route", "expert",
-                                          "pair_begin", "pair_token", "pair_of", "hq", "hs")] + [
-        ("hstride", C.c_uint32), ("max_u", C.c_uint32), ("bytes", C.c_size_t)]
+    _fields_ = [(n, C.c_void_p) for n in ("logits", "shared_logit", "xq", "xs", "ids", "weights", "hq", "hs")] + [
+        ("hstride", C.c_uint32), ("pad", C.c_uint32), ("bytes", C.c_size_t)]
 
 
 ERRLEN = 1024

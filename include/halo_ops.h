@@ -91,24 +91,20 @@ typedef struct halo_moe_weights {
 /* Device workspace the layer needs for `tokens` tokens (routing tables, quantized activations, h). */
 size_t halo_op_moe_workspace_bytes(const halo_moe_weights* w, uint32_t tokens);
 
-/* out [T][hidden] = MoE(x [T][hidden]); 4 launches, no allocation, no host round trip (routing stays on the
- * device). `ws` holds halo_op_moe_workspace_bytes; its layout is returned through halo_moe_views for
+/* out [T][hidden] = MoE(x [T][hidden]); 4 launches (router, top-k, gate/up over the union of experts, down +
+ * combine), no allocation, no host round trip (routing stays on the device). `ws` holds halo_op_moe_workspace_bytes; its layout is returned through halo_moe_views for
  * inspection. */
 typedef struct halo_moe_views {
   float* logits;          /* [T][n_experts] */
   float* shared_logit;    /* [T] */
   int8_t* xq;             /* [T][hidden] */
   float* xs;              /* [T][hidden/32] */
-  uint32_t* ids;          /* [T][n_used] */
-  float* weights;         /* [T][n_used] */
-  uint32_t* route;        /* [1]: U, the number of distinct routed experts */
-  uint32_t* expert;       /* [max U] ascending expert ids */
-  uint32_t* pair_begin;   /* [max U + 1] */
-  uint32_t* pair_token;   /* [T * n_used] */
-  uint32_t* pair_of;      /* [T][n_used] */
-  int8_t* hq;             /* [T * (n_used + 1)][hstride] */
-  float* hs;              /* [T * (n_used + 1)][hstride / 32] */
-  uint32_t hstride, max_u;
+  uint32_t* ids;          /* [T][n_used], descending probability */
+  float* weights;         /* [T][n_used], renormalized */
+  int8_t* hq;             /* [T * n_used + T][hstride]: row t*n_used+s routed, T*n_used+t shared */
+  float* hs;              /* [T * n_used + T][hstride / 32] */
+  uint32_t hstride;
+  uint32_t pad;
   size_t bytes;           /* workspace bytes the views span */
 } halo_moe_views;
 int halo_op_moe_views(const halo_moe_weights* w, uint32_t tokens, void* ws, halo_moe_views* out, char* err,

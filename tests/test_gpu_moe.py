@@ -4,7 +4,8 @@ Checks, per token count T in {1, 4, 16}:
   * router logits within 1e-5 * sum|w x| of a float64 product;
   * top-k ids and renormalized weights equal to the oracle's RouteTopK applied to the GPU logits (bitwise ids,
     weights to 1e-6), and to the oracle's route of its own float64 logits except at measured near-ties;
-  * the union tables (U distinct experts ascending, each expert's pairs in token order, pair_of consistent);
+  * every routed pair's h written (the union of experts is computed inside the gate/up launch: only the first
+    token selecting an expert computes it, for all its tokens);
   * quantized activations bit-exact; h codes equal to the oracle's composition (SwiGLU of the exact-integer
     gate/up GEMVs, quantized per 32) except at rounding-boundary flips of +-1;
   * the layer output within 1e-5 * magnitude of the oracle composition fed the GPU's h codes, and within BASELINE's
@@ -52,11 +53,7 @@ def test_moe_decode_matches_oracle(dev, layer, T):
     sgl = _view(ws, base, v.shared_logit, T, np.float32)
     ids = _view(ws, base, v.ids, T * k, np.uint32).reshape(T, k)
     wts = _view(ws, base, v.weights, T * k, np.float32).reshape(T, k)
-    U = int(_view(ws, base, v.route, 1, np.uint32)[0])
-    expert = _view(ws, base, v.expert, U, np.uint32)
-    pbeg = _view(ws, base, v.pair_begin, U + 1, np.uint32)
-    ptok = _view(ws, base, v.pair_token, T * k, np.uint32)
-    pof = _view(ws, base, v.pair_of, T * k, np.uint32).reshape(T, k)
+    pof = np.arange(T * k, dtype=np.uint32).reshape(T, k)  # h row of (t, s) is t * k + s
     gxq = _view(ws, base, v.xq, T * L.H, np.int8).reshape(T, L.H)
     gxs = _view(ws, base, v.xs, T * L.H // 32, np.float32).reshape(T, -1)
     hstride = v.hstride
@@ -84,17 +81,6 @@ def test_moe_decode_matches_oracle(dev, layer, T):
         if fi.tolist() != oi.tolist():
             srt = np.sort(want_logits[t])[::-1]
             assert np.min(np.abs(np.diff(srt[: k + 1]))) < 1e-5, "routing differs away from a tie"
-
-    # union tables
-    uniq = sorted(set(ids.reshape(-1).tolist()))
-    assert U == len(uniq) and expert.tolist() == uniq
-    assert pbeg[0] == 0 and pbeg[-1] == T * k and np.all(np.diff(pbeg.astype(np.int64)) > 0)
-    for u, e in enumerate(uniq):
-        toks = [t for t in range(T) if e in ids[t]]
-        assert ptok[pbeg[u]: pbeg[u + 1]].tolist() == toks
-        for t in toks:
-            s = ids[t].tolist().index(e)
-            assert pbeg[u] <= pof[t, s] < pbeg[u + 1] and ptok[pof[t, s]] == t
 
     # activations
     xq, xs = O.quantize(x)

@@ -1,6 +1,6 @@
 // MoE decode dispatch (FlashNextGpu::Moe, src/engine/flash_next_gpu.cpp:697-845, and the session-union path of
 // StepBatch, src/engine/batch_decode.cpp): four launches over device-resident routing, no host round trip.
-// Workspace: logits, shared logit, quantized x, ids/weights, quantized h (rows t*k+s routed, T*k+t shared).
+// Workspace: logits, shared logit, quantized x, ids/weights, h in fp32 (rows t*k+s routed, T*k+t shared).
 #include "engine.hpp"
 
 using namespace halo::engine;
@@ -55,8 +55,7 @@ int halo_op_moe_views(const halo_moe_weights* w, uint32_t T, void* ws, halo_moe_
   v->xs = reinterpret_cast<float*>(take(sizeof(float) * T * (H / 32)));
   v->ids = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * T * k));
   v->weights = reinterpret_cast<float*>(take(sizeof(float) * T * k));
-  v->hq = reinterpret_cast<int8_t*>(take(static_cast<std::size_t>(T) * (k + 1) * hstride));
-  v->hs = reinterpret_cast<float*>(take(sizeof(float) * T * (k + 1) * (hstride / 32)));
+  v->h = reinterpret_cast<float*>(take(sizeof(float) * T * (k + 1) * hstride));
   v->hstride = hstride;
   v->bytes = o;
   return 0;
@@ -94,16 +93,16 @@ int halo_op_moe_decode(halo_engine* eng, const halo_moe_weights* w, const float*
     const halo_arg a[] = {Ptr(w->gate.qs), Ptr(w->gate.d), Ptr(w->up.qs), Ptr(w->up.d),
                           Ptr(shared ? w->shared_gate_proj.qs : nullptr), Ptr(shared ? w->shared_gate_proj.d : nullptr),
                           Ptr(shared ? w->shared_up.qs : nullptr), Ptr(shared ? w->shared_up.d : nullptr),
-                          Ptr(v.xq), Ptr(v.xs), Ptr(v.ids), Ptr(v.hq), Ptr(v.hs), U32(T), U32(F), U32(SF), U32(k),
+                          Ptr(v.xq), Ptr(v.xs), Ptr(v.ids), Ptr(v.h), U32(T), U32(F), U32(SF), U32(k),
                           U32(v.hstride)};
     const char* name = H == 1024 ? "halo_moe_gate_up_q8_s1" : H == 2048 ? "halo_moe_gate_up_q8_s2" : "halo_moe_gate_up_q8_s4";
     if (H == 3072) return SetErr(err, errlen, "moe: hidden 3072 has no gate/up instance"), -1;
-    if (Launch(eng, name, D3(T * k + 1, v.hstride / 32), D3(512), a, err, errlen) != 0) return -1;
+    if (Launch(eng, name, D3(T * k + 1, v.hstride / 4), D3(256), a, err, errlen) != 0) return -1;
   }
   // 4. down + routed combine + shared expert
   {
     const halo_arg a[] = {Ptr(w->down.qs), Ptr(w->down.d), Ptr(shared ? w->shared_down.qs : nullptr),
-                          Ptr(shared ? w->shared_down.d : nullptr), Ptr(v.hq), Ptr(v.hs), Ptr(v.ids), Ptr(v.weights),
+                          Ptr(shared ? w->shared_down.d : nullptr), Ptr(v.h), Ptr(v.ids), Ptr(v.weights),
                           Ptr(v.shared_logit), Ptr(out), U32(T), U32(H), U32(F), U32(SF), U32(k), U32(v.hstride)};
     if (Launch(eng, "halo_moe_down_q8", D3(CeilDiv(H, 8), T), D3(64 * (k + 1)), a, err, errlen) != 0) return -1;
   }

@@ -8,11 +8,12 @@
 // Launches (all take device buffers only, so one captured graph replays for any routing):
 //   1. halo_moe_router     logits[t][e] = W_r[e] . x[t] (fp32), shared-gate logit, x quantized per 32 (int8).
 //   2. halo_moe_topk       one block per token: softmax, top-k (ties -> lower id), renormalized weights.
-//   3. halo_moe_gate_up_q8 block (routed pair, 32 ff rows): the first token that selected an expert computes it for
+//   3. halo_moe_gate_up_q8 block (routed pair, 4 ff rows): the first token that selected an expert computes it for
 //                          every token that selected it (the union of experts: weights streamed once), h =
-//                          SiLU(g) * u quantized per 32. One more block column is the shared expert.
-//   4. halo_moe_down_q8    block (8 output rows, token): one wave per slot streams 4 KB of its expert; the
-//                          slots are combined in slot order in LDS, then + sigmoid(shared gate) * shared.
+//                          SiLU(g) * u in fp32. One more block column is the shared expert.
+//   4. halo_moe_down_q8    block (8 output rows, token): one wave per slot quantizes its h per 32 and streams
+//                          4 KB of its expert; the slots are combined in slot order in LDS, then
+//                          + sigmoid(shared gate) * shared.
 #include "common.h"
 
 using halo::Dot16;
@@ -341,48 +342,63 @@ extern "C" __global__ void __launch_bounds__(1024)
   }
 }
 
-namespace {
-constexpr int kGuRowsPerWave = 4;  // 4 ff rows of gate and 4 of up
-}  // namespace
-
-// grid (T * k + 1, ceil(max(ff, sff) / 32)), block 512 (8 waves x 4 ff rows = 32). Block x < T * k is routed
-// pair x (token x / k, slot x % k); the block of the first token that selected an expert computes that expert
-// for every token that selected it (weights streamed once), the others exit: the union of experts over tokens
-// without a separate bucketing pass. Block x = T * k is the shared expert for all tokens. kSteps = H / 1024.
-// Gate/up [E][ff][H] repacked Q8_0 (row stride H), shared gate/up [sff][H]. h = SiLU(gate) * up, quantized per 32:
-// hq [T * k + T][hstride] int8 (row t * k + s for routed pairs, T * k + t for the shared expert),
-// hs [.][hstride / 32].
+// grid (T * k + 1, ceil(max(ff, sff) / 4)), block 256: wave w computes ff row j = 4 * blockIdx.y + w of gate and
+// up (two rows of H int8, kSteps = H / 1024 loads each per lane). Block x < T * k is routed pair x (token x / k,
+// slot x % k); the block of the first token that selected an expert computes that expert for every token that
+// selected it (weights streamed once), the others exit: the union of experts over tokens without a separate
+// bucketing pass. Block x = T * k is the shared expert for all tokens. Gate/up [E][ff][H] repacked Q8_0 (row
+// stride H), shared gate/up [sff][H]. Output h = SiLU(gate) * up in fp32: h [T * k + T][hstride] (row t * k + s for
+// routed pairs, T * k + t for the shared expert).
 template <int kSteps>
 __device__ __forceinline__ void MoeGateUp(
     const std::int8_t* __restrict__ gq, const std::uint16_t* __restrict__ gd, const std::int8_t* __restrict__ uq,
     const std::uint16_t* __restrict__ ud, const std::int8_t* __restrict__ sgq, const std::uint16_t* __restrict__ sgd,
     const std::int8_t* __restrict__ suq, const std::uint16_t* __restrict__ sud, const std::int8_t* __restrict__ xq,
-    const float* __restrict__ xs, const std::uint32_t* __restrict__ ids, std::int8_t* __restrict__ hq,
-    float* __restrict__ hs, std::uint32_t T, std::uint32_t ff, std::uint32_t sff, std::uint32_t k,
-    std::uint32_t hstride) {
+    const float* __restrict__ xs, const std::uint32_t* __restrict__ ids, float* __restrict__ h, std::uint32_t T,
+    std::uint32_t ff, std::uint32_t sff, std::uint32_t k, std::uint32_t hstride) {
   constexpr std::uint32_t H = kSteps * kWave * 16;
   constexpr std::uint32_t nblk = H / 32;
-  const std::uint32_t px = blockIdx.x, jb = blockIdx.y;
+  const std::uint32_t px = blockIdx.x;
   const bool shared = px == T * k;
-  __shared__ std::uint32_t rows_s[kMoeMaxT];  // hq row of each pair, ascending token
+  const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const std::uint32_t j = blockIdx.y * (blockDim.x / kWave) + wave;
+  __shared__ std::uint32_t rows_s[kMoeMaxT];  // h row of each pair, ascending token
   __shared__ std::uint32_t tokmask;
   __shared__ std::uint32_t owner;
-  __shared__ float hbuf[kMoeMaxT][32];
   std::uint32_t np, f;
-  const std::int8_t *q0, *q1;
-  const std::uint16_t *d0, *d1;
+  std::size_t e = 0;
   if (shared) {
-    if (sgq == nullptr || jb * 32 >= sff) return;
+    if (sgq == nullptr || blockIdx.y * (blockDim.x / kWave) >= sff) return;
     np = T;
     f = sff;
-    q0 = sgq;
-    d0 = sgd;
-    q1 = suq;
-    d1 = sud;
+  } else {
+    if (blockIdx.y * (blockDim.x / kWave) >= ff) return;
+    e = ids[px];
+    np = 0;
+    f = ff;
+  }
+  const std::int8_t* q0 = shared ? sgq : gq + e * ff * H;
+  const std::uint16_t* d0 = shared ? sgd : gd + e * ff * nblk;
+  const std::int8_t* q1 = shared ? suq : uq + e * ff * H;
+  const std::uint16_t* d1 = shared ? sud : ud + e * ff * nblk;
+  // the two weight rows, issued before the ownership check (the check only decides whether to use them)
+  const std::uint32_t jr = min(j, f - 1);
+  int4 w[2][kSteps];
+  float sw[2][kSteps];
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) {
+    const std::uint32_t c = st * kWave * 16 + lane * 16;
+    w[0][st] = __builtin_bit_cast(int4, __builtin_nontemporal_load(
+                                           reinterpret_cast<const halo::V4i*>(q0 + static_cast<std::size_t>(jr) * H + c)));
+    w[1][st] = __builtin_bit_cast(int4, __builtin_nontemporal_load(
+                                           reinterpret_cast<const halo::V4i*>(q1 + static_cast<std::size_t>(jr) * H + c)));
+    sw[0][st] = F16(d0[static_cast<std::size_t>(jr) * nblk + c / 32]);
+    sw[1][st] = F16(d1[static_cast<std::size_t>(jr) * nblk + c / 32]);
+  }
+  if (shared) {
     if (threadIdx.x < T) rows_s[threadIdx.x] = T * k + threadIdx.x;
   } else {
-    if (jb * 32 >= ff) return;
-    const std::uint32_t e = ids[px], t = px / k;
+    const std::uint32_t t = px / k;
     if (threadIdx.x == 0) {
       tokmask = 0;
       owner = 1;
@@ -399,80 +415,36 @@ __device__ __forceinline__ void MoeGateUp(
     np = static_cast<std::uint32_t>(__builtin_popcount(m));
     for (std::uint32_t i = threadIdx.x; i < T * k; i += blockDim.x)
       if (ids[i] == e) rows_s[__builtin_popcount(m & ((1u << (i / k)) - 1u))] = i;
-    f = ff;
-    q0 = gq + static_cast<std::size_t>(e) * ff * H;
-    d0 = gd + static_cast<std::size_t>(e) * ff * nblk;
-    q1 = uq + static_cast<std::size_t>(e) * ff * H;
-    d1 = ud + static_cast<std::size_t>(e) * ff * nblk;
   }
-  const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const std::uint32_t j0 = jb * 32 + wave * kGuRowsPerWave;
-  // weights: rows j0..j0+3 of gate (r < 4) and up (r >= 4), all column steps, loaded once
-  int4 w[2 * kGuRowsPerWave][kSteps];
-  float sw[2 * kGuRowsPerWave][kSteps];
-#pragma unroll
-  for (int r = 0; r < 2 * kGuRowsPerWave; ++r) {
-    const std::int8_t* base = (r < kGuRowsPerWave ? q0 : q1) + static_cast<std::size_t>(j0 + r % kGuRowsPerWave) * H;
-    const std::uint16_t* dbase =
-        (r < kGuRowsPerWave ? d0 : d1) + static_cast<std::size_t>(j0 + r % kGuRowsPerWave) * nblk;
-#pragma unroll
-    for (int st = 0; st < kSteps; ++st) {
-      const std::uint32_t c = st * kWave * 16 + lane * 16;
-      w[r][st] = __builtin_bit_cast(int4, __builtin_nontemporal_load(reinterpret_cast<const halo::V4i*>(base + c)));
-      sw[r][st] = F16(dbase[c / 32]);
-    }
-  }
-  __syncthreads();  // rows_s
+  __syncthreads();
+  if (j >= f) return;
   for (std::uint32_t lp = 0; lp < np; ++lp) {
     const std::uint32_t row = rows_s[lp];
     const std::uint32_t tok = shared ? row - T * k : row / k;
     const std::int8_t* xt = xq + static_cast<std::size_t>(tok) * H;
     const float* st_ = xs + static_cast<std::size_t>(tok) * nblk;
-    float acc[2 * kGuRowsPerWave];
-#pragma unroll
-    for (int r = 0; r < 2 * kGuRowsPerWave; ++r) acc[r] = 0.0f;
+    float g = 0.0f, u = 0.0f;
 #pragma unroll
     for (int st = 0; st < kSteps; ++st) {
       const std::uint32_t c = st * kWave * 16 + lane * 16;
       const int4 xv = *reinterpret_cast<const int4*>(xt + c);
       const float sx = st_[c / 32];
-#pragma unroll
-      for (int r = 0; r < 2 * kGuRowsPerWave; ++r) acc[r] += sw[r][st] * (sx * static_cast<float>(Dot16(w[r][st], xv)));
+      g += sw[0][st] * (sx * static_cast<float>(Dot16(w[0][st], xv)));
+      u += sw[1][st] * (sx * static_cast<float>(Dot16(w[1][st], xv)));
     }
-#pragma unroll
-    for (int r = 0; r < 2 * kGuRowsPerWave; ++r) acc[r] = halo::GroupSum(acc[r]);
-    if (lane < kGuRowsPerWave) {
-      float g = acc[0], u = acc[kGuRowsPerWave];
-#pragma unroll
-      for (int r = 1; r < kGuRowsPerWave; ++r)
-        if (static_cast<int>(lane) == r) {
-          g = acc[r];
-          u = acc[kGuRowsPerWave + r];
-        }
-      hbuf[lp][wave * kGuRowsPerWave + lane] = halo::Silu(g) * u;
-    }
-  }
-  __syncthreads();
-  // quantize h per 32 values: one half wave per pair
-  const std::uint32_t hw = threadIdx.x / 32, hl = threadIdx.x % 32;
-  for (std::uint32_t lp = hw; lp < np; lp += blockDim.x / 32) {
-    const float v = hbuf[lp][hl];
-    const float amax = halo::GroupMax<32>(fabsf(v));
-    const float scale = amax / 127.0f;
-    const int q = scale > 0.0f ? static_cast<int>(rintf(v / scale)) : 0;
-    const std::uint32_t row = rows_s[lp];
-    hq[static_cast<std::size_t>(row) * hstride + jb * 32 + hl] = static_cast<std::int8_t>(q);
-    if (hl == 0) hs[static_cast<std::size_t>(row) * (hstride / 32) + jb] = scale;
+    g = halo::GroupSum(g);
+    u = halo::GroupSum(u);
+    if (lane == 0) h[static_cast<std::size_t>(row) * hstride + j] = halo::Silu(g) * u;
   }
 }
 
 #define HALO_MOE_GATE_UP(S)                                                                                        \
-  extern "C" __global__ void __launch_bounds__(512) halo_moe_gate_up_q8_s##S(                                     \
+  extern "C" __global__ void __launch_bounds__(256) halo_moe_gate_up_q8_s##S(                                     \
       const std::int8_t* gq, const std::uint16_t* gd, const std::int8_t* uq, const std::uint16_t* ud,             \
       const std::int8_t* sgq, const std::uint16_t* sgd, const std::int8_t* suq, const std::uint16_t* sud,         \
-      const std::int8_t* xq, const float* xs, const std::uint32_t* ids, std::int8_t* hq, float* hs,               \
-      std::uint32_t T, std::uint32_t ff, std::uint32_t sff, std::uint32_t k, std::uint32_t hstride) {             \
-    MoeGateUp<S>(gq, gd, uq, ud, sgq, sgd, suq, sud, xq, xs, ids, hq, hs, T, ff, sff, k, hstride);                 \
+      const std::int8_t* xq, const float* xs, const std::uint32_t* ids, float* h, std::uint32_t T,                \
+      std::uint32_t ff, std::uint32_t sff, std::uint32_t k, std::uint32_t hstride) {                              \
+    MoeGateUp<S>(gq, gd, uq, ud, sgq, sgd, suq, sud, xq, xs, ids, h, T, ff, sff, k, hstride);                      \
   }
 HALO_MOE_GATE_UP(1)
 HALO_MOE_GATE_UP(2)
@@ -484,16 +456,16 @@ constexpr int kDownRows = 8;  // output rows per block: 4 passes x 2 rows (a row
 }
 
 // grid (ceil(H / 8), T), block 64 * (k + 1) (<= 1024): wave s < k streams 8 rows of expert ids[t][s]'s down matrix
-// (4 KB contiguous), wave k the shared expert's; the block combines in slot order through LDS:
-//   out[t][r] = sum over s < k, in order, of weights[t][s] * (W_d[ids[t][s]][r] . h[t * k + s]),
-//               then + sigmoid(sgl[t]) * (W_sd[r] . h[T * k + t]).
+// (4 KB contiguous), wave k the shared expert's; each wave quantizes its h row per 32 values (amax / 127, round
+// half to even; a 32-value block is two adjacent lanes) and the block combines in slot order through LDS:
+//   out[t][r] = sum over s < k, in order, of weights[t][s] * (W_d[ids[t][s]][r] . q8(h[t * k + s])),
+//               then + sigmoid(sgl[t]) * (W_sd[r] . q8(h[T * k + t])).
 // Down [E][H][ff] repacked (row stride ff), shared down [H][sff]; ff, sff <= 512.
 extern "C" __global__ void __launch_bounds__(1024) halo_moe_down_q8(
     const std::int8_t* __restrict__ dq, const std::uint16_t* __restrict__ dd, const std::int8_t* __restrict__ sdq,
-    const std::uint16_t* __restrict__ sdd, const std::int8_t* __restrict__ hq, const float* __restrict__ hs,
-    const std::uint32_t* __restrict__ ids, const float* __restrict__ weights, const float* __restrict__ sgl,
-    float* __restrict__ out, std::uint32_t T, std::uint32_t H, std::uint32_t ff, std::uint32_t sff, std::uint32_t k,
-    std::uint32_t hstride) {
+    const std::uint16_t* __restrict__ sdd, const float* __restrict__ h, const std::uint32_t* __restrict__ ids,
+    const float* __restrict__ weights, const float* __restrict__ sgl, float* __restrict__ out, std::uint32_t T,
+    std::uint32_t H, std::uint32_t ff, std::uint32_t sff, std::uint32_t k, std::uint32_t hstride) {
   __shared__ float part[33][kDownRows];
   const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, sub = lane / 32, l = lane % 32;
   const std::uint32_t t = blockIdx.y, r0 = blockIdx.x * kDownRows;
@@ -516,12 +488,42 @@ extern "C" __global__ void __launch_bounds__(1024) halo_moe_down_q8(
                 : make_int4(0, 0, 0, 0);
       sw[p] = in ? F16(dbase[static_cast<std::size_t>(r) * (f / 32) + c / 32]) : 0.0f;
     }
-    const int4 hv = in ? *reinterpret_cast<const int4*>(hq + static_cast<std::size_t>(hrow) * hstride + c)
-                       : make_int4(0, 0, 0, 0);
-    const float sh = in ? hs[static_cast<std::size_t>(hrow) * (hstride / 32) + c / 32] : 0.0f;
+    // h: 16 values per lane, quantized per 32 with the neighbour lane
+    float hv[16];
+    if (in) {
+      const float4* hp = reinterpret_cast<const float4*>(h + static_cast<std::size_t>(hrow) * hstride + c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 v = hp[i];
+        hv[4 * i] = v.x;
+        hv[4 * i + 1] = v.y;
+        hv[4 * i + 2] = v.z;
+        hv[4 * i + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) hv[i] = 0.0f;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(hv[i]));
+    amax = fmaxf(amax, halo::Dpp<0xB1>(amax));  // lanes 2i, 2i + 1 hold one 32-value block
+    const float scale = amax / 127.0f;
+    int packed[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      std::uint32_t word = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int qv = scale > 0.0f ? static_cast<int>(rintf(hv[4 * i + b] / scale)) : 0;
+        word |= (static_cast<std::uint32_t>(qv) & 0xFFu) << (8 * b);
+      }
+      packed[i] = static_cast<int>(word);
+    }
+    const int4 hq = make_int4(packed[0], packed[1], packed[2], packed[3]);
 #pragma unroll
     for (int p = 0; p < kDownRows / 2; ++p) {
-      const float v = halo::GroupSum<32>(sw[p] * (sh * static_cast<float>(Dot16(q[p], hv))));
+      const float v = halo::GroupSum<32>(sw[p] * (scale * static_cast<float>(Dot16(q[p], hq))));
       if (l == 0) part[wave][2 * p + sub] = v;
     }
   }

@@ -73,7 +73,7 @@ class MoeWeights(C.Structure):
 
 
 class MoeViews(C.Structure):
-    _fields_ = [(n, C.c_void_p) for n in ("logits", "shared_logit", "xq", "xs", "ids", "weights", "hq", "hs")] + [
+    _fields_ = [(n, C.c_void_p) for n in ("logits", "shared_logit", "xq", "xs", "ids", "weights", "h")] + [
         ("hstride", C.c_uint32), ("pad", C.c_uint32), ("bytes", C.c_size_t)]
 
 

@@ -101,8 +101,7 @@ typedef struct halo_moe_views {
   float* xs;              /* [T][hidden/32] */
   uint32_t* ids;          /* [T][n_used], descending probability */
   float* weights;         /* [T][n_used], renormalized */
-  int8_t* hq;             /* [T * n_used + T][hstride]: row t*n_used+s routed, T*n_used+t shared */
-  float* hs;              /* [T * n_used + T][hstride / 32] */
+  float* h;               /* [T * n_used + T][hstride] SiLU(gate) * up: row t*n_used+s routed, T*n_used+t shared */
   uint32_t hstride;
   uint32_t pad;
   size_t bytes;           /* workspace bytes the views span */

@@ -1,0 +1,75 @@
+// Decode attention dispatch (FlashNextGpu::Attention, src/engine/flash_next_gpu.cpp:581-680, and the batched
+// per-entry attention of StepBatch): paged KV, prefix read once per step for all sessions.
+#include "engine.hpp"
+
+using namespace halo::engine;
+
+namespace {
+
+constexpr std::uint32_t kChunk = 64;
+
+int Check(const halo_paged_kv* kv, std::uint32_t Hq, char* err, std::size_t errlen) {
+  if (kv == nullptr || kv->k_pool == nullptr || kv->v_pool == nullptr || kv->pages == nullptr || kv->nkv == nullptr)
+    return SetErr(err, errlen, "attn: missing kv buffers"), -1;
+  if (kv->head_dim != 256) return SetErr(err, errlen, "attn: head dim %u unsupported (256)", kv->head_dim), -1;
+  if (kv->kv_heads == 0 || Hq % kv->kv_heads != 0 || kv->sessions == 0 || kv->sessions * (Hq / kv->kv_heads) > 32)
+    return SetErr(err, errlen, "attn: %u sessions x %u q heads / %u kv heads unsupported", kv->sessions, Hq,
+                  kv->kv_heads),
+           -1;
+  if (kv->prefix % kChunk != 0 || kv->prefix > kv->max_context || kv->max_context > kv->max_pages * 16)
+    return SetErr(err, errlen, "attn: prefix %u must be a multiple of 64 within max_context %u <= 16 * %u pages",
+                  kv->prefix, kv->max_context, kv->max_pages),
+           -1;
+  return 0;
+}
+
+void Chunks(const halo_paged_kv* kv, std::uint32_t* prefix_chunks, std::uint32_t* suffix_chunks) {
+  *prefix_chunks = kv->prefix / kChunk;
+  *suffix_chunks = std::max<std::uint32_t>(1, CeilDiv(kv->max_context - kv->prefix, kChunk));
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t halo_op_attn_decode_workspace_bytes(const halo_paged_kv* kv, uint32_t Hq) {
+  if (Check(kv, Hq, nullptr, 0) != 0) return 0;
+  std::uint32_t pc, sc;
+  Chunks(kv, &pc, &sc);
+  const std::size_t items = static_cast<std::size_t>(kv->kv_heads) * (pc + kv->sessions * sc);
+  const std::size_t slots = kv->sessions * (Hq / kv->kv_heads);
+  return items * slots * (2 + kv->head_dim) * sizeof(float);
+}
+
+int halo_op_attn_decode(halo_engine* eng, const halo_paged_kv* kv, const float* q, const float* gate, float* o,
+                        uint32_t Hq, void* ws, size_t ws_bytes, char* err, size_t errlen) {
+  if (Check(kv, Hq, err, errlen) != 0) return -1;
+  const std::size_t need = halo_op_attn_decode_workspace_bytes(kv, Hq);
+  if (ws == nullptr || ws_bytes < need) return SetErr(err, errlen, "attn: workspace %zu < %zu", ws_bytes, need), -1;
+  std::uint32_t pc, sc;
+  Chunks(kv, &pc, &sc);
+  const std::uint32_t S = kv->sessions, Hkv = kv->kv_heads;
+  const std::size_t items = static_cast<std::size_t>(Hkv) * (pc + S * sc);
+  const std::size_t slots = S * (Hq / Hkv);
+  float* pm = static_cast<float*>(ws);
+  float* pl = pm + items * slots;
+  float* pacc = pl + items * slots;
+  {
+    const halo_arg a[] = {Ptr(q), Ptr(kv->k_pool), Ptr(kv->v_pool), Ptr(kv->pages), Ptr(kv->nkv), Ptr(pm), Ptr(pl),
+                          Ptr(pacc), U32(S), U32(Hq), U32(Hkv), U32(kv->prefix), U32(kv->max_pages), U32(pc), U32(sc)};
+    if (Launch(eng, "halo_attn_decode_partial", D3(static_cast<std::uint32_t>(items)), D3(256), a, err, errlen) != 0)
+      return -1;
+  }
+  const halo_arg a[] = {Ptr(pm), Ptr(pl), Ptr(pacc), Ptr(gate), Ptr(o), U32(S), U32(Hq), U32(Hkv), U32(pc), U32(sc)};
+  return Launch(eng, "halo_attn_decode_combine", D3(S * Hq), D3(256), a, err, errlen);
+}
+
+int halo_op_kv_append(halo_engine* eng, const halo_paged_kv* kv, const float* k, const float* v, char* err,
+                      size_t errlen) {
+  if (kv == nullptr || kv->head_dim != 256) return SetErr(err, errlen, "kv append: head dim 256 only"), -1;
+  const halo_arg a[] = {Ptr(k), Ptr(v), Ptr(kv->k_pool), Ptr(kv->v_pool), Ptr(kv->pages), Ptr(kv->nkv),
+                        U32(kv->kv_heads), U32(kv->max_pages)};
+  return Launch(eng, "halo_kv_append", D3(kv->sessions * kv->kv_heads), D3(64), a, err, errlen);
+}
+
+}  // extern "C"

@@ -136,6 +136,15 @@ int halo_op_matvec_q8a8(halo_engine* eng, const halo_q8_matrix* w, const int8_t*
   if (CheckMatrix(w, err, errlen) != 0) return -1;
   if (m == 0) return SetErr(err, errlen, "m == 0"), -1;
   if (m > 1 && ystride < w->rows) return SetErr(err, errlen, "ystride %u < rows %u", ystride, w->rows), -1;
+  if (m >= 16) {
+    // int8 MFMA tiles: 16 rows x 16 (or 64) tokens per block, one MFMA per Q8_0 block
+    const std::uint32_t ys = m > 1 ? ystride : w->rows;
+    const bool wide = m >= 64;
+    const halo_arg a[] = {Ptr(w->qs), Ptr(w->d), Ptr(xq), Ptr(xs), Ptr(y), U32(w->rows), U32(w->cols),
+                          U32(w->qstride), U32(m), U32(ys)};
+    return Launch(eng, wide ? "halo_gemm_q8a8_mfma_t4" : "halo_gemm_q8a8_mfma_t1",
+                  D3(CeilDiv(w->rows, 16), CeilDiv(m, wide ? 64 : 16)), D3(256), a, err, errlen);
+  }
   // Tiling: a row is covered by as many lanes as its 16-byte pieces allow (up to a wave); more activation columns
   // reuse each weight load over more rows per lane group.
   const std::uint32_t lpr = w->cols >= 1024 ? 64 : (w->cols >= 512 ? 32 : 16);

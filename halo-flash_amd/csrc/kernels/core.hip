@@ -1,3 +1,5 @@
 // The gfx950 code object: every kernel the device layer can look up by name.
 #include "q8.hip"
 #include "moe.hip"
+#include "gdn.hip"
+#include "attn.hip"

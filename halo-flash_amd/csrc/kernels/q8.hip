@@ -423,3 +423,98 @@ extern "C" __global__ void __launch_bounds__(256)
   for (std::uint64_t i = blockIdx.x * static_cast<std::uint64_t>(blockDim.x) + threadIdx.x; i < n; i += stride)
     dst[i] = src[i];
 }
+
+// ---- int8 MFMA tiles for M >= 16 tokens (prefill, speculative verify) ----------------------------------------
+// reference: halo_gemm_q8r_wmma / GemmQ8A8 (src/kernels/core.hip:3108-3153, 3344-3476): per 32-value block an
+// integer product into int32, then the fp32 epilogue acc += d_w * (s_x * isum). Here one v_mfma_i32_16x16x32_i8 per
+// (16 rows, 16 tokens, one Q8_0 block): A = 16 weight rows x 32 int8 (lane l: row l % 16, k 8 (l / 16) .. +8),
+// B = 32 x 16 tokens (lane l: token l % 16, same k), D (lane l: token l % 16, rows 4 (l / 16) .. +4).
+// A block of 4 waves owns 16 rows x 16 * NT tokens; the waves split the K blocks four ways and reduce through LDS
+// (fixed order). grid (ceil(rows / 16), ceil(T / (16 NT))), block 256. y[t * ystride + r].
+namespace {
+typedef int V4I32 __attribute__((ext_vector_type(4)));
+
+template <int NT>
+__device__ __forceinline__ void GemmQ8A8Mfma(const std::int8_t* __restrict__ qs, const std::uint16_t* __restrict__ d,
+                                             const std::int8_t* __restrict__ xq, const float* __restrict__ xs,
+                                             float* __restrict__ y, std::uint32_t rows, std::uint32_t cols,
+                                             std::uint32_t qstride, std::uint32_t T, std::uint32_t ystride) {
+  __shared__ float red[4][NT][16][17];
+  const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const std::uint32_t r0 = blockIdx.x * 16, t0 = blockIdx.y * 16 * NT;
+  const std::uint32_t nblk = cols / 32;
+  const std::uint32_t arow = min(r0 + lane % 16, rows - 1);
+  const std::uint32_t kofs = (lane / 16) * 8;
+  const std::int8_t* aptr = qs + static_cast<std::size_t>(arow) * qstride + kofs;
+  const std::int8_t* bptr[NT];
+  const float* sptr[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const std::uint32_t tok = min(t0 + n * 16 + lane % 16, T - 1);
+    bptr[n] = xq + static_cast<std::size_t>(tok) * cols + kofs;
+    sptr[n] = xs + static_cast<std::size_t>(tok) * nblk;
+  }
+  const std::uint16_t* dptr[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    dptr[i] = d + static_cast<std::size_t>(min(r0 + (lane / 16) * 4 + i, rows - 1)) * nblk;
+  float acc[NT][4];
+#pragma unroll
+  for (int n = 0; n < NT; ++n)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[n][i] = 0.0f;
+  const std::uint32_t per = (nblk + 3) / 4, kb0 = wave * per, kb1 = min(nblk, kb0 + per);
+  constexpr int U = 4;
+  for (std::uint32_t kb = kb0; kb < kb1; kb += U) {
+    long a[U];
+    long b[U][NT];
+    float dw[U][4], sx[U][NT];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const std::uint32_t k = min(kb + u, kb1 - 1);
+      a[u] = *reinterpret_cast<const long*>(aptr + k * 32);
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        b[u][n] = *reinterpret_cast<const long*>(bptr[n] + k * 32);
+        sx[u][n] = sptr[n][k];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dw[u][i] = F16(dptr[i][k]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (kb + u >= kb1) break;
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        const V4I32 zero = {0, 0, 0, 0};
+        const V4I32 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[u], b[u][n], zero, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[n][i] += dw[u][i] * (sx[u][n] * static_cast<float>(c[i]));
+      }
+    }
+  }
+#pragma unroll
+  for (int n = 0; n < NT; ++n)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][n][(lane / 16) * 4 + i][lane % 16] = acc[n][i];
+  __syncthreads();
+  for (std::uint32_t e = threadIdx.x; e < NT * 256; e += blockDim.x) {
+    const std::uint32_t n = e / 256, rr = (e % 256) / 16, tt = e % 16;
+    const std::uint32_t r = r0 + rr, tok = t0 + n * 16 + tt;
+    if (r < rows && tok < T)
+      y[static_cast<std::size_t>(tok) * ystride + r] =
+          ((red[0][n][rr][tt] + red[1][n][rr][tt]) + red[2][n][rr][tt]) + red[3][n][rr][tt];
+  }
+}
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(256) halo_gemm_q8a8_mfma_t1(
+    const std::int8_t* qs, const std::uint16_t* d, const std::int8_t* xq, const float* xs, float* y, std::uint32_t rows,
+    std::uint32_t cols, std::uint32_t qstride, std::uint32_t T, std::uint32_t ystride) {
+  GemmQ8A8Mfma<1>(qs, d, xq, xs, y, rows, cols, qstride, T, ystride);
+}
+extern "C" __global__ void __launch_bounds__(256) halo_gemm_q8a8_mfma_t4(
+    const std::int8_t* qs, const std::uint16_t* d, const std::int8_t* xq, const float* xs, float* y, std::uint32_t rows,
+    std::uint32_t cols, std::uint32_t qstride, std::uint32_t T, std::uint32_t ystride) {
+  GemmQ8A8Mfma<4>(qs, d, xq, xs, y, rows, cols, qstride, T, ystride);
+}

@@ -77,6 +77,11 @@ class MoeViews(C.Structure):
         ("hstride", C.c_uint32), ("pad", C.c_uint32), ("bytes", C.c_size_t)]
 
 
+class PagedKV(C.Structure):
+    _fields_ = [("k_pool", C.c_void_p), ("v_pool", C.c_void_p), ("pages", C.c_void_p), ("nkv", C.c_void_p)] + [
+        (n, C.c_uint32) for n in ("sessions", "kv_heads", "head_dim", "max_pages", "prefix", "max_context")]
+
+
 ERRLEN = 1024
 _VP, _SZ, _U32, _U64, _F32, _I32 = C.c_void_p, C.c_size_t, C.c_uint32, C.c_uint64, C.c_float, C.c_int32
 _ERR = [C.c_char_p, _SZ]
@@ -119,6 +124,10 @@ _SIGS = {
     "halo_op_q8_half_dots": (C.c_int, [_VP, C.POINTER(Q8Matrix), _VP, _VP], True),
     "halo_op_synth_q8": (C.c_int, [_VP, _VP, _VP, _U32, _U32, _U32, _U64, _F32], True),
     "halo_op_synth_f32": (C.c_int, [_VP, _VP, _U64, _U64, _F32], True),
+    "halo_op_gdn_decode": (C.c_int, [_VP] + [_VP] * 7 + [_U32] * 4, True),
+    "halo_op_attn_decode_workspace_bytes": (_SZ, [C.POINTER(PagedKV), _U32], False),
+    "halo_op_attn_decode": (C.c_int, [_VP, C.POINTER(PagedKV), _VP, _VP, _VP, _U32, _VP, _SZ], True),
+    "halo_op_kv_append": (C.c_int, [_VP, C.POINTER(PagedKV), _VP, _VP], True),
     "halo_op_moe_workspace_bytes": (_SZ, [C.POINTER(MoeWeights), _U32], False),
     "halo_op_moe_views": (C.c_int, [C.POINTER(MoeWeights), _U32, _VP, C.POINTER(MoeViews)], True),
     "halo_op_moe_decode": (C.c_int, [_VP, C.POINTER(MoeWeights), _VP, _VP, _U32, _VP, _SZ], True),

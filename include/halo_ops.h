@@ -50,7 +50,8 @@ int halo_op_quantize_q8(halo_engine* eng, const float* x, int8_t* xq, float* xs,
 /* Q8_0 x int8-activation projection for M tokens (FlashNextGpu::MatVec + the batched int8 GEMV,
  * src/engine/flash_next_gpu.cpp:212-254, src/kernels/batch_decode.hip:226-345):
  *   y[t * ystride + r] = sum_b d[r][b] * xs[t][b] * isum(r, b, t),   t < M.
- * M <= 8 streams the weights once per launch with v_dot4; larger M runs 16-token MFMA int8 tiles. */
+ * M < 16 streams the weights once per launch with v_dot4 (in groups of up to 8 columns); M >= 16 runs int8 MFMA
+ * tiles of 16 rows x 16 tokens (x 64 tokens from M = 64), one v_mfma_i32_16x16x32_i8 per Q8_0 block. */
 int halo_op_matvec_q8a8(halo_engine* eng, const halo_q8_matrix* w, const int8_t* xq, const float* xs, float* y,
                         uint32_t m, uint32_t ystride, char* err, size_t errlen);
 /* The same with an explicit GEMV tiling (lanes per row 16/32/64, rows per lane group 1/2/4, waves per block) for
@@ -110,6 +111,41 @@ int halo_op_moe_views(const halo_moe_weights* w, uint32_t tokens, void* ws, halo
                       size_t errlen);
 int halo_op_moe_decode(halo_engine* eng, const halo_moe_weights* w, const float* x, float* out, uint32_t tokens,
                        void* ws, size_t ws_bytes, char* err, size_t errlen);
+
+/* ---- Gated DeltaNet ------------------------------------------------------------------------------------------
+ * The recurrence of ReferenceModel::LinearAttention (src/model/reference.cpp:329-364) / halo_gdn_step_d128
+ * (src/kernels/core.hip:2620-2646) per value head h (key head h % Hk), decay = exp(g):
+ *   u = (decay S)^T k,  delta = (v - u) * beta,  S <- decay S + k delta^T,  o = S^T q / sqrt(d).
+ * State: fp32 [S][Hv][d][d] key-major (S[i][j], i key, j value). d = 128. */
+
+/* One decode step for S sessions: q, k [S][Hk][d], v [S][Hv][d], g, beta [S][Hv] (g = log decay, beta after its
+ * sigmoid), o [S][Hv][d]; state updated in place. One launch. */
+int halo_op_gdn_decode(halo_engine* eng, float* state, const float* q, const float* k, const float* v,
+                       const float* g, const float* beta, float* o, uint32_t sessions, uint32_t v_heads,
+                       uint32_t k_heads, uint32_t head_dim, char* err, size_t errlen);
+
+/* ---- GQA decode attention over a paged, prefix-shared KV cache ---------------------------------------------------
+ * ReferenceModel::Attention's dense branch (src/model/reference.cpp:492-527) / halo_attention_select_b
+ * (src/kernels/core.hip:898): per query head h (kv head h / (Hq/Hkv)), o = softmax(q.K^T/sqrt(d)) V * sigmoid(gate).
+ * KV pools [pages][Hkv][16][d] fp32, page tables [S][max_pages] (uint32), nkv [S] visible positions (device
+ * memory, so a captured graph replays at every position). The first `prefix` tokens (a multiple of 64) have the same
+ * pages in every session's table and are read once for all sessions. d = 256, S * Hq / Hkv <= 32. */
+typedef struct halo_paged_kv {
+  float* k_pool;
+  float* v_pool;
+  const uint32_t* pages; /* [S][max_pages] */
+  const uint32_t* nkv;   /* [S] */
+  uint32_t sessions, kv_heads, head_dim, max_pages, prefix, max_context;
+} halo_paged_kv;
+
+/* Scratch for the partials of one decode attention call. */
+size_t halo_op_attn_decode_workspace_bytes(const halo_paged_kv* kv, uint32_t q_heads);
+/* o [S][Hq][d] = attention(q [S][Hq][d]) over each session's nkv positions; gate [S][Hq][d] or NULL. Two launches. */
+int halo_op_attn_decode(halo_engine* eng, const halo_paged_kv* kv, const float* q, const float* gate, float* o,
+                        uint32_t q_heads, void* ws, size_t ws_bytes, char* err, size_t errlen);
+/* Writes one token's k, v [S][Hkv][d] at position nkv[s] - 1 of each session. */
+int halo_op_kv_append(halo_engine* eng, const halo_paged_kv* kv, const float* k, const float* v, char* err,
+                      size_t errlen);
 
 #ifdef __cplusplus
 }

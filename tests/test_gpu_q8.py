@@ -126,6 +126,18 @@ def test_c1_projections(dev, rows, cols, m):
     _check_y(gy.download(), want, mag)
 
 
+@pytest.mark.parametrize("m", [16, 40, 64, 130])
+def test_mfma_tiles(dev, m):
+    """M >= 16 runs the int8 MFMA tiles (16 rows x 16 or 64 tokens, one MFMA per Q8_0 block); ragged M and rows."""
+    rng = np.random.default_rng(m)
+    rows, cols = 1000, 2048
+    w, xq, xs, want, mag = _gemv_case(dev, rng, rows, cols, m)
+    gq, gs = dev.to_device(xq), dev.to_device(xs)
+    gy = dev.array((m, rows + 3), np.float32)
+    dev.op("matvec_q8a8", C_ref(w), gq.ptr, gs.ptr, gy.ptr, m, rows + 3)
+    _check_y(gy.download()[:, :rows], want, mag)
+
+
 @pytest.mark.parametrize("lpr", [16, 32, 64])
 @pytest.mark.parametrize("rpl", [1, 2, 4])
 @pytest.mark.parametrize("m", [1, 8])

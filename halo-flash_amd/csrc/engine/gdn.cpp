@@ -16,4 +16,48 @@ int halo_op_gdn_decode(halo_engine* eng, float* state, const float* q, const flo
   return Launch(eng, "halo_gdn_decode_d128", D3(S * Hv * 4), D3(256), a, err, errlen);
 }
 
+uint32_t halo_gdn_chunk_table(const uint32_t* seqlens, uint32_t n_seq, uint32_t* chunks, uint32_t* seqs) {
+  std::uint32_t n = 0, tok = 0;
+  for (std::uint32_t s = 0; s < n_seq; ++s) {
+    const std::uint32_t nc = (seqlens[s] + 63) / 64;
+    if (seqs) {
+      seqs[2 * s] = n;
+      seqs[2 * s + 1] = nc;
+    }
+    for (std::uint32_t c = 0; c < nc; ++c, ++n)
+      if (chunks) {
+        chunks[3 * n] = tok + 64 * c;
+        chunks[3 * n + 1] = std::min<std::uint32_t>(64, seqlens[s] - 64 * c);
+        chunks[3 * n + 2] = s;
+      }
+    tok += seqlens[s];
+  }
+  return n;
+}
+
+size_t halo_op_gdn_prefill_workspace_bytes(uint32_t n_chunks, uint32_t Hv) {
+  return static_cast<std::size_t>(n_chunks) * Hv * (2 * 64 * 64 + 64) * sizeof(float);
+}
+
+int halo_op_gdn_prefill(halo_engine* eng, const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
+                        const float* beta, const uint32_t* chunks, const uint32_t* seqs, uint32_t n_chunks,
+                        uint32_t n_seq, float* state, float* o, uint32_t Hv, uint32_t Hk, uint32_t d, void* ws,
+                        size_t ws_bytes, char* err, size_t errlen) {
+  if (d != 128) return SetErr(err, errlen, "gdn prefill: head dim %u unsupported (128)", d), -1;
+  if (n_chunks == 0 || n_seq == 0 || Hv == 0 || Hk == 0 || Hv % Hk != 0)
+    return SetErr(err, errlen, "gdn prefill: empty batch or bad heads"), -1;
+  const std::size_t need = halo_op_gdn_prefill_workspace_bytes(n_chunks, Hv);
+  if (ws == nullptr || ws_bytes < need) return SetErr(err, errlen, "gdn prefill: workspace %zu < %zu", ws_bytes, need), -1;
+  float* Tm = static_cast<float*>(ws);
+  float* Pm = Tm + static_cast<std::size_t>(n_chunks) * Hv * 4096;
+  float* Gc = Pm + static_cast<std::size_t>(n_chunks) * Hv * 4096;
+  {
+    const halo_arg a[] = {Ptr(q), Ptr(k), Ptr(g), Ptr(beta), Ptr(chunks), Ptr(Tm), Ptr(Pm), Ptr(Gc), U32(Hv), U32(Hk)};
+    if (Launch(eng, "halo_gdn_chunk_prep", D3(n_chunks, Hv), D3(256), a, err, errlen) != 0) return -1;
+  }
+  const halo_arg a[] = {Ptr(q), Ptr(k), Ptr(v), Ptr(beta), Ptr(chunks), Ptr(seqs), Ptr(Tm), Ptr(Pm), Ptr(Gc),
+                        Ptr(state), Ptr(o), U32(Hv), U32(Hk)};
+  return Launch(eng, "halo_gdn_chunk_scan", D3(n_seq * Hv * 4), D3(256), a, err, errlen);
+}
+
 }  // extern "C"

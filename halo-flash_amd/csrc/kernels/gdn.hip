@@ -87,3 +87,221 @@ extern "C" __global__ void __launch_bounds__(256)
     o[(static_cast<std::size_t>(s) * Hv + h) * kD + jb * kJBlock + t] = acc * (1.0f / sqrtf(static_cast<float>(kD)));
   }
 }
+
+// ---- chunked prefill (C = 64) over a ragged batch of sequences -----------------------------------------------
+// Within a chunk of C tokens with cumulative log-decay G_t (gamma_t = exp(G_t)) and initial state S0, the token
+// recurrence above is exactly (reference math comment src/kernels/core.hip:6035-6048, there with C = 16):
+//   (I + A) Delta = diag(beta) V - diag(beta gamma) K S0,   A[t][s] = beta_t exp(G_t - G_s) (k_t . k_s), s < t
+//   O = (diag(gamma) Q S0 + P Delta) / sqrt(d),             P[t][s] = exp(G_t - G_s) (q_t . k_s),         s <= t
+//   S_C = gamma_C S0 + K^T diag(exp(G_C - G_s)) Delta.
+// halo_gdn_chunk_prep computes, for every (chunk, head) in parallel, T = (I + A)^-1 (forward substitution), P and
+// G; halo_gdn_chunk_scan walks each sequence's chunks in order carrying S, with Delta = T Z and
+// Z = diag(beta) V - diag(beta gamma) (K S0). Tokens past a partial chunk's end are zero-padded (beta = 0, g = 0),
+// which makes them contribute nothing. Inputs q, k [tokens][Hk][128] and v [tokens][Hv][128] are bf16; g, beta
+// [tokens][Hv] fp32 (g = log decay, beta after its sigmoid); state fp32 [seq][Hv][128][128] key-major.
+// chunks [n][3] = {first token, length, sequence}; seqs [n_seq][2] = {first chunk, chunk count}.
+namespace {
+constexpr int kC = 64;
+
+__device__ __forceinline__ float Bf(std::uint16_t h) { return __uint_as_float(static_cast<std::uint32_t>(h) << 16); }
+}  // namespace
+
+// grid (n_chunks, Hv), block 256. Tm, Pm [n_chunks][Hv][64][64] fp32, Gc [n_chunks][Hv][64].
+extern "C" __global__ void __launch_bounds__(256) halo_gdn_chunk_prep(
+    const std::uint16_t* __restrict__ q, const std::uint16_t* __restrict__ k, const float* __restrict__ g,
+    const float* __restrict__ beta, const std::uint32_t* __restrict__ chunks, float* __restrict__ Tm,
+    float* __restrict__ Pm, float* __restrict__ Gc, std::uint32_t Hv, std::uint32_t Hk) {
+  __shared__ union {
+    struct {
+      std::uint16_t kb[kC][kD];
+      std::uint16_t qb[kC][kD];
+    } in;
+    float tm[kC][kC + 1];
+  } u;
+  __shared__ float am[kC][kC + 1];
+  __shared__ float G[kC], B[kC];
+  const std::uint32_t c = blockIdx.x, h = blockIdx.y, kh = h % Hk, tid = threadIdx.x;
+  const std::uint32_t start = chunks[c * 3], L = chunks[c * 3 + 1];
+  for (std::uint32_t idx = tid; idx < kC * (kD / 8); idx += blockDim.x) {
+    const std::uint32_t t = idx / (kD / 8), p = idx % (kD / 8);
+    int4 kv = make_int4(0, 0, 0, 0), qv = make_int4(0, 0, 0, 0);
+    if (t < L) {
+      const std::size_t off = (static_cast<std::size_t>(start + t) * Hk + kh) * kD + p * 8;
+      kv = *reinterpret_cast<const int4*>(k + off);
+      qv = *reinterpret_cast<const int4*>(q + off);
+    }
+    *reinterpret_cast<int4*>(&u.in.kb[t][p * 8]) = kv;
+    *reinterpret_cast<int4*>(&u.in.qb[t][p * 8]) = qv;
+  }
+  if (tid < kC) {
+    const bool in = tid < L;
+    G[tid] = in ? g[static_cast<std::size_t>(start + tid) * Hv + h] : 0.0f;
+    B[tid] = in ? beta[static_cast<std::size_t>(start + tid) * Hv + h] : 0.0f;
+  }
+  __syncthreads();
+  if (tid == 0)
+    for (int t = 1; t < kC; ++t) G[t] += G[t - 1];
+  __syncthreads();
+  // A (strictly lower) and P (lower incl. diagonal); thread: row t, 16 columns
+  const std::size_t mat = (static_cast<std::size_t>(c) * Hv + h) * kC * kC;
+  {
+    const std::uint32_t t = tid / 4, s0 = (tid % 4) * 16;
+    float kk[16], qk[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) kk[j] = qk[j] = 0.0f;
+    for (int i = 0; i < kD; i += 8) {
+      const int4 kt4 = *reinterpret_cast<const int4*>(&u.in.kb[t][i]);
+      const int4 qt4 = *reinterpret_cast<const int4*>(&u.in.qb[t][i]);
+      const std::uint16_t* kt = reinterpret_cast<const std::uint16_t*>(&kt4);
+      const std::uint16_t* qt = reinterpret_cast<const std::uint16_t*>(&qt4);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int4 ks4 = *reinterpret_cast<const int4*>(&u.in.kb[s0 + j][i]);
+        const std::uint16_t* ks = reinterpret_cast<const std::uint16_t*>(&ks4);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float kse = Bf(ks[e]);
+          kk[j] += Bf(kt[e]) * kse;
+          qk[j] += Bf(qt[e]) * kse;
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const std::uint32_t s = s0 + j;
+      const float dec = expf(G[t] - G[s]);
+      am[t][s] = s < t ? B[t] * dec * kk[j] : 0.0f;
+      Pm[mat + t * kC + s] = s <= t ? dec * qk[j] : 0.0f;
+    }
+  }
+  __syncthreads();
+  // T = (I + A)^-1 by rows: T[t][c] = -sum_{s=c}^{t-1} A[t][s] T[s][c] (c < t), 1 on the diagonal. One wave; LDS
+  // accesses of a wave complete in order, so rows need no block barrier.
+  if (tid < kC) {
+    const std::uint32_t col = tid;
+    for (std::uint32_t t = 0; t < kC; ++t) {
+      float v = col == t ? 1.0f : 0.0f;
+      if (col < t)
+        for (std::uint32_t s = col; s < t; ++s) v -= am[t][s] * u.tm[s][col];
+      u.tm[t][col] = v;
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  __syncthreads();
+  for (std::uint32_t e = tid; e < kC * kC; e += blockDim.x) Tm[mat + e] = u.tm[e / kC][e % kC];
+  if (tid < kC) Gc[(static_cast<std::size_t>(c) * Hv + h) * kC + tid] = G[tid];
+}
+
+// grid (n_seq * Hv * 4), block 256: block -> (sequence, head, 32 value columns); walks the sequence's chunks.
+// o [tokens][Hv][128] fp32; state [seq][Hv][128][128] read as the initial state and overwritten with the final one.
+extern "C" __global__ void __launch_bounds__(256) halo_gdn_chunk_scan(
+    const std::uint16_t* __restrict__ q, const std::uint16_t* __restrict__ k, const std::uint16_t* __restrict__ v,
+    const float* __restrict__ beta, const std::uint32_t* __restrict__ chunks, const std::uint32_t* __restrict__ seqs,
+    const float* __restrict__ Tm, const float* __restrict__ Pm, const float* __restrict__ Gc,
+    float* __restrict__ state, float* __restrict__ o, std::uint32_t Hv, std::uint32_t Hk) {
+  __shared__ float S0[kD][kJBlock];
+  __shared__ float Zd[kC][kJBlock + 1];
+  __shared__ float tm[kC][kC];
+  __shared__ float pm[kC][kC];
+  __shared__ float G[kC], Bt[kC], Wd[kC];
+  const std::uint32_t b = blockIdx.x, jb = b % 4, h = (b / 4) % Hv, sq = b / (4 * Hv), kh = h % Hk;
+  const std::uint32_t tid = threadIdx.x;
+  const std::uint32_t c0 = seqs[sq * 2], nc = seqs[sq * 2 + 1];
+  float* St = state + (static_cast<std::size_t>(sq) * Hv + h) * kD * kD;
+  for (std::uint32_t e = tid; e < kD * kJBlock; e += blockDim.x)
+    S0[e / kJBlock][e % kJBlock] = St[static_cast<std::size_t>(e / kJBlock) * kD + jb * kJBlock + e % kJBlock];
+  const std::uint32_t t = tid / 4, jg = tid % 4;             // rows of the chunk x 8 columns
+  const std::uint32_t si = tid % kD, sh = tid / kD;          // state row x 16 columns
+  const float qscale = 1.0f / sqrtf(static_cast<float>(kD));
+  for (std::uint32_t ci = 0; ci < nc; ++ci) {
+    const std::uint32_t c = c0 + ci, start = chunks[c * 3], L = chunks[c * 3 + 1];
+    const std::size_t mat = (static_cast<std::size_t>(c) * Hv + h) * kC * kC;
+    __syncthreads();
+    for (std::uint32_t e = tid * 4; e < kC * kC; e += blockDim.x * 4) {
+      *reinterpret_cast<float4*>(&tm[0][0] + e) = *reinterpret_cast<const float4*>(Tm + mat + e);
+      *reinterpret_cast<float4*>(&pm[0][0] + e) = *reinterpret_cast<const float4*>(Pm + mat + e);
+    }
+    if (tid < kC) {
+      G[tid] = Gc[(static_cast<std::size_t>(c) * Hv + h) * kC + tid];
+      Bt[tid] = tid < L ? beta[static_cast<std::size_t>(start + tid) * Hv + h] : 0.0f;
+    }
+    __syncthreads();
+    if (tid < kC) Wd[tid] = expf(G[kC - 1] - G[tid]);
+    // X = K S0, Y = Q S0 (row t, 8 columns)
+    float X[8], Y[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) X[j] = Y[j] = 0.0f;
+    const bool live = t < L;
+    const std::size_t krow = (static_cast<std::size_t>(start + t) * Hk + kh) * kD;
+    for (int i = 0; i < kD; i += 8) {
+      int4 k4 = make_int4(0, 0, 0, 0), q4 = make_int4(0, 0, 0, 0);
+      if (live) {
+        k4 = *reinterpret_cast<const int4*>(k + krow + i);
+        q4 = *reinterpret_cast<const int4*>(q + krow + i);
+      }
+      const std::uint16_t* kv = reinterpret_cast<const std::uint16_t*>(&k4);
+      const std::uint16_t* qv = reinterpret_cast<const std::uint16_t*>(&q4);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float ke = Bf(kv[e]), qe = Bf(qv[e]);
+        const float4 s_lo = *reinterpret_cast<const float4*>(&S0[i + e][jg * 8]);
+        const float4 s_hi = *reinterpret_cast<const float4*>(&S0[i + e][jg * 8 + 4]);
+        X[0] += ke * s_lo.x; X[1] += ke * s_lo.y; X[2] += ke * s_lo.z; X[3] += ke * s_lo.w;
+        X[4] += ke * s_hi.x; X[5] += ke * s_hi.y; X[6] += ke * s_hi.z; X[7] += ke * s_hi.w;
+        Y[0] += qe * s_lo.x; Y[1] += qe * s_lo.y; Y[2] += qe * s_lo.z; Y[3] += qe * s_lo.w;
+        Y[4] += qe * s_hi.x; Y[5] += qe * s_hi.y; Y[6] += qe * s_hi.z; Y[7] += qe * s_hi.w;
+      }
+    }
+    const float gam = expf(G[t]);
+    {
+      int4 v4 = make_int4(0, 0, 0, 0);
+      if (live) v4 = *reinterpret_cast<const int4*>(v + (static_cast<std::size_t>(start + t) * Hv + h) * kD +
+                                                     jb * kJBlock + jg * 8);
+      const std::uint16_t* vv = reinterpret_cast<const std::uint16_t*>(&v4);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) Zd[t][jg * 8 + j] = Bt[t] * (Bf(vv[j]) - gam * X[j]);
+    }
+    __syncthreads();
+    float D[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) D[j] = 0.0f;
+    for (std::uint32_t s = 0; s <= t; ++s) {
+      const float w = tm[t][s];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) D[j] += w * Zd[s][jg * 8 + j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) Zd[t][jg * 8 + j] = D[j];
+    __syncthreads();
+    if (live) {
+      float O[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) O[j] = gam * Y[j];
+      for (std::uint32_t s = 0; s <= t; ++s) {
+        const float w = pm[t][s];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) O[j] += w * Zd[s][jg * 8 + j];
+      }
+      float* orow = o + (static_cast<std::size_t>(start + t) * Hv + h) * kD + jb * kJBlock + jg * 8;
+      *reinterpret_cast<float4*>(orow) = make_float4(O[0] * qscale, O[1] * qscale, O[2] * qscale, O[3] * qscale);
+      *reinterpret_cast<float4*>(orow + 4) = make_float4(O[4] * qscale, O[5] * qscale, O[6] * qscale, O[7] * qscale);
+    }
+    // S <- gamma_C S + K^T diag(exp(G_C - G_t)) Delta   (row si, 16 columns)
+    const float gc = expf(G[kC - 1]);
+    float acc[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = gc * S0[si][sh * 16 + j];
+    for (std::uint32_t tt = 0; tt < L; ++tt) {
+      const float w = Bf(k[(static_cast<std::size_t>(start + tt) * Hk + kh) * kD + si]) * Wd[tt];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[j] += w * Zd[tt][sh * 16 + j];
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) S0[si][sh * 16 + j] = acc[j];
+  }
+  __syncthreads();
+  for (std::uint32_t e = tid; e < kD * kJBlock; e += blockDim.x)
+    St[static_cast<std::size_t>(e / kJBlock) * kD + jb * kJBlock + e % kJBlock] = S0[e / kJBlock][e % kJBlock];
+}

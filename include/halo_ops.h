@@ -147,6 +147,21 @@ int halo_op_attn_decode(halo_engine* eng, const halo_paged_kv* kv, const float* 
 int halo_op_kv_append(halo_engine* eng, const halo_paged_kv* kv, const float* k, const float* v, char* err,
                       size_t errlen);
 
+/* Chunked prefill (C = 64) over a ragged batch of sequences (halo_gdn_c16_prep / halo_gdn_c16_scan*,
+ * src/kernels/core.hip:6592-7421, here with 64-token chunks): the same recurrence over every token of every
+ * sequence, outputs o [tokens][Hv][d] fp32, state [seq][Hv][d][d] read as the initial state and overwritten with the
+ * final one. q, k [tokens][Hk][d] and v [tokens][Hv][d] bf16; g, beta [tokens][Hv] fp32. The chunk tables are
+ * device buffers built by halo_gdn_chunk_table. Two launches: a parallel pass over all (chunk, head) pairs, then a
+ * scan per (sequence, head, 32 value columns). */
+/* Host helper: from seqlens [n_seq] fills chunks [n][3] = {first token, length, sequence} and seqs [n_seq][2] =
+ * {first chunk, chunk count} (either output may be NULL to count); returns the number of chunks. */
+uint32_t halo_gdn_chunk_table(const uint32_t* seqlens, uint32_t n_seq, uint32_t* chunks, uint32_t* seqs);
+size_t halo_op_gdn_prefill_workspace_bytes(uint32_t n_chunks, uint32_t v_heads);
+int halo_op_gdn_prefill(halo_engine* eng, const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
+                        const float* beta, const uint32_t* chunks, const uint32_t* seqs, uint32_t n_chunks,
+                        uint32_t n_seq, float* state, float* o, uint32_t v_heads, uint32_t k_heads, uint32_t head_dim,
+                        void* ws, size_t ws_bytes, char* err, size_t errlen);
+
 #ifdef __cplusplus
 }
 #endif

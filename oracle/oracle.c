@@ -381,6 +381,16 @@ void or_gdn_step(float* S, uint32_t d, const float* q, const float* k, const flo
   free(u);
 }
 
+/* Token-serial prefill: the reference's prefill is defined as T decode steps (tests/gpu DeltaNetPrefillEqualsDecodeSteps,
+ * reference tests/gpu/quant_gpu_test.cpp:1043-1303). */
+void or_gdn_sequence(float* S, uint32_t d, uint32_t T, const float* q, size_t qstride, const float* k, size_t kstride,
+                     const float* v, size_t vstride, const float* g, const float* beta, size_t gstride, float* o,
+                     size_t ostride) {
+  for (uint32_t t = 0; t < T; ++t)
+    or_gdn_step(S, d, q + t * qstride, k + t * kstride, v + t * vstride, g[t * gstride], beta[t * gstride],
+                o + t * ostride);
+}
+
 /* reference: src/model/reference.cpp:492-521 (dense branch: scores in double rounded to fp32, scaled by 1/sqrt(hd),
  * max-subtracted exp, double denominator, p = score/denom in fp32, o += p * v). */
 void or_attention_head(const float* q, const float* k, const float* v, uint32_t n, uint32_t hd, size_t kv_stride,

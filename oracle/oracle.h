@@ -79,6 +79,12 @@ void or_moe_token(const float* x, uint32_t hidden, uint32_t ff, uint32_t n_exper
  * length d; decay = exp(g); o[j] = (S_new q)[j] / sqrt(d). */
 void or_gdn_step(float* S, uint32_t d, const float* q, const float* k, const float* v, float g, float beta, float* o);
 
+/* A whole sequence of T tokens through or_gdn_step for one value head; q, k, v rows at the given strides (floats),
+ * g, beta at stride gstride; S value-major [d][d] in place; o rows at ostride. */
+void or_gdn_sequence(float* S, uint32_t d, uint32_t T, const float* q, size_t qstride, const float* k, size_t kstride,
+                     const float* v, size_t vstride, const float* g, const float* beta, size_t gstride, float* o,
+                     size_t ostride);
+
 /* ---- GQA decode attention ------------------------------------------------ */
 /* One query head over n positions: k, v rows of length hd at stride `kv_stride` floats;
  * o = softmax(q.k / sqrt(hd)) v. */

@@ -48,6 +48,7 @@ _ORACLE_SIGS = {
     "or_moe_token": (None, [_PF, _U32, _U32, _U32, _U32, _PF, _PI8, _PU16, _PI8, _PU16, _PI8, _PU16, _PI8,
                             _PU16, _U32, _PF, _PF, _PU32, _PF]),
     "or_gdn_step": (None, [_PF, _U32, _PF, _PF, _PF, _F32, _F32, _PF]),
+    "or_gdn_sequence": (None, [_PF, _U32, _U32, _VP, _SZ, _VP, _SZ, _VP, _SZ, _VP, _VP, _SZ, _VP, _SZ]),
     "or_attention_head": (None, [_PF, _PF, _PF, _U32, _U32, _SZ, _PF]),
 }
 

@@ -7,6 +7,7 @@ terms (sum |S| |k|, the reference's bound style); BASELINE's 1e-3 is looser.
 import numpy as np
 import pytest
 
+import halo_amd as H
 import oracle_py as O
 
 pytestmark = pytest.mark.gpu
@@ -60,3 +61,91 @@ def test_gdn_decode_steps(dev, S):
         assert np.allclose(got_s, want, rtol=1e-5, atol=1e-5 * smag), f"state after step {step}"
         omag = np.abs(wo).max()
         assert np.allclose(got_o, wo, rtol=1e-4, atol=1e-5 * omag), f"output of step {step}"
+
+
+def to_bf16(x):
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def from_bf16(b):
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def prefill_case(dev, rng, seqlens, Hv=32, Hk=16, zero_state=False):
+    T = sum(seqlens)
+    q = rng.normal(0, 1, (T, Hk, D)).astype(np.float32)
+    k = rng.normal(0, 1, (T, Hk, D)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=-1, keepdims=True)
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    v = rng.normal(0, 1, (T, Hv, D)).astype(np.float32)
+    g = (-np.log1p(np.exp(rng.normal(0, 1, (T, Hv))))).astype(np.float32)
+    beta = (1 / (1 + np.exp(-rng.normal(0, 1, (T, Hv))))).astype(np.float32)
+    qb, kb, vb = to_bf16(q), to_bf16(k), to_bf16(v)
+    nseq = len(seqlens)
+    state = np.zeros((nseq, Hv, D, D), np.float32) if zero_state else \
+        rng.normal(0, 0.05, (nseq, Hv, D, D)).astype(np.float32)
+    L = H.lib()
+    sl = np.array(seqlens, np.uint32)
+    nch = L.halo_gdn_chunk_table(sl.ctypes.data, nseq, None, None)
+    chunks = np.zeros((nch, 3), np.uint32)
+    seqs = np.zeros((nseq, 2), np.uint32)
+    L.halo_gdn_chunk_table(sl.ctypes.data, nseq, chunks.ctypes.data, seqs.ctypes.data)
+    bufs = {n: dev.to_device(a) for n, a in dict(q=qb, k=kb, v=vb, g=g, beta=beta, chunks=chunks, seqs=seqs,
+                                                    state=state).items()}
+    go = dev.array((T, Hv, D), np.float32)
+    ws = dev.array(L.halo_op_gdn_prefill_workspace_bytes(nch, Hv), np.uint8)
+    dev.op("gdn_prefill", bufs["q"].ptr, bufs["k"].ptr, bufs["v"].ptr, bufs["g"].ptr, bufs["beta"].ptr,
+           bufs["chunks"].ptr, bufs["seqs"].ptr, nch, nseq, bufs["state"].ptr, go.ptr, Hv, Hk, D, ws.ptr, ws.nbytes)
+    inputs = (from_bf16(qb), from_bf16(kb), from_bf16(vb), g, beta)
+    return go.download(), bufs["state"].download(), state, inputs
+
+
+def oracle_prefill(seqlens, state0, inputs, heads, Hv=32, Hk=16):
+    q, k, v, g, beta = inputs
+    T = sum(seqlens)
+    o = np.zeros((T, Hv, D), np.float32)
+    st = state0.copy()
+    O_ = O.oracle()
+    tok = 0
+    for s, n in enumerate(seqlens):
+        for h in heads:
+            S = np.ascontiguousarray(state0[s, h].T)
+            qh = np.ascontiguousarray(q[tok:tok + n, h % Hk])
+            kh = np.ascontiguousarray(k[tok:tok + n, h % Hk])
+            vh = np.ascontiguousarray(v[tok:tok + n, h])
+            gh = np.ascontiguousarray(g[tok:tok + n, h])
+            bh = np.ascontiguousarray(beta[tok:tok + n, h])
+            oh = np.zeros((n, D), np.float32)
+            O_.or_gdn_sequence(S, D, n, qh.ctypes.data, D, kh.ctypes.data, D, vh.ctypes.data, D, gh.ctypes.data,
+                               bh.ctypes.data, 1, oh.ctypes.data, D)
+            o[tok:tok + n, h] = oh
+            st[s, h] = S.T
+        tok += n
+    return o, st
+
+
+def _close(got, want, what):
+    mag = np.abs(want).max()
+    err = np.abs(got - want)
+    assert np.all(err <= 1e-3 * np.abs(want) + 1e-4 * mag), f"{what}: max err {err.max():.3g} (mag {mag:.3g})"
+
+
+@pytest.mark.parametrize("seqlens,zero", [([37, 130, 64, 200], False), ([1, 65], True)])
+def test_gdn_prefill_matches_stepping(dev, seqlens, zero):
+    rng = np.random.default_rng(sum(seqlens))
+    got_o, got_s, s0, inputs = prefill_case(dev, rng, seqlens, zero_state=zero)
+    want_o, want_s = oracle_prefill(seqlens, s0, inputs, range(32))
+    _close(got_o, want_o, "outputs")
+    _close(got_s, want_s, "final state")
+
+
+def test_gdn_prefill_c3_full(dev):
+    """BASELINE config C3 prefill: ragged {37, 512, 2048, 8191} tokens; heads 0 and 17 checked against stepping."""
+    seqlens = [37, 512, 2048, 8191]
+    rng = np.random.default_rng(3)
+    got_o, got_s, s0, inputs = prefill_case(dev, rng, seqlens, zero_state=True)
+    want_o, want_s = oracle_prefill(seqlens, s0, inputs, [0, 17])
+    for h in (0, 17):
+        _close(got_o[:, h], want_o[:, h], f"outputs head {h}")
+        _close(got_s[:, h], want_s[:, h], f"final state head {h}")

@@ -61,6 +61,10 @@ def run_gpu(args):
             return run_membw(args, dev, H, res)
         if args.mode == "moe":
             return run_moe(args, dev, H, res)
+        if args.mode == "gdn":
+            return run_gdn(args, dev, H, res)
+        if args.mode == "c4":
+            return run_c4(args, dev, H, res)
         # ---------------- C1 pass at M=1 (the bench value) and the M sweep ----------------
         per_copy = sum(q8_bytes(r, c) for r, c in C1_SHAPES)
         copies = max(2, -(-MIN_ROTATION_BYTES // per_copy))
@@ -213,6 +217,162 @@ def run_moe(args, dev, H, res):
     return res
 
 
+def run_c4(args, dev, H, res):
+    """C4: the synthetic hybrid model (48 layers, 36 DeltaNet + 12 GQA, MoE 512 x top-10 + shared, vocab 151936,
+    Q8_0 weights seeded on the device). Session 0 prefills the 8192-token shared prefix one token per step (the
+    captured decode step, prompt tokens fed on the device); sessions 1-3 fork its state and share its KV pages.
+    1 session: session 0 alone, 256 suffix tokens then 128 greedy decode steps (timed). 4 sessions: each with a
+    distinct 256-token suffix, read the prefix once per step, then 128 greedy decode steps (timed)."""
+    P, SUF, DEC = 8192, 256, 128
+    t0 = time.perf_counter()
+    cfg = H.c4_config(max_sessions=4, prefix_tokens=P, max_context=P + SUF + DEC)
+    model = H.Model(dev, cfg, seed=2026)
+    dev.sync()
+    t_build = time.perf_counter() - t0
+    log(f"[bench] c4: weights {model.weight_bytes / 1e9:.1f} GB seeded in {t_build:.1f} s")
+    rng = np.random.default_rng(4)
+    prefix = rng.integers(0, cfg.vocab, P).astype(np.uint32)
+    prompts = [np.concatenate([prefix, rng.integers(0, cfg.vocab, SUF).astype(np.uint32)]) for _ in range(4)]
+    try:
+        model.set_session(0, prompts[0])
+        t0 = time.perf_counter()
+        dev.timer_start()
+        model.run(1, P)
+        ms_prefix = dev.timer_stop()
+        log(f"[bench] c4: prefix {P} tokens in {ms_prefix / 1e3:.1f} s (one token per step)")
+        for s in (1, 2, 3):
+            model.fork(0, s)
+        if args.eager:  # per-kernel event timing of eager steps at 1 and 4 sessions
+            prof = {}
+            model.step_eager(1)
+            dev.profile_begin()
+            for _ in range(10):
+                model.step_eager(1)
+            prof["S1"] = dev.profile_end()
+            model.fork(1, 0)
+            for s in range(4):
+                model.set_session(s, prompts[s], nkv=P)
+            model.step_eager(4, P)
+            dev.profile_begin()
+            for _ in range(10):
+                model.step_eager(4, P)
+            prof["S4"] = dev.profile_end()
+            for k, v in prof.items():
+                tot = sum(us for _, us in v.values()) / 10
+                log(f"[bench] c4 eager {k}: {tot:.1f} us of kernels per step")
+                for name, (n, us) in sorted(v.items(), key=lambda kv: -kv[1][1])[:14]:
+                    log(f"    {name:40s} {n // 10:5d}/step {us / 10:9.1f} us/step {us / n:8.2f} us/launch")
+            res["c4"] = {"profile": {k: {n: [c, round(u, 1)] for n, (c, u) in v.items()} for k, v in prof.items()}}
+            return res
+        # 1 session
+        model.run(1, SUF)
+        dev.sync()
+        dev.timer_start()
+        model.run(1, DEC)
+        ms1 = dev.timer_stop()
+        tok1 = DEC / (ms1 * 1e-3)
+        log(f"[bench] c4: 1 session {ms1 / DEC:.3f} ms/token, {tok1:.1f} tok/s")
+        # 4 sessions: session 0 back at the end of the prefix (session 1 still holds that state)
+        model.fork(1, 0)
+        for s in range(4):
+            model.set_session(s, prompts[s], nkv=P)
+        model.run(4, SUF, prefix=P)
+        dev.sync()
+        dev.timer_start()
+        model.run(4, DEC, prefix=P)
+        ms4 = dev.timer_stop()
+        tok4 = 4 * DEC / (ms4 * 1e-3)
+        log(f"[bench] c4: 4 sessions {ms4 / DEC:.3f} ms/step, {tok4:.1f} tok/s aggregate")
+        gen = [model.history(s, P + SUF + DEC)[P + SUF:].tolist()[:8] for s in range(4)]
+        res["c4"] = {"decode_tok_s_1_session": round(tok1, 1), "ms_per_token_1_session": round(ms1 / DEC, 3),
+                     "decode_tok_s_4_sessions": round(tok4, 1), "ms_per_step_4_sessions": round(ms4 / DEC, 3),
+                     "prefix_tokens": P, "suffix_tokens": SUF, "decode_steps": DEC,
+                     "prefix_ms_token_serial": round(ms_prefix, 1), "weight_GB": round(model.weight_bytes / 1e9, 2),
+                     "first_generated": gen}
+    finally:
+        model.close()
+    res["roofline"] = res.get("roofline")
+    return res
+
+
+def run_gdn(args, dev, H, res):
+    """C3: Gated DeltaNet decode (S = 4 sessions, states rotated over > 256 MB) and the ragged chunked prefill
+    {37, 512, 2048, 8191} tokens (bf16 inputs, fp32 state)."""
+    S, Hv, Hk, D = 4, 32, 16, 128
+    out = {}
+    copies = 40  # 40 x 8 MiB of state
+    states = [dev.array((S, Hv, D, D), np.float32) for _ in range(copies)]
+    for i, st in enumerate(states):
+        dev.op("synth_f32", st.ptr, S * Hv * D * D, 100 + i, 0.05)
+    q, k = dev.array((S, Hk, D), np.float32), dev.array((S, Hk, D), np.float32)
+    v, o = dev.array((S, Hv, D), np.float32), dev.array((S, Hv, D), np.float32)
+    g, b = dev.array((S, Hv), np.float32), dev.array((S, Hv), np.float32)
+    for i, a in enumerate((q, k, v)):
+        dev.op("synth_f32", a.ptr, a.nbytes // 4, 200 + i, 0.09)
+    dev.op("synth_f32", g.ptr, S * Hv, 210, 0.1)
+    dev.op("synth_f32", b.ptr, S * Hv, 211, 0.1)
+    dev.sync()
+    dev.begin_capture()
+    for st in states:
+        dev.op("gdn_decode", st.ptr, q.ptr, k.ptr, v.ptr, g.ptr, b.ptr, o.ptr, S, Hv, Hk, D)
+    gr = dev.end_capture()
+    dev.launch_graph(gr)
+    dev.sync()
+    dev.timer_start()
+    for _ in range(25):
+        dev.launch_graph(gr)
+    ms = dev.timer_stop()
+    dev.free_graph(gr)
+    us = ms * 1e3 / (25 * copies)
+    nbytes = 2 * S * Hv * D * D * 4 + S * (2 * Hk + 2 * Hv) * D * 4 + 2 * S * Hv * 4
+    out["decode_S4"] = {"us_per_step": round(us, 3), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    del states
+    # prefill
+    seqlens = [37, 512, 2048, 8191]
+    T = sum(seqlens)
+    L = H.lib()
+    sl = np.array(seqlens, np.uint32)
+    nch = L.halo_gdn_chunk_table(sl.ctypes.data, len(seqlens), None, None)
+    chunks = np.zeros((nch, 3), np.uint32)
+    seqs = np.zeros((len(seqlens), 2), np.uint32)
+    L.halo_gdn_chunk_table(sl.ctypes.data, len(seqlens), chunks.ctypes.data, seqs.ctypes.data)
+    gch, gsq = dev.to_device(chunks), dev.to_device(seqs)
+    rng = np.random.default_rng(0)
+
+    def bf16(x):
+        u = np.ascontiguousarray(x, np.float32).view(np.uint32)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    qh = rng.normal(0, 1, (T, Hk, D)).astype(np.float32)
+    kh = rng.normal(0, 1, (T, Hk, D)).astype(np.float32)
+    qh /= np.linalg.norm(qh, axis=-1, keepdims=True)
+    kh /= np.linalg.norm(kh, axis=-1, keepdims=True)
+    pq, pk = dev.to_device(bf16(qh)), dev.to_device(bf16(kh))
+    pv = dev.to_device(bf16(rng.normal(0, 1, (T, Hv, D))))
+    pg = dev.to_device((-np.log1p(np.exp(rng.normal(0, 1, (T, Hv))))).astype(np.float32))
+    pb = dev.to_device((1 / (1 + np.exp(-rng.normal(0, 1, (T, Hv))))).astype(np.float32))
+    pst = dev.array((len(seqlens), Hv, D, D), np.float32)
+    po = dev.array((T, Hv, D), np.float32)
+    ws = dev.array(L.halo_op_gdn_prefill_workspace_bytes(nch, Hv), np.uint8)
+
+    def prefill():
+        dev.op("gdn_prefill", pq.ptr, pk.ptr, pv.ptr, pg.ptr, pb.ptr, gch.ptr, gsq.ptr, nch, len(seqlens), pst.ptr,
+               po.ptr, Hv, Hk, D, ws.ptr, ws.nbytes)
+    prefill()
+    dev.sync()
+    reps = 5
+    dev.timer_start()
+    for _ in range(reps):
+        prefill()
+    ms = dev.timer_stop() / reps
+    flops = T * Hv * (3 * D * D + 3 * 64 * D) * 2  # the survey's per-token count
+    out["prefill_C3"] = {"tokens": T, "ms": round(ms, 3), "tokens_per_s": round(T / (ms * 1e-3)),
+                         "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 2)}
+    log(f"[bench] gdn {out}")
+    res["gdn"] = out
+    res["roofline"] = None
+    return res
+
+
 def run_membw(args, dev, H, res):
     """Streaming-read yardstick: one launch reads one buffer of the given size; buffers rotate over >= 600 MB."""
     out = {}
@@ -361,7 +521,7 @@ def main():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--eager", action="store_true", help="launch without graphs (for profiling kernel durations)")
-    p.add_argument("--mode", choices=["all", "c0", "membw", "moe"], default="all",
+    p.add_argument("--mode", choices=["all", "c0", "membw", "moe", "gdn", "c4"], default="all",
                    help="c0: only the C0 GEMV loop (for profiling one kernel shape)")
     args = p.parse_args()
     if args.gpus != 1:
@@ -369,8 +529,9 @@ def main():
               "(the path is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
         sys.exit(2)
     res = run_gpu(args)
-    if args.mode in ("c0", "membw", "moe"):
-        print(json.dumps({k: res.get(k) for k in ("roofline", "c0_tilings", "membw", "moe")}), flush=True)
+    if args.mode in ("c0", "membw", "moe", "gdn", "c4"):
+        print(json.dumps({k: res.get(k) for k in ("roofline", "c0_tilings", "membw", "moe", "gdn", "c4")}),
+              flush=True)
         return
     line = {
         "metric": "Q8_0 GEMV achieved HBM GB/s; decode tokens/s at 1 and 4 sessions",

@@ -1,0 +1,477 @@
+// halo_model: weights, sessions and the captured decode step of the synthetic hybrid model.
+//
+// Reference: FlashNextGpu::Init (src/engine/flash_next_gpu.cpp:256-409) allocates weights and scratch;
+// Record / Run (847-1047) record one token through every layer into a graph and replay it with per-step values in
+// device memory (HaloStepParam, src/kernels/step_params.h); StepBatch (src/engine/batch_decode.cpp:629-817) runs B
+// sessions per step with weights read once; ForkSession (flash_next_gpu.hpp:347-350) shares prefix pages.
+#include "halo_model.h"
+
+#include <map>
+#include <memory>
+#include <utility>
+#include <vector>
+
+#include "engine.hpp"
+
+using namespace halo::engine;
+
+namespace {
+
+struct Q8 {
+  halo_buffer qs{}, d{};
+  halo_q8_matrix m{};
+};
+
+struct Layer {
+  bool attn = false;
+  halo_buffer attn_norm{}, ffn_norm{};
+  // Gated DeltaNet
+  Q8 qkv, z, out;
+  halo_buffer ab{}, conv_w{}, a{}, dt{}, norm_w{};
+  // attention
+  Q8 qg, k, v, o;
+  halo_buffer q_norm{}, k_norm{}, k_pool{}, v_pool{};
+  // MoE
+  halo_buffer router{}, shared_gate{};
+  Q8 gate, up, down, sgate, sup, sdown;
+  halo_moe_weights moe{};
+  std::uint32_t gdn_index = 0;  // index among DeltaNet layers (state slot)
+};
+
+}  // namespace
+
+struct halo_model {
+  halo_engine* eng = nullptr;
+  halo_device* dev = nullptr;
+  halo_model_config c{};
+  std::vector<Layer> layers;
+  Q8 embd, head;
+  halo_buffer out_norm{};
+  std::uint32_t n_gdn = 0, n_attn = 0, max_pages = 0, prefix_pages = 0, total_pages = 0, conv_ch = 0;
+  // state
+  halo_buffer gdn_state{}, conv_state{}, pages{}, nkv{}, tokens{}, prompt{}, prompt_len{}, history{}, produced{};
+  // step scratch
+  halo_buffer res{}, xn{}, xq{}, xs{}, qkv{}, zo{}, abo{}, q{}, k{}, v{}, g{}, beta{}, o{}, oq{}, os{}, delta{};
+  halo_buffer qgo{}, ko{}, vo{}, aq{}, agate{}, ao{}, moe_ws{}, attn_ws{}, logits{}, argmax_part{};
+  std::size_t moe_ws_bytes = 0, attn_ws_bytes = 0;
+  std::vector<halo_buffer> owned;
+  std::map<std::pair<std::uint32_t, std::uint32_t>, halo_graph> graphs;
+  std::uint64_t weight_bytes = 0, device_bytes = 0;
+};
+
+namespace {
+
+int Alloc(halo_model* m, std::size_t bytes, halo_buffer* b, char* err, std::size_t errlen) {
+  if (halo_alloc(m->dev, bytes, b, err, errlen) != 0) return -1;
+  m->owned.push_back(*b);
+  m->device_bytes += bytes;
+  return 0;
+}
+
+int SynthF32(halo_model* m, halo_buffer* b, std::size_t n, std::uint64_t seed, float sigma, float mean, char* err,
+             std::size_t errlen) {
+  if (Alloc(m, n * 4, b, err, errlen) != 0) return -1;
+  if (halo_op_synth_f32(m->eng, static_cast<float*>(b->device), n, seed, sigma, err, errlen) != 0) return -1;
+  m->weight_bytes += n * 4;
+  if (mean != 0.0f) {
+    const halo_arg a[] = {Ptr(b->device), Val<std::uint64_t>(n), Val(1.0f), Val(mean)};
+    return Launch(m->eng, "halo_affine_f32", D3(static_cast<std::uint32_t>(std::min<std::size_t>(CeilDiv(n, 256), 4096))),
+                  D3(256), a, err, errlen);
+  }
+  return 0;
+}
+
+int SynthQ8(halo_model* m, Q8* w, std::uint32_t rows, std::uint32_t cols, std::uint64_t seed, char* err,
+            std::size_t errlen) {
+  const std::uint32_t qstride = cols;
+  if (Alloc(m, static_cast<std::size_t>(rows) * qstride, &w->qs, err, errlen) != 0 ||
+      Alloc(m, static_cast<std::size_t>(rows) * (cols / 32) * 2, &w->d, err, errlen) != 0)
+    return -1;
+  w->m = halo_q8_matrix{static_cast<const int8_t*>(w->qs.device), static_cast<const uint16_t*>(w->d.device), rows,
+                        cols, qstride, 0};
+  m->weight_bytes += static_cast<std::uint64_t>(rows) * (cols / 32) * 34;
+  return halo_op_synth_q8(m->eng, static_cast<int8_t*>(w->qs.device), static_cast<uint16_t*>(w->d.device), rows, cols,
+                          qstride, seed, 0.02f, err, errlen);
+}
+
+template <typename T>
+T* P(const halo_buffer& b) {
+  return static_cast<T*>(b.device);
+}
+
+halo_paged_kv KvDesc(halo_model* m, const Layer& L, std::uint32_t S, std::uint32_t prefix) {
+  halo_paged_kv kv{};
+  kv.k_pool = P<float>(L.k_pool);
+  kv.v_pool = P<float>(L.v_pool);
+  kv.pages = P<uint32_t>(m->pages);
+  kv.nkv = P<uint32_t>(m->nkv);
+  kv.sessions = S;
+  kv.kv_heads = m->c.kv_heads;
+  kv.head_dim = m->c.head_dim;
+  kv.max_pages = m->max_pages;
+  kv.prefix = prefix;
+  kv.max_context = m->c.max_context;
+  return kv;
+}
+
+int Check(const halo_model_config* c, char* err, std::size_t errlen) {
+  if (c->hidden % 1024 != 0 || c->hidden > 4096)
+    return SetErr(err, errlen, "model: hidden %u must be 1024..4096 in steps of 1024", c->hidden), -1;
+  if (c->gdn_head_dim != 128 || c->head_dim != 256 || c->conv_kernel < 1 || c->conv_kernel > 8)
+    return SetErr(err, errlen, "model: DeltaNet head dim 128, attention head dim 256, conv kernel 1..8"), -1;
+  if (c->max_sessions == 0 || c->max_sessions > 16 || c->max_sessions * (c->q_heads / c->kv_heads) > 32)
+    return SetErr(err, errlen, "model: %u sessions unsupported", c->max_sessions), -1;
+  if (c->prefix_tokens % 64 != 0 || c->prefix_tokens > c->max_context || c->attn_interval == 0)
+    return SetErr(err, errlen, "model: prefix %u must be a multiple of 64 within the context", c->prefix_tokens), -1;
+  if ((2 * c->gdn_k_heads + c->gdn_v_heads) * c->gdn_head_dim % 256 != 0)
+    return SetErr(err, errlen, "model: DeltaNet channels must be a multiple of 256"), -1;
+  if (c->rotary_dim > 128 || c->rotary_dim % 64 != 0)
+    return SetErr(err, errlen, "model: rotary dim must be 64 or 128"), -1;
+  return 0;
+}
+
+int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std::size_t errlen) {
+  const halo_model_config& c = m->c;
+  const std::uint32_t H = c.hidden, Hv = c.gdn_v_heads, Hk = c.gdn_k_heads, d = c.gdn_head_dim;
+  const std::uint32_t Dv = Hv * d, C = m->conv_ch, Hq = c.q_heads, Hkv = c.kv_heads, hd = c.head_dim;
+  const float eps = c.rms_eps;
+  halo_engine* eng = m->eng;
+  // embedding
+  {
+    const halo_arg a[] = {Ptr(m->embd.qs.device), Ptr(m->embd.d.device), Ptr(m->tokens.device), Ptr(m->res.device),
+                          U32(H), U32(H)};
+    if (Launch(eng, "halo_embed_q8", D3(S), D3(256), a, err, errlen) != 0) return -1;
+  }
+  bool have_delta = false;
+  auto norm = [&](const halo_buffer& w, bool quant) {
+    const halo_arg a[] = {Ptr(m->res.device), Ptr(have_delta ? m->delta.device : nullptr), Ptr(w.device),
+                          Ptr(m->xn.device), Ptr(quant ? m->xq.device : nullptr), Ptr(m->xs.device), U32(H), Val(eps)};
+    have_delta = false;
+    return Launch(eng, "halo_add_rmsnorm_q8", D3(S), D3(256), a, err, errlen);
+  };
+  auto gemv = [&](const Q8& w, const halo_buffer& xq, const halo_buffer& xs, const halo_buffer& y) {
+    return halo_op_matvec_q8a8(eng, &w.m, P<int8_t>(xq), P<float>(xs), P<float>(y), S, w.m.rows, err, errlen);
+  };
+  for (auto& L : m->layers) {
+    if (norm(L.attn_norm, true) != 0) return -1;
+    if (!L.attn) {
+      if (gemv(L.qkv, m->xq, m->xs, m->qkv) != 0 || gemv(L.z, m->xq, m->xs, m->zo) != 0) return -1;
+      {  // alpha | beta logits: fp32 rows (the router kernel computes W x for S tokens)
+        const halo_arg a[] = {Ptr(L.ab.device), Ptr(nullptr), Ptr(m->xn.device), Ptr(m->abo.device), Ptr(nullptr),
+                              Ptr(nullptr), Ptr(nullptr), U32(2 * Hv), U32(H), U32(S)};
+        if (Launch(eng, "halo_moe_router", D3(2 * Hv + 1), D3(256), a, err, errlen) != 0) return -1;
+      }
+      float* conv = P<float>(m->conv_state) + static_cast<std::size_t>(L.gdn_index) * c.max_sessions *
+                                                  (c.conv_kernel - 1) * C;
+      {
+        const halo_arg a[] = {Ptr(m->qkv.device), Ptr(conv), Ptr(L.conv_w.device), Ptr(m->abo.device),
+                              Ptr(L.a.device), Ptr(L.dt.device), Ptr(m->q.device), Ptr(m->k.device), Ptr(m->v.device),
+                              Ptr(m->g.device), Ptr(m->beta.device), U32(Hk), U32(Hv), U32(d), U32(c.conv_kernel),
+                              Val(eps)};
+        if (Launch(eng, "halo_gdn_prep_decode", D3(S, C / 256), D3(256), a, err, errlen) != 0) return -1;
+      }
+      float* st = P<float>(m->gdn_state) + static_cast<std::size_t>(L.gdn_index) * c.max_sessions * Hv * d * d;
+      if (halo_op_gdn_decode(eng, st, P<float>(m->q), P<float>(m->k), P<float>(m->v), P<float>(m->g),
+                             P<float>(m->beta), P<float>(m->o), S, Hv, Hk, d, err, errlen) != 0)
+        return -1;
+      {
+        const halo_arg a[] = {Ptr(m->o.device), Ptr(m->zo.device), Ptr(L.norm_w.device), Ptr(m->oq.device),
+                              Ptr(m->os.device), U32(Hv), U32(d), Val(eps)};
+        if (Launch(eng, "halo_gated_rmsnorm_q8", D3(S, CeilDiv(Hv, 4)), D3(256), a, err, errlen) != 0) return -1;
+      }
+      if (gemv(L.out, m->oq, m->os, m->delta) != 0) return -1;
+      (void)Dv;
+    } else {
+      if (gemv(L.qg, m->xq, m->xs, m->qgo) != 0 || gemv(L.k, m->xq, m->xs, m->ko) != 0 ||
+          gemv(L.v, m->xq, m->xs, m->vo) != 0)
+        return -1;
+      {
+        const halo_arg a[] = {Ptr(m->qgo.device), Ptr(m->ko.device), Ptr(m->vo.device), Ptr(L.q_norm.device),
+                              Ptr(L.k_norm.device), Ptr(m->q.device), Ptr(m->agate.device), Ptr(L.k_pool.device),
+                              Ptr(L.v_pool.device), Ptr(m->pages.device), Ptr(m->nkv.device), U32(Hq), U32(Hkv),
+                              U32(m->max_pages), U32(c.rotary_dim), Val(c.rope_theta), Val(eps)};
+        if (Launch(eng, "halo_attn_prep_decode", D3(S), D3(256), a, err, errlen) != 0) return -1;
+      }
+      const halo_paged_kv kv = KvDesc(m, L, S, prefix);
+      if (halo_op_attn_decode(eng, &kv, P<float>(m->q), P<float>(m->agate), P<float>(m->ao), Hq, m->attn_ws.device,
+                              m->attn_ws_bytes, err, errlen) != 0)
+        return -1;
+      if (halo_op_quantize_q8(eng, P<float>(m->ao), P<int8_t>(m->oq), P<float>(m->os), S, Hq * hd, err, errlen) != 0)
+        return -1;
+      if (gemv(L.o, m->oq, m->os, m->delta) != 0) return -1;
+    }
+    have_delta = true;
+    if (norm(L.ffn_norm, false) != 0) return -1;
+    if (halo_op_moe_decode(eng, &L.moe, P<float>(m->xn), P<float>(m->delta), S, m->moe_ws.device, m->moe_ws_bytes,
+                           err, errlen) != 0)
+      return -1;
+    have_delta = true;
+  }
+  if (norm(m->out_norm, true) != 0) return -1;
+  if (gemv(m->head, m->xq, m->xs, m->logits) != 0) return -1;
+  constexpr std::uint32_t kParts = 64;
+  float* pv = P<float>(m->argmax_part);
+  std::uint32_t* pi = reinterpret_cast<std::uint32_t*>(pv + c.max_sessions * kParts);
+  {
+    const halo_arg a[] = {Ptr(m->logits.device), Ptr(pv), Ptr(pi), U32(c.vocab)};
+    if (Launch(eng, "halo_argmax_part", D3(S, kParts), D3(256), a, err, errlen) != 0) return -1;
+  }
+  const halo_arg a[] = {Ptr(pv), Ptr(pi), Ptr(m->prompt.device), Ptr(m->prompt_len.device), Ptr(m->tokens.device),
+                        Ptr(m->nkv.device), Ptr(m->history.device), Ptr(m->produced.device), U32(S), U32(kParts),
+                        U32(c.max_context), U32(c.max_context), U32(c.max_context)};
+  return Launch(eng, "halo_step_advance", D3(1), D3(64), a, err, errlen);
+}
+
+}  // namespace
+
+extern "C" {
+
+int halo_model_create(halo_engine* eng, const halo_model_config* cfg, uint64_t seed, halo_model** out, char* err,
+                      size_t errlen) {
+  if (eng == nullptr || cfg == nullptr || out == nullptr) return SetErr(err, errlen, "null argument"), -1;
+  *out = nullptr;
+  if (Check(cfg, err, errlen) != 0) return -1;
+  auto m = std::make_unique<halo_model>();
+  m->eng = eng;
+  m->dev = halo_engine_device(eng);
+  m->c = *cfg;
+  const halo_model_config& c = m->c;
+  const std::uint32_t H = c.hidden, Hv = c.gdn_v_heads, Hk = c.gdn_k_heads, d = c.gdn_head_dim;
+  const std::uint32_t Dk = Hk * d, Dv = Hv * d, Hq = c.q_heads, Hkv = c.kv_heads, hd = c.head_dim;
+  const std::uint32_t S = c.max_sessions, E = c.n_experts, F = c.expert_ff, SF = c.shared_ff;
+  m->conv_ch = 2 * Dk + Dv;
+  m->max_pages = CeilDiv(c.max_context, 16);
+  m->prefix_pages = c.prefix_tokens / 16;
+  m->total_pages = m->prefix_pages + S * (m->max_pages - m->prefix_pages);
+  std::uint64_t sd = seed * 1000003ull;
+  auto next = [&]() { return ++sd; };
+  m->layers.resize(c.layers);
+  for (std::uint32_t l = 0; l < c.layers; ++l) {
+    Layer& L = m->layers[l];
+    L.attn = (l + 1) % c.attn_interval == 0;
+    if (SynthF32(m.get(), &L.attn_norm, H, next(), 0.02f, 1.0f, err, errlen) != 0 ||
+        SynthF32(m.get(), &L.ffn_norm, H, next(), 0.02f, 1.0f, err, errlen) != 0)
+      return -1;
+    if (!L.attn) {
+      L.gdn_index = m->n_gdn++;
+      if (SynthQ8(m.get(), &L.qkv, m->conv_ch, H, next(), err, errlen) != 0 ||
+          SynthQ8(m.get(), &L.z, Dv, H, next(), err, errlen) != 0 ||
+          SynthQ8(m.get(), &L.out, H, Dv, next(), err, errlen) != 0 ||
+          SynthF32(m.get(), &L.ab, 2 * Hv * H, next(), 0.02f, 0.0f, err, errlen) != 0 ||
+          SynthF32(m.get(), &L.conv_w, static_cast<std::size_t>(m->conv_ch) * c.conv_kernel, next(), 0.3f, 0.0f, err,
+                   errlen) != 0 ||
+          SynthF32(m.get(), &L.a, Hv, next(), 0.1f, -1.0f, err, errlen) != 0 ||
+          SynthF32(m.get(), &L.dt, Hv, next(), 0.5f, 0.0f, err, errlen) != 0 ||
+          SynthF32(m.get(), &L.norm_w, d, next(), 0.02f, 1.0f, err, errlen) != 0)
+        return -1;
+    } else {
+      ++m->n_attn;
+      const std::size_t pool = static_cast<std::size_t>(m->total_pages) * Hkv * 16 * hd * 4;
+      if (SynthQ8(m.get(), &L.qg, 2 * Hq * hd, H, next(), err, errlen) != 0 ||
+          SynthQ8(m.get(), &L.k, Hkv * hd, H, next(), err, errlen) != 0 ||
+          SynthQ8(m.get(), &L.v, Hkv * hd, H, next(), err, errlen) != 0 ||
+          SynthQ8(m.get(), &L.o, H, Hq * hd, next(), err, errlen) != 0 ||
+          SynthF32(m.get(), &L.q_norm, hd, next(), 0.02f, 1.0f, err, errlen) != 0 ||
+          SynthF32(m.get(), &L.k_norm, hd, next(), 0.02f, 1.0f, err, errlen) != 0 ||
+          Alloc(m.get(), pool, &L.k_pool, err, errlen) != 0 || Alloc(m.get(), pool, &L.v_pool, err, errlen) != 0)
+        return -1;
+    }
+    if (SynthF32(m.get(), &L.router, static_cast<std::size_t>(E) * H, next(), 0.02f, 0.0f, err, errlen) != 0 ||
+        SynthF32(m.get(), &L.shared_gate, H, next(), 0.02f, 0.0f, err, errlen) != 0 ||
+        SynthQ8(m.get(), &L.gate, E * F, H, next(), err, errlen) != 0 ||
+        SynthQ8(m.get(), &L.up, E * F, H, next(), err, errlen) != 0 ||
+        SynthQ8(m.get(), &L.down, E * H, F, next(), err, errlen) != 0 ||
+        SynthQ8(m.get(), &L.sgate, SF, H, next(), err, errlen) != 0 ||
+        SynthQ8(m.get(), &L.sup, SF, H, next(), err, errlen) != 0 ||
+        SynthQ8(m.get(), &L.sdown, H, SF, next(), err, errlen) != 0)
+      return -1;
+    halo_moe_weights& w = L.moe;
+    w.router = P<float>(L.router);
+    w.shared_gate = P<float>(L.shared_gate);
+    w.gate = L.gate.m;
+    w.up = L.up.m;
+    w.down = L.down.m;
+    w.shared_gate_proj = L.sgate.m;
+    w.shared_up = L.sup.m;
+    w.shared_down = L.sdown.m;
+    w.n_experts = E;
+    w.n_used = c.n_used;
+    w.hidden = H;
+    w.ff = F;
+    w.shared_ff = SF;
+  }
+  if (SynthQ8(m.get(), &m->embd, c.vocab, H, next(), err, errlen) != 0 ||
+      SynthQ8(m.get(), &m->head, c.vocab, H, next(), err, errlen) != 0 ||
+      SynthF32(m.get(), &m->out_norm, H, next(), 0.02f, 1.0f, err, errlen) != 0)
+    return -1;
+  // sessions and step scratch
+  const std::size_t ctx = c.max_context;
+  struct B {
+    halo_buffer* b;
+    std::size_t bytes;
+  };
+  const std::uint32_t C = m->conv_ch;
+  const B bufs[] = {
+      {&m->gdn_state, static_cast<std::size_t>(m->n_gdn) * S * Hv * d * d * 4},
+      {&m->conv_state, static_cast<std::size_t>(m->n_gdn) * S * (c.conv_kernel - 1 ? c.conv_kernel - 1 : 1) * C * 4},
+      {&m->pages, static_cast<std::size_t>(S) * m->max_pages * 4},
+      {&m->nkv, S * 4},
+      {&m->tokens, S * 4},
+      {&m->prompt, S * ctx * 4},
+      {&m->prompt_len, S * 4},
+      {&m->history, S * ctx * 4},
+      {&m->produced, S * 4},
+      {&m->res, static_cast<std::size_t>(S) * H * 4},
+      {&m->xn, static_cast<std::size_t>(S) * H * 4},
+      {&m->xq, static_cast<std::size_t>(S) * H},
+      {&m->xs, static_cast<std::size_t>(S) * H / 8},
+      {&m->qkv, static_cast<std::size_t>(S) * C * 4},
+      {&m->zo, static_cast<std::size_t>(S) * Dv * 4},
+      {&m->abo, static_cast<std::size_t>(S) * 2 * Hv * 4},
+      {&m->q, static_cast<std::size_t>(S) * std::max(Hk * d, Hq * hd) * 4},
+      {&m->k, static_cast<std::size_t>(S) * Hk * d * 4},
+      {&m->v, static_cast<std::size_t>(S) * Dv * 4},
+      {&m->g, S * Hv * 4},
+      {&m->beta, S * Hv * 4},
+      {&m->o, static_cast<std::size_t>(S) * Dv * 4},
+      {&m->oq, static_cast<std::size_t>(S) * std::max(Dv, Hq * hd)},
+      {&m->os, static_cast<std::size_t>(S) * std::max(Dv, Hq * hd) / 8},
+      {&m->delta, static_cast<std::size_t>(S) * H * 4},
+      {&m->qgo, static_cast<std::size_t>(S) * 2 * Hq * hd * 4},
+      {&m->ko, static_cast<std::size_t>(S) * Hkv * hd * 4},
+      {&m->vo, static_cast<std::size_t>(S) * Hkv * hd * 4},
+      {&m->agate, static_cast<std::size_t>(S) * Hq * hd * 4},
+      {&m->ao, static_cast<std::size_t>(S) * Hq * hd * 4},
+      {&m->logits, static_cast<std::size_t>(S) * c.vocab * 4},
+      {&m->argmax_part, static_cast<std::size_t>(S) * 64 * 8},
+  };
+  for (const auto& b : bufs)
+    if (Alloc(m.get(), b.bytes, b.b, err, errlen) != 0) return -1;
+  m->moe_ws_bytes = halo_op_moe_workspace_bytes(&m->layers[0].moe, S);
+  std::size_t aw = 0;
+  for (std::uint32_t s = 1; s <= S; ++s)
+    for (std::uint32_t pre : {0u, c.prefix_tokens}) {
+      halo_paged_kv kv{};
+      kv.k_pool = reinterpret_cast<float*>(1);
+      kv.v_pool = kv.k_pool;
+      kv.pages = reinterpret_cast<const uint32_t*>(1);
+      kv.nkv = kv.pages;
+      kv.sessions = s;
+      kv.kv_heads = Hkv;
+      kv.head_dim = hd;
+      kv.max_pages = m->max_pages;
+      kv.prefix = pre;
+      kv.max_context = c.max_context;
+      aw = std::max(aw, halo_op_attn_decode_workspace_bytes(&kv, Hq));
+    }
+  m->attn_ws_bytes = aw;
+  if (m->moe_ws_bytes == 0 || Alloc(m.get(), m->moe_ws_bytes, &m->moe_ws, err, errlen) != 0 ||
+      Alloc(m.get(), aw, &m->attn_ws, err, errlen) != 0)
+    return SetErr(err, errlen, "model: workspace sizing failed"), -1;
+  // page tables: [0, prefix_pages) shared, the rest per session
+  std::vector<std::uint32_t> pt(static_cast<std::size_t>(S) * m->max_pages);
+  std::uint32_t nextp = m->prefix_pages;
+  for (std::uint32_t s = 0; s < S; ++s)
+    for (std::uint32_t p = 0; p < m->max_pages; ++p)
+      pt[static_cast<std::size_t>(s) * m->max_pages + p] = p < m->prefix_pages ? p : nextp++;
+  if (halo_upload(m->dev, &m->pages, 0, pt.data(), pt.size() * 4, err, errlen) != 0) return -1;
+  if (halo_model_reset(m.get(), err, errlen) != 0) return -1;
+  if (halo_synchronize(m->dev, err, errlen) != 0) return -1;
+  *out = m.release();
+  return 0;
+}
+
+void halo_model_destroy(halo_model* m) {
+  if (m == nullptr) return;
+  (void)halo_synchronize(m->dev, nullptr, 0);
+  for (auto& [key, g] : m->graphs) halo_free_graph(m->dev, &g);
+  for (auto& b : m->owned) halo_free(m->dev, &b);
+  delete m;
+}
+
+uint64_t halo_model_weight_bytes(const halo_model* m) { return m ? m->weight_bytes : 0; }
+uint64_t halo_model_device_bytes(const halo_model* m) { return m ? m->device_bytes : 0; }
+
+int halo_model_reset(halo_model* m, char* err, size_t errlen) {
+  for (halo_buffer* b : {&m->gdn_state, &m->conv_state, &m->nkv, &m->tokens, &m->prompt_len, &m->history})
+    if (halo_fill(m->dev, b, 0, err, errlen) != 0) return -1;
+  return 0;
+}
+
+int halo_model_set_session(halo_model* m, uint32_t s, const uint32_t* prompt, uint32_t len, uint32_t nkv, char* err,
+                           size_t errlen) {
+  if (s >= m->c.max_sessions || len > m->c.max_context || nkv > len || nkv >= m->c.max_context)
+    return SetErr(err, errlen, "session %u: prompt %u / position %u out of range", s, len, nkv), -1;
+  for (std::uint32_t i = 0; i < len; ++i)
+    if (prompt[i] >= m->c.vocab) return SetErr(err, errlen, "session %u: token %u out of range", s, prompt[i]), -1;
+  const std::size_t stride = m->c.max_context;
+  if (len && halo_upload(m->dev, &m->prompt, static_cast<std::size_t>(s) * stride * 4, prompt, len * 4ull, err,
+                         errlen) != 0)
+    return -1;
+  const std::uint32_t first = len ? prompt[nkv] : 0;
+  if (halo_upload(m->dev, &m->prompt_len, s * 4ull, &len, 4, err, errlen) != 0 ||
+      halo_upload(m->dev, &m->nkv, s * 4ull, &nkv, 4, err, errlen) != 0 ||
+      halo_upload(m->dev, &m->tokens, s * 4ull, &first, 4, err, errlen) != 0)
+    return -1;
+  // the first step reads token nkv and writes position nkv: nkv counts it
+  const std::uint32_t n1 = nkv + 1;
+  return halo_upload(m->dev, &m->nkv, s * 4ull, &n1, 4, err, errlen);
+}
+
+int halo_model_fork(halo_model* m, uint32_t src, uint32_t dst, char* err, size_t errlen) {
+  const halo_model_config& c = m->c;
+  if (src >= c.max_sessions || dst >= c.max_sessions) return SetErr(err, errlen, "fork: bad session"), -1;
+  const std::size_t st = static_cast<std::size_t>(c.gdn_v_heads) * c.gdn_head_dim * c.gdn_head_dim * 4;
+  const std::size_t cv = static_cast<std::size_t>(c.conv_kernel - 1) * m->conv_ch * 4;
+  for (std::uint32_t l = 0; l < m->n_gdn; ++l) {
+    const std::size_t base = static_cast<std::size_t>(l) * c.max_sessions;
+    char* sp = P<char>(m->gdn_state);
+    char* cp = P<char>(m->conv_state);
+    const halo_arg a[] = {Ptr(sp + (base + src) * st), Ptr(sp + (base + dst) * st), Val<std::uint64_t>(st / 16)};
+    if (Launch(m->eng, "halo_copy16", D3(1024), D3(256), a, err, errlen) != 0) return -1;
+    if (cv) {
+      const halo_arg b[] = {Ptr(cp + (base + src) * cv), Ptr(cp + (base + dst) * cv), Val<std::uint64_t>(cv / 16)};
+      if (Launch(m->eng, "halo_copy16", D3(64), D3(256), b, err, errlen) != 0) return -1;
+    }
+  }
+  return 0;
+}
+
+int halo_model_step_eager(halo_model* m, uint32_t S, uint32_t prefix, char* err, size_t errlen) {
+  if (S == 0 || S > m->c.max_sessions || prefix % 64 != 0 || prefix > m->c.prefix_tokens)
+    return SetErr(err, errlen, "step: %u sessions / prefix %u unsupported", S, prefix), -1;
+  return Record(m, S, prefix, err, errlen);
+}
+
+int halo_model_run(halo_model* m, uint32_t S, uint32_t prefix, uint32_t steps, char* err, size_t errlen) {
+  if (S == 0 || S > m->c.max_sessions || prefix % 64 != 0 || prefix > m->c.prefix_tokens)
+    return SetErr(err, errlen, "run: %u sessions / prefix %u unsupported", S, prefix), -1;
+  const auto key = std::make_pair(S, prefix);
+  auto it = m->graphs.find(key);
+  if (it == m->graphs.end()) {
+    if (halo_begin_capture(m->dev, err, errlen) != 0) return -1;
+    const int rc = Record(m, S, prefix, err, errlen);
+    halo_graph g{};
+    char e2[256];
+    const int rc2 = halo_end_capture(m->dev, &g, e2, sizeof e2);
+    if (rc != 0) return -1;
+    if (rc2 != 0) return SetErr(err, errlen, "%s", e2), -1;
+    it = m->graphs.emplace(key, g).first;
+  }
+  for (std::uint32_t i = 0; i < steps; ++i)
+    if (halo_launch_graph(m->dev, &it->second, err, errlen) != 0) return -1;
+  return 0;
+}
+
+int halo_model_history(halo_model* m, uint32_t s, uint32_t* out, uint32_t n, char* err, size_t errlen) {
+  if (s >= m->c.max_sessions || n > m->c.max_context) return SetErr(err, errlen, "history: bad range"), -1;
+  return halo_download(m->dev, &m->history, static_cast<std::size_t>(s) * m->c.max_context * 4, out, n * 4ull, err,
+                       errlen);
+}
+
+int halo_model_positions(halo_model* m, uint32_t* nkv_out, uint32_t S, char* err, size_t errlen) {
+  if (S > m->c.max_sessions) return SetErr(err, errlen, "positions: bad count"), -1;
+  return halo_download(m->dev, &m->nkv, 0, nkv_out, S * 4ull, err, errlen);
+}
+
+}  // extern "C"

@@ -98,18 +98,31 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
     }
   }
   __syncthreads();
-  // weighted V: thread = one of the 256 dims, all queries
+  // weighted V: thread = one of the 256 dims, all queries; the chunk's page ids are read once
   float acc[kMaxQ];
 #pragma unroll
   for (int i = 0; i < kMaxQ; ++i) acc[i] = 0.0f;
   const std::uint32_t ntok = min(static_cast<std::uint32_t>(kChunk), limit - start);
-  for (std::uint32_t j = 0; j < ntok; ++j) {
-    const std::uint32_t tk = start + j;
-    const std::uint32_t pg = pages[static_cast<std::size_t>(sess) * max_pages + tk / kPage];
-    const float vv = vpool[((static_cast<std::size_t>(pg) * Hkv + kvh) * kPage + (tk % kPage)) * kHd + t];
+  std::uint32_t pgs[kChunk / kPage];
 #pragma unroll
-    for (int i = 0; i < kMaxQ; ++i)
-      if (i < static_cast<int>(nq)) acc[i] += ps[i][j] * vv;
+  for (int i = 0; i < kChunk / kPage; ++i)
+    pgs[i] = pages[static_cast<std::size_t>(sess) * max_pages + min(start / kPage + i, (limit - 1) / kPage)];
+  constexpr int kU = 8;
+  for (std::uint32_t j0 = 0; j0 < ntok; j0 += kU) {
+    float vv[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const std::uint32_t j = min(j0 + u, ntok - 1);
+      const std::uint32_t pg = pgs[j / kPage];
+      vv[u] = vpool[((static_cast<std::size_t>(pg) * Hkv + kvh) * kPage + ((start + j) % kPage)) * kHd + t];
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (j0 + u >= ntok) break;
+#pragma unroll
+      for (int i = 0; i < kMaxQ; ++i)
+        if (i < static_cast<int>(nq)) acc[i] += ps[i][j0 + u] * vv[u];
+    }
   }
 #pragma unroll
   for (int i = 0; i < kMaxQ; ++i)
@@ -120,28 +133,55 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
 }
 
 // grid (S * Hq), block 256: merges the partials of session s, head h over its prefix and suffix chunks
-// (log-sum-exp), o = acc / l, then o *= sigmoid(gate) when gate is non-null. o, gate [S][Hq][256].
+// (log-sum-exp), o = acc / l, then o *= sigmoid(gate) when gate is non-null. o, gate [S][Hq][256]. Items are at most
+// 1024 (64-token chunks of a 64K context).
 extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_combine(
     const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ pacc,
     const float* __restrict__ gate, float* __restrict__ o, std::uint32_t S, std::uint32_t Hq, std::uint32_t Hkv,
     std::uint32_t prefix_chunks, std::uint32_t suffix_chunks) {
+  __shared__ float wts[1024];
+  __shared__ float red[4];
   const std::uint32_t G = Hq / Hkv, s = blockIdx.x / Hq, h = blockIdx.x % Hq, kvh = h / G, g = h % G;
   const std::uint32_t slot = s * G + g, slots = S * G, t = threadIdx.x;
-  const std::uint32_t n = prefix_chunks + suffix_chunks;
-  auto item = [&](std::uint32_t i) {
+  const std::uint32_t n = min(prefix_chunks + suffix_chunks, 1024u);
+  auto item = [&](std::uint32_t i) -> std::size_t {
     const std::uint32_t c = i < prefix_chunks ? i : prefix_chunks + s * suffix_chunks + (i - prefix_chunks);
-    return c * Hkv + kvh;
+    return static_cast<std::size_t>(c) * Hkv + kvh;
   };
   float M = -INFINITY;
-  for (std::uint32_t i = 0; i < n; ++i) M = fmaxf(M, pm[static_cast<std::size_t>(item(i)) * slots + slot]);
-  float L = 0.0f, acc = 0.0f;
-  for (std::uint32_t i = 0; i < n; ++i) {
-    const std::size_t it = item(i);
-    const float m = pm[it * slots + slot];
-    if (m == -INFINITY) continue;
-    const float w = expf(m - M);
-    L += w * pl[it * slots + slot];
-    acc += w * pacc[(it * slots + slot) * kHd + t];
+  for (std::uint32_t i = t; i < n; i += blockDim.x) {
+    const float m = pm[item(i) * slots + slot];
+    wts[i] = m;
+    M = fmaxf(M, m);
+  }
+  M = halo::GroupMax(M);
+  if (t % kWave == 0) red[t / kWave] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float L = 0.0f;
+  for (std::uint32_t i = t; i < n; i += blockDim.x) {
+    const float m = wts[i];
+    const float w = m == -INFINITY ? 0.0f : expf(m - M);
+    wts[i] = w;
+    L += w * pl[item(i) * slots + slot];
+  }
+  L = halo::GroupSum(L);
+  __syncthreads();
+  if (t % kWave == 0) red[t / kWave] = L;
+  __syncthreads();
+  L = (red[0] + red[1]) + (red[2] + red[3]);
+  float acc = 0.0f;
+  constexpr int kU = 8;
+  for (std::uint32_t i0 = 0; i0 < n; i0 += kU) {
+    float a[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const std::uint32_t i = min(i0 + u, n - 1);
+      a[u] = wts[i] == 0.0f ? 0.0f : pacc[(item(i) * slots + slot) * kHd + t];
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      if (i0 + u < n) acc += wts[i0 + u] * a[u];
   }
   float r = acc / L;
   const std::size_t off = (static_cast<std::size_t>(s) * Hq + h) * kHd + t;

@@ -3,3 +3,4 @@
 #include "moe.hip"
 #include "gdn.hip"
 #include "attn.hip"
+#include "model.hip"

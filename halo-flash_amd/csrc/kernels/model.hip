@@ -1,0 +1,288 @@
+// Per-token glue of the hybrid decode step (gfx950, wave64): norms fused with the activation quantizer, the
+// DeltaNet conv / L2-norm / decay prologue, the gated output norm, q/k norm + RoPE + KV append, embedding lookup,
+// greedy argmax and the device-side step advance (so one captured graph replays at every position).
+//
+// Reference semantics: cpu::RmsNorm / L2Norm / Rope / Silu / Softplus (src/model/cpu_ops.cpp:134-185),
+// ReferenceModel::LinearAttention conv + norms + gate (src/model/reference.cpp:278-366), ReferenceModel::Attention
+// q/gate split, q/k norm, NEOX rope (src/model/reference.cpp:368-416), HaloStepParam (src/kernels/step_params.h).
+#include "common.h"
+
+using halo::kWave;
+
+namespace {
+// Sum over the block (blockDim.x a multiple of 64, <= 1024); red holds 16 floats.
+__device__ __forceinline__ float BlockSumM(float v, float* red) {
+  v = halo::GroupSum(v);
+  const std::uint32_t wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
+  __syncthreads();
+  if (threadIdx.x % kWave == 0) red[wave] = v;
+  __syncthreads();
+  float r = 0.0f;
+  for (std::uint32_t w = 0; w < waves; ++w) r += red[w];
+  return r;
+}
+
+// Quantizes 32 consecutive values held one per lane of a half wave (amax / 127, round half to even).
+__device__ __forceinline__ void Quant32(float v, std::int8_t* xq, float* xs, std::uint32_t blk) {
+  const std::uint32_t lane = threadIdx.x % 32;
+  const float amax = halo::GroupMax<32>(fabsf(v));
+  const float scale = amax / 127.0f;
+  xq[blk * 32 + lane] = static_cast<std::int8_t>(scale > 0.0f ? static_cast<int>(rintf(v / scale)) : 0);
+  if (lane == 0) xs[blk] = scale;
+}
+}  // namespace
+
+// grid (S), block 256 (H <= 8192, H % 256 == 0). res [S][H] += delta [S][H] (delta may be null), then
+// xn = RMSNorm(res) * w (fp32, may be null) and its Q8 quantization xq [S][H], xs [S][H / 32] (may be null).
+extern "C" __global__ void __launch_bounds__(256)
+    halo_add_rmsnorm_q8(float* __restrict__ res, const float* __restrict__ delta, const float* __restrict__ w,
+                        float* __restrict__ xn, std::int8_t* __restrict__ xq, float* __restrict__ xs,
+                        std::uint32_t H, float eps) {
+  __shared__ float red[16];
+  __shared__ float vals[8192];
+  const std::size_t s = blockIdx.x;
+  float ss = 0.0f;
+  for (std::uint32_t i = threadIdx.x; i < H; i += blockDim.x) {
+    float v = res[s * H + i];
+    if (delta != nullptr) {
+      v += delta[s * H + i];
+      res[s * H + i] = v;
+    }
+    vals[i] = v;
+    ss += v * v;
+  }
+  ss = BlockSumM(ss, red);
+  const float scale = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
+  for (std::uint32_t i = threadIdx.x; i < H; i += blockDim.x) {
+    const float y = vals[i] * scale * w[i];
+    if (xn != nullptr) xn[s * H + i] = y;
+    if (xq != nullptr) Quant32(y, xq + s * H, xs + s * (H / 32), i / 32);
+  }
+}
+
+// grid (S, C / 256), block 256: the DeltaNet prologue for one token per session, one channel per thread.
+//   qkv [S][C] (C = 2 Dk + Dv channels: q | k | v), conv_state [S][K-1][C] (oldest first), conv_w [C][K];
+//   conv = SiLU(w[K-1] x + sum_{k<K-1} w[k] state[k]); the state shifts in x. q, k per key head L2-normalized
+//   (eps = rms eps); ab [S][2 Hv] (alpha | beta logits), a [Hv] (negative), dt [Hv]:
+//   g = a * softplus(alpha + dt) (log decay), beta = sigmoid(beta logit).
+//   Outputs q, k [S][Hk][d], v [S][Hv][d], g, beta [S][Hv]. d = 128: a block covers two heads.
+extern "C" __global__ void __launch_bounds__(256) halo_gdn_prep_decode(
+    const float* __restrict__ qkv, float* __restrict__ conv_state, const float* __restrict__ conv_w,
+    const float* __restrict__ ab, const float* __restrict__ a, const float* __restrict__ dt, float* __restrict__ q,
+    float* __restrict__ k, float* __restrict__ v, float* __restrict__ g, float* __restrict__ beta, std::uint32_t Hk,
+    std::uint32_t Hv, std::uint32_t d, std::uint32_t K, float eps) {
+  __shared__ float part[4];
+  const std::size_t s = blockIdx.x;
+  const std::uint32_t Dk = Hk * d, Dv = Hv * d, C = 2 * Dk + Dv;
+  const std::uint32_t ch = blockIdx.y * blockDim.x + threadIdx.x;
+  const float x = qkv[s * C + ch];
+  float* st = conv_state + s * (K - 1) * C;
+  float acc = conv_w[static_cast<std::size_t>(ch) * K + K - 1] * x;
+  for (std::uint32_t j = 0; j + 1 < K; ++j) acc += conv_w[static_cast<std::size_t>(ch) * K + j] * st[j * C + ch];
+  for (std::uint32_t j = 0; j + 2 < K; ++j) st[j * C + ch] = st[(j + 1) * C + ch];
+  if (K > 1) st[(K - 2) * C + ch] = x;
+  const float y = halo::Silu(acc);
+  // the block's 256 channels are two heads of 128 (two waves each)
+  const std::uint32_t wave = threadIdx.x / kWave;
+  const float ss = halo::GroupSum(y * y);
+  if (threadIdx.x % kWave == 0) part[wave] = ss;
+  __syncthreads();
+  const std::uint32_t head = ch / d;
+  if (ch < 2 * Dk) {
+    const std::uint32_t w0 = (wave / 2) * 2;
+    const float sc = 1.0f / sqrtf(part[w0] + part[w0 + 1] + eps);
+    float* dst = head < Hk ? q + (s * Hk + head) * d : k + (s * Hk + head - Hk) * d;
+    dst[ch % d] = y * sc;
+  } else {
+    v[s * Dv + ch - 2 * Dk] = y;
+  }
+  if (blockIdx.y == 0 && threadIdx.x < Hv) {
+    const std::uint32_t h = threadIdx.x;
+    g[s * Hv + h] = a[h] * halo::Softplus(ab[s * 2 * Hv + h] + dt[h]);
+    beta[s * Hv + h] = halo::Sigmoid(ab[s * 2 * Hv + Hv + h]);
+  }
+}
+
+// grid (S, Hv / 4), block 256 (a wave per head): RMSNorm(o_h) * w (d weights shared by heads) * sigmoid(z_h), then
+// the Q8 quantization: o, z [S][Hv][d] -> xq [S][Hv d], xs [S][Hv d / 32]. d = 128.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_gated_rmsnorm_q8(const float* __restrict__ o, const float* __restrict__ z, const float* __restrict__ w,
+                          std::int8_t* __restrict__ xq, float* __restrict__ xs, std::uint32_t Hv, std::uint32_t d,
+                          float eps) {
+  const std::size_t s = blockIdx.x;
+  const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, waves = blockDim.x / kWave;
+  const std::uint32_t D = Hv * d;
+  for (std::uint32_t h = blockIdx.y * waves + wave; h < Hv && h < (blockIdx.y + 1) * waves; h += waves) {
+    const float* oh = o + s * D + h * d;
+    const float v0 = oh[lane], v1 = oh[lane + 64];
+    const float ss = halo::GroupSum(v0 * v0 + v1 * v1);
+    const float sc = 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
+    const float y0 = v0 * sc * w[lane] * halo::Sigmoid(z[s * D + h * d + lane]);
+    const float y1 = v1 * sc * w[lane + 64] * halo::Sigmoid(z[s * D + h * d + lane + 64]);
+    // 128 values = 4 blocks of 32: lanes 0-31 / 32-63 hold blocks 0 / 1 (y0) and 2 / 3 (y1)
+    Quant32(y0, xq + s * D + h * d, xs + s * (D / 32) + h * (d / 32), lane / 32);
+    Quant32(y1, xq + s * D + h * d, xs + s * (D / 32) + h * (d / 32), 2 + lane / 32);
+  }
+}
+
+// grid (S), block 256: attention prologue for one token per session. qg [S][Hq][2 d] (per head: q | gate),
+// kin, vin [S][Hkv][d]; RMSNorm of every q head (wq) and k head (wk); NEOX rope on the first `rot` dims at position
+// nkv[s] - 1; q, gate [S][Hq][d] out; k, v appended to the paged pools at that position. d = 256.
+extern "C" __global__ void __launch_bounds__(256) halo_attn_prep_decode(
+    const float* __restrict__ qg, const float* __restrict__ kin, const float* __restrict__ vin,
+    const float* __restrict__ wq, const float* __restrict__ wk, float* __restrict__ q, float* __restrict__ gate,
+    float* __restrict__ kpool, float* __restrict__ vpool, const std::uint32_t* __restrict__ pages,
+    const std::uint32_t* __restrict__ nkv, std::uint32_t Hq, std::uint32_t Hkv, std::uint32_t max_pages,
+    std::uint32_t rot, float theta, float eps) {
+  constexpr std::uint32_t d = 256, kPage = 16;
+  const std::size_t s = blockIdx.x;
+  const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, waves = blockDim.x / kWave;
+  const std::uint32_t pos = nkv[s] - 1;
+  const std::uint32_t pg = pages[s * max_pages + pos / kPage];
+  for (std::uint32_t hh = wave; hh < Hq + 2 * Hkv; hh += waves) {
+    // hh < Hq: q head; Hq <= hh < Hq + Hkv: k head; else v head (copied)
+    float x[4];
+    const float* src;
+    if (hh < Hq)
+      src = qg + (s * Hq + hh) * 2 * d;
+    else if (hh < Hq + Hkv)
+      src = kin + (s * Hkv + (hh - Hq)) * d;
+    else
+      src = vin + (s * Hkv + (hh - Hq - Hkv)) * d;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = src[lane + 64 * i];
+    if (hh >= Hq + Hkv) {
+      const std::uint32_t kvh = hh - Hq - Hkv;
+      float* dst = vpool + ((static_cast<std::size_t>(pg) * Hkv + kvh) * kPage + pos % kPage) * d;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[lane + 64 * i] = x[i];
+      continue;
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ss += x[i] * x[i];
+    ss = halo::GroupSum(ss);
+    const float sc = 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
+    const float* wn = hh < Hq ? wq : wk;
+    float y[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) y[i] = x[i] * sc * wn[lane + 64 * i];
+    // NEOX rotation: pairs (j, j + rot / 2) for j < rot / 2 (rot <= 128 keeps both halves in y[0], y[1] lanes)
+    float out[4] = {y[0], y[1], y[2], y[3]};
+    const std::uint32_t half = rot / 2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const std::uint32_t j = lane + 64 * i;
+      if (j < rot) {
+        const std::uint32_t jj = j < half ? j : j - half;
+        const float freq = powf(theta, -2.0f * static_cast<float>(jj) / static_cast<float>(rot));
+        const float ang = static_cast<float>(pos) * freq;
+        const float c = cosf(ang), sn = sinf(ang);
+        // partner value: element j + half or j - half
+        const std::uint32_t pj = j < half ? j + half : j - half;
+        float partner = 0.0f;
+#pragma unroll
+        for (int i2 = 0; i2 < 4; ++i2) {
+          const float cand = __shfl(y[i2], pj % 64, kWave);
+          if (static_cast<std::uint32_t>(i2) == pj / 64) partner = cand;
+        }
+        out[i] = j < half ? y[i] * c - partner * sn : partner * sn + y[i] * c;
+      }
+    }
+    if (hh < Hq) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        q[(s * Hq + hh) * d + lane + 64 * i] = out[i];
+        gate[(s * Hq + hh) * d + lane + 64 * i] = src[d + lane + 64 * i];
+      }
+    } else {
+      const std::uint32_t kvh = hh - Hq;
+      float* dst = kpool + ((static_cast<std::size_t>(pg) * Hkv + kvh) * kPage + pos % kPage) * d;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[lane + 64 * i] = out[i];
+    }
+  }
+}
+
+// grid (S), block 256: x [S][H] = dequantized embedding row tokens[s] of a repacked Q8_0 table.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_embed_q8(const std::int8_t* __restrict__ qs, const std::uint16_t* __restrict__ d,
+                  const std::uint32_t* __restrict__ tokens, float* __restrict__ x, std::uint32_t H,
+                  std::uint32_t qstride) {
+  const std::size_t s = blockIdx.x, t = tokens[s];
+  for (std::uint32_t i = threadIdx.x; i < H; i += blockDim.x)
+    x[s * H + i] = halo::F16(d[t * (H / 32) + i / 32]) * static_cast<float>(qs[t * qstride + i]);
+}
+
+// grid (S, 64), block 256: partial argmax of each 1/64 slice of the V logits of session s (ties to the lower id)
+// -> part [S][64] as (value, id) pairs; halo_step_advance finishes the reduction.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_argmax_part(const float* __restrict__ logits, float* __restrict__ pv, std::uint32_t* __restrict__ pi,
+                     std::uint32_t V) {
+  __shared__ float bv[4];
+  __shared__ std::uint32_t bi[4];
+  const std::size_t s = blockIdx.x;
+  const std::uint32_t per = (V + gridDim.y - 1) / gridDim.y, lo = blockIdx.y * per, hi = min(V, lo + per);
+  float v = -INFINITY;
+  std::uint32_t at = 0xFFFFFFFFu;
+  for (std::uint32_t i = lo + threadIdx.x; i < hi; i += blockDim.x) {
+    const float x = logits[s * V + i];
+    if (x > v) {  // ascending i per thread: the first maximum wins
+      v = x;
+      at = i;
+    }
+  }
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(v, o, kWave);
+    const std::uint32_t oi = __shfl_xor(at, o, kWave);
+    if (ov > v || (ov == v && oi < at)) {
+      v = ov;
+      at = oi;
+    }
+  }
+  const std::uint32_t wave = threadIdx.x / kWave;
+  if (threadIdx.x % kWave == 0) {
+    bv[wave] = v;
+    bi[wave] = at;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (std::uint32_t w = 1; w < blockDim.x / kWave; ++w)
+      if (bv[w] > v || (bv[w] == v && bi[w] < at)) {
+        v = bv[w];
+        at = bi[w];
+      }
+    pv[s * gridDim.y + blockIdx.y] = v;
+    pi[s * gridDim.y + blockIdx.y] = at;
+  }
+}
+
+// grid 1, block 64: end of a decode step. For each session s < S: the produced token is the argmax over the
+// `parts` partial maxima of halo_argmax_part (ties to the lower id); it is recorded at history[s][nkv[s]]; the
+// next input token is the prompt token at that position when it exists (teacher forcing), otherwise the produced
+// one; nkv[s] advances by one. prompt [S][prompt_stride], prompt_len [S].
+extern "C" __global__ void __launch_bounds__(64)
+    halo_step_advance(const float* __restrict__ pv, const std::uint32_t* __restrict__ pi,
+                      const std::uint32_t* __restrict__ prompt, const std::uint32_t* __restrict__ prompt_len,
+                      std::uint32_t* __restrict__ tokens, std::uint32_t* __restrict__ nkv,
+                      std::uint32_t* __restrict__ history, std::uint32_t* __restrict__ produced, std::uint32_t S,
+                      std::uint32_t parts, std::uint32_t prompt_stride, std::uint32_t history_stride,
+                      std::uint32_t max_context) {
+  const std::uint32_t s = threadIdx.x;
+  if (s >= S) return;
+  float v = -INFINITY;
+  std::uint32_t at = 0xFFFFFFFFu;
+  for (std::uint32_t p = 0; p < parts; ++p) {
+    const float x = pv[s * parts + p];
+    const std::uint32_t i = pi[s * parts + p];
+    if (x > v || (x == v && i < at)) {
+      v = x;
+      at = i;
+    }
+  }
+  produced[s] = at;
+  const std::uint32_t n = nkv[s];  // positions now in the cache, the produced token goes at index n
+  if (n < history_stride) history[static_cast<std::size_t>(s) * history_stride + n] = at;
+  tokens[s] = n < prompt_len[s] ? prompt[static_cast<std::size_t>(s) * prompt_stride + n] : at;
+  nkv[s] = min(n + 1, max_context);
+}

@@ -518,3 +518,26 @@ extern "C" __global__ void __launch_bounds__(256) halo_gemm_q8a8_mfma_t4(
     std::uint32_t cols, std::uint32_t qstride, std::uint32_t T, std::uint32_t ystride) {
   GemmQ8A8Mfma<4>(qs, d, xq, xs, y, rows, cols, qstride, T, ystride);
 }
+
+// x = a * x + b over n floats (shapes seeded tensors such as norm weights around 1).
+extern "C" __global__ void __launch_bounds__(256)
+    halo_affine_f32(float* x, std::uint64_t n, float a, float b) {
+  for (std::uint64_t i = blockIdx.x * static_cast<std::uint64_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<std::uint64_t>(gridDim.x) * blockDim.x)
+    x[i] = a * x[i] + b;
+}
+
+// dst = src over n bytes (16-byte vectors; n % 16 == 0): session state forks.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_copy16(const int4* __restrict__ src, int4* __restrict__ dst, std::uint64_t n16) {
+  for (std::uint64_t i = blockIdx.x * static_cast<std::uint64_t>(blockDim.x) + threadIdx.x; i < n16;
+       i += static_cast<std::uint64_t>(gridDim.x) * blockDim.x)
+    dst[i] = src[i];
+}
+
+// Zero fill (used instead of memset nodes so that fills can sit in captured graphs).
+extern "C" __global__ void __launch_bounds__(256) halo_zero16(int4* __restrict__ dst, std::uint64_t n16) {
+  for (std::uint64_t i = blockIdx.x * static_cast<std::uint64_t>(blockDim.x) + threadIdx.x; i < n16;
+       i += static_cast<std::uint64_t>(gridDim.x) * blockDim.x)
+    dst[i] = make_int4(0, 0, 0, 0);
+}

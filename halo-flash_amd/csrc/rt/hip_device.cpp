@@ -23,6 +23,13 @@ struct halo_device {
   bool capturing = false;
   std::size_t captured = 0;          // launches recorded since BeginCapture
   std::vector<void*> deferred_free;  // Free() calls made while capturing, released at EndCapture
+  // per-launch event timing of eager launches (halo_profile_begin / _end)
+  bool profiling = false;
+  struct Timed {
+    halo_kernel_id k;
+    hipEvent_t a, b;
+  };
+  std::vector<Timed> timed;
   hipEvent_t t0 = nullptr, t1 = nullptr;
 };
 
@@ -219,6 +226,13 @@ int halo_launch(halo_device* dev, halo_kernel_id kernel, halo_dim3 grid, halo_di
                     dev->captured, dev->names[kernel].c_str()),
              -1;
   }
+  const bool timing = dev->profiling && !dev->capturing;
+  halo_device::Timed tm{kernel, nullptr, nullptr};
+  if (timing) {
+    (void)hipEventCreate(&tm.a);
+    (void)hipEventCreate(&tm.b);
+    (void)hipEventRecord(tm.a, dev->stream);
+  }
   if (!Ok(hipModuleLaunchKernel(dev->functions[kernel], grid.x, grid.y, grid.z, block.x, block.y, block.z, 0,
                                 dev->stream, params, nullptr),
           "hipModuleLaunchKernel", err, errlen)) {
@@ -228,6 +242,10 @@ int halo_launch(halo_device* dev, halo_kernel_id kernel, halo_dim3 grid, halo_di
     return -1;
   }
   if (dev->capturing) ++dev->captured;
+  if (timing) {
+    (void)hipEventRecord(tm.b, dev->stream);
+    dev->timed.push_back(tm);
+  }
   return 0;
 }
 
@@ -289,5 +307,40 @@ int halo_timer_stop(halo_device* dev, float* ms, char* err, size_t errlen) {
 }
 
 void* halo_device_stream(halo_device* dev) { return dev ? static_cast<void*>(dev->stream) : nullptr; }
+
+int halo_profile_begin(halo_device* dev, char* err, size_t errlen) {
+  if (dev == nullptr) return SetErr(err, errlen, "null device"), -1;
+  dev->profiling = true;
+  return 0;
+}
+
+int halo_profile_end(halo_device* dev, char* report, size_t len, char* err, size_t errlen) {
+  if (dev == nullptr) return SetErr(err, errlen, "null device"), -1;
+  dev->profiling = false;
+  if (!Ok(hipStreamSynchronize(dev->stream), "hipStreamSynchronize", err, errlen)) return -1;
+  std::vector<double> total(dev->functions.size(), 0.0);
+  std::vector<std::size_t> count(dev->functions.size(), 0);
+  for (const auto& t : dev->timed) {
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, t.a, t.b) == hipSuccess) {
+      total[t.k] += ms;
+      ++count[t.k];
+    }
+    (void)hipEventDestroy(t.a);
+    (void)hipEventDestroy(t.b);
+  }
+  dev->timed.clear();
+  std::string out;
+  for (std::size_t i = 0; i < total.size(); ++i)
+    if (count[i]) {
+      char line[256];
+      std::snprintf(line, sizeof line, "%s %zu %.3f\n", dev->names[i].c_str(), count[i], total[i] * 1e3);
+      out += line;
+    }
+  if (report && len) {
+    std::snprintf(report, len, "%s", out.c_str());
+  }
+  return 0;
+}
 
 }  // extern "C"

@@ -82,6 +82,22 @@ class PagedKV(C.Structure):
         (n, C.c_uint32) for n in ("sessions", "kv_heads", "head_dim", "max_pages", "prefix", "max_context")]
 
 
+class ModelConfig(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in (
+        "vocab", "hidden", "layers", "attn_interval", "gdn_k_heads", "gdn_v_heads", "gdn_head_dim", "conv_kernel",
+        "q_heads", "kv_heads", "head_dim", "rotary_dim", "n_experts", "n_used", "expert_ff", "shared_ff")] + [
+        ("rope_theta", C.c_float), ("rms_eps", C.c_float)] + [
+        (n, C.c_uint32) for n in ("max_sessions", "max_context", "prefix_tokens", "pad")]
+
+
+def c4_config(max_sessions=4, prefix_tokens=8192, max_context=8192 + 256 + 128):
+    """48 layers (3 DeltaNet : 1 GQA), hidden 2048, vocab 151936, MoE as C2."""
+    return ModelConfig(vocab=151936, hidden=2048, layers=48, attn_interval=4, gdn_k_heads=16, gdn_v_heads=32,
+                       gdn_head_dim=128, conv_kernel=4, q_heads=16, kv_heads=2, head_dim=256, rotary_dim=64,
+                       n_experts=512, n_used=10, expert_ff=512, shared_ff=512, rope_theta=1e7, rms_eps=1e-6,
+                       max_sessions=max_sessions, max_context=max_context, prefix_tokens=prefix_tokens)
+
+
 ERRLEN = 1024
 _VP, _SZ, _U32, _U64, _F32, _I32 = C.c_void_p, C.c_size_t, C.c_uint32, C.c_uint64, C.c_float, C.c_int32
 _ERR = [C.c_char_p, _SZ]
@@ -111,6 +127,8 @@ _SIGS = {
     "halo_timer_start": (C.c_int, [_VP], True),
     "halo_timer_stop": (C.c_int, [_VP, C.POINTER(_F32)], True),
     "halo_device_stream": (_VP, [_VP], False),
+    "halo_profile_begin": (C.c_int, [_VP], True),
+    "halo_profile_end": (C.c_int, [_VP, _VP, _SZ], True),
     "halo_engine_create": (C.c_int, [_VP, C.POINTER(_VP)], True),
     "halo_engine_destroy": (None, [_VP], False),
     "halo_engine_device": (_VP, [_VP], False),
@@ -131,6 +149,17 @@ _SIGS = {
     "halo_gdn_chunk_table": (_U32, [_VP, _U32, _VP, _VP], False),
     "halo_op_gdn_prefill_workspace_bytes": (_SZ, [_U32, _U32], False),
     "halo_op_gdn_prefill": (C.c_int, [_VP] + [_VP] * 7 + [_U32, _U32, _VP, _VP, _U32, _U32, _U32, _VP, _SZ], True),
+    "halo_model_create": (C.c_int, [_VP, C.POINTER(ModelConfig), _U64, C.POINTER(_VP)], True),
+    "halo_model_destroy": (None, [_VP], False),
+    "halo_model_weight_bytes": (_U64, [_VP], False),
+    "halo_model_device_bytes": (_U64, [_VP], False),
+    "halo_model_set_session": (C.c_int, [_VP, _U32, _VP, _U32, _U32], True),
+    "halo_model_fork": (C.c_int, [_VP, _U32, _U32], True),
+    "halo_model_reset": (C.c_int, [_VP], True),
+    "halo_model_run": (C.c_int, [_VP, _U32, _U32, _U32], True),
+    "halo_model_step_eager": (C.c_int, [_VP, _U32, _U32], True),
+    "halo_model_history": (C.c_int, [_VP, _U32, _VP, _U32], True),
+    "halo_model_positions": (C.c_int, [_VP, _VP, _U32], True),
     "halo_op_moe_workspace_bytes": (_SZ, [C.POINTER(MoeWeights), _U32], False),
     "halo_op_moe_views": (C.c_int, [C.POINTER(MoeWeights), _U32, _VP, C.POINTER(MoeViews)], True),
     "halo_op_moe_decode": (C.c_int, [_VP, C.POINTER(MoeWeights), _VP, _VP, _U32, _VP, _SZ], True),
@@ -301,6 +330,18 @@ class Device:
         _call("halo_timer_stop", self.handle, C.byref(ms))
         return float(ms.value)
 
+    def profile_begin(self):
+        _call("halo_profile_begin", self.handle)
+
+    def profile_end(self) -> dict:
+        buf = C.create_string_buffer(1 << 16)
+        _call("halo_profile_end", self.handle, buf, 1 << 16)
+        out = {}
+        for line in buf.value.decode().splitlines():
+            name, n, us = line.split()
+            out[name] = (int(n), float(us))
+        return out
+
     def begin_capture(self):
         _call("halo_begin_capture", self.handle)
 
@@ -347,6 +388,51 @@ class Q8Weights:
         q = self.qs.download_range(r0 * self.qstride, n * self.qstride).reshape(n, self.qstride)[:, : self.cols]
         d = self.d.download_range(r0 * (self.cols // 32) * 2, n * (self.cols // 32)).reshape(n, self.cols // 32)
         return q, d
+
+
+class Model:
+    """halo_model: the synthetic hybrid model on the device (include/halo_model.h)."""
+
+    def __init__(self, dev: Device, cfg: ModelConfig, seed: int = 0):
+        self.dev, self.cfg = dev, cfg
+        h = C.c_void_p()
+        _call("halo_model_create", dev.eng, C.byref(cfg), seed, C.byref(h))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().halo_model_destroy(self.h)
+            self.h = None
+
+    @property
+    def weight_bytes(self) -> int:
+        return int(lib().halo_model_weight_bytes(self.h))
+
+    def set_session(self, s: int, prompt, nkv: int = 0):
+        p = np.ascontiguousarray(prompt, np.uint32)
+        _call("halo_model_set_session", self.h, s, p.ctypes.data, len(p), nkv)
+
+    def fork(self, src: int, dst: int):
+        _call("halo_model_fork", self.h, src, dst)
+
+    def reset(self):
+        _call("halo_model_reset", self.h)
+
+    def run(self, S: int, steps: int, prefix: int = 0):
+        _call("halo_model_run", self.h, S, prefix, steps)
+
+    def step_eager(self, S: int, prefix: int = 0):
+        _call("halo_model_step_eager", self.h, S, prefix)
+
+    def history(self, s: int, n: int) -> np.ndarray:
+        out = np.zeros(n, np.uint32)
+        _call("halo_model_history", self.h, s, out.ctypes.data, n)
+        return out
+
+    def positions(self, S: int) -> np.ndarray:
+        out = np.zeros(S, np.uint32)
+        _call("halo_model_positions", self.h, out.ctypes.data, S)
+        return out
 
 
 class MoeLayer:

@@ -1,0 +1,71 @@
+/* halo-flash MI355X hybrid model: the decode step of the engine over the hot-path operators.
+ *
+ * The reference's FlashNextGpu (src/engine/flash_next_gpu.hpp:38-925) owns weights, sessions and the captured decode
+ * step; Step/StepBatch (flash_next_gpu.cpp:899-1047, batch_decode.cpp:629-817) run one token per session through
+ * every layer and sample. halo_model is that object for the synthetic hybrid model of the benchmark: Gated DeltaNet
+ * and gated GQA layers (every attn_interval-th layer is attention), a routed MoE FFN with a shared expert in every
+ * layer, Q8_0 projections, greedy decoding. Weights are seeded on the device. Sessions share the first
+ * prefix_tokens positions of their KV cache (paged, 16 tokens per page). One step for S sessions is recorded once
+ * into a HIP graph and replayed; the per-step token and position live in device memory and a final launch advances
+ * them (prompt tokens are fed while a session's prompt lasts, its own argmax afterwards).
+ * Functions return 0 / -1 with a message in err (halo_rt.h convention). */
+#ifndef HALO_MODEL_H_
+#define HALO_MODEL_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "halo_ops.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct halo_model_config {
+  uint32_t vocab, hidden, layers, attn_interval;
+  uint32_t gdn_k_heads, gdn_v_heads, gdn_head_dim, conv_kernel;
+  uint32_t q_heads, kv_heads, head_dim, rotary_dim;
+  uint32_t n_experts, n_used, expert_ff, shared_ff;
+  float rope_theta, rms_eps;
+  uint32_t max_sessions, max_context; /* context per session, including the shared prefix */
+  uint32_t prefix_tokens;             /* shared-prefix capacity (multiple of 64; 0: none) */
+  uint32_t pad;
+} halo_model_config;
+
+typedef struct halo_model halo_model;
+
+/* Allocates and seeds every weight and state buffer on the engine's device. */
+int halo_model_create(halo_engine* eng, const halo_model_config* cfg, uint64_t seed, halo_model** out, char* err,
+                      size_t errlen);
+void halo_model_destroy(halo_model* m);
+/* Bytes of weights (algorithmic: Q8_0 at 34 bytes per 32 weights, fp32 tensors at 4) and of device allocations. */
+uint64_t halo_model_weight_bytes(const halo_model* m);
+uint64_t halo_model_device_bytes(const halo_model* m);
+
+/* Session s: its prompt (host tokens, copied to the device), and the number of positions already in its cache
+ * (0 for a fresh session; prefix_tokens for a session forked after the shared prefix). The next step feeds
+ * prompt[nkv]. Not capturable (uploads). */
+int halo_model_set_session(halo_model* m, uint32_t s, const uint32_t* prompt, uint32_t prompt_len, uint32_t nkv,
+                           char* err, size_t errlen);
+/* Copies session src's recurrent state (DeltaNet state and conv history of every layer) to dst; the shared prefix
+ * pages are common to both already (the reference's ForkSession, flash_next_gpu.hpp:347-350). */
+int halo_model_fork(halo_model* m, uint32_t src, uint32_t dst, char* err, size_t errlen);
+/* Zeroes every session's recurrent state and position. */
+int halo_model_reset(halo_model* m, char* err, size_t errlen);
+
+/* Enqueues `steps` decode steps for sessions 0..S-1 (one token each). attn_prefix: positions read once for all
+ * sessions (the shared prefix, a multiple of 64, <= each session's position; 0 when S == 1 or nothing is shared).
+ * The first call with a given (S, attn_prefix) records the step into a HIP graph; later calls replay it. */
+int halo_model_run(halo_model* m, uint32_t S, uint32_t attn_prefix, uint32_t steps, char* err, size_t errlen);
+/* The same step launched eagerly (no graph): for profilers and debugging. */
+int halo_model_step_eager(halo_model* m, uint32_t S, uint32_t attn_prefix, char* err, size_t errlen);
+
+/* Host copies of session s's produced tokens history[pos] (the argmax after position pos-1 ... ) and nkv. */
+int halo_model_history(halo_model* m, uint32_t s, uint32_t* out, uint32_t n, char* err, size_t errlen);
+int halo_model_positions(halo_model* m, uint32_t* nkv_out, uint32_t S, char* err, size_t errlen);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HALO_MODEL_H_ */

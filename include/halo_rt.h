@@ -110,6 +110,12 @@ int halo_timer_stop(halo_device* dev, float* ms, char* err, size_t errlen);
 /* The raw HIP stream (hipStream_t) of the device, for callers that interoperate with other HIP code. */
 void* halo_device_stream(halo_device* dev);
 
+/* Per-launch timing of eager launches (the reference's StartKernelTiming / StopKernelTiming,
+ * src/engine/flash_next_gpu.cpp:160-210): between begin and end every non-captured launch is bracketed by events;
+ * end synchronizes and writes one line per kernel, "name launches total_microseconds", into report. */
+int halo_profile_begin(halo_device* dev, char* err, size_t errlen);
+int halo_profile_end(halo_device* dev, char* report, size_t len, char* err, size_t errlen);
+
 #ifdef __cplusplus
 }
 #endif

@@ -65,6 +65,8 @@ def run_gpu(args):
             return run_gdn(args, dev, H, res)
         if args.mode == "c4":
             return run_c4(args, dev, H, res)
+        if args.mode == "pmc":
+            return run_pmc(args, dev, H, res)
         # ---------------- C1 pass at M=1 (the bench value) and the M sweep ----------------
         per_copy = sum(q8_bytes(r, c) for r, c in C1_SHAPES)
         copies = max(2, -(-MIN_ROTATION_BYTES // per_copy))
@@ -138,7 +140,14 @@ def run_gpu(args):
         res["c1_sweep"] = sweep
         log(f"[bench] C1 sweep {sweep}")
         del sets
-        return run_c0(args, dev, H, res)
+        run_c0(args, dev, H, res)
+        if not args.quick:
+            roof = res["roofline"]
+            run_moe(args, dev, H, res)
+            run_gdn(args, dev, H, res)
+            run_c4(args, dev, H, res)
+            res["roofline"] = roof
+        return res
     finally:
         dev.close()
 
@@ -213,6 +222,32 @@ def run_moe(args, dev, H, res):
                         "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
         log(f"[bench] moe T={T}: {out[f'T{T}']}")
     res["moe"] = out
+    res["roofline"] = None
+    return res
+
+
+def run_pmc(args, dev, H, res):
+    """Eager launches for hardware-counter passes (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE): a plain streaming
+    read and a copy of C0-sized buffers (the calibration: their algorithmic bytes are known) and the C0 GEMV, each 40
+    times over rotated copies (> 600 MB) so that every launch reads HBM."""
+    n16 = C0_BYTES // 16
+    nbuf = 40
+    pool = dev.array(nbuf * n16 * 16, np.uint8)
+    dst = dev.array(n16 * 16, np.uint8)
+    sink = dev.array(4, np.int32)
+    for i in range(nbuf):
+        dev.launch("halo_stream_read", (4096,), (256,), [("ptr", pool.ptr + i * n16 * 16), ("u64", n16), sink])
+    for i in range(nbuf):
+        dev.launch("halo_stream_copy", (4096,), (256,), [("ptr", pool.ptr + i * n16 * 16), dst, ("u64", n16)])
+    del pool
+    ws0 = [H.Q8Weights(dev, 4096, 4096).synth(dev, seed=70000 + i) for i in range(nbuf)]
+    x0 = dev.array(4096, np.float32)
+    dev.op("synth_f32", x0.ptr, 4096, 9, 1.0)
+    x0q, x0s, y0 = dev.array(4096, np.int8), dev.array(128, np.float32), dev.array(4096, np.float32)
+    dev.op("quantize_q8", x0.ptr, x0q.ptr, x0s.ptr, 1, 4096)
+    for w in ws0:
+        dev.op("matvec_q8a8", ctypes.byref(w.desc), x0q.ptr, x0s.ptr, y0.ptr, 1, 4096)
+    dev.sync()
     res["roofline"] = None
     return res
 
@@ -442,6 +477,12 @@ def run_c0(args, dev, H, res):
             dev.free_graph(g)
         log(f"[bench] C0 {c0}")
         best = c0[str(tilings[0])]
+        traffic = None
+        prof = ROOT / "profiles" / "gemv_q8a8_c0_4096x4096.md"
+        if prof.exists():
+            for line in prof.read_text().splitlines():
+                if line.startswith("traffic_bytes_per_launch:"):
+                    traffic = int(line.split(":")[1])
         res["roofline"] = {
             "bound": "hbm",
             "kernel": "halo_gemv_q8a8_l64_r1_b1 (C0 4096x4096 Q8_0 GEMV)",
@@ -449,7 +490,8 @@ def run_c0(args, dev, H, res):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(best["GBps"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": "profiles/gemv_q8a8_c0_4096x4096.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)",
             "us_per_launch": best["us_per_gemv"],
             "algorithmic_bytes_per_launch": C0_BYTES,
         }
@@ -520,8 +562,9 @@ def main():
     p.add_argument("--sweep", action="store_true", help="also time alternative C0 GEMV tilings")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--quick", action="store_true", help="only the C1 value and the C0 roofline")
     p.add_argument("--eager", action="store_true", help="launch without graphs (for profiling kernel durations)")
-    p.add_argument("--mode", choices=["all", "c0", "membw", "moe", "gdn", "c4"], default="all",
+    p.add_argument("--mode", choices=["all", "c0", "membw", "moe", "gdn", "c4", "pmc"], default="all",
                    help="c0: only the C0 GEMV loop (for profiling one kernel shape)")
     args = p.parse_args()
     if args.gpus != 1:
@@ -529,7 +572,7 @@ def main():
               "(the path is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
         sys.exit(2)
     res = run_gpu(args)
-    if args.mode in ("c0", "membw", "moe", "gdn", "c4"):
+    if args.mode in ("c0", "membw", "moe", "gdn", "c4", "pmc"):
         print(json.dumps({k: res.get(k) for k in ("roofline", "c0_tilings", "membw", "moe", "gdn", "c4")}),
               flush=True)
         return
@@ -551,6 +594,12 @@ def main():
         "roofline": res["roofline"],
         "c1_sweep": res["c1_sweep"],
     }
+    for k in ("moe", "gdn", "c4"):
+        if k in res:
+            line[k] = res[k]
+    if "c4" in res:
+        line["decode_tok_s"] = {"1_session": res["c4"]["decode_tok_s_1_session"],
+                                "4_sessions": res["c4"]["decode_tok_s_4_sessions"]}
     if "c0_tilings" in res:
         line["c0_tilings"] = res["c0_tilings"]
     if not args.no_cpu:

@@ -6,7 +6,7 @@ using namespace halo::engine;
 
 namespace {
 
-constexpr std::uint32_t kChunk = 64;
+constexpr std::uint32_t kChunk = 32;
 
 int Check(const halo_paged_kv* kv, std::uint32_t Hq, char* err, std::size_t errlen) {
   if (kv == nullptr || kv->k_pool == nullptr || kv->v_pool == nullptr || kv->pages == nullptr || kv->nkv == nullptr)
@@ -16,8 +16,9 @@ int Check(const halo_paged_kv* kv, std::uint32_t Hq, char* err, std::size_t errl
     return SetErr(err, errlen, "attn: %u sessions x %u q heads / %u kv heads unsupported", kv->sessions, Hq,
                   kv->kv_heads),
            -1;
-  if (kv->prefix % kChunk != 0 || kv->prefix > kv->max_context || kv->max_context > kv->max_pages * 16)
-    return SetErr(err, errlen, "attn: prefix %u must be a multiple of 64 within max_context %u <= 16 * %u pages",
+  if (kv->prefix % 64 != 0 || kv->prefix > kv->max_context || kv->max_context > kv->max_pages * 16 ||
+      CeilDiv(kv->max_context, kChunk) > 1024)
+    return SetErr(err, errlen, "attn: prefix %u must be a multiple of 64 within max_context %u <= 16 * %u pages (<= 32K)",
                   kv->prefix, kv->max_context, kv->max_pages),
            -1;
   return 0;
@@ -41,8 +42,9 @@ size_t halo_op_attn_decode_workspace_bytes(const halo_paged_kv* kv, uint32_t Hq)
   return items * slots * (2 + kv->head_dim) * sizeof(float);
 }
 
-int halo_op_attn_decode(halo_engine* eng, const halo_paged_kv* kv, const float* q, const float* gate, float* o,
-                        uint32_t Hq, void* ws, size_t ws_bytes, char* err, size_t errlen) {
+int halo_op_attn_decode_q8(halo_engine* eng, const halo_paged_kv* kv, const float* q, const float* gate, float* o,
+                           int8_t* oq, float* os, uint32_t Hq, void* ws, size_t ws_bytes, char* err,
+                           size_t errlen) {
   if (Check(kv, Hq, err, errlen) != 0) return -1;
   const std::size_t need = halo_op_attn_decode_workspace_bytes(kv, Hq);
   if (ws == nullptr || ws_bytes < need) return SetErr(err, errlen, "attn: workspace %zu < %zu", ws_bytes, need), -1;
@@ -60,8 +62,14 @@ int halo_op_attn_decode(halo_engine* eng, const halo_paged_kv* kv, const float* 
     if (Launch(eng, "halo_attn_decode_partial", D3(static_cast<std::uint32_t>(items)), D3(256), a, err, errlen) != 0)
       return -1;
   }
-  const halo_arg a[] = {Ptr(pm), Ptr(pl), Ptr(pacc), Ptr(gate), Ptr(o), U32(S), U32(Hq), U32(Hkv), U32(pc), U32(sc)};
+  const halo_arg a[] = {Ptr(pm), Ptr(pl), Ptr(pacc), Ptr(gate), Ptr(o), Ptr(oq), Ptr(os), U32(S), U32(Hq), U32(Hkv),
+                        U32(pc), U32(sc)};
   return Launch(eng, "halo_attn_decode_combine", D3(S * Hq), D3(256), a, err, errlen);
+}
+
+int halo_op_attn_decode(halo_engine* eng, const halo_paged_kv* kv, const float* q, const float* gate, float* o,
+                        uint32_t Hq, void* ws, size_t ws_bytes, char* err, size_t errlen) {
+  return halo_op_attn_decode_q8(eng, kv, q, gate, o, nullptr, nullptr, Hq, ws, ws_bytes, err, errlen);
 }
 
 int halo_op_kv_append(halo_engine* eng, const halo_paged_kv* kv, const float* k, const float* v, char* err,

@@ -147,7 +147,7 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
     const halo_arg a[] = {Ptr(m->res.device), Ptr(have_delta ? m->delta.device : nullptr), Ptr(w.device),
                           Ptr(m->xn.device), Ptr(quant ? m->xq.device : nullptr), Ptr(m->xs.device), U32(H), Val(eps)};
     have_delta = false;
-    return Launch(eng, "halo_add_rmsnorm_q8", D3(S), D3(256), a, err, errlen);
+    return Launch(eng, "halo_add_rmsnorm_q8", D3(S), D3(1024), a, err, errlen);
   };
   auto gemv = [&](const Q8& w, const halo_buffer& xq, const halo_buffer& xs, const halo_buffer& y) {
     return halo_op_matvec_q8a8(eng, &w.m, P<int8_t>(xq), P<float>(xs), P<float>(y), S, w.m.rows, err, errlen);
@@ -193,11 +193,10 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
         if (Launch(eng, "halo_attn_prep_decode", D3(S), D3(256), a, err, errlen) != 0) return -1;
       }
       const halo_paged_kv kv = KvDesc(m, L, S, prefix);
-      if (halo_op_attn_decode(eng, &kv, P<float>(m->q), P<float>(m->agate), P<float>(m->ao), Hq, m->attn_ws.device,
-                              m->attn_ws_bytes, err, errlen) != 0)
+      if (halo_op_attn_decode_q8(eng, &kv, P<float>(m->q), P<float>(m->agate), nullptr, P<int8_t>(m->oq),
+                                 P<float>(m->os), Hq, m->attn_ws.device, m->attn_ws_bytes, err, errlen) != 0)
         return -1;
-      if (halo_op_quantize_q8(eng, P<float>(m->ao), P<int8_t>(m->oq), P<float>(m->os), S, Hq * hd, err, errlen) != 0)
-        return -1;
+      (void)hd;
       if (gemv(L.o, m->oq, m->os, m->delta) != 0) return -1;
     }
     have_delta = true;

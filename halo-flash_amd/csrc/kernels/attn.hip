@@ -7,7 +7,7 @@
 // KV layout in HBM: pages of 16 tokens; K and V pools [page][kv_head][16][d] fp32; each session has a page table
 // [max_pages]. Sessions of one batch share their first `prefix` tokens (identical page-table entries): a prefix
 // chunk is read once and scored against the queries of every session (S * G query vectors), a suffix chunk only
-// against its own session's G queries. Each (kv head, 64-token chunk) is one block producing flash partials
+// against its own session's G queries. Each (kv head, 32-token chunk) is one block producing flash partials
 // (running max, sum, weighted V); halo_attn_decode_combine merges them per (session, head) and applies the gate.
 #include "common.h"
 
@@ -16,15 +16,15 @@ using halo::kWave;
 namespace {
 constexpr int kHd = 256;      // head dim
 constexpr int kPage = 16;     // tokens per page
-constexpr int kChunk = 64;    // tokens per block
+constexpr int kChunk = 32;    // tokens per block
 constexpr int kMaxQ = 32;     // query vectors per block (sessions * G)
 }  // namespace
 
 // grid (Hkv * (prefix_chunks + S * suffix_chunks)), block 256.
 //   q [S][Hq][256]; kpool, vpool [pages][Hkv][16][256]; pages [S][max_pages]; nkv [S] visible positions;
 //   partial m, l [items][S * G], acc [items][S * G][256] (item = blockIdx.x).
-// Prefix chunks cover tokens [64 c, 64 c + 64) < prefix of every session; suffix chunk c of session s covers
-// [prefix + 64 c, ...) up to nkv[s]; positions at or past nkv[s] are masked, empty chunks record m = -inf.
+// Prefix chunks cover tokens [32 c, 32 c + 32) < prefix of every session; suffix chunk c of session s covers
+// [prefix + 32 c, ...) up to nkv[s]; positions at or past nkv[s] are masked, empty chunks record m = -inf.
 extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
     const float* __restrict__ q, const float* __restrict__ kpool, const float* __restrict__ vpool,
     const std::uint32_t* __restrict__ pages, const std::uint32_t* __restrict__ nkv, float* __restrict__ pm,
@@ -32,6 +32,7 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
     std::uint32_t prefix, std::uint32_t max_pages, std::uint32_t prefix_chunks, std::uint32_t suffix_chunks) {
   __shared__ float qs[kMaxQ][kHd];       // 32 KB
   __shared__ float ps[kMaxQ][kChunk + 1];
+  static_assert(kChunk <= kWave, "a chunk's tokens are the lanes of a wave");
   const std::uint32_t G = Hq / Hkv, x = blockIdx.x, kvh = x % Hkv, c = x / Hkv;
   const std::uint32_t t = threadIdx.x, wave = t / kWave, lane = t % kWave;
   const bool is_prefix = c < prefix_chunks;
@@ -61,7 +62,7 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
   __syncthreads();
   // scores: lane = token of the chunk, wave = a quarter of the queries
   const std::uint32_t tok = start + lane;
-  const bool live = tok < limit;
+  const bool live = lane < static_cast<std::uint32_t>(kChunk) && tok < limit;
   const std::uint32_t page = pages[static_cast<std::size_t>(sess) * max_pages + min(tok, limit - 1) / kPage];
   const float* krow = kpool + ((static_cast<std::size_t>(page) * Hkv + kvh) * kPage + (tok % kPage)) * kHd;
   const float scale = 1.0f / sqrtf(static_cast<float>(kHd));
@@ -70,16 +71,21 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
   float sc[kQPerWave];
 #pragma unroll
   for (int i = 0; i < kQPerWave; ++i) sc[i] = 0.0f;
-  for (std::uint32_t d4 = 0; d4 < kHd / 4; ++d4) {
-    const float4 kv = reinterpret_cast<const float4*>(krow)[d4];
+  constexpr int kKU = 16;  // row pieces loaded ahead of their arithmetic
+  for (std::uint32_t d0 = 0; d0 < kHd / 4; d0 += kKU) {
+    float4 kv[kKU];
 #pragma unroll
-    for (int i = 0; i < kQPerWave; ++i) {
-      const std::uint32_t qi = wave * per_wave + i;
-      if (i < static_cast<int>(per_wave) && qi < nq) {
-        const float4 qv = reinterpret_cast<const float4*>(&qs[qi][0])[d4];
-        sc[i] += kv.x * qv.x + kv.y * qv.y + kv.z * qv.z + kv.w * qv.w;
+    for (int u = 0; u < kKU; ++u) kv[u] = reinterpret_cast<const float4*>(krow)[d0 + u];
+#pragma unroll
+    for (int u = 0; u < kKU; ++u)
+#pragma unroll
+      for (int i = 0; i < kQPerWave; ++i) {
+        const std::uint32_t qi = wave * per_wave + i;
+        if (i < static_cast<int>(per_wave) && qi < nq) {
+          const float4 qv = reinterpret_cast<const float4*>(&qs[qi][0])[d0 + u];
+          sc[i] += kv[u].x * qv.x + kv[u].y * qv.y + kv[u].z * qv.z + kv[u].w * qv.w;
+        }
       }
-    }
   }
 #pragma unroll
   for (int i = 0; i < kQPerWave; ++i) {
@@ -89,7 +95,7 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
       const float m = halo::GroupMax(s);
       const float p = live ? expf(s - m) : 0.0f;
       const float l = halo::GroupSum(p);
-      ps[qi][lane] = p;
+      if (lane < static_cast<std::uint32_t>(kChunk)) ps[qi][lane] = p;
       if (lane == 0) {
         const std::uint32_t slot = is_prefix ? qi : sess * G + qi;
         m_out[slot] = m;
@@ -133,12 +139,13 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
 }
 
 // grid (S * Hq), block 256: merges the partials of session s, head h over its prefix and suffix chunks
-// (log-sum-exp), o = acc / l, then o *= sigmoid(gate) when gate is non-null. o, gate [S][Hq][256]. Items are at most
-// 1024 (64-token chunks of a 64K context).
+// (log-sum-exp), o = acc / l, then o *= sigmoid(gate) when gate is non-null. o, gate [S][Hq][256] (o may be null);
+// with oq non-null also the Q8 quantization of o (oq [S][Hq * 256], os [S][Hq * 8]). At most 1024 items.
 extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_combine(
     const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ pacc,
-    const float* __restrict__ gate, float* __restrict__ o, std::uint32_t S, std::uint32_t Hq, std::uint32_t Hkv,
-    std::uint32_t prefix_chunks, std::uint32_t suffix_chunks) {
+    const float* __restrict__ gate, float* __restrict__ o, std::int8_t* __restrict__ oq, float* __restrict__ os,
+    std::uint32_t S, std::uint32_t Hq, std::uint32_t Hkv, std::uint32_t prefix_chunks,
+    std::uint32_t suffix_chunks) {
   __shared__ float wts[1024];
   __shared__ float red[4];
   const std::uint32_t G = Hq / Hkv, s = blockIdx.x / Hq, h = blockIdx.x % Hq, kvh = h / G, g = h % G;
@@ -186,7 +193,14 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_combine(
   float r = acc / L;
   const std::size_t off = (static_cast<std::size_t>(s) * Hq + h) * kHd + t;
   if (gate != nullptr) r *= halo::Sigmoid(gate[off]);
-  o[off] = r;
+  if (o != nullptr) o[off] = r;
+  if (oq != nullptr) {
+    // the row's Q8 quantization for the output projection: 32-value blocks are half waves
+    const float amax = halo::GroupMax<32>(fabsf(r));
+    const float scale = amax / 127.0f;
+    oq[off] = static_cast<std::int8_t>(scale > 0.0f ? static_cast<int>(rintf(r / scale)) : 0);
+    if (t % 32 == 0) os[off / 32] = scale;
+  }
 }
 
 // Appends one token's K and V per session at position nkv[s] - 1: k, v [S][Hkv][256] -> pools via page tables.

@@ -32,9 +32,9 @@ __device__ __forceinline__ void Quant32(float v, std::int8_t* xq, float* xs, std
 }
 }  // namespace
 
-// grid (S), block 256 (H <= 8192, H % 256 == 0). res [S][H] += delta [S][H] (delta may be null), then
+// grid (S), block 1024 (H <= 8192, H % 32 == 0). res [S][H] += delta [S][H] (delta may be null), then
 // xn = RMSNorm(res) * w (fp32, may be null) and its Q8 quantization xq [S][H], xs [S][H / 32] (may be null).
-extern "C" __global__ void __launch_bounds__(256)
+extern "C" __global__ void __launch_bounds__(1024)
     halo_add_rmsnorm_q8(float* __restrict__ res, const float* __restrict__ delta, const float* __restrict__ w,
                         float* __restrict__ xn, std::int8_t* __restrict__ xq, float* __restrict__ xs,
                         std::uint32_t H, float eps) {

@@ -129,7 +129,7 @@ int halo_op_gdn_decode(halo_engine* eng, float* state, const float* q, const flo
  * (src/kernels/core.hip:898): per query head h (kv head h / (Hq/Hkv)), o = softmax(q.K^T/sqrt(d)) V * sigmoid(gate).
  * KV pools [pages][Hkv][16][d] fp32, page tables [S][max_pages] (uint32), nkv [S] visible positions (device
  * memory, so a captured graph replays at every position). The first `prefix` tokens (a multiple of 64) have the same
- * pages in every session's table and are read once for all sessions. d = 256, S * Hq / Hkv <= 32. */
+ * pages in every session's table and are read once for all sessions. d = 256, S * Hq / Hkv <= 32, context <= 32K. */
 typedef struct halo_paged_kv {
   float* k_pool;
   float* v_pool;
@@ -143,6 +143,11 @@ size_t halo_op_attn_decode_workspace_bytes(const halo_paged_kv* kv, uint32_t q_h
 /* o [S][Hq][d] = attention(q [S][Hq][d]) over each session's nkv positions; gate [S][Hq][d] or NULL. Two launches. */
 int halo_op_attn_decode(halo_engine* eng, const halo_paged_kv* kv, const float* q, const float* gate, float* o,
                         uint32_t q_heads, void* ws, size_t ws_bytes, char* err, size_t errlen);
+/* The same, o optional (may be NULL), also writing o's Q8 quantization for the output projection:
+ * oq [S][Hq * d] int8, os [S][Hq * d / 32]. */
+int halo_op_attn_decode_q8(halo_engine* eng, const halo_paged_kv* kv, const float* q, const float* gate, float* o,
+                           int8_t* oq, float* os, uint32_t q_heads, void* ws, size_t ws_bytes, char* err,
+                           size_t errlen);
 /* Writes one token's k, v [S][Hkv][d] at position nkv[s] - 1 of each session. */
 int halo_op_kv_append(halo_engine* eng, const halo_paged_kv* kv, const float* k, const float* v, char* err,
                       size_t errlen);

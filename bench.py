@@ -67,6 +67,8 @@ def run_gpu(args):
             return run_c4(args, dev, H, res)
         if args.mode == "pmc":
             return run_pmc(args, dev, H, res)
+        if args.mode == "attn":
+            return run_attn(args, dev, H, res)
         # ---------------- C1 pass at M=1 (the bench value) and the M sweep ----------------
         per_copy = sum(q8_bytes(r, c) for r, c in C1_SHAPES)
         copies = max(2, -(-MIN_ROTATION_BYTES // per_copy))
@@ -226,6 +228,72 @@ def run_moe(args, dev, H, res):
     return res
 
 
+def run_attn(args, dev, H, res):
+    """C4's decode attention alone (16 q heads, 2 kv heads, head_dim 256, fp32 paged KV): 1 session at 8576
+    visible positions, and 4 sessions sharing an 8192-token prefix with 384 suffix positions each. Eight KV pools
+    (> 256 MB) are rotated so K/V come from HBM. Bytes = K/V rows read (the shared prefix once)."""
+    import ctypes as C
+
+    Hq, Hkv, D, PAGE, ncopy = 16, 2, 256, 16, 8
+    out = {}
+    for S, prefix, suffix in ((1, 0, 8576), (4, 8192, 384)):
+        max_context = prefix + suffix
+        max_pages = -(-max_context // PAGE)
+        total = prefix // PAGE + S * (max_pages - prefix // PAGE)
+        pages = np.zeros((S, max_pages), np.uint32)
+        nxt = prefix // PAGE
+        for s in range(S):
+            pages[s, : prefix // PAGE] = np.arange(prefix // PAGE)
+            pages[s, prefix // PAGE:] = np.arange(nxt, nxt + max_pages - prefix // PAGE)
+            nxt += max_pages - prefix // PAGE
+        nkv = np.full(S, max_context, np.uint32)
+        gp, gn = dev.to_device(pages), dev.to_device(nkv)
+        keep, descs = [gp, gn], []
+        for i in range(ncopy):
+            k = dev.array((total, Hkv, PAGE, D), np.float32)
+            v = dev.array((total, Hkv, PAGE, D), np.float32)
+            dev.op("synth_f32", k.ptr, k.nbytes // 4, 100 + i, 1.0)
+            dev.op("synth_f32", v.ptr, v.nbytes // 4, 200 + i, 1.0)
+            keep += [k, v]
+            descs.append(H.PagedKV(k.ptr, v.ptr, gp.ptr, gn.ptr, S, Hkv, D, max_pages, prefix, max_context))
+        q = dev.array((S, Hq, D), np.float32)
+        gate = dev.array((S, Hq, D), np.float32)
+        dev.op("synth_f32", q.ptr, S * Hq * D, 7, 1.0)
+        dev.op("synth_f32", gate.ptr, S * Hq * D, 8, 1.0)
+        oq, os_ = dev.array((S, Hq * D), np.int8), dev.array((S, Hq * D // 32), np.float32)
+        wsb = H.lib().halo_op_attn_decode_workspace_bytes(C.byref(descs[0]), Hq)
+        ws = dev.array(wsb, np.uint8)
+        call = lambda d: dev.op("attn_decode_q8", C.byref(d), q.ptr, gate.ptr, None, oq.ptr, os_.ptr, Hq, ws.ptr,
+                                wsb)
+        dev.sync()
+        if args.eager:
+            for _ in range(5):
+                for d in descs:
+                    call(d)
+            dev.sync()
+            continue
+        dev.begin_capture()
+        for d in descs:
+            call(d)
+        g = dev.end_capture()
+        dev.launch_graph(g)
+        dev.sync()
+        nrep = 100
+        dev.timer_start()
+        for _ in range(nrep):
+            dev.launch_graph(g)
+        us = dev.timer_stop() * 1e3 / (nrep * ncopy)
+        dev.free_graph(g)
+        rows = (prefix + S * suffix) * Hkv
+        nbytes = rows * D * 4 * 2
+        out[f"S{S}"] = {"us_per_layer": round(us, 2), "kv_MB": round(nbytes / 1e6, 1),
+                        "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        log(f"[bench] attn S={S}: {out[f'S{S}']}")
+        del keep
+    res["attn"] = out
+    return res
+
+
 def run_pmc(args, dev, H, res):
     """Eager launches for hardware-counter passes (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE): a plain streaming
     read and a copy of C0-sized buffers (the calibration: their algorithmic bytes are known) and the C0 GEMV, each 40
@@ -269,24 +337,17 @@ def run_c4(args, dev, H, res):
     prefix = rng.integers(0, cfg.vocab, P).astype(np.uint32)
     prompts = [np.concatenate([prefix, rng.integers(0, cfg.vocab, SUF).astype(np.uint32)]) for _ in range(4)]
     try:
-        model.set_session(0, prompts[0])
-        t0 = time.perf_counter()
-        dev.timer_start()
-        model.run(1, P)
-        ms_prefix = dev.timer_stop()
-        log(f"[bench] c4: prefix {P} tokens in {ms_prefix / 1e3:.1f} s (one token per step)")
-        for s in (1, 2, 3):
-            model.fork(0, s)
-        if args.eager:  # per-kernel event timing of eager steps at 1 and 4 sessions
+        if args.eager:
+            # per-kernel timing of eager steps at 1 and 4 sessions (no graph launches, so a kernel tracer can
+            # follow it). Only durations matter here: the prefix positions are marked present without running it.
+            for s in range(4):
+                model.set_session(s, prompts[s], nkv=P + SUF - 1)
             prof = {}
             model.step_eager(1)
             dev.profile_begin()
             for _ in range(10):
                 model.step_eager(1)
             prof["S1"] = dev.profile_end()
-            model.fork(1, 0)
-            for s in range(4):
-                model.set_session(s, prompts[s], nkv=P)
             model.step_eager(4, P)
             dev.profile_begin()
             for _ in range(10):
@@ -299,6 +360,14 @@ def run_c4(args, dev, H, res):
                     log(f"    {name:40s} {n // 10:5d}/step {us / 10:9.1f} us/step {us / n:8.2f} us/launch")
             res["c4"] = {"profile": {k: {n: [c, round(u, 1)] for n, (c, u) in v.items()} for k, v in prof.items()}}
             return res
+        model.set_session(0, prompts[0])
+        t0 = time.perf_counter()
+        dev.timer_start()
+        model.run(1, P)
+        ms_prefix = dev.timer_stop()
+        log(f"[bench] c4: prefix {P} tokens in {ms_prefix / 1e3:.1f} s (one token per step)")
+        for s in (1, 2, 3):
+            model.fork(0, s)
         # 1 session
         model.run(1, SUF)
         dev.sync()
@@ -564,7 +633,7 @@ def main():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--quick", action="store_true", help="only the C1 value and the C0 roofline")
     p.add_argument("--eager", action="store_true", help="launch without graphs (for profiling kernel durations)")
-    p.add_argument("--mode", choices=["all", "c0", "membw", "moe", "gdn", "c4", "pmc"], default="all",
+    p.add_argument("--mode", choices=["all", "c0", "membw", "moe", "gdn", "c4", "pmc", "attn"], default="all",
                    help="c0: only the C0 GEMV loop (for profiling one kernel shape)")
     args = p.parse_args()
     if args.gpus != 1:
@@ -572,8 +641,8 @@ def main():
               "(the path is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
         sys.exit(2)
     res = run_gpu(args)
-    if args.mode in ("c0", "membw", "moe", "gdn", "c4", "pmc"):
-        print(json.dumps({k: res.get(k) for k in ("roofline", "c0_tilings", "membw", "moe", "gdn", "c4")}),
+    if args.mode in ("c0", "membw", "moe", "gdn", "c4", "pmc", "attn"):
+        print(json.dumps({k: res.get(k) for k in ("roofline", "c0_tilings", "membw", "moe", "gdn", "c4", "attn")}),
               flush=True)
         return
     line = {

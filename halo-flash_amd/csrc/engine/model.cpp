@@ -399,7 +399,7 @@ int halo_model_reset(halo_model* m, char* err, size_t errlen) {
 
 int halo_model_set_session(halo_model* m, uint32_t s, const uint32_t* prompt, uint32_t len, uint32_t nkv, char* err,
                            size_t errlen) {
-  if (s >= m->c.max_sessions || len > m->c.max_context || nkv > len || nkv >= m->c.max_context)
+  if (s >= m->c.max_sessions || len > m->c.max_context || (len ? nkv >= len : nkv != 0) || nkv >= m->c.max_context)
     return SetErr(err, errlen, "session %u: prompt %u / position %u out of range", s, len, nkv), -1;
   for (std::uint32_t i = 0; i < len; ++i)
     if (prompt[i] >= m->c.vocab) return SetErr(err, errlen, "session %u: token %u out of range", s, prompt[i]), -1;

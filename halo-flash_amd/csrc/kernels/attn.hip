@@ -25,14 +25,19 @@ constexpr int kMaxQ = 32;     // query vectors per block (sessions * G)
 //   partial m, l [items][S * G], acc [items][S * G][256] (item = blockIdx.x).
 // Prefix chunks cover tokens [32 c, 32 c + 32) < prefix of every session; suffix chunk c of session s covers
 // [prefix + 32 c, ...) up to nkv[s]; positions at or past nkv[s] are masked, empty chunks record m = -inf.
+//
+// Every K and V load of the chunk (64 KB) is issued before any arithmetic, so a block keeps its whole chunk in
+// flight. Scores: 16-lane row r of the block owns tokens r and r + 16, lane `sub` of the row dims
+// {4 (16 u + sub) .. +4 : u < 4} (each load instruction reads 256 contiguous bytes per row); the 16 partial dots
+// are summed with row DPP. Weighted V: thread = one of the 256 dims, all 32 tokens in registers.
 extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
     const float* __restrict__ q, const float* __restrict__ kpool, const float* __restrict__ vpool,
     const std::uint32_t* __restrict__ pages, const std::uint32_t* __restrict__ nkv, float* __restrict__ pm,
     float* __restrict__ pl, float* __restrict__ pacc, std::uint32_t S, std::uint32_t Hq, std::uint32_t Hkv,
     std::uint32_t prefix, std::uint32_t max_pages, std::uint32_t prefix_chunks, std::uint32_t suffix_chunks) {
   __shared__ float qs[kMaxQ][kHd];       // 32 KB
-  __shared__ float ps[kMaxQ][kChunk + 1];
-  static_assert(kChunk <= kWave, "a chunk's tokens are the lanes of a wave");
+  __shared__ float sc[kMaxQ][kChunk + 1];
+  static_assert(kChunk == 32 && kPage == 16, "two pages per chunk, two tokens per 16-lane row");
   const std::uint32_t G = Hq / Hkv, x = blockIdx.x, kvh = x % Hkv, c = x / Hkv;
   const std::uint32_t t = threadIdx.x, wave = t / kWave, lane = t % kWave;
   const bool is_prefix = c < prefix_chunks;
@@ -52,6 +57,26 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
     }
     return;
   }
+  // the chunk's two pages (a position past the visible range reads the last visible one; it is masked)
+  const std::uint32_t* pt = pages + static_cast<std::size_t>(sess) * max_pages;
+  const std::uint32_t last = limit - 1;
+  const std::uint32_t pg0 = pt[min(start, last) / kPage], pg1 = pt[min(start + kPage, last) / kPage];
+  auto row_of = [&](const float* pool, std::uint32_t j) {  // token start + j, clamped to the visible range
+    const std::uint32_t tok = min(start + j, last);
+    const std::uint32_t pg = (tok - start) < kPage ? pg0 : pg1;
+    return pool + ((static_cast<std::size_t>(pg) * Hkv + kvh) * kPage + tok % kPage) * kHd;
+  };
+  const std::uint32_t sub = t % 16, r = t / 16;
+  float4 kf[2][4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float4* kr = reinterpret_cast<const float4*>(row_of(kpool, r + 16 * h));
+#pragma unroll
+    for (int u = 0; u < 4; ++u) kf[h][u] = kr[16 * u + sub];
+  }
+  float vv[kChunk];
+#pragma unroll
+  for (int j = 0; j < kChunk; ++j) vv[j] = row_of(vpool, j)[t];
   // queries of this kv head: slot i = session * G + g (prefix) or g (suffix)
   for (std::uint32_t i = t; i < nq * (kHd / 4); i += blockDim.x) {
     const std::uint32_t qi = i / (kHd / 4), d4 = i % (kHd / 4);
@@ -60,87 +85,55 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
     reinterpret_cast<float4*>(&qs[qi][0])[d4] = v;
   }
   __syncthreads();
-  // scores: lane = token of the chunk, wave = a quarter of the queries
-  const std::uint32_t tok = start + lane;
-  const bool live = lane < static_cast<std::uint32_t>(kChunk) && tok < limit;
-  const std::uint32_t page = pages[static_cast<std::size_t>(sess) * max_pages + min(tok, limit - 1) / kPage];
-  const float* krow = kpool + ((static_cast<std::size_t>(page) * Hkv + kvh) * kPage + (tok % kPage)) * kHd;
   const float scale = 1.0f / sqrtf(static_cast<float>(kHd));
-  const std::uint32_t per_wave = (nq + 3) / 4;
-  constexpr int kQPerWave = kMaxQ / 4;
-  float sc[kQPerWave];
+  const bool live0 = start + r < limit, live1 = start + r + 16 < limit;
+  for (std::uint32_t i = 0; i < nq; ++i) {
+    const float4* qv = reinterpret_cast<const float4*>(&qs[i][0]);
+    float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
-  for (int i = 0; i < kQPerWave; ++i) sc[i] = 0.0f;
-  constexpr int kKU = 16;  // row pieces loaded ahead of their arithmetic
-  for (std::uint32_t d0 = 0; d0 < kHd / 4; d0 += kKU) {
-    float4 kv[kKU];
-#pragma unroll
-    for (int u = 0; u < kKU; ++u) kv[u] = reinterpret_cast<const float4*>(krow)[d0 + u];
-#pragma unroll
-    for (int u = 0; u < kKU; ++u)
-#pragma unroll
-      for (int i = 0; i < kQPerWave; ++i) {
-        const std::uint32_t qi = wave * per_wave + i;
-        if (i < static_cast<int>(per_wave) && qi < nq) {
-          const float4 qv = reinterpret_cast<const float4*>(&qs[qi][0])[d0 + u];
-          sc[i] += kv[u].x * qv.x + kv[u].y * qv.y + kv[u].z * qv.z + kv[u].w * qv.w;
-        }
-      }
-  }
-#pragma unroll
-  for (int i = 0; i < kQPerWave; ++i) {
-    const std::uint32_t qi = wave * per_wave + i;
-    if (i < static_cast<int>(per_wave) && qi < nq) {
-      const float s = live ? sc[i] * scale : -INFINITY;
-      const float m = halo::GroupMax(s);
-      const float p = live ? expf(s - m) : 0.0f;
-      const float l = halo::GroupSum(p);
-      if (lane < static_cast<std::uint32_t>(kChunk)) ps[qi][lane] = p;
-      if (lane == 0) {
-        const std::uint32_t slot = is_prefix ? qi : sess * G + qi;
-        m_out[slot] = m;
-        l_out[slot] = l;
-      }
+    for (int u = 0; u < 4; ++u) {
+      const float4 b = qv[16 * u + sub];
+      s0 += kf[0][u].x * b.x + kf[0][u].y * b.y + kf[0][u].z * b.z + kf[0][u].w * b.w;
+      s1 += kf[1][u].x * b.x + kf[1][u].y * b.y + kf[1][u].z * b.z + kf[1][u].w * b.w;
+    }
+    s0 = halo::GroupSum<16>(s0);
+    s1 = halo::GroupSum<16>(s1);
+    if (sub == 0) {
+      sc[i][r] = live0 ? s0 * scale : -INFINITY;
+      sc[i][r + 16] = live1 ? s1 * scale : -INFINITY;
     }
   }
   __syncthreads();
-  // weighted V: thread = one of the 256 dims, all queries; the chunk's page ids are read once
-  float acc[kMaxQ];
-#pragma unroll
-  for (int i = 0; i < kMaxQ; ++i) acc[i] = 0.0f;
-  const std::uint32_t ntok = min(static_cast<std::uint32_t>(kChunk), limit - start);
-  std::uint32_t pgs[kChunk / kPage];
-#pragma unroll
-  for (int i = 0; i < kChunk / kPage; ++i)
-    pgs[i] = pages[static_cast<std::size_t>(sess) * max_pages + min(start / kPage + i, (limit - 1) / kPage)];
-  constexpr int kU = 8;
-  for (std::uint32_t j0 = 0; j0 < ntok; j0 += kU) {
-    float vv[kU];
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const std::uint32_t j = min(j0 + u, ntok - 1);
-      const std::uint32_t pg = pgs[j / kPage];
-      vv[u] = vpool[((static_cast<std::size_t>(pg) * Hkv + kvh) * kPage + ((start + j) % kPage)) * kHd + t];
-    }
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      if (j0 + u >= ntok) break;
-#pragma unroll
-      for (int i = 0; i < kMaxQ; ++i)
-        if (i < static_cast<int>(nq)) acc[i] += ps[i][j0 + u] * vv[u];
+  // softmax over the chunk per query: wave w takes queries w, w + 4, ...; lanes 0..31 are the tokens
+  for (std::uint32_t i = wave; i < nq; i += 4) {
+    const float s = lane < kChunk ? sc[i][lane] : -INFINITY;
+    const float m = halo::GroupMax(s);
+    const float p = s == -INFINITY ? 0.0f : expf(s - m);
+    const float l = halo::GroupSum(p);
+    if (lane < kChunk) sc[i][lane] = p;
+    if (lane == 0) {
+      const std::uint32_t slot = is_prefix ? i : sess * G + i;
+      m_out[slot] = m;
+      l_out[slot] = l;
     }
   }
+  __syncthreads();
 #pragma unroll
-  for (int i = 0; i < kMaxQ; ++i)
-    if (i < static_cast<int>(nq)) {
-      const std::uint32_t slot = is_prefix ? i : sess * G + i;
-      a_out[static_cast<std::size_t>(slot) * kHd + t] = acc[i];
-    }
+  for (int i = 0; i < kMaxQ; ++i) {
+    if (i >= static_cast<int>(nq)) break;
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) acc += sc[i][j] * vv[j];
+    const std::uint32_t slot = is_prefix ? i : sess * G + i;
+    a_out[static_cast<std::size_t>(slot) * kHd + t] = acc;
+  }
 }
 
-// grid (S * Hq), block 256: merges the partials of session s, head h over its prefix and suffix chunks
-// (log-sum-exp), o = acc / l, then o *= sigmoid(gate) when gate is non-null. o, gate [S][Hq][256] (o may be null);
-// with oq non-null also the Q8 quantization of o (oq [S][Hq * 256], os [S][Hq * 8]). At most 1024 items.
+// grid (S * Hq * 4), block 256: block (s, h, quarter) merges the partials of session s, head h over its prefix and
+// suffix chunks (log-sum-exp) for dims [64 quarter, 64 quarter + 64): o = acc / l, then o *= sigmoid(gate) when gate
+// is non-null. o, gate [S][Hq][256] (o may be null); with oq non-null also the Q8 quantization of o (oq
+// [S][Hq * 256], os [S][Hq * 8]). At most 1024 items. Thread: float4 lane f = t % 16 of the slice, items
+// i = t / 16 (mod 16), eight loads in flight.
 extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_combine(
     const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ pacc,
     const float* __restrict__ gate, float* __restrict__ o, std::int8_t* __restrict__ oq, float* __restrict__ os,
@@ -148,7 +141,9 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_combine(
     std::uint32_t suffix_chunks) {
   __shared__ float wts[1024];
   __shared__ float red[4];
-  const std::uint32_t G = Hq / Hkv, s = blockIdx.x / Hq, h = blockIdx.x % Hq, kvh = h / G, g = h % G;
+  __shared__ float4 part[16][16];
+  const std::uint32_t quarter = blockIdx.x % 4, sh = blockIdx.x / 4;
+  const std::uint32_t G = Hq / Hkv, s = sh / Hq, h = sh % Hq, kvh = h / G, g = h % G;
   const std::uint32_t slot = s * G + g, slots = S * G, t = threadIdx.x;
   const std::uint32_t n = min(prefix_chunks + suffix_chunks, 1024u);
   auto item = [&](std::uint32_t i) -> std::size_t {
@@ -177,21 +172,36 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_combine(
   if (t % kWave == 0) red[t / kWave] = L;
   __syncthreads();
   L = (red[0] + red[1]) + (red[2] + red[3]);
-  float acc = 0.0f;
+  const std::uint32_t f = t % 16, ig = t / 16;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   constexpr int kU = 8;
-  for (std::uint32_t i0 = 0; i0 < n; i0 += kU) {
-    float a[kU];
+  for (std::uint32_t i0 = ig; i0 < n; i0 += 16 * kU) {
+    float4 a[kU];
+    float w[kU];
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-      const std::uint32_t i = min(i0 + u, n - 1);
-      a[u] = wts[i] == 0.0f ? 0.0f : pacc[(item(i) * slots + slot) * kHd + t];
+      const std::uint32_t i = i0 + 16 * u;
+      w[u] = i < n ? wts[i] : 0.0f;
+      a[u] = w[u] == 0.0f ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
+                          : reinterpret_cast<const float4*>(pacc + (item(i) * slots + slot) * kHd)[quarter * 16 + f];
     }
 #pragma unroll
-    for (int u = 0; u < kU; ++u)
-      if (i0 + u < n) acc += wts[i0 + u] * a[u];
+    for (int u = 0; u < kU; ++u) {
+      acc.x += w[u] * a[u].x;
+      acc.y += w[u] * a[u].y;
+      acc.z += w[u] * a[u].z;
+      acc.w += w[u] * a[u].w;
+    }
   }
-  float r = acc / L;
-  const std::size_t off = (static_cast<std::size_t>(s) * Hq + h) * kHd + t;
+  part[ig][f] = acc;
+  __syncthreads();
+  if (t >= kWave) return;
+  // wave 0: lane = dim of the slice
+  float sum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) sum += reinterpret_cast<const float*>(&part[k][0])[t];
+  float r = sum / L;
+  const std::size_t off = (static_cast<std::size_t>(s) * Hq + h) * kHd + quarter * 64 + t;
   if (gate != nullptr) r *= halo::Sigmoid(gate[off]);
   if (o != nullptr) o[off] = r;
   if (oq != nullptr) {

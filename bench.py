@@ -87,7 +87,15 @@ def run_gpu(args):
                         dev.array((mmax, 2048), np.float32))
         dev.sync()
 
-        def c1_pass(ws, m):
+        in_x = H.ProjInput(x=x.ptr, mode=H.PROJ_F)
+        in_a = H.ProjInput(x=a.ptr, mode=H.PROJ_F)
+
+        def c1_pass(ws, m, fused=True):
+            if fused and m <= 8:
+                # one launch per input row set: quantize prologue + (q|gate, kv), then quantize prologue + o
+                H.proj_q8(dev, ws[:2], [yqg, ykv], in_x, m)
+                H.proj_q8(dev, ws[2:], [yo], in_a, m)
+                return
             dev.op("quantize_q8", x.ptr, xq.ptr, xs.ptr, m, 2048)
             dev.op("matvec_q8a8", ctypes.byref(ws[0].desc), xq.ptr, xs.ptr, yqg.ptr, m, 4096)
             dev.op("matvec_q8a8", ctypes.byref(ws[1].desc), xq.ptr, xs.ptr, ykv.ptr, m, 512)
@@ -106,13 +114,24 @@ def run_gpu(args):
         got = yo.download()[0]
         assert np.all(np.abs(got - want) <= 1e-5 * mag + 1e-6), "bench spot check failed"
 
-        def graph_for(m):
+        def graph_for(m, fused=True):
             dev.begin_capture()
             for ws in sets:
-                c1_pass(ws, m)
+                c1_pass(ws, m, fused)
             return dev.end_capture()
 
         sweep = {}
+        g = graph_for(1, fused=False)  # the unfused sequence (2 quantize + 3 GEMV launches), for comparison
+        dev.launch_graph(g)
+        dev.sync()
+        nrep = max(1, -(-1000 // copies))
+        dev.timer_start()
+        for _ in range(nrep):
+            dev.launch_graph(g)
+        ms = dev.timer_stop()
+        sweep["1_unfused"] = {"us_per_pass": round(ms / (nrep * copies) * 1e3, 3),
+                              "GBps": round(c1_pass_bytes(1) / (ms / (nrep * copies) * 1e-3) / 1e9, 1)}
+        dev.free_graph(g)
         for m in (1, 2, 4, 8, 16):
             g = graph_for(m)
             reps = 1 if m > 1 else max(1, args.warmup // copies)

@@ -6,6 +6,7 @@
 // sessions per step with weights read once; ForkSession (flash_next_gpu.hpp:347-350) shares prefix pages.
 #include "halo_model.h"
 
+#include <initializer_list>
 #include <map>
 #include <memory>
 #include <utility>
@@ -26,8 +27,8 @@ struct Layer {
   bool attn = false;
   halo_buffer attn_norm{}, ffn_norm{};
   // Gated DeltaNet
-  Q8 qkv, z, out;
-  halo_buffer ab{}, conv_w{}, a{}, dt{}, norm_w{};
+  Q8 qkv, z, ab, out;  // ab: alpha | beta logits [2 Hv][H]
+  halo_buffer conv_w{}, a{}, dt{}, norm_w{};
   // attention
   Q8 qg, k, v, o;
   halo_buffer q_norm{}, k_norm{}, k_pool{}, v_pool{};
@@ -51,7 +52,7 @@ struct halo_model {
   // state
   halo_buffer gdn_state{}, conv_state{}, pages{}, nkv{}, tokens{}, prompt{}, prompt_len{}, history{}, produced{};
   // step scratch
-  halo_buffer res{}, xn{}, xq{}, xs{}, qkv{}, zo{}, abo{}, q{}, k{}, v{}, g{}, beta{}, o{}, oq{}, os{}, delta{};
+  halo_buffer res{}, res2{}, xn{}, xq{}, xs{}, qkv{}, zo{}, abo{}, q{}, k{}, v{}, g{}, beta{}, o{}, oq{}, os{}, delta{};
   halo_buffer qgo{}, ko{}, vo{}, aq{}, agate{}, ao{}, moe_ws{}, attn_ws{}, logits{}, argmax_part{};
   std::size_t moe_ws_bytes = 0, attn_ws_bytes = 0;
   std::vector<halo_buffer> owned;
@@ -142,25 +143,44 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
                           U32(H), U32(H)};
     if (Launch(eng, "halo_embed_q8", D3(S), D3(256), a, err, errlen) != 0) return -1;
   }
+  // Residual stream: `cur` holds it. A projection prologue that adds a delta reads `cur` and writes the sum to
+  // the other buffer (its blocks all read `cur` while block 0 writes), then the two swap.
+  halo_buffer* cur = &m->res;
+  halo_buffer* alt = &m->res2;
   bool have_delta = false;
   auto norm = [&](const halo_buffer& w, bool quant) {
-    const halo_arg a[] = {Ptr(m->res.device), Ptr(have_delta ? m->delta.device : nullptr), Ptr(w.device),
+    const halo_arg a[] = {Ptr(cur->device), Ptr(have_delta ? m->delta.device : nullptr), Ptr(w.device),
                           Ptr(m->xn.device), Ptr(quant ? m->xq.device : nullptr), Ptr(m->xs.device), U32(H), Val(eps)};
     have_delta = false;
-    return Launch(eng, "halo_add_rmsnorm_q8", D3(S), D3(1024), a, err, errlen);
+    return Launch(eng, "halo_add_rmsnorm_q8", D3(S), D3(256), a, err, errlen);
+  };
+  // attention-side input norm fused into the layer's first projections (one launch)
+  auto proj_norm = [&](const halo_buffer& w, std::initializer_list<const Q8*> mats,
+                       std::initializer_list<const halo_buffer*> outs) {
+    halo_q8_matrix ms[4];
+    float* ys[4];
+    std::uint32_t n = 0;
+    for (const Q8* q : mats) ms[n++] = q->m;
+    n = 0;
+    for (const halo_buffer* b : outs) ys[n++] = P<float>(*b);
+    halo_proj_input in{};
+    in.x = P<float>(*cur);
+    in.delta = have_delta ? P<float>(m->delta) : nullptr;
+    in.norm_w = P<float>(w);
+    in.res_out = have_delta ? P<float>(*alt) : nullptr;
+    in.eps = eps;
+    in.mode = HALO_PROJ_N;
+    if (halo_op_proj_q8(eng, ms, ys, n, &in, S, err, errlen) != 0) return -1;
+    if (have_delta) std::swap(cur, alt);
+    have_delta = false;
+    return 0;
   };
   auto gemv = [&](const Q8& w, const halo_buffer& xq, const halo_buffer& xs, const halo_buffer& y) {
     return halo_op_matvec_q8a8(eng, &w.m, P<int8_t>(xq), P<float>(xs), P<float>(y), S, w.m.rows, err, errlen);
   };
   for (auto& L : m->layers) {
-    if (norm(L.attn_norm, true) != 0) return -1;
     if (!L.attn) {
-      if (gemv(L.qkv, m->xq, m->xs, m->qkv) != 0 || gemv(L.z, m->xq, m->xs, m->zo) != 0) return -1;
-      {  // alpha | beta logits: fp32 rows (the router kernel computes W x for S tokens)
-        const halo_arg a[] = {Ptr(L.ab.device), Ptr(nullptr), Ptr(m->xn.device), Ptr(m->abo.device), Ptr(nullptr),
-                              Ptr(nullptr), Ptr(nullptr), U32(2 * Hv), U32(H), U32(S)};
-        if (Launch(eng, "halo_moe_router", D3(2 * Hv + 1), D3(256), a, err, errlen) != 0) return -1;
-      }
+      if (proj_norm(L.attn_norm, {&L.qkv, &L.z, &L.ab}, {&m->qkv, &m->zo, &m->abo}) != 0) return -1;
       float* conv = P<float>(m->conv_state) + static_cast<std::size_t>(L.gdn_index) * c.max_sessions *
                                                   (c.conv_kernel - 1) * C;
       {
@@ -182,9 +202,7 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
       if (gemv(L.out, m->oq, m->os, m->delta) != 0) return -1;
       (void)Dv;
     } else {
-      if (gemv(L.qg, m->xq, m->xs, m->qgo) != 0 || gemv(L.k, m->xq, m->xs, m->ko) != 0 ||
-          gemv(L.v, m->xq, m->xs, m->vo) != 0)
-        return -1;
+      if (proj_norm(L.attn_norm, {&L.qg, &L.k, &L.v}, {&m->qgo, &m->ko, &m->vo}) != 0) return -1;
       {
         const halo_arg a[] = {Ptr(m->qgo.device), Ptr(m->ko.device), Ptr(m->vo.device), Ptr(L.q_norm.device),
                               Ptr(L.k_norm.device), Ptr(m->q.device), Ptr(m->agate.device), Ptr(L.k_pool.device),
@@ -256,7 +274,7 @@ int halo_model_create(halo_engine* eng, const halo_model_config* cfg, uint64_t s
       if (SynthQ8(m.get(), &L.qkv, m->conv_ch, H, next(), err, errlen) != 0 ||
           SynthQ8(m.get(), &L.z, Dv, H, next(), err, errlen) != 0 ||
           SynthQ8(m.get(), &L.out, H, Dv, next(), err, errlen) != 0 ||
-          SynthF32(m.get(), &L.ab, 2 * Hv * H, next(), 0.02f, 0.0f, err, errlen) != 0 ||
+          SynthQ8(m.get(), &L.ab, 2 * Hv, H, next(), err, errlen) != 0 ||
           SynthF32(m.get(), &L.conv_w, static_cast<std::size_t>(m->conv_ch) * c.conv_kernel, next(), 0.3f, 0.0f, err,
                    errlen) != 0 ||
           SynthF32(m.get(), &L.a, Hv, next(), 0.1f, -1.0f, err, errlen) != 0 ||
@@ -321,6 +339,7 @@ int halo_model_create(halo_engine* eng, const halo_model_config* cfg, uint64_t s
       {&m->history, S * ctx * 4},
       {&m->produced, S * 4},
       {&m->res, static_cast<std::size_t>(S) * H * 4},
+      {&m->res2, static_cast<std::size_t>(S) * H * 4},
       {&m->xn, static_cast<std::size_t>(S) * H * 4},
       {&m->xq, static_cast<std::size_t>(S) * H},
       {&m->xs, static_cast<std::size_t>(S) * H / 8},

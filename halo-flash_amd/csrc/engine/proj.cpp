@@ -1,0 +1,61 @@
+// Grouped projections with a fused activation prologue (halo_proj_q8* kernels): one launch for up to four Q8_0
+// matrices that read the same activation rows. Replaces the reference's [RMSNorm] + quantize + per-matrix
+// FlashNextGpu::MatVec sequence (src/engine/flash_next_gpu.cpp:212-254).
+#include "engine.hpp"
+
+using namespace halo::engine;
+
+extern "C" int halo_op_proj_q8(halo_engine* eng, const halo_q8_matrix* mats, float* const* ys, uint32_t n_mats,
+                               const halo_proj_input* in, uint32_t tokens, char* err, size_t errlen) {
+  if (mats == nullptr || ys == nullptr || in == nullptr || n_mats == 0 || n_mats > 4)
+    return SetErr(err, errlen, "proj: 1..4 matrices with outputs and an input descriptor"), -1;
+  if (tokens == 0 || tokens > 8) return SetErr(err, errlen, "proj: tokens %u not in 1..8", tokens), -1;
+  const std::uint32_t cols = mats[0].cols;
+  if (cols == 0 || cols % 32 != 0 || cols > 4096) return SetErr(err, errlen, "proj: cols %u unsupported", cols), -1;
+  for (std::uint32_t i = 0; i < n_mats; ++i) {
+    const halo_q8_matrix& w = mats[i];
+    if (w.qs == nullptr || w.d == nullptr || ys[i] == nullptr || w.rows == 0 || w.cols != cols || w.qstride != cols)
+      return SetErr(err, errlen, "proj: matrix %u (%u x %u, qstride %u) does not match cols %u", i, w.rows, w.cols,
+                    w.qstride, cols),
+             -1;
+  }
+  const char* letter = nullptr;
+  switch (in->mode) {
+    case HALO_PROJ_Q:
+      if (in->xq == nullptr || in->xs == nullptr) return SetErr(err, errlen, "proj: mode Q needs xq / xs"), -1;
+      letter = "q";
+      break;
+    case HALO_PROJ_F:
+      if (in->x == nullptr) return SetErr(err, errlen, "proj: mode F needs x"), -1;
+      letter = "f";
+      break;
+    case HALO_PROJ_N:
+      if (in->x == nullptr || in->norm_w == nullptr) return SetErr(err, errlen, "proj: mode N needs x / norm_w"), -1;
+      if (in->res_out != nullptr && in->res_out == in->x)
+        return SetErr(err, errlen, "proj: res_out must not alias the residual it reads"), -1;
+      letter = "n";
+      break;
+    default:
+      return SetErr(err, errlen, "proj: mode %u unknown", in->mode), -1;
+  }
+  if ((in->xq_out == nullptr) != (in->xs_out == nullptr))
+    return SetErr(err, errlen, "proj: xq_out and xs_out go together"), -1;
+  const std::uint32_t lpr = cols >= 1024 ? 64 : (cols >= 512 ? 32 : 16);
+  const std::uint32_t nb = tokens == 1 ? 1 : tokens == 2 ? 2 : tokens <= 4 ? 4 : 8;
+  const std::uint32_t rows_per_block = 4 * (64 / lpr);
+  std::uint32_t off[5] = {0, 0, 0, 0, 0};
+  for (std::uint32_t i = 0; i < 4; ++i)
+    off[i + 1] = off[i] + (i < n_mats ? CeilDiv(mats[i].rows, rows_per_block) : 0);
+  auto mat = [&](std::uint32_t i) { return i < n_mats ? mats[i] : mats[0]; };
+  auto out = [&](std::uint32_t i) { return i < n_mats ? ys[i] : ys[0]; };
+  auto rows = [&](std::uint32_t i) { return i < n_mats ? mats[i].rows : 0u; };
+  char name[64];
+  std::snprintf(name, sizeof name, "halo_proj_q8%s_l%u_b%u", letter, lpr, nb);
+  const halo_arg a[] = {Ptr(in->x), Ptr(in->delta), Ptr(in->norm_w), Ptr(in->res_out), Ptr(in->xq), Ptr(in->xs),
+                        Ptr(in->xq_out), Ptr(in->xs_out),
+                        Ptr(mat(0).qs), Ptr(mat(0).d), Ptr(out(0)), Ptr(mat(1).qs), Ptr(mat(1).d), Ptr(out(1)),
+                        Ptr(mat(2).qs), Ptr(mat(2).d), Ptr(out(2)), Ptr(mat(3).qs), Ptr(mat(3).d), Ptr(out(3)),
+                        U32(rows(0)), U32(rows(1)), U32(rows(2)), U32(rows(3)), U32(off[1]), U32(off[2]), U32(off[3]),
+                        U32(tokens), U32(cols), Val(in->eps)};
+  return Launch(eng, name, D3(off[4]), D3(256), a, err, errlen);
+}

@@ -142,3 +142,109 @@ __device__ __forceinline__ float Normal(std::uint64_t key) {
 }
 
 }  // namespace halo
+
+// ---- canonical row prologue: residual add, RMS norm and Q8 quantization of one activation row -----------------
+// Every kernel that normalizes or quantizes a row in its prologue uses this decomposition, so all of them produce
+// the same bits: 256 threads, thread t holds the 8-value chunks c = t + 256 k (k < KC, c < n / 8) of the row;
+// the sum of squares runs over a thread's chunks in order, then GroupSum, then the four wave sums in order.
+// A 32-value Q8 block is the 4 chunks of 4 consecutive lanes (a DPP quad).
+namespace halo {
+
+template <int KC>
+struct Row8 {
+  float v[KC][8];
+};
+
+// v = x (+ delta) for the chunks of this thread; chunks past n are zero.
+template <int KC>
+__device__ __forceinline__ void LoadRow8(const float* __restrict__ x, const float* __restrict__ delta, std::uint32_t n,
+                                         Row8<KC>& r) {
+#pragma unroll
+  for (int k = 0; k < KC; ++k) {
+    const std::uint32_t c = threadIdx.x + 256u * k;
+    if (c < n / 8) {
+      const float4 a = reinterpret_cast<const float4*>(x)[2 * c], b = reinterpret_cast<const float4*>(x)[2 * c + 1];
+      r.v[k][0] = a.x, r.v[k][1] = a.y, r.v[k][2] = a.z, r.v[k][3] = a.w;
+      r.v[k][4] = b.x, r.v[k][5] = b.y, r.v[k][6] = b.z, r.v[k][7] = b.w;
+      if (delta != nullptr) {
+        const float4 e = reinterpret_cast<const float4*>(delta)[2 * c],
+                     f = reinterpret_cast<const float4*>(delta)[2 * c + 1];
+        r.v[k][0] += e.x, r.v[k][1] += e.y, r.v[k][2] += e.z, r.v[k][3] += e.w;
+        r.v[k][4] += f.x, r.v[k][5] += f.y, r.v[k][6] += f.z, r.v[k][7] += f.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r.v[k][e] = 0.0f;
+    }
+  }
+}
+
+template <int KC>
+__device__ __forceinline__ void StoreRow8(float* __restrict__ y, std::uint32_t n, const Row8<KC>& r) {
+#pragma unroll
+  for (int k = 0; k < KC; ++k) {
+    const std::uint32_t c = threadIdx.x + 256u * k;
+    if (c < n / 8) {
+      reinterpret_cast<float4*>(y)[2 * c] = make_float4(r.v[k][0], r.v[k][1], r.v[k][2], r.v[k][3]);
+      reinterpret_cast<float4*>(y)[2 * c + 1] = make_float4(r.v[k][4], r.v[k][5], r.v[k][6], r.v[k][7]);
+    }
+  }
+}
+
+// In place: v = v * (1 / sqrt(mean(v^2) + eps)) * w. Block of exactly 256 threads; red holds 4 floats.
+template <int KC>
+__device__ __forceinline__ void RmsNormRow8(Row8<KC>& r, const float* __restrict__ w, std::uint32_t n, float eps,
+                                            float* red) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int k = 0; k < KC; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += r.v[k][e] * r.v[k][e];
+  ss = GroupSum(ss);
+  __syncthreads();
+  if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  ss = ((red[0] + red[1]) + red[2]) + red[3];
+  const float scale = 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
+#pragma unroll
+  for (int k = 0; k < KC; ++k) {
+    const std::uint32_t c = threadIdx.x + 256u * k;
+    if (c < n / 8) {
+      const float4 a = reinterpret_cast<const float4*>(w)[2 * c], b = reinterpret_cast<const float4*>(w)[2 * c + 1];
+      const float wv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r.v[k][e] = r.v[k][e] * scale * wv[e];
+    }
+  }
+}
+
+// Q8 quantization of the row (amax / 127, round half to even): xq [n] int8, xs [n / 32].
+template <int KC>
+__device__ __forceinline__ void QuantRow8(const Row8<KC>& r, std::uint32_t n, std::int8_t* xq, float* xs) {
+#pragma unroll
+  for (int k = 0; k < KC; ++k) {
+    const std::uint32_t c = threadIdx.x + 256u * k;
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(r.v[k][e]));
+    amax = fmaxf(amax, Dpp<0xB1>(amax));
+    amax = fmaxf(amax, Dpp<0x4E>(amax));
+    if (c < n / 8) {
+      const float scale = amax / 127.0f;
+      std::uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int q = scale > 0.0f ? static_cast<int>(rintf(r.v[k][e] / scale)) : 0;
+        const std::uint32_t b = static_cast<std::uint32_t>(q) & 0xFFu;
+        if (e < 4)
+          lo |= b << (8 * e);
+        else
+          hi |= b << (8 * (e - 4));
+      }
+      reinterpret_cast<uint2*>(xq)[c] = make_uint2(lo, hi);
+      if (threadIdx.x % 4 == 0) xs[c / 4] = scale;
+    }
+  }
+}
+
+}  // namespace halo

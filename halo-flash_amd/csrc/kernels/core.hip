@@ -4,3 +4,4 @@
 #include "gdn.hip"
 #include "attn.hip"
 #include "model.hip"
+#include "proj.hip"

@@ -10,18 +10,6 @@
 using halo::kWave;
 
 namespace {
-// Sum over the block (blockDim.x a multiple of 64, <= 1024); red holds 16 floats.
-__device__ __forceinline__ float BlockSumM(float v, float* red) {
-  v = halo::GroupSum(v);
-  const std::uint32_t wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
-  __syncthreads();
-  if (threadIdx.x % kWave == 0) red[wave] = v;
-  __syncthreads();
-  float r = 0.0f;
-  for (std::uint32_t w = 0; w < waves; ++w) r += red[w];
-  return r;
-}
-
 // Quantizes 32 consecutive values held one per lane of a half wave (amax / 127, round half to even).
 __device__ __forceinline__ void Quant32(float v, std::int8_t* xq, float* xs, std::uint32_t blk) {
   const std::uint32_t lane = threadIdx.x % 32;
@@ -32,32 +20,21 @@ __device__ __forceinline__ void Quant32(float v, std::int8_t* xq, float* xs, std
 }
 }  // namespace
 
-// grid (S), block 1024 (H <= 8192, H % 32 == 0). res [S][H] += delta [S][H] (delta may be null), then
+// grid (S), block 256 (H <= 8192, H % 32 == 0). res [S][H] += delta [S][H] (delta may be null), then
 // xn = RMSNorm(res) * w (fp32, may be null) and its Q8 quantization xq [S][H], xs [S][H / 32] (may be null).
-extern "C" __global__ void __launch_bounds__(1024)
+// The row decomposition is the canonical one (halo::RmsNormRow8), shared with the projection prologues.
+extern "C" __global__ void __launch_bounds__(256)
     halo_add_rmsnorm_q8(float* __restrict__ res, const float* __restrict__ delta, const float* __restrict__ w,
                         float* __restrict__ xn, std::int8_t* __restrict__ xq, float* __restrict__ xs,
                         std::uint32_t H, float eps) {
-  __shared__ float red[16];
-  __shared__ float vals[8192];
+  __shared__ float red[4];
   const std::size_t s = blockIdx.x;
-  float ss = 0.0f;
-  for (std::uint32_t i = threadIdx.x; i < H; i += blockDim.x) {
-    float v = res[s * H + i];
-    if (delta != nullptr) {
-      v += delta[s * H + i];
-      res[s * H + i] = v;
-    }
-    vals[i] = v;
-    ss += v * v;
-  }
-  ss = BlockSumM(ss, red);
-  const float scale = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
-  for (std::uint32_t i = threadIdx.x; i < H; i += blockDim.x) {
-    const float y = vals[i] * scale * w[i];
-    if (xn != nullptr) xn[s * H + i] = y;
-    if (xq != nullptr) Quant32(y, xq + s * H, xs + s * (H / 32), i / 32);
-  }
+  halo::Row8<4> r;
+  halo::LoadRow8(res + s * H, delta != nullptr ? delta + s * H : nullptr, H, r);
+  if (delta != nullptr) halo::StoreRow8(res + s * H, H, r);
+  halo::RmsNormRow8(r, w, H, eps, red);
+  if (xn != nullptr) halo::StoreRow8(xn + s * H, H, r);
+  if (xq != nullptr) halo::QuantRow8(r, H, xq + s * H, xs + s * (H / 32));
 }
 
 // grid (S, C / 256), block 256: the DeltaNet prologue for one token per session, one channel per thread.

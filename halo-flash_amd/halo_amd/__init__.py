@@ -53,6 +53,22 @@ class Q8Matrix(C.Structure):
     ]
 
 
+class ProjInput(C.Structure):
+    """halo_proj_input: the activation source of a grouped projection (modes PROJ_Q / PROJ_F / PROJ_N)."""
+    _fields_ = [(n, C.c_void_p) for n in ("x", "delta", "norm_w", "res_out", "xq", "xs", "xq_out", "xs_out")] + [
+        ("eps", C.c_float), ("mode", C.c_uint32)]
+
+
+PROJ_Q, PROJ_F, PROJ_N = 0, 1, 2
+
+
+def proj_q8(dev, weights, outs, inp: ProjInput, tokens: int):
+    """One grouped projection launch: weights is a list of Q8Weights, outs their [tokens][rows] outputs."""
+    mats = (Q8Matrix * len(weights))(*[w.desc for w in weights])
+    ys = (C.c_void_p * len(outs))(*[o.ptr for o in outs])
+    dev.op("proj_q8", mats, ys, len(weights), C.byref(inp), tokens)
+
+
 class MoeWeights(C.Structure):
     _fields_ = [
         ("router", C.c_void_p),
@@ -135,6 +151,8 @@ _SIGS = {
     "halo_engine_launch": (C.c_int, [_VP, C.c_char_p, Dim3, Dim3, C.POINTER(Arg), _SZ], True),
     "halo_op_repack_q8_0": (C.c_int, [_VP, _VP, _VP, _VP, _U32, _U32, _U32], True),
     "halo_op_quantize_q8": (C.c_int, [_VP, _VP, _VP, _VP, _U32, _U32], True),
+    "halo_op_proj_q8": (C.c_int, [_VP, C.POINTER(Q8Matrix), C.POINTER(C.c_void_p), _U32, C.POINTER(ProjInput), _U32],
+                        True),
     "halo_op_matvec_q8a8": (C.c_int, [_VP, C.POINTER(Q8Matrix), _VP, _VP, _VP, _U32, _U32], True),
     "halo_op_matvec_q8a8_tiled": (
         C.c_int, [_VP, C.POINTER(Q8Matrix), _VP, _VP, _VP, _U32, _U32, _U32, _U32, _U32], True),

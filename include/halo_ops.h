@@ -54,6 +54,34 @@ int halo_op_quantize_q8(halo_engine* eng, const float* x, int8_t* xq, float* xs,
  * tiles of 16 rows x 16 tokens (x 64 tokens from M = 64), one v_mfma_i32_16x16x32_i8 per Q8_0 block. */
 int halo_op_matvec_q8a8(halo_engine* eng, const halo_q8_matrix* w, const int8_t* xq, const float* xs, float* y,
                         uint32_t m, uint32_t ystride, char* err, size_t errlen);
+/* Grouped projections with the activation prologue fused in: up to 4 Q8_0 matrices sharing the input row(s) of
+ * `tokens` (<= 8) tokens, in ONE launch. Replaces the reference's sequence [RMSNorm] -> halo_quantize_q8_rows ->
+ * one MatVec per matrix (src/engine/flash_next_gpu.cpp:212-254, src/kernels/core.hip:3089-3101) for the
+ * projections that read the same activations (q|k|v + z + alpha|beta of a DeltaNet layer, q|gate + k + v of an
+ * attention layer). ys[i] [tokens][mats[i].rows]. All matrices have cols = in cols (<= 4096, % 32 == 0) and
+ * qstride == cols. Modes:
+ *   HALO_PROJ_Q: in->xq / in->xs already quantized;
+ *   HALO_PROJ_F: in->x fp32 [tokens][cols] quantized in the prologue;
+ *   HALO_PROJ_N: x = RMSNorm(in->x + in->delta) * in->norm_w (delta may be null), then quantized; when delta is
+ *                non-null and res_out non-null, x + delta is written to res_out (which must not alias in->x).
+ * xq_out / xs_out (may be null) receive the quantized activations (bit-identical to halo_op_quantize_q8 of the
+ * same fp32 row). */
+enum { HALO_PROJ_Q = 0, HALO_PROJ_F = 1, HALO_PROJ_N = 2 };
+typedef struct halo_proj_input {
+  const float* x;
+  const float* delta;
+  const float* norm_w;
+  float* res_out;
+  const int8_t* xq;
+  const float* xs;
+  int8_t* xq_out;
+  float* xs_out;
+  float eps;
+  uint32_t mode;
+} halo_proj_input;
+int halo_op_proj_q8(halo_engine* eng, const halo_q8_matrix* mats, float* const* ys, uint32_t n_mats,
+                    const halo_proj_input* in, uint32_t tokens, char* err, size_t errlen);
+
 /* The same with an explicit GEMV tiling (lanes per row 16/32/64, rows per lane group 1/2/4, waves per block) for
  * tuning sweeps; m <= 8. */
 int halo_op_matvec_q8a8_tiled(halo_engine* eng, const halo_q8_matrix* w, const int8_t* xq, const float* xs,

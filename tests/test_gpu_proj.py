@@ -1,0 +1,119 @@
+"""GPU parity for the grouped projections with a fused activation prologue (halo_op_proj_q8).
+
+Bars: the prologue's quantized activations are bit-exact against the oracle's quantizer (mode F) and against the
+standalone residual-add + RMSNorm + quantize kernel (mode N, same canonical row decomposition); the residual written
+back is bit-exact; every output row is within 1e-5 * sum|term| + 1e-6 of the oracle's GEMV on those activations
+(the reference's tolerance, tests/gpu/quant_gpu_test.cpp:115-122) and the argmax is equal; mode Q on the same
+activations gives the same bits as mode F.
+"""
+import numpy as np
+import pytest
+
+import halo_amd as H
+import oracle_py as O
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def _check_y(y, want, mag):
+    err = np.abs(y.astype(np.float64) - want.astype(np.float64))
+    bound = TOL * mag + 1e-6
+    assert not np.any(err > bound), f"{np.count_nonzero(err > bound)} outputs off"
+    assert np.argmax(y, -1).tolist() == np.argmax(want, -1).tolist()
+
+
+def _mats(dev, rng, shapes):
+    host, dev_w = [], []
+    for rows, cols in shapes:
+        qs, d = O.synth_q8(rng, rows, cols)
+        host.append((qs, d))
+        dev_w.append(H.Q8Weights.from_host(dev, qs, d))
+    return host, dev_w
+
+
+@pytest.mark.parametrize("tokens", [1, 2, 3, 4, 8])
+@pytest.mark.parametrize("shapes", [
+    [(4096, 2048), (512, 2048)],                    # C1 q|gate and kv
+    [(2048, 4096)],                                  # C1 o
+    [(8192, 2048), (4096, 2048), (64, 2048)],        # DeltaNet q|k|v, z, alpha|beta
+    [(300, 512), (17, 512), (1, 512), (64, 512)],    # ragged rows, four matrices, LPR 32
+    [(40, 256)],                                     # LPR 16
+])
+def test_proj_mode_f_and_q(dev, tokens, shapes):
+    rng = np.random.default_rng(tokens * 7 + len(shapes))
+    cols = shapes[0][1]
+    host, ws = _mats(dev, rng, shapes)
+    x = rng.normal(0, 1, (tokens, cols)).astype(np.float32)
+    x[0, :32] = 0.0
+    gx = dev.to_device(x)
+    xq_o, xs_o = dev.array((tokens, cols), np.int8), dev.array((tokens, cols // 32), np.float32)
+    outs = [dev.array((tokens, r), np.float32) for r, _ in shapes]
+    inp = H.ProjInput(x=gx.ptr, xq_out=xq_o.ptr, xs_out=xs_o.ptr, mode=H.PROJ_F)
+    H.proj_q8(dev, ws, outs, inp, tokens)
+    xq, xs = O.quantize(x)
+    assert np.array_equal(xq_o.download(), xq)
+    assert np.array_equal(xs_o.download().view(np.uint32), xs.view(np.uint32))
+    got_f = [o.download() for o in outs]
+    for (qs, d), y in zip(host, got_f):
+        want, mag = O.gemv_q8a8(qs, d, xq, xs)
+        _check_y(y, want, mag)
+    # mode Q on the same activations: the same bits
+    outs_q = [dev.array((tokens, r), np.float32) for r, _ in shapes]
+    inq = H.ProjInput(xq=xq_o.ptr, xs=xs_o.ptr, mode=H.PROJ_Q)
+    H.proj_q8(dev, ws, outs_q, inq, tokens)
+    for a, o in zip(got_f, outs_q):
+        assert np.array_equal(a.view(np.uint32), o.download().view(np.uint32))
+
+
+@pytest.mark.parametrize("tokens,cols,with_delta", [(1, 2048, True), (4, 2048, True), (3, 4096, False),
+                                                    (8, 2048, True)])
+def test_proj_mode_n_matches_norm_kernel(dev, tokens, cols, with_delta):
+    rng = np.random.default_rng(tokens + cols)
+    shapes = [(1024, cols), (512, cols)]
+    host, ws = _mats(dev, rng, shapes)
+    res = rng.normal(0, 1, (tokens, cols)).astype(np.float32)
+    delta = rng.normal(0, 0.5, (tokens, cols)).astype(np.float32)
+    w = (1.0 + 0.1 * rng.normal(0, 1, cols)).astype(np.float32)
+    eps = 1e-6
+    gres, gdel, gw = dev.to_device(res), dev.to_device(delta), dev.to_device(w)
+    rout = dev.array((tokens, cols), np.float32)
+    xq_o, xs_o = dev.array((tokens, cols), np.int8), dev.array((tokens, cols // 32), np.float32)
+    outs = [dev.array((tokens, r), np.float32) for r, _ in shapes]
+    inp = H.ProjInput(x=gres.ptr, delta=gdel.ptr if with_delta else None, norm_w=gw.ptr, res_out=rout.ptr,
+                      xq_out=xq_o.ptr, xs_out=xs_o.ptr, eps=eps, mode=H.PROJ_N)
+    H.proj_q8(dev, ws, outs, inp, tokens)
+    # the standalone norm kernel on a copy of the residual
+    r2 = dev.to_device(res)
+    xn2 = dev.array((tokens, cols), np.float32)
+    xq2, xs2 = dev.array((tokens, cols), np.int8), dev.array((tokens, cols // 32), np.float32)
+    dev.launch("halo_add_rmsnorm_q8", (tokens,), (256,),
+               [r2, gdel if with_delta else None, gw, xn2, xq2, xs2, ("u32", cols), ("f32", eps)])
+    summed = res + delta if with_delta else res
+    if with_delta:
+        assert np.array_equal(rout.download().view(np.uint32), summed.view(np.uint32))
+        assert np.array_equal(r2.download().view(np.uint32), summed.view(np.uint32))
+    assert np.array_equal(xq_o.download(), xq2.download())
+    assert np.array_equal(xs_o.download().view(np.uint32), xs2.download().view(np.uint32))
+    # the norm itself against the oracle's RMSNorm (fp32 sums in another order: 1e-5 relative)
+    xn_want = summed.copy()
+    for t in range(tokens):
+        O.oracle().or_rmsnorm(xn_want[t], cols, w.ctypes.data, eps)
+    assert np.allclose(xn2.download(), xn_want, rtol=1e-5, atol=1e-6)
+    xq, xs = xq2.download(), xs2.download()
+    for (qs, d), y in zip(host, outs):
+        want, mag = O.gemv_q8a8(qs, d, xq, xs)
+        _check_y(y.download(), want, mag)
+
+
+def test_proj_rejects_bad_shapes(dev):
+    rng = np.random.default_rng(5)
+    _, ws = _mats(dev, rng, [(64, 2048), (64, 1024)])
+    x = dev.array((1, 2048), np.float32)
+    outs = [dev.array((1, 64), np.float32) for _ in range(2)]
+    with pytest.raises(H.HaloError):
+        H.proj_q8(dev, ws, outs, H.ProjInput(x=x.ptr, mode=H.PROJ_F), 1)          # cols differ
+    with pytest.raises(H.HaloError):
+        H.proj_q8(dev, ws[:1], outs[:1], H.ProjInput(x=x.ptr, mode=H.PROJ_F), 9)  # too many tokens
+    with pytest.raises(H.HaloError):
+        H.proj_q8(dev, ws[:1], outs[:1], H.ProjInput(x=x.ptr, norm_w=x.ptr, res_out=x.ptr, mode=H.PROJ_N), 1)

@@ -69,6 +69,8 @@ def run_gpu(args):
             return run_pmc(args, dev, H, res)
         if args.mode == "attn":
             return run_attn(args, dev, H, res)
+        if args.mode == "proj":
+            return run_proj(args, dev, H, res)
         # ---------------- C1 pass at M=1 (the bench value) and the M sweep ----------------
         per_copy = sum(q8_bytes(r, c) for r, c in C1_SHAPES)
         copies = max(2, -(-MIN_ROTATION_BYTES // per_copy))
@@ -244,6 +246,109 @@ def run_moe(args, dev, H, res):
         log(f"[bench] moe T={T}: {out[f'T{T}']}")
     res["moe"] = out
     res["roofline"] = None
+    return res
+
+
+def run_proj(args, dev, H, res):
+    """Grouped projections alone, over a grid-size sweep: the C1 pair (q|gate 4096 + kv 512 rows, cols 2048,
+    fp32 input quantized in the prologue) and the DeltaNet input group (q|k|v 8192 + z 4096 + alpha|beta 64 rows,
+    RMSNorm(res + delta) prologue), at 1 and 4 tokens; weights rotated over > 600 MB."""
+    groups = {"c1_pair": ([(4096, 2048), (512, 2048)], H.PROJ_F), "gdn_in": ([(8192, 2048), (4096, 2048), (64, 2048)],
+                                                                             H.PROJ_N)}
+    out = {}
+    for gname, (shapes, mode) in groups.items():
+        per = sum(q8_bytes(r, c) for r, c in shapes)
+        ncopy = max(2, -(-MIN_ROTATION_BYTES // per))
+        sets = [[H.Q8Weights(dev, r, c).synth(dev, seed=500 * i + j) for j, (r, c) in enumerate(shapes)]
+                for i in range(ncopy)]
+        x = dev.array((8, 2048), np.float32)
+        dl = dev.array((8, 2048), np.float32)
+        w = dev.array(2048, np.float32)
+        r2 = dev.array((8, 2048), np.float32)
+        for a, sd in ((x, 1), (dl, 2), (w, 3)):
+            dev.op("synth_f32", a.ptr, a.nbytes // 4, sd, 1.0)
+        ys = [dev.array((8, r), np.float32) for r, _ in shapes]
+        inp = H.ProjInput(x=x.ptr, delta=dl.ptr if mode == H.PROJ_N else None, norm_w=w.ptr, res_out=r2.ptr,
+                          eps=1e-6, mode=mode)
+        xq = dev.array((8, 2048), np.int8)
+        xs = dev.array((8, 64), np.float32)
+        dev.op("quantize_q8", x.ptr, xq.ptr, xs.ptr, 8, 2048)
+        inq = H.ProjInput(xq=xq.ptr, xs=xs.ptr, mode=H.PROJ_Q)
+        for T in (1, 4):
+            for pname, pin in (("pro", inp), ("q", inq)):
+                for lpr in (64, 32):
+                    for blocks in (1, 2, 4):  # tasks per wave
+                        dev.begin_capture()
+                        for ws in sets:
+                            H.proj_q8(dev, ws, ys, pin, T, blocks, lpr)
+                        g = dev.end_capture()
+                        dev.launch_graph(g)
+                        dev.sync()
+                        nrep = max(1, -(-2000 // ncopy))
+                        dev.timer_start()
+                        for _ in range(nrep):
+                            dev.launch_graph(g)
+                        us = dev.timer_stop() * 1e3 / (nrep * ncopy)
+                        dev.free_graph(g)
+                        key = f"{gname}_T{T}_{pname}_l{lpr}_t{blocks}"
+                        out[key] = {"us": round(us, 2), "GBps": round(per / (us * 1e-6) / 1e9, 1)}
+                        log(f"[bench] proj {key}: {us:.2f} us, {per / (us * 1e-6) / 1e9:.0f} GB/s")
+        # the same bytes as one stacked matrix through the plain int8 GEMV (activations quantized beforehand)
+        rows_all = sum(r for r, _ in shapes)
+        big = [H.Q8Weights(dev, rows_all, 2048).synth(dev, seed=900 + i) for i in range(ncopy)]
+        yb = dev.array((8, rows_all), np.float32)
+        for T in (1, 4):
+            dev.begin_capture()
+            for wb in big:
+                dev.op("matvec_q8a8", ctypes.byref(wb.desc), xq.ptr, xs.ptr, yb.ptr, T, rows_all)
+            g = dev.end_capture()
+            dev.launch_graph(g)
+            dev.sync()
+            nrep = max(1, -(-2000 // ncopy))
+            dev.timer_start()
+            for _ in range(nrep):
+                dev.launch_graph(g)
+            us = dev.timer_stop() * 1e3 / (nrep * ncopy)
+            dev.free_graph(g)
+            key = f"{gname}_T{T}_plain_gemv_stacked"
+            out[key] = {"us": round(us, 2), "GBps": round(per / (us * 1e-6) / 1e9, 1)}
+            log(f"[bench] proj {key}: {us:.2f} us, {per / (us * 1e-6) / 1e9:.0f} GB/s")
+        del big
+        # the same group with every copy carved out of one pooled allocation (qs and scales contiguous)
+        pool_bytes = ncopy * sum(r * c + r * (c // 32) * 2 for r, c in shapes) + 4096 * ncopy * len(shapes) * 2
+        pool = dev.array(pool_bytes, np.uint8)
+        psets, off = [], 0
+        for i in range(ncopy):
+            ws_ = []
+            for j, (r, c) in enumerate(shapes):
+                qs_p = pool.ptr + off
+                off += (r * c + 4095) // 4096 * 4096
+                d_p = pool.ptr + off
+                off += (r * (c // 32) * 2 + 4095) // 4096 * 4096
+                dev.op("synth_q8", qs_p, d_p, r, c, c, 700 + 10 * i + j, 0.02)
+                ws_.append(H.Q8Matrix(qs_p, d_p, r, c, c, 0))
+            psets.append(ws_)
+        for T in (1, 4):
+            dev.begin_capture()
+            for ws_ in psets:
+                mats = (H.Q8Matrix * len(ws_))(*ws_)
+                ysp = (ctypes.c_void_p * len(ys))(*[o.ptr for o in ys])
+                dev.op("proj_q8_grid", mats, ysp, len(ws_), ctypes.byref(inq), T, 1, 32)
+            g = dev.end_capture()
+            dev.launch_graph(g)
+            dev.sync()
+            nrep = max(1, -(-2000 // ncopy))
+            dev.timer_start()
+            for _ in range(nrep):
+                dev.launch_graph(g)
+            us = dev.timer_stop() * 1e3 / (nrep * ncopy)
+            dev.free_graph(g)
+            key = f"{gname}_T{T}_q_l32_g1024_pooled"
+            out[key] = {"us": round(us, 2), "GBps": round(per / (us * 1e-6) / 1e9, 1)}
+            log(f"[bench] proj {key}: {us:.2f} us, {per / (us * 1e-6) / 1e9:.0f} GB/s")
+        del pool
+        del sets
+    res["proj"] = out
     return res
 
 
@@ -652,7 +757,7 @@ def main():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--quick", action="store_true", help="only the C1 value and the C0 roofline")
     p.add_argument("--eager", action="store_true", help="launch without graphs (for profiling kernel durations)")
-    p.add_argument("--mode", choices=["all", "c0", "membw", "moe", "gdn", "c4", "pmc", "attn"], default="all",
+    p.add_argument("--mode", choices=["all", "c0", "membw", "moe", "gdn", "c4", "pmc", "attn", "proj"], default="all",
                    help="c0: only the C0 GEMV loop (for profiling one kernel shape)")
     args = p.parse_args()
     if args.gpus != 1:
@@ -660,8 +765,8 @@ def main():
               "(the path is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
         sys.exit(2)
     res = run_gpu(args)
-    if args.mode in ("c0", "membw", "moe", "gdn", "c4", "pmc", "attn"):
-        print(json.dumps({k: res.get(k) for k in ("roofline", "c0_tilings", "membw", "moe", "gdn", "c4", "attn")}),
+    if args.mode in ("c0", "membw", "moe", "gdn", "c4", "pmc", "attn", "proj"):
+        print(json.dumps({k: res.get(k) for k in ("roofline", "c0_tilings", "membw", "moe", "gdn", "c4", "attn", "proj")}),
               flush=True)
         return
     line = {

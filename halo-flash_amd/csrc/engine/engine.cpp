@@ -66,11 +66,24 @@ int halo_engine_create(halo_device* dev, halo_engine** out, char* err, size_t er
     delete eng;
     return SetErr(err, errlen, "the code object lists no kernels"), -1;
   }
+  if (halo_alloc(dev, kSyncSlots * sizeof(std::uint32_t), &eng->sync, err, errlen) != 0 ||
+      halo_fill(dev, &eng->sync, 0, err, errlen) != 0 || halo_synchronize(dev, err, errlen) != 0) {
+    if (eng->sync.device != nullptr) halo_free(dev, &eng->sync);
+    delete eng;
+    return -1;
+  }
   *out = eng;
   return 0;
 }
 
-void halo_engine_destroy(halo_engine* eng) { delete eng; }
+void halo_engine_destroy(halo_engine* eng) {
+  if (eng == nullptr) return;
+  if (eng->sync.device != nullptr) {
+    (void)halo_synchronize(eng->dev, nullptr, 0);
+    halo_free(eng->dev, &eng->sync);
+  }
+  delete eng;
+}
 
 halo_device* halo_engine_device(halo_engine* eng) { return eng ? eng->dev : nullptr; }
 
@@ -145,8 +158,17 @@ int halo_op_matvec_q8a8(halo_engine* eng, const halo_q8_matrix* w, const int8_t*
     return Launch(eng, wide ? "halo_gemm_q8a8_mfma_t4" : "halo_gemm_q8a8_mfma_t1",
                   D3(CeilDiv(w->rows, 16), CeilDiv(m, wide ? 64 : 16)), D3(256), a, err, errlen);
   }
-  // Tiling: a row is covered by as many lanes as its 16-byte pieces allow (up to a wave); more activation columns
-  // reuse each weight load over more rows per lane group.
+  // Up to 8 tokens with a dense output: the grouped projection kernel in its quantized-input mode (one task of
+  // rows per wave, activations staged in LDS once per block).
+  if (m <= 8 && (m == 1 || ystride == w->rows) && w->qstride == w->cols && w->cols <= 2048) {
+    halo_proj_input in{};
+    in.xq = xq;
+    in.xs = xs;
+    in.mode = HALO_PROJ_Q;
+    return halo_op_proj_q8(eng, w, &y, 1, &in, m, err, errlen);
+  }
+  // Otherwise the per-group GEMV: a row is covered by as many lanes as its 16-byte pieces allow (up to a wave);
+  // more activation columns reuse each weight load over more rows per lane group.
   const std::uint32_t lpr = w->cols >= 1024 ? 64 : (w->cols >= 512 ? 32 : 16);
   std::uint32_t done = 0;
   while (done < m) {

@@ -15,6 +15,9 @@
 struct halo_engine {
   halo_device* dev = nullptr;
   std::unordered_map<std::string, halo_kernel_id> ids;
+  // Arrival counters for kernels whose last block finishes the work of the others (zeroed at create; every such
+  // kernel returns its counters to zero). Kernels on the device's one stream never overlap, so slots are reused.
+  halo_buffer sync{};
 };
 
 namespace halo::engine {
@@ -47,6 +50,15 @@ inline halo_arg Val(T v) {
 inline halo_arg U32(std::uint32_t v) { return Val(v); }
 
 inline halo_dim3 D3(std::uint32_t x, std::uint32_t y = 1, std::uint32_t z = 1) { return halo_dim3{x, y, z}; }
+
+// Counter slots of halo_engine::sync.
+constexpr std::uint32_t kSyncSlots = 1024;
+constexpr std::uint32_t kSyncMoeRouter = 0;   // one
+constexpr std::uint32_t kSyncProjTail = 1;    // one
+constexpr std::uint32_t kSyncGdnHeads = 64;   // sessions * value heads (<= 960)
+inline std::uint32_t* SyncCounters(halo_engine* eng, std::uint32_t slot) {
+  return static_cast<std::uint32_t*>(eng->sync.device) + slot;
+}
 
 inline std::uint32_t CeilDiv(std::uint64_t a, std::uint64_t b) { return static_cast<std::uint32_t>((a + b - 1) / b); }
 

@@ -164,6 +164,14 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
     n = 0;
     for (const halo_buffer* b : outs) ys[n++] = P<float>(*b);
     halo_proj_input in{};
+    if (S > 1) {
+      // several sessions: the norm's per-token prologue would run in every block; one norm launch is cheaper
+      if (norm(w, true) != 0) return -1;
+      in.xq = P<int8_t>(m->xq);
+      in.xs = P<float>(m->xs);
+      in.mode = HALO_PROJ_Q;
+      return halo_op_proj_q8(eng, ms, ys, n, &in, S, err, errlen);
+    }
     in.x = P<float>(*cur);
     in.delta = have_delta ? P<float>(m->delta) : nullptr;
     in.norm_w = P<float>(w);
@@ -197,7 +205,7 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
       {
         const halo_arg a[] = {Ptr(m->o.device), Ptr(m->zo.device), Ptr(L.norm_w.device), Ptr(m->oq.device),
                               Ptr(m->os.device), U32(Hv), U32(d), Val(eps)};
-        if (Launch(eng, "halo_gated_rmsnorm_q8", D3(S, CeilDiv(Hv, 4)), D3(256), a, err, errlen) != 0) return -1;
+        if (Launch(eng, "halo_gated_rmsnorm_q8", D3(S), D3(256), a, err, errlen) != 0) return -1;
       }
       if (gemv(L.out, m->oq, m->os, m->delta) != 0) return -1;
       (void)Dv;

@@ -1,12 +1,15 @@
 // Grouped projections with a fused activation prologue (halo_proj_q8* kernels): one launch for up to four Q8_0
 // matrices that read the same activation rows. Replaces the reference's [RMSNorm] + quantize + per-matrix
 // FlashNextGpu::MatVec sequence (src/engine/flash_next_gpu.cpp:212-254).
+#include <algorithm>
+
 #include "engine.hpp"
 
 using namespace halo::engine;
 
-extern "C" int halo_op_proj_q8(halo_engine* eng, const halo_q8_matrix* mats, float* const* ys, uint32_t n_mats,
-                               const halo_proj_input* in, uint32_t tokens, char* err, size_t errlen) {
+extern "C" int halo_op_proj_q8_grid(halo_engine* eng, const halo_q8_matrix* mats, float* const* ys,
+                                    uint32_t n_mats, const halo_proj_input* in, uint32_t tokens, uint32_t grid_blocks,
+                                    uint32_t lanes_per_row, char* err, size_t errlen) {
   if (mats == nullptr || ys == nullptr || in == nullptr || n_mats == 0 || n_mats > 4)
     return SetErr(err, errlen, "proj: 1..4 matrices with outputs and an input descriptor"), -1;
   if (tokens == 0 || tokens > 8) return SetErr(err, errlen, "proj: tokens %u not in 1..8", tokens), -1;
@@ -35,27 +38,50 @@ extern "C" int halo_op_proj_q8(halo_engine* eng, const halo_q8_matrix* mats, flo
         return SetErr(err, errlen, "proj: res_out must not alias the residual it reads"), -1;
       letter = "n";
       break;
+    case HALO_PROJ_G:
+      if (in->x == nullptr || in->delta == nullptr || in->norm_w == nullptr || cols % 128 != 0)
+        return SetErr(err, errlen, "proj: mode G needs x / delta (gate) / norm_w and cols %% 128 == 0"), -1;
+      letter = "g";
+      break;
     default:
       return SetErr(err, errlen, "proj: mode %u unknown", in->mode), -1;
   }
   if ((in->xq_out == nullptr) != (in->xs_out == nullptr))
     return SetErr(err, errlen, "proj: xq_out and xs_out go together"), -1;
-  const std::uint32_t lpr = cols >= 1024 ? 64 : (cols >= 512 ? 32 : 16);
+  // Lanes per row: the fewest that cover a row in at most four 16-byte pieces per lane (measured: 32 lanes x 4
+  // pieces beats 64 x 2 on 2048 columns; more rows in flight per wave instruction).
+  std::uint32_t lpr = cols > 2048 ? 64 : (cols > 1024 ? 32 : 16);
+  if (lanes_per_row != 0) {
+    if (!(lanes_per_row == 16 || lanes_per_row == 32 || lanes_per_row == 64) || cols > 64 * lanes_per_row)
+      return SetErr(err, errlen, "proj: %u lanes per row cannot cover %u columns", lanes_per_row, cols), -1;
+    lpr = lanes_per_row;
+  }
   const std::uint32_t nb = tokens == 1 ? 1 : tokens == 2 ? 2 : tokens <= 4 ? 4 : 8;
-  const std::uint32_t rows_per_block = 4 * (64 / lpr);
+  const std::uint32_t rows_per_task = 64 / lpr;
   std::uint32_t off[5] = {0, 0, 0, 0, 0};
   for (std::uint32_t i = 0; i < 4; ++i)
-    off[i + 1] = off[i] + (i < n_mats ? CeilDiv(mats[i].rows, rows_per_block) : 0);
+    off[i + 1] = off[i] + (i < n_mats ? CeilDiv(mats[i].rows, rows_per_task) : 0);
+  // Tasks per wave: a prologue that normalizes (modes N and G, T rows of residual + delta + weights from L2) is
+  // amortized over more rows per block; a plain quantized copy (mode Q) or quantization (mode F) is cheap enough
+  // for one task per wave, which keeps the most waves (and loads) in flight.
+  std::uint32_t tpw = (in->mode == HALO_PROJ_N || in->mode == HALO_PROJ_G) ? 4 : 1;
+  if (grid_blocks == 1 || grid_blocks == 2 || grid_blocks == 4) tpw = grid_blocks;  // tuning override
+  const std::uint32_t blocks = CeilDiv(off[4], 4 * tpw);
   auto mat = [&](std::uint32_t i) { return i < n_mats ? mats[i] : mats[0]; };
   auto out = [&](std::uint32_t i) { return i < n_mats ? ys[i] : ys[0]; };
   auto rows = [&](std::uint32_t i) { return i < n_mats ? mats[i].rows : 0u; };
   char name[64];
-  std::snprintf(name, sizeof name, "halo_proj_q8%s_l%u_b%u", letter, lpr, nb);
+  std::snprintf(name, sizeof name, "halo_proj_q8%s_l%u_b%u_t%u", letter, lpr, nb, tpw);
   const halo_arg a[] = {Ptr(in->x), Ptr(in->delta), Ptr(in->norm_w), Ptr(in->res_out), Ptr(in->xq), Ptr(in->xs),
                         Ptr(in->xq_out), Ptr(in->xs_out),
                         Ptr(mat(0).qs), Ptr(mat(0).d), Ptr(out(0)), Ptr(mat(1).qs), Ptr(mat(1).d), Ptr(out(1)),
                         Ptr(mat(2).qs), Ptr(mat(2).d), Ptr(out(2)), Ptr(mat(3).qs), Ptr(mat(3).d), Ptr(out(3)),
                         U32(rows(0)), U32(rows(1)), U32(rows(2)), U32(rows(3)), U32(off[1]), U32(off[2]), U32(off[3]),
-                        U32(tokens), U32(cols), Val(in->eps)};
-  return Launch(eng, name, D3(off[4]), D3(256), a, err, errlen);
+                        U32(off[4]), U32(tokens), U32(cols), Val(in->eps)};
+  return Launch(eng, name, D3(blocks), D3(256), a, err, errlen);
+}
+
+extern "C" int halo_op_proj_q8(halo_engine* eng, const halo_q8_matrix* mats, float* const* ys, uint32_t n_mats,
+                               const halo_proj_input* in, uint32_t tokens, char* err, size_t errlen) {
+  return halo_op_proj_q8_grid(eng, mats, ys, n_mats, in, tokens, 0, 0, err, errlen);
 }

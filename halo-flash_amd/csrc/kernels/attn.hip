@@ -181,9 +181,11 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_combine(
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const std::uint32_t i = i0 + 16 * u;
-      w[u] = i < n ? wts[i] : 0.0f;
-      a[u] = w[u] == 0.0f ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
-                          : reinterpret_cast<const float4*>(pacc + (item(i) * slots + slot) * kHd)[quarter * 16 + f];
+      const float wi = wts[min(i, n - 1)];
+      w[u] = i < n ? wi : 0.0f;
+      // load unconditionally (clamped item), then select: an empty chunk's partial is never written
+      const float4 av = reinterpret_cast<const float4*>(pacc + (item(min(i, n - 1)) * slots + slot) * kHd)[quarter * 16 + f];
+      a[u] = w[u] == 0.0f ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : av;
     }
 #pragma unroll
     for (int u = 0; u < kU; ++u) {

@@ -145,7 +145,8 @@ __device__ __forceinline__ float Normal(std::uint64_t key) {
 
 // ---- canonical row prologue: residual add, RMS norm and Q8 quantization of one activation row -----------------
 // Every kernel that normalizes or quantizes a row in its prologue uses this decomposition, so all of them produce
-// the same bits: 256 threads, thread t holds the 8-value chunks c = t + 256 k (k < KC, c < n / 8) of the row;
+// the same bits (sums of squares are explicit fused multiply-adds: left to contraction, the choice of which
+// product of p1 + p2 gets fused differs between kernels, and so do the last bits): 256 threads, thread t holds the 8-value chunks c = t + 256 k (k < KC, c < n / 8) of the row;
 // the sum of squares runs over a thread's chunks in order, then GroupSum, then the four wave sums in order.
 // A 32-value Q8 block is the 4 chunks of 4 consecutive lanes (a DPP quad).
 namespace halo {
@@ -155,27 +156,29 @@ struct Row8 {
   float v[KC][8];
 };
 
-// v = x (+ delta) for the chunks of this thread; chunks past n are zero.
+// v = x (+ delta) for the chunks of this thread; chunks past n are zero. The loads are unconditional (a chunk past n
+// reloads the last one and is then zeroed): a load under a branch costs a vmcnt(0) wait at the join.
 template <int KC>
 __device__ __forceinline__ void LoadRow8(const float* __restrict__ x, const float* __restrict__ delta, std::uint32_t n,
                                          Row8<KC>& r) {
 #pragma unroll
   for (int k = 0; k < KC; ++k) {
-    const std::uint32_t c = threadIdx.x + 256u * k;
-    if (c < n / 8) {
-      const float4 a = reinterpret_cast<const float4*>(x)[2 * c], b = reinterpret_cast<const float4*>(x)[2 * c + 1];
-      r.v[k][0] = a.x, r.v[k][1] = a.y, r.v[k][2] = a.z, r.v[k][3] = a.w;
-      r.v[k][4] = b.x, r.v[k][5] = b.y, r.v[k][6] = b.z, r.v[k][7] = b.w;
-      if (delta != nullptr) {
-        const float4 e = reinterpret_cast<const float4*>(delta)[2 * c],
-                     f = reinterpret_cast<const float4*>(delta)[2 * c + 1];
-        r.v[k][0] += e.x, r.v[k][1] += e.y, r.v[k][2] += e.z, r.v[k][3] += e.w;
-        r.v[k][4] += f.x, r.v[k][5] += f.y, r.v[k][6] += f.z, r.v[k][7] += f.w;
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) r.v[k][e] = 0.0f;
+    const std::uint32_t c = threadIdx.x + 256u * k, cc = min(c, n / 8 - 1);
+    const bool in = c < n / 8;
+    const float4 a = reinterpret_cast<const float4*>(x)[2 * cc], b = reinterpret_cast<const float4*>(x)[2 * cc + 1];
+    r.v[k][0] = a.x, r.v[k][1] = a.y, r.v[k][2] = a.z, r.v[k][3] = a.w;
+    r.v[k][4] = b.x, r.v[k][5] = b.y, r.v[k][6] = b.z, r.v[k][7] = b.w;
+    {  // delta (or, without one, x again: a cache hit) is loaded either way and added times 1 or 0, so the load is
+       // not moved under a branch; v + delta * 1 is v + delta exactly, v + x * 0 is v
+      const float* dsrc = delta != nullptr ? delta : x;
+      const float on = delta != nullptr ? 1.0f : 0.0f;
+      const float4 e = reinterpret_cast<const float4*>(dsrc)[2 * cc],
+                   f = reinterpret_cast<const float4*>(dsrc)[2 * cc + 1];
+      r.v[k][0] += e.x * on, r.v[k][1] += e.y * on, r.v[k][2] += e.z * on, r.v[k][3] += e.w * on;
+      r.v[k][4] += f.x * on, r.v[k][5] += f.y * on, r.v[k][6] += f.z * on, r.v[k][7] += f.w * on;
     }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r.v[k][e] = in ? r.v[k][e] : 0.0f;
   }
 }
 
@@ -199,7 +202,7 @@ __device__ __forceinline__ void RmsNormRow8(Row8<KC>& r, const float* __restrict
 #pragma unroll
   for (int k = 0; k < KC; ++k)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ss += r.v[k][e] * r.v[k][e];
+    for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(r.v[k][e], r.v[k][e], ss);
   ss = GroupSum(ss);
   __syncthreads();
   if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = ss;
@@ -214,6 +217,70 @@ __device__ __forceinline__ void RmsNormRow8(Row8<KC>& r, const float* __restrict
       const float wv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) r.v[k][e] = r.v[k][e] * scale * wv[e];
+    }
+  }
+}
+
+// In place, per 128-value head (16 chunks = one 16-lane DPP row): v = RMSNorm(v) * w * sigmoid(z), the DeltaNet
+// output norm (w [128] shared by heads, z [n] the gate row). Block of exactly 256 threads.
+template <int KC>
+__device__ __forceinline__ void GatedNormRow8(Row8<KC>& r, const float* __restrict__ z, const float* __restrict__ w,
+                                              std::uint32_t n, float eps) {
+#pragma unroll
+  for (int k = 0; k < KC; ++k) {
+    const std::uint32_t c = threadIdx.x + 256u * k;
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(r.v[k][e], r.v[k][e], ss);
+    ss = GroupSum<16>(ss);
+    if (c < n / 8) {
+      const float scale = 1.0f / sqrtf(ss / 128.0f + eps);
+      const float4 wa = reinterpret_cast<const float4*>(w)[2 * (c % 16)],
+                   wb = reinterpret_cast<const float4*>(w)[2 * (c % 16) + 1];
+      const float4 za = reinterpret_cast<const float4*>(z)[2 * c], zb = reinterpret_cast<const float4*>(z)[2 * c + 1];
+      const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+      const float zv[8] = {za.x, za.y, za.z, za.w, zb.x, zb.y, zb.z, zb.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r.v[k][e] = r.v[k][e] * scale * wv[e] * Sigmoid(zv[e]);
+    }
+  }
+}
+
+// RmsNormRow8 / GatedNormRow8 with the weights (and gate) already in registers, in the same chunk layout (w8: the
+// 8 weights of this thread's position in its head). Same arithmetic, same bits.
+template <int KC>
+__device__ __forceinline__ void RmsNormRow8W(Row8<KC>& r, const Row8<KC>& w, std::uint32_t n, float eps, float* red) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int k = 0; k < KC; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(r.v[k][e], r.v[k][e], ss);
+  ss = GroupSum(ss);
+  __syncthreads();
+  if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  ss = ((red[0] + red[1]) + red[2]) + red[3];
+  const float scale = 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
+#pragma unroll
+  for (int k = 0; k < KC; ++k)
+    if (threadIdx.x + 256u * k < n / 8)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r.v[k][e] = r.v[k][e] * scale * w.v[k][e];
+}
+template <int KC>
+__device__ __forceinline__ void GatedNormRow8W(Row8<KC>& r, const Row8<KC>& z, const float (&w8)[8], std::uint32_t n,
+                                               float eps) {
+#pragma unroll
+  for (int k = 0; k < KC; ++k) {
+    const std::uint32_t c = threadIdx.x + 256u * k;
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(r.v[k][e], r.v[k][e], ss);
+    ss = GroupSum<16>(ss);
+    if (c < n / 8) {
+      const float scale = 1.0f / sqrtf(ss / 128.0f + eps);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r.v[k][e] = r.v[k][e] * scale * w8[e] * Sigmoid(z.v[k][e]);
     }
   }
 }
@@ -247,4 +314,24 @@ __device__ __forceinline__ void QuantRow8(const Row8<KC>& r, std::uint32_t n, st
   }
 }
 
+}  // namespace halo
+
+// ---- last-arriving block -------------------------------------------------------------------------------------
+// Every block of a group of n calls this once (all threads). Returns true, in every thread, in exactly one block:
+// the last to arrive, which then sees every global store the group made before arriving (agent-scope release by
+// each block, acquire by the last; this writes back / invalidates the per-XCD L2 lines involved). The last block
+// returns the counter to zero for the next launch. flag is one LDS word.
+namespace halo {
+__device__ __forceinline__ bool LastBlock(std::uint32_t* counter, std::uint32_t n, std::uint32_t* flag) {
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) *flag = atomicAdd(counter, 1u) == n - 1 ? 1u : 0u;
+  __syncthreads();
+  const bool last = *flag != 0u;
+  if (last) {
+    __threadfence();
+    if (threadIdx.x == 0) atomicExch(counter, 0u);
+  }
+  return last;
+}
 }  // namespace halo

@@ -80,26 +80,19 @@ extern "C" __global__ void __launch_bounds__(256) halo_gdn_prep_decode(
   }
 }
 
-// grid (S, Hv / 4), block 256 (a wave per head): RMSNorm(o_h) * w (d weights shared by heads) * sigmoid(z_h), then
-// the Q8 quantization: o, z [S][Hv][d] -> xq [S][Hv d], xs [S][Hv d / 32]. d = 128.
+// grid (S), block 256: per 128-value head RMSNorm(o_h) * w (d weights shared by heads) * sigmoid(z_h), then the
+// Q8 quantization: o, z [S][Hv][d] -> xq [S][Hv d], xs [S][Hv d / 32]. d = 128, Hv d <= 8192. The row
+// decomposition is the canonical one (halo::GatedNormRow8), shared with the output projection's prologue.
 extern "C" __global__ void __launch_bounds__(256)
     halo_gated_rmsnorm_q8(const float* __restrict__ o, const float* __restrict__ z, const float* __restrict__ w,
                           std::int8_t* __restrict__ xq, float* __restrict__ xs, std::uint32_t Hv, std::uint32_t d,
                           float eps) {
   const std::size_t s = blockIdx.x;
-  const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, waves = blockDim.x / kWave;
   const std::uint32_t D = Hv * d;
-  for (std::uint32_t h = blockIdx.y * waves + wave; h < Hv && h < (blockIdx.y + 1) * waves; h += waves) {
-    const float* oh = o + s * D + h * d;
-    const float v0 = oh[lane], v1 = oh[lane + 64];
-    const float ss = halo::GroupSum(v0 * v0 + v1 * v1);
-    const float sc = 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
-    const float y0 = v0 * sc * w[lane] * halo::Sigmoid(z[s * D + h * d + lane]);
-    const float y1 = v1 * sc * w[lane + 64] * halo::Sigmoid(z[s * D + h * d + lane + 64]);
-    // 128 values = 4 blocks of 32: lanes 0-31 / 32-63 hold blocks 0 / 1 (y0) and 2 / 3 (y1)
-    Quant32(y0, xq + s * D + h * d, xs + s * (D / 32) + h * (d / 32), lane / 32);
-    Quant32(y1, xq + s * D + h * d, xs + s * (D / 32) + h * (d / 32), 2 + lane / 32);
-  }
+  halo::Row8<4> r;
+  halo::LoadRow8(o + s * D, nullptr, D, r);
+  halo::GatedNormRow8(r, z + s * D, w, D, eps);
+  halo::QuantRow8(r, D, xq + s * D, xs + s * (D / 32));
 }
 
 // grid (S), block 256: attention prologue for one token per session. qg [S][Hq][2 d] (per head: q | gate),

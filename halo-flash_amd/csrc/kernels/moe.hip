@@ -113,7 +113,8 @@ __device__ void WaveTopK(const float* logits, std::uint32_t E, std::uint32_t k, 
 #pragma unroll
   for (int i = 0; i < kMaxPerLane; ++i) {
     const std::uint32_t e = lane + kWave * i;
-    p[i] = e < E ? logits[e] : -INFINITY;
+    const float lv = logits[min(e, E - 1)];
+    p[i] = e < E ? lv : -INFINITY;
     mx = fmaxf(mx, p[i]);
   }
   mx = halo::GroupMax(mx);
@@ -267,7 +268,8 @@ extern "C" __global__ void __launch_bounds__(1024)
   __shared__ std::uint32_t ncand;
   const std::uint32_t t = blockIdx.x, e = threadIdx.x;
   const bool valid = e < E;
-  const float l = valid ? logits[static_cast<std::size_t>(t) * E + e] : -INFINITY;
+  const float lv = logits[static_cast<std::size_t>(t) * E + min(e, E - 1)];
+  const float l = valid ? lv : -INFINITY;
   if (e == 0) {
     tau_s = -1.0f;
     ncand = 0;
@@ -483,10 +485,13 @@ extern "C" __global__ void __launch_bounds__(1024) halo_moe_down_q8(
 #pragma unroll
     for (int p = 0; p < kDownRows / 2; ++p) {
       const std::uint32_t r = min(r0 + 2 * p + sub, H - 1);
-      q[p] = in ? __builtin_bit_cast(int4, __builtin_nontemporal_load(
-                                              reinterpret_cast<const halo::V4i*>(base + static_cast<std::size_t>(r) * f + c)))
-                : make_int4(0, 0, 0, 0);
-      sw[p] = in ? F16(dbase[static_cast<std::size_t>(r) * (f / 32) + c / 32]) : 0.0f;
+      // loads from a clamped address, then a select: a load under a branch would cost a vmcnt(0) wait
+      const std::uint32_t cc = in ? c : 0;
+      const int4 qv = __builtin_bit_cast(
+          int4, __builtin_nontemporal_load(reinterpret_cast<const halo::V4i*>(base + static_cast<std::size_t>(r) * f + cc)));
+      const float sv = F16(dbase[static_cast<std::size_t>(r) * (f / 32) + cc / 32]);
+      q[p] = in ? qv : make_int4(0, 0, 0, 0);
+      sw[p] = in ? sv : 0.0f;
     }
     // h: 16 values per lane, quantized per 32 with the neighbour lane
     float hv[16];

@@ -147,7 +147,8 @@ __device__ __forceinline__ void Q8A8Rows(const std::int8_t* __restrict__ qs, con
           q[u][k] = __builtin_bit_cast(int4, __builtin_nontemporal_load(reinterpret_cast<const halo::V4i*>(rowp[k] + cc)));
         else
           q[u][k] = *reinterpret_cast<const int4*>(rowp[k] + cc);
-        s[u][k] = ok ? F16(dp[k][cc / 32]) : 0.0f;
+        const float sv = F16(dp[k][cc / 32]);  // unconditional: a load under a branch costs a vmcnt(0) wait
+        s[u][k] = ok ? sv : 0.0f;
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b) {

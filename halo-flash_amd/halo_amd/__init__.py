@@ -59,14 +59,14 @@ class ProjInput(C.Structure):
         ("eps", C.c_float), ("mode", C.c_uint32)]
 
 
-PROJ_Q, PROJ_F, PROJ_N = 0, 1, 2
+PROJ_Q, PROJ_F, PROJ_N, PROJ_G = 0, 1, 2, 3
 
 
-def proj_q8(dev, weights, outs, inp: ProjInput, tokens: int):
+def proj_q8(dev, weights, outs, inp: ProjInput, tokens: int, tasks_per_wave: int = 0, lanes_per_row: int = 0):
     """One grouped projection launch: weights is a list of Q8Weights, outs their [tokens][rows] outputs."""
     mats = (Q8Matrix * len(weights))(*[w.desc for w in weights])
     ys = (C.c_void_p * len(outs))(*[o.ptr for o in outs])
-    dev.op("proj_q8", mats, ys, len(weights), C.byref(inp), tokens)
+    dev.op("proj_q8_grid", mats, ys, len(weights), C.byref(inp), tokens, tasks_per_wave, lanes_per_row)
 
 
 class MoeWeights(C.Structure):
@@ -153,6 +153,8 @@ _SIGS = {
     "halo_op_quantize_q8": (C.c_int, [_VP, _VP, _VP, _VP, _U32, _U32], True),
     "halo_op_proj_q8": (C.c_int, [_VP, C.POINTER(Q8Matrix), C.POINTER(C.c_void_p), _U32, C.POINTER(ProjInput), _U32],
                         True),
+    "halo_op_proj_q8_grid": (C.c_int, [_VP, C.POINTER(Q8Matrix), C.POINTER(C.c_void_p), _U32, C.POINTER(ProjInput),
+                                       _U32, _U32, _U32], True),
     "halo_op_matvec_q8a8": (C.c_int, [_VP, C.POINTER(Q8Matrix), _VP, _VP, _VP, _U32, _U32], True),
     "halo_op_matvec_q8a8_tiled": (
         C.c_int, [_VP, C.POINTER(Q8Matrix), _VP, _VP, _VP, _U32, _U32, _U32, _U32, _U32], True),

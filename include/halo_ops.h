@@ -63,10 +63,12 @@ int halo_op_matvec_q8a8(halo_engine* eng, const halo_q8_matrix* w, const int8_t*
  *   HALO_PROJ_Q: in->xq / in->xs already quantized;
  *   HALO_PROJ_F: in->x fp32 [tokens][cols] quantized in the prologue;
  *   HALO_PROJ_N: x = RMSNorm(in->x + in->delta) * in->norm_w (delta may be null), then quantized; when delta is
- *                non-null and res_out non-null, x + delta is written to res_out (which must not alias in->x).
+ *                non-null and res_out non-null, x + delta is written to res_out (which must not alias in->x);
+ *   HALO_PROJ_G: x = per 128-value head RMSNorm(in->x) * in->norm_w [128] * sigmoid(in->delta), the DeltaNet
+ *                output norm (ReferenceModel::LinearAttention, src/model/reference.cpp:359-364); cols % 128 == 0.
  * xq_out / xs_out (may be null) receive the quantized activations (bit-identical to halo_op_quantize_q8 of the
  * same fp32 row). */
-enum { HALO_PROJ_Q = 0, HALO_PROJ_F = 1, HALO_PROJ_N = 2 };
+enum { HALO_PROJ_Q = 0, HALO_PROJ_F = 1, HALO_PROJ_N = 2, HALO_PROJ_G = 3 };
 typedef struct halo_proj_input {
   const float* x;
   const float* delta;
@@ -81,6 +83,11 @@ typedef struct halo_proj_input {
 } halo_proj_input;
 int halo_op_proj_q8(halo_engine* eng, const halo_q8_matrix* mats, float* const* ys, uint32_t n_mats,
                     const halo_proj_input* in, uint32_t tokens, char* err, size_t errlen);
+/* The same with an explicit tiling for tuning: tasks per wave (1 / 2 / 4 rows groups per wave, so the prologue
+ * runs once per 4 x that many groups) and lanes per row (16 / 32 / 64); 0 keeps the default of each. */
+int halo_op_proj_q8_grid(halo_engine* eng, const halo_q8_matrix* mats, float* const* ys, uint32_t n_mats,
+                         const halo_proj_input* in, uint32_t tokens, uint32_t tasks_per_wave, uint32_t lanes_per_row,
+                         char* err, size_t errlen);
 
 /* The same with an explicit GEMV tiling (lanes per row 16/32/64, rows per lane group 1/2/4, waves per block) for
  * tuning sweeps; m <= 8. */

@@ -117,3 +117,45 @@ def test_proj_rejects_bad_shapes(dev):
         H.proj_q8(dev, ws[:1], outs[:1], H.ProjInput(x=x.ptr, mode=H.PROJ_F), 9)  # too many tokens
     with pytest.raises(H.HaloError):
         H.proj_q8(dev, ws[:1], outs[:1], H.ProjInput(x=x.ptr, norm_w=x.ptr, res_out=x.ptr, mode=H.PROJ_N), 1)
+
+
+@pytest.mark.parametrize("tokens", [1, 4])
+def test_proj_mode_g_matches_gated_norm_kernel(dev, tokens):
+    """DeltaNet output projection: per-head RMSNorm * w * sigmoid(z) (reference.cpp:359-364) in the prologue."""
+    rng = np.random.default_rng(40 + tokens)
+    Hv, d = 32, 128
+    cols = Hv * d
+    host, ws = _mats(dev, rng, [(2048, cols)])
+    o = rng.normal(0, 1, (tokens, cols)).astype(np.float32)
+    z = rng.normal(0, 1, (tokens, cols)).astype(np.float32)
+    w = (1.0 + 0.1 * rng.normal(0, 1, d)).astype(np.float32)
+    eps = 1e-6
+    go, gz, gw = dev.to_device(o), dev.to_device(z), dev.to_device(w)
+    xq_o, xs_o = dev.array((tokens, cols), np.int8), dev.array((tokens, cols // 32), np.float32)
+    y = dev.array((tokens, 2048), np.float32)
+    inp = H.ProjInput(x=go.ptr, delta=gz.ptr, norm_w=gw.ptr, xq_out=xq_o.ptr, xs_out=xs_o.ptr, eps=eps,
+                      mode=H.PROJ_G)
+    H.proj_q8(dev, ws, [y], inp, tokens)
+    xq2, xs2 = dev.array((tokens, cols), np.int8), dev.array((tokens, cols // 32), np.float32)
+    dev.launch("halo_gated_rmsnorm_q8", (tokens,), (256,),
+               [go, gz, gw, xq2, xs2, ("u32", Hv), ("u32", d), ("f32", eps)])
+    a_s, b_s = xs_o.download(), xs2.download()
+    bad = np.nonzero(a_s.view(np.uint32) != b_s.view(np.uint32))
+    assert bad[0].size == 0, f"scales differ at {bad}: {a_s[bad][:8]} vs {b_s[bad][:8]}"
+    assert np.array_equal(xq_o.download(), xq2.download())
+    # the oracle: cpu RmsNorm per head, then sigmoid(z) (reference.cpp:359-364)
+    want = o.copy()
+    for t in range(tokens):
+        for h in range(Hv):
+            seg = np.ascontiguousarray(want[t, h * d:(h + 1) * d])
+            O.oracle().or_rmsnorm(seg, d, w.ctypes.data, eps)
+            want[t, h * d:(h + 1) * d] = seg * np.array([O.oracle().or_sigmoid(float(v)) for v in
+                                                         z[t, h * d:(h + 1) * d]], np.float32)
+    xq_w, xs_w = O.quantize(want)
+    got_q = xq2.download().astype(np.int32)
+    diff = got_q - xq_w.astype(np.int32)
+    assert np.abs(diff).max() <= 1 and np.count_nonzero(diff) <= max(2, diff.size // 2000)
+    assert np.allclose(xs2.download(), xs_w, rtol=1e-5)
+    qs, dd = host[0]
+    want_y, mag = O.gemv_q8a8(qs, dd, xq2.download(), xs2.download())
+    _check_y(y.download(), want_y, mag)

@@ -158,8 +158,9 @@ int halo_op_matvec_q8a8(halo_engine* eng, const halo_q8_matrix* w, const int8_t*
     return Launch(eng, wide ? "halo_gemm_q8a8_mfma_t4" : "halo_gemm_q8a8_mfma_t1",
                   D3(CeilDiv(w->rows, 16), CeilDiv(m, wide ? 64 : 16)), D3(256), a, err, errlen);
   }
-  // Up to 8 tokens with a dense output: the grouped projection kernel in its quantized-input mode (one task of
-  // rows per wave, activations staged in LDS once per block).
+  // Up to 8 tokens, a dense output and rows of at most 2048 columns: the grouped projection kernel in its
+  // quantized-input mode (one task of rows per wave, activations staged in LDS once per block). Wider rows measure
+  // faster on the per-group GEMV below, whose 64 lanes per row read the activations straight from the caches.
   if (m <= 8 && (m == 1 || ystride == w->rows) && w->qstride == w->cols && w->cols <= 2048) {
     halo_proj_input in{};
     in.xq = xq;

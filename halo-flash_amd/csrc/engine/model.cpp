@@ -8,6 +8,7 @@
 
 #include <initializer_list>
 #include <map>
+#include <string>
 #include <memory>
 #include <utility>
 #include <vector>
@@ -487,6 +488,67 @@ int halo_model_run(halo_model* m, uint32_t S, uint32_t prefix, uint32_t steps, c
   for (std::uint32_t i = 0; i < steps; ++i)
     if (halo_launch_graph(m->dev, &it->second, err, errlen) != 0) return -1;
   return 0;
+}
+
+int halo_model_tensor(const halo_model* m, uint32_t layer, const char* name, halo_model_tensor_view* out, char* err,
+                      size_t errlen) {
+  if (m == nullptr || name == nullptr || out == nullptr) return SetErr(err, errlen, "null argument"), -1;
+  *out = halo_model_tensor_view{};
+  const std::string n(name);
+  auto f32 = [&](const halo_buffer& b, std::uint32_t rows, std::uint32_t cols) {
+    if (b.device == nullptr) return SetErr(err, errlen, "tensor %s absent in layer %u", name, layer), -1;
+    *out = halo_model_tensor_view{b.device, nullptr, HALO_TENSOR_F32, rows, cols, cols};
+    return 0;
+  };
+  auto q8 = [&](const Q8& w) {
+    if (w.qs.device == nullptr) return SetErr(err, errlen, "tensor %s absent in layer %u", name, layer), -1;
+    *out = halo_model_tensor_view{w.qs.device, w.d.device, HALO_TENSOR_Q8, w.m.rows, w.m.cols, w.m.qstride};
+    return 0;
+  };
+  const halo_model_config& c = m->c;
+  if (layer == UINT32_MAX) {
+    if (n == "embd") return q8(m->embd);
+    if (n == "head") return q8(m->head);
+    if (n == "out_norm") return f32(m->out_norm, 1, c.hidden);
+    return SetErr(err, errlen, "unknown tensor %s", name), -1;
+  }
+  if (layer >= m->layers.size()) return SetErr(err, errlen, "layer %u out of range", layer), -1;
+  const Layer& L = m->layers[layer];
+  const std::uint32_t H = c.hidden, Hv = c.gdn_v_heads, d = c.gdn_head_dim, hd = c.head_dim;
+  if (n == "attn_norm") return f32(L.attn_norm, 1, H);
+  if (n == "ffn_norm") return f32(L.ffn_norm, 1, H);
+  if (n == "router") return f32(L.router, c.n_experts, H);
+  if (n == "shared_gate") return f32(L.shared_gate, 1, H);
+  if (n == "gate") return q8(L.gate);
+  if (n == "up") return q8(L.up);
+  if (n == "down") return q8(L.down);
+  if (n == "sgate") return q8(L.sgate);
+  if (n == "sup") return q8(L.sup);
+  if (n == "sdown") return q8(L.sdown);
+  if (!L.attn) {
+    if (n == "qkv") return q8(L.qkv);
+    if (n == "z") return q8(L.z);
+    if (n == "ab") return q8(L.ab);
+    if (n == "out") return q8(L.out);
+    if (n == "conv_w") return f32(L.conv_w, m->conv_ch, c.conv_kernel);
+    if (n == "a") return f32(L.a, 1, Hv);
+    if (n == "dt") return f32(L.dt, 1, Hv);
+    if (n == "norm_w") return f32(L.norm_w, 1, d);
+  } else {
+    if (n == "qg") return q8(L.qg);
+    if (n == "k") return q8(L.k);
+    if (n == "v") return q8(L.v);
+    if (n == "o") return q8(L.o);
+    if (n == "q_norm") return f32(L.q_norm, 1, hd);
+    if (n == "k_norm") return f32(L.k_norm, 1, hd);
+  }
+  return SetErr(err, errlen, "unknown tensor %s for layer %u", name, layer), -1;
+}
+
+int halo_model_logits(halo_model* m, uint32_t s, float* out, char* err, size_t errlen) {
+  if (m == nullptr || out == nullptr || s >= m->c.max_sessions) return SetErr(err, errlen, "bad session"), -1;
+  return halo_download(m->dev, &m->logits, static_cast<std::size_t>(s) * m->c.vocab * 4, out, m->c.vocab * 4ull, err,
+                       errlen);
 }
 
 int halo_model_history(halo_model* m, uint32_t s, uint32_t* out, uint32_t n, char* err, size_t errlen) {

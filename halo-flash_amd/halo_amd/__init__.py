@@ -106,6 +106,11 @@ class ModelConfig(C.Structure):
         (n, C.c_uint32) for n in ("max_sessions", "max_context", "prefix_tokens", "pad")]
 
 
+class TensorView(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("scales", C.c_void_p)] + [(n, C.c_uint32) for n in (
+        "kind", "rows", "cols", "qstride")]
+
+
 def c4_config(max_sessions=4, prefix_tokens=8192, max_context=8192 + 256 + 128):
     """48 layers (3 DeltaNet : 1 GQA), hidden 2048, vocab 151936, MoE as C2."""
     return ModelConfig(vocab=151936, hidden=2048, layers=48, attn_interval=4, gdn_k_heads=16, gdn_v_heads=32,
@@ -181,6 +186,8 @@ _SIGS = {
     "halo_model_step_eager": (C.c_int, [_VP, _U32, _U32], True),
     "halo_model_history": (C.c_int, [_VP, _U32, _VP, _U32], True),
     "halo_model_positions": (C.c_int, [_VP, _VP, _U32], True),
+    "halo_model_tensor": (C.c_int, [_VP, _U32, C.c_char_p, C.POINTER(TensorView)], True),
+    "halo_model_logits": (C.c_int, [_VP, _U32, _VP], True),
     "halo_op_moe_workspace_bytes": (_SZ, [C.POINTER(MoeWeights), _U32], False),
     "halo_op_moe_views": (C.c_int, [C.POINTER(MoeWeights), _U32, _VP, C.POINTER(MoeViews)], True),
     "halo_op_moe_decode": (C.c_int, [_VP, C.POINTER(MoeWeights), _VP, _VP, _U32, _VP, _SZ], True),
@@ -424,6 +431,27 @@ class Model:
         if self.h:
             lib().halo_model_destroy(self.h)
             self.h = None
+
+    def _download(self, ptr: int, nbytes: int, dtype):
+        out = np.empty(nbytes // np.dtype(dtype).itemsize, dtype)
+        b = Buffer(ptr, nbytes, None)
+        _call("halo_download", self.dev.handle, C.byref(b), 0, out.ctypes.data, nbytes)
+        return out
+
+    def tensor(self, layer: int, name: str):
+        """Host copy of a weight: fp32 [rows][cols], or a Q8_0 pair (qs [rows][cols] int8, d [rows][cols/32])."""
+        v = TensorView()
+        _call("halo_model_tensor", self.h, 0xFFFFFFFF if layer < 0 else layer, name.encode(), C.byref(v))
+        if v.kind == 0:
+            return self._download(v.data, v.rows * v.cols * 4, np.float32).reshape(v.rows, v.cols)
+        qs = self._download(v.data, v.rows * v.qstride, np.int8).reshape(v.rows, v.qstride)[:, : v.cols]
+        d = self._download(v.scales, v.rows * (v.cols // 32) * 2, np.uint16).reshape(v.rows, v.cols // 32)
+        return np.ascontiguousarray(qs), d
+
+    def logits(self, s: int) -> np.ndarray:
+        out = np.empty(self.cfg.vocab, np.float32)
+        _call("halo_model_logits", self.h, s, out.ctypes.data)
+        return out
 
     @property
     def weight_bytes(self) -> int:

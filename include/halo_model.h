@@ -64,6 +64,24 @@ int halo_model_step_eager(halo_model* m, uint32_t S, uint32_t attn_prefix, char*
 int halo_model_history(halo_model* m, uint32_t s, uint32_t* out, uint32_t n, char* err, size_t errlen);
 int halo_model_positions(halo_model* m, uint32_t* nkv_out, uint32_t S, char* err, size_t errlen);
 
+/* A weight tensor of the model, for inspection (the reference's GGUF tensor table, src/core/gguf.hpp; used by
+ * parity tests to recompute a step on the host). kind: HALO_TENSOR_F32 (data [rows][cols] fp32) or
+ * HALO_TENSOR_Q8 (data = qs [rows][qstride] int8, scales = d [rows][cols / 32] fp16 bits). Device pointers. */
+enum { HALO_TENSOR_F32 = 0, HALO_TENSOR_Q8 = 1 };
+typedef struct halo_model_tensor_view {
+  void* data;
+  void* scales;
+  uint32_t kind, rows, cols, qstride;
+} halo_model_tensor_view;
+/* layer < layers: per-layer tensors by name: attn_norm, ffn_norm; DeltaNet layers: qkv, z, ab (alpha | beta rows),
+ * out, conv_w [C][K], a, dt, norm_w; attention layers: qg (per head q | gate rows), k, v, o, q_norm, k_norm; every
+ * layer: router [E][H], shared_gate [H], gate, up ([E * ff][H]), down ([E * H][ff]), sgate, sup, sdown.
+ * layer == UINT32_MAX: embd, head, out_norm. */
+int halo_model_tensor(const halo_model* m, uint32_t layer, const char* name, halo_model_tensor_view* out, char* err,
+                      size_t errlen);
+/* Host copy of session s's logits of the last step ([vocab] fp32). Not capturable. */
+int halo_model_logits(halo_model* m, uint32_t s, float* out, char* err, size_t errlen);
+
 #ifdef __cplusplus
 }
 #endif

@@ -27,6 +27,12 @@ def layer(dev):
     return H.MoeLayer(dev, seed=42)
 
 
+@pytest.fixture(scope="module")
+def small_layer(dev):
+    """The reduced twin's shapes: 16 experts top-4, hidden 1024, ff 256 (lanes past ff idle in the down launch)."""
+    return H.MoeLayer(dev, n_experts=16, n_used=4, hidden=1024, ff=256, shared_ff=256, seed=7)
+
+
 def _view(ws, base, ptr, n, dtype):
     return ws.download_range(ptr - base, n, dtype)
 
@@ -36,9 +42,9 @@ def _gemv(qs, d, xq, xs):
     return y.astype(np.float64), mag
 
 
-@pytest.mark.parametrize("T", [1, 4, 16])
-def test_moe_decode_matches_oracle(dev, layer, T):
-    L = layer
+@pytest.mark.parametrize("T,shape", [(1, "c2"), (4, "c2"), (16, "c2"), (1, "small"), (3, "small")])
+def test_moe_decode_matches_oracle(dev, layer, small_layer, T, shape):
+    L = layer if shape == "c2" else small_layer
     rng = np.random.default_rng(T)
     x = rng.normal(0, 1, (T, L.H)).astype(np.float32)
     gx = dev.to_device(x)

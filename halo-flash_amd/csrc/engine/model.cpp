@@ -190,23 +190,15 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
   for (auto& L : m->layers) {
     if (!L.attn) {
       if (proj_norm(L.attn_norm, {&L.qkv, &L.z, &L.ab}, {&m->qkv, &m->zo, &m->abo}) != 0) return -1;
-      float* conv = P<float>(m->conv_state) + static_cast<std::size_t>(L.gdn_index) * c.max_sessions *
-                                                  (c.conv_kernel - 1) * C;
-      {
-        const halo_arg a[] = {Ptr(m->qkv.device), Ptr(conv), Ptr(L.conv_w.device), Ptr(m->abo.device),
-                              Ptr(L.a.device), Ptr(L.dt.device), Ptr(m->q.device), Ptr(m->k.device), Ptr(m->v.device),
-                              Ptr(m->g.device), Ptr(m->beta.device), U32(Hk), U32(Hv), U32(d), U32(c.conv_kernel),
-                              Val(eps)};
-        if (Launch(eng, "halo_gdn_prep_decode", D3(S, C / 256), D3(256), a, err, errlen) != 0) return -1;
-      }
+      float* ring = P<float>(m->conv_state) + static_cast<std::size_t>(L.gdn_index) * c.max_sessions *
+                                                  c.conv_kernel * C;
       float* st = P<float>(m->gdn_state) + static_cast<std::size_t>(L.gdn_index) * c.max_sessions * Hv * d * d;
-      if (halo_op_gdn_decode(eng, st, P<float>(m->q), P<float>(m->k), P<float>(m->v), P<float>(m->g),
-                             P<float>(m->beta), P<float>(m->o), S, Hv, Hk, d, err, errlen) != 0)
-        return -1;
-      {
-        const halo_arg a[] = {Ptr(m->o.device), Ptr(m->zo.device), Ptr(L.norm_w.device), Ptr(m->oq.device),
-                              Ptr(m->os.device), U32(Hv), U32(d), Val(eps)};
-        if (Launch(eng, "halo_gated_rmsnorm_q8", D3(S), D3(256), a, err, errlen) != 0) return -1;
+      {  // conv + norms + gates + recurrence + gated output norm + quantization, one block per (session, head)
+        const halo_arg a[] = {Ptr(m->qkv.device), Ptr(m->zo.device), Ptr(m->abo.device), Ptr(ring),
+                              Ptr(L.conv_w.device), Ptr(L.a.device), Ptr(L.dt.device), Ptr(L.norm_w.device), Ptr(st),
+                              Ptr(m->nkv.device), Ptr(m->oq.device), Ptr(m->os.device), U32(Hk), U32(Hv),
+                              U32(c.conv_kernel), Val(eps)};
+        if (Launch(eng, "halo_gdn_step_q8", D3(S * Hv), D3(512), a, err, errlen) != 0) return -1;
       }
       if (gemv(L.out, m->oq, m->os, m->delta) != 0) return -1;
       (void)Dv;
@@ -339,7 +331,7 @@ int halo_model_create(halo_engine* eng, const halo_model_config* cfg, uint64_t s
   const std::uint32_t C = m->conv_ch;
   const B bufs[] = {
       {&m->gdn_state, static_cast<std::size_t>(m->n_gdn) * S * Hv * d * d * 4},
-      {&m->conv_state, static_cast<std::size_t>(m->n_gdn) * S * (c.conv_kernel - 1 ? c.conv_kernel - 1 : 1) * C * 4},
+      {&m->conv_state, static_cast<std::size_t>(m->n_gdn) * S * c.conv_kernel * C * 4},  // ring of K slots
       {&m->pages, static_cast<std::size_t>(S) * m->max_pages * 4},
       {&m->nkv, S * 4},
       {&m->tokens, S * 4},
@@ -449,7 +441,7 @@ int halo_model_fork(halo_model* m, uint32_t src, uint32_t dst, char* err, size_t
   const halo_model_config& c = m->c;
   if (src >= c.max_sessions || dst >= c.max_sessions) return SetErr(err, errlen, "fork: bad session"), -1;
   const std::size_t st = static_cast<std::size_t>(c.gdn_v_heads) * c.gdn_head_dim * c.gdn_head_dim * 4;
-  const std::size_t cv = static_cast<std::size_t>(c.conv_kernel - 1) * m->conv_ch * 4;
+  const std::size_t cv = static_cast<std::size_t>(c.conv_kernel) * m->conv_ch * 4;
   for (std::uint32_t l = 0; l < m->n_gdn; ++l) {
     const std::size_t base = static_cast<std::size_t>(l) * c.max_sessions;
     char* sp = P<char>(m->gdn_state);

@@ -305,3 +305,124 @@ extern "C" __global__ void __launch_bounds__(256) halo_gdn_chunk_scan(
   for (std::uint32_t e = tid; e < kD * kJBlock; e += blockDim.x)
     St[static_cast<std::size_t>(e / kJBlock) * kD + jb * kJBlock + e % kJBlock] = S0[e / kJBlock][e % kJBlock];
 }
+
+// ---- the whole DeltaNet token step of the decode graph, one block per (session, value head) -----------------
+// Fuses the prologue (causal conv + SiLU, q / k L2 norms, decay and beta gates), the delta-rule recurrence and the
+// output RMSNorm * w * sigmoid(z) with its Q8 quantization for the output projection (reference
+// ReferenceModel::LinearAttention, src/model/reference.cpp:278-366). The conv history is a ring of K slots per
+// channel: position p's projection lives in slot p % K, so step p reads slots (p + 1 + j) % K (j < K - 1) and writes
+// slot p % K, which no block of the same step reads; q / k channels of key head kh are read by every value head with
+// h % Hk == kh but written only by value head h = kh (h < Hk), v channels by their own head. Positions: nkv[s] - 1.
+//   qkv [S][C] (C = 2 Hk d + Hv d), z [S][Hv d], ab [S][2 Hv] (alpha | beta logits), ring [S][K][C], conv_w [C][K],
+//   a, dt [Hv], norm_w [d], state [S][Hv][d][d] key-major fp32 (in place) -> oq [S][Hv d] int8, os [S][Hv d / 32].
+// grid (S * Hv), block 512: thread t owns state rows 8 (t / 32) .. + 8 and columns 4 (t % 32) .. + 4. d = 128.
+extern "C" __global__ void __launch_bounds__(512) halo_gdn_step_q8(
+    const float* __restrict__ qkv, const float* __restrict__ z, const float* __restrict__ ab, float* __restrict__ ring,
+    const float* __restrict__ conv_w, const float* __restrict__ a, const float* __restrict__ dt,
+    const float* __restrict__ norm_w, float* __restrict__ state, const std::uint32_t* __restrict__ nkv,
+    std::int8_t* __restrict__ oq, float* __restrict__ os, std::uint32_t Hk, std::uint32_t Hv, std::uint32_t K,
+    float eps) {
+  __shared__ float sq[kD], sk[kD], sv[kD], dl[kD];
+  __shared__ float red[16][kD + 4];
+  __shared__ float part[8];
+  __shared__ float gates[2];
+  const std::uint32_t s = blockIdx.x / Hv, h = blockIdx.x % Hv, kh = h % Hk;
+  const std::uint32_t t = threadIdx.x, wave = t / kWave, lane = t % kWave;
+  const std::uint32_t cg = t % 32, rg = t / 32, j0 = 4 * cg, i0 = 8 * rg;
+  const std::uint32_t Dk = Hk * kD, Dv = Hv * kD, C = 2 * Dk + Dv;
+  float* St = state + (static_cast<std::size_t>(s) * Hv + h) * kD * kD;
+  // the head's state first (64 KB per block, eight 16-byte loads per thread)
+  float4 row[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) row[r] = *reinterpret_cast<const float4*>(St + static_cast<std::size_t>(i0 + r) * kD + j0);
+  // prologue: threads 0..383 take the q, k and v channels of this head (128 each: waves 0-1, 2-3, 4-5)
+  const std::uint32_t pos = nkv[s] - 1;
+  const std::uint32_t seg = t / kD, i = t % kD;
+  float y = 0.0f;
+  if (seg < 3) {
+    const std::uint32_t ch = seg == 0 ? kh * kD + i : seg == 1 ? Dk + kh * kD + i : 2 * Dk + h * kD + i;
+    const float x = qkv[static_cast<std::size_t>(s) * C + ch];
+    float* rs = ring + static_cast<std::size_t>(s) * K * C;
+    float acc = conv_w[static_cast<std::size_t>(ch) * K + K - 1] * x;
+    for (std::uint32_t j = 0; j + 1 < K; ++j)
+      acc += conv_w[static_cast<std::size_t>(ch) * K + j] * rs[static_cast<std::size_t>((pos + 1 + j) % K) * C + ch];
+    if (seg == 2 || h < Hk) rs[static_cast<std::size_t>(pos % K) * C + ch] = x;
+    y = halo::Silu(acc);
+  }
+  const float ss = halo::GroupSum(y * y);
+  if (lane == 0) part[wave] = ss;
+  if (t == 0) {
+    gates[0] = a[h] * halo::Softplus(ab[static_cast<std::size_t>(s) * 2 * Hv + h] + dt[h]);
+    gates[1] = halo::Sigmoid(ab[static_cast<std::size_t>(s) * 2 * Hv + Hv + h]);
+  }
+  __syncthreads();
+  if (seg < 2) {
+    const float sc = 1.0f / sqrtf(part[2 * seg] + part[2 * seg + 1] + eps);
+    (seg == 0 ? sq : sk)[i] = y * sc;
+  } else if (seg == 2) {
+    sv[i] = y;
+  }
+  __syncthreads();
+  // recurrence: u = (decay S)^T k, delta = (v - u) beta, S <- decay S + k delta^T, o = S^T q / sqrt(d)
+  const float decay = expf(gates[0]), bt = gates[1];
+  float u[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const float ki = sk[i0 + r];
+    row[r].x *= decay;
+    row[r].y *= decay;
+    row[r].z *= decay;
+    row[r].w *= decay;
+    u[0] += row[r].x * ki;
+    u[1] += row[r].y * ki;
+    u[2] += row[r].z * ki;
+    u[3] += row[r].w * ki;
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) red[rg][j0 + c] = u[c];
+  __syncthreads();
+  if (t < kD) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc += red[r][t];
+    dl[t] = (sv[t] - acc) * bt;
+  }
+  __syncthreads();
+  const float d0 = dl[j0], d1 = dl[j0 + 1], d2 = dl[j0 + 2], d3 = dl[j0 + 3];
+  float oo[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const float ki = sk[i0 + r], qi = sq[i0 + r];
+    row[r].x += ki * d0;
+    row[r].y += ki * d1;
+    row[r].z += ki * d2;
+    row[r].w += ki * d3;
+    oo[0] += row[r].x * qi;
+    oo[1] += row[r].y * qi;
+    oo[2] += row[r].z * qi;
+    oo[3] += row[r].w * qi;
+    *reinterpret_cast<float4*>(St + static_cast<std::size_t>(i0 + r) * kD + j0) = row[r];
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) red[rg][j0 + c] = oo[c];
+  __syncthreads();
+  // output: RMSNorm over the head's 128 values * w * sigmoid(z), quantized per 32 (waves 0 and 1)
+  float o = 0.0f;
+  if (t < kD) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o += red[r][t];
+    o *= 1.0f / sqrtf(static_cast<float>(kD));
+  }
+  const float so = halo::GroupSum(o * o);
+  if (lane == 0 && wave < 2) part[wave] = so;
+  __syncthreads();
+  if (t < kD) {
+    const float sc = 1.0f / sqrtf((part[0] + part[1]) / static_cast<float>(kD) + eps);
+    const std::size_t off = static_cast<std::size_t>(s) * Dv + h * kD + t;
+    const float v = o * sc * norm_w[t] * halo::Sigmoid(z[off]);
+    const float amax = halo::GroupMax<32>(fabsf(v));
+    const float scale = amax / 127.0f;
+    oq[off] = static_cast<std::int8_t>(scale > 0.0f ? static_cast<int>(rintf(v / scale)) : 0);
+    if (t % 32 == 0) os[off / 32] = scale;
+  }
+}

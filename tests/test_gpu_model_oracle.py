@@ -4,7 +4,8 @@ restatement in tests/model_ref.py, which composes the oracle's primitives the wa
 A twin of C4 (4 layers: 3 DeltaNet + 1 GQA, hidden 1024, 16 experts top-4 + shared, vocab 2048) is stepped on the
 GPU one token at a time (prompt tokens teacher-forced, then greedy) and on the host in lockstep.
 
-Bars: the first step (no recurrent history) within 1e-5 of max|logits|. Every step within 3e-2 of max|logits|
+Bars: the first four steps (history in the recurrent state, the conv ring and the KV cache, no quantizer flip yet
+with this seed) within 1e-5 of max|logits|. Every step within 3e-2 of max|logits|
 and the same produced token unless the host's top two logits are closer than that. The looser bound is the
 Q8 activation quantizers: both paths quantize fp32 rows that differ in the last bits (parallel vs sequential
 sums), so a value sitting on a rounding boundary can land one code apart (measured: 1 in ~200 MoE calls moves a
@@ -46,8 +47,8 @@ def test_decode_steps_match_host_reference(dev):
             scale = float(np.max(np.abs(want)))
             err = float(np.max(np.abs(got - want))) / scale
             worst = max(worst, err)
-            if i == 0:
-                assert err <= 1e-5, f"first step: logits off by {err:.2e} of max|logits|"
+            if i < 4:
+                assert err <= 1e-5, f"step {i}: logits off by {err:.2e} of max|logits|"
             assert err <= 3e-2, f"step {i}: logits off by {err:.2e} of max|logits|"
             top = np.argsort(want)[::-1]
             if int(np.argmax(got)) != int(top[0]):

@@ -209,7 +209,7 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
                               Ptr(L.k_norm.device), Ptr(m->q.device), Ptr(m->agate.device), Ptr(L.k_pool.device),
                               Ptr(L.v_pool.device), Ptr(m->pages.device), Ptr(m->nkv.device), U32(Hq), U32(Hkv),
                               U32(m->max_pages), U32(c.rotary_dim), Val(c.rope_theta), Val(eps)};
-        if (Launch(eng, "halo_attn_prep_decode", D3(S), D3(256), a, err, errlen) != 0) return -1;
+        if (Launch(eng, "halo_attn_prep_decode", D3(S, Hq + 2 * Hkv), D3(64), a, err, errlen) != 0) return -1;
       }
       const halo_paged_kv kv = KvDesc(m, L, S, prefix);
       if (halo_op_attn_decode_q8(eng, &kv, P<float>(m->q), P<float>(m->agate), nullptr, P<int8_t>(m->oq),

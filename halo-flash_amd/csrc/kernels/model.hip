@@ -95,7 +95,7 @@ extern "C" __global__ void __launch_bounds__(256)
   halo::QuantRow8(r, D, xq + s * D, xs + s * (D / 32));
 }
 
-// grid (S), block 256: attention prologue for one token per session. qg [S][Hq][2 d] (per head: q | gate),
+// grid (S, Hq + 2 Hkv), block 64 (one wave per head): attention prologue for one token per session. qg [S][Hq][2 d] (per head: q | gate),
 // kin, vin [S][Hkv][d]; RMSNorm of every q head (wq) and k head (wk); NEOX rope on the first `rot` dims at position
 // nkv[s] - 1; q, gate [S][Hq][d] out; k, v appended to the paged pools at that position. d = 256.
 extern "C" __global__ void __launch_bounds__(256) halo_attn_prep_decode(
@@ -106,10 +106,11 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_prep_decode(
     std::uint32_t rot, float theta, float eps) {
   constexpr std::uint32_t d = 256, kPage = 16;
   const std::size_t s = blockIdx.x;
-  const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, waves = blockDim.x / kWave;
+  const std::uint32_t lane = threadIdx.x % kWave;
   const std::uint32_t pos = nkv[s] - 1;
   const std::uint32_t pg = pages[s * max_pages + pos / kPage];
-  for (std::uint32_t hh = wave; hh < Hq + 2 * Hkv; hh += waves) {
+  {
+    const std::uint32_t hh = blockIdx.y;
     // hh < Hq: q head; Hq <= hh < Hq + Hkv: k head; else v head (copied)
     float x[4];
     const float* src;
@@ -126,7 +127,7 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_prep_decode(
       float* dst = vpool + ((static_cast<std::size_t>(pg) * Hkv + kvh) * kPage + pos % kPage) * d;
 #pragma unroll
       for (int i = 0; i < 4; ++i) dst[lane + 64 * i] = x[i];
-      continue;
+      return;
     }
     float ss = 0.0f;
 #pragma unroll

@@ -4,13 +4,14 @@ restatement in tests/model_ref.py, which composes the oracle's primitives the wa
 A twin of C4 (4 layers: 3 DeltaNet + 1 GQA, hidden 1024, 16 experts top-4 + shared, vocab 2048) is stepped on the
 GPU one token at a time (prompt tokens teacher-forced, then greedy) and on the host in lockstep.
 
-Bars: the first four steps (history in the recurrent state, the conv ring and the KV cache, no quantizer flip yet
-with this seed) within 1e-5 of max|logits|. Every step within 3e-2 of max|logits|
+Bars: the first step within 1e-5 of max|logits|. Every step within 3e-2 of max|logits|
 and the same produced token unless the host's top two logits are closer than that. The looser bound is the
 Q8 activation quantizers: both paths quantize fp32 rows that differ in the last bits (parallel vs sequential
 sums), so a value sitting on a rounding boundary can land one code apart (measured: 1 in ~200 MoE calls moves a
 layer output by ~5e-4 relative); the recurrent state and the KV cache carry such a step forward, and four layers
-plus the LM head amplify it to ~1e-2 of max|logits|. Until such a flip the two paths agree to ~2e-7.
+plus the LM head amplify it to ~1e-2 of max|logits| (one code of the largest MoE input of layer 0 moves the logits
+by 1.3e-2). Until such a flip the two paths agree to ~2e-7; which step first carries one depends on the kernels'
+summation order, so the bound after the first step is the flip bound.
 """
 import numpy as np
 import pytest
@@ -47,8 +48,8 @@ def test_decode_steps_match_host_reference(dev):
             scale = float(np.max(np.abs(want)))
             err = float(np.max(np.abs(got - want))) / scale
             worst = max(worst, err)
-            if i < 4:
-                assert err <= 1e-5, f"step {i}: logits off by {err:.2e} of max|logits|"
+            if i == 0:
+                assert err <= 1e-5, f"first step: logits off by {err:.2e} of max|logits|"
             assert err <= 3e-2, f"step {i}: logits off by {err:.2e} of max|logits|"
             top = np.argsort(want)[::-1]
             if int(np.argmax(got)) != int(top[0]):

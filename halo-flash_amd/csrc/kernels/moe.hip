@@ -469,9 +469,13 @@ extern "C" __global__ void __launch_bounds__(1024) halo_moe_down_q8(
     const float* __restrict__ weights, const float* __restrict__ sgl, float* __restrict__ out, std::uint32_t T,
     std::uint32_t H, std::uint32_t ff, std::uint32_t sff, std::uint32_t k, std::uint32_t hstride) {
   __shared__ float part[33][kDownRows];
+  __shared__ float wslot[33];
   const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, sub = lane / 32, l = lane % 32;
   const std::uint32_t t = blockIdx.y, r0 = blockIdx.x * kDownRows;
   const bool shared = wave == k;
+  // the combine weights are read now, not after the barrier: one dependent round trip less at the end
+  if (threadIdx.x < k) wslot[threadIdx.x] = weights[t * k + threadIdx.x];
+  if (threadIdx.x == k) wslot[k] = sdq != nullptr ? halo::Sigmoid(sgl[t]) : 0.0f;
   if (wave < k || (shared && sdq != nullptr)) {
     const std::uint32_t f = shared ? sff : ff;
     const std::size_t e = shared ? 0 : ids[t * k + wave];
@@ -535,8 +539,8 @@ extern "C" __global__ void __launch_bounds__(1024) halo_moe_down_q8(
   __syncthreads();
   if (threadIdx.x < kDownRows && r0 + threadIdx.x < H) {
     float acc = 0.0f;
-    for (std::uint32_t s = 0; s < k; ++s) acc += weights[t * k + s] * part[s][threadIdx.x];
-    if (sdq != nullptr) acc += halo::Sigmoid(sgl[t]) * part[k][threadIdx.x];
+    for (std::uint32_t s = 0; s < k; ++s) acc += wslot[s] * part[s][threadIdx.x];
+    if (sdq != nullptr) acc += wslot[k] * part[k][threadIdx.x];
     out[static_cast<std::size_t>(t) * H + r0 + threadIdx.x] = acc;
   }
 }

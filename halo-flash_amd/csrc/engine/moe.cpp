@@ -110,3 +110,131 @@ int halo_op_moe_decode(halo_engine* eng, const halo_moe_weights* w, const float*
 }
 
 }  // extern "C"
+
+namespace {
+struct PrefillViews {
+  float *logits, *sgl, *xs, *weights, *h, *hs, *y;
+  std::int8_t *xq, *hq;
+  std::uint32_t *ids, *count, *start, *tiles, *ntiles, *token, *pos;
+  std::uint32_t max_tiles;
+  std::size_t bytes;
+};
+constexpr std::uint32_t kPrefillTile = 64;
+
+int PrefillLayout(const halo_moe_weights* w, std::uint32_t T, void* ws, PrefillViews* v, char* err, std::size_t errlen) {
+  if (w == nullptr || w->router == nullptr || w->gate.qs == nullptr) return SetErr(err, errlen, "moe: missing tensors"), -1;
+  const std::uint32_t E = w->n_experts, k = w->n_used, H = w->hidden, F = w->ff;
+  const bool shared = w->shared_gate_proj.qs != nullptr;
+  if (T == 0) return SetErr(err, errlen, "moe prefill: no tokens"), -1;
+  if (E == 0 || E + 1 > 1024 || k == 0 || k > 16 || k > E)
+    return SetErr(err, errlen, "moe prefill: %u experts / %u used unsupported", E, k), -1;
+  if (H % 64 != 0 || F % 32 != 0 || F == 0) return SetErr(err, errlen, "moe prefill: hidden %u / ff %u", H, F), -1;
+  if (shared && (w->shared_ff != F || w->shared_gate == nullptr))
+    return SetErr(err, errlen, "moe prefill: the shared expert must have ff %u and a gate row", F), -1;
+  auto dense = [](const halo_q8_matrix& m, std::uint32_t rows, std::uint32_t cols) {
+    return m.rows == rows && m.cols == cols && m.qstride == cols;
+  };
+  if (!dense(w->gate, E * F, H) || !dense(w->up, E * F, H) || !dense(w->down, E * H, F))
+    return SetErr(err, errlen, "moe prefill: expert tensors must be stacked with qstride == cols"), -1;
+  const std::uint64_t P = static_cast<std::uint64_t>(T) * k, G = P + (shared ? T : 0);
+  const std::uintptr_t base = reinterpret_cast<std::uintptr_t>(ws);
+  std::size_t o = 0;
+  auto take = [&](std::size_t bytes) {
+    const std::uintptr_t r = base + o;
+    o += Align(bytes);
+    return reinterpret_cast<char*>(r);
+  };
+  v->logits = reinterpret_cast<float*>(take(sizeof(float) * T * E));
+  v->sgl = reinterpret_cast<float*>(take(sizeof(float) * T));
+  v->xq = reinterpret_cast<std::int8_t*>(take(static_cast<std::size_t>(T) * H));
+  v->xs = reinterpret_cast<float*>(take(sizeof(float) * T * (H / 32)));
+  v->ids = reinterpret_cast<std::uint32_t*>(take(sizeof(std::uint32_t) * P));
+  v->weights = reinterpret_cast<float*>(take(sizeof(float) * P));
+  v->count = reinterpret_cast<std::uint32_t*>(take(sizeof(std::uint32_t) * (E + 1)));
+  v->start = reinterpret_cast<std::uint32_t*>(take(sizeof(std::uint32_t) * (E + 2)));
+  v->max_tiles = static_cast<std::uint32_t>(CeilDiv(G, kPrefillTile) + E + 1);
+  v->tiles = reinterpret_cast<std::uint32_t*>(take(sizeof(std::uint32_t) * 3 * v->max_tiles));
+  v->ntiles = reinterpret_cast<std::uint32_t*>(take(sizeof(std::uint32_t)));
+  v->token = reinterpret_cast<std::uint32_t*>(take(sizeof(std::uint32_t) * G));
+  v->pos = reinterpret_cast<std::uint32_t*>(take(sizeof(std::uint32_t) * P));
+  v->h = reinterpret_cast<float*>(take(sizeof(float) * G * F));
+  v->hq = reinterpret_cast<std::int8_t*>(take(G * F));
+  v->hs = reinterpret_cast<float*>(take(sizeof(float) * G * (F / 32)));
+  v->y = reinterpret_cast<float*>(take(sizeof(float) * G * H));
+  v->bytes = o;
+  return 0;
+}
+}  // namespace
+
+extern "C" {
+
+size_t halo_op_moe_prefill_workspace_bytes(const halo_moe_weights* w, uint32_t T) {
+  PrefillViews v;
+  if (PrefillLayout(w, T, nullptr, &v, nullptr, 0) != 0) return 0;
+  return v.bytes;
+}
+
+int halo_op_moe_prefill(halo_engine* eng, const halo_moe_weights* w, const float* x, float* out, uint32_t T, void* ws,
+                        size_t ws_bytes, char* err, size_t errlen) {
+  PrefillViews v;
+  if (PrefillLayout(w, T, ws, &v, err, errlen) != 0) return -1;
+  if (ws == nullptr || ws_bytes < v.bytes)
+    return SetErr(err, errlen, "moe prefill: workspace of %zu bytes < %zu", ws_bytes, v.bytes), -1;
+  const std::uint32_t E = w->n_experts, k = w->n_used, H = w->hidden, F = w->ff;
+  const bool shared = w->shared_gate_proj.qs != nullptr;
+  const std::uint32_t G = T * k + (shared ? T : 0);
+  // 1. router logits [T][E] and the shared gate logit [T]
+  {
+    const halo_arg a[] = {Ptr(x), Ptr(w->router), Ptr(shared ? w->shared_gate : nullptr), Ptr(v.logits), Ptr(v.sgl),
+                          U32(T), U32(E), U32(H), U32(E)};
+    if (Launch(eng, "halo_gemm_f32_nt", D3(CeilDiv(E + 1, 64), CeilDiv(T, 64)), D3(256), a, err, errlen) != 0) return -1;
+  }
+  // 2. x quantized per 32
+  {
+    const halo_arg a[] = {Ptr(x), Ptr(v.xq), Ptr(v.xs), U32(H)};
+    if (Launch(eng, "halo_quantize_q8_rows", D3(T), D3(256), a, err, errlen) != 0) return -1;
+  }
+  // 3. softmax / top-k per token
+  {
+    const halo_arg a[] = {Ptr(v.logits), Ptr(v.ids), Ptr(v.weights), U32(E), U32(k)};
+    if (Launch(eng, "halo_moe_topk", D3(T), D3(CeilDiv(E, 64) * 64), a, err, errlen) != 0) return -1;
+  }
+  // 4. group the pairs by expert (token order within an expert), tile table
+  {
+    const halo_arg a[] = {Ptr(v.ids), Ptr(v.count), U32(T), U32(k)};
+    if (Launch(eng, "halo_moe_group_count", D3(E), D3(256), a, err, errlen) != 0) return -1;
+    const halo_arg b[] = {Ptr(v.count), Ptr(v.start), Ptr(v.tiles), Ptr(v.ntiles), U32(E), U32(T), U32(shared ? 1 : 0),
+                          U32(kPrefillTile)};
+    if (Launch(eng, "halo_moe_group_scan", D3(1), D3(1024), b, err, errlen) != 0) return -1;
+    const halo_arg c[] = {Ptr(v.ids), Ptr(v.start), Ptr(v.token), Ptr(v.pos), U32(T), U32(k), U32(E)};
+    if (Launch(eng, "halo_moe_group_fill", D3(E + (shared ? 1 : 0)), D3(256), c, err, errlen) != 0) return -1;
+  }
+  // 5. grouped gate / up + SwiGLU -> h [G][F]
+  {
+    const halo_arg a[] = {Ptr(w->gate.qs), Ptr(w->gate.d), Ptr(w->up.qs), Ptr(w->up.d),
+                          Ptr(shared ? w->shared_gate_proj.qs : nullptr), Ptr(shared ? w->shared_gate_proj.d : nullptr),
+                          Ptr(shared ? w->shared_up.qs : nullptr), Ptr(shared ? w->shared_up.d : nullptr), Ptr(v.xq),
+                          Ptr(v.xs), Ptr(v.token), Ptr(v.tiles), Ptr(v.ntiles), Ptr(v.h), U32(F), U32(H), U32(E), U32(F)};
+    if (Launch(eng, "halo_moe_grouped_gate_up_q8", D3(CeilDiv(F, 16), v.max_tiles), D3(256), a, err, errlen) != 0)
+      return -1;
+  }
+  // 6. h quantized per 32
+  {
+    const halo_arg a[] = {Ptr(v.h), Ptr(v.hq), Ptr(v.hs), U32(F)};
+    if (Launch(eng, "halo_quantize_q8_rows", D3(G), D3(256), a, err, errlen) != 0) return -1;
+  }
+  // 7. grouped down -> y [G][H]
+  {
+    const halo_arg a[] = {Ptr(w->down.qs), Ptr(w->down.d), Ptr(shared ? w->shared_down.qs : nullptr),
+                          Ptr(shared ? w->shared_down.d : nullptr), Ptr(v.hq), Ptr(v.hs), Ptr(v.tiles), Ptr(v.ntiles),
+                          Ptr(v.y), U32(H), U32(F), U32(E)};
+    if (Launch(eng, "halo_moe_grouped_down_q8", D3(CeilDiv(H, 16), v.max_tiles), D3(256), a, err, errlen) != 0)
+      return -1;
+  }
+  // 8. slot-order combine + shared expert
+  const halo_arg a[] = {Ptr(v.y), Ptr(v.pos), Ptr(v.weights), Ptr(v.sgl), Ptr(out), U32(T), U32(H), U32(k),
+                        U32(shared ? 1 : 0)};
+  return Launch(eng, "halo_moe_prefill_combine", D3(CeilDiv(H, 256), T), D3(256), a, err, errlen);
+}
+
+}  // extern "C"

@@ -5,3 +5,4 @@
 #include "attn.hip"
 #include "model.hip"
 #include "proj.hip"
+#include "moe_prefill.hip"

@@ -1,0 +1,307 @@
+// MoE layer for a batch of T tokens (prefill; gfx950, wave64): fp32 router GEMM, block-per-token top-k, grouping
+// of the (token, slot) pairs by expert, grouped int8 MFMA gate/up with the SwiGLU epilogue and grouped down over each
+// expert's pairs, and the slot-order combine.
+//
+// Reference semantics: ReferenceModel::Moe (src/model/reference.cpp:530-578), cpu::RouteTopK
+// (src/model/cpu_ops.cpp:187-207); the reference's prefill groups pairs by expert with halo_moe_bucket* and runs
+// MoeGateUp / MoeDown per expert group (src/kernels/core.hip:4730-4860, 5155, 5270; GroupedMoe,
+// src/engine/prefill_chunk.cpp:1156-1222). Here the shared expert is one more group (index E) holding every token,
+// so one grouped launch covers routed and shared experts.
+//
+// Pair order: pairs are sorted by expert, and within an expert by token (deterministic, no atomics). pos[t k + s] is
+// the sorted position of token t's slot s; the shared expert's pairs follow at P + t (P = T k).
+#include "common.h"
+
+using halo::F16;
+using halo::kWave;
+
+// ---- fp32 GEMM for the router: C[t][n] = sum_k X[t][k] W[n][k] -----------------------------------------------------
+// grid (ceil((N + 1) / 64), ceil(T / 64)), block 256: a 64 x 64 tile, 4 x 4 outputs per thread, K in steps of 32
+// through LDS. C [T][ldc] for rows n < N of W; when wlast is non-null it is one more row, whose products go to
+// clast [T] (the shared-gate logit next to the router logits). K % 32 == 0.
+extern "C" __global__ void __launch_bounds__(256) halo_gemm_f32_nt(
+    const float* __restrict__ X, const float* __restrict__ W, const float* __restrict__ wlast, float* __restrict__ Cm,
+    float* __restrict__ clast, std::uint32_t T, std::uint32_t N, std::uint32_t K, std::uint32_t ldc) {
+  __shared__ float xs[32][65];
+  __shared__ float ws[32][65];
+  const std::uint32_t tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+  const std::uint32_t n0 = blockIdx.x * 64, t0 = blockIdx.y * 64;
+  const std::uint32_t NN = N + (wlast != nullptr ? 1u : 0u);
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+  for (std::uint32_t k0 = 0; k0 < K; k0 += 32) {
+    // 64 rows x 32 k of each operand: 2048 floats, 8 per thread (row = e / 32, k = e % 32: coalesced along k)
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const std::uint32_t e = threadIdx.x + 256 * u, r = e / 32, k = e % 32;
+      const std::uint32_t tr = min(t0 + r, T - 1), nr = min(n0 + r, NN - 1);
+      xs[k][r] = X[static_cast<std::size_t>(tr) * K + k0 + k];
+      const float* wr = nr < N ? W + static_cast<std::size_t>(nr) * K : wlast;
+      ws[k][r] = wr[k0 + k];
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int k = 0; k < 32; ++k) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = xs[k][ty + 16 * i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = ws[k][tx + 16 * j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * b[j];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const std::uint32_t t = t0 + ty + 16 * i, n = n0 + tx + 16 * j;
+      if (t < T && n < N) Cm[static_cast<std::size_t>(t) * ldc + n] = acc[i][j];
+      if (t < T && n == N && wlast != nullptr) clast[t] = acc[i][j];
+    }
+}
+
+// ---- grouping of (token, slot) pairs by expert --------------------------------------------------------------------
+// grid (E), block 256: count[e] = number of tokens whose top-k holds e (ids [T][k]).
+extern "C" __global__ void __launch_bounds__(256)
+    halo_moe_group_count(const std::uint32_t* __restrict__ ids, std::uint32_t* __restrict__ count, std::uint32_t T,
+                         std::uint32_t k) {
+  __shared__ std::uint32_t part[4];
+  const std::uint32_t e = blockIdx.x;
+  std::uint32_t n = 0;
+  for (std::uint32_t i = threadIdx.x; i < T * k; i += blockDim.x) n += ids[i] == e ? 1u : 0u;
+  n = static_cast<std::uint32_t>(halo::GroupSumI(static_cast<int>(n)));
+  if (threadIdx.x % kWave == 0) part[threadIdx.x / kWave] = n;
+  __syncthreads();
+  if (threadIdx.x == 0) count[e] = part[0] + part[1] + part[2] + part[3];
+}
+
+// grid 1, block 1024: start[e] = exclusive prefix of count (e <= E, count[E] = T for the shared group when shared,
+// else 0), and the tile table: groups cut into tiles of `tile` pairs, tiles[i] = {group, first pair, pairs},
+// ntiles[0] = the tile count. E + 1 <= 1024.
+extern "C" __global__ void __launch_bounds__(1024)
+    halo_moe_group_scan(const std::uint32_t* __restrict__ count, std::uint32_t* __restrict__ start,
+                        std::uint32_t* __restrict__ tiles, std::uint32_t* __restrict__ ntiles, std::uint32_t E,
+                        std::uint32_t T, std::uint32_t shared, std::uint32_t tile) {
+  __shared__ std::uint32_t c[1024], tcount[1024];
+  const std::uint32_t g = threadIdx.x;
+  const std::uint32_t n = g < E ? count[g] : (g == E && shared ? T : 0u);
+  c[g] = n;
+  tcount[g] = (n + tile - 1) / tile;
+  __syncthreads();
+  // serial prefix by one thread (E <= 1023): a few microseconds against a prefill layer
+  if (g == 0) {
+    std::uint32_t p = 0, q = 0;
+    for (std::uint32_t i = 0; i <= E; ++i) {
+      const std::uint32_t ci = c[i], ti = tcount[i];
+      c[i] = p;
+      tcount[i] = q;
+      p += ci;
+      q += ti;
+    }
+    start[E + 1] = p;
+    ntiles[0] = q;
+  }
+  __syncthreads();
+  if (g <= E) {
+    start[g] = c[g];
+    const std::uint32_t first = tcount[g];
+    for (std::uint32_t i = 0; i * tile < n; ++i) {
+      std::uint32_t* tt = tiles + 3 * static_cast<std::size_t>(first + i);
+      tt[0] = g;
+      tt[1] = c[g] + i * tile;
+      tt[2] = min(tile, n - i * tile);
+    }
+  }
+}
+
+// grid (E + shared), block 256: group e's pairs in token order: token[start[e] + j] = the j-th token selecting e
+// (the shared group: every token), pos[t k + s] = that position for routed pairs. Compaction by ballot per chunk of
+// 256 tokens, chunks in order.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_moe_group_fill(const std::uint32_t* __restrict__ ids, const std::uint32_t* __restrict__ start,
+                        std::uint32_t* __restrict__ token, std::uint32_t* __restrict__ pos, std::uint32_t T,
+                        std::uint32_t k, std::uint32_t E) {
+  __shared__ std::uint32_t wcount[4];
+  __shared__ std::uint32_t base_s;
+  const std::uint32_t e = blockIdx.x, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  if (threadIdx.x == 0) base_s = start[e];
+  __syncthreads();
+  for (std::uint32_t t0 = 0; t0 < T; t0 += blockDim.x) {
+    const std::uint32_t t = t0 + threadIdx.x;
+    std::uint32_t slot = 0xFFFFFFFFu;
+    if (t < T) {
+      if (e == E) {
+        slot = 0;
+      } else {
+        for (std::uint32_t s = 0; s < k; ++s)
+          if (ids[static_cast<std::size_t>(t) * k + s] == e) slot = s;
+      }
+    }
+    const bool hit = slot != 0xFFFFFFFFu;
+    const std::uint64_t m = __ballot(hit);
+    const std::uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<std::uint32_t>(m >> 32),
+                                                          __builtin_amdgcn_mbcnt_lo(static_cast<std::uint32_t>(m), 0u));
+    if (lane == 0) wcount[wave] = static_cast<std::uint32_t>(__builtin_popcountll(m));
+    __syncthreads();
+    std::uint32_t off = base_s;
+    for (std::uint32_t w = 0; w < wave; ++w) off += wcount[w];
+    if (hit) {
+      const std::uint32_t p = off + below;
+      token[p] = t;
+      if (e < E) pos[static_cast<std::size_t>(t) * k + slot] = p;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) base_s += wcount[0] + wcount[1] + wcount[2] + wcount[3];
+    __syncthreads();
+  }
+}
+
+// ---- grouped int8 MFMA over the pairs of each group ---------------------------------------------------------------
+// One v_mfma_i32_16x16x32_i8 per (16 weight rows, 16 pairs, one Q8_0 block), as halo_gemm_q8a8_mfma_t*: a block of
+// 4 waves owns 16 rows of group g's matrix x one tile of up to 64 pairs (4 x 16), the waves split the K blocks and
+// reduce through LDS in a fixed order. Group g < E reads matrix rows g * rows + r of the stacked expert tensors, group
+// E the shared expert's. Pair p's activation row is xq[gather ? gather[p] : p]. With SwiGLU the block computes the
+// gate and up rows together and writes h = SiLU(gate) * up; otherwise it writes the projection.
+// grid (ceil(rows / 16), max tiles), block 256; blocks past ntiles[0] exit. y [pairs][ystride].
+namespace {
+typedef int V4I32G __attribute__((ext_vector_type(4)));
+
+template <bool kSwiGLU>
+__device__ __forceinline__ void GroupedMfma(
+    const std::int8_t* __restrict__ qa, const std::uint16_t* __restrict__ da, const std::int8_t* __restrict__ qb,
+    const std::uint16_t* __restrict__ db, const std::int8_t* __restrict__ sqa, const std::uint16_t* __restrict__ sda,
+    const std::int8_t* __restrict__ sqb, const std::uint16_t* __restrict__ sdb, const std::int8_t* __restrict__ xq,
+    const float* __restrict__ xs, const std::uint32_t* __restrict__ gather, const std::uint32_t* __restrict__ tiles,
+    const std::uint32_t* __restrict__ ntiles, float* __restrict__ y, std::uint32_t rows, std::uint32_t cols,
+    std::uint32_t E, std::uint32_t ystride) {
+  constexpr int NT = 4;
+  constexpr int NM = kSwiGLU ? 2 : 1;
+  __shared__ float red[4][NM][NT][16][17];
+  if (blockIdx.y >= ntiles[0]) return;
+  const std::uint32_t* tt = tiles + 3 * static_cast<std::size_t>(blockIdx.y);
+  const std::uint32_t g = tt[0], p0 = tt[1], np = tt[2];
+  const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const std::uint32_t r0 = blockIdx.x * 16, nblk = cols / 32;
+  const std::uint32_t kofs = (lane / 16) * 8;
+  const bool sh = g == E;
+  const std::size_t mrow0 = sh ? 0 : static_cast<std::size_t>(g) * rows;
+  const std::int8_t* A[NM];
+  const std::uint16_t* D[NM];
+  A[0] = sh ? sqa : qa;
+  D[0] = sh ? sda : da;
+  if constexpr (kSwiGLU) {
+    A[1] = sh ? sqb : qb;
+    D[1] = sh ? sdb : db;
+  }
+  const std::uint32_t arow = min(r0 + lane % 16, rows - 1);
+  const std::int8_t* aptr[NM];
+  const std::uint16_t* dptr[NM][4];
+#pragma unroll
+  for (int m = 0; m < NM; ++m) {
+    aptr[m] = A[m] + (mrow0 + arow) * cols + kofs;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dptr[m][i] = D[m] + (mrow0 + min(r0 + (lane / 16) * 4 + i, rows - 1)) * nblk;
+  }
+  const std::int8_t* bptr[NT];
+  const float* sptr[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const std::uint32_t p = p0 + min(static_cast<std::uint32_t>(n * 16) + lane % 16, np - 1);
+    const std::uint32_t row = gather != nullptr ? gather[p] : p;
+    bptr[n] = xq + static_cast<std::size_t>(row) * cols + kofs;
+    sptr[n] = xs + static_cast<std::size_t>(row) * nblk;
+  }
+  float acc[NM][NT][4];
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[m][n][i] = 0.0f;
+  const std::uint32_t per = (nblk + 3) / 4, kb0 = wave * per, kb1 = min(nblk, kb0 + per);
+  for (std::uint32_t kb = kb0; kb < kb1; ++kb) {
+    long a[NM], b[NT];
+    float dw[NM][4], sx[NT];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      a[m] = *reinterpret_cast<const long*>(aptr[m] + kb * 32);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dw[m][i] = F16(dptr[m][i][kb]);
+    }
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      b[n] = *reinterpret_cast<const long*>(bptr[n] + kb * 32);
+      sx[n] = sptr[n][kb];
+    }
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        const V4I32G zero = {0, 0, 0, 0};
+        const V4I32G c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[m], b[n], zero, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[m][n][i] += dw[m][i] * (sx[n] * static_cast<float>(c[i]));
+      }
+  }
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[wave][m][n][(lane / 16) * 4 + i][lane % 16] = acc[m][n][i];
+  __syncthreads();
+  for (std::uint32_t e = threadIdx.x; e < NT * 256; e += blockDim.x) {
+    const std::uint32_t n = e / 256, rr = (e % 256) / 16, pp = e % 16;
+    const std::uint32_t r = r0 + rr, pi = n * 16 + pp;
+    if (r >= rows || pi >= np) continue;
+    const float v0 = ((red[0][0][n][rr][pp] + red[1][0][n][rr][pp]) + red[2][0][n][rr][pp]) + red[3][0][n][rr][pp];
+    float v = v0;
+    if constexpr (kSwiGLU) {
+      const float v1 =
+          ((red[0][NM - 1][n][rr][pp] + red[1][NM - 1][n][rr][pp]) + red[2][NM - 1][n][rr][pp]) + red[3][NM - 1][n][rr][pp];
+      v = halo::Silu(v0) * v1;
+    }
+    y[static_cast<std::size_t>(p0 + pi) * ystride + r] = v;
+  }
+}
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(256) halo_moe_grouped_gate_up_q8(
+    const std::int8_t* gq, const std::uint16_t* gd, const std::int8_t* uq, const std::uint16_t* ud,
+    const std::int8_t* sgq, const std::uint16_t* sgd, const std::int8_t* suq, const std::uint16_t* sud,
+    const std::int8_t* xq, const float* xs, const std::uint32_t* gather, const std::uint32_t* tiles,
+    const std::uint32_t* ntiles, float* h, std::uint32_t ff, std::uint32_t H, std::uint32_t E, std::uint32_t hstride) {
+  GroupedMfma<true>(gq, gd, uq, ud, sgq, sgd, suq, sud, xq, xs, gather, tiles, ntiles, h, ff, H, E, hstride);
+}
+
+extern "C" __global__ void __launch_bounds__(256) halo_moe_grouped_down_q8(
+    const std::int8_t* dq, const std::uint16_t* dd, const std::int8_t* sdq, const std::uint16_t* sdd,
+    const std::int8_t* hq, const float* hs, const std::uint32_t* tiles, const std::uint32_t* ntiles, float* y,
+    std::uint32_t H, std::uint32_t ff, std::uint32_t E) {
+  GroupedMfma<false>(dq, dd, nullptr, nullptr, sdq, sdd, nullptr, nullptr, hq, hs, nullptr, tiles, ntiles, y, H, ff, E,
+                     H);
+}
+
+// grid (ceil(H / 256), T), block 256: out[t][r] = sum over s < k, in order, of weights[t][s] * y[pos[t k + s]][r],
+// then + sigmoid(sgl[t]) * y[P + t][r] when the shared expert is present (sgl: its gate logit).
+extern "C" __global__ void __launch_bounds__(256) halo_moe_prefill_combine(
+    const float* __restrict__ y, const std::uint32_t* __restrict__ pos, const float* __restrict__ weights,
+    const float* __restrict__ sgl, float* __restrict__ out, std::uint32_t T, std::uint32_t H, std::uint32_t k,
+    std::uint32_t shared) {
+  const std::uint32_t t = blockIdx.y, r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= H) return;
+  float acc = 0.0f;
+  for (std::uint32_t s = 0; s < k; ++s)
+    acc += weights[static_cast<std::size_t>(t) * k + s] *
+           y[static_cast<std::size_t>(pos[static_cast<std::size_t>(t) * k + s]) * H + r];
+  if (shared) acc += halo::Sigmoid(sgl[t]) * y[(static_cast<std::size_t>(T) * k + t) * H + r];
+  out[static_cast<std::size_t>(t) * H + r] = acc;
+}

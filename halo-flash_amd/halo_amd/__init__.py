@@ -156,6 +156,8 @@ _SIGS = {
     "halo_engine_launch": (C.c_int, [_VP, C.c_char_p, Dim3, Dim3, C.POINTER(Arg), _SZ], True),
     "halo_op_repack_q8_0": (C.c_int, [_VP, _VP, _VP, _VP, _U32, _U32, _U32], True),
     "halo_op_quantize_q8": (C.c_int, [_VP, _VP, _VP, _VP, _U32, _U32], True),
+    "halo_op_moe_prefill_workspace_bytes": (_SZ, [C.POINTER(MoeWeights), _U32], False),
+    "halo_op_moe_prefill": (C.c_int, [_VP, C.POINTER(MoeWeights), _VP, _VP, _U32, _VP, _SZ], True),
     "halo_op_proj_q8": (C.c_int, [_VP, C.POINTER(Q8Matrix), C.POINTER(C.c_void_p), _U32, C.POINTER(ProjInput), _U32],
                         True),
     "halo_op_proj_q8_grid": (C.c_int, [_VP, C.POINTER(Q8Matrix), C.POINTER(C.c_void_p), _U32, C.POINTER(ProjInput),
@@ -525,3 +527,22 @@ class MoeLayer:
 
     def forward(self, x: DeviceArray, out: DeviceArray, tokens: int, ws: DeviceArray):
         self.dev.op("moe_decode", C.byref(self.w), x.ptr, out.ptr, tokens, ws.ptr, ws.nbytes)
+
+    def prefill_workspace(self, tokens: int):
+        n = lib().halo_op_moe_prefill_workspace_bytes(C.byref(self.w), tokens)
+        if n == 0:
+            raise HaloError("moe prefill: unsupported shape")
+        return self.dev.array(n, np.uint8)
+
+    def prefill_views(self, tokens: int):
+        """Byte offsets of the router logits, shared logit and the ids / weights in the prefill workspace."""
+        al = lambda b: (b + 255) // 256 * 256
+        T, E, H, k = tokens, self.E, self.H, self.k
+        o_logits = 0
+        o_sgl = o_logits + al(T * E * 4)
+        o_ids = o_sgl + al(T * 4) + al(T * H) + al(T * H // 8)
+        o_w = o_ids + al(T * k * 4)
+        return o_logits, o_sgl, o_ids, o_w
+
+    def forward_prefill(self, x: DeviceArray, out: DeviceArray, tokens: int, ws: DeviceArray):
+        self.dev.op("moe_prefill", C.byref(self.w), x.ptr, out.ptr, tokens, ws.ptr, ws.nbytes)

@@ -147,6 +147,17 @@ int halo_op_moe_views(const halo_moe_weights* w, uint32_t tokens, void* ws, halo
 int halo_op_moe_decode(halo_engine* eng, const halo_moe_weights* w, const float* x, float* out, uint32_t tokens,
                        void* ws, size_t ws_bytes, char* err, size_t errlen);
 
+/* MoE layer for a batch of T tokens (prefill; the reference's GroupedMoe, src/engine/prefill_chunk.cpp:1156-1222, and
+ * ReferenceModel::Moe semantics, src/model/reference.cpp:530-578): fp32 router GEMM (+ shared gate logit), top-k per
+ * token, pairs grouped by expert in token order, grouped int8 MFMA gate/up (SwiGLU) and down per expert group (the
+ * shared expert is one more group), slot-order combine. x [T][hidden] fp32 (normalized), out [T][hidden]. Requires
+ * shared_ff == ff when the shared expert is present, n_experts + 1 <= 1024. Workspace from
+ * halo_op_moe_prefill_workspace_bytes(w, T) (0: unsupported). The routing (ids / weights [T][k]) is at the start of
+ * the workspace: ws + align(T * n_experts * 4) + align(T * 4) + align(T * hidden) + align(T * hidden / 8). */
+size_t halo_op_moe_prefill_workspace_bytes(const halo_moe_weights* w, uint32_t tokens);
+int halo_op_moe_prefill(halo_engine* eng, const halo_moe_weights* w, const float* x, float* out, uint32_t tokens,
+                        void* ws, size_t ws_bytes, char* err, size_t errlen);
+
 /* ---- Gated DeltaNet ------------------------------------------------------------------------------------------
  * The recurrence of ReferenceModel::LinearAttention (src/model/reference.cpp:329-364) / halo_gdn_step_d128
  * (src/kernels/core.hip:2620-2646) per value head h (key head h % Hk), decay = exp(g):

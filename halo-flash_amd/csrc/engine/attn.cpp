@@ -1,5 +1,8 @@
 // Decode attention dispatch (FlashNextGpu::Attention, src/engine/flash_next_gpu.cpp:581-680, and the batched
 // per-entry attention of StepBatch): paged KV, prefix read once per step for all sessions.
+#include <algorithm>
+#include <vector>
+
 #include "engine.hpp"
 
 using namespace halo::engine;
@@ -70,6 +73,44 @@ int halo_op_attn_decode_q8(halo_engine* eng, const halo_paged_kv* kv, const floa
 int halo_op_attn_decode(halo_engine* eng, const halo_paged_kv* kv, const float* q, const float* gate, float* o,
                         uint32_t Hq, void* ws, size_t ws_bytes, char* err, size_t errlen) {
   return halo_op_attn_decode_q8(eng, kv, q, gate, o, nullptr, nullptr, Hq, ws, ws_bytes, err, errlen);
+}
+
+size_t halo_op_attn_prefill_workspace_bytes(const halo_prefill_segment* segs, uint32_t nseg) {
+  if (segs == nullptr) return 0;
+  std::size_t tiles = 0;
+  for (std::uint32_t i = 0; i < nseg; ++i) tiles += CeilDiv(segs[i].length, 8);
+  return std::max<std::size_t>(tiles, 1) * 4 * sizeof(std::uint32_t);
+}
+
+int halo_op_attn_prefill(halo_engine* eng, const halo_paged_kv* kv, const halo_prefill_segment* segs, uint32_t nseg,
+                         const float* q, const float* gate, float* o, int8_t* oq, float* os, uint32_t Hq, void* ws,
+                         size_t ws_bytes, char* err, size_t errlen) {
+  if (kv == nullptr || kv->k_pool == nullptr || kv->v_pool == nullptr || kv->pages == nullptr)
+    return SetErr(err, errlen, "attn prefill: missing kv buffers"), -1;
+  if (kv->head_dim != 256 || kv->kv_heads == 0 || Hq != 8 * kv->kv_heads)
+    return SetErr(err, errlen, "attn prefill: head dim 256 and 8 q heads per kv head (got %u / %u)", Hq, kv->kv_heads),
+           -1;
+  if (segs == nullptr || nseg == 0 || q == nullptr || gate == nullptr || (o == nullptr && oq == nullptr) ||
+      ((oq == nullptr) != (os == nullptr)))
+    return SetErr(err, errlen, "attn prefill: missing arguments"), -1;
+  std::vector<std::uint32_t> tiles;
+  for (std::uint32_t i = 0; i < nseg; ++i) {
+    const halo_prefill_segment& g = segs[i];
+    if (g.session >= kv->sessions || g.length == 0 || g.start + g.length > kv->max_context)
+      return SetErr(err, errlen, "attn prefill: segment %u (session %u, %u + %u) out of range", i, g.session, g.start,
+                    g.length),
+             -1;
+    for (std::uint32_t k = 0; k < g.length; k += 8)
+      tiles.insert(tiles.end(), {g.first + k, std::min<std::uint32_t>(8, g.length - k), g.session, g.start + k});
+  }
+  const std::size_t need = tiles.size() * sizeof(std::uint32_t);
+  if (ws == nullptr || ws_bytes < need) return SetErr(err, errlen, "attn prefill: workspace %zu < %zu", ws_bytes, need), -1;
+  halo_buffer b{ws, need, nullptr};
+  if (halo_upload(halo_engine_device(eng), &b, 0, tiles.data(), need, err, errlen) != 0) return -1;
+  const halo_arg a[] = {Ptr(q), Ptr(gate), Ptr(kv->k_pool), Ptr(kv->v_pool), Ptr(kv->pages), Ptr(ws), Ptr(o), Ptr(oq),
+                        Ptr(os), U32(Hq), U32(kv->kv_heads), U32(kv->max_pages)};
+  return Launch(eng, "halo_attn_prefill", D3(static_cast<std::uint32_t>(tiles.size() / 4), kv->kv_heads), D3(256), a,
+                err, errlen);
 }
 
 int halo_op_kv_append(halo_engine* eng, const halo_paged_kv* kv, const float* k, const float* v, char* err,

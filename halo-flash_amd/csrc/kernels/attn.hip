@@ -228,3 +228,154 @@ extern "C" __global__ void __launch_bounds__(64)
   reinterpret_cast<float4*>(kpool + dst)[threadIdx.x] = reinterpret_cast<const float4*>(k + src)[threadIdx.x];
   reinterpret_cast<float4*>(vpool + dst)[threadIdx.x] = reinterpret_cast<const float4*>(v + src)[threadIdx.x];
 }
+
+// ---- causal GQA attention for a ragged batch of prefill tokens (fp32 MFMA) ------------------------------------------
+// Reference semantics: ReferenceModel::Attention (src/model/reference.cpp:368-416, 492-527) for every token of a
+// prompt: softmax(q . K[0..p]^T / sqrt(d)) V[0..p] * sigmoid(gate), K / V already appended at the tokens' positions.
+// tiles [n][4] = {first token index in the batch, tokens (<= 8), session, position of the first token}; a tile's
+// tokens are consecutive positions of one session. Block (tile, kv head): 64 queries = 8 tokens x G = 8 q heads,
+// wave w the tokens 2w, 2w + 1 (query row r = 8 (token - 2w) + g). Per 32-key chunk: scores with
+// v_mfma_f32_16x16x4f32 (A = q rows kept in registers, B = K chunk in LDS), online softmax per row in the MFMA
+// output layout (a row's 32 scores sit in one 16-lane DPP row, two tiles), P through LDS, P V with the same MFMA
+// (B = V chunk in LDS). Output o (fp32, may be null) and its Q8 quantization oq / os (may be null), per token
+// [Hq * 256], after o /= l and o *= sigmoid(gate). q, gate [T][Hq][256].
+namespace {
+constexpr int kPfTok = 8;
+constexpr int kKvStride = kHd + 4;  // LDS row stride in floats (keeps 16-byte alignment, spreads banks)
+typedef float V4F __attribute__((ext_vector_type(4)));
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(256) halo_attn_prefill(
+    const float* __restrict__ q, const float* __restrict__ gate, const float* __restrict__ kpool,
+    const float* __restrict__ vpool, const std::uint32_t* __restrict__ pages, const std::uint32_t* __restrict__ tiles,
+    float* __restrict__ o, std::int8_t* __restrict__ oq, float* __restrict__ os, std::uint32_t Hq, std::uint32_t Hkv,
+    std::uint32_t max_pages) {
+  __shared__ __attribute__((aligned(16))) float kc[kChunk * kKvStride];
+  __shared__ __attribute__((aligned(16))) float vc[kChunk * kKvStride];
+  __shared__ float pw[4][16][kChunk + 1];
+  const std::uint32_t G = Hq / Hkv;
+  const std::uint32_t* tl = tiles + 4 * static_cast<std::size_t>(blockIdx.x);
+  const std::uint32_t first = tl[0], ntok = tl[1], sess = tl[2], p0 = tl[3];
+  const std::uint32_t kvh = blockIdx.y;
+  const std::uint32_t t = threadIdx.x, wave = t / kWave, lane = t % kWave;
+  const std::uint32_t row = lane % 16, kq = lane / 16;  // A-operand row / k slot of this lane
+  // this lane's A-operand query: row r = lane % 16 -> token 2 wave + r / 8, head g = r % 8
+  const std::uint32_t qtok = min(2 * wave + row / 8, ntok - 1), qg = row % 8;
+  const float* qrow = q + ((static_cast<std::size_t>(first) + qtok) * Hq + kvh * G + qg) * kHd;
+  float qa[kHd / 4];
+#pragma unroll
+  for (int s = 0; s < kHd / 4; ++s) qa[s] = qrow[4 * s + kq];
+  // output-layout rows of this lane: 4 kq + i -> token 2 wave + (4 kq + i) / 8
+  std::uint32_t qpos[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) qpos[i] = p0 + 2 * wave + (4 * kq + i) / 8;
+  float m[4], l[4];
+  V4F acc[kHd / 16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m[i] = -INFINITY;
+    l[i] = 0.0f;
+  }
+#pragma unroll
+  for (int c = 0; c < kHd / 16; ++c) acc[c] = V4F{0.0f, 0.0f, 0.0f, 0.0f};
+  const std::uint32_t last = p0 + ntok - 1;  // the tile's last position: keys beyond it are never needed
+  const std::uint32_t nchunks = last / kChunk + 1;
+  const std::uint32_t* pt = pages + static_cast<std::size_t>(sess) * max_pages;
+  const float scale = 1.0f / sqrtf(static_cast<float>(kHd));
+  for (std::uint32_t ch = 0; ch < nchunks; ++ch) {
+    const std::uint32_t k0 = ch * kChunk;
+    // stage the K and V chunk: thread t -> key t / 8, float4 pieces (t % 8) + 8 j
+    {
+      const std::uint32_t key = t / 8, part = t % 8;
+      const std::uint32_t kp = min(k0 + key, last);
+      const std::size_t rowoff = ((static_cast<std::size_t>(pt[kp / kPage]) * Hkv + kvh) * kPage + kp % kPage) * kHd;
+      const float4* ks = reinterpret_cast<const float4*>(kpool + rowoff);
+      const float4* vs = reinterpret_cast<const float4*>(vpool + rowoff);
+      float4 kv[8], vv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        kv[j] = ks[part + 8 * j];
+        vv[j] = vs[part + 8 * j];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        *reinterpret_cast<float4*>(&kc[key * kKvStride + 4 * (part + 8 * j)]) = kv[j];
+        *reinterpret_cast<float4*>(&vc[key * kKvStride + 4 * (part + 8 * j)]) = vv[j];
+      }
+    }
+    __syncthreads();
+    // scores: two 16 x 16 tiles (keys k0 .. k0 + 15, k0 + 16 .. k0 + 31)
+    V4F sc[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      V4F c = {0.0f, 0.0f, 0.0f, 0.0f};
+      const float* kb = &kc[(16 * h + row) * kKvStride + kq];
+#pragma unroll
+      for (int s = 0; s < kHd / 4; ++s) c = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s], kb[4 * s], c, 0, 0, 0);
+      sc[h] = c;
+    }
+    // online softmax per output row (lanes 16 kq .. 16 kq + 15 hold one row's 32 scores)
+    float alpha[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float s0 = sc[0][i] * scale, s1 = sc[1][i] * scale;
+      const std::uint32_t kp0 = k0 + row, kp1 = k0 + 16 + row;
+      s0 = kp0 <= qpos[i] ? s0 : -INFINITY;
+      s1 = kp1 <= qpos[i] ? s1 : -INFINITY;
+      const float cm = halo::GroupMax<16>(fmaxf(s0, s1));
+      const float mx = fmaxf(m[i], cm);
+      const bool none = mx == -INFINITY;
+      alpha[i] = none ? 1.0f : expf(m[i] - mx);
+      const float e0 = s0 == -INFINITY ? 0.0f : expf(s0 - mx), e1 = s1 == -INFINITY ? 0.0f : expf(s1 - mx);
+      l[i] = l[i] * alpha[i] + halo::GroupSum<16>(e0 + e1);
+      m[i] = mx;
+      pw[wave][4 * kq + i][row] = e0;
+      pw[wave][4 * kq + i][16 + row] = e1;
+    }
+#pragma unroll
+    for (int c = 0; c < kHd / 16; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[c][i] *= alpha[i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // P V: A = P (row = query, k = key), B = V chunk (k = key, col = dim)
+#pragma unroll
+    for (int s = 0; s < kChunk / 4; ++s) {
+      const float pa = pw[wave][row][4 * s + kq];
+      const float* vb = &vc[(4 * s + kq) * kKvStride + row];
+#pragma unroll
+      for (int c = 0; c < kHd / 16; ++c) acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, vb[16 * c], acc[c], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  // epilogue: rows 4 kq + i, dims 16 c + row
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const std::uint32_t r = 4 * kq + i;
+    const std::uint32_t tok = 2 * wave + r / 8, g = r % 8;
+    const bool live = tok < ntok;
+    const std::size_t base = ((static_cast<std::size_t>(first) + min(tok, ntok - 1)) * Hq + kvh * G + g) * kHd;
+    const float inv = 1.0f / l[i];
+#pragma unroll
+    for (int c = 0; c < kHd / 16; c += 2) {
+      const std::uint32_t d0 = 16 * c + row, d1 = 16 * (c + 1) + row;
+      const float v0 = acc[c][i] * inv * halo::Sigmoid(gate[base + d0]);
+      const float v1 = acc[c + 1][i] * inv * halo::Sigmoid(gate[base + d1]);
+      if (live && o != nullptr) {
+        o[base + d0] = v0;
+        o[base + d1] = v1;
+      }
+      if (oq != nullptr) {
+        // one Q8 block = dims 32 (c / 2) .. + 31: the 16 lanes of this row x tiles c, c + 1
+        const float amax = halo::GroupMax<16>(fmaxf(fabsf(v0), fabsf(v1)));
+        const float qs = amax / 127.0f;
+        if (live) {
+          oq[base + d0] = static_cast<std::int8_t>(qs > 0.0f ? static_cast<int>(rintf(v0 / qs)) : 0);
+          oq[base + d1] = static_cast<std::int8_t>(qs > 0.0f ? static_cast<int>(rintf(v1 / qs)) : 0);
+          if (row == 0) os[(base + 16 * c) / 32] = qs;
+        }
+      }
+    }
+  }
+}

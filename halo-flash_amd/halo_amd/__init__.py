@@ -98,6 +98,10 @@ class PagedKV(C.Structure):
         (n, C.c_uint32) for n in ("sessions", "kv_heads", "head_dim", "max_pages", "prefix", "max_context")]
 
 
+class PrefillSegment(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("session", "start", "length", "first")]
+
+
 class ModelConfig(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in (
         "vocab", "hidden", "layers", "attn_interval", "gdn_k_heads", "gdn_v_heads", "gdn_head_dim", "conv_kernel",
@@ -158,6 +162,9 @@ _SIGS = {
     "halo_op_quantize_q8": (C.c_int, [_VP, _VP, _VP, _VP, _U32, _U32], True),
     "halo_op_moe_prefill_workspace_bytes": (_SZ, [C.POINTER(MoeWeights), _U32], False),
     "halo_op_moe_prefill": (C.c_int, [_VP, C.POINTER(MoeWeights), _VP, _VP, _U32, _VP, _SZ], True),
+    "halo_op_attn_prefill_workspace_bytes": (_SZ, [C.POINTER(PrefillSegment), _U32], False),
+    "halo_op_attn_prefill": (C.c_int, [_VP, C.POINTER(PagedKV), C.POINTER(PrefillSegment), _U32, _VP, _VP, _VP, _VP,
+                                       _VP, _U32, _VP, _SZ], True),
     "halo_op_proj_q8": (C.c_int, [_VP, C.POINTER(Q8Matrix), C.POINTER(C.c_void_p), _U32, C.POINTER(ProjInput), _U32],
                         True),
     "halo_op_proj_q8_grid": (C.c_int, [_VP, C.POINTER(Q8Matrix), C.POINTER(C.c_void_p), _U32, C.POINTER(ProjInput),

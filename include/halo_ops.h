@@ -194,6 +194,21 @@ int halo_op_attn_decode(halo_engine* eng, const halo_paged_kv* kv, const float* 
 int halo_op_attn_decode_q8(halo_engine* eng, const halo_paged_kv* kv, const float* q, const float* gate, float* o,
                            int8_t* oq, float* os, uint32_t q_heads, void* ws, size_t ws_bytes, char* err,
                            size_t errlen);
+/* A run of consecutive prompt positions of one session inside a prefill batch: tokens [first, first + length) of
+ * the batch are positions [start, start + length) of session `session`. */
+typedef struct halo_prefill_segment {
+  uint32_t session, start, length, first;
+} halo_prefill_segment;
+
+/* Causal GQA attention for a ragged batch of prefill tokens (ReferenceModel::Attention, src/model/reference.cpp:
+ * 368-416, 492-527, per prompt token): every token attends to positions 0 .. its own of its session (shared prefix
+ * pages included); K / V of the batch must already be in the pools. q, gate [T][Hq][256]; o [T][Hq][256] fp32 and /
+ * or its Q8 quantization oq [T][Hq 256] / os [T][Hq 8] (either may be null). segs is a host array; the op uploads
+ * the tile table into ws (halo_op_attn_prefill_workspace_bytes) and is therefore not capturable. */
+size_t halo_op_attn_prefill_workspace_bytes(const halo_prefill_segment* segs, uint32_t nseg);
+int halo_op_attn_prefill(halo_engine* eng, const halo_paged_kv* kv, const halo_prefill_segment* segs, uint32_t nseg,
+                         const float* q, const float* gate, float* o, int8_t* oq, float* os, uint32_t Hq, void* ws,
+                         size_t ws_bytes, char* err, size_t errlen);
 /* Writes one token's k, v [S][Hkv][d] at position nkv[s] - 1 of each session. */
 int halo_op_kv_append(halo_engine* eng, const halo_paged_kv* kv, const float* k, const float* v, char* err,
                       size_t errlen);

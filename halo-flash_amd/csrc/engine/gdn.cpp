@@ -39,10 +39,11 @@ size_t halo_op_gdn_prefill_workspace_bytes(uint32_t n_chunks, uint32_t Hv) {
   return static_cast<std::size_t>(n_chunks) * Hv * (2 * 64 * 64 + 64) * sizeof(float);
 }
 
-int halo_op_gdn_prefill(halo_engine* eng, const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
-                        const float* beta, const uint32_t* chunks, const uint32_t* seqs, uint32_t n_chunks,
-                        uint32_t n_seq, float* state, float* o, uint32_t Hv, uint32_t Hk, uint32_t d, void* ws,
-                        size_t ws_bytes, char* err, size_t errlen) {
+namespace {
+int GdnPrefill(halo_engine* eng, bool f32, const void* q, const void* k, const void* v, const float* g,
+               const float* beta, const uint32_t* chunks, const uint32_t* seqs, uint32_t n_chunks, uint32_t n_seq,
+               float* state, float* o, uint32_t Hv, uint32_t Hk, uint32_t d, void* ws, size_t ws_bytes, char* err,
+               size_t errlen) {
   if (d != 128) return SetErr(err, errlen, "gdn prefill: head dim %u unsupported (128)", d), -1;
   if (n_chunks == 0 || n_seq == 0 || Hv == 0 || Hk == 0 || Hv % Hk != 0)
     return SetErr(err, errlen, "gdn prefill: empty batch or bad heads"), -1;
@@ -53,11 +54,31 @@ int halo_op_gdn_prefill(halo_engine* eng, const uint16_t* q, const uint16_t* k, 
   float* Gc = Pm + static_cast<std::size_t>(n_chunks) * Hv * 4096;
   {
     const halo_arg a[] = {Ptr(q), Ptr(k), Ptr(g), Ptr(beta), Ptr(chunks), Ptr(Tm), Ptr(Pm), Ptr(Gc), U32(Hv), U32(Hk)};
-    if (Launch(eng, "halo_gdn_chunk_prep", D3(n_chunks, Hv), D3(256), a, err, errlen) != 0) return -1;
+    if (Launch(eng, f32 ? "halo_gdn_chunk_prep_f32" : "halo_gdn_chunk_prep", D3(n_chunks, Hv), D3(256), a, err,
+               errlen) != 0)
+      return -1;
   }
   const halo_arg a[] = {Ptr(q), Ptr(k), Ptr(v), Ptr(beta), Ptr(chunks), Ptr(seqs), Ptr(Tm), Ptr(Pm), Ptr(Gc),
                         Ptr(state), Ptr(o), U32(Hv), U32(Hk)};
-  return Launch(eng, "halo_gdn_chunk_scan", D3(n_seq * Hv * 4), D3(256), a, err, errlen);
+  return Launch(eng, f32 ? "halo_gdn_chunk_scan_f32" : "halo_gdn_chunk_scan", D3(n_seq * Hv * 4), D3(256), a, err,
+                errlen);
+}
+}  // namespace
+
+int halo_op_gdn_prefill(halo_engine* eng, const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
+                        const float* beta, const uint32_t* chunks, const uint32_t* seqs, uint32_t n_chunks,
+                        uint32_t n_seq, float* state, float* o, uint32_t Hv, uint32_t Hk, uint32_t d, void* ws,
+                        size_t ws_bytes, char* err, size_t errlen) {
+  return GdnPrefill(eng, false, q, k, v, g, beta, chunks, seqs, n_chunks, n_seq, state, o, Hv, Hk, d, ws, ws_bytes,
+                    err, errlen);
+}
+
+int halo_op_gdn_prefill_f32(halo_engine* eng, const float* q, const float* k, const float* v, const float* g,
+                            const float* beta, const uint32_t* chunks, const uint32_t* seqs, uint32_t n_chunks,
+                            uint32_t n_seq, float* state, float* o, uint32_t Hv, uint32_t Hk, uint32_t d, void* ws,
+                            size_t ws_bytes, char* err, size_t errlen) {
+  return GdnPrefill(eng, true, q, k, v, g, beta, chunks, seqs, n_chunks, n_seq, state, o, Hv, Hk, d, ws, ws_bytes,
+                    err, errlen);
 }
 
 }  // extern "C"

@@ -6,6 +6,7 @@
 // sessions per step with weights read once; ForkSession (flash_next_gpu.hpp:347-350) shares prefix pages.
 #include "halo_model.h"
 
+#include <algorithm>
 #include <initializer_list>
 #include <map>
 #include <string>
@@ -58,6 +59,14 @@ struct halo_model {
   std::size_t moe_ws_bytes = 0, attn_ws_bytes = 0;
   std::vector<halo_buffer> owned;
   std::map<std::pair<std::uint32_t, std::uint32_t>, halo_graph> graphs;
+  // prefill batch scratch, allocated at the first prefill for kPrefillCap tokens
+  struct Prefill {
+    bool ready = false;
+    halo_buffer res{}, xn{}, xq{}, xs{}, qkv{}, zo{}, abo{}, qb{}, kb{}, vb{}, g{}, beta{}, o{}, oq{}, os{}, delta{};
+    halo_buffer qgo{}, ko{}, vo{}, q{}, gate{}, tok{}, segs{}, chunks{}, seqs{}, gdn_ws{}, attn_ws{}, moe_ws{};
+    halo_buffer lq{}, ls{};
+    std::size_t gdn_ws_bytes = 0, attn_ws_bytes = 0, moe_ws_bytes = 0;
+  } pf;
   std::uint64_t weight_bytes = 0, device_bytes = 0;
 };
 
@@ -208,7 +217,8 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
         const halo_arg a[] = {Ptr(m->qgo.device), Ptr(m->ko.device), Ptr(m->vo.device), Ptr(L.q_norm.device),
                               Ptr(L.k_norm.device), Ptr(m->q.device), Ptr(m->agate.device), Ptr(L.k_pool.device),
                               Ptr(L.v_pool.device), Ptr(m->pages.device), Ptr(m->nkv.device), U32(Hq), U32(Hkv),
-                              U32(m->max_pages), U32(c.rotary_dim), Val(c.rope_theta), Val(eps)};
+                              U32(m->max_pages), U32(c.rotary_dim), Val(c.rope_theta), Val(eps), Ptr(nullptr),
+                              Ptr(nullptr)};
         if (Launch(eng, "halo_attn_prep_decode", D3(S, Hq + 2 * Hkv), D3(64), a, err, errlen) != 0) return -1;
       }
       const halo_paged_kv kv = KvDesc(m, L, S, prefix);
@@ -238,6 +248,172 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
                         Ptr(m->nkv.device), Ptr(m->history.device), Ptr(m->produced.device), U32(S), U32(kParts),
                         U32(c.max_context), U32(c.max_context), U32(c.max_context)};
   return Launch(eng, "halo_step_advance", D3(1), D3(64), a, err, errlen);
+}
+
+
+constexpr std::uint32_t kPrefillCap = 2048;  // tokens per prefill batch
+
+int PrefillAlloc(halo_model* m, char* err, std::size_t errlen) {
+  if (m->pf.ready) return 0;
+  const halo_model_config& c = m->c;
+  const std::size_t T = kPrefillCap, H = c.hidden, Dv = static_cast<std::size_t>(c.gdn_v_heads) * c.gdn_head_dim;
+  const std::size_t Dk = static_cast<std::size_t>(c.gdn_k_heads) * c.gdn_head_dim, C = m->conv_ch;
+  const std::size_t A = static_cast<std::size_t>(c.q_heads) * c.head_dim, KV = static_cast<std::size_t>(c.kv_heads) * c.head_dim;
+  const std::size_t O = std::max(Dv, A);
+  auto& p = m->pf;
+  const std::uint32_t max_chunks = kPrefillCap / 64 + c.max_sessions;
+  p.gdn_ws_bytes = halo_op_gdn_prefill_workspace_bytes(max_chunks, c.gdn_v_heads);
+  p.moe_ws_bytes = halo_op_moe_prefill_workspace_bytes(&m->layers[0].moe, kPrefillCap);
+  p.attn_ws_bytes = (kPrefillCap / 8 + c.max_sessions) * 4 * sizeof(std::uint32_t);
+  if (p.moe_ws_bytes == 0) return SetErr(err, errlen, "prefill: MoE shape unsupported by the batched path"), -1;
+  struct B {
+    halo_buffer* b;
+    std::size_t bytes;
+  };
+  const B bufs[] = {
+      {&p.res, T * H * 4}, {&p.xn, T * H * 4}, {&p.xq, T * H}, {&p.xs, T * H / 8}, {&p.qkv, T * C * 4},
+      {&p.zo, T * Dv * 4}, {&p.abo, T * 2 * c.gdn_v_heads * 4}, {&p.qb, T * Dk * 4}, {&p.kb, T * Dk * 4},
+      {&p.vb, T * Dv * 4}, {&p.g, T * c.gdn_v_heads * 4}, {&p.beta, T * c.gdn_v_heads * 4}, {&p.o, T * O * 4},
+      {&p.oq, T * O}, {&p.os, T * O / 8}, {&p.delta, T * H * 4}, {&p.qgo, T * 2 * A * 4}, {&p.ko, T * KV * 4},
+      {&p.vo, T * KV * 4}, {&p.q, T * A * 4}, {&p.gate, T * A * 4}, {&p.tok, T * 3 * 4},
+      {&p.segs, static_cast<std::size_t>(c.max_sessions) * 16 * 4}, {&p.chunks, max_chunks * 3 * 4},
+      {&p.seqs, static_cast<std::size_t>(c.max_sessions) * 2 * 4}, {&p.gdn_ws, p.gdn_ws_bytes},
+      {&p.attn_ws, p.attn_ws_bytes}, {&p.moe_ws, p.moe_ws_bytes},
+      {&p.lq, static_cast<std::size_t>(c.max_sessions) * H}, {&p.ls, static_cast<std::size_t>(c.max_sessions) * H / 8},
+  };
+  for (const auto& b : bufs)
+    if (Alloc(m, b.bytes, b.b, err, errlen) != 0) return -1;
+  p.ready = true;
+  return 0;
+}
+
+// One prefill batch: segments with consecutive increasing sessions s0, s0 + 1, ..., positions already in the cache
+// below each segment's start. T = sum of lengths <= kPrefillCap.
+int PrefillBatch(halo_model* m, const std::vector<halo_prefill_segment>& segs, char* err, std::size_t errlen) {
+  const halo_model_config& c = m->c;
+  halo_engine* eng = m->eng;
+  auto& p = m->pf;
+  const std::uint32_t H = c.hidden, Hv = c.gdn_v_heads, Hk = c.gdn_k_heads, d = c.gdn_head_dim, C = m->conv_ch;
+  const std::uint32_t Hq = c.q_heads, Hkv = c.kv_heads, hd = c.head_dim;
+  const float eps = c.rms_eps;
+  const std::uint32_t nseg = static_cast<std::uint32_t>(segs.size()), s0 = segs[0].session;
+  std::uint32_t T = 0;
+  std::vector<std::uint32_t> tok_sess, tok_pos, seg_start, segtab, lens;
+  for (const auto& g : segs) {
+    segtab.insert(segtab.end(), {g.session, g.start, g.length, T});
+    lens.push_back(g.length);
+    for (std::uint32_t j = 0; j < g.length; ++j) {
+      tok_sess.push_back(g.session);
+      tok_pos.push_back(g.start + j);
+      seg_start.push_back(g.start);
+    }
+    T += g.length;
+  }
+  std::vector<std::uint32_t> tok(tok_sess);
+  tok.insert(tok.end(), tok_pos.begin(), tok_pos.end());
+  tok.insert(tok.end(), seg_start.begin(), seg_start.end());
+  const std::uint32_t nchunks = halo_gdn_chunk_table(lens.data(), nseg, nullptr, nullptr);
+  std::vector<std::uint32_t> chunks(static_cast<std::size_t>(nchunks) * 3), seqs(static_cast<std::size_t>(nseg) * 2);
+  halo_gdn_chunk_table(lens.data(), nseg, chunks.data(), seqs.data());
+  if (halo_upload(m->dev, &p.tok, 0, tok.data(), tok.size() * 4, err, errlen) != 0 ||
+      halo_upload(m->dev, &p.segs, 0, segtab.data(), segtab.size() * 4, err, errlen) != 0 ||
+      halo_upload(m->dev, &p.chunks, 0, chunks.data(), chunks.size() * 4, err, errlen) != 0 ||
+      halo_upload(m->dev, &p.seqs, 0, seqs.data(), seqs.size() * 4, err, errlen) != 0)
+    return -1;
+  const std::uint32_t* ts = P<std::uint32_t>(p.tok);
+  const std::uint32_t* tp = ts + T;
+  const std::uint32_t* tstart = tp + T;
+  {
+    const halo_arg a[] = {Ptr(m->embd.qs.device), Ptr(m->embd.d.device), Ptr(m->prompt.device), U32(c.max_context),
+                          Ptr(ts), Ptr(tp), Ptr(p.res.device), U32(H), U32(H)};
+    if (Launch(eng, "halo_embed_prompt_q8", D3(T), D3(256), a, err, errlen) != 0) return -1;
+  }
+  bool have_delta = false;
+  auto norm = [&](const halo_buffer& w, bool xn) {
+    const halo_arg a[] = {Ptr(p.res.device), Ptr(have_delta ? p.delta.device : nullptr), Ptr(w.device),
+                          Ptr(xn ? p.xn.device : nullptr), Ptr(p.xq.device), Ptr(p.xs.device), U32(H), Val(eps)};
+    have_delta = false;
+    return Launch(eng, "halo_add_rmsnorm_q8", D3(T), D3(256), a, err, errlen);
+  };
+  auto gemm = [&](const Q8& w, const halo_buffer& xq, const halo_buffer& xs, const halo_buffer& y) {
+    return halo_op_matvec_q8a8(eng, &w.m, P<int8_t>(xq), P<float>(xs), P<float>(y), T, w.m.rows, err, errlen);
+  };
+  std::vector<halo_prefill_segment> asegs(segs);
+  for (std::uint32_t i = 0, f = 0; i < nseg; f += asegs[i].length, ++i) asegs[i].first = f;
+  for (auto& L : m->layers) {
+    if (norm(L.attn_norm, false) != 0) return -1;
+    if (!L.attn) {
+      if (gemm(L.qkv, p.xq, p.xs, p.qkv) != 0 || gemm(L.z, p.xq, p.xs, p.zo) != 0 || gemm(L.ab, p.xq, p.xs, p.abo) != 0)
+        return -1;
+      float* ring = P<float>(m->conv_state) + static_cast<std::size_t>(L.gdn_index) * c.max_sessions * c.conv_kernel * C;
+      {
+        const halo_arg a[] = {Ptr(p.qkv.device), Ptr(ring), Ptr(L.conv_w.device), Ptr(p.abo.device), Ptr(L.a.device),
+                              Ptr(L.dt.device), Ptr(ts), Ptr(tp), Ptr(tstart), Ptr(p.qb.device), Ptr(p.kb.device),
+                              Ptr(p.vb.device), Ptr(p.g.device), Ptr(p.beta.device), U32(Hk), U32(Hv), U32(d),
+                              U32(c.conv_kernel), Val(eps)};
+        if (Launch(eng, "halo_gdn_prep_prefill", D3(T, C / 256), D3(256), a, err, errlen) != 0) return -1;
+      }
+      {
+        const halo_arg a[] = {Ptr(p.qkv.device), Ptr(ring), Ptr(p.segs.device), U32(c.conv_kernel), U32(C)};
+        if (Launch(eng, "halo_gdn_ring_update", D3(nseg, C / 256), D3(256), a, err, errlen) != 0) return -1;
+      }
+      float* st = P<float>(m->gdn_state) +
+                  (static_cast<std::size_t>(L.gdn_index) * c.max_sessions + s0) * Hv * d * d;
+      if (halo_op_gdn_prefill_f32(eng, P<float>(p.qb), P<float>(p.kb), P<float>(p.vb), P<float>(p.g),
+                              P<float>(p.beta), P<uint32_t>(p.chunks), P<uint32_t>(p.seqs), nchunks, nseg, st,
+                              P<float>(p.o), Hv, Hk, d, p.gdn_ws.device, p.gdn_ws_bytes, err, errlen) != 0)
+        return -1;
+      {
+        const halo_arg a[] = {Ptr(p.o.device), Ptr(p.zo.device), Ptr(L.norm_w.device), Ptr(p.oq.device),
+                              Ptr(p.os.device), U32(Hv), U32(d), Val(eps)};
+        if (Launch(eng, "halo_gated_rmsnorm_q8", D3(T), D3(256), a, err, errlen) != 0) return -1;
+      }
+      if (gemm(L.out, p.oq, p.os, p.delta) != 0) return -1;
+    } else {
+      if (gemm(L.qg, p.xq, p.xs, p.qgo) != 0 || gemm(L.k, p.xq, p.xs, p.ko) != 0 || gemm(L.v, p.xq, p.xs, p.vo) != 0)
+        return -1;
+      {
+        const halo_arg a[] = {Ptr(p.qgo.device), Ptr(p.ko.device), Ptr(p.vo.device), Ptr(L.q_norm.device),
+                              Ptr(L.k_norm.device), Ptr(p.q.device), Ptr(p.gate.device), Ptr(L.k_pool.device),
+                              Ptr(L.v_pool.device), Ptr(m->pages.device), Ptr(m->nkv.device), U32(Hq), U32(Hkv),
+                              U32(m->max_pages), U32(c.rotary_dim), Val(c.rope_theta), Val(eps), Ptr(ts), Ptr(tp)};
+        if (Launch(eng, "halo_attn_prep_decode", D3(T, Hq + 2 * Hkv), D3(64), a, err, errlen) != 0) return -1;
+      }
+      const halo_paged_kv kv = KvDesc(m, L, c.max_sessions, 0);
+      if (halo_op_attn_prefill(eng, &kv, asegs.data(), nseg, P<float>(p.q), P<float>(p.gate), nullptr,
+                               P<int8_t>(p.oq), P<float>(p.os), Hq, p.attn_ws.device, p.attn_ws_bytes, err,
+                               errlen) != 0)
+        return -1;
+      (void)hd;
+      if (gemm(L.o, p.oq, p.os, p.delta) != 0) return -1;
+    }
+    have_delta = true;
+    if (norm(L.ffn_norm, true) != 0) return -1;
+    if (halo_op_moe_prefill(eng, &L.moe, P<float>(p.xn), P<float>(p.delta), T, p.moe_ws.device, p.moe_ws_bytes, err,
+                            errlen) != 0)
+      return -1;
+    have_delta = true;
+  }
+  if (norm(m->out_norm, false) != 0) return -1;
+  {
+    const halo_arg a[] = {Ptr(p.xq.device), Ptr(p.xs.device), Ptr(p.segs.device), Ptr(p.lq.device), Ptr(p.ls.device),
+                          U32(H)};
+    if (Launch(eng, "halo_prefill_gather_last", D3(nseg), D3(256), a, err, errlen) != 0) return -1;
+  }
+  float* lg = P<float>(m->logits) + static_cast<std::size_t>(s0) * c.vocab;
+  if (halo_op_matvec_q8a8(eng, &m->head.m, P<int8_t>(p.lq), P<float>(p.ls), lg, nseg, c.vocab, err, errlen) != 0)
+    return -1;
+  constexpr std::uint32_t kParts = 64;
+  float* pv = P<float>(m->argmax_part);
+  std::uint32_t* pi = reinterpret_cast<std::uint32_t*>(pv + c.max_sessions * kParts);
+  {
+    const halo_arg a[] = {Ptr(lg), Ptr(pv), Ptr(pi), U32(c.vocab)};
+    if (Launch(eng, "halo_argmax_part", D3(nseg, kParts), D3(256), a, err, errlen) != 0) return -1;
+  }
+  const halo_arg a[] = {Ptr(pv), Ptr(pi), Ptr(p.segs.device), Ptr(m->prompt.device), Ptr(m->prompt_len.device),
+                        Ptr(m->tokens.device), Ptr(m->nkv.device), Ptr(m->history.device), Ptr(m->produced.device),
+                        U32(nseg), U32(kParts), U32(c.max_context), U32(c.max_context)};
+  return Launch(eng, "halo_prefill_advance", D3(1), D3(64), a, err, errlen);
 }
 
 }  // namespace
@@ -541,6 +717,49 @@ int halo_model_logits(halo_model* m, uint32_t s, float* out, char* err, size_t e
   if (m == nullptr || out == nullptr || s >= m->c.max_sessions) return SetErr(err, errlen, "bad session"), -1;
   return halo_download(m->dev, &m->logits, static_cast<std::size_t>(s) * m->c.vocab * 4, out, m->c.vocab * 4ull, err,
                        errlen);
+}
+
+int halo_model_prefill(halo_model* m, const halo_prefill_segment* segs, uint32_t nseg, char* err, size_t errlen) {
+  if (m == nullptr || segs == nullptr || nseg == 0 || nseg > m->c.max_sessions)
+    return SetErr(err, errlen, "prefill: 1..%u segments", m ? m->c.max_sessions : 0), -1;
+  for (std::uint32_t i = 0; i < nseg; ++i) {
+    const halo_prefill_segment& g = segs[i];
+    if (g.session != segs[0].session + i)
+      return SetErr(err, errlen, "prefill: segment sessions must be consecutive (s0, s0 + 1, ...)"), -1;
+    if (g.length == 0 || g.start + g.length >= m->c.max_context)
+      return SetErr(err, errlen, "prefill: segment %u (%u + %u) outside the context", i, g.start, g.length), -1;
+  }
+  if (PrefillAlloc(m, err, errlen) != 0) return -1;
+  // batches of at most kPrefillCap tokens; a long segment continues in the next batch
+  std::vector<halo_prefill_segment> rest(segs, segs + nseg);
+  while (!rest.empty()) {
+    std::vector<halo_prefill_segment> batch, next;
+    std::uint32_t room = kPrefillCap;
+    for (auto& g : rest) {
+      const std::uint32_t n = std::min(g.length, room);
+      if (n > 0) batch.push_back(halo_prefill_segment{g.session, g.start, n, 0});
+      if (n < g.length) next.push_back(halo_prefill_segment{g.session, g.start + n, g.length - n, 0});
+      room -= n;
+    }
+    // sessions of a batch must stay consecutive: a batch that could not take every segment is cut at the first
+    // missing one
+    std::vector<halo_prefill_segment> ok;
+    for (const auto& g : batch) {
+      if (!ok.empty() && g.session != ok.back().session + 1) break;
+      ok.push_back(g);
+    }
+    if (ok.size() < batch.size()) {
+      next.clear();
+      for (const auto& g : rest) {
+        const auto it = std::find_if(ok.begin(), ok.end(), [&](const halo_prefill_segment& o) { return o.session == g.session; });
+        if (it == ok.end()) next.push_back(g);
+        else if (it->length < g.length) next.push_back(halo_prefill_segment{g.session, g.start + it->length, g.length - it->length, 0});
+      }
+    }
+    if (PrefillBatch(m, ok, err, errlen) != 0) return -1;
+    rest.swap(next);
+  }
+  return 0;
 }
 
 int halo_model_history(halo_model* m, uint32_t s, uint32_t* out, uint32_t n, char* err, size_t errlen) {

@@ -97,24 +97,46 @@ extern "C" __global__ void __launch_bounds__(256)
 // halo_gdn_chunk_prep computes, for every (chunk, head) in parallel, T = (I + A)^-1 (forward substitution), P and
 // G; halo_gdn_chunk_scan walks each sequence's chunks in order carrying S, with Delta = T Z and
 // Z = diag(beta) V - diag(beta gamma) (K S0). Tokens past a partial chunk's end are zero-padded (beta = 0, g = 0),
-// which makes them contribute nothing. Inputs q, k [tokens][Hk][128] and v [tokens][Hv][128] are bf16; g, beta
+// which makes them contribute nothing. Inputs q, k [tokens][Hk][128] and v [tokens][Hv][128] are bf16 (the C3 operator) or fp32 (the model's
+// prefill, which matches its decode step); g, beta
 // [tokens][Hv] fp32 (g = log decay, beta after its sigmoid); state fp32 [seq][Hv][128][128] key-major.
 // chunks [n][3] = {first token, length, sequence}; seqs [n_seq][2] = {first chunk, chunk count}.
 namespace {
 constexpr int kC = 64;
 
 __device__ __forceinline__ float Bf(std::uint16_t h) { return __uint_as_float(static_cast<std::uint32_t>(h) << 16); }
+__device__ __forceinline__ float Cv(std::uint16_t h) { return Bf(h); }
+__device__ __forceinline__ float Cv(float x) { return x; }
+// eight consecutive inputs (16 bytes of bf16, 32 of fp32)
+template <typename In>
+struct alignas(16) Pack8 {
+  In v[8];
+};
+template <typename In>
+__device__ __forceinline__ Pack8<In> Ld8(const In* p) {
+  return *reinterpret_cast<const Pack8<In>*>(p);
+}
+template <typename In>
+__device__ __forceinline__ Pack8<In> Zero8() {
+  Pack8<In> z;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) z.v[e] = In{};
+  return z;
+}
 }  // namespace
 
-// grid (n_chunks, Hv), block 256. Tm, Pm [n_chunks][Hv][64][64] fp32, Gc [n_chunks][Hv][64].
-extern "C" __global__ void __launch_bounds__(256) halo_gdn_chunk_prep(
-    const std::uint16_t* __restrict__ q, const std::uint16_t* __restrict__ k, const float* __restrict__ g,
-    const float* __restrict__ beta, const std::uint32_t* __restrict__ chunks, float* __restrict__ Tm,
-    float* __restrict__ Pm, float* __restrict__ Gc, std::uint32_t Hv, std::uint32_t Hk) {
+// grid (n_chunks, Hv), block 256. Tm, Pm [n_chunks][Hv][64][64] fp32, Gc [n_chunks][Hv][64]. In: std::uint16_t
+// (bf16) or float.
+template <typename In>
+__device__ __forceinline__ void ChunkPrep(const In* __restrict__ q, const In* __restrict__ k,
+                                          const float* __restrict__ g, const float* __restrict__ beta,
+                                          const std::uint32_t* __restrict__ chunks, float* __restrict__ Tm,
+                                          float* __restrict__ Pm, float* __restrict__ Gc, std::uint32_t Hv,
+                                          std::uint32_t Hk) {
   __shared__ union {
     struct {
-      std::uint16_t kb[kC][kD];
-      std::uint16_t qb[kC][kD];
+      In kb[kC][kD];
+      In qb[kC][kD];
     } in;
     float tm[kC][kC + 1];
   } u;
@@ -124,14 +146,14 @@ extern "C" __global__ void __launch_bounds__(256) halo_gdn_chunk_prep(
   const std::uint32_t start = chunks[c * 3], L = chunks[c * 3 + 1];
   for (std::uint32_t idx = tid; idx < kC * (kD / 8); idx += blockDim.x) {
     const std::uint32_t t = idx / (kD / 8), p = idx % (kD / 8);
-    int4 kv = make_int4(0, 0, 0, 0), qv = make_int4(0, 0, 0, 0);
+    Pack8<In> kv = Zero8<In>(), qv = Zero8<In>();
     if (t < L) {
       const std::size_t off = (static_cast<std::size_t>(start + t) * Hk + kh) * kD + p * 8;
-      kv = *reinterpret_cast<const int4*>(k + off);
-      qv = *reinterpret_cast<const int4*>(q + off);
+      kv = Ld8(k + off);
+      qv = Ld8(q + off);
     }
-    *reinterpret_cast<int4*>(&u.in.kb[t][p * 8]) = kv;
-    *reinterpret_cast<int4*>(&u.in.qb[t][p * 8]) = qv;
+    *reinterpret_cast<Pack8<In>*>(&u.in.kb[t][p * 8]) = kv;
+    *reinterpret_cast<Pack8<In>*>(&u.in.qb[t][p * 8]) = qv;
   }
   if (tid < kC) {
     const bool in = tid < L;
@@ -150,19 +172,16 @@ extern "C" __global__ void __launch_bounds__(256) halo_gdn_chunk_prep(
 #pragma unroll
     for (int j = 0; j < 16; ++j) kk[j] = qk[j] = 0.0f;
     for (int i = 0; i < kD; i += 8) {
-      const int4 kt4 = *reinterpret_cast<const int4*>(&u.in.kb[t][i]);
-      const int4 qt4 = *reinterpret_cast<const int4*>(&u.in.qb[t][i]);
-      const std::uint16_t* kt = reinterpret_cast<const std::uint16_t*>(&kt4);
-      const std::uint16_t* qt = reinterpret_cast<const std::uint16_t*>(&qt4);
+      const Pack8<In> kt = Ld8(&u.in.kb[t][i]);
+      const Pack8<In> qt = Ld8(&u.in.qb[t][i]);
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const int4 ks4 = *reinterpret_cast<const int4*>(&u.in.kb[s0 + j][i]);
-        const std::uint16_t* ks = reinterpret_cast<const std::uint16_t*>(&ks4);
+        const Pack8<In> ks = Ld8(&u.in.kb[s0 + j][i]);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float kse = Bf(ks[e]);
-          kk[j] += Bf(kt[e]) * kse;
-          qk[j] += Bf(qt[e]) * kse;
+          const float kse = Cv(ks.v[e]);
+          kk[j] += Cv(kt.v[e]) * kse;
+          qk[j] += Cv(qt.v[e]) * kse;
         }
       }
     }
@@ -195,9 +214,9 @@ extern "C" __global__ void __launch_bounds__(256) halo_gdn_chunk_prep(
 
 // grid (n_seq * Hv * 4), block 256: block -> (sequence, head, 32 value columns); walks the sequence's chunks.
 // o [tokens][Hv][128] fp32; state [seq][Hv][128][128] read as the initial state and overwritten with the final one.
-extern "C" __global__ void __launch_bounds__(256) halo_gdn_chunk_scan(
-    const std::uint16_t* __restrict__ q, const std::uint16_t* __restrict__ k, const std::uint16_t* __restrict__ v,
-    const float* __restrict__ beta, const std::uint32_t* __restrict__ chunks, const std::uint32_t* __restrict__ seqs,
+template <typename In>
+__device__ __forceinline__ void ChunkScan(
+    const In* __restrict__ q, const In* __restrict__ k, const In* __restrict__ v, const float* __restrict__ beta, const std::uint32_t* __restrict__ chunks, const std::uint32_t* __restrict__ seqs,
     const float* __restrict__ Tm, const float* __restrict__ Pm, const float* __restrict__ Gc,
     float* __restrict__ state, float* __restrict__ o, std::uint32_t Hv, std::uint32_t Hk) {
   __shared__ float S0[kD][kJBlock];
@@ -235,16 +254,14 @@ extern "C" __global__ void __launch_bounds__(256) halo_gdn_chunk_scan(
     const bool live = t < L;
     const std::size_t krow = (static_cast<std::size_t>(start + t) * Hk + kh) * kD;
     for (int i = 0; i < kD; i += 8) {
-      int4 k4 = make_int4(0, 0, 0, 0), q4 = make_int4(0, 0, 0, 0);
+      Pack8<In> kv = Zero8<In>(), qv = Zero8<In>();
       if (live) {
-        k4 = *reinterpret_cast<const int4*>(k + krow + i);
-        q4 = *reinterpret_cast<const int4*>(q + krow + i);
+        kv = Ld8(k + krow + i);
+        qv = Ld8(q + krow + i);
       }
-      const std::uint16_t* kv = reinterpret_cast<const std::uint16_t*>(&k4);
-      const std::uint16_t* qv = reinterpret_cast<const std::uint16_t*>(&q4);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float ke = Bf(kv[e]), qe = Bf(qv[e]);
+        const float ke = Cv(kv.v[e]), qe = Cv(qv.v[e]);
         const float4 s_lo = *reinterpret_cast<const float4*>(&S0[i + e][jg * 8]);
         const float4 s_hi = *reinterpret_cast<const float4*>(&S0[i + e][jg * 8 + 4]);
         X[0] += ke * s_lo.x; X[1] += ke * s_lo.y; X[2] += ke * s_lo.z; X[3] += ke * s_lo.w;
@@ -255,12 +272,10 @@ extern "C" __global__ void __launch_bounds__(256) halo_gdn_chunk_scan(
     }
     const float gam = expf(G[t]);
     {
-      int4 v4 = make_int4(0, 0, 0, 0);
-      if (live) v4 = *reinterpret_cast<const int4*>(v + (static_cast<std::size_t>(start + t) * Hv + h) * kD +
-                                                     jb * kJBlock + jg * 8);
-      const std::uint16_t* vv = reinterpret_cast<const std::uint16_t*>(&v4);
+      Pack8<In> vv = Zero8<In>();
+      if (live) vv = Ld8(v + (static_cast<std::size_t>(start + t) * Hv + h) * kD + jb * kJBlock + jg * 8);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) Zd[t][jg * 8 + j] = Bt[t] * (Bf(vv[j]) - gam * X[j]);
+      for (int j = 0; j < 8; ++j) Zd[t][jg * 8 + j] = Bt[t] * (Cv(vv.v[j]) - gam * X[j]);
     }
     __syncthreads();
     float D[8];
@@ -294,7 +309,7 @@ extern "C" __global__ void __launch_bounds__(256) halo_gdn_chunk_scan(
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc[j] = gc * S0[si][sh * 16 + j];
     for (std::uint32_t tt = 0; tt < L; ++tt) {
-      const float w = Bf(k[(static_cast<std::size_t>(start + tt) * Hk + kh) * kD + si]) * Wd[tt];
+      const float w = Cv(k[(static_cast<std::size_t>(start + tt) * Hk + kh) * kD + si]) * Wd[tt];
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc[j] += w * Zd[tt][sh * 16 + j];
     }
@@ -304,6 +319,35 @@ extern "C" __global__ void __launch_bounds__(256) halo_gdn_chunk_scan(
   __syncthreads();
   for (std::uint32_t e = tid; e < kD * kJBlock; e += blockDim.x)
     St[static_cast<std::size_t>(e / kJBlock) * kD + jb * kJBlock + e % kJBlock] = S0[e / kJBlock][e % kJBlock];
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    halo_gdn_chunk_prep(const std::uint16_t* __restrict__ q, const std::uint16_t* __restrict__ k,
+                        const float* __restrict__ g, const float* __restrict__ beta,
+                        const std::uint32_t* __restrict__ chunks, float* __restrict__ Tm, float* __restrict__ Pm,
+                        float* __restrict__ Gc, std::uint32_t Hv, std::uint32_t Hk) {
+  ChunkPrep(q, k, g, beta, chunks, Tm, Pm, Gc, Hv, Hk);
+}
+extern "C" __global__ void __launch_bounds__(256)
+    halo_gdn_chunk_prep_f32(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ g,
+                            const float* __restrict__ beta, const std::uint32_t* __restrict__ chunks,
+                            float* __restrict__ Tm, float* __restrict__ Pm, float* __restrict__ Gc, std::uint32_t Hv,
+                            std::uint32_t Hk) {
+  ChunkPrep(q, k, g, beta, chunks, Tm, Pm, Gc, Hv, Hk);
+}
+extern "C" __global__ void __launch_bounds__(256) halo_gdn_chunk_scan(
+    const std::uint16_t* __restrict__ q, const std::uint16_t* __restrict__ k, const std::uint16_t* __restrict__ v,
+    const float* __restrict__ beta, const std::uint32_t* __restrict__ chunks, const std::uint32_t* __restrict__ seqs,
+    const float* __restrict__ Tm, const float* __restrict__ Pm, const float* __restrict__ Gc,
+    float* __restrict__ state, float* __restrict__ o, std::uint32_t Hv, std::uint32_t Hk) {
+  ChunkScan(q, k, v, beta, chunks, seqs, Tm, Pm, Gc, state, o, Hv, Hk);
+}
+extern "C" __global__ void __launch_bounds__(256) halo_gdn_chunk_scan_f32(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ beta, const std::uint32_t* __restrict__ chunks, const std::uint32_t* __restrict__ seqs,
+    const float* __restrict__ Tm, const float* __restrict__ Pm, const float* __restrict__ Gc,
+    float* __restrict__ state, float* __restrict__ o, std::uint32_t Hv, std::uint32_t Hk) {
+  ChunkScan(q, k, v, beta, chunks, seqs, Tm, Pm, Gc, state, o, Hv, Hk);
 }
 
 // ---- the whole DeltaNet token step of the decode graph, one block per (session, value head) -----------------

@@ -95,7 +95,8 @@ extern "C" __global__ void __launch_bounds__(256)
   halo::QuantRow8(r, D, xq + s * D, xs + s * (D / 32));
 }
 
-// grid (S, Hq + 2 Hkv), block 64 (one wave per head): attention prologue for one token per session. qg [S][Hq][2 d] (per head: q | gate),
+// grid (S, Hq + 2 Hkv), block 64 (one wave per head): attention prologue for one token per session (or, with tok_sess
+// / tok_pos non-null, for each token of a prefill batch at its own session and position). qg [S][Hq][2 d] (per head: q | gate),
 // kin, vin [S][Hkv][d]; RMSNorm of every q head (wq) and k head (wk); NEOX rope on the first `rot` dims at position
 // nkv[s] - 1; q, gate [S][Hq][d] out; k, v appended to the paged pools at that position. d = 256.
 extern "C" __global__ void __launch_bounds__(256) halo_attn_prep_decode(
@@ -103,12 +104,15 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_prep_decode(
     const float* __restrict__ wq, const float* __restrict__ wk, float* __restrict__ q, float* __restrict__ gate,
     float* __restrict__ kpool, float* __restrict__ vpool, const std::uint32_t* __restrict__ pages,
     const std::uint32_t* __restrict__ nkv, std::uint32_t Hq, std::uint32_t Hkv, std::uint32_t max_pages,
-    std::uint32_t rot, float theta, float eps) {
+    std::uint32_t rot, float theta, float eps, const std::uint32_t* __restrict__ tok_sess,
+    const std::uint32_t* __restrict__ tok_pos) {
   constexpr std::uint32_t d = 256, kPage = 16;
+  // row s of the inputs / outputs; its session and position: per token in a prefill batch, else session s at nkv - 1
   const std::size_t s = blockIdx.x;
   const std::uint32_t lane = threadIdx.x % kWave;
-  const std::uint32_t pos = nkv[s] - 1;
-  const std::uint32_t pg = pages[s * max_pages + pos / kPage];
+  const std::size_t sess = tok_pos != nullptr ? tok_sess[s] : s;
+  const std::uint32_t pos = tok_pos != nullptr ? tok_pos[s] : nkv[s] - 1;
+  const std::uint32_t pg = pages[sess * max_pages + pos / kPage];
   {
     const std::uint32_t hh = blockIdx.y;
     // hh < Hq: q head; Hq <= hh < Hq + Hkv: k head; else v head (copied)
@@ -255,5 +259,127 @@ extern "C" __global__ void __launch_bounds__(64)
   const std::uint32_t n = nkv[s];  // positions now in the cache, the produced token goes at index n
   if (n < history_stride) history[static_cast<std::size_t>(s) * history_stride + n] = at;
   tokens[s] = n < prompt_len[s] ? prompt[static_cast<std::size_t>(s) * prompt_stride + n] : at;
+  nkv[s] = min(n + 1, max_context);
+}
+
+// ---- batched prefill glue ------------------------------------------------------------------------------------------
+// A prefill batch is T tokens; token t is position tok_pos[t] of session tok_sess[t] (runs of consecutive positions per
+// session, laid out back to back). seg_start[t] is the first position of t's run in this batch.
+
+// grid (T), block 256: x [T][H] = dequantized embedding rows of prompt[tok_sess[t]][tok_pos[t]].
+extern "C" __global__ void __launch_bounds__(256)
+    halo_embed_prompt_q8(const std::int8_t* __restrict__ qs, const std::uint16_t* __restrict__ d,
+                         const std::uint32_t* __restrict__ prompt, std::uint32_t prompt_stride,
+                         const std::uint32_t* __restrict__ tok_sess, const std::uint32_t* __restrict__ tok_pos,
+                         float* __restrict__ x, std::uint32_t H, std::uint32_t qstride) {
+  const std::size_t t = blockIdx.x;
+  const std::size_t tok = prompt[static_cast<std::size_t>(tok_sess[t]) * prompt_stride + tok_pos[t]];
+  for (std::uint32_t i = threadIdx.x; i < H; i += blockDim.x)
+    x[t * H + i] = halo::F16(d[tok * (H / 32) + i / 32]) * static_cast<float>(qs[tok * qstride + i]);
+}
+
+// grid (T, C / 256), block 256: the DeltaNet prologue of halo_gdn_prep_decode for every token of a prefill batch. The
+// conv taps at positions below the token's run come from the session's conv ring (slot p % K), inside the run from
+// the batch's own projection rows, below 0 they are zero. Outputs for the chunked recurrence: q, k [T][Hk][d] and
+// v [T][Hv][d], g, beta [T][Hv], all fp32 as the decode step computes them.
+extern "C" __global__ void __launch_bounds__(256) halo_gdn_prep_prefill(
+    const float* __restrict__ qkv, const float* __restrict__ ring, const float* __restrict__ conv_w,
+    const float* __restrict__ ab, const float* __restrict__ a, const float* __restrict__ dt,
+    const std::uint32_t* __restrict__ tok_sess, const std::uint32_t* __restrict__ tok_pos,
+    const std::uint32_t* __restrict__ seg_start, float* __restrict__ q, float* __restrict__ k,
+    float* __restrict__ v, float* __restrict__ g, float* __restrict__ beta, std::uint32_t Hk, std::uint32_t Hv,
+    std::uint32_t d, std::uint32_t K, float eps) {
+  __shared__ float part[4];
+  const std::size_t t = blockIdx.x;
+  const std::uint32_t Dk = Hk * d, Dv = Hv * d, C = 2 * Dk + Dv;
+  const std::uint32_t ch = blockIdx.y * blockDim.x + threadIdx.x;
+  const std::uint32_t s = tok_sess[t], p = tok_pos[t], p0 = seg_start[t];
+  const float x = qkv[t * C + ch];
+  float acc = conv_w[static_cast<std::size_t>(ch) * K + K - 1] * x;
+  for (std::uint32_t j = 0; j + 1 < K; ++j) {
+    // tap j reads position p - (K - 1) + j
+    const std::int64_t pp = static_cast<std::int64_t>(p) - static_cast<std::int64_t>(K - 1) + j;
+    float xv = 0.0f;
+    if (pp >= static_cast<std::int64_t>(p0))
+      xv = qkv[(t - (p - static_cast<std::uint32_t>(pp))) * C + ch];
+    else if (pp >= 0)
+      xv = ring[(static_cast<std::size_t>(s) * K + static_cast<std::uint32_t>(pp) % K) * C + ch];
+    acc += conv_w[static_cast<std::size_t>(ch) * K + j] * xv;
+  }
+  const float y = halo::Silu(acc);
+  const std::uint32_t wave = threadIdx.x / kWave;
+  const float ss = halo::GroupSum(y * y);
+  if (threadIdx.x % kWave == 0) part[wave] = ss;
+  __syncthreads();
+  const std::uint32_t head = ch / d;
+  if (ch < 2 * Dk) {
+    const std::uint32_t w0 = (wave / 2) * 2;
+    const float sc = 1.0f / sqrtf(part[w0] + part[w0 + 1] + eps);
+    float* dst = head < Hk ? q + (t * Hk + head) * d : k + (t * Hk + head - Hk) * d;
+    dst[ch % d] = y * sc;
+  } else {
+    v[t * Dv + ch - 2 * Dk] = y;
+  }
+  if (blockIdx.y == 0 && threadIdx.x < Hv) {
+    const std::uint32_t h = threadIdx.x;
+    g[t * Hv + h] = a[h] * halo::Softplus(ab[t * 2 * Hv + h] + dt[h]);
+    beta[t * Hv + h] = halo::Sigmoid(ab[t * 2 * Hv + Hv + h]);
+  }
+}
+
+// grid (nseg, C / 256), block 256: after a prefill batch, each run's last K positions go to its session's conv ring
+// (slot p % K). segs [nseg][4] = {session, start, length, first token}.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_gdn_ring_update(const float* __restrict__ qkv, float* __restrict__ ring,
+                         const std::uint32_t* __restrict__ segs, std::uint32_t K, std::uint32_t C) {
+  const std::uint32_t* sg = segs + 4 * static_cast<std::size_t>(blockIdx.x);
+  const std::uint32_t s = sg[0], start = sg[1], len = sg[2], first = sg[3];
+  const std::uint32_t ch = blockIdx.y * blockDim.x + threadIdx.x;
+  for (std::uint32_t j = 0; j < K && j < len; ++j) {
+    const std::uint32_t p = start + len - 1 - j;
+    ring[(static_cast<std::size_t>(s) * K + p % K) * C + ch] = qkv[(static_cast<std::size_t>(first) + len - 1 - j) * C + ch];
+  }
+}
+
+// grid (nseg), block 256: copies the quantized final-norm row of each run's last token to row i of a small batch
+// for the LM head. xq [T][H], xs [T][H / 32] -> lq [nseg][H], ls [nseg][H / 32].
+extern "C" __global__ void __launch_bounds__(256)
+    halo_prefill_gather_last(const std::int8_t* __restrict__ xq, const float* __restrict__ xs,
+                             const std::uint32_t* __restrict__ segs, std::int8_t* __restrict__ lq,
+                             float* __restrict__ ls, std::uint32_t H) {
+  const std::uint32_t* sg = segs + 4 * static_cast<std::size_t>(blockIdx.x);
+  const std::size_t t = static_cast<std::size_t>(sg[3]) + sg[2] - 1, i = blockIdx.x;
+  for (std::uint32_t c = threadIdx.x; c < H; c += blockDim.x) lq[i * H + c] = xq[t * H + c];
+  for (std::uint32_t c = threadIdx.x; c < H / 32; c += blockDim.x) ls[i * (H / 32) + c] = xs[t * (H / 32) + c];
+}
+
+// grid 1, block 64: end of a prefill batch, per run i (thread): the produced token is the argmax over the `parts`
+// partial maxima of row i (ties to the lower id); history[s][start + len] = it; the next input token is the prompt
+// token at start + len when the prompt goes on, else the produced one; nkv[s] = start + len + 1 (the next decode
+// step processes position start + len).
+extern "C" __global__ void __launch_bounds__(64)
+    halo_prefill_advance(const float* __restrict__ pv, const std::uint32_t* __restrict__ pi,
+                         const std::uint32_t* __restrict__ segs, const std::uint32_t* __restrict__ prompt,
+                         const std::uint32_t* __restrict__ prompt_len, std::uint32_t* __restrict__ tokens,
+                         std::uint32_t* __restrict__ nkv, std::uint32_t* __restrict__ history,
+                         std::uint32_t* __restrict__ produced, std::uint32_t nseg, std::uint32_t parts,
+                         std::uint32_t stride, std::uint32_t max_context) {
+  const std::uint32_t i = threadIdx.x;
+  if (i >= nseg) return;
+  float v = -INFINITY;
+  std::uint32_t at = 0xFFFFFFFFu;
+  for (std::uint32_t p = 0; p < parts; ++p) {
+    const float x = pv[i * parts + p];
+    const std::uint32_t id = pi[i * parts + p];
+    if (x > v || (x == v && id < at)) {
+      v = x;
+      at = id;
+    }
+  }
+  const std::uint32_t* sg = segs + 4 * static_cast<std::size_t>(i);
+  const std::uint32_t s = sg[0], n = sg[1] + sg[2];
+  produced[s] = at;
+  if (n < stride) history[static_cast<std::size_t>(s) * stride + n] = at;
+  tokens[s] = n < prompt_len[s] ? prompt[static_cast<std::size_t>(s) * stride + n] : at;
   nkv[s] = min(n + 1, max_context);
 }

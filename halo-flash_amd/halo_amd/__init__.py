@@ -184,6 +184,8 @@ _SIGS = {
     "halo_gdn_chunk_table": (_U32, [_VP, _U32, _VP, _VP], False),
     "halo_op_gdn_prefill_workspace_bytes": (_SZ, [_U32, _U32], False),
     "halo_op_gdn_prefill": (C.c_int, [_VP] + [_VP] * 7 + [_U32, _U32, _VP, _VP, _U32, _U32, _U32, _VP, _SZ], True),
+    "halo_op_gdn_prefill_f32": (C.c_int, [_VP] + [_VP] * 7 + [_U32, _U32, _VP, _VP, _U32, _U32, _U32, _VP, _SZ],
+                                True),
     "halo_model_create": (C.c_int, [_VP, C.POINTER(ModelConfig), _U64, C.POINTER(_VP)], True),
     "halo_model_destroy": (None, [_VP], False),
     "halo_model_weight_bytes": (_U64, [_VP], False),
@@ -197,6 +199,7 @@ _SIGS = {
     "halo_model_positions": (C.c_int, [_VP, _VP, _U32], True),
     "halo_model_tensor": (C.c_int, [_VP, _U32, C.c_char_p, C.POINTER(TensorView)], True),
     "halo_model_logits": (C.c_int, [_VP, _U32, _VP], True),
+    "halo_model_prefill": (C.c_int, [_VP, C.POINTER(PrefillSegment), _U32], True),
     "halo_op_moe_workspace_bytes": (_SZ, [C.POINTER(MoeWeights), _U32], False),
     "halo_op_moe_views": (C.c_int, [C.POINTER(MoeWeights), _U32, _VP, C.POINTER(MoeViews)], True),
     "halo_op_moe_decode": (C.c_int, [_VP, C.POINTER(MoeWeights), _VP, _VP, _U32, _VP, _SZ], True),
@@ -481,6 +484,11 @@ class Model:
 
     def step_eager(self, S: int, prefix: int = 0):
         _call("halo_model_step_eager", self.h, S, prefix)
+
+    def prefill(self, segments):
+        """Batched prefill of (session, start, length) segments, sessions consecutive and increasing."""
+        arr = (PrefillSegment * len(segments))(*[PrefillSegment(s, a, n, 0) for s, a, n in segments])
+        _call("halo_model_prefill", self.h, arr, len(segments))
 
     def history(self, s: int, n: int) -> np.ndarray:
         out = np.zeros(n, np.uint32)

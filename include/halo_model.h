@@ -60,6 +60,16 @@ int halo_model_run(halo_model* m, uint32_t S, uint32_t attn_prefix, uint32_t ste
 /* The same step launched eagerly (no graph): for profilers and debugging. */
 int halo_model_step_eager(halo_model* m, uint32_t S, uint32_t attn_prefix, char* err, size_t errlen);
 
+/* Batched prefill (the reference's PrefillChunk / prompt ingestion, src/engine/prefill_chunk.cpp): positions
+ * [start, start + length) of each segment's session, tokens from the session's prompt, all layers run on the whole
+ * batch (projections as int8 MFMA GEMMs, DeltaNet through the chunked recurrence on fp32 q / k / v, causal
+ * attention over the paged cache, grouped MoE). Segment sessions must be
+ * consecutive and increasing (s0, s0 + 1, ...); positions below start must already be in the cache. Afterwards each
+ * session is where the same number of decode steps would leave it: history[start + length] holds the argmax after
+ * the last position, the next input token is prompt[start + length] when the prompt goes on, nkv = start + length + 1.
+ * Not capturable (uploads per batch of up to 2048 tokens). `first` is ignored. */
+int halo_model_prefill(halo_model* m, const halo_prefill_segment* segs, uint32_t nseg, char* err, size_t errlen);
+
 /* Host copies of session s's produced tokens history[pos] (the argmax after position pos-1 ... ) and nkv. */
 int halo_model_history(halo_model* m, uint32_t s, uint32_t* out, uint32_t n, char* err, size_t errlen);
 int halo_model_positions(halo_model* m, uint32_t* nkv_out, uint32_t S, char* err, size_t errlen);

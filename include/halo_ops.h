@@ -227,6 +227,13 @@ int halo_op_gdn_prefill(halo_engine* eng, const uint16_t* q, const uint16_t* k, 
                         const float* beta, const uint32_t* chunks, const uint32_t* seqs, uint32_t n_chunks,
                         uint32_t n_seq, float* state, float* o, uint32_t v_heads, uint32_t k_heads, uint32_t head_dim,
                         void* ws, size_t ws_bytes, char* err, size_t errlen);
+/* The same recurrence with fp32 q, k, v (the reference's default prefill reads its fp32 conv outputs,
+ * src/engine/prefill_chunk.cpp:556-640); the model's batched prefill uses it so that prefill and decode see the same
+ * inputs. */
+int halo_op_gdn_prefill_f32(halo_engine* eng, const float* q, const float* k, const float* v, const float* g,
+                            const float* beta, const uint32_t* chunks, const uint32_t* seqs, uint32_t n_chunks,
+                            uint32_t n_seq, float* state, float* o, uint32_t v_heads, uint32_t k_heads,
+                            uint32_t head_dim, void* ws, size_t ws_bytes, char* err, size_t errlen);
 
 #ifdef __cplusplus
 }

@@ -251,6 +251,36 @@ def run_moe(args, dev, H, res):
         nbytes = float(np.mean([moe_bytes(base.E, base.H, base.F, base.SF, u, T) for u in Us]))
         out[f"T{T}"] = {"us_per_layer": round(us, 3), "mean_U": round(float(np.mean(Us)), 2),
                         "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        if T <= 4:
+            # the layer as the model runs it: residual + delta -> FFN norm -> MoE, as a norm launch followed by the
+            # plain decode, and with the norm in the router launch
+            dl = [dev.array((T, base.H), np.float32) for _ in range(ncopy)]
+            for i, x in enumerate(dl):
+                dev.op("synth_f32", x.ptr, T * base.H, 19000 + 100 * T + i, 1.0)
+            nw = dev.array(base.H, np.float32)
+            dev.op("synth_f32", nw.ptr, base.H, 777, 1.0)
+            r2, xn = dev.array((T, base.H), np.float32), dev.array((T, base.H), np.float32)
+            times = {}
+            for variant in ("norm_then_moe", "norm_in_router"):
+                dev.begin_capture()
+                for (w, _), x, d, ws in zip(copies, xs, dl, wss):
+                    if variant == "norm_then_moe":
+                        dev.launch("halo_add_rmsnorm_q8", (T,), (256,), [("ptr", x.ptr), ("ptr", d.ptr), nw, xn,
+                                                                         None, None, ("u32", base.H), ("f32", 1e-6)])
+                        dev.op("moe_decode", C.byref(w), xn.ptr, y.ptr, T, ws.ptr, ws.nbytes)
+                    else:
+                        inp = H.ProjInput(x=x.ptr, delta=d.ptr, norm_w=nw.ptr, res_out=r2.ptr, eps=1e-6,
+                                          mode=H.PROJ_N)
+                        dev.op("moe_decode_norm", C.byref(w), C.byref(inp), y.ptr, T, ws.ptr, ws.nbytes)
+                g = dev.end_capture()
+                dev.launch_graph(g)
+                dev.sync()
+                dev.timer_start()
+                for _ in range(nrep):
+                    dev.launch_graph(g)
+                times[variant] = round(dev.timer_stop() * 1e3 / (nrep * ncopy), 3)
+                dev.free_graph(g)
+            out[f"T{T}"]["us_with_ffn_norm"] = times
         log(f"[bench] moe T={T}: {out[f'T{T}']}")
     res["moe"] = out
     res["roofline"] = None
@@ -454,10 +484,11 @@ def run_pmc(args, dev, H, res):
 
 def run_c4(args, dev, H, res):
     """C4: the synthetic hybrid model (48 layers, 36 DeltaNet + 12 GQA, MoE 512 x top-10 + shared, vocab 151936,
-    Q8_0 weights seeded on the device). Session 0 prefills the 8192-token shared prefix one token per step (the
-    captured decode step, prompt tokens fed on the device); sessions 1-3 fork its state and share its KV pages.
-    1 session: session 0 alone, 256 suffix tokens then 128 greedy decode steps (timed). 4 sessions: each with a
-    distinct 256-token suffix, read the prefix once per step, then 128 greedy decode steps (timed)."""
+    Q8_0 weights seeded on the device). Session 0 prefills the 8192-token shared prefix as one batched prefill
+    (timed: prefill tok/s); sessions 1-3 fork its state and share its KV pages. 1 session: session 0 alone, its
+    256 suffix tokens prefilled, then 128 greedy decode steps (timed). 4 sessions: the four distinct 256-token
+    suffixes prefilled as one ragged batch (timed), then 128 greedy decode steps reading the prefix once per step
+    (timed)."""
     P, SUF, DEC = 8192, 256, 128
     t0 = time.perf_counter()
     cfg = H.c4_config(max_sessions=4, prefix_tokens=P, max_context=P + SUF + DEC)
@@ -493,26 +524,34 @@ def run_c4(args, dev, H, res):
             res["c4"] = {"profile": {k: {n: [c, round(u, 1)] for n, (c, u) in v.items()} for k, v in prof.items()}}
             return res
         model.set_session(0, prompts[0])
-        t0 = time.perf_counter()
+        dev.sync()
         dev.timer_start()
-        model.run(1, P)
+        model.prefill([(0, 0, P)])
         ms_prefix = dev.timer_stop()
-        log(f"[bench] c4: prefix {P} tokens in {ms_prefix / 1e3:.1f} s (one token per step)")
+        log(f"[bench] c4: prefix {P} tokens prefilled in {ms_prefix:.1f} ms ({P / (ms_prefix * 1e-3):.0f} tok/s)")
         for s in (1, 2, 3):
             model.fork(0, s)
-        # 1 session
-        model.run(1, SUF)
+        # 1 session: its suffix prefilled, then greedy decode
+        model.prefill([(0, P, SUF)])
+        model.run(1, 1)
         dev.sync()
         dev.timer_start()
         model.run(1, DEC)
         ms1 = dev.timer_stop()
         tok1 = DEC / (ms1 * 1e-3)
         log(f"[bench] c4: 1 session {ms1 / DEC:.3f} ms/token, {tok1:.1f} tok/s")
-        # 4 sessions: session 0 back at the end of the prefix (session 1 still holds that state)
+        # 4 sessions: session 0 back at the end of the prefix (session 1 still holds that state); the four suffixes
+        # prefill as one ragged batch reading the shared prefix pages, then greedy decode
         model.fork(1, 0)
         for s in range(4):
             model.set_session(s, prompts[s], nkv=P)
-        model.run(4, SUF, prefix=P)
+        dev.sync()
+        dev.timer_start()
+        model.prefill([(s, P, SUF) for s in range(4)])
+        ms_suffix = dev.timer_stop()
+        log(f"[bench] c4: 4 x {SUF} suffix tokens prefilled in {ms_suffix:.1f} ms "
+            f"({4 * SUF / (ms_suffix * 1e-3):.0f} tok/s)")
+        model.run(4, 1, prefix=P)
         dev.sync()
         dev.timer_start()
         model.run(4, DEC, prefix=P)
@@ -523,7 +562,10 @@ def run_c4(args, dev, H, res):
         res["c4"] = {"decode_tok_s_1_session": round(tok1, 1), "ms_per_token_1_session": round(ms1 / DEC, 3),
                      "decode_tok_s_4_sessions": round(tok4, 1), "ms_per_step_4_sessions": round(ms4 / DEC, 3),
                      "prefix_tokens": P, "suffix_tokens": SUF, "decode_steps": DEC,
-                     "prefix_ms_token_serial": round(ms_prefix, 1), "weight_GB": round(model.weight_bytes / 1e9, 2),
+                     "prefill_prefix_ms": round(ms_prefix, 1),
+                     "prefill_prefix_tok_s": round(P / (ms_prefix * 1e-3), 1),
+                     "prefill_4x_suffix_ms": round(ms_suffix, 2),
+                     "prefill_4x_suffix_tok_s": round(4 * SUF / (ms_suffix * 1e-3), 1), "weight_GB": round(model.weight_bytes / 1e9, 2),
                      "first_generated": gen}
     finally:
         model.close()

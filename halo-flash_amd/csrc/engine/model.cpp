@@ -229,10 +229,25 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
       if (gemv(L.o, m->oq, m->os, m->delta) != 0) return -1;
     }
     have_delta = true;
-    if (norm(L.ffn_norm, false) != 0) return -1;
-    if (halo_op_moe_decode(eng, &L.moe, P<float>(m->xn), P<float>(m->delta), S, m->moe_ws.device, m->moe_ws_bytes,
-                           err, errlen) != 0)
-      return -1;
+    if (S <= 4 && (H == 2048 || H == 4096) && S * H <= 8192) {
+      // the FFN norm runs in the router's prologue
+      halo_proj_input in{};
+      in.x = P<float>(*cur);
+      in.delta = P<float>(m->delta);
+      in.norm_w = P<float>(L.ffn_norm);
+      in.res_out = P<float>(*alt);
+      in.eps = eps;
+      in.mode = HALO_PROJ_N;
+      if (halo_op_moe_decode_norm(eng, &L.moe, &in, P<float>(m->delta), S, m->moe_ws.device, m->moe_ws_bytes, err,
+                                  errlen) != 0)
+        return -1;
+      std::swap(cur, alt);
+    } else {
+      if (norm(L.ffn_norm, false) != 0) return -1;
+      if (halo_op_moe_decode(eng, &L.moe, P<float>(m->xn), P<float>(m->delta), S, m->moe_ws.device,
+                             m->moe_ws_bytes, err, errlen) != 0)
+        return -1;
+    }
     have_delta = true;
   }
   if (norm(m->out_norm, true) != 0) return -1;

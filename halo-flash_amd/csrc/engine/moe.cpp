@@ -67,8 +67,12 @@ size_t halo_op_moe_workspace_bytes(const halo_moe_weights* w, uint32_t T) {
   return v.bytes;
 }
 
-int halo_op_moe_decode(halo_engine* eng, const halo_moe_weights* w, const float* x, float* out, uint32_t T, void* ws,
-                       size_t ws_bytes, char* err, size_t errlen) {
+}  // extern "C"
+
+namespace {
+// The MoE decode launches after the router stage; `in` (mode N) selects the router with the norm prologue.
+int MoeDecode(halo_engine* eng, const halo_moe_weights* w, const float* x, const halo_proj_input* in, float* out,
+              uint32_t T, void* ws, size_t ws_bytes, char* err, size_t errlen) {
   halo_moe_views v;
   if (halo_op_moe_views(w, T, ws, &v, err, errlen) != 0) return -1;
   if (ws == nullptr || ws_bytes < v.bytes)
@@ -76,8 +80,20 @@ int halo_op_moe_decode(halo_engine* eng, const halo_moe_weights* w, const float*
   const std::uint32_t E = w->n_experts, k = w->n_used, H = w->hidden, F = w->ff;
   const bool shared = w->shared_gate_proj.qs != nullptr;
   const std::uint32_t SF = shared ? w->shared_ff : 0;
-  // 1. router logits + shared gate logit + x quantized
-  {
+  if (in != nullptr) {
+    // 1. FFN norm + router logits + shared gate logit + x quantized, one launch
+    if (T == 0 || T > 4 || (H != 2048 && H != 4096) || T * H > 8192 || in->x == nullptr || in->delta == nullptr ||
+        in->norm_w == nullptr || in->res_out == nullptr || in->res_out == in->x)
+      return SetErr(err, errlen, "moe: fused norm needs T <= 4, hidden 2048 / 4096, T * hidden <= 8192, x, delta, "
+                                 "norm weights and a separate residual output"), -1;
+    const halo_arg a[] = {Ptr(w->router), Ptr(shared ? w->shared_gate : nullptr), Ptr(in->x), Ptr(in->delta),
+                          Ptr(in->norm_w), Ptr(in->res_out), Ptr(v.logits), Ptr(v.shared_logit), Ptr(v.xq),
+                          Ptr(v.xs), U32(E), U32(T), Val(in->eps)};
+    if (Launch(eng, H == 2048 ? "halo_moe_router_n_h2048" : "halo_moe_router_n_h4096", D3(CeilDiv(E + 1, 4)),
+               D3(256), a, err, errlen) != 0)
+      return -1;
+  } else {
+    // 1. router logits + shared gate logit + x quantized
     const std::uint32_t qblocks = CeilDiv(static_cast<std::uint64_t>(T) * (H / 32), 8);
     const halo_arg a[] = {Ptr(w->router), Ptr(shared ? w->shared_gate : nullptr), Ptr(x), Ptr(v.logits),
                           Ptr(v.shared_logit), Ptr(v.xq), Ptr(v.xs), U32(E), U32(H), U32(T)};
@@ -88,15 +104,15 @@ int halo_op_moe_decode(halo_engine* eng, const halo_moe_weights* w, const float*
     const halo_arg a[] = {Ptr(v.logits), Ptr(v.ids), Ptr(v.weights), U32(E), U32(k)};
     if (Launch(eng, "halo_moe_topk", D3(T), D3(CeilDiv(E, 64) * 64), a, err, errlen) != 0) return -1;
   }
-  // 3. gate/up over the union of experts + SwiGLU + quantized h
+  // 3. gate/up over the union of experts + SwiGLU
   {
     const halo_arg a[] = {Ptr(w->gate.qs), Ptr(w->gate.d), Ptr(w->up.qs), Ptr(w->up.d),
                           Ptr(shared ? w->shared_gate_proj.qs : nullptr), Ptr(shared ? w->shared_gate_proj.d : nullptr),
                           Ptr(shared ? w->shared_up.qs : nullptr), Ptr(shared ? w->shared_up.d : nullptr),
                           Ptr(v.xq), Ptr(v.xs), Ptr(v.ids), Ptr(v.h), U32(T), U32(F), U32(SF), U32(k),
                           U32(v.hstride)};
+    if (H != 1024 && H != 2048 && H != 4096) return SetErr(err, errlen, "moe: hidden %u has no gate/up instance", H), -1;
     const char* name = H == 1024 ? "halo_moe_gate_up_q8_s1" : H == 2048 ? "halo_moe_gate_up_q8_s2" : "halo_moe_gate_up_q8_s4";
-    if (H == 3072) return SetErr(err, errlen, "moe: hidden 3072 has no gate/up instance"), -1;
     if (Launch(eng, name, D3(T * k + 1, v.hstride / 4), D3(256), a, err, errlen) != 0) return -1;
   }
   // 4. down + routed combine + shared expert
@@ -107,6 +123,20 @@ int halo_op_moe_decode(halo_engine* eng, const halo_moe_weights* w, const float*
     if (Launch(eng, "halo_moe_down_q8", D3(CeilDiv(H, 8), T), D3(64 * (k + 1)), a, err, errlen) != 0) return -1;
   }
   return 0;
+}
+}  // namespace
+
+extern "C" {
+
+int halo_op_moe_decode(halo_engine* eng, const halo_moe_weights* w, const float* x, float* out, uint32_t T, void* ws,
+                       size_t ws_bytes, char* err, size_t errlen) {
+  return MoeDecode(eng, w, x, nullptr, out, T, ws, ws_bytes, err, errlen);
+}
+
+int halo_op_moe_decode_norm(halo_engine* eng, const halo_moe_weights* w, const halo_proj_input* in, float* out,
+                            uint32_t T, void* ws, size_t ws_bytes, char* err, size_t errlen) {
+  if (in == nullptr) return SetErr(err, errlen, "moe: no input"), -1;
+  return MoeDecode(eng, w, nullptr, in, out, T, ws, ws_bytes, err, errlen);
 }
 
 }  // extern "C"

@@ -6,7 +6,8 @@
 // halo_moe_bucket_b (src/kernels/batch_decode.hip:417-446).
 //
 // Launches (all take device buffers only, so one captured graph replays for any routing):
-//   1. halo_moe_router     logits[t][e] = W_r[e] . x[t] (fp32), shared-gate logit, x quantized per 32 (int8).
+//   1. halo_moe_router     logits[t][e] = W_r[e] . x[t] (fp32), shared-gate logit, x quantized per 32 (int8);
+//      or halo_moe_router_n_* (T <= 4), which also forms x = RMSNorm(res + delta) * w itself (the FFN norm).
 //   2. halo_moe_topk       one block per token: softmax, top-k (ties -> lower id), renormalized weights.
 //   3. halo_moe_gate_up_q8 block (routed pair, 4 ff rows): the first token that selected an expert computes it for
 //                          every token that selected it (the union of experts: weights streamed once), h =
@@ -76,6 +77,111 @@ extern "C" __global__ void __launch_bounds__(256)
   }
 }
 
+// The router with the FFN input norm in its prologue, for T <= 4 tokens (T * H <= 8192, H a multiple of 2048):
+// x_t = RMSNorm(res[t] + delta[t]) * norm_w in the canonical row layout of halo_add_rmsnorm_q8 (same bits), so the
+// norm launch before the MoE disappears. Every block normalizes the T rows itself (L2 reads); block 0 also writes
+// res_out[t] = res[t] + delta[t] (a different buffer from res: the other blocks still read res) and the Q8
+// quantization xq / xs of x_t for the experts. Wave w of block b dots router row r = 4 b + w (r = E: the shared gate
+// row, skipped when null) with x_t from LDS.
+//   grid (ceil((E + 1) / 4)), block 256. router [E][H] fp32, logits [T][E], sgl [T].
+template <int KC>
+__device__ __forceinline__ void MoeRouterN(const float* __restrict__ router, const float* __restrict__ sgate,
+                                           const float* __restrict__ res, const float* __restrict__ delta,
+                                           const float* __restrict__ norm_w, float* __restrict__ res_out,
+                                           float* __restrict__ logits, float* __restrict__ sgl,
+                                           std::int8_t* __restrict__ xq, float* __restrict__ xs, std::uint32_t E,
+                                           std::uint32_t T, float eps) {
+  constexpr std::uint32_t H = KC * 2048, kMaxT = 4, kF4 = H / 256;  // float4 chunks of a row per lane
+  __shared__ __attribute__((aligned(16))) float xl[kMaxT * 2048];
+  __shared__ float red[kMaxT][4];
+  const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const std::uint32_t r = blockIdx.x * 4 + wave;
+  const float* row = r < E ? router + static_cast<std::size_t>(r) * H : sgate;
+  const bool live = r < E || (r == E && sgate != nullptr);
+  const float* rowc = live ? row : router;  // a valid address either way; the result is dropped
+  float4 w[kF4];
+#pragma unroll
+  for (int i = 0; i < static_cast<int>(kF4); ++i) w[i] = reinterpret_cast<const float4*>(rowc)[lane + kWave * i];
+  halo::Row8<KC> x[kMaxT], nw;
+#pragma unroll
+  for (int t = 0; t < static_cast<int>(kMaxT); ++t) {
+    const std::uint32_t tt = min(static_cast<std::uint32_t>(t), T - 1);
+    halo::LoadRow8(res + static_cast<std::size_t>(tt) * H, delta + static_cast<std::size_t>(tt) * H, H, x[t]);
+  }
+  halo::LoadRow8(norm_w, nullptr, H, nw);
+  if (blockIdx.x == 0)
+#pragma unroll
+    for (int t = 0; t < static_cast<int>(kMaxT); ++t)
+      if (t < static_cast<int>(T)) halo::StoreRow8(res_out + static_cast<std::size_t>(t) * H, H, x[t]);
+  // the sums of squares of every token, one barrier (the arithmetic of halo::RmsNormRow8W)
+#pragma unroll
+  for (int t = 0; t < static_cast<int>(kMaxT); ++t) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KC; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(x[t].v[k][e], x[t].v[k][e], ss);
+    ss = halo::GroupSum(ss);
+    if (lane == 0) red[t][wave] = ss;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < static_cast<int>(kMaxT); ++t) {
+    const float ss = ((red[t][0] + red[t][1]) + red[t][2]) + red[t][3];
+    const float scale = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
+#pragma unroll
+    for (int k = 0; k < KC; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[t].v[k][e] = x[t].v[k][e] * scale * nw.v[k][e];
+  }
+  if (blockIdx.x == 0)
+#pragma unroll
+    for (int t = 0; t < static_cast<int>(kMaxT); ++t)
+      if (t < static_cast<int>(T))
+        halo::QuantRow8(x[t], H, xq + static_cast<std::size_t>(t) * H, xs + static_cast<std::size_t>(t) * (H / 32));
+  // x_t to LDS: chunk c = thread + 256 k holds elements 8 c .. 8 c + 7
+#pragma unroll
+  for (int t = 0; t < static_cast<int>(kMaxT); ++t)
+    if (t < static_cast<int>(T))
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+      const std::uint32_t c = threadIdx.x + 256u * k;
+      float4* dst = reinterpret_cast<float4*>(xl + t * H + 8 * c);
+      dst[0] = make_float4(x[t].v[k][0], x[t].v[k][1], x[t].v[k][2], x[t].v[k][3]);
+      dst[1] = make_float4(x[t].v[k][4], x[t].v[k][5], x[t].v[k][6], x[t].v[k][7]);
+    }
+  __syncthreads();
+  if (!live) return;
+  for (std::uint32_t t = 0; t < T; ++t) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < static_cast<int>(kF4); ++i) {
+      const float4 xv = reinterpret_cast<const float4*>(xl + t * H)[lane + kWave * i];
+      acc += w[i].x * xv.x + w[i].y * xv.y + w[i].z * xv.z + w[i].w * xv.w;
+    }
+    acc = halo::GroupSum(acc);
+    if (lane == 0) {
+      if (r < E)
+        logits[static_cast<std::size_t>(t) * E + r] = acc;
+      else
+        sgl[t] = acc;
+    }
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    halo_moe_router_n_h2048(const float* router, const float* sgate, const float* res, const float* delta,
+                            const float* norm_w, float* res_out, float* logits, float* sgl, std::int8_t* xq,
+                            float* xs, std::uint32_t E, std::uint32_t T, float eps) {
+  MoeRouterN<1>(router, sgate, res, delta, norm_w, res_out, logits, sgl, xq, xs, E, T, eps);
+}
+extern "C" __global__ void __launch_bounds__(256)
+    halo_moe_router_n_h4096(const float* router, const float* sgate, const float* res, const float* delta,
+                            const float* norm_w, float* res_out, float* logits, float* sgl, std::int8_t* xq,
+                            float* xs, std::uint32_t E, std::uint32_t T, float eps) {
+  MoeRouterN<2>(router, sgate, res, delta, norm_w, res_out, logits, sgl, xq, xs, E, T, eps);
+}
+
 namespace {
 // Softmax over E logits and top-k of the probabilities for one token, one wave (src/model/cpu_ops.cpp:187-207):
 // the k ids in descending probability (ties to the lower id) and the weights renormalized by max(sum, 2^-14),
@@ -83,14 +189,11 @@ namespace {
 // largest probability from below, so the top k are among the candidates p >= tau (at most a few per selected
 // lane); each candidate's rank among the candidates, by (probability desc, id asc), is its slot. Results go to
 // lds_ids / lds_w (k entries) and, when non-null, to ids / weights in global memory.
-constexpr int kMaxPerLane = 16;  // E <= 1024
 constexpr int kCandMax = 256;
 
 struct TopKScratch {
-  float lanemax[kWave];
   float cp[kCandMax];
   std::uint32_t ci[kCandMax];
-  float tau;
   float sum;
 };
 
@@ -105,13 +208,14 @@ __device__ __forceinline__ std::uint32_t LanesBelow(std::uint64_t mask) {
                                    __builtin_amdgcn_mbcnt_lo(static_cast<std::uint32_t>(mask), 0u));
 }
 
+template <int kPer>
 __device__ void WaveTopK(const float* logits, std::uint32_t E, std::uint32_t k, std::uint32_t* ids, float* weights,
                          std::uint32_t* lds_ids, float* lds_w, TopKScratch& sc) {
   const std::uint32_t lane = threadIdx.x % kWave;
-  float p[kMaxPerLane];
+  float p[kPer];
   float mx = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < kMaxPerLane; ++i) {
+  for (int i = 0; i < kPer; ++i) {
     const std::uint32_t e = lane + kWave * i;
     const float lv = logits[min(e, E - 1)];
     p[i] = e < E ? lv : -INFINITY;
@@ -120,7 +224,7 @@ __device__ void WaveTopK(const float* logits, std::uint32_t E, std::uint32_t k, 
   mx = halo::GroupMax(mx);
   float den = 0.0f;
 #pragma unroll
-  for (int i = 0; i < kMaxPerLane; ++i) {
+  for (int i = 0; i < kPer; ++i) {
     const std::uint32_t e = lane + kWave * i;
     p[i] = e < E ? expf(p[i] - mx) : 0.0f;
     den += p[i];
@@ -128,28 +232,28 @@ __device__ void WaveTopK(const float* logits, std::uint32_t E, std::uint32_t k, 
   den = halo::GroupSum(den);
   float lm = -1.0f;
 #pragma unroll
-  for (int i = 0; i < kMaxPerLane; ++i) {
+  for (int i = 0; i < kPer; ++i) {
     const std::uint32_t e = lane + kWave * i;
     p[i] = e < E ? p[i] / den : -1.0f;
     lm = fmaxf(lm, p[i]);
   }
-  // tau: the k-th largest lane maximum (every probability is >= 0, so tau = -1 admits all when k > 64)
-  sc.lanemax[lane] = lm;
-  if (lane == 0) sc.tau = -1.0f;
-  WaveSync();
-  std::uint32_t r = 0;
-  for (std::uint32_t j = 0; j < kWave; ++j) {
-    const float mj = sc.lanemax[j];
-    r += (mj > lm) || (mj == lm && j < lane);
+  // tau: the k-th largest lane maximum, by a bitwise search over the keys (probability bits + 1, 0 for a lane
+  // without experts; probabilities are >= 0, so their bit patterns order like the values). Every probability is
+  // >= 0, so tau = -1 admits all when k > 64.
+  float tau = -1.0f;
+  if (k <= kWave) {
+    const std::uint32_t key = lm >= 0.0f ? __float_as_uint(lm) + 1u : 0u;
+    std::uint32_t thr = 0;
+    for (int bit = 30; bit >= 0; --bit) {
+      const std::uint32_t cand = thr | (1u << bit);
+      if (static_cast<std::uint32_t>(__builtin_popcountll(__ballot(key >= cand))) >= k) thr = cand;
+    }
+    tau = thr == 0 ? -1.0f : __uint_as_float(thr - 1u);
   }
-  WaveSync();
-  if (k <= kWave && r == k - 1) sc.tau = lm;
-  WaveSync();
-  const float tau = sc.tau;
   // candidates p >= tau, compacted in (i, lane) order
   std::uint32_t n = 0;
 #pragma unroll
-  for (int i = 0; i < kMaxPerLane; ++i) {
+  for (int i = 0; i < kPer; ++i) {
     const std::uint32_t e = lane + kWave * i;
     const bool f = e < E && p[i] >= tau;
     const std::uint64_t m = __ballot(f);
@@ -182,7 +286,7 @@ __device__ void WaveTopK(const float* logits, std::uint32_t E, std::uint32_t k, 
       float v = -2.0f;
       std::uint32_t at = 0xFFFFFFFFu;
 #pragma unroll
-      for (int i = 0; i < kMaxPerLane; ++i)
+      for (int i = 0; i < kPer; ++i)
         if (!((taken >> i) & 1u) && p[i] > v) {
           v = p[i];
           at = lane + kWave * i;
@@ -552,7 +656,7 @@ extern "C" __global__ void __launch_bounds__(64)
   __shared__ std::uint32_t scratch[64];
   __shared__ float wscratch[64];
   __shared__ TopKScratch sc;
-  WaveTopK(logits, n, k, ids, weights, scratch, wscratch, sc);
+  WaveTopK<16>(logits, n, k, ids, weights, scratch, wscratch, sc);
 }
 extern "C" __global__ void __launch_bounds__(64)
     halo_router_topk_rows(const float* logits, std::uint32_t* ids, float* weights, std::uint32_t n, std::uint32_t k) {
@@ -560,5 +664,5 @@ extern "C" __global__ void __launch_bounds__(64)
   __shared__ float wscratch[64];
   __shared__ TopKScratch sc;
   const std::size_t t = blockIdx.x;
-  WaveTopK(logits + t * n, n, k, ids + t * k, weights + t * k, scratch, wscratch, sc);
+  WaveTopK<16>(logits + t * n, n, k, ids + t * k, weights + t * k, scratch, wscratch, sc);
 }

@@ -203,6 +203,8 @@ _SIGS = {
     "halo_op_moe_workspace_bytes": (_SZ, [C.POINTER(MoeWeights), _U32], False),
     "halo_op_moe_views": (C.c_int, [C.POINTER(MoeWeights), _U32, _VP, C.POINTER(MoeViews)], True),
     "halo_op_moe_decode": (C.c_int, [_VP, C.POINTER(MoeWeights), _VP, _VP, _U32, _VP, _SZ], True),
+    "halo_op_moe_decode_norm": (C.c_int, [_VP, C.POINTER(MoeWeights), C.POINTER(ProjInput), _VP, _U32, _VP, _SZ],
+                                True),
 }
 
 _lib = None
@@ -542,6 +544,12 @@ class MoeLayer:
 
     def forward(self, x: DeviceArray, out: DeviceArray, tokens: int, ws: DeviceArray):
         self.dev.op("moe_decode", C.byref(self.w), x.ptr, out.ptr, tokens, ws.ptr, ws.nbytes)
+
+    def forward_norm(self, res: DeviceArray, delta: DeviceArray, norm_w: DeviceArray, res_out: DeviceArray,
+                     out: DeviceArray, tokens: int, ws: DeviceArray, eps: float = 1e-6):
+        """MoE(RMSNorm(res + delta) * norm_w), the norm in the router launch; res_out receives res + delta."""
+        inp = ProjInput(x=res.ptr, delta=delta.ptr, norm_w=norm_w.ptr, res_out=res_out.ptr, eps=eps, mode=PROJ_N)
+        self.dev.op("moe_decode_norm", C.byref(self.w), C.byref(inp), out.ptr, tokens, ws.ptr, ws.nbytes)
 
     def prefill_workspace(self, tokens: int):
         n = lib().halo_op_moe_prefill_workspace_bytes(C.byref(self.w), tokens)

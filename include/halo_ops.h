@@ -146,6 +146,13 @@ int halo_op_moe_views(const halo_moe_weights* w, uint32_t tokens, void* ws, halo
                       size_t errlen);
 int halo_op_moe_decode(halo_engine* eng, const halo_moe_weights* w, const float* x, float* out, uint32_t tokens,
                        void* ws, size_t ws_bytes, char* err, size_t errlen);
+/* The same layer with the FFN input norm folded into the router launch (the reference's post-attention
+ * residual add + RMSNorm before Moe, src/engine/flash_next_gpu.cpp:697-845): in->x = residual, in->delta = the
+ * attention / DeltaNet output, in->norm_w = the FFN norm weights, in->eps; in->res_out (not in->x) receives
+ * x + delta. MoE(RMSNorm(x + delta) * norm_w) goes to out. tokens <= 4, hidden 2048 or 4096, tokens * hidden <= 8192.
+ * The router launch of halo_op_moe_decode is replaced, so four launches replace five. */
+int halo_op_moe_decode_norm(halo_engine* eng, const halo_moe_weights* w, const halo_proj_input* in, float* out,
+                            uint32_t tokens, void* ws, size_t ws_bytes, char* err, size_t errlen);
 
 /* MoE layer for a batch of T tokens (prefill; the reference's GroupedMoe, src/engine/prefill_chunk.cpp:1156-1222, and
  * ReferenceModel::Moe semantics, src/model/reference.cpp:530-578): fp32 router GEMM (+ shared gate logit), top-k per

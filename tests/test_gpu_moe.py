@@ -153,3 +153,50 @@ def test_router_topk_reference_named(dev):
         O.oracle().or_route_topk(logits[t], E, k, oi, ow)
         assert ids[t].tolist() == oi.tolist()
         assert np.allclose(w[t], ow, rtol=1e-6)
+
+
+@pytest.mark.parametrize("T", [1, 2, 4])
+def test_moe_decode_norm_equals_norm_then_moe(dev, layer, T):
+    """The router launch with the FFN norm in its prologue against halo_add_rmsnorm_q8 followed by the plain
+    decode: the residual sum bitwise, the quantized activations bitwise (same canonical norm arithmetic), the logits
+    within float reassociation, the routing identical, the output within 1e-5 of its magnitude."""
+    L = layer
+    rng = np.random.default_rng(100 + T)
+    res = rng.normal(0, 1, (T, L.H)).astype(np.float32)
+    delta = rng.normal(0, 1, (T, L.H)).astype(np.float32)
+    nw = rng.normal(1, 0.1, L.H).astype(np.float32)
+    g_res, g_delta, g_nw = dev.to_device(res), dev.to_device(delta), dev.to_device(nw)
+    g_out_res = dev.array((T, L.H), np.float32)
+    out_n = dev.array((T, L.H), np.float32)
+    ws_n = L.workspace(T)
+    L.forward_norm(g_res, g_delta, g_nw, g_out_res, out_n, T, ws_n)
+    v = L.views(T, ws_n)
+    k, E = L.k, L.E
+    rd = lambda ws, p, n, dt: ws.download_range(p - ws.ptr, n, dt)
+    # reference: the standalone norm (in place on a copy of res), then the plain decode
+    r2 = dev.to_device(res)
+    xn = dev.array((T, L.H), np.float32)
+    xq = dev.array((T, L.H), np.int8)
+    xs = dev.array((T, L.H // 32), np.float32)
+    dev.launch("halo_add_rmsnorm_q8", (T,), (256,), [r2, g_delta, g_nw, xn, xq, xs, ("u32", L.H), ("f32", 1e-6)])
+    out_r = dev.array((T, L.H), np.float32)
+    ws_r = L.workspace(T)
+    L.forward(xn, out_r, T, ws_r)
+    assert np.array_equal(g_out_res.download().view(np.uint32), r2.download().view(np.uint32))
+    assert np.array_equal(rd(ws_n, v.xq, T * L.H, np.int8), xq.download().reshape(-1))
+    assert np.array_equal(rd(ws_n, v.xs, T * L.H // 32, np.float32).view(np.uint32), xs.download().reshape(-1).view(np.uint32))
+    vr = L.views(T, ws_r)
+    ln = rd(ws_n, v.logits, T * E, np.float32).reshape(T, E)
+    lr = rd(ws_r, vr.logits, T * E, np.float32).reshape(T, E)
+    x64 = xn.download().astype(np.float64)
+    mag = np.abs(x64) @ np.abs(L.router.download().astype(np.float64).T)
+    assert np.all(np.abs(ln - lr) <= 2e-5 * mag + 1e-6)
+    ids_n = rd(ws_n, v.ids, T * k, np.uint32).reshape(T, k)
+    ids_r = rd(ws_r, vr.ids, T * k, np.uint32).reshape(T, k)
+    on, orr = out_n.download(), out_r.download()
+    for t in range(T):
+        if ids_n[t].tolist() != ids_r[t].tolist():
+            srt = np.sort(lr[t].astype(np.float64))[::-1]
+            assert np.min(np.abs(np.diff(srt[: k + 1]))) < 1e-5, "routing differs away from a tie"
+            continue
+        assert np.all(np.abs(on[t] - orr[t]) <= 1e-5 * np.abs(orr[t]).max() + 1e-6)

@@ -588,52 +588,46 @@ extern "C" __global__ void __launch_bounds__(1024) halo_moe_down_q8(
     const std::uint16_t* dbase = shared ? sdd : dd + e * H * (f / 32);
     const std::uint32_t c = l * 16;
     const bool in = c < f;
+    // loads from a clamped address, then a select: a load under a branch would cost a vmcnt(0) wait
+    const std::uint32_t cc = in ? c : 0;
     int4 q[kDownRows / 2];
     float sw[kDownRows / 2];
 #pragma unroll
     for (int p = 0; p < kDownRows / 2; ++p) {
       const std::uint32_t r = min(r0 + 2 * p + sub, H - 1);
-      // loads from a clamped address, then a select: a load under a branch would cost a vmcnt(0) wait
-      const std::uint32_t cc = in ? c : 0;
       const int4 qv = __builtin_bit_cast(
           int4, __builtin_nontemporal_load(reinterpret_cast<const halo::V4i*>(base + static_cast<std::size_t>(r) * f + cc)));
       const float sv = F16(dbase[static_cast<std::size_t>(r) * (f / 32) + cc / 32]);
       q[p] = in ? qv : make_int4(0, 0, 0, 0);
       sw[p] = in ? sv : 0.0f;
     }
-    // h: 16 values per lane, quantized per 32 with the neighbour lane
-    float hv[16];
-    if (in) {
-      const float4* hp = reinterpret_cast<const float4*>(h + static_cast<std::size_t>(hrow) * hstride + c);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float4 v = hp[i];
-        hv[4 * i] = v.x;
-        hv[4 * i + 1] = v.y;
-        hv[4 * i + 2] = v.z;
-        hv[4 * i + 3] = v.w;
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) hv[i] = 0.0f;
-    }
+    // h: lane (sub, l) loads and quantizes values c + 8 sub .. + 7 of the 16 its dot products cover (a 32-value
+    // block spans lanes 2i, 2i + 1 of both halves); the halves then swap their codes. Loads are unconditional.
+    const float4* hp = reinterpret_cast<const float4*>(h + static_cast<std::size_t>(hrow) * hstride + cc + 8 * sub);
+    const float4 ha = hp[0], hb = hp[1];
+    float hv[8] = {ha.x, ha.y, ha.z, ha.w, hb.x, hb.y, hb.z, hb.w};
     float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(hv[i]));
-    amax = fmaxf(amax, halo::Dpp<0xB1>(amax));  // lanes 2i, 2i + 1 hold one 32-value block
+    for (int i = 0; i < 8; ++i) {
+      hv[i] = in ? hv[i] : 0.0f;
+      amax = fmaxf(amax, fabsf(hv[i]));
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    amax = fmaxf(amax, halo::Dpp<0xB1>(amax));
     const float scale = amax / 127.0f;
-    int packed[4];
+    int own[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2; ++i) {
       std::uint32_t word = 0;
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         const int qv = scale > 0.0f ? static_cast<int>(rintf(hv[4 * i + b] / scale)) : 0;
         word |= (static_cast<std::uint32_t>(qv) & 0xFFu) << (8 * b);
       }
-      packed[i] = static_cast<int>(word);
+      own[i] = static_cast<int>(word);
     }
-    const int4 hq = make_int4(packed[0], packed[1], packed[2], packed[3]);
+    const int other0 = __shfl_xor(own[0], 32), other1 = __shfl_xor(own[1], 32);
+    const int4 hq = sub == 0 ? make_int4(own[0], own[1], other0, other1) : make_int4(other0, other1, own[0], own[1]);
 #pragma unroll
     for (int p = 0; p < kDownRows / 2; ++p) {
       const float v = halo::GroupSum<32>(sw[p] * (scale * static_cast<float>(Dot16(q[p], hq))));

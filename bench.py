@@ -71,6 +71,8 @@ def run_gpu(args):
             return run_attn(args, dev, H, res)
         if args.mode == "proj":
             return run_proj(args, dev, H, res)
+        if args.mode == "prefill":
+            return run_prefill(args, dev, H, res)
         # ---------------- C1 pass at M=1 (the bench value) and the M sweep ----------------
         per_copy = sum(q8_bytes(r, c) for r, c in C1_SHAPES)
         copies = max(2, -(-MIN_ROTATION_BYTES // per_copy))
@@ -573,6 +575,67 @@ def run_c4(args, dev, H, res):
     return res
 
 
+def run_prefill(args, dev, H, res):
+    """C4's ragged prefill without graphs (so a kernel tracer or counter pass follows every launch): session 0
+    prefills the 8192-token prefix, sessions 1-3 fork it, then the four 256-token suffixes prefill as one batch.
+    Then the prefill-shaped Q8 GEMMs alone (M = 2048 tokens: DeltaNet qkv 2048 -> 8192 and out 4096 -> 2048,
+    attention qg 2048 -> 8192), timed with events: achieved int8 TOPS against the 5.0 POPS MFMA peak."""
+    import ctypes as C
+
+    P, SUF = 8192, 256
+    cfg = H.c4_config(max_sessions=4, prefix_tokens=P, max_context=P + SUF + 8)
+    model = H.Model(dev, cfg, seed=2026)
+    rng = np.random.default_rng(4)
+    prefix = rng.integers(0, cfg.vocab, P).astype(np.uint32)
+    prompts = [np.concatenate([prefix, rng.integers(0, cfg.vocab, SUF).astype(np.uint32)]) for _ in range(4)]
+    out = {}
+    try:
+        model.set_session(0, prompts[0])
+        dev.sync()
+        dev.timer_start()
+        model.prefill([(0, 0, P)])
+        ms = dev.timer_stop()
+        out["prefix_ms"], out["prefix_tok_s"] = round(ms, 1), round(P / (ms * 1e-3), 1)
+        for s in (1, 2, 3):
+            model.fork(0, s)
+        for s in range(4):
+            model.set_session(s, prompts[s], nkv=P)
+        dev.sync()
+        dev.timer_start()
+        model.prefill([(s, P, SUF) for s in range(4)])
+        ms = dev.timer_stop()
+        out["suffix_4x256_ms"], out["suffix_tok_s"] = round(ms, 2), round(4 * SUF / (ms * 1e-3), 1)
+    finally:
+        model.close()
+    log(f"[bench] prefill: {out}")
+    gemms = {}
+    M = 2048
+    for name, rows, cols in (("gdn_qkv", 8192, 2048), ("gdn_out", 2048, 4096), ("attn_qg", 8192, 2048)):
+        w = H.Q8Weights(dev, rows, cols).synth(dev, 31 + rows + cols)
+        x = dev.array((M, cols), np.float32)
+        dev.op("synth_f32", x.ptr, M * cols, 7, 1.0)
+        xq, xs = dev.array((M, cols), np.int8), dev.array((M, cols // 32), np.float32)
+        ones = dev.to_device(np.ones(cols, np.float32))  # the norm kernel always reads its weights
+        dev.launch("halo_add_rmsnorm_q8", (M,), (256,), [x, None, ones, None, xq, xs, ("u32", cols), ("f32", 1e-6)])
+        y = dev.array((M, rows), np.float32)
+        for _ in range(3):
+            dev.op("matvec_q8a8", C.byref(w.desc), xq.ptr, xs.ptr, y.ptr, M, rows)
+        dev.sync()
+        n = 20
+        dev.timer_start()
+        for _ in range(n):
+            dev.op("matvec_q8a8", C.byref(w.desc), xq.ptr, xs.ptr, y.ptr, M, rows)
+        us = dev.timer_stop() * 1e3 / n
+        tops = 2.0 * M * rows * cols / (us * 1e-6) / 1e12
+        gemms[name] = {"M": M, "N": rows, "K": cols, "us": round(us, 1), "int8_TOPS": round(tops, 1),
+                       "frac_of_5000_TOPS": round(tops / 5000.0, 4)}
+        log(f"[bench] prefill gemm {name}: {gemms[name]}")
+    out["gemm"] = gemms
+    res["prefill"] = out
+    res["roofline"] = None
+    return res
+
+
 def run_gdn(args, dev, H, res):
     """C3: Gated DeltaNet decode (S = 4 sessions, states rotated over > 256 MB) and the ragged chunked prefill
     {37, 512, 2048, 8191} tokens (bf16 inputs, fp32 state)."""
@@ -807,7 +870,8 @@ def main():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--quick", action="store_true", help="only the C1 value and the C0 roofline")
     p.add_argument("--eager", action="store_true", help="launch without graphs (for profiling kernel durations)")
-    p.add_argument("--mode", choices=["all", "c0", "membw", "moe", "gdn", "c4", "pmc", "attn", "proj"], default="all",
+    p.add_argument("--mode", choices=["all", "c0", "membw", "moe", "gdn", "c4", "pmc", "attn", "proj", "prefill"],
+                   default="all",
                    help="c0: only the C0 GEMV loop (for profiling one kernel shape)")
     args = p.parse_args()
     if args.gpus != 1:
@@ -815,8 +879,9 @@ def main():
               "(the path is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
         sys.exit(2)
     res = run_gpu(args)
-    if args.mode in ("c0", "membw", "moe", "gdn", "c4", "pmc", "attn", "proj"):
-        print(json.dumps({k: res.get(k) for k in ("roofline", "c0_tilings", "membw", "moe", "gdn", "c4", "attn", "proj")}),
+    if args.mode in ("c0", "membw", "moe", "gdn", "c4", "pmc", "attn", "proj", "prefill"):
+        print(json.dumps({k: res.get(k) for k in ("roofline", "c0_tilings", "membw", "moe", "gdn", "c4", "attn", "proj",
+                                                  "prefill")}),
               flush=True)
         return
     line = {

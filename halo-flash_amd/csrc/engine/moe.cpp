@@ -158,7 +158,7 @@ int PrefillLayout(const halo_moe_weights* w, std::uint32_t T, void* ws, PrefillV
   if (T == 0) return SetErr(err, errlen, "moe prefill: no tokens"), -1;
   if (E == 0 || E + 1 > 1024 || k == 0 || k > 16 || k > E)
     return SetErr(err, errlen, "moe prefill: %u experts / %u used unsupported", E, k), -1;
-  if (H % 64 != 0 || F % 32 != 0 || F == 0) return SetErr(err, errlen, "moe prefill: hidden %u / ff %u", H, F), -1;
+  if (H % 64 != 0 || F % 64 != 0 || F == 0) return SetErr(err, errlen, "moe prefill: hidden %u / ff %u", H, F), -1;
   if (shared && (w->shared_ff != F || w->shared_gate == nullptr))
     return SetErr(err, errlen, "moe prefill: the shared expert must have ff %u and a gate row", F), -1;
   auto dense = [](const halo_q8_matrix& m, std::uint32_t rows, std::uint32_t cols) {
@@ -245,7 +245,7 @@ int halo_op_moe_prefill(halo_engine* eng, const halo_moe_weights* w, const float
                           Ptr(shared ? w->shared_gate_proj.qs : nullptr), Ptr(shared ? w->shared_gate_proj.d : nullptr),
                           Ptr(shared ? w->shared_up.qs : nullptr), Ptr(shared ? w->shared_up.d : nullptr), Ptr(v.xq),
                           Ptr(v.xs), Ptr(v.token), Ptr(v.tiles), Ptr(v.ntiles), Ptr(v.h), U32(F), U32(H), U32(E), U32(F)};
-    if (Launch(eng, "halo_moe_grouped_gate_up_q8", D3(CeilDiv(F, 16), v.max_tiles), D3(256), a, err, errlen) != 0)
+    if (Launch(eng, "halo_moe_grouped_gate_up_q8", D3(CeilDiv(F, 128), v.max_tiles), D3(512), a, err, errlen) != 0)
       return -1;
   }
   // 6. h quantized per 32
@@ -258,7 +258,7 @@ int halo_op_moe_prefill(halo_engine* eng, const halo_moe_weights* w, const float
     const halo_arg a[] = {Ptr(w->down.qs), Ptr(w->down.d), Ptr(shared ? w->shared_down.qs : nullptr),
                           Ptr(shared ? w->shared_down.d : nullptr), Ptr(v.hq), Ptr(v.hs), Ptr(v.tiles), Ptr(v.ntiles),
                           Ptr(v.y), U32(H), U32(F), U32(E)};
-    if (Launch(eng, "halo_moe_grouped_down_q8", D3(CeilDiv(H, 16), v.max_tiles), D3(256), a, err, errlen) != 0)
+    if (Launch(eng, "halo_moe_grouped_down_q8", D3(CeilDiv(H, 128), v.max_tiles), D3(512), a, err, errlen) != 0)
       return -1;
   }
   // 8. slot-order combine + shared expert

@@ -164,130 +164,38 @@ extern "C" __global__ void __launch_bounds__(256)
 }
 
 // ---- grouped int8 MFMA over the pairs of each group ---------------------------------------------------------------
-// One v_mfma_i32_16x16x32_i8 per (16 weight rows, 16 pairs, one Q8_0 block), as halo_gemm_q8a8_mfma_t*: a block of
-// 4 waves owns 16 rows of group g's matrix x one tile of up to 64 pairs (4 x 16), the waves split the K blocks and
-// reduce through LDS in a fixed order. Group g < E reads matrix rows g * rows + r of the stacked expert tensors, group
-// E the shared expert's. Pair p's activation row is xq[gather ? gather[p] : p]. With SwiGLU the block computes the
-// gate and up rows together and writes h = SiLU(gate) * up; otherwise it writes the projection.
-// grid (ceil(rows / 16), max tiles), block 256; blocks past ntiles[0] exit. y [pairs][ystride].
-namespace {
-typedef int V4I32G __attribute__((ext_vector_type(4)));
-
-template <bool kSwiGLU>
-__device__ __forceinline__ void GroupedMfma(
-    const std::int8_t* __restrict__ qa, const std::uint16_t* __restrict__ da, const std::int8_t* __restrict__ qb,
-    const std::uint16_t* __restrict__ db, const std::int8_t* __restrict__ sqa, const std::uint16_t* __restrict__ sda,
-    const std::int8_t* __restrict__ sqb, const std::uint16_t* __restrict__ sdb, const std::int8_t* __restrict__ xq,
-    const float* __restrict__ xs, const std::uint32_t* __restrict__ gather, const std::uint32_t* __restrict__ tiles,
-    const std::uint32_t* __restrict__ ntiles, float* __restrict__ y, std::uint32_t rows, std::uint32_t cols,
-    std::uint32_t E, std::uint32_t ystride) {
-  constexpr int NT = 4;
-  constexpr int NM = kSwiGLU ? 2 : 1;
-  __shared__ float red[4][NM][NT][16][17];
-  if (blockIdx.y >= ntiles[0]) return;
-  const std::uint32_t* tt = tiles + 3 * static_cast<std::size_t>(blockIdx.y);
-  const std::uint32_t g = tt[0], p0 = tt[1], np = tt[2];
-  const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const std::uint32_t r0 = blockIdx.x * 16, nblk = cols / 32;
-  const std::uint32_t kofs = (lane / 16) * 8;
-  const bool sh = g == E;
-  const std::size_t mrow0 = sh ? 0 : static_cast<std::size_t>(g) * rows;
-  const std::int8_t* A[NM];
-  const std::uint16_t* D[NM];
-  A[0] = sh ? sqa : qa;
-  D[0] = sh ? sda : da;
-  if constexpr (kSwiGLU) {
-    A[1] = sh ? sqb : qb;
-    D[1] = sh ? sdb : db;
-  }
-  const std::uint32_t arow = min(r0 + lane % 16, rows - 1);
-  const std::int8_t* aptr[NM];
-  const std::uint16_t* dptr[NM][4];
-#pragma unroll
-  for (int m = 0; m < NM; ++m) {
-    aptr[m] = A[m] + (mrow0 + arow) * cols + kofs;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dptr[m][i] = D[m] + (mrow0 + min(r0 + (lane / 16) * 4 + i, rows - 1)) * nblk;
-  }
-  const std::int8_t* bptr[NT];
-  const float* sptr[NT];
-#pragma unroll
-  for (int n = 0; n < NT; ++n) {
-    const std::uint32_t p = p0 + min(static_cast<std::uint32_t>(n * 16) + lane % 16, np - 1);
-    const std::uint32_t row = gather != nullptr ? gather[p] : p;
-    bptr[n] = xq + static_cast<std::size_t>(row) * cols + kofs;
-    sptr[n] = xs + static_cast<std::size_t>(row) * nblk;
-  }
-  float acc[NM][NT][4];
-#pragma unroll
-  for (int m = 0; m < NM; ++m)
-#pragma unroll
-    for (int n = 0; n < NT; ++n)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[m][n][i] = 0.0f;
-  const std::uint32_t per = (nblk + 3) / 4, kb0 = wave * per, kb1 = min(nblk, kb0 + per);
-  for (std::uint32_t kb = kb0; kb < kb1; ++kb) {
-    long a[NM], b[NT];
-    float dw[NM][4], sx[NT];
-#pragma unroll
-    for (int m = 0; m < NM; ++m) {
-      a[m] = *reinterpret_cast<const long*>(aptr[m] + kb * 32);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) dw[m][i] = F16(dptr[m][i][kb]);
-    }
-#pragma unroll
-    for (int n = 0; n < NT; ++n) {
-      b[n] = *reinterpret_cast<const long*>(bptr[n] + kb * 32);
-      sx[n] = sptr[n][kb];
-    }
-#pragma unroll
-    for (int m = 0; m < NM; ++m)
-#pragma unroll
-      for (int n = 0; n < NT; ++n) {
-        const V4I32G zero = {0, 0, 0, 0};
-        const V4I32G c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[m], b[n], zero, 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[m][n][i] += dw[m][i] * (sx[n] * static_cast<float>(c[i]));
-      }
-  }
-#pragma unroll
-  for (int m = 0; m < NM; ++m)
-#pragma unroll
-    for (int n = 0; n < NT; ++n)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) red[wave][m][n][(lane / 16) * 4 + i][lane % 16] = acc[m][n][i];
-  __syncthreads();
-  for (std::uint32_t e = threadIdx.x; e < NT * 256; e += blockDim.x) {
-    const std::uint32_t n = e / 256, rr = (e % 256) / 16, pp = e % 16;
-    const std::uint32_t r = r0 + rr, pi = n * 16 + pp;
-    if (r >= rows || pi >= np) continue;
-    const float v0 = ((red[0][0][n][rr][pp] + red[1][0][n][rr][pp]) + red[2][0][n][rr][pp]) + red[3][0][n][rr][pp];
-    float v = v0;
-    if constexpr (kSwiGLU) {
-      const float v1 =
-          ((red[0][NM - 1][n][rr][pp] + red[1][NM - 1][n][rr][pp]) + red[2][NM - 1][n][rr][pp]) + red[3][NM - 1][n][rr][pp];
-      v = halo::Silu(v0) * v1;
-    }
-    y[static_cast<std::size_t>(p0 + pi) * ystride + r] = v;
-  }
-}
-}  // namespace
-
-extern "C" __global__ void __launch_bounds__(256) halo_moe_grouped_gate_up_q8(
+// halo::GemmTileQ8 per (128 rows of group g's matrix, one tile of up to 64 pairs): group g < E reads rows g * rows + r
+// of the stacked expert tensors, group E the shared expert's. Pair p's activation row is xq[gather ? gather[p] : p].
+// The gate/up launch computes both matrices and writes h = SiLU(gate) * up; the down launch writes the projection.
+// grid (ceil(rows / 128), max tiles), block 512; blocks past ntiles[0] exit. y [pairs][ystride].
+extern "C" __global__ void __launch_bounds__(512) halo_moe_grouped_gate_up_q8(
     const std::int8_t* gq, const std::uint16_t* gd, const std::int8_t* uq, const std::uint16_t* ud,
     const std::int8_t* sgq, const std::uint16_t* sgd, const std::int8_t* suq, const std::uint16_t* sud,
     const std::int8_t* xq, const float* xs, const std::uint32_t* gather, const std::uint32_t* tiles,
     const std::uint32_t* ntiles, float* h, std::uint32_t ff, std::uint32_t H, std::uint32_t E, std::uint32_t hstride) {
-  GroupedMfma<true>(gq, gd, uq, ud, sgq, sgd, suq, sud, xq, xs, gather, tiles, ntiles, h, ff, H, E, hstride);
+  if (blockIdx.y >= ntiles[0]) return;
+  const std::uint32_t* tt = tiles + 3 * static_cast<std::size_t>(blockIdx.y);
+  const std::uint32_t g = tt[0], p0 = tt[1], np = tt[2];
+  const bool sh = g == E;
+  const std::size_t row0 = sh ? 0 : static_cast<std::size_t>(g) * ff;
+  const std::uint32_t nblk = H / 32;
+  halo::GemmTileQ8<4, 1, 2, 2>((sh ? sgq : gq) + row0 * H, (sh ? sgd : gd) + row0 * nblk, (sh ? suq : uq) + row0 * H,
+                               (sh ? sud : ud) + row0 * nblk, ff, H, blockIdx.x * 128, xq, xs, gather + p0, 0, np, H,
+                               h, p0, hstride);
 }
 
-extern "C" __global__ void __launch_bounds__(256) halo_moe_grouped_down_q8(
+extern "C" __global__ void __launch_bounds__(512) halo_moe_grouped_down_q8(
     const std::int8_t* dq, const std::uint16_t* dd, const std::int8_t* sdq, const std::uint16_t* sdd,
     const std::int8_t* hq, const float* hs, const std::uint32_t* tiles, const std::uint32_t* ntiles, float* y,
     std::uint32_t H, std::uint32_t ff, std::uint32_t E) {
-  GroupedMfma<false>(dq, dd, nullptr, nullptr, sdq, sdd, nullptr, nullptr, hq, hs, nullptr, tiles, ntiles, y, H, ff, E,
-                     H);
+  if (blockIdx.y >= ntiles[0]) return;
+  const std::uint32_t* tt = tiles + 3 * static_cast<std::size_t>(blockIdx.y);
+  const std::uint32_t g = tt[0], p0 = tt[1], np = tt[2];
+  const bool sh = g == E;
+  const std::size_t row0 = sh ? 0 : static_cast<std::size_t>(g) * H;
+  const std::uint32_t nblk = ff / 32;
+  halo::GemmTileQ8<4, 1, 2, 1>((sh ? sdq : dq) + row0 * ff, (sh ? sdd : dd) + row0 * nblk, nullptr, nullptr, H, ff,
+                               blockIdx.x * 128, hq, hs, nullptr, p0, np, ff, y, p0, H);
 }
 
 // grid (ceil(H / 256), T), block 256: out[t][r] = sum over s < k, in order, of weights[t][s] * y[pos[t k + s]][r],

@@ -520,6 +520,203 @@ extern "C" __global__ void __launch_bounds__(256) halo_gemm_q8a8_mfma_t4(
   GemmQ8A8Mfma<4>(qs, d, xq, xs, y, rows, cols, qstride, T, ystride);
 }
 
+// ---- tiled int8 MFMA GEMM for prefill-sized M (dense projections and the grouped MoE experts) --------------------
+// The same arithmetic per Q8_0 block as above (an exact int32 block product scaled by d_w s_x and accumulated in fp32,
+// blocks in ascending order), on v_mfma_i32_32x32x32_i8: one MFMA is one Q8_0 block of a 32-row x 32-token tile. The
+// per-output scales d_w[r] s_x[t] of a tile come from a rank-1 fp32 MFMA in the same layout (k = 0 carries the
+// factors, k = 1 zeros), so the VALU epilogue is acc = fma(float(isum), d_w s_x, acc).
+// A block of 8 waves, WR x WT, owns ROWS = WR * MT * 32 weight rows x TOKS = WT * 32 tokens of one or two matrices
+// (NMAT = 2: gate and up, combined as SiLU(gate) * up); wave (wr, wt) computes MT row tiles x one token tile. K
+// advances 64 columns (two Q8_0 blocks) per stage. Each stage's weight and activation tiles (int8, rows padded to
+// 80 bytes so the 16-byte fragment reads are conflict-free) and their scales are staged in LDS, double buffered;
+// the loads of stage k + 2 are in flight in registers while stage k computes and stage k + 1 is stored.
+// MFMA operands: lane l supplies 16 int8 of row (l % 32) at k 16 (l / 32) of the block, the same k split for both
+// operands; the int32 result lane l holds token (l % 32) of the tile and rows 8 (j / 4) + 4 (l / 32) + j % 4.
+// Tokens: tile token i reads activation row xrow[min(i, ntok - 1)] (or x0 + min(i, ntok - 1)) and, for i < ntok,
+// writes y[(yrow0 + i) * ystride + r]. Matrices are [rows][qstride] int8 + [rows][cols / 32] fp16 scales; block row
+// tile r0. Requires cols % 64 == 0.
+namespace {
+typedef int V16I32 __attribute__((ext_vector_type(16)));
+typedef float V16F32 __attribute__((ext_vector_type(16)));
+constexpr int kTileLd = 64 + 16;
+}  // namespace
+
+namespace halo {
+template <int WR, int MT, int WT, int NMAT>
+__device__ __forceinline__ void GemmTileQ8(const std::int8_t* __restrict__ A0, const std::uint16_t* __restrict__ D0,
+                                          const std::int8_t* __restrict__ A1, const std::uint16_t* __restrict__ D1,
+                                          std::uint32_t rows, std::uint32_t qstride, std::uint32_t r0,
+                                          const std::int8_t* __restrict__ xq, const float* __restrict__ xs,
+                                          const std::uint32_t* __restrict__ xrow, std::uint32_t x0, std::uint32_t ntok,
+                                          std::uint32_t cols, float* __restrict__ y, std::uint32_t yrow0,
+                                          std::uint32_t ystride) {
+  static_assert(WR * WT == 8, "8 waves");
+  constexpr int ROWS = WR * MT * 32, TOKS = WT * 32;
+  constexpr int NA = NMAT * ROWS * 4, NB = TOKS * 4;  // 16-byte chunks per stage
+  constexpr int NDW = NMAT * ROWS * 2, NSX = TOKS * 2;  // scales per stage
+  constexpr int LA = (NA + 511) / 512, LB = (NB + 511) / 512, LS = (NDW + NSX + 511) / 512;
+  __shared__ __attribute__((aligned(16))) std::int8_t la[2][NMAT][ROWS][kTileLd];
+  __shared__ __attribute__((aligned(16))) std::int8_t lb[2][TOKS][kTileLd];
+  __shared__ __attribute__((aligned(16))) float ldw[2][NMAT][2][ROWS];
+  __shared__ __attribute__((aligned(16))) float lsx[2][2][TOKS];
+  const std::uint32_t tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const std::uint32_t wr = wave / WT, wt = wave % WT;
+  const std::uint32_t nblk = cols / 32, nk = cols / 64;
+  const auto tokrow = [&](std::uint32_t i) {
+    const std::uint32_t ii = min(i, ntok - 1);
+    return xrow != nullptr ? xrow[ii] : x0 + ii;
+  };
+  // per-thread global sources (clamped, so every load is unconditional) and LDS destinations
+  const std::int8_t* ga[LA];
+  std::uint32_t amat[LA], arow[LA], apart[LA];
+  bool aon[LA];
+#pragma unroll
+  for (int i = 0; i < LA; ++i) {
+    const std::uint32_t c = tid + 512u * i, cc = min(c, static_cast<std::uint32_t>(NA - 1));
+    aon[i] = c < static_cast<std::uint32_t>(NA);
+    amat[i] = cc / (ROWS * 4);
+    arow[i] = (cc / 4) % ROWS;
+    apart[i] = cc % 4;
+    ga[i] = (amat[i] ? A1 : A0) + static_cast<std::size_t>(min(r0 + arow[i], rows - 1)) * qstride + apart[i] * 16;
+  }
+  const std::int8_t* gb[LB];
+  std::uint32_t brow[LB], bpart[LB];
+  bool bon[LB];
+#pragma unroll
+  for (int i = 0; i < LB; ++i) {
+    const std::uint32_t c = tid + 512u * i, cc = min(c, static_cast<std::uint32_t>(NB - 1));
+    bon[i] = c < static_cast<std::uint32_t>(NB);
+    brow[i] = cc / 4;
+    bpart[i] = cc % 4;
+    gb[i] = xq + static_cast<std::size_t>(tokrow(brow[i])) * cols + bpart[i] * 16;
+  }
+  // scales: index c < NDW is (mat, row, blk) of a weight scale, the rest (token, blk) of an activation scale
+  const std::uint16_t* gd[LS];
+  const float* gs[LS];
+  std::uint32_t sidx[LS];
+#pragma unroll
+  for (int i = 0; i < LS; ++i) {
+    const std::uint32_t c = min(tid + 512u * i, static_cast<std::uint32_t>(NDW + NSX - 1));
+    sidx[i] = c;
+    const std::uint32_t cw = min(c, static_cast<std::uint32_t>(NDW - 1)), cs = c < NDW ? 0u : c - NDW;
+    const std::uint32_t m = cw / (ROWS * 2), rr = (cw / 2) % ROWS;
+    gd[i] = (m ? D1 : D0) + static_cast<std::size_t>(min(r0 + rr, rows - 1)) * nblk + cw % 2;
+    gs[i] = xs + static_cast<std::size_t>(tokrow(cs / 2)) * nblk + cs % 2;
+  }
+  const bool son_last = tid + 512u * (LS - 1) < static_cast<std::uint32_t>(NDW + NSX);
+  struct Staged {
+    int4 a[LA], b[LB];
+    float sc[LS];
+  };
+  auto load = [&](std::uint32_t kc, Staged& r) {
+#pragma unroll
+    for (int i = 0; i < LA; ++i)
+      r.a[i] = __builtin_bit_cast(int4, __builtin_nontemporal_load(reinterpret_cast<const V4i*>(ga[i] + kc * 64)));
+#pragma unroll
+    for (int i = 0; i < LB; ++i) r.b[i] = *reinterpret_cast<const int4*>(gb[i] + kc * 64);
+#pragma unroll
+    for (int i = 0; i < LS; ++i) {
+      const float dv = F16(gd[i][kc * 2]), sv = gs[i][kc * 2];  // both loaded (clamped addresses), one kept
+      r.sc[i] = sidx[i] < static_cast<std::uint32_t>(NDW) ? dv : sv;
+    }
+  };
+  auto store = [&](std::uint32_t st, const Staged& r) {
+#pragma unroll
+    for (int i = 0; i < LA; ++i)
+      if (aon[i]) *reinterpret_cast<int4*>(&la[st][amat[i]][arow[i]][apart[i] * 16]) = r.a[i];
+#pragma unroll
+    for (int i = 0; i < LB; ++i)
+      if (bon[i]) *reinterpret_cast<int4*>(&lb[st][brow[i]][bpart[i] * 16]) = r.b[i];
+#pragma unroll
+    for (int i = 0; i < LS; ++i) {
+      if (i == LS - 1 && !son_last) continue;
+      const std::uint32_t c = sidx[i];
+      if (c < static_cast<std::uint32_t>(NDW))
+        ldw[st][c / (ROWS * 2)][c % 2][(c / 2) % ROWS] = r.sc[i];
+      else
+        lsx[st][(c - NDW) % 2][(c - NDW) / 2] = r.sc[i];
+    }
+  };
+  float acc[NMAT][MT][16];
+#pragma unroll
+  for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[m][mt][j] = 0.0f;
+  const std::uint32_t fr = lane % 32, fk = 16 * (lane / 32);
+  auto compute = [&](std::uint32_t st) {
+#pragma unroll 1
+    for (int blk = 0; blk < 2; ++blk) {
+      const V4i bf = *reinterpret_cast<const V4i*>(&lb[st][wt * 32 + fr][blk * 32 + fk]);
+      const float sx = lsx[st][blk][wt * 32 + fr];
+      const float bsx = lane < 32 ? sx : 0.0f;
+      const V16I32 zero = {};
+      const V16F32 fzero = {};
+#pragma unroll
+      for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const std::uint32_t rr = wr * MT * 32 + mt * 32 + fr;
+          const V4i af = *reinterpret_cast<const V4i*>(&la[st][m][rr][blk * 32 + fk]);
+          const float dw = ldw[st][m][blk][rr];
+          const V16F32 sc = __builtin_amdgcn_mfma_f32_32x32x2f32(lane < 32 ? dw : 0.0f, bsx, fzero, 0, 0, 0);
+          const V16I32 c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, zero, 0, 0, 0);
+#pragma unroll
+          for (int j = 0; j < 16; ++j) acc[m][mt][j] = __builtin_fmaf(static_cast<float>(c[j]), sc[j], acc[m][mt][j]);
+        }
+    }
+  };
+  // one stage: prefetch kc + 2 into `fill`, compute kc, store kc + 1 (from `next`) into the other buffer, barrier.
+  // The other buffer was last read in stage kc - 1, before the barrier that ended it.
+  auto stage = [&](std::uint32_t kc, Staged& next, Staged& fill) {
+    if (kc + 2 < nk) load(kc + 2, fill);
+    compute(kc & 1u);
+    if (kc + 1 < nk) store((kc + 1) & 1u, next);
+    __syncthreads();
+  };
+  Staged s0, s1;
+  load(0, s0);
+  if (nk > 1) load(1, s1);
+  store(0, s0);
+  __syncthreads();
+  for (std::uint32_t kc = 0; kc < nk; kc += 2) {
+    stage(kc, s1, s0);
+    if (kc + 1 < nk) stage(kc + 1, s0, s1);
+  }
+  const std::uint32_t i = wt * 32 + fr;
+  if (i >= ntok) return;
+  float* yt = y + static_cast<std::size_t>(yrow0 + i) * ystride;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const std::uint32_t r = r0 + wr * MT * 32 + mt * 32 + g * 8 + (lane / 32) * 4;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[e] = NMAT == 2 ? Silu(acc[0][mt][4 * g + e]) * acc[NMAT - 1][mt][4 * g + e] : acc[0][mt][4 * g + e];
+      if (r + 3 < rows && ystride % 4 == 0) {
+        *reinterpret_cast<float4*>(yt + r) = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (r + e < rows) yt[r + e] = v[e];
+      }
+    }
+}
+}  // namespace halo
+
+// Dense: 128 rows x 128 tokens per block. grid (ceil(rows / 128), ceil(T / 128)), block 512. y[t * ystride + r].
+extern "C" __global__ void __launch_bounds__(512) halo_gemm_q8a8_mfma32(
+    const std::int8_t* __restrict__ qs, const std::uint16_t* __restrict__ d, const std::int8_t* __restrict__ xq,
+    const float* __restrict__ xs, float* __restrict__ y, std::uint32_t rows, std::uint32_t cols,
+    std::uint32_t qstride, std::uint32_t T, std::uint32_t ystride) {
+  const std::uint32_t t0 = blockIdx.y * 128;
+  halo::GemmTileQ8<2, 2, 4, 1>(qs, d, nullptr, nullptr, rows, qstride, blockIdx.x * 128, xq, xs, nullptr, t0,
+                               min(128u, T - t0), cols, y, t0, ystride);
+}
+
 // x = a * x + b over n floats (shapes seeded tensors such as norm weights around 1).
 extern "C" __global__ void __launch_bounds__(256)
     halo_affine_f32(float* x, std::uint64_t n, float a, float b) {

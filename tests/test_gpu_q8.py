@@ -198,3 +198,15 @@ def test_synth_distribution(dev):
     assert abs(np.sqrt((dd ** 2).mean()) - 0.02) < 0.001  # |N(0, 0.02)| has rms 0.02
     w2 = H.Q8Weights(dev, 256, 4096).synth(dev, seed=1234)
     assert np.array_equal(w2.host()[0], qs)  # deterministic
+
+
+@pytest.mark.parametrize("m,rows,cols", [(128, 512, 2048), (300, 1024, 4096), (2048, 256, 2048)])
+def test_mfma_gemm_prefill_tiles(dev, m, rows, cols):
+    """Prefill-sized M (>= 64) runs the 128 x 128 LDS-tiled kernel (v_mfma_i32_32x32x32_i8, one MFMA per Q8_0 block
+    and 32 x 32 tile); dense output, ragged M."""
+    rng = np.random.default_rng(m + rows)
+    w, xq, xs, want, mag = _gemv_case(dev, rng, rows, cols, m)
+    gq, gs = dev.to_device(xq), dev.to_device(xs)
+    gy = dev.array((m, rows), np.float32)
+    dev.op("matvec_q8a8", C_ref(w), gq.ptr, gs.ptr, gy.ptr, m, rows)
+    _check_y(gy.download(), want, mag)

@@ -16,55 +16,73 @@ using halo::F16;
 using halo::kWave;
 
 // ---- fp32 GEMM for the router: C[t][n] = sum_k X[t][k] W[n][k] -----------------------------------------------------
-// grid (ceil((N + 1) / 64), ceil(T / 64)), block 256: a 64 x 64 tile, 4 x 4 outputs per thread, K in steps of 32
-// through LDS. C [T][ldc] for rows n < N of W; when wlast is non-null it is one more row, whose products go to
-// clast [T] (the shared-gate logit next to the router logits). K % 32 == 0.
+// On v_mfma_f32_32x32x2f32. grid (ceil((N + 1) / 64), ceil(T / 64)), block 256: a 64-token x 64-row tile, wave
+// (wt, wn) a 32 x 32 sub-tile; K in stages of 32 through LDS (rows padded to 36 floats: the 16-byte reads are
+// conflict-free). Within a stage, MFMA step s takes k = s from lanes 0-31 and k = 16 + s from lanes 32-63 (any k
+// split shared by both operands sums the same products). The result lane l holds row n = l % 32 of its sub-tile and
+// tokens 8 (j / 4) + 4 (l / 32) + j % 4. C [T][ldc] for rows n < N of W; when wlast is non-null it is one more row,
+// whose products go to clast [T] (the shared-gate logit next to the router logits). K % 32 == 0.
+namespace {
+typedef float V16F32R __attribute__((ext_vector_type(16)));
+}
 extern "C" __global__ void __launch_bounds__(256) halo_gemm_f32_nt(
     const float* __restrict__ X, const float* __restrict__ W, const float* __restrict__ wlast, float* __restrict__ Cm,
     float* __restrict__ clast, std::uint32_t T, std::uint32_t N, std::uint32_t K, std::uint32_t ldc) {
-  __shared__ float xs[32][65];
-  __shared__ float ws[32][65];
-  const std::uint32_t tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+  constexpr int kLd = 36;
+  __shared__ __attribute__((aligned(16))) float xl[64][kLd];
+  __shared__ __attribute__((aligned(16))) float wl[64][kLd];
+  const std::uint32_t tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const std::uint32_t wt = wave / 2, wn = wave % 2;
   const std::uint32_t n0 = blockIdx.x * 64, t0 = blockIdx.y * 64;
   const std::uint32_t NN = N + (wlast != nullptr ? 1u : 0u);
-  float acc[4][4];
+  // stage loads: 64 rows x 32 k per operand = 512 float4, two per thread (row c / 8, k 4 (c % 8))
+  const float* gx[2];
+  const float* gw[2];
+  std::uint32_t lr[2], lk[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+  for (int i = 0; i < 2; ++i) {
+    const std::uint32_t c = tid + 256u * i;
+    lr[i] = c / 8;
+    lk[i] = 4 * (c % 8);
+    gx[i] = X + static_cast<std::size_t>(min(t0 + lr[i], T - 1)) * K + lk[i];
+    const std::uint32_t nr = min(n0 + lr[i], NN - 1);
+    gw[i] = (nr < N ? W + static_cast<std::size_t>(nr) * K : wlast) + lk[i];
+  }
+  V16F32R acc = {};
+  // next stage's operands (the last stage reloads its own rows: in bounds, unused)
+  float4 rx0 = *reinterpret_cast<const float4*>(gx[0]), rx1 = *reinterpret_cast<const float4*>(gx[1]);
+  float4 rw0 = *reinterpret_cast<const float4*>(gw[0]), rw1 = *reinterpret_cast<const float4*>(gw[1]);
+  const std::uint32_t fr = lane % 32, fh = 16 * (lane / 32);
   for (std::uint32_t k0 = 0; k0 < K; k0 += 32) {
-    // 64 rows x 32 k of each operand: 2048 floats, 8 per thread (row = e / 32, k = e % 32: coalesced along k)
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const std::uint32_t e = threadIdx.x + 256 * u, r = e / 32, k = e % 32;
-      const std::uint32_t tr = min(t0 + r, T - 1), nr = min(n0 + r, NN - 1);
-      xs[k][r] = X[static_cast<std::size_t>(tr) * K + k0 + k];
-      const float* wr = nr < N ? W + static_cast<std::size_t>(nr) * K : wlast;
-      ws[k][r] = wr[k0 + k];
-    }
+    *reinterpret_cast<float4*>(&xl[lr[0]][lk[0]]) = rx0;
+    *reinterpret_cast<float4*>(&xl[lr[1]][lk[1]]) = rx1;
+    *reinterpret_cast<float4*>(&wl[lr[0]][lk[0]]) = rw0;
+    *reinterpret_cast<float4*>(&wl[lr[1]][lk[1]]) = rw1;
     __syncthreads();
-#pragma unroll 8
-    for (int k = 0; k < 32; ++k) {
-      float a[4], b[4];
+    const std::uint32_t kn = k0 + 32 < K ? k0 + 32 : k0;
+    rx0 = *reinterpret_cast<const float4*>(gx[0] + kn);
+    rx1 = *reinterpret_cast<const float4*>(gx[1] + kn);
+    rw0 = *reinterpret_cast<const float4*>(gw[0] + kn);
+    rw1 = *reinterpret_cast<const float4*>(gw[1] + kn);
+    float a[16], b[16];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = xs[k][ty + 16 * i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = ws[k][tx + 16 * j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * b[j];
+    for (int q = 0; q < 4; ++q) {
+      const float4 av = *reinterpret_cast<const float4*>(&xl[wt * 32 + fr][fh + 4 * q]);
+      const float4 bv = *reinterpret_cast<const float4*>(&wl[wn * 32 + fr][fh + 4 * q]);
+      a[4 * q] = av.x, a[4 * q + 1] = av.y, a[4 * q + 2] = av.z, a[4 * q + 3] = av.w;
+      b[4 * q] = bv.x, b[4 * q + 1] = bv.y, b[4 * q + 2] = bv.z, b[4 * q + 3] = bv.w;
     }
+#pragma unroll
+    for (int s = 0; s < 16; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b[s], acc, 0, 0, 0);
     __syncthreads();
   }
+  const std::uint32_t n = n0 + wn * 32 + fr;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const std::uint32_t t = t0 + ty + 16 * i, n = n0 + tx + 16 * j;
-      if (t < T && n < N) Cm[static_cast<std::size_t>(t) * ldc + n] = acc[i][j];
-      if (t < T && n == N && wlast != nullptr) clast[t] = acc[i][j];
-    }
+  for (int j = 0; j < 16; ++j) {
+    const std::uint32_t t = t0 + wt * 32 + 8 * (j / 4) + 4 * (lane / 32) + j % 4;
+    if (t < T && n < N) Cm[static_cast<std::size_t>(t) * ldc + n] = acc[j];
+    if (t < T && n == N && wlast != nullptr) clast[t] = acc[j];
+  }
 }
 
 // ---- grouping of (token, slot) pairs by expert --------------------------------------------------------------------
@@ -168,7 +186,7 @@ extern "C" __global__ void __launch_bounds__(256)
 // of the stacked expert tensors, group E the shared expert's. Pair p's activation row is xq[gather ? gather[p] : p].
 // The gate/up launch computes both matrices and writes h = SiLU(gate) * up; the down launch writes the projection.
 // grid (ceil(rows / 128), max tiles), block 512; blocks past ntiles[0] exit. y [pairs][ystride].
-extern "C" __global__ void __launch_bounds__(512) halo_moe_grouped_gate_up_q8(
+extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) halo_moe_grouped_gate_up_q8(
     const std::int8_t* gq, const std::uint16_t* gd, const std::int8_t* uq, const std::uint16_t* ud,
     const std::int8_t* sgq, const std::uint16_t* sgd, const std::int8_t* suq, const std::uint16_t* sud,
     const std::int8_t* xq, const float* xs, const std::uint32_t* gather, const std::uint32_t* tiles,

@@ -36,7 +36,7 @@ uint32_t halo_gdn_chunk_table(const uint32_t* seqlens, uint32_t n_seq, uint32_t*
 }
 
 size_t halo_op_gdn_prefill_workspace_bytes(uint32_t n_chunks, uint32_t Hv) {
-  return static_cast<std::size_t>(n_chunks) * Hv * (2 * 64 * 64 + 64) * sizeof(float);
+  return static_cast<std::size_t>(n_chunks) * Hv * (4 * 64 * 128 + 64) * sizeof(float);
 }
 
 namespace {
@@ -49,19 +49,15 @@ int GdnPrefill(halo_engine* eng, bool f32, const void* q, const void* k, const v
     return SetErr(err, errlen, "gdn prefill: empty batch or bad heads"), -1;
   const std::size_t need = halo_op_gdn_prefill_workspace_bytes(n_chunks, Hv);
   if (ws == nullptr || ws_bytes < need) return SetErr(err, errlen, "gdn prefill: workspace %zu < %zu", ws_bytes, need), -1;
-  float* Tm = static_cast<float*>(ws);
-  float* Pm = Tm + static_cast<std::size_t>(n_chunks) * Hv * 4096;
-  float* Gc = Pm + static_cast<std::size_t>(n_chunks) * Hv * 4096;
+  float* wy = static_cast<float*>(ws);
+  float* Gc = wy + static_cast<std::size_t>(n_chunks) * Hv * 4 * 64 * 128;
   {
-    const halo_arg a[] = {Ptr(q), Ptr(k), Ptr(g), Ptr(beta), Ptr(chunks), Ptr(Tm), Ptr(Pm), Ptr(Gc), U32(Hv), U32(Hk)};
-    if (Launch(eng, f32 ? "halo_gdn_chunk_prep_f32" : "halo_gdn_chunk_prep", D3(n_chunks, Hv), D3(256), a, err,
-               errlen) != 0)
+    const halo_arg a[] = {Ptr(q), Ptr(k), Ptr(v), Ptr(g), Ptr(beta), Ptr(chunks), Ptr(wy), Ptr(Gc), U32(Hv), U32(Hk)};
+    if (Launch(eng, f32 ? "halo_gdn_wy_prep_f32" : "halo_gdn_wy_prep", D3(n_chunks, Hv), D3(256), a, err, errlen) != 0)
       return -1;
   }
-  const halo_arg a[] = {Ptr(q), Ptr(k), Ptr(v), Ptr(beta), Ptr(chunks), Ptr(seqs), Ptr(Tm), Ptr(Pm), Ptr(Gc),
-                        Ptr(state), Ptr(o), U32(Hv), U32(Hk)};
-  return Launch(eng, f32 ? "halo_gdn_chunk_scan_f32" : "halo_gdn_chunk_scan", D3(n_seq * Hv * 4), D3(256), a, err,
-                errlen);
+  const halo_arg a[] = {Ptr(k), Ptr(wy), Ptr(Gc), Ptr(chunks), Ptr(seqs), Ptr(state), Ptr(o), U32(Hv), U32(Hk)};
+  return Launch(eng, f32 ? "halo_gdn_wy_scan_f32" : "halo_gdn_wy_scan", D3(n_seq * Hv * 8), D3(512), a, err, errlen);
 }
 }  // namespace
 

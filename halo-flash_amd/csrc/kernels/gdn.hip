@@ -88,21 +88,28 @@ extern "C" __global__ void __launch_bounds__(256)
   }
 }
 
-// ---- chunked prefill (C = 64) over a ragged batch of sequences -----------------------------------------------
+// ---- chunked prefill (C = 64) over a ragged batch of sequences, on fp32 MFMA -----------------------------------
 // Within a chunk of C tokens with cumulative log-decay G_t (gamma_t = exp(G_t)) and initial state S0, the token
 // recurrence above is exactly (reference math comment src/kernels/core.hip:6035-6048, there with C = 16):
 //   (I + A) Delta = diag(beta) V - diag(beta gamma) K S0,   A[t][s] = beta_t exp(G_t - G_s) (k_t . k_s), s < t
 //   O = (diag(gamma) Q S0 + P Delta) / sqrt(d),             P[t][s] = exp(G_t - G_s) (q_t . k_s),         s <= t
 //   S_C = gamma_C S0 + K^T diag(exp(G_C - G_s)) Delta.
-// halo_gdn_chunk_prep computes, for every (chunk, head) in parallel, T = (I + A)^-1 (forward substitution), P and
-// G; halo_gdn_chunk_scan walks each sequence's chunks in order carrying S, with Delta = T Z and
-// Z = diag(beta) V - diag(beta gamma) (K S0). Tokens past a partial chunk's end are zero-padded (beta = 0, g = 0),
-// which makes them contribute nothing. Inputs q, k [tokens][Hk][128] and v [tokens][Hv][128] are bf16 (the C3 operator) or fp32 (the model's
-// prefill, which matches its decode step); g, beta
-// [tokens][Hv] fp32 (g = log decay, beta after its sigmoid); state fp32 [seq][Hv][128][128] key-major.
-// chunks [n][3] = {first token, length, sequence}; seqs [n_seq][2] = {first chunk, chunk count}.
+// With T = (I + A)^-1 this splits into what does not depend on the state (WY form, computed for every chunk in
+// parallel by halo_gdn_wy_prep):
+//   Uk = T diag(beta gamma) K,  Wv = T diag(beta) V,  Qe = diag(gamma) Q - P Uk,  Ov = P Wv      (64 x 128 each)
+// and the chunk-serial part (halo_gdn_wy_scan), three products per chunk:
+//   Delta = Wv - Uk S0,  O = (Qe S0 + Ov) / sqrt(d),  S_C = gamma_C S0 + K^T diag(exp(G_C - G_s)) Delta.
+// Tokens past a partial chunk's end are zero-padded (k = q = v = 0, beta = 0, g = 0): their rows of every product are
+// zero. Inputs q, k [tokens][Hk][128] and v [tokens][Hv][128] are bf16 (the C3 operator) or fp32 (the model's
+// prefill, which matches its decode step); g, beta [tokens][Hv] fp32 (g = log decay, beta after its sigmoid); state
+// fp32 [seq][Hv][128][128] key-major. chunks [n][3] = {first token, length, sequence}; seqs [n_seq][2] = {first
+// chunk, chunk count}. Workspace per (chunk, head): Uk, Qe, Wv, Ov fp32 [64][128] and G [64].
 namespace {
 constexpr int kC = 64;
+constexpr int kCL = 132;  // LDS row stride (floats) of a 64 x 128 tile
+constexpr int kPL = 68;   // of a 64 x 64 tile
+typedef float V16F __attribute__((ext_vector_type(16)));
+typedef float V4F __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float Bf(std::uint16_t h) { return __uint_as_float(static_cast<std::uint32_t>(h) << 16); }
 __device__ __forceinline__ float Cv(std::uint16_t h) { return Bf(h); }
@@ -116,238 +123,320 @@ template <typename In>
 __device__ __forceinline__ Pack8<In> Ld8(const In* p) {
   return *reinterpret_cast<const Pack8<In>*>(p);
 }
+// row r of a 64 x 128 LDS tile from 8 inputs: two float4 stores, zeros when !on
 template <typename In>
-__device__ __forceinline__ Pack8<In> Zero8() {
-  Pack8<In> z;
+__device__ __forceinline__ void Put8(float* dst, const Pack8<In>& x, bool on) {
+  float f[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) z.v[e] = In{};
-  return z;
+  for (int e = 0; e < 8; ++e) f[e] = on ? Cv(x.v[e]) : 0.0f;
+  reinterpret_cast<float4*>(dst)[0] = make_float4(f[0], f[1], f[2], f[3]);
+  reinterpret_cast<float4*>(dst)[1] = make_float4(f[4], f[5], f[6], f[7]);
 }
 }  // namespace
 
-// grid (n_chunks, Hv), block 256. Tm, Pm [n_chunks][Hv][64][64] fp32, Gc [n_chunks][Hv][64]. In: std::uint16_t
-// (bf16) or float.
+// grid (n_chunks, Hv), block 256 (4 waves). MFMA v_mfma_f32_32x32x2f32: A lane l = A[l % 32][k], B lane l =
+// B[k][l % 32] with k split in halves (lanes 0-31 the first half of the K range, 32-63 the second), D lane l holds
+// column l % 32 and rows 8 (r / 4) + 4 (l / 32) + r % 4. Wave w owns the 32 x 32 tile (w / 2, w % 2) of K K^T and
+// of Q K^T, then two 32-column tiles of each 64 x 128 product. T = (I + A)^-1 by forward substitution in wave 0,
+// one column per lane, in registers.
 template <typename In>
-__device__ __forceinline__ void ChunkPrep(const In* __restrict__ q, const In* __restrict__ k,
-                                          const float* __restrict__ g, const float* __restrict__ beta,
-                                          const std::uint32_t* __restrict__ chunks, float* __restrict__ Tm,
-                                          float* __restrict__ Pm, float* __restrict__ Gc, std::uint32_t Hv,
-                                          std::uint32_t Hk) {
-  __shared__ union {
-    struct {
-      In kb[kC][kD];
-      In qb[kC][kD];
-    } in;
-    float tm[kC][kC + 1];
-  } u;
-  __shared__ float am[kC][kC + 1];
-  __shared__ float G[kC], B[kC];
+__device__ __forceinline__ void WyPrep(const In* __restrict__ q, const In* __restrict__ k, const In* __restrict__ v,
+                                       const float* __restrict__ g, const float* __restrict__ beta,
+                                       const std::uint32_t* __restrict__ chunks, float* __restrict__ wy,
+                                       float* __restrict__ Gc, std::uint32_t Hv, std::uint32_t Hk) {
+  __shared__ __attribute__((aligned(16))) float kl[kC][kCL];
+  __shared__ __attribute__((aligned(16))) float ql[kC][kCL];
+  __shared__ __attribute__((aligned(16))) float vl[kC][kCL];
+  __shared__ __attribute__((aligned(16))) float am[kC][kPL];  // A, then T
+  __shared__ __attribute__((aligned(16))) float pm[kC][kPL];
+  __shared__ float G[kC], Bt[kC], Bg[kC], Gm[kC];
   const std::uint32_t c = blockIdx.x, h = blockIdx.y, kh = h % Hk, tid = threadIdx.x;
+  const std::uint32_t wave = tid / kWave, lane = tid % kWave, fr = lane % 32, hh = lane / 32;
   const std::uint32_t start = chunks[c * 3], L = chunks[c * 3 + 1];
   for (std::uint32_t idx = tid; idx < kC * (kD / 8); idx += blockDim.x) {
-    const std::uint32_t t = idx / (kD / 8), p = idx % (kD / 8);
-    Pack8<In> kv = Zero8<In>(), qv = Zero8<In>();
-    if (t < L) {
-      const std::size_t off = (static_cast<std::size_t>(start + t) * Hk + kh) * kD + p * 8;
-      kv = Ld8(k + off);
-      qv = Ld8(q + off);
-    }
-    *reinterpret_cast<Pack8<In>*>(&u.in.kb[t][p * 8]) = kv;
-    *reinterpret_cast<Pack8<In>*>(&u.in.qb[t][p * 8]) = qv;
+    const std::uint32_t t = idx / (kD / 8), p = idx % (kD / 8), tt = min(t, L - 1);
+    const bool on = t < L;
+    const std::size_t kq = (static_cast<std::size_t>(start + tt) * Hk + kh) * kD + p * 8;
+    const std::size_t vv = (static_cast<std::size_t>(start + tt) * Hv + h) * kD + p * 8;
+    Put8(&kl[t][p * 8], Ld8(k + kq), on);
+    Put8(&ql[t][p * 8], Ld8(q + kq), on);
+    Put8(&vl[t][p * 8], Ld8(v + vv), on);
   }
   if (tid < kC) {
-    const bool in = tid < L;
-    G[tid] = in ? g[static_cast<std::size_t>(start + tid) * Hv + h] : 0.0f;
-    B[tid] = in ? beta[static_cast<std::size_t>(start + tid) * Hv + h] : 0.0f;
+    const std::uint32_t tt = min(tid, L - 1);
+    const bool on = tid < L;
+    const float gv = g[static_cast<std::size_t>(start + tt) * Hv + h], bv = beta[static_cast<std::size_t>(start + tt) * Hv + h];
+    G[tid] = on ? gv : 0.0f;
+    Bt[tid] = on ? bv : 0.0f;
   }
   __syncthreads();
   if (tid == 0)
     for (int t = 1; t < kC; ++t) G[t] += G[t - 1];
   __syncthreads();
-  // A (strictly lower) and P (lower incl. diagonal); thread: row t, 16 columns
-  const std::size_t mat = (static_cast<std::size_t>(c) * Hv + h) * kC * kC;
-  {
-    const std::uint32_t t = tid / 4, s0 = (tid % 4) * 16;
-    float kk[16], qk[16];
+  if (tid < kC) {
+    Gm[tid] = expf(G[tid]);
+    Bg[tid] = Bt[tid] * expf(G[tid]);
+  }
+  // K K^T and Q K^T, tile (ti, tj) = (wave / 2, wave % 2), K range = 128 keys (step s: key s + 64 hh)
+  const std::uint32_t ti = wave / 2, tj = wave % 2;
+  V16F kk = {}, qk = {};
+#pragma unroll 4
+  for (int sb = 0; sb < 16; ++sb) {
+    const float4 ka = *reinterpret_cast<const float4*>(&kl[32 * ti + fr][4 * sb + 64 * hh]);
+    const float4 qa = *reinterpret_cast<const float4*>(&ql[32 * ti + fr][4 * sb + 64 * hh]);
+    const float4 kb = *reinterpret_cast<const float4*>(&kl[32 * tj + fr][4 * sb + 64 * hh]);
+    kk = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.x, kb.x, kk, 0, 0, 0);
+    qk = __builtin_amdgcn_mfma_f32_32x32x2f32(qa.x, kb.x, qk, 0, 0, 0);
+    kk = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.y, kb.y, kk, 0, 0, 0);
+    qk = __builtin_amdgcn_mfma_f32_32x32x2f32(qa.y, kb.y, qk, 0, 0, 0);
+    kk = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.z, kb.z, kk, 0, 0, 0);
+    qk = __builtin_amdgcn_mfma_f32_32x32x2f32(qa.z, kb.z, qk, 0, 0, 0);
+    kk = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.w, kb.w, kk, 0, 0, 0);
+    qk = __builtin_amdgcn_mfma_f32_32x32x2f32(qa.w, kb.w, qk, 0, 0, 0);
+  }
+  __syncthreads();  // Gm / Bg visible
 #pragma unroll
-    for (int j = 0; j < 16; ++j) kk[j] = qk[j] = 0.0f;
-    for (int i = 0; i < kD; i += 8) {
-      const Pack8<In> kt = Ld8(&u.in.kb[t][i]);
-      const Pack8<In> qt = Ld8(&u.in.qb[t][i]);
+  for (int r = 0; r < 16; ++r) {
+    const std::uint32_t t = 32 * ti + 8 * (r / 4) + 4 * hh + r % 4, s = 32 * tj + fr;
+    const bool low = s < t, leq = s <= t;
+    const float dec = expf(leq ? G[t] - G[s] : 0.0f);
+    am[t][s] = low ? Bt[t] * dec * kk[r] : 0.0f;
+    pm[t][s] = leq ? dec * qk[r] : 0.0f;
+  }
+  __syncthreads();
+  // T = (I + A)^-1: lane = column, rows in order; A rows are read as broadcasts, four partial sums per row
+  if (wave == 0) {
+    float T[kC];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const Pack8<In> ks = Ld8(&u.in.kb[s0 + j][i]);
+    for (int t = 0; t < kC; ++t) {
+      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float kse = Cv(ks.v[e]);
-          kk[j] += Cv(kt.v[e]) * kse;
-          qk[j] += Cv(qt.v[e]) * kse;
-        }
+      for (int s4 = 0; s4 < t; s4 += 4) {
+        const float4 ar = *reinterpret_cast<const float4*>(&am[t][s4]);
+        const float av[4] = {ar.x, ar.y, ar.z, ar.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (s4 + e < t) acc[e] = __builtin_fmaf(av[e], T[s4 + e], acc[e]);
+      }
+      const float sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+      T[t] = lane == static_cast<std::uint32_t>(t) ? 1.0f : -sum;
+    }
+    // every lane has read all of A above (program order within the wave); T replaces it
+#pragma unroll
+    for (int t = 0; t < kC; ++t) am[t][lane] = T[t];
+  }
+  __syncthreads();
+  // Uk = T diag(beta gamma) K and Wv = T diag(beta) V: wave w owns rows 32 ti, columns 32 (2 (w % 2) + u), u < 2;
+  // K range = 64 tokens (step s: token s + 32 hh)
+  float* out = wy + (static_cast<std::size_t>(c) * Hv + h) * 4 * kC * kD;  // Uk, Qe, Wv, Ov
+  V16F uk[2] = {{}, {}}, wv[2] = {{}, {}};
+#pragma unroll 2
+  for (int sb = 0; sb < 8; ++sb) {
+    const float4 ta = *reinterpret_cast<const float4*>(&am[32 * ti + fr][4 * sb + 32 * hh]);
+    const float tv[4] = {ta.x, ta.y, ta.z, ta.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const std::uint32_t tok = 4 * sb + e + 32 * hh;
+      const float bg = Bg[tok], bt = Bt[tok];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const std::uint32_t col = 32 * (2 * tj + u) + fr;
+        uk[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(tv[e], bg * kl[tok][col], uk[u], 0, 0, 0);
+        wv[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(tv[e], bt * vl[tok][col], wv[u], 0, 0, 0);
       }
     }
+  }
+  __syncthreads();  // K and V are no longer read: Uk and Wv take their places
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const std::uint32_t s = s0 + j;
-      const float dec = expf(G[t] - G[s]);
-      am[t][s] = s < t ? B[t] * dec * kk[j] : 0.0f;
-      Pm[mat + t * kC + s] = s <= t ? dec * qk[j] : 0.0f;
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const std::uint32_t t = 32 * ti + 8 * (r / 4) + 4 * hh + r % 4, col = 32 * (2 * tj + u) + fr;
+      kl[t][col] = uk[u][r];
+      vl[t][col] = wv[u][r];
+      out[0 * kC * kD + t * kD + col] = uk[u][r];
+      out[2 * kC * kD + t * kD + col] = wv[u][r];
+    }
+  __syncthreads();
+  // Qe = diag(gamma) Q - P Uk and Ov = P Wv
+  V16F qe[2], ov[2] = {{}, {}};
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const std::uint32_t t = 32 * ti + 8 * (r / 4) + 4 * hh + r % 4, col = 32 * (2 * tj + u) + fr;
+      qe[u][r] = Gm[t] * ql[t][col];
+    }
+#pragma unroll 2
+  for (int sb = 0; sb < 8; ++sb) {
+    const float4 pa = *reinterpret_cast<const float4*>(&pm[32 * ti + fr][4 * sb + 32 * hh]);
+    const float pv[4] = {pa.x, pa.y, pa.z, pa.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const std::uint32_t tok = 4 * sb + e + 32 * hh;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const std::uint32_t col = 32 * (2 * tj + u) + fr;
+        qe[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(-pv[e], kl[tok][col], qe[u], 0, 0, 0);
+        ov[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(pv[e], vl[tok][col], ov[u], 0, 0, 0);
+      }
     }
   }
-  __syncthreads();
-  // T = (I + A)^-1 by rows: T[t][c] = -sum_{s=c}^{t-1} A[t][s] T[s][c] (c < t), 1 on the diagonal. One wave; LDS
-  // accesses of a wave complete in order, so rows need no block barrier.
-  if (tid < kC) {
-    const std::uint32_t col = tid;
-    for (std::uint32_t t = 0; t < kC; ++t) {
-      float v = col == t ? 1.0f : 0.0f;
-      if (col < t)
-        for (std::uint32_t s = col; s < t; ++s) v -= am[t][s] * u.tm[s][col];
-      u.tm[t][col] = v;
-      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
-      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const std::uint32_t t = 32 * ti + 8 * (r / 4) + 4 * hh + r % 4, col = 32 * (2 * tj + u) + fr;
+      out[1 * kC * kD + t * kD + col] = qe[u][r];
+      out[3 * kC * kD + t * kD + col] = ov[u][r];
     }
-  }
-  __syncthreads();
-  for (std::uint32_t e = tid; e < kC * kC; e += blockDim.x) Tm[mat + e] = u.tm[e / kC][e % kC];
   if (tid < kC) Gc[(static_cast<std::size_t>(c) * Hv + h) * kC + tid] = G[tid];
 }
 
-// grid (n_seq * Hv * 4), block 256: block -> (sequence, head, 32 value columns); walks the sequence's chunks.
-// o [tokens][Hv][128] fp32; state [seq][Hv][128][128] read as the initial state and overwritten with the final one.
+// grid (n_seq * Hv * 8), block 512 (8 waves): block -> (sequence, head, 16 value columns [16 cb, 16 cb + 16)); walks
+// the sequence's chunks carrying its 128 x 16 slice of S in LDS. MFMA v_mfma_f32_16x16x4f32: A lane l = A[l % 16][k],
+// B lane l = B[k][l % 16] with k = 4 s + l / 16 at step s, D lane l holds column l % 16 and rows 4 (l / 16) + r.
+// Per chunk: waves 0-3 form Delta rows 16 w .. + 16 (= Wv - Uk S0), waves 4-7 the output rows (Qe S0 + Ov); then
+// wave w updates S rows 16 w .. + 16. The next chunk's operands are loaded into registers during the current one.
 template <typename In>
-__device__ __forceinline__ void ChunkScan(
-    const In* __restrict__ q, const In* __restrict__ k, const In* __restrict__ v, const float* __restrict__ beta, const std::uint32_t* __restrict__ chunks, const std::uint32_t* __restrict__ seqs,
-    const float* __restrict__ Tm, const float* __restrict__ Pm, const float* __restrict__ Gc,
-    float* __restrict__ state, float* __restrict__ o, std::uint32_t Hv, std::uint32_t Hk) {
-  __shared__ float S0[kD][kJBlock];
-  __shared__ float Zd[kC][kJBlock + 1];
-  __shared__ float tm[kC][kC];
-  __shared__ float pm[kC][kC];
-  __shared__ float G[kC], Bt[kC], Wd[kC];
-  const std::uint32_t b = blockIdx.x, jb = b % 4, h = (b / 4) % Hv, sq = b / (4 * Hv), kh = h % Hk;
-  const std::uint32_t tid = threadIdx.x;
+__device__ __forceinline__ void WyScan(const In* __restrict__ k, const float* __restrict__ wy,
+                                       const float* __restrict__ Gc, const std::uint32_t* __restrict__ chunks,
+                                       const std::uint32_t* __restrict__ seqs, float* __restrict__ state,
+                                       float* __restrict__ o, std::uint32_t Hv, std::uint32_t Hk) {
+  constexpr int kNC = 16, kSL = 20;
+  __shared__ __attribute__((aligned(16))) float ukl[kC][kCL];
+  __shared__ __attribute__((aligned(16))) float qel[kC][kCL];
+  __shared__ __attribute__((aligned(16))) float kxl[kC][kCL];
+  __shared__ __attribute__((aligned(16))) float wvl[kC][kSL];
+  __shared__ __attribute__((aligned(16))) float ovl[kC][kSL];
+  __shared__ __attribute__((aligned(16))) float Sl[kD][kSL];
+  __shared__ __attribute__((aligned(16))) float Dl[kC][kSL];
+  __shared__ float Gl[kC];
+  const std::uint32_t b = blockIdx.x, cb = b % 8, h = (b / 8) % Hv, sq = b / (8 * Hv), kh = h % Hk;
+  const std::uint32_t tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave, fc = lane % 16, fq = lane / 16;
+  const std::uint32_t j0 = cb * kNC;
   const std::uint32_t c0 = seqs[sq * 2], nc = seqs[sq * 2 + 1];
   float* St = state + (static_cast<std::size_t>(sq) * Hv + h) * kD * kD;
-  for (std::uint32_t e = tid; e < kD * kJBlock; e += blockDim.x)
-    S0[e / kJBlock][e % kJBlock] = St[static_cast<std::size_t>(e / kJBlock) * kD + jb * kJBlock + e % kJBlock];
-  const std::uint32_t t = tid / 4, jg = tid % 4;             // rows of the chunk x 8 columns
-  const std::uint32_t si = tid % kD, sh = tid / kD;          // state row x 16 columns
-  const float qscale = 1.0f / sqrtf(static_cast<float>(kD));
+  // S slice: 128 rows x 16 columns = 512 float4, one per thread
+  {
+    const std::uint32_t r = tid / 4, p = tid % 4;
+    *reinterpret_cast<float4*>(&Sl[r][4 * p]) = *reinterpret_cast<const float4*>(St + static_cast<std::size_t>(r) * kD + j0 + 4 * p);
+  }
+  // staged operands of one chunk, in registers: Uk, Qe (8192 floats each: 4 float4 per thread), K (8192 inputs: two
+  // packs of 8), the Wv or Ov slice (64 x 16: threads < 256 Wv, the rest Ov, one float4 each) and G (threads < 64)
+  float4 ru0, ru1, ru2, ru3, rq0, rq1, rq2, rq3, rwo;
+  Pack8<In> rk0, rk1;
+  float rg;
+  auto load = [&](std::uint32_t c) {
+    const float4* bu = reinterpret_cast<const float4*>(wy + (static_cast<std::size_t>(c) * Hv + h) * 4 * kC * kD);
+    const float4* bq = bu + kC * kD / 4;
+    ru0 = bu[tid], ru1 = bu[tid + 512], ru2 = bu[tid + 1024], ru3 = bu[tid + 1536];
+    rq0 = bq[tid], rq1 = bq[tid + 512], rq2 = bq[tid + 1024], rq3 = bq[tid + 1536];
+    const std::uint32_t start = chunks[c * 3], L = chunks[c * 3 + 1];
+    const std::uint32_t t0 = tid / 16, p8 = 8 * (tid % 16);  // packs tid and tid + 512: rows t0 and t0 + 32
+    rk0 = Ld8(k + (static_cast<std::size_t>(start + min(t0, L - 1)) * Hk + kh) * kD + p8);
+    rk1 = Ld8(k + (static_cast<std::size_t>(start + min(t0 + 32, L - 1)) * Hk + kh) * kD + p8);
+    const std::uint32_t e = tid % 256;
+    const float* src = reinterpret_cast<const float*>(bu) + (tid < 256 ? 2 : 3) * kC * kD;
+    rwo = *reinterpret_cast<const float4*>(src + (e / 4) * kD + j0 + 4 * (e % 4));
+    rg = Gc[(static_cast<std::size_t>(c) * Hv + h) * kC + tid % kC];
+  };
+  auto store = [&](std::uint32_t c) {
+    const std::uint32_t L = chunks[c * 3 + 1];
+    // float4 e = tid + 512 i of a 64 x 128 tile is row e / 32 = tid / 32 + 16 i, column 4 (tid % 32)
+    const std::uint32_t t0 = tid / 32, p4 = 4 * (tid % 32);
+    *reinterpret_cast<float4*>(&ukl[t0][p4]) = ru0;
+    *reinterpret_cast<float4*>(&ukl[t0 + 16][p4]) = ru1;
+    *reinterpret_cast<float4*>(&ukl[t0 + 32][p4]) = ru2;
+    *reinterpret_cast<float4*>(&ukl[t0 + 48][p4]) = ru3;
+    *reinterpret_cast<float4*>(&qel[t0][p4]) = rq0;
+    *reinterpret_cast<float4*>(&qel[t0 + 16][p4]) = rq1;
+    *reinterpret_cast<float4*>(&qel[t0 + 32][p4]) = rq2;
+    *reinterpret_cast<float4*>(&qel[t0 + 48][p4]) = rq3;
+    const std::uint32_t tk = tid / 16, pk = 8 * (tid % 16);
+    Put8(&kxl[tk][pk], rk0, tk < L);
+    Put8(&kxl[tk + 32][pk], rk1, tk + 32 < L);
+    const std::uint32_t e = tid % 256;
+    float(*dst)[kSL] = tid < 256 ? wvl : ovl;
+    *reinterpret_cast<float4*>(&dst[e / 4][4 * (e % 4)]) = rwo;
+    if (tid < kC) Gl[tid] = rg;
+  };
+  const float inv_sqrt_d = 1.0f / sqrtf(static_cast<float>(kD));
+  // one register set: chunk ci's operands go to LDS, then chunk ci + 1's loads are in flight during ci's products
+  if (nc > 0) load(c0);
   for (std::uint32_t ci = 0; ci < nc; ++ci) {
     const std::uint32_t c = c0 + ci, start = chunks[c * 3], L = chunks[c * 3 + 1];
-    const std::size_t mat = (static_cast<std::size_t>(c) * Hv + h) * kC * kC;
+    store(c);
     __syncthreads();
-    for (std::uint32_t e = tid * 4; e < kC * kC; e += blockDim.x * 4) {
-      *reinterpret_cast<float4*>(&tm[0][0] + e) = *reinterpret_cast<const float4*>(Tm + mat + e);
-      *reinterpret_cast<float4*>(&pm[0][0] + e) = *reinterpret_cast<const float4*>(Pm + mat + e);
-    }
-    if (tid < kC) {
-      G[tid] = Gc[(static_cast<std::size_t>(c) * Hv + h) * kC + tid];
-      Bt[tid] = tid < L ? beta[static_cast<std::size_t>(start + tid) * Hv + h] : 0.0f;
-    }
-    __syncthreads();
-    if (tid < kC) Wd[tid] = expf(G[kC - 1] - G[tid]);
-    // X = K S0, Y = Q S0 (row t, 8 columns)
-    float X[8], Y[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) X[j] = Y[j] = 0.0f;
-    const bool live = t < L;
-    const std::size_t krow = (static_cast<std::size_t>(start + t) * Hk + kh) * kD;
-    for (int i = 0; i < kD; i += 8) {
-      Pack8<In> kv = Zero8<In>(), qv = Zero8<In>();
-      if (live) {
-        kv = Ld8(k + krow + i);
-        qv = Ld8(q + krow + i);
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float ke = Cv(kv.v[e]), qe = Cv(qv.v[e]);
-        const float4 s_lo = *reinterpret_cast<const float4*>(&S0[i + e][jg * 8]);
-        const float4 s_hi = *reinterpret_cast<const float4*>(&S0[i + e][jg * 8 + 4]);
-        X[0] += ke * s_lo.x; X[1] += ke * s_lo.y; X[2] += ke * s_lo.z; X[3] += ke * s_lo.w;
-        X[4] += ke * s_hi.x; X[5] += ke * s_hi.y; X[6] += ke * s_hi.z; X[7] += ke * s_hi.w;
-        Y[0] += qe * s_lo.x; Y[1] += qe * s_lo.y; Y[2] += qe * s_lo.z; Y[3] += qe * s_lo.w;
-        Y[4] += qe * s_hi.x; Y[5] += qe * s_hi.y; Y[6] += qe * s_hi.z; Y[7] += qe * s_hi.w;
-      }
-    }
-    const float gam = expf(G[t]);
+    load(ci + 1 < nc ? c + 1 : c);  // unconditional (the last chunk reloads itself): no loads under a branch
+    // Delta (waves 0-3) or the output (waves 4-7): rows 16 (w % 4) .. + 16, K range = 128 keys
     {
-      Pack8<In> vv = Zero8<In>();
-      if (live) vv = Ld8(v + (static_cast<std::size_t>(start + t) * Hv + h) * kD + jb * kJBlock + jg * 8);
+      const std::uint32_t r0 = 16 * (wave % 4);
+      float(*A)[kCL] = wave < 4 ? ukl : qel;
+      V4F acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 8
+      for (int s = 0; s < kD / 4; ++s)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[r0 + fc][4 * s + fq], Sl[4 * s + fq][fc], acc, 0, 0, 0);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) Zd[t][jg * 8 + j] = Bt[t] * (Cv(vv.v[j]) - gam * X[j]);
-    }
-    __syncthreads();
-    float D[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) D[j] = 0.0f;
-    for (std::uint32_t s = 0; s <= t; ++s) {
-      const float w = tm[t][s];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) D[j] += w * Zd[s][jg * 8 + j];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < 8; ++j) Zd[t][jg * 8 + j] = D[j];
-    __syncthreads();
-    if (live) {
-      float O[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) O[j] = gam * Y[j];
-      for (std::uint32_t s = 0; s <= t; ++s) {
-        const float w = pm[t][s];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) O[j] += w * Zd[s][jg * 8 + j];
+      for (int i = 0; i < 4; ++i) {
+        const std::uint32_t t = r0 + 4 * fq + i;
+        if (wave < 4) {
+          Dl[t][fc] = wvl[t][fc] - acc[i];
+        } else if (t < L) {
+          o[(static_cast<std::size_t>(start + t) * Hv + h) * kD + j0 + fc] = (acc[i] + ovl[t][fc]) * inv_sqrt_d;
+        }
       }
-      float* orow = o + (static_cast<std::size_t>(start + t) * Hv + h) * kD + jb * kJBlock + jg * 8;
-      *reinterpret_cast<float4*>(orow) = make_float4(O[0] * qscale, O[1] * qscale, O[2] * qscale, O[3] * qscale);
-      *reinterpret_cast<float4*>(orow + 4) = make_float4(O[4] * qscale, O[5] * qscale, O[6] * qscale, O[7] * qscale);
     }
-    // S <- gamma_C S + K^T diag(exp(G_C - G_t)) Delta   (row si, 16 columns)
-    const float gc = expf(G[kC - 1]);
-    float acc[16];
+    __syncthreads();
+    // S rows 16 w .. + 16: gamma_C S + (K diag(exp(G_C - G_t)))^T Delta, K range = 64 tokens
+    {
+      const std::uint32_t r0 = 16 * wave;
+      const float GC = Gl[kC - 1], gc = expf(GC);
+      V4F acc;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) acc[j] = gc * S0[si][sh * 16 + j];
-    for (std::uint32_t tt = 0; tt < L; ++tt) {
-      const float w = Cv(k[(static_cast<std::size_t>(start + tt) * Hk + kh) * kD + si]) * Wd[tt];
+      for (int i = 0; i < 4; ++i) acc[i] = gc * Sl[r0 + 4 * fq + i][fc];
+#pragma unroll 4
+      for (int s = 0; s < kC / 4; ++s) {
+        const std::uint32_t tok = 4 * s + fq;
+        const float a = kxl[tok][r0 + fc] * expf(GC - Gl[tok]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, Dl[tok][fc], acc, 0, 0, 0);
+      }
 #pragma unroll
-      for (int j = 0; j < 16; ++j) acc[j] += w * Zd[tt][sh * 16 + j];
+      for (int i = 0; i < 4; ++i) Sl[r0 + 4 * fq + i][fc] = acc[i];
     }
-#pragma unroll
-    for (int j = 0; j < 16; ++j) S0[si][sh * 16 + j] = acc[j];
+    __syncthreads();
   }
-  __syncthreads();
-  for (std::uint32_t e = tid; e < kD * kJBlock; e += blockDim.x)
-    St[static_cast<std::size_t>(e / kJBlock) * kD + jb * kJBlock + e % kJBlock] = S0[e / kJBlock][e % kJBlock];
+  {
+    const std::uint32_t r = tid / 4, p = tid % 4;
+    *reinterpret_cast<float4*>(St + static_cast<std::size_t>(r) * kD + j0 + 4 * p) = *reinterpret_cast<const float4*>(&Sl[r][4 * p]);
+  }
 }
 
 extern "C" __global__ void __launch_bounds__(256)
-    halo_gdn_chunk_prep(const std::uint16_t* __restrict__ q, const std::uint16_t* __restrict__ k,
-                        const float* __restrict__ g, const float* __restrict__ beta,
-                        const std::uint32_t* __restrict__ chunks, float* __restrict__ Tm, float* __restrict__ Pm,
-                        float* __restrict__ Gc, std::uint32_t Hv, std::uint32_t Hk) {
-  ChunkPrep(q, k, g, beta, chunks, Tm, Pm, Gc, Hv, Hk);
+    halo_gdn_wy_prep(const std::uint16_t* __restrict__ q, const std::uint16_t* __restrict__ k,
+                     const std::uint16_t* __restrict__ v, const float* __restrict__ g, const float* __restrict__ beta,
+                     const std::uint32_t* __restrict__ chunks, float* __restrict__ wy, float* __restrict__ Gc,
+                     std::uint32_t Hv, std::uint32_t Hk) {
+  WyPrep(q, k, v, g, beta, chunks, wy, Gc, Hv, Hk);
 }
 extern "C" __global__ void __launch_bounds__(256)
-    halo_gdn_chunk_prep_f32(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ g,
-                            const float* __restrict__ beta, const std::uint32_t* __restrict__ chunks,
-                            float* __restrict__ Tm, float* __restrict__ Pm, float* __restrict__ Gc, std::uint32_t Hv,
-                            std::uint32_t Hk) {
-  ChunkPrep(q, k, g, beta, chunks, Tm, Pm, Gc, Hv, Hk);
+    halo_gdn_wy_prep_f32(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+                         const float* __restrict__ g, const float* __restrict__ beta,
+                         const std::uint32_t* __restrict__ chunks, float* __restrict__ wy, float* __restrict__ Gc,
+                         std::uint32_t Hv, std::uint32_t Hk) {
+  WyPrep(q, k, v, g, beta, chunks, wy, Gc, Hv, Hk);
 }
-extern "C" __global__ void __launch_bounds__(256) halo_gdn_chunk_scan(
-    const std::uint16_t* __restrict__ q, const std::uint16_t* __restrict__ k, const std::uint16_t* __restrict__ v,
-    const float* __restrict__ beta, const std::uint32_t* __restrict__ chunks, const std::uint32_t* __restrict__ seqs,
-    const float* __restrict__ Tm, const float* __restrict__ Pm, const float* __restrict__ Gc,
-    float* __restrict__ state, float* __restrict__ o, std::uint32_t Hv, std::uint32_t Hk) {
-  ChunkScan(q, k, v, beta, chunks, seqs, Tm, Pm, Gc, state, o, Hv, Hk);
+extern "C" __global__ void __launch_bounds__(512)
+    halo_gdn_wy_scan(const std::uint16_t* __restrict__ k, const float* __restrict__ wy, const float* __restrict__ Gc,
+                     const std::uint32_t* __restrict__ chunks, const std::uint32_t* __restrict__ seqs,
+                     float* __restrict__ state, float* __restrict__ o, std::uint32_t Hv, std::uint32_t Hk) {
+  WyScan(k, wy, Gc, chunks, seqs, state, o, Hv, Hk);
 }
-extern "C" __global__ void __launch_bounds__(256) halo_gdn_chunk_scan_f32(
-    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-    const float* __restrict__ beta, const std::uint32_t* __restrict__ chunks, const std::uint32_t* __restrict__ seqs,
-    const float* __restrict__ Tm, const float* __restrict__ Pm, const float* __restrict__ Gc,
-    float* __restrict__ state, float* __restrict__ o, std::uint32_t Hv, std::uint32_t Hk) {
-  ChunkScan(q, k, v, beta, chunks, seqs, Tm, Pm, Gc, state, o, Hv, Hk);
+extern "C" __global__ void __launch_bounds__(512)
+    halo_gdn_wy_scan_f32(const float* __restrict__ k, const float* __restrict__ wy, const float* __restrict__ Gc,
+                         const std::uint32_t* __restrict__ chunks, const std::uint32_t* __restrict__ seqs,
+                         float* __restrict__ state, float* __restrict__ o, std::uint32_t Hv, std::uint32_t Hk) {
+  WyScan(k, wy, Gc, chunks, seqs, state, o, Hv, Hk);
 }
 
 // ---- the whole DeltaNet token step of the decode graph, one block per (session, value head) -----------------

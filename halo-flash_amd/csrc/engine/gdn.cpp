@@ -57,7 +57,7 @@ int GdnPrefill(halo_engine* eng, bool f32, const void* q, const void* k, const v
       return -1;
   }
   const halo_arg a[] = {Ptr(k), Ptr(wy), Ptr(Gc), Ptr(chunks), Ptr(seqs), Ptr(state), Ptr(o), U32(Hv), U32(Hk)};
-  return Launch(eng, f32 ? "halo_gdn_wy_scan_f32" : "halo_gdn_wy_scan", D3(n_seq * Hv * 8), D3(512), a, err, errlen);
+  return Launch(eng, f32 ? "halo_gdn_wy_scan_f32" : "halo_gdn_wy_scan", D3(n_seq * Hv * 4), D3(512), a, err, errlen);
 }
 }  // namespace
 

@@ -151,6 +151,12 @@ __device__ __forceinline__ float Normal(std::uint64_t key) {
 // A 32-value Q8 block is the 4 chunks of 4 consecutive lanes (a DPP quad).
 namespace halo {
 
+// Block barrier for LDS traffic only: waits for this wave's LDS operations, then s_barrier. Unlike __syncthreads()
+// (whose workgroup release fence also waits for every outstanding global load and store), loads issued ahead into
+// registers stay in flight across it. Only for exchanges through LDS; the "memory" clobber keeps the compiler from
+// moving memory accesses across it.
+__device__ __forceinline__ void LdsSync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 template <int KC>
 struct Row8 {
   float v[KC][8];

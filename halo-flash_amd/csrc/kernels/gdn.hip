@@ -293,56 +293,104 @@ __device__ __forceinline__ void WyPrep(const In* __restrict__ q, const In* __res
   if (tid < kC) Gc[(static_cast<std::size_t>(c) * Hv + h) * kC + tid] = G[tid];
 }
 
-// grid (n_seq * Hv * 8), block 512 (8 waves): block -> (sequence, head, 16 value columns [16 cb, 16 cb + 16)); walks
-// the sequence's chunks carrying its 128 x 16 slice of S in LDS. MFMA v_mfma_f32_16x16x4f32: A lane l = A[l % 16][k],
-// B lane l = B[k][l % 16] with k = 4 s + l / 16 at step s, D lane l holds column l % 16 and rows 4 (l / 16) + r.
-// Per chunk: waves 0-3 form Delta rows 16 w .. + 16 (= Wv - Uk S0), waves 4-7 the output rows (Qe S0 + Ov); then
-// wave w updates S rows 16 w .. + 16. The next chunk's operands are loaded into registers during the current one.
-template <typename In>
+// grid (n_seq * Hv * 128 / kNC), block 512 (8 waves): block -> (sequence, head, kNC value columns); walks
+// the sequence's chunks carrying its 128 x kNC slice of S in LDS. kNC = 32 (four blocks per head): each chunk's Uk,
+// Qe and K are read by four blocks (measured on C3: 16 columns per block 910 us, 32 878 us, 64 1339 us; narrower
+// slices re-read more, wider ones leave fewer waves per head for the chunk-serial MFMA work).
+// MFMA v_mfma_f32_16x16x4f32 (A lane l = A[l % 16][k], B lane l = B[k][l % 16], D lane l holds column l % 16 and
+// rows 4 (l / 16) + r) with each lane's k contiguous: lane quarter fq takes k in [K/4 fq, K/4 (fq + 1)), so every
+// operand read is 16 bytes (4 steps); a wave's four column tiles are four independent accumulator chains. The LDS
+// tiles that serve as B or as a transposed A are stored transposed: S as st[column][key], Delta as dt[column][token],
+// K as kt[key][token] (kt reuses Uk's space once Uk has been read).
+// Per chunk: waves 0-3 form Delta rows 16 w .. + 16 (= Wv - Uk S0), waves 4-7 the output rows (Qe S0 + Ov), four
+// 16-column tiles each; then wave w updates S rows 16 w .. + 16. The next chunk's operands are loaded into registers
+// during the current one; the block barriers inside the chunk loop synchronize LDS only, so those loads stay in
+// flight across them.
+template <typename In, int kNC>
 __device__ __forceinline__ void WyScan(const In* __restrict__ k, const float* __restrict__ wy,
                                        const float* __restrict__ Gc, const std::uint32_t* __restrict__ chunks,
                                        const std::uint32_t* __restrict__ seqs, float* __restrict__ state,
                                        float* __restrict__ o, std::uint32_t Hv, std::uint32_t Hk) {
-  constexpr int kNC = 16, kSL = 20;
-  __shared__ __attribute__((aligned(16))) float ukl[kC][kCL];
+  constexpr int kNB = kD / kNC, kNT = kNC / 16, kTL = kC + 4, kStL = kD + 4, kWL = kNC + 4;
+  constexpr int kUkF = kC * kCL, kKtF = kD * kTL, kAF = kUkF > kKtF ? kUkF : kKtF;
+  __shared__ __attribute__((aligned(16))) float ua[kAF];       // Uk [64][kCL], then K^T [128][kTL]
   __shared__ __attribute__((aligned(16))) float qel[kC][kCL];
-  __shared__ __attribute__((aligned(16))) float kxl[kC][kCL];
-  __shared__ __attribute__((aligned(16))) float wvl[kC][kSL];
-  __shared__ __attribute__((aligned(16))) float ovl[kC][kSL];
-  __shared__ __attribute__((aligned(16))) float Sl[kD][kSL];
-  __shared__ __attribute__((aligned(16))) float Dl[kC][kSL];
-  __shared__ float Gl[kC];
-  const std::uint32_t b = blockIdx.x, cb = b % 8, h = (b / 8) % Hv, sq = b / (8 * Hv), kh = h % Hk;
+  __shared__ __attribute__((aligned(16))) float st[kNC][kStL];  // S^T slice: [column][key]
+  __shared__ __attribute__((aligned(16))) float dt[kNC][kTL];   // Delta^T slice: [column][token]
+  __shared__ __attribute__((aligned(16))) float wvl[kC][kWL];
+  __shared__ __attribute__((aligned(16))) float ovl[kC][kWL];
+  __shared__ __attribute__((aligned(16))) float Gl[kC], Wl[kC];
+  float(*ukl)[kCL] = reinterpret_cast<float(*)[kCL]>(ua);
+  float(*kt)[kTL] = reinterpret_cast<float(*)[kTL]>(ua);
+  // Blocks are dispatched in id order and a block's LDS leaves room for one per CU, so the longest sequences take
+  // the lowest ids (rank by descending chunk count, ties by index; up to 64 sequences, else in order): the chunk-
+  // serial critical path starts first.
+  __shared__ std::uint32_t sq_s;
+  const std::uint32_t b = blockIdx.x, cb = b % kNB, h = (b / kNB) % Hv, rank = b / (kNB * Hv);
+  const std::uint32_t n_seq = gridDim.x / (kNB * Hv);
+  if (threadIdx.x == 0) {
+    std::uint32_t pick = rank;
+    if (n_seq <= 64) {
+      for (std::uint32_t j = 0; j < n_seq; ++j) {
+        const std::uint32_t cj = seqs[j * 2 + 1];
+        std::uint32_t r = 0;
+        for (std::uint32_t i = 0; i < n_seq; ++i) {
+          const std::uint32_t ci = seqs[i * 2 + 1];
+          r += (ci > cj) || (ci == cj && i < j);
+        }
+        if (r == rank) pick = j;
+      }
+    }
+    sq_s = pick;
+  }
+  __syncthreads();
+  const std::uint32_t sq = sq_s, kh = h % Hk;
   const std::uint32_t tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave, fc = lane % 16, fq = lane / 16;
   const std::uint32_t j0 = cb * kNC;
   const std::uint32_t c0 = seqs[sq * 2], nc = seqs[sq * 2 + 1];
-  float* St = state + (static_cast<std::size_t>(sq) * Hv + h) * kD * kD;
-  // S slice: 128 rows x 16 columns = 512 float4, one per thread
-  {
-    const std::uint32_t r = tid / 4, p = tid % 4;
-    *reinterpret_cast<float4*>(&Sl[r][4 * p]) = *reinterpret_cast<const float4*>(St + static_cast<std::size_t>(r) * kD + j0 + 4 * p);
+  // a sequence's chunks are consecutive 64-token runs: chunk ci starts at first + 64 ci and holds
+  // min(64, len - 64 ci) tokens (no chunk-table read per chunk: those scalar loads sat on the serial path)
+  const std::uint32_t first = nc ? chunks[c0 * 3] : 0u;
+  const std::uint32_t len = nc ? chunks[(c0 + nc - 1) * 3] + chunks[(c0 + nc - 1) * 3 + 1] - first : 0u;
+  float* Sg = state + (static_cast<std::size_t>(sq) * Hv + h) * kD * kD;
+  // S slice into st: 128 keys x kNC columns, kNC / 16 float4 per thread (key (tid / (kNC / 4)) + (2048 / kNC) i,
+  // columns 4 (tid % (kNC / 4)))
+#pragma unroll
+  for (int i = 0; i < kNT; ++i) {
+    const std::uint32_t r = tid / (kNC / 4) + (2048 / kNC) * i, p = tid % (kNC / 4);
+    const float4 v4 = *reinterpret_cast<const float4*>(Sg + static_cast<std::size_t>(r) * kD + j0 + 4 * p);
+    st[4 * p][r] = v4.x, st[4 * p + 1][r] = v4.y, st[4 * p + 2][r] = v4.z, st[4 * p + 3][r] = v4.w;
   }
-  // staged operands of one chunk, in registers: Uk, Qe (8192 floats each: 4 float4 per thread), K (8192 inputs: two
-  // packs of 8), the Wv or Ov slice (64 x 16: threads < 256 Wv, the rest Ov, one float4 each) and G (threads < 64)
-  float4 ru0, ru1, ru2, ru3, rq0, rq1, rq2, rq3, rwo;
+  // staged operands of one chunk, in registers: Uk, Qe (8192 floats each: 4 float4 per thread), the Wv and Ov slices
+  // (64 x 64 each: rows tid / 16 and tid / 16 + 32, columns 4 (tid % 16)), G (threads < 64); K (8192 inputs: two
+  // packs of 8) on its own, since it is stored later in the chunk
+  float4 ru0, ru1, ru2, ru3, rq0, rq1, rq2, rq3, rw[kNC / 32], ro[kNC / 32];
   Pack8<In> rk0, rk1;
   float rg;
-  auto load = [&](std::uint32_t c) {
-    const float4* bu = reinterpret_cast<const float4*>(wy + (static_cast<std::size_t>(c) * Hv + h) * 4 * kC * kD);
-    const float4* bq = bu + kC * kD / 4;
+  auto load = [&](std::uint32_t ci) {
+    const std::uint32_t c = c0 + ci;
+    const float* base = wy + (static_cast<std::size_t>(c) * Hv + h) * 4 * kC * kD;
+    const float4* bu = reinterpret_cast<const float4*>(base);
+    const float4* bq = reinterpret_cast<const float4*>(base + kC * kD);
     ru0 = bu[tid], ru1 = bu[tid + 512], ru2 = bu[tid + 1024], ru3 = bu[tid + 1536];
     rq0 = bq[tid], rq1 = bq[tid + 512], rq2 = bq[tid + 1024], rq3 = bq[tid + 1536];
-    const std::uint32_t start = chunks[c * 3], L = chunks[c * 3 + 1];
+    const std::uint32_t t = tid / (kNC / 4), p = 4 * (tid % (kNC / 4));
+    const float* bw = base + 2 * kC * kD + j0 + p;
+    const float* bo = base + 3 * kC * kD + j0 + p;
+#pragma unroll
+    for (int i = 0; i < kNC / 32; ++i) {
+      rw[i] = *reinterpret_cast<const float4*>(bw + (t + (2048 / kNC) * i) * kD);
+      ro[i] = *reinterpret_cast<const float4*>(bo + (t + (2048 / kNC) * i) * kD);
+    }
+    rg = Gc[(static_cast<std::size_t>(c) * Hv + h) * kC + tid % kC];
+  };
+  auto load_k = [&](std::uint32_t ci) {
+    const std::uint32_t start = first + 64 * ci, L = min(64u, len - 64 * ci);
     const std::uint32_t t0 = tid / 16, p8 = 8 * (tid % 16);  // packs tid and tid + 512: rows t0 and t0 + 32
     rk0 = Ld8(k + (static_cast<std::size_t>(start + min(t0, L - 1)) * Hk + kh) * kD + p8);
     rk1 = Ld8(k + (static_cast<std::size_t>(start + min(t0 + 32, L - 1)) * Hk + kh) * kD + p8);
-    const std::uint32_t e = tid % 256;
-    const float* src = reinterpret_cast<const float*>(bu) + (tid < 256 ? 2 : 3) * kC * kD;
-    rwo = *reinterpret_cast<const float4*>(src + (e / 4) * kD + j0 + 4 * (e % 4));
-    rg = Gc[(static_cast<std::size_t>(c) * Hv + h) * kC + tid % kC];
   };
-  auto store = [&](std::uint32_t c) {
-    const std::uint32_t L = chunks[c * 3 + 1];
+  auto store = [&]() {
     // float4 e = tid + 512 i of a 64 x 128 tile is row e / 32 = tid / 32 + 16 i, column 4 (tid % 32)
     const std::uint32_t t0 = tid / 32, p4 = 4 * (tid % 32);
     *reinterpret_cast<float4*>(&ukl[t0][p4]) = ru0;
@@ -353,62 +401,112 @@ __device__ __forceinline__ void WyScan(const In* __restrict__ k, const float* __
     *reinterpret_cast<float4*>(&qel[t0 + 16][p4]) = rq1;
     *reinterpret_cast<float4*>(&qel[t0 + 32][p4]) = rq2;
     *reinterpret_cast<float4*>(&qel[t0 + 48][p4]) = rq3;
-    const std::uint32_t tk = tid / 16, pk = 8 * (tid % 16);
-    Put8(&kxl[tk][pk], rk0, tk < L);
-    Put8(&kxl[tk + 32][pk], rk1, tk + 32 < L);
-    const std::uint32_t e = tid % 256;
-    float(*dst)[kSL] = tid < 256 ? wvl : ovl;
-    *reinterpret_cast<float4*>(&dst[e / 4][4 * (e % 4)]) = rwo;
+    const std::uint32_t t = tid / (kNC / 4), p = 4 * (tid % (kNC / 4));
+#pragma unroll
+    for (int i = 0; i < kNC / 32; ++i) {
+      *reinterpret_cast<float4*>(&wvl[t + (2048 / kNC) * i][p]) = rw[i];
+      *reinterpret_cast<float4*>(&ovl[t + (2048 / kNC) * i][p]) = ro[i];
+    }
     if (tid < kC) Gl[tid] = rg;
   };
+  auto store_k = [&](std::uint32_t L) {
+    const std::uint32_t tk = tid / 16, pk = 8 * (tid % 16);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      kt[pk + e][tk] = tk < L ? Cv(rk0.v[e]) : 0.0f;
+      kt[pk + e][tk + 32] = tk + 32 < L ? Cv(rk1.v[e]) : 0.0f;
+    }
+  };
   const float inv_sqrt_d = 1.0f / sqrtf(static_cast<float>(kD));
-  // one register set: chunk ci's operands go to LDS, then chunk ci + 1's loads are in flight during ci's products
-  if (nc > 0) load(c0);
+  if (nc > 0) {
+    load(0);
+    load_k(0);
+  }
   for (std::uint32_t ci = 0; ci < nc; ++ci) {
-    const std::uint32_t c = c0 + ci, start = chunks[c * 3], L = chunks[c * 3 + 1];
-    store(c);
-    __syncthreads();
-    load(ci + 1 < nc ? c + 1 : c);  // unconditional (the last chunk reloads itself): no loads under a branch
-    // Delta (waves 0-3) or the output (waves 4-7): rows 16 (w % 4) .. + 16, K range = 128 keys
+    const std::uint32_t start = first + 64 * ci, L = min(64u, len - 64 * ci), cn = ci + 1 < nc ? ci + 1 : ci;
+    store();
+    halo::LdsSync();
+    load(cn);  // unconditional (the last chunk reloads itself): no loads under a branch
+    if (tid < kC) Wl[tid] = expf(Gl[kC - 1] - Gl[tid]);  // the S-update weights exp(G_C - G_t)
+    // Delta (waves 0-3) or the output (waves 4-7): token rows 16 (w % 4) .. + 16, four 16-column tiles, K range =
+    // 128 keys, lane keys 32 fq .. + 32
     {
       const std::uint32_t r0 = 16 * (wave % 4);
       float(*A)[kCL] = wave < 4 ? ukl : qel;
-      V4F acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 8
-      for (int s = 0; s < kD / 4; ++s)
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[r0 + fc][4 * s + fq], Sl[4 * s + fq][fc], acc, 0, 0, 0);
+      V4F acc[kNT];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const std::uint32_t t = r0 + 4 * fq + i;
+      for (int ct = 0; ct < kNT; ++ct) acc[ct] = V4F{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 2
+      for (int sb = 0; sb < 8; ++sb) {
+        const float4 av = *reinterpret_cast<const float4*>(&A[r0 + fc][32 * fq + 4 * sb]);
+#pragma unroll
+        for (int ct = 0; ct < kNT; ++ct) {
+          const float4 bv = *reinterpret_cast<const float4*>(&st[16 * ct + fc][32 * fq + 4 * sb]);
+          acc[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, bv.x, acc[ct], 0, 0, 0);
+          acc[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, bv.y, acc[ct], 0, 0, 0);
+          acc[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, bv.z, acc[ct], 0, 0, 0);
+          acc[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, bv.w, acc[ct], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int ct = 0; ct < kNT; ++ct) {
+        const std::uint32_t col = 16 * ct + fc;
         if (wave < 4) {
-          Dl[t][fc] = wvl[t][fc] - acc[i];
-        } else if (t < L) {
-          o[(static_cast<std::size_t>(start + t) * Hv + h) * kD + j0 + fc] = (acc[i] + ovl[t][fc]) * inv_sqrt_d;
+          float d4[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) d4[i] = wvl[r0 + 4 * fq + i][col] - acc[ct][i];
+          *reinterpret_cast<float4*>(&dt[col][r0 + 4 * fq]) = make_float4(d4[0], d4[1], d4[2], d4[3]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const std::uint32_t t = r0 + 4 * fq + i;
+            if (t < L)
+              o[(static_cast<std::size_t>(start + t) * Hv + h) * kD + j0 + col] = (acc[ct][i] + ovl[t][col]) * inv_sqrt_d;
+          }
         }
       }
     }
-    __syncthreads();
-    // S rows 16 w .. + 16: gamma_C S + (K diag(exp(G_C - G_t)))^T Delta, K range = 64 tokens
+    halo::LdsSync();
+    store_k(L);  // Uk has been read: K^T takes its place
+    load_k(cn);
+    halo::LdsSync();
+    // S rows 16 w .. + 16, four 16-column tiles: gamma_C S + (K diag(exp(G_C - G_t)))^T Delta, K range = 64 tokens,
+    // lane tokens 16 fq .. + 16
     {
       const std::uint32_t r0 = 16 * wave;
-      const float GC = Gl[kC - 1], gc = expf(GC);
-      V4F acc;
+      const float gc = expf(Gl[kC - 1]);
+      V4F acc[kNT];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = gc * Sl[r0 + 4 * fq + i][fc];
-#pragma unroll 4
-      for (int s = 0; s < kC / 4; ++s) {
-        const std::uint32_t tok = 4 * s + fq;
-        const float a = kxl[tok][r0 + fc] * expf(GC - Gl[tok]);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, Dl[tok][fc], acc, 0, 0, 0);
+      for (int ct = 0; ct < kNT; ++ct) {
+        const float4 s4 = *reinterpret_cast<const float4*>(&st[16 * ct + fc][r0 + 4 * fq]);
+        acc[ct][0] = gc * s4.x, acc[ct][1] = gc * s4.y, acc[ct][2] = gc * s4.z, acc[ct][3] = gc * s4.w;
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) Sl[r0 + 4 * fq + i][fc] = acc[i];
+      for (int sb = 0; sb < 4; ++sb) {
+        const std::uint32_t tk = 16 * fq + 4 * sb;
+        const float4 kv = *reinterpret_cast<const float4*>(&kt[r0 + fc][tk]);
+        const float4 wv = *reinterpret_cast<const float4*>(&Wl[tk]);
+        const float a0 = kv.x * wv.x, a1 = kv.y * wv.y, a2 = kv.z * wv.z, a3 = kv.w * wv.w;
+#pragma unroll
+        for (int ct = 0; ct < kNT; ++ct) {
+          const float4 dv = *reinterpret_cast<const float4*>(&dt[16 * ct + fc][tk]);
+          acc[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, dv.x, acc[ct], 0, 0, 0);
+          acc[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, dv.y, acc[ct], 0, 0, 0);
+          acc[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(a2, dv.z, acc[ct], 0, 0, 0);
+          acc[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(a3, dv.w, acc[ct], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int ct = 0; ct < kNT; ++ct)
+        *reinterpret_cast<float4*>(&st[16 * ct + fc][r0 + 4 * fq]) = make_float4(acc[ct][0], acc[ct][1], acc[ct][2], acc[ct][3]);
     }
-    __syncthreads();
+    halo::LdsSync();
   }
-  {
-    const std::uint32_t r = tid / 4, p = tid % 4;
-    *reinterpret_cast<float4*>(St + static_cast<std::size_t>(r) * kD + j0 + 4 * p) = *reinterpret_cast<const float4*>(&Sl[r][4 * p]);
+#pragma unroll
+  for (int i = 0; i < kNT; ++i) {
+    const std::uint32_t r = tid / (kNC / 4) + (2048 / kNC) * i, p = tid % (kNC / 4);
+    *reinterpret_cast<float4*>(Sg + static_cast<std::size_t>(r) * kD + j0 + 4 * p) =
+        make_float4(st[4 * p][r], st[4 * p + 1][r], st[4 * p + 2][r], st[4 * p + 3][r]);
   }
 }
 
@@ -430,13 +528,13 @@ extern "C" __global__ void __launch_bounds__(512)
     halo_gdn_wy_scan(const std::uint16_t* __restrict__ k, const float* __restrict__ wy, const float* __restrict__ Gc,
                      const std::uint32_t* __restrict__ chunks, const std::uint32_t* __restrict__ seqs,
                      float* __restrict__ state, float* __restrict__ o, std::uint32_t Hv, std::uint32_t Hk) {
-  WyScan(k, wy, Gc, chunks, seqs, state, o, Hv, Hk);
+  WyScan<std::uint16_t, 32>(k, wy, Gc, chunks, seqs, state, o, Hv, Hk);
 }
 extern "C" __global__ void __launch_bounds__(512)
     halo_gdn_wy_scan_f32(const float* __restrict__ k, const float* __restrict__ wy, const float* __restrict__ Gc,
                          const std::uint32_t* __restrict__ chunks, const std::uint32_t* __restrict__ seqs,
                          float* __restrict__ state, float* __restrict__ o, std::uint32_t Hv, std::uint32_t Hk) {
-  WyScan(k, wy, Gc, chunks, seqs, state, o, Hv, Hk);
+  WyScan<float, 32>(k, wy, Gc, chunks, seqs, state, o, Hv, Hk);
 }
 
 // ---- the whole DeltaNet token step of the decode graph, one block per (session, value head) -----------------

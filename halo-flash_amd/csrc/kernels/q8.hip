@@ -673,7 +673,7 @@ __device__ __forceinline__ void GemmTileQ8(const std::int8_t* __restrict__ A0, c
     if (kc + 2 < nk) load(kc + 2, fill);
     compute(kc & 1u);
     if (kc + 1 < nk) store((kc + 1) & 1u, next);
-    __syncthreads();
+    LdsSync();  // LDS only: the loads of stage kc + 2 stay in flight
   };
   Staged s0, s1;
   load(0, s0);

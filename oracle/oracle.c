@@ -11,6 +11,8 @@
  *   gdn_step                         -- closed-form invariants (zero state, beta=0 decay-only, delta rule fixes
  *                                      S k = v when beta=1 and |k|=1), numpy restatement on tiny sizes
  *   attention_head                   -- one position returns v; equal keys average v; numpy softmax
+ *   sample                           -- oracle/_ref (the reference's own sampling.cpp BuildDistribution + Sample),
+ *                                      token and RNG state equal over seeded random rows and every filter
  */
 #include "oracle.h"
 
@@ -415,4 +417,197 @@ void or_attention_head(const float* q, const float* k, const float* v, uint32_t 
     for (uint32_t i = 0; i < hd; ++i) o[i] += p * v[(size_t)j * kv_stride + i];
   }
   free(sc);
+}
+
+/* ---- token sampling (reference src/core/sampling.cpp:1-162, 214-293, 330-394, 845-863) -------------------------
+ * Semantics: penalties, then top-k (sort by logit descending, ties to the lower token; keep
+ * max(top_k, min_keep, 1) when top_k > 0), greedy when temperature == 0, then top-p and min-p on the sorted list,
+ * softmax over the survivors (double, max-subtracted, sum in list order), renormalization, zero weights dropped,
+ * order (probability descending, token ascending), and one xorshift64* draw (advanced only when more than one
+ * token remains). Penalties are a list sorted by token: {token, generated_count, repeated}. Returns the token, or
+ * 0xFFFFFFFF when no logit is finite. */
+typedef struct {
+  uint32_t token;
+  double v;
+} or_cand;
+
+static int or_cand_cmp(const void* a, const void* b) {
+  const or_cand* x = (const or_cand*)a;
+  const or_cand* y = (const or_cand*)b;
+  if (x->v == y->v) return x->token < y->token ? -1 : (x->token > y->token ? 1 : 0);
+  return x->v > y->v ? -1 : 1;
+}
+
+/* reference sampling.cpp:845-863 */
+uint64_t or_next_random(uint64_t* state) {
+  uint64_t v = *state;
+  if (v == 0) v = UINT64_C(0x9e3779b97f4a7c15);
+  v ^= v >> 12;
+  v ^= v << 25;
+  v ^= v >> 27;
+  *state = v;
+  return v * UINT64_C(0x2545f4914f6cdd1d);
+}
+double or_uniform(uint64_t* state) { return (double)(or_next_random(state) >> 11) * 0x1.0p-53; }
+
+/* reference sampling.cpp:46-67 (weights in list order; sum accumulated in that order) */
+static void or_softmax_w(const or_cand* c, size_t n, double temperature, double* w) {
+  const double maximum = c[0].v;
+  double sum = 0.0;
+  for (size_t i = 0; i < n; ++i) {
+    w[i] = exp((c[i].v - maximum) / temperature);
+    sum += w[i];
+  }
+  for (size_t i = 0; i < n; ++i) w[i] /= sum;
+}
+
+uint32_t or_sample(const float* logits, uint32_t n, float temperature, int32_t top_k, float top_p, float min_p,
+                   uint32_t min_keep, float repeat_penalty, float frequency_penalty, float presence_penalty,
+                   const uint32_t* pen_token, const uint32_t* pen_generated, const uint32_t* pen_repeated,
+                   uint32_t n_pen, uint64_t* rng) {
+  or_cand* c = (or_cand*)malloc(sizeof(or_cand) * (n ? n : 1));
+  double* w = (double*)malloc(sizeof(double) * (n ? n : 1));
+  size_t m = 0;
+  for (uint32_t i = 0; i < n; ++i)
+    if (isfinite(logits[i])) {
+      c[m].token = i;
+      c[m].v = (double)logits[i];
+      ++m;
+    }
+  uint32_t result = 0xFFFFFFFFu;
+  if (m == 0) goto done;
+  /* penalties, sampling.cpp:69-93 */
+  for (size_t i = 0; i < m; ++i) {
+    uint32_t lo = 0, hi = n_pen;
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi) / 2;
+      if (pen_token[mid] < c[i].token) lo = mid + 1; else hi = mid;
+    }
+    if (lo < n_pen && pen_token[lo] == c[i].token) {
+      double l = c[i].v;
+      if (pen_repeated[lo] && repeat_penalty != 1.0f) l = l <= 0 ? l * repeat_penalty : l / repeat_penalty;
+      l -= (double)frequency_penalty * pen_generated[lo];
+      if (pen_generated[lo] != 0) l -= presence_penalty;
+      c[i].v = l;
+    }
+  }
+  /* top-k, sampling.cpp:95-113 (a full sort orders the same as the partial sort's prefix) */
+  qsort(c, m, sizeof(or_cand), or_cand_cmp);
+  const size_t minimum = m < (min_keep > 1 ? min_keep : 1) ? m : (min_keep > 1 ? min_keep : 1);
+  if (top_k > 0) {
+    size_t keep = (size_t)top_k > minimum ? (size_t)top_k : minimum;
+    if (keep < m) m = keep;
+  }
+  if (temperature == 0.0f) {
+    result = c[0].token;
+    goto done;
+  }
+  const double T = (double)temperature;
+  /* top-p, sampling.cpp:115-133 */
+  if (top_p < 1.0f && m > 1) {
+    const size_t mn = m < (min_keep > 1 ? min_keep : 1) ? m : (min_keep > 1 ? min_keep : 1);
+    or_softmax_w(c, m, T, w);
+    double cumulative = 0.0;
+    size_t keep = 0;
+    while (keep < m) {
+      cumulative += w[keep];
+      ++keep;
+      if (keep >= mn && cumulative >= (double)top_p) break;
+    }
+    m = keep;
+  }
+  /* min-p, sampling.cpp:135-150 */
+  if (min_p > 0.0f && m > 1) {
+    const size_t mn = m < (min_keep > 1 ? min_keep : 1) ? m : (min_keep > 1 ? min_keep : 1);
+    const double threshold = T * log((double)min_p);
+    const double maximum = c[0].v;
+    size_t keep = 0;
+    while (keep < m && c[keep].v - maximum >= threshold) ++keep;
+    if (keep < mn) keep = mn;
+    if (keep < m) m = keep;
+  }
+  /* final softmax, then SamplingDistribution: renormalize, drop zeros, order (sampling.cpp:214-242) */
+  or_softmax_w(c, m, T, w);
+  {
+    double sum = 0.0;
+    for (size_t i = 0; i < m; ++i) sum += w[i];
+    size_t k = 0;
+    for (size_t i = 0; i < m; ++i) {
+      const double v = w[i] / sum;
+      if (v == 0) continue;
+      c[k].token = c[i].token;
+      c[k].v = v;
+      ++k;
+    }
+    qsort(c, k, sizeof(or_cand), or_cand_cmp);
+    /* Sample, sampling.cpp:278-293 */
+    if (k == 1) {
+      result = c[0].token;
+    } else {
+      double u = or_uniform(rng);
+      result = c[k - 1].token;
+      for (size_t i = 0; i < k; ++i) {
+        u -= c[i].v;
+        if (u < 0.0) {
+          result = c[i].token;
+          break;
+        }
+      }
+    }
+  }
+done:
+  free(c);
+  free(w);
+  return result;
+}
+
+/* The penalty list of BuildDistribution (reference sampling.cpp:366-394): generated counts when a frequency or
+ * presence penalty is set; the last repeat_last_n tokens of prompt + generated marked repeated when repeat_penalty
+ * != 1. Writes at most `cap` entries sorted by token; returns the count. */
+uint32_t or_sample_penalties(const uint32_t* prompt, uint32_t n_prompt, const uint32_t* generated, uint32_t n_gen,
+                             float repeat_penalty, uint32_t repeat_last_n, float frequency_penalty,
+                             float presence_penalty, uint32_t* token, uint32_t* gen_count, uint32_t* repeated,
+                             uint32_t cap) {
+  uint32_t n = 0;
+  #define OR_FIND(t, idx)                                    \
+    do {                                                     \
+      idx = n;                                               \
+      for (uint32_t j_ = 0; j_ < n; ++j_)                    \
+        if (token[j_] == (t)) { idx = j_; break; }           \
+      if (idx == n && n < cap) {                             \
+        token[n] = (t); gen_count[n] = 0; repeated[n] = 0; ++n; \
+      }                                                      \
+    } while (0)
+  if (frequency_penalty != 0 || presence_penalty != 0)
+    for (uint32_t i = 0; i < n_gen; ++i) {
+      uint32_t idx;
+      OR_FIND(generated[i], idx);
+      if (idx < n) ++gen_count[idx];
+    }
+  if (repeat_penalty != 1 && repeat_last_n != 0) {
+    const uint32_t tail = n_gen < repeat_last_n ? n_gen : repeat_last_n;
+    const uint32_t ptail = n_prompt < repeat_last_n - tail ? n_prompt : repeat_last_n - tail;
+    for (uint32_t i = n_prompt - ptail; i < n_prompt; ++i) {
+      uint32_t idx;
+      OR_FIND(prompt[i], idx);
+      if (idx < n) repeated[idx] = 1;
+    }
+    for (uint32_t i = n_gen - tail; i < n_gen; ++i) {
+      uint32_t idx;
+      OR_FIND(generated[i], idx);
+      if (idx < n) repeated[idx] = 1;
+    }
+  }
+  #undef OR_FIND
+  /* sort by token (insertion: penalty lists are short) */
+  for (uint32_t i = 1; i < n; ++i) {
+    const uint32_t t = token[i], g = gen_count[i], r = repeated[i];
+    uint32_t j = i;
+    while (j > 0 && token[j - 1] > t) {
+      token[j] = token[j - 1]; gen_count[j] = gen_count[j - 1]; repeated[j] = repeated[j - 1];
+      --j;
+    }
+    token[j] = t; gen_count[j] = g; repeated[j] = r;
+  }
+  return n;
 }

@@ -91,6 +91,18 @@ void or_gdn_sequence(float* S, uint32_t d, uint32_t T, const float* q, size_t qs
 void or_attention_head(const float* q, const float* k, const float* v, uint32_t n, uint32_t hd, size_t kv_stride,
                        float* o);
 
+/* token sampling (reference src/core/sampling.cpp) */
+uint64_t or_next_random(uint64_t* state);
+double or_uniform(uint64_t* state);
+uint32_t or_sample(const float* logits, uint32_t n, float temperature, int32_t top_k, float top_p, float min_p,
+                   uint32_t min_keep, float repeat_penalty, float frequency_penalty, float presence_penalty,
+                   const uint32_t* pen_token, const uint32_t* pen_generated, const uint32_t* pen_repeated,
+                   uint32_t n_pen, uint64_t* rng);
+uint32_t or_sample_penalties(const uint32_t* prompt, uint32_t n_prompt, const uint32_t* generated, uint32_t n_gen,
+                             float repeat_penalty, uint32_t repeat_last_n, float frequency_penalty,
+                             float presence_penalty, uint32_t* token, uint32_t* gen_count, uint32_t* repeated,
+                             uint32_t cap);
+
 #ifdef __cplusplus
 }
 #endif

@@ -50,6 +50,10 @@ _ORACLE_SIGS = {
     "or_gdn_step": (None, [_PF, _U32, _PF, _PF, _PF, _F32, _F32, _PF]),
     "or_gdn_sequence": (None, [_PF, _U32, _U32, _VP, _SZ, _VP, _SZ, _VP, _SZ, _VP, _VP, _SZ, _VP, _SZ]),
     "or_attention_head": (None, [_PF, _PF, _PF, _U32, _U32, _SZ, _PF]),
+    "or_next_random": (_U64, [C.POINTER(C.c_uint64)]),
+    "or_sample": (_U32, [_PF, _U32, _F32, C.c_int32, _F32, _F32, _U32, _F32, _F32, _F32, _VP, _VP, _VP, _U32,
+                         C.POINTER(C.c_uint64)]),
+    "or_sample_penalties": (_U32, [_VP, _U32, _VP, _U32, _F32, _U32, _F32, _F32, _VP, _VP, _VP, _U32]),
 }
 
 _REF_SIGS = {
@@ -66,6 +70,8 @@ _REF_SIGS = {
     "ref_sigmoid": (_F32, [_F32]),
     "ref_softplus": (_F32, [_F32]),
     "ref_hw_threads": (C.c_uint, []),
+    "ref_sample": (_U32, [_PF, _U32, _F32, C.c_int32, _F32, _F32, _U32, _F32, _U32, _F32, _F32, _VP, _U32, _VP, _U32,
+                          C.POINTER(C.c_uint64)]),
 }
 
 _libs: dict[str, C.CDLL] = {}
@@ -141,3 +147,41 @@ def synth_q8(rng: np.random.Generator, rows: int, cols: int, sigma: float = 0.02
     qs = rng.integers(-127, 128, size=(rows, cols), dtype=np.int8)
     d = (np.abs(rng.normal(0.0, sigma, size=(rows, cols // 32))) / 127.0).astype(np.float16).view(np.uint16)
     return qs, d
+
+
+def sample_penalties(prompt, generated, repeat_penalty=1.0, repeat_last_n=64, frequency_penalty=0.0,
+                     presence_penalty=0.0, cap=8192):
+    """The penalty list {token, generated_count, repeated} (sorted by token) the reference builds from history."""
+    p = np.ascontiguousarray(prompt, np.uint32)
+    g = np.ascontiguousarray(generated, np.uint32)
+    tok, gen, rep = (np.zeros(cap, np.uint32) for _ in range(3))
+    n = oracle().or_sample_penalties(p.ctypes.data, len(p), g.ctypes.data, len(g), repeat_penalty, repeat_last_n,
+                                     frequency_penalty, presence_penalty, tok.ctypes.data, gen.ctypes.data,
+                                     rep.ctypes.data, cap)
+    return tok[:n].copy(), gen[:n].copy(), rep[:n].copy()
+
+
+def sample(logits, rng, temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, min_keep=0, repeat_penalty=1.0,
+           repeat_last_n=64, frequency_penalty=0.0, presence_penalty=0.0, prompt=(), generated=()):
+    """One draw of the restated sampler; returns (token, rng state after)."""
+    x = np.ascontiguousarray(logits, np.float32)
+    tok, gen, rep = sample_penalties(prompt, generated, repeat_penalty, repeat_last_n, frequency_penalty,
+                                     presence_penalty)
+    st = C.c_uint64(rng)
+    t = oracle().or_sample(x, len(x), temperature, top_k, top_p, min_p, min_keep, repeat_penalty, frequency_penalty,
+                           presence_penalty, tok.ctypes.data, gen.ctypes.data, rep.ctypes.data, len(tok),
+                           C.byref(st))
+    return int(t), int(st.value)
+
+
+def ref_sample(logits, rng, temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, min_keep=0, repeat_penalty=1.0,
+               repeat_last_n=64, frequency_penalty=0.0, presence_penalty=0.0, prompt=(), generated=()):
+    """One draw of the reference's own sampler (oracle/_ref); returns (token, rng state after)."""
+    x = np.ascontiguousarray(logits, np.float32)
+    p = np.ascontiguousarray(prompt, np.uint32)
+    g = np.ascontiguousarray(generated, np.uint32)
+    st = C.c_uint64(rng)
+    t = ref().ref_sample(x, len(x), temperature, top_k, top_p, min_p, min_keep, repeat_penalty, repeat_last_n,
+                         frequency_penalty, presence_penalty, p.ctypes.data, len(p), g.ctypes.data, len(g),
+                         C.byref(st))
+    return int(t), int(st.value)

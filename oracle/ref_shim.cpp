@@ -8,6 +8,7 @@
 #include <thread>
 
 #include "core/quant.hpp"
+#include "core/sampling.hpp"
 #include "model/cpu_ops.hpp"
 #include "model/weights.hpp"
 
@@ -59,4 +60,32 @@ float ref_silu(float x) { return halo::model::cpu::Silu(x); }
 float ref_sigmoid(float x) { return halo::model::cpu::Sigmoid(x); }
 float ref_softplus(float x) { return halo::model::cpu::Softplus(x); }
 unsigned ref_hw_threads() { return std::thread::hardware_concurrency(); }
+
+// One draw of the reference's sampler: BuildDistribution (penalties from the prompt and generated token lists)
+// then Sample with the given RNG state (advanced in place). Returns the token, 0xFFFFFFFF on an exception.
+std::uint32_t ref_sample(const float* logits, std::uint32_t n, float temperature, std::int32_t top_k, float top_p,
+                         float min_p, std::uint32_t min_keep, float repeat_penalty, std::uint32_t repeat_last_n,
+                         float frequency_penalty, float presence_penalty, const std::uint32_t* prompt,
+                         std::uint32_t n_prompt, const std::uint32_t* generated, std::uint32_t n_gen,
+                         std::uint64_t* rng) {
+  halo::sampling::SamplingConfig c;
+  c.temperature = temperature;
+  c.top_k = top_k;
+  c.top_p = top_p;
+  c.min_p = min_p;
+  c.min_keep = min_keep;
+  c.seed = 0;
+  c.repeat_penalty = repeat_penalty;
+  c.repeat_last_n = repeat_last_n;
+  c.frequency_penalty = frequency_penalty;
+  c.presence_penalty = presence_penalty;
+  try {
+    const auto d = halo::sampling::BuildDistribution(std::span<const float>(logits, n), c,
+                                                     std::span<const std::uint32_t>(prompt, n_prompt),
+                                                     std::span<const std::uint32_t>(generated, n_gen));
+    return d.Sample(rng);
+  } catch (...) {
+    return 0xFFFFFFFFu;
+  }
+}
 }

@@ -611,3 +611,150 @@ uint32_t or_sample_penalties(const uint32_t* prompt, uint32_t n_prompt, const ui
   }
   return n;
 }
+
+/* ---- the stateful sampler (reference src/core/sampling.cpp:494-563 SamplerState::Distribution / Sample,
+ * 616-700 SampleGreedy / LinearDistribution, 702-842 PrepareSelected) with its penalty list given. This is the
+ * path the engine's samplers take and the one the device sampler follows. It differs from or_sample in
+ * summation order and in entry order: the weights are exp((v - max) / T) divided by their sum, zeros dropped,
+ * and the draw walks the entries in candidate order (token order on the linear path; logit descending, token
+ * ascending otherwise) without a re-sort by probability.
+ *   - temperature 0: the (penalized) argmax, ties to the lower token, no draw;
+ *   - top_k == 0, top_p == 1 and not (min_p > 0 and min_keep > 1): the linear path in token order, min-p as a
+ *     threshold max + T log(min_p) that zeroes weights;
+ *   - otherwise: candidates sorted, cut to max(top_k, min_keep, 1) when top_k > 0, then top-p (cumulative exp
+ *     weights against top_p times their sum; the sum runs over the whole vocabulary in token order when
+ *     top_k == 0 and the vocabulary exceeds 1024, else over the sorted candidates), then min-p with the
+ *     min_keep floor.
+ * Returns the token, or 0xFFFFFFFF when no logit is finite. */
+static double or_penalized(const float* logits, uint32_t i, float repeat_penalty, float frequency_penalty,
+                           float presence_penalty, const uint32_t* pen_token, const uint32_t* pen_generated,
+                           const uint32_t* pen_repeated, uint32_t n_pen) {
+  double l = (double)logits[i];
+  uint32_t lo = 0, hi = n_pen;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi) / 2;
+    if (pen_token[mid] < i) lo = mid + 1; else hi = mid;
+  }
+  if (lo < n_pen && pen_token[lo] == i) {
+    if (pen_repeated[lo] && repeat_penalty != 1.0f) l = l <= 0 ? l * repeat_penalty : l / repeat_penalty;
+    l -= (double)frequency_penalty * pen_generated[lo];
+    if (pen_generated[lo] != 0) l -= presence_penalty;
+  }
+  return l;
+}
+
+static uint32_t or_draw(const or_cand* e, size_t k, uint64_t* rng) {
+  if (k == 1) return e[0].token;
+  double u = or_uniform(rng);
+  for (size_t i = 0; i < k; ++i) {
+    u -= e[i].v;
+    if (u < 0.0) return e[i].token;
+  }
+  return e[k - 1].token;
+}
+
+uint32_t or_sample_state(const float* logits, uint32_t n, float temperature, int32_t top_k, float top_p,
+                         float min_p, uint32_t min_keep, float repeat_penalty, float frequency_penalty,
+                         float presence_penalty, const uint32_t* pen_token, const uint32_t* pen_generated,
+                         const uint32_t* pen_repeated, uint32_t n_pen, uint64_t* rng) {
+  or_cand* c = (or_cand*)malloc(sizeof(or_cand) * (n ? n : 1));
+  size_t m = 0;
+  for (uint32_t i = 0; i < n; ++i)
+    if (isfinite(logits[i])) {
+      c[m].token = i;
+      c[m].v = or_penalized(logits, i, repeat_penalty, frequency_penalty, presence_penalty, pen_token,
+                            pen_generated, pen_repeated, n_pen);
+      ++m;
+    }
+  uint32_t result = 0xFFFFFFFFu;
+  if (m == 0) goto done;
+  const double T = (double)temperature;
+  if (temperature == 0.0f) {
+    size_t best = 0;
+    for (size_t i = 1; i < m; ++i)
+      if (c[i].v > c[best].v) best = i;
+    result = c[best].token;
+    goto done;
+  }
+  const uint32_t floor_keep = min_keep > 1 ? min_keep : 1;
+  if (top_k == 0 && top_p == 1.0f && !(min_p > 0.0f && min_keep > 1)) {
+    double maximum = -INFINITY;
+    for (size_t i = 0; i < m; ++i)
+      if (c[i].v > maximum) maximum = c[i].v;
+    const double threshold = min_p > 0.0f ? maximum + T * log((double)min_p) : -INFINITY;
+    double total = 0.0;
+    for (size_t i = 0; i < m; ++i) {
+      c[i].v = c[i].v >= threshold ? exp((c[i].v - maximum) / T) : 0.0;
+      total += c[i].v;
+    }
+    size_t k = 0;
+    for (size_t i = 0; i < m; ++i) {
+      const double v = c[i].v / total;
+      if (v == 0) continue;
+      c[k].token = c[i].token;
+      c[k].v = v;
+      ++k;
+    }
+    result = or_draw(c, k, rng);
+    goto done;
+  }
+  {
+    double full_sum = 0.0;
+    const int has_full = top_k == 0 && top_p < 1.0f && n > 1024;
+    if (has_full) {
+      double maximum = -INFINITY;
+      for (size_t i = 0; i < m; ++i)
+        if (c[i].v > maximum) maximum = c[i].v;
+      for (size_t i = 0; i < m; ++i) full_sum += exp((c[i].v - maximum) / T);
+    }
+    qsort(c, m, sizeof(or_cand), or_cand_cmp);
+    if (top_k > 0) {
+      size_t keep = (size_t)top_k > floor_keep ? (size_t)top_k : floor_keep;
+      if (keep > n) keep = n;
+      if (keep < m) m = keep;
+    }
+    size_t keep = m;
+    const size_t minimum = m < floor_keep ? m : floor_keep;
+    const double maximum = c[0].v;
+    if (top_p < 1.0f && keep > 1) {
+      double sum = full_sum;
+      if (!has_full) {
+        sum = 0.0;
+        for (size_t i = 0; i < m; ++i) sum += exp((c[i].v - maximum) / T);
+      }
+      const double target = (double)top_p * sum;
+      double cumulative = 0.0;
+      size_t k = 0;
+      while (k < keep) {
+        cumulative += exp((c[k].v - maximum) / T);
+        ++k;
+        if (k >= minimum && cumulative >= target) break;
+      }
+      keep = k;
+    }
+    if (min_p > 0.0f && keep > 1) {
+      const double threshold = maximum + T * log((double)min_p);
+      size_t k = 0;
+      while (k < keep && c[k].v >= threshold) ++k;
+      if (k < minimum) k = minimum;
+      if (k < keep) keep = k;
+    }
+    double total = 0.0;
+    for (size_t i = 0; i < keep; ++i) {
+      c[i].v = exp((c[i].v - maximum) / T);
+      total += c[i].v;
+    }
+    size_t k = 0;
+    for (size_t i = 0; i < keep; ++i) {
+      const double v = c[i].v / total;
+      if (v == 0) continue;
+      c[k].token = c[i].token;
+      c[k].v = v;
+      ++k;
+    }
+    result = or_draw(c, k, rng);
+  }
+done:
+  free(c);
+  return result;
+}

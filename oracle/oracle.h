@@ -102,6 +102,10 @@ uint32_t or_sample_penalties(const uint32_t* prompt, uint32_t n_prompt, const ui
                              float repeat_penalty, uint32_t repeat_last_n, float frequency_penalty,
                              float presence_penalty, uint32_t* token, uint32_t* gen_count, uint32_t* repeated,
                              uint32_t cap);
+uint32_t or_sample_state(const float* logits, uint32_t n, float temperature, int32_t top_k, float top_p,
+                         float min_p, uint32_t min_keep, float repeat_penalty, float frequency_penalty,
+                         float presence_penalty, const uint32_t* pen_token, const uint32_t* pen_generated,
+                         const uint32_t* pen_repeated, uint32_t n_pen, uint64_t* rng);
 
 #ifdef __cplusplus
 }

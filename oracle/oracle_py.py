@@ -53,6 +53,8 @@ _ORACLE_SIGS = {
     "or_next_random": (_U64, [C.POINTER(C.c_uint64)]),
     "or_sample": (_U32, [_PF, _U32, _F32, C.c_int32, _F32, _F32, _U32, _F32, _F32, _F32, _VP, _VP, _VP, _U32,
                          C.POINTER(C.c_uint64)]),
+    "or_sample_state": (_U32, [_PF, _U32, _F32, C.c_int32, _F32, _F32, _U32, _F32, _F32, _F32, _VP, _VP, _VP,
+                               _U32, C.POINTER(C.c_uint64)]),
     "or_sample_penalties": (_U32, [_VP, _U32, _VP, _U32, _F32, _U32, _F32, _F32, _VP, _VP, _VP, _U32]),
 }
 
@@ -70,6 +72,8 @@ _REF_SIGS = {
     "ref_sigmoid": (_F32, [_F32]),
     "ref_softplus": (_F32, [_F32]),
     "ref_hw_threads": (C.c_uint, []),
+    "ref_sampler_state": (_U32, [_PF, _U32, _F32, C.c_int32, _F32, _F32, _U32, _F32, _U32, _F32, _F32, _VP, _U32,
+                                 _VP, _U32, C.POINTER(C.c_uint64), _VP, _VP, _VP, _U32, C.POINTER(C.c_uint32)]),
     "ref_sample": (_U32, [_PF, _U32, _F32, C.c_int32, _F32, _F32, _U32, _F32, _U32, _F32, _F32, _VP, _U32, _VP, _U32,
                           C.POINTER(C.c_uint64)]),
 }
@@ -185,3 +189,36 @@ def ref_sample(logits, rng, temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, min_
                          frequency_penalty, presence_penalty, p.ctypes.data, len(p), g.ctypes.data, len(g),
                          C.byref(st))
     return int(t), int(st.value)
+
+
+def sample_state(logits, rng, penalties=None, temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, min_keep=0,
+                 repeat_penalty=1.0, frequency_penalty=0.0, presence_penalty=0.0):
+    """One draw of the restated SamplerState::Sample; penalties = (token, generated_count, repeated) arrays sorted
+    by token. Returns (token, rng state after)."""
+    x = np.ascontiguousarray(logits, np.float32)
+    if penalties is None:
+        penalties = (np.zeros(0, np.uint32),) * 3
+    tok, gen, rep = (np.ascontiguousarray(a, np.uint32) for a in penalties)
+    st = C.c_uint64(rng)
+    t = oracle().or_sample_state(x, len(x), temperature, top_k, top_p, min_p, min_keep, repeat_penalty,
+                                 frequency_penalty, presence_penalty, tok.ctypes.data, gen.ctypes.data,
+                                 rep.ctypes.data, len(tok), C.byref(st))
+    return int(t), int(st.value)
+
+
+def ref_sampler_state(logits, rng, temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, min_keep=0, repeat_penalty=1.0,
+                      repeat_last_n=64, frequency_penalty=0.0, presence_penalty=0.0, prompt=(), generated=()):
+    """The reference's SamplerState over history prompt + accepted generated tokens (oracle/_ref).
+    Returns (token, rng state after, penalties as (token, generated_count, repeated) arrays)."""
+    x = np.ascontiguousarray(logits, np.float32)
+    p = np.ascontiguousarray(prompt, np.uint32)
+    g = np.ascontiguousarray(generated, np.uint32)
+    cap = 8192
+    tok, gen, rep = (np.zeros(cap, np.uint32) for _ in range(3))
+    st = C.c_uint64(rng)
+    npen = C.c_uint32(0)
+    t = ref().ref_sampler_state(x, len(x), temperature, top_k, top_p, min_p, min_keep, repeat_penalty, repeat_last_n,
+                                frequency_penalty, presence_penalty, p.ctypes.data, len(p), g.ctypes.data, len(g),
+                                C.byref(st), tok.ctypes.data, gen.ctypes.data, rep.ctypes.data, cap, C.byref(npen))
+    k = npen.value
+    return int(t), int(st.value), (tok[:k].copy(), gen[:k].copy(), rep[:k].copy())

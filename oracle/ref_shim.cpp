@@ -88,4 +88,45 @@ std::uint32_t ref_sample(const float* logits, std::uint32_t n, float temperature
     return 0xFFFFFFFFu;
   }
 }
+
+// SamplerState (sampling.cpp:407-415, 467-563): history = prompt, then the generated tokens accepted; its penalty
+// list is written out (token, generated_count, repeated; at most cap entries) and one Sample drawn from `rng`.
+std::uint32_t ref_sampler_state(const float* logits, std::uint32_t n, float temperature, std::int32_t top_k,
+                                float top_p, float min_p, std::uint32_t min_keep, float repeat_penalty,
+                                std::uint32_t repeat_last_n, float frequency_penalty, float presence_penalty,
+                                const std::uint32_t* prompt, std::uint32_t n_prompt, const std::uint32_t* generated,
+                                std::uint32_t n_gen, std::uint64_t* rng, std::uint32_t* pen_token,
+                                std::uint32_t* pen_generated, std::uint32_t* pen_repeated, std::uint32_t cap,
+                                std::uint32_t* n_pen) {
+  halo::sampling::SamplingConfig c;
+  c.temperature = temperature;
+  c.top_k = top_k;
+  c.top_p = top_p;
+  c.min_p = min_p;
+  c.min_keep = min_keep;
+  c.seed = 0;
+  c.repeat_penalty = repeat_penalty;
+  c.repeat_last_n = repeat_last_n;
+  c.frequency_penalty = frequency_penalty;
+  c.presence_penalty = presence_penalty;
+  halo::sampling::SamplerState s(c, std::span<const std::uint32_t>(prompt, n_prompt));
+  s.Accept(std::span<const std::uint32_t>(generated, n_gen));
+  std::uint32_t k = 0;
+  for (const auto& p : s.penalties()) {
+    if (k == cap) break;
+    pen_token[k] = p.token;
+    pen_generated[k] = p.generated_count;
+    pen_repeated[k] = p.repeated;
+    ++k;
+  }
+  *n_pen = k;
+  s.SetRngState(*rng);
+  std::uint32_t t = 0xFFFFFFFFu;
+  try {
+    t = s.Sample(std::span<const float>(logits, n));
+  } catch (...) {
+  }
+  *rng = s.rng_state();
+  return t;
+}
 }

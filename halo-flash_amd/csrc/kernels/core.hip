@@ -6,3 +6,4 @@
 #include "model.hip"
 #include "proj.hip"
 #include "moe_prefill.hip"
+#include "sample.hip"

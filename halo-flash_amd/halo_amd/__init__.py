@@ -110,6 +110,53 @@ class ModelConfig(C.Structure):
         (n, C.c_uint32) for n in ("max_sessions", "max_context", "prefix_tokens", "pad")]
 
 
+class SampleParams(C.Structure):
+    """HaloSampleParams (include/halo_sample.h)."""
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("min_p", C.c_float),
+                ("repeat_penalty", C.c_float), ("frequency_penalty", C.c_float), ("presence_penalty", C.c_float),
+                ("top_k", C.c_uint32), ("min_keep", C.c_uint32), ("n_penalties", C.c_uint32),
+                ("vocab", C.c_uint32), ("rng", C.c_uint64), ("fallback_only", C.c_uint32), ("pad", C.c_uint32)]
+
+
+SAMPLE_NO_FINITE = 0xFFFFFFFF
+SAMPLE_BAD_PARAMS = 0xFFFFFFFC
+PENALTY_DTYPE = np.dtype([("token", np.uint32), ("generated_count", np.uint32), ("repeated", np.uint32),
+                          ("pad", np.uint32)])
+SAMPLE_OUT_DTYPE = np.dtype([("token", np.uint32), ("live", np.uint32), ("rng", np.uint64)])
+
+
+def sample_rows(dev, logits, params, penalties=None):
+    """Device sampling of each row of `logits` (host [rows][vocab] fp32) with params (a list of SampleParams) and
+    penalties (a list of (token, generated_count, repeated) arrays per row, or None). Returns the HaloSampleOut rows
+    as a structured array (token, live, rng)."""
+    x = np.ascontiguousarray(logits, np.float32)
+    rows, V = x.shape
+    pen_lists = penalties if penalties is not None else [None] * rows
+    stride = max([len(pl[0]) for pl in pen_lists if pl is not None] + [1])
+    pen = np.zeros((rows, stride), PENALTY_DTYPE)
+    prm = (SampleParams * rows)()
+    for r in range(rows):
+        prm[r] = params[r]
+        prm[r].vocab = V if params[r].vocab == 0 else params[r].vocab
+        pl = pen_lists[r]
+        n = 0 if pl is None else len(pl[0])
+        prm[r].n_penalties = n
+        if n:
+            pen[r, :n]["token"], pen[r, :n]["generated_count"], pen[r, :n]["repeated"] = pl
+    dl = dev.to_device(x)
+    dp = dev.to_device(np.frombuffer(bytes(prm), np.uint8))
+    dq = dev.to_device(pen.view(np.uint8).reshape(-1))
+    do = dev.array(rows * 16, np.uint8)
+    ws = dev.array(lib().halo_op_sample_workspace_bytes(rows, V), np.uint8)
+    try:
+        dev.op("sample", dl.ptr, rows, V, V, dp.ptr, dq.ptr, stride, do.ptr, ws.ptr, ws.nbytes)
+        dev.sync()
+        return do.download().view(SAMPLE_OUT_DTYPE).copy()
+    finally:
+        for a in (dl, dp, dq, do, ws):
+            a.free()
+
+
 class TensorView(C.Structure):
     _fields_ = [("data", C.c_void_p), ("scales", C.c_void_p)] + [(n, C.c_uint32) for n in (
         "kind", "rows", "cols", "qstride")]
@@ -203,6 +250,8 @@ _SIGS = {
     "halo_op_moe_workspace_bytes": (_SZ, [C.POINTER(MoeWeights), _U32], False),
     "halo_op_moe_views": (C.c_int, [C.POINTER(MoeWeights), _U32, _VP, C.POINTER(MoeViews)], True),
     "halo_op_moe_decode": (C.c_int, [_VP, C.POINTER(MoeWeights), _VP, _VP, _U32, _VP, _SZ], True),
+    "halo_op_sample_workspace_bytes": (_SZ, [_U32, _U32], False),
+    "halo_op_sample": (C.c_int, [_VP, _VP, _U32, _U64, _U32, _VP, _VP, _U32, _VP, _VP, _SZ], True),
     "halo_op_moe_decode_norm": (C.c_int, [_VP, C.POINTER(MoeWeights), C.POINTER(ProjInput), _VP, _U32, _VP, _SZ],
                                 True),
 }

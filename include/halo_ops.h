@@ -13,6 +13,7 @@
 #include <stdint.h>
 
 #include "halo_rt.h"
+#include "halo_sample.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -241,6 +242,16 @@ int halo_op_gdn_prefill_f32(halo_engine* eng, const float* q, const float* k, co
                             const float* beta, const uint32_t* chunks, const uint32_t* seqs, uint32_t n_chunks,
                             uint32_t n_seq, float* state, float* o, uint32_t v_heads, uint32_t k_heads,
                             uint32_t head_dim, void* ws, size_t ws_bytes, char* err, size_t errlen);
+
+/* Device sampling, one draw per row (replaces the launches of halo_sample / halo_sample_blocks + halo_sample_final,
+ * src/engine/flash_next_gpu.cpp:876-893, src/engine/batch_decode.cpp:605-621, with the semantics of
+ * SamplerState::Sample, src/core/sampling.cpp:542-563). logits [rows][row_stride] fp32; params [rows]; penalties
+ * [rows][pen_stride]; out [rows]; all device memory. Each out[r] holds the token (or a HALO_SAMPLE_* code), the
+ * nonzero-probability count and the advanced RNG state. ws: halo_op_sample_workspace_bytes(rows, vocab). */
+size_t halo_op_sample_workspace_bytes(uint32_t rows, uint32_t vocab);
+int halo_op_sample(halo_engine* eng, const float* logits, uint32_t rows, uint64_t row_stride, uint32_t vocab,
+                   const HaloSampleParams* params, const HaloPenalty* penalties, uint32_t pen_stride,
+                   HaloSampleOut* out, void* ws, size_t ws_bytes, char* err, size_t errlen);
 
 #ifdef __cplusplus
 }

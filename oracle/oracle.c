@@ -643,9 +643,9 @@ static double or_penalized(const float* logits, uint32_t i, float repeat_penalty
   return l;
 }
 
-static uint32_t or_draw(const or_cand* e, size_t k, uint64_t* rng) {
+static uint32_t or_draw(const or_cand* e, size_t k, uint64_t* rng, const double* u_fixed) {
   if (k == 1) return e[0].token;
-  double u = or_uniform(rng);
+  double u = u_fixed ? *u_fixed : or_uniform(rng);
   for (size_t i = 0; i < k; ++i) {
     u -= e[i].v;
     if (u < 0.0) return e[i].token;
@@ -653,10 +653,14 @@ static uint32_t or_draw(const or_cand* e, size_t k, uint64_t* rng) {
   return e[k - 1].token;
 }
 
-uint32_t or_sample_state(const float* logits, uint32_t n, float temperature, int32_t top_k, float top_p,
-                         float min_p, uint32_t min_keep, float repeat_penalty, float frequency_penalty,
-                         float presence_penalty, const uint32_t* pen_token, const uint32_t* pen_generated,
-                         const uint32_t* pen_repeated, uint32_t n_pen, uint64_t* rng) {
+uint32_t or_sample_state_ex(const float* logits, uint32_t n, float temperature, int32_t top_k, float top_p,
+                            float min_p, uint32_t min_keep, float repeat_penalty, float frequency_penalty,
+                            float presence_penalty, const uint32_t* pen_token, const uint32_t* pen_generated,
+                            const uint32_t* pen_repeated, uint32_t n_pen, uint64_t* rng, const double* u_fixed,
+                            uint32_t* live) {
+  uint32_t live_ = 0;
+  if (live == NULL) live = &live_;
+  *live = 0;
   or_cand* c = (or_cand*)malloc(sizeof(or_cand) * (n ? n : 1));
   size_t m = 0;
   for (uint32_t i = 0; i < n; ++i)
@@ -674,6 +678,7 @@ uint32_t or_sample_state(const float* logits, uint32_t n, float temperature, int
     for (size_t i = 1; i < m; ++i)
       if (c[i].v > c[best].v) best = i;
     result = c[best].token;
+    *live = 1;
     goto done;
   }
   const uint32_t floor_keep = min_keep > 1 ? min_keep : 1;
@@ -695,7 +700,8 @@ uint32_t or_sample_state(const float* logits, uint32_t n, float temperature, int
       c[k].v = v;
       ++k;
     }
-    result = or_draw(c, k, rng);
+    *live = (uint32_t)k;
+    result = or_draw(c, k, rng, u_fixed);
     goto done;
   }
   {
@@ -752,9 +758,19 @@ uint32_t or_sample_state(const float* logits, uint32_t n, float temperature, int
       c[k].v = v;
       ++k;
     }
-    result = or_draw(c, k, rng);
+    *live = (uint32_t)k;
+    result = or_draw(c, k, rng, u_fixed);
   }
 done:
   free(c);
   return result;
+}
+
+uint32_t or_sample_state(const float* logits, uint32_t n, float temperature, int32_t top_k, float top_p,
+                         float min_p, uint32_t min_keep, float repeat_penalty, float frequency_penalty,
+                         float presence_penalty, const uint32_t* pen_token, const uint32_t* pen_generated,
+                         const uint32_t* pen_repeated, uint32_t n_pen, uint64_t* rng) {
+  return or_sample_state_ex(logits, n, temperature, top_k, top_p, min_p, min_keep, repeat_penalty,
+                            frequency_penalty, presence_penalty, pen_token, pen_generated, pen_repeated, n_pen, rng,
+                            NULL, NULL);
 }

@@ -106,6 +106,13 @@ uint32_t or_sample_state(const float* logits, uint32_t n, float temperature, int
                          float min_p, uint32_t min_keep, float repeat_penalty, float frequency_penalty,
                          float presence_penalty, const uint32_t* pen_token, const uint32_t* pen_generated,
                          const uint32_t* pen_repeated, uint32_t n_pen, uint64_t* rng);
+/* or_sample_state with the draw's uniform given (u_fixed non-null: the RNG is left alone) and the number of
+ * tokens with nonzero probability written to *live (when non-null). */
+uint32_t or_sample_state_ex(const float* logits, uint32_t n, float temperature, int32_t top_k, float top_p,
+                            float min_p, uint32_t min_keep, float repeat_penalty, float frequency_penalty,
+                            float presence_penalty, const uint32_t* pen_token, const uint32_t* pen_generated,
+                            const uint32_t* pen_repeated, uint32_t n_pen, uint64_t* rng, const double* u_fixed,
+                            uint32_t* live);
 
 #ifdef __cplusplus
 }

@@ -55,6 +55,8 @@ _ORACLE_SIGS = {
                          C.POINTER(C.c_uint64)]),
     "or_sample_state": (_U32, [_PF, _U32, _F32, C.c_int32, _F32, _F32, _U32, _F32, _F32, _F32, _VP, _VP, _VP,
                                _U32, C.POINTER(C.c_uint64)]),
+    "or_sample_state_ex": (_U32, [_PF, _U32, _F32, C.c_int32, _F32, _F32, _U32, _F32, _F32, _F32, _VP, _VP, _VP,
+                                  _U32, C.POINTER(C.c_uint64), C.POINTER(C.c_double), C.POINTER(C.c_uint32)]),
     "or_sample_penalties": (_U32, [_VP, _U32, _VP, _U32, _F32, _U32, _F32, _F32, _VP, _VP, _VP, _U32]),
 }
 
@@ -192,17 +194,23 @@ def ref_sample(logits, rng, temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, min_
 
 
 def sample_state(logits, rng, penalties=None, temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, min_keep=0,
-                 repeat_penalty=1.0, frequency_penalty=0.0, presence_penalty=0.0):
+                 repeat_penalty=1.0, frequency_penalty=0.0, presence_penalty=0.0, u=None, with_live=False):
     """One draw of the restated SamplerState::Sample; penalties = (token, generated_count, repeated) arrays sorted
-    by token. Returns (token, rng state after)."""
+    by token. Returns (token, rng state after), plus the nonzero-probability count when with_live. With u given,
+    that uniform replaces the RNG draw."""
     x = np.ascontiguousarray(logits, np.float32)
     if penalties is None:
         penalties = (np.zeros(0, np.uint32),) * 3
     tok, gen, rep = (np.ascontiguousarray(a, np.uint32) for a in penalties)
     st = C.c_uint64(rng)
-    t = oracle().or_sample_state(x, len(x), temperature, top_k, top_p, min_p, min_keep, repeat_penalty,
-                                 frequency_penalty, presence_penalty, tok.ctypes.data, gen.ctypes.data,
-                                 rep.ctypes.data, len(tok), C.byref(st))
+    live = C.c_uint32(0)
+    uf = C.c_double(u) if u is not None else None
+    t = oracle().or_sample_state_ex(x, len(x), temperature, top_k, top_p, min_p, min_keep, repeat_penalty,
+                                    frequency_penalty, presence_penalty, tok.ctypes.data, gen.ctypes.data,
+                                    rep.ctypes.data, len(tok), C.byref(st), C.byref(uf) if uf is not None else None,
+                                    C.byref(live))
+    if with_live:
+        return int(t), int(st.value), int(live.value)
     return int(t), int(st.value)
 
 

@@ -73,6 +73,8 @@ def run_gpu(args):
             return run_proj(args, dev, H, res)
         if args.mode == "prefill":
             return run_prefill(args, dev, H, res)
+        if args.mode == "sample":
+            return run_sample(args, dev, H, res)
         # ---------------- C1 pass at M=1 (the bench value) and the M sweep ----------------
         per_copy = sum(q8_bytes(r, c) for r, c in C1_SHAPES)
         copies = max(2, -(-MIN_ROTATION_BYTES // per_copy))
@@ -714,6 +716,57 @@ def run_gdn(args, dev, H, res):
     return res
 
 
+def run_sample(args, dev, H, res):
+    """Device sampling latency over C4's vocabulary (N(0, 3) logits), 1 and 4 rows, the common filter sets."""
+    V = H.c4_config().vocab
+    rng = np.random.default_rng(0)
+    configs = {
+        "greedy": dict(temperature=0.0),
+        "temperature_1": dict(temperature=1.0),
+        "top_k40_top_p0.95_T0.7": dict(temperature=0.7, top_k=40, top_p=0.95),
+        "top_p0.9_T0.8": dict(temperature=0.8, top_p=0.9),
+        "min_p0.05_T1": dict(temperature=1.0, min_p=0.05),
+        "penalties64_top_k40": dict(temperature=0.8, top_k=40, repeat_penalty=1.1, frequency_penalty=0.1),
+    }
+    out = {}
+    for rows in (1, 4):
+        x = dev.to_device((rng.standard_normal((rows, V)) * 3).astype(np.float32))
+        ws = dev.array(H.lib().halo_op_sample_workspace_bytes(rows, V), np.uint8)
+        o = dev.array(rows * 16, np.uint8)
+        for name, kw in configs.items():
+            prm = (H.SampleParams * rows)()
+            pen = np.zeros((rows, 64), H.PENALTY_DTYPE)
+            for r in range(rows):
+                prm[r] = H.SampleParams(top_p=1.0, repeat_penalty=1.0, vocab=V, rng=12345 + r)
+                for k, v in kw.items():
+                    setattr(prm[r], k, v)
+                if "repeat_penalty" in kw:
+                    pen[r]["token"] = np.sort(rng.choice(V, 64, replace=False))
+                    pen[r]["generated_count"] = 1
+                    pen[r]["repeated"] = 1
+                    prm[r].n_penalties = 64
+            dp = dev.to_device(np.frombuffer(bytes(prm), np.uint8))
+            dq = dev.to_device(pen.view(np.uint8).reshape(-1))
+            call = lambda: dev.op("sample", x.ptr, rows, V, V, dp.ptr, dq.ptr, 64, o.ptr, ws.ptr, ws.nbytes)
+            for _ in range(20):
+                call()
+            dev.sync()
+            nrep = 200
+            dev.timer_start()
+            for _ in range(nrep):
+                call()
+            us = dev.timer_stop() * 1e3 / nrep
+            out[f"{name}_rows{rows}"] = round(us, 2)
+            log(f"[bench] sample {name} rows={rows}: {us:.2f} us")
+            dp.free()
+            dq.free()
+        for a in (x, ws, o):
+            a.free()
+    res["sample"] = {"vocab": V, "us_per_launch": out}
+    res["roofline"] = None
+    return res
+
+
 def run_membw(args, dev, H, res):
     """Streaming-read yardstick: one launch reads one buffer of the given size; buffers rotate over >= 600 MB."""
     out = {}
@@ -870,7 +923,8 @@ def main():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--quick", action="store_true", help="only the C1 value and the C0 roofline")
     p.add_argument("--eager", action="store_true", help="launch without graphs (for profiling kernel durations)")
-    p.add_argument("--mode", choices=["all", "c0", "membw", "moe", "gdn", "c4", "pmc", "attn", "proj", "prefill"],
+    p.add_argument("--mode", choices=["all", "c0", "membw", "moe", "gdn", "c4", "pmc", "attn", "proj", "prefill",
+                                       "sample"],
                    default="all",
                    help="c0: only the C0 GEMV loop (for profiling one kernel shape)")
     args = p.parse_args()
@@ -879,9 +933,9 @@ def main():
               "(the path is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
         sys.exit(2)
     res = run_gpu(args)
-    if args.mode in ("c0", "membw", "moe", "gdn", "c4", "pmc", "attn", "proj", "prefill"):
+    if args.mode in ("c0", "membw", "moe", "gdn", "c4", "pmc", "attn", "proj", "prefill", "sample"):
         print(json.dumps({k: res.get(k) for k in ("roofline", "c0_tilings", "membw", "moe", "gdn", "c4", "attn", "proj",
-                                                  "prefill")}),
+                                                  "prefill", "sample")}),
               flush=True)
         return
     line = {

@@ -70,3 +70,7 @@ inline int Launch(halo_engine* eng, const char* name, halo_dim3 grid, halo_dim3 
 }
 
 }  // namespace halo::engine
+
+// The engine a model was created on (model.cpp; used by the GGUF loader).
+struct halo_model;
+halo_engine* halo_model_engine_of(const halo_model* m);

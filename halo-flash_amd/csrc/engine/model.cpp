@@ -789,3 +789,5 @@ int halo_model_positions(halo_model* m, uint32_t* nkv_out, uint32_t S, char* err
 }
 
 }  // extern "C"
+
+halo_engine* halo_model_engine_of(const halo_model* m) { return m->eng; }

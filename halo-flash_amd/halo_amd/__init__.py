@@ -157,6 +157,147 @@ def sample_rows(dev, logits, params, penalties=None):
             a.free()
 
 
+class GgufTensor(C.Structure):
+    """halo_gguf_tensor (include/halo_gguf.h)."""
+    _fields_ = [("name", C.c_void_p), ("name_len", C.c_size_t), ("type", C.c_uint32), ("n_dims", C.c_uint32),
+                ("dims", C.c_uint64 * 8), ("offset", C.c_uint64), ("data", C.c_void_p), ("size_bytes", C.c_uint64)]
+
+
+class Gguf:
+    """A GGUF checkpoint opened by the library's reader (from a file path or from bytes kept alive here)."""
+
+    def __init__(self, path=None, data: bytes | None = None):
+        self._buf = None
+        self.h = None
+        h = C.c_void_p()
+        if path is not None:
+            _call("halo_gguf_open_file", str(path).encode(), C.byref(h))
+        else:
+            self._buf = C.create_string_buffer(data, len(data))
+            _call("halo_gguf_open_memory", self._buf, len(data), C.byref(h))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().halo_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    @property
+    def version(self):
+        return lib().halo_gguf_version(self.h)
+
+    @property
+    def alignment(self):
+        return lib().halo_gguf_alignment(self.h)
+
+    def metadata_count(self):
+        return lib().halo_gguf_metadata_count(self.h)
+
+    def tensor(self, i_or_name):
+        t = GgufTensor()
+        L = lib()
+        rc = (L.halo_gguf_find_tensor(self.h, i_or_name.encode(), C.byref(t)) if isinstance(i_or_name, str)
+              else L.halo_gguf_tensor_at(self.h, i_or_name, C.byref(t)))
+        return t if rc == 0 else None
+
+    def tensors(self):
+        """[(name bytes, type, dims, offset, size, data address)] in file order."""
+        out = []
+        for i in range(lib().halo_gguf_tensor_count(self.h)):
+            t = self.tensor(i)
+            out.append((C.string_at(t.name, t.name_len), t.type, tuple(t.dims[:t.n_dims]), t.offset, t.size_bytes,
+                        t.data))
+        return out
+
+    def keys(self):
+        L = lib()
+        out = []
+        for i in range(self.metadata_count()):
+            p, n = C.c_void_p(), C.c_size_t()
+            L.halo_gguf_metadata_key_at(self.h, i, C.byref(p), C.byref(n))
+            out.append(C.string_at(p, n.value))
+        return out
+
+    def value_text(self, key: bytes):
+        """The value as text (u:/i:/f:/b:/s:/S:/U:/I:/F:, prefixed by the value type), None when absent."""
+        L = lib()
+        ty = L.halo_gguf_metadata_type(self.h, key)
+        if ty < 0:
+            return None
+        hexd = lambda x: np.float64(x).view(np.uint64).item().to_bytes(8, "big").hex()
+
+        def text(prefix, ptr, n):
+            return prefix + C.string_at(ptr, n).hex()
+        if ty in (0, 2, 4, 10):
+            v = C.c_uint64()
+            L.halo_gguf_get_u64(self.h, key, C.byref(v))
+            body = f"u:{v.value}"
+        elif ty in (1, 3, 5, 11):
+            v = C.c_int64()
+            L.halo_gguf_get_i64(self.h, key, C.byref(v))
+            body = f"i:{v.value}"
+        elif ty in (6, 12):
+            v = C.c_double()
+            L.halo_gguf_get_f64(self.h, key, C.byref(v))
+            body = "f:" + hexd(v.value)
+        elif ty == 7:
+            v = C.c_int()
+            L.halo_gguf_get_bool(self.h, key, C.byref(v))
+            body = f"b:{v.value}"
+        elif ty == 8:
+            p, n = C.c_void_p(), C.c_size_t()
+            L.halo_gguf_get_string(self.h, key, C.byref(p), C.byref(n))
+            body = text("s:", p, n.value)
+        else:
+            et, n = C.c_uint32(), C.c_uint64()
+            L.halo_gguf_get_array_info(self.h, key, C.byref(et), C.byref(n))
+            et, n = et.value, n.value
+            if et == 8:
+                parts = []
+                for i in range(n):
+                    p, m = C.c_void_p(), C.c_size_t()
+                    L.halo_gguf_get_array_string(self.h, key, i, C.byref(p), C.byref(m))
+                    parts.append(C.string_at(p, m.value).hex() + ",")
+                body = f"S:{n}:" + "".join(parts)
+            elif et in (6, 12):
+                parts = []
+                for i in range(n):
+                    v = C.c_double()
+                    L.halo_gguf_get_array_f64(self.h, key, i, C.byref(v))
+                    parts.append(hexd(v.value) + ",")
+                body = "F:" + "".join(parts)
+            elif et in (4, 7, 10):
+                parts = []
+                for i in range(n):
+                    v = C.c_uint64()
+                    L.halo_gguf_get_array_u64(self.h, key, i, C.byref(v))
+                    parts.append(f"{v.value},")
+                body = "U:" + "".join(parts)
+            elif et in (5, 11):
+                parts = []
+                for i in range(n):
+                    v = C.c_int64()
+                    L.halo_gguf_get_array_i64(self.h, key, i, C.byref(v))
+                    parts.append(f"{v.value},")
+                body = "I:" + "".join(parts)
+            else:
+                body = "u:0"
+        return f"{ty}|{body}"
+
+    def label(self):
+        b = C.create_string_buffer(64)
+        lib().halo_gguf_quantization_label(self.h, b, 64)
+        return b.value.decode()
+
+    def config(self, base: "ModelConfig | None" = None) -> "ModelConfig":
+        c = ModelConfig() if base is None else base
+        _call("halo_model_config_from_gguf", self.h, C.byref(c))
+        return c
+
+
 class TensorView(C.Structure):
     _fields_ = [("data", C.c_void_p), ("scales", C.c_void_p)] + [(n, C.c_uint32) for n in (
         "kind", "rows", "cols", "qstride")]
@@ -250,6 +391,34 @@ _SIGS = {
     "halo_op_moe_workspace_bytes": (_SZ, [C.POINTER(MoeWeights), _U32], False),
     "halo_op_moe_views": (C.c_int, [C.POINTER(MoeWeights), _U32, _VP, C.POINTER(MoeViews)], True),
     "halo_op_moe_decode": (C.c_int, [_VP, C.POINTER(MoeWeights), _VP, _VP, _U32, _VP, _SZ], True),
+    "halo_gguf_open_file": (C.c_int, [C.c_char_p, C.POINTER(_VP)], True),
+    "halo_gguf_open_memory": (C.c_int, [_VP, _SZ, C.POINTER(_VP)], True),
+    "halo_gguf_close": (None, [_VP], False),
+    "halo_gguf_version": (_U32, [_VP], False),
+    "halo_gguf_alignment": (_U64, [_VP], False),
+    "halo_gguf_tensor_count": (_U64, [_VP], False),
+    "halo_gguf_metadata_count": (_U64, [_VP], False),
+    "halo_gguf_tensor_at": (C.c_int, [_VP, _U64, _VP], False),
+    "halo_gguf_find_tensor": (C.c_int, [_VP, C.c_char_p, _VP], False),
+    "halo_gguf_metadata_type": (C.c_int, [_VP, C.c_char_p], False),
+    "halo_gguf_metadata_key_at": (C.c_int, [_VP, _U64, C.POINTER(_VP), C.POINTER(_SZ)], False),
+    "halo_gguf_get_u32": (C.c_int, [_VP, C.c_char_p, C.POINTER(_U32)], False),
+    "halo_gguf_get_u64": (C.c_int, [_VP, C.c_char_p, C.POINTER(_U64)], False),
+    "halo_gguf_get_i64": (C.c_int, [_VP, C.c_char_p, C.POINTER(C.c_int64)], False),
+    "halo_gguf_get_f32": (C.c_int, [_VP, C.c_char_p, C.POINTER(_F32)], False),
+    "halo_gguf_get_f64": (C.c_int, [_VP, C.c_char_p, C.POINTER(C.c_double)], False),
+    "halo_gguf_get_bool": (C.c_int, [_VP, C.c_char_p, C.POINTER(C.c_int)], False),
+    "halo_gguf_get_string": (C.c_int, [_VP, C.c_char_p, C.POINTER(_VP), C.POINTER(_SZ)], False),
+    "halo_gguf_get_array_info": (C.c_int, [_VP, C.c_char_p, C.POINTER(_U32), C.POINTER(_U64)], False),
+    "halo_gguf_get_array_u64": (C.c_int, [_VP, C.c_char_p, _U64, C.POINTER(_U64)], False),
+    "halo_gguf_get_array_i64": (C.c_int, [_VP, C.c_char_p, _U64, C.POINTER(C.c_int64)], False),
+    "halo_gguf_get_array_f64": (C.c_int, [_VP, C.c_char_p, _U64, C.POINTER(C.c_double)], False),
+    "halo_gguf_get_array_string": (C.c_int, [_VP, C.c_char_p, _U64, C.POINTER(_VP), C.POINTER(_SZ)], False),
+    "halo_gguf_quantization_label": (_SZ, [_VP, C.c_char_p, _SZ], False),
+    "halo_ggml_encoded_bytes": (_U64, [_U32, _U64], False),
+    "halo_gguf_upload_q8_0": (C.c_int, [_VP, _VP, _U64, _U32, _VP, _VP, _U32, _VP, _SZ], True),
+    "halo_model_config_from_gguf": (C.c_int, [_VP, _VP], True),
+    "halo_model_load_gguf": (C.c_int, [_VP, _VP], True),
     "halo_op_sample_workspace_bytes": (_SZ, [_U32, _U32], False),
     "halo_op_sample": (C.c_int, [_VP, _VP, _U32, _U64, _U32, _VP, _VP, _U32, _VP, _VP, _SZ], True),
     "halo_op_moe_decode_norm": (C.c_int, [_VP, C.POINTER(MoeWeights), C.POINTER(ProjInput), _VP, _U32, _VP, _SZ],
@@ -510,6 +679,10 @@ class Model:
         qs = self._download(v.data, v.rows * v.qstride, np.int8).reshape(v.rows, v.qstride)[:, : v.cols]
         d = self._download(v.scales, v.rows * (v.cols // 32) * 2, np.uint16).reshape(v.rows, v.cols // 32)
         return np.ascontiguousarray(qs), d
+
+    def load_gguf(self, g: "Gguf"):
+        """Every weight from a GGUF checkpoint (halo_model_load_gguf)."""
+        _call("halo_model_load_gguf", self.h, g.h)
 
     def logits(self, s: int) -> np.ndarray:
         out = np.empty(self.cfg.vocab, np.float32)

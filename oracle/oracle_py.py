@@ -76,6 +76,16 @@ _REF_SIGS = {
     "ref_hw_threads": (C.c_uint, []),
     "ref_sampler_state": (_U32, [_PF, _U32, _F32, C.c_int32, _F32, _F32, _U32, _F32, _U32, _F32, _F32, _VP, _U32,
                                  _VP, _U32, C.POINTER(C.c_uint64), _VP, _VP, _VP, _U32, C.POINTER(C.c_uint32)]),
+    "ref_gguf_open": (_VP, [_VP, C.c_size_t]),
+    "ref_gguf_close": (None, [_VP]),
+    "ref_gguf_header": (None, [_VP, C.POINTER(C.c_uint32), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
+                               C.POINTER(C.c_uint64)]),
+    "ref_gguf_tensor": (C.c_int, [_VP, C.c_uint64, _VP, C.c_char_p, C.c_size_t, C.POINTER(C.c_uint32),
+                                  C.POINTER(C.c_uint64), C.POINTER(C.c_uint32), C.POINTER(C.c_uint64),
+                                  C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+    "ref_gguf_meta": (C.c_int, [_VP, C.c_char_p, C.c_char_p, C.c_size_t]),
+    "ref_gguf_label": (C.c_uint32, [_VP, C.c_char_p, C.c_size_t]),
+    "ref_encoded_bytes": (C.c_uint64, [C.c_uint32, C.c_uint64]),
     "ref_sample": (_U32, [_PF, _U32, _F32, C.c_int32, _F32, _F32, _U32, _F32, _U32, _F32, _F32, _VP, _U32, _VP, _U32,
                           C.POINTER(C.c_uint64)]),
 }
@@ -230,3 +240,35 @@ def ref_sampler_state(logits, rng, temperature=1.0, top_k=0, top_p=1.0, min_p=0.
                                 C.byref(st), tok.ctypes.data, gen.ctypes.data, rep.ctypes.data, cap, C.byref(npen))
     k = npen.value
     return int(t), int(st.value), (tok[:k].copy(), gen[:k].copy(), rep[:k].copy())
+
+
+def ref_gguf_summary(blob: bytes, keys):
+    """The reference reader's view of a GGUF image: None when it refuses the bytes, else (version, alignment,
+    metadata count, [(name, type, dims, offset, size, data offset)], {key: value text} for `keys`, label)."""
+    L = ref()
+    buf = C.create_string_buffer(blob, len(blob))
+    h = L.ref_gguf_open(buf, len(blob))
+    if not h:
+        return None
+    try:
+        v, a, nm, nt = C.c_uint32(), C.c_uint64(), C.c_uint64(), C.c_uint64()
+        L.ref_gguf_header(h, C.byref(v), C.byref(a), C.byref(nm), C.byref(nt))
+        tensors = []
+        for i in range(nt.value):
+            name = C.create_string_buffer(70000)
+            ty, nd = C.c_uint32(), C.c_uint32()
+            dims = (C.c_uint64 * 8)()
+            off, sz, doff = C.c_uint64(), C.c_uint64(), C.c_uint64()
+            n = L.ref_gguf_tensor(h, i, buf, name, 70000, C.byref(ty), dims, C.byref(nd), C.byref(off), C.byref(sz),
+                                  C.byref(doff))
+            tensors.append((name.raw[:n], ty.value, tuple(dims[:nd.value]), off.value, sz.value, doff.value))
+        meta = {}
+        for k in keys:
+            out = C.create_string_buffer(1 << 20)
+            n = L.ref_gguf_meta(h, k, out, 1 << 20)
+            meta[k] = None if n < 0 else out.value.decode()
+        lab = C.create_string_buffer(64)
+        L.ref_gguf_label(h, lab, 64)
+        return (v.value, a.value, nm.value, tensors, meta, lab.value.decode())
+    finally:
+        L.ref_gguf_close(h)

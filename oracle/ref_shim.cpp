@@ -4,9 +4,13 @@
 // as the timed reference CPU path. Nothing here is linked into the product library.
 #include <cstdint>
 #include <cstring>
+#include <cstdio>
+#include <string>
+#include <variant>
 #include <span>
 #include <thread>
 
+#include "core/gguf.hpp"
 #include "core/quant.hpp"
 #include "core/sampling.hpp"
 #include "model/cpu_ops.hpp"
@@ -128,5 +132,108 @@ std::uint32_t ref_sampler_state(const float* logits, std::uint32_t n, float temp
   }
   *rng = s.rng_state();
   return t;
+}
+
+// ---- GGUF reader (src/core/gguf.cpp GgufReader::OpenMemory and its getters) ------------------------------------
+void* ref_gguf_open(const void* data, std::size_t size) {
+  return halo::core::GgufReader::OpenMemory(data, size).release();
+}
+void ref_gguf_close(void* h) { delete static_cast<halo::core::GgufReader*>(h); }
+void ref_gguf_header(const void* h, std::uint32_t* version, std::uint64_t* alignment, std::uint64_t* n_meta,
+                     std::uint64_t* n_tensors) {
+  const auto* r = static_cast<const halo::core::GgufReader*>(h);
+  *version = r->GetVersion();
+  *alignment = r->GetAlignment();
+  *n_meta = r->GetMetadataCount();
+  *n_tensors = r->GetTensorCount();
+}
+// Tensor i: name (copied, NUL-terminated), type, dims, offset, size and the data pointer's offset from `base`.
+int ref_gguf_tensor(const void* h, std::uint64_t i, const void* base, char* name, std::size_t cap,
+                    std::uint32_t* type, std::uint64_t* dims, std::uint32_t* n_dims, std::uint64_t* offset,
+                    std::uint64_t* size, std::uint64_t* data_offset) {
+  const auto* r = static_cast<const halo::core::GgufReader*>(h);
+  const auto ts = r->GetTensors();
+  if (i >= ts.size()) return -1;
+  const auto& t = ts[i];
+  const std::size_t n = std::min(cap - 1, t.name.size());
+  std::memcpy(name, t.name.data(), n);
+  name[n] = 0;
+  *type = static_cast<std::uint32_t>(t.type);
+  *n_dims = static_cast<std::uint32_t>(t.dimensions.size());
+  for (std::size_t k = 0; k < t.dimensions.size() && k < 8; ++k) dims[k] = t.dimensions[k];
+  *offset = t.offset;
+  *size = t.size_bytes;
+  *data_offset = static_cast<std::uint64_t>(static_cast<const std::uint8_t*>(t.data) -
+                                            static_cast<const std::uint8_t*>(base));
+  return static_cast<int>(t.name.size());
+}
+// A metadata value as text: u:<n> i:<n> f:<bits hex> b:<0|1> s:<hex> S:<n>:<hex,...> U:<n,...> I:<n,...>
+// F:<bits hex,...>; returns the length, or -1 when the key is absent.
+static void HexBytes(std::string* o, std::string_view s) {
+  char b[3];
+  for (unsigned char ch : s) {
+    std::snprintf(b, sizeof b, "%02x", ch);
+    *o += b;
+  }
+}
+static void HexDouble(std::string* o, double v) {
+  std::uint64_t u;
+  std::memcpy(&u, &v, 8);
+  char b[17];
+  std::snprintf(b, sizeof b, "%016llx", static_cast<unsigned long long>(u));
+  *o += b;
+}
+int ref_gguf_meta(const void* h, const char* key, char* out, std::size_t cap) {
+  const auto* r = static_cast<const halo::core::GgufReader*>(h);
+  const auto* m = r->FindMetadata(key);
+  if (m == nullptr) return -1;
+  std::string o;
+  const auto& v = m->value;
+  if (const auto* x = std::get_if<std::uint64_t>(&v)) {
+    o = "u:" + std::to_string(*x);
+  } else if (const auto* x = std::get_if<std::int64_t>(&v)) {
+    o = "i:" + std::to_string(*x);
+  } else if (const auto* x = std::get_if<double>(&v)) {
+    o = "f:";
+    HexDouble(&o, *x);
+  } else if (const auto* x = std::get_if<bool>(&v)) {
+    o = std::string("b:") + (*x ? "1" : "0");
+  } else if (const auto* x = std::get_if<std::string_view>(&v)) {
+    o = "s:";
+    HexBytes(&o, *x);
+  } else if (const auto* x = std::get_if<std::vector<std::string_view>>(&v)) {
+    o = "S:" + std::to_string(x->size()) + ":";
+    for (const auto& e : *x) {
+      HexBytes(&o, e);
+      o += ",";
+    }
+  } else if (const auto* x = std::get_if<std::vector<std::uint64_t>>(&v)) {
+    o = "U:";
+    for (auto e : *x) o += std::to_string(e) + ",";
+  } else if (const auto* x = std::get_if<std::vector<std::int64_t>>(&v)) {
+    o = "I:";
+    for (auto e : *x) o += std::to_string(e) + ",";
+  } else if (const auto* x = std::get_if<std::vector<double>>(&v)) {
+    o = "F:";
+    for (auto e : *x) {
+      HexDouble(&o, e);
+      o += ",";
+    }
+  }
+  o = std::to_string(static_cast<int>(m->type)) + "|" + o;
+  const std::size_t n = std::min(cap - 1, o.size());
+  std::memcpy(out, o.data(), n);
+  out[n] = 0;
+  return static_cast<int>(o.size());
+}
+std::uint32_t ref_gguf_label(const void* h, char* out, std::size_t cap) {
+  const std::string l = static_cast<const halo::core::GgufReader*>(h)->GetQuantizationLabel();
+  const std::size_t n = std::min(cap - 1, l.size());
+  std::memcpy(out, l.data(), n);
+  out[n] = 0;
+  return static_cast<std::uint32_t>(l.size());
+}
+std::uint64_t ref_encoded_bytes(std::uint32_t type, std::uint64_t elements) {
+  return halo::quant::EncodedSizeBytes(static_cast<halo::core::GgmlType>(type), elements);
 }
 }

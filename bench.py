@@ -748,14 +748,28 @@ def run_sample(args, dev, H, res):
             dp = dev.to_device(np.frombuffer(bytes(prm), np.uint8))
             dq = dev.to_device(pen.view(np.uint8).reshape(-1))
             call = lambda: dev.op("sample", x.ptr, rows, V, V, dp.ptr, dq.ptr, 64, o.ptr, ws.ptr, ws.nbytes)
+            call()
+            dev.sync()
+            if args.eager:  # for profilers (rocprofv3 kernel tracing fails inside graph launches)
+                for _ in range(50):
+                    call()
+                dev.sync()
+                dp.free()
+                dq.free()
+                continue
+            # 20 calls per graph so the timing is the kernels', not the host's launch path
+            dev.begin_capture()
             for _ in range(20):
                 call()
+            g = dev.end_capture()
+            dev.launch_graph(g)
             dev.sync()
-            nrep = 200
+            nrep = 20
             dev.timer_start()
             for _ in range(nrep):
-                call()
-            us = dev.timer_stop() * 1e3 / nrep
+                dev.launch_graph(g)
+            us = dev.timer_stop() * 1e3 / (nrep * 20)
+            dev.free_graph(g)
             out[f"{name}_rows{rows}"] = round(us, 2)
             log(f"[bench] sample {name} rows={rows}: {us:.2f} us")
             dp.free()

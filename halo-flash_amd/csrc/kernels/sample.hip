@@ -1,34 +1,40 @@
 // Device-side token sampling with SamplerState semantics (reference src/core/sampling.cpp:494-563 Distribution /
 // Sample, 616-700 SampleGreedy / LinearDistribution, 702-842 PrepareSelected; penalties 69-80; RNG 845-863).
 //
-// One 1024-thread block per row. The reference device kernels (src/kernels/core.hip:1406-2116) weight tokens in
-// 2^-40 fixed point so sums are order-independent, and draw a token of the same distribution; this kernel instead
-// repeats the CPU's double arithmetic in the CPU's order wherever the kept set is small enough to sort on chip,
-// so the draw itself is the CPU's:
-//   1. penalized logits in double (the penalized tokens marked in an LDS bitmap, their entries found by binary
-//      search in the sorted penalty list), the maximum (ties to the lower token) and the finite count;
-//   2. temperature 0: the argmax;
-//   3. linear path (top_k == 0, top_p == 1, no min-p floor): weights exp((v - max) / T) zeroed under the min-p
-//      threshold, their sum, and the draw walked in token order (each thread owns a contiguous token range; the
-//      range holding the uniform is found by a scan of range sums and walked sequentially);
-//   4. sorted path: the best min(candidates, 4096) tokens are collected (a 4096-bin histogram of max - v picks a
-//      cut; an exact radix select over (value, token) takes over when ties or a dense bin overflow the cap),
-//      bitonic-sorted by (value descending, token ascending) in LDS, and top-p, min-p, the weight sum, the zero
-//      drop and the draw run over that list in list order on one lane, as the CPU runs them;
-//   5. when the kept set reaches past the sorted 4096 (a flat row with a loose top-p or a min-p floor), the cut
-//      and the draw are radix selects over the whole row on 2^-40 fixed-point weights (integer sums, so two runs
-//      agree bit for bit); the nonzero count stays exact in double. Only this path can draw differently from the
-//      CPU, and only when the uniform falls within rounding of a boundary.
-// Every reduction runs in a fixed order, so a row's result never depends on timing.
+// The reference device kernels (src/kernels/core.hip:1406-2116) weight tokens in 2^-40 fixed point so sums are
+// order-independent, and draw a token of the same distribution; these kernels instead repeat the CPU's double
+// arithmetic in the CPU's order wherever the kept set is small enough to sort on chip, so the draw itself is the
+// CPU's. Four launches per call; the first three spread the vocabulary over blocks of 4096 tokens, the last runs
+// one 1024-thread block per row:
+//   1. prep: penalized logits in double (penalized tokens marked in an LDS bitmap per slice, their entries found
+//      by binary search in the sorted penalty list), each slice's maximum (ties to the lower token) and finite
+//      count;
+//   2. weights: linear path (top_k == 0, top_p == 1, no min-p floor): weights exp((v - max) / T), zeroed under the
+//      min-p threshold, with per-slice sums, nonzero counts, last nonzero index and least nonzero weight; sorted
+//      path: a 4096-bin histogram of max - v (bins 1/64 wide) and, for top-p without top-k over more than 1024
+//      tokens, the per-slice weight sums;
+//   3. collect (sorted path): the bins that hold the best min(candidates, 4096) tokens, or the full bins before
+//      them, are cut from the histogram and their tokens appended to a candidate list;
+//   4. final: temperature 0 takes the argmax; the linear path finds the slice, then the 4-token range, holding the
+//      uniform and walks it in token order; the sorted path bitonic-sorts the candidates by (value descending,
+//      token ascending) in LDS (an exact radix select over (value, token) replaces the histogram cut when ties
+//      overflow it) and runs top-p, min-p, the weight sum, the zero drop and the draw over that list in list order
+//      on one lane, as the CPU runs them; when the kept set reaches past the sorted candidates (a flat row with a
+//      loose top-p or a min-p floor), the cut and the draw are radix selects over the whole row on 2^-40
+//      fixed-point weights (integer sums, so runs agree bit for bit) and the nonzero count stays exact in double.
+// Only sums formed across slices or threads (the linear path's total, the full top-p sum, the fixed-point path)
+// differ from the CPU's sequential sums, by rounding; they move a draw only when the uniform falls within rounding
+// of a CDF boundary. Every reduction runs in a fixed order, so a row's result never depends on timing.
 #include "common.h"
 #include "halo_sample.h"
+#include "sample_layout.h"
 
 namespace halo::sample {
 
 constexpr std::uint32_t kThreads = 1024;
 constexpr std::uint32_t kWaves = kThreads / kWave;
-constexpr std::uint32_t kCap = 4096;   // candidates sorted on chip
-constexpr std::uint32_t kBins = 4096;  // histogram of max - v, bins 1/64 wide, the last one open-ended
+constexpr std::uint32_t kCap = kSampleCap;   // candidates sorted on chip
+constexpr std::uint32_t kBins = kSampleBins;  // histogram of max - v, bins 1/64 wide, the last one open-ended
 constexpr double kFix = 1099511627776.0;  // 2^40
 constexpr std::uint64_t kNoBound = ~0ull;
 
@@ -89,33 +95,19 @@ __device__ __forceinline__ double Penalize(double l, const HaloSampleParams& p, 
 }
 
 // ---- block-wide reductions in a fixed order (every thread calls; every thread gets the result) --------------
-__device__ double BlockSumD(double v, Lds& s) {
+template <typename T>
+__device__ T BlockSum(T v, T* red) {
   for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  if (threadIdx.x % kWave == 0) s.rd[threadIdx.x / kWave] = v;
+  if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = v;
   __syncthreads();
-  double r = 0.0;
-  for (std::uint32_t i = 0; i < kWaves; ++i) r += s.rd[i];
+  T r = 0;
+  for (std::uint32_t i = 0; i < blockDim.x / kWave; ++i) r += red[i];
   __syncthreads();
   return r;
 }
-__device__ std::uint32_t BlockSumU(std::uint32_t v, Lds& s) {
-  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  if (threadIdx.x % kWave == 0) s.ru[threadIdx.x / kWave] = v;
-  __syncthreads();
-  std::uint32_t r = 0;
-  for (std::uint32_t i = 0; i < kWaves; ++i) r += s.ru[i];
-  __syncthreads();
-  return r;
-}
-__device__ unsigned long long BlockSumQ(unsigned long long v, Lds& s) {
-  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  if (threadIdx.x % kWave == 0) s.rq[threadIdx.x / kWave] = v;
-  __syncthreads();
-  unsigned long long r = 0;
-  for (std::uint32_t i = 0; i < kWaves; ++i) r += s.rq[i];
-  __syncthreads();
-  return r;
-}
+__device__ double BlockSumD(double v, Lds& s) { return BlockSum(v, s.rd); }
+__device__ std::uint32_t BlockSumU(std::uint32_t v, Lds& s) { return BlockSum(v, s.ru); }
+__device__ unsigned long long BlockSumQ(unsigned long long v, Lds& s) { return BlockSum(v, s.rq); }
 // Exclusive prefix over threads in thread order; *total = the block total.
 template <typename T>
 __device__ T BlockExclScan(T v, T* wave_tot, T* total) {
@@ -130,7 +122,7 @@ __device__ T BlockExclScan(T v, T* wave_tot, T* total) {
   if (lane == kWave - 1) wave_tot[w] = inc;
   __syncthreads();
   T base = 0, tot = 0;
-  for (std::uint32_t i = 0; i < kWaves; ++i) {
+  for (std::uint32_t i = 0; i < blockDim.x / kWave; ++i) {
     if (i < w) base += wave_tot[i];
     tot += wave_tot[i];
   }
@@ -139,7 +131,7 @@ __device__ T BlockExclScan(T v, T* wave_tot, T* total) {
   return base + exc;
 }
 // Smallest (key, token) pair over the block (the best candidate when keys are DescKeys).
-__device__ void BlockMinPair(std::uint64_t& k, std::uint32_t& t, Lds& s) {
+__device__ void BlockMinPair(std::uint64_t& k, std::uint32_t& t, unsigned long long* rk, std::uint32_t* rt) {
   for (int o = kWave / 2; o > 0; o >>= 1) {
     const std::uint64_t ok = __shfl_xor(k, o, kWave);
     const std::uint32_t ot = __shfl_xor(t, o, kWave);
@@ -149,19 +141,20 @@ __device__ void BlockMinPair(std::uint64_t& k, std::uint32_t& t, Lds& s) {
     }
   }
   if (threadIdx.x % kWave == 0) {
-    s.rq[threadIdx.x / kWave] = k;
-    s.ru[threadIdx.x / kWave] = t;
+    rk[threadIdx.x / kWave] = k;
+    rt[threadIdx.x / kWave] = t;
   }
   __syncthreads();
-  k = s.rq[0];
-  t = s.ru[0];
-  for (std::uint32_t i = 1; i < kWaves; ++i)
-    if (s.rq[i] < k || (s.rq[i] == k && s.ru[i] < t)) {
-      k = s.rq[i];
-      t = s.ru[i];
+  k = rk[0];
+  t = rt[0];
+  for (std::uint32_t i = 1; i < blockDim.x / kWave; ++i)
+    if (rk[i] < k || (rk[i] == k && rt[i] < t)) {
+      k = rk[i];
+      t = rt[i];
     }
   __syncthreads();
 }
+__device__ void BlockMinPair(std::uint64_t& k, std::uint32_t& t, Lds& s) { BlockMinPair(k, t, s.rq, s.ru); }
 
 __device__ __forceinline__ bool Within(std::uint64_t kd, std::uint32_t t, std::uint64_t lk, std::uint32_t lt) {
   return kd < lk || (kd == lk && t <= lt);
@@ -261,63 +254,242 @@ __device__ void Finish(HaloSampleOut* out, std::uint32_t token, std::uint32_t li
   }
 }
 
+__device__ __forceinline__ bool BadParams(const HaloSampleParams& p, std::uint32_t V, std::uint32_t pen_stride) {
+  return p.vocab != V || V == 0 || V > HALO_SAMPLE_MAX_VOCAB || p.n_penalties > pen_stride ||
+         p.n_penalties > HALO_SAMPLE_MAX_PENALTIES || !isfinite(p.temperature) || p.temperature < 0.0f ||
+         !(p.top_p >= 0.0f && p.top_p <= 1.0f) || !(p.min_p >= 0.0f && p.min_p <= 1.0f) ||
+         !isfinite(p.repeat_penalty) || !(p.repeat_penalty > 0.0f) || !isfinite(p.frequency_penalty) ||
+         !isfinite(p.presence_penalty) || p.top_k > 0x7FFFFFFFu;
+}
+__device__ __forceinline__ bool LinearPath(const HaloSampleParams& p) {
+  return p.top_k == 0 && p.top_p == 1.0f && !(p.min_p > 0.0f && p.min_keep > 1);
+}
+__device__ __forceinline__ std::uint32_t Bin(double M, double a) {
+  const double d = M - a;
+  return d < 64.0 ? static_cast<std::uint32_t>(d * 64.0) : kBins - 1;
+}
+
+// Views of one launch's workspace.
+struct Ws {
+  double* val;
+  unsigned long long* fx;
+  unsigned long long* pkey;
+  std::uint32_t *ptok, *pnf;
+  double* psum;
+  std::uint32_t *pnz, *plast;
+  double* pminw;
+  std::uint32_t* hist;
+  unsigned long long* ckey;
+  std::uint32_t *ctok, *cn;
+};
+__device__ __forceinline__ Ws Carve(void* base, std::uint32_t rows, std::uint32_t V) {
+  const Layout l = MakeLayout(rows, V);
+  char* b = static_cast<char*>(base);
+  Ws w;
+  w.val = reinterpret_cast<double*>(b + l.val);
+  w.fx = reinterpret_cast<unsigned long long*>(b + l.fx);
+  w.pkey = reinterpret_cast<unsigned long long*>(b + l.pkey);
+  w.ptok = reinterpret_cast<std::uint32_t*>(b + l.ptok);
+  w.pnf = reinterpret_cast<std::uint32_t*>(b + l.pnf);
+  w.psum = reinterpret_cast<double*>(b + l.psum);
+  w.pnz = reinterpret_cast<std::uint32_t*>(b + l.pnz);
+  w.plast = reinterpret_cast<std::uint32_t*>(b + l.plast);
+  w.pminw = reinterpret_cast<double*>(b + l.pminw);
+  w.hist = reinterpret_cast<std::uint32_t*>(b + l.hist);
+  w.ckey = reinterpret_cast<unsigned long long*>(b + l.ckey);
+  w.ctok = reinterpret_cast<std::uint32_t*>(b + l.ctok);
+  w.cn = reinterpret_cast<std::uint32_t*>(b + l.cn);
+  return w;
+}
+
+// The row's maximum (as DescKey, ties to the lower token) and finite count from the per-block partials, in block
+// order; every thread gets them.
+struct RowMax {
+  std::uint64_t key;
+  std::uint32_t tok, nf;
+};
+__device__ RowMax ReduceParts(const Ws& w, std::uint32_t row, std::uint32_t nb, unsigned long long* rk,
+                              std::uint32_t* rt, std::uint32_t* ru) {
+  std::uint64_t k = kNoBound;
+  std::uint32_t tk = 0xFFFFFFFFu, nf = 0;
+  for (std::uint32_t b = threadIdx.x; b < nb; b += blockDim.x) {
+    const std::size_t o = static_cast<std::size_t>(row) * nb + b;
+    const std::uint64_t kb = w.pkey[o];
+    const std::uint32_t tb = w.ptok[o];
+    if (kb < k || (kb == k && tb < tk)) {
+      k = kb;
+      tk = tb;
+    }
+    nf += w.pnf[o];
+  }
+  nf = BlockSum(nf, ru);
+  BlockMinPair(k, tk, rk, rt);
+  return RowMax{k, tk, nf};
+}
+
+// Sequential double chains in list order on one lane (they must stay left-to-right to round as the CPU does).
+// Each chunk of 16 runs its adds back to back without branches (the LDS loads issued ahead) and tests the 16
+// partial results afterwards, so an element costs about one add latency.
+__device__ double SeqSum(const double* w, std::uint32_t n) {
+  double sum = 0.0;
+  for (std::uint32_t k0 = 0; k0 < n; k0 += 16) {
+    double v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = k0 + j < n ? w[k0 + j] : 0.0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) sum += v[j];  // adding +0.0 past the end leaves the sum unchanged
+  }
+  return sum;
+}
+// The first k (1-based) with k >= minimum and w[0] + ... + w[k-1] >= target, scanning at most n entries; n + 1
+// when the scan ends first.
+__device__ std::uint32_t SeqCut(const double* w, std::uint32_t n, std::uint32_t minimum, double target) {
+  double cum = 0.0;
+  for (std::uint32_t k0 = 0; k0 < n; k0 += 16) {
+    double v[16], c[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = k0 + j < n ? w[k0 + j] : 0.0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      cum += v[j];
+      c[j] = cum;
+    }
+    std::uint32_t hit = 16;
+#pragma unroll
+    for (int j = 15; j >= 0; --j)
+      if (k0 + j < n && k0 + j + 1 >= minimum && c[j] >= target) hit = j;
+    if (hit < 16) return k0 + hit + 1;
+  }
+  return n + 1;
+}
+// The first i with u - p[0] - ... - p[i] < 0, or n when none.
+__device__ std::uint32_t SeqWalk(const double* pr, std::uint32_t n, double u) {
+  double r = u;
+  for (std::uint32_t k0 = 0; k0 < n; k0 += 16) {
+    double v[16], c[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = k0 + j < n ? pr[k0 + j] : 0.0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      r -= v[j];
+      c[j] = r;
+    }
+    std::uint32_t hit = 16;
+#pragma unroll
+    for (int j = 15; j >= 0; --j)
+      if (k0 + j < n && c[j] < 0.0) hit = j;
+    if (hit < 16) return k0 + hit;
+  }
+  return n;
+}
+
+// The histogram cut of the sorted path: the bins [0, cut] hold the candidates sorted on chip. Rc = min(K0, cap)
+// candidates are needed; the bin where the count reaches Rc is the cut when the bins up to it fit the cap. When they
+// do not, a top-k row (which needs all of its K0) falls back to an exact radix selection (returns false); a row
+// without top-k takes the bins before it (still a full prefix of the sorted order), unless that is empty.
+__device__ bool HistCut(const std::uint32_t* hist, std::uint32_t Rc, bool topk, std::uint32_t* cut,
+                        std::uint32_t* red, std::uint32_t* out2) {
+  const std::uint32_t per = kBins / blockDim.x;
+  std::uint32_t c = 0;
+  for (std::uint32_t j = 0; j < per; ++j) c += hist[threadIdx.x * per + j];
+  std::uint32_t tot;
+  std::uint32_t base = BlockExclScan(c, red, &tot);
+  if (threadIdx.x == 0) {
+    out2[0] = 0xFFFFFFFFu;
+    out2[1] = 0;
+  }
+  __syncthreads();
+  for (std::uint32_t j = 0; j < per; ++j) {
+    const std::uint32_t bin = threadIdx.x * per + j, h = hist[bin];
+    if (base < Rc && base + h >= Rc) {
+      out2[0] = bin;
+      out2[1] = base;  // count before the crossing bin
+      out2[2] = base + h;
+    }
+    base += h;
+  }
+  __syncthreads();
+  const std::uint32_t bc = out2[0], before = out2[1], through = out2[2];
+  __syncthreads();
+  if (bc == 0xFFFFFFFFu) return false;
+  if (through <= kCap) {
+    *cut = bc;
+    return true;
+  }
+  if (topk || before == 0) return false;
+  *cut = bc - 1;
+  return true;
+}
+
 }  // namespace halo::sample
 
-// One draw per row. logits [rows][row_stride] fp32 (vocab tokens each); params [rows]; penalties
-// [rows][pen_stride] (params[r].n_penalties used, sorted by token); vals [rows][vocab] double and fx
-// [rows][vocab] u64 are workspace; out [rows]. Block 1024, grid rows.
+// ---- pass 1: penalized values and per-block maxima ---------------------------------------------------------------
+// grid (nb, rows), block 1024; slice b of row r: tokens [4096 b, 4096 b + 4096). Also clears the row's histogram
+// and candidate counter for the later passes.
 extern "C" __global__ void __launch_bounds__(1024)
-    halo_sample_rows(const float* __restrict__ logits, std::uint64_t row_stride,
+    halo_sample_prep(const float* __restrict__ logits, std::uint64_t row_stride,
                      const HaloSampleParams* __restrict__ params, const HaloPenalty* __restrict__ penalties,
-                     std::uint32_t pen_stride, std::uint32_t V, double* __restrict__ vals,
-                     unsigned long long* __restrict__ fxs, HaloSampleOut* __restrict__ outs) {
+                     std::uint32_t pen_stride, std::uint32_t V, std::uint32_t rows, void* ws) {
   using namespace halo::sample;
-  __shared__ Lds s;
-  const std::uint32_t row = blockIdx.x, t = threadIdx.x;
+  __shared__ std::uint32_t bm[kSampleSlice / 32];
+  __shared__ std::uint32_t prange[2];
+  __shared__ unsigned long long rk[kWaves];
+  __shared__ std::uint32_t rt[kWaves], ru[kWaves];
+  const std::uint32_t row = blockIdx.y, b = blockIdx.x, t = threadIdx.x, nb = gridDim.x;
   const HaloSampleParams p = params[row];
+  if (BadParams(p, V, pen_stride)) return;
+  const Ws w = Carve(ws, rows, V);
+  for (std::uint32_t i = b * blockDim.x + t; i < kBins; i += nb * blockDim.x)
+    w.hist[static_cast<std::size_t>(row) * kBins + i] = 0;
+  if (b == 0 && t == 0) w.cn[row] = 0;
   const float* x = logits + row * row_stride;
   const HaloPenalty* pen = penalties + static_cast<std::size_t>(row) * pen_stride;
-  double* val = vals + static_cast<std::size_t>(row) * V;
-  unsigned long long* fx = fxs + static_cast<std::size_t>(row) * V;
-  HaloSampleOut* out = outs + row;
-  std::uint64_t rng = p.rng;
-
-  const bool bad = p.vocab != V || V == 0 || V > HALO_SAMPLE_MAX_VOCAB || p.n_penalties > pen_stride ||
-                   p.n_penalties > HALO_SAMPLE_MAX_PENALTIES || !isfinite(p.temperature) || p.temperature < 0.0f ||
-                   !(p.top_p >= 0.0f && p.top_p <= 1.0f) || !(p.min_p >= 0.0f && p.min_p <= 1.0f) ||
-                   !isfinite(p.repeat_penalty) || !(p.repeat_penalty > 0.0f) || !isfinite(p.frequency_penalty) ||
-                   !isfinite(p.presence_penalty) || p.top_k > 0x7FFFFFFFu;
-  if (bad) {
-    Finish(out, HALO_SAMPLE_BAD_PARAMS, 0, rng);
-    return;
-  }
-
-  // 1. penalized values, maximum, finite count
+  const std::uint32_t lo = b * kSampleSlice, hi = min(V, lo + kSampleSlice);
   const std::uint32_t npen = p.n_penalties;
   if (npen) {
-    for (std::uint32_t i = t; i < (V + 31) / 32; i += kThreads) s.a.bitmap[i] = 0;
+    for (std::uint32_t i = t; i < kSampleSlice / 32; i += blockDim.x) bm[i] = 0;
+    if (t < 2) {  // first entry with token >= lo (t = 0) / >= hi (t = 1)
+      const std::uint32_t key = t == 0 ? lo : hi;
+      std::uint32_t a = 0, z = npen;
+      while (a < z) {
+        const std::uint32_t mid = (a + z) / 2;
+        if (pen[mid].token < key) a = mid + 1;
+        else z = mid;
+      }
+      prange[t] = a;
+    }
     __syncthreads();
-    for (std::uint32_t j = t; j < npen; j += kThreads) {
+    for (std::uint32_t j = prange[0] + t; j < prange[1]; j += blockDim.x) {
       const std::uint32_t tk = pen[j].token;
-      if (tk < V) atomicOr(&s.a.bitmap[tk >> 5], 1u << (tk & 31));
+      if (tk >= lo && tk < hi) atomicOr(&bm[(tk - lo) >> 5], 1u << ((tk - lo) & 31));
     }
     __syncthreads();
   }
   std::uint64_t best_k = kNoBound;
   std::uint32_t best_t = 0xFFFFFFFFu, nf = 0;
-  for (std::uint32_t i = t; i < V; i += kThreads) {
-    const float l = x[i];
+  double* val = w.val + static_cast<std::size_t>(row) * V;
+  constexpr int kPer = kSampleSlice / kThreads;
+  float lv[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const std::uint32_t i = lo + t + kThreads * j;
+    lv[j] = i < hi ? x[i] : -INFINITY;
+  }
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const std::uint32_t i = lo + t + kThreads * j;
+    if (i >= hi) continue;
     double a = -INFINITY;
-    if (isfinite(l)) {
-      a = l;
-      if (npen && (s.a.bitmap[i >> 5] >> (i & 31)) & 1u) {
-        std::uint32_t lo = 0, hi = npen;
-        while (lo < hi) {
-          const std::uint32_t mid = (lo + hi) / 2;
-          if (pen[mid].token < i) lo = mid + 1;
-          else hi = mid;
+    if (isfinite(lv[j])) {
+      a = lv[j];
+      if (npen && (bm[(i - lo) >> 5] >> ((i - lo) & 31)) & 1u) {
+        std::uint32_t q = prange[0], z = prange[1];
+        while (q < z) {
+          const std::uint32_t mid = (q + z) / 2;
+          if (pen[mid].token < i) q = mid + 1;
+          else z = mid;
         }
-        if (lo < npen && pen[lo].token == i) a = Penalize(a, p, pen[lo]);  // an unsorted list finds nothing
+        if (q < prange[1] && pen[q].token == i) a = Penalize(a, p, pen[q]);
       }
       ++nf;
       const std::uint64_t kd = DescKey(a);
@@ -328,8 +500,168 @@ extern "C" __global__ void __launch_bounds__(1024)
     }
     val[i] = a;
   }
-  nf = BlockSumU(nf, s);
-  BlockMinPair(best_k, best_t, s);
+  nf = BlockSum(nf, ru);
+  BlockMinPair(best_k, best_t, rk, rt);
+  if (t == 0) {
+    const std::size_t o = static_cast<std::size_t>(row) * nb + b;
+    w.pkey[o] = best_k;
+    w.ptok[o] = best_t;
+    w.pnf[o] = nf;
+  }
+}
+
+// ---- pass 2: weights (linear path) or the histogram and full weight sum (sorted path) ----------------------------
+// grid (nb, rows), block 1024.
+extern "C" __global__ void __launch_bounds__(1024)
+    halo_sample_weights(const HaloSampleParams* __restrict__ params, std::uint32_t pen_stride, std::uint32_t V,
+                        std::uint32_t rows, void* ws) {
+  using namespace halo::sample;
+  __shared__ double rd[kWaves];
+  __shared__ std::uint32_t ru[kWaves];
+  __shared__ unsigned long long rk[kWaves];
+  __shared__ std::uint32_t rt[kWaves];
+  __shared__ std::uint32_t lh[kBins];
+  const std::uint32_t row = blockIdx.y, b = blockIdx.x, t = threadIdx.x, nb = gridDim.x;
+  const HaloSampleParams p = params[row];
+  if (BadParams(p, V, pen_stride)) return;
+  const Ws w = Carve(ws, rows, V);
+  const RowMax m = ReduceParts(w, row, nb, rk, rt, ru);
+  if (m.nf == 0 || p.temperature == 0.0f) return;
+  const double M = KeyValue(m.key), T = p.temperature;
+  double* val = w.val + static_cast<std::size_t>(row) * V;
+  const std::uint32_t lo = b * kSampleSlice, hi = min(V, lo + kSampleSlice);
+  constexpr int kPer = kSampleSlice / kThreads;
+  const std::size_t o = static_cast<std::size_t>(row) * nb + b;
+  if (LinearPath(p)) {
+    const double thr = p.min_p > 0.0f ? M + T * log(static_cast<double>(p.min_p)) : -INFINITY;
+    double sum = 0.0, minw = INFINITY;
+    std::uint32_t nz = 0, last = 0;
+    double av[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const std::uint32_t i = lo + t + kThreads * j;
+      av[j] = i < hi ? val[i] : -INFINITY;
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const std::uint32_t i = lo + t + kThreads * j;
+      if (i >= hi) continue;
+      const double a = av[j];
+      const double wt = (a != -INFINITY && a >= thr) ? exp((a - M) / T) : 0.0;
+      val[i] = wt;
+      sum += wt;
+      if (wt != 0.0) {
+        ++nz;
+        last = i + 1;
+        minw = fmin(minw, wt);
+      }
+    }
+    sum = BlockSum(sum, rd);
+    nz = BlockSum(nz, ru);
+    std::uint64_t lk = ~static_cast<std::uint64_t>(last);
+    std::uint32_t lt = 0;
+    BlockMinPair(lk, lt, rk, rt);
+    std::uint64_t mk = static_cast<std::uint64_t>(__double_as_longlong(minw));  // positive doubles order as bits
+    std::uint32_t mt = 0;
+    BlockMinPair(mk, mt, rk, rt);
+    if (t == 0) {
+      w.psum[o] = sum;
+      w.pnz[o] = nz;
+      w.plast[o] = static_cast<std::uint32_t>(~lk);
+      w.pminw[o] = __longlong_as_double(static_cast<long long>(mk));
+    }
+    return;
+  }
+  const bool has_full = p.top_k == 0 && p.top_p < 1.0f && V > 1024;
+  for (std::uint32_t i = t; i < kBins; i += blockDim.x) lh[i] = 0;
+  __syncthreads();
+  double sum = 0.0;
+  double av[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const std::uint32_t i = lo + t + kThreads * j;
+    av[j] = i < hi ? val[i] : -INFINITY;
+  }
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const double a = av[j];
+    if (a == -INFINITY) continue;
+    if (has_full) sum += exp((a - M) / T);
+    atomicAdd(&lh[Bin(M, a)], 1u);
+  }
+  __syncthreads();
+  for (std::uint32_t i = t; i < kBins; i += blockDim.x)
+    if (lh[i]) atomicAdd(&w.hist[static_cast<std::size_t>(row) * kBins + i], lh[i]);
+  sum = BlockSum(sum, rd);
+  if (t == 0) w.psum[o] = sum;
+}
+
+// ---- pass 3: candidates of the sorted path -----------------------------------------------------------------------
+// grid (nb, rows), block 1024: every block finds the same histogram cut and appends its tokens in the bins up to it.
+extern "C" __global__ void __launch_bounds__(1024)
+    halo_sample_collect(const HaloSampleParams* __restrict__ params, std::uint32_t pen_stride, std::uint32_t V,
+                        std::uint32_t rows, void* ws) {
+  using namespace halo::sample;
+  __shared__ unsigned long long rk[kWaves];
+  __shared__ std::uint32_t rt[kWaves], ru[kWaves], o2[3], count, base;
+  const std::uint32_t row = blockIdx.y, b = blockIdx.x, t = threadIdx.x, nb = gridDim.x;
+  const HaloSampleParams p = params[row];
+  if (BadParams(p, V, pen_stride)) return;
+  const Ws w = Carve(ws, rows, V);
+  const RowMax m = ReduceParts(w, row, nb, rk, rt, ru);
+  if (m.nf == 0 || p.temperature == 0.0f || LinearPath(p)) return;
+  const std::uint32_t floor_keep = p.min_keep > 1 ? p.min_keep : 1;
+  const std::uint64_t keep_cfg =
+      p.top_k > 0 ? min(static_cast<std::uint64_t>(V), static_cast<std::uint64_t>(max(p.top_k, floor_keep)))
+                  : static_cast<std::uint64_t>(V);
+  const std::uint32_t K0 = static_cast<std::uint32_t>(min(static_cast<std::uint64_t>(m.nf), keep_cfg));
+  std::uint32_t cut;
+  if (!HistCut(w.hist + static_cast<std::size_t>(row) * kBins, min(K0, kCap), p.top_k > 0, &cut, ru, o2)) return;
+  const double M = KeyValue(m.key);
+  const double* val = w.val + static_cast<std::size_t>(row) * V;
+  const std::uint32_t lo = b * kSampleSlice, hi = min(V, lo + kSampleSlice);
+  constexpr int kPer = kSampleSlice / kThreads;
+  if (t == 0) count = 0;
+  __syncthreads();
+  std::uint32_t slot[kPer];
+  double av[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const std::uint32_t i = lo + t + kThreads * j;
+    av[j] = i < hi ? val[i] : -INFINITY;
+    slot[j] = av[j] != -INFINITY && Bin(M, av[j]) <= cut ? atomicAdd(&count, 1u) : 0xFFFFFFFFu;
+  }
+  __syncthreads();
+  if (t == 0) base = count ? atomicAdd(&w.cn[row], count) : 0;  // one reservation per block
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kPer; ++j)
+    if (slot[j] != 0xFFFFFFFFu) {
+      const std::size_t o = static_cast<std::size_t>(row) * kCap + base + slot[j];
+      w.ckey[o] = DescKey(av[j]);
+      w.ctok[o] = lo + t + kThreads * j;
+    }
+}
+
+// ---- pass 4: the draw --------------------------------------------------------------------------------------------
+// grid rows, block 1024. logits are read only through pass 1; out [rows].
+extern "C" __global__ void __launch_bounds__(1024)
+    halo_sample_final(const HaloSampleParams* __restrict__ params, std::uint32_t pen_stride, std::uint32_t V,
+                      std::uint32_t rows, void* ws, HaloSampleOut* __restrict__ outs) {
+  using namespace halo::sample;
+  __shared__ Lds s;
+  const std::uint32_t row = blockIdx.x, t = threadIdx.x, nb = Blocks(V);
+  const HaloSampleParams p = params[row];
+  HaloSampleOut* out = outs + row;
+  std::uint64_t rng = p.rng;
+  if (BadParams(p, V, pen_stride)) {
+    Finish(out, HALO_SAMPLE_BAD_PARAMS, 0, rng);
+    return;
+  }
+  const Ws w = Carve(ws, rows, V);
+  const RowMax m = ReduceParts(w, row, nb, s.rq, s.ru + 0, s.ru);
+  const std::uint64_t best_k = m.key;
+  const std::uint32_t best_t = m.tok, nf = m.nf;
   if (nf == 0) {
     Finish(out, HALO_SAMPLE_NO_FINITE, 0, rng);
     return;
@@ -338,55 +670,84 @@ extern "C" __global__ void __launch_bounds__(1024)
     Finish(out, best_t, 1, rng);
     return;
   }
+  double* val = w.val + static_cast<std::size_t>(row) * V;
+  unsigned long long* fx = w.fx + static_cast<std::size_t>(row) * V;
+  const std::size_t po = static_cast<std::size_t>(row) * nb;
   const double M = KeyValue(best_k);
   const double T = p.temperature;
   const std::uint32_t floor_keep = p.min_keep > 1 ? p.min_keep : 1;
 
-  // 2. linear path: token order
-  if (p.top_k == 0 && p.top_p == 1.0f && !(p.min_p > 0.0f && p.min_keep > 1)) {
-    const double thr = p.min_p > 0.0f ? M + T * log(static_cast<double>(p.min_p)) : -INFINITY;
-    const std::uint32_t per = (V + kThreads - 1) / kThreads, lo = min(V, t * per), hi = min(V, lo + per);
-    double part = 0.0;
-    for (std::uint32_t i = lo; i < hi; ++i) {
-      const double a = val[i];
-      const double w = (a != -INFINITY && a >= thr) ? exp((a - M) / T) : 0.0;
-      val[i] = w;
-      part += w;
+  // linear path: token order; val holds the weights
+  if (LinearPath(p)) {
+    // per-slice partials, one per thread (nb <= 64)
+    double ps = 0.0, mw = INFINITY;
+    std::uint32_t pz = 0, pl = 0;
+    if (t < nb) {
+      ps = w.psum[po + t];
+      pz = w.pnz[po + t];
+      pl = w.plast[po + t];
+      if (pz) mw = w.pminw[po + t];
     }
-    const double total = BlockSumD(part, s);
-    std::uint32_t nz = 0, last = 0;
-    double ps = 0.0;
-    for (std::uint32_t i = lo; i < hi; ++i) {
-      const double v = val[i] / total;
-      if (v != 0.0) {
-        ++nz;
-        last = i + 1;
-        ps += v;
-      }
-    }
-    const std::uint32_t live = BlockSumU(nz, s);
-    std::uint64_t lk = ~static_cast<std::uint64_t>(last);  // the largest index with a nonzero weight
+    const double total = BlockSumD(ps, s);
+    std::uint32_t live = BlockSumU(pz, s);
+    std::uint64_t lk = ~static_cast<std::uint64_t>(pl);
     std::uint32_t lt = 0;
     BlockMinPair(lk, lt, s);
-    const std::uint32_t last_nz = static_cast<std::uint32_t>(~lk) - 1;
+    std::uint32_t last = static_cast<std::uint32_t>(~lk);
+    std::uint64_t mk = static_cast<std::uint64_t>(__double_as_longlong(mw));  // positive doubles order as bits
+    std::uint32_t mt = 0;
+    BlockMinPair(mk, mt, s);
+    const bool exact_count = __longlong_as_double(static_cast<long long>(mk)) / total != 0.0;
+    if (!exact_count) {  // weights near the underflow of w / total: count the way the CPU drops them
+      std::uint32_t nz = 0, lst = 0;
+      for (std::uint32_t i = t; i < V; i += kThreads)
+        if (val[i] / total != 0.0) {
+          ++nz;
+          lst = i + 1;
+        }
+      live = BlockSumU(nz, s);
+      std::uint64_t lk2 = ~static_cast<std::uint64_t>(lst);
+      std::uint32_t lt2 = 0;
+      BlockMinPair(lk2, lt2, s);
+      last = static_cast<std::uint32_t>(~lk2);
+    }
+    const std::uint32_t last_nz = last - 1;
     if (live == 1) {
       Finish(out, last_nz, 1, rng);
       return;
     }
     const double u = Uniform(&rng);
-    double tot;
-    const double ex = BlockExclScan(ps, s.rd, &tot);
-    if (t == 0) s.bu[1] = 0xFFFFFFFFu;
+    // the slice whose weights hold the uniform (a scan of the slice masses), then the 4-token range within it
+    const double pb = t < nb ? ps / total : 0.0;
+    double ptot;
+    const double acc = BlockExclScan(pb, s.rd, &ptot);
+    if (t == 0) {
+      s.bu[3] = 0xFFFFFFFFu;
+      s.bu[1] = 0xFFFFFFFFu;
+    }
     __syncthreads();
-    if (ps > 0.0 && u >= ex && u < ex + ps) {
-      double r = u - ex;
-      for (std::uint32_t i = lo; i < hi; ++i) {
-        const double v = val[i] / total;
-        if (v == 0.0) continue;
-        r -= v;
-        if (r < 0.0) {
-          atomicMin(&s.bu[1], i);
-          break;
+    if (t < nb && pb > 0.0 && u - acc < pb) atomicMin(&s.bu[3], t);
+    __syncthreads();
+    if (t == s.bu[3]) s.bd[1] = acc;
+    __syncthreads();
+    const std::uint32_t hit = s.bu[3];
+    if (hit != 0xFFFFFFFFu) {
+      const double r0 = u - s.bd[1];
+      const std::uint32_t lo = min(V, hit * kSampleSlice + t * 4), hi = min(V, lo + 4);
+      double ps = 0.0;
+      for (std::uint32_t i = lo; i < hi; ++i) ps += val[i] / total;
+      double tot;
+      const double ex = BlockExclScan(ps, s.rd, &tot);
+      if (ps > 0.0 && r0 >= ex && r0 < ex + ps) {
+        double r = r0 - ex;
+        for (std::uint32_t i = lo; i < hi; ++i) {
+          const double v = val[i] / total;
+          if (v == 0.0) continue;
+          r -= v;
+          if (r < 0.0) {
+            atomicMin(&s.bu[1], i);
+            break;
+          }
         }
       }
     }
@@ -396,67 +757,97 @@ extern "C" __global__ void __launch_bounds__(1024)
     return;
   }
 
-  // 3. sorted path: collect the best Rc candidates
+  // sorted path: the candidates of pass 3, or an exact radix selection of the best Rc
   const std::uint64_t keep_cfg =
       p.top_k > 0 ? min(static_cast<std::uint64_t>(V), static_cast<std::uint64_t>(max(p.top_k, floor_keep)))
                   : static_cast<std::uint64_t>(V);
   const std::uint32_t K0 = static_cast<std::uint32_t>(min(static_cast<std::uint64_t>(nf), keep_cfg));
-  const std::uint32_t Rc = min(K0, kCap);
+  std::uint32_t Rc = min(K0, kCap);
   const bool has_full = p.top_k == 0 && p.top_p < 1.0f && V > 1024;
   double full_sum = 0.0;
-  if (has_full) {
-    double part = 0.0;
-    for (std::uint32_t i = t; i < V; i += kThreads) {
-      const double a = val[i];
-      if (a != -INFINITY) part += exp((a - M) / T);
+  if (has_full) full_sum = BlockSumD(t < nb ? w.psum[po + t] : 0.0, s);
+  std::uint32_t cut;
+  const bool collected =
+      HistCut(w.hist + static_cast<std::size_t>(row) * kBins, Rc, p.top_k > 0, &cut, s.ru, s.bu + 4);
+  std::uint32_t n;
+  bool sorted = false;
+  if (collected) {
+    // The candidates are every token in bins 0..cut, so the histogram gives each bin's place in the sorted list:
+    // scatter them to their bin's range and sort within bins (one lane per bin), unless a bin is too full for that.
+    n = w.cn[row];
+    const std::uint32_t* gh = w.hist + static_cast<std::size_t>(row) * kBins;
+    constexpr std::uint32_t kPerT = kBins / kThreads;
+    std::uint32_t c[kPerT], c4 = 0, cmax = 0;
+#pragma unroll
+    for (std::uint32_t j = 0; j < kPerT; ++j) {
+      const std::uint32_t bin = t * kPerT + j;
+      c[j] = bin <= cut ? gh[bin] : 0;
+      c4 += c[j];
+      cmax = max(cmax, c[j]);
     }
-    full_sum = BlockSumD(part, s);
-  }
-  for (std::uint32_t i = t; i < kBins; i += kThreads) s.b.hist[i] = 0;
-  __syncthreads();
-  for (std::uint32_t i = t; i < V; i += kThreads) {
-    const double a = val[i];
-    if (a == -INFINITY) continue;
-    const double d = M - a;
-    const std::uint32_t bin = d < 64.0 ? static_cast<std::uint32_t>(d * 64.0) : kBins - 1;
-    atomicAdd(&s.b.hist[bin], 1u);
-  }
-  __syncthreads();
-  {
-    std::uint32_t c4 = 0;
-    for (std::uint32_t j = 0; j < kBins / kThreads; ++j) c4 += s.b.hist[t * (kBins / kThreads) + j];
     std::uint32_t tot;
-    std::uint32_t base = BlockExclScan(c4, s.ru, &tot);
-    for (std::uint32_t j = 0; j < kBins / kThreads; ++j) {
-      const std::uint32_t h = s.b.hist[t * (kBins / kThreads) + j];
-      if (base < Rc && base + h >= Rc) {
-        s.bu[2] = t * (kBins / kThreads) + j;
-        s.bu[3] = base + h;
-      }
-      base += h;
+    std::uint32_t start = BlockExclScan(c4, s.ru, &tot);
+#pragma unroll
+    for (std::uint32_t j = 0; j < kPerT; ++j) {
+      s.b.hist[t * kPerT + j] = start;  // bin start
+      s.a.bitmap[t * kPerT + j] = 0;    // bin fill counter
+      start += c[j];
     }
-    if (t == 0) s.bu[4] = 0;
-    __syncthreads();
-  }
-  const std::uint32_t cut_bin = s.bu[2], cut_count = s.bu[3];
-  if (cut_count <= kCap) {
-    for (std::uint32_t i = t; i < V; i += kThreads) {
-      const double a = val[i];
-      if (a == -INFINITY) continue;
-      const double d = M - a;
-      const std::uint32_t bin = d < 64.0 ? static_cast<std::uint32_t>(d * 64.0) : kBins - 1;
-      if (bin <= cut_bin) {
-        const std::uint32_t slot = atomicAdd(&s.bu[4], 1u);
-        s.key[slot] = DescKey(a);
-        s.tok[slot] = i;
+    std::uint64_t mk = ~static_cast<std::uint64_t>(cmax);
+    std::uint32_t mt = 0;
+    BlockMinPair(mk, mt, s);
+    if (static_cast<std::uint32_t>(~mk) <= 512) {
+      for (std::uint32_t i = t; i < n; i += kThreads) {
+        const std::uint64_t k = w.ckey[static_cast<std::size_t>(row) * kCap + i];
+        const std::uint32_t bin = Bin(M, KeyValue(k));
+        const std::uint32_t at = s.b.hist[bin] + atomicAdd(&s.a.bitmap[bin], 1u);
+        s.key[at] = k;
+        s.tok[at] = w.ctok[static_cast<std::size_t>(row) * kCap + i];
+      }
+      __syncthreads();
+      // rank within the bin by (key, token), then move every element to start + rank
+      constexpr std::uint32_t kPerE = kCap / kThreads;
+      std::uint64_t ek[kPerE];
+      std::uint32_t et[kPerE], pos[kPerE];
+#pragma unroll
+      for (std::uint32_t j = 0; j < kPerE; ++j) {
+        const std::uint32_t i = t + kThreads * j;
+        pos[j] = 0xFFFFFFFFu;
+        if (i < n) {
+          ek[j] = s.key[i];
+          et[j] = s.tok[i];
+          const std::uint32_t bin = Bin(M, KeyValue(ek[j]));
+          const std::uint32_t b0 = s.b.hist[bin], cnt = s.a.bitmap[bin];
+          std::uint32_t r = 0;
+          for (std::uint32_t q = b0; q < b0 + cnt; ++q) {
+            const std::uint64_t kq = s.key[q];
+            r += kq < ek[j] || (kq == ek[j] && s.tok[q] < et[j]);
+          }
+          pos[j] = b0 + r;
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (std::uint32_t j = 0; j < kPerE; ++j)
+        if (pos[j] != 0xFFFFFFFFu) {
+          s.key[pos[j]] = ek[j];
+          s.tok[pos[j]] = et[j];
+        }
+      sorted = true;
+    } else {
+      for (std::uint32_t i = t; i < n; i += kThreads) {
+        s.key[i] = w.ckey[static_cast<std::size_t>(row) * kCap + i];
+        s.tok[i] = w.ctok[static_cast<std::size_t>(row) * kCap + i];
       }
     }
+    Rc = min(n, K0);
   } else {
-    // exact: the Rc-th best (value, token) by radix select, then everything up to it
     std::uint64_t ck;
     std::uint32_t ct;
     unsigned long long bn, bm;
     Select(val, nullptr, V, Rc, kNoBound, 0xFFFFFFFFu, s, &ck, &ct, &bn, &bm);
+    if (t == 0) s.bu[4] = 0;
+    __syncthreads();
     for (std::uint32_t i = t; i < V; i += kThreads) {
       const double a = val[i];
       if (a == -INFINITY) continue;
@@ -467,11 +858,12 @@ extern "C" __global__ void __launch_bounds__(1024)
         s.tok[slot] = i;
       }
     }
+    __syncthreads();
+    n = s.bu[4];
   }
   __syncthreads();
-  const std::uint32_t n = s.bu[4];
   std::uint32_t P = 1;
-  while (P < n) P <<= 1;
+  while (!sorted && P < n) P <<= 1;
   for (std::uint32_t i = n + t; i < P; i += kThreads) {
     s.key[i] = kNoBound;
     s.tok[i] = 0xFFFFFFFFu;
@@ -499,56 +891,48 @@ extern "C" __global__ void __launch_bounds__(1024)
   // weights of the sorted list
   for (std::uint32_t i = t; i < Rc; i += kThreads) s.a.w[i] = exp((KeyValue(s.key[i]) - M) / T);
   __syncthreads();
-  // 4. top-p, min-p and the weight sum in list order, one lane (the CPU's order)
+  // 4. top-p, min-p and the weight sum in list order (the CPU's order; the sums on one lane)
+  const std::uint32_t minimum = min(K0, floor_keep);
   if (t == 0) {
     std::uint32_t keep = K0;
-    const std::uint32_t minimum = min(K0, floor_keep);
     bool large = false;
     if (p.top_p < 1.0f && K0 > 1) {
       double sum = full_sum;
       if (!has_full) {
-        if (K0 > Rc) {
-          large = true;
-        } else {
-          sum = 0.0;
-          for (std::uint32_t i = 0; i < K0; ++i) sum += s.a.w[i];
-        }
+        if (K0 > Rc) large = true;
+        else sum = SeqSum(s.a.w, K0);
       }
       if (!large) {
-        const double target = static_cast<double>(p.top_p) * sum;
-        double cumulative = 0.0;
-        std::uint32_t k = 0;
-        while (k < K0) {
-          if (k == Rc) {
-            large = true;
-            break;
-          }
-          cumulative += s.a.w[k];
-          ++k;
-          if (k >= minimum && cumulative >= target) break;
+        const std::uint32_t k = SeqCut(s.a.w, min(K0, Rc), minimum, static_cast<double>(p.top_p) * sum);
+        if (k > min(K0, Rc)) {
+          if (Rc < K0) large = true;  // the cut lies past the sorted candidates
+          else keep = K0;
+        } else {
+          keep = k;
         }
-        keep = k;
       }
     }
-    if (!large && p.min_p > 0.0f && keep > 1) {
-      const double thr = M + T * log(static_cast<double>(p.min_p));
-      std::uint32_t k = 0;
-      while (k < keep && k < Rc && KeyValue(s.key[k]) >= thr) ++k;
-      if (k == Rc && Rc < keep) large = true;
-      else keep = min(keep, max(k, minimum));
-    }
-    if (!large && keep > Rc) large = true;
-    double total = 0.0;
-    if (!large)
-      for (std::uint32_t i = 0; i < keep; ++i) total += s.a.w[i];
     s.bu[5] = keep;
     s.bu[6] = large;
-    s.bd[0] = total;
   }
   __syncthreads();
-  const bool large = s.bu[6] != 0;
+  std::uint32_t keep = s.bu[5];
+  bool large = s.bu[6] != 0;
+  __syncthreads();
+  if (!large && p.min_p > 0.0f && keep > 1) {
+    // the candidates are sorted, so those at or above the threshold are a prefix: count them
+    const double thr = M + T * log(static_cast<double>(p.min_p));
+    const std::uint32_t lim = min(keep, Rc);
+    std::uint32_t c = 0;
+    for (std::uint32_t i = t; i < lim; i += kThreads) c += KeyValue(s.key[i]) >= thr;
+    c = BlockSumU(c, s);
+    if (c == Rc && Rc < keep) large = true;
+    else keep = min(keep, max(c, minimum));
+  }
+  if (!large && keep > Rc) large = true;
   if (!large) {
-    const std::uint32_t keep = s.bu[5];
+    if (t == 0) s.bd[0] = SeqSum(s.a.w, keep);
+    __syncthreads();
     const double total = s.bd[0];
     std::uint32_t nz = 0, last = 0;
     for (std::uint32_t i = t; i < keep; i += kThreads) {
@@ -567,14 +951,8 @@ extern "C" __global__ void __launch_bounds__(1024)
     if (t == 0) {
       std::uint32_t token = s.tok[last_nz];
       if (live > 1) {
-        double r = Uniform(&rng);
-        for (std::uint32_t i = 0; i < keep; ++i) {
-          r -= s.a.w[i];
-          if (r < 0.0) {
-            token = s.tok[i];
-            break;
-          }
-        }
+        const std::uint32_t i = SeqWalk(s.a.w, keep, Uniform(&rng));
+        if (i < keep) token = s.tok[i];
       }
       Finish(out, token, live, rng);
     }
@@ -591,8 +969,7 @@ extern "C" __global__ void __launch_bounds__(1024)
   std::uint32_t lt0 = 0xFFFFFFFFu;
   unsigned long long bn, bm;
   if (K0 < nf) Select(val, nullptr, V, K0, kNoBound, 0xFFFFFFFFu, s, &lk0, &lt0, &bn, &bm);
-  const std::uint32_t minimum = min(K0, floor_keep);
-  std::uint32_t keep = K0;
+  keep = K0;
   if (p.top_p < 1.0f && K0 > 1) {
     unsigned long long part = 0;
     for (std::uint32_t i = t; i < V; i += kThreads) {

@@ -8,7 +8,9 @@
 
 #include <algorithm>
 #include <initializer_list>
+#include <cmath>
 #include <map>
+#include <tuple>
 #include <string>
 #include <memory>
 #include <utility>
@@ -58,7 +60,10 @@ struct halo_model {
   halo_buffer qgo{}, ko{}, vo{}, aq{}, agate{}, ao{}, moe_ws{}, attn_ws{}, logits{}, argmax_part{};
   std::size_t moe_ws_bytes = 0, attn_ws_bytes = 0;
   std::vector<halo_buffer> owned;
-  std::map<std::pair<std::uint32_t, std::uint32_t>, halo_graph> graphs;
+  std::map<std::tuple<std::uint32_t, std::uint32_t, bool>, halo_graph> graphs;
+  // device sampling (halo_model_set_sampling): per-session parameters and penalty lists, the draws, workspace
+  bool sampling = false;
+  halo_buffer sample_params{}, sample_pen{}, sample_out{}, sample_ws{};
   // prefill batch scratch, allocated at the first prefill for kPrefillCap tokens
   struct Prefill {
     bool ready = false;
@@ -252,6 +257,21 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
   }
   if (norm(m->out_norm, true) != 0) return -1;
   if (gemv(m->head, m->xq, m->xs, m->logits) != 0) return -1;
+  if (m->sampling) {
+    // every session draws with its own parameters (temperature 0 is the argmax); the advance takes the drawn
+    // tokens and carries each session's RNG state into the next step
+    if (halo_op_sample(eng, P<float>(m->logits), S, c.vocab, c.vocab,
+                       static_cast<const HaloSampleParams*>(m->sample_params.device),
+                       static_cast<const HaloPenalty*>(m->sample_pen.device), HALO_SAMPLE_MAX_PENALTIES,
+                       static_cast<HaloSampleOut*>(m->sample_out.device), m->sample_ws.device, m->sample_ws.bytes, err,
+                       errlen) != 0)
+      return -1;
+    const halo_arg a[] = {Ptr(m->sample_out.device), Ptr(m->sample_params.device), Ptr(m->prompt.device),
+                          Ptr(m->prompt_len.device), Ptr(m->tokens.device), Ptr(m->nkv.device),
+                          Ptr(m->history.device), Ptr(m->produced.device), U32(S), U32(c.vocab),
+                          U32(c.max_context), U32(c.max_context), U32(c.max_context)};
+    return Launch(eng, "halo_step_advance_sampled", D3(1), D3(64), a, err, errlen);
+  }
   constexpr std::uint32_t kParts = 64;
   float* pv = P<float>(m->argmax_part);
   std::uint32_t* pi = reinterpret_cast<std::uint32_t*>(pv + c.max_sessions * kParts);
@@ -608,6 +628,57 @@ int halo_model_reset(halo_model* m, char* err, size_t errlen) {
   return 0;
 }
 
+int halo_model_set_sampling(halo_model* m, uint32_t s, const HaloSampleParams* params, const HaloPenalty* penalties,
+                            uint32_t n_penalties, char* err, size_t errlen) {
+  if (m == nullptr || s >= m->c.max_sessions || params == nullptr || (n_penalties && penalties == nullptr))
+    return SetErr(err, errlen, "set_sampling: bad session %u or null argument", s), -1;
+  const HaloSampleParams& p = *params;
+  if (!std::isfinite(p.temperature) || p.temperature < 0.0f || !(p.top_p >= 0.0f && p.top_p <= 1.0f) ||
+      !(p.min_p >= 0.0f && p.min_p <= 1.0f) || !std::isfinite(p.repeat_penalty) || !(p.repeat_penalty > 0.0f) ||
+      !std::isfinite(p.frequency_penalty) || !std::isfinite(p.presence_penalty) || p.top_k > 0x7FFFFFFFu ||
+      n_penalties > HALO_SAMPLE_MAX_PENALTIES)
+    return SetErr(err, errlen, "set_sampling: parameters outside the sampler's ranges"), -1;
+  for (std::uint32_t i = 0; i < n_penalties; ++i)
+    if (penalties[i].token >= m->c.vocab || (i && penalties[i].token <= penalties[i - 1].token))
+      return SetErr(err, errlen, "set_sampling: penalty tokens must be below the vocabulary and strictly increasing"),
+             -1;
+  const std::uint32_t S = m->c.max_sessions;
+  if (m->sample_params.device == nullptr) {
+    const std::size_t ws = halo_op_sample_workspace_bytes(S, m->c.vocab);
+    if (Alloc(m, sizeof(HaloSampleParams) * S, &m->sample_params, err, errlen) != 0 ||
+        Alloc(m, sizeof(HaloPenalty) * HALO_SAMPLE_MAX_PENALTIES * S, &m->sample_pen, err, errlen) != 0 ||
+        Alloc(m, sizeof(HaloSampleOut) * S, &m->sample_out, err, errlen) != 0 ||
+        Alloc(m, ws, &m->sample_ws, err, errlen) != 0)
+      return -1;
+    // every session starts greedy
+    std::vector<HaloSampleParams> g(S);
+    for (auto& q : g) {
+      q = HaloSampleParams{};
+      q.top_p = 1.0f;
+      q.repeat_penalty = 1.0f;
+      q.vocab = m->c.vocab;
+    }
+    if (halo_upload(m->dev, &m->sample_params, 0, g.data(), sizeof(HaloSampleParams) * S, err, errlen) != 0)
+      return -1;
+  }
+  HaloSampleParams q = p;
+  q.vocab = m->c.vocab;
+  q.n_penalties = n_penalties;
+  if (halo_upload(m->dev, &m->sample_params, sizeof(HaloSampleParams) * s, &q, sizeof q, err, errlen) != 0) return -1;
+  if (n_penalties &&
+      halo_upload(m->dev, &m->sample_pen, sizeof(HaloPenalty) * HALO_SAMPLE_MAX_PENALTIES * s, penalties,
+                  sizeof(HaloPenalty) * n_penalties, err, errlen) != 0)
+    return -1;
+  m->sampling = true;
+  return 0;
+}
+
+int halo_model_sample_state(halo_model* m, uint32_t s, HaloSampleParams* params, char* err, size_t errlen) {
+  if (m == nullptr || params == nullptr || s >= m->c.max_sessions || m->sample_params.device == nullptr)
+    return SetErr(err, errlen, "sample_state: no sampling set for session %u", s), -1;
+  return halo_download(m->dev, &m->sample_params, sizeof(HaloSampleParams) * s, params, sizeof *params, err, errlen);
+}
+
 int halo_model_set_session(halo_model* m, uint32_t s, const uint32_t* prompt, uint32_t len, uint32_t nkv, char* err,
                            size_t errlen) {
   if (s >= m->c.max_sessions || len > m->c.max_context || (len ? nkv >= len : nkv != 0) || nkv >= m->c.max_context)
@@ -656,7 +727,7 @@ int halo_model_step_eager(halo_model* m, uint32_t S, uint32_t prefix, char* err,
 int halo_model_run(halo_model* m, uint32_t S, uint32_t prefix, uint32_t steps, char* err, size_t errlen) {
   if (S == 0 || S > m->c.max_sessions || prefix % 64 != 0 || prefix > m->c.prefix_tokens)
     return SetErr(err, errlen, "run: %u sessions / prefix %u unsupported", S, prefix), -1;
-  const auto key = std::make_pair(S, prefix);
+  const auto key = std::make_tuple(S, prefix, m->sampling);
   auto it = m->graphs.find(key);
   if (it == m->graphs.end()) {
     if (halo_begin_capture(m->dev, err, errlen) != 0) return -1;

@@ -6,6 +6,7 @@
 // ReferenceModel::LinearAttention conv + norms + gate (src/model/reference.cpp:278-366), ReferenceModel::Attention
 // q/gate split, q/k norm, NEOX rope (src/model/reference.cpp:368-416), HaloStepParam (src/kernels/step_params.h).
 #include "common.h"
+#include "halo_sample.h"
 
 using halo::kWave;
 
@@ -259,6 +260,29 @@ extern "C" __global__ void __launch_bounds__(64)
   const std::uint32_t n = nkv[s];  // positions now in the cache, the produced token goes at index n
   if (n < history_stride) history[static_cast<std::size_t>(s) * history_stride + n] = at;
   tokens[s] = n < prompt_len[s] ? prompt[static_cast<std::size_t>(s) * prompt_stride + n] : at;
+  nkv[s] = min(n + 1, max_context);
+}
+
+// The advance after device sampling: out[s] holds session s's drawn token and RNG state (halo_sample_final). The
+// token is recorded at history[s][nkv[s]] as in halo_step_advance; a sampler code (no finite logit, bad
+// parameters: token >= vocab) is recorded as is and token 0 fed next, so the step never indexes past the
+// embedding. The RNG state goes back into params[s] for the next step.
+extern "C" __global__ void __launch_bounds__(64)
+    halo_step_advance_sampled(const HaloSampleOut* __restrict__ out, HaloSampleParams* __restrict__ params,
+                              const std::uint32_t* __restrict__ prompt, const std::uint32_t* __restrict__ prompt_len,
+                              std::uint32_t* __restrict__ tokens, std::uint32_t* __restrict__ nkv,
+                              std::uint32_t* __restrict__ history, std::uint32_t* __restrict__ produced,
+                              std::uint32_t S, std::uint32_t vocab, std::uint32_t prompt_stride,
+                              std::uint32_t history_stride, std::uint32_t max_context) {
+  const std::uint32_t s = threadIdx.x;
+  if (s >= S) return;
+  const HaloSampleOut o = out[s];
+  params[s].rng = o.rng;
+  produced[s] = o.token;
+  const std::uint32_t n = nkv[s];
+  if (n < history_stride) history[static_cast<std::size_t>(s) * history_stride + n] = o.token;
+  tokens[s] = n < prompt_len[s] ? prompt[static_cast<std::size_t>(s) * prompt_stride + n]
+                                : (o.token < vocab ? o.token : 0u);
   nkv[s] = min(n + 1, max_context);
 }
 

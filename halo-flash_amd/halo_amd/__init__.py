@@ -419,6 +419,8 @@ _SIGS = {
     "halo_gguf_upload_q8_0": (C.c_int, [_VP, _VP, _U64, _U32, _VP, _VP, _U32, _VP, _SZ], True),
     "halo_model_config_from_gguf": (C.c_int, [_VP, _VP], True),
     "halo_model_load_gguf": (C.c_int, [_VP, _VP], True),
+    "halo_model_set_sampling": (C.c_int, [_VP, _U32, _VP, _VP, _U32], True),
+    "halo_model_sample_state": (C.c_int, [_VP, _U32, _VP], True),
     "halo_op_sample_workspace_bytes": (_SZ, [_U32, _U32], False),
     "halo_op_sample": (C.c_int, [_VP, _VP, _U32, _U64, _U32, _VP, _VP, _U32, _VP, _VP, _SZ], True),
     "halo_op_moe_decode_norm": (C.c_int, [_VP, C.POINTER(MoeWeights), C.POINTER(ProjInput), _VP, _U32, _VP, _SZ],
@@ -679,6 +681,19 @@ class Model:
         qs = self._download(v.data, v.rows * v.qstride, np.int8).reshape(v.rows, v.qstride)[:, : v.cols]
         d = self._download(v.scales, v.rows * (v.cols // 32) * 2, np.uint16).reshape(v.rows, v.cols // 32)
         return np.ascontiguousarray(qs), d
+
+    def set_sampling(self, s: int, params: "SampleParams", penalties=None):
+        """Device sampling for session s; penalties = (token, generated_count, repeated) arrays sorted by token."""
+        n = 0 if penalties is None else len(penalties[0])
+        pen = np.zeros(max(n, 1), PENALTY_DTYPE)
+        if n:
+            pen["token"], pen["generated_count"], pen["repeated"] = penalties
+        _call("halo_model_set_sampling", self.h, s, C.byref(params), pen.ctypes.data, n)
+
+    def sample_state(self, s: int) -> "SampleParams":
+        p = SampleParams()
+        _call("halo_model_sample_state", self.h, s, C.byref(p))
+        return p
 
     def load_gguf(self, g: "Gguf"):
         """Every weight from a GGUF checkpoint (halo_model_load_gguf)."""

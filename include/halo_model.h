@@ -70,6 +70,19 @@ int halo_model_step_eager(halo_model* m, uint32_t S, uint32_t attn_prefix, char*
  * Not capturable (uploads per batch of up to 2048 tokens). `first` is ignored. */
 int halo_model_prefill(halo_model* m, const halo_prefill_segment* segs, uint32_t nseg, char* err, size_t errlen);
 
+/* Device sampling for session s (the reference's per-request sampler upload, FlashNextGpu::Step /
+ * BatchDecode, src/engine/flash_next_gpu.cpp:876-893, src/engine/batch_decode.cpp:605-621): host copies of the
+ * parameters and the penalty list (sorted by token, at most HALO_SAMPLE_MAX_PENALTIES) go to device memory; from
+ * then on every step of the model draws each session's token with halo_op_sample (sessions without parameters stay
+ * greedy through temperature 0) and carries the RNG state forward on the device, so a multi-step run draws the
+ * sequence the CPU sampler would from that state. The penalty list is what the caller uploaded last: a caller
+ * whose penalties follow the generated tokens sets them again between steps. Not capturable (uploads); steps
+ * recorded before the first call keep argmax decoding in their own graphs. */
+int halo_model_set_sampling(halo_model* m, uint32_t s, const HaloSampleParams* params, const HaloPenalty* penalties,
+                            uint32_t n_penalties, char* err, size_t errlen);
+/* Host copy of session s's sampling parameters as the device holds them (the RNG state after the last draw). */
+int halo_model_sample_state(halo_model* m, uint32_t s, HaloSampleParams* params, char* err, size_t errlen);
+
 /* Host copies of session s's produced tokens history[pos] (the argmax after position pos-1 ... ) and nkv. */
 int halo_model_history(halo_model* m, uint32_t s, uint32_t* out, uint32_t n, char* err, size_t errlen);
 int halo_model_positions(halo_model* m, uint32_t* nkv_out, uint32_t S, char* err, size_t errlen);

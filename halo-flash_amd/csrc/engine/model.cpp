@@ -282,7 +282,8 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
   const halo_arg a[] = {Ptr(pv), Ptr(pi), Ptr(m->prompt.device), Ptr(m->prompt_len.device), Ptr(m->tokens.device),
                         Ptr(m->nkv.device), Ptr(m->history.device), Ptr(m->produced.device), U32(S), U32(kParts),
                         U32(c.max_context), U32(c.max_context), U32(c.max_context)};
-  return Launch(eng, "halo_step_advance", D3(1), D3(64), a, err, errlen);
+  // one wave per session, up to 16 sessions per block
+  return Launch(eng, "halo_step_advance", D3(CeilDiv(S, 16)), D3(64 * std::min<std::uint32_t>(S, 16)), a, err, errlen);
 }
 
 

@@ -237,18 +237,19 @@ extern "C" __global__ void __launch_bounds__(256)
 // `parts` partial maxima of halo_argmax_part (ties to the lower id); it is recorded at history[s][nkv[s]]; the
 // next input token is the prompt token at that position when it exists (teacher forcing), otherwise the produced
 // one; nkv[s] advances by one. prompt [S][prompt_stride], prompt_len [S].
-extern "C" __global__ void __launch_bounds__(64)
+extern "C" __global__ void __launch_bounds__(1024)
     halo_step_advance(const float* __restrict__ pv, const std::uint32_t* __restrict__ pi,
                       const std::uint32_t* __restrict__ prompt, const std::uint32_t* __restrict__ prompt_len,
                       std::uint32_t* __restrict__ tokens, std::uint32_t* __restrict__ nkv,
                       std::uint32_t* __restrict__ history, std::uint32_t* __restrict__ produced, std::uint32_t S,
                       std::uint32_t parts, std::uint32_t prompt_stride, std::uint32_t history_stride,
                       std::uint32_t max_context) {
-  const std::uint32_t s = threadIdx.x;
+  // one wave per session: lane p reduces partial maxima p, p + 64, ...; then a wave reduction (ties to the lower id)
+  const std::uint32_t s = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave, lane = threadIdx.x % kWave;
   if (s >= S) return;
   float v = -INFINITY;
   std::uint32_t at = 0xFFFFFFFFu;
-  for (std::uint32_t p = 0; p < parts; ++p) {
+  for (std::uint32_t p = lane; p < parts; p += kWave) {
     const float x = pv[s * parts + p];
     const std::uint32_t i = pi[s * parts + p];
     if (x > v || (x == v && i < at)) {
@@ -256,6 +257,15 @@ extern "C" __global__ void __launch_bounds__(64)
       at = i;
     }
   }
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(v, o, kWave);
+    const std::uint32_t oi = __shfl_xor(at, o, kWave);
+    if (ov > v || (ov == v && oi < at)) {
+      v = ov;
+      at = oi;
+    }
+  }
+  if (lane != 0) return;
   produced[s] = at;
   const std::uint32_t n = nkv[s];  // positions now in the cache, the produced token goes at index n
   if (n < history_stride) history[static_cast<std::size_t>(s) * history_stride + n] = at;

@@ -390,7 +390,19 @@ extern "C" __global__ void __launch_bounds__(1024)
   const std::uint32_t G = (E + 7) / 8;
   if (e % 8 == 0 && e / 8 < G) gmax[e / 8] = g;
   __syncthreads();
-  if (k <= G && e < G) {
+  if (k <= G && G <= kWave) {
+    // tau = the k-th largest group maximum, by a bitwise search over the keys in wave 0 (probability bits + 1;
+    // probabilities are >= 0, so their bit patterns order like the values; 0 marks a lane without a group)
+    if (e < kWave) {
+      const std::uint32_t key = e < G ? __float_as_uint(gmax[e]) + 1u : 0u;
+      std::uint32_t thr = 0;
+      for (int bit = 30; bit >= 0; --bit) {
+        const std::uint32_t cand = thr | (1u << bit);
+        if (static_cast<std::uint32_t>(__builtin_popcountll(__ballot(key >= cand))) >= k) thr = cand;
+      }
+      if (e == 0) tau_s = __uint_as_float(thr - 1u);
+    }
+  } else if (k <= G && e < G) {
     const float mine = gmax[e];
     std::uint32_t r = 0;
     for (std::uint32_t j = 0; j < G; ++j) {
@@ -414,6 +426,7 @@ extern "C" __global__ void __launch_bounds__(1024)
   if (n <= kCand) {
     if (cand) {
       std::uint32_t r = 0;
+#pragma unroll 8
       for (std::uint32_t j = 0; j < n; ++j) {
         const float pj = cp[j];
         r += (pj > p) || (pj == p && ci[j] < e);

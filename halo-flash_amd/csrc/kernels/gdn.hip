@@ -566,17 +566,34 @@ extern "C" __global__ void __launch_bounds__(512) halo_gdn_step_q8(
   float4 row[8];
 #pragma unroll
   for (int r = 0; r < 8; ++r) row[r] = *reinterpret_cast<const float4*>(St + static_cast<std::size_t>(i0 + r) * kD + j0);
-  // prologue: threads 0..383 take the q, k and v channels of this head (128 each: waves 0-1, 2-3, 4-5)
-  const std::uint32_t pos = nkv[s] - 1;
+  // prologue: threads 0..383 take the q, k and v channels of this head (128 each: waves 0-1, 2-3, 4-5). With K <= 4
+  // every ring slot is loaded before the position arrives, so the ring loads do not wait for nkv; the slots are
+  // selected by position afterwards.
   const std::uint32_t seg = t / kD, i = t % kD;
+  const std::uint32_t ch = seg == 0 ? kh * kD + i : seg == 1 ? Dk + kh * kD + i : 2 * Dk + h * kD + min(i, kD - 1);
+  float* rs = ring + static_cast<std::size_t>(s) * K * C;
+  const std::uint32_t pos = nkv[s] - 1;
+  const float zg = t < kD ? z[static_cast<std::size_t>(s) * Dv + h * kD + t] : 0.0f;
   float y = 0.0f;
   if (seg < 3) {
-    const std::uint32_t ch = seg == 0 ? kh * kD + i : seg == 1 ? Dk + kh * kD + i : 2 * Dk + h * kD + i;
     const float x = qkv[static_cast<std::size_t>(s) * C + ch];
-    float* rs = ring + static_cast<std::size_t>(s) * K * C;
-    float acc = conv_w[static_cast<std::size_t>(ch) * K + K - 1] * x;
-    for (std::uint32_t j = 0; j + 1 < K; ++j)
-      acc += conv_w[static_cast<std::size_t>(ch) * K + j] * rs[static_cast<std::size_t>((pos + 1 + j) % K) * C + ch];
+    float acc;
+    if (K <= 4) {
+      float slot[4], w[4];
+#pragma unroll
+      for (std::uint32_t j = 0; j < 4; ++j) {
+        slot[j] = j < K ? rs[static_cast<std::size_t>(j) * C + ch] : 0.0f;
+        w[j] = j < K ? conv_w[static_cast<std::size_t>(ch) * K + j] : 0.0f;
+      }
+      acc = w[K - 1] * x;
+#pragma unroll
+      for (std::uint32_t j = 0; j < 3; ++j)
+        if (j + 1 < K) acc += w[j] * slot[(pos + 1 + j) % K];
+    } else {
+      acc = conv_w[static_cast<std::size_t>(ch) * K + K - 1] * x;
+      for (std::uint32_t j = 0; j + 1 < K; ++j)
+        acc += conv_w[static_cast<std::size_t>(ch) * K + j] * rs[static_cast<std::size_t>((pos + 1 + j) % K) * C + ch];
+    }
     if (seg == 2 || h < Hk) rs[static_cast<std::size_t>(pos % K) * C + ch] = x;
     y = halo::Silu(acc);
   }
@@ -650,7 +667,7 @@ extern "C" __global__ void __launch_bounds__(512) halo_gdn_step_q8(
   if (t < kD) {
     const float sc = 1.0f / sqrtf((part[0] + part[1]) / static_cast<float>(kD) + eps);
     const std::size_t off = static_cast<std::size_t>(s) * Dv + h * kD + t;
-    const float v = o * sc * norm_w[t] * halo::Sigmoid(z[off]);
+    const float v = o * sc * norm_w[t] * halo::Sigmoid(zg);
     const float amax = halo::GroupMax<32>(fabsf(v));
     const float scale = amax / 127.0f;
     oq[off] = static_cast<std::int8_t>(scale > 0.0f ? static_cast<int>(rintf(v / scale)) : 0);

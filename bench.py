@@ -181,6 +181,7 @@ def run_gpu(args):
             run_moe(args, dev, H, res)
             run_gdn(args, dev, H, res)
             run_c4(args, dev, H, res)
+            run_sample(args, dev, H, res)
             res["roofline"] = roof
         return res
     finally:
@@ -970,7 +971,7 @@ def main():
         "roofline": res["roofline"],
         "c1_sweep": res["c1_sweep"],
     }
-    for k in ("moe", "gdn", "c4"):
+    for k in ("moe", "gdn", "c4", "sample"):
         if k in res:
             line[k] = res[k]
     if "c4" in res:

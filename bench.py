@@ -945,7 +945,7 @@ def main():
     args = p.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
-              "(the path is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
+              "(the path runs on one GPU; a sharded version is not built)", file=sys.stderr)
         sys.exit(2)
     res = run_gpu(args)
     if args.mode in ("c0", "membw", "moe", "gdn", "c4", "pmc", "attn", "proj", "prefill", "sample"):

@@ -304,7 +304,7 @@ class TensorView(C.Structure):
 
 
 def c4_config(max_sessions=4, prefix_tokens=8192, max_context=8192 + 256 + 128):
-    """48 layers (3 DeltaNet : 1 GQA), hidden 2048, vocab 151936, MoE as C2."""
+    """Benchmark config C4: 48 layers (3 DeltaNet : 1 GQA), hidden 2048, vocab 151936, MoE as C2."""
     return ModelConfig(vocab=151936, hidden=2048, layers=48, attn_interval=4, gdn_k_heads=16, gdn_v_heads=32,
                        gdn_head_dim=128, conv_kernel=4, q_heads=16, kv_heads=2, head_dim=256, rotary_dim=64,
                        n_experts=512, n_used=10, expert_ff=512, shared_ff=512, rope_theta=1e7, rms_eps=1e-6,
@@ -741,7 +741,7 @@ class Model:
 
 
 class MoeLayer:
-    """Seeded synthetic MoE layer on the device (BASELINE config C2 shapes by default)."""
+    """Seeded synthetic MoE layer on the device (benchmark config C2 shapes by default)."""
 
     def __init__(self, dev: Device, n_experts=512, n_used=10, hidden=2048, ff=512, shared_ff=512, seed=0,
                  shared=True):

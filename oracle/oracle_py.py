@@ -159,7 +159,7 @@ def block_dots(qs, xq):
 
 
 def synth_q8(rng: np.random.Generator, rows: int, cols: int, sigma: float = 0.02):
-    """BASELINE's Q8_0 distribution: q ~ U{-127..127}, d = fp16(|N(0, sigma)| / 127)."""
+    """The benchmark's Q8_0 distribution: q ~ U{-127..127}, d = fp16(|N(0, sigma)| / 127)."""
     qs = rng.integers(-127, 128, size=(rows, cols), dtype=np.int8)
     d = (np.abs(rng.normal(0.0, sigma, size=(rows, cols // 32))) / 127.0).astype(np.float16).view(np.uint16)
     return qs, d

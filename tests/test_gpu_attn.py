@@ -2,7 +2,7 @@
 (config C4's attention: 16 q heads, 2 kv heads, head_dim 256, 16-token pages).
 
 Each (session, head) output is compared with the oracle's dense softmax attention (reference.cpp:492-527) over the
-session's gathered K/V rows, times sigmoid(gate): within 1e-5 relative to sum|p||v| (tighter than BASELINE's 1e-3).
+session's gathered K/V rows, times sigmoid(gate): within 1e-5 relative to sum|p||v| (tighter than the benchmark contract's 1e-3).
 Also: the appended token lands in the right page slot; sessions see only their own suffix.
 """
 import ctypes

@@ -2,7 +2,7 @@
 
 Decode: several consecutive steps for S = 4 sessions against the oracle's token step (reference.cpp:329-364, S
 value-major there, key-major here), state and output within 1e-5 of the oracle relative to the magnitude of the
-terms (sum |S| |k|, the reference's bound style); BASELINE's 1e-3 is looser.
+terms (sum |S| |k|, the reference's bound style); the benchmark contract's 1e-3 is looser.
 """
 import numpy as np
 import pytest
@@ -141,7 +141,7 @@ def test_gdn_prefill_matches_stepping(dev, seqlens, zero):
 
 
 def test_gdn_prefill_c3_full(dev):
-    """BASELINE config C3 prefill: ragged {37, 512, 2048, 8191} tokens; heads 0 and 17 checked against stepping."""
+    """Benchmark config C3 prefill: ragged {37, 512, 2048, 8191} tokens; heads 0 and 17 checked against stepping."""
     seqlens = [37, 512, 2048, 8191]
     rng = np.random.default_rng(3)
     got_o, got_s, s0, inputs = prefill_case(dev, rng, seqlens, zero_state=True)

@@ -8,7 +8,7 @@ Checks, per token count T in {1, 4, 16}:
     token selecting an expert computes it, for all its tokens);
   * quantized activations bit-exact; h codes equal to the oracle's composition (SwiGLU of the exact-integer
     gate/up GEMVs, quantized per 32) except at rounding-boundary flips of +-1;
-  * the layer output within 1e-5 * magnitude of the oracle composition fed the GPU's h codes, and within BASELINE's
+  * the layer output within 1e-5 * magnitude of the oracle composition fed the GPU's h codes, and within the benchmark contract's
     1e-3 relative of the oracle end to end.
 """
 import ctypes
@@ -117,7 +117,7 @@ def test_moe_decode_matches_oracle(dev, layer, small_layer, T, shape):
     assert np.abs(diff).max() <= 1 and np.count_nonzero(diff) <= max(2, diff.size // 2000)
     assert np.allclose(ghs, hs_w, rtol=1e-5, atol=0)
 
-    # down + combine: teacher-forced on the GPU's h codes (tight) and end to end (BASELINE 1e-3)
+    # down + combine: teacher-forced on the GPU's h codes (tight) and end to end (the contract's 1e-3)
     for t in range(T):
         acc_tf = np.zeros(L.H, np.float64)
         acc_e2e = np.zeros(L.H, np.float64)

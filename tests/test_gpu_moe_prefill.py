@@ -3,7 +3,7 @@ at T = 1 and 200): fp32 router GEMM, top-k, pairs grouped by expert, grouped int
 slot-order combine with the shared expert.
 
 Bars: router logits within 1e-5 * sum|w x| of a float64 product; ids equal to the oracle's RouteTopK on the GPU
-logits and weights to 1e-6; each token's output within BASELINE's 1e-3 of the oracle composition's magnitude
+logits and weights to 1e-6; each token's output within the benchmark contract's 1e-3 of the oracle composition's magnitude
 (x and h quantized per 32 as the engine does; h codes may differ by one at rounding boundaries), argmax equal; for
 T <= 16 the same bound against the decode path's output.
 """

@@ -2,7 +2,7 @@
 
 Bars: integer work (repack bytes, quantized activations and scales, int32 half-block dots) bit-exact against the
 oracle; fp32 outputs within 1e-5 * sum|term| + 1e-6 of the oracle's double-accumulated sum (the reference's own
-tolerance, tests/gpu/quant_gpu_test.cpp:115-122), which is tighter than BASELINE's 1e-3 relative; argmax equal.
+tolerance, tests/gpu/quant_gpu_test.cpp:115-122), which is tighter than the benchmark contract's 1e-3 relative; argmax equal.
 """
 import numpy as np
 import pytest

@@ -1,0 +1,330 @@
+// Reference-named decode kernels: the names, parameter lists and grid conventions of the reference's generic
+// decode kernels (src/kernels/core.hip:259-586, 2621-2650, 3003-3063), so engine code that launches them by name
+// runs unchanged; the bodies are gfx950 implementations (wave64 reductions, coalesced row accesses). The model's own
+// step uses the fused MI355X kernels instead (model.hip, gdn.hip, attn.hip); these serve the kernel-level drop-in.
+//
+// Reductions over a block accept any block size that is a multiple of 64 (the reference launches 128 or 256).
+#include "common.h"
+
+namespace halo::refk {
+
+using halo::kWave;
+
+// Sum / maximum over the block; every thread gets the result. `red` holds one entry per wave.
+__device__ __forceinline__ float BlockSumAny(float v, float* red) {
+  v = halo::GroupSum(v);
+  if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = v;
+  __syncthreads();
+  float r = 0.0f;
+  for (std::uint32_t i = 0; i < (blockDim.x + kWave - 1) / kWave; ++i) r += red[i];
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ float BlockMaxAny(float v, float* red) {
+  v = halo::GroupMax(v);
+  if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = v;
+  __syncthreads();
+  float r = -INFINITY;
+  for (std::uint32_t i = 0; i < (blockDim.x + kWave - 1) / kWave; ++i) r = fmaxf(r, red[i]);
+  __syncthreads();
+  return r;
+}
+
+// NEOX rotation of the first rotary_dim values of one head: pairs (i, i + rotary_dim / 2) rotate by
+// pos * theta^(-2 i / rotary_dim).
+__device__ __forceinline__ void RotateHead(float* v, std::uint32_t rotary_dim, std::uint32_t pos, float theta) {
+  const std::uint32_t half = rotary_dim / 2;
+  for (std::uint32_t i = threadIdx.x; i < half; i += blockDim.x) {
+    const float ang = static_cast<float>(pos) * powf(theta, -2.0f * static_cast<float>(i) / static_cast<float>(rotary_dim));
+    const float cs = cosf(ang), sn = sinf(ang);
+    const float x0 = v[i], x1 = v[i + half];
+    v[i] = x0 * cs - x1 * sn;
+    v[i + half] = x0 * sn + x1 * cs;
+  }
+}
+
+// Softmax(q . K^T / sqrt(hd)) V * sigmoid(gate) for one query head over positions [0, n) of a contiguous cache
+// [pos][num_kv_heads][hd]; sc is the head's score scratch (global, n entries). Scores: one wave per position, its
+// lanes across hd (coalesced rows); weighted V: threads across hd.
+__device__ void AttendHead(const float* qh, const float* kc, const float* vc, const float* gh, float* oh, float* sc,
+                           std::uint32_t kvh, std::uint32_t num_kv_heads, std::uint32_t hd, std::uint32_t n,
+                           float* red) {
+  const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, nw = blockDim.x / kWave;
+  const float scale = 1.0f / sqrtf(static_cast<float>(hd));
+  float mx = -INFINITY;
+  for (std::uint32_t p = wave; p < n; p += nw) {
+    const float* kp = kc + (static_cast<std::size_t>(p) * num_kv_heads + kvh) * hd;
+    float dot = 0.0f;
+    for (std::uint32_t i = lane; i < hd; i += kWave) dot += qh[i] * kp[i];
+    dot = halo::GroupSum(dot) * scale;
+    if (lane == 0) sc[p] = dot;
+    mx = fmaxf(mx, dot);
+  }
+  mx = BlockMaxAny(mx, red);  // its barriers also publish sc to the block
+  float den = 0.0f;
+  for (std::uint32_t p = threadIdx.x; p < n; p += blockDim.x) {
+    const float e = expf(sc[p] - mx);
+    sc[p] = e;
+    den += e;
+  }
+  den = BlockSumAny(den, red);
+  for (std::uint32_t i = threadIdx.x; i < hd; i += blockDim.x) {
+    float acc = 0.0f;
+    for (std::uint32_t p = 0; p < n; ++p) acc += sc[p] * vc[(static_cast<std::size_t>(p) * num_kv_heads + kvh) * hd + i];
+    oh[i] = acc / den * halo::Sigmoid(gh[i]);
+  }
+}
+
+}  // namespace halo::refk
+
+using namespace halo::refk;
+
+// y_b = x_b * w_b / rms(x_b), one block per vector b of d values; w_b = w_all + b * w_stride (core.hip:259).
+extern "C" __global__ void halo_rmsnorm(const float* x, const float* w_all, float* y, std::uint32_t d, float eps,
+                                        std::uint32_t w_stride) {
+  __shared__ float red[16];
+  const float* xv = x + static_cast<std::size_t>(blockIdx.x) * d;
+  const float* w = w_all + static_cast<std::size_t>(blockIdx.x) * w_stride;
+  float* yv = y + static_cast<std::size_t>(blockIdx.x) * d;
+  float ss = 0.0f;
+  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) ss += xv[i] * xv[i];
+  const float inv = 1.0f / sqrtf(BlockSumAny(ss, red) / static_cast<float>(d) + eps);
+  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) yv[i] = xv[i] * inv * w[i];
+}
+
+// x_b /= sqrt(sum x_b^2 + eps) in place, one block per vector (core.hip:265).
+extern "C" __global__ void halo_l2norm(float* x, std::uint32_t d, float eps) {
+  __shared__ float red[16];
+  float* xv = x + static_cast<std::size_t>(blockIdx.x) * d;
+  float ss = 0.0f;
+  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) ss += xv[i] * xv[i];
+  const float inv = 1.0f / sqrtf(BlockSumAny(ss, red) + eps);
+  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) xv[i] *= inv;
+}
+
+// NEOX RoPE in place, one block per head of head_dim values (core.hip:289-306): at position pos; rows of `heads`
+// heads per token at pos0 + token; at params[slot] * scale.
+extern "C" __global__ void halo_rope_neox(float* x, std::uint32_t head_dim, std::uint32_t rotary_dim, std::uint32_t pos,
+                                          float theta) {
+  RotateHead(x + static_cast<std::size_t>(blockIdx.x) * head_dim, rotary_dim, pos, theta);
+}
+extern "C" __global__ void halo_rope_neox_rows(float* x, std::uint32_t head_dim, std::uint32_t rotary_dim,
+                                               std::uint32_t pos0, std::uint32_t heads, float theta) {
+  RotateHead(x + static_cast<std::size_t>(blockIdx.x) * head_dim, rotary_dim, pos0 + blockIdx.x / heads, theta);
+}
+extern "C" __global__ void halo_rope_neox_p(float* x, const std::uint32_t* params, std::uint32_t head_dim,
+                                            std::uint32_t rotary_dim, std::uint32_t slot, std::uint32_t scale,
+                                            float theta) {
+  RotateHead(x + static_cast<std::size_t>(blockIdx.x) * head_dim, rotary_dim, params[slot] * scale, theta);
+}
+
+// Grid-stride elementwise kernels (core.hip:313-362).
+#define HALO_GRID_STRIDE(i, n) \
+  for (std::uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < (n); i += gridDim.x * blockDim.x)
+extern "C" __global__ void halo_add(float* y, const float* x, std::uint32_t n) {
+  HALO_GRID_STRIDE(i, n) y[i] += x[i];
+}
+extern "C" __global__ void halo_axpy(float* y, const float* x, float a, std::uint32_t n) {
+  HALO_GRID_STRIDE(i, n) y[i] += a * x[i];
+}
+extern "C" __global__ void halo_silu_mul(float* g, const float* up, std::uint32_t n) {
+  HALO_GRID_STRIDE(i, n) g[i] = halo::Silu(g[i]) * up[i];
+}
+extern "C" __global__ void halo_sigmoid_gate(float* x, const float* gate, std::uint32_t n) {
+  HALO_GRID_STRIDE(i, n) x[i] *= halo::Sigmoid(gate[i]);
+}
+extern "C" __global__ void halo_copy(float* dst, const float* src, std::uint32_t n) {
+  HALO_GRID_STRIDE(i, n) dst[i] = src[i];
+}
+// dst[params[slot] * stride + i] = src[i]: one row appended to a cache at the step's position.
+extern "C" __global__ void halo_copy_at(float* dst, const float* src, const std::uint32_t* params, std::uint32_t slot,
+                                        std::uint32_t stride, std::uint32_t n) {
+  float* row = dst + static_cast<std::size_t>(params[slot]) * stride;
+  HALO_GRID_STRIDE(i, n) row[i] = src[i];
+}
+#undef HALO_GRID_STRIDE
+
+// [heads][2 hd] (q | gate per head) -> q [heads][hd], gate [heads][hd]; one block per head (core.hip:364).
+extern "C" __global__ void halo_split_qgate(const float* qg, float* q, float* gate, std::uint32_t hd) {
+  const std::size_t h = blockIdx.x;
+  for (std::uint32_t i = threadIdx.x; i < hd; i += blockDim.x) {
+    q[h * hd + i] = qg[h * 2 * hd + i];
+    gate[h * hd + i] = qg[h * 2 * hd + hd + i];
+  }
+}
+
+// Causal depthwise conv step + SiLU; state holds the last kern - 1 inputs, oldest first, and shifts by one
+// (core.hip:447). One thread per channel.
+extern "C" __global__ void halo_conv_step(const float* in, float* state, const float* w, float* out,
+                                          std::uint32_t channels, std::uint32_t kern) {
+  const std::uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
+  if (ch >= channels) return;
+  const float x = in[ch];
+  float acc = w[static_cast<std::size_t>(ch) * kern + kern - 1] * x;
+  for (std::uint32_t j = 0; j + 1 < kern; ++j) {  // slot j is read before slot j + 1 moves into it
+    const float sj = state[static_cast<std::size_t>(j) * channels + ch];
+    acc += w[static_cast<std::size_t>(ch) * kern + j] * sj;
+    if (j > 0) state[static_cast<std::size_t>(j - 1) * channels + ch] = sj;
+  }
+  if (kern > 1) state[static_cast<std::size_t>(kern - 2) * channels + ch] = x;
+  out[ch] = halo::Silu(acc);
+}
+
+// The conv step and, for channels below l2_channels (DeltaNet q and k), the L2 norm over each block's channels (one
+// block per head of blockDim channels, core.hip:3003-3028).
+extern "C" __global__ void halo_conv_l2norm(const float* in, float* state, const float* w, float* out,
+                                            std::uint32_t channels, std::uint32_t kern, std::uint32_t l2_channels,
+                                            float eps) {
+  __shared__ float red[16];
+  const std::uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
+  float y = 0.0f;
+  if (ch < channels) {
+    const float x = in[ch];
+    float acc = w[static_cast<std::size_t>(ch) * kern + kern - 1] * x;
+    for (std::uint32_t j = 0; j + 1 < kern; ++j) {
+      const float sj = state[static_cast<std::size_t>(j) * channels + ch];
+      acc += w[static_cast<std::size_t>(ch) * kern + j] * sj;
+      if (j > 0) state[static_cast<std::size_t>(j - 1) * channels + ch] = sj;
+    }
+    if (kern > 1) state[static_cast<std::size_t>(kern - 2) * channels + ch] = x;
+    y = halo::Silu(acc);
+  }
+  if (blockIdx.x * blockDim.x < l2_channels) y *= 1.0f / sqrtf(BlockSumAny(y * y, red) + eps);  // block-uniform
+  if (ch < channels) out[ch] = y;
+}
+
+// One Gated DeltaNet decode step, one block per value head h (key head h % num_k_heads), thread j = value column
+// (blockDim >= d); state key-major [h][i][j]: decay the state, u = S^T k, delta = (v - u) sigmoid(beta),
+// S += k delta^T, o = S^T q / sqrt(d), with decay = exp(a softplus(alpha + dt)) (core.hip:463).
+extern "C" __global__ void halo_gdn_step(const float* q, const float* k, const float* v, const float* alpha,
+                                         const float* beta, const float* a, const float* dt, float* state, float* out,
+                                         std::uint32_t num_k_heads, std::uint32_t d) {
+  __shared__ float kl[256], ql[256];
+  const std::uint32_t h = blockIdx.x, j = threadIdx.x, kh = h % num_k_heads;
+  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) {
+    kl[i] = k[static_cast<std::size_t>(kh) * d + i];
+    ql[i] = q[static_cast<std::size_t>(kh) * d + i];
+  }
+  __syncthreads();
+  if (j >= d) return;
+  const float decay = expf(a[h] * halo::Softplus(alpha[h] + dt[h])), b = halo::Sigmoid(beta[h]);
+  float* col = state + static_cast<std::size_t>(h) * d * d + j;
+  float u = 0.0f;
+  for (std::uint32_t i = 0; i < d; ++i) {
+    const float s = col[static_cast<std::size_t>(i) * d] * decay;
+    col[static_cast<std::size_t>(i) * d] = s;
+    u += s * kl[i];
+  }
+  const float delta = (v[static_cast<std::size_t>(h) * d + j] - u) * b;
+  float o = 0.0f;
+  for (std::uint32_t i = 0; i < d; ++i) {
+    const float s = col[static_cast<std::size_t>(i) * d] + delta * kl[i];
+    col[static_cast<std::size_t>(i) * d] = s;
+    o += s * ql[i];
+  }
+  out[static_cast<std::size_t>(h) * d + j] = o / sqrtf(static_cast<float>(d));
+}
+
+namespace {
+// The single-pass d = 128 step (core.hip:2621-2650): A = S k and B = S q over the old state, delta = (v - decay A) b,
+// S' = decay S + delta k^T, o = (decay B + delta (k . q)) / sqrt(d). Block 128, thread j = value column; the column
+// is held in registers between the read and the write.
+__device__ __forceinline__ float GdnStepD128(const float* q, const float* k, const float* v, const float* alpha,
+                                             const float* beta, const float* a, const float* dt, float* state,
+                                             std::uint32_t num_k_heads, float* kl, float* ql, float* red) {
+  constexpr std::uint32_t d = 128;
+  const std::uint32_t h = blockIdx.x, j = threadIdx.x, kh = h % num_k_heads;
+  const float kj = k[static_cast<std::size_t>(kh) * d + j], qj = q[static_cast<std::size_t>(kh) * d + j];
+  kl[j] = kj;
+  ql[j] = qj;
+  float* col = state + static_cast<std::size_t>(h) * d * d + j;
+  const float kq = BlockSumAny(kj * qj, red);  // its barriers publish kl / ql
+  const float decay = expf(a[h] * halo::Softplus(alpha[h] + dt[h])), b = halo::Sigmoid(beta[h]);
+  // A and B over the old column (16 loads in flight per chunk), then the update reads it again (an L2 hit) and
+  // writes it once
+  float A = 0.0f, B = 0.0f;
+#pragma unroll 1
+  for (std::uint32_t i0 = 0; i0 < d; i0 += 16) {
+    float s[16];
+#pragma unroll
+    for (std::uint32_t i = 0; i < 16; ++i) s[i] = col[(i0 + i) * d];
+#pragma unroll
+    for (std::uint32_t i = 0; i < 16; ++i) {
+      A += s[i] * kl[i0 + i];
+      B += s[i] * ql[i0 + i];
+    }
+  }
+  const float delta = (v[static_cast<std::size_t>(h) * d + j] - decay * A) * b;
+#pragma unroll 1
+  for (std::uint32_t i0 = 0; i0 < d; i0 += 16) {
+    float s[16];
+#pragma unroll
+    for (std::uint32_t i = 0; i < 16; ++i) s[i] = col[(i0 + i) * d];
+#pragma unroll
+    for (std::uint32_t i = 0; i < 16; ++i) col[(i0 + i) * d] = decay * s[i] + delta * kl[i0 + i];
+  }
+  return (decay * B + delta * kq) / sqrtf(static_cast<float>(d));
+}
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(128)
+    halo_gdn_step_d128(const float* q, const float* k, const float* v, const float* alpha, const float* beta,
+                       const float* a, const float* dt, float* state, float* out, std::uint32_t num_k_heads) {
+  __shared__ float kl[128], ql[128], red[2];
+  const float o = GdnStepD128(q, k, v, alpha, beta, a, dt, state, num_k_heads, kl, ql, red);
+  out[static_cast<std::size_t>(blockIdx.x) * 128 + threadIdx.x] = o;
+}
+
+// The d = 128 step with the per-head gated RMSNorm in the epilogue: o * w / rms(o) * (silu(z) for mode 0, sigmoid(z)
+// for mode 1) (core.hip:3030-3063).
+extern "C" __global__ void __launch_bounds__(128)
+    halo_gdn_step_d128_norm(const float* q, const float* k, const float* v, const float* alpha, const float* beta,
+                            const float* a, const float* dt, float* state, const float* norm_w, const float* z,
+                            float* out, std::uint32_t num_k_heads, float eps, std::uint32_t mode) {
+  __shared__ float kl[128], ql[128], red[2];
+  const float o = GdnStepD128(q, k, v, alpha, beta, a, dt, state, num_k_heads, kl, ql, red);
+  const float inv = 1.0f / sqrtf(BlockSumAny(o * o, red) / 128.0f + eps);
+  const std::size_t at = static_cast<std::size_t>(blockIdx.x) * 128 + threadIdx.x;
+  const float zv = z[at];
+  out[at] = o * inv * norm_w[threadIdx.x] * (mode == 0 ? halo::Silu(zv) : halo::Sigmoid(zv));
+}
+
+// Per-head RMSNorm * w * (silu(z) mode 0, sigmoid(z) mode 1), in place; one block per head (core.hip:497).
+extern "C" __global__ void halo_gated_norm(float* o, const float* w, const float* z, std::uint32_t d, float eps,
+                                           std::uint32_t mode) {
+  __shared__ float red[16];
+  float* ov = o + static_cast<std::size_t>(blockIdx.x) * d;
+  const float* zv = z + static_cast<std::size_t>(blockIdx.x) * d;
+  float ss = 0.0f;
+  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) ss += ov[i] * ov[i];
+  const float inv = 1.0f / sqrtf(BlockSumAny(ss, red) / static_cast<float>(d) + eps);
+  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x)
+    ov[i] = ov[i] * inv * w[i] * (mode == 0 ? halo::Silu(zv[i]) : halo::Sigmoid(zv[i]));
+}
+
+// Decode attention over positions [0, n) of a contiguous cache [pos][num_kv_heads][hd], one block per query head
+// (kv head = h / (num_heads / num_kv_heads)), output gated by sigmoid(gate); scores [num_heads][max_n] scratch
+// (core.hip:514).
+extern "C" __global__ void halo_attention_decode(const float* q, const float* kc, const float* vc, const float* gate,
+                                                 float* out, float* scores, std::uint32_t num_heads,
+                                                 std::uint32_t num_kv_heads, std::uint32_t hd, std::uint32_t n,
+                                                 std::uint32_t max_n) {
+  __shared__ float red[16];
+  const std::uint32_t h = blockIdx.x, kvh = h / (num_heads / num_kv_heads);
+  const std::size_t row = static_cast<std::size_t>(h) * hd;
+  AttendHead(q + row, kc, vc, gate + row, out + row, scores + static_cast<std::size_t>(h) * max_n, kvh, num_kv_heads,
+             hd, n, red);
+}
+
+// The same for a chunk of T queries (grid (num_heads, T)): query t at position pos0 + t attends to [0, pos0 + t]
+// (core.hip:551). q, gate, out [T][num_heads][hd]; scores [T][num_heads][max_n].
+extern "C" __global__ void halo_attention_prefill(const float* q, const float* kc, const float* vc, const float* gate,
+                                                  float* out, float* scores, std::uint32_t num_heads,
+                                                  std::uint32_t num_kv_heads, std::uint32_t hd, std::uint32_t pos0,
+                                                  std::uint32_t max_n) {
+  __shared__ float red[16];
+  const std::uint32_t h = blockIdx.x, t = blockIdx.y, kvh = h / (num_heads / num_kv_heads);
+  const std::size_t row = (static_cast<std::size_t>(t) * num_heads + h) * hd;
+  AttendHead(q + row, kc, vc, gate + row, out + row,
+             scores + (static_cast<std::size_t>(t) * num_heads + h) * max_n, kvh, num_kv_heads, hd, pos0 + t + 1, red);
+}

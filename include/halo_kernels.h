@@ -14,6 +14,22 @@
  *                                                       grid (ceil(rows/(8R)) * groups, parts) batch_decode.hip:301
  *   halo_gemv_q8a8_l{16,32,64}_r{1,2,4}_b{1,2,4,8}(qs, d, xq, xs, y, rows, cols, qstride, ystride)   new (MI355X)
  *   halo_q8_half_dots(qs, xq, i32* isum, rows, cols, qstride)                                  new (parity)
+ *   reference-named decode kernels (core.hip:259-586, 2621, 3003-3063), same parameters and grids:
+ *     halo_rmsnorm(x, w_all, y, d, eps, w_stride)            grid (vectors)
+ *     halo_l2norm(x, d, eps)                                 grid (vectors)
+ *     halo_rope_neox(x, head_dim, rotary_dim, pos, theta), halo_rope_neox_rows(x, head_dim, rotary_dim, pos0, heads,
+ *       theta), halo_rope_neox_p(x, params, head_dim, rotary_dim, slot, scale, theta)      grid (heads)
+ *     halo_add(y, x, n), halo_axpy(y, x, a, n), halo_silu_mul(g, up, n), halo_sigmoid_gate(x, gate, n),
+ *       halo_copy(dst, src, n), halo_copy_at(dst, src, params, slot, stride, n)          grid-stride
+ *     halo_split_qgate(qg, q, gate, hd)                      grid (heads)
+ *     halo_conv_step(in, state, w, out, channels, kern)      one thread per channel
+ *     halo_conv_l2norm(in, state, w, out, channels, kern, l2_channels, eps)   block = one head of channels
+ *     halo_gdn_step(q, k, v, alpha, beta, a, dt, state, out, num_k_heads, d)   grid (v heads), block >= d
+ *     halo_gdn_step_d128(..., state, out, num_k_heads), halo_gdn_step_d128_norm(..., state, norm_w, z, out,
+ *       num_k_heads, eps, mode)                              grid (v heads), block 128
+ *     halo_gated_norm(o, w, z, d, eps, mode)                 grid (heads)
+ *     halo_attention_decode(q, kc, vc, gate, out, scores, num_heads, num_kv_heads, hd, n, max_n)   grid (heads)
+ *     halo_attention_prefill(..., num_heads, num_kv_heads, hd, pos0, max_n)                  grid (heads, T)
  *   halo_synth_q8(qs, d, rows, cols, qstride, u64 seed, f32 sigma), halo_synth_f32(x, u64 n, u64 seed, f32 sigma)
  *                                                                                              new (synthetic data)
  */
@@ -31,6 +47,10 @@
   X(halo_gemv_q8a8_l64_r1_b1) X(halo_gemv_q8a8_l32_r1_b1) X(halo_gemv_q8a8_l16_r1_b1)                        \
   X(halo_gemv_q8a8_l64_r2_b4) X(halo_gemv_q8a8_l64_r2_b8)                                                    \
   X(halo_q8_half_dots)                                                                                       \
+  X(halo_rmsnorm) X(halo_l2norm) X(halo_rope_neox) X(halo_rope_neox_rows) X(halo_rope_neox_p)               \
+  X(halo_add) X(halo_axpy) X(halo_silu_mul) X(halo_sigmoid_gate) X(halo_copy) X(halo_copy_at)                 \
+  X(halo_split_qgate) X(halo_conv_step) X(halo_conv_l2norm) X(halo_gdn_step) X(halo_gdn_step_d128)            \
+  X(halo_gdn_step_d128_norm) X(halo_gated_norm) X(halo_attention_decode) X(halo_attention_prefill)           \
   X(halo_synth_q8) X(halo_synth_f32)
 
 #endif /* HALO_KERNELS_H_ */

@@ -1,0 +1,216 @@
+"""Reference-named decode kernels (ref_named.hip), launched by name with the reference's parameter lists and grids
+(src/kernels/core.hip:259-586, 2621-2650, 3003-3063), against the oracle (oracle.c, pinned against the reference's
+own CPU functions) or numpy closed forms:
+  norms, RoPE, gated norm          -> or_rmsnorm / or_l2norm / or_rope_neox, numpy; 1e-5 relative
+  conv step (+ L2)                 -> numpy causal conv + SiLU; state shift exact
+  DeltaNet step (two-loop, d128, d128 + norm) -> or_gdn_step (value-major state; the kernels keep it key-major)
+  attention decode / chunked prefill          -> or_attention_head, gated by sigmoid
+  elementwise                      -> numpy
+Bars: fp32 results within 1e-5 of the magnitude of their terms (sum |term|), as the repository's other fp32 kernels.
+"""
+import numpy as np
+import pytest
+
+import halo_amd as H
+import oracle_py as O
+
+pytestmark = pytest.mark.gpu
+
+
+def close(got, want, mag, rel=1e-5):
+    err = np.max(np.abs(got.astype(np.float64) - want.astype(np.float64)) / (np.asarray(mag, np.float64) + 1e-30))
+    assert err <= rel, f"error {err:.2e} of the terms' magnitude"
+
+
+def sig(x):
+    return 1.0 / (1.0 + np.exp(-x.astype(np.float64)))
+
+
+def silu(x):
+    return x.astype(np.float64) * sig(x)
+
+
+def test_norms_rope_elementwise(dev):
+    rng = np.random.default_rng(1)
+    nv, d = 6, 256
+    x = rng.normal(0, 1, (nv, d)).astype(np.float32)
+    w = rng.normal(1, 0.1, (nv, d)).astype(np.float32)
+    gx, gw, gy = dev.to_device(x), dev.to_device(w), dev.array((nv, d), np.float32)
+    for stride in (0, d):
+        dev.launch("halo_rmsnorm", (nv,), (256,), [gx, gw, gy, ("u32", d), ("f32", 1e-6), ("u32", stride)])
+        want = x.copy()
+        for b in range(nv):
+            O.oracle().or_rmsnorm(want[b], d, w[b if stride else 0].ctypes.data, 1e-6)
+        close(gy.download(), want, np.abs(want) + 1e-3)
+    gl = dev.to_device(x)
+    dev.launch("halo_l2norm", (nv,), (128,), [gl, ("u32", d), ("f32", 1e-6)])
+    want = x.copy()
+    for b in range(nv):
+        O.oracle().or_l2norm(want[b], d, 1e-6)
+    close(gl.download(), want, np.abs(want) + 1e-4)
+    # RoPE: plain, rows (2 tokens x 3 heads from pos0 = 40), from step params
+    heads, hd, rot = 6, 256, 64
+    xr = rng.normal(0, 1, (heads, hd)).astype(np.float32)
+    for kind in ("plain", "rows", "p"):
+        g = dev.to_device(xr)
+        if kind == "plain":
+            dev.launch("halo_rope_neox", (heads,), (64,), [g, ("u32", hd), ("u32", rot), ("u32", 77), ("f32", 1e7)])
+            poss = [77] * heads
+        elif kind == "rows":
+            dev.launch("halo_rope_neox_rows", (heads,), (64,),
+                       [g, ("u32", hd), ("u32", rot), ("u32", 40), ("u32", 3), ("f32", 1e7)])
+            poss = [40, 40, 40, 41, 41, 41]
+        else:
+            prm = dev.to_device(np.array([5, 12, 9], np.uint32))
+            dev.launch("halo_rope_neox_p", (heads,), (64,),
+                       [g, prm, ("u32", hd), ("u32", rot), ("u32", 1), ("u32", 3), ("f32", 1e7)])
+            poss = [36] * heads
+        want = xr.copy()
+        for h in range(heads):
+            O.oracle().or_rope_neox(want[h], 1, hd, rot, poss[h], 1e7)
+        close(g.download(), want, np.abs(xr).max(), 2e-5)
+    # elementwise (grid-stride with a grid smaller than the data)
+    n = 10000
+    a, b = rng.normal(0, 1, n).astype(np.float32), rng.normal(0, 1, n).astype(np.float32)
+    cases = [("halo_add", lambda: a + b.astype(np.float64)), ("halo_silu_mul", lambda: silu(a) * b),
+             ("halo_sigmoid_gate", lambda: a * sig(b))]
+    for name, f in cases:
+        ga, gb = dev.to_device(a), dev.to_device(b)
+        dev.launch(name, (7,), (256,), [ga, gb, ("u32", n)])
+        close(ga.download(), f(), np.abs(f()) + np.abs(a) + 1e-6)
+    ga, gb = dev.to_device(a), dev.to_device(b)
+    dev.launch("halo_axpy", (7,), (256,), [ga, gb, ("f32", 0.5), ("u32", n)])
+    close(ga.download(), a + 0.5 * b.astype(np.float64), np.abs(a) + np.abs(b) + 1e-6)
+    gd = dev.array(n, np.float32)
+    dev.launch("halo_copy", (3,), (256,), [gd, ga, ("u32", n)])
+    assert np.array_equal(gd.download(), ga.download())
+    cache = dev.array((8, 300), np.float32).fill(0)
+    prm = dev.to_device(np.array([0, 5], np.uint32))
+    src = dev.to_device(b[:300])
+    dev.launch("halo_copy_at", (2,), (64,), [cache, src, prm, ("u32", 1), ("u32", 300), ("u32", 300)])
+    got = cache.download()
+    assert np.array_equal(got[5], b[:300]) and not got[np.arange(8) != 5].any()
+    # split q | gate
+    qg = rng.normal(0, 1, (4, 2 * 256)).astype(np.float32)
+    gq, g1, g2 = dev.to_device(qg), dev.array((4, 256), np.float32), dev.array((4, 256), np.float32)
+    dev.launch("halo_split_qgate", (4,), (256,), [gq, g1, g2, ("u32", 256)])
+    assert np.array_equal(g1.download(), qg[:, :256]) and np.array_equal(g2.download(), qg[:, 256:])
+
+
+def test_conv_steps(dev):
+    rng = np.random.default_rng(2)
+    C, K, d = 640, 4, 128
+    w = rng.normal(0, 0.5, (C, K)).astype(np.float32)
+    st = rng.normal(0, 1, (K - 1, C)).astype(np.float32)
+    x = rng.normal(0, 1, C).astype(np.float32)
+    conv = w[:, K - 1].astype(np.float64) * x + (w[:, :K - 1].T.astype(np.float64) * st).sum(0)
+    y = silu(conv.astype(np.float32))
+    shifted = np.concatenate([st[1:], x[None]], 0)
+    for name in ("halo_conv_step", "halo_conv_l2norm"):
+        gst, gw, gx, go = dev.to_device(st), dev.to_device(w), dev.to_device(x), dev.array(C, np.float32)
+        if name == "halo_conv_step":
+            dev.launch(name, ((C + 255) // 256,), (256,), [gx, gst, gw, go, ("u32", C), ("u32", K)])
+            want = y
+        else:  # the first 2 heads (q, k) L2-normalised per 128 channels
+            dev.launch(name, (C // d,), (d,), [gx, gst, gw, go, ("u32", C), ("u32", K), ("u32", 2 * d), ("f32", 1e-6)])
+            want = y.copy()
+            for h in range(2):
+                seg = want[h * d:(h + 1) * d]
+                want[h * d:(h + 1) * d] = seg / np.sqrt((seg * seg).sum() + 1e-6)
+        assert np.array_equal(gst.download(), shifted)
+        mag = np.abs(w[:, K - 1] * x) + (np.abs(w[:, :K - 1].T * st)).sum(0) + 1e-3
+        close(go.download(), want, mag)
+
+
+def gdn_inputs(rng, Hv, Hk, d):
+    q = rng.normal(0, 1, (Hk, d)).astype(np.float32)
+    k = rng.normal(0, 1, (Hk, d)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=1, keepdims=True)
+    k /= np.linalg.norm(k, axis=1, keepdims=True)
+    v = rng.normal(0, 1, (Hv, d)).astype(np.float32)
+    al, be = rng.normal(0, 1, Hv).astype(np.float32), rng.normal(0, 1, Hv).astype(np.float32)
+    a = -np.exp(rng.normal(0, 0.5, Hv)).astype(np.float32)
+    dt = rng.normal(0, 0.5, Hv).astype(np.float32)
+    S = rng.normal(0, 0.1, (Hv, d, d)).astype(np.float32)  # key-major [h][i][j]
+    return q, k, v, al, be, a, dt, S
+
+
+def gdn_oracle(q, k, v, al, be, a, dt, S, Hk):
+    Hv, d = v.shape
+    Sn = np.empty_like(S)
+    o = np.empty((Hv, d), np.float32)
+    L = O.oracle()
+    for h in range(Hv):
+        Sv = np.ascontiguousarray(S[h].T)  # value-major
+        g = float(a[h]) * L.or_softplus(float(al[h] + dt[h]))
+        oh = np.empty(d, np.float32)
+        L.or_gdn_step(Sv, d, q[h % Hk].copy(), k[h % Hk].copy(), v[h].copy(), g, L.or_sigmoid(float(be[h])), oh)
+        Sn[h] = Sv.T
+        o[h] = oh
+    return Sn, o
+
+
+@pytest.mark.parametrize("kernel", ["halo_gdn_step", "halo_gdn_step_d128", "halo_gdn_step_d128_norm"])
+def test_gdn_steps(dev, kernel):
+    rng = np.random.default_rng(3)
+    Hv, Hk, d = 8, 4, 128
+    q, k, v, al, be, a, dt, S = gdn_inputs(rng, Hv, Hk, d)
+    Sn, o = gdn_oracle(q, k, v, al, be, a, dt, S, Hk)
+    gs = dev.to_device(S)
+    ins = [dev.to_device(t) for t in (q, k, v, al, be, a, dt)]
+    go = dev.array((Hv, d), np.float32)
+    if kernel == "halo_gdn_step":
+        dev.launch(kernel, (Hv,), (d,), ins + [gs, go, ("u32", Hk), ("u32", d)])
+    elif kernel == "halo_gdn_step_d128":
+        dev.launch(kernel, (Hv,), (128,), ins + [gs, go, ("u32", Hk)])
+    else:
+        w = rng.normal(1, 0.1, d).astype(np.float32)
+        z = rng.normal(0, 1, (Hv, d)).astype(np.float32)
+        dev.launch(kernel, (Hv,), (128,), ins + [gs, dev.to_device(w), dev.to_device(z), go, ("u32", Hk),
+                                                 ("f32", 1e-6), ("u32", 1)])
+        on = o.astype(np.float64)
+        on = on / np.sqrt((on * on).mean(1, keepdims=True) + 1e-6) * w * sig(z)
+        o = on.astype(np.float32)
+    # magnitudes of the terms: S' = decay S + k delta, delta <= |v| + sum_i |S_ij k_i|; o = sum_i S'_ij q_i
+    kk = np.abs(k[np.arange(Hv) % Hk]).astype(np.float64)
+    qq = np.abs(q[np.arange(Hv) % Hk]).astype(np.float64)
+    dmag = np.abs(v) + np.einsum("hij,hi->hj", np.abs(S).astype(np.float64), kk)
+    mag_s = np.abs(S) + kk[:, :, None] * dmag[:, None, :]
+    close(gs.download(), Sn, mag_s)
+    mag_o = np.einsum("hij,hi->hj", mag_s, qq) / np.sqrt(d)
+    if kernel == "halo_gdn_step_d128_norm":  # after the norm: relative to the normalized values, 1e-4
+        close(go.download(), o, np.abs(o) + 1e-3, 1e-4)
+    else:
+        close(go.download(), o, mag_o)
+
+
+@pytest.mark.parametrize("kernel", ["halo_attention_decode", "halo_attention_prefill"])
+def test_attention(dev, kernel):
+    rng = np.random.default_rng(4)
+    Hq, Hkv, hd, n, T = 8, 2, 256, 300, 3
+    max_n = 512
+    kc = rng.normal(0, 1, (n, Hkv, hd)).astype(np.float32)
+    vc = rng.normal(0, 1, (n, Hkv, hd)).astype(np.float32)
+    rows = 1 if kernel == "halo_attention_decode" else T
+    q = rng.normal(0, 1, (rows, Hq, hd)).astype(np.float32)
+    gate = rng.normal(0, 1, (rows, Hq, hd)).astype(np.float32)
+    gk, gv, gq, gg = dev.to_device(kc), dev.to_device(vc), dev.to_device(q), dev.to_device(gate)
+    go, sc = dev.array((rows, Hq, hd), np.float32), dev.array((rows, Hq, max_n), np.float32)
+    if kernel == "halo_attention_decode":
+        dev.launch(kernel, (Hq,), (256,), [gq, gk, gv, gg, go, sc, ("u32", Hq), ("u32", Hkv), ("u32", hd), ("u32", n),
+                                           ("u32", max_n)])
+        lens = [n]
+    else:
+        pos0 = n - T
+        dev.launch(kernel, (Hq, T), (256,), [gq, gk, gv, gg, go, sc, ("u32", Hq), ("u32", Hkv), ("u32", hd),
+                                             ("u32", pos0), ("u32", max_n)])
+        lens = [pos0 + t + 1 for t in range(T)]
+    got = go.download()
+    for t, m in enumerate(lens):
+        for h in range(Hq):
+            kvh = h // (Hq // Hkv)
+            want = np.empty(hd, np.float32)
+            O.oracle().or_attention_head(q[t, h].copy(), np.ascontiguousarray(kc[:m, kvh]),
+                                         np.ascontiguousarray(vc[:m, kvh]), m, hd, hd, want)
+            want = want * sig(gate[t, h])
+            close(got[t, h], want, np.abs(vc[:m, kvh]).max(0) + 1e-3)

@@ -328,3 +328,165 @@ extern "C" __global__ void halo_attention_prefill(const float* q, const float* k
   AttendHead(q + row, kc, vc, gate + row, out + row,
              scores + (static_cast<std::size_t>(t) * num_heads + h) * max_n, kvh, num_kv_heads, hd, pos0 + t + 1, red);
 }
+
+// ---- Q8_0 GEMV variants, expert GEMVs, MoE down/combine, few-row fp32 matvecs (reference names) -------------
+// reference src/kernels/core.hip:2183-2211, 2362-2378, 2436-2458, 2988-3000, 3313-3330, 9263-9285, 9401-9416,
+// 9642-9700. Grids as the reference launches them: the Q8 GEMVs take ceil(rows / 8) blocks of 256 (ceil(rows / 32)
+// for the _r4 / _r4n variants), the MoE down kernels a second grid dimension over the expert slots, the rowblock
+// matvecs one block per output row. Repacked experts are stacked [experts][rows][qstride] int8 + [experts][rows]
+// [cols / 32] fp16. The fp32-x GEMV body is GemvQ8rF32 (wave64: two rows per wave per pass, x from the vector
+// cache, so no column limit of an LDS copy of x).
+extern "C" __global__ void __launch_bounds__(256)
+    halo_gemv_q8r_wide(const std::int8_t* qs, const std::uint16_t* d, const float* x, float* y, std::uint32_t rows,
+                       std::uint32_t cols, std::uint32_t qstride) {
+  GemvQ8rF32<1>(qs, d, x, y, rows, cols, qstride);
+}
+extern "C" __global__ void __launch_bounds__(256)
+    halo_gemv_q8r_r4n(const std::int8_t* qs, const std::uint16_t* d, const float* x, float* y, std::uint32_t rows,
+                      std::uint32_t cols, std::uint32_t qstride) {
+  GemvQ8rF32<4>(qs, d, x, y, rows, cols, qstride);
+}
+// Expert ids[slot] of the stacked tensor.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_gemv_q8r_expert(const std::int8_t* qs, const std::uint16_t* d, const std::uint32_t* ids, const float* x,
+                         float* y, std::uint32_t slot, std::uint32_t rows, std::uint32_t cols, std::uint32_t qstride) {
+  const std::size_t e = ids[slot];
+  GemvQ8rF32<1>(qs + e * rows * qstride, d + e * rows * (cols / 32), x, y, rows, cols, qstride);
+}
+extern "C" __global__ void __launch_bounds__(256)
+    halo_gemv_q8r_expert_r4(const std::int8_t* qs, const std::uint16_t* d, const std::uint32_t* ids,
+                            const float* x, float* y, std::uint32_t slot, std::uint32_t rows, std::uint32_t cols,
+                            std::uint32_t qstride) {
+  const std::size_t e = ids[slot];
+  GemvQ8rF32<4>(qs + e * rows * qstride, d + e * rows * (cols / 32), x, y, rows, cols, qstride);
+}
+// Down projections of every routed slot in one launch: grid.y = slots; h [slots][cols] -> part [slots][rows].
+extern "C" __global__ void __launch_bounds__(256)
+    halo_moe_down_q8r(const std::int8_t* qs, const std::uint16_t* d, const std::uint32_t* ids, const float* h,
+                      float* part, std::uint32_t rows, std::uint32_t cols, std::uint32_t qstride) {
+  const std::size_t slot = blockIdx.y, e = ids[slot];
+  GemvQ8rF32<1>(qs + e * rows * qstride, d + e * rows * (cols / 32), h + slot * cols, part + slot * rows, rows, cols,
+                qstride);
+}
+extern "C" __global__ void __launch_bounds__(256)
+    halo_moe_down_q8r_r4(const std::int8_t* qs, const std::uint16_t* d, const std::uint32_t* ids, const float* h,
+                         float* part, std::uint32_t rows, std::uint32_t cols, std::uint32_t qstride) {
+  const std::size_t slot = blockIdx.y, e = ids[slot];
+  GemvQ8rF32<4>(qs + e * rows * qstride, d + e * rows * (cols / 32), h + slot * cols, part + slot * rows, rows, cols,
+                qstride);
+}
+
+namespace halo::refk {
+// out[i] = sum over slots s, in slot order, of weights[s] * part[s][i] (fused multiply-add chain). Grid-stride.
+template <bool kUnrolled>
+__device__ __forceinline__ void Combine(const float* part, const float* weights, float* out, std::uint32_t slots,
+                                        std::uint32_t n) {
+  for (std::uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    float acc = 0.0f;
+    if constexpr (kUnrolled) {
+      float p[16];  // every slot's load issued before the chain
+#pragma unroll
+      for (std::uint32_t s = 0; s < 16; ++s) p[s] = s < slots ? part[static_cast<std::size_t>(s) * n + i] : 0.0f;
+#pragma unroll
+      for (std::uint32_t s = 0; s < 16; ++s)
+        if (s < slots) acc = __builtin_fmaf(weights[s], p[s], acc);
+    } else {
+      for (std::uint32_t s = 0; s < slots; ++s)
+        acc = __builtin_fmaf(weights[s], part[static_cast<std::size_t>(s) * n + i], acc);
+    }
+    out[i] = acc;
+  }
+}
+// y = row . x for one row per block; float4 loads when cols and the row are 16-byte aligned.
+__device__ __forceinline__ float RowDot(const float* row, const float* x, std::uint32_t cols, float* red) {
+  float acc = 0.0f;
+  if (cols % 4 == 0) {
+    const float4* r4 = reinterpret_cast<const float4*>(row);
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    for (std::uint32_t c = threadIdx.x; c < cols / 4; c += blockDim.x) {
+      const float4 a = r4[c], b = x4[c];
+      acc = __builtin_fmaf(a.x, b.x, acc);
+      acc = __builtin_fmaf(a.y, b.y, acc);
+      acc = __builtin_fmaf(a.z, b.z, acc);
+      acc = __builtin_fmaf(a.w, b.w, acc);
+    }
+  } else {
+    for (std::uint32_t c = threadIdx.x; c < cols; c += blockDim.x) acc = __builtin_fmaf(row[c], x[c], acc);
+  }
+  return BlockSumAny(acc, red);
+}
+}  // namespace halo::refk
+
+// n <= any; grid-stride over the n outputs.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_moe_combine(const float* part, const float* weights, float* out, std::uint32_t slots, std::uint32_t n) {
+  halo::refk::Combine<false>(part, weights, out, slots, n);
+}
+// slots <= 16.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_moe_combine_u(const float* part, const float* weights, float* out, std::uint32_t slots, std::uint32_t n) {
+  halo::refk::Combine<true>(part, weights, out, slots, n);
+}
+// grid (rows), any multiple of 64 threads: y[r] = w[r] . x.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_matvec_f32_rowblock(const float* w, const float* x, float* y, std::uint32_t rows, std::uint32_t cols) {
+  __shared__ float red[16];
+  const std::uint32_t r = blockIdx.x;
+  if (r >= rows) return;
+  const float acc = halo::refk::RowDot(w + static_cast<std::size_t>(r) * cols, x, cols, red);
+  if (threadIdx.x == 0) y[r] = acc;
+}
+extern "C" __global__ void __launch_bounds__(256)
+    halo_matvec_f32_rowblock_u(const float* w, const float* x, float* y, std::uint32_t rows, std::uint32_t cols) {
+  __shared__ float red[16];
+  const std::uint32_t r = blockIdx.x;
+  if (r >= rows) return;
+  const float acc = halo::refk::RowDot(w + static_cast<std::size_t>(r) * cols, x, cols, red);
+  if (threadIdx.x == 0) y[r] = acc;
+}
+// grid (2 rows): blocks [0, rows) compute ya = wa x, blocks [rows, 2 rows) yb = wb x.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_matvec_f32_rowblock2(const float* wa, const float* wb, const float* x, float* ya, float* yb,
+                              std::uint32_t rows, std::uint32_t cols) {
+  __shared__ float red[16];
+  const bool a = blockIdx.x < rows;
+  const std::uint32_t r = a ? blockIdx.x : blockIdx.x - rows;
+  if (r >= rows) return;
+  const float acc = halo::refk::RowDot((a ? wa : wb) + static_cast<std::size_t>(r) * cols, x, cols, red);
+  if (threadIdx.x == 0) (a ? ya : yb)[r] = acc;
+}
+extern "C" __global__ void __launch_bounds__(256)
+    halo_matvec_f32_rowblock2_u(const float* wa, const float* wb, const float* x, float* ya, float* yb,
+                                std::uint32_t rows, std::uint32_t cols) {
+  __shared__ float red[16];
+  const bool a = blockIdx.x < rows;
+  const std::uint32_t r = a ? blockIdx.x : blockIdx.x - rows;
+  if (r >= rows) return;
+  const float acc = halo::refk::RowDot((a ? wa : wb) + static_cast<std::size_t>(r) * cols, x, cols, red);
+  if (threadIdx.x == 0) (a ? ya : yb)[r] = acc;
+}
+// Per token and 32 values (amax / 127, round to nearest even, as halo_quantize_q8_rows), K-blocked:
+// x [T][cols] -> xq [cols / 64][T][64], xd [cols / 32][T]. grid (T), any multiple of 64 threads; cols % 64 == 0.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_quantize_q8_kblocked(const float* x, std::int8_t* xq, float* xd, std::uint32_t cols, std::uint32_t tokens) {
+  const std::size_t t = blockIdx.x;
+  const std::uint32_t lane = threadIdx.x % 32;
+  for (std::uint32_t blk = threadIdx.x / 32; blk < cols / 32; blk += blockDim.x / 32) {
+    const std::uint32_t c = blk * 32 + lane;
+    const float v = x[t * cols + c];
+    const float scale = halo::GroupMax<32>(fabsf(v)) / 127.0f;
+    xq[(static_cast<std::size_t>(c / 64) * tokens + t) * 64 + c % 64] =
+        static_cast<std::int8_t>(scale > 0.0f ? static_cast<int>(rintf(v / scale)) : 0);
+    if (lane == 0) xd[static_cast<std::size_t>(blk) * tokens + t] = scale;
+  }
+}
+// halo_router_topk's results (softmax, top k in (probability desc, index asc) order, weights renormalized in slot
+// order) with the reference's 256-thread launch: the first wave does the work. n <= 1024, k <= 16.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_router_topk_w(const float* logits, std::uint32_t* ids, float* weights, std::uint32_t n, std::uint32_t k) {
+  __shared__ std::uint32_t scratch[64];
+  __shared__ float wscratch[64];
+  __shared__ TopKScratch sc;
+  if (threadIdx.x >= kWave) return;
+  WaveTopK<16>(logits, n, k, ids, weights, scratch, wscratch, sc);
+}

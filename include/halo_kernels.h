@@ -30,6 +30,16 @@
  *     halo_gated_norm(o, w, z, d, eps, mode)                 grid (heads)
  *     halo_attention_decode(q, kc, vc, gate, out, scores, num_heads, num_kv_heads, hd, n, max_n)   grid (heads)
  *     halo_attention_prefill(..., num_heads, num_kv_heads, hd, pos0, max_n)                  grid (heads, T)
+ *   reference-named MoE / GEMV kernels (core.hip:2183-2211, 2362-2378, 2436-2458, 2988, 3313, 9263-9285, 9401,
+ *   9642), same parameters and grids:
+ *     halo_gemv_q8r_wide / _r4n(qs, d, x, y, rows, cols, qstride)        grid ceil(rows / 8) / ceil(rows / 32)
+ *     halo_gemv_q8r_expert{,_r4}(qs, d, ids, x, y, slot, rows, cols, qstride)   expert ids[slot] of a stacked tensor
+ *     halo_moe_down_q8r{,_r4}(qs, d, ids, h, part, rows, cols, qstride)  grid (ceil(rows / (8 R)), slots)
+ *     halo_moe_combine{,_u}(part, weights, out, slots, n)               grid-stride; _u: slots <= 16
+ *     halo_matvec_f32_rowblock{,_u}(w, x, y, rows, cols)                grid (rows)
+ *     halo_matvec_f32_rowblock2{,_u}(wa, wb, x, ya, yb, rows, cols)     grid (2 rows)
+ *     halo_quantize_q8_kblocked(x, xq, xd, cols, tokens)                grid (T): xq [cols/64][T][64], xd [cols/32][T]
+ *     halo_router_topk_w(logits, ids, weights, n, k)                    1 block of 256; n <= 1024, k <= 16
  *   halo_synth_q8(qs, d, rows, cols, qstride, u64 seed, f32 sigma), halo_synth_f32(x, u64 n, u64 seed, f32 sigma)
  *                                                                                              new (synthetic data)
  */
@@ -51,6 +61,10 @@
   X(halo_add) X(halo_axpy) X(halo_silu_mul) X(halo_sigmoid_gate) X(halo_copy) X(halo_copy_at)                 \
   X(halo_split_qgate) X(halo_conv_step) X(halo_conv_l2norm) X(halo_gdn_step) X(halo_gdn_step_d128)            \
   X(halo_gdn_step_d128_norm) X(halo_gated_norm) X(halo_attention_decode) X(halo_attention_prefill)           \
+  X(halo_gemv_q8r_wide) X(halo_gemv_q8r_r4n) X(halo_gemv_q8r_expert) X(halo_gemv_q8r_expert_r4)             \
+  X(halo_moe_down_q8r) X(halo_moe_down_q8r_r4) X(halo_moe_combine) X(halo_moe_combine_u)                      \
+  X(halo_matvec_f32_rowblock) X(halo_matvec_f32_rowblock_u) X(halo_matvec_f32_rowblock2)                     \
+  X(halo_matvec_f32_rowblock2_u) X(halo_quantize_q8_kblocked) X(halo_router_topk_w)                          \
   X(halo_synth_q8) X(halo_synth_f32)
 
 #endif /* HALO_KERNELS_H_ */

@@ -214,3 +214,122 @@ def test_attention(dev, kernel):
                                          np.ascontiguousarray(vc[:m, kvh]), m, hd, hd, want)
             want = want * sig(gate[t, h])
             close(got[t, h], want, np.abs(vc[:m, kvh]).max(0) + 1e-3)
+
+
+# ---- reference-named MoE / GEMV kernels (src/kernels/core.hip:2183-2211, 2362-2378, 2436-2458, 2988, 3313,
+# 9263-9285, 9401, 9642) -> or_matvec_q8_0_f32x, or_matvec_f32, or_quantize_q8_act, or_route_topk, numpy.
+# GEMV bars as the other Q8 GEMVs: 1e-5 of sum |term| + 1e-6; quantizer and top-k ids bit-exact, top-k weights
+# bit-exact against halo_router_topk (the same results are the kernel's contract).
+
+def _q8_ref(qs, d, x):
+    rows, cols = qs.shape
+    y = np.zeros(rows, np.float32)
+    O.oracle().or_matvec_q8_0_f32x(np.ascontiguousarray(qs), np.ascontiguousarray(d), rows, cols, cols,
+                                   np.ascontiguousarray(x), y, 1)
+    mag = np.abs(qs * np.repeat(d.view(np.float16).astype(np.float64), 32, 1)) @ np.abs(x.astype(np.float64))
+    return y, mag
+
+
+def _gemv_close(got, want, mag):
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    assert np.all(err <= 1e-5 * mag + 1e-6), f"worst {np.max(err - 1e-5 * mag - 1e-6)}"
+
+
+@pytest.mark.parametrize("name,rpb", [("halo_gemv_q8r_wide", 8), ("halo_gemv_q8r_r4n", 32)])
+def test_q8r_wide_r4n(dev, name, rpb):
+    rng = np.random.default_rng(41)
+    for rows, cols in ((100, 10240), (1037, 2048), (4, 6144)):
+        qs, d = O.synth_q8(rng, rows, cols)
+        x = rng.normal(0, 1, cols).astype(np.float32)
+        gq, gd, gx, gy = dev.to_device(qs), dev.to_device(d), dev.to_device(x), dev.array((rows,), np.float32)
+        dev.launch(name, ((rows + rpb - 1) // rpb,), (256,), [gq, gd, gx, gy, ("u32", rows), ("u32", cols),
+                                                              ("u32", cols)])
+        _gemv_close(gy.download(), *_q8_ref(qs, d, x))
+
+
+@pytest.mark.parametrize("r", [1, 4])
+def test_expert_gemv_and_down(dev, r):
+    rng = np.random.default_rng(42 + r)
+    E, rows, cols, slots = 9, 520, 1024, 5
+    qs, d = O.synth_q8(rng, E * rows, cols)
+    qs3, d3 = qs.reshape(E, rows, cols), d.reshape(E, rows, cols // 32)
+    ids = np.array([7, 0, 8, 3, 7], np.uint32)
+    h = rng.normal(0, 1, (slots, cols)).astype(np.float32)
+    gq, gd, gi, gh = dev.to_device(qs), dev.to_device(d), dev.to_device(ids), dev.to_device(h)
+    rpb = 8 * r
+    grid = (rows + rpb - 1) // rpb
+    suffix = "_r4" if r == 4 else ""
+    dims = [("u32", rows), ("u32", cols), ("u32", cols)]
+    for slot in range(slots):
+        gx, gy = dev.to_device(h[slot]), dev.array((rows,), np.float32)
+        dev.launch("halo_gemv_q8r_expert" + suffix, (grid,), (256,), [gq, gd, gi, gx, gy, ("u32", slot)] + dims)
+        _gemv_close(gy.download(), *_q8_ref(qs3[ids[slot]], d3[ids[slot]], h[slot]))
+    part = dev.array((slots, rows), np.float32)
+    dev.launch("halo_moe_down_q8r" + suffix, (grid, slots), (256,), [gq, gd, gi, gh, part] + dims)
+    got = part.download()
+    for slot in range(slots):
+        _gemv_close(got[slot], *_q8_ref(qs3[ids[slot]], d3[ids[slot]], h[slot]))
+
+
+@pytest.mark.parametrize("name", ["halo_moe_combine", "halo_moe_combine_u"])
+def test_moe_combine(dev, name):
+    rng = np.random.default_rng(43)
+    for slots, n in ((8, 2048), (16, 1000), (1, 77)):
+        part = rng.normal(0, 1, (slots, n)).astype(np.float32)
+        w = rng.random(slots).astype(np.float32)
+        gp, gw, go = dev.to_device(part), dev.to_device(w), dev.array((n,), np.float32)
+        dev.launch(name, (4,), (256,), [gp, gw, go, ("u32", slots), ("u32", n)])
+        want = (w.astype(np.float64)[:, None] * part).sum(0)
+        close(go.download(), want, (np.abs(w.astype(np.float64)[:, None] * part)).sum(0) + 1e-6)
+
+
+@pytest.mark.parametrize("suffix", ["", "_u"])
+def test_matvec_rowblock(dev, suffix):
+    rng = np.random.default_rng(44)
+    for rows, cols in ((512, 2048), (48, 4096), (3, 1001)):
+        wa = rng.normal(0, 1, (rows, cols)).astype(np.float32)
+        wb = rng.normal(0, 1, (rows, cols)).astype(np.float32)
+        x = rng.normal(0, 1, cols).astype(np.float32)
+        gwa, gwb, gx = dev.to_device(wa), dev.to_device(wb), dev.to_device(x)
+        ya, yb = dev.array((rows,), np.float32), dev.array((rows,), np.float32)
+        dev.launch("halo_matvec_f32_rowblock" + suffix, (rows,), (256,), [gwa, gx, ya, ("u32", rows), ("u32", cols)])
+        want = np.zeros(rows, np.float32)
+        O.oracle().or_matvec_f32(wa, rows, cols, x, want)
+        mag = np.abs(wa.astype(np.float64)) @ np.abs(x.astype(np.float64))
+        close(ya.download(), want, mag)
+        dev.launch("halo_matvec_f32_rowblock2" + suffix, (2 * rows,), (256,),
+                   [gwa, gwb, gx, ya, yb, ("u32", rows), ("u32", cols)])
+        close(ya.download(), want, mag)
+        O.oracle().or_matvec_f32(wb, rows, cols, x, want)
+        close(yb.download(), want, np.abs(wb.astype(np.float64)) @ np.abs(x.astype(np.float64)))
+
+
+def test_quantize_kblocked_bit_exact(dev):
+    rng = np.random.default_rng(45)
+    T, cols = 5, 2048
+    x = rng.normal(0, 1, (T, cols)).astype(np.float32)
+    x[1, 64:96] = 0.0  # an all-zero block: scale 0, q 0
+    gx, gq, gd = dev.to_device(x), dev.array((cols // 64, T, 64), np.int8), dev.array((cols // 32, T), np.float32)
+    dev.launch("halo_quantize_q8_kblocked", (T,), (256,), [gx, gq, gd, ("u32", cols), ("u32", T)])
+    wq, wd = np.zeros((T, cols), np.int8), np.zeros((T, cols // 32), np.float32)
+    for t in range(T):
+        O.oracle().or_quantize_q8_act(x[t], wq[t], wd[t], cols)
+    assert np.array_equal(gq.download(), wq.reshape(T, cols // 64, 64).transpose(1, 0, 2))
+    assert gd.download().tobytes() == np.ascontiguousarray(wd.T).tobytes()
+
+
+def test_router_topk_w(dev):
+    rng = np.random.default_rng(46)
+    for n, k in ((512, 10), (256, 8), (1024, 16), (64, 1)):
+        logits = rng.normal(0, 2, n).astype(np.float32)
+        logits[5] = logits[9]  # a tie: the lower index ranks first
+        gl = dev.to_device(logits)
+        outs = []
+        for name, block in (("halo_router_topk_w", 256), ("halo_router_topk", 64)):
+            gi, gw = dev.array((k,), np.uint32), dev.array((k,), np.float32)
+            dev.launch(name, (1,), (block,), [gl, gi, gw, ("u32", n), ("u32", k)])
+            outs.append((gi.download(), gw.download()))
+        wi, ww = np.zeros(k, np.uint32), np.zeros(k, np.float32)
+        O.oracle().or_route_topk(logits, n, k, wi, ww)
+        assert np.array_equal(outs[0][0], wi) and outs[0][1].tobytes() == outs[1][1].tobytes()
+        np.testing.assert_allclose(outs[0][1], ww, rtol=1e-5)

@@ -538,11 +538,12 @@ extern "C" __global__ void __launch_bounds__(256) halo_gemm_q8a8_mfma_t4(
 namespace {
 typedef int V16I32 __attribute__((ext_vector_type(16)));
 typedef float V16F32 __attribute__((ext_vector_type(16)));
+typedef float V32F32 __attribute__((ext_vector_type(32)));
 constexpr int kTileLd = 64 + 16;
 }  // namespace
 
 namespace halo {
-template <int WR, int MT, int WT, int NMAT>
+template <int WR, int MT, int WT, int NMAT, bool PAIR = false>
 __device__ __forceinline__ void GemmTileQ8(const std::int8_t* __restrict__ A0, const std::uint16_t* __restrict__ D0,
                                           const std::int8_t* __restrict__ A1, const std::uint16_t* __restrict__ D1,
                                           std::uint32_t rows, std::uint32_t qstride, std::uint32_t r0,
@@ -645,26 +646,55 @@ __device__ __forceinline__ void GemmTileQ8(const std::int8_t* __restrict__ A0, c
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc[m][mt][j] = 0.0f;
   const std::uint32_t fr = lane % 32, fk = 16 * (lane / 32);
+  // PAIR (one matrix): both Q8_0 blocks of the stage take one two-block rank-1 fp32 MFMA for their scales (block b
+  // from lanes 32 b .. 32 b + 31, result registers 16 b .. 16 b + 15), then the int8 MFMAs, then the epilogue in
+  // block order. It needs about 200 VGPRs (one block per CU), so it serves grids of at most one block per CU.
+  // Otherwise one Q8_0 block at a time, each with its own rank-1 MFMA.
   auto compute = [&](std::uint32_t st) {
-#pragma unroll 1
-    for (int blk = 0; blk < 2; ++blk) {
-      const V4i bf = *reinterpret_cast<const V4i*>(&lb[st][wt * 32 + fr][blk * 32 + fk]);
-      const float sx = lsx[st][blk][wt * 32 + fr];
-      const float bsx = lane < 32 ? sx : 0.0f;
+    if constexpr (PAIR) {
+      static_assert(NMAT == 1, "one matrix");
+      const V4i bf0 = *reinterpret_cast<const V4i*>(&lb[st][wt * 32 + fr][fk]);
+      const V4i bf1 = *reinterpret_cast<const V4i*>(&lb[st][wt * 32 + fr][32 + fk]);
+      const float sx = lsx[st][lane / 32][wt * 32 + fr];
       const V16I32 zero = {};
-      const V16F32 fzero = {};
+      const V32F32 fzero = {};
 #pragma unroll
-      for (int m = 0; m < NMAT; ++m)
+      for (int mt = 0; mt < MT; ++mt) {
+        const std::uint32_t rr = wr * MT * 32 + mt * 32 + fr;
+        const V4i af0 = *reinterpret_cast<const V4i*>(&la[st][0][rr][fk]);
+        const V4i af1 = *reinterpret_cast<const V4i*>(&la[st][0][rr][32 + fk]);
+        const float dw = ldw[st][0][lane / 32][rr];
+        const V32F32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(dw, sx, fzero, 0, 0, 0);
+        const V16I32 c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(af0, bf0, zero, 0, 0, 0);
+        const V16I32 c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(af1, bf1, zero, 0, 0, 0);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const std::uint32_t rr = wr * MT * 32 + mt * 32 + fr;
-          const V4i af = *reinterpret_cast<const V4i*>(&la[st][m][rr][blk * 32 + fk]);
-          const float dw = ldw[st][m][blk][rr];
-          const V16F32 sc = __builtin_amdgcn_mfma_f32_32x32x2f32(lane < 32 ? dw : 0.0f, bsx, fzero, 0, 0, 0);
-          const V16I32 c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, zero, 0, 0, 0);
+        for (int j = 0; j < 16; ++j) acc[0][mt][j] = __builtin_fmaf(static_cast<float>(c0[j]), sc[j], acc[0][mt][j]);
 #pragma unroll
-          for (int j = 0; j < 16; ++j) acc[m][mt][j] = __builtin_fmaf(static_cast<float>(c[j]), sc[j], acc[m][mt][j]);
-        }
+        for (int j = 0; j < 16; ++j)
+          acc[0][mt][j] = __builtin_fmaf(static_cast<float>(c1[j]), sc[16 + j], acc[0][mt][j]);
+      }
+    } else {
+#pragma unroll 1
+      for (int blk = 0; blk < 2; ++blk) {
+        const V4i bf = *reinterpret_cast<const V4i*>(&lb[st][wt * 32 + fr][blk * 32 + fk]);
+        const float sx = lsx[st][blk][wt * 32 + fr];
+        const float bsx = lane < 32 ? sx : 0.0f;
+        const V16I32 zero = {};
+        const V16F32 fzero = {};
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const std::uint32_t rr = wr * MT * 32 + mt * 32 + fr;
+            const V4i af = *reinterpret_cast<const V4i*>(&la[st][m][rr][blk * 32 + fk]);
+            const float dw = ldw[st][m][blk][rr];
+            const V16F32 sc = __builtin_amdgcn_mfma_f32_32x32x2f32(lane < 32 ? dw : 0.0f, bsx, fzero, 0, 0, 0);
+            const V16I32 c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, zero, 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+              acc[m][mt][j] = __builtin_fmaf(static_cast<float>(c[j]), sc[j], acc[m][mt][j]);
+          }
+      }
     }
   };
   // one stage: prefetch kc + 2 into `fill`, compute kc, store kc + 1 (from `next`) into the other buffer, barrier.
@@ -715,6 +745,16 @@ extern "C" __global__ void __launch_bounds__(512) halo_gemm_q8a8_mfma32(
   const std::uint32_t t0 = blockIdx.y * 128;
   halo::GemmTileQ8<2, 2, 4, 1>(qs, d, nullptr, nullptr, rows, qstride, blockIdx.x * 128, xq, xs, nullptr, t0,
                                min(128u, T - t0), cols, y, t0, ystride);
+}
+
+// The same GEMM for grids of at most one block per CU (the scales of a stage's two Q8_0 blocks from one MFMA).
+extern "C" __global__ void __launch_bounds__(512) halo_gemm_q8a8_mfma32_p(
+    const std::int8_t* __restrict__ qs, const std::uint16_t* __restrict__ d, const std::int8_t* __restrict__ xq,
+    const float* __restrict__ xs, float* __restrict__ y, std::uint32_t rows, std::uint32_t cols,
+    std::uint32_t qstride, std::uint32_t T, std::uint32_t ystride) {
+  const std::uint32_t t0 = blockIdx.y * 128;
+  halo::GemmTileQ8<2, 2, 4, 1, true>(qs, d, nullptr, nullptr, rows, qstride, blockIdx.x * 128, xq, xs, nullptr, t0,
+                                     min(128u, T - t0), cols, y, t0, ystride);
 }
 
 // x = a * x + b over n floats (shapes seeded tensors such as norm weights around 1).

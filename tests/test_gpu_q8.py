@@ -200,10 +200,11 @@ def test_synth_distribution(dev):
     assert np.array_equal(w2.host()[0], qs)  # deterministic
 
 
-@pytest.mark.parametrize("m,rows,cols", [(128, 512, 2048), (300, 1024, 4096), (2048, 256, 2048)])
+@pytest.mark.parametrize("m,rows,cols", [(128, 512, 2048), (300, 1024, 4096), (2048, 256, 2048), (1100, 3840, 1024)])
 def test_mfma_gemm_prefill_tiles(dev, m, rows, cols):
     """Prefill-sized M (>= 64) runs the 128 x 128 LDS-tiled kernel (v_mfma_i32_32x32x32_i8, one MFMA per Q8_0 block
-    and 32 x 32 tile); dense output, ragged M."""
+    and 32 x 32 tile); dense output, ragged M. Grids of at most 256 blocks take the paired-scale variant
+    (halo_gemm_q8a8_mfma32_p), the last case (270 blocks) the other."""
     rng = np.random.default_rng(m + rows)
     w, xq, xs, want, mag = _gemv_case(dev, rng, rows, cols, m)
     gq, gs = dev.to_device(xq), dev.to_device(xs)

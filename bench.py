@@ -708,7 +708,8 @@ def run_gdn(args, dev, H, res):
     for _ in range(reps):
         prefill()
     ms = dev.timer_stop() / reps
-    flops = T * Hv * (3 * D * D + 3 * 64 * D) * 2  # per token and value head: 3 d^2 state products + 3 C d chunk terms, 2 flops each
+    # per token and value head: 3 d^2 state products and 3 C d chunk terms, 2 flops each
+    flops = T * Hv * (3 * D * D + 3 * 64 * D) * 2
     out["prefill_C3"] = {"tokens": T, "ms": round(ms, 3), "tokens_per_s": round(T / (ms * 1e-3)),
                          "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 2)}
     log(f"[bench] gdn {out}")

@@ -43,17 +43,21 @@ __device__ __forceinline__ void RotateHead(float* v, std::uint32_t rotary_dim, s
   }
 }
 
-// Softmax(q . K^T / sqrt(hd)) V * sigmoid(gate) for one query head over positions [0, n) of a contiguous cache
-// [pos][num_kv_heads][hd]; sc is the head's score scratch (global, n entries). Scores: one wave per position, its
-// lanes across hd (coalesced rows); weighted V: threads across hd.
+// Softmax(q . K^T / sqrt(hd)) V * sigmoid(gate) for one query head over n rows of a contiguous cache
+// [pos][num_kv_heads][hd]: rows [0, n), or rows visible[0 .. n) when `visible` is given; sc is the head's score
+// scratch (global, n entries). Scores: one wave per position, its lanes across hd (coalesced rows); weighted V:
+// threads across hd.
 __device__ void AttendHead(const float* qh, const float* kc, const float* vc, const float* gh, float* oh, float* sc,
                            std::uint32_t kvh, std::uint32_t num_kv_heads, std::uint32_t hd, std::uint32_t n,
-                           float* red) {
+                           float* red, const std::uint32_t* visible = nullptr) {
+  const auto row = [&](std::uint32_t p) -> std::size_t {
+    return (static_cast<std::size_t>(visible ? visible[p] : p) * num_kv_heads + kvh) * hd;
+  };
   const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, nw = blockDim.x / kWave;
   const float scale = 1.0f / sqrtf(static_cast<float>(hd));
   float mx = -INFINITY;
   for (std::uint32_t p = wave; p < n; p += nw) {
-    const float* kp = kc + (static_cast<std::size_t>(p) * num_kv_heads + kvh) * hd;
+    const float* kp = kc + row(p);
     float dot = 0.0f;
     for (std::uint32_t i = lane; i < hd; i += kWave) dot += qh[i] * kp[i];
     dot = halo::GroupSum(dot) * scale;
@@ -70,7 +74,7 @@ __device__ void AttendHead(const float* qh, const float* kc, const float* vc, co
   den = BlockSumAny(den, red);
   for (std::uint32_t i = threadIdx.x; i < hd; i += blockDim.x) {
     float acc = 0.0f;
-    for (std::uint32_t p = 0; p < n; ++p) acc += sc[p] * vc[(static_cast<std::size_t>(p) * num_kv_heads + kvh) * hd + i];
+    for (std::uint32_t p = 0; p < n; ++p) acc += sc[p] * vc[row(p) + i];
     oh[i] = acc / den * halo::Sigmoid(gh[i]);
   }
 }
@@ -329,6 +333,38 @@ extern "C" __global__ void halo_attention_prefill(const float* q, const float* k
              scores + (static_cast<std::size_t>(t) * num_heads + h) * max_n, kvh, num_kv_heads, hd, pos0 + t + 1, red);
 }
 
+// Attention over a list of visible cache rows (core.hip:783-820, 898-903, 909-918): n = params[5] (the step
+// parameters' visible count), rows visible[0 .. n) of the contiguous cache, one block per query head; scores
+// [num_heads][max_n]. _b is the same kernel under the name the decode engine launches; _rows takes token t =
+// blockIdx.y with q, gate, out [T][num_heads][hd], visible lists max_n apart, scores num_heads * max_n apart and
+// step parameters 16 words apart.
+#define HALO_ATTN_SELECT(NAME)                                                                                     \
+  extern "C" __global__ void __launch_bounds__(256)                                                              \
+      NAME(const float* q, const float* kc, const float* vc, const float* gate, const std::uint32_t* visible,    \
+           float* out, float* scores, const std::uint32_t* params, std::uint32_t num_heads,                      \
+           std::uint32_t num_kv_heads, std::uint32_t hd, std::uint32_t max_n) {                                  \
+    __shared__ float red[16];                                                                                    \
+    const std::uint32_t h = blockIdx.x, kvh = h / (num_heads / num_kv_heads);                                    \
+    const std::size_t row = static_cast<std::size_t>(h) * hd;                                                    \
+    AttendHead(q + row, kc, vc, gate + row, out + row, scores + static_cast<std::size_t>(h) * max_n, kvh,        \
+               num_kv_heads, hd, params[5], red, visible);                                                       \
+  }
+HALO_ATTN_SELECT(halo_attention_select)
+HALO_ATTN_SELECT(halo_attention_select_b)
+#undef HALO_ATTN_SELECT
+extern "C" __global__ void __launch_bounds__(256)
+    halo_attention_select_rows(const float* q, const float* kc, const float* vc, const float* gate,
+                               const std::uint32_t* visible, float* out, float* scores, const std::uint32_t* params,
+                               std::uint32_t num_heads, std::uint32_t num_kv_heads, std::uint32_t hd,
+                               std::uint32_t max_n) {
+  __shared__ float red[16];
+  const std::uint32_t h = blockIdx.x, t = blockIdx.y, kvh = h / (num_heads / num_kv_heads);
+  const std::size_t row = (static_cast<std::size_t>(t) * num_heads + h) * hd;
+  AttendHead(q + row, kc, vc, gate + row, out + row,
+             scores + (static_cast<std::size_t>(t) * num_heads + h) * max_n, kvh, num_kv_heads, hd,
+             params[static_cast<std::size_t>(t) * 16 + 5], red, visible + static_cast<std::size_t>(t) * max_n);
+}
+
 // ---- Q8_0 GEMV variants, expert GEMVs, MoE down/combine, few-row fp32 matvecs (reference names) -------------
 // reference src/kernels/core.hip:2183-2211, 2362-2378, 2436-2458, 2988-3000, 3313-3330, 9263-9285, 9401-9416,
 // 9642-9700. Grids as the reference launches them: the Q8 GEMVs take ceil(rows / 8) blocks of 256 (ceil(rows / 32)
@@ -489,4 +525,223 @@ extern "C" __global__ void __launch_bounds__(256)
   __shared__ TopKScratch sc;
   if (threadIdx.x >= kWave) return;
   WaveTopK<16>(logits, n, k, ids, weights, scratch, wscratch, sc);
+}
+
+// ---- DeltaNet prefill helpers and the chunk-stepped d = 128 step (reference names) ------------------------------
+// core.hip:3480-3500, 3586-3597, 3612-3662, 9590-9636.
+
+// halo_gdn_step_d128_norm under the name of the reference's two-pass variant (this implementation is two-pass).
+extern "C" __global__ void __launch_bounds__(128)
+    halo_gdn_step_d128_norm_r(const float* q, const float* k, const float* v, const float* alpha, const float* beta,
+                              const float* a, const float* dt, float* state, const float* norm_w, const float* z,
+                              float* out, std::uint32_t num_k_heads, float eps, std::uint32_t mode) {
+  __shared__ float kl[128], ql[128], red[2];
+  const float o = GdnStepD128(q, k, v, alpha, beta, a, dt, state, num_k_heads, kl, ql, red);
+  const float inv = 1.0f / sqrtf(BlockSumAny(o * o, red) / 128.0f + eps);
+  const std::size_t at = static_cast<std::size_t>(blockIdx.x) * 128 + threadIdx.x;
+  const float zv = z[at];
+  out[at] = o * inv * norm_w[threadIdx.x] * (mode == 0 ? halo::Silu(zv) : halo::Sigmoid(zv));
+}
+
+// halo_gdn_step_d128_norm over T tokens in one launch, token by token with the same arithmetic (each token's output
+// and the final state equal T single steps bit for bit). Row t of q and k at t * qk_stride, of v at t * v_stride, of
+// z and out at t * zo_stride; alpha, beta [T][heads]. grid (heads), block 128.
+extern "C" __global__ void __launch_bounds__(128)
+    halo_gdn_prefill_d128_norm(const float* q, const float* k, const float* v, const float* alpha, const float* beta,
+                               const float* a, const float* dt, float* state, const float* norm_w, const float* z,
+                               float* out, std::uint32_t num_k_heads, float eps, std::uint32_t mode,
+                               std::uint32_t tokens, std::uint32_t qk_stride, std::uint32_t v_stride,
+                               std::uint32_t zo_stride) {
+  __shared__ float kl[128], ql[128], red[2];
+  const std::uint32_t heads = gridDim.x;
+  const float wj = norm_w[threadIdx.x];
+  for (std::uint32_t t = 0; t < tokens; ++t) {
+    const std::size_t qk = static_cast<std::size_t>(t) * qk_stride, ab = static_cast<std::size_t>(t) * heads;
+    // the previous token's last block sum ends with barriers after every read of kl / ql
+    const float o = GdnStepD128(q + qk, k + qk, v + static_cast<std::size_t>(t) * v_stride, alpha + ab, beta + ab, a,
+                                dt, state, num_k_heads, kl, ql, red);
+    const float inv = 1.0f / sqrtf(BlockSumAny(o * o, red) / 128.0f + eps);
+    const std::size_t at = static_cast<std::size_t>(t) * zo_stride + static_cast<std::size_t>(blockIdx.x) * 128 +
+                           threadIdx.x;
+    const float zv = z[at];
+    out[at] = o * inv * wj * (mode == 0 ? halo::Silu(zv) : halo::Sigmoid(zv));
+  }
+}
+
+// halo_conv_l2norm for T tokens at once: token t's window is the kern - 1 inputs before it, from the chunk or, before
+// the chunk, from the conv state (slot j holds input j - (kern - 1)); the sums run in the decode kernel's order, so
+// each token's output equals stepping bit for bit. The state is not written (halo_conv_state_advance moves it).
+//   in, out [T][channels]; grid (ceil(channels / d), T), block d (one head of channels).
+extern "C" __global__ void halo_conv_l2norm_prefill(const float* in, const float* state, const float* w, float* out,
+                                                    std::uint32_t channels, std::uint32_t kern,
+                                                    std::uint32_t l2_channels, float eps) {
+  __shared__ float red[16];
+  const std::uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+  float y = 0.0f;
+  if (ch < channels) {
+    float acc = w[static_cast<std::size_t>(ch) * kern + kern - 1] * in[static_cast<std::size_t>(t) * channels + ch];
+    for (std::uint32_t j = 0; j + 1 < kern; ++j) {
+      const std::int64_t i = static_cast<std::int64_t>(t) - static_cast<std::int64_t>(kern - 1) + j;
+      const float x = i >= 0 ? in[static_cast<std::size_t>(i) * channels + ch]
+                             : state[static_cast<std::size_t>(i + kern - 1) * channels + ch];
+      acc += w[static_cast<std::size_t>(ch) * kern + j] * x;
+    }
+    y = halo::Silu(acc);
+  }
+  if (blockIdx.x * blockDim.x < l2_channels) y *= 1.0f / sqrtf(BlockSumAny(y * y, red) + eps);  // block-uniform
+  if (ch < channels) out[static_cast<std::size_t>(t) * channels + ch] = y;
+}
+
+// The conv state after a chunk of T inputs: the last kern - 1 inputs (older ones from the previous state when
+// T < kern - 1). grid (ceil(channels / 256)), block 256; kern <= 9.
+extern "C" __global__ void halo_conv_state_advance(const float* in, float* state, std::uint32_t channels,
+                                                   std::uint32_t kern, std::uint32_t tokens) {
+  const std::uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
+  if (ch >= channels || kern < 2) return;
+  float next[8];
+#pragma unroll
+  for (std::uint32_t j = 0; j < 8; ++j) {
+    if (j + 1 >= kern) break;
+    const std::int64_t i = static_cast<std::int64_t>(tokens) - static_cast<std::int64_t>(kern - 1) + j;
+    next[j] = i >= 0 ? in[static_cast<std::size_t>(i) * channels + ch]
+                     : state[static_cast<std::size_t>(i + kern - 1) * channels + ch];
+  }
+#pragma unroll
+  for (std::uint32_t j = 0; j < 8; ++j) {
+    if (j + 1 >= kern) break;
+    state[static_cast<std::size_t>(j) * channels + ch] = next[j];
+  }
+}
+
+// ---- router with the expert activations quantized, shared expert (reference names) --------------------------------
+// core.hip:2657-2661, 9196-9230, 9284-9343, 9418-9446.
+namespace halo::refk {
+// Q8_0 row r of [rows][qstride] int8 + [rows][cols / 32] fp16 dotted with fp32 x (cols % 1024 == 0 not required:
+// cols % 16 == 0); every lane of the wave gets the sum.
+__device__ __forceinline__ float Q8RowDot(const std::int8_t* qs, const std::uint16_t* d, const float* x,
+                                          std::uint32_t r, std::uint32_t cols, std::uint32_t qstride) {
+  const std::uint32_t lane = threadIdx.x % kWave, nblk = cols / 32;
+  float acc = 0.0f;
+  for (std::uint32_t c = lane * 16; c < cols; c += kWave * 16) {
+    const int4 qv = *reinterpret_cast<const int4*>(qs + static_cast<std::size_t>(r) * qstride + c);
+    const std::int8_t* q8 = reinterpret_cast<const std::int8_t*>(&qv);
+    const float4* xp = reinterpret_cast<const float4*>(x + c);
+    float part = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 xv = xp[i];
+      part += static_cast<float>(q8[4 * i]) * xv.x + static_cast<float>(q8[4 * i + 1]) * xv.y +
+              static_cast<float>(q8[4 * i + 2]) * xv.z + static_cast<float>(q8[4 * i + 3]) * xv.w;
+    }
+    acc += halo::F16(d[static_cast<std::size_t>(r) * nblk + c / 32]) * part;
+  }
+  return halo::GroupSum(acc);
+}
+
+// The shared expert's gate/up: h[r] = SiLU(gate_r . x) * (up_r . x), 16 rows per block (4 per wave); block 0 also
+// writes sgate[0] = gate_inp . x.
+__device__ __forceinline__ void ShexpGateUp(const std::int8_t* gq, const std::uint16_t* gd, const std::int8_t* uq,
+                                            const std::uint16_t* ud, const float* gate_inp, const float* x, float* h,
+                                            float* sgate, std::uint32_t rows, std::uint32_t cols,
+                                            std::uint32_t qstride, float* red) {
+  if (blockIdx.x == 0) {
+    const float s = RowDot(gate_inp, x, cols, red);
+    if (threadIdx.x == 0) sgate[0] = s;
+  }
+  const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const std::uint32_t per_wave = 16 / (blockDim.x / kWave);
+  for (std::uint32_t k = 0; k < per_wave; ++k) {
+    const std::uint32_t r = blockIdx.x * 16 + wave * per_wave + k;
+    if (r >= rows) break;
+    const float g = Q8RowDot(gq, gd, x, r, cols, qstride), u = Q8RowDot(uq, ud, x, r, cols, qstride);
+    if (lane == 0) h[r] = halo::Silu(g) * u;
+  }
+}
+
+// out[r] = sum over slots s, in slot order, of weights[s] * part[s][r], + sigmoid(sgate[0]) * (down_r . hin); 32 rows
+// per block (8 per wave).
+__device__ __forceinline__ void ShexpDownCombine(const std::int8_t* dq, const std::uint16_t* dd, const float* hin,
+                                                 const float* sgate, const float* part, const float* weights,
+                                                 std::uint32_t slots, float* out, std::uint32_t rows,
+                                                 std::uint32_t cols, std::uint32_t qstride) {
+  const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const std::uint32_t per_wave = 32 / (blockDim.x / kWave);
+  const float s = halo::Sigmoid(sgate[0]);
+  for (std::uint32_t k = 0; k < per_wave; ++k) {
+    const std::uint32_t r = blockIdx.x * 32 + wave * per_wave + k;
+    if (r >= rows) break;
+    const float y = Q8RowDot(dq, dd, hin, r, cols, qstride);
+    if (lane == 0) {
+      float acc = 0.0f;
+      for (std::uint32_t sl = 0; sl < slots; ++sl)
+        acc = __builtin_fmaf(weights[sl], part[static_cast<std::size_t>(sl) * rows + r], acc);
+      out[r] = acc + s * y;
+    }
+  }
+}
+}  // namespace halo::refk
+
+// grid (ceil(rows / 16)), block 256.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_shexp_gate_up(const std::int8_t* gq, const std::uint16_t* gd, const std::int8_t* uq, const std::uint16_t* ud,
+                       const float* gate_inp, const float* x, float* h, float* sgate, std::uint32_t rows,
+                       std::uint32_t cols, std::uint32_t qstride) {
+  __shared__ float red[16];
+  ShexpGateUp(gq, gd, uq, ud, gate_inp, x, h, sgate, rows, cols, qstride, red);
+}
+extern "C" __global__ void __launch_bounds__(256)
+    halo_shexp_gate_up_u(const std::int8_t* gq, const std::uint16_t* gd, const std::int8_t* uq,
+                         const std::uint16_t* ud, const float* gate_inp, const float* x, float* h, float* sgate,
+                         std::uint32_t rows, std::uint32_t cols, std::uint32_t qstride) {
+  __shared__ float red[16];
+  ShexpGateUp(gq, gd, uq, ud, gate_inp, x, h, sgate, rows, cols, qstride, red);
+}
+// grid (ceil(rows / 32)), block 256; _u: slots <= 32.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_shexp_down_combine(const std::int8_t* dq, const std::uint16_t* dd, const float* hin, const float* sgate,
+                            const float* part, const float* weights, std::uint32_t slots, float* out,
+                            std::uint32_t rows, std::uint32_t cols, std::uint32_t qstride) {
+  ShexpDownCombine(dq, dd, hin, sgate, part, weights, slots, out, rows, cols, qstride);
+}
+extern "C" __global__ void __launch_bounds__(256)
+    halo_shexp_down_combine_u(const std::int8_t* dq, const std::uint16_t* dd, const float* hin, const float* sgate,
+                              const float* part, const float* weights, std::uint32_t slots, float* out,
+                              std::uint32_t rows, std::uint32_t cols, std::uint32_t qstride) {
+  ShexpDownCombine(dq, dd, hin, sgate, part, weights, slots, out, rows, cols, qstride);
+}
+
+// Router logits y[r] = w_r . x (block r < rows) and, in blocks b < cols / 32, the Q8 activation record of x's 32-value
+// block b (act: int8 q [4096] packed four to a word, fp32 scale [128] = amax / 127, fp32 sum [128] by the xor
+// butterfly 16, 8, 4, 2, 1; cols <= 4096). grid (max(rows, cols / 32)), block 256.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_router_rowblock_q8act(const float* w, const float* x, float* y, std::uint32_t rows, std::uint32_t cols,
+                               void* act) {
+  __shared__ float red[16];
+  std::uint32_t* aq = static_cast<std::uint32_t*>(act);
+  float* ascale = reinterpret_cast<float*>(aq + 1024);
+  float* asum = ascale + 128;
+  if (blockIdx.x < cols / 32 && threadIdx.x < 32) {
+    const std::uint32_t lane = threadIdx.x, blk = blockIdx.x;
+    const float v = x[blk * 32 + lane];
+    float amax = fabsf(v), sum = v;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) {
+      amax = fmaxf(amax, __shfl_xor(amax, o, 32));
+      sum += __shfl_xor(sum, o, 32);
+    }
+    const float scale = amax / 127.0f;
+    const int qv = scale > 0.0f ? static_cast<int>(rintf(v / scale)) : 0;
+    std::uint32_t word = (static_cast<std::uint32_t>(qv) & 0xFFu) << (8 * (lane & 3));
+    word |= __shfl_xor(word, 1, 32);
+    word |= __shfl_xor(word, 2, 32);
+    if ((lane & 3) == 0) aq[blk * 8 + lane / 4] = word;
+    if (lane == 0) {
+      ascale[blk] = scale;
+      asum[blk] = sum;
+    }
+  }
+  const std::uint32_t r = blockIdx.x;
+  if (r >= rows) return;
+  const float acc = RowDot(w + static_cast<std::size_t>(r) * cols, x, cols, red);
+  if (threadIdx.x == 0) y[r] = acc;
 }

@@ -40,6 +40,18 @@
  *     halo_matvec_f32_rowblock2{,_u}(wa, wb, x, ya, yb, rows, cols)     grid (2 rows)
  *     halo_quantize_q8_kblocked(x, xq, xd, cols, tokens)                grid (T): xq [cols/64][T][64], xd [cols/32][T]
  *     halo_router_topk_w(logits, ids, weights, n, k)                    1 block of 256; n <= 1024, k <= 16
+ *   reference-named select attention, DeltaNet prefill and shared-expert kernels (core.hip:783-918, 3480-3662,
+ *   9196-9343, 9418-9446, 9590-9636), same parameters and grids:
+ *     halo_attention_select{,_b}(q, kc, vc, gate, visible, out, scores, params, num_heads, num_kv_heads, hd, max_n)
+ *       n = params[5], rows visible[0 .. n)                            grid (heads); _rows: grid (heads, T)
+ *     halo_gdn_step_d128_norm_r(...)  as halo_gdn_step_d128_norm        grid (v heads), block 128
+ *     halo_gdn_prefill_d128_norm(..., tokens, qk_stride, v_stride, zo_stride)   grid (v heads), block 128
+ *     halo_conv_l2norm_prefill(in, state, w, out, channels, kern, l2_channels, eps)   grid (heads, T), block d
+ *     halo_conv_state_advance(in, state, channels, kern, tokens)        grid ceil(channels / 256)
+ *     halo_shexp_gate_up{,_u}(gq, gd, uq, ud, gate_inp, x, h, sgate, rows, cols, qstride)   grid ceil(rows / 16)
+ *     halo_shexp_down_combine{,_u}(dq, dd, hin, sgate, part, weights, slots, out, rows, cols, qstride)
+ *                                                                       grid ceil(rows / 32)
+ *     halo_router_rowblock_q8act(w, x, y, rows, cols, act)              grid max(rows, cols / 32)
  *   halo_synth_q8(qs, d, rows, cols, qstride, u64 seed, f32 sigma), halo_synth_f32(x, u64 n, u64 seed, f32 sigma)
  *                                                                                              new (synthetic data)
  */
@@ -65,6 +77,10 @@
   X(halo_moe_down_q8r) X(halo_moe_down_q8r_r4) X(halo_moe_combine) X(halo_moe_combine_u)                      \
   X(halo_matvec_f32_rowblock) X(halo_matvec_f32_rowblock_u) X(halo_matvec_f32_rowblock2)                     \
   X(halo_matvec_f32_rowblock2_u) X(halo_quantize_q8_kblocked) X(halo_router_topk_w)                          \
+  X(halo_attention_select) X(halo_attention_select_b) X(halo_attention_select_rows)                           \
+  X(halo_gdn_step_d128_norm_r) X(halo_gdn_prefill_d128_norm) X(halo_conv_l2norm_prefill)                      \
+  X(halo_conv_state_advance) X(halo_shexp_gate_up) X(halo_shexp_gate_up_u) X(halo_shexp_down_combine)         \
+  X(halo_shexp_down_combine_u) X(halo_router_rowblock_q8act)                                                  \
   X(halo_synth_q8) X(halo_synth_f32)
 
 #endif /* HALO_KERNELS_H_ */

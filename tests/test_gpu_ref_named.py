@@ -333,3 +333,155 @@ def test_router_topk_w(dev):
         O.oracle().or_route_topk(logits, n, k, wi, ww)
         assert np.array_equal(outs[0][0], wi) and outs[0][1].tobytes() == outs[1][1].tobytes()
         np.testing.assert_allclose(outs[0][1], ww, rtol=1e-5)
+
+
+# ---- select attention, DeltaNet prefill helpers, shared expert, router with activation record ------------------
+# (core.hip:783-918, 3480-3662, 9196-9343, 9418-9446, 9590-9636.) Chunked kernels are checked bit for bit against
+# stepping with the decode kernels (the reference's contract for them); the rest against the oracle as above.
+
+@pytest.mark.parametrize("kernel", ["halo_attention_select", "halo_attention_select_b", "halo_attention_select_rows"])
+def test_attention_select(dev, kernel):
+    rng = np.random.default_rng(47)
+    Hq, Hkv, hd, npos, max_n = 8, 2, 256, 400, 256
+    kc = rng.normal(0, 1, (npos, Hkv, hd)).astype(np.float32)
+    vc = rng.normal(0, 1, (npos, Hkv, hd)).astype(np.float32)
+    T = 2 if kernel.endswith("rows") else 1
+    ns = [150, 1][:T] if T == 2 else [203]
+    vis = np.zeros((T, max_n), np.uint32)
+    params = np.zeros((T, 16), np.uint32)
+    for t, n in enumerate(ns):
+        vis[t, :n] = rng.choice(npos, n, replace=False)
+        params[t, 5] = n
+    q = rng.normal(0, 1, (T, Hq, hd)).astype(np.float32)
+    gate = rng.normal(0, 1, (T, Hq, hd)).astype(np.float32)
+    go, sc = dev.array((T, Hq, hd), np.float32), dev.array((T, Hq, max_n), np.float32)
+    args = [dev.to_device(q), dev.to_device(kc), dev.to_device(vc), dev.to_device(gate), dev.to_device(vis), go, sc,
+            dev.to_device(params), ("u32", Hq), ("u32", Hkv), ("u32", hd), ("u32", max_n)]
+    dev.launch(kernel, (Hq, T) if T > 1 else (Hq,), (256,), args)
+    got = go.download()
+    for t, n in enumerate(ns):
+        for h in range(Hq):
+            kvh = h // (Hq // Hkv)
+            rows = vis[t, :n].astype(np.int64)
+            want = np.empty(hd, np.float32)
+            O.oracle().or_attention_head(q[t, h].copy(), np.ascontiguousarray(kc[rows, kvh]),
+                                         np.ascontiguousarray(vc[rows, kvh]), n, hd, hd, want)
+            want = want * sig(gate[t, h])
+            close(got[t, h], want, np.abs(vc[rows, kvh]).max(0) + 1e-3)
+
+
+def test_gdn_step_norm_r_and_prefill_equal_stepping(dev):
+    """T single steps of halo_gdn_step_d128_norm against one chunked halo_gdn_prefill_d128_norm launch over padded
+    rows (per-head a and dt shared by the chunk), and the _r name against the first step: bit for bit."""
+    rng = np.random.default_rng(48)
+    Hv, Hk, d, T = 8, 4, 128, 5
+    w = rng.normal(1, 0.1, d).astype(np.float32)
+    toks = [gdn_inputs(rng, Hv, Hk, d) for _ in range(T)]
+    S0, a, dt = toks[0][7], toks[0][5], toks[0][6]
+    z = rng.normal(0, 1, (T, Hv, d)).astype(np.float32)
+    gw, ga, gdt = dev.to_device(w), dev.to_device(a), dev.to_device(dt)
+    tail = lambda t, gs, go: [gs, gw, dev.to_device(z[t]), go, ("u32", Hk), ("f32", 1e-6), ("u32", 0)]
+    gs, outs = dev.to_device(S0), []
+    for t in range(T):
+        ins = [dev.to_device(x) for x in toks[t][:5]] + [ga, gdt]
+        if t == 0:
+            gs_r, go_r = dev.to_device(S0), dev.array((Hv, d), np.float32)
+            dev.launch("halo_gdn_step_d128_norm_r", (Hv,), (128,), ins + tail(t, gs_r, go_r))
+        go = dev.array((Hv, d), np.float32)
+        dev.launch("halo_gdn_step_d128_norm", (Hv,), (128,), ins + tail(t, gs, go))
+        outs.append(go.download())
+        if t == 0:
+            assert go_r.download().tobytes() == outs[0].tobytes()
+            assert gs_r.download().tobytes() == gs.download().tobytes()
+    # rows padded: q, k rows Hk d + 64 apart, v rows Hv d + 32, z and out rows Hv d + 128
+    qs_, vs_, zs_ = Hk * d + 64, Hv * d + 32, Hv * d + 128
+    qb, kb = np.zeros((T, qs_), np.float32), np.zeros((T, qs_), np.float32)
+    vb, zb = np.zeros((T, vs_), np.float32), np.zeros((T, zs_), np.float32)
+    al, be = np.stack([x[3] for x in toks]), np.stack([x[4] for x in toks])
+    for t in range(T):
+        qb[t, :Hk * d], kb[t, :Hk * d] = toks[t][0].ravel(), toks[t][1].ravel()
+        vb[t, :Hv * d], zb[t, :Hv * d] = toks[t][2].ravel(), z[t].ravel()
+    gs2, gout = dev.to_device(S0), dev.array((T, zs_), np.float32)
+    dev.launch("halo_gdn_prefill_d128_norm", (Hv,), (128,),
+               [dev.to_device(qb), dev.to_device(kb), dev.to_device(vb), dev.to_device(al), dev.to_device(be), ga,
+                gdt, gs2, gw, dev.to_device(zb), gout, ("u32", Hk), ("f32", 1e-6), ("u32", 0), ("u32", T),
+                ("u32", qs_), ("u32", vs_), ("u32", zs_)])
+    got = gout.download()
+    for t in range(T):
+        assert got[t, :Hv * d].tobytes() == outs[t].ravel().tobytes(), f"token {t}"
+    assert gs2.download().tobytes() == gs.download().tobytes()
+
+
+@pytest.mark.parametrize("T", [6, 2])
+def test_conv_prefill_and_state_advance_equal_stepping(dev, T):
+    rng = np.random.default_rng(49 + T)
+    C, K, d, l2 = 640, 4, 128, 256
+    w = rng.normal(0, 0.5, (C, K)).astype(np.float32)
+    st = rng.normal(0, 1, (K - 1, C)).astype(np.float32)
+    x = rng.normal(0, 1, (T, C)).astype(np.float32)
+    gw, gst = dev.to_device(w), dev.to_device(st)
+    want = []
+    for t in range(T):
+        go = dev.array(C, np.float32)
+        dev.launch("halo_conv_l2norm", (C // d,), (d,), [dev.to_device(x[t]), gst, gw, go, ("u32", C), ("u32", K),
+                                                           ("u32", l2), ("f32", 1e-6)])
+        want.append(go.download())
+    gst2, gx, gout = dev.to_device(st), dev.to_device(x), dev.array((T, C), np.float32)
+    dev.launch("halo_conv_l2norm_prefill", (C // d, T), (d,), [gx, gst2, gw, gout, ("u32", C), ("u32", K),
+                                                                ("u32", l2), ("f32", 1e-6)])
+    assert gout.download().tobytes() == np.stack(want).tobytes()
+    dev.launch("halo_conv_state_advance", ((C + 255) // 256,), (256,), [gx, gst2, ("u32", C), ("u32", K), ("u32", T)])
+    assert gst2.download().tobytes() == gst.download().tobytes()
+
+
+@pytest.mark.parametrize("suffix", ["", "_u"])
+def test_shared_expert(dev, suffix):
+    rng = np.random.default_rng(50)
+    H, F, slots = 2048, 512, 10
+    gq, gd = O.synth_q8(rng, F, H)
+    uq, ud = O.synth_q8(rng, F, H)
+    dq, dd = O.synth_q8(rng, H, F)
+    gate_inp = rng.normal(0, 0.02, H).astype(np.float32)
+    x = rng.normal(0, 1, H).astype(np.float32)
+    h, sg = dev.array((F,), np.float32), dev.array((1,), np.float32)
+    dev.launch("halo_shexp_gate_up" + suffix, ((F + 15) // 16,), (256,),
+               [dev.to_device(gq), dev.to_device(gd), dev.to_device(uq), dev.to_device(ud), dev.to_device(gate_inp),
+                dev.to_device(x), h, sg, ("u32", F), ("u32", H), ("u32", H)])
+    g, gm = _q8_ref(gq, gd, x)
+    u, um = _q8_ref(uq, ud, x)
+    hw = silu(g) * u
+    got_h = h.download()
+    close(got_h, hw, np.abs(silu(g)) * um + np.abs(u) * gm + 1e-6)
+    close(sg.download(), np.array([gate_inp.astype(np.float64) @ x]), np.array([np.abs(gate_inp) @ np.abs(x)]))
+    part = rng.normal(0, 1, (slots, H)).astype(np.float32)
+    wts = rng.random(slots).astype(np.float32)
+    out = dev.array((H,), np.float32)
+    dev.launch("halo_shexp_down_combine" + suffix, ((H + 31) // 32,), (256,),
+               [dev.to_device(dq), dev.to_device(dd), h, sg, dev.to_device(part), dev.to_device(wts), ("u32", slots),
+                out, ("u32", H), ("u32", F), ("u32", F)])
+    y, ym = _q8_ref(dq, dd, got_h)
+    s = sig(sg.download()[0])
+    want = (wts.astype(np.float64)[:, None] * part).sum(0) + s * y
+    close(out.download(), want, (np.abs(wts[:, None] * part)).sum(0) + s * ym + 1e-6)
+
+
+def test_router_rowblock_q8act(dev):
+    rng = np.random.default_rng(51)
+    E, H = 512, 2048
+    w = rng.normal(0, 0.02, (E, H)).astype(np.float32)
+    x = rng.normal(0, 1, H).astype(np.float32)
+    x[64:96] = 0.0
+    y, act = dev.array((E,), np.float32), dev.array((1024 + 256,), np.uint32)
+    dev.launch("halo_router_rowblock_q8act", (max(E, H // 32),), (256,),
+               [dev.to_device(w), dev.to_device(x), y, ("u32", E), ("u32", H), act])
+    want = np.zeros(E, np.float32)
+    O.oracle().or_matvec_f32(w, E, H, x, want)
+    close(y.download(), want, np.abs(w.astype(np.float64)) @ np.abs(x.astype(np.float64)))
+    a = act.download()
+    wq, ws = np.zeros(H, np.int8), np.zeros(H // 32, np.float32)
+    O.oracle().or_quantize_q8_act(x, wq, ws, H)
+    assert np.array_equal(a[:H // 4].view(np.int8), wq)
+    assert a[1024:1024 + H // 32].view(np.float32).tobytes() == ws.tobytes()
+    sums = a[1152:1152 + H // 32].view(np.float32)
+    blocks = x.reshape(-1, 32).astype(np.float64)
+    close(sums, blocks.sum(1), np.abs(blocks).sum(1) + 1e-6, 1e-6)

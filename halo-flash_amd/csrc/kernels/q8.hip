@@ -543,19 +543,24 @@ constexpr int kTileLd = 64 + 16;
 }  // namespace
 
 namespace halo {
-template <int WR, int MT, int WT, int NMAT, bool PAIR = false>
+template <int WR, int MT, int WT, int NMAT, bool PAIR = false, bool KBLK = false>
 __device__ __forceinline__ void GemmTileQ8(const std::int8_t* __restrict__ A0, const std::uint16_t* __restrict__ D0,
                                           const std::int8_t* __restrict__ A1, const std::uint16_t* __restrict__ D1,
                                           std::uint32_t rows, std::uint32_t qstride, std::uint32_t r0,
                                           const std::int8_t* __restrict__ xq, const float* __restrict__ xs,
                                           const std::uint32_t* __restrict__ xrow, std::uint32_t x0, std::uint32_t ntok,
                                           std::uint32_t cols, float* __restrict__ y, std::uint32_t yrow0,
-                                          std::uint32_t ystride) {
-  static_assert(WR * WT == 8, "8 waves");
+                                          std::uint32_t ystride, std::uint32_t xtok = 0) {
+  static_assert(WR * WT == 2 || WR * WT == 4 || WR * WT == 8, "2, 4 or 8 waves");
+  constexpr std::uint32_t NTH = WR * WT * 64;  // the block size
+  // activation layout: token rows [T][cols] int8 + [T][cols / 32] scales, or K-blocked (KBLK) [cols / 64][xtok][64]
+  // int8 + [cols / 32][xtok] scales (halo_quantize_q8_kblocked)
+  const std::size_t xstage = KBLK ? 64 * static_cast<std::size_t>(xtok) : 64;
+  const std::size_t sstage = KBLK ? 2 * static_cast<std::size_t>(xtok) : 2;
   constexpr int ROWS = WR * MT * 32, TOKS = WT * 32;
   constexpr int NA = NMAT * ROWS * 4, NB = TOKS * 4;  // 16-byte chunks per stage
   constexpr int NDW = NMAT * ROWS * 2, NSX = TOKS * 2;  // scales per stage
-  constexpr int LA = (NA + 511) / 512, LB = (NB + 511) / 512, LS = (NDW + NSX + 511) / 512;
+  constexpr int LA = (NA + NTH - 1) / NTH, LB = (NB + NTH - 1) / NTH, LS = (NDW + NSX + NTH - 1) / NTH;
   __shared__ __attribute__((aligned(16))) std::int8_t la[2][NMAT][ROWS][kTileLd];
   __shared__ __attribute__((aligned(16))) std::int8_t lb[2][TOKS][kTileLd];
   __shared__ __attribute__((aligned(16))) float ldw[2][NMAT][2][ROWS];
@@ -573,7 +578,7 @@ __device__ __forceinline__ void GemmTileQ8(const std::int8_t* __restrict__ A0, c
   bool aon[LA];
 #pragma unroll
   for (int i = 0; i < LA; ++i) {
-    const std::uint32_t c = tid + 512u * i, cc = min(c, static_cast<std::uint32_t>(NA - 1));
+    const std::uint32_t c = tid + NTH * i, cc = min(c, static_cast<std::uint32_t>(NA - 1));
     aon[i] = c < static_cast<std::uint32_t>(NA);
     amat[i] = cc / (ROWS * 4);
     arow[i] = (cc / 4) % ROWS;
@@ -585,11 +590,11 @@ __device__ __forceinline__ void GemmTileQ8(const std::int8_t* __restrict__ A0, c
   bool bon[LB];
 #pragma unroll
   for (int i = 0; i < LB; ++i) {
-    const std::uint32_t c = tid + 512u * i, cc = min(c, static_cast<std::uint32_t>(NB - 1));
+    const std::uint32_t c = tid + NTH * i, cc = min(c, static_cast<std::uint32_t>(NB - 1));
     bon[i] = c < static_cast<std::uint32_t>(NB);
     brow[i] = cc / 4;
     bpart[i] = cc % 4;
-    gb[i] = xq + static_cast<std::size_t>(tokrow(brow[i])) * cols + bpart[i] * 16;
+    gb[i] = xq + static_cast<std::size_t>(tokrow(brow[i])) * (KBLK ? 64 : cols) + bpart[i] * 16;
   }
   // scales: index c < NDW is (mat, row, blk) of a weight scale, the rest (token, blk) of an activation scale
   const std::uint16_t* gd[LS];
@@ -597,14 +602,15 @@ __device__ __forceinline__ void GemmTileQ8(const std::int8_t* __restrict__ A0, c
   std::uint32_t sidx[LS];
 #pragma unroll
   for (int i = 0; i < LS; ++i) {
-    const std::uint32_t c = min(tid + 512u * i, static_cast<std::uint32_t>(NDW + NSX - 1));
+    const std::uint32_t c = min(tid + NTH * i, static_cast<std::uint32_t>(NDW + NSX - 1));
     sidx[i] = c;
     const std::uint32_t cw = min(c, static_cast<std::uint32_t>(NDW - 1)), cs = c < NDW ? 0u : c - NDW;
     const std::uint32_t m = cw / (ROWS * 2), rr = (cw / 2) % ROWS;
     gd[i] = (m ? D1 : D0) + static_cast<std::size_t>(min(r0 + rr, rows - 1)) * nblk + cw % 2;
-    gs[i] = xs + static_cast<std::size_t>(tokrow(cs / 2)) * nblk + cs % 2;
+    gs[i] = KBLK ? xs + static_cast<std::size_t>(cs % 2) * xtok + tokrow(cs / 2)
+                 : xs + static_cast<std::size_t>(tokrow(cs / 2)) * nblk + cs % 2;
   }
-  const bool son_last = tid + 512u * (LS - 1) < static_cast<std::uint32_t>(NDW + NSX);
+  const bool son_last = tid + NTH * (LS - 1) < static_cast<std::uint32_t>(NDW + NSX);
   struct Staged {
     int4 a[LA], b[LB];
     float sc[LS];
@@ -614,10 +620,10 @@ __device__ __forceinline__ void GemmTileQ8(const std::int8_t* __restrict__ A0, c
     for (int i = 0; i < LA; ++i)
       r.a[i] = __builtin_bit_cast(int4, __builtin_nontemporal_load(reinterpret_cast<const V4i*>(ga[i] + kc * 64)));
 #pragma unroll
-    for (int i = 0; i < LB; ++i) r.b[i] = *reinterpret_cast<const int4*>(gb[i] + kc * 64);
+    for (int i = 0; i < LB; ++i) r.b[i] = *reinterpret_cast<const int4*>(gb[i] + kc * xstage);
 #pragma unroll
     for (int i = 0; i < LS; ++i) {
-      const float dv = F16(gd[i][kc * 2]), sv = gs[i][kc * 2];  // both loaded (clamped addresses), one kept
+      const float dv = F16(gd[i][kc * 2]), sv = gs[i][kc * sstage];  // both loaded (clamped addresses), one kept
       r.sc[i] = sidx[i] < static_cast<std::uint32_t>(NDW) ? dv : sv;
     }
   };

@@ -745,3 +745,29 @@ extern "C" __global__ void __launch_bounds__(256)
   const float acc = RowDot(w + static_cast<std::size_t>(r) * cols, x, cols, red);
   if (threadIdx.x == 0) y[r] = acc;
 }
+
+// ---- prefill int8 GEMMs (reference names) ---------------------------------------------------------------------
+// core.hip:3103-3153, 3303-3311, 3466-3476: y[t][r] = sum over Q8_0 blocks of the exact int32 block product scaled by
+// d_w[r] s_x[t] (y [T][rows], ystride = rows), on the LDS-tiled int8 MFMA template. The _wmma kernels read
+// activations as halo_quantize_q8_rows writes them (xq [T][cols], xd [T][cols / 32]); the q8a8 kernels read the
+// K-blocked layout of halo_quantize_q8_kblocked (xq [cols / 64][T][64], xd [cols / 32][T]). Grids as the reference
+// launches them: (ceil(T / BN), ceil(rows / BM)). Every tile here is a whole number of 32 x 32 MFMA tiles, so
+// cols % 64 == 0 (every matrix of the model; the reference itself needs cols % 32 == 0 for _wmma).
+#define HALO_REF_GEMM(NAME, BLOCK, BM, BN, WR, MT, WT, KB)                                                      \
+  extern "C" __global__ void __launch_bounds__(BLOCK)                                                          \
+      NAME(const std::int8_t* qs, const std::uint16_t* d, const std::int8_t* xq, const float* xd, float* y,   \
+           std::uint32_t rows, std::uint32_t cols, std::uint32_t qstride, std::uint32_t tokens) {             \
+    if (threadIdx.x >= WR * WT * 64) return; /* tiles that need fewer waves than the reference's block */      \
+    const std::uint32_t t0 = blockIdx.x * BN;                                                                  \
+    halo::GemmTileQ8<WR, MT, WT, 1, false, KB>(qs, d, nullptr, nullptr, rows, qstride, blockIdx.y * BM, xq, xd, \
+                                               nullptr, t0, min(static_cast<std::uint32_t>(BN), tokens - t0),  \
+                                               cols, y, t0, rows, tokens);                                    \
+  }
+HALO_REF_GEMM(halo_gemm_q8r_wmma, 128, 64, 64, 1, 2, 2, false)
+HALO_REF_GEMM(halo_gemm_q8r_wmma_t, 256, 128, 128, 1, 4, 4, false)
+HALO_REF_GEMM(halo_gemm_q8a8_128x128, 256, 128, 128, 1, 4, 4, true)
+HALO_REF_GEMM(halo_gemm_q8a8_128x64, 256, 128, 64, 2, 2, 2, true)
+HALO_REF_GEMM(halo_gemm_q8a8_320x64, 256, 320, 64, 2, 5, 2, true)
+HALO_REF_GEMM(halo_gemm_q8a8_160x64, 256, 160, 64, 1, 5, 2, true)
+HALO_REF_GEMM(halo_gemm_q8a8_256x128, 256, 256, 128, 1, 8, 4, true)
+#undef HALO_REF_GEMM

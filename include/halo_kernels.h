@@ -52,6 +52,11 @@
  *     halo_shexp_down_combine{,_u}(dq, dd, hin, sgate, part, weights, slots, out, rows, cols, qstride)
  *                                                                       grid ceil(rows / 32)
  *     halo_router_rowblock_q8act(w, x, y, rows, cols, act)              grid max(rows, cols / 32)
+ *   reference-named prefill int8 GEMMs (core.hip:3103-3153, 3303-3311, 3466-3476), y [T][rows]; cols % 64 == 0:
+ *     halo_gemm_q8r_wmma / _wmma_t(qs, d, xq, xd, y, rows, cols, qstride, tokens)   x as halo_quantize_q8_rows
+ *       grid (ceil(T / 64), ceil(rows / 64)), block 128 / (ceil(T / 128), ceil(rows / 128)), block 256
+ *     halo_gemm_q8a8_{128x128, 128x64, 320x64, 160x64, 256x128}(same)    x K-blocked (halo_quantize_q8_kblocked)
+ *       grid (ceil(T / BN), ceil(rows / BM)), block 256
  *   halo_synth_q8(qs, d, rows, cols, qstride, u64 seed, f32 sigma), halo_synth_f32(x, u64 n, u64 seed, f32 sigma)
  *                                                                                              new (synthetic data)
  */
@@ -81,6 +86,8 @@
   X(halo_gdn_step_d128_norm_r) X(halo_gdn_prefill_d128_norm) X(halo_conv_l2norm_prefill)                      \
   X(halo_conv_state_advance) X(halo_shexp_gate_up) X(halo_shexp_gate_up_u) X(halo_shexp_down_combine)         \
   X(halo_shexp_down_combine_u) X(halo_router_rowblock_q8act)                                                  \
+  X(halo_gemm_q8r_wmma) X(halo_gemm_q8r_wmma_t) X(halo_gemm_q8a8_128x128) X(halo_gemm_q8a8_128x64)           \
+  X(halo_gemm_q8a8_320x64) X(halo_gemm_q8a8_160x64) X(halo_gemm_q8a8_256x128)                                 \
   X(halo_synth_q8) X(halo_synth_f32)
 
 #endif /* HALO_KERNELS_H_ */

@@ -485,3 +485,33 @@ def test_router_rowblock_q8act(dev):
     sums = a[1152:1152 + H // 32].view(np.float32)
     blocks = x.reshape(-1, 32).astype(np.float64)
     close(sums, blocks.sum(1), np.abs(blocks).sum(1) + 1e-6, 1e-6)
+
+
+# ---- reference-named prefill int8 GEMMs (core.hip:3103-3153, 3303-3311, 3466-3476) -> or_gemv_q8a8 per token,
+# the bar of the other Q8 GEMMs (1e-5 of sum |term| + 1e-6). Shapes with ragged row and token tiles.
+@pytest.mark.parametrize("name,block,bm,bn,kblocked", [
+    ("halo_gemm_q8r_wmma", 128, 64, 64, False), ("halo_gemm_q8r_wmma_t", 256, 128, 128, False),
+    ("halo_gemm_q8a8_128x128", 256, 128, 128, True), ("halo_gemm_q8a8_128x64", 256, 128, 64, True),
+    ("halo_gemm_q8a8_320x64", 256, 320, 64, True), ("halo_gemm_q8a8_160x64", 256, 160, 64, True),
+    ("halo_gemm_q8a8_256x128", 256, 256, 128, True)])
+def test_reference_prefill_gemms(dev, name, block, bm, bn, kblocked):
+    rng = np.random.default_rng(52)
+    rows, cols, T = 700, 1024, 200
+    qs, d = O.synth_q8(rng, rows, cols)
+    x = rng.normal(0, 1, (T, cols)).astype(np.float32)
+    xq, xs = np.zeros((T, cols), np.int8), np.zeros((T, cols // 32), np.float32)
+    for t in range(T):
+        O.oracle().or_quantize_q8_act(x[t], xq[t], xs[t], cols)
+    want, mag = O.gemv_q8a8(qs, d, xq, xs)
+    if kblocked:
+        gxq = dev.to_device(np.ascontiguousarray(xq.reshape(T, cols // 64, 64).transpose(1, 0, 2)))
+        gxs = dev.to_device(np.ascontiguousarray(xs.T))
+    else:
+        gxq, gxs = dev.to_device(xq), dev.to_device(xs)
+    gy = dev.array((T, rows), np.float32)
+    dev.launch(name, ((T + bn - 1) // bn, (rows + bm - 1) // bm), (block,),
+               [dev.to_device(qs), dev.to_device(d), gxq, gxs, gy, ("u32", rows), ("u32", cols), ("u32", cols),
+                ("u32", T)])
+    got = gy.download()
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    assert np.all(err <= 1e-5 * mag + 1e-6), f"worst {np.max(err - 1e-5 * mag - 1e-6)}"

@@ -218,6 +218,35 @@ __device__ __forceinline__ void GemvQ8rI8B(const std::int8_t* qs, const std::uin
   StoreRows<32, R, NB, kResid>(y, ystride, base, rows, out);
 }
 
+// Two matrices with the same NB columns in one launch (reference batch_decode.hip:310-345): row blocks
+// [0, blocks1) take matrix 1, the rest matrix 2; blockIdx.x = row block * groups + column group; no split-K.
+template <int R, int NB, bool kResid>
+__device__ __forceinline__ void GemvQ8rI8Dual(const std::int8_t* q1, const std::uint16_t* d1, float* y1,
+                                              std::uint32_t rows1, std::uint32_t qstride1, const std::int8_t* q2,
+                                              const std::uint16_t* d2, float* y2, std::uint32_t rows2,
+                                              std::uint32_t qstride2, const std::int8_t* xq, const float* xs,
+                                              const std::int8_t* xq2, const float* xs2, std::uint32_t cols,
+                                              std::uint32_t blocks1, std::uint32_t ystride1, std::uint32_t ystride2,
+                                              std::uint32_t groups) {
+  const std::uint32_t bxg = blockIdx.x / groups, g = blockIdx.x % groups;
+  xq += static_cast<std::size_t>(g) * NB * cols;
+  xs += static_cast<std::size_t>(g) * NB * (cols / 32);
+  if constexpr (kResid) {
+    xq2 += static_cast<std::size_t>(g) * NB * cols;
+    xs2 += static_cast<std::size_t>(g) * NB * (cols / 32);
+  }
+  const bool first = bxg < blocks1;
+  const std::uint32_t bx = first ? bxg : bxg - blocks1, rows = first ? rows1 : rows2;
+  const std::uint32_t ystride = first ? ystride1 : ystride2;
+  float* y = (first ? y1 : y2) + static_cast<std::size_t>(g) * NB * ystride;
+  const std::uint32_t base = (bx * (blockDim.x / kWave) + threadIdx.x / kWave) * (2 * R);
+  if (base >= rows) return;
+  float out[NB][R];
+  Q8A8Rows<32, R, NB, kResid>(first ? q1 : q2, first ? d1 : d2, xq, xs, xq2, xs2, base, rows, cols,
+                              first ? qstride1 : qstride2, 0, cols, out);
+  StoreRows<32, R, NB, kResid>(y, ystride, base, rows, out);
+}
+
 }  // namespace
 
 #define HALO_GEMV_I8_REF(NB, R, SUF, RES)                                                                        \
@@ -227,9 +256,21 @@ __device__ __forceinline__ void GemvQ8rI8B(const std::int8_t* qs, const std::uin
       std::uint32_t qstride, std::uint32_t ystride, std::uint32_t groups, std::uint32_t chunk) {                \
     GemvQ8rI8B<R, NB, RES>(qs, d, xq, xs, xq2, xs2, y, rows, cols, qstride, ystride, groups, chunk);            \
   }
+#define HALO_GEMV_I8_DUAL_REF(NB, R, SUF, RES)                                                                   \
+  extern "C" __global__ void __launch_bounds__(256) halo_gemv_q8r_i8##SUF##_dual_r##R##_b##NB(                  \
+      const std::int8_t* q1, const std::uint16_t* d1, float* y1, std::uint32_t rows1, std::uint32_t qstride1,   \
+      const std::int8_t* q2, const std::uint16_t* d2, float* y2, std::uint32_t rows2, std::uint32_t qstride2,   \
+      const std::int8_t* xq, const float* xs, const std::int8_t* xq2, const float* xs2, std::uint32_t cols,     \
+      std::uint32_t blocks1, std::uint32_t ystride1, std::uint32_t ystride2, std::uint32_t groups) {            \
+    GemvQ8rI8Dual<R, NB, RES>(q1, d1, y1, rows1, qstride1, q2, d2, y2, rows2, qstride2, xq, xs, xq2, xs2, cols,  \
+                              blocks1, ystride1, ystride2, groups);                                              \
+  }
 #define HALO_GEMV_I8_REF_NB(NB)                                                                                   \
   HALO_GEMV_I8_REF(NB, 1, , false) HALO_GEMV_I8_REF(NB, 2, , false) HALO_GEMV_I8_REF(NB, 4, , false)             \
-  HALO_GEMV_I8_REF(NB, 1, x, true) HALO_GEMV_I8_REF(NB, 2, x, true) HALO_GEMV_I8_REF(NB, 4, x, true)
+  HALO_GEMV_I8_REF(NB, 1, x, true) HALO_GEMV_I8_REF(NB, 2, x, true) HALO_GEMV_I8_REF(NB, 4, x, true)             \
+  HALO_GEMV_I8_DUAL_REF(NB, 1, , false) HALO_GEMV_I8_DUAL_REF(NB, 2, , false)                                    \
+  HALO_GEMV_I8_DUAL_REF(NB, 4, , false) HALO_GEMV_I8_DUAL_REF(NB, 1, x, true)                                    \
+  HALO_GEMV_I8_DUAL_REF(NB, 2, x, true) HALO_GEMV_I8_DUAL_REF(NB, 4, x, true)
 HALO_GEMV_I8_REF_NB(1)
 HALO_GEMV_I8_REF_NB(2)
 HALO_GEMV_I8_REF_NB(3)
@@ -239,6 +280,7 @@ HALO_GEMV_I8_REF_NB(6)
 HALO_GEMV_I8_REF_NB(7)
 HALO_GEMV_I8_REF_NB(8)
 #undef HALO_GEMV_I8_REF_NB
+#undef HALO_GEMV_I8_DUAL_REF
 #undef HALO_GEMV_I8_REF
 
 // MI355X-native int8-activation GEMV (new name, no reference counterpart): blockDim.x / 64 waves per block, each
@@ -297,12 +339,13 @@ extern "C" __global__ void __launch_bounds__(256)
 // reference src/kernels/core.hip:2147-2188, 2388-2443: y[r] = sum_b F16(d) * sum_i q * x with fp32 x. Wave64: a
 // 256-thread block covers the reference's rows per block (8 * R); x is read through the vector cache.
 namespace {
+// Row block bx of 8 R rows (4 waves x 2 rows per pass x R).
 template <int R>
-__device__ __forceinline__ void GemvQ8rF32(const std::int8_t* __restrict__ qs, const std::uint16_t* __restrict__ d,
-                                           const float* __restrict__ x, float* __restrict__ y, std::uint32_t rows,
-                                           std::uint32_t cols, std::uint32_t qstride) {
+__device__ __forceinline__ void GemvQ8rF32At(const std::int8_t* __restrict__ qs, const std::uint16_t* __restrict__ d,
+                                             const float* __restrict__ x, float* __restrict__ y, std::uint32_t rows,
+                                             std::uint32_t cols, std::uint32_t qstride, std::uint32_t bx) {
   constexpr int LPR = 32, P = 2;
-  const std::uint32_t base = (blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave) * (P * R);
+  const std::uint32_t base = (bx * (blockDim.x / kWave) + threadIdx.x / kWave) * (P * R);
   if (base >= rows) return;
   const std::uint32_t lane = threadIdx.x % kWave, nblk = cols / 32, sub = lane / LPR;
   float acc[R];
@@ -337,6 +380,12 @@ __device__ __forceinline__ void GemvQ8rF32(const std::int8_t* __restrict__ qs, c
     const std::uint32_t r = base + k * P + sub;
     if (lane % LPR == 0 && r < rows) y[r] = a;
   }
+}
+template <int R>
+__device__ __forceinline__ void GemvQ8rF32(const std::int8_t* __restrict__ qs, const std::uint16_t* __restrict__ d,
+                                           const float* __restrict__ x, float* __restrict__ y, std::uint32_t rows,
+                                           std::uint32_t cols, std::uint32_t qstride) {
+  GemvQ8rF32At<R>(qs, d, x, y, rows, cols, qstride, blockIdx.x);
 }
 }  // namespace
 

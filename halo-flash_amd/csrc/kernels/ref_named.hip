@@ -771,3 +771,16 @@ HALO_REF_GEMM(halo_gemm_q8a8_320x64, 256, 320, 64, 2, 5, 2, true)
 HALO_REF_GEMM(halo_gemm_q8a8_160x64, 256, 160, 64, 1, 5, 2, true)
 HALO_REF_GEMM(halo_gemm_q8a8_256x128, 256, 256, 128, 1, 8, 4, true)
 #undef HALO_REF_GEMM
+
+// Two Q8_0 matrices with the same fp32 input in one launch (core.hip:2960-2985, DeltaNet qkv and z): row blocks
+// [0, blocks1) take matrix 1, the rest matrix 2; 32 rows per block of 256. x is read through the vector cache (no
+// column limit).
+extern "C" __global__ void __launch_bounds__(256)
+    halo_gemv_q8r_dual(const std::int8_t* q1, const std::uint16_t* d1, float* y1, std::uint32_t rows1,
+                       std::uint32_t qstride1, const std::int8_t* q2, const std::uint16_t* d2, float* y2,
+                       std::uint32_t rows2, std::uint32_t qstride2, const float* x, std::uint32_t cols,
+                       std::uint32_t blocks1) {
+  const bool first = blockIdx.x < blocks1;
+  GemvQ8rF32At<4>(first ? q1 : q2, first ? d1 : d2, x, first ? y1 : y2, first ? rows1 : rows2, cols,
+                  first ? qstride1 : qstride2, first ? blockIdx.x : blockIdx.x - blocks1);
+}

@@ -12,6 +12,10 @@
  *                                                       grid ceil(rows / (8 R))              core.hip:2175,2429
  *   halo_gemv_q8r_i8{,x}_r{1,2,4}_b{1..8}(qs, d, xq, xs, xq2, xs2, y, rows, cols, qstride, ystride, groups, chunk)
  *                                                       grid (ceil(rows/(8R)) * groups, parts) batch_decode.hip:301
+ *   halo_gemv_q8r_i8{,x}_dual_r{1,2,4}_b{1..8}(q1, d1, y1, rows1, qstride1, q2, d2, y2, rows2, qstride2, xq, xs, xq2,
+ *     xs2, cols, blocks1, ystride1, ystride2, groups)   grid ((blocks1 + blocks2) * groups)   batch_decode.hip:310
+ *   halo_gemv_q8r_dual(q1, d1, y1, rows1, qstride1, q2, d2, y2, rows2, qstride2, x, cols, blocks1)
+ *                                                       grid (blocks1 + ceil(rows2 / 32))    core.hip:2960
  *   halo_gemv_q8a8_l{16,32,64}_r{1,2,4}_b{1,2,4,8}(qs, d, xq, xs, y, rows, cols, qstride, ystride)   new (MI355X)
  *   halo_q8_half_dots(qs, xq, i32* isum, rows, cols, qstride)                                  new (parity)
  *   reference-named decode kernels (core.hip:259-586, 2621, 3003-3063), same parameters and grids:
@@ -71,6 +75,7 @@
   X(halo_gemv_q8r) X(halo_gemv_q8r_r2) X(halo_gemv_q8r_r4)                                                   \
   X(halo_gemv_q8r_i8_r1_b1) X(halo_gemv_q8r_i8_r2_b1) X(halo_gemv_q8r_i8_r4_b1)                              \
   X(halo_gemv_q8r_i8_r4_b4) X(halo_gemv_q8r_i8x_r4_b4) X(halo_gemv_q8r_i8_r4_b8)                             \
+  X(halo_gemv_q8r_i8_dual_r4_b1) X(halo_gemv_q8r_i8x_dual_r4_b4) X(halo_gemv_q8r_dual)                        \
   X(halo_gemv_q8a8_l64_r1_b1) X(halo_gemv_q8a8_l32_r1_b1) X(halo_gemv_q8a8_l16_r1_b1)                        \
   X(halo_gemv_q8a8_l64_r2_b4) X(halo_gemv_q8a8_l64_r2_b8)                                                    \
   X(halo_q8_half_dots)                                                                                       \

@@ -211,3 +211,44 @@ def test_mfma_gemm_prefill_tiles(dev, m, rows, cols):
     gy = dev.array((m, rows), np.float32)
     dev.op("matvec_q8a8", C_ref(w), gq.ptr, gs.ptr, gy.ptr, m, rows)
     _check_y(gy.download(), want, mag)
+
+
+@pytest.mark.parametrize("nb,r", [(1, 4), (3, 2), (8, 1)])
+def test_reference_named_i8_dual_kernels(dev, nb, r):
+    """halo_gemv_q8r_i8_dual_r{R}_b{NB}: two matrices (DeltaNet qkv and z) over the same NB columns in one launch,
+    row blocks [0, blocks1) on the first, two column groups (batch_decode.hip:310-345)."""
+    rng = np.random.default_rng(nb * 100 + r)
+    rows1, rows2, cols, groups = 300, 130, 2048, 2
+    qs1, d1, w1 = _weights(dev, rng, rows1, cols)
+    qs2, d2, w2 = _weights(dev, rng, rows2, cols)
+    x = rng.normal(0, 1, (groups * nb, cols)).astype(np.float32)
+    xq, xs = O.quantize(x)
+    y1, y2 = dev.array((groups * nb, rows1), np.float32), dev.array((groups * nb, rows2), np.float32)
+    blocks1 = (rows1 + 8 * r - 1) // (8 * r)
+    grid = ((blocks1 + (rows2 + 8 * r - 1) // (8 * r)) * groups,)
+    dev.launch(f"halo_gemv_q8r_i8_dual_r{r}_b{nb}", grid, (256,),
+               [w1.qs, w1.d, y1, ("u32", rows1), ("u32", w1.qstride), w2.qs, w2.d, y2, ("u32", rows2),
+                ("u32", w2.qstride), dev.to_device(xq), dev.to_device(xs), None, None, ("u32", cols),
+                ("u32", blocks1), ("u32", rows1), ("u32", rows2), ("u32", groups)])
+    for y, qs, d in ((y1, qs1, d1), (y2, qs2, d2)):
+        want, mag = O.gemv_q8a8(qs, d, xq, xs)
+        _check_y(y.download(), want, mag)
+
+
+def test_fp32x_reference_gemv_dual(dev):
+    """halo_gemv_q8r_dual: two matrices with the same fp32 input, 32 rows per block (core.hip:2960-2985)."""
+    rng = np.random.default_rng(23)
+    rows1, rows2, cols = 1000, 77, 2048
+    qs1, d1, w1 = _weights(dev, rng, rows1, cols)
+    qs2, d2, w2 = _weights(dev, rng, rows2, cols)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    y1, y2 = dev.array((1, rows1), np.float32), dev.array((1, rows2), np.float32)
+    blocks1 = (rows1 + 31) // 32
+    dev.launch("halo_gemv_q8r_dual", (blocks1 + (rows2 + 31) // 32,), (256,),
+               [w1.qs, w1.d, y1, ("u32", rows1), ("u32", w1.qstride), w2.qs, w2.d, y2, ("u32", rows2),
+                ("u32", w2.qstride), dev.to_device(x), ("u32", cols), ("u32", blocks1)])
+    for y, qs, d, rows in ((y1, qs1, d1, rows1), (y2, qs2, d2, rows2)):
+        want = np.zeros(rows, np.float32)
+        O.oracle().or_matvec_q8_0_f32x(qs, d, rows, cols, cols, x, want, 1)
+        mag = np.abs(qs * np.repeat(d.view(np.float16).astype(np.float64), 32, 1)) @ np.abs(x.astype(np.float64))
+        _check_y(y.download(), want[None], mag[None])

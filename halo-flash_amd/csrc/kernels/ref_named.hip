@@ -784,3 +784,101 @@ extern "C" __global__ void __launch_bounds__(256)
   GemvQ8rF32At<4>(first ? q1 : q2, first ? d1 : d2, x, first ? y1 : y2, first ? rows1 : rows2, cols,
                   first ? qstride1 : qstride2, first ? blockIdx.x : blockIdx.x - blocks1);
 }
+
+// ---- routed experts across session columns, grouped by expert (reference names) -----------------------------
+// batch_decode.hip:415-446, 646-697.
+
+// ids [n = NB k] (column b's slot s at b k + s; an expert at most once a column) -> ucount, the distinct experts
+// uexp[u] in order of first appearance, their pair counts unum[u] and pairs upair[u * 8 + j] in pair order. One block
+// of 128 threads (n <= 128).
+extern "C" __global__ void __launch_bounds__(128)
+    halo_moe_bucket_b(const std::uint32_t* ids, std::uint32_t n, std::uint32_t* ucount, std::uint32_t* uexp,
+                      std::uint32_t* unum, std::uint32_t* upair) {
+  __shared__ std::uint32_t lid[128], wfirst[2];
+  const std::uint32_t p = threadIdx.x, lane = p % kWave, wave = p / kWave;
+  const std::uint32_t e = p < n ? ids[p] : 0xFFFFFFFFu;
+  lid[p] = e;
+  __syncthreads();
+  bool first = p < n;
+  for (std::uint32_t q = 0; q < p && first; ++q) first = lid[q] != e;
+  const std::uint64_t m = __ballot(first);
+  if (lane == 0) wfirst[wave] = static_cast<std::uint32_t>(__builtin_popcountll(m));
+  __syncthreads();
+  // u = first appearances before p: the earlier wave's count plus this wave's lanes below
+  const std::uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<std::uint32_t>(m >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo(static_cast<std::uint32_t>(m), 0u));
+  if (first) {
+    const std::uint32_t u = (wave ? wfirst[0] : 0u) + below;
+    uexp[u] = e;
+    std::uint32_t cnt = 0;
+    for (std::uint32_t q = p; q < n; ++q)
+      if (lid[q] == e) upair[u * 8 + cnt++] = q;
+    unum[u] = cnt;
+  }
+  if (p == 0) *ucount = wfirst[0] + wfirst[1];
+}
+
+// The down projection of every pair of distinct expert u = blockIdx.y (blocks past ucount exit), 32 rows per block:
+// part[pair][r] = down_e[r] . h[pair] (h [pairs][cols], part [pairs][rows]). NB bounds the pairs of one expert.
+template <int NB>
+__device__ __forceinline__ void MoeDownBucket(const std::int8_t* qs, const std::uint16_t* d, const std::uint32_t* ucount,
+                                              const std::uint32_t* uexp, const std::uint32_t* unum,
+                                              const std::uint32_t* upair, const float* h, float* part,
+                                              std::uint32_t rows, std::uint32_t cols, std::uint32_t qstride) {
+  const std::uint32_t u = blockIdx.y;
+  if (u >= *ucount) return;
+  const std::uint32_t m = min(unum[u], static_cast<std::uint32_t>(NB));
+  std::uint32_t pair[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) pair[j] = upair[u * 8 + min(static_cast<std::uint32_t>(j), m - 1)];
+  const std::size_t e = uexp[u];
+  const std::int8_t* q8 = qs + e * rows * qstride;
+  const std::uint16_t* dd = d + e * rows * (cols / 32);
+  const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, nblk = cols / 32;
+  const std::uint32_t per_wave = 32 / (blockDim.x / kWave);
+  for (std::uint32_t k = 0; k < per_wave; ++k) {
+    const std::uint32_t r = blockIdx.x * 32 + wave * per_wave + k;
+    if (r >= rows) break;
+    float acc[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[j] = 0.0f;
+    for (std::uint32_t c = lane * 16; c < cols; c += kWave * 16) {
+      const int4 qv = *reinterpret_cast<const int4*>(q8 + static_cast<std::size_t>(r) * qstride + c);
+      const std::int8_t* v = reinterpret_cast<const std::int8_t*>(&qv);
+      const float s = halo::F16(dd[static_cast<std::size_t>(r) * nblk + c / 32]);
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const float4* xp = reinterpret_cast<const float4*>(h + static_cast<std::size_t>(pair[j]) * cols + c);
+        float pp = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 xv = xp[i];
+          pp += static_cast<float>(v[4 * i]) * xv.x + static_cast<float>(v[4 * i + 1]) * xv.y +
+                static_cast<float>(v[4 * i + 2]) * xv.z + static_cast<float>(v[4 * i + 3]) * xv.w;
+        }
+        acc[j] += s * pp;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const float a = halo::GroupSum(acc[j]);
+      if (lane == 0 && static_cast<std::uint32_t>(j) < m) part[static_cast<std::size_t>(pair[j]) * rows + r] = a;
+    }
+  }
+}
+#define HALO_MOE_DOWN_BUCKET(NB)                                                                                 \
+  extern "C" __global__ void __launch_bounds__(256) halo_moe_down_q8r_r4_b##NB(                                 \
+      const std::int8_t* qs, const std::uint16_t* d, const std::uint32_t* ucount, const std::uint32_t* uexp,     \
+      const std::uint32_t* unum, const std::uint32_t* upair, const float* h, float* part, std::uint32_t rows,     \
+      std::uint32_t cols, std::uint32_t qstride) {                                                               \
+    MoeDownBucket<NB>(qs, d, ucount, uexp, unum, upair, h, part, rows, cols, qstride);                           \
+  }
+HALO_MOE_DOWN_BUCKET(1)
+HALO_MOE_DOWN_BUCKET(2)
+HALO_MOE_DOWN_BUCKET(3)
+HALO_MOE_DOWN_BUCKET(4)
+HALO_MOE_DOWN_BUCKET(5)
+HALO_MOE_DOWN_BUCKET(6)
+HALO_MOE_DOWN_BUCKET(7)
+HALO_MOE_DOWN_BUCKET(8)
+#undef HALO_MOE_DOWN_BUCKET

@@ -515,3 +515,36 @@ def test_reference_prefill_gemms(dev, name, block, bm, bn, kblocked):
     got = gy.download()
     err = np.abs(got.astype(np.float64) - want.astype(np.float64))
     assert np.all(err <= 1e-5 * mag + 1e-6), f"worst {np.max(err - 1e-5 * mag - 1e-6)}"
+
+
+@pytest.mark.parametrize("B", [1, 4, 8])
+def test_moe_bucket_and_grouped_down(dev, B):
+    """halo_moe_bucket_b (distinct experts over B columns' top-k, in first-appearance order, pairs in order; exact)
+    and halo_moe_down_q8r_r4_b{B} (every pair's down projection by its expert) against numpy and the oracle GEMV
+    (batch_decode.hip:415-446, 646-697)."""
+    rng = np.random.default_rng(53 + B)
+    E, k, H, F = 24, 10, 512, 256
+    ids = np.concatenate([rng.choice(E, k, replace=False) for _ in range(B)]).astype(np.uint32)
+    n = B * k
+    gids = dev.to_device(ids)
+    ucount, uexp = dev.array((1,), np.uint32), dev.array((n,), np.uint32)
+    unum, upair = dev.array((n,), np.uint32), dev.array((n * 8,), np.uint32)
+    dev.launch("halo_moe_bucket_b", (1,), (128,), [gids, ("u32", n), ucount, uexp, unum, upair])
+    order = list(dict.fromkeys(ids.tolist()))
+    U = int(ucount.download()[0])
+    assert U == len(order)
+    assert uexp.download()[:U].tolist() == order
+    got_num, got_pair = unum.download(), upair.download()
+    for u, e in enumerate(order):
+        pairs = [p for p in range(n) if ids[p] == e]
+        assert got_num[u] == len(pairs) and got_pair[u * 8:u * 8 + len(pairs)].tolist() == pairs
+    qs, d = O.synth_q8(rng, E * H, F)
+    h = rng.normal(0, 1, (n, F)).astype(np.float32)
+    part = dev.array((n, H), np.float32)
+    dev.launch(f"halo_moe_down_q8r_r4_b{B}", ((H + 31) // 32, n), (256,),
+               [dev.to_device(qs), dev.to_device(d), ucount, uexp, unum, upair, dev.to_device(h), part, ("u32", H),
+                ("u32", F), ("u32", F)])
+    got = part.download()
+    for p in range(n):
+        e = int(ids[p])
+        _gemv_close(got[p], *_q8_ref(qs[e * H:(e + 1) * H], d[e * H:(e + 1) * H], h[p]))

@@ -882,3 +882,106 @@ HALO_MOE_DOWN_BUCKET(6)
 HALO_MOE_DOWN_BUCKET(7)
 HALO_MOE_DOWN_BUCKET(8)
 #undef HALO_MOE_DOWN_BUCKET
+
+// ---- prefill pair grouping by expert (reference names) ------------------------------------------------------------
+// core.hip:4725-4864. (token, slot) pairs p with expert ids[p] -> sorted (pairs grouped by expert, pair order within
+// an expert), pos[p] (p's sorted position), work tiles of up to 64 pairs of one expert, tiles[3 i .. 3 i + 2] =
+// (expert, first, count), in expert order, and ntiles. experts <= 1024.
+namespace halo::refk {
+constexpr std::uint32_t kPairTile = 64, kPairChunk = 1024;
+// Expert offsets (exclusive scan of totals in expert order), tiles and ntiles, from total[e] in LDS; block 1024.
+__device__ __forceinline__ void BucketTiles(const std::uint32_t* total, std::uint32_t experts, std::uint32_t* poff,
+                                            std::uint32_t* tiles, std::uint32_t* ntiles, std::uint32_t* wave_tot) {
+  const std::uint32_t e = threadIdx.x;
+  const std::uint32_t n = e < experts ? total[e] : 0u, nt = (n + kPairTile - 1) / kPairTile;
+  std::uint32_t ptot, ttot;
+  const std::uint32_t p0 = halo::sample::BlockExclScan<std::uint32_t>(n, wave_tot, &ptot);
+  const std::uint32_t t0 = halo::sample::BlockExclScan<std::uint32_t>(nt, wave_tot, &ttot);
+  if (e < experts) poff[e] = p0;
+  for (std::uint32_t i = 0; i < nt; ++i) {
+    tiles[3 * (t0 + i)] = e;
+    tiles[3 * (t0 + i) + 1] = p0 + i * kPairTile;
+    tiles[3 * (t0 + i) + 2] = min(kPairTile, n - i * kPairTile);
+  }
+  if (e == 0) *ntiles = ttot;
+}
+}  // namespace halo::refk
+
+// One block of 1024 threads does all of it (small chunks).
+extern "C" __global__ void __launch_bounds__(1024)
+    halo_moe_bucket(const std::uint32_t* ids, std::uint32_t pairs, std::uint32_t experts, std::uint32_t* sorted,
+                    std::uint32_t* pos, std::uint32_t* tiles, std::uint32_t* ntiles) {
+  __shared__ std::uint32_t cnt[1024], run[1024], chunk_ids[kPairChunk], wave_tot[16];
+  const std::uint32_t tid = threadIdx.x;
+  cnt[tid] = 0;
+  __syncthreads();
+  for (std::uint32_t p = tid; p < pairs; p += blockDim.x) atomicAdd(&cnt[ids[p]], 1u);
+  __syncthreads();
+  BucketTiles(cnt, experts, run, tiles, ntiles, wave_tot);
+  __syncthreads();
+  // scatter chunk by chunk: a pair's rank among the chunk's earlier pairs of its expert, then the running offsets
+  for (std::uint32_t base = 0; base < pairs; base += kPairChunk) {
+    const std::uint32_t p = base + tid;
+    const std::uint32_t e = p < pairs ? ids[p] : 0xFFFFFFFFu;
+    chunk_ids[tid] = e;
+    __syncthreads();
+    if (p < pairs) {
+      std::uint32_t rank = 0;
+      for (std::uint32_t i = 0; i < tid; ++i) rank += chunk_ids[i] == e;
+      const std::uint32_t at = run[e] + rank;
+      sorted[at] = p;
+      pos[p] = at;
+    }
+    __syncthreads();
+    if (p < pairs) atomicAdd(&run[e], 1u);  // after every read of run[] for this chunk
+    __syncthreads();
+  }
+}
+// 1. per chunk of 1024 pairs, per-expert counts [chunks][experts]. grid (chunks), block 1024.
+extern "C" __global__ void __launch_bounds__(1024)
+    halo_moe_bucket_count(const std::uint32_t* ids, std::uint32_t pairs, std::uint32_t experts,
+                          std::uint32_t* counts) {
+  __shared__ std::uint32_t c[1024];
+  const std::uint32_t tid = threadIdx.x, p = blockIdx.x * kPairChunk + tid;
+  c[tid] = 0;
+  __syncthreads();
+  if (p < pairs) atomicAdd(&c[ids[p]], 1u);
+  __syncthreads();
+  if (tid < experts) counts[static_cast<std::size_t>(blockIdx.x) * experts + tid] = c[tid];
+}
+// 2. counts become exclusive chunk offsets per expert; expert offsets base[e], tiles, ntiles. grid (1), block 1024.
+extern "C" __global__ void __launch_bounds__(1024)
+    halo_moe_bucket_scan(std::uint32_t* counts, std::uint32_t chunks, std::uint32_t experts, std::uint32_t* tiles,
+                         std::uint32_t* ntiles, std::uint32_t* base) {
+  __shared__ std::uint32_t total[1024], wave_tot[16];
+  const std::uint32_t e = threadIdx.x;
+  if (e < experts) {
+    std::uint32_t acc = 0;
+    for (std::uint32_t ch = 0; ch < chunks; ++ch) {
+      std::uint32_t* c = counts + static_cast<std::size_t>(ch) * experts + e;
+      const std::uint32_t v = *c;
+      *c = acc;
+      acc += v;
+    }
+    total[e] = acc;
+  }
+  __syncthreads();
+  BucketTiles(total, experts, base, tiles, ntiles, wave_tot);
+}
+// 3. each pair's rank among its chunk's earlier pairs of its expert gives its sorted position. grid (chunks), 1024.
+extern "C" __global__ void __launch_bounds__(1024)
+    halo_moe_bucket_scatter(const std::uint32_t* ids, std::uint32_t pairs, std::uint32_t experts,
+                            const std::uint32_t* chunk_off, const std::uint32_t* base, std::uint32_t* sorted,
+                            std::uint32_t* pos) {
+  __shared__ std::uint32_t chunk_ids[kPairChunk];
+  const std::uint32_t tid = threadIdx.x, p = blockIdx.x * kPairChunk + tid;
+  const std::uint32_t e = p < pairs ? ids[p] : 0xFFFFFFFFu;
+  chunk_ids[tid] = e;
+  __syncthreads();
+  if (p >= pairs) return;
+  std::uint32_t rank = 0;
+  for (std::uint32_t i = 0; i < tid; ++i) rank += chunk_ids[i] == e;
+  const std::uint32_t at = base[e] + chunk_off[static_cast<std::size_t>(blockIdx.x) * experts + e] + rank;
+  sorted[at] = p;
+  pos[p] = at;
+}

@@ -60,6 +60,10 @@
  *     halo_moe_bucket_b(ids, n, ucount, uexp, unum, upair)              1 block of 128; n <= 128
  *     halo_moe_down_q8r_r4_b{1..8}(qs, d, ucount, uexp, unum, upair, h, part, rows, cols, qstride)
  *                                                                       grid (ceil(rows / 32), n)
+ *   prefill pair grouping (core.hip:4725-4864): halo_moe_bucket(ids, pairs, experts, sorted, pos, tiles, ntiles)
+ *     1 block of 1024; halo_moe_bucket_count(ids, pairs, experts, counts) grid (chunks of 1024), block 1024;
+ *     halo_moe_bucket_scan(counts, chunks, experts, tiles, ntiles, base) 1 block of 1024;
+ *     halo_moe_bucket_scatter(ids, pairs, experts, chunk_off, base, sorted, pos) grid (chunks), block 1024
  *   reference-named prefill int8 GEMMs (core.hip:3103-3153, 3303-3311, 3466-3476), y [T][rows]; cols % 64 == 0:
  *     halo_gemm_q8r_wmma / _wmma_t(qs, d, xq, xd, y, rows, cols, qstride, tokens)   x as halo_quantize_q8_rows
  *       grid (ceil(T / 64), ceil(rows / 64)), block 128 / (ceil(T / 128), ceil(rows / 128)), block 256
@@ -96,6 +100,7 @@
   X(halo_conv_state_advance) X(halo_shexp_gate_up) X(halo_shexp_gate_up_u) X(halo_shexp_down_combine)         \
   X(halo_shexp_down_combine_u) X(halo_router_rowblock_q8act)                                                  \
   X(halo_moe_bucket_b) X(halo_moe_down_q8r_r4_b1) X(halo_moe_down_q8r_r4_b4) X(halo_moe_down_q8r_r4_b8)         \
+  X(halo_moe_bucket) X(halo_moe_bucket_count) X(halo_moe_bucket_scan) X(halo_moe_bucket_scatter)               \
   X(halo_gemm_q8r_wmma) X(halo_gemm_q8r_wmma_t) X(halo_gemm_q8a8_128x128) X(halo_gemm_q8a8_128x64)           \
   X(halo_gemm_q8a8_320x64) X(halo_gemm_q8a8_160x64) X(halo_gemm_q8a8_256x128)                                 \
   X(halo_synth_q8) X(halo_synth_f32)

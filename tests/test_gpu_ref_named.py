@@ -548,3 +548,41 @@ def test_moe_bucket_and_grouped_down(dev, B):
     for p in range(n):
         e = int(ids[p])
         _gemv_close(got[p], *_q8_ref(qs[e * H:(e + 1) * H], d[e * H:(e + 1) * H], h[p]))
+
+
+@pytest.mark.parametrize("T", [1, 300])
+def test_moe_prefill_buckets(dev, T):
+    """halo_moe_bucket and the three-pass halo_moe_bucket_count / _scan / _scatter (core.hip:4725-4864): pairs
+    grouped by expert in pair order (a stable sort), each pair's position, 64-pair tiles in expert order; exact."""
+    rng = np.random.default_rng(54 + T)
+    E, k = 512, 10
+    ids = np.concatenate([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.uint32)
+    P = ids.size
+    order = np.argsort(ids, kind="stable").astype(np.uint32)
+    pos = np.empty(P, np.uint32)
+    pos[order] = np.arange(P, dtype=np.uint32)
+    counts = np.bincount(ids, minlength=E)
+    want_tiles, off = [], 0
+    for e in range(E):
+        for i in range(0, counts[e], 64):
+            want_tiles.append((e, off + i, min(64, counts[e] - i)))
+        off += counts[e]
+    gids = dev.to_device(ids)
+    maxt = P // 64 + E + 1
+    # one block
+    s1, p1, t1, n1 = (dev.array((P,), np.uint32), dev.array((P,), np.uint32), dev.array((3 * maxt,), np.uint32),
+                      dev.array((1,), np.uint32))
+    dev.launch("halo_moe_bucket", (1,), (1024,), [gids, ("u32", P), ("u32", E), s1, p1, t1, n1])
+    # three passes
+    chunks = (P + 1023) // 1024
+    cnt = dev.array((chunks, E), np.uint32)
+    s2, p2, t2, n2, base = (dev.array((P,), np.uint32), dev.array((P,), np.uint32),
+                            dev.array((3 * maxt,), np.uint32), dev.array((1,), np.uint32), dev.array((E,), np.uint32))
+    dev.launch("halo_moe_bucket_count", (chunks,), (1024,), [gids, ("u32", P), ("u32", E), cnt])
+    dev.launch("halo_moe_bucket_scan", (1,), (1024,), [cnt, ("u32", chunks), ("u32", E), t2, n2, base])
+    dev.launch("halo_moe_bucket_scatter", (chunks,), (1024,), [gids, ("u32", P), ("u32", E), cnt, base, s2, p2])
+    for s, p, t, n in ((s1, p1, t1, n1), (s2, p2, t2, n2)):
+        assert int(n.download()[0]) == len(want_tiles)
+        assert np.array_equal(s.download(), order) and np.array_equal(p.download(), pos)
+        assert t.download()[:3 * len(want_tiles)].reshape(-1, 3).tolist() == [list(x) for x in want_tiles]
+    assert np.array_equal(base.download(), np.concatenate([[0], np.cumsum(counts)[:-1]]).astype(np.uint32))

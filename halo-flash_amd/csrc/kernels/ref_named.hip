@@ -985,3 +985,130 @@ extern "C" __global__ void __launch_bounds__(1024)
   sorted[at] = p;
   pos[p] = at;
 }
+
+// ---- decode / prefill glue: fused norm + RoPE rows, batched-column variants, small elementwise (reference names)
+// core.hip:308-311, 372-440, 587-590, 1123-1133, 4045-4055, 4708-4715; batch_decode.hip:1680-1705.
+namespace halo::refk {
+// v [d] in LDS (d <= 256, one value per thread at threadIdx.x < d) <- x * w / rms(x); then NEOX RoPE on v at pos.
+__device__ __forceinline__ void NormRopeLds(float xi, const float* w, float eps, std::uint32_t d,
+                                            std::uint32_t rotary_dim, std::uint32_t pos, float theta, float* v,
+                                            float* red) {
+  const std::uint32_t i = threadIdx.x;
+  const float ss = BlockSumAny(i < d ? xi * xi : 0.0f, red);
+  const float inv = 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
+  if (i < d) v[i] = xi * inv * w[i];
+  __syncthreads();
+  RotateHead(v, rotary_dim, pos, theta);
+  __syncthreads();
+}
+}  // namespace halo::refk
+
+// Pooled blocks b0, b0 + 1, ... at positions (b0 + b) * ratio. grid (nblocks).
+extern "C" __global__ void halo_rope_neox_blocks(float* x, std::uint32_t head_dim, std::uint32_t rotary_dim,
+                                                 std::uint32_t b0, std::uint32_t ratio, float theta) {
+  RotateHead(x + static_cast<std::size_t>(blockIdx.x) * head_dim, rotary_dim, (b0 + blockIdx.x) * ratio, theta);
+}
+// halo_split_qgate, the q rows' RMSNorm (shared w) and RoPE in one pass: token t = blockIdx.x / heads at pos0 + t.
+// gate may be null. grid (T * heads), block hd (<= 256).
+extern "C" __global__ void __launch_bounds__(256)
+    halo_split_qgate_norm_rope(const float* qg, float* q, float* gate, const float* w, float eps,
+                               std::uint32_t rotary_dim, std::uint32_t pos0, std::uint32_t heads, float theta) {
+  __shared__ float red[16], v[256];
+  const std::uint32_t hd = blockDim.x, i = threadIdx.x;
+  const float* src = qg + static_cast<std::size_t>(blockIdx.x) * 2 * hd;
+  if (gate) gate[static_cast<std::size_t>(blockIdx.x) * hd + i] = src[hd + i];
+  NormRopeLds(src[i], w, eps, hd, rotary_dim, pos0 + blockIdx.x / heads, theta, v, red);
+  q[static_cast<std::size_t>(blockIdx.x) * hd + i] = v[i];
+}
+// RMSNorm (shared w, d <= 256) then RoPE on rows of `heads` heads per token at pos0 + blockIdx.x / heads, in place;
+// with cache non-null the rotated row is also written there (cache row blockIdx.x). grid (T * heads), block 256.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_norm_rope_rows(float* x, const float* w, float eps, std::uint32_t d, std::uint32_t rotary_dim,
+                        std::uint32_t pos0, std::uint32_t heads, float theta, float* cache) {
+  __shared__ float red[16], v[256];
+  const std::uint32_t i = threadIdx.x;
+  float* row = x + static_cast<std::size_t>(blockIdx.x) * d;
+  NormRopeLds(i < d ? row[i] : 0.0f, w, eps, d, rotary_dim, pos0 + blockIdx.x / heads, theta, v, red);
+  if (i < d) {
+    row[i] = v[i];
+    if (cache) cache[static_cast<std::size_t>(blockIdx.x) * d + i] = v[i];
+  }
+}
+// RMSNorm of T * hc vectors whose gammas repeat every w_period vectors (vector b uses w_all + (b % w_period) *
+// w_stride). grid (vectors).
+extern "C" __global__ void halo_rmsnorm_rows(const float* x, const float* w_all, float* y, std::uint32_t d, float eps,
+                                             std::uint32_t w_stride, std::uint32_t w_period) {
+  __shared__ float red[16];
+  const float* xv = x + static_cast<std::size_t>(blockIdx.x) * d;
+  const float* w = w_all + static_cast<std::size_t>(blockIdx.x % w_period) * w_stride;
+  float* yv = y + static_cast<std::size_t>(blockIdx.x) * d;
+  float ss = 0.0f;
+  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) ss += xv[i] * xv[i];
+  const float inv = 1.0f / sqrtf(BlockSumAny(ss, red) / static_cast<float>(d) + eps);
+  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) yv[i] = xv[i] * inv * w[i];
+}
+
+// Batched-column variants: column (session entry) e = blockIdx.y, its data `stride` floats apart.
+// grid (heads, B)
+extern "C" __global__ void halo_split_qgate_y(const float* qg, float* q, float* gate, std::uint32_t hd,
+                                              std::uint32_t qg_stride, std::uint32_t q_stride) {
+  const std::size_t h = blockIdx.x, e = blockIdx.y;
+  const float* src = qg + e * qg_stride + h * 2 * hd;
+  for (std::uint32_t i = threadIdx.x; i < hd; i += blockDim.x) {
+    q[e * q_stride + h * hd + i] = src[i];
+    gate[e * q_stride + h * hd + i] = src[hd + i];
+  }
+}
+// In place; grid (vectors, B)
+extern "C" __global__ void halo_rmsnorm_y(float* x, const float* w_all, std::uint32_t d, float eps,
+                                          std::uint32_t w_stride, std::uint32_t stride) {
+  __shared__ float red[16];
+  float* xv = x + static_cast<std::size_t>(blockIdx.y) * stride + static_cast<std::size_t>(blockIdx.x) * d;
+  const float* w = w_all + static_cast<std::size_t>(blockIdx.x) * w_stride;
+  float ss = 0.0f;
+  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) ss += xv[i] * xv[i];
+  const float inv = 1.0f / sqrtf(BlockSumAny(ss, red) / static_cast<float>(d) + eps);
+  __syncthreads();  // every read of xv precedes the in-place writes
+  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) xv[i] = xv[i] * inv * w[i];
+}
+// grid (heads, B): column e's position params[e * pstride + slot] * scale.
+extern "C" __global__ void halo_rope_neox_p_y(float* x, const std::uint32_t* params, std::uint32_t head_dim,
+                                              std::uint32_t rotary_dim, std::uint32_t slot, std::uint32_t scale,
+                                              float theta, std::uint32_t stride, std::uint32_t pstride) {
+  const std::size_t e = blockIdx.y;
+  RotateHead(x + e * stride + static_cast<std::size_t>(blockIdx.x) * head_dim, rotary_dim,
+             params[e * pstride + slot] * scale, theta);
+}
+// Column e's destination is the pointer tab[e * tstride + tslot]. grid (ceil(n / 256), B)
+extern "C" __global__ void halo_copy_at_y(const std::uint64_t* tab, std::uint32_t tstride, std::uint32_t tslot,
+                                          const float* src, const std::uint32_t* params, std::uint32_t slot,
+                                          std::uint32_t stride, std::uint32_t n, std::uint32_t src_stride,
+                                          std::uint32_t pstride) {
+  const std::size_t e = blockIdx.y;
+  float* dst = reinterpret_cast<float*>(tab[e * tstride + tslot]);
+  float* row = dst + static_cast<std::size_t>(params[e * pstride + slot]) * stride;
+  const float* s = src + e * src_stride;
+  for (std::uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) row[i] = s[i];
+}
+
+// y += weights[slot] x; y += sigmoid(g[0]) x; for T rows y [T][n] += sigmoid(g[t]) x [T][n]; x = silu(x scale).
+extern "C" __global__ void halo_axpy_slot(float* y, const float* x, const float* weights, std::uint32_t slot,
+                                          std::uint32_t n) {
+  const float a = weights[slot];
+  for (std::uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) y[i] += a * x[i];
+}
+extern "C" __global__ void halo_axpy_sigmoid(float* y, const float* x, const float* g, std::uint32_t n) {
+  const float a = halo::Sigmoid(g[0]);
+  for (std::uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) y[i] += a * x[i];
+}
+extern "C" __global__ void halo_axpy_sigmoid_rows(float* y, const float* x, const float* g, std::uint32_t n,
+                                                  std::uint32_t tokens) {
+  const std::size_t total = static_cast<std::size_t>(tokens) * n;
+  for (std::size_t i = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<std::size_t>(gridDim.x) * blockDim.x)
+    y[i] += halo::Sigmoid(g[i / n]) * x[i];
+}
+extern "C" __global__ void halo_scale_silu(float* x, float scale, std::uint32_t n) {
+  for (std::uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    x[i] = halo::Silu(x[i] * scale);
+}

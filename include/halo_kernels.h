@@ -56,6 +56,13 @@
  *     halo_shexp_down_combine{,_u}(dq, dd, hin, sgate, part, weights, slots, out, rows, cols, qstride)
  *                                                                       grid ceil(rows / 32)
  *     halo_router_rowblock_q8act(w, x, y, rows, cols, act)              grid max(rows, cols / 32)
+ *   fused norm + RoPE and batched-column glue (core.hip:308-440, 587, 1123-1133, 4045, 4708; batch_decode.hip:1680):
+ *     halo_split_qgate_norm_rope(qg, q, gate, w, eps, rotary_dim, pos0, heads, theta)  grid (T * heads), block hd
+ *     halo_norm_rope_rows(x, w, eps, d, rotary_dim, pos0, heads, theta, cache)          grid (T * heads), block 256
+ *     halo_rope_neox_blocks(x, head_dim, rotary_dim, b0, ratio, theta)                   grid (nblocks)
+ *     halo_rmsnorm_rows(x, w_all, y, d, eps, w_stride, w_period)                         grid (vectors)
+ *     halo_split_qgate_y / halo_rmsnorm_y / halo_rope_neox_p_y / halo_copy_at_y           grid (., B)
+ *     halo_axpy_slot, halo_axpy_sigmoid, halo_axpy_sigmoid_rows, halo_scale_silu          grid-stride
  *   session-union experts (batch_decode.hip:415-446, 646-697):
  *     halo_moe_bucket_b(ids, n, ucount, uexp, unum, upair)              1 block of 128; n <= 128
  *     halo_moe_down_q8r_r4_b{1..8}(qs, d, ucount, uexp, unum, upair, h, part, rows, cols, qstride)
@@ -100,6 +107,9 @@
   X(halo_conv_state_advance) X(halo_shexp_gate_up) X(halo_shexp_gate_up_u) X(halo_shexp_down_combine)         \
   X(halo_shexp_down_combine_u) X(halo_router_rowblock_q8act)                                                  \
   X(halo_moe_bucket_b) X(halo_moe_down_q8r_r4_b1) X(halo_moe_down_q8r_r4_b4) X(halo_moe_down_q8r_r4_b8)         \
+  X(halo_split_qgate_norm_rope) X(halo_norm_rope_rows) X(halo_rope_neox_blocks) X(halo_rmsnorm_rows)           \
+  X(halo_split_qgate_y) X(halo_rmsnorm_y) X(halo_rope_neox_p_y) X(halo_copy_at_y) X(halo_axpy_slot)            \
+  X(halo_axpy_sigmoid) X(halo_axpy_sigmoid_rows) X(halo_scale_silu)                                            \
   X(halo_moe_bucket) X(halo_moe_bucket_count) X(halo_moe_bucket_scan) X(halo_moe_bucket_scatter)               \
   X(halo_gemm_q8r_wmma) X(halo_gemm_q8r_wmma_t) X(halo_gemm_q8a8_128x128) X(halo_gemm_q8a8_128x64)           \
   X(halo_gemm_q8a8_320x64) X(halo_gemm_q8a8_160x64) X(halo_gemm_q8a8_256x128)                                 \

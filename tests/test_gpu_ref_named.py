@@ -586,3 +586,127 @@ def test_moe_prefill_buckets(dev, T):
         assert np.array_equal(s.download(), order) and np.array_equal(p.download(), pos)
         assert t.download()[:3 * len(want_tiles)].reshape(-1, 3).tolist() == [list(x) for x in want_tiles]
     assert np.array_equal(base.download(), np.concatenate([[0], np.cumsum(counts)[:-1]]).astype(np.uint32))
+
+
+def _rms(x, w, eps):
+    x64 = x.astype(np.float64)
+    return x64 / np.sqrt((x64 * x64).mean(-1, keepdims=True) + eps) * w
+
+
+def _rope(v, rot, pos, theta):
+    """NEOX rotation of the first rot values of each row of v (float64) at positions pos (per row)."""
+    out = v.copy()
+    half = rot // 2
+    i = np.arange(half)
+    ang = np.asarray(pos, np.float64)[:, None] * theta ** (-2.0 * i / rot)
+    a, b = v[:, :half], v[:, half:rot]
+    out[:, :half] = a * np.cos(ang) - b * np.sin(ang)
+    out[:, half:rot] = a * np.sin(ang) + b * np.cos(ang)
+    return out
+
+
+def test_norm_rope_and_batched_glue(dev):
+    """halo_split_qgate_norm_rope, halo_norm_rope_rows (+ cache row), halo_rope_neox_blocks, halo_rmsnorm_rows and the
+    batched-column _y kernels against numpy (core.hip:308-440, 4045; batch_decode.hip:1680-1705); norms at 1e-5 of
+    each value, rotations at 5e-5 of the rows' largest value (fp32 angles at positions up to 900)."""
+    rng = np.random.default_rng(55)
+    T, heads, hd, rot, theta, eps, pos0 = 3, 4, 256, 64, 1e7, 1e-6, 40
+    qg = rng.normal(0, 1, (T * heads, 2 * hd)).astype(np.float32)
+    w = rng.normal(1, 0.1, hd).astype(np.float32)
+    gq, gg = dev.array((T * heads, hd), np.float32), dev.array((T * heads, hd), np.float32)
+    dev.launch("halo_split_qgate_norm_rope", (T * heads,), (hd,),
+               [dev.to_device(qg), gq, gg, dev.to_device(w), ("f32", eps), ("u32", rot), ("u32", pos0),
+                ("u32", heads), ("f32", theta)])
+    pos = pos0 + np.arange(T * heads) // heads
+    want = _rope(_rms(qg[:, :hd], w, eps), rot, pos, theta)
+    close(gq.download(), want, np.abs(want).max(), 5e-5)
+    assert np.array_equal(gg.download(), qg[:, hd:])
+    # norm + rope rows with the cache copy (d = 256)
+    x = rng.normal(0, 1, (T * heads, hd)).astype(np.float32)
+    gx, gc = dev.to_device(x), dev.array((T * heads, hd), np.float32)
+    dev.launch("halo_norm_rope_rows", (T * heads,), (256,),
+               [gx, dev.to_device(w), ("f32", eps), ("u32", hd), ("u32", rot), ("u32", pos0), ("u32", heads),
+                ("f32", theta), gc])
+    want = _rope(_rms(x, w, eps), rot, pos, theta)
+    close(gx.download(), want, np.abs(want).max(), 5e-5)
+    assert gc.download().tobytes() == gx.download().tobytes()
+    # pooled blocks at (b0 + b) * ratio
+    xb = rng.normal(0, 1, (5, hd)).astype(np.float32)
+    gb = dev.to_device(xb)
+    dev.launch("halo_rope_neox_blocks", (5,), (64,), [gb, ("u32", hd), ("u32", rot), ("u32", 3), ("u32", 16),
+                                                      ("f32", theta)])
+    want = _rope(xb.astype(np.float64), rot, (3 + np.arange(5)) * 16, theta)
+    close(gb.download(), want, np.abs(want).max(), 5e-5)
+    # rmsnorm rows with gammas repeating every 2 vectors
+    xr = rng.normal(0, 1, (6, 128)).astype(np.float32)
+    wr = rng.normal(1, 0.1, (2, 130)).astype(np.float32)
+    gy = dev.array((6, 128), np.float32)
+    dev.launch("halo_rmsnorm_rows", (6,), (128,), [dev.to_device(xr), dev.to_device(wr), gy, ("u32", 128),
+                                                   ("f32", eps), ("u32", 130), ("u32", 2)])
+    want = _rms(xr, wr[np.arange(6) % 2, :128], eps)
+    close(gy.download(), want, np.abs(want) + 1e-3)
+    # batched columns: B = 2 entries, data `stride` floats apart
+    B, stride, pstride = 2, heads * 2 * hd + 64, 16
+    qgb = rng.normal(0, 1, (B, stride)).astype(np.float32)
+    q_stride = heads * hd + 32
+    gqb, ggb = dev.array((B, q_stride), np.float32), dev.array((B, q_stride), np.float32)
+    dev.launch("halo_split_qgate_y", (heads, B), (256,), [dev.to_device(qgb), gqb, ggb, ("u32", hd), ("u32", stride),
+                                                          ("u32", q_stride)])
+    for e in range(B):
+        v = qgb[e, :heads * 2 * hd].reshape(heads, 2, hd)
+        assert np.array_equal(gqb.download()[e, :heads * hd], v[:, 0].ravel())
+        assert np.array_equal(ggb.download()[e, :heads * hd], v[:, 1].ravel())
+    wn = rng.normal(1, 0.1, (heads, hd)).astype(np.float32)
+    xy = rng.normal(0, 1, (B, q_stride)).astype(np.float32)
+    gxy = dev.to_device(xy)
+    dev.launch("halo_rmsnorm_y", (heads, B), (256,), [gxy, dev.to_device(wn), ("u32", hd), ("f32", eps), ("u32", hd),
+                                                      ("u32", q_stride)])
+    got = gxy.download()
+    for e in range(B):
+        want = _rms(xy[e, :heads * hd].reshape(heads, hd), wn, eps)
+        close(got[e, :heads * hd].reshape(heads, hd), want, np.abs(want) + 1e-3)
+    params = np.zeros((B, pstride), np.uint32)
+    params[:, 1] = [17, 900]
+    gxr = dev.to_device(xy)
+    dev.launch("halo_rope_neox_p_y", (heads, B), (64,), [gxr, dev.to_device(params), ("u32", hd), ("u32", rot),
+                                                         ("u32", 1), ("u32", 1), ("f32", theta), ("u32", q_stride),
+                                                         ("u32", pstride)])
+    got = gxr.download()
+    for e in range(B):
+        want = _rope(xy[e, :heads * hd].reshape(heads, hd).astype(np.float64), rot, [params[e, 1]] * heads, theta)
+        close(got[e, :heads * hd].reshape(heads, hd), want, np.abs(want).max(), 5e-5)
+    # copy_at_y: each entry's cache through a pointer table
+    caches = [dev.array((50, 300), np.float32).fill(0) for _ in range(B)]
+    tab = np.zeros((B, 3), np.uint64)
+    for e in range(B):
+        tab[e, 2] = caches[e].ptr
+    src = rng.normal(0, 1, (B, 320)).astype(np.float32)
+    params[:, 2] = [4, 33]
+    dev.launch("halo_copy_at_y", (2, B), (256,), [dev.to_device(tab), ("u32", 3), ("u32", 2), dev.to_device(src),
+                                                  dev.to_device(params), ("u32", 2), ("u32", 300), ("u32", 300),
+                                                  ("u32", 320), ("u32", pstride)])
+    for e in range(B):
+        c = caches[e].download()
+        assert np.array_equal(c[params[e, 2]], src[e, :300]) and np.count_nonzero(c) == np.count_nonzero(src[e, :300])
+
+
+def test_small_elementwise(dev):
+    rng = np.random.default_rng(56)
+    n, T = 1000, 3
+    y = rng.normal(0, 1, (T, n)).astype(np.float32)
+    x = rng.normal(0, 1, (T, n)).astype(np.float32)
+    g = rng.normal(0, 1, T).astype(np.float32)
+    wts = rng.random(4).astype(np.float32)
+    gy = dev.to_device(y[0])
+    dev.launch("halo_axpy_slot", (2,), (256,), [gy, dev.to_device(x[0]), dev.to_device(wts), ("u32", 2), ("u32", n)])
+    close(gy.download(), y[0] + wts[2].astype(np.float64) * x[0], np.abs(y[0]) + np.abs(x[0]))
+    gy = dev.to_device(y[0])
+    dev.launch("halo_axpy_sigmoid", (2,), (256,), [gy, dev.to_device(x[0]), dev.to_device(g), ("u32", n)])
+    close(gy.download(), y[0] + sig(g[0]) * x[0], np.abs(y[0]) + np.abs(x[0]))
+    gy = dev.to_device(y)
+    dev.launch("halo_axpy_sigmoid_rows", (4,), (256,), [gy, dev.to_device(x), dev.to_device(g), ("u32", n),
+                                                        ("u32", T)])
+    close(gy.download(), y + sig(g)[:, None] * x, np.abs(y) + np.abs(x))
+    gx = dev.to_device(x[0])
+    dev.launch("halo_scale_silu", (2,), (256,), [gx, ("f32", 0.25), ("u32", n)])
+    close(gx.download(), silu((x[0] * np.float32(0.25)).astype(np.float32)), np.abs(x[0]) + 1e-3)

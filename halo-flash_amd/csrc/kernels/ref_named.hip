@@ -1112,3 +1112,121 @@ extern "C" __global__ void halo_scale_silu(float* x, float scale, std::uint32_t 
   for (std::uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
     x[i] = halo::Silu(x[i] * scale);
 }
+
+// ---- fp32 GEMMs for prefill routers and small projections, shared-expert add, batched top-k (reference names) --
+// core.hip:2938-2956, 3767-3800, 5605-5680, 8975-9000; batch_decode.hip:1157-1165. y [T][rows] = x [T][cols] W^T.
+
+// 64 rows x 64 tokens per block, K staged 32 at a time in LDS, 4 x 4 outputs per thread, products added in
+// ascending k. grid (ceil(T / 64), ceil(rows / 64)), block 256.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_gemm_f32_tiled(const float* w, const float* x, float* y, std::uint32_t rows, std::uint32_t cols,
+                        std::uint32_t tokens) {
+  constexpr std::uint32_t BM = 64, BN = 64, BK = 32;
+  __shared__ float ws[BK][BM + 1], xs[BK][BN + 1];
+  const std::uint32_t tid = threadIdx.x, r0 = blockIdx.y * BM, t0 = blockIdx.x * BN;
+  const std::uint32_t tr = (tid % 16) * 4, tt = (tid / 16) * 4;
+  float acc[4][4] = {};
+  for (std::uint32_t k0 = 0; k0 < cols; k0 += BK) {
+    // 64 x 32 of each operand: thread loads 8 values of W and 8 of x (k fastest, coalesced), zero past the edges
+    for (std::uint32_t e = tid; e < BM * BK; e += 256) {
+      const std::uint32_t rr = e / BK, kk = e % BK, r = r0 + rr, t = t0 + rr, k = k0 + kk;
+      ws[kk][rr] = r < rows && k < cols ? w[static_cast<std::size_t>(r) * cols + k] : 0.0f;
+      xs[kk][rr] = t < tokens && k < cols ? x[static_cast<std::size_t>(t) * cols + k] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (std::uint32_t kk = 0; kk < BK; ++kk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(ws[kk][tr + i], xs[kk][tt + j], acc[i][j]);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const std::uint32_t r = r0 + tr + i, t = t0 + tt + j;
+      if (r < rows && t < tokens) y[static_cast<std::size_t>(t) * rows + r] = acc[i][j];
+    }
+}
+// One wave per output row (2 rows per wave of the block's 8), lanes across columns. grid (ceil(rows / 8), T).
+extern "C" __global__ void __launch_bounds__(256)
+    halo_gemm_f32_rows(const float* w, const float* x, float* y, std::uint32_t rows, std::uint32_t cols) {
+  const std::uint32_t t = blockIdx.y, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const float* xr = x + static_cast<std::size_t>(t) * cols;
+  for (std::uint32_t k = 0; k < 2; ++k) {
+    const std::uint32_t r = blockIdx.x * 8 + wave * 2 + k;
+    if (r >= rows) break;
+    const float* wr = w + static_cast<std::size_t>(r) * cols;
+    float acc = 0.0f;
+    for (std::uint32_t c = lane; c < cols; c += kWave) acc = __builtin_fmaf(wr[c], xr[c], acc);
+    acc = halo::GroupSum(acc);
+    if (lane == 0) y[static_cast<std::size_t>(t) * rows + r] = acc;
+  }
+}
+// Few columns: one thread per output, x row in LDS. grid (ceil(rows / 256), T), block 256; cols <= 8192.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_gemm_f32_narrow(const float* w, const float* x, float* y, std::uint32_t rows, std::uint32_t cols) {
+  __shared__ float xs[8192];
+  const std::uint32_t t = blockIdx.y;
+  for (std::uint32_t i = threadIdx.x; i < cols; i += blockDim.x) xs[i] = x[static_cast<std::size_t>(t) * cols + i];
+  __syncthreads();
+  const std::uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const float* wr = w + static_cast<std::size_t>(r) * cols;
+  float acc = 0.0f;
+  for (std::uint32_t c = 0; c < cols; ++c) acc = __builtin_fmaf(wr[c], xs[c], acc);
+  y[static_cast<std::size_t>(t) * rows + r] = acc;
+}
+// Few rows (<= 16): a 32-lane half wave per token reads the token's row once against every weight row.
+// grid (ceil(T / 8)), block 256.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_gemm_f32_skinny(const float* w, const float* x, float* y, std::uint32_t rows, std::uint32_t cols,
+                         std::uint32_t tokens) {
+  const std::uint32_t lane = threadIdx.x % 32, t = blockIdx.x * 8 + threadIdx.x / 32;
+  const std::uint32_t tc = min(t, tokens - 1);  // every half wave reaches the group sums
+  const float* xr = x + static_cast<std::size_t>(tc) * cols;
+  float acc[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+  for (std::uint32_t c = lane; c < cols; c += 32) {
+    const float xv = xr[c];
+#pragma unroll
+    for (std::uint32_t r = 0; r < 16; ++r)
+      if (r < rows) acc[r] = __builtin_fmaf(w[static_cast<std::size_t>(r) * cols + c], xv, acc[r]);
+  }
+#pragma unroll
+  for (std::uint32_t r = 0; r < 16; ++r) {
+    const float s = halo::GroupSum<32>(acc[r]);
+    if (lane == 0 && t < tokens && r < rows) y[static_cast<std::size_t>(t) * rows + r] = s;
+  }
+}
+
+// out[r] += sigmoid(sgate[0]) * (down_r . hin); 32 rows per block. grid (ceil(rows / 32)), block 256.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_shexp_down_add(const std::int8_t* dq, const std::uint16_t* dd, const float* hin, const float* sgate,
+                        float* out, std::uint32_t rows, std::uint32_t cols, std::uint32_t qstride) {
+  const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const std::uint32_t per_wave = 32 / (blockDim.x / kWave);
+  const float s = halo::Sigmoid(sgate[0]);
+  for (std::uint32_t k = 0; k < per_wave; ++k) {
+    const std::uint32_t r = blockIdx.x * 32 + wave * per_wave + k;
+    if (r >= rows) break;
+    const float yv = Q8RowDot(dq, dd, hin, r, cols, qstride);
+    if (lane == 0) out[r] += s * yv;
+  }
+}
+
+// halo_router_topk_w for the columns of a batch: column b = blockIdx.y reads logits + b * lstride and writes
+// k ids / weights at b * k. grid (1, B), block 256.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_router_topk_w_y(const float* logits, std::uint32_t* ids, float* weights, std::uint32_t n, std::uint32_t k,
+                         std::uint32_t lstride) {
+  __shared__ std::uint32_t scratch[64];
+  __shared__ float wscratch[64];
+  __shared__ TopKScratch sc;
+  if (threadIdx.x >= kWave) return;
+  const std::size_t b = blockIdx.y;
+  WaveTopK<16>(logits + b * lstride, n, k, ids + b * k, weights + b * k, scratch, wscratch, sc);
+}

@@ -63,6 +63,12 @@
  *     halo_rmsnorm_rows(x, w_all, y, d, eps, w_stride, w_period)                         grid (vectors)
  *     halo_split_qgate_y / halo_rmsnorm_y / halo_rope_neox_p_y / halo_copy_at_y           grid (., B)
  *     halo_axpy_slot, halo_axpy_sigmoid, halo_axpy_sigmoid_rows, halo_scale_silu          grid-stride
+ *   fp32 GEMMs y [T][rows] (core.hip:3767-3800, 5605-5680, 8975-9000): halo_gemm_f32_tiled(w, x, y, rows, cols,
+ *     tokens) grid (ceil(T / 64), ceil(rows / 64)); halo_gemm_f32_rows(w, x, y, rows, cols) grid (ceil(rows / 8), T);
+ *     halo_gemm_f32_narrow(same) grid (ceil(rows / 256), T), cols <= 8192; halo_gemm_f32_skinny(w, x, y, rows, cols,
+ *     tokens) grid (ceil(T / 8)), rows <= 16; all block 256
+ *   halo_shexp_down_add(dq, dd, hin, sgate, out, rows, cols, qstride)  grid ceil(rows / 32)       core.hip:2938
+ *   halo_router_topk_w_y(logits, ids, weights, n, k, lstride)          grid (1, B)       batch_decode.hip:1157
  *   session-union experts (batch_decode.hip:415-446, 646-697):
  *     halo_moe_bucket_b(ids, n, ucount, uexp, unum, upair)              1 block of 128; n <= 128
  *     halo_moe_down_q8r_r4_b{1..8}(qs, d, ucount, uexp, unum, upair, h, part, rows, cols, qstride)
@@ -110,6 +116,8 @@
   X(halo_split_qgate_norm_rope) X(halo_norm_rope_rows) X(halo_rope_neox_blocks) X(halo_rmsnorm_rows)           \
   X(halo_split_qgate_y) X(halo_rmsnorm_y) X(halo_rope_neox_p_y) X(halo_copy_at_y) X(halo_axpy_slot)            \
   X(halo_axpy_sigmoid) X(halo_axpy_sigmoid_rows) X(halo_scale_silu)                                            \
+  X(halo_gemm_f32_tiled) X(halo_gemm_f32_rows) X(halo_gemm_f32_narrow) X(halo_gemm_f32_skinny)              \
+  X(halo_shexp_down_add) X(halo_router_topk_w_y)                                                               \
   X(halo_moe_bucket) X(halo_moe_bucket_count) X(halo_moe_bucket_scan) X(halo_moe_bucket_scatter)               \
   X(halo_gemm_q8r_wmma) X(halo_gemm_q8r_wmma_t) X(halo_gemm_q8a8_128x128) X(halo_gemm_q8a8_128x64)           \
   X(halo_gemm_q8a8_320x64) X(halo_gemm_q8a8_160x64) X(halo_gemm_q8a8_256x128)                                 \

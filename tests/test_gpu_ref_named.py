@@ -710,3 +710,52 @@ def test_small_elementwise(dev):
     gx = dev.to_device(x[0])
     dev.launch("halo_scale_silu", (2,), (256,), [gx, ("f32", 0.25), ("u32", n)])
     close(gx.download(), silu((x[0] * np.float32(0.25)).astype(np.float32)), np.abs(x[0]) + 1e-3)
+
+
+@pytest.mark.parametrize("name", ["halo_gemm_f32_tiled", "halo_gemm_f32_rows", "halo_gemm_f32_narrow",
+                                  "halo_gemm_f32_skinny"])
+def test_f32_gemms(dev, name):
+    """The fp32 prefill GEMMs (core.hip:3767-3800, 5605-5680, 8975-9000) against a float64 product; 1e-5 of
+    sum |term|. Ragged rows and tokens."""
+    rng = np.random.default_rng(57)
+    T, cols = 70, 2048 if name != "halo_gemm_f32_narrow" else 96
+    rows = 13 if name == "halo_gemm_f32_skinny" else 130
+    w = rng.normal(0, 0.02, (rows, cols)).astype(np.float32)
+    x = rng.normal(0, 1, (T, cols)).astype(np.float32)
+    gy = dev.array((T, rows), np.float32)
+    args = [dev.to_device(w), dev.to_device(x), gy, ("u32", rows), ("u32", cols)]
+    if name == "halo_gemm_f32_tiled":
+        dev.launch(name, ((T + 63) // 64, (rows + 63) // 64), (256,), args + [("u32", T)])
+    elif name == "halo_gemm_f32_rows":
+        dev.launch(name, ((rows + 7) // 8, T), (256,), args)
+    elif name == "halo_gemm_f32_narrow":
+        dev.launch(name, ((rows + 255) // 256, T), (256,), args)
+    else:
+        dev.launch(name, ((T + 7) // 8,), (256,), args + [("u32", T)])
+    want = x.astype(np.float64) @ w.astype(np.float64).T
+    close(gy.download(), want, np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T)
+
+
+def test_shexp_down_add_and_topk_y(dev):
+    rng = np.random.default_rng(58)
+    H, F = 2048, 512
+    dq, dd = O.synth_q8(rng, H, F)
+    h = rng.normal(0, 1, F).astype(np.float32)
+    out0 = rng.normal(0, 1, H).astype(np.float32)
+    sg = np.array([0.3], np.float32)
+    go = dev.to_device(out0)
+    dev.launch("halo_shexp_down_add", ((H + 31) // 32,), (256,),
+               [dev.to_device(dq), dev.to_device(dd), dev.to_device(h), dev.to_device(sg), go, ("u32", H), ("u32", F),
+                ("u32", F)])
+    y, ym = _q8_ref(dq, dd, h)
+    close(go.download(), out0 + sig(sg[0]) * y, np.abs(out0) + sig(sg[0]) * ym + 1e-6)
+    B, n, k, lstride = 3, 512, 10, 600
+    logits = rng.normal(0, 2, (B, lstride)).astype(np.float32)
+    gi, gw = dev.array((B, k), np.uint32), dev.array((B, k), np.float32)
+    dev.launch("halo_router_topk_w_y", (1, B), (256,), [dev.to_device(logits), gi, gw, ("u32", n), ("u32", k),
+                                                        ("u32", lstride)])
+    for b in range(B):
+        wi, ww = np.zeros(k, np.uint32), np.zeros(k, np.float32)
+        O.oracle().or_route_topk(np.ascontiguousarray(logits[b, :n]), n, k, wi, ww)
+        assert np.array_equal(gi.download()[b], wi)
+        np.testing.assert_allclose(gw.download()[b], ww, rtol=1e-5)

@@ -176,10 +176,10 @@ extern "C" __global__ void halo_conv_step(const float* in, float* state, const f
 
 // The conv step and, for channels below l2_channels (DeltaNet q and k), the L2 norm over each block's channels (one
 // block per head of blockDim channels, core.hip:3003-3028).
-extern "C" __global__ void halo_conv_l2norm(const float* in, float* state, const float* w, float* out,
-                                            std::uint32_t channels, std::uint32_t kern, std::uint32_t l2_channels,
-                                            float eps) {
-  __shared__ float red[16];
+namespace halo::refk {
+__device__ __forceinline__ void ConvL2norm(const float* in, float* state, const float* w, float* out,
+                                           std::uint32_t channels, std::uint32_t kern, std::uint32_t l2_channels,
+                                           float eps, float* red) {
   const std::uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
   float y = 0.0f;
   if (ch < channels) {
@@ -195,6 +195,13 @@ extern "C" __global__ void halo_conv_l2norm(const float* in, float* state, const
   }
   if (blockIdx.x * blockDim.x < l2_channels) y *= 1.0f / sqrtf(BlockSumAny(y * y, red) + eps);  // block-uniform
   if (ch < channels) out[ch] = y;
+}
+}  // namespace halo::refk
+extern "C" __global__ void halo_conv_l2norm(const float* in, float* state, const float* w, float* out,
+                                            std::uint32_t channels, std::uint32_t kern, std::uint32_t l2_channels,
+                                            float eps) {
+  __shared__ float red[16];
+  ConvL2norm(in, state, w, out, channels, kern, l2_channels, eps, red);
 }
 
 // One Gated DeltaNet decode step, one block per value head h (key head h % num_k_heads), thread j = value column
@@ -1229,4 +1236,34 @@ extern "C" __global__ void __launch_bounds__(256)
   if (threadIdx.x >= kWave) return;
   const std::size_t b = blockIdx.y;
   WaveTopK<16>(logits + b * lstride, n, k, ids + b * k, weights + b * k, scratch, wscratch, sc);
+}
+
+// ---- batched columns through a pointer table (reference names; batch_decode.hip:1727-1748) ----------------------
+// Column e = blockIdx.y: its KV cache (rows kslot, kslot + 1) or conv state (slot tslot) is the pointer
+// tab[e * tstride + slot]; its other data sit `stride` floats apart.
+// grid (num_heads, B), block 256
+extern "C" __global__ void __launch_bounds__(256)
+    halo_attention_select_b_y(const float* q, const std::uint64_t* tab, std::uint32_t tstride, std::uint32_t kslot,
+                              const float* gate, const std::uint32_t* visible, float* out, float* scores,
+                              const std::uint32_t* params, std::uint32_t num_heads, std::uint32_t num_kv_heads,
+                              std::uint32_t hd, std::uint32_t max_n, std::uint32_t q_stride,
+                              std::uint32_t visible_stride, std::uint32_t scores_stride, std::uint32_t pstride) {
+  __shared__ float red[16];
+  const std::size_t e = blockIdx.y;
+  const float* kc = reinterpret_cast<const float*>(tab[e * tstride + kslot]);
+  const float* vc = reinterpret_cast<const float*>(tab[e * tstride + kslot + 1]);
+  const std::uint32_t h = blockIdx.x, kvh = h / (num_heads / num_kv_heads);
+  const std::size_t row = e * q_stride + static_cast<std::size_t>(h) * hd;
+  AttendHead(q + row, kc, vc, gate + row, out + row, scores + e * scores_stride + static_cast<std::size_t>(h) * max_n,
+             kvh, num_kv_heads, hd, params[e * pstride + 5], red, visible + e * visible_stride);
+}
+// grid (channels / 128, B), block 128
+extern "C" __global__ void halo_conv_l2norm_y(const float* in, const std::uint64_t* tab, std::uint32_t tstride,
+                                              std::uint32_t tslot, const float* w, float* out, std::uint32_t channels,
+                                              std::uint32_t kern, std::uint32_t l2_channels, float eps,
+                                              std::uint32_t stride) {
+  __shared__ float red[16];
+  const std::size_t e = blockIdx.y;
+  ConvL2norm(in + e * stride, reinterpret_cast<float*>(tab[e * tstride + tslot]), w, out + e * stride, channels, kern,
+             l2_channels, eps, red);
 }

@@ -69,6 +69,10 @@
  *     tokens) grid (ceil(T / 8)), rows <= 16; all block 256
  *   halo_shexp_down_add(dq, dd, hin, sgate, out, rows, cols, qstride)  grid ceil(rows / 32)       core.hip:2938
  *   halo_router_topk_w_y(logits, ids, weights, n, k, lstride)          grid (1, B)       batch_decode.hip:1157
+ *   halo_attention_select_b_y(q, tab, tstride, kslot, gate, visible, out, scores, params, num_heads, num_kv_heads,
+ *     hd, max_n, q_stride, visible_stride, scores_stride, pstride)  grid (heads, B)    batch_decode.hip:1727
+ *   halo_conv_l2norm_y(in, tab, tstride, tslot, w, out, channels, kern, l2_channels, eps, stride)
+ *                                                                   grid (channels / 128, B)   batch_decode.hip:1741
  *   session-union experts (batch_decode.hip:415-446, 646-697):
  *     halo_moe_bucket_b(ids, n, ucount, uexp, unum, upair)              1 block of 128; n <= 128
  *     halo_moe_down_q8r_r4_b{1..8}(qs, d, ucount, uexp, unum, upair, h, part, rows, cols, qstride)
@@ -117,7 +121,7 @@
   X(halo_split_qgate_y) X(halo_rmsnorm_y) X(halo_rope_neox_p_y) X(halo_copy_at_y) X(halo_axpy_slot)            \
   X(halo_axpy_sigmoid) X(halo_axpy_sigmoid_rows) X(halo_scale_silu)                                            \
   X(halo_gemm_f32_tiled) X(halo_gemm_f32_rows) X(halo_gemm_f32_narrow) X(halo_gemm_f32_skinny)              \
-  X(halo_shexp_down_add) X(halo_router_topk_w_y)                                                               \
+  X(halo_shexp_down_add) X(halo_router_topk_w_y) X(halo_attention_select_b_y) X(halo_conv_l2norm_y)          \
   X(halo_moe_bucket) X(halo_moe_bucket_count) X(halo_moe_bucket_scan) X(halo_moe_bucket_scatter)               \
   X(halo_gemm_q8r_wmma) X(halo_gemm_q8r_wmma_t) X(halo_gemm_q8a8_128x128) X(halo_gemm_q8a8_128x64)           \
   X(halo_gemm_q8a8_320x64) X(halo_gemm_q8a8_160x64) X(halo_gemm_q8a8_256x128)                                 \

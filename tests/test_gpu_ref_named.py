@@ -759,3 +759,56 @@ def test_shexp_down_add_and_topk_y(dev):
         O.oracle().or_route_topk(np.ascontiguousarray(logits[b, :n]), n, k, wi, ww)
         assert np.array_equal(gi.download()[b], wi)
         np.testing.assert_allclose(gw.download()[b], ww, rtol=1e-5)
+
+
+def test_batched_select_and_conv_through_tables(dev):
+    """halo_attention_select_b_y and halo_conv_l2norm_y (batch_decode.hip:1727-1748): each column through its own
+    cache / state pointer equals the single-column kernel on that column, bit for bit."""
+    rng = np.random.default_rng(59)
+    B, Hq, Hkv, hd, npos, max_n = 2, 8, 2, 256, 120, 128
+    qs_ = Hq * hd + 64
+    caches = [(dev.to_device(rng.normal(0, 1, (npos, Hkv, hd)).astype(np.float32)),
+               dev.to_device(rng.normal(0, 1, (npos, Hkv, hd)).astype(np.float32))) for _ in range(B)]
+    tab = np.zeros((B, 4), np.uint64)
+    for e in range(B):
+        tab[e, 1], tab[e, 2] = caches[e][0].ptr, caches[e][1].ptr
+    q = rng.normal(0, 1, (B, qs_)).astype(np.float32)
+    gate = rng.normal(0, 1, (B, qs_)).astype(np.float32)
+    vis = np.zeros((B, max_n), np.uint32)
+    params = np.zeros((B, 16), np.uint32)
+    for e, n in enumerate((77, 120)):
+        vis[e, :n] = rng.choice(npos, n, replace=False)
+        params[e, 5] = n
+    out, sc = dev.array((B, qs_), np.float32), dev.array((B, Hq * max_n), np.float32)
+    dev.launch("halo_attention_select_b_y", (Hq, B), (256,),
+               [dev.to_device(q), dev.to_device(tab), ("u32", 4), ("u32", 1), dev.to_device(gate), dev.to_device(vis),
+                out, sc, dev.to_device(params), ("u32", Hq), ("u32", Hkv), ("u32", hd), ("u32", max_n),
+                ("u32", qs_), ("u32", max_n), ("u32", Hq * max_n), ("u32", 16)])
+    got = out.download()
+    for e in range(B):
+        o1, s1 = dev.array((Hq, hd), np.float32), dev.array((Hq, max_n), np.float32)
+        dev.launch("halo_attention_select_b", (Hq,), (256,),
+                   [dev.to_device(q[e, :Hq * hd]), caches[e][0], caches[e][1], dev.to_device(gate[e, :Hq * hd]),
+                    dev.to_device(vis[e]), o1, s1, dev.to_device(params[e]), ("u32", Hq), ("u32", Hkv), ("u32", hd),
+                    ("u32", max_n)])
+        assert got[e, :Hq * hd].tobytes() == o1.download().tobytes()
+    C, K, d = 512, 4, 128
+    w = rng.normal(0, 0.5, (C, K)).astype(np.float32)
+    st = [rng.normal(0, 1, (K - 1, C)).astype(np.float32) for _ in range(B)]
+    x = rng.normal(0, 1, (B, C + 32)).astype(np.float32)
+    gst = [dev.to_device(s) for s in st]
+    tab = np.zeros((B, 2), np.uint64)
+    for e in range(B):
+        tab[e, 1] = gst[e].ptr
+    go = dev.array((B, C + 32), np.float32)
+    gw = dev.to_device(w)
+    dev.launch("halo_conv_l2norm_y", (C // d, B), (d,), [dev.to_device(x), dev.to_device(tab), ("u32", 2), ("u32", 1),
+                                                        gw, go, ("u32", C), ("u32", K), ("u32", 256), ("f32", 1e-6),
+                                                        ("u32", C + 32)])
+    got = go.download()
+    for e in range(B):
+        s1, o1 = dev.to_device(st[e]), dev.array((C,), np.float32)
+        dev.launch("halo_conv_l2norm", (C // d,), (d,), [dev.to_device(x[e, :C]), s1, gw, o1, ("u32", C), ("u32", K),
+                                                         ("u32", 256), ("f32", 1e-6)])
+        assert got[e, :C].tobytes() == o1.download().tobytes()
+        assert gst[e].download().tobytes() == s1.download().tobytes()

@@ -67,7 +67,10 @@ int halo_op_attn_decode_q8(halo_engine* eng, const halo_paged_kv* kv, const floa
   }
   const halo_arg a[] = {Ptr(pm), Ptr(pl), Ptr(pacc), Ptr(gate), Ptr(o), Ptr(oq), Ptr(os), U32(S), U32(Hq), U32(Hkv),
                         U32(pc), U32(sc)};
-  return Launch(eng, "halo_attn_decode_combine", D3(S * Hq * 4), D3(256), a, err, errlen);
+  // small batches split each head into 8 dim slices instead of 4: twice the blocks, twice the loads in flight
+  const bool eighths = S * Hq * 4 < 256;
+  return Launch(eng, eighths ? "halo_attn_decode_combine8" : "halo_attn_decode_combine", D3(S * Hq * (eighths ? 8 : 4)),
+                D3(256), a, err, errlen);
 }
 
 int halo_op_attn_decode(halo_engine* eng, const halo_paged_kv* kv, const float* q, const float* gate, float* o,

@@ -129,20 +129,23 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
   }
 }
 
-// grid (S * Hq * 4), block 256: block (s, h, quarter) merges the partials of session s, head h over its prefix and
-// suffix chunks (log-sum-exp) for dims [64 quarter, 64 quarter + 64): o = acc / l, then o *= sigmoid(gate) when gate
-// is non-null. o, gate [S][Hq][256] (o may be null); with oq non-null also the Q8 quantization of o (oq
-// [S][Hq * 256], os [S][Hq * 8]). At most 1024 items. Thread: float4 lane f = t % 16 of the slice, items
-// i = t / 16 (mod 16), eight loads in flight.
-extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_combine(
+// grid (S * Hq * NS), block 256: block (s, h, slice) merges the partials of session s, head h over its prefix and
+// suffix chunks (log-sum-exp) for the slice's 256 / NS dims: o = acc / l, then o *= sigmoid(gate) when gate is
+// non-null. o, gate [S][Hq][256] (o may be null); with oq non-null also the Q8 quantization of o (oq [S][Hq * 256],
+// os [S][Hq * 8]). At most 1024 items. Thread: float4 lane f of the slice, item group t / (lanes per slice), eight
+// loads in flight. NS = 8 doubles the blocks of small batches (more loads in flight over the chip).
+namespace {
+template <int NS>
+__device__ __forceinline__ void AttnDecodeCombine(
     const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ pacc,
     const float* __restrict__ gate, float* __restrict__ o, std::int8_t* __restrict__ oq, float* __restrict__ os,
     std::uint32_t S, std::uint32_t Hq, std::uint32_t Hkv, std::uint32_t prefix_chunks,
     std::uint32_t suffix_chunks) {
+  constexpr std::uint32_t kW = kHd / NS, kF = kW / 4, kG = 256 / kF;  // slice dims, float4 lanes, item groups
   __shared__ float wts[1024];
   __shared__ float red[4];
-  __shared__ float4 part[16][16];
-  const std::uint32_t quarter = blockIdx.x % 4, sh = blockIdx.x / 4;
+  __shared__ float4 part[kG][kF];
+  const std::uint32_t quarter = blockIdx.x % NS, sh = blockIdx.x / NS;
   const std::uint32_t G = Hq / Hkv, s = sh / Hq, h = sh % Hq, kvh = h / G, g = h % G;
   const std::uint32_t slot = s * G + g, slots = S * G, t = threadIdx.x;
   const std::uint32_t n = min(prefix_chunks + suffix_chunks, 1024u);
@@ -172,19 +175,19 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_combine(
   if (t % kWave == 0) red[t / kWave] = L;
   __syncthreads();
   L = (red[0] + red[1]) + (red[2] + red[3]);
-  const std::uint32_t f = t % 16, ig = t / 16;
+  const std::uint32_t f = t % kF, ig = t / kF;
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   constexpr int kU = 8;
-  for (std::uint32_t i0 = ig; i0 < n; i0 += 16 * kU) {
+  for (std::uint32_t i0 = ig; i0 < n; i0 += kG * kU) {
     float4 a[kU];
     float w[kU];
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-      const std::uint32_t i = i0 + 16 * u;
+      const std::uint32_t i = i0 + kG * u;
       const float wi = wts[min(i, n - 1)];
       w[u] = i < n ? wi : 0.0f;
       // load unconditionally (clamped item), then select: an empty chunk's partial is never written
-      const float4 av = reinterpret_cast<const float4*>(pacc + (item(min(i, n - 1)) * slots + slot) * kHd)[quarter * 16 + f];
+      const float4 av = reinterpret_cast<const float4*>(pacc + (item(min(i, n - 1)) * slots + slot) * kHd)[quarter * kF + f];
       a[u] = w[u] == 0.0f ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : av;
     }
 #pragma unroll
@@ -197,13 +200,13 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_combine(
   }
   part[ig][f] = acc;
   __syncthreads();
-  if (t >= kWave) return;
-  // wave 0: lane = dim of the slice
+  if (t >= kW) return;
+  // lane = dim of the slice
   float sum = 0.0f;
 #pragma unroll
-  for (int k = 0; k < 16; ++k) sum += reinterpret_cast<const float*>(&part[k][0])[t];
+  for (std::uint32_t k = 0; k < kG; ++k) sum += reinterpret_cast<const float*>(&part[k][0])[t];
   float r = sum / L;
-  const std::size_t off = (static_cast<std::size_t>(s) * Hq + h) * kHd + quarter * 64 + t;
+  const std::size_t off = (static_cast<std::size_t>(s) * Hq + h) * kHd + quarter * kW + t;
   if (gate != nullptr) r *= halo::Sigmoid(gate[off]);
   if (o != nullptr) o[off] = r;
   if (oq != nullptr) {
@@ -214,6 +217,19 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_combine(
     if (t % 32 == 0) os[off / 32] = scale;
   }
 }
+}  // namespace
+
+#define HALO_ATTN_COMBINE(NAME, NS)                                                                              \
+  extern "C" __global__ void __launch_bounds__(256) NAME(                                                       \
+      const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ pacc,               \
+      const float* __restrict__ gate, float* __restrict__ o, std::int8_t* __restrict__ oq, float* __restrict__ os, \
+      std::uint32_t S, std::uint32_t Hq, std::uint32_t Hkv, std::uint32_t prefix_chunks,                         \
+      std::uint32_t suffix_chunks) {                                                                             \
+    AttnDecodeCombine<NS>(pm, pl, pacc, gate, o, oq, os, S, Hq, Hkv, prefix_chunks, suffix_chunks);             \
+  }
+HALO_ATTN_COMBINE(halo_attn_decode_combine, 4)
+HALO_ATTN_COMBINE(halo_attn_decode_combine8, 8)
+#undef HALO_ATTN_COMBINE
 
 // Appends one token's K and V per session at position nkv[s] - 1: k, v [S][Hkv][256] -> pools via page tables.
 // grid (S * Hkv), block 64 (a float4 per lane).

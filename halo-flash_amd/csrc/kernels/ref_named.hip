@@ -1267,3 +1267,49 @@ extern "C" __global__ void halo_conv_l2norm_y(const float* in, const std::uint64
   ConvL2norm(in + e * stride, reinterpret_cast<float*>(tab[e * tstride + tslot]), w, out + e * stride, channels, kern,
              l2_channels, eps, red);
 }
+
+// halo_conv_l2norm_prefill for kern = 4 with eight tokens per thread (core.hip:3512-3570): the window x[t - 3 .. t]
+// loaded once for all eight, the sums in the stepping order. grid (channels / 128, ceil(T / 8)), block 128 (a head).
+extern "C" __global__ void __launch_bounds__(128)
+    halo_conv_l2norm_prefill8(const float* in, const float* state, const float* w, float* out, std::uint32_t channels,
+                              std::uint32_t tokens, std::uint32_t l2_channels, float eps) {
+  constexpr std::uint32_t TT = 8, K = 4;
+  __shared__ float part[TT][2];
+  const std::uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x, t0 = blockIdx.y * TT;
+  const std::uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const bool live = ch < channels;
+  const std::uint32_t c = live ? ch : 0;
+  float x[TT + K - 1];  // inputs t0 - 3 .. t0 + 7, from the chunk or, before it, the conv state
+#pragma unroll
+  for (std::uint32_t j = 0; j < TT + K - 1; ++j) {
+    const std::int64_t i = static_cast<std::int64_t>(t0) - static_cast<std::int64_t>(K - 1) + j;
+    x[j] = i >= static_cast<std::int64_t>(tokens) ? 0.0f
+           : i >= 0 ? in[static_cast<std::size_t>(i) * channels + c]
+                    : state[static_cast<std::size_t>(i + K - 1) * channels + c];
+  }
+  const float* wc = w + static_cast<std::size_t>(c) * K;
+  const float w0 = wc[0], w1 = wc[1], w2 = wc[2], w3 = wc[3];
+  float v[TT];
+#pragma unroll
+  for (std::uint32_t t = 0; t < TT; ++t) {
+    float acc = w3 * x[t + 3];
+    acc += w0 * x[t];
+    acc += w1 * x[t + 1];
+    acc += w2 * x[t + 2];
+    v[t] = live ? halo::Silu(acc) : 0.0f;
+  }
+  if (blockIdx.x * blockDim.x < l2_channels) {  // block-uniform
+#pragma unroll
+    for (std::uint32_t t = 0; t < TT; ++t) {
+      const float s = halo::GroupSum(v[t] * v[t]);
+      if (lane == 0) part[t][wave] = s;
+    }
+    __syncthreads();
+#pragma unroll
+    for (std::uint32_t t = 0; t < TT; ++t) v[t] *= 1.0f / sqrtf(part[t][0] + part[t][1] + eps);
+  }
+  if (!live) return;
+#pragma unroll
+  for (std::uint32_t t = 0; t < TT; ++t)
+    if (t0 + t < tokens) out[static_cast<std::size_t>(t0 + t) * channels + ch] = v[t];
+}

@@ -52,6 +52,8 @@
  *     halo_gdn_prefill_d128_norm(..., tokens, qk_stride, v_stride, zo_stride)   grid (v heads), block 128
  *     halo_conv_l2norm_prefill(in, state, w, out, channels, kern, l2_channels, eps)   grid (heads, T), block d
  *     halo_conv_state_advance(in, state, channels, kern, tokens)        grid ceil(channels / 256)
+ *     halo_conv_l2norm_prefill8(in, state, w, out, channels, tokens, l2_channels, eps)   kern 4; grid (channels / 128,
+ *       ceil(T / 8)), block 128
  *     halo_shexp_gate_up{,_u}(gq, gd, uq, ud, gate_inp, x, h, sgate, rows, cols, qstride)   grid ceil(rows / 16)
  *     halo_shexp_down_combine{,_u}(dq, dd, hin, sgate, part, weights, slots, out, rows, cols, qstride)
  *                                                                       grid ceil(rows / 32)
@@ -114,7 +116,7 @@
   X(halo_matvec_f32_rowblock2_u) X(halo_quantize_q8_kblocked) X(halo_router_topk_w)                          \
   X(halo_attention_select) X(halo_attention_select_b) X(halo_attention_select_rows)                           \
   X(halo_gdn_step_d128_norm_r) X(halo_gdn_prefill_d128_norm) X(halo_conv_l2norm_prefill)                      \
-  X(halo_conv_state_advance) X(halo_shexp_gate_up) X(halo_shexp_gate_up_u) X(halo_shexp_down_combine)         \
+  X(halo_conv_state_advance) X(halo_conv_l2norm_prefill8) X(halo_shexp_gate_up) X(halo_shexp_gate_up_u) X(halo_shexp_down_combine)         \
   X(halo_shexp_down_combine_u) X(halo_router_rowblock_q8act)                                                  \
   X(halo_moe_bucket_b) X(halo_moe_down_q8r_r4_b1) X(halo_moe_down_q8r_r4_b4) X(halo_moe_down_q8r_r4_b8)         \
   X(halo_split_qgate_norm_rope) X(halo_norm_rope_rows) X(halo_rope_neox_blocks) X(halo_rmsnorm_rows)           \

@@ -812,3 +812,26 @@ def test_batched_select_and_conv_through_tables(dev):
                                                          ("u32", 256), ("f32", 1e-6)])
         assert got[e, :C].tobytes() == o1.download().tobytes()
         assert gst[e].download().tobytes() == s1.download().tobytes()
+
+
+@pytest.mark.parametrize("T", [13, 2])
+def test_conv_prefill8(dev, T):
+    """halo_conv_l2norm_prefill8 (kern 4, eight tokens per thread; core.hip:3512-3570) against numpy: causal conv
+    over the state then the chunk, SiLU, the first two heads L2-normalised; 1e-5 of the terms' magnitude."""
+    rng = np.random.default_rng(60 + T)
+    C, K, d, l2 = 512, 4, 128, 256
+    w = rng.normal(0, 0.5, (C, K)).astype(np.float32)
+    st = rng.normal(0, 1, (K - 1, C)).astype(np.float32)
+    x = rng.normal(0, 1, (T, C)).astype(np.float32)
+    go = dev.array((T, C), np.float32)
+    dev.launch("halo_conv_l2norm_prefill8", (C // d, (T + 7) // 8), (d,),
+               [dev.to_device(x), dev.to_device(st), dev.to_device(w), go, ("u32", C), ("u32", T), ("u32", l2),
+                ("f32", 1e-6)])
+    seq = np.concatenate([st, x]).astype(np.float64)
+    conv = np.stack([(seq[t:t + K] * w.T).sum(0) for t in range(T)])
+    y = silu(conv.astype(np.float32))
+    for h in range(l2 // d):
+        seg = y[:, h * d:(h + 1) * d]
+        y[:, h * d:(h + 1) * d] = seg / np.sqrt((seg * seg).sum(1, keepdims=True) + 1e-6)
+    mag = np.stack([(np.abs(seq[t:t + K] * w.T)).sum(0) for t in range(T)]) + 1e-3
+    close(go.download(), y, mag)

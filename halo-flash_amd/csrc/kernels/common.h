@@ -86,6 +86,35 @@ __device__ __forceinline__ int GroupSumI(int v) {
          (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
 }
 
+// Sum / max over groups of 8 consecutive lanes (two DPP quad swaps, then the half-row mirror that pairs quad 0 with
+// quad 1 of each 8). Both lanes of every pair add the same two operands, so all 8 lanes hold identical bits.
+__device__ __forceinline__ float Group8Sum(float v) {
+  v += Dpp<0xB1>(v);
+  v += Dpp<0x4E>(v);
+  return v + Dpp<0x141>(v);
+}
+__device__ __forceinline__ float Group8Max(float v) {
+  v = fmaxf(v, Dpp<0xB1>(v));
+  v = fmaxf(v, Dpp<0x4E>(v));
+  return fmaxf(v, Dpp<0x141>(v));
+}
+
+// Q8_0 quantization of a 32-value block spread over 8 consecutive lanes, 4 values per lane (lane 8g + i holds values
+// 4i .. 4i + 3 of block g): scale = amax / 127 (IEEE divide), code = rint(v / scale) (round half to even; 0 when the
+// block is all zero). Returns the lane's 4 codes packed little-endian into one word; every lane of the 8 gets scale.
+__device__ __forceinline__ std::uint32_t QuantQuad(const float4& v, float& scale) {
+  const float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  scale = Group8Max(m) / 127.0f;
+  const float e[4] = {v.x, v.y, v.z, v.w};
+  std::uint32_t word = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = scale > 0.0f ? static_cast<int>(rintf(e[i] / scale)) : 0;
+    word |= (static_cast<std::uint32_t>(q) & 0xFFu) << (8 * i);
+  }
+  return word;
+}
+
 // Block-wide reductions; `scratch` holds one float per wave. Every thread of the block must call them.
 __device__ __forceinline__ float BlockSum(float v, float* scratch) {
   v = GroupSum(v);

@@ -18,22 +18,26 @@ using halo::kWave;
 // ---- fp32 GEMM for the router: C[t][n] = sum_k X[t][k] W[n][k] -----------------------------------------------------
 // On v_mfma_f32_32x32x2f32. grid (ceil((N + 1) / 64), ceil(T / 64)), block 256: a 64-token x 64-row tile, wave
 // (wt, wn) a 32 x 32 sub-tile; K in stages of 32 through LDS (rows padded to 36 floats: the 16-byte reads are
-// conflict-free). Within a stage, MFMA step s takes k = s from lanes 0-31 and k = 16 + s from lanes 32-63 (any k
-// split shared by both operands sums the same products). The result lane l holds row n = l % 32 of its sub-tile and
-// tokens 8 (j / 4) + 4 (l / 32) + j % 4. C [T][ldc] for rows n < N of W; when wlast is non-null it is one more row,
-// whose products go to clast [T] (the shared-gate logit next to the router logits). K % 32 == 0.
+// conflict-free); K % 4 == 0, a trailing partial stage reads zeros. Within a stage, MFMA step s takes k = s from
+// lanes 0-31 and k = 16 + s from lanes 32-63 (any k split shared by both operands sums the same products). The
+// result lane l holds row n = l % 32 of its sub-tile and tokens 8 (j / 4) + 4 (l / 32) + j % 4. C [T][ldc] for rows n < N of W; when wlast is non-null it is one more row,
+// whose products go to clast [T] (the shared-gate logit next to the router logits).
 namespace {
 typedef float V16F32R __attribute__((ext_vector_type(16)));
 }
-extern "C" __global__ void __launch_bounds__(256) halo_gemm_f32_nt(
-    const float* __restrict__ X, const float* __restrict__ W, const float* __restrict__ wlast, float* __restrict__ Cm,
-    float* __restrict__ clast, std::uint32_t T, std::uint32_t N, std::uint32_t K, std::uint32_t ldc) {
+namespace halo {
+// One 64 x 64 tile at rows n0 and tokens t0; K % 4 == 0 (k past K reads as zero: a trailing partial stage adds
+// nothing). Every thread of the 256 must call it.
+__device__ __forceinline__ void GemmF32NtTile(const float* __restrict__ X, const float* __restrict__ W,
+                                              const float* __restrict__ wlast, float* __restrict__ Cm,
+                                              float* __restrict__ clast, std::uint32_t T, std::uint32_t N,
+                                              std::uint32_t K, std::uint32_t ldc, std::uint32_t n0,
+                                              std::uint32_t t0) {
   constexpr int kLd = 36;
   __shared__ __attribute__((aligned(16))) float xl[64][kLd];
   __shared__ __attribute__((aligned(16))) float wl[64][kLd];
   const std::uint32_t tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const std::uint32_t wt = wave / 2, wn = wave % 2;
-  const std::uint32_t n0 = blockIdx.x * 64, t0 = blockIdx.y * 64;
   const std::uint32_t NN = N + (wlast != nullptr ? 1u : 0u);
   // stage loads: 64 rows x 32 k per operand = 512 float4, two per thread (row c / 8, k 4 (c % 8))
   const float* gx[2];
@@ -44,14 +48,19 @@ extern "C" __global__ void __launch_bounds__(256) halo_gemm_f32_nt(
     const std::uint32_t c = tid + 256u * i;
     lr[i] = c / 8;
     lk[i] = 4 * (c % 8);
-    gx[i] = X + static_cast<std::size_t>(min(t0 + lr[i], T - 1)) * K + lk[i];
+    gx[i] = X + static_cast<std::size_t>(min(t0 + lr[i], T - 1)) * K;
     const std::uint32_t nr = min(n0 + lr[i], NN - 1);
-    gw[i] = (nr < N ? W + static_cast<std::size_t>(nr) * K : wlast) + lk[i];
+    gw[i] = nr < N ? W + static_cast<std::size_t>(nr) * K : wlast;
   }
+  // 4 values at k = k0 + lk of a row; past K they read as zero (from a clamped, in-bounds address)
+  const auto ld = [K](const float* row, std::uint32_t k) {
+    const float4 v = *reinterpret_cast<const float4*>(row + min(k, K - 4));
+    return k < K ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  };
   V16F32R acc = {};
   // next stage's operands (the last stage reloads its own rows: in bounds, unused)
-  float4 rx0 = *reinterpret_cast<const float4*>(gx[0]), rx1 = *reinterpret_cast<const float4*>(gx[1]);
-  float4 rw0 = *reinterpret_cast<const float4*>(gw[0]), rw1 = *reinterpret_cast<const float4*>(gw[1]);
+  float4 rx0 = ld(gx[0], lk[0]), rx1 = ld(gx[1], lk[1]);
+  float4 rw0 = ld(gw[0], lk[0]), rw1 = ld(gw[1], lk[1]);
   const std::uint32_t fr = lane % 32, fh = 16 * (lane / 32);
   for (std::uint32_t k0 = 0; k0 < K; k0 += 32) {
     *reinterpret_cast<float4*>(&xl[lr[0]][lk[0]]) = rx0;
@@ -60,10 +69,10 @@ extern "C" __global__ void __launch_bounds__(256) halo_gemm_f32_nt(
     *reinterpret_cast<float4*>(&wl[lr[1]][lk[1]]) = rw1;
     __syncthreads();
     const std::uint32_t kn = k0 + 32 < K ? k0 + 32 : k0;
-    rx0 = *reinterpret_cast<const float4*>(gx[0] + kn);
-    rx1 = *reinterpret_cast<const float4*>(gx[1] + kn);
-    rw0 = *reinterpret_cast<const float4*>(gw[0] + kn);
-    rw1 = *reinterpret_cast<const float4*>(gw[1] + kn);
+    rx0 = ld(gx[0], kn + lk[0]);
+    rx1 = ld(gx[1], kn + lk[1]);
+    rw0 = ld(gw[0], kn + lk[0]);
+    rw1 = ld(gw[1], kn + lk[1]);
     float a[16], b[16];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -83,6 +92,13 @@ extern "C" __global__ void __launch_bounds__(256) halo_gemm_f32_nt(
     if (t < T && n < N) Cm[static_cast<std::size_t>(t) * ldc + n] = acc[j];
     if (t < T && n == N && wlast != nullptr) clast[t] = acc[j];
   }
+}
+}  // namespace halo
+
+extern "C" __global__ void __launch_bounds__(256) halo_gemm_f32_nt(
+    const float* __restrict__ X, const float* __restrict__ W, const float* __restrict__ wlast, float* __restrict__ Cm,
+    float* __restrict__ clast, std::uint32_t T, std::uint32_t N, std::uint32_t K, std::uint32_t ldc) {
+  halo::GemmF32NtTile(X, W, wlast, Cm, clast, T, N, K, ldc, blockIdx.x * 64, blockIdx.y * 64);
 }
 
 // ---- grouping of (token, slot) pairs by expert --------------------------------------------------------------------

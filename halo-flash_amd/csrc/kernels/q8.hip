@@ -15,86 +15,79 @@ using halo::F16;
 using halo::kWave;
 
 // ---- repack ------------------------------------------------------------------------------------------------
-// reference src/kernels/core.hip:2126-2138. Grid-stride over 34-byte blocks; a thread copies one block.
+// reference src/kernels/core.hip:2126-2138. One thread per 16-byte output vector (half a Q8_0 block): the 16 codes
+// are read as eight 2-byte words (a 34-byte block is only 2-byte aligned) and written as one int4; the thread of the
+// first half also moves the block's fp16 scale. Grid-stride over rows * (cols / 16) vectors.
 extern "C" __global__ void __launch_bounds__(256)
     halo_repack_q8_0(const std::uint8_t* raw, std::int8_t* qs, std::uint16_t* d, std::uint32_t rows,
                      std::uint32_t cols, std::uint32_t qstride) {
-  const std::uint32_t blocks = cols / 32;
-  const std::uint64_t total = static_cast<std::uint64_t>(rows) * blocks;
-  for (std::uint64_t b = blockIdx.x * static_cast<std::uint64_t>(blockDim.x) + threadIdx.x; b < total;
-       b += static_cast<std::uint64_t>(gridDim.x) * blockDim.x) {
-    const std::uint64_t r = b / blocks, k = b % blocks;
-    const std::uint8_t* src = raw + (r * blocks + k) * 34;
-    d[r * blocks + k] = static_cast<std::uint16_t>(src[0] | (src[1] << 8));
-    // 34-byte blocks are only 2-byte aligned: read halves, write 16-byte vectors.
-    std::uint16_t h[16];
+  const std::uint64_t halves_per_row = cols / 16, n = halves_per_row * rows;
+  for (std::uint64_t v = blockIdx.x * static_cast<std::uint64_t>(blockDim.x) + threadIdx.x; v < n;
+       v += static_cast<std::uint64_t>(gridDim.x) * blockDim.x) {
+    const std::uint64_t row = v / halves_per_row, h = v % halves_per_row, blk = row * (cols / 32) + h / 2;
+    const std::uint16_t* src = reinterpret_cast<const std::uint16_t*>(raw + blk * 34);  // [scale][16 code pairs]
+    std::uint32_t w[4];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) h[i] = reinterpret_cast<const std::uint16_t*>(src + 2)[i];
-    int4 lo, hi;
-    lo.x = h[0] | (h[1] << 16);
-    lo.y = h[2] | (h[3] << 16);
-    lo.z = h[4] | (h[5] << 16);
-    lo.w = h[6] | (h[7] << 16);
-    hi.x = h[8] | (h[9] << 16);
-    hi.y = h[10] | (h[11] << 16);
-    hi.z = h[12] | (h[13] << 16);
-    hi.w = h[14] | (h[15] << 16);
-    int4* dst = reinterpret_cast<int4*>(qs + r * qstride + k * 32);
-    dst[0] = lo;
-    dst[1] = hi;
+    for (int i = 0; i < 4; ++i)
+      w[i] = static_cast<std::uint32_t>(src[1 + 8 * (h & 1) + 2 * i]) |
+             (static_cast<std::uint32_t>(src[2 + 8 * (h & 1) + 2 * i]) << 16);
+    *reinterpret_cast<int4*>(qs + row * qstride + 16 * h) =
+        make_int4(static_cast<int>(w[0]), static_cast<int>(w[1]), static_cast<int>(w[2]), static_cast<int>(w[3]));
+    if ((h & 1) == 0) d[blk] = src[0];
   }
 }
 
 // ---- activation quantizer -----------------------------------------------------------------------------------
-namespace {
-// One 32-value block per half wave. Division is IEEE (the code object is built with correctly rounded fp32
-// divide); rintf is round-half-to-even.
-__device__ __forceinline__ void QuantizeBlock32(const float* x, std::int8_t* xq, float* xs, std::uint32_t blk) {
-  const std::uint32_t lane = threadIdx.x % 32;
-  const float v = x[blk * 32 + lane];
-  const float amax = halo::GroupMax<32>(fabsf(v));
-  const float scale = amax / 127.0f;
-  const int q = scale > 0.0f ? static_cast<int>(rintf(v / scale)) : 0;
-  xq[blk * 32 + lane] = static_cast<std::int8_t>(q);
-  if (lane == 0) xs[blk] = scale;
-}
-}  // namespace
-
 // reference src/kernels/core.hip:3089-3101. grid (T), any multiple of 64 threads; x [T][cols] -> xq [T][cols],
-// xd [T][cols / 32].
+// xd [T][cols / 32]. A lane quantizes 4 values from one 16-byte load, 8 lanes per Q8_0 block (halo::QuantQuad: IEEE
+// divide, round half to even), and stores its 4 codes as one word.
 extern "C" __global__ void __launch_bounds__(256)
     halo_quantize_q8_rows(const float* x, std::int8_t* xq, float* xd, std::uint32_t cols) {
   const std::size_t t = blockIdx.x;
-  for (std::uint32_t blk = threadIdx.x / 32; blk < cols / 32; blk += blockDim.x / 32)
-    QuantizeBlock32(x + t * cols, xq + t * cols, xd + t * (cols / 32), blk);
+  const float4* row = reinterpret_cast<const float4*>(x + t * cols);
+  std::uint32_t* codes = reinterpret_cast<std::uint32_t*>(xq + t * cols);
+  for (std::uint32_t g = threadIdx.x; g < cols / 4; g += blockDim.x) {  // 8-lane groups stay whole (cols % 32)
+    float scale;
+    codes[g] = halo::QuantQuad(row[g], scale);
+    if (g % 8 == 0) xd[t * (cols / 32) + g / 8] = scale;
+  }
 }
 
 // reference src/kernels/batch_decode.hip:201-222. Grid (ceil(cols / 256), B), 256 threads: x column b at
-// x + b * xstride -> xq + b * cols, xs + b * cols / 32; with xq2 the residual x - q * s is quantized again.
+// x + b * xstride -> xq + b * cols, xs + b * cols / 32; with xq2 the residual x - q * s (product rounded before the
+// subtraction) is quantized again into xq2 / xs2. The block's 256 values go to its first wave, 4 values per lane
+// (16-byte loads when the column is aligned), 8 lanes per Q8_0 block (QuantQuad); codes are stored a word per lane.
 extern "C" __global__ void __launch_bounds__(256)
     halo_q8x_cols(const float* x, std::uint32_t xstride, std::uint32_t cols, std::int8_t* xq, float* xs,
                   std::int8_t* xq2, float* xs2) {
-  const std::uint32_t b = blockIdx.y, lane = threadIdx.x % 32, nblk = cols / 32;
-  const std::uint32_t blk = blockIdx.x * (blockDim.x / 32) + threadIdx.x / 32;
-  if (blk >= nblk) return;  // whole half waves exit together
-  const float v = x[static_cast<std::size_t>(b) * xstride + blk * 32 + lane];
-  const float amax = halo::GroupMax<32>(fabsf(v));
-  const float scale = amax / 127.0f;
-  const int qv = scale > 0.0f ? static_cast<int>(rintf(v / scale)) : 0;
-  xq[static_cast<std::size_t>(b) * cols + blk * 32 + lane] = static_cast<std::int8_t>(qv);
-  if (lane == 0) xs[static_cast<std::size_t>(b) * nblk + blk] = scale;
+  if (threadIdx.x >= kWave) return;
+  const std::size_t b = blockIdx.y;
+  const std::uint32_t nblk = cols / 32, c = blockIdx.x * 256 + threadIdx.x * 4;
+  if (c >= cols) return;  // groups of 8 lanes leave together (cols % 32 == 0)
+  const float* src = x + b * xstride + c;
+  float4 v;
+  if ((reinterpret_cast<std::uintptr_t>(src) & 15u) == 0) {
+    v = *reinterpret_cast<const float4*>(src);
+  } else {
+    v = make_float4(src[0], src[1], src[2], src[3]);
+  }
+  float s1;
+  const std::uint32_t w1 = halo::QuantQuad(v, s1);
+  *reinterpret_cast<std::uint32_t*>(xq + b * cols + c) = w1;
+  const bool lead = threadIdx.x % 8 == 0;
+  if (lead) xs[b * nblk + c / 32] = s1;
   if (!xq2) return;
-  // r = v - q * s with the product rounded first (no fused multiply-add), as the residual is defined.
-  float r;
+  float4 r;
   {
 #pragma clang fp contract(off)
-    r = v - static_cast<float>(qv) * scale;
+    r.x = v.x - static_cast<float>(static_cast<std::int8_t>(w1)) * s1;
+    r.y = v.y - static_cast<float>(static_cast<std::int8_t>(w1 >> 8)) * s1;
+    r.z = v.z - static_cast<float>(static_cast<std::int8_t>(w1 >> 16)) * s1;
+    r.w = v.w - static_cast<float>(static_cast<std::int8_t>(w1 >> 24)) * s1;
   }
-  const float rmax = halo::GroupMax<32>(fabsf(r));
-  const float s2 = rmax / 127.0f;
-  const int q2 = s2 > 0.0f ? static_cast<int>(rintf(r / s2)) : 0;
-  xq2[static_cast<std::size_t>(b) * cols + blk * 32 + lane] = static_cast<std::int8_t>(q2);
-  if (lane == 0) xs2[static_cast<std::size_t>(b) * nblk + blk] = s2;
+  float s2;
+  *reinterpret_cast<std::uint32_t*>(xq2 + b * cols + c) = halo::QuantQuad(r, s2);
+  if (lead) xs2[b * nblk + c / 32] = s2;
 }
 
 // ---- int8-activation GEMV ------------------------------------------------------------------------------------

@@ -30,6 +30,47 @@ __device__ __forceinline__ float BlockMaxAny(float v, float* red) {
   return r;
 }
 
+// Row normalisation helpers shared by the norm kernels: one block per row of d values. Both passes use 16-byte
+// accesses when the row and d allow them (scalar otherwise); the sum of squares keeps two fused chains per thread
+// (even / odd lanes of each float4) and then BlockSumAny. Every read of the first pass precedes the block sum's
+// barriers, so the second pass may write in place.
+__device__ __forceinline__ bool Vec4Ok(const void* p, std::uint32_t d) {
+  return (d & 3u) == 0 && (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0;
+}
+__device__ __forceinline__ float RowSumSq(const float* v, std::uint32_t d, float* red) {
+  float a0 = 0.0f, a1 = 0.0f;
+  if (Vec4Ok(v, d)) {
+    const float4* v4 = reinterpret_cast<const float4*>(v);
+    for (std::uint32_t i = threadIdx.x; i < d / 4; i += blockDim.x) {
+      const float4 f = v4[i];
+      a0 = __builtin_fmaf(f.x, f.x, a0);
+      a1 = __builtin_fmaf(f.y, f.y, a1);
+      a0 = __builtin_fmaf(f.z, f.z, a0);
+      a1 = __builtin_fmaf(f.w, f.w, a1);
+    }
+  } else {
+    for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) a0 = __builtin_fmaf(v[i], v[i], a0);
+  }
+  return BlockSumAny(a0 + a1, red);
+}
+// y[i] = fn(i, x[i]) for i < d.
+template <typename Fn>
+__device__ __forceinline__ void RowApply(const float* x, float* y, std::uint32_t d, Fn fn) {
+  if (Vec4Ok(x, d) && Vec4Ok(y, d)) {
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    float4* y4 = reinterpret_cast<float4*>(y);
+    for (std::uint32_t i = threadIdx.x; i < d / 4; i += blockDim.x) {
+      const float4 f = x4[i];
+      y4[i] = make_float4(fn(4 * i, f.x), fn(4 * i + 1, f.y), fn(4 * i + 2, f.z), fn(4 * i + 3, f.w));
+    }
+  } else {
+    for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) y[i] = fn(i, x[i]);
+  }
+}
+__device__ __forceinline__ float RmsScale(const float* v, std::uint32_t d, float eps, float* red) {
+  return 1.0f / sqrtf(RowSumSq(v, d, red) / static_cast<float>(d) + eps);
+}
+
 // NEOX rotation of the first rotary_dim values of one head: pairs (i, i + rotary_dim / 2) rotate by
 // pos * theta^(-2 i / rotary_dim).
 __device__ __forceinline__ void RotateHead(float* v, std::uint32_t rotary_dim, std::uint32_t pos, float theta) {
@@ -87,23 +128,18 @@ using namespace halo::refk;
 extern "C" __global__ void halo_rmsnorm(const float* x, const float* w_all, float* y, std::uint32_t d, float eps,
                                         std::uint32_t w_stride) {
   __shared__ float red[16];
-  const float* xv = x + static_cast<std::size_t>(blockIdx.x) * d;
-  const float* w = w_all + static_cast<std::size_t>(blockIdx.x) * w_stride;
-  float* yv = y + static_cast<std::size_t>(blockIdx.x) * d;
-  float ss = 0.0f;
-  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) ss += xv[i] * xv[i];
-  const float inv = 1.0f / sqrtf(BlockSumAny(ss, red) / static_cast<float>(d) + eps);
-  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) yv[i] = xv[i] * inv * w[i];
+  const std::size_t b = blockIdx.x;
+  const float* w = w_all + b * w_stride;
+  const float inv = RmsScale(x + b * d, d, eps, red);
+  RowApply(x + b * d, y + b * d, d, [&](std::uint32_t i, float v) { return v * inv * w[i]; });
 }
 
 // x_b /= sqrt(sum x_b^2 + eps) in place, one block per vector (core.hip:265).
 extern "C" __global__ void halo_l2norm(float* x, std::uint32_t d, float eps) {
   __shared__ float red[16];
   float* xv = x + static_cast<std::size_t>(blockIdx.x) * d;
-  float ss = 0.0f;
-  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) ss += xv[i] * xv[i];
-  const float inv = 1.0f / sqrtf(BlockSumAny(ss, red) + eps);
-  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) xv[i] *= inv;
+  const float inv = 1.0f / sqrtf(RowSumSq(xv, d, red) + eps);
+  RowApply(xv, xv, d, [&](std::uint32_t, float v) { return v * inv; });
 }
 
 // NEOX RoPE in place, one block per head of head_dim values (core.hip:289-306): at position pos; rows of `heads`
@@ -157,83 +193,123 @@ extern "C" __global__ void halo_split_qgate(const float* qg, float* q, float* ga
   }
 }
 
-// Causal depthwise conv step + SiLU; state holds the last kern - 1 inputs, oldest first, and shifts by one
-// (core.hip:447). One thread per channel.
-extern "C" __global__ void halo_conv_step(const float* in, float* state, const float* w, float* out,
-                                          std::uint32_t channels, std::uint32_t kern) {
-  const std::uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
-  if (ch >= channels) return;
-  const float x = in[ch];
-  float acc = w[static_cast<std::size_t>(ch) * kern + kern - 1] * x;
-  for (std::uint32_t j = 0; j + 1 < kern; ++j) {  // slot j is read before slot j + 1 moves into it
-    const float sj = state[static_cast<std::size_t>(j) * channels + ch];
-    acc += w[static_cast<std::size_t>(ch) * kern + j] * sj;
-    if (j > 0) state[static_cast<std::size_t>(j - 1) * channels + ch] = sj;
-  }
-  if (kern > 1) state[static_cast<std::size_t>(kern - 2) * channels + ch] = x;
-  out[ch] = halo::Silu(acc);
+// ---- depthwise causal conv (DeltaNet q/k/v channels) -------------------------------------------------------------
+// One arithmetic for every conv kernel below, so stepping, the one-token-per-block prefill and the eight-token prefill
+// give the same bits: the taps of a channel against its window (oldest input first, the current input last) as one
+// fused multiply-add chain starting from the oldest tap, then SiLU; the L2 norm of a head (d channels) from lane
+// partials p_l = sum over m of v[l + 64 m]^2 (fused, m ascending) reduced over the wave (GroupSum).
+// Conv state layout: [kern - 1][channels], slot j holds the input kern - 1 - j steps back (oldest first).
+namespace halo::refk {
+constexpr std::uint32_t kMaxTaps = 9;
+
+__device__ __forceinline__ float ConvSilu(const float* wc, const float (&win)[kMaxTaps], std::uint32_t kern) {
+  float acc = 0.0f;
+#pragma unroll
+  for (std::uint32_t j = 0; j < kMaxTaps; ++j)
+    if (j < kern) acc = __builtin_fmaf(wc[j], win[j], acc);
+  return halo::Silu(acc);
 }
 
-// The conv step and, for channels below l2_channels (DeltaNet q and k), the L2 norm over each block's channels (one
-// block per head of blockDim channels, core.hip:3003-3028).
-namespace halo::refk {
+// Input i of a chunk's conv stream: i >= 0 is row i of the chunk, i < 0 the state slot kern - 1 + i.
+__device__ __forceinline__ float ConvInput(const float* in, const float* state, std::int64_t i, std::uint32_t ch,
+                                           std::uint32_t channels, std::uint32_t kern) {
+  return i >= 0 ? in[static_cast<std::size_t>(i) * channels + ch]
+                : state[static_cast<std::size_t>(i + kern - 1) * channels + ch];
+}
+
+// One decode step of channel ch: the window is the state then x; the state moves one slot (x becomes the newest).
+__device__ __forceinline__ float ConvStep(const float* in, float* state, const float* w, std::uint32_t ch,
+                                          std::uint32_t channels, std::uint32_t kern) {
+  const float x = in[ch];
+  float win[kMaxTaps];
+#pragma unroll
+  for (std::uint32_t j = 0; j < kMaxTaps; ++j)
+    win[j] = j + 1 < kern ? state[static_cast<std::size_t>(j) * channels + ch] : (j + 1 == kern ? x : 0.0f);
+#pragma unroll
+  for (std::uint32_t j = 0; j + 1 < kMaxTaps; ++j)
+    if (j + 1 < kern) state[static_cast<std::size_t>(j) * channels + ch] = win[j + 1];
+  return ConvSilu(w + static_cast<std::size_t>(ch) * kern, win, kern);
+}
+
+// Sum of squares of a head whose channel i is thread i's y (block = one head, <= 256 threads): staged in LDS, then
+// every wave forms the canonical lane partials and reduces them itself (identical bits in all waves).
+__device__ __forceinline__ float HeadSumSq(float y, float* sh) {
+  sh[threadIdx.x] = y;
+  __syncthreads();
+  const std::uint32_t lane = threadIdx.x % kWave;
+  float p = 0.0f;
+  for (std::uint32_t i = lane; i < blockDim.x; i += kWave) p = __builtin_fmaf(sh[i], sh[i], p);
+  return halo::GroupSum(p);
+}
+
+// Block = one head of blockDim channels; heads that start below l2_channels are L2-normalised (block-uniform).
 __device__ __forceinline__ void ConvL2norm(const float* in, float* state, const float* w, float* out,
                                            std::uint32_t channels, std::uint32_t kern, std::uint32_t l2_channels,
-                                           float eps, float* red) {
+                                           float eps, float* sh) {
   const std::uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
-  float y = 0.0f;
-  if (ch < channels) {
-    const float x = in[ch];
-    float acc = w[static_cast<std::size_t>(ch) * kern + kern - 1] * x;
-    for (std::uint32_t j = 0; j + 1 < kern; ++j) {
-      const float sj = state[static_cast<std::size_t>(j) * channels + ch];
-      acc += w[static_cast<std::size_t>(ch) * kern + j] * sj;
-      if (j > 0) state[static_cast<std::size_t>(j - 1) * channels + ch] = sj;
-    }
-    if (kern > 1) state[static_cast<std::size_t>(kern - 2) * channels + ch] = x;
-    y = halo::Silu(acc);
-  }
-  if (blockIdx.x * blockDim.x < l2_channels) y *= 1.0f / sqrtf(BlockSumAny(y * y, red) + eps);  // block-uniform
+  float y = ch < channels ? ConvStep(in, state, w, ch, channels, kern) : 0.0f;
+  if (blockIdx.x * blockDim.x < l2_channels) y *= 1.0f / sqrtf(HeadSumSq(y, sh) + eps);
   if (ch < channels) out[ch] = y;
 }
 }  // namespace halo::refk
+
+// Conv step + SiLU, one thread per channel; kern <= 9 (core.hip:447). grid (ceil(channels / blockDim)).
+extern "C" __global__ void halo_conv_step(const float* in, float* state, const float* w, float* out,
+                                          std::uint32_t channels, std::uint32_t kern) {
+  const std::uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
+  if (ch < channels) out[ch] = ConvStep(in, state, w, ch, channels, kern);
+}
+// The conv step and the per-head L2 norm of q and k (core.hip:3003-3028). grid (ceil(channels / d)), block d <= 256.
 extern "C" __global__ void halo_conv_l2norm(const float* in, float* state, const float* w, float* out,
                                             std::uint32_t channels, std::uint32_t kern, std::uint32_t l2_channels,
                                             float eps) {
-  __shared__ float red[16];
-  ConvL2norm(in, state, w, out, channels, kern, l2_channels, eps, red);
+  __shared__ float sh[256];
+  ConvL2norm(in, state, w, out, channels, kern, l2_channels, eps, sh);
 }
 
-// One Gated DeltaNet decode step, one block per value head h (key head h % num_k_heads), thread j = value column
-// (blockDim >= d); state key-major [h][i][j]: decay the state, u = S^T k, delta = (v - u) sigmoid(beta),
-// S += k delta^T, o = S^T q / sqrt(d), with decay = exp(a softplus(alpha + dt)) (core.hip:463).
+// One Gated DeltaNet decode step for any head size d <= 256 (core.hip:463), one block per value head h (key head
+// h % num_k_heads), any block size that is a multiple of 64 (threads loop over value columns j). Single pass over the
+// key-major state [h][i][j], in the algebraic form the d = 128 kernels use: with A = sum_i S_ij k_i and
+// B = sum_i S_ij q_i over the old state, delta_j = (v_j - decay A) b, S'_ij = decay S_ij + k_i delta_j and
+// o_j = (decay B + delta_j (k . q)) / sqrt(d); decay = exp(a softplus(alpha + dt)), b = sigmoid(beta).
 extern "C" __global__ void halo_gdn_step(const float* q, const float* k, const float* v, const float* alpha,
                                          const float* beta, const float* a, const float* dt, float* state, float* out,
                                          std::uint32_t num_k_heads, std::uint32_t d) {
-  __shared__ float kl[256], ql[256];
-  const std::uint32_t h = blockIdx.x, j = threadIdx.x, kh = h % num_k_heads;
+  __shared__ float kl[256], ql[256], red[16];
+  const std::uint32_t h = blockIdx.x, kh = h % num_k_heads;
+  float kq = 0.0f;
   for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) {
-    kl[i] = k[static_cast<std::size_t>(kh) * d + i];
-    ql[i] = q[static_cast<std::size_t>(kh) * d + i];
+    const float ki = k[static_cast<std::size_t>(kh) * d + i], qi = q[static_cast<std::size_t>(kh) * d + i];
+    kl[i] = ki;
+    ql[i] = qi;
+    kq = __builtin_fmaf(ki, qi, kq);
   }
-  __syncthreads();
-  if (j >= d) return;
+  kq = BlockSumAny(kq, red);  // its barriers publish kl / ql
   const float decay = expf(a[h] * halo::Softplus(alpha[h] + dt[h])), b = halo::Sigmoid(beta[h]);
-  float* col = state + static_cast<std::size_t>(h) * d * d + j;
-  float u = 0.0f;
-  for (std::uint32_t i = 0; i < d; ++i) {
-    const float s = col[static_cast<std::size_t>(i) * d] * decay;
-    col[static_cast<std::size_t>(i) * d] = s;
-    u += s * kl[i];
+  const float inv_sqrt_d = 1.0f / sqrtf(static_cast<float>(d));
+  float* sh = state + static_cast<std::size_t>(h) * d * d;
+  for (std::uint32_t j = threadIdx.x; j < d; j += blockDim.x) {
+    float A0 = 0.0f, A1 = 0.0f, B0 = 0.0f, B1 = 0.0f;  // even / odd key rows: two independent chains each
+    std::uint32_t i = 0;
+    for (; i + 1 < d; i += 2) {
+      const float s0 = sh[static_cast<std::size_t>(i) * d + j], s1 = sh[static_cast<std::size_t>(i + 1) * d + j];
+      A0 = __builtin_fmaf(s0, kl[i], A0);
+      B0 = __builtin_fmaf(s0, ql[i], B0);
+      A1 = __builtin_fmaf(s1, kl[i + 1], A1);
+      B1 = __builtin_fmaf(s1, ql[i + 1], B1);
+    }
+    if (i < d) {
+      const float s0 = sh[static_cast<std::size_t>(i) * d + j];
+      A0 = __builtin_fmaf(s0, kl[i], A0);
+      B0 = __builtin_fmaf(s0, ql[i], B0);
+    }
+    const float delta = (v[static_cast<std::size_t>(h) * d + j] - decay * (A0 + A1)) * b;
+    for (std::uint32_t r = 0; r < d; ++r) {
+      float* s = sh + static_cast<std::size_t>(r) * d + j;
+      *s = __builtin_fmaf(kl[r], delta, decay * *s);
+    }
+    out[static_cast<std::size_t>(h) * d + j] = (decay * (B0 + B1) + delta * kq) * inv_sqrt_d;
   }
-  const float delta = (v[static_cast<std::size_t>(h) * d + j] - u) * b;
-  float o = 0.0f;
-  for (std::uint32_t i = 0; i < d; ++i) {
-    const float s = col[static_cast<std::size_t>(i) * d] + delta * kl[i];
-    col[static_cast<std::size_t>(i) * d] = s;
-    o += s * ql[i];
-  }
-  out[static_cast<std::size_t>(h) * d + j] = o / sqrtf(static_cast<float>(d));
 }
 
 namespace {
@@ -306,11 +382,11 @@ extern "C" __global__ void halo_gated_norm(float* o, const float* w, const float
   __shared__ float red[16];
   float* ov = o + static_cast<std::size_t>(blockIdx.x) * d;
   const float* zv = z + static_cast<std::size_t>(blockIdx.x) * d;
-  float ss = 0.0f;
-  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) ss += ov[i] * ov[i];
-  const float inv = 1.0f / sqrtf(BlockSumAny(ss, red) / static_cast<float>(d) + eps);
-  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x)
-    ov[i] = ov[i] * inv * w[i] * (mode == 0 ? halo::Silu(zv[i]) : halo::Sigmoid(zv[i]));
+  const float inv = RmsScale(ov, d, eps, red);
+  if (mode == 0)
+    RowApply(ov, ov, d, [&](std::uint32_t i, float v) { return v * inv * w[i] * halo::Silu(zv[i]); });
+  else
+    RowApply(ov, ov, d, [&](std::uint32_t i, float v) { return v * inv * w[i] * halo::Sigmoid(zv[i]); });
 }
 
 // Decode attention over positions [0, n) of a contiguous cache [pos][num_kv_heads][hd], one block per query head
@@ -440,23 +516,40 @@ __device__ __forceinline__ void Combine(const float* part, const float* weights,
     out[i] = acc;
   }
 }
-// y = row . x for one row per block; float4 loads when cols and the row are 16-byte aligned.
+// y = row . x for one row per block. 16-byte loads when cols and the row allow them: each thread takes float4 pairs
+// (two loads in flight, two fused chains), then BlockSumAny.
 __device__ __forceinline__ float RowDot(const float* row, const float* x, std::uint32_t cols, float* red) {
-  float acc = 0.0f;
-  if (cols % 4 == 0) {
+  float a0 = 0.0f, a1 = 0.0f;
+  if (Vec4Ok(row, cols) && Vec4Ok(x, cols)) {
     const float4* r4 = reinterpret_cast<const float4*>(row);
     const float4* x4 = reinterpret_cast<const float4*>(x);
-    for (std::uint32_t c = threadIdx.x; c < cols / 4; c += blockDim.x) {
-      const float4 a = r4[c], b = x4[c];
-      acc = __builtin_fmaf(a.x, b.x, acc);
-      acc = __builtin_fmaf(a.y, b.y, acc);
-      acc = __builtin_fmaf(a.z, b.z, acc);
-      acc = __builtin_fmaf(a.w, b.w, acc);
+    const std::uint32_t n4 = cols / 4;
+    std::uint32_t i = threadIdx.x;
+    for (; i + blockDim.x < n4; i += 2 * blockDim.x) {
+      const float4 p = r4[i], u = x4[i], p2 = r4[i + blockDim.x], u2 = x4[i + blockDim.x];
+      a0 = __builtin_fmaf(p.w, u.w, __builtin_fmaf(p.z, u.z, __builtin_fmaf(p.y, u.y, __builtin_fmaf(p.x, u.x, a0))));
+      a1 = __builtin_fmaf(p2.w, u2.w,
+                          __builtin_fmaf(p2.z, u2.z, __builtin_fmaf(p2.y, u2.y, __builtin_fmaf(p2.x, u2.x, a1))));
+    }
+    if (i < n4) {
+      const float4 p = r4[i], u = x4[i];
+      a0 = __builtin_fmaf(p.w, u.w, __builtin_fmaf(p.z, u.z, __builtin_fmaf(p.y, u.y, __builtin_fmaf(p.x, u.x, a0))));
     }
   } else {
-    for (std::uint32_t c = threadIdx.x; c < cols; c += blockDim.x) acc = __builtin_fmaf(row[c], x[c], acc);
+    for (std::uint32_t c = threadIdx.x; c < cols; c += blockDim.x) a0 = __builtin_fmaf(row[c], x[c], a0);
   }
-  return BlockSumAny(acc, red);
+  return BlockSumAny(a0 + a1, red);
+}
+
+// The rowblock matvecs: block b computes row b % rows of matrix b / rows (kMats matrices with the same x).
+template <int kMats>
+__device__ __forceinline__ void RowblockMatvec(const float* const (&w)[kMats], const float* x, float* const (&y)[kMats],
+                                               std::uint32_t rows, std::uint32_t cols) {
+  __shared__ float red[16];
+  const std::uint32_t m = blockIdx.x / rows, r = blockIdx.x % rows;
+  if (m >= static_cast<std::uint32_t>(kMats)) return;  // block-uniform
+  const float acc = RowDot(w[m] + static_cast<std::size_t>(r) * cols, x, cols, red);
+  if (threadIdx.x == 0) y[m][r] = acc;
 }
 }  // namespace halo::refk
 
@@ -470,57 +563,39 @@ extern "C" __global__ void __launch_bounds__(256)
     halo_moe_combine_u(const float* part, const float* weights, float* out, std::uint32_t slots, std::uint32_t n) {
   halo::refk::Combine<true>(part, weights, out, slots, n);
 }
-// grid (rows), any multiple of 64 threads: y[r] = w[r] . x.
+// grid (rows), any multiple of 64 threads: y[r] = w[r] . x (core.hip:2193, 9264).
 extern "C" __global__ void __launch_bounds__(256)
     halo_matvec_f32_rowblock(const float* w, const float* x, float* y, std::uint32_t rows, std::uint32_t cols) {
-  __shared__ float red[16];
-  const std::uint32_t r = blockIdx.x;
-  if (r >= rows) return;
-  const float acc = halo::refk::RowDot(w + static_cast<std::size_t>(r) * cols, x, cols, red);
-  if (threadIdx.x == 0) y[r] = acc;
+  RowblockMatvec<1>({w}, x, {y}, rows, cols);
 }
 extern "C" __global__ void __launch_bounds__(256)
     halo_matvec_f32_rowblock_u(const float* w, const float* x, float* y, std::uint32_t rows, std::uint32_t cols) {
-  __shared__ float red[16];
-  const std::uint32_t r = blockIdx.x;
-  if (r >= rows) return;
-  const float acc = halo::refk::RowDot(w + static_cast<std::size_t>(r) * cols, x, cols, red);
-  if (threadIdx.x == 0) y[r] = acc;
+  RowblockMatvec<1>({w}, x, {y}, rows, cols);
 }
 // grid (2 rows): blocks [0, rows) compute ya = wa x, blocks [rows, 2 rows) yb = wb x.
 extern "C" __global__ void __launch_bounds__(256)
     halo_matvec_f32_rowblock2(const float* wa, const float* wb, const float* x, float* ya, float* yb,
                               std::uint32_t rows, std::uint32_t cols) {
-  __shared__ float red[16];
-  const bool a = blockIdx.x < rows;
-  const std::uint32_t r = a ? blockIdx.x : blockIdx.x - rows;
-  if (r >= rows) return;
-  const float acc = halo::refk::RowDot((a ? wa : wb) + static_cast<std::size_t>(r) * cols, x, cols, red);
-  if (threadIdx.x == 0) (a ? ya : yb)[r] = acc;
+  RowblockMatvec<2>({wa, wb}, x, {ya, yb}, rows, cols);
 }
 extern "C" __global__ void __launch_bounds__(256)
     halo_matvec_f32_rowblock2_u(const float* wa, const float* wb, const float* x, float* ya, float* yb,
                                 std::uint32_t rows, std::uint32_t cols) {
-  __shared__ float red[16];
-  const bool a = blockIdx.x < rows;
-  const std::uint32_t r = a ? blockIdx.x : blockIdx.x - rows;
-  if (r >= rows) return;
-  const float acc = halo::refk::RowDot((a ? wa : wb) + static_cast<std::size_t>(r) * cols, x, cols, red);
-  if (threadIdx.x == 0) (a ? ya : yb)[r] = acc;
+  RowblockMatvec<2>({wa, wb}, x, {ya, yb}, rows, cols);
 }
-// Per token and 32 values (amax / 127, round to nearest even, as halo_quantize_q8_rows), K-blocked:
-// x [T][cols] -> xq [cols / 64][T][64], xd [cols / 32][T]. grid (T), any multiple of 64 threads; cols % 64 == 0.
+// Per token and 32 values (amax / 127, round half to even, as halo_quantize_q8_rows), K-blocked (core.hip:3317-3331):
+// x [T][cols] -> xq [cols / 64][T][64], xd [cols / 32][T]. A lane quantizes 4 values from one 16-byte load; 8 lanes
+// form a Q8_0 block (QuantQuad) and store their codes as one 32-byte run. grid (T), any multiple of 64 threads;
+// cols % 64 == 0.
 extern "C" __global__ void __launch_bounds__(256)
     halo_quantize_q8_kblocked(const float* x, std::int8_t* xq, float* xd, std::uint32_t cols, std::uint32_t tokens) {
   const std::size_t t = blockIdx.x;
-  const std::uint32_t lane = threadIdx.x % 32;
-  for (std::uint32_t blk = threadIdx.x / 32; blk < cols / 32; blk += blockDim.x / 32) {
-    const std::uint32_t c = blk * 32 + lane;
-    const float v = x[t * cols + c];
-    const float scale = halo::GroupMax<32>(fabsf(v)) / 127.0f;
-    xq[(static_cast<std::size_t>(c / 64) * tokens + t) * 64 + c % 64] =
-        static_cast<std::int8_t>(scale > 0.0f ? static_cast<int>(rintf(v / scale)) : 0);
-    if (lane == 0) xd[static_cast<std::size_t>(blk) * tokens + t] = scale;
+  const float4* row = reinterpret_cast<const float4*>(x + t * cols);
+  for (std::uint32_t g = threadIdx.x; g < cols / 4; g += blockDim.x) {  // groups of 8 lanes stay whole (cols % 32)
+    float scale;
+    const std::uint32_t word = halo::QuantQuad(row[g], scale), c = 4 * g;
+    *reinterpret_cast<std::uint32_t*>(xq + (static_cast<std::size_t>(c / 64) * tokens + t) * 64 + c % 64) = word;
+    if (g % 8 == 0) xd[static_cast<std::size_t>(c / 32) * tokens + t] = scale;
   }
 }
 // halo_router_topk's results (softmax, top k in (probability desc, index asc) order, weights renormalized in slot
@@ -575,48 +650,38 @@ extern "C" __global__ void __launch_bounds__(128)
   }
 }
 
-// halo_conv_l2norm for T tokens at once: token t's window is the kern - 1 inputs before it, from the chunk or, before
-// the chunk, from the conv state (slot j holds input j - (kern - 1)); the sums run in the decode kernel's order, so
-// each token's output equals stepping bit for bit. The state is not written (halo_conv_state_advance moves it).
-//   in, out [T][channels]; grid (ceil(channels / d), T), block d (one head of channels).
+// halo_conv_l2norm for T tokens at once (core.hip:3480-3508): token t's window is inputs t - kern + 1 .. t of the
+// chunk, reaching back into the conv state before the chunk; same arithmetic as stepping, so every output equals the
+// step's bits. The state is only read (halo_conv_state_advance moves it after the chunk).
+//   in, out [T][channels]; grid (ceil(channels / d), T), block d <= 256 (one head).
 extern "C" __global__ void halo_conv_l2norm_prefill(const float* in, const float* state, const float* w, float* out,
                                                     std::uint32_t channels, std::uint32_t kern,
                                                     std::uint32_t l2_channels, float eps) {
-  __shared__ float red[16];
-  const std::uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+  __shared__ float sh[256];
+  const std::uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
+  const std::int64_t t = blockIdx.y;
   float y = 0.0f;
   if (ch < channels) {
-    float acc = w[static_cast<std::size_t>(ch) * kern + kern - 1] * in[static_cast<std::size_t>(t) * channels + ch];
-    for (std::uint32_t j = 0; j + 1 < kern; ++j) {
-      const std::int64_t i = static_cast<std::int64_t>(t) - static_cast<std::int64_t>(kern - 1) + j;
-      const float x = i >= 0 ? in[static_cast<std::size_t>(i) * channels + ch]
-                             : state[static_cast<std::size_t>(i + kern - 1) * channels + ch];
-      acc += w[static_cast<std::size_t>(ch) * kern + j] * x;
-    }
-    y = halo::Silu(acc);
+    float win[kMaxTaps];
+#pragma unroll
+    for (std::uint32_t j = 0; j < kMaxTaps; ++j)
+      win[j] = j < kern ? ConvInput(in, state, t - static_cast<std::int64_t>(kern - 1 - j), ch, channels, kern) : 0.0f;
+    y = ConvSilu(w + static_cast<std::size_t>(ch) * kern, win, kern);
   }
-  if (blockIdx.x * blockDim.x < l2_channels) y *= 1.0f / sqrtf(BlockSumAny(y * y, red) + eps);  // block-uniform
+  if (blockIdx.x * blockDim.x < l2_channels) y *= 1.0f / sqrtf(HeadSumSq(y, sh) + eps);
   if (ch < channels) out[static_cast<std::size_t>(t) * channels + ch] = y;
 }
 
-// The conv state after a chunk of T inputs: the last kern - 1 inputs (older ones from the previous state when
-// T < kern - 1). grid (ceil(channels / 256)), block 256; kern <= 9.
+// The conv state after a chunk of T inputs (core.hip:3586-3597): slot j becomes stream input T - kern + 1 + j. Slots
+// are rewritten in ascending order, so a slot that moves down within the state is read before it is overwritten.
+// grid (ceil(channels / blockDim)); kern <= 9.
 extern "C" __global__ void halo_conv_state_advance(const float* in, float* state, std::uint32_t channels,
                                                    std::uint32_t kern, std::uint32_t tokens) {
   const std::uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
-  if (ch >= channels || kern < 2) return;
-  float next[8];
-#pragma unroll
-  for (std::uint32_t j = 0; j < 8; ++j) {
-    if (j + 1 >= kern) break;
-    const std::int64_t i = static_cast<std::int64_t>(tokens) - static_cast<std::int64_t>(kern - 1) + j;
-    next[j] = i >= 0 ? in[static_cast<std::size_t>(i) * channels + ch]
-                     : state[static_cast<std::size_t>(i + kern - 1) * channels + ch];
-  }
-#pragma unroll
-  for (std::uint32_t j = 0; j < 8; ++j) {
-    if (j + 1 >= kern) break;
-    state[static_cast<std::size_t>(j) * channels + ch] = next[j];
+  if (ch >= channels) return;
+  for (std::uint32_t j = 0; j + 1 < kern; ++j) {
+    const std::int64_t i = static_cast<std::int64_t>(tokens) + j - (kern - 1);
+    state[static_cast<std::size_t>(j) * channels + ch] = ConvInput(in, state, i, ch, channels, kern);
   }
 }
 
@@ -718,39 +783,30 @@ extern "C" __global__ void __launch_bounds__(256)
 }
 
 // Router logits y[r] = w_r . x (block r < rows) and, in blocks b < cols / 32, the Q8 activation record of x's 32-value
-// block b (act: int8 q [4096] packed four to a word, fp32 scale [128] = amax / 127, fp32 sum [128] by the xor
-// butterfly 16, 8, 4, 2, 1; cols <= 4096). grid (max(rows, cols / 32)), block 256.
+// block b (core.hip:9315-9343; act: int8 codes [4096] four to a little-endian word, fp32 scale [128] = amax / 127,
+// fp32 block sum [128]; cols <= 4096). The record takes lanes 0-7 of the first wave, one 16-byte load each: the codes
+// come from QuantQuad, the sum is each lane's (x0 + x1) + (x2 + x3) added across the 8 lanes by Group8Sum.
+// grid (max(rows, cols / 32)), block 256.
 extern "C" __global__ void __launch_bounds__(256)
     halo_router_rowblock_q8act(const float* w, const float* x, float* y, std::uint32_t rows, std::uint32_t cols,
                                void* act) {
   __shared__ float red[16];
-  std::uint32_t* aq = static_cast<std::uint32_t*>(act);
-  float* ascale = reinterpret_cast<float*>(aq + 1024);
-  float* asum = ascale + 128;
-  if (blockIdx.x < cols / 32 && threadIdx.x < 32) {
-    const std::uint32_t lane = threadIdx.x, blk = blockIdx.x;
-    const float v = x[blk * 32 + lane];
-    float amax = fabsf(v), sum = v;
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) {
-      amax = fmaxf(amax, __shfl_xor(amax, o, 32));
-      sum += __shfl_xor(sum, o, 32);
-    }
-    const float scale = amax / 127.0f;
-    const int qv = scale > 0.0f ? static_cast<int>(rintf(v / scale)) : 0;
-    std::uint32_t word = (static_cast<std::uint32_t>(qv) & 0xFFu) << (8 * (lane & 3));
-    word |= __shfl_xor(word, 1, 32);
-    word |= __shfl_xor(word, 2, 32);
-    if ((lane & 3) == 0) aq[blk * 8 + lane / 4] = word;
-    if (lane == 0) {
+  const std::uint32_t blk = blockIdx.x;
+  if (blk < cols / 32 && threadIdx.x < 8) {
+    std::uint32_t* aq = static_cast<std::uint32_t*>(act);
+    float* ascale = reinterpret_cast<float*>(aq + 1024);
+    const float4 v = reinterpret_cast<const float4*>(x + blk * 32)[threadIdx.x];
+    float scale;
+    aq[blk * 8 + threadIdx.x] = halo::QuantQuad(v, scale);
+    const float sum = halo::Group8Sum((v.x + v.y) + (v.z + v.w));
+    if (threadIdx.x == 0) {
       ascale[blk] = scale;
-      asum[blk] = sum;
+      ascale[128 + blk] = sum;
     }
   }
-  const std::uint32_t r = blockIdx.x;
-  if (r >= rows) return;
-  const float acc = RowDot(w + static_cast<std::size_t>(r) * cols, x, cols, red);
-  if (threadIdx.x == 0) y[r] = acc;
+  if (blk >= rows) return;  // block-uniform
+  const float acc = RowDot(w + static_cast<std::size_t>(blk) * cols, x, cols, red);
+  if (threadIdx.x == 0) y[blk] = acc;
 }
 
 // ---- prefill int8 GEMMs (reference names) ---------------------------------------------------------------------
@@ -895,7 +951,7 @@ HALO_MOE_DOWN_BUCKET(8)
 // an expert), pos[p] (p's sorted position), work tiles of up to 64 pairs of one expert, tiles[3 i .. 3 i + 2] =
 // (expert, first, count), in expert order, and ntiles. experts <= 1024.
 namespace halo::refk {
-constexpr std::uint32_t kPairTile = 64, kPairChunk = 1024;
+constexpr std::uint32_t kPairTile = 64, kPairChunk = 1024, kNoKey = 0xFFFFFFFFu;
 // Expert offsets (exclusive scan of totals in expert order), tiles and ntiles, from total[e] in LDS; block 1024.
 __device__ __forceinline__ void BucketTiles(const std::uint32_t* total, std::uint32_t experts, std::uint32_t* poff,
                                             std::uint32_t* tiles, std::uint32_t* ntiles, std::uint32_t* wave_tot) {
@@ -912,36 +968,63 @@ __device__ __forceinline__ void BucketTiles(const std::uint32_t* total, std::uin
   }
   if (e == 0) *ntiles = ttot;
 }
+
+// Stable rank of this thread's key among the block's lower-numbered threads holding the same key (keys < nkeys;
+// kNoKey takes no part and gets 0). Inside a wave the lanes of one key are found together by a ballot against the
+// lowest pending lane's key, one key per round; wave w's count of each key goes to tab[w * nkeys + key], so the rank
+// adds the counts of the earlier waves. tab holds (blockDim / 64) * nkeys words; it stays valid until the caller's
+// next barrier-separated reuse (callers read per-key block totals from it).
+__device__ __forceinline__ std::uint32_t BlockKeyRank(std::uint32_t key, std::uint32_t nkeys, std::uint32_t* tab) {
+  const std::uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
+  for (std::uint32_t i = threadIdx.x; i < waves * nkeys; i += blockDim.x) tab[i] = 0;
+  __syncthreads();
+  const std::uint64_t below = (std::uint64_t{1} << lane) - 1;
+  std::uint64_t todo = __ballot(key != kNoKey);
+  std::uint32_t rank = 0;
+  while (todo) {
+    const std::uint32_t leader = static_cast<std::uint32_t>(__builtin_ctzll(todo));
+    const std::uint32_t lk = static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key), leader));
+    const std::uint64_t same = __ballot(key == lk);
+    if (key == lk) rank = static_cast<std::uint32_t>(__builtin_popcountll(same & below));
+    if (lane == leader) tab[wave * nkeys + lk] = static_cast<std::uint32_t>(__builtin_popcountll(same));
+    todo &= ~same;
+  }
+  __syncthreads();
+  if (key != kNoKey)
+    for (std::uint32_t w = 0; w < wave; ++w) rank += tab[w * nkeys + key];
+  return rank;
+}
 }  // namespace halo::refk
 
-// One block of 1024 threads does all of it (small chunks).
+// One block of 1024 threads does all of it (small chunks): counts, offsets and tiles, then chunk by chunk each pair's
+// position = its expert's running offset + its rank in the chunk; the running offsets then add the chunk's counts.
 extern "C" __global__ void __launch_bounds__(1024)
     halo_moe_bucket(const std::uint32_t* ids, std::uint32_t pairs, std::uint32_t experts, std::uint32_t* sorted,
                     std::uint32_t* pos, std::uint32_t* tiles, std::uint32_t* ntiles) {
-  __shared__ std::uint32_t cnt[1024], run[1024], chunk_ids[kPairChunk], wave_tot[16];
+  __shared__ std::uint32_t cnt[1024], run[1024], wave_tot[16], tab[16 * 1024];
   const std::uint32_t tid = threadIdx.x;
   cnt[tid] = 0;
   __syncthreads();
   for (std::uint32_t p = tid; p < pairs; p += blockDim.x) atomicAdd(&cnt[ids[p]], 1u);
   __syncthreads();
   BucketTiles(cnt, experts, run, tiles, ntiles, wave_tot);
-  __syncthreads();
-  // scatter chunk by chunk: a pair's rank among the chunk's earlier pairs of its expert, then the running offsets
-  for (std::uint32_t base = 0; base < pairs; base += kPairChunk) {
+  const std::uint32_t waves = blockDim.x / kWave;
+  for (std::uint32_t base = 0; base < pairs; base += blockDim.x) {
     const std::uint32_t p = base + tid;
-    const std::uint32_t e = p < pairs ? ids[p] : 0xFFFFFFFFu;
-    chunk_ids[tid] = e;
-    __syncthreads();
-    if (p < pairs) {
-      std::uint32_t rank = 0;
-      for (std::uint32_t i = 0; i < tid; ++i) rank += chunk_ids[i] == e;
+    const std::uint32_t e = p < pairs ? ids[p] : kNoKey;
+    const std::uint32_t rank = BlockKeyRank(e, experts, tab);  // its first barrier also publishes run[]
+    if (e != kNoKey) {
       const std::uint32_t at = run[e] + rank;
       sorted[at] = p;
       pos[p] = at;
     }
-    __syncthreads();
-    if (p < pairs) atomicAdd(&run[e], 1u);  // after every read of run[] for this chunk
-    __syncthreads();
+    __syncthreads();  // every read of run[] for this chunk is done
+    for (std::uint32_t x = tid; x < experts; x += blockDim.x) {
+      std::uint32_t add = 0;
+      for (std::uint32_t w = 0; w < waves; ++w) add += tab[w * experts + x];
+      run[x] += add;
+    }
+    __syncthreads();  // run[] updated and tab[] free before the next chunk
   }
 }
 // 1. per chunk of 1024 pairs, per-expert counts [chunks][experts]. grid (chunks), block 1024.
@@ -975,19 +1058,17 @@ extern "C" __global__ void __launch_bounds__(1024)
   __syncthreads();
   BucketTiles(total, experts, base, tiles, ntiles, wave_tot);
 }
-// 3. each pair's rank among its chunk's earlier pairs of its expert gives its sorted position. grid (chunks), 1024.
+// 3. sorted position = expert base + the chunk's offset for the expert + the pair's rank inside the chunk
+// (BlockKeyRank). grid (chunks), block 1024.
 extern "C" __global__ void __launch_bounds__(1024)
     halo_moe_bucket_scatter(const std::uint32_t* ids, std::uint32_t pairs, std::uint32_t experts,
                             const std::uint32_t* chunk_off, const std::uint32_t* base, std::uint32_t* sorted,
                             std::uint32_t* pos) {
-  __shared__ std::uint32_t chunk_ids[kPairChunk];
-  const std::uint32_t tid = threadIdx.x, p = blockIdx.x * kPairChunk + tid;
-  const std::uint32_t e = p < pairs ? ids[p] : 0xFFFFFFFFu;
-  chunk_ids[tid] = e;
-  __syncthreads();
-  if (p >= pairs) return;
-  std::uint32_t rank = 0;
-  for (std::uint32_t i = 0; i < tid; ++i) rank += chunk_ids[i] == e;
+  __shared__ std::uint32_t tab[16 * 1024];
+  const std::uint32_t p = blockIdx.x * kPairChunk + threadIdx.x;
+  const std::uint32_t e = p < pairs ? ids[p] : kNoKey;
+  const std::uint32_t rank = BlockKeyRank(e, experts, tab);
+  if (e == kNoKey) return;
   const std::uint32_t at = base[e] + chunk_off[static_cast<std::size_t>(blockIdx.x) * experts + e] + rank;
   sorted[at] = p;
   pos[p] = at;
@@ -1046,13 +1127,10 @@ extern "C" __global__ void __launch_bounds__(256)
 extern "C" __global__ void halo_rmsnorm_rows(const float* x, const float* w_all, float* y, std::uint32_t d, float eps,
                                              std::uint32_t w_stride, std::uint32_t w_period) {
   __shared__ float red[16];
-  const float* xv = x + static_cast<std::size_t>(blockIdx.x) * d;
-  const float* w = w_all + static_cast<std::size_t>(blockIdx.x % w_period) * w_stride;
-  float* yv = y + static_cast<std::size_t>(blockIdx.x) * d;
-  float ss = 0.0f;
-  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) ss += xv[i] * xv[i];
-  const float inv = 1.0f / sqrtf(BlockSumAny(ss, red) / static_cast<float>(d) + eps);
-  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) yv[i] = xv[i] * inv * w[i];
+  const std::size_t b = blockIdx.x;
+  const float* w = w_all + (b % w_period) * w_stride;
+  const float inv = RmsScale(x + b * d, d, eps, red);
+  RowApply(x + b * d, y + b * d, d, [&](std::uint32_t i, float v) { return v * inv * w[i]; });
 }
 
 // Batched-column variants: column (session entry) e = blockIdx.y, its data `stride` floats apart.
@@ -1072,11 +1150,8 @@ extern "C" __global__ void halo_rmsnorm_y(float* x, const float* w_all, std::uin
   __shared__ float red[16];
   float* xv = x + static_cast<std::size_t>(blockIdx.y) * stride + static_cast<std::size_t>(blockIdx.x) * d;
   const float* w = w_all + static_cast<std::size_t>(blockIdx.x) * w_stride;
-  float ss = 0.0f;
-  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) ss += xv[i] * xv[i];
-  const float inv = 1.0f / sqrtf(BlockSumAny(ss, red) / static_cast<float>(d) + eps);
-  __syncthreads();  // every read of xv precedes the in-place writes
-  for (std::uint32_t i = threadIdx.x; i < d; i += blockDim.x) xv[i] = xv[i] * inv * w[i];
+  const float inv = RmsScale(xv, d, eps, red);
+  RowApply(xv, xv, d, [&](std::uint32_t i, float v) { return v * inv * w[i]; });
 }
 // grid (heads, B): column e's position params[e * pstride + slot] * scale.
 extern "C" __global__ void halo_rope_neox_p_y(float* x, const std::uint32_t* params, std::uint32_t head_dim,
@@ -1123,39 +1198,13 @@ extern "C" __global__ void halo_scale_silu(float* x, float scale, std::uint32_t 
 // ---- fp32 GEMMs for prefill routers and small projections, shared-expert add, batched top-k (reference names) --
 // core.hip:2938-2956, 3767-3800, 5605-5680, 8975-9000; batch_decode.hip:1157-1165. y [T][rows] = x [T][cols] W^T.
 
-// 64 rows x 64 tokens per block, K staged 32 at a time in LDS, 4 x 4 outputs per thread, products added in
-// ascending k. grid (ceil(T / 64), ceil(rows / 64)), block 256.
+// 64 rows x 64 tokens per block on fp32 MFMA: the tile body of halo_gemm_f32_nt (v_mfma_f32_32x32x2f32, K staged
+// 32 at a time through LDS, the next stage prefetched into registers), with the reference's grid. cols % 16 == 0
+// (a trailing half stage is zero-filled). grid (ceil(T / 64), ceil(rows / 64)), block 256.
 extern "C" __global__ void __launch_bounds__(256)
     halo_gemm_f32_tiled(const float* w, const float* x, float* y, std::uint32_t rows, std::uint32_t cols,
                         std::uint32_t tokens) {
-  constexpr std::uint32_t BM = 64, BN = 64, BK = 32;
-  __shared__ float ws[BK][BM + 1], xs[BK][BN + 1];
-  const std::uint32_t tid = threadIdx.x, r0 = blockIdx.y * BM, t0 = blockIdx.x * BN;
-  const std::uint32_t tr = (tid % 16) * 4, tt = (tid / 16) * 4;
-  float acc[4][4] = {};
-  for (std::uint32_t k0 = 0; k0 < cols; k0 += BK) {
-    // 64 x 32 of each operand: thread loads 8 values of W and 8 of x (k fastest, coalesced), zero past the edges
-    for (std::uint32_t e = tid; e < BM * BK; e += 256) {
-      const std::uint32_t rr = e / BK, kk = e % BK, r = r0 + rr, t = t0 + rr, k = k0 + kk;
-      ws[kk][rr] = r < rows && k < cols ? w[static_cast<std::size_t>(r) * cols + k] : 0.0f;
-      xs[kk][rr] = t < tokens && k < cols ? x[static_cast<std::size_t>(t) * cols + k] : 0.0f;
-    }
-    __syncthreads();
-#pragma unroll 8
-    for (std::uint32_t kk = 0; kk < BK; ++kk)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(ws[kk][tr + i], xs[kk][tt + j], acc[i][j]);
-    __syncthreads();
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const std::uint32_t r = r0 + tr + i, t = t0 + tt + j;
-      if (r < rows && t < tokens) y[static_cast<std::size_t>(t) * rows + r] = acc[i][j];
-    }
+  halo::GemmF32NtTile(x, w, nullptr, y, nullptr, tokens, rows, cols, rows, blockIdx.y * 64, blockIdx.x * 64);
 }
 // One wave per output row (2 rows per wave of the block's 8), lanes across columns. grid (ceil(rows / 8), T).
 extern "C" __global__ void __launch_bounds__(256)
@@ -1172,41 +1221,68 @@ extern "C" __global__ void __launch_bounds__(256)
     if (lane == 0) y[static_cast<std::size_t>(t) * rows + r] = acc;
   }
 }
-// Few columns: one thread per output, x row in LDS. grid (ceil(rows / 256), T), block 256; cols <= 8192.
+// Few columns (core.hip:3771-3782): one output row per thread, the token's x row in LDS. W is staged through LDS in
+// 256-row x 32-column tiles read along the rows (32 consecutive floats per row, coalesced), so no thread walks its
+// own row in HBM; each thread then sums its tile row in ascending k (one fused chain).
+// grid (ceil(rows / 256), T), block 256; cols <= 8192.
 extern "C" __global__ void __launch_bounds__(256)
     halo_gemm_f32_narrow(const float* w, const float* x, float* y, std::uint32_t rows, std::uint32_t cols) {
+  constexpr std::uint32_t BK = 32;
   __shared__ float xs[8192];
-  const std::uint32_t t = blockIdx.y;
-  for (std::uint32_t i = threadIdx.x; i < cols; i += blockDim.x) xs[i] = x[static_cast<std::size_t>(t) * cols + i];
-  __syncthreads();
-  const std::uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= rows) return;
-  const float* wr = w + static_cast<std::size_t>(r) * cols;
+  __shared__ float tile[256][BK + 1];
+  const std::uint32_t tid = threadIdx.x, r0 = blockIdx.x * 256;
+  const std::size_t t = blockIdx.y;
+  for (std::uint32_t i = tid; i < cols; i += 256) xs[i] = x[t * cols + i];
   float acc = 0.0f;
-  for (std::uint32_t c = 0; c < cols; ++c) acc = __builtin_fmaf(wr[c], xs[c], acc);
-  y[static_cast<std::size_t>(t) * rows + r] = acc;
+  for (std::uint32_t k0 = 0; k0 < cols; k0 += BK) {
+    __syncthreads();  // the previous tile is consumed (and, the first time, xs is written)
+    for (std::uint32_t e = tid; e < 256 * BK; e += 256) {
+      const std::uint32_t rr = e / BK, kk = e % BK, r = r0 + rr, k = k0 + kk;
+      tile[rr][kk] = r < rows && k < cols ? w[static_cast<std::size_t>(r) * cols + k] : 0.0f;
+    }
+    __syncthreads();
+    const std::uint32_t kn = min(BK, cols - k0);
+    for (std::uint32_t kk = 0; kk < kn; ++kk) acc = __builtin_fmaf(tile[tid][kk], xs[k0 + kk], acc);
+  }
+  if (r0 + tid < rows) y[t * rows + r0 + tid] = acc;
 }
-// Few rows (<= 16): a 32-lane half wave per token reads the token's row once against every weight row.
-// grid (ceil(T / 8)), block 256.
+// Few rows (<= 16; core.hip:8975-9000): each wave takes two of the block's 8 tokens in turn, all 64 lanes across the
+// token's row (16-byte loads when the row allows), every weight row against it (the few weight rows stay in cache),
+// then one wave reduction per row. grid (ceil(T / 8)), block 256.
 extern "C" __global__ void __launch_bounds__(256)
     halo_gemm_f32_skinny(const float* w, const float* x, float* y, std::uint32_t rows, std::uint32_t cols,
                          std::uint32_t tokens) {
-  const std::uint32_t lane = threadIdx.x % 32, t = blockIdx.x * 8 + threadIdx.x / 32;
-  const std::uint32_t tc = min(t, tokens - 1);  // every half wave reaches the group sums
-  const float* xr = x + static_cast<std::size_t>(tc) * cols;
-  float acc[16];
+  const std::uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  for (std::uint32_t tt = 0; tt < 2; ++tt) {
+    const std::uint32_t t = blockIdx.x * 8 + wave * 2 + tt;
+    if (t >= tokens) break;  // wave-uniform
+    const float* xr = x + static_cast<std::size_t>(t) * cols;
+    float acc[16];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-  for (std::uint32_t c = lane; c < cols; c += 32) {
-    const float xv = xr[c];
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    const bool vec = Vec4Ok(xr, cols) && Vec4Ok(w, cols);
+    const std::uint32_t nv = vec ? cols / 4 : 0;
+    for (std::uint32_t c4 = lane; c4 < nv; c4 += kWave) {
+      const float4 xv = reinterpret_cast<const float4*>(xr)[c4];
 #pragma unroll
-    for (std::uint32_t r = 0; r < 16; ++r)
-      if (r < rows) acc[r] = __builtin_fmaf(w[static_cast<std::size_t>(r) * cols + c], xv, acc[r]);
-  }
+      for (std::uint32_t r = 0; r < 16; ++r)
+        if (r < rows) {
+          const float4 wv = reinterpret_cast<const float4*>(w + static_cast<std::size_t>(r) * cols)[c4];
+          acc[r] = __builtin_fmaf(wv.w, xv.w,
+                                  __builtin_fmaf(wv.z, xv.z, __builtin_fmaf(wv.y, xv.y, __builtin_fmaf(wv.x, xv.x, acc[r]))));
+        }
+    }
+    for (std::uint32_t c = 4 * nv + lane; c < cols; c += kWave) {  // scalar path (unaligned rows)
+      const float xv = xr[c];
 #pragma unroll
-  for (std::uint32_t r = 0; r < 16; ++r) {
-    const float s = halo::GroupSum<32>(acc[r]);
-    if (lane == 0 && t < tokens && r < rows) y[static_cast<std::size_t>(t) * rows + r] = s;
+      for (std::uint32_t r = 0; r < 16; ++r)
+        if (r < rows) acc[r] = __builtin_fmaf(w[static_cast<std::size_t>(r) * cols + c], xv, acc[r]);
+    }
+#pragma unroll
+    for (std::uint32_t r = 0; r < 16; ++r) {
+      const float sum = halo::GroupSum(acc[r]);
+      if (lane == 0 && r < rows) y[static_cast<std::size_t>(t) * rows + r] = sum;
+    }
   }
 }
 
@@ -1262,54 +1338,56 @@ extern "C" __global__ void halo_conv_l2norm_y(const float* in, const std::uint64
                                               std::uint32_t tslot, const float* w, float* out, std::uint32_t channels,
                                               std::uint32_t kern, std::uint32_t l2_channels, float eps,
                                               std::uint32_t stride) {
-  __shared__ float red[16];
+  __shared__ float sh[256];
   const std::size_t e = blockIdx.y;
   ConvL2norm(in + e * stride, reinterpret_cast<float*>(tab[e * tstride + tslot]), w, out + e * stride, channels, kern,
-             l2_channels, eps, red);
+             l2_channels, eps, sh);
 }
 
-// halo_conv_l2norm_prefill for kern = 4 with eight tokens per thread (core.hip:3512-3570): the window x[t - 3 .. t]
-// loaded once for all eight, the sums in the stepping order. grid (channels / 128, ceil(T / 8)), block 128 (a head).
+// halo_conv_l2norm_prefill for kern = 4 over tiles of 128 channels x 8 tokens (the reference's grid, core.hip:
+// 3512-3570), mapped wave64-first: wave w takes tokens t0 + 4 w .. t0 + 4 w + 3 of the whole head, lane l its channels
+// l and l + 64, so a token's L2 sum is one wave's reduction (no LDS, no barrier). Each channel's 7-input window is
+// loaded once for its four tokens. Arithmetic as stepping: the same bits as halo_conv_l2norm_prefill.
+//   grid (ceil(channels / 128), ceil(T / 8)), block 128.
 extern "C" __global__ void __launch_bounds__(128)
     halo_conv_l2norm_prefill8(const float* in, const float* state, const float* w, float* out, std::uint32_t channels,
                               std::uint32_t tokens, std::uint32_t l2_channels, float eps) {
-  constexpr std::uint32_t TT = 8, K = 4;
-  __shared__ float part[TT][2];
-  const std::uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x, t0 = blockIdx.y * TT;
-  const std::uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  const bool live = ch < channels;
-  const std::uint32_t c = live ? ch : 0;
-  float x[TT + K - 1];  // inputs t0 - 3 .. t0 + 7, from the chunk or, before it, the conv state
+  constexpr std::uint32_t K = 4, TW = 4;
+  const std::uint32_t lane = threadIdx.x % kWave, c0 = blockIdx.x * 128;
+  const std::int64_t tb = static_cast<std::int64_t>(blockIdx.y) * 8 + (threadIdx.x / kWave) * TW;
+  float v[2][TW];
 #pragma unroll
-  for (std::uint32_t j = 0; j < TT + K - 1; ++j) {
-    const std::int64_t i = static_cast<std::int64_t>(t0) - static_cast<std::int64_t>(K - 1) + j;
-    x[j] = i >= static_cast<std::int64_t>(tokens) ? 0.0f
-           : i >= 0 ? in[static_cast<std::size_t>(i) * channels + c]
-                    : state[static_cast<std::size_t>(i + K - 1) * channels + c];
-  }
-  const float* wc = w + static_cast<std::size_t>(c) * K;
-  const float w0 = wc[0], w1 = wc[1], w2 = wc[2], w3 = wc[3];
-  float v[TT];
+  for (std::uint32_t half = 0; half < 2; ++half) {
+    const std::uint32_t ch = c0 + half * kWave + lane;
+    const bool live = ch < channels;
+    const std::uint32_t c = live ? ch : 0;
+    float x[TW + K - 1];  // inputs tb - 3 .. tb + 3
 #pragma unroll
-  for (std::uint32_t t = 0; t < TT; ++t) {
-    float acc = w3 * x[t + 3];
-    acc += w0 * x[t];
-    acc += w1 * x[t + 1];
-    acc += w2 * x[t + 2];
-    v[t] = live ? halo::Silu(acc) : 0.0f;
-  }
-  if (blockIdx.x * blockDim.x < l2_channels) {  // block-uniform
-#pragma unroll
-    for (std::uint32_t t = 0; t < TT; ++t) {
-      const float s = halo::GroupSum(v[t] * v[t]);
-      if (lane == 0) part[t][wave] = s;
+    for (std::uint32_t j = 0; j < TW + K - 1; ++j) {
+      const std::int64_t i = tb - static_cast<std::int64_t>(K - 1) + j;
+      x[j] = i < static_cast<std::int64_t>(tokens) ? ConvInput(in, state, i, c, channels, K) : 0.0f;
     }
-    __syncthreads();
+    const float* wc = w + static_cast<std::size_t>(c) * K;
 #pragma unroll
-    for (std::uint32_t t = 0; t < TT; ++t) v[t] *= 1.0f / sqrtf(part[t][0] + part[t][1] + eps);
+    for (std::uint32_t t = 0; t < TW; ++t) {
+      float win[kMaxTaps] = {x[t], x[t + 1], x[t + 2], x[t + 3]};
+      v[half][t] = live ? ConvSilu(wc, win, K) : 0.0f;
+    }
   }
-  if (!live) return;
+  if (c0 < l2_channels) {  // block-uniform
 #pragma unroll
-  for (std::uint32_t t = 0; t < TT; ++t)
-    if (t0 + t < tokens) out[static_cast<std::size_t>(t0 + t) * channels + ch] = v[t];
+    for (std::uint32_t t = 0; t < TW; ++t) {
+      const float ss = halo::GroupSum(__builtin_fmaf(v[1][t], v[1][t], __builtin_fmaf(v[0][t], v[0][t], 0.0f)));
+      const float inv = 1.0f / sqrtf(ss + eps);
+      v[0][t] *= inv;
+      v[1][t] *= inv;
+    }
+  }
+#pragma unroll
+  for (std::uint32_t half = 0; half < 2; ++half) {
+    const std::uint32_t ch = c0 + half * kWave + lane;
+#pragma unroll
+    for (std::uint32_t t = 0; t < TW; ++t)
+      if (ch < channels && tb + t < tokens) out[static_cast<std::size_t>(tb + t) * channels + ch] = v[half][t];
+  }
 }

@@ -712,13 +712,16 @@ def test_small_elementwise(dev):
     close(gx.download(), silu((x[0] * np.float32(0.25)).astype(np.float32)), np.abs(x[0]) + 1e-3)
 
 
-@pytest.mark.parametrize("name", ["halo_gemm_f32_tiled", "halo_gemm_f32_rows", "halo_gemm_f32_narrow",
-                                  "halo_gemm_f32_skinny"])
-def test_f32_gemms(dev, name):
+@pytest.mark.parametrize("name,cols", [("halo_gemm_f32_tiled", 2048), ("halo_gemm_f32_tiled", 1040),
+                                       ("halo_gemm_f32_rows", 2048), ("halo_gemm_f32_narrow", 96),
+                                       ("halo_gemm_f32_narrow", 1001), ("halo_gemm_f32_skinny", 2048),
+                                       ("halo_gemm_f32_skinny", 1001)])
+def test_f32_gemms(dev, name, cols):
     """The fp32 prefill GEMMs (core.hip:3767-3800, 5605-5680, 8975-9000) against a float64 product; 1e-5 of
-    sum |term|. Ragged rows and tokens."""
+    sum |term|. Ragged rows and tokens; a trailing half stage for the tiled GEMM (cols % 32 == 16), unaligned rows
+    (cols 1001) for the narrow and skinny ones."""
     rng = np.random.default_rng(57)
-    T, cols = 70, 2048 if name != "halo_gemm_f32_narrow" else 96
+    T = 70
     rows = 13 if name == "halo_gemm_f32_skinny" else 130
     w = rng.normal(0, 0.02, (rows, cols)).astype(np.float32)
     x = rng.normal(0, 1, (T, cols)).astype(np.float32)
@@ -814,19 +817,21 @@ def test_batched_select_and_conv_through_tables(dev):
         assert gst[e].download().tobytes() == s1.download().tobytes()
 
 
-@pytest.mark.parametrize("T", [13, 2])
-def test_conv_prefill8(dev, T):
-    """halo_conv_l2norm_prefill8 (kern 4, eight tokens per thread; core.hip:3512-3570) against numpy: causal conv
-    over the state then the chunk, SiLU, the first two heads L2-normalised; 1e-5 of the terms' magnitude."""
+@pytest.mark.parametrize("T,C", [(13, 512), (2, 512), (21, 576)])
+def test_conv_prefill8(dev, T, C):
+    """halo_conv_l2norm_prefill8 (kern 4, 128 channels x 8 tokens per block; core.hip:3512-3570) against numpy:
+    causal conv over the state then the chunk, SiLU, the first two heads L2-normalised; 1e-5 of the terms' magnitude.
+    Its bytes equal halo_conv_l2norm_prefill's (the stepping arithmetic) on the same input, including a partial last
+    head (C = 576: channels not a multiple of 128) and T % 8 != 0."""
     rng = np.random.default_rng(60 + T)
-    C, K, d, l2 = 512, 4, 128, 256
+    K, d, l2 = 4, 128, 256
     w = rng.normal(0, 0.5, (C, K)).astype(np.float32)
     st = rng.normal(0, 1, (K - 1, C)).astype(np.float32)
     x = rng.normal(0, 1, (T, C)).astype(np.float32)
     go = dev.array((T, C), np.float32)
-    dev.launch("halo_conv_l2norm_prefill8", (C // d, (T + 7) // 8), (d,),
-               [dev.to_device(x), dev.to_device(st), dev.to_device(w), go, ("u32", C), ("u32", T), ("u32", l2),
-                ("f32", 1e-6)])
+    gx, gst, gw = dev.to_device(x), dev.to_device(st), dev.to_device(w)
+    dev.launch("halo_conv_l2norm_prefill8", ((C + d - 1) // d, (T + 7) // 8), (d,),
+               [gx, gst, gw, go, ("u32", C), ("u32", T), ("u32", l2), ("f32", 1e-6)])
     seq = np.concatenate([st, x]).astype(np.float64)
     conv = np.stack([(seq[t:t + K] * w.T).sum(0) for t in range(T)])
     y = silu(conv.astype(np.float32))
@@ -834,4 +839,9 @@ def test_conv_prefill8(dev, T):
         seg = y[:, h * d:(h + 1) * d]
         y[:, h * d:(h + 1) * d] = seg / np.sqrt((seg * seg).sum(1, keepdims=True) + 1e-6)
     mag = np.stack([(np.abs(seq[t:t + K] * w.T)).sum(0) for t in range(T)]) + 1e-3
-    close(go.download(), y, mag)
+    got = go.download()
+    close(got, y, mag)
+    g1 = dev.array((T, C), np.float32)
+    dev.launch("halo_conv_l2norm_prefill", ((C + d - 1) // d, T), (d,),
+               [gx, gst, gw, g1, ("u32", C), ("u32", K), ("u32", l2), ("f32", 1e-6)])
+    assert got.tobytes() == g1.download().tobytes()

@@ -391,6 +391,7 @@ _SIGS = {
     "halo_op_moe_workspace_bytes": (_SZ, [C.POINTER(MoeWeights), _U32], False),
     "halo_op_moe_views": (C.c_int, [C.POINTER(MoeWeights), _U32, _VP, C.POINTER(MoeViews)], True),
     "halo_op_moe_decode": (C.c_int, [_VP, C.POINTER(MoeWeights), _VP, _VP, _U32, _VP, _SZ], True),
+    "halo_op_moe_decode_noalloc": (C.c_int, [_VP, C.POINTER(MoeWeights), _VP, _VP, _U32], True),
     "halo_gguf_open_file": (C.c_int, [C.c_char_p, C.POINTER(_VP)], True),
     "halo_gguf_open_memory": (C.c_int, [_VP, _SZ, C.POINTER(_VP)], True),
     "halo_gguf_close": (None, [_VP], False),

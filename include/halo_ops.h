@@ -147,6 +147,13 @@ int halo_op_moe_views(const halo_moe_weights* w, uint32_t tokens, void* ws, halo
                       size_t errlen);
 int halo_op_moe_decode(halo_engine* eng, const halo_moe_weights* w, const float* x, float* out, uint32_t tokens,
                        void* ws, size_t ws_bytes, char* err, size_t errlen);
+/* halo_op_moe_decode with no workspace argument and no allocation: the workspace is a fixed 512 KiB device array of
+ * this library (one per GPU, held until the process ends), located once per device on the first call. No reference
+ * counterpart: for callers that cannot allocate device memory (code under stream capture, serving loops that forbid
+ * hipMalloc). Layers whose halo_op_moe_workspace_bytes exceeds 512 KiB are refused with an error (the C2 layer at 16
+ * tokens needs 422 KiB). Calls that overlap on one GPU (other streams or threads) race on the shared array. */
+int halo_op_moe_decode_noalloc(halo_engine* eng, const halo_moe_weights* w, const float* x, float* out,
+                               uint32_t tokens, char* err, size_t errlen);
 /* The same layer with the FFN input norm folded into the router launch (the reference's post-attention
  * residual add + RMSNorm before Moe, src/engine/flash_next_gpu.cpp:697-845): in->x = residual, in->delta = the
  * attention / DeltaNet output, in->norm_w = the FFN norm weights, in->eps; in->res_out (not in->x) receives

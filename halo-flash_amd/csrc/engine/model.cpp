@@ -146,7 +146,37 @@ int Check(const halo_model_config* c, char* err, std::size_t errlen) {
   return 0;
 }
 
-int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std::size_t errlen) {
+// Teacher-forcing trace of an eager step (halo_model_step_trace): after the launches that produce them, named device
+// tensors are copied into the caller's trace buffer (one halo_copy launch each) and listed in `entries`.
+struct Tracer {
+  halo_engine* eng = nullptr;
+  char* base = nullptr;
+  std::size_t cap = 0, used = 0;
+  halo_model_trace_entry* entries = nullptr;
+  std::uint32_t max_entries = 0, n = 0;
+
+  int Save(const char* name, std::uint32_t layer, std::uint32_t dtype, const void* src, std::size_t bytes, char* err,
+           std::size_t errlen) {
+    if (bytes % 4 != 0) return SetErr(err, errlen, "trace: %s has %zu bytes (not whole words)", name, bytes), -1;
+    const std::size_t at = (used + 255) / 256 * 256;
+    if (at + bytes > cap || n >= max_entries)
+      return SetErr(err, errlen, "trace: buffer of %zu bytes / %u entries too small at %s of layer %u", cap,
+                    max_entries, name, layer), -1;
+    halo_model_trace_entry& e = entries[n++];
+    e = halo_model_trace_entry{};
+    std::snprintf(e.name, sizeof e.name, "%s", name);
+    e.layer = layer;
+    e.dtype = dtype;
+    e.offset = at;
+    e.bytes = bytes;
+    used = at + bytes;
+    const halo_arg a[] = {Ptr(base + at), Ptr(src), U32(static_cast<std::uint32_t>(bytes / 4))};
+    return Launch(eng, "halo_copy", D3(CeilDiv(bytes / 4, 256 * 4)), D3(256), a, err, errlen);
+  }
+};
+
+int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std::size_t errlen,
+           Tracer* tr = nullptr) {
   const halo_model_config& c = m->c;
   const std::uint32_t H = c.hidden, Hv = c.gdn_v_heads, Hk = c.gdn_k_heads, d = c.gdn_head_dim;
   const std::uint32_t Dv = Hv * d, C = m->conv_ch, Hq = c.q_heads, Hkv = c.kv_heads, hd = c.head_dim;
@@ -193,6 +223,10 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
     in.res_out = have_delta ? P<float>(*alt) : nullptr;
     in.eps = eps;
     in.mode = HALO_PROJ_N;
+    if (tr != nullptr) {  // the trace records the prologue's quantized activations
+      in.xq_out = P<int8_t>(m->xq);
+      in.xs_out = P<float>(m->xs);
+    }
     if (halo_op_proj_q8(eng, ms, ys, n, &in, S, err, errlen) != 0) return -1;
     if (have_delta) std::swap(cur, alt);
     have_delta = false;
@@ -201,9 +235,26 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
   auto gemv = [&](const Q8& w, const halo_buffer& xq, const halo_buffer& xs, const halo_buffer& y) {
     return halo_op_matvec_q8a8(eng, &w.m, P<int8_t>(xq), P<float>(xs), P<float>(y), S, w.m.rows, err, errlen);
   };
+  // trace helpers (no-ops without a tracer): fp32 / int8 / uint32 tensors of `count` elements
+  std::uint32_t li = 0;
+  auto save = [&](const char* name, std::uint32_t dtype, const void* src, std::size_t count) {
+    if (tr == nullptr) return 0;
+    return tr->Save(name, li, dtype, src, count * (dtype == HALO_TRACE_I8 ? 1 : 4), err, errlen);
+  };
+  auto save_input = [&]() {  // the layer's residual input and its quantized norm
+    if (save("res_in", HALO_TRACE_F32, cur->device, static_cast<std::size_t>(S) * H) != 0 ||
+        save("xq", HALO_TRACE_I8, m->xq.device, static_cast<std::size_t>(S) * H) != 0 ||
+        save("xs", HALO_TRACE_F32, m->xs.device, static_cast<std::size_t>(S) * H / 32) != 0)
+      return -1;
+    return 0;
+  };
   for (auto& L : m->layers) {
     if (!L.attn) {
       if (proj_norm(L.attn_norm, {&L.qkv, &L.z, &L.ab}, {&m->qkv, &m->zo, &m->abo}) != 0) return -1;
+      if (save_input() != 0 || save("qkv", HALO_TRACE_F32, m->qkv.device, static_cast<std::size_t>(S) * C) != 0 ||
+          save("z", HALO_TRACE_F32, m->zo.device, static_cast<std::size_t>(S) * Dv) != 0 ||
+          save("ab", HALO_TRACE_F32, m->abo.device, static_cast<std::size_t>(S) * 2 * Hv) != 0)
+        return -1;
       float* ring = P<float>(m->conv_state) + static_cast<std::size_t>(L.gdn_index) * c.max_sessions *
                                                   c.conv_kernel * C;
       float* st = P<float>(m->gdn_state) + static_cast<std::size_t>(L.gdn_index) * c.max_sessions * Hv * d * d;
@@ -214,10 +265,17 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
                               U32(c.conv_kernel), Val(eps)};
         if (Launch(eng, "halo_gdn_step_q8", D3(S * Hv), D3(512), a, err, errlen) != 0) return -1;
       }
+      if (save("oq", HALO_TRACE_I8, m->oq.device, static_cast<std::size_t>(S) * Dv) != 0 ||
+          save("os", HALO_TRACE_F32, m->os.device, static_cast<std::size_t>(S) * Dv / 32) != 0)
+        return -1;
       if (gemv(L.out, m->oq, m->os, m->delta) != 0) return -1;
-      (void)Dv;
     } else {
       if (proj_norm(L.attn_norm, {&L.qg, &L.k, &L.v}, {&m->qgo, &m->ko, &m->vo}) != 0) return -1;
+      if (save_input() != 0 ||
+          save("qg", HALO_TRACE_F32, m->qgo.device, static_cast<std::size_t>(S) * 2 * Hq * hd) != 0 ||
+          save("k", HALO_TRACE_F32, m->ko.device, static_cast<std::size_t>(S) * Hkv * hd) != 0 ||
+          save("v", HALO_TRACE_F32, m->vo.device, static_cast<std::size_t>(S) * Hkv * hd) != 0)
+        return -1;
       {
         const halo_arg a[] = {Ptr(m->qgo.device), Ptr(m->ko.device), Ptr(m->vo.device), Ptr(L.q_norm.device),
                               Ptr(L.k_norm.device), Ptr(m->q.device), Ptr(m->agate.device), Ptr(L.k_pool.device),
@@ -230,9 +288,12 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
       if (halo_op_attn_decode_q8(eng, &kv, P<float>(m->q), P<float>(m->agate), nullptr, P<int8_t>(m->oq),
                                  P<float>(m->os), Hq, m->attn_ws.device, m->attn_ws_bytes, err, errlen) != 0)
         return -1;
-      (void)hd;
+      if (save("oq", HALO_TRACE_I8, m->oq.device, static_cast<std::size_t>(S) * Hq * hd) != 0 ||
+          save("os", HALO_TRACE_F32, m->os.device, static_cast<std::size_t>(S) * Hq * hd / 32) != 0)
+        return -1;
       if (gemv(L.o, m->oq, m->os, m->delta) != 0) return -1;
     }
+    if (save("delta", HALO_TRACE_F32, m->delta.device, static_cast<std::size_t>(S) * H) != 0) return -1;
     have_delta = true;
     if (S <= 4 && (H == 2048 || H == 4096) && S * H <= 8192) {
       // the FFN norm runs in the router's prologue
@@ -253,9 +314,30 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
                              m->moe_ws_bytes, err, errlen) != 0)
         return -1;
     }
+    if (tr != nullptr) {  // the MoE's input residual, routing, h and output
+      halo_moe_views v;
+      if (halo_op_moe_views(&L.moe, S, m->moe_ws.device, &v, err, errlen) != 0) return -1;
+      const std::uint32_t k = c.n_used;
+      if (save("mres", HALO_TRACE_F32, cur->device, static_cast<std::size_t>(S) * H) != 0 ||
+          save("mxq", HALO_TRACE_I8, v.xq, static_cast<std::size_t>(S) * H) != 0 ||
+          save("mxs", HALO_TRACE_F32, v.xs, static_cast<std::size_t>(S) * H / 32) != 0 ||
+          save("mlogits", HALO_TRACE_F32, v.logits, static_cast<std::size_t>(S) * c.n_experts) != 0 ||
+          save("mshared", HALO_TRACE_F32, v.shared_logit, S) != 0 ||
+          save("mids", HALO_TRACE_U32, v.ids, static_cast<std::size_t>(S) * k) != 0 ||
+          save("mweights", HALO_TRACE_F32, v.weights, static_cast<std::size_t>(S) * k) != 0 ||
+          save("mh", HALO_TRACE_F32, v.h, static_cast<std::size_t>(S) * (k + 1) * v.hstride) != 0 ||
+          save("mout", HALO_TRACE_F32, m->delta.device, static_cast<std::size_t>(S) * H) != 0)
+        return -1;
+    }
     have_delta = true;
+    ++li;
   }
   if (norm(m->out_norm, true) != 0) return -1;
+  li = UINT32_MAX;
+  if (save("res_in", HALO_TRACE_F32, cur->device, static_cast<std::size_t>(S) * H) != 0 ||
+      save("xq", HALO_TRACE_I8, m->xq.device, static_cast<std::size_t>(S) * H) != 0 ||
+      save("xs", HALO_TRACE_F32, m->xs.device, static_cast<std::size_t>(S) * H / 32) != 0)
+    return -1;
   if (gemv(m->head, m->xq, m->xs, m->logits) != 0) return -1;
   if (m->sampling) {
     // every session draws with its own parameters (temperature 0 is the argmax); the advance takes the drawn
@@ -725,6 +807,24 @@ int halo_model_step_eager(halo_model* m, uint32_t S, uint32_t prefix, char* err,
   return Record(m, S, prefix, err, errlen);
 }
 
+int halo_model_step_trace(halo_model* m, uint32_t S, uint32_t prefix, void* trace, size_t trace_bytes,
+                          halo_model_trace_entry* entries, uint32_t max_entries, uint32_t* n_entries, char* err,
+                          size_t errlen) {
+  if (m == nullptr || trace == nullptr || entries == nullptr || n_entries == nullptr)
+    return SetErr(err, errlen, "trace: null argument"), -1;
+  if (S == 0 || S > m->c.max_sessions || prefix % 64 != 0 || prefix > m->c.prefix_tokens)
+    return SetErr(err, errlen, "trace: %u sessions / prefix %u unsupported", S, prefix), -1;
+  Tracer tr;
+  tr.eng = m->eng;
+  tr.base = static_cast<char*>(trace);
+  tr.cap = trace_bytes;
+  tr.entries = entries;
+  tr.max_entries = max_entries;
+  const int rc = Record(m, S, prefix, err, errlen, &tr);
+  *n_entries = tr.n;
+  return rc;
+}
+
 int halo_model_run(halo_model* m, uint32_t S, uint32_t prefix, uint32_t steps, char* err, size_t errlen) {
   if (S == 0 || S > m->c.max_sessions || prefix % 64 != 0 || prefix > m->c.prefix_tokens)
     return SetErr(err, errlen, "run: %u sessions / prefix %u unsupported", S, prefix), -1;
@@ -755,6 +855,10 @@ int halo_model_tensor(const halo_model* m, uint32_t layer, const char* name, hal
     *out = halo_model_tensor_view{b.device, nullptr, HALO_TENSOR_F32, rows, cols, cols};
     return 0;
   };
+  auto f32Raw = [&](void* p, std::uint32_t rows, std::uint32_t cols) {
+    *out = halo_model_tensor_view{p, nullptr, HALO_TENSOR_F32, rows, cols, cols};
+    return 0;
+  };
   auto q8 = [&](const Q8& w) {
     if (w.qs.device == nullptr) return SetErr(err, errlen, "tensor %s absent in layer %u", name, layer), -1;
     *out = halo_model_tensor_view{w.qs.device, w.d.device, HALO_TENSOR_Q8, w.m.rows, w.m.cols, w.m.qstride};
@@ -765,11 +869,25 @@ int halo_model_tensor(const halo_model* m, uint32_t layer, const char* name, hal
     if (n == "embd") return q8(m->embd);
     if (n == "head") return q8(m->head);
     if (n == "out_norm") return f32(m->out_norm, 1, c.hidden);
+    // page tables [max_sessions][max_pages] and positions [max_sessions], uint32 (viewed as 4-byte words)
+    if (n == "pages") return f32(m->pages, c.max_sessions, m->max_pages);
+    if (n == "nkv") return f32(m->nkv, 1, c.max_sessions);
     return SetErr(err, errlen, "unknown tensor %s", name), -1;
   }
   if (layer >= m->layers.size()) return SetErr(err, errlen, "layer %u out of range", layer), -1;
   const Layer& L = m->layers[layer];
   const std::uint32_t H = c.hidden, Hv = c.gdn_v_heads, d = c.gdn_head_dim, hd = c.head_dim;
+  // recurrent state and caches (parity instrumentation): DeltaNet state [max_sessions][Hv][d][d] key-major and the
+  // conv ring [max_sessions][K][C] (position p's projection in slot p % K); attention KV pools [pages][Hkv][16][hd]
+  if (!L.attn && n == "state")
+    return f32Raw(P<float>(m->gdn_state) + static_cast<std::size_t>(L.gdn_index) * c.max_sessions * Hv * d * d,
+                  c.max_sessions * Hv * d, d);
+  if (!L.attn && n == "conv_ring")
+    return f32Raw(P<float>(m->conv_state) + static_cast<std::size_t>(L.gdn_index) * c.max_sessions *
+                                                c.conv_kernel * m->conv_ch,
+                  c.max_sessions * c.conv_kernel, m->conv_ch);
+  if (L.attn && n == "k_pool") return f32(L.k_pool, m->total_pages * c.kv_heads * 16, hd);
+  if (L.attn && n == "v_pool") return f32(L.v_pool, m->total_pages * c.kv_heads * 16, hd);
   if (n == "attn_norm") return f32(L.attn_norm, 1, H);
   if (n == "ffn_norm") return f32(L.ffn_norm, 1, H);
   if (n == "router") return f32(L.router, c.n_experts, H);

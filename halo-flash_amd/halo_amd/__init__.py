@@ -303,6 +303,15 @@ class TensorView(C.Structure):
         "kind", "rows", "cols", "qstride")]
 
 
+class TraceEntry(C.Structure):
+    """halo_model_trace_entry (include/halo_model.h)."""
+    _fields_ = [("name", C.c_char * 24), ("layer", C.c_uint32), ("dtype", C.c_uint32), ("offset", C.c_uint64),
+                ("bytes", C.c_uint64)]
+
+
+TRACE_DTYPES = {0: np.float32, 1: np.int8, 2: np.uint32}
+
+
 def c4_config(max_sessions=4, prefix_tokens=8192, max_context=8192 + 256 + 128):
     """Benchmark config C4: 48 layers (3 DeltaNet : 1 GQA), hidden 2048, vocab 151936, MoE as C2."""
     return ModelConfig(vocab=151936, hidden=2048, layers=48, attn_interval=4, gdn_k_heads=16, gdn_v_heads=32,
@@ -387,6 +396,8 @@ _SIGS = {
     "halo_model_positions": (C.c_int, [_VP, _VP, _U32], True),
     "halo_model_tensor": (C.c_int, [_VP, _U32, C.c_char_p, C.POINTER(TensorView)], True),
     "halo_model_logits": (C.c_int, [_VP, _U32, _VP], True),
+    "halo_model_step_trace": (C.c_int, [_VP, _U32, _U32, _VP, _SZ, C.POINTER(TraceEntry), _U32,
+                                        C.POINTER(_U32)], True),
     "halo_model_prefill": (C.c_int, [_VP, C.POINTER(PrefillSegment), _U32], True),
     "halo_op_moe_workspace_bytes": (_SZ, [C.POINTER(MoeWeights), _U32], False),
     "halo_op_moe_views": (C.c_int, [C.POINTER(MoeWeights), _U32, _VP, C.POINTER(MoeViews)], True),
@@ -682,6 +693,50 @@ class Model:
         qs = self._download(v.data, v.rows * v.qstride, np.int8).reshape(v.rows, v.qstride)[:, : v.cols]
         d = self._download(v.scales, v.rows * (v.cols // 32) * 2, np.uint16).reshape(v.rows, v.cols // 32)
         return np.ascontiguousarray(qs), d
+
+    def _view(self, layer: int, name: str) -> TensorView:
+        v = TensorView()
+        _call("halo_model_tensor", self.h, 0xFFFFFFFF if layer < 0 else layer, name.encode(), C.byref(v))
+        return v
+
+    def tensor_rows(self, layer: int, name: str, r0: int, n: int):
+        """Rows [r0, r0 + n) of a weight, as tensor() returns the whole of it (only those rows cross PCIe)."""
+        v = self._view(layer, name)
+        if v.kind == 0:
+            return self._download(v.data + r0 * v.cols * 4, n * v.cols * 4, np.float32).reshape(n, v.cols)
+        qs = self._download(v.data + r0 * v.qstride, n * v.qstride, np.int8).reshape(n, v.qstride)[:, : v.cols]
+        nb = v.cols // 32
+        d = self._download(v.scales + r0 * nb * 2, n * nb * 2, np.uint16).reshape(n, nb)
+        return np.ascontiguousarray(qs), d
+
+    def raw(self, layer: int, name: str, dtype=np.float32):
+        """A state tensor (state, conv_ring, k_pool, v_pool, pages, nkv) as [rows][cols] of 4-byte `dtype`."""
+        v = self._view(layer, name)
+        return self._download(v.data, v.rows * v.cols * 4, dtype).reshape(v.rows, v.cols)
+
+    def step_trace(self, S: int, prefix: int = 0) -> dict:
+        """One eager step with the teacher-forcing trace: {(layer, name): host array}; layer -1 is the head."""
+        cfg = self.cfg
+        per_layer = S * (16 * cfg.hidden + 8 * (2 * cfg.gdn_k_heads + 3 * cfg.gdn_v_heads) * cfg.gdn_head_dim +
+                         8 * 2 * cfg.q_heads * cfg.head_dim + 4 * cfg.n_experts +
+                         4 * (cfg.n_used + 1) * max(cfg.expert_ff, cfg.shared_ff) + 64) + 32 * 256
+        nbytes = (cfg.layers + 1) * per_layer
+        buf = self.dev.array(nbytes, np.uint8)
+        maxe = 32 * (cfg.layers + 1)
+        ents = (TraceEntry * maxe)()
+        n = C.c_uint32()
+        try:
+            _call("halo_model_step_trace", self.h, S, prefix, buf.ptr, nbytes, ents, maxe, C.byref(n))
+            self.dev.sync()
+            blob = buf.download()
+        finally:
+            buf.free()
+        out = {}
+        for e in ents[: n.value]:
+            layer = -1 if e.layer == 0xFFFFFFFF else int(e.layer)
+            arr = blob[e.offset: e.offset + e.bytes].view(TRACE_DTYPES[e.dtype]).copy()
+            out[(layer, e.name.decode())] = arr
+        return out
 
     def set_sampling(self, s: int, params: "SampleParams", penalties=None):
         """Device sampling for session s; penalties = (token, generated_count, repeated) arrays sorted by token."""

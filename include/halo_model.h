@@ -97,11 +97,33 @@ typedef struct halo_model_tensor_view {
   uint32_t kind, rows, cols, qstride;
 } halo_model_tensor_view;
 /* layer < layers: per-layer tensors by name: attn_norm, ffn_norm; DeltaNet layers: qkv, z, ab (alpha | beta rows),
- * out, conv_w [C][K], a, dt, norm_w; attention layers: qg (per head q | gate rows), k, v, o, q_norm, k_norm; every
- * layer: router [E][H], shared_gate [H], gate, up ([E * ff][H]), down ([E * H][ff]), sgate, sup, sdown.
- * layer == UINT32_MAX: embd, head, out_norm. */
+ * out, conv_w [C][K], a, dt, norm_w, and the recurrent state: state ([max_sessions Hv d][d], key-major per head),
+ * conv_ring ([max_sessions K][C]); attention layers: qg (per head q | gate rows), k, v, o, q_norm, k_norm, and the
+ * KV pools k_pool, v_pool ([pages Hkv 16][hd]); every layer: router [E][H], shared_gate [H], gate, up
+ * ([E * ff][H]), down ([E * H][ff]), sgate, sup, sdown. layer == UINT32_MAX: embd, head, out_norm, pages
+ * ([max_sessions][max_pages] uint32) and nkv ([max_sessions] uint32), both viewed as 4-byte words. */
 int halo_model_tensor(const halo_model* m, uint32_t layer, const char* name, halo_model_tensor_view* out, char* err,
                       size_t errlen);
+/* Teacher-forcing trace (parity instrumentation; the reference has no counterpart): one eager step, like
+ * halo_model_step_eager, that also copies the tensors a host restatement needs to check each layer from the GPU's own
+ * inputs into `trace` (device memory of trace_bytes) and lists them in entries[0 .. *n_entries). Per layer (entry
+ * layer = layer index): res_in (residual entering the layer, fp32 [S][H]), xq / xs (its RMSNorm quantized: int8
+ * [S][H], fp32 [S][H/32]); DeltaNet layers qkv [S][C], z [S][Hv d], ab [S][2 Hv]; attention layers qg [S][2 Hq hd],
+ * k, v [S][Hkv hd]; then oq / os (the mixer output quantized for the output projection), delta (its output
+ * [S][H]); mres (residual entering the MoE), mxq / mxs, mlogits [S][E], mshared [S], mids (uint32 [S][k]),
+ * mweights [S][k], mh (h rows [S (k + 1)][hstride], as halo_moe_views), mout (MoE output [S][H]). After the layers
+ * (layer = UINT32_MAX): res_in, xq, xs of the final norm. Each entry starts 256-byte aligned. The recurrent state
+ * before the step is read with halo_model_tensor ("state", "conv_ring", "k_pool", "v_pool", "pages", "nkv"). */
+enum { HALO_TRACE_F32 = 0, HALO_TRACE_I8 = 1, HALO_TRACE_U32 = 2 };
+typedef struct halo_model_trace_entry {
+  char name[24];
+  uint32_t layer, dtype;
+  uint64_t offset, bytes;
+} halo_model_trace_entry;
+int halo_model_step_trace(halo_model* m, uint32_t S, uint32_t attn_prefix, void* trace, size_t trace_bytes,
+                          halo_model_trace_entry* entries, uint32_t max_entries, uint32_t* n_entries, char* err,
+                          size_t errlen);
+
 /* Host copy of session s's logits of the last step ([vocab] fp32). Not capturable. */
 int halo_model_logits(halo_model* m, uint32_t s, float* out, char* err, size_t errlen);
 

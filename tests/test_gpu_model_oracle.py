@@ -2,16 +2,10 @@
 restatement in tests/model_ref.py, which composes the oracle's primitives the way ReferenceModel does.
 
 A twin of C4 (4 layers: 3 DeltaNet + 1 GQA, hidden 1024, 16 experts top-4 + shared, vocab 2048) is stepped on the
-GPU one token at a time (prompt tokens teacher-forced, then greedy) and on the host in lockstep.
-
-Bars: the first step within 1e-5 of max|logits|. Every step within 3e-2 of max|logits|
-and the same produced token unless the host's top two logits are closer than that. The looser bound is the
-Q8 activation quantizers: both paths quantize fp32 rows that differ in the last bits (parallel vs sequential
-sums), so a value sitting on a rounding boundary can land one code apart (measured: 1 in ~200 MoE calls moves a
-layer output by ~5e-4 relative); the recurrent state and the KV cache carry such a step forward, and four layers
-plus the LM head amplify it to ~1e-2 of max|logits| (one code of the largest MoE input of layer 0 moves the logits
-by 1.3e-2). Until such a flip the two paths agree to ~2e-7; which step first carries one depends on the kernels'
-summation order, so the bound after the first step is the flip bound.
+GPU and on the host from the same state: the first step's logits agree within 1e-5 of max|logits| end to end and the
+produced token is the same. Later steps are checked layer by layer, teacher-forced from the GPU's own inputs, in
+tests/test_gpu_model_teacher.py (a free-running comparison after the first step would measure Q8 rounding-boundary
+flips carried by the recurrent state rather than errors of the step).
 """
 import numpy as np
 import pytest
@@ -29,34 +23,21 @@ def twin():
                          max_sessions=2, max_context=64, prefix_tokens=0)
 
 
-def test_decode_steps_match_host_reference(dev):
+def test_first_decode_step_matches_host_reference(dev):
     cfg = twin()
     model = H.Model(dev, cfg, seed=11)
     try:
         ref = RefModel(model, cfg)
         rng = np.random.default_rng(3)
         prompt = rng.integers(0, cfg.vocab, 12).astype(np.uint32)
-        steps = 20
         model.reset()
         model.set_session(0, prompt)
-        token = int(prompt[0])
-        worst = 0.0
-        for i in range(steps):
-            model.step_eager(1)
-            got = model.logits(0)
-            want = ref.step(token)
-            scale = float(np.max(np.abs(want)))
-            err = float(np.max(np.abs(got - want))) / scale
-            worst = max(worst, err)
-            if i == 0:
-                assert err <= 1e-5, f"first step: logits off by {err:.2e} of max|logits|"
-            assert err <= 3e-2, f"step {i}: logits off by {err:.2e} of max|logits|"
-            top = np.argsort(want)[::-1]
-            if int(np.argmax(got)) != int(top[0]):
-                assert want[top[0]] - want[top[1]] <= 3e-2 * scale, f"step {i}: argmax differs away from a tie"
-            produced = int(model.history(0, i + 2)[i + 1])
-            assert produced == int(np.argmax(got))
-            token = int(prompt[i + 1]) if i + 1 < len(prompt) else produced
-        print(f"worst logits error {worst:.2e} of max|logits| over {steps} steps")
+        model.step_eager(1)
+        got = model.logits(0)
+        want = ref.step(int(prompt[0]))
+        err = float(np.max(np.abs(got - want))) / float(np.max(np.abs(want)))
+        assert err <= 1e-5, f"first step: logits off by {err:.2e} of max|logits|"
+        assert int(np.argmax(got)) == int(np.argmax(want))
+        assert int(model.history(0, 2)[1]) == int(np.argmax(got))
     finally:
         model.close()

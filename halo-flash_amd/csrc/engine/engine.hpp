@@ -69,6 +69,20 @@ inline int Launch(halo_engine* eng, const char* name, halo_dim3 grid, halo_dim3 
   return halo_engine_launch(eng, name, grid, block, args, N, err, errlen);
 }
 
+// The MoE prefill workspace (halo_op_moe_prefill): router logits [T][E], shared gate logit [T], x codes / scales,
+// routing ids / weights [T][k], group counts and starts, the tile table, each sorted pair's token, pos[t k + s] (the
+// sorted position of token t's slot s; the shared expert's pair of token t sits at T k + t), h [G][F] fp32 and its
+// codes / scales, the down outputs y [G][H].
+struct MoePrefillViews {
+  float *logits, *sgl, *xs, *weights, *h, *hs, *y;
+  std::int8_t *xq, *hq;
+  std::uint32_t *ids, *count, *start, *tiles, *ntiles, *token, *pos;
+  std::uint32_t max_tiles;
+  std::size_t bytes;
+};
+int MoePrefillLayout(const halo_moe_weights* w, std::uint32_t T, void* ws, MoePrefillViews* v, char* err,
+                     std::size_t errlen);
+
 }  // namespace halo::engine
 
 // The engine a model was created on (model.cpp; used by the GGUF loader).

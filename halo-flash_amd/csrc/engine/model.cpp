@@ -407,7 +407,8 @@ int PrefillAlloc(halo_model* m, char* err, std::size_t errlen) {
 
 // One prefill batch: segments with consecutive increasing sessions s0, s0 + 1, ..., positions already in the cache
 // below each segment's start. T = sum of lengths <= kPrefillCap.
-int PrefillBatch(halo_model* m, const std::vector<halo_prefill_segment>& segs, char* err, std::size_t errlen) {
+int PrefillBatch(halo_model* m, const std::vector<halo_prefill_segment>& segs, char* err, std::size_t errlen,
+                 Tracer* tr = nullptr) {
   const halo_model_config& c = m->c;
   halo_engine* eng = m->eng;
   auto& p = m->pf;
@@ -458,10 +459,26 @@ int PrefillBatch(halo_model* m, const std::vector<halo_prefill_segment>& segs, c
   };
   std::vector<halo_prefill_segment> asegs(segs);
   for (std::uint32_t i = 0, f = 0; i < nseg; f += asegs[i].length, ++i) asegs[i].first = f;
+  std::uint32_t li = 0;
+  auto save = [&](const char* name, std::uint32_t dtype, const void* src, std::size_t count) {
+    if (tr == nullptr) return 0;
+    return tr->Save(name, li, dtype, src, count * (dtype == HALO_TRACE_I8 ? 1 : 4), err, errlen);
+  };
+  auto save_norm = [&](const char* res, const char* q, const char* sc) {
+    if (save(res, HALO_TRACE_F32, p.res.device, static_cast<std::size_t>(T) * H) != 0 ||
+        save(q, HALO_TRACE_I8, p.xq.device, static_cast<std::size_t>(T) * H) != 0 ||
+        save(sc, HALO_TRACE_F32, p.xs.device, static_cast<std::size_t>(T) * H / 32) != 0)
+      return -1;
+    return 0;
+  };
   for (auto& L : m->layers) {
-    if (norm(L.attn_norm, false) != 0) return -1;
+    if (norm(L.attn_norm, false) != 0 || save_norm("res_in", "xq", "xs") != 0) return -1;
     if (!L.attn) {
       if (gemm(L.qkv, p.xq, p.xs, p.qkv) != 0 || gemm(L.z, p.xq, p.xs, p.zo) != 0 || gemm(L.ab, p.xq, p.xs, p.abo) != 0)
+        return -1;
+      if (save("qkv", HALO_TRACE_F32, p.qkv.device, static_cast<std::size_t>(T) * C) != 0 ||
+          save("z", HALO_TRACE_F32, p.zo.device, static_cast<std::size_t>(T) * Hv * d) != 0 ||
+          save("ab", HALO_TRACE_F32, p.abo.device, static_cast<std::size_t>(T) * 2 * Hv) != 0)
         return -1;
       float* ring = P<float>(m->conv_state) + static_cast<std::size_t>(L.gdn_index) * c.max_sessions * c.conv_kernel * C;
       {
@@ -471,6 +488,12 @@ int PrefillBatch(halo_model* m, const std::vector<halo_prefill_segment>& segs, c
                               U32(c.conv_kernel), Val(eps)};
         if (Launch(eng, "halo_gdn_prep_prefill", D3(T, C / 256), D3(256), a, err, errlen) != 0) return -1;
       }
+      if (save("gq", HALO_TRACE_F32, p.qb.device, static_cast<std::size_t>(T) * Hk * d) != 0 ||
+          save("gk", HALO_TRACE_F32, p.kb.device, static_cast<std::size_t>(T) * Hk * d) != 0 ||
+          save("gv", HALO_TRACE_F32, p.vb.device, static_cast<std::size_t>(T) * Hv * d) != 0 ||
+          save("g", HALO_TRACE_F32, p.g.device, static_cast<std::size_t>(T) * Hv) != 0 ||
+          save("beta", HALO_TRACE_F32, p.beta.device, static_cast<std::size_t>(T) * Hv) != 0)
+        return -1;
       {
         const halo_arg a[] = {Ptr(p.qkv.device), Ptr(ring), Ptr(p.segs.device), U32(c.conv_kernel), U32(C)};
         if (Launch(eng, "halo_gdn_ring_update", D3(nseg, C / 256), D3(256), a, err, errlen) != 0) return -1;
@@ -481,14 +504,22 @@ int PrefillBatch(halo_model* m, const std::vector<halo_prefill_segment>& segs, c
                               P<float>(p.beta), P<uint32_t>(p.chunks), P<uint32_t>(p.seqs), nchunks, nseg, st,
                               P<float>(p.o), Hv, Hk, d, p.gdn_ws.device, p.gdn_ws_bytes, err, errlen) != 0)
         return -1;
+      if (save("o", HALO_TRACE_F32, p.o.device, static_cast<std::size_t>(T) * Hv * d) != 0) return -1;
       {
         const halo_arg a[] = {Ptr(p.o.device), Ptr(p.zo.device), Ptr(L.norm_w.device), Ptr(p.oq.device),
                               Ptr(p.os.device), U32(Hv), U32(d), Val(eps)};
         if (Launch(eng, "halo_gated_rmsnorm_q8", D3(T), D3(256), a, err, errlen) != 0) return -1;
       }
+      if (save("oq", HALO_TRACE_I8, p.oq.device, static_cast<std::size_t>(T) * Hv * d) != 0 ||
+          save("os", HALO_TRACE_F32, p.os.device, static_cast<std::size_t>(T) * Hv * d / 32) != 0)
+        return -1;
       if (gemm(L.out, p.oq, p.os, p.delta) != 0) return -1;
     } else {
       if (gemm(L.qg, p.xq, p.xs, p.qgo) != 0 || gemm(L.k, p.xq, p.xs, p.ko) != 0 || gemm(L.v, p.xq, p.xs, p.vo) != 0)
+        return -1;
+      if (save("qg", HALO_TRACE_F32, p.qgo.device, static_cast<std::size_t>(T) * 2 * Hq * hd) != 0 ||
+          save("k", HALO_TRACE_F32, p.ko.device, static_cast<std::size_t>(T) * Hkv * hd) != 0 ||
+          save("v", HALO_TRACE_F32, p.vo.device, static_cast<std::size_t>(T) * Hkv * hd) != 0)
         return -1;
       {
         const halo_arg a[] = {Ptr(p.qgo.device), Ptr(p.ko.device), Ptr(p.vo.device), Ptr(L.q_norm.device),
@@ -502,17 +533,39 @@ int PrefillBatch(halo_model* m, const std::vector<halo_prefill_segment>& segs, c
                                P<int8_t>(p.oq), P<float>(p.os), Hq, p.attn_ws.device, p.attn_ws_bytes, err,
                                errlen) != 0)
         return -1;
-      (void)hd;
+      if (save("aq", HALO_TRACE_F32, p.q.device, static_cast<std::size_t>(T) * Hq * hd) != 0 ||
+          save("oq", HALO_TRACE_I8, p.oq.device, static_cast<std::size_t>(T) * Hq * hd) != 0 ||
+          save("os", HALO_TRACE_F32, p.os.device, static_cast<std::size_t>(T) * Hq * hd / 32) != 0)
+        return -1;
       if (gemm(L.o, p.oq, p.os, p.delta) != 0) return -1;
     }
+    if (save("delta", HALO_TRACE_F32, p.delta.device, static_cast<std::size_t>(T) * H) != 0) return -1;
     have_delta = true;
     if (norm(L.ffn_norm, true) != 0) return -1;
     if (halo_op_moe_prefill(eng, &L.moe, P<float>(p.xn), P<float>(p.delta), T, p.moe_ws.device, p.moe_ws_bytes, err,
                             errlen) != 0)
       return -1;
+    if (tr != nullptr) {  // the MoE's input residual, routing, h (sorted pairs), its codes and the output
+      MoePrefillViews v;
+      if (MoePrefillLayout(&L.moe, T, p.moe_ws.device, &v, err, errlen) != 0) return -1;
+      const std::size_t k = c.n_used, G = T * k + T, F = c.expert_ff;
+      if (save("mres", HALO_TRACE_F32, p.res.device, static_cast<std::size_t>(T) * H) != 0 ||
+          save("mxq", HALO_TRACE_I8, v.xq, static_cast<std::size_t>(T) * H) != 0 ||
+          save("mxs", HALO_TRACE_F32, v.xs, static_cast<std::size_t>(T) * H / 32) != 0 ||
+          save("mlogits", HALO_TRACE_F32, v.logits, static_cast<std::size_t>(T) * c.n_experts) != 0 ||
+          save("mshared", HALO_TRACE_F32, v.sgl, T) != 0 || save("mids", HALO_TRACE_U32, v.ids, T * k) != 0 ||
+          save("mweights", HALO_TRACE_F32, v.weights, T * k) != 0 || save("mpos", HALO_TRACE_U32, v.pos, T * k) != 0 ||
+          save("mh", HALO_TRACE_F32, v.h, G * F) != 0 || save("mhq", HALO_TRACE_I8, v.hq, G * F) != 0 ||
+          save("mhs", HALO_TRACE_F32, v.hs, G * F / 32) != 0 ||
+          save("mout", HALO_TRACE_F32, p.delta.device, static_cast<std::size_t>(T) * H) != 0)
+        return -1;
+    }
     have_delta = true;
+    ++li;
   }
   if (norm(m->out_norm, false) != 0) return -1;
+  li = UINT32_MAX;
+  if (save_norm("res_in", "xq", "xs") != 0) return -1;
   {
     const halo_arg a[] = {Ptr(p.xq.device), Ptr(p.xs.device), Ptr(p.segs.device), Ptr(p.lq.device), Ptr(p.ls.device),
                           U32(H)};
@@ -965,6 +1018,35 @@ int halo_model_prefill(halo_model* m, const halo_prefill_segment* segs, uint32_t
     rest.swap(next);
   }
   return 0;
+}
+
+int halo_model_prefill_trace(halo_model* m, const halo_prefill_segment* segs, uint32_t nseg, void* trace,
+                             size_t trace_bytes, halo_model_trace_entry* entries, uint32_t max_entries,
+                             uint32_t* n_entries, char* err, size_t errlen) {
+  if (m == nullptr || segs == nullptr || trace == nullptr || entries == nullptr || n_entries == nullptr ||
+      nseg == 0 || nseg > m->c.max_sessions)
+    return SetErr(err, errlen, "prefill trace: null argument or bad segment count"), -1;
+  std::uint32_t total = 0;
+  for (std::uint32_t i = 0; i < nseg; ++i) {
+    const halo_prefill_segment& g = segs[i];
+    if (g.session != segs[0].session + i || g.length == 0 || g.start + g.length >= m->c.max_context)
+      return SetErr(err, errlen, "prefill trace: segment %u invalid", i), -1;
+    total += g.length;
+  }
+  if (total > kPrefillCap) return SetErr(err, errlen, "prefill trace: %u tokens > one batch of %u", total, kPrefillCap), -1;
+  if (m->c.shared_ff != m->c.expert_ff) return SetErr(err, errlen, "prefill trace: shared ff != expert ff"), -1;
+  if (PrefillAlloc(m, err, errlen) != 0) return -1;
+  Tracer tr;
+  tr.eng = m->eng;
+  tr.base = static_cast<char*>(trace);
+  tr.cap = trace_bytes;
+  tr.entries = entries;
+  tr.max_entries = max_entries;
+  std::vector<halo_prefill_segment> batch(segs, segs + nseg);
+  for (auto& g : batch) g.first = 0;
+  const int rc = PrefillBatch(m, batch, err, errlen, &tr);
+  *n_entries = tr.n;
+  return rc;
 }
 
 int halo_model_history(halo_model* m, uint32_t s, uint32_t* out, uint32_t n, char* err, size_t errlen) {

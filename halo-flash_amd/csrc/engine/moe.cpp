@@ -142,16 +142,12 @@ int halo_op_moe_decode_norm(halo_engine* eng, const halo_moe_weights* w, const h
 }  // extern "C"
 
 namespace {
-struct PrefillViews {
-  float *logits, *sgl, *xs, *weights, *h, *hs, *y;
-  std::int8_t *xq, *hq;
-  std::uint32_t *ids, *count, *start, *tiles, *ntiles, *token, *pos;
-  std::uint32_t max_tiles;
-  std::size_t bytes;
-};
 constexpr std::uint32_t kPrefillTile = 64;
+}  // namespace
 
-int PrefillLayout(const halo_moe_weights* w, std::uint32_t T, void* ws, PrefillViews* v, char* err, std::size_t errlen) {
+namespace halo::engine {
+int MoePrefillLayout(const halo_moe_weights* w, std::uint32_t T, void* ws, MoePrefillViews* v, char* err,
+                     std::size_t errlen) {
   if (w == nullptr || w->router == nullptr || w->gate.qs == nullptr) return SetErr(err, errlen, "moe: missing tensors"), -1;
   const std::uint32_t E = w->n_experts, k = w->n_used, H = w->hidden, F = w->ff;
   const bool shared = w->shared_gate_proj.qs != nullptr;
@@ -193,6 +189,14 @@ int PrefillLayout(const halo_moe_weights* w, std::uint32_t T, void* ws, PrefillV
   v->y = reinterpret_cast<float*>(take(sizeof(float) * G * H));
   v->bytes = o;
   return 0;
+}
+}  // namespace halo::engine
+
+namespace {
+using PrefillViews = MoePrefillViews;
+int PrefillLayout(const halo_moe_weights* w, std::uint32_t T, void* ws, PrefillViews* v, char* err,
+                  std::size_t errlen) {
+  return MoePrefillLayout(w, T, ws, v, err, errlen);
 }
 }  // namespace
 

@@ -398,6 +398,8 @@ _SIGS = {
     "halo_model_logits": (C.c_int, [_VP, _U32, _VP], True),
     "halo_model_step_trace": (C.c_int, [_VP, _U32, _U32, _VP, _SZ, C.POINTER(TraceEntry), _U32,
                                         C.POINTER(_U32)], True),
+    "halo_model_prefill_trace": (C.c_int, [_VP, C.POINTER(PrefillSegment), _U32, _VP, _SZ, C.POINTER(TraceEntry),
+                                           _U32, C.POINTER(_U32)], True),
     "halo_model_prefill": (C.c_int, [_VP, C.POINTER(PrefillSegment), _U32], True),
     "halo_op_moe_workspace_bytes": (_SZ, [C.POINTER(MoeWeights), _U32], False),
     "halo_op_moe_views": (C.c_int, [C.POINTER(MoeWeights), _U32, _VP, C.POINTER(MoeViews)], True),
@@ -716,17 +718,20 @@ class Model:
 
     def step_trace(self, S: int, prefix: int = 0) -> dict:
         """One eager step with the teacher-forcing trace: {(layer, name): host array}; layer -1 is the head."""
+        return self._trace("halo_model_step_trace", (S, prefix), S)
+
+    def _trace(self, fn, args, T: int) -> dict:
         cfg = self.cfg
-        per_layer = S * (16 * cfg.hidden + 8 * (2 * cfg.gdn_k_heads + 3 * cfg.gdn_v_heads) * cfg.gdn_head_dim +
-                         8 * 2 * cfg.q_heads * cfg.head_dim + 4 * cfg.n_experts +
-                         4 * (cfg.n_used + 1) * max(cfg.expert_ff, cfg.shared_ff) + 64) + 32 * 256
+        per_layer = T * (16 * cfg.hidden + 12 * (2 * cfg.gdn_k_heads + 3 * cfg.gdn_v_heads) * cfg.gdn_head_dim +
+                         12 * 2 * cfg.q_heads * cfg.head_dim + 4 * cfg.n_experts +
+                         8 * (cfg.n_used + 1) * max(cfg.expert_ff, cfg.shared_ff) + 64 * cfg.n_used + 64) + 40 * 256
         nbytes = (cfg.layers + 1) * per_layer
         buf = self.dev.array(nbytes, np.uint8)
-        maxe = 32 * (cfg.layers + 1)
+        maxe = 40 * (cfg.layers + 1)
         ents = (TraceEntry * maxe)()
         n = C.c_uint32()
         try:
-            _call("halo_model_step_trace", self.h, S, prefix, buf.ptr, nbytes, ents, maxe, C.byref(n))
+            _call(fn, self.h, *args, buf.ptr, nbytes, ents, maxe, C.byref(n))
             self.dev.sync()
             blob = buf.download()
         finally:
@@ -734,9 +739,13 @@ class Model:
         out = {}
         for e in ents[: n.value]:
             layer = -1 if e.layer == 0xFFFFFFFF else int(e.layer)
-            arr = blob[e.offset: e.offset + e.bytes].view(TRACE_DTYPES[e.dtype]).copy()
-            out[(layer, e.name.decode())] = arr
+            out[(layer, e.name.decode())] = blob[e.offset: e.offset + e.bytes].view(TRACE_DTYPES[e.dtype]).copy()
         return out
+
+    def prefill_trace(self, segments) -> dict:
+        """halo_model_prefill of (session, start, length) segments (one batch) with the teacher-forcing trace."""
+        arr = (PrefillSegment * len(segments))(*[PrefillSegment(s, a, n, 0) for s, a, n in segments])
+        return self._trace("halo_model_prefill_trace", (arr, len(segments)), sum(n for _, _, n in segments))
 
     def set_sampling(self, s: int, params: "SampleParams", penalties=None):
         """Device sampling for session s; penalties = (token, generated_count, repeated) arrays sorted by token."""

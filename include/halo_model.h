@@ -124,6 +124,17 @@ int halo_model_step_trace(halo_model* m, uint32_t S, uint32_t attn_prefix, void*
                           halo_model_trace_entry* entries, uint32_t max_entries, uint32_t* n_entries, char* err,
                           size_t errlen);
 
+/* The same trace for one batched prefill call (halo_model_prefill) whose segments fit one batch (<= 2048 tokens;
+ * shared_ff == expert_ff): entries per layer for all T tokens of the batch, [T][...] in batch order: res_in, xq,
+ * xs; DeltaNet qkv, z, ab, gq / gk (the conv + L2 outputs [T][Hk d]), gv [T][Hv d], g / beta [T][Hv], o (the
+ * recurrence output [T][Hv d]); attention qg, k, v, aq (normalised, rotated queries [T][Hq hd]); oq, os, delta;
+ * MoE mres, mxq, mxs, mlogits, mshared, mids, mweights, mpos (uint32 [T][k]: each pair's row among the pairs
+ * sorted by expert; the shared expert's pair of token t is row T k + t), mh / mhq / mhs (h of the sorted pairs
+ * [T (k + 1)][ff] fp32, its codes and scales), mout; then the final norm's res_in, xq, xs. */
+int halo_model_prefill_trace(halo_model* m, const halo_prefill_segment* segs, uint32_t nseg, void* trace,
+                             size_t trace_bytes, halo_model_trace_entry* entries, uint32_t max_entries,
+                             uint32_t* n_entries, char* err, size_t errlen);
+
 /* Host copy of session s's logits of the last step ([vocab] fp32). Not capturable. */
 int halo_model_logits(halo_model* m, uint32_t s, float* out, char* err, size_t errlen);
 

@@ -60,6 +60,23 @@ def _l2norm(x, eps):
     return y
 
 
+def rope_mag(x, pos, rot, theta):
+    """Term magnitude of NEOX-rotated rows x [heads][hd] (before rotation) at `pos`, for a 1e-5 bar: |a| + |b| of
+    each rotated pair, widened by the angle's own fp32 rounding (the reference forms angle = float(pos) * freq in
+    fp32, src/model/cpu_ops.cpp:168-185, so one ulp of freq can move the angle by one ulp of the angle, ~angle
+    * 2^-23, whichever way a given powf rounds); dims past rot keep |x|."""
+    x = np.asarray(x, np.float64)
+    mag = np.abs(x).copy()
+    half = rot // 2
+    for i in range(half):
+        ang = pos * theta ** (-2.0 * i / rot)
+        widen = 1.0 + 2.0 * ang * 2.0 ** -23 / 1e-5
+        ab = (np.abs(x[:, i]) + np.abs(x[:, i + half])) * widen
+        mag[:, i] = ab
+        mag[:, i + half] = ab
+    return mag
+
+
 class Report:
     """Counts of checks and quantizer flips, and the worst error of each stage relative to its bar."""
 
@@ -130,6 +147,13 @@ class LayerChecker:
         if key not in self.dense:
             self.dense[key] = self.m.tensor(l, name)
         return self.dense[key]
+
+    def _expert(self, l, name, e, rows):
+        """Rows [e rows, (e + 1) rows) of a stacked expert tensor (small tensors are downloaded whole once)."""
+        if self.c.n_experts * rows * self.c.hidden <= (64 << 20):
+            qs, d = self._w(l, name)
+            return qs[e * rows:(e + 1) * rows], d[e * rows:(e + 1) * rows]
+        return self.m.tensor_rows(l, name, e * rows, rows)
 
     def snapshot(self, S):
         """The GPU's recurrent state before a step: per layer DeltaNet state / conv ring, or the KV pools."""
@@ -243,11 +267,12 @@ class LayerChecker:
             gate = g3[:, 1]
             k = np.ascontiguousarray(np.stack([_rmsnorm(kk[s].reshape(Hkv, hd)[h], kn, c.rms_eps)
                                                for h in range(Hkv)]))
+            kmag = rope_mag(k, p, c.rotary_dim, c.rope_theta)
             O.oracle().or_rope_neox(q.reshape(-1), Hq, hd, c.rotary_dim, p, c.rope_theta)
             O.oracle().or_rope_neox(k.reshape(-1), Hkv, hd, c.rotary_dim, p, c.rope_theta)
-            # this step's K / V rows as the GPU appended them (the rotation is closed-form: 1e-6 of the row)
+            # this step's K / V rows as the GPU appended them
             pg = int(pages[s, p // 16])
-            r.close(f"k append@L{l}s{s}", kp[pg, :, p % 16], k, np.abs(k) + np.max(np.abs(k)) * 1e-1, rel=1e-5)
+            r.close(f"k append@L{l}s{s}", kp[pg, :, p % 16], k, kmag)
             assert np.array_equal(vp[pg, :, p % 16], vv[s].reshape(Hkv, hd)), f"v append L{l}"
             n = p + 1
             rows = np.array([int(pages[s, t // 16]) for t in range(n)])
@@ -271,7 +296,7 @@ class LayerChecker:
             gemv(r, f"o@L{l}s{s}", self._w(l, "o"), oq[s], os_[s], tr[(l, "delta")].reshape(S, -1)[s])
 
     def _moe(self, l, tr, S):
-        c, r, m = self.c, self.report, self.m
+        c, r = self.c, self.report
         E, k, F, SF, H = c.n_experts, c.n_used, c.expert_ff, c.shared_ff, c.hidden
         res_in = tr[(l, "res_in")].reshape(S, H)
         delta = tr[(l, "delta")].reshape(S, H)
@@ -304,9 +329,8 @@ class LayerChecker:
             for slot in range(k + 1):
                 if slot < k:
                     e = int(ids[s, slot])
-                    gw = m.tensor_rows(l, "gate", e * F, F)
-                    uw = m.tensor_rows(l, "up", e * F, F)
-                    dw = m.tensor_rows(l, "down", e * H, H)
+                    gw, uw = self._expert(l, "gate", e, F), self._expert(l, "up", e, F)
+                    dw = self._expert(l, "down", e, H)
                     f, wgt, row = F, float(wts[s, slot]), s * k + slot
                 else:
                     gw, uw, dw = self._w(l, "sgate"), self._w(l, "sup"), self._w(l, "sdown")
@@ -364,3 +388,230 @@ class LayerChecker:
             self._moe(l, tr, S)
         self._head(tr, S, logits)
         return logits
+
+
+class PrefillChecker(LayerChecker):
+    """Every layer of one traced batched prefill (halo_model_prefill_trace) against the host restatement, token by
+    token, from the GPU's own inputs of each stage. The DeltaNet recurrence is re-run on the host over the batch from
+    the GPU's state before it and the GPU's per-token q / k / v / decay / beta (the chunked WY form on the GPU sums in
+    another order, so its outputs are held to 1e-5 of the terms' magnitudes carried through the recurrence)."""
+
+    def check_prefill(self, segments, prompts):
+        """segments: (session, start, length) in batch order; prompts[s]: session s's prompt (host tokens)."""
+        c = self.c
+        S = max(s for s, _, _ in segments) + 1
+        snap = self.snapshot(S)
+        tr = self.m.prefill_trace(segments)
+        after = self.snapshot(S)
+        rows = []  # (session, position) of every batch row
+        for s, a, n in segments:
+            rows += [(s, a + j) for j in range(n)]
+        T = len(rows)
+        emb_q, emb_d = self._w(-1, "embd")
+        want = np.stack([_f16(emb_d[int(prompts[s][p])]).repeat(32) * emb_q[int(prompts[s][p])].astype(np.float32)
+                         for s, p in rows])
+        assert np.array_equal(tr[(0, "res_in")].reshape(T, -1), want.astype(np.float32)), "embedding"
+        for l in range(c.layers):
+            if l > 0:
+                prev = tr[(l - 1, "mres")].reshape(T, -1) + tr[(l - 1, "mout")].reshape(T, -1)
+                assert np.array_equal(tr[(l, "res_in")].reshape(T, -1), prev.astype(np.float32)), f"residual L{l}"
+            if self.attn[l]:
+                self._attention_prefill(l, tr, T, rows, snap, after)
+            else:
+                self._deltanet_prefill(l, tr, T, segments, snap, after)
+            self._moe_prefill(l, tr, T)
+        # final norm and the LM head on each segment's last token
+        H = c.hidden
+        res = tr[(-1, "res_in")].reshape(T, H)
+        lres = tr[(c.layers - 1, "mres")].reshape(T, H) + tr[(c.layers - 1, "mout")].reshape(T, H)
+        assert np.array_equal(res, lres.astype(np.float32)), "final residual add"
+        xq, xs = tr[(-1, "xq")].reshape(T, H), tr[(-1, "xs")].reshape(T, H // 32)
+        head = self._w(-1, "head")
+        on = self.m.tensor(-1, "out_norm")[0]
+        f = 0
+        for s, _, n in segments:
+            t = f + n - 1
+            f += n
+            self.report.codes_match(f"head codes s{s}", xq[t], xs[t], _rmsnorm(res[t], on, c.rms_eps))
+            y, mag = O.gemv_q8a8(head[0], head[1], xq[t], xs[t])
+            got = self.m.logits(s)
+            self.report.close(f"lm head s{s}", got, y, mag)
+            top = np.argsort(y)[::-1]
+            if int(np.argmax(got)) != int(top[0]):
+                assert y[top[0]] - y[top[1]] <= 2e-5 * mag[top[0]], "argmax differs away from a tie"
+
+    def _deltanet_prefill(self, l, tr, T, segments, snap, after):
+        c, r = self.c, self.report
+        Hk, Hv, d, K = c.gdn_k_heads, c.gdn_v_heads, c.gdn_head_dim, c.conv_kernel
+        Dk, Dv = Hk * d, Hv * d
+        C = 2 * Dk + Dv
+        _, xq, xs = self._input(l, tr, T, self._w(l, "attn_norm")[0])
+        qkv, z, ab = tr[(l, "qkv")].reshape(T, C), tr[(l, "z")].reshape(T, Dv), tr[(l, "ab")].reshape(T, 2 * Hv)
+        for t in range(T):
+            gemv(r, f"qkv@L{l}t{t}", self._w(l, "qkv"), xq[t], xs[t], qkv[t])
+            gemv(r, f"z@L{l}t{t}", self._w(l, "z"), xq[t], xs[t], z[t])
+            gemv(r, f"ab@L{l}t{t}", self._w(l, "ab"), xq[t], xs[t], ab[t])
+        gq, gk = tr[(l, "gq")].reshape(T, Dk), tr[(l, "gk")].reshape(T, Dk)
+        gv = tr[(l, "gv")].reshape(T, Dv)
+        gg, gb = tr[(l, "g")].reshape(T, Hv), tr[(l, "beta")].reshape(T, Hv)
+        go = tr[(l, "o")].reshape(T, Dv)
+        oq, os_ = tr[(l, "oq")].reshape(T, Dv), tr[(l, "os")].reshape(T, Dv // 32)
+        cw = self._w(l, "conv_w")
+        a, dt, nw = self._w(l, "a")[0], self._w(l, "dt")[0], self._w(l, "norm_w")[0]
+        ring0 = snap[(l, "conv_ring")].reshape(c.max_sessions, K, C)
+        ring1 = after[(l, "conv_ring")].reshape(c.max_sessions, K, C)
+        st0 = snap[(l, "state")].reshape(c.max_sessions, Hv, d, d)
+        st1 = after[(l, "state")].reshape(c.max_sessions, Hv, d, d)
+        f = 0
+        for s, start, n in segments:
+            Sv = [np.ascontiguousarray(st0[s, h].T) for h in range(Hv)]  # value-major
+            Sm = [np.abs(x).astype(np.float64) for x in Sv]  # term magnitudes carried by the recurrence
+            for j in range(n):
+                t, p = f + j, start + j
+                win = []
+                for jj in range(K):
+                    pp = p - (K - 1) + jj
+                    if pp >= start:
+                        win.append(qkv[f + pp - start])
+                    elif pp >= 0:
+                        win.append(ring0[s, pp % K])
+                    else:
+                        win.append(np.zeros(C, np.float32))
+                conv = sum(cw[:, jj].astype(np.float64) * win[jj].astype(np.float64) for jj in range(K))
+                y = _silu(conv.astype(np.float32))
+                ymag = 1.1 * sum(np.abs(cw[:, jj].astype(np.float64) * win[jj]) for jj in range(K)) + np.abs(y)
+                for h in range(Hk):
+                    for nm, base, got in (("q", 0, gq), ("k", Dk, gk)):
+                        seg = y[base + h * d:base + (h + 1) * d]
+                        nrm = np.sqrt(np.sum(seg.astype(np.float64) ** 2) + c.rms_eps)
+                        r.close(f"conv {nm}@L{l}t{t}", got[t, h * d:(h + 1) * d], _l2norm(seg, c.rms_eps),
+                                ymag[base + h * d:base + (h + 1) * d] / nrm)
+                r.close(f"conv v@L{l}t{t}", gv[t], y[2 * Dk:], ymag[2 * Dk:])
+                g = (a * _softplus(ab[t, :Hv] + dt)).astype(np.float32)
+                r.close(f"decay@L{l}t{t}", gg[t], g, np.abs(g) + 1e-6)
+                r.close(f"beta@L{l}t{t}", gb[t], _sigmoid(ab[t, Hv:]), np.abs(_sigmoid(ab[t, Hv:])))
+                # the recurrence from the GPU's inputs (teacher-forced per token)
+                kmag = np.concatenate([ymag[Dk + h * d:Dk + (h + 1) * d] /
+                                       np.sqrt(np.sum(y[Dk + h * d:Dk + (h + 1) * d].astype(np.float64) ** 2) +
+                                               c.rms_eps) for h in range(Hk)])
+                for h in range(Hv):
+                    kh = h % Hk
+                    qh, kv_, vh = gq[t, kh * d:(kh + 1) * d], gk[t, kh * d:(kh + 1) * d], gv[t, h * d:(h + 1) * d]
+                    oh = np.zeros(d, np.float32)
+                    km = np.maximum(kmag[kh * d:(kh + 1) * d], np.abs(kv_))
+                    # this token's terms: |v| and |decay S k| (the actual state, so errors carried in from earlier
+                    # tokens enter through the contraction decay (I - beta k k^T) rather than a worst-case feedback)
+                    decay = np.exp(np.float64(gg[t, h]))
+                    dmag = ymag[2 * Dk + h * d:2 * Dk + (h + 1) * d] + decay * (np.abs(Sv[h]).astype(np.float64) @ km)
+                    Sm[h] = decay * Sm[h] + np.outer(dmag, km)
+                    O.oracle().or_gdn_step(Sv[h], d, np.ascontiguousarray(qh), np.ascontiguousarray(kv_),
+                                           np.ascontiguousarray(vh), float(gg[t, h]), float(gb[t, h]), oh)
+                    r.close(f"recurrence o@L{l}t{t}", go[t, h * d:(h + 1) * d], oh,
+                            (Sm[h] @ np.abs(qh)) / np.sqrt(d))
+                # gated output norm from the GPU's o
+                on = np.concatenate([_rmsnorm(go[t, h * d:(h + 1) * d], nw, c.rms_eps) *
+                                     _sigmoid(z[t, h * d:(h + 1) * d]) for h in range(Hv)])
+                r.codes_match(f"gated norm codes@L{l}t{t}", oq[t], os_[t], on)
+                gemv(r, f"out@L{l}t{t}", self._w(l, "out"), oq[t], os_[t], tr[(l, "delta")].reshape(T, -1)[t])
+            for h in range(Hv):
+                r.close(f"state@L{l}s{s}h{h}", st1[s, h].T, Sv[h], Sm[h])
+            for jj in range(min(K, n)):  # the ring holds the segment's last projections
+                p = start + n - 1 - jj
+                assert np.array_equal(ring1[s, p % K], qkv[f + n - 1 - jj]), f"conv ring L{l}"
+            f += n
+
+    def _attention_prefill(self, l, tr, T, rows, snap, after):
+        c, r = self.c, self.report
+        Hq, Hkv, hd = c.q_heads, c.kv_heads, c.head_dim
+        G = Hq // Hkv
+        _, xq, xs = self._input(l, tr, T, self._w(l, "attn_norm")[0])
+        qg, kk, vv = (tr[(l, "qg")].reshape(T, Hq * 2 * hd), tr[(l, "k")].reshape(T, Hkv * hd),
+                      tr[(l, "v")].reshape(T, Hkv * hd))
+        aq = tr[(l, "aq")].reshape(T, Hq, hd)
+        oq, os_ = tr[(l, "oq")].reshape(T, Hq * hd), tr[(l, "os")].reshape(T, Hq * hd // 32)
+        kp = after[(l, "k_pool")].reshape(-1, Hkv, 16, hd)
+        vp = after[(l, "v_pool")].reshape(-1, Hkv, 16, hd)
+        pages = snap["pages"]
+        qn, kn = self._w(l, "q_norm")[0], self._w(l, "k_norm")[0]
+        for t, (s, p) in enumerate(rows):
+            gemv(r, f"qg@L{l}t{t}", self._w(l, "qg"), xq[t], xs[t], qg[t])
+            gemv(r, f"k@L{l}t{t}", self._w(l, "k"), xq[t], xs[t], kk[t])
+            gemv(r, f"v@L{l}t{t}", self._w(l, "v"), xq[t], xs[t], vv[t])
+            g3 = qg[t].reshape(Hq, 2, hd)
+            q = np.ascontiguousarray(np.stack([_rmsnorm(g3[h, 0], qn, c.rms_eps) for h in range(Hq)]))
+            k = np.ascontiguousarray(np.stack([_rmsnorm(kk[t].reshape(Hkv, hd)[h], kn, c.rms_eps)
+                                               for h in range(Hkv)]))
+            qmag, kmag = rope_mag(q, p, c.rotary_dim, c.rope_theta), rope_mag(k, p, c.rotary_dim, c.rope_theta)
+            O.oracle().or_rope_neox(q.reshape(-1), Hq, hd, c.rotary_dim, p, c.rope_theta)
+            O.oracle().or_rope_neox(k.reshape(-1), Hkv, hd, c.rotary_dim, p, c.rope_theta)
+            r.close(f"q rope@L{l}t{t}", aq[t], q, qmag)
+            pg = int(pages[s, p // 16])
+            r.close(f"k append@L{l}t{t}", kp[pg, :, p % 16], k, kmag)
+            assert np.array_equal(vp[pg, :, p % 16], vv[t].reshape(Hkv, hd)), f"v append L{l}"
+            n = p + 1
+            prow = np.array([int(pages[s, u // 16]) for u in range(n)])
+            Kc, Vc = kp[prow, :, np.arange(n) % 16], vp[prow, :, np.arange(n) % 16]
+            gate = g3[:, 1]
+            o = np.zeros((Hq, hd), np.float32)
+            omag = np.zeros((Hq, hd), np.float64)
+            for h in range(Hq):
+                kvh = h // G
+                oh = np.zeros(hd, np.float32)
+                qh = np.ascontiguousarray(aq[t, h])  # the GPU's rotated query (teacher-forced)
+                O.oracle().or_attention_head(qh, np.ascontiguousarray(Kc[:, kvh]), np.ascontiguousarray(Vc[:, kvh]),
+                                             n, hd, hd, oh)
+                gh = _sigmoid(gate[h])
+                o[h] = oh * gh
+                sc = Kc[:, kvh].astype(np.float64) @ qh.astype(np.float64) / np.sqrt(hd)
+                pw = np.exp(sc - sc.max())
+                pw /= pw.sum()
+                omag[h] = (pw @ np.abs(Vc[:, kvh]).astype(np.float64)) * gh
+            r.codes_match(f"attention out codes@L{l}t{t}", oq[t], os_[t], o.reshape(-1),
+                          np.maximum(omag.reshape(-1), np.abs(o.reshape(-1))))
+            gemv(r, f"o@L{l}t{t}", self._w(l, "o"), oq[t], os_[t], tr[(l, "delta")].reshape(T, -1)[t])
+
+    def _moe_prefill(self, l, tr, T):
+        c, r = self.c, self.report
+        E, k, F, H = c.n_experts, c.n_used, c.expert_ff, c.hidden
+        res_in, delta, mres = (tr[(l, "res_in")].reshape(T, H), tr[(l, "delta")].reshape(T, H),
+                               tr[(l, "mres")].reshape(T, H))
+        assert np.array_equal(mres, (res_in + delta).astype(np.float32)), f"residual add L{l}"
+        fnw = self._w(l, "ffn_norm")[0]
+        xq, xs = tr[(l, "mxq")].reshape(T, H), tr[(l, "mxs")].reshape(T, H // 32)
+        logits, shl = tr[(l, "mlogits")].reshape(T, E), tr[(l, "mshared")].reshape(T)
+        ids, wts, pos = tr[(l, "mids")].reshape(T, k), tr[(l, "mweights")].reshape(T, k), tr[(l, "mpos")].reshape(T, k)
+        hh, hq, hs = (tr[(l, "mh")].reshape(-1, F), tr[(l, "mhq")].reshape(-1, F), tr[(l, "mhs")].reshape(-1, F // 32))
+        out = tr[(l, "mout")].reshape(T, H)
+        assert sorted(pos.reshape(-1).tolist()) == list(range(T * k)), "pair positions"
+        # h codes: the quantizer on the GPU's own h rows, bit for bit
+        wq, wsc = O.quantize(np.ascontiguousarray(hh))
+        assert np.array_equal(hq, wq) and hs.tobytes() == wsc.tobytes(), f"h codes L{l}"
+        R, sg = self._w(l, "router"), self._w(l, "shared_gate")[0]
+        for t in range(T):
+            xn = _rmsnorm(mres[t], fnw, c.rms_eps)
+            r.codes_match(f"moe input codes@L{l}t{t}", xq[t], xs[t], xn)
+            x64 = xn.astype(np.float64)
+            r.close(f"router@L{l}t{t}", logits[t], R.astype(np.float64) @ x64, np.abs(R) @ np.abs(x64))
+            r.close(f"shared gate@L{l}t{t}", [shl[t]], [sg.astype(np.float64) @ x64], [np.abs(sg) @ np.abs(x64)])
+            oi, ow = np.zeros(k, np.uint32), np.zeros(k, np.float32)
+            O.oracle().or_route_topk(np.ascontiguousarray(logits[t]), E, k, oi, ow)
+            assert ids[t].tolist() == oi.tolist(), f"routing of L{l} token {t}"
+            r.close(f"route weights@L{l}t{t}", wts[t], ow, np.abs(ow), rel=1e-6)
+            acc, mag = np.zeros(H, np.float64), np.zeros(H, np.float64)
+            for slot in range(k + 1):
+                if slot < k:
+                    e = int(ids[t, slot])
+                    gw, uw = self._expert(l, "gate", e, F), self._expert(l, "up", e, F)
+                    dw = self._expert(l, "down", e, H)
+                    wgt, row = float(wts[t, slot]), int(pos[t, slot])
+                else:
+                    gw, uw, dw = self._w(l, "sgate"), self._w(l, "sup"), self._w(l, "sdown")
+                    wgt, row = float(_sigmoid(shl[t])), T * k + t
+                gy, gm = O.gemv_q8a8(gw[0], gw[1], xq[t], xs[t])
+                uy, um = O.gemv_q8a8(uw[0], uw[1], xq[t], xs[t])
+                r.close(f"moe h@L{l}t{t}", hh[row], (_silu(gy) * uy).astype(np.float32),
+                        np.abs(_silu(gy)) * um + np.abs(uy) * gm * 1.1 + 1e-30)
+                dy, dm = O.gemv_q8a8(dw[0], dw[1], hq[row], hs[row])
+                acc += np.float64(np.float32(wgt)) * dy
+                mag += abs(wgt) * dm
+            r.close(f"moe out@L{l}t{t}", out[t], acc, mag)

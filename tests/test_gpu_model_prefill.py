@@ -1,22 +1,21 @@
-"""GPU checks of batched prefill (halo_model_prefill) on reduced twins of config C4.
+"""GPU checks of batched prefill (halo_model_prefill) on reduced twins of config C4, teacher-forced per layer.
 
 A ragged batch of prompts is prefilled in one call (projections as int8 GEMMs, DeltaNet through the chunked
-recurrence, causal attention over the paged cache, grouped MoE) and compared with
-  - the host restatement in tests/model_ref.py fed the same tokens one at a time (ReferenceModel's path), and
-  - the engine's own token-serial decode steps over the same prompt.
-Bars: logits within 3e-2 of max|logits| (the Q8 activation quantizer flip bound of the whole-step parity test; the
-prefill path sums the DeltaNet recurrence in chunks rather than token by token), and the produced
-token equal unless the reference's top two logits are closer than that.
+recurrence, causal attention over the paged cache, grouped MoE). halo_model_prefill_trace records every layer's
+inputs and outputs for all tokens of the batch, and tests/teacher.py (PrefillChecker) recomputes every stage from the
+GPU's own inputs of that stage, token by token: fp32 outputs within 1e-5 of their terms' magnitude (the chunked
+DeltaNet recurrence is re-run token-serially on the host from the GPU's state before the batch, the magnitudes carried
+through it), integer work exact, quantizer rounding-boundary flips counted. Calls that continue earlier ones (split
+prompts, batches of 2,048, suffixes after a shared prefix) are each checked from the state the previous call left,
+and the decode steps after a prefill are checked the same way (LayerChecker).
 """
 import numpy as np
 import pytest
 
 import halo_amd as H
-from model_ref import RefModel
+from teacher import LayerChecker, PrefillChecker
 
 pytestmark = pytest.mark.gpu
-
-BAR = 3e-2
 
 
 def twin(max_sessions=2, prefix=0, ctx=64):
@@ -27,125 +26,102 @@ def twin(max_sessions=2, prefix=0, ctx=64):
                          max_sessions=max_sessions, max_context=ctx, prefix_tokens=prefix)
 
 
-def rel(got, want):
-    return float(np.max(np.abs(got - want))) / float(np.max(np.abs(want)))
+def _flips_ok(rep):
+    print(f"{rep.flips} flips in {rep.codes} codes; worst error / bar per stage {rep.worst}")
+    assert rep.flips <= max(4, rep.codes // 10000)
 
 
-def check_token(got, want, what):
-    top = np.argsort(want)[::-1]
-    if int(np.argmax(got)) != int(top[0]):
-        assert want[top[0]] - want[top[1]] <= BAR * np.max(np.abs(want)), f"{what}: argmax differs away from a tie"
-
-
-def test_ragged_prefill_then_decode_matches_host_reference(dev):
+def test_ragged_prefill_then_decode(dev):
     cfg = twin()
     model = H.Model(dev, cfg, seed=11)
     try:
         rng = np.random.default_rng(4)
         prompts = [rng.integers(0, cfg.vocab, 12).astype(np.uint32), rng.integers(0, cfg.vocab, 9).astype(np.uint32)]
-        refs = [RefModel(model, cfg), RefModel(model, cfg)]
-        want = []
-        for ref, p in zip(refs, prompts):
-            for t in p[:-1]:
-                w = ref.step(int(t))
-            want.append(w)
         model.reset()
         for s, p in enumerate(prompts):
             model.set_session(s, p)
+        pc = PrefillChecker(model, cfg)
         # every prompt token but the last: the last one is the first decode step's input
-        model.prefill([(0, 0, 11), (1, 0, 8)])
-        for s in range(2):
-            got = model.logits(s)
-            err = rel(got, want[s])
-            print(f"session {s}: prefill logits error {err:.2e}")
-            assert err <= BAR
-            check_token(got, want[s], f"session {s} prefill")
+        pc.check_prefill([(0, 0, 11), (1, 0, 8)], prompts)
         assert model.positions(2).tolist() == [12, 9]
+        for s in range(2):
+            assert int(model.history(s, len(prompts[s]))[len(prompts[s]) - 1]) == int(np.argmax(model.logits(s)))
         # decode on from there, both sessions in one batch: the last prompt token, then greedy
+        lc = LayerChecker(model, cfg)
+        lc.report = pc.report
         tokens = [int(prompts[0][-1]), int(prompts[1][-1])]
         for i in range(6):
-            model.step_eager(2)
+            logits = lc.check_step(2, tokens)
             for s in range(2):
-                got = model.logits(s)
-                w = refs[s].step(tokens[s])
-                err = rel(got, w)
-                assert err <= BAR, f"session {s} decode step {i}: {err:.2e}"
-                check_token(got, w, f"session {s} decode step {i}")
                 n = len(prompts[s]) + i
                 tokens[s] = int(model.history(s, n + 1)[n])
-                assert tokens[s] == int(np.argmax(got))
+                assert tokens[s] == int(np.argmax(logits[s]))
+        _flips_ok(pc.report)
     finally:
         model.close()
 
 
-def test_split_prefill_equals_whole_and_token_serial(dev):
-    """Prefill in two calls (a chunk boundary inside the DeltaNet scan and the conv taps reaching back into the
-    ring) against one call and against decode steps; the conv ring and state carry over between calls."""
+def test_split_prefill_calls(dev):
+    """Prefill in three calls (a chunk boundary inside the DeltaNet scan, a one-token call, the conv taps reaching
+    back into the ring); each call is checked from the state the previous one left. The whole prompt in one call
+    gives the same bits as itself run twice (deterministic kernels)."""
     cfg = twin(max_sessions=1, ctx=256)
     model = H.Model(dev, cfg, seed=3)
     try:
         rng = np.random.default_rng(5)
         prompt = rng.integers(0, cfg.vocab, 200).astype(np.uint32)
         n = 150
+        pc = PrefillChecker(model, cfg)
         model.reset()
         model.set_session(0, prompt)
-        for _ in range(n):
-            model.step_eager(1)
-        serial = model.logits(0)
-        model.reset()
-        model.set_session(0, prompt)
-        model.prefill([(0, 0, n)])
-        whole = model.logits(0)
-        model.reset()
-        model.set_session(0, prompt)
-        model.prefill([(0, 0, 66)])
-        model.prefill([(0, 66, 1)])
-        model.prefill([(0, 67, n - 67)])
-        split = model.logits(0)
-        e1, e2 = rel(whole, serial), rel(split, whole)
-        print(f"whole vs serial {e1:.2e}, split vs whole {e2:.2e}")
-        assert e1 <= BAR and e2 <= BAR
-        check_token(whole, serial, "whole")
-        # the next decode step continues from the prefilled state
-        model.step_eager(1)
-        after = model.logits(0)
-        model.reset()
-        model.set_session(0, prompt)
-        for _ in range(n + 1):
-            model.step_eager(1)
-        assert rel(after, model.logits(0)) <= BAR
+        for seg in ((0, 0, 66), (0, 66, 1), (0, 67, n - 67)):
+            pc.check_prefill([seg], [prompt])
+        assert model.positions(1).tolist() == [n + 1]
+        lc = LayerChecker(model, cfg)
+        lc.report = pc.report
+        lc.check_step(1, [int(prompt[n])])
+        whole = []
+        for _ in range(2):
+            model.reset()
+            model.set_session(0, prompt)
+            model.prefill([(0, 0, n)])
+            whole.append(model.logits(0))
+        assert whole[0].tobytes() == whole[1].tobytes()
+        _flips_ok(pc.report)
     finally:
         model.close()
 
 
+@pytest.mark.timeout(600)
 def test_prefill_longer_than_one_batch(dev):
-    """2,500 tokens: the call splits into batches of 2,048; the second continues state, ring and cache."""
-    cfg = twin(max_sessions=1, ctx=2560)
+    """2,100 tokens: halo_model_prefill splits the call into batches of 2,048 and 52; the same two batches, traced,
+    are checked layer by layer (the second from the state, ring and cache the first left), and the one-call prefill
+    gives the same logits bit for bit."""
+    cfg = twin(max_sessions=1, ctx=2176)
     model = H.Model(dev, cfg, seed=8)
     try:
         rng = np.random.default_rng(6)
-        prompt = rng.integers(0, cfg.vocab, 2510).astype(np.uint32)
-        n = 2500
+        prompt = rng.integers(0, cfg.vocab, 2110).astype(np.uint32)
+        n = 2100
+        pc = PrefillChecker(model, cfg)
         model.reset()
         model.set_session(0, prompt)
-        model.run(1, n)
-        serial = model.logits(0)
+        pc.check_prefill([(0, 0, 2048)], [prompt])
+        pc.check_prefill([(0, 2048, n - 2048)], [prompt])
+        traced = model.logits(0)
         model.reset()
         model.set_session(0, prompt)
         model.prefill([(0, 0, n)])
-        got = model.logits(0)
-        err = rel(got, serial)
-        print(f"2500-token prefill vs serial decode {err:.2e}")
-        assert err <= BAR
-        check_token(got, serial, "long prefill")
+        assert model.logits(0).tobytes() == traced.tobytes()
         assert model.positions(1).tolist() == [n + 1]
+        _flips_ok(pc.report)
     finally:
         model.close()
 
 
 def test_prefill_suffixes_after_shared_prefix(dev):
     """Session 0 prefills a 64-token prefix, session 1 forks it, then both suffixes prefill in one ragged batch
-    reading the shared prefix pages; against the same procedure done with decode steps."""
+    reading the shared prefix pages; both calls checked layer by layer."""
     cfg = twin(max_sessions=2, prefix=64, ctx=256)
     model = H.Model(dev, cfg, seed=5)
     try:
@@ -153,27 +129,14 @@ def test_prefill_suffixes_after_shared_prefix(dev):
         prefix = rng.integers(0, cfg.vocab, 64).astype(np.uint32)
         a = np.concatenate([prefix, rng.integers(0, cfg.vocab, 40).astype(np.uint32)])
         b = np.concatenate([prefix, rng.integers(0, cfg.vocab, 17).astype(np.uint32)])
+        pc = PrefillChecker(model, cfg)
         model.reset()
         model.set_session(0, a)
-        model.run(1, 64)
+        pc.check_prefill([(0, 0, 64)], [a])
         model.fork(0, 1)
         model.set_session(1, b, nkv=64)
-        for _ in range(16):
-            model.run(2, 1, prefix=64)
-        model.run(1, 40 - 17)
-        want = [model.logits(0), model.logits(1)]
-        model.reset()
-        model.set_session(0, a)
-        model.prefill([(0, 0, 64)])
-        model.fork(0, 1)
-        model.set_session(1, b, nkv=64)
-        model.prefill([(0, 64, 39), (1, 64, 16)])
-        for s in range(2):
-            got = model.logits(s)
-            err = rel(got, want[s])
-            print(f"session {s}: suffix prefill vs decode {err:.2e}")
-            assert err <= BAR
-            check_token(got, want[s], f"session {s}")
+        pc.check_prefill([(0, 64, 39), (1, 64, 16)], [a, b])
         assert model.positions(2).tolist() == [104, 81]
+        _flips_ok(pc.report)
     finally:
         model.close()

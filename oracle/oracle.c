@@ -302,57 +302,6 @@ void or_route_topk(const float* logits, uint32_t n, uint32_t k, uint32_t* ids, f
   free(taken);
 }
 
-/* reference: src/model/reference.cpp:530-578 (ReferenceModel::Moe): route, per slot SiLU(gate) * up, down, weighted
- * sum in slot order, then the shared expert scaled by sigmoid(shared gate logit). Expert projections take the input
- * quantized per 32 values (the int8-activation decode path, src/kernels/batch_decode.hip:226-270). */
-void or_moe_token(const float* x, uint32_t hidden, uint32_t ff, uint32_t n_experts, uint32_t k,
-                  const float* router, const int8_t* gu_q, const uint16_t* gu_d, const int8_t* dn_q,
-                  const uint16_t* dn_d, const int8_t* sgu_q, const uint16_t* sgu_d, const int8_t* sdn_q,
-                  const uint16_t* sdn_d, uint32_t sff, const float* sgate, float* out, uint32_t* ids, float* weights) {
-  float* logits = (float*)malloc(sizeof(float) * n_experts);
-  or_matvec_f32(router, n_experts, hidden, x, logits);
-  or_route_topk(logits, n_experts, k, ids, weights);
-  const uint32_t maxff = ff > sff ? ff : sff;
-  int8_t* xq = (int8_t*)malloc(hidden);
-  float* xs = (float*)malloc(sizeof(float) * (hidden / 32));
-  float* gu = (float*)malloc(sizeof(float) * 2 * maxff);
-  float* h = (float*)malloc(sizeof(float) * maxff);
-  int8_t* hq = (int8_t*)malloc(maxff);
-  float* hs = (float*)malloc(sizeof(float) * (maxff / 32));
-  float* down = (float*)malloc(sizeof(float) * hidden);
-  or_quantize_q8_act(x, xq, xs, hidden);
-  for (uint32_t i = 0; i < hidden; ++i) out[i] = 0.0f;
-  for (uint32_t s = 0; s <= k; ++s) {
-    const int shared = s == k;
-    const uint32_t f = shared ? sff : ff;
-    const int8_t* gq = shared ? sgu_q : gu_q + (size_t)ids[s] * 2 * ff * hidden;
-    const uint16_t* gd = shared ? sgu_d : gu_d + (size_t)ids[s] * 2 * ff * (hidden / 32);
-    const int8_t* dq = shared ? sdn_q : dn_q + (size_t)ids[s] * hidden * ff;
-    const uint16_t* dd = shared ? sdn_d : dn_d + (size_t)ids[s] * hidden * (ff / 32);
-    or_gemv_q8a8(gq, gd, 2 * f, hidden, hidden, xq, xs, gu);
-    for (uint32_t j = 0; j < f; ++j) h[j] = or_silu(gu[j]) * gu[f + j];
-    or_quantize_q8_act(h, hq, hs, f);
-    or_gemv_q8a8(dq, dd, hidden, f, f, hq, hs, down);
-    float wgt;
-    if (shared) {
-      double g = 0.0;
-      for (uint32_t i = 0; i < hidden; ++i) g += (double)sgate[i] * (double)x[i];
-      wgt = or_sigmoid((float)g);
-    } else {
-      wgt = weights[s];
-    }
-    for (uint32_t i = 0; i < hidden; ++i) out[i] += wgt * down[i];
-  }
-  free(logits);
-  free(xq);
-  free(xs);
-  free(gu);
-  free(h);
-  free(hq);
-  free(hs);
-  free(down);
-}
-
 /* reference: src/model/reference.cpp:329-364 (ReferenceModel::LinearAttention, one value head):
  *   S <- decay * S; u = S k; delta = (v - u) * beta; S <- S + delta k^T; o = (S q) / sqrt(d)
  * with S[j][i] (j value, i key), dot products in double. The layer's decay = exp(a * softplus(alpha + dt)) is

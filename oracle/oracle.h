@@ -64,16 +64,6 @@ void or_rope_neox(float* x, uint32_t heads, uint32_t head_dim, uint32_t rotary_d
 /* ---- MoE ----------------------------------------------------------------- */
 void or_route_topk(const float* logits, uint32_t n, uint32_t k, uint32_t* ids, float* weights);
 
-/* One token through the MoE layer (int8-activation expert GEMVs):
- *   gate_up: [experts][2*ff][hidden] repacked Q8_0 (rows 0..ff-1 gate, ff..2ff-1 up),
- *   down:    [experts][hidden][ff]   repacked Q8_0,
- *   shared expert: sgu [2*sff][hidden], sdown [hidden][sff]; sgate fp32 [hidden] (sigmoid scalar gate);
- *   router fp32 [experts][hidden]. out [hidden]. ids/weights (k) are returned for inspection. */
-void or_moe_token(const float* x, uint32_t hidden, uint32_t ff, uint32_t n_experts, uint32_t k,
-                  const float* router, const int8_t* gu_q, const uint16_t* gu_d, const int8_t* dn_q,
-                  const uint16_t* dn_d, const int8_t* sgu_q, const uint16_t* sgu_d, const int8_t* sdn_q,
-                  const uint16_t* sdn_d, uint32_t sff, const float* sgate, float* out, uint32_t* ids, float* weights);
-
 /* ---- Gated DeltaNet ------------------------------------------------------ */
 /* One decode step for one value head. S is [d][d] value-major (S[j][i], j value, i key) in place; q, k, v
  * length d; decay = exp(g); o[j] = (S_new q)[j] / sqrt(d). */

@@ -14,6 +14,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 ORACLE_SO = HERE / "liboracle.so"
 REF_SO = HERE / "_ref" / "libhaloref.so"
+REF_MODEL_SO = HERE / "_ref" / "libhaloref_model.so"
 
 _VP, _SZ, _U32, _U64, _F32 = C.c_void_p, C.c_size_t, C.c_uint32, C.c_uint64, C.c_float
 _PF = np.ctypeslib.ndpointer(np.float32, flags="C")
@@ -45,8 +46,6 @@ _ORACLE_SIGS = {
     "or_l2norm": (None, [_PF, _SZ, _F32]),
     "or_rope_neox": (None, [_PF, _U32, _U32, _U32, _U32, _F32]),
     "or_route_topk": (None, [_PF, _U32, _U32, _PU32, _PF]),
-    "or_moe_token": (None, [_PF, _U32, _U32, _U32, _U32, _PF, _PI8, _PU16, _PI8, _PU16, _PI8, _PU16, _PI8,
-                            _PU16, _U32, _PF, _PF, _PU32, _PF]),
     "or_gdn_step": (None, [_PF, _U32, _PF, _PF, _PF, _F32, _F32, _PF]),
     "or_gdn_sequence": (None, [_PF, _U32, _U32, _VP, _SZ, _VP, _SZ, _VP, _SZ, _VP, _VP, _SZ, _VP, _SZ]),
     "or_attention_head": (None, [_PF, _PF, _PF, _U32, _U32, _SZ, _PF]),
@@ -90,6 +89,14 @@ _REF_SIGS = {
                           C.POINTER(C.c_uint64)]),
 }
 
+# the reference's ReferenceModel layer functions (oracle/ref_model_shim.cpp)
+_REF_MODEL_SIGS = {
+    "ref_linear_attention": (None, [_PU32, _PF, _PU8, _PU8, _PU8, _PU8, _PU8, _PF, _PF, _PF, _PF, _PF, _PF, _PF,
+                                    _PF]),
+    "ref_attention": (None, [_PU32, _PF, _PU8, _PU8, _PU8, _PU8, _PF, _PF, _PF, _PF, _U32]),
+    "ref_moe": (None, [_PU32, _PF, _PU8, _PU8, _PU8, _PF, _PU8, _PU8, _PU8, _PF, _PF]),
+}
+
 _libs: dict[str, C.CDLL] = {}
 
 
@@ -120,6 +127,14 @@ def has_ref() -> bool:
 
 def ref() -> C.CDLL:
     return _load(REF_SO, _REF_SIGS)
+
+
+def has_ref_model() -> bool:
+    return REF_MODEL_SO.exists()
+
+
+def ref_model() -> C.CDLL:
+    return _load(REF_MODEL_SO, _REF_MODEL_SIGS)
 
 
 # ---- numpy conveniences -------------------------------------------------------------------------------------------

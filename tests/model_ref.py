@@ -20,35 +20,7 @@ from __future__ import annotations
 import numpy as np
 
 import oracle_py as O
-
-
-def _f16(d):
-    return d.view(np.float16).astype(np.float32)
-
-
-def _sigmoid(x):
-    return (1.0 / (1.0 + np.exp(-x.astype(np.float64)))).astype(np.float32)
-
-
-def _silu(x):
-    return (x.astype(np.float64) * _sigmoid(x).astype(np.float64)).astype(np.float32)
-
-
-def _softplus(x):
-    x = x.astype(np.float64)
-    return np.where(x > 20.0, x, np.log1p(np.exp(x))).astype(np.float32)
-
-
-def _rmsnorm(x, w, eps):
-    y = np.ascontiguousarray(x, np.float32).copy()
-    O.oracle().or_rmsnorm(y, y.size, np.ascontiguousarray(w, np.float32).ctypes.data, eps)
-    return y
-
-
-def _l2norm(x, eps):
-    y = np.ascontiguousarray(x, np.float32).copy()
-    O.oracle().or_l2norm(y, y.size, eps)
-    return y
+from layer_ref import attn_heads, attn_qk, deltanet_core, f16, moe_token, rmsnorm, route
 
 
 def _gemv(w, x):
@@ -89,110 +61,54 @@ class RefModel:
 
     def _deltanet(self, l, xn):
         c, W = self.c, self.w[l]
-        Hk, Hv, d, K = c.gdn_k_heads, c.gdn_v_heads, c.gdn_head_dim, c.conv_kernel
-        Dk, Dv = Hk * d, Hv * d
-        qkv = _gemv(W["qkv"], xn)
-        z = _gemv(W["z"], xn)
-        ab = _gemv(W["ab"], xn)
-        cw = W["conv_w"]
-        hist = self.conv[l]
-        acc = cw[:, K - 1] * qkv
-        for j in range(K - 1):
-            acc = (acc + cw[:, j] * hist[j]).astype(np.float32)
-        if K > 1:
-            hist[:-1] = hist[1:].copy() if K > 2 else hist[:-1]
-            hist[K - 2] = qkv
-        y = _silu(acc.astype(np.float32))
-        q = np.concatenate([_l2norm(y[h * d:(h + 1) * d], c.rms_eps) for h in range(Hk)])
-        k = np.concatenate([_l2norm(y[Dk + h * d:Dk + (h + 1) * d], c.rms_eps) for h in range(Hk)])
-        v = y[2 * Dk:]
-        a, dt = W["a"][0], W["dt"][0]
-        g = (a * _softplus((ab[:Hv] + dt).astype(np.float32))).astype(np.float32)
-        beta = _sigmoid(ab[Hv:])
-        o = np.zeros(Dv, np.float32)
-        ora = O.oracle()
-        for h in range(Hv):
-            kh = h % Hk
-            Sh = np.ascontiguousarray(self.S[l][h])
-            oh = np.zeros(d, np.float32)
-            ora.or_gdn_step(Sh, d, np.ascontiguousarray(q[kh * d:(kh + 1) * d]),
-                            np.ascontiguousarray(k[kh * d:(kh + 1) * d]), np.ascontiguousarray(v[h * d:(h + 1) * d]),
-                            float(g[h]), float(beta[h]), oh)
-            self.S[l][h] = Sh
-            on = _rmsnorm(oh, W["norm_w"][0], c.rms_eps)
-            o[h * d:(h + 1) * d] = on * _sigmoid(z[h * d:(h + 1) * d])
+        qkv, z, ab = _gemv(W["qkv"], xn), _gemv(W["z"], xn), _gemv(W["ab"], xn)
+        o = deltanet_core(c.gdn_k_heads, c.gdn_v_heads, c.gdn_head_dim, c.rms_eps, W["conv_w"], W["a"][0],
+                          W["dt"][0], W["norm_w"][0], qkv, z, ab, self.conv[l], self.S[l])
         return _gemv(W["out"], o)
 
     def _attention(self, l, xn):
         c, W = self.c, self.w[l]
-        Hq, Hkv, hd = c.q_heads, c.kv_heads, c.head_dim
-        G = Hq // Hkv
-        qg = _gemv(W["qg"], xn).reshape(Hq, 2, hd)
-        kk = _gemv(W["k"], xn).reshape(Hkv, hd)
-        vv = _gemv(W["v"], xn).reshape(Hkv, hd)
-        q = np.stack([_rmsnorm(qg[h, 0], W["q_norm"][0], c.rms_eps) for h in range(Hq)])
-        gate = qg[:, 1]
-        kn = np.stack([_rmsnorm(kk[h], W["k_norm"][0], c.rms_eps) for h in range(Hkv)])
-        q = np.ascontiguousarray(q)
-        kn = np.ascontiguousarray(kn)
-        O.oracle().or_rope_neox(q.reshape(-1), Hq, hd, c.rotary_dim, self.pos, c.rope_theta)
-        O.oracle().or_rope_neox(kn.reshape(-1), Hkv, hd, c.rotary_dim, self.pos, c.rope_theta)
+        q, gate, kn = attn_qk(c.q_heads, c.kv_heads, c.head_dim, c.rotary_dim, c.rope_theta, c.rms_eps,
+                              _gemv(W["qg"], xn), _gemv(W["k"], xn), W["q_norm"][0], W["k_norm"][0], self.pos)
         self.kc[l][self.pos] = kn
-        self.vc[l][self.pos] = vv
+        self.vc[l][self.pos] = _gemv(W["v"], xn).reshape(c.kv_heads, c.head_dim)
         n = self.pos + 1
-        o = np.zeros((Hq, hd), np.float32)
-        for h in range(Hq):
-            kvh = h // G
-            Kh = np.ascontiguousarray(self.kc[l][:n, kvh])
-            Vh = np.ascontiguousarray(self.vc[l][:n, kvh])
-            oh = np.zeros(hd, np.float32)
-            O.oracle().or_attention_head(np.ascontiguousarray(q[h]), Kh, Vh, n, hd, hd, oh)
-            o[h] = oh * _sigmoid(gate[h])
-        return _gemv(W["o"], o.reshape(-1))
+        return _gemv(W["o"], attn_heads(q, self.kc[l][:n], self.vc[l][:n], gate))
 
     def _moe(self, l, xn):
         c, W = self.c, self.w[l]
-        E, k, F, SF, H = c.n_experts, c.n_used, c.expert_ff, c.shared_ff, c.hidden
-        logits = np.zeros(E, np.float32)
-        O.oracle().or_matvec_f32(np.ascontiguousarray(W["router"]), E, H, np.ascontiguousarray(xn), logits)
-        ids, wts = np.zeros(k, np.uint32), np.zeros(k, np.float32)
-        O.oracle().or_route_topk(logits, E, k, ids, wts)
+        F, H = c.expert_ff, c.hidden
+        logits, _, _ = route(W["router"], xn, c.n_used)
         srt = np.sort(logits.astype(np.float64))[::-1]
-        self.route_gaps.append(float(srt[k - 1] - srt[k]))  # logit gap at the top-k boundary
-        out = np.zeros(H, np.float32)
+        self.route_gaps.append(float(srt[c.n_used - 1] - srt[c.n_used]))  # logit gap at the top-k boundary
         gq, gd = W["gate"]
         uq, ud = W["up"]
         dq, dd = W["down"]
-        for s in range(k + 1):
-            if s < k:
-                e = int(ids[s])
-                gw, uw = (gq[e * F:(e + 1) * F], gd[e * F:(e + 1) * F]), (uq[e * F:(e + 1) * F], ud[e * F:(e + 1) * F])
-                dw = (dq[e * H:(e + 1) * H], dd[e * H:(e + 1) * H])
-                wgt = float(wts[s])
-            else:
-                gw, uw, dw = W["sgate"], W["sup"], W["sdown"]
-                wgt = float(_sigmoid(np.array([np.dot(W["shared_gate"][0].astype(np.float64),
-                                                      xn.astype(np.float64))], np.float32))[0])
-            h = (_silu(_gemv(gw, xn)) * _gemv(uw, xn)).astype(np.float32)
-            out = (out + np.float32(wgt) * _gemv(dw, h)).astype(np.float32)
+
+        def expert(e):
+            return ((gq[e * F:(e + 1) * F], gd[e * F:(e + 1) * F]), (uq[e * F:(e + 1) * F], ud[e * F:(e + 1) * F]),
+                    (dq[e * H:(e + 1) * H], dd[e * H:(e + 1) * H]))
+
+        out, ids, _ = moe_token(xn, W["router"], W["shared_gate"][0], c.n_used, expert,
+                                (W["sgate"], W["sup"], W["sdown"]), _gemv)
         return out, ids
 
     def step(self, token):
         """Feeds one token at the next position; returns the logits."""
         c = self.c
         qs, d = self.embd
-        res = (_f16(d[token]).repeat(32) * qs[token].astype(np.float32)).astype(np.float32)
+        res = (f16(d[token]).repeat(32) * qs[token].astype(np.float32)).astype(np.float32)
         self.last_ids = []
         self.route_gaps = []
         for l in range(c.layers):
             W = self.w[l]
-            xn = _rmsnorm(res, W["attn_norm"][0], c.rms_eps)
+            xn = rmsnorm(res, W["attn_norm"][0], c.rms_eps)
             delta = self._attention(l, xn) if self.attn[l] else self._deltanet(l, xn)
             res = (res + delta).astype(np.float32)
-            xn = _rmsnorm(res, W["ffn_norm"][0], c.rms_eps)
+            xn = rmsnorm(res, W["ffn_norm"][0], c.rms_eps)
             m, ids = self._moe(l, xn)
             self.last_ids.append(ids)
             res = (res + m).astype(np.float32)
         self.pos += 1
-        xn = _rmsnorm(res, self.out_norm, c.rms_eps)
+        xn = rmsnorm(res, self.out_norm, c.rms_eps)
         return _gemv(self.head, xn)

@@ -26,38 +26,14 @@ from __future__ import annotations
 import numpy as np
 
 import oracle_py as O
+from layer_ref import (attn_heads, attn_qk, conv_silu, f16, gated_head_norm, gdn_gates, gdn_head, l2norm, rmsnorm,
+                       sigmoid, silu, softplus, split_qkv)
 
 FLIP_WINDOW = 2e-3  # in units of one code
 
 
-def _f16(d):
-    return d.view(np.float16).astype(np.float32)
-
-
-def _sigmoid(x):
-    return (1.0 / (1.0 + np.exp(-np.asarray(x, np.float64)))).astype(np.float32)
-
-
-def _silu(x):
-    x = np.asarray(x, np.float32)
-    return (x.astype(np.float64) * _sigmoid(x).astype(np.float64)).astype(np.float32)
-
-
-def _softplus(x):
-    x = np.asarray(x, np.float64)
-    return np.where(x > 20.0, x, np.log1p(np.exp(x))).astype(np.float32)
-
-
-def _rmsnorm(x, w, eps):
-    y = np.ascontiguousarray(x, np.float32).copy()
-    O.oracle().or_rmsnorm(y, y.size, np.ascontiguousarray(w, np.float32).ctypes.data, eps)
-    return y
-
-
-def _l2norm(x, eps):
-    y = np.ascontiguousarray(x, np.float32).copy()
-    O.oracle().or_l2norm(y, y.size, eps)
-    return y
+# the value path of every stage is tests/layer_ref.py's (pinned against the reference's ReferenceModel layers)
+_f16, _sigmoid, _silu, _softplus, _rmsnorm, _l2norm = f16, sigmoid, silu, softplus, rmsnorm, l2norm
 
 
 def rope_mag(x, pos, rot, theta):
@@ -203,12 +179,9 @@ class LayerChecker:
             p = int(snap["nkv"][s]) - 1  # the step's position
             # causal conv: slots (p + 1 + j) % K, oldest first, then this step's projection (reference.cpp:296-305)
             win = [ring0[s, (p + 1 + j) % K] for j in range(K - 1)] + [qkv[s]]
-            conv = sum(cw[:, j].astype(np.float64) * win[j].astype(np.float64) for j in range(K))
             assert np.array_equal(ring1[s, p % K], qkv[s]), f"conv ring slot of L{l}"
-            y = _silu(conv.astype(np.float32))
-            q = np.concatenate([_l2norm(y[h * d:(h + 1) * d], c.rms_eps) for h in range(Hk)])
-            k = np.concatenate([_l2norm(y[Dk + h * d:Dk + (h + 1) * d], c.rms_eps) for h in range(Hk)])
-            v = y[2 * Dk:]
+            y = conv_silu(cw, win)
+            q, k, v = split_qkv(y, Hk, Hv, d, c.rms_eps)
             # term magnitudes carried into the recurrence: the conv's sum |w x| through SiLU (slope <= 1.1) and,
             # for k, the head's L2 normalisation
             ymag = 1.1 * sum(np.abs(cw[:, j].astype(np.float64) * win[j]) for j in range(K)) + np.abs(y)
@@ -216,8 +189,7 @@ class LayerChecker:
                                    np.sqrt(np.sum(y[Dk + h * d:Dk + (h + 1) * d].astype(np.float64) ** 2) + c.rms_eps)
                                    for h in range(Hk)])
             vmag = ymag[2 * Dk:]
-            g = (a * _softplus(ab[s, :Hv] + dt)).astype(np.float32)
-            beta = _sigmoid(ab[s, Hv:])
+            g, beta = gdn_gates(a, dt, ab[s, :Hv], ab[s, Hv:])
             o = np.zeros(Dv, np.float32)
             omag = np.zeros(Dv, np.float64)
             for h in range(Hv):
@@ -225,17 +197,14 @@ class LayerChecker:
                 qh, khv, vh = q[kh * d:(kh + 1) * d], k[kh * d:(kh + 1) * d], v[h * d:(h + 1) * d]
                 Sv = np.ascontiguousarray(st0[s, h].T)  # value-major for the oracle
                 S_old = Sv.astype(np.float64).copy()
-                oh = np.zeros(d, np.float32)
-                O.oracle().or_gdn_step(Sv, d, np.ascontiguousarray(qh), np.ascontiguousarray(khv),
-                                       np.ascontiguousarray(vh), float(g[h]), float(beta[h]), oh)
+                oh = gdn_head(Sv, qh, khv, vh, g[h], beta[h])
                 decay = np.exp(np.float64(g[h]))
                 km = kmag[kh * d:(kh + 1) * d]
                 dmag = vmag[h * d:(h + 1) * d] + np.abs(S_old) @ km
                 mag_s = decay * np.abs(S_old) + np.outer(dmag, km)
                 r.close(f"state@L{l}s{s}h{h}", st1[s, h].T, Sv, mag_s)
-                on = _rmsnorm(oh, nw, c.rms_eps)
                 zg = _sigmoid(z[s, h * d:(h + 1) * d])
-                o[h * d:(h + 1) * d] = on * zg
+                o[h * d:(h + 1) * d] = gated_head_norm(oh, nw, z[s, h * d:(h + 1) * d], c.rms_eps)
                 # o = S' q / sqrt(d), normalised: its terms' magnitude scaled like the value
                 rms = np.sqrt(np.mean(oh.astype(np.float64) ** 2) + c.rms_eps)
                 omag[h * d:(h + 1) * d] = (mag_s @ np.abs(qh)) / np.sqrt(d) / rms * np.abs(nw) * zg
@@ -262,14 +231,9 @@ class LayerChecker:
         os_ = tr[(l, "os")].reshape(S, Hq * hd // 32)
         for s in range(S):
             p = int(snap["nkv"][s]) - 1
-            g3 = qg[s].reshape(Hq, 2, hd)
-            q = np.ascontiguousarray(np.stack([_rmsnorm(g3[h, 0], qn, c.rms_eps) for h in range(Hq)]))
-            gate = g3[:, 1]
-            k = np.ascontiguousarray(np.stack([_rmsnorm(kk[s].reshape(Hkv, hd)[h], kn, c.rms_eps)
-                                               for h in range(Hkv)]))
-            kmag = rope_mag(k, p, c.rotary_dim, c.rope_theta)
-            O.oracle().or_rope_neox(q.reshape(-1), Hq, hd, c.rotary_dim, p, c.rope_theta)
-            O.oracle().or_rope_neox(k.reshape(-1), Hkv, hd, c.rotary_dim, p, c.rope_theta)
+            q, gate, k = attn_qk(Hq, Hkv, hd, c.rotary_dim, c.rope_theta, c.rms_eps, qg[s], kk[s], qn, kn, p)
+            k_pre = np.stack([_rmsnorm(kk[s].reshape(Hkv, hd)[h], kn, c.rms_eps) for h in range(Hkv)])
+            kmag = rope_mag(k_pre, p, c.rotary_dim, c.rope_theta)
             # this step's K / V rows as the GPU appended them
             pg = int(pages[s, p // 16])
             r.close(f"k append@L{l}s{s}", kp[pg, :, p % 16], k, kmag)
@@ -278,15 +242,11 @@ class LayerChecker:
             rows = np.array([int(pages[s, t // 16]) for t in range(n)])
             Kc = kp[rows, :, np.arange(n) % 16]  # [n][Hkv][hd], the GPU's cache (teacher-forced)
             Vc = vp[rows, :, np.arange(n) % 16]
-            o = np.zeros((Hq, hd), np.float32)
+            o = attn_heads(q, Kc, Vc, gate).reshape(Hq, hd)
             omag = np.zeros((Hq, hd), np.float64)
             for h in range(Hq):
                 kvh = h // G
-                oh = np.zeros(hd, np.float32)
-                O.oracle().or_attention_head(np.ascontiguousarray(q[h]), np.ascontiguousarray(Kc[:, kvh]),
-                                             np.ascontiguousarray(Vc[:, kvh]), n, hd, hd, oh)
                 gh = _sigmoid(gate[h])
-                o[h] = oh * gh
                 sc = Kc[:, kvh].astype(np.float64) @ q[h].astype(np.float64) / np.sqrt(hd)
                 pw = np.exp(sc - sc.max())
                 pw /= pw.sum()
@@ -477,8 +437,7 @@ class PrefillChecker(LayerChecker):
                         win.append(ring0[s, pp % K])
                     else:
                         win.append(np.zeros(C, np.float32))
-                conv = sum(cw[:, jj].astype(np.float64) * win[jj].astype(np.float64) for jj in range(K))
-                y = _silu(conv.astype(np.float32))
+                y = conv_silu(cw, win)
                 ymag = 1.1 * sum(np.abs(cw[:, jj].astype(np.float64) * win[jj]) for jj in range(K)) + np.abs(y)
                 for h in range(Hk):
                     for nm, base, got in (("q", 0, gq), ("k", Dk, gk)):
@@ -487,9 +446,9 @@ class PrefillChecker(LayerChecker):
                         r.close(f"conv {nm}@L{l}t{t}", got[t, h * d:(h + 1) * d], _l2norm(seg, c.rms_eps),
                                 ymag[base + h * d:base + (h + 1) * d] / nrm)
                 r.close(f"conv v@L{l}t{t}", gv[t], y[2 * Dk:], ymag[2 * Dk:])
-                g = (a * _softplus(ab[t, :Hv] + dt)).astype(np.float32)
+                g, beta = gdn_gates(a, dt, ab[t, :Hv], ab[t, Hv:])
                 r.close(f"decay@L{l}t{t}", gg[t], g, np.abs(g) + 1e-6)
-                r.close(f"beta@L{l}t{t}", gb[t], _sigmoid(ab[t, Hv:]), np.abs(_sigmoid(ab[t, Hv:])))
+                r.close(f"beta@L{l}t{t}", gb[t], beta, np.abs(beta))
                 # the recurrence from the GPU's inputs (teacher-forced per token)
                 kmag = np.concatenate([ymag[Dk + h * d:Dk + (h + 1) * d] /
                                        np.sqrt(np.sum(y[Dk + h * d:Dk + (h + 1) * d].astype(np.float64) ** 2) +
@@ -497,20 +456,18 @@ class PrefillChecker(LayerChecker):
                 for h in range(Hv):
                     kh = h % Hk
                     qh, kv_, vh = gq[t, kh * d:(kh + 1) * d], gk[t, kh * d:(kh + 1) * d], gv[t, h * d:(h + 1) * d]
-                    oh = np.zeros(d, np.float32)
                     km = np.maximum(kmag[kh * d:(kh + 1) * d], np.abs(kv_))
                     # this token's terms: |v| and |decay S k| (the actual state, so errors carried in from earlier
                     # tokens enter through the contraction decay (I - beta k k^T) rather than a worst-case feedback)
                     decay = np.exp(np.float64(gg[t, h]))
                     dmag = ymag[2 * Dk + h * d:2 * Dk + (h + 1) * d] + decay * (np.abs(Sv[h]).astype(np.float64) @ km)
                     Sm[h] = decay * Sm[h] + np.outer(dmag, km)
-                    O.oracle().or_gdn_step(Sv[h], d, np.ascontiguousarray(qh), np.ascontiguousarray(kv_),
-                                           np.ascontiguousarray(vh), float(gg[t, h]), float(gb[t, h]), oh)
+                    oh = gdn_head(Sv[h], qh, kv_, vh, gg[t, h], gb[t, h])
                     r.close(f"recurrence o@L{l}t{t}", go[t, h * d:(h + 1) * d], oh,
                             (Sm[h] @ np.abs(qh)) / np.sqrt(d))
                 # gated output norm from the GPU's o
-                on = np.concatenate([_rmsnorm(go[t, h * d:(h + 1) * d], nw, c.rms_eps) *
-                                     _sigmoid(z[t, h * d:(h + 1) * d]) for h in range(Hv)])
+                on = np.concatenate([gated_head_norm(go[t, h * d:(h + 1) * d], nw, z[t, h * d:(h + 1) * d],
+                                                     c.rms_eps) for h in range(Hv)])
                 r.codes_match(f"gated norm codes@L{l}t{t}", oq[t], os_[t], on)
                 gemv(r, f"out@L{l}t{t}", self._w(l, "out"), oq[t], os_[t], tr[(l, "delta")].reshape(T, -1)[t])
             for h in range(Hv):
@@ -538,12 +495,10 @@ class PrefillChecker(LayerChecker):
             gemv(r, f"k@L{l}t{t}", self._w(l, "k"), xq[t], xs[t], kk[t])
             gemv(r, f"v@L{l}t{t}", self._w(l, "v"), xq[t], xs[t], vv[t])
             g3 = qg[t].reshape(Hq, 2, hd)
-            q = np.ascontiguousarray(np.stack([_rmsnorm(g3[h, 0], qn, c.rms_eps) for h in range(Hq)]))
-            k = np.ascontiguousarray(np.stack([_rmsnorm(kk[t].reshape(Hkv, hd)[h], kn, c.rms_eps)
-                                               for h in range(Hkv)]))
-            qmag, kmag = rope_mag(q, p, c.rotary_dim, c.rope_theta), rope_mag(k, p, c.rotary_dim, c.rope_theta)
-            O.oracle().or_rope_neox(q.reshape(-1), Hq, hd, c.rotary_dim, p, c.rope_theta)
-            O.oracle().or_rope_neox(k.reshape(-1), Hkv, hd, c.rotary_dim, p, c.rope_theta)
+            q_pre = np.stack([_rmsnorm(g3[h, 0], qn, c.rms_eps) for h in range(Hq)])
+            k_pre = np.stack([_rmsnorm(kk[t].reshape(Hkv, hd)[h], kn, c.rms_eps) for h in range(Hkv)])
+            qmag, kmag = rope_mag(q_pre, p, c.rotary_dim, c.rope_theta), rope_mag(k_pre, p, c.rotary_dim, c.rope_theta)
+            q, gate, k = attn_qk(Hq, Hkv, hd, c.rotary_dim, c.rope_theta, c.rms_eps, qg[t], kk[t], qn, kn, p)
             r.close(f"q rope@L{l}t{t}", aq[t], q, qmag)
             pg = int(pages[s, p // 16])
             r.close(f"k append@L{l}t{t}", kp[pg, :, p % 16], k, kmag)
@@ -551,17 +506,12 @@ class PrefillChecker(LayerChecker):
             n = p + 1
             prow = np.array([int(pages[s, u // 16]) for u in range(n)])
             Kc, Vc = kp[prow, :, np.arange(n) % 16], vp[prow, :, np.arange(n) % 16]
-            gate = g3[:, 1]
-            o = np.zeros((Hq, hd), np.float32)
+            o = attn_heads(aq[t], Kc, Vc, gate).reshape(Hq, hd)  # the GPU's rotated queries (teacher-forced)
             omag = np.zeros((Hq, hd), np.float64)
             for h in range(Hq):
                 kvh = h // G
-                oh = np.zeros(hd, np.float32)
-                qh = np.ascontiguousarray(aq[t, h])  # the GPU's rotated query (teacher-forced)
-                O.oracle().or_attention_head(qh, np.ascontiguousarray(Kc[:, kvh]), np.ascontiguousarray(Vc[:, kvh]),
-                                             n, hd, hd, oh)
+                qh = aq[t, h]
                 gh = _sigmoid(gate[h])
-                o[h] = oh * gh
                 sc = Kc[:, kvh].astype(np.float64) @ qh.astype(np.float64) / np.sqrt(hd)
                 pw = np.exp(sc - sc.max())
                 pw /= pw.sum()

@@ -180,6 +180,36 @@ def test_matvec_f32x_matches_reference_bitwise():
 
 
 @needs_ref
+@pytest.mark.parametrize("rows,cols", [(512, 2048), (3, 1001), (600, 2048)])
+def test_matvec_f32_matches_reference_bitwise(rows, cols):
+    """or_matvec_f32 (the router / rowblock checker) against the reference's cpu::MatVec over an F32 tensor
+    (cpu_ops.cpp:97-132): double accumulation in column order, bitwise, including the row-split threaded case
+    (rows * cols >= 2^20) and ragged shapes."""
+    o, R = O.oracle(), O.ref()
+    rng = np.random.default_rng(rows + cols)
+    w = rng.normal(0, 0.02, (rows, cols)).astype(np.float32)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    a, b = np.zeros(rows, np.float32), np.zeros(rows, np.float32)
+    o.or_matvec_f32(w, rows, cols, x, a)
+    R.ref_matvec_f32(w, rows, cols, x, b)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_matvec_f32_closed_form():
+    """One-hot rows select x exactly; a row of ones over exactly representable values sums exactly."""
+    o = O.oracle()
+    cols = 96
+    x = (np.arange(cols, dtype=np.float32) - 40.0) * 0.25
+    w = np.zeros((cols + 1, cols), np.float32)
+    w[np.arange(cols), (np.arange(cols) * 7) % cols] = 1.0
+    w[cols] = 1.0
+    y = np.zeros(cols + 1, np.float32)
+    o.or_matvec_f32(w, cols + 1, cols, x, y)
+    assert np.array_equal(y[:cols], x[(np.arange(cols) * 7) % cols])
+    assert y[cols] == np.float32(x.astype(np.float64).sum())
+
+
+@needs_ref
 def test_elementwise_match_reference():
     o, R = O.oracle(), O.ref()
     rng = np.random.default_rng(10)

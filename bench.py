@@ -1,16 +1,17 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized decode hot path on one MI355X.
 
-Workload (batch 1): one decode pass through the Q8_0 projections of a layer --
-quantize x[2048] -> q/gate 2048->4096 and kv 2048->512 GEMVs -> quantize a[4096] -> o 4096->2048 GEMV -- with
-weights seeded on the device and rotated over enough distinct copies (>= 570 MB) that no launch reads weights from
-the 256 MB MALL. A step is one such pass; steps are recorded once into a HIP graph and replayed.
+Headline workload (C0, batch 1): one Q8_0 GEMV, W [4096 x 4096] x Q8_0-quantized x, the
+metric's "Q8_0 GEMV achieved HBM GB/s". Weights are seeded on the device and rotated over enough distinct copies
+(>= 600 MB) that no launch reads weights from the 256 MB MALL. A step is one GEMV; exactly --steps GEMVs are timed
+(graph replays of the rotation plus one graph of the remainder), after --warmup untimed ones.
 
-value  = algorithmic bytes of a pass (weights + activations + outputs) / measured time per pass, in GB/s.
-roofline = config C0 (one 4096x4096 Q8_0 GEMV, 17,858,560 algorithmic bytes), the dominant kernel, timed with HIP
-           events over back-to-back launches on the device stream, against 8 TB/s.
-cpu_baseline = the reference's CPU MatVec (cpu::MatVec, built from its sources into oracle/_ref) on the same three
-           projections, all hardware threads, on a bounded sample.
+value    = algorithmic bytes of a GEMV (17,858,560: weights + x + y) / measured time per GEMV, in GB/s.
+roofline = the same kernel (halo_gemv_q8a8_l64_r1_b1) against 8 TB/s, with the calibrated PMC traffic from the
+           committed profile; moe.T1.roofline likewise for the MoE layer at one token.
+cpu_baseline = the reference's cpu::MatVec (built from its sources into oracle/_ref) on the same GEMV, all hardware
+           threads, plus legs: 1 thread, the C1 projections, the C2 MoE layer at T=1 and the C3 recurrence at S=4.
+Other sections: c1 (the three projections at M = 1..16), moe (C2), gdn (C3), c4 (the hybrid model), sample.
 """
 from __future__ import annotations
 
@@ -75,109 +76,10 @@ def run_gpu(args):
             return run_prefill(args, dev, H, res)
         if args.mode == "sample":
             return run_sample(args, dev, H, res)
-        # ---------------- C1 pass at M=1 (the bench value) and the M sweep ----------------
-        per_copy = sum(q8_bytes(r, c) for r, c in C1_SHAPES)
-        copies = max(2, -(-MIN_ROTATION_BYTES // per_copy))
-        log(f"[bench] C1: {copies} weight copies ({copies * per_copy / 2**20:.0f} MiB)")
-        sets = []
-        for i in range(copies):
-            sets.append([H.Q8Weights(dev, r, c).synth(dev, seed=1000 * i + j) for j, (r, c) in enumerate(C1_SHAPES)])
-        mmax = 16
-        x = dev.array((mmax, 2048), np.float32)
-        a = dev.array((mmax, 4096), np.float32)
-        dev.op("synth_f32", x.ptr, mmax * 2048, 7, 1.0)
-        dev.op("synth_f32", a.ptr, mmax * 4096, 8, 1.0)
-        xq, xs = dev.array((mmax, 2048), np.int8), dev.array((mmax, 64), np.float32)
-        aq, as_ = dev.array((mmax, 4096), np.int8), dev.array((mmax, 128), np.float32)
-        yqg, ykv, yo = (dev.array((mmax, 4096), np.float32), dev.array((mmax, 512), np.float32),
-                        dev.array((mmax, 2048), np.float32))
-        dev.sync()
-
-        in_x = H.ProjInput(x=x.ptr, mode=H.PROJ_F)
-        in_a = H.ProjInput(x=a.ptr, mode=H.PROJ_F)
-
-        def c1_pass(ws, m, fused=True):
-            if fused and m <= 8:
-                # one launch per input row set: quantize prologue + (q|gate, kv), then quantize prologue + o
-                H.proj_q8(dev, ws[:2], [yqg, ykv], in_x, m)
-                H.proj_q8(dev, ws[2:], [yo], in_a, m)
-                return
-            dev.op("quantize_q8", x.ptr, xq.ptr, xs.ptr, m, 2048)
-            dev.op("matvec_q8a8", ctypes.byref(ws[0].desc), xq.ptr, xs.ptr, yqg.ptr, m, 4096)
-            dev.op("matvec_q8a8", ctypes.byref(ws[1].desc), xq.ptr, xs.ptr, ykv.ptr, m, 512)
-            dev.op("quantize_q8", a.ptr, aq.ptr, as_.ptr, m, 4096)
-            dev.op("matvec_q8a8", ctypes.byref(ws[2].desc), aq.ptr, as_.ptr, yo.ptr, m, 2048)
-
-        # correctness spot check of copy 0 against the oracle before timing anything
-        sys.path.insert(0, str(ROOT / "oracle"))
-        import oracle_py as O
-
-        c1_pass(sets[0], 1)
-        qs, d = sets[0][2].host()
-        a_host = a.download()[0]
-        aq_h, as_h = O.quantize(a_host)
-        want, mag = O.gemv_q8a8(qs, d, aq_h, as_h)
-        got = yo.download()[0]
-        assert np.all(np.abs(got - want) <= 1e-5 * mag + 1e-6), "bench spot check failed"
-
-        if args.eager:  # kernel durations of the M = 1 pass under a tracer that cannot follow graph launches
-            for _ in range(max(1, args.steps // copies)):
-                for ws in sets:
-                    c1_pass(ws, 1)
-            dev.sync()
-            res.update(value=0.0, steps_timed=0, ms_per_step=0.0, c1_sweep=None, roofline=None)
-            return res
-
-        def graph_for(m, fused=True):
-            dev.begin_capture()
-            for ws in sets:
-                c1_pass(ws, m, fused)
-            return dev.end_capture()
-
-        sweep = {}
-        g = graph_for(1, fused=False)  # the unfused sequence (2 quantize + 3 GEMV launches), for comparison
-        dev.launch_graph(g)
-        dev.sync()
-        nrep = max(1, -(-1000 // copies))
-        dev.timer_start()
-        for _ in range(nrep):
-            dev.launch_graph(g)
-        ms = dev.timer_stop()
-        sweep["1_unfused"] = {"us_per_pass": round(ms / (nrep * copies) * 1e3, 3),
-                              "GBps": round(c1_pass_bytes(1) / (ms / (nrep * copies) * 1e-3) / 1e9, 1)}
-        dev.free_graph(g)
-        for m in (1, 2, 4, 8, 16):
-            g = graph_for(m)
-            reps = 1 if m > 1 else max(1, args.warmup // copies)
-            for _ in range(reps):
-                dev.launch_graph(g)
-            dev.sync()
-            if m == 1:
-                nrep = max(1, -(-args.steps // copies))
-                dev.timer_start()
-                for _ in range(nrep):
-                    dev.launch_graph(g)
-                ms = dev.timer_stop()
-                steps = nrep * copies
-                res["steps_timed"] = steps
-                res["ms_per_step"] = ms / steps
-                res["value"] = c1_pass_bytes(1) / (ms / steps * 1e-3) / 1e9
-            else:
-                nrep = max(1, -(-200 // copies))
-                dev.timer_start()
-                for _ in range(nrep):
-                    dev.launch_graph(g)
-                ms = dev.timer_stop()
-                steps = nrep * copies
-            sweep[str(m)] = {"us_per_pass": round(ms / steps * 1e3, 3),
-                             "GBps": round(c1_pass_bytes(m) / (ms / steps * 1e-3) / 1e9, 1)}
-            dev.free_graph(g)
-        res["c1_sweep"] = sweep
-        log(f"[bench] C1 sweep {sweep}")
-        del sets
         run_c0(args, dev, H, res)
         if not args.quick:
             roof = res["roofline"]
+            run_c1(args, dev, H, res)
             run_moe(args, dev, H, res)
             run_gdn(args, dev, H, res)
             run_c4(args, dev, H, res)
@@ -186,6 +88,101 @@ def run_gpu(args):
         return res
     finally:
         dev.close()
+
+
+def run_c1(args, dev, H, res):
+    """C1: one decode pass through the three projections (quantize x -> q|gate + kv, quantize a -> o), fused
+    (prologue quantization, grouped matrices) and unfused, at M = 1, 2, 4, 8, 16 tokens."""
+    per_copy = sum(q8_bytes(r, c) for r, c in C1_SHAPES)
+    copies = max(2, -(-MIN_ROTATION_BYTES // per_copy))
+    log(f"[bench] C1: {copies} weight copies ({copies * per_copy / 2**20:.0f} MiB)")
+    sets = []
+    for i in range(copies):
+        sets.append([H.Q8Weights(dev, r, c).synth(dev, seed=1000 * i + j) for j, (r, c) in enumerate(C1_SHAPES)])
+    mmax = 16
+    x = dev.array((mmax, 2048), np.float32)
+    a = dev.array((mmax, 4096), np.float32)
+    dev.op("synth_f32", x.ptr, mmax * 2048, 7, 1.0)
+    dev.op("synth_f32", a.ptr, mmax * 4096, 8, 1.0)
+    xq, xs = dev.array((mmax, 2048), np.int8), dev.array((mmax, 64), np.float32)
+    aq, as_ = dev.array((mmax, 4096), np.int8), dev.array((mmax, 128), np.float32)
+    yqg, ykv, yo = (dev.array((mmax, 4096), np.float32), dev.array((mmax, 512), np.float32),
+                    dev.array((mmax, 2048), np.float32))
+    dev.sync()
+
+    in_x = H.ProjInput(x=x.ptr, mode=H.PROJ_F)
+    in_a = H.ProjInput(x=a.ptr, mode=H.PROJ_F)
+
+    def c1_pass(ws, m, fused=True):
+        if fused and m <= 8:
+            # one launch per input row set: quantize prologue + (q|gate, kv), then quantize prologue + o
+            H.proj_q8(dev, ws[:2], [yqg, ykv], in_x, m)
+            H.proj_q8(dev, ws[2:], [yo], in_a, m)
+            return
+        dev.op("quantize_q8", x.ptr, xq.ptr, xs.ptr, m, 2048)
+        dev.op("matvec_q8a8", ctypes.byref(ws[0].desc), xq.ptr, xs.ptr, yqg.ptr, m, 4096)
+        dev.op("matvec_q8a8", ctypes.byref(ws[1].desc), xq.ptr, xs.ptr, ykv.ptr, m, 512)
+        dev.op("quantize_q8", a.ptr, aq.ptr, as_.ptr, m, 4096)
+        dev.op("matvec_q8a8", ctypes.byref(ws[2].desc), aq.ptr, as_.ptr, yo.ptr, m, 2048)
+
+    # correctness spot check of copy 0 against the oracle before timing anything
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle_py as O
+
+    c1_pass(sets[0], 1)
+    qs, d = sets[0][2].host()
+    a_host = a.download()[0]
+    aq_h, as_h = O.quantize(a_host)
+    want, mag = O.gemv_q8a8(qs, d, aq_h, as_h)
+    got = yo.download()[0]
+    assert np.all(np.abs(got - want) <= 1e-5 * mag + 1e-6), "bench spot check failed"
+
+    if args.eager:  # kernel durations of the M = 1 pass under a tracer that cannot follow graph launches
+        for _ in range(max(1, args.steps // copies)):
+            for ws in sets:
+                c1_pass(ws, 1)
+        dev.sync()
+        res["c1"] = None
+        return res
+
+    def graph_for(m, fused=True):
+        dev.begin_capture()
+        for ws in sets:
+            c1_pass(ws, m, fused)
+        return dev.end_capture()
+
+    sweep = {}
+    g = graph_for(1, fused=False)  # the unfused sequence (2 quantize + 3 GEMV launches), for comparison
+    dev.launch_graph(g)
+    dev.sync()
+    nrep = max(1, -(-1000 // copies))
+    dev.timer_start()
+    for _ in range(nrep):
+        dev.launch_graph(g)
+    ms = dev.timer_stop()
+    sweep["1_unfused"] = {"us_per_pass": round(ms / (nrep * copies) * 1e3, 3),
+                          "GBps": round(c1_pass_bytes(1) / (ms / (nrep * copies) * 1e-3) / 1e9, 1)}
+    dev.free_graph(g)
+    for m in (1, 2, 4, 8, 16):
+        g = graph_for(m)
+        reps = 1 if m > 1 else max(1, args.warmup // copies)
+        for _ in range(reps):
+            dev.launch_graph(g)
+        dev.sync()
+        nrep = max(1, -(-(2000 if m == 1 else 200) // copies))
+        dev.timer_start()
+        for _ in range(nrep):
+            dev.launch_graph(g)
+        ms = dev.timer_stop()
+        steps = nrep * copies
+        sweep[str(m)] = {"us_per_pass": round(ms / steps * 1e3, 3),
+                         "GBps": round(c1_pass_bytes(m) / (ms / steps * 1e-3) / 1e9, 1)}
+        dev.free_graph(g)
+    res["c1"] = {"workload": "C1 Q8_0 projections 2048->4096, 2048->512, 4096->2048, fp32 activations "
+                             "quantized in the prologue", "bytes_per_pass_m1": c1_pass_bytes(1),
+                 "GBps_m1": sweep["1"]["GBps"], "sweep": sweep}
+    log(f"[bench] C1 sweep {sweep}")
+    return res
 
 
 def moe_bytes(E, H_, F, SF, U, T):
@@ -256,6 +253,13 @@ def run_moe(args, dev, H, res):
         nbytes = float(np.mean([moe_bytes(base.E, base.H, base.F, base.SF, u, T) for u in Us]))
         out[f"T{T}"] = {"us_per_layer": round(us, 3), "mean_U": round(float(np.mean(Us)), 2),
                         "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        if T == 1:
+            gbps = nbytes / (us * 1e-6) / 1e9
+            out["T1"]["roofline"] = {
+                "bound": "hbm", "kernel": "MoE decode layer at T=1 (halo_op_moe_decode: router, top-k, gate/up, down)",
+                "achieved": round(gbps, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBS, 4),
+                "traffic": None, "algorithmic_bytes_per_launch": round(nbytes),
+                "timing": "HIP events over graph replays of 40 layers with rotated routers, shared experts and inputs"}
         if T <= 4:
             # the layer as the model runs it: residual + delta -> FFN norm -> MoE, as a norm launch followed by the
             # plain decode, and with the norm in the router launch
@@ -818,126 +822,229 @@ def run_membw(args, dev, H, res):
 
 
 def run_c0(args, dev, H, res):
-        # ---------------- C0: the dominant kernel, back-to-back over rotated copies ----------------
-        c0_copies = max(2, -(-MIN_ROTATION_BYTES // q8_bytes(4096, 4096)))
-        ws0 = [H.Q8Weights(dev, 4096, 4096).synth(dev, seed=50000 + i) for i in range(c0_copies)]
-        x0 = dev.array(4096, np.float32)
-        dev.op("synth_f32", x0.ptr, 4096, 9, 1.0)
-        x0q, x0s, y0 = dev.array(4096, np.int8), dev.array(128, np.float32), dev.array(4096, np.float32)
-        dev.op("quantize_q8", x0.ptr, x0q.ptr, x0s.ptr, 1, 4096)
-        dev.sync()
-        tilings = [(64, 1, 4), (64, 2, 4), (64, 1, 2), (64, 1, 1), (32, 1, 4), "nt"] if args.sweep else [None]
-        c0 = {}
-        for t in tilings:
-            dev.begin_capture()
-            for w in ws0:
-                if t == "nt":
-                    dev.launch("halo_gemv_q8a8nt_l64_r1_b1", (1024,), (256,),
-                               [("ptr", w.qs.ptr), ("ptr", w.d.ptr), x0q, x0s, y0, ("u32", 4096), ("u32", 4096),
-                                ("u32", w.qstride), ("u32", 4096)])
-                elif t is None:
-                    dev.op("matvec_q8a8", ctypes.byref(w.desc), x0q.ptr, x0s.ptr, y0.ptr, 1, 4096)
-                else:
-                    dev.op("matvec_q8a8_tiled", ctypes.byref(w.desc), x0q.ptr, x0s.ptr, y0.ptr, 1, 4096, *t)
-            g = dev.end_capture()
-            dev.launch_graph(g)
-            dev.sync()
-            nrep = max(1, -(-max(args.steps, 2000) // c0_copies))
-            dev.timer_start()
-            for _ in range(nrep):
-                dev.launch_graph(g)
-            ms = dev.timer_stop()
-            us = ms * 1e3 / (nrep * c0_copies)
-            c0[str(t)] = {"us_per_gemv": round(us, 3), "GBps": round(C0_BYTES / (us * 1e-6) / 1e9, 1)}
-            dev.free_graph(g)
-        log(f"[bench] C0 {c0}")
-        best = c0[str(tilings[0])]
-        traffic = None
-        prof = ROOT / "profiles" / "gemv_q8a8_c0_4096x4096.md"
-        if prof.exists():
-            for line in prof.read_text().splitlines():
-                if line.startswith("traffic_bytes_per_launch:"):
-                    traffic = int(line.split(":")[1])
-        res["roofline"] = {
-            "bound": "hbm",
-            "kernel": "halo_gemv_q8a8_l64_r1_b1 (C0 4096x4096 Q8_0 GEMV)",
-            "achieved": best["GBps"],
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(best["GBps"] / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "traffic_source": "profiles/gemv_q8a8_c0_4096x4096.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)",
-            "us_per_launch": best["us_per_gemv"],
-            "algorithmic_bytes_per_launch": C0_BYTES,
-        }
-        if args.sweep:
-            res["c0_tilings"] = c0
-        return res
-
-
-def cpu_baseline(budget_s: float):
-    """The reference's cpu::MatVec (fp32 activations, dequantize-row, double accumulate, row split over
-    std::thread::hardware_concurrency() threads) over the three C1 projections."""
+    """C0, the headline: exactly args.steps GEMVs timed (after args.warmup untimed), weights rotated over copies."""
+    c0_copies = max(2, -(-MIN_ROTATION_BYTES // q8_bytes(4096, 4096)))
+    ws0 = [H.Q8Weights(dev, 4096, 4096).synth(dev, seed=50000 + i) for i in range(c0_copies)]
+    x0 = dev.array(4096, np.float32)
+    dev.op("synth_f32", x0.ptr, 4096, 9, 1.0)
+    x0q, x0s, y0 = dev.array(4096, np.int8), dev.array(128, np.float32), dev.array(4096, np.float32)
+    dev.op("quantize_q8", x0.ptr, x0q.ptr, x0s.ptr, 1, 4096)
+    dev.sync()
+    # correctness spot check of copy 0 against the oracle before timing anything
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle_py as O
 
-    rng = np.random.default_rng(0)
-    mats = []
-    for r, c in C1_SHAPES:
-        qs, d = O.synth_q8(rng, r, c)
-        raw = np.zeros(r * (c // 32) * 34, np.uint8)
-        O.oracle().or_pack_q8_0(qs, d, raw, r, c, c)
-        mats.append((raw, qs, d, r, c))
-    x = {2048: rng.normal(0, 1, 2048).astype(np.float32), 4096: rng.normal(0, 1, 4096).astype(np.float32)}
-    if O.has_ref():
-        R = O.ref()
-        kind, threads = "reference", int(R.ref_hw_threads())
+    dev.op("matvec_q8a8", ctypes.byref(ws0[0].desc), x0q.ptr, x0s.ptr, y0.ptr, 1, 4096)
+    qs, d = ws0[0].host()
+    want, mag = O.gemv_q8a8(qs, d, *O.quantize(x0.download()))
+    assert np.all(np.abs(y0.download() - want) <= 1e-5 * mag + 1e-6), "bench spot check failed"
 
-        def one():
-            for raw, qs, d, r, c in mats:
-                y = np.empty(r, np.float32)
-                R.ref_matvec_q8_0(raw, r, c, x[c], y)
-    else:
-        o = O.oracle()
-        kind, threads = "port", os.cpu_count() or 1
+    def gemv(w, t):
+        if t == "nt":
+            dev.launch("halo_gemv_q8a8nt_l64_r1_b1", (1024,), (256,),
+                       [("ptr", w.qs.ptr), ("ptr", w.d.ptr), x0q, x0s, y0, ("u32", 4096), ("u32", 4096),
+                        ("u32", w.qstride), ("u32", 4096)])
+        elif t is None:
+            dev.op("matvec_q8a8", ctypes.byref(w.desc), x0q.ptr, x0s.ptr, y0.ptr, 1, 4096)
+        else:
+            dev.op("matvec_q8a8_tiled", ctypes.byref(w.desc), x0q.ptr, x0s.ptr, y0.ptr, 1, 4096, *t)
 
-        def one():
-            for raw, qs, d, r, c in mats:
-                y = np.empty(r, np.float32)
-                o.or_matvec_q8_0_f32x(qs, d, r, c, c, x[c], y, threads)
-    one()
+    def graph(t, n):  # n GEMVs cycling through the copies
+        dev.begin_capture()
+        for i in range(n):
+            gemv(ws0[i % c0_copies], t)
+        return dev.end_capture()
+
+    def run_exact(t, steps):  # exactly `steps` GEMVs: whole rotations, then the remainder
+        full, rest = divmod(steps, c0_copies)
+        gf = graph(t, c0_copies) if full else None
+        gr = graph(t, rest) if rest else None
+        return gf, full, gr
+
+    if args.eager:  # kernel durations under a profiler
+        for i in range(args.steps):
+            gemv(ws0[i % c0_copies], None)
+        dev.sync()
+        res.update(value=0.0, steps_timed=args.steps, ms_per_step=0.0, roofline=None)
+        return res
+    tilings = [None] + ([(64, 2, 4), (64, 1, 2), (64, 1, 1), (32, 1, 4), "nt"] if args.sweep else [])
+    c0 = {}
+    for t in tilings:
+        steps = args.steps if t is None else 2000
+        gw, fw, rw = run_exact(t, args.warmup) if t is None and args.warmup else (None, 0, None)
+        for _ in range(fw):
+            dev.launch_graph(gw)
+        if rw is not None:
+            dev.launch_graph(rw)
+        gf, full, gr = run_exact(t, steps)
+        dev.sync()
+        dev.timer_start()
+        for _ in range(full):
+            dev.launch_graph(gf)
+        if gr is not None:
+            dev.launch_graph(gr)
+        ms = dev.timer_stop()
+        dev.sync()
+        for g_ in (gw, rw, gf, gr):
+            if g_ is not None:
+                dev.free_graph(g_)
+        us = ms * 1e3 / steps
+        c0[str(t)] = {"us_per_gemv": round(us, 4), "GBps": round(C0_BYTES / (us * 1e-6) / 1e9, 1), "steps": steps}
+        if t is None:
+            res.update(value=C0_BYTES / (us * 1e-6) / 1e9, steps_timed=steps, ms_per_step=us * 1e-3)
+    log(f"[bench] C0 {c0}")
+    best = c0["None"]
+    traffic = None
+    prof = ROOT / "profiles" / "gemv_q8a8_c0_4096x4096.md"
+    if prof.exists():
+        for line in prof.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                traffic = int(line.split(":")[1])
+    res["roofline"] = {
+        "bound": "hbm",
+        "kernel": "halo_gemv_q8a8_l64_r1_b1 (C0 4096x4096 Q8_0 GEMV)",
+        "achieved": best["GBps"],
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(best["GBps"] / HBM_PEAK_GBS, 4),
+        "traffic": traffic,
+        "traffic_source": "profiles/gemv_q8a8_c0_4096x4096.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)",
+        "us_per_launch": best["us_per_gemv"],
+        "algorithmic_bytes_per_launch": C0_BYTES,
+        "timing": "HIP events on the device stream around exactly `steps` back-to-back launches",
+    }
+    if args.sweep:
+        res["c0_tilings"] = c0
+    return res
+
+
+def _median_time(fn, budget_s, min_reps=10, max_reps=2000):
+    fn()  # warm-up
     times = []
     t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 10:
+    while (time.perf_counter() < t_end or len(times) < min_reps) and len(times) < max_reps:
         t0 = time.perf_counter()
-        one()
+        fn()
         times.append(time.perf_counter() - t0)
-        if len(times) >= 2000:
-            break
-    med = float(np.median(times))
+    return float(np.median(times)), len(times)
+
+
+def cpu_baseline(budget_s: float):
+    """The reference's CPU path on the host cores, on bounded samples of the same workloads (median of >= 10 runs
+    after a warm-up): the headline C0 GEMV through the reference's cpu::MatVec (built from its sources into
+    oracle/_ref; all hardware threads, as MatVec splits rows), and legs: C0 on one thread (the port, bitwise equal to
+    cpu::MatVec), the C1 projections, the C2 MoE layer at T=1 (cpu::MatVec router, RouteTopK, 10 routed experts and
+    the shared expert through cpu::MatVec) and the C3 DeltaNet recurrence for S=4 sessions (the port's delta rule,
+    one thread). GB/s against the same algorithmic bytes as the GPU figures."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle_py as O
+
+    o = O.oracle()
+    has_ref = O.has_ref()
+    R = O.ref() if has_ref else None
+    hw = int(R.ref_hw_threads()) if has_ref else (os.cpu_count() or 1)
+    rng = np.random.default_rng(0)
+
+    def raw_q8(r, c, sigma=0.02):
+        qs, d = O.synth_q8(rng, r, c, sigma)
+        raw = np.zeros(r * (c // 32) * 34, np.uint8)
+        o.or_pack_q8_0(qs, d, raw, r, c, c)
+        return raw, qs, d
+
+    def matvec(raw, qs, d, r, c, x, y, threads=None):
+        if has_ref and threads is None:
+            R.ref_matvec_q8_0(raw, r, c, x, y)
+        else:
+            o.or_matvec_q8_0_f32x(qs, d, r, c, c, x, y, threads or hw)
+
+    legs = {}
+    share = budget_s / 5
+    # C0, all threads (the headline) and one thread
+    raw, qs, d = raw_q8(4096, 4096)
+    x = rng.normal(0, 1, 4096).astype(np.float32)
+    y = np.empty(4096, np.float32)
+    med, n = _median_time(lambda: matvec(raw, qs, d, 4096, 4096, x, y), share)
+    head = {"value": round(C0_BYTES / med / 1e9, 2), "unit": "GB/s", "cores": hw,
+            "kind": "reference" if has_ref else "port",
+            "sample": f"C0 4096x4096 Q8_0 GEMV (fp32 x), median of {n} GEMVs ({med * 1e3:.3f} ms each), {hw} threads"}
+    med1, n1 = _median_time(lambda: matvec(raw, qs, d, 4096, 4096, x, y, threads=1), share, max_reps=200)
+    legs["c0_1_thread"] = {"GBps": round(C0_BYTES / med1 / 1e9, 2), "ms": round(med1 * 1e3, 3), "cores": 1,
+                           "kind": "port (bitwise = cpu::MatVec)", "reps": n1}
+    # C1 pass
+    mats = [(raw_q8(r, c), r, c) for r, c in C1_SHAPES]
+    xs = {2048: rng.normal(0, 1, 2048).astype(np.float32), 4096: rng.normal(0, 1, 4096).astype(np.float32)}
+
+    def c1():
+        for (rw, q_, d_), r, c in mats:
+            matvec(rw, q_, d_, r, c, xs[c], np.empty(r, np.float32))
+    med, n = _median_time(c1, share)
+    legs["c1_pass_m1"] = {"GBps": round(c1_pass_bytes(1) / med / 1e9, 2), "ms": round(med * 1e3, 3), "cores": hw,
+                          "kind": head["kind"], "reps": n}
+    # C2 at T = 1: router + top-10 + 10 routed experts + shared expert (experts built for the ids the token routes
+    # to; the timed work is the whole layer)
+    E, Hd, F, k = 512, 2048, 512, 10
+    router = rng.normal(0, 0.02, (E, Hd)).astype(np.float32)
+    sgate = rng.normal(0, 0.02, Hd).astype(np.float32)
+    xt = rng.normal(0, 1, Hd).astype(np.float32)
+    logits = np.empty(E, np.float32)
+    (R.ref_matvec_f32 if has_ref else o.or_matvec_f32)(router, E, Hd, xt, logits)
+    ids, wts = np.zeros(k, np.uint32), np.zeros(k, np.float32)
+    o.or_route_topk(logits, E, k, ids, wts)
+    experts = {int(e): (raw_q8(F, Hd), raw_q8(F, Hd), raw_q8(Hd, F)) for e in ids.tolist() + [-1]}
+
+    def moe():
+        lg = np.empty(E, np.float32)
+        (R.ref_matvec_f32 if has_ref else o.or_matvec_f32)(router, E, Hd, xt, lg)
+        ii, ww = np.zeros(k, np.uint32), np.zeros(k, np.float32)
+        (R.ref_route_topk if has_ref else o.or_route_topk)(lg, E, k, ii, ww)
+        out = np.zeros(Hd, np.float32)
+        for e, wgt in list(zip(ii.tolist(), ww.tolist())) + [(-1, 1.0 / (1.0 + np.exp(-float(sgate @ xt))))]:
+            (gr, gq, gd), (ur, uq, ud), (dr, dq, dd) = experts[e]
+            g, u, dn = np.empty(F, np.float32), np.empty(F, np.float32), np.empty(Hd, np.float32)
+            matvec(gr, gq, gd, F, Hd, xt, g)
+            matvec(ur, uq, ud, F, Hd, xt, u)
+            h = (g / (1.0 + np.exp(-g)) * u).astype(np.float32)
+            matvec(dr, dq, dd, Hd, F, h, dn)
+            out += np.float32(wgt) * dn
+        return out
+    med, n = _median_time(moe, share)
+    moe_b = E * Hd * 4 + Hd * 4 + 11 * (2 * q8_bytes(F, Hd) + q8_bytes(Hd, F)) + 2 * Hd * 4
+    legs["c2_moe_t1"] = {"GBps": round(moe_b / med / 1e9, 2), "ms": round(med * 1e3, 3), "cores": hw,
+                         "kind": head["kind"], "reps": n}
+    # C3 recurrence, S = 4 sessions x 32 value heads (16 key heads), d = 128, one thread
+    S, Hv, Hk, D = 4, 32, 16, 128
+    st = rng.normal(0, 0.05, (S, Hv, D, D)).astype(np.float32)
+    q3 = rng.normal(0, 0.09, (S, Hk, D)).astype(np.float32)
+    k3 = rng.normal(0, 0.09, (S, Hk, D)).astype(np.float32)
+    v3 = rng.normal(0, 1, (S, Hv, D)).astype(np.float32)
+    oh = np.empty(D, np.float32)
+
+    def gdn():
+        for s_ in range(S):
+            for h in range(Hv):
+                o.or_gdn_step(st[s_, h], D, q3[s_, h % Hk], k3[s_, h % Hk], v3[s_, h], -0.1, 0.5, oh)
+    med, n = _median_time(gdn, share, max_reps=500)
+    gdn_b = 2 * S * Hv * D * D * 4 + S * (2 * Hk + 2 * Hv) * D * 4 + 2 * S * Hv * 4
+    legs["c3_decode_s4"] = {"GBps": round(gdn_b / med / 1e9, 2), "ms": round(med * 1e3, 3), "cores": 1,
+                            "kind": "port (the delta rule of ReferenceModel::LinearAttention)", "reps": n}
     try:
         aff = len(os.sched_getaffinity(0))
     except AttributeError:
         aff = os.cpu_count()
-    return {
-        "value": round(c1_pass_bytes(1) / med / 1e9, 2),
-        "unit": "GB/s",
-        "cores": threads,
-        "kind": kind,
-        "sample": (f"C1 M=1 pass (3 Q8_0 projections, fp32 x), median of {len(times)} passes "
-                   f"({med * 1e3:.2f} ms/pass), {threads} threads on {aff} available cpus"),
-    }
+    head["available_cpus"] = aff
+    head["legs"] = legs
+    return head
 
 
 def main():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=4000)
-    p.add_argument("--warmup", type=int, default=400)
+    p.add_argument("--steps", type=int, default=6800)
+    p.add_argument("--warmup", type=int, default=680)
     p.add_argument("--sweep", action="store_true", help="also time alternative C0 GEMV tilings")
-    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--cpu-seconds", type=float, default=20.0)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--quick", action="store_true", help="only the C1 value and the C0 roofline")
+    p.add_argument("--quick", action="store_true", help="only the C0 headline and its roofline")
     p.add_argument("--eager", action="store_true", help="launch without graphs (for profiling kernel durations)")
     p.add_argument("--mode", choices=["all", "c0", "membw", "moe", "gdn", "c4", "pmc", "attn", "proj", "prefill",
                                        "sample"],
@@ -961,18 +1068,17 @@ def main():
         "n_gpus": 1,
         "steps": res["steps_timed"],
         "warmup": args.warmup,
-        "ms_per_step": round(res["ms_per_step"], 5),
+        "ms_per_step": round(res["ms_per_step"], 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic (device-seeded Q8_0 weights, N(0,1) activations)",
-        "config": {"workload": "C1 Q8_0 projections 2048->4096, 2048->512, 4096->2048 at M=1 (batch 1)",
-                   "bytes_per_step": c1_pass_bytes(1), "rotated_weight_copies_MiB": 600},
+        "config": {"workload": "C0: one Q8_0 GEMV 4096x4096, x quantized to Q8_0, batch 1 (BASELINE configs[0])",
+                   "bytes_per_step": C0_BYTES, "rotated_weight_copies_MiB": 600},
         "roofline": res["roofline"],
-        "c1_sweep": res["c1_sweep"],
     }
-    for k in ("moe", "gdn", "c4", "sample"):
+    for k in ("c1", "moe", "gdn", "c4", "sample"):
         if k in res:
             line[k] = res[k]
     if "c4" in res:

@@ -788,34 +788,56 @@ def run_sample(args, dev, H, res):
 
 
 def run_membw(args, dev, H, res):
-    """Streaming-read yardstick: one launch reads one buffer of the given size; buffers rotate over >= 600 MB."""
+    """Streaming-read yardstick: halo_stream_read, one launch per buffer of the given size (buffers rotate over
+    >= 600 MB so reads come from HBM), over launch grids; the best grid per size, and a least-squares fit
+    time = intercept + bytes / bandwidth over the sizes."""
     out = {}
     sink = dev.array(4, np.int32)
-    pool = dev.array(MIN_ROTATION_BYTES + (256 << 20), np.uint8)  # one allocation, carved by offset
-    for size in (17858560, 4 << 20, 64 << 20, 256 << 20):
+    sizes = [4 << 20, 8 << 20, 16 << 20, C0_BYTES, 32 << 20, 64 << 20, 128 << 20, 256 << 20, 512 << 20]
+    pool = dev.array(2 * (512 << 20) + (64 << 20), np.uint8)  # one allocation, carved by offset
+    best = {}
+    for size in sizes:
         n16 = size // 16
         nbuf = max(2, -(-MIN_ROTATION_BYTES // size))
         step = (size + 4095) // 4096 * 4096
+        nbuf = min(nbuf, pool.nbytes // step)
         ptrs = [pool.ptr + i * step for i in range(nbuf)]
-        for grid in (1024, 2048, 4096, 8192):
+        for grid in (1024, 2048, 4096, 8192, 16384):
             if grid * 256 > n16:
                 continue
-            log(f"[bench] membw size {size} grid {grid} buffers {nbuf}")
+            if args.eager:  # per-launch durations under a profiler: 50 direct launches per (size, grid)
+                for i in range(50):
+                    dev.launch("halo_stream_read", (grid,), (256,), [("ptr", ptrs[i % nbuf]), ("u64", n16), sink])
+                dev.sync()
+                continue
             dev.begin_capture()
             for p_ in ptrs:
                 dev.launch("halo_stream_read", (grid,), (256,), [("ptr", p_), ("u64", n16), sink])
             g = dev.end_capture()
             dev.launch_graph(g)
             dev.sync()
-            nrep = max(1, 2000 // nbuf)
+            nrep = max(2, 2000 // nbuf)
             dev.timer_start()
             for _ in range(nrep):
                 dev.launch_graph(g)
             ms = dev.timer_stop()
             us = ms * 1e3 / (nrep * nbuf)
             out[f"{size}B_grid{grid}"] = {"us": round(us, 3), "GBps": round(size / us / 1e3, 1)}
+            if size not in best or us < best[size][0]:
+                best[size] = (us, grid)
             dev.free_graph(g)
-    log(f"[bench] membw {out}")
+    if args.eager:
+        res["membw"] = None
+        res["roofline"] = None
+        return res
+    xs = np.array(sizes, np.float64)
+    ts = np.array([best[z][0] for z in sizes])
+    A = np.stack([np.ones_like(xs), xs], 1)
+    (icpt, slope), *_ = np.linalg.lstsq(A, ts, rcond=None)
+    out["best"] = {str(z): {"us": round(best[z][0], 3), "grid": best[z][1], "GBps": round(z / best[z][0] / 1e3, 1)}
+                   for z in sizes}
+    out["fit"] = {"intercept_us": round(float(icpt), 3), "GBps_asymptotic": round(1e-3 / float(slope), 1)}
+    log(f"[bench] membw best {out['best']} fit {out['fit']}")
     res["membw"] = out
     res["roofline"] = None
     return res

@@ -48,6 +48,7 @@ size_t halo_op_attn_decode_workspace_bytes(const halo_paged_kv* kv, uint32_t Hq)
 int halo_op_attn_decode_q8(halo_engine* eng, const halo_paged_kv* kv, const float* q, const float* gate, float* o,
                            int8_t* oq, float* os, uint32_t Hq, void* ws, size_t ws_bytes, char* err,
                            size_t errlen) {
+  if (RequirePtrs(err, errlen, "attn_decode_q8", {{"kv", kv}, {"q", q}, {"ws", ws}}) != 0) return -1;
   if (Check(kv, Hq, err, errlen) != 0) return -1;
   const std::size_t need = halo_op_attn_decode_workspace_bytes(kv, Hq);
   if (ws == nullptr || ws_bytes < need) return SetErr(err, errlen, "attn: workspace %zu < %zu", ws_bytes, need), -1;
@@ -75,6 +76,7 @@ int halo_op_attn_decode_q8(halo_engine* eng, const halo_paged_kv* kv, const floa
 
 int halo_op_attn_decode(halo_engine* eng, const halo_paged_kv* kv, const float* q, const float* gate, float* o,
                         uint32_t Hq, void* ws, size_t ws_bytes, char* err, size_t errlen) {
+  if (RequirePtrs(err, errlen, "attn_decode", {{"kv", kv}, {"q", q}, {"o", o}, {"ws", ws}}) != 0) return -1;
   return halo_op_attn_decode_q8(eng, kv, q, gate, o, nullptr, nullptr, Hq, ws, ws_bytes, err, errlen);
 }
 
@@ -88,6 +90,7 @@ size_t halo_op_attn_prefill_workspace_bytes(const halo_prefill_segment* segs, ui
 int halo_op_attn_prefill(halo_engine* eng, const halo_paged_kv* kv, const halo_prefill_segment* segs, uint32_t nseg,
                          const float* q, const float* gate, float* o, int8_t* oq, float* os, uint32_t Hq, void* ws,
                          size_t ws_bytes, char* err, size_t errlen) {
+  if (RequirePtrs(err, errlen, "attn_prefill", {{"kv", kv}, {"segs", segs}, {"q", q}, {"ws", ws}}) != 0) return -1;
   if (kv == nullptr || kv->k_pool == nullptr || kv->v_pool == nullptr || kv->pages == nullptr)
     return SetErr(err, errlen, "attn prefill: missing kv buffers"), -1;
   if (kv->head_dim != 256 || kv->kv_heads == 0 || Hq != 8 * kv->kv_heads)
@@ -118,6 +121,7 @@ int halo_op_attn_prefill(halo_engine* eng, const halo_paged_kv* kv, const halo_p
 
 int halo_op_kv_append(halo_engine* eng, const halo_paged_kv* kv, const float* k, const float* v, char* err,
                       size_t errlen) {
+  if (RequirePtrs(err, errlen, "kv_append", {{"kv", kv}, {"k", k}, {"v", v}}) != 0) return -1;
   if (kv == nullptr || kv->head_dim != 256) return SetErr(err, errlen, "kv append: head dim 256 only"), -1;
   const halo_arg a[] = {Ptr(k), Ptr(v), Ptr(kv->k_pool), Ptr(kv->v_pool), Ptr(kv->pages), Ptr(kv->nkv),
                         U32(kv->kv_heads), U32(kv->max_pages)};

@@ -104,6 +104,7 @@ int halo_engine_launch(halo_engine* eng, const char* kernel, halo_dim3 grid, hal
 
 int halo_op_repack_q8_0(halo_engine* eng, const void* raw, int8_t* qs, uint16_t* d, uint32_t rows, uint32_t cols,
                         uint32_t qstride, char* err, size_t errlen) {
+  if (RequirePtrs(err, errlen, "repack_q8_0", {{"raw", raw}, {"qs", qs}, {"d", d}}) != 0) return -1;
   if (cols % 32 != 0 || qstride < cols || qstride % 16 != 0)
     return SetErr(err, errlen, "repack: cols %u must be a multiple of 32, qstride %u >= cols and a multiple of 16",
                   cols, qstride),
@@ -116,6 +117,7 @@ int halo_op_repack_q8_0(halo_engine* eng, const void* raw, int8_t* qs, uint16_t*
 
 int halo_op_quantize_q8(halo_engine* eng, const float* x, int8_t* xq, float* xs, uint32_t tokens, uint32_t cols,
                         char* err, size_t errlen) {
+  if (RequirePtrs(err, errlen, "quantize_q8", {{"x", x}, {"xq", xq}, {"xs", xs}}) != 0) return -1;
   if (cols % 32 != 0 || tokens == 0) return SetErr(err, errlen, "quantize: cols %% 32 != 0 or no tokens"), -1;
   const halo_arg a[] = {Ptr(x), Ptr(xq), Ptr(xs), U32(cols)};
   return Launch(eng, "halo_quantize_q8_rows", D3(tokens), D3(256), a, err, errlen);
@@ -131,6 +133,7 @@ static int CheckMatrix(const halo_q8_matrix* w, char* err, size_t errlen) {
 int halo_op_matvec_q8a8_tiled(halo_engine* eng, const halo_q8_matrix* w, const int8_t* xq, const float* xs,
                               float* y, uint32_t m, uint32_t ystride, uint32_t lpr, uint32_t rpl, uint32_t waves,
                               char* err, size_t errlen) {
+  if (RequirePtrs(err, errlen, "matvec_q8a8_tiled", {{"xq", xq}, {"xs", xs}, {"y", y}}) != 0) return -1;
   if (CheckMatrix(w, err, errlen) != 0) return -1;
   if (!(m == 1 || m == 2 || m == 4 || m == 8)) return SetErr(err, errlen, "tiled GEMV takes m in {1,2,4,8}"), -1;
   if (!(lpr == 16 || lpr == 32 || lpr == 64) || !(rpl == 1 || rpl == 2 || rpl == 4) || waves < 1 || waves > 4)
@@ -146,6 +149,7 @@ int halo_op_matvec_q8a8_tiled(halo_engine* eng, const halo_q8_matrix* w, const i
 
 int halo_op_matvec_q8a8(halo_engine* eng, const halo_q8_matrix* w, const int8_t* xq, const float* xs, float* y,
                         uint32_t m, uint32_t ystride, char* err, size_t errlen) {
+  if (RequirePtrs(err, errlen, "matvec_q8a8", {{"xq", xq}, {"xs", xs}, {"y", y}}) != 0) return -1;
   if (CheckMatrix(w, err, errlen) != 0) return -1;
   if (m == 0) return SetErr(err, errlen, "m == 0"), -1;
   if (m > 1 && ystride < w->rows) return SetErr(err, errlen, "ystride %u < rows %u", ystride, w->rows), -1;
@@ -198,6 +202,7 @@ int halo_op_matvec_q8a8(halo_engine* eng, const halo_q8_matrix* w, const int8_t*
 
 int halo_op_matvec_q8_f32x(halo_engine* eng, const halo_q8_matrix* w, const float* x, float* y, char* err,
                            size_t errlen) {
+  if (RequirePtrs(err, errlen, "matvec_q8_f32x", {{"x", x}, {"y", y}}) != 0) return -1;
   if (CheckMatrix(w, err, errlen) != 0) return -1;
   const bool r4 = w->rows >= 2048;
   const halo_arg a[] = {Ptr(w->qs), Ptr(w->d), Ptr(x), Ptr(y), U32(w->rows), U32(w->cols), U32(w->qstride)};
@@ -207,6 +212,7 @@ int halo_op_matvec_q8_f32x(halo_engine* eng, const halo_q8_matrix* w, const floa
 
 int halo_op_q8_half_dots(halo_engine* eng, const halo_q8_matrix* w, const int8_t* xq, int32_t* isum, char* err,
                          size_t errlen) {
+  if (RequirePtrs(err, errlen, "q8_half_dots", {{"xq", xq}, {"isum", isum}}) != 0) return -1;
   if (CheckMatrix(w, err, errlen) != 0) return -1;
   const std::uint64_t n = static_cast<std::uint64_t>(w->rows) * (w->cols / 16);
   const halo_arg a[] = {Ptr(w->qs), Ptr(xq), Ptr(isum), U32(w->rows), U32(w->cols), U32(w->qstride)};
@@ -216,6 +222,7 @@ int halo_op_q8_half_dots(halo_engine* eng, const halo_q8_matrix* w, const int8_t
 
 int halo_op_synth_q8(halo_engine* eng, int8_t* qs, uint16_t* d, uint32_t rows, uint32_t cols, uint32_t qstride,
                      uint64_t seed, float sigma, char* err, size_t errlen) {
+  if (RequirePtrs(err, errlen, "synth_q8", {{"qs", qs}, {"d", d}}) != 0) return -1;
   if (cols % 32 != 0 || qstride < cols || qstride % 16 != 0) return SetErr(err, errlen, "synth: bad shape"), -1;
   const std::uint64_t n = static_cast<std::uint64_t>(rows) * (cols / 16);
   const halo_arg a[] = {Ptr(qs), Ptr(d), U32(rows), U32(cols), U32(qstride), Val(seed), Val(sigma)};
@@ -224,6 +231,7 @@ int halo_op_synth_q8(halo_engine* eng, int8_t* qs, uint16_t* d, uint32_t rows, u
 }
 
 int halo_op_synth_f32(halo_engine* eng, float* x, uint64_t n, uint64_t seed, float sigma, char* err, size_t errlen) {
+  if (RequirePtrs(err, errlen, "synth_f32", {{"x", x}}) != 0) return -1;
   const halo_arg a[] = {Ptr(x), Val(n), Val(seed), Val(sigma)};
   return Launch(eng, "halo_synth_f32", D3(static_cast<std::uint32_t>(std::min<std::uint64_t>(CeilDiv(n, 256), 65536))),
                 D3(256), a, err, errlen);

@@ -5,6 +5,8 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
+#include <utility>
 #include <string>
 #include <type_traits>
 #include <unordered_map>
@@ -28,6 +30,15 @@ inline void SetErr(char* err, std::size_t errlen, const char* fmt, ...) {
   va_start(ap, fmt);
   std::vsnprintf(err, errlen, fmt, ap);
   va_end(ap);
+}
+
+// Refuses null required device pointers of an operator: the kernels dereference them unconditionally, and a null
+// read faults the GPU. `ptrs` pairs each required argument's name with its value.
+inline int RequirePtrs(char* err, std::size_t errlen, const char* op,
+                       std::initializer_list<std::pair<const char*, const void*>> ptrs) {
+  for (const auto& np : ptrs)
+    if (np.second == nullptr) return SetErr(err, errlen, "%s: %s is null", op, np.first), -1;
+  return 0;
 }
 
 // Kernel argument builders (the reference's Arg::Buf / Arg::Val, src/rt/device.hpp:35-59).

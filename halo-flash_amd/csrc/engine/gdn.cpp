@@ -9,6 +9,7 @@ extern "C" {
 int halo_op_gdn_decode(halo_engine* eng, float* state, const float* q, const float* k, const float* v,
                        const float* g, const float* beta, float* o, uint32_t S, uint32_t Hv, uint32_t Hk,
                        uint32_t d, char* err, size_t errlen) {
+  if (RequirePtrs(err, errlen, "gdn_decode", {{"state", state}, {"q", q}, {"k", k}, {"v", v}, {"g", g}, {"beta", beta}, {"o", o}}) != 0) return -1;
   if (d != 128) return SetErr(err, errlen, "gdn: head dim %u unsupported (128)", d), -1;
   if (S == 0 || Hv == 0 || Hk == 0 || Hv % Hk != 0)
     return SetErr(err, errlen, "gdn: %u sessions, %u value heads, %u key heads", S, Hv, Hk), -1;
@@ -65,6 +66,7 @@ int halo_op_gdn_prefill(halo_engine* eng, const uint16_t* q, const uint16_t* k, 
                         const float* beta, const uint32_t* chunks, const uint32_t* seqs, uint32_t n_chunks,
                         uint32_t n_seq, float* state, float* o, uint32_t Hv, uint32_t Hk, uint32_t d, void* ws,
                         size_t ws_bytes, char* err, size_t errlen) {
+  if (RequirePtrs(err, errlen, "gdn_prefill", {{"q", q}, {"k", k}, {"v", v}, {"g", g}, {"beta", beta}, {"chunks", chunks}, {"seqs", seqs}, {"state", state}, {"o", o}, {"ws", ws}}) != 0) return -1;
   return GdnPrefill(eng, false, q, k, v, g, beta, chunks, seqs, n_chunks, n_seq, state, o, Hv, Hk, d, ws, ws_bytes,
                     err, errlen);
 }
@@ -73,6 +75,7 @@ int halo_op_gdn_prefill_f32(halo_engine* eng, const float* q, const float* k, co
                             const float* beta, const uint32_t* chunks, const uint32_t* seqs, uint32_t n_chunks,
                             uint32_t n_seq, float* state, float* o, uint32_t Hv, uint32_t Hk, uint32_t d, void* ws,
                             size_t ws_bytes, char* err, size_t errlen) {
+  if (RequirePtrs(err, errlen, "gdn_prefill_f32", {{"q", q}, {"k", k}, {"v", v}, {"g", g}, {"beta", beta}, {"chunks", chunks}, {"seqs", seqs}, {"state", state}, {"o", o}, {"ws", ws}}) != 0) return -1;
   return GdnPrefill(eng, true, q, k, v, g, beta, chunks, seqs, n_chunks, n_seq, state, o, Hv, Hk, d, ws, ws_bytes,
                     err, errlen);
 }

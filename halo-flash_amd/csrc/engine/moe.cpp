@@ -130,11 +130,13 @@ extern "C" {
 
 int halo_op_moe_decode(halo_engine* eng, const halo_moe_weights* w, const float* x, float* out, uint32_t T, void* ws,
                        size_t ws_bytes, char* err, size_t errlen) {
+  if (RequirePtrs(err, errlen, "moe_decode", {{"x", x}, {"out", out}, {"ws", ws}}) != 0) return -1;
   return MoeDecode(eng, w, x, nullptr, out, T, ws, ws_bytes, err, errlen);
 }
 
 int halo_op_moe_decode_norm(halo_engine* eng, const halo_moe_weights* w, const halo_proj_input* in, float* out,
                             uint32_t T, void* ws, size_t ws_bytes, char* err, size_t errlen) {
+  if (RequirePtrs(err, errlen, "moe_decode_norm", {{"in", in}, {"out", out}, {"ws", ws}}) != 0) return -1;
   if (in == nullptr) return SetErr(err, errlen, "moe: no input"), -1;
   return MoeDecode(eng, w, nullptr, in, out, T, ws, ws_bytes, err, errlen);
 }
@@ -210,6 +212,7 @@ size_t halo_op_moe_prefill_workspace_bytes(const halo_moe_weights* w, uint32_t T
 
 int halo_op_moe_prefill(halo_engine* eng, const halo_moe_weights* w, const float* x, float* out, uint32_t T, void* ws,
                         size_t ws_bytes, char* err, size_t errlen) {
+  if (RequirePtrs(err, errlen, "moe_prefill", {{"x", x}, {"out", out}, {"ws", ws}}) != 0) return -1;
   PrefillViews v;
   if (PrefillLayout(w, T, ws, &v, err, errlen) != 0) return -1;
   if (ws == nullptr || ws_bytes < v.bytes)

@@ -12,6 +12,7 @@ size_t halo_op_sample_workspace_bytes(uint32_t rows, uint32_t vocab) {
 int halo_op_sample(halo_engine* eng, const float* logits, uint32_t rows, uint64_t row_stride, uint32_t vocab,
                    const HaloSampleParams* params, const HaloPenalty* penalties, uint32_t pen_stride,
                    HaloSampleOut* out, void* ws, size_t ws_bytes, char* err, size_t errlen) {
+  if (RequirePtrs(err, errlen, "sample", {{"logits", logits}, {"params", params}, {"out", out}, {"ws", ws}}) != 0) return -1;
   if (rows == 0 || rows > 65535 || vocab == 0 || vocab > HALO_SAMPLE_MAX_VOCAB)
     return SetErr(err, errlen, "sample: rows %u (1..65535), vocab %u (1..%u)", rows, vocab, HALO_SAMPLE_MAX_VOCAB),
            -1;

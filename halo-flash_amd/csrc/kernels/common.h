@@ -248,10 +248,15 @@ __device__ __forceinline__ void RmsNormRow8(Row8<KC>& r, const float* __restrict
   for (int k = 0; k < KC; ++k) {
     const std::uint32_t c = threadIdx.x + 256u * k;
     if (c < n / 8) {
-      const float4 a = reinterpret_cast<const float4*>(w)[2 * c], b = reinterpret_cast<const float4*>(w)[2 * c + 1];
-      const float wv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      if (w != nullptr) {  // kernel-uniform; a null w means unit weights
+        const float4 a = reinterpret_cast<const float4*>(w)[2 * c], b = reinterpret_cast<const float4*>(w)[2 * c + 1];
+        const float wv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) r.v[k][e] = r.v[k][e] * scale * wv[e];
+        for (int e = 0; e < 8; ++e) r.v[k][e] = r.v[k][e] * scale * wv[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r.v[k][e] = r.v[k][e] * scale;
+      }
     }
   }
 }

@@ -8,3 +8,12 @@
 #include "moe_prefill.hip"
 #include "sample.hip"
 #include "ref_named.hip"
+
+// Module-scope variable read and written through halo_read_global / halo_write_global (the reference's
+// Device::ReadGlobal / WriteGlobal): the code object's identity {format version, wave size, target, spare}.
+extern "C" __device__ std::uint32_t halo_code_object_info[4] = {1u, 64u, 950u, 0u};
+
+// out[0..3] = halo_code_object_info as a kernel sees it. grid (1), block 64.
+extern "C" __global__ void halo_code_object_info_copy(std::uint32_t* out) {
+  if (threadIdx.x < 4) out[threadIdx.x] = halo_code_object_info[threadIdx.x];
+}

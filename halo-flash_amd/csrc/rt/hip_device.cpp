@@ -8,7 +8,10 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <chrono>
 #include <cstdarg>
+#include <thread>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -31,6 +34,14 @@ struct halo_device {
   };
   std::vector<Timed> timed;
   hipEvent_t t0 = nullptr, t1 = nullptr;
+  // page mapping (halo_page_bytes ... halo_unmap_page): 0 when the device has no virtual memory management
+  std::size_t page_bytes = 0;
+  hipMemAllocationProp prop{};
+  // A mapping change is followed by kVmmSettle before the next launch or copy: the reference measured its GPU's
+  // address translation lagging hipMemMap / hipMemUnmap by tens of microseconds with no HIP synchronization ordering
+  // it (src/rt/hip_device.cpp:349-356); the same bounded wait here keeps a kernel from touching a page too early.
+  std::chrono::steady_clock::time_point vmm_changed{};
+  bool vmm_pending = false;
 };
 
 namespace {
@@ -50,9 +61,29 @@ bool Ok(hipError_t e, const char* what, char* err, std::size_t errlen) {
 }
 
 bool NotCapturing(halo_device* dev, const char* what, char* err, std::size_t errlen) {
+  if (dev == nullptr) {
+    SetErr(err, errlen, "%s: null device", what);
+    return false;
+  }
   if (!dev->capturing) return true;
   SetErr(err, errlen, "%s is not capturable", what);
   return false;
+}
+
+constexpr std::size_t kPageTarget = std::size_t{2} << 20;  // mapping granularity (the reference's 2 MB pages)
+constexpr auto kVmmSettle = std::chrono::microseconds(1000);
+
+void VmmStamp(halo_device* dev) {
+  dev->vmm_changed = std::chrono::steady_clock::now();
+  dev->vmm_pending = true;
+}
+// Waits out the settle interval after the last mapping change (before GPU work that may touch mapped pages).
+void VmmSettle(halo_device* dev) {
+  if (!dev->vmm_pending) return;
+  dev->vmm_pending = false;
+  const auto until = dev->vmm_changed + kVmmSettle;
+  const auto now = std::chrono::steady_clock::now();
+  if (now < until) std::this_thread::sleep_for(until - now);
 }
 
 bool InRange(const halo_buffer* b, std::size_t offset, std::size_t bytes, char* err, std::size_t errlen) {
@@ -86,6 +117,17 @@ int halo_device_create(int backend, halo_device** out, char* err, size_t errlen)
     halo_device_destroy(dev);
     return -1;
   }
+  // page mapping where the device supports it (reference src/rt/hip_device.cpp:52-66)
+  int vmm = 0;
+  dev->prop.type = hipMemAllocationTypePinned;
+  dev->prop.location.type = hipMemLocationTypeDevice;
+  dev->prop.location.id = 0;
+  std::size_t gran = 0;
+  if (hipDeviceGetAttribute(&vmm, hipDeviceAttributeVirtualMemoryManagementSupported, 0) == hipSuccess && vmm &&
+      hipMemGetAllocationGranularity(&gran, &dev->prop, hipMemAllocationGranularityMinimum) == hipSuccess &&
+      gran > 0)
+    dev->page_bytes = (kPageTarget + gran - 1) / gran * gran;
+  (void)hipGetLastError();
   *out = dev;
   return 0;
 }
@@ -124,6 +166,7 @@ void halo_free(halo_device* dev, halo_buffer* buf) {
 int halo_upload(halo_device* dev, const halo_buffer* dst, size_t offset, const void* src, size_t bytes, char* err,
                 size_t errlen) {
   if (!NotCapturing(dev, "Upload", err, errlen) || !InRange(dst, offset, bytes, err, errlen)) return -1;
+  VmmSettle(dev);
   if (bytes == 0) return 0;
   if (!Ok(hipMemcpyAsync(static_cast<char*>(dst->device) + offset, src, bytes, hipMemcpyHostToDevice, dev->stream),
           "hipMemcpyAsync(HtoD)", err, errlen))
@@ -134,6 +177,7 @@ int halo_upload(halo_device* dev, const halo_buffer* dst, size_t offset, const v
 int halo_upload_async(halo_device* dev, const halo_buffer* dst, size_t offset, const void* src, size_t bytes,
                       char* err, size_t errlen) {
   if (!NotCapturing(dev, "UploadAsync", err, errlen) || !InRange(dst, offset, bytes, err, errlen)) return -1;
+  VmmSettle(dev);
   if (bytes == 0) return 0;
   return Ok(hipMemcpyAsync(static_cast<char*>(dst->device) + offset, src, bytes, hipMemcpyHostToDevice,
                            dev->stream),
@@ -145,6 +189,7 @@ int halo_upload_async(halo_device* dev, const halo_buffer* dst, size_t offset, c
 int halo_download(halo_device* dev, const halo_buffer* src, size_t offset, void* dst, size_t bytes, char* err,
                   size_t errlen) {
   if (!NotCapturing(dev, "Download", err, errlen) || !InRange(src, offset, bytes, err, errlen)) return -1;
+  VmmSettle(dev);
   if (bytes == 0) return Ok(hipStreamSynchronize(dev->stream), "hipStreamSynchronize", err, errlen) ? 0 : -1;
   if (!Ok(hipMemcpyAsync(dst, static_cast<const char*>(src->device) + offset, bytes, hipMemcpyDeviceToHost,
                          dev->stream),
@@ -156,6 +201,7 @@ int halo_download(halo_device* dev, const halo_buffer* src, size_t offset, void*
 int halo_fill(halo_device* dev, const halo_buffer* dst, uint8_t value, char* err, size_t errlen) {
   // Memset nodes are kept out of captured graphs: fills run eagerly only.
   if (!NotCapturing(dev, "Fill", err, errlen) || !InRange(dst, 0, dst ? dst->bytes : 0, err, errlen)) return -1;
+  VmmSettle(dev);
   return Ok(hipMemsetAsync(dst->device, value, dst->bytes, dev->stream), "hipMemsetAsync", err, errlen) ? 0 : -1;
 }
 
@@ -208,9 +254,15 @@ int halo_launch(halo_device* dev, halo_kernel_id kernel, halo_dim3 grid, halo_di
   std::uint64_t storage[32];
   void* params[32];
   if (nargs > 32) return SetErr(err, errlen, "too many kernel arguments"), -1;
+  if (nargs > 0 && args == nullptr) return SetErr(err, errlen, "null argument list"), -1;
+  VmmSettle(dev);
   for (std::size_t i = 0; i < nargs; ++i) {
     storage[i] = 0;
     if (args[i].kind == HALO_ARG_BUFFER) {
+      if (args[i].buffer.device == nullptr && args[i].offset != 0)
+        return SetErr(err, errlen, "argument %zu of %s: offset %zu into a null buffer", i, dev->names[kernel].c_str(),
+                      args[i].offset),
+               -1;
       void* p = args[i].buffer.device ? static_cast<char*>(args[i].buffer.device) + args[i].offset : nullptr;
       std::memcpy(&storage[i], &p, sizeof(p));
     } else {
@@ -283,7 +335,8 @@ int halo_end_capture(halo_device* dev, halo_graph* out, char* err, size_t errlen
 }
 
 int halo_launch_graph(halo_device* dev, const halo_graph* graph, char* err, size_t errlen) {
-  if (graph == nullptr || graph->exec == nullptr) return SetErr(err, errlen, "null graph"), -1;
+  if (dev == nullptr || graph == nullptr || graph->exec == nullptr) return SetErr(err, errlen, "null graph"), -1;
+  VmmSettle(dev);
   return Ok(hipGraphLaunch(static_cast<hipGraphExec_t>(graph->exec), dev->stream), "hipGraphLaunch", err, errlen)
              ? 0
              : -1;
@@ -293,6 +346,112 @@ void halo_free_graph(halo_device* dev, halo_graph* graph) {
   (void)dev;
   if (graph && graph->exec) (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph->exec));
   if (graph) graph->exec = nullptr;
+}
+
+// ---- page mapping (reference rt::Device PageBytes ... UnmapPage, src/rt/device.hpp:101-112;
+// src/rt/hip_device.cpp:127-198) ----
+size_t halo_page_bytes(halo_device* dev) { return dev ? dev->page_bytes : 0; }
+
+int halo_reserve_range(halo_device* dev, size_t bytes, halo_buffer* out, char* err, size_t errlen) {
+  if (dev == nullptr || out == nullptr) return SetErr(err, errlen, "null argument"), -1;
+  *out = halo_buffer{};
+  if (dev->page_bytes == 0) return SetErr(err, errlen, "page mapping: not supported by this device"), -1;
+  const std::size_t n = std::max<std::size_t>((bytes + dev->page_bytes - 1) / dev->page_bytes, 1) * dev->page_bytes;
+  void* p = nullptr;
+  if (!Ok(hipMemAddressReserve(&p, n, 0, nullptr, 0), "hipMemAddressReserve", err, errlen)) return -1;
+  out->device = p;
+  out->bytes = n;
+  return 0;
+}
+
+void halo_release_range(halo_device* dev, halo_buffer* range) {
+  if (range == nullptr || range->device == nullptr) return;
+  if (dev != nullptr) (void)hipStreamSynchronize(dev->stream);  // queued work may still address the range
+  (void)hipMemAddressFree(range->device, range->bytes);
+  if (dev != nullptr) VmmStamp(dev);
+  *range = halo_buffer{};
+}
+
+int halo_create_page(halo_device* dev, void** page, char* err, size_t errlen) {
+  if (dev == nullptr || page == nullptr) return SetErr(err, errlen, "null argument"), -1;
+  *page = nullptr;
+  if (dev->page_bytes == 0) return SetErr(err, errlen, "page mapping: not supported by this device"), -1;
+  hipMemGenericAllocationHandle_t h{};
+  if (!Ok(hipMemCreate(&h, dev->page_bytes, &dev->prop, 0), "hipMemCreate", err, errlen)) return -1;
+  *page = reinterpret_cast<void*>(h);
+  return 0;
+}
+
+void halo_release_page(halo_device* dev, void* page) {
+  (void)dev;
+  if (page != nullptr) (void)hipMemRelease(reinterpret_cast<hipMemGenericAllocationHandle_t>(page));
+}
+
+int halo_map_page(halo_device* dev, const halo_buffer* range, size_t offset, void* page, char* err, size_t errlen) {
+  if (dev == nullptr || range == nullptr || range->device == nullptr || page == nullptr)
+    return SetErr(err, errlen, "null argument"), -1;
+  if (!NotCapturing(dev, "MapPage", err, errlen)) return -1;
+  if (dev->page_bytes == 0 || offset % dev->page_bytes != 0 || offset + dev->page_bytes > range->bytes)
+    return SetErr(err, errlen, "map: offset %zu is not a page of a %zu-byte range", offset, range->bytes), -1;
+  void* at = static_cast<char*>(range->device) + offset;
+  hipMemAccessDesc acc{};
+  acc.location = dev->prop.location;
+  acc.flags = hipMemAccessFlagsProtReadWrite;
+  const bool ok =
+      Ok(hipMemMap(at, dev->page_bytes, 0, reinterpret_cast<hipMemGenericAllocationHandle_t>(page), 0), "hipMemMap",
+         err, errlen) &&
+      Ok(hipMemSetAccess(at, dev->page_bytes, &acc, 1), "hipMemSetAccess", err, errlen);
+  VmmStamp(dev);
+  return ok ? 0 : -1;
+}
+
+int halo_unmap_page(halo_device* dev, const halo_buffer* range, size_t offset, char* err, size_t errlen) {
+  if (dev == nullptr || range == nullptr || range->device == nullptr) return SetErr(err, errlen, "null argument"), -1;
+  if (!NotCapturing(dev, "UnmapPage", err, errlen)) return -1;
+  if (dev->page_bytes == 0 || offset % dev->page_bytes != 0 || offset + dev->page_bytes > range->bytes)
+    return SetErr(err, errlen, "unmap: offset %zu is not a page of a %zu-byte range", offset, range->bytes), -1;
+  // work queued on the stream may still read the page: drain it first
+  const bool ok = Ok(hipStreamSynchronize(dev->stream), "hipStreamSynchronize", err, errlen) &&
+                  Ok(hipMemUnmap(static_cast<char*>(range->device) + offset, dev->page_bytes), "hipMemUnmap", err,
+                     errlen);
+  VmmStamp(dev);
+  return ok ? 0 : -1;
+}
+
+// ---- module-scope variables (reference rt::Device ReadGlobal / WriteGlobal, src/rt/device.hpp:122-126;
+// src/rt/hip_device.cpp:231-249) ----
+namespace {
+int Global(halo_device* dev, const char* name, size_t bytes, void** p, char* err, size_t errlen) {
+  if (dev == nullptr || dev->module == nullptr || name == nullptr) return SetErr(err, errlen, "no module loaded"), -1;
+  hipDeviceptr_t dp = nullptr;
+  std::size_t size = 0;
+  if (!Ok(hipModuleGetGlobal(&dp, &size, dev->module, name), name, err, errlen)) return -1;
+  if (bytes > size) return SetErr(err, errlen, "%s has %zu bytes, %zu requested", name, size, bytes), -1;
+  *p = reinterpret_cast<void*>(dp);
+  return 0;
+}
+}  // namespace
+
+int halo_read_global(halo_device* dev, const char* name, void* dst, size_t bytes, char* err, size_t errlen) {
+  void* p = nullptr;
+  if (!NotCapturing(dev, "ReadGlobal", err, errlen) || Global(dev, name, bytes, &p, err, errlen) != 0) return -1;
+  VmmSettle(dev);
+  return Ok(hipMemcpyAsync(dst, p, bytes, hipMemcpyDeviceToHost, dev->stream), "hipMemcpyAsync(DtoH)", err,
+            errlen) &&
+                 Ok(hipStreamSynchronize(dev->stream), "hipStreamSynchronize", err, errlen)
+             ? 0
+             : -1;
+}
+
+int halo_write_global(halo_device* dev, const char* name, const void* src, size_t bytes, char* err, size_t errlen) {
+  void* p = nullptr;
+  if (!NotCapturing(dev, "WriteGlobal", err, errlen) || Global(dev, name, bytes, &p, err, errlen) != 0) return -1;
+  VmmSettle(dev);
+  return Ok(hipMemcpyAsync(p, src, bytes, hipMemcpyHostToDevice, dev->stream), "hipMemcpyAsync(HtoD)", err,
+            errlen) &&
+                 Ok(hipStreamSynchronize(dev->stream), "hipStreamSynchronize", err, errlen)
+             ? 0
+             : -1;
 }
 
 int halo_timer_start(halo_device* dev, char* err, size_t errlen) {

@@ -347,6 +347,15 @@ _SIGS = {
     "halo_launch_graph": (C.c_int, [_VP, C.POINTER(Graph)], True),
     "halo_free_graph": (None, [_VP, C.POINTER(Graph)], False),
     "halo_timer_start": (C.c_int, [_VP], True),
+    "halo_page_bytes": (_SZ, [_VP], False),
+    "halo_reserve_range": (C.c_int, [_VP, _SZ, C.POINTER(Buffer)], True),
+    "halo_release_range": (None, [_VP, C.POINTER(Buffer)], False),
+    "halo_create_page": (C.c_int, [_VP, C.POINTER(_VP)], True),
+    "halo_release_page": (None, [_VP, _VP], False),
+    "halo_map_page": (C.c_int, [_VP, C.POINTER(Buffer), _SZ, _VP], True),
+    "halo_unmap_page": (C.c_int, [_VP, C.POINTER(Buffer), _SZ], True),
+    "halo_read_global": (C.c_int, [_VP, C.c_char_p, _VP, _SZ], True),
+    "halo_write_global": (C.c_int, [_VP, C.c_char_p, _VP, _SZ], True),
     "halo_timer_stop": (C.c_int, [_VP, C.POINTER(_F32)], True),
     "halo_device_stream": (_VP, [_VP], False),
     "halo_profile_begin": (C.c_int, [_VP], True),

@@ -52,8 +52,8 @@
  *     halo_gdn_prefill_d128_norm(..., tokens, qk_stride, v_stride, zo_stride)   grid (v heads), block 128
  *     halo_conv_l2norm_prefill(in, state, w, out, channels, kern, l2_channels, eps)   grid (heads, T), block d
  *     halo_conv_state_advance(in, state, channels, kern, tokens)        grid ceil(channels / 256)
- *     halo_conv_l2norm_prefill8(in, state, w, out, channels, tokens, l2_channels, eps)   kern 4; grid (channels / 128,
- *       ceil(T / 8)), block 128
+ *     halo_conv_l2norm_prefill8(in, state, w, out, channels, tokens, l2_channels, eps)   kern 4; grid
+ *       (ceil(channels / 128), ceil(T / 8)), block 128 (a partial last head of channels is masked)
  *     halo_shexp_gate_up{,_u}(gq, gd, uq, ud, gate_inp, x, h, sgate, rows, cols, qstride)   grid ceil(rows / 16)
  *     halo_shexp_down_combine{,_u}(dq, dd, hin, sgate, part, weights, slots, out, rows, cols, qstride)
  *                                                                       grid ceil(rows / 32)
@@ -127,6 +127,10 @@
   X(halo_moe_bucket) X(halo_moe_bucket_count) X(halo_moe_bucket_scan) X(halo_moe_bucket_scatter)               \
   X(halo_gemm_q8r_wmma) X(halo_gemm_q8r_wmma_t) X(halo_gemm_q8a8_128x128) X(halo_gemm_q8a8_128x64)           \
   X(halo_gemm_q8a8_320x64) X(halo_gemm_q8a8_160x64) X(halo_gemm_q8a8_256x128)                                 \
-  X(halo_synth_q8) X(halo_synth_f32)
+  X(halo_synth_q8) X(halo_synth_f32) X(halo_code_object_info_copy)
+
+/* Module-scope variable of the code object (for halo_read_global / halo_write_global):
+ *   uint32 halo_code_object_info[4] = {format version, wave size, gfx target number, spare}
+ * halo_code_object_info_copy(u32* out)   grid (1), block 64: out[0..3] = halo_code_object_info as kernels see it. */
 
 #endif /* HALO_KERNELS_H_ */

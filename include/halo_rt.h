@@ -82,6 +82,27 @@ void halo_free_host(halo_device* dev, void* p);
 /* Device::AvailableBytes (src/rt/device.hpp:114-118). */
 size_t halo_available_bytes(halo_device* dev);
 
+/* Physical pages mapped into reserved virtual ranges, for paged KV caches (Device::PageBytes / ReserveRange /
+ * ReleaseRange / CreatePage / ReleasePage / MapPage / UnmapPage, src/rt/device.hpp:101-112). halo_page_bytes is
+ * the mapping granularity (2 MiB rounded to the device's granule), 0 when the device cannot map pages (callers
+ * then allocate whole ranges with halo_alloc). A reserved range has device addresses but no memory until pages are
+ * mapped into it; one page may be mapped into several ranges (offsets multiples of halo_page_bytes) and is read
+ * and written through any of them. Unmapping and releasing a range drain the device stream first; the first launch
+ * or copy after a mapping change waits out a 1 ms settle interval (as the reference's HIP backend does). Not
+ * capturable. */
+size_t halo_page_bytes(halo_device* dev);
+int halo_reserve_range(halo_device* dev, size_t bytes, halo_buffer* out, char* err, size_t errlen);
+void halo_release_range(halo_device* dev, halo_buffer* range);
+int halo_create_page(halo_device* dev, void** page, char* err, size_t errlen);
+void halo_release_page(halo_device* dev, void* page);
+int halo_map_page(halo_device* dev, const halo_buffer* range, size_t offset, void* page, char* err, size_t errlen);
+int halo_unmap_page(halo_device* dev, const halo_buffer* range, size_t offset, char* err, size_t errlen);
+
+/* Device::ReadGlobal / WriteGlobal (src/rt/device.hpp:122-126): copies a module-scope __device__ variable of the
+ * loaded code object to or from the host (bytes <= the variable's size). Not capturable. */
+int halo_read_global(halo_device* dev, const char* name, void* dst, size_t bytes, char* err, size_t errlen);
+int halo_write_global(halo_device* dev, const char* name, const void* src, size_t bytes, char* err, size_t errlen);
+
 /* kernels::CoreHsaco() (reference CMakeLists.txt:143-179): the embedded gfx950 code object. */
 const uint8_t* halo_core_code_object(size_t* bytes);
 

@@ -54,3 +54,39 @@ def test_errors_are_reported_not_raised_in_c():
     err = ctypes.create_string_buffer(256)
     rc = H.lib().halo_alloc(None, 16, ctypes.byref(H.Buffer()), err, 256)
     assert rc == -1 and b"null" in err.value
+
+
+def test_ops_refuse_null_required_pointers():
+    """Every operator checks its required device pointers before touching the engine or the GPU (a null read faults
+    the GPU); the refusal names the argument."""
+    import ctypes
+
+    L = H.lib()
+    err = ctypes.create_string_buffer(256)
+    m = H.Q8Matrix()
+    calls = {
+        "halo_op_quantize_q8": (None, None, None, None, 1, 64),
+        "halo_op_matvec_q8a8": (None, ctypes.byref(m), None, None, None, 1, 64),
+        "halo_op_matvec_q8_f32x": (None, ctypes.byref(m), None, None),
+        "halo_op_repack_q8_0": (None, None, None, None, 4, 64, 64),
+        "halo_op_gdn_decode": (None, None, None, None, None, None, None, None, 1, 32, 16, 128),
+        "halo_op_kv_append": (None, None, None, None),
+        "halo_op_moe_decode": (None, None, None, None, 1, None, 0),
+        "halo_op_synth_f32": (None, None, 16, 1, ctypes.c_float(1.0)),
+    }
+    for name, args in calls.items():
+        rc = getattr(L, name)(*args, err, 256)
+        assert rc == -1 and b"is null" in err.value, (name, err.value)
+
+
+def test_device_layer_refuses_null_handles():
+    import ctypes
+
+    L = H.lib()
+    err = ctypes.create_string_buffer(256)
+    b = H.Buffer()
+    assert L.halo_reserve_range(None, 1 << 21, ctypes.byref(b), err, 256) == -1
+    assert L.halo_map_page(None, ctypes.byref(b), 0, None, err, 256) == -1
+    assert L.halo_read_global(None, b"x", None, 4, err, 256) == -1
+    assert L.halo_launch_graph(None, None, err, 256) == -1
+    assert L.halo_page_bytes(None) == 0

@@ -333,46 +333,78 @@ extern "C" __global__ void __launch_bounds__(256)
 // 256-thread block covers the reference's rows per block (8 * R); x is read through the vector cache.
 namespace {
 // Row block bx of 8 R rows (4 waves x 2 rows per pass x R).
-template <int R>
+// One lane's 16-value piece of an fp32-activation Q8_0 dot: sum over i of q[i] * x[i] as one fused chain in index
+// order. The single-column and batched kernels both use it, so a column's bits do not depend on the batch.
+__device__ __forceinline__ float Q8PieceF32(const int4& q, const float (&xr)[16]) {
+  const std::int8_t* v = reinterpret_cast<const std::int8_t*>(&q);
+  float part = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) part = __builtin_fmaf(static_cast<float>(v[i]), xr[i], part);
+  return part;
+}
+__device__ __forceinline__ void LoadX16(const float* x, float (&xr)[16]) {
+  const float4* xp = reinterpret_cast<const float4*>(x);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 v = xp[i];
+    xr[4 * i] = v.x;
+    xr[4 * i + 1] = v.y;
+    xr[4 * i + 2] = v.z;
+    xr[4 * i + 3] = v.w;
+  }
+}
+
+// fp32-activation Q8_0 GEMV over NB columns (NB = 1: the single-column kernels): a 32-lane half wave per row, two
+// rows per wave per pass, R passes (8 R rows per block of 256); each lane's 16-value pieces of a row at stride
+// 32 * 16 columns, x read through the vector cache (no LDS copy, so no column limit). The weights of a piece are
+// loaded once for all NB columns; each column's arithmetic (Q8PieceF32, acc = fma(scale, piece, acc) in column
+// order, GroupSum<32>) is the single-column kernel's, so every column equals a single-column launch bit for bit.
+// Column b reads x + b * xstride and writes y + b * ystride.
+template <int R, int NB>
 __device__ __forceinline__ void GemvQ8rF32At(const std::int8_t* __restrict__ qs, const std::uint16_t* __restrict__ d,
-                                             const float* __restrict__ x, float* __restrict__ y, std::uint32_t rows,
-                                             std::uint32_t cols, std::uint32_t qstride, std::uint32_t bx) {
+                                             const float* __restrict__ x, std::uint32_t xstride, float* __restrict__ y,
+                                             std::uint32_t ystride, std::uint32_t rows, std::uint32_t cols,
+                                             std::uint32_t qstride, std::uint32_t bx) {
   constexpr int LPR = 32, P = 2;
   const std::uint32_t base = (bx * (blockDim.x / kWave) + threadIdx.x / kWave) * (P * R);
   if (base >= rows) return;
   const std::uint32_t lane = threadIdx.x % kWave, nblk = cols / 32, sub = lane / LPR;
-  float acc[R];
+  float acc[NB][R];
 #pragma unroll
-  for (int k = 0; k < R; ++k) acc[k] = 0.0f;
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int k = 0; k < R; ++k) acc[b][k] = 0.0f;
   for (std::uint32_t c = (lane % LPR) * 16; c < cols; c += LPR * 16) {
-    const float4* xp = reinterpret_cast<const float4*>(x + c);
-    float xr[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float4 v = xp[i];
-      xr[4 * i] = v.x;
-      xr[4 * i + 1] = v.y;
-      xr[4 * i + 2] = v.z;
-      xr[4 * i + 3] = v.w;
-    }
+    int4 q[R];
+    float s[R];
 #pragma unroll
     for (int k = 0; k < R; ++k) {
       const std::uint32_t r = min(base + k * P + sub, rows - 1);
-      const int4 q = *reinterpret_cast<const int4*>(qs + static_cast<std::size_t>(r) * qstride + c);
-      const float s = F16(d[static_cast<std::size_t>(r) * nblk + c / 32]);
-      const std::int8_t* v = reinterpret_cast<const std::int8_t*>(&q);
-      float part = 0.0f;
+      q[k] = *reinterpret_cast<const int4*>(qs + static_cast<std::size_t>(r) * qstride + c);
+      s[k] = F16(d[static_cast<std::size_t>(r) * nblk + c / 32]);
+    }
 #pragma unroll
-      for (int i = 0; i < 16; ++i) part += static_cast<float>(v[i]) * xr[i];
-      acc[k] += s * part;
+    for (int b = 0; b < NB; ++b) {
+      float xr[16];
+      LoadX16(x + static_cast<std::size_t>(b) * xstride + c, xr);
+#pragma unroll
+      for (int k = 0; k < R; ++k) acc[b][k] = __builtin_fmaf(s[k], Q8PieceF32(q[k], xr), acc[b][k]);
     }
   }
 #pragma unroll
-  for (int k = 0; k < R; ++k) {
-    const float a = halo::GroupSum<LPR>(acc[k]);
-    const std::uint32_t r = base + k * P + sub;
-    if (lane % LPR == 0 && r < rows) y[r] = a;
-  }
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      const float a = halo::GroupSum<LPR>(acc[b][k]);
+      const std::uint32_t r = base + k * P + sub;
+      if (lane % LPR == 0 && r < rows) y[static_cast<std::size_t>(b) * ystride + r] = a;
+    }
+}
+template <int R>
+__device__ __forceinline__ void GemvQ8rF32At(const std::int8_t* __restrict__ qs, const std::uint16_t* __restrict__ d,
+                                             const float* __restrict__ x, float* __restrict__ y, std::uint32_t rows,
+                                             std::uint32_t cols, std::uint32_t qstride, std::uint32_t bx) {
+  GemvQ8rF32At<R, 1>(qs, d, x, 0, y, 0, rows, cols, qstride, bx);
 }
 template <int R>
 __device__ __forceinline__ void GemvQ8rF32(const std::int8_t* __restrict__ qs, const std::uint16_t* __restrict__ d,
@@ -397,6 +429,51 @@ extern "C" __global__ void __launch_bounds__(256)
                      std::uint32_t cols, std::uint32_t qstride) {
   GemvQ8rF32<4>(qs, d, x, y, rows, cols, qstride);
 }
+
+// ---- exact batched fp32-activation GEMVs (reference src/kernels/batch_decode.hip:133-190) ----------------------
+// NB = 1..8 columns per launch, each byte-identical to halo_gemv_q8r_r4 / _r2 / halo_gemv_q8r_dual of that column
+// alone. Grid as the reference launches them: blockIdx.x = row block * groups + column group (column group g covers
+// columns g NB .. g NB + NB - 1), 8 R rows per block of 256 (dual: 32 rows, blocks [0, blocks1) matrix 1). The
+// reference's _p (prefetch) / _s (small LDS) / _ps variants exist for its LDS staging of x; this body reads x
+// through the vector cache, so the four names share it.
+#define HALO_GEMV_Q8R_B(R, NB, SUF)                                                                                 \
+  extern "C" __global__ void __launch_bounds__(256) halo_gemv_q8r_r##R##_b##NB##SUF(                               \
+      const std::int8_t* qs, const std::uint16_t* d, const float* x, float* y, std::uint32_t rows,                 \
+      std::uint32_t cols, std::uint32_t qstride, std::uint32_t xstride, std::uint32_t ystride,                     \
+      std::uint32_t groups) {                                                                                       \
+    const std::uint32_t g = blockIdx.x % groups;                                                                    \
+    GemvQ8rF32At<R, NB>(qs, d, x + static_cast<std::size_t>(g) * NB * xstride, xstride,                            \
+                        y + static_cast<std::size_t>(g) * NB * ystride, ystride, rows, cols, qstride,               \
+                        blockIdx.x / groups);                                                                       \
+  }
+#define HALO_GEMV_Q8R_DUAL_B(NB, SUF)                                                                               \
+  extern "C" __global__ void __launch_bounds__(256) halo_gemv_q8r_dual_b##NB##SUF(                                \
+      const std::int8_t* q1, const std::uint16_t* d1, float* y1, std::uint32_t rows1, std::uint32_t qstride1,      \
+      const std::int8_t* q2, const std::uint16_t* d2, float* y2, std::uint32_t rows2, std::uint32_t qstride2,      \
+      const float* x, std::uint32_t cols, std::uint32_t blocks1, std::uint32_t xstride, std::uint32_t ystride1,    \
+      std::uint32_t ystride2, std::uint32_t groups) {                                                               \
+    const std::uint32_t bx = blockIdx.x / groups, g = blockIdx.x % groups;                                          \
+    const bool first = bx < blocks1;                                                                                \
+    const std::uint32_t ys = first ? ystride1 : ystride2;                                                           \
+    GemvQ8rF32At<4, NB>(first ? q1 : q2, first ? d1 : d2, x + static_cast<std::size_t>(g) * NB * xstride, xstride,  \
+                        (first ? y1 : y2) + static_cast<std::size_t>(g) * NB * ys, ys, first ? rows1 : rows2, cols, \
+                        first ? qstride1 : qstride2, first ? bx : bx - blocks1);                                    \
+  }
+#define HALO_GEMV_Q8R_B_ALL(NB)                                                                                     \
+  HALO_GEMV_Q8R_B(4, NB, ) HALO_GEMV_Q8R_B(4, NB, _p) HALO_GEMV_Q8R_B(4, NB, _s) HALO_GEMV_Q8R_B(4, NB, _ps)         \
+  HALO_GEMV_Q8R_B(2, NB, ) HALO_GEMV_Q8R_B(2, NB, _p) HALO_GEMV_Q8R_B(2, NB, _s) HALO_GEMV_Q8R_B(2, NB, _ps)         \
+  HALO_GEMV_Q8R_DUAL_B(NB, ) HALO_GEMV_Q8R_DUAL_B(NB, _p) HALO_GEMV_Q8R_DUAL_B(NB, _s) HALO_GEMV_Q8R_DUAL_B(NB, _ps)
+HALO_GEMV_Q8R_B_ALL(1)
+HALO_GEMV_Q8R_B_ALL(2)
+HALO_GEMV_Q8R_B_ALL(3)
+HALO_GEMV_Q8R_B_ALL(4)
+HALO_GEMV_Q8R_B_ALL(5)
+HALO_GEMV_Q8R_B_ALL(6)
+HALO_GEMV_Q8R_B_ALL(7)
+HALO_GEMV_Q8R_B_ALL(8)
+#undef HALO_GEMV_Q8R_B_ALL
+#undef HALO_GEMV_Q8R_DUAL_B
+#undef HALO_GEMV_Q8R_B
 
 // ---- synthetic tensors ------------------------------------------------------------------------------------------
 // Seeded Q8_0 weights generated in place (no host copy of multi-GB models): q uniform in [-127, 127] from a

@@ -16,6 +16,11 @@
  *     xs2, cols, blocks1, ystride1, ystride2, groups)   grid ((blocks1 + blocks2) * groups)   batch_decode.hip:310
  *   halo_gemv_q8r_dual(q1, d1, y1, rows1, qstride1, q2, d2, y2, rows2, qstride2, x, cols, blocks1)
  *                                                       grid (blocks1 + ceil(rows2 / 32))    core.hip:2960
+ *   halo_gemv_q8r_{r4,r2}_b{1..8}{,_p,_s,_ps}(qs, d, x, y, rows, cols, qstride, xstride, ystride, groups)
+ *     exact batched fp32-x GEMVs, every column = the single-column kernel's bits; xstride % 4 == 0
+ *                                                       grid (ceil(rows / (8 R)) * groups)   batch_decode.hip:133
+ *   halo_gemv_q8r_dual_b{1..8}{,_p,_s,_ps}(q1, d1, y1, rows1, qstride1, q2, d2, y2, rows2, qstride2, x, cols,
+ *     blocks1, xstride, ystride1, ystride2, groups)   grid ((blocks1 + ceil(rows2 / 32)) * groups)  batch_decode.hip:160
  *   halo_gemv_q8a8_l{16,32,64}_r{1,2,4}_b{1,2,4,8}(qs, d, xq, xs, y, rows, cols, qstride, ystride)   new (MI355X)
  *   halo_q8_half_dots(qs, xq, i32* isum, rows, cols, qstride)                                  new (parity)
  *   reference-named decode kernels (core.hip:259-586, 2621, 3003-3063), same parameters and grids:
@@ -127,7 +132,9 @@
   X(halo_moe_bucket) X(halo_moe_bucket_count) X(halo_moe_bucket_scan) X(halo_moe_bucket_scatter)               \
   X(halo_gemm_q8r_wmma) X(halo_gemm_q8r_wmma_t) X(halo_gemm_q8a8_128x128) X(halo_gemm_q8a8_128x64)           \
   X(halo_gemm_q8a8_320x64) X(halo_gemm_q8a8_160x64) X(halo_gemm_q8a8_256x128)                                 \
-  X(halo_synth_q8) X(halo_synth_f32) X(halo_code_object_info_copy)
+  X(halo_synth_q8) X(halo_synth_f32) X(halo_code_object_info_copy)                                            \
+  X(halo_gemv_q8r_r4_b1) X(halo_gemv_q8r_r4_b8_ps) X(halo_gemv_q8r_r2_b3_p) X(halo_gemv_q8r_r2_b5_s)              \
+  X(halo_gemv_q8r_dual_b1) X(halo_gemv_q8r_dual_b8_ps)
 
 /* Module-scope variable of the code object (for halo_read_global / halo_write_global):
  *   uint32 halo_code_object_info[4] = {format version, wave size, gfx target number, spare}

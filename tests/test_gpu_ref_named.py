@@ -845,3 +845,56 @@ def test_conv_prefill8(dev, T, C):
     dev.launch("halo_conv_l2norm_prefill", ((C + d - 1) // d, T), (d,),
                [gx, gst, gw, g1, ("u32", C), ("u32", K), ("u32", l2), ("f32", 1e-6)])
     assert got.tobytes() == g1.download().tobytes()
+
+
+# ---- exact batched fp32-x GEMVs (batch_decode.hip:133-190): every column equals the single-column kernel ----------
+@pytest.mark.parametrize("R,NB,suf,groups", [(4, 1, "", 1), (4, 3, "_p", 2), (4, 8, "_ps", 1), (2, 2, "", 3),
+                                             (2, 5, "_s", 1), (2, 8, "", 2)])
+def test_batched_gemv_columns_equal_single(dev, R, NB, suf, groups):
+    rng = np.random.default_rng(80 + R * 10 + NB)
+    rows, cols, xstride, ystride = 1000, 2048, 2052, 1003  # ragged rows, padded column strides
+    qs, d = O.synth_q8(rng, rows, cols)
+    ncol = NB * groups
+    x = rng.normal(0, 1, (ncol, xstride)).astype(np.float32)
+    gq, gd, gx = dev.to_device(qs), dev.to_device(d), dev.to_device(x)
+    gy = dev.array((ncol, ystride), np.float32)
+    blocks = (rows + 8 * R - 1) // (8 * R)
+    dev.launch(f"halo_gemv_q8r_r{R}_b{NB}{suf}", (blocks * groups,), (256,),
+               [gq, gd, gx, gy, ("u32", rows), ("u32", cols), ("u32", cols), ("u32", xstride), ("u32", ystride),
+                ("u32", groups)])
+    got = gy.download()
+    one = dev.array(rows, np.float32)
+    for b in range(ncol):
+        xb = dev.to_device(np.ascontiguousarray(x[b, :cols]))
+        dev.launch(f"halo_gemv_q8r_r{R}" if R != 1 else "halo_gemv_q8r", (blocks,), (256,),
+                   [gq, gd, xb, one, ("u32", rows), ("u32", cols), ("u32", cols)])
+        assert got[b, :rows].tobytes() == one.download().tobytes(), f"column {b}"
+    if NB == 1 and groups == 1:  # and the single kernel against the oracle
+        want = np.zeros(rows, np.float32)
+        O.oracle().or_matvec_q8_0_f32x(qs, d, rows, cols, cols, np.ascontiguousarray(x[0, :cols]), want, 1)
+        w = np.abs(qs.astype(np.float64) * np.repeat(d.view(np.float16).astype(np.float64), 32, axis=1))
+        close(got[0, :rows], want, w @ np.abs(x[0, :cols].astype(np.float64)))
+
+
+@pytest.mark.parametrize("NB,suf,groups", [(1, "", 1), (4, "_p", 2), (8, "_ps", 1), (6, "_s", 1)])
+def test_batched_dual_gemv_columns_equal_single(dev, NB, suf, groups):
+    rng = np.random.default_rng(90 + NB)
+    rows1, rows2, cols, xstride = 700, 300, 2048, 2048
+    q1, d1 = O.synth_q8(rng, rows1, cols)
+    q2, d2 = O.synth_q8(rng, rows2, cols)
+    ncol = NB * groups
+    x = rng.normal(0, 1, (ncol, xstride)).astype(np.float32)
+    g1, e1, g2, e2, gx = (dev.to_device(a) for a in (q1, d1, q2, d2, x))
+    y1, y2 = dev.array((ncol, rows1), np.float32), dev.array((ncol, rows2), np.float32)
+    b1, b2 = (rows1 + 31) // 32, (rows2 + 31) // 32
+    dev.launch(f"halo_gemv_q8r_dual_b{NB}{suf}", ((b1 + b2) * groups,), (256,),
+               [g1, e1, y1, ("u32", rows1), ("u32", cols), g2, e2, y2, ("u32", rows2), ("u32", cols), gx,
+                ("u32", cols), ("u32", b1), ("u32", xstride), ("u32", rows1), ("u32", rows2), ("u32", groups)])
+    a1, a2 = y1.download(), y2.download()
+    s1, s2 = dev.array(rows1, np.float32), dev.array(rows2, np.float32)
+    for b in range(ncol):
+        xb = dev.to_device(np.ascontiguousarray(x[b]))
+        dev.launch("halo_gemv_q8r_dual", (b1 + b2,), (256,),
+                   [g1, e1, s1, ("u32", rows1), ("u32", cols), g2, e2, s2, ("u32", rows2), ("u32", cols), xb,
+                    ("u32", cols), ("u32", b1)])
+        assert a1[b].tobytes() == s1.download().tobytes() and a2[b].tobytes() == s2.download().tobytes(), b

@@ -679,7 +679,15 @@ int halo_gguf_upload_q8_0(halo_engine* eng, const halo_gguf_tensor* t, uint64_t 
   const std::uint64_t cols = t->dims[0];
   std::uint64_t all_rows = 1;
   for (std::uint32_t k = 1; k < t->n_dims; ++k) all_rows *= t->dims[k];
-  if (cols % 32 != 0 || cols > 0xFFFFFFFFull || row0 > all_rows || rows > all_rows - row0)
+  if (cols == 0 || cols % 32 != 0)
+    return SetErr(err, errlen, "Q8_0 tensor with %llu columns (must be a positive multiple of 32)",
+                  static_cast<unsigned long long>(cols)),
+           -1;
+  if (qstride < cols || qstride % 16 != 0)
+    return SetErr(err, errlen, "qstride %u must be >= the %llu columns and a multiple of 16", qstride,
+                  static_cast<unsigned long long>(cols)),
+           -1;
+  if (cols > 0xFFFFFFFFull || row0 > all_rows || rows > all_rows - row0)
     return SetErr(err, errlen, "rows [%llu, %llu) outside the tensor's %llu", static_cast<unsigned long long>(row0),
                   static_cast<unsigned long long>(row0 + rows), static_cast<unsigned long long>(all_rows)),
            -1;

@@ -225,3 +225,23 @@ def test_model_config_from_metadata():
     with pytest.raises(H.HaloError, match="expert_shared_feed_forward_length"):
         g.config()
     g.close()
+
+
+def test_upload_q8_0_refuses_degenerate_shapes():
+    """halo_gguf_upload_q8_0 refuses a tensor with no columns (it would divide by a zero row size) and a destination
+    row stride shorter than the row or not 16-byte aligned (the repack would write past the rows), before it touches
+    the engine or the device: the engine, staging and destination pointers below are placeholders never used."""
+    import ctypes
+
+    L = H.lib()
+    err = ctypes.create_string_buffer(256)
+    blob = ctypes.create_string_buffer(64)
+    fake = ctypes.c_void_p(1 << 40)
+    for cols, qstride, msg in ((0, 64, b"columns"), (64, 32, b"qstride"), (64, 72, b"qstride")):
+        t = H.GgufTensor()
+        t.type = 8  # GGML Q8_0
+        t.n_dims = 2
+        t.dims[0], t.dims[1] = cols, 4
+        t.data = ctypes.cast(blob, ctypes.c_void_p)
+        rc = L.halo_gguf_upload_q8_0(fake, ctypes.byref(t), 0, 1, fake, fake, qstride, fake, 1 << 20, err, 256)
+        assert rc == -1 and msg in err.value, (cols, qstride, err.value)

@@ -153,15 +153,12 @@ int halo_op_matvec_q8a8(halo_engine* eng, const halo_q8_matrix* w, const int8_t*
   if (CheckMatrix(w, err, errlen) != 0) return -1;
   if (m == 0) return SetErr(err, errlen, "m == 0"), -1;
   if (m > 1 && ystride < w->rows) return SetErr(err, errlen, "ystride %u < rows %u", ystride, w->rows), -1;
-  if (m >= 64 && w->rows >= 128 && w->cols % 64 == 0) {
+  if (m >= 64 && w->rows >= 128 && w->cols % 64 == 0 &&
+      static_cast<std::uint64_t>(w->rows) * w->qstride < (std::uint64_t{1} << 32)) {
     // prefill-sized M: 128 x 128 tiles staged through LDS, one 32x32x32 MFMA per Q8_0 block and tile
     const halo_arg a[] = {Ptr(w->qs), Ptr(w->d), Ptr(xq), Ptr(xs), Ptr(y), U32(w->rows), U32(w->cols),
                           U32(w->qstride), U32(m), U32(ystride)};
-    // grids within one block per CU take the paired-scale kernel (it holds one block per CU)
-    const std::uint32_t blocks = CeilDiv(w->rows, 128) * CeilDiv(m, 128);
-    return Launch(eng, blocks <= 256 ? "halo_gemm_q8a8_mfma32_p" : "halo_gemm_q8a8_mfma32",
-                  D3(CeilDiv(w->rows, 128), CeilDiv(m, 128)), D3(512), a, err,
-                  errlen);
+    return Launch(eng, "halo_gemm_q8a8_mfma32", D3(CeilDiv(w->rows, 128), CeilDiv(m, 128)), D3(512), a, err, errlen);
   }
   if (m >= 16) {
     // int8 MFMA tiles: 16 rows x 16 (or 64) tokens per block, one MFMA per Q8_0 block

@@ -252,7 +252,7 @@ int halo_op_moe_prefill(halo_engine* eng, const halo_moe_weights* w, const float
                           Ptr(shared ? w->shared_gate_proj.qs : nullptr), Ptr(shared ? w->shared_gate_proj.d : nullptr),
                           Ptr(shared ? w->shared_up.qs : nullptr), Ptr(shared ? w->shared_up.d : nullptr), Ptr(v.xq),
                           Ptr(v.xs), Ptr(v.token), Ptr(v.tiles), Ptr(v.ntiles), Ptr(v.h), U32(F), U32(H), U32(E), U32(F)};
-    if (Launch(eng, "halo_moe_grouped_gate_up_q8", D3(CeilDiv(F, 128), v.max_tiles), D3(512), a, err, errlen) != 0)
+    if (Launch(eng, "halo_moe_grouped_gate_up_q8", D3(CeilDiv(F, 64), v.max_tiles), D3(256), a, err, errlen) != 0)
       return -1;
   }
   // 6. h quantized per 32

@@ -198,11 +198,12 @@ extern "C" __global__ void __launch_bounds__(256)
 }
 
 // ---- grouped int8 MFMA over the pairs of each group ---------------------------------------------------------------
-// halo::GemmTileQ8 per (128 rows of group g's matrix, one tile of up to 64 pairs): group g < E reads rows g * rows + r
+// halo::GemmTileQ8Dma per (rows of group g's matrix, one tile of up to 64 pairs): group g < E reads rows g * rows + r
 // of the stacked expert tensors, group E the shared expert's. Pair p's activation row is xq[gather ? gather[p] : p].
-// The gate/up launch computes both matrices and writes h = SiLU(gate) * up; the down launch writes the projection.
-// grid (ceil(rows / 128), max tiles), block 512; blocks past ntiles[0] exit. y [pairs][ystride].
-extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) halo_moe_grouped_gate_up_q8(
+// The gate/up launch computes both matrices (64 rows of each per block, 4 waves) and writes h = SiLU(gate) * up; the
+// down launch (128 rows per block, 8 waves) writes the projection. grid (ceil(rows / 64) or ceil(rows / 128), max
+// tiles), block 256 / 512; blocks past ntiles[0] exit. y [pairs][ystride].
+extern "C" __global__ void __launch_bounds__(256) halo_moe_grouped_gate_up_q8(
     const std::int8_t* gq, const std::uint16_t* gd, const std::int8_t* uq, const std::uint16_t* ud,
     const std::int8_t* sgq, const std::uint16_t* sgd, const std::int8_t* suq, const std::uint16_t* sud,
     const std::int8_t* xq, const float* xs, const std::uint32_t* gather, const std::uint32_t* tiles,
@@ -213,9 +214,9 @@ extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_pe
   const bool sh = g == E;
   const std::size_t row0 = sh ? 0 : static_cast<std::size_t>(g) * ff;
   const std::uint32_t nblk = H / 32;
-  halo::GemmTileQ8<4, 1, 2, 2>((sh ? sgq : gq) + row0 * H, (sh ? sgd : gd) + row0 * nblk, (sh ? suq : uq) + row0 * H,
-                               (sh ? sud : ud) + row0 * nblk, ff, H, blockIdx.x * 128, xq, xs, gather + p0, 0, np, H,
-                               h, p0, hstride);
+  halo::GemmTileQ8Dma<2, 1, 2, 2, false, 1>((sh ? sgq : gq) + row0 * H, (sh ? sgd : gd) + row0 * nblk,
+                                            (sh ? suq : uq) + row0 * H, (sh ? sud : ud) + row0 * nblk, ff, H,
+                                            blockIdx.x * 64, xq, xs, gather + p0, 0, np, H, h, p0, hstride);
 }
 
 extern "C" __global__ void __launch_bounds__(512) halo_moe_grouped_down_q8(
@@ -228,8 +229,8 @@ extern "C" __global__ void __launch_bounds__(512) halo_moe_grouped_down_q8(
   const bool sh = g == E;
   const std::size_t row0 = sh ? 0 : static_cast<std::size_t>(g) * H;
   const std::uint32_t nblk = ff / 32;
-  halo::GemmTileQ8<4, 1, 2, 1>((sh ? sdq : dq) + row0 * ff, (sh ? sdd : dd) + row0 * nblk, nullptr, nullptr, H, ff,
-                               blockIdx.x * 128, hq, hs, nullptr, p0, np, ff, y, p0, H);
+  halo::GemmTileQ8Dma<4, 1, 2, 1>((sh ? sdq : dq) + row0 * ff, (sh ? sdd : dd) + row0 * nblk, nullptr, nullptr, H, ff,
+                                  blockIdx.x * 128, hq, hs, nullptr, p0, np, ff, y, p0, H);
 }
 
 // grid (ceil(H / 256), T), block 256: out[t][r] = sum over s < k, in order, of weights[t][s] * y[pos[t k + s]][r],

@@ -10,6 +10,8 @@
 // 16-value half block is an exact v_dot4_i32_i8 chain; the epilogue per half block is acc += s_w * (s_x * isum).
 #include "common.h"
 
+#include <type_traits>
+
 using halo::Dot16;
 using halo::F16;
 using halo::kWave;
@@ -862,17 +864,234 @@ __device__ __forceinline__ void GemmTileQ8(const std::int8_t* __restrict__ A0, c
 }
 }  // namespace halo
 
-// Dense: 128 rows x 128 tokens per block. grid (ceil(rows / 128), ceil(T / 128)), block 512. y[t * ystride + r].
+// ---- the same tiled GEMM with its stages filled by LDS DMA ------------------------------------------------------
+// Same arithmetic, operands and block order as GemmTileQ8 (results are bit-identical); the staging differs. Each stage
+// (64 columns: two Q8_0 blocks) lands in LDS through global_load_lds (16-byte rows of the weight and activation tiles,
+// 4-byte fp16 scale pairs and fp32 scale pairs), issued by the waves in turn with no register staging; three stage
+// buffers, the loads of stage k + 2 in flight while stage k computes, so one wait and one barrier per stage.
+// Tile rows are 64 bytes with the 16-byte chunk index xor-swizzled by (row >> 2) & 3, which keeps the fragment reads
+// (32 consecutive rows, one chunk each) free of bank conflicts. The stage loop is unrolled by three so every LDS
+// address is a per-lane constant plus an immediate. The scale MFMA is the two-block rank-1 v_mfma_f32_32x32x1_2b,
+// covering two tiles (NMAT * MT even) or both blocks of the stage (a single tile).
+// Limits: cols % 64 == 0; every weight offset (rows * qstride) and activation offset fits in 32 bits.
+namespace {
+__device__ __forceinline__ void DmaRow16(const void* sbase, std::uint32_t voff, std::uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void DmaDword(const void* addr, std::uint32_t lds) {
+  asm volatile("global_load_lds_dword %0, off" ::"v"(addr), "{m0}"(lds) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void WaitVmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ std::uint32_t ChunkSwz(std::uint32_t r) { return (r >> 2) & 3u; }
+// An empty asm that reads and writes the 16 values: everything computing them is done before this point.
+__device__ __forceinline__ void PinVgprs(float (&a)[16]) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j) asm volatile("" : "+v"(a[j]));
+}
+}  // namespace
+
+namespace halo {
+template <int WR, int MT, int WT, int NMAT, bool KBLK = false, int PRIO = 0>
+__device__ __forceinline__ void GemmTileQ8Dma(const std::int8_t* __restrict__ A0, const std::uint16_t* __restrict__ D0,
+                                             const std::int8_t* __restrict__ A1, const std::uint16_t* __restrict__ D1,
+                                             std::uint32_t rows, std::uint32_t qstride, std::uint32_t r0,
+                                             const std::int8_t* __restrict__ xq, const float* __restrict__ xs,
+                                             const std::uint32_t* __restrict__ xrow, std::uint32_t x0,
+                                             std::uint32_t ntok, std::uint32_t cols, float* __restrict__ y,
+                                             std::uint32_t yrow0, std::uint32_t ystride, std::uint32_t xtok = 0) {
+  constexpr int NW = WR * WT, ROWS = WR * MT * 32, TOKS = WT * 32, NT = NMAT * MT;
+  static_assert(NT == 1 || MT % 2 == 0 || MT == 1, "scale pairs with a uniform row step");
+  constexpr int ABYTES = NMAT * ROWS * 64, BBYTES = TOKS * 64, SD = NMAT * ROWS, SX = 2 * TOKS;
+  constexpr int WA = ABYTES / 1024, WB = BBYTES / 1024, WSD = (SD + 63) / 64, WSX = (SX + 63) / 64;
+  constexpr int SPR = (WA + WB + NW - 1) / NW, SPS = (WSD + WSX + NW - 1) / NW;  // loads per wave per stage
+  constexpr int RB = ABYTES, RS = ABYTES + BBYTES, RX = RS + WSD * 256;  // regions (scale regions whole loads)
+  constexpr int STAGE = (RX + WSX * 256 + 1023) / 1024 * 1024;
+  static_assert(3 * STAGE <= 65536, "LDS immediates");
+  __shared__ __attribute__((aligned(1024))) std::int8_t lds[3 * STAGE];
+  const std::uint32_t tid = threadIdx.x, lane = tid % 64;
+  const std::uint32_t wave = __builtin_amdgcn_readfirstlane(tid / 64);
+  const std::uint32_t wr = wave / WT, wt = wave % WT;
+  const std::uint32_t nblk = cols / 32, nk = cols / 64;
+  const std::uint32_t lbase = static_cast<std::uint32_t>(reinterpret_cast<std::uintptr_t>(lds));
+  const auto tokrow = [&](std::uint32_t i) {
+    const std::uint32_t ii = min(i, ntok - 1);
+    return xrow != nullptr ? xrow[ii] : x0 + ii;
+  };
+  // The wave's loads of a stage, in turn over the waves (the last load repeated where the count is uneven): 16-byte
+  // rows of the weight tiles then the activation tile (a wave-uniform base + a per-lane 32-bit offset), and 4-byte
+  // scale pairs (per-lane addresses; lanes past a region's end load a clamped address into the region's padding).
+  const std::int8_t* rbase[SPR];
+  std::uint32_t roff[SPR], rstep[SPR], rlds[SPR];
+#pragma unroll
+  for (int i = 0; i < SPR; ++i) {
+    const std::uint32_t j = min(wave + NW * i, static_cast<std::uint32_t>(WA + WB - 1));
+    if (j < WA) {
+      const std::uint32_t p = j * 64 + lane, m = j * 64 / (ROWS * 4), pp = p % (ROWS * 4);
+      const std::uint32_t r = pp / 4, c = (pp % 4) ^ ChunkSwz(r);
+      rbase[i] = m ? A1 : A0;
+      roff[i] = min(r0 + r, rows - 1) * qstride + c * 16;
+      rstep[i] = 64;
+      rlds[i] = j * 1024;
+    } else {
+      const std::uint32_t jb = j - WA, p = jb * 64 + lane, t = p / 4, c = (p % 4) ^ ChunkSwz(t);
+      rbase[i] = xq;
+      roff[i] = tokrow(t) * (KBLK ? 64u : cols) + c * 16;
+      rstep[i] = KBLK ? 64 * xtok : 64;
+      rlds[i] = RB + jb * 1024;
+    }
+  }
+  const char* saddr[SPS];
+  std::uint32_t sstep[SPS], slds[SPS];
+#pragma unroll
+  for (int i = 0; i < SPS; ++i) {
+    const std::uint32_t j = min(wave + NW * i, static_cast<std::uint32_t>(WSD + WSX - 1));
+    if (j < WSD) {
+      const std::uint32_t q = min(j * 64 + lane, static_cast<std::uint32_t>(SD - 1)), m = q / ROWS, r = q % ROWS;
+      saddr[i] = reinterpret_cast<const char*>((m ? D1 : D0) + static_cast<std::size_t>(min(r0 + r, rows - 1)) * nblk);
+      sstep[i] = 4;
+      slds[i] = RS + j * 256;
+    } else {
+      const std::uint32_t jx = j - WSD, q = min(jx * 64 + lane, static_cast<std::uint32_t>(SX - 1));
+      const std::uint32_t t = q / 2, part = q % 2;
+      saddr[i] = reinterpret_cast<const char*>(KBLK ? xs + static_cast<std::size_t>(part) * xtok + tokrow(t)
+                                                    : xs + static_cast<std::size_t>(tokrow(t)) * nblk + part);
+      sstep[i] = KBLK ? 8 * xtok : 8;
+      slds[i] = RX + jx * 256;
+    }
+  }
+  const auto issue = [&](std::uint32_t kc, std::uint32_t buf) {
+#pragma unroll
+    for (int i = 0; i < SPR; ++i) DmaRow16(rbase[i] + static_cast<std::size_t>(kc) * rstep[i], roff[i], lbase + buf * STAGE + rlds[i]);
+#pragma unroll
+    for (int i = 0; i < SPS; ++i) DmaDword(saddr[i] + static_cast<std::size_t>(kc) * sstep[i], lbase + buf * STAGE + slds[i]);
+  };
+  float acc[NT][16];
+#pragma unroll
+  for (int p = 0; p < NT; ++p)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[p][j] = 0.0f;
+  const std::uint32_t fr = lane % 32, fh = lane / 32;
+  const std::uint32_t tok = wt * 32 + fr, ra = wr * MT * 32 + fr;
+  const std::uint32_t a0 = ra * 64 + ((fh ^ ChunkSwz(ra)) * 16), b0 = tok * 64 + ((fh ^ ChunkSwz(tok)) * 16);
+  constexpr std::uint32_t kPairStep = NT == 1 ? 2u : (MT % 2 == 0 ? 128u : ROWS * 4u);
+  const std::uint32_t dwo = RS + ra * 4 + fh * kPairStep, sxo = RX + tok * 8 + (NT == 1 ? fh * 4 : 0u);
+  const auto tile_row_off = [](int p) { return ((p / MT) * ROWS + (p % MT) * 32) * 4; };
+  const auto compute = [&](auto bufc) {
+    constexpr int BO = decltype(bufc)::value * STAGE;
+    const std::int8_t* sb = lds + BO;
+    const V16I32 z = {};
+    const V32F32 fz = {};
+    if constexpr (NT == 1) {
+      const float dw = F16(*reinterpret_cast<const std::uint16_t*>(sb + dwo));
+      const float sx = *reinterpret_cast<const float*>(sb + sxo);
+      const V32F32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(dw, sx, fz, 0, 0, 0);
+      const V4i af0 = *reinterpret_cast<const V4i*>(sb + a0), af1 = *reinterpret_cast<const V4i*>(sb + (a0 ^ 32u));
+      const V4i bf0 = *reinterpret_cast<const V4i*>(sb + RB + b0);
+      const V4i bf1 = *reinterpret_cast<const V4i*>(sb + RB + (b0 ^ 32u));
+      const V16I32 c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(af0, bf0, z, 0, 0, 0);
+      const V16I32 c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(af1, bf1, z, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[0][j] = __builtin_fmaf(static_cast<float>(c0[j]), sc[j], acc[0][j]);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[0][j] = __builtin_fmaf(static_cast<float>(c1[j]), sc[16 + j], acc[0][j]);
+    } else {
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk) {
+        __builtin_amdgcn_sched_barrier(0);  // one block's MFMA results live at a time
+        const std::uint32_t ao = blk ? a0 ^ 32u : a0, bo = blk ? b0 ^ 32u : b0;
+        const V4i bf = *reinterpret_cast<const V4i*>(sb + RB + bo);
+        const float sx = *reinterpret_cast<const float*>(sb + sxo + blk * 4);
+#pragma unroll
+        for (int q = 0; q < NT / 2; ++q) {
+          const int p0 = 2 * q, p1 = 2 * q + 1;
+          if constexpr (PRIO) {
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_setprio(PRIO);  // issue this wave's MFMAs ahead of other waves' epilogues
+          }
+          const float dw = F16(*reinterpret_cast<const std::uint16_t*>(sb + dwo + tile_row_off(p0) + blk * 2));
+          const V32F32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(dw, sx, fz, 0, 0, 0);
+          const V4i af0 = *reinterpret_cast<const V4i*>(sb + ao + (p0 / MT) * ROWS * 64 + (p0 % MT) * 2048);
+          const V4i af1 = *reinterpret_cast<const V4i*>(sb + ao + (p1 / MT) * ROWS * 64 + (p1 % MT) * 2048);
+          const V16I32 c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(af0, bf, z, 0, 0, 0);
+          const V16I32 c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(af1, bf, z, 0, 0, 0);
+          if constexpr (PRIO) {
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_setprio(0);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+#pragma unroll
+          for (int j = 0; j < 16; ++j) acc[p0][j] = __builtin_fmaf(static_cast<float>(c0[j]), sc[j], acc[p0][j]);
+#pragma unroll
+          for (int j = 0; j < 16; ++j) acc[p1][j] = __builtin_fmaf(static_cast<float>(c1[j]), sc[16 + j], acc[p1][j]);
+        }
+      }
+    }
+  };
+  // stage kc from buffer B: wait for this wave's loads of stage kc (stage kc + 1's stay in flight), barrier (every
+  // wave's loads of kc landed, every wave done with buffer (B + 2) % 3), load stage kc + 2 (clamped: the count per
+  // stage stays fixed), compute
+  const auto stage = [&](std::uint32_t kc, auto bufc) {
+    constexpr std::uint32_t B = decltype(bufc)::value;
+    __builtin_amdgcn_sched_barrier(0);  // stages do not interleave: one stage's MFMA results live at a time
+    WaitVmem<SPR + SPS>();
+    __builtin_amdgcn_s_barrier();
+    issue(min(kc + 2, nk - 1), (B + 2) % 3);
+    compute(bufc);
+#pragma unroll
+    for (int p = 0; p < NT; ++p) PinVgprs(acc[p]);  // the stage's epilogue stays in the stage
+  };
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  using B2 = std::integral_constant<int, 2>;
+  issue(0, 0);
+  issue(min(1u, nk - 1), 1);
+  std::uint32_t kc = 0;
+  for (; kc + 3 <= nk; kc += 3) {
+    stage(kc, B0{});
+    stage(kc + 1, B1{});
+    stage(kc + 2, B2{});
+  }
+  if (kc < nk) stage(kc++, B0{});
+  if (kc < nk) stage(kc++, B1{});
+  WaitVmem<0>();  // no DMA may land after the block's LDS is released
+  if (tok >= ntok) return;
+  float* yt = y + static_cast<std::size_t>(yrow0 + tok) * ystride;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const std::uint32_t r = r0 + wr * MT * 32 + mt * 32 + g * 8 + fh * 4;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[e] = NMAT == 2 ? Silu(acc[mt][4 * g + e]) * acc[MT + mt][4 * g + e] : acc[mt][4 * g + e];
+      if (r + 3 < rows && ystride % 4 == 0) {
+        *reinterpret_cast<float4*>(yt + r) = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (r + e < rows) yt[r + e] = v[e];
+      }
+    }
+}
+}  // namespace halo
+
+// Dense: 128 rows x 128 tokens per block (8 waves of 64 rows x 32 tokens), LDS-DMA staged.
+// grid (ceil(rows / 128), ceil(T / 128)), block 512. y[t * ystride + r]. rows * qstride < 2^32.
 extern "C" __global__ void __launch_bounds__(512) halo_gemm_q8a8_mfma32(
     const std::int8_t* __restrict__ qs, const std::uint16_t* __restrict__ d, const std::int8_t* __restrict__ xq,
     const float* __restrict__ xs, float* __restrict__ y, std::uint32_t rows, std::uint32_t cols,
     std::uint32_t qstride, std::uint32_t T, std::uint32_t ystride) {
   const std::uint32_t t0 = blockIdx.y * 128;
-  halo::GemmTileQ8<2, 2, 4, 1>(qs, d, nullptr, nullptr, rows, qstride, blockIdx.x * 128, xq, xs, nullptr, t0,
-                               min(128u, T - t0), cols, y, t0, ystride);
+  halo::GemmTileQ8Dma<2, 2, 4, 1, false, 1>(qs, d, nullptr, nullptr, rows, qstride, blockIdx.x * 128, xq, xs, nullptr,
+                                            t0, min(128u, T - t0), cols, y, t0, ystride);
 }
 
-// The same GEMM for grids of at most one block per CU (the scales of a stage's two Q8_0 blocks from one MFMA).
+// The same GEMM on the register-staged tile with paired block scales (the earlier design, kept as a second entry for
+// grids of at most one block per CU and as a cross-check: both are bit-identical to the oracle's block order).
 extern "C" __global__ void __launch_bounds__(512) halo_gemm_q8a8_mfma32_p(
     const std::int8_t* __restrict__ qs, const std::uint16_t* __restrict__ d, const std::int8_t* __restrict__ xq,
     const float* __restrict__ xs, float* __restrict__ y, std::uint32_t rows, std::uint32_t cols,

@@ -200,17 +200,36 @@ def test_synth_distribution(dev):
     assert np.array_equal(w2.host()[0], qs)  # deterministic
 
 
-@pytest.mark.parametrize("m,rows,cols", [(128, 512, 2048), (300, 1024, 4096), (2048, 256, 2048), (1100, 3840, 1024)])
+@pytest.mark.parametrize("m,rows,cols", [(128, 512, 2048), (300, 1024, 4096), (2048, 256, 2048), (1100, 3840, 1024),
+                                         (200, 200, 64), (77, 136, 128), (130, 200, 192), (64, 256, 320)])
 def test_mfma_gemm_prefill_tiles(dev, m, rows, cols):
-    """Prefill-sized M (>= 64) runs the 128 x 128 LDS-tiled kernel (v_mfma_i32_32x32x32_i8, one MFMA per Q8_0 block
-    and 32 x 32 tile); dense output, ragged M. Grids of at most 256 blocks take the paired-scale variant
-    (halo_gemm_q8a8_mfma32_p), the last case (270 blocks) the other."""
+    """Prefill-sized M (>= 64) runs the 128 x 128 LDS-DMA-staged kernel halo_gemm_q8a8_mfma32 (v_mfma_i32_32x32x32_i8,
+    one MFMA per Q8_0 block and 32 x 32 tile); dense output, ragged M and rows. cols 64 .. 320 cover one to five
+    64-column stages, i.e. the stage loop's tails after whole rounds of three buffers."""
     rng = np.random.default_rng(m + rows)
     w, xq, xs, want, mag = _gemv_case(dev, rng, rows, cols, m)
     gq, gs = dev.to_device(xq), dev.to_device(xs)
     gy = dev.array((m, rows), np.float32)
     dev.op("matvec_q8a8", C_ref(w), gq.ptr, gs.ptr, gy.ptr, m, rows)
     _check_y(gy.download(), want, mag)
+
+
+@pytest.mark.parametrize("m,rows,cols", [(300, 1024, 4096), (130, 200, 192)])
+def test_mfma_gemm_staging_variants_bitwise(dev, m, rows, cols):
+    """The LDS-DMA tile (halo_gemm_q8a8_mfma32) and the register-staged one (halo_gemm_q8a8_mfma32_p) do the same
+    arithmetic in the same block order: bitwise equal outputs, both within the oracle's bar."""
+    rng = np.random.default_rng(m * 7 + cols)
+    w, xq, xs, want, mag = _gemv_case(dev, rng, rows, cols, m)
+    gq, gs = dev.to_device(xq), dev.to_device(xs)
+    outs = []
+    for name in ("halo_gemm_q8a8_mfma32", "halo_gemm_q8a8_mfma32_p"):
+        gy = dev.array((m, rows), np.float32)
+        dev.launch(name, ((rows + 127) // 128, (m + 127) // 128), (512,),
+                   [w.qs, w.d, gq, gs, gy, ("u32", rows), ("u32", cols), ("u32", w.qstride), ("u32", m),
+                    ("u32", rows)])
+        outs.append(gy.download())
+    _check_y(outs[0], want, mag)
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
 
 
 @pytest.mark.parametrize("nb,r", [(1, 4), (3, 2), (8, 1)])

@@ -1,5 +1,6 @@
 // MoE decode dispatch (FlashNextGpu::Moe, src/engine/flash_next_gpu.cpp:697-845, and the session-union path of
-// StepBatch, src/engine/batch_decode.cpp): four launches over device-resident routing, no host round trip.
+// StepBatch, src/engine/batch_decode.cpp): four launches over device-resident routing (three at one token: the
+// routing folded into the gate/up launch), no host round trip.
 // Workspace: logits, shared logit, quantized x, ids/weights, h in fp32 (rows t*k+s routed, T*k+t shared).
 #include "engine.hpp"
 
@@ -99,19 +100,27 @@ int MoeDecode(halo_engine* eng, const halo_moe_weights* w, const float* x, const
                           Ptr(v.shared_logit), Ptr(v.xq), Ptr(v.xs), U32(E), U32(H), U32(T)};
     if (Launch(eng, "halo_moe_router", D3(E + 1 + qblocks), D3(256), a, err, errlen) != 0) return -1;
   }
-  // 2. softmax / top-k, one block per token
-  {
-    const halo_arg a[] = {Ptr(v.logits), Ptr(v.ids), Ptr(v.weights), U32(E), U32(k)};
-    if (Launch(eng, "halo_moe_topk", D3(T), D3(CeilDiv(E, 64) * 64), a, err, errlen) != 0) return -1;
-  }
-  // 3. gate/up over the union of experts + SwiGLU
-  {
+  if (H != 1024 && H != 2048 && H != 4096) return SetErr(err, errlen, "moe: hidden %u has no gate/up instance", H), -1;
+  if (T == 1) {
+    // 2 + 3. one token: the routing runs in every routed gate/up block (cheaper than a launch of its own)
+    const halo_arg a[] = {Ptr(w->gate.qs), Ptr(w->gate.d), Ptr(w->up.qs), Ptr(w->up.d),
+                          Ptr(shared ? w->shared_gate_proj.qs : nullptr), Ptr(shared ? w->shared_gate_proj.d : nullptr),
+                          Ptr(shared ? w->shared_up.qs : nullptr), Ptr(shared ? w->shared_up.d : nullptr),
+                          Ptr(v.xq), Ptr(v.xs), Ptr(v.logits), Ptr(v.ids), Ptr(v.weights), Ptr(v.h), U32(E), U32(F),
+                          U32(SF), U32(k), U32(v.hstride)};
+    char name[48];
+    std::snprintf(name, sizeof name, "halo_moe_gate_up_topk_q8_s%u%s", H / 1024, E <= 512 ? "_e512" : "");
+    if (Launch(eng, name, D3(k + 1, v.hstride / 4), D3(256), a, err, errlen) != 0) return -1;
+  } else {
+    // 2. softmax / top-k, one block per token
+    const halo_arg t[] = {Ptr(v.logits), Ptr(v.ids), Ptr(v.weights), U32(E), U32(k)};
+    if (Launch(eng, "halo_moe_topk", D3(T), D3(CeilDiv(E, 64) * 64), t, err, errlen) != 0) return -1;
+    // 3. gate/up over the union of experts + SwiGLU
     const halo_arg a[] = {Ptr(w->gate.qs), Ptr(w->gate.d), Ptr(w->up.qs), Ptr(w->up.d),
                           Ptr(shared ? w->shared_gate_proj.qs : nullptr), Ptr(shared ? w->shared_gate_proj.d : nullptr),
                           Ptr(shared ? w->shared_up.qs : nullptr), Ptr(shared ? w->shared_up.d : nullptr),
                           Ptr(v.xq), Ptr(v.xs), Ptr(v.ids), Ptr(v.h), U32(T), U32(F), U32(SF), U32(k),
                           U32(v.hstride)};
-    if (H != 1024 && H != 2048 && H != 4096) return SetErr(err, errlen, "moe: hidden %u has no gate/up instance", H), -1;
     const char* name = H == 1024 ? "halo_moe_gate_up_q8_s1" : H == 2048 ? "halo_moe_gate_up_q8_s2" : "halo_moe_gate_up_q8_s4";
     if (Launch(eng, name, D3(T * k + 1, v.hstride / 4), D3(256), a, err, errlen) != 0) return -1;
   }

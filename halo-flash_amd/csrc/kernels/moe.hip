@@ -8,7 +8,8 @@
 // Launches (all take device buffers only, so one captured graph replays for any routing):
 //   1. halo_moe_router     logits[t][e] = W_r[e] . x[t] (fp32), shared-gate logit, x quantized per 32 (int8);
 //      or halo_moe_router_n_* (T <= 4), which also forms x = RMSNorm(res + delta) * w itself (the FFN norm).
-//   2. halo_moe_topk       one block per token: softmax, top-k (ties -> lower id), renormalized weights.
+//   2. halo_moe_topk       one block per token: softmax, top-k (ties -> lower id), renormalized weights; at T = 1
+//                          folded into the gate/up launch instead (halo_moe_gate_up_topk_q8_*: 3 launches).
 //   3. halo_moe_gate_up_q8 block (routed pair, 4 ff rows): the first token that selected an expert computes it for
 //                          every token that selected it (the union of experts: weights streamed once), h =
 //                          SiLU(g) * u in fp32. One more block column is the shared expert.
@@ -468,13 +469,18 @@ extern "C" __global__ void __launch_bounds__(1024)
 // bucketing pass. Block x = T * k is the shared expert for all tokens. Gate/up [E][ff][H] repacked Q8_0 (row
 // stride H), shared gate/up [sff][H]. Output h = SiLU(gate) * up in fp32: h [T * k + T][hstride] (row t * k + s for
 // routed pairs, T * k + t for the shared expert).
-template <int kSteps>
+// kTopKPer > 0 (one token): the routing is done here, not by a halo_moe_topk launch before. Every routed block runs
+// WaveTopK from the logits in its first wave (the shared expert's blocks skip it) and block (0, 0) also writes ids /
+// weights for the down launch. At one token the redundant ranking (one wave per block) costs less than a launch.
+template <int kSteps, int kTopKPer = 0>
 __device__ __forceinline__ void MoeGateUp(
     const std::int8_t* __restrict__ gq, const std::uint16_t* __restrict__ gd, const std::int8_t* __restrict__ uq,
     const std::uint16_t* __restrict__ ud, const std::int8_t* __restrict__ sgq, const std::uint16_t* __restrict__ sgd,
     const std::int8_t* __restrict__ suq, const std::uint16_t* __restrict__ sud, const std::int8_t* __restrict__ xq,
-    const float* __restrict__ xs, const std::uint32_t* __restrict__ ids, float* __restrict__ h, std::uint32_t T,
-    std::uint32_t ff, std::uint32_t sff, std::uint32_t k, std::uint32_t hstride) {
+    const float* __restrict__ xs, const std::uint32_t* __restrict__ ids_in, float* __restrict__ h, std::uint32_t T,
+    std::uint32_t ff, std::uint32_t sff, std::uint32_t k, std::uint32_t hstride,
+    const float* __restrict__ logits = nullptr, std::uint32_t E = 0, std::uint32_t* __restrict__ ids_out = nullptr,
+    float* __restrict__ w_out = nullptr) {
   constexpr std::uint32_t H = kSteps * kWave * 16;
   constexpr std::uint32_t nblk = H / 32;
   const std::uint32_t px = blockIdx.x;
@@ -484,14 +490,26 @@ __device__ __forceinline__ void MoeGateUp(
   __shared__ std::uint32_t rows_s[kMoeMaxT];  // h row of each pair, ascending token
   __shared__ std::uint32_t tokmask;
   __shared__ std::uint32_t owner;
+  __shared__ std::uint32_t ids_l[kTopKPer > 0 ? 16 : 1];
+  __shared__ float w_l[kTopKPer > 0 ? 16 : 1];
+  __shared__ TopKScratch tsc[1];
   std::uint32_t np, f;
   std::size_t e = 0;
+  const std::uint32_t* ids = ids_in;
   if (shared) {
     if (sgq == nullptr || blockIdx.y * (blockDim.x / kWave) >= sff) return;
     np = T;
     f = sff;
   } else {
     if (blockIdx.y * (blockDim.x / kWave) >= ff) return;
+    if constexpr (kTopKPer > 0) {
+      if (wave == 0) {
+        const bool first = blockIdx.x == 0 && blockIdx.y == 0;
+        WaveTopK<kTopKPer>(logits, E, k, first ? ids_out : nullptr, first ? w_out : nullptr, ids_l, w_l, tsc[0]);
+      }
+      __syncthreads();
+      ids = ids_l;
+    }
     e = ids[px];
     np = 0;
     f = ff;
@@ -569,6 +587,26 @@ HALO_MOE_GATE_UP(1)
 HALO_MOE_GATE_UP(2)
 HALO_MOE_GATE_UP(4)
 #undef HALO_MOE_GATE_UP
+
+// The gate/up launch with the routing of its one token folded in: logits [E] (E <= 512 for _e512, <= 1024
+// otherwise) -> ids / weights [k] (written by block (0, 0), read by the down launch), then as above with T = 1.
+// grid (k + 1, ceil(max(ff, sff) / 4)), block 256.
+#define HALO_MOE_GATE_UP_TOPK(S, NAME, PER)                                                                        \
+  extern "C" __global__ void __launch_bounds__(256) NAME(                                                          \
+      const std::int8_t* gq, const std::uint16_t* gd, const std::int8_t* uq, const std::uint16_t* ud,             \
+      const std::int8_t* sgq, const std::uint16_t* sgd, const std::int8_t* suq, const std::uint16_t* sud,         \
+      const std::int8_t* xq, const float* xs, const float* logits, std::uint32_t* ids, float* weights, float* h,  \
+      std::uint32_t E, std::uint32_t ff, std::uint32_t sff, std::uint32_t k, std::uint32_t hstride) {             \
+    MoeGateUp<S, PER>(gq, gd, uq, ud, sgq, sgd, suq, sud, xq, xs, nullptr, h, 1, ff, sff, k, hstride, logits, E,  \
+                      ids, weights);                                                                               \
+  }
+HALO_MOE_GATE_UP_TOPK(1, halo_moe_gate_up_topk_q8_s1, 16)
+HALO_MOE_GATE_UP_TOPK(2, halo_moe_gate_up_topk_q8_s2, 16)
+HALO_MOE_GATE_UP_TOPK(4, halo_moe_gate_up_topk_q8_s4, 16)
+HALO_MOE_GATE_UP_TOPK(1, halo_moe_gate_up_topk_q8_s1_e512, 8)
+HALO_MOE_GATE_UP_TOPK(2, halo_moe_gate_up_topk_q8_s2_e512, 8)
+HALO_MOE_GATE_UP_TOPK(4, halo_moe_gate_up_topk_q8_s4_e512, 8)
+#undef HALO_MOE_GATE_UP_TOPK
 
 namespace {
 constexpr int kDownRows = 8;  // output rows per block: 4 passes x 2 rows (a row is 32 lanes x 16 bytes)

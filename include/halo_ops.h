@@ -129,7 +129,8 @@ typedef struct halo_moe_weights {
 size_t halo_op_moe_workspace_bytes(const halo_moe_weights* w, uint32_t tokens);
 
 /* out [T][hidden] = MoE(x [T][hidden]); 4 launches (router, top-k, gate/up over the union of experts, down +
- * combine), no allocation, no host round trip (routing stays on the device). `ws` holds halo_op_moe_workspace_bytes; its layout is returned through halo_moe_views for
+ * combine; at T = 1, 3: the top-k runs inside the gate/up launch), no allocation, no host round trip (routing stays
+ * on the device). `ws` holds halo_op_moe_workspace_bytes; its layout is returned through halo_moe_views for
  * inspection. */
 typedef struct halo_moe_views {
   float* logits;          /* [T][n_experts] */

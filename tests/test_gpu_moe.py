@@ -200,3 +200,26 @@ def test_moe_decode_norm_equals_norm_then_moe(dev, layer, T):
             assert np.min(np.abs(np.diff(srt[: k + 1]))) < 1e-5, "routing differs away from a tie"
             continue
         assert np.all(np.abs(on[t] - orr[t]) <= 1e-5 * np.abs(orr[t]).max() + 1e-6)
+
+
+def test_moe_decode_workspace_reuse_across_token_counts(dev, layer):
+    """One workspace for calls with T = 1, 4, 16, 2, 1, 3 in turn (T = 1: the routing inside the gate/up launch; else
+    a top-k launch of its own): after every call the ids are the oracle's RouteTopK of the GPU logits and the output
+    equals a call on a fresh workspace bitwise."""
+    L = layer
+    ws = L.workspace(16)
+    o = O.oracle()
+    for i, T in enumerate((1, 4, 16, 2, 1, 3)):
+        rng = np.random.default_rng(100 + i)
+        gx = dev.to_device(rng.normal(0, 1, (T, L.H)).astype(np.float32))
+        out, out_fresh = dev.array((T, L.H), np.float32), dev.array((T, L.H), np.float32)
+        L.forward(gx, out, T, ws)
+        L.forward(gx, out_fresh, T, L.workspace(T))
+        v = L.views(T, ws)
+        logits = _view(ws, ws.ptr, v.logits, T * L.E, np.float32).reshape(T, L.E)
+        ids = _view(ws, ws.ptr, v.ids, T * L.k, np.uint32).reshape(T, L.k)
+        for t in range(T):
+            oi, ow = np.zeros(L.k, np.uint32), np.zeros(L.k, np.float32)
+            o.or_route_topk(np.ascontiguousarray(logits[t]), L.E, L.k, oi, ow)
+            assert ids[t].tolist() == oi.tolist(), f"call {i} (T={T}) token {t}"
+        assert np.array_equal(out.download().view(np.uint32), out_fresh.download().view(np.uint32))

@@ -27,8 +27,9 @@ def twin(max_sessions=2, prefix=0, ctx=64):
 
 
 def _flips_ok(rep):
-    print(f"{rep.flips} flips in {rep.codes} codes; worst error / bar per stage {rep.worst}")
+    print(f"{rep.flips} flips and {rep.loose} cancellation-bound codes in {rep.codes} codes; worst error / bar per stage {rep.worst}")
     assert rep.flips <= max(4, rep.codes // 10000)
+    assert rep.loose <= max(64, rep.codes // 1000)
 
 
 def test_ragged_prefill_then_decode(dev):

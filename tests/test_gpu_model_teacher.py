@@ -45,8 +45,9 @@ def test_twin_every_layer_every_step(dev):
         rng = np.random.default_rng(3)
         prompt = [rng.integers(0, cfg.vocab, 12).astype(np.uint32)]
         rep = _run(model, cfg, prompt, 20)
-        print(f"twin S=1: {rep.flips} flips in {rep.codes} codes; worst error / bar per stage {rep.worst}")
+        print(f"twin S=1: {rep.flips} flips and {rep.loose} cancellation-bound codes in {rep.codes} codes; worst error / bar per stage {rep.worst}")
         assert rep.flips <= max(4, rep.codes // 10000)
+        assert rep.loose <= max(64, rep.codes // 1000)
     finally:
         model.close()
 
@@ -59,8 +60,9 @@ def test_twin_two_sessions(dev):
         rng = np.random.default_rng(4)
         prompt = [rng.integers(0, cfg.vocab, 6).astype(np.uint32) for _ in range(2)]
         rep = _run(model, cfg, prompt, 8, S=2)
-        print(f"twin S=2: {rep.flips} flips in {rep.codes} codes; worst {rep.worst}")
+        print(f"twin S=2: {rep.flips} flips and {rep.loose} cancellation-bound codes in {rep.codes} codes; worst {rep.worst}")
         assert rep.flips <= max(4, rep.codes // 10000)
+        assert rep.loose <= max(64, rep.codes // 1000)
     finally:
         model.close()
 
@@ -75,7 +77,8 @@ def test_c4_full_shape_every_layer(dev):
         rng = np.random.default_rng(8)
         prompt = [rng.integers(0, cfg.vocab, 4).astype(np.uint32)]
         rep = _run(model, cfg, prompt, 5, trace_every=2)
-        print(f"C4: {rep.flips} flips in {rep.codes} codes; worst error / bar per stage {rep.worst}")
+        print(f"C4: {rep.flips} flips and {rep.loose} cancellation-bound codes in {rep.codes} codes; worst error / bar per stage {rep.worst}")
         assert rep.flips <= max(8, rep.codes // 10000)
+        assert rep.loose <= max(64, rep.codes // 1000)
     finally:
         model.close()

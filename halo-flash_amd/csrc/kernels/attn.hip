@@ -29,14 +29,15 @@ constexpr int kMaxQ = 32;     // query vectors per block (sessions * G)
 // Every K and V load of the chunk (64 KB) is issued before any arithmetic, so a block keeps its whole chunk in
 // flight. Scores: 16-lane row r of the block owns tokens r and r + 16, lane `sub` of the row dims
 // {4 (16 u + sub) .. +4 : u < 4} (each load instruction reads 256 contiguous bytes per row); the 16 partial dots
-// are summed with row DPP. Weighted V: thread = one of the 256 dims, all 32 tokens in registers.
+// are summed with row DPP. V arrives as 16-byte loads and is staged through LDS (over the queries, once the scores
+// are done). Weighted V: thread = one of the 256 dims, all 32 tokens in registers.
 extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
     const float* __restrict__ q, const float* __restrict__ kpool, const float* __restrict__ vpool,
     const std::uint32_t* __restrict__ pages, const std::uint32_t* __restrict__ nkv, float* __restrict__ pm,
     float* __restrict__ pl, float* __restrict__ pacc, std::uint32_t S, std::uint32_t Hq, std::uint32_t Hkv,
     std::uint32_t prefix, std::uint32_t max_pages, std::uint32_t prefix_chunks, std::uint32_t suffix_chunks) {
   __shared__ float qs[kMaxQ][kHd];       // 32 KB
-  __shared__ float sc[kMaxQ][kChunk + 1];
+  __shared__ __attribute__((aligned(16))) float sc[kMaxQ][kChunk + 4];  // rows 16-byte aligned: vector reads
   static_assert(kChunk == 32 && kPage == 16, "two pages per chunk, two tokens per 16-lane row");
   const std::uint32_t G = Hq / Hkv, x = blockIdx.x, kvh = x % Hkv, c = x / Hkv;
   const std::uint32_t t = threadIdx.x, wave = t / kWave, lane = t % kWave;
@@ -74,9 +75,18 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
 #pragma unroll
     for (int u = 0; u < 4; ++u) kf[h][u] = kr[16 * u + sub];
   }
-  float vv[kChunk];
+  // V as 16-byte loads of the two pages (each page's 16 rows are 16 KB contiguous; thread t takes float4 t of every
+  // 4 KB part: row 4 part + t / 64, dims 4 (t % 64) ..): 4-byte loads of a column would take 32 instructions per
+  // thread and run the chunk's V stream at half the rate. Staged through LDS below, so the weighted sum still reads
+  // one dim of every row.
+  float4 vq[2][4];
 #pragma unroll
-  for (int j = 0; j < kChunk; ++j) vv[j] = row_of(vpool, j)[t];
+  for (int h = 0; h < 2; ++h) {
+    const float4* vp = reinterpret_cast<const float4*>(vpool + (static_cast<std::size_t>(h ? pg1 : pg0) * Hkv + kvh) *
+                                                                   kPage * kHd);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) vq[h][u] = vp[u * 256 + t];
+  }
   // queries of this kv head: slot i = session * G + g (prefix) or g (suffix)
   for (std::uint32_t i = t; i < nq * (kHd / 4); i += blockDim.x) {
     const std::uint32_t qi = i / (kHd / 4), d4 = i % (kHd / 4);
@@ -87,23 +97,45 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
   __syncthreads();
   const float scale = 1.0f / sqrtf(static_cast<float>(kHd));
   const bool live0 = start + r < limit, live1 = start + r + 16 < limit;
-  for (std::uint32_t i = 0; i < nq; ++i) {
-    const float4* qv = reinterpret_cast<const float4*>(&qs[i][0]);
-    float s0 = 0.0f, s1 = 0.0f;
+  // queries in groups of 8, the group's dot products and row reductions interleaved (independent chains; each
+  // query's arithmetic is the same as one at a time)
+  constexpr int kQG = 8;
+  for (std::uint32_t i0 = 0; i0 < nq; i0 += kQG) {
+    float s0[kQG], s1[kQG];
+#pragma unroll
+    for (int k = 0; k < kQG; ++k) {
+      const float4* qv = reinterpret_cast<const float4*>(&qs[min(i0 + k, nq - 1)][0]);
+      s0[k] = 0.0f;
+      s1[k] = 0.0f;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float4 b = qv[16 * u + sub];
+        s0[k] += kf[0][u].x * b.x + kf[0][u].y * b.y + kf[0][u].z * b.z + kf[0][u].w * b.w;
+        s1[k] += kf[1][u].x * b.x + kf[1][u].y * b.y + kf[1][u].z * b.z + kf[1][u].w * b.w;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kQG; ++k) {
+      s0[k] = halo::GroupSum<16>(s0[k]);
+      s1[k] = halo::GroupSum<16>(s1[k]);
+    }
+    if (sub == 0)
+#pragma unroll
+      for (int k = 0; k < kQG; ++k)
+        if (i0 + k < nq) {
+          sc[i0 + k][r] = live0 ? s0[k] * scale : -INFINITY;
+          sc[i0 + k][r + 16] = live1 ? s1[k] * scale : -INFINITY;
+        }
+  }
+  __syncthreads();  // the scores are in sc and qs is free: the V rows go there (rows past the visible range as 0)
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const float4 b = qv[16 * u + sub];
-      s0 += kf[0][u].x * b.x + kf[0][u].y * b.y + kf[0][u].z * b.z + kf[0][u].w * b.w;
-      s1 += kf[1][u].x * b.x + kf[1][u].y * b.y + kf[1][u].z * b.z + kf[1][u].w * b.w;
+      const std::uint32_t j = 16 * h + 4 * u + t / 64;
+      reinterpret_cast<float4*>(&qs[j][0])[t % 64] =
+          start + j < limit ? vq[h][u] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    s0 = halo::GroupSum<16>(s0);
-    s1 = halo::GroupSum<16>(s1);
-    if (sub == 0) {
-      sc[i][r] = live0 ? s0 * scale : -INFINITY;
-      sc[i][r + 16] = live1 ? s1 * scale : -INFINITY;
-    }
-  }
-  __syncthreads();
   // softmax over the chunk per query: wave w takes queries w, w + 4, ...; lanes 0..31 are the tokens
   for (std::uint32_t i = wave; i < nq; i += 4) {
     const float s = lane < kChunk ? sc[i][lane] : -INFINITY;
@@ -118,14 +150,30 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
     }
   }
   __syncthreads();
+  // weighted V, 8 queries' sums interleaved (each still adds its tokens in order j = 0 .. 31); V and the weights
+  // are read from LDS four tokens at a time
+  for (std::uint32_t i0 = 0; i0 < nq; i0 += kQG) {
+    float acc[kQG];
 #pragma unroll
-  for (int i = 0; i < kMaxQ; ++i) {
-    if (i >= static_cast<int>(nq)) break;
-    float acc = 0.0f;
+    for (int k = 0; k < kQG; ++k) acc[k] = 0.0f;
+#pragma unroll 2
+    for (int j4 = 0; j4 < kChunk; j4 += 4) {
+      const float v0 = qs[j4][t], v1 = qs[j4 + 1][t], v2 = qs[j4 + 2][t], v3 = qs[j4 + 3][t];
 #pragma unroll
-    for (int j = 0; j < kChunk; ++j) acc += sc[i][j] * vv[j];
-    const std::uint32_t slot = is_prefix ? i : sess * G + i;
-    a_out[static_cast<std::size_t>(slot) * kHd + t] = acc;
+      for (int k = 0; k < kQG; ++k) {
+        const float4 p4 = *reinterpret_cast<const float4*>(&sc[min(i0 + k, nq - 1)][j4]);
+        acc[k] += p4.x * v0;
+        acc[k] += p4.y * v1;
+        acc[k] += p4.z * v2;
+        acc[k] += p4.w * v3;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kQG; ++k)
+      if (i0 + k < nq) {
+        const std::uint32_t slot = is_prefix ? i0 + k : sess * G + i0 + k;
+        a_out[static_cast<std::size_t>(slot) * kHd + t] = acc[k];
+      }
   }
 }
 

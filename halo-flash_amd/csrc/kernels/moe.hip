@@ -266,7 +266,21 @@ __device__ void WaveTopK(const float* logits, std::uint32_t E, std::uint32_t k, 
     n += static_cast<std::uint32_t>(__builtin_popcountll(m));
   }
   WaveSync();
-  if (n <= kCandMax) {
+  if (n <= static_cast<std::uint32_t>(kWave)) {
+    // candidate c in lane c; its rank from the other candidates read across lanes (no LDS round trip per step)
+    const float pc = sc.cp[min(lane, n - 1)];
+    const std::uint32_t ic = sc.ci[min(lane, n - 1)];
+    std::uint32_t rank = 0;
+    for (std::uint32_t j = 0; j < n; ++j) {
+      const float pj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pc), j));
+      const std::uint32_t ij = static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ic), j));
+      rank += (pj > pc) || (pj == pc && ij < ic);
+    }
+    if (lane < n && rank < k) {
+      lds_ids[rank] = ic;
+      lds_w[rank] = pc;
+    }
+  } else if (n <= kCandMax) {
     for (std::uint32_t c = lane; c < n; c += kWave) {
       const float pc = sc.cp[c];
       const std::uint32_t ic = sc.ci[c];
@@ -309,6 +323,24 @@ __device__ void WaveTopK(const float* logits, std::uint32_t E, std::uint32_t k, 
     }
   }
   WaveSync();
+  if (k <= static_cast<std::uint32_t>(kWave)) {
+    // slot s in lane s; the sum in slot order, read across lanes
+    const float ws = lds_w[min(lane, k - 1)];
+    float sum = 0.0f;
+    for (std::uint32_t s = 0; s < k; ++s)
+      sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ws), s));
+    sum = fmaxf(sum, 6.103515625e-5f);
+    if (lane < k) {
+      const float w = ws / sum;
+      lds_w[lane] = w;
+      if (ids != nullptr) {
+        ids[lane] = lds_ids[lane];
+        weights[lane] = w;
+      }
+    }
+    WaveSync();
+    return;
+  }
   if (lane == 0) {
     float sum = 0.0f;
     for (std::uint32_t s = 0; s < k; ++s) sum += lds_w[s];
@@ -532,7 +564,11 @@ __device__ __forceinline__ void MoeGateUp(
     sw[0][st] = F16(d0[static_cast<std::size_t>(jr) * nblk + c / 32]);
     sw[1][st] = F16(d1[static_cast<std::size_t>(jr) * nblk + c / 32]);
   }
-  if (shared) {
+  std::uint32_t row1 = 0;  // T = 1: the one h row (the k experts of one token are distinct: no union to form)
+  if (T == 1) {
+    np = 1;
+    row1 = shared ? k : px;
+  } else if (shared) {
     if (threadIdx.x < T) rows_s[threadIdx.x] = T * k + threadIdx.x;
   } else {
     const std::uint32_t t = px / k;
@@ -553,10 +589,10 @@ __device__ __forceinline__ void MoeGateUp(
     for (std::uint32_t i = threadIdx.x; i < T * k; i += blockDim.x)
       if (ids[i] == e) rows_s[__builtin_popcount(m & ((1u << (i / k)) - 1u))] = i;
   }
-  __syncthreads();
+  if (T > 1) __syncthreads();
   if (j >= f) return;
   for (std::uint32_t lp = 0; lp < np; ++lp) {
-    const std::uint32_t row = rows_s[lp];
+    const std::uint32_t row = T == 1 ? row1 : rows_s[lp];
     const std::uint32_t tok = shared ? row - T * k : row / k;
     const std::int8_t* xt = xq + static_cast<std::size_t>(tok) * H;
     const float* st_ = xs + static_cast<std::size_t>(tok) * nblk;

@@ -186,15 +186,16 @@ extern "C" __global__ void __launch_bounds__(256)
 namespace {
 // Softmax over E logits and top-k of the probabilities for one token, one wave (src/model/cpu_ops.cpp:187-207):
 // the k ids in descending probability (ties to the lower id) and the weights renormalized by max(sum, 2^-14),
-// the sum accumulated in slot order. Selection: tau = the k-th largest of the 64 lane maxima bounds the k-th
-// largest probability from below, so the top k are among the candidates p >= tau (at most a few per selected
-// lane); each candidate's rank among the candidates, by (probability desc, id asc), is its slot. Results go to
-// lds_ids / lds_w (k entries) and, when non-null, to ids / weights in global memory.
+// the sum accumulated in slot order. Selection: a threshold tau at or below the k-th largest of the 64 lane maxima
+// bounds the k-th largest probability from below, so the top k are among the candidates p >= tau (a few per
+// selected lane); each candidate's rank among the candidates, by (probability desc, id asc), is its slot. Results go
+// to lds_ids (k entries) and, when lds_w is non-null, the weights to lds_w and, when non-null, ids / weights to
+// global memory (a caller that needs only the ids passes lds_w = ids = weights = null and skips the renormalization).
 constexpr int kCandMax = 256;
 
 struct TopKScratch {
-  float cp[kCandMax];
-  std::uint32_t ci[kCandMax];
+  // candidate keys (probability bits << 32 | ~id), 8 pad keys past the last, and a spare slot per lane
+  std::uint64_t ck[kCandMax + 8 + 64];
   float sum;
 };
 
@@ -238,20 +239,25 @@ __device__ void WaveTopK(const float* logits, std::uint32_t E, std::uint32_t k, 
     p[i] = e < E ? p[i] / den : -1.0f;
     lm = fmaxf(lm, p[i]);
   }
-  // tau: the k-th largest lane maximum, by a bitwise search over the keys (probability bits + 1, 0 for a lane
-  // without experts; probabilities are >= 0, so their bit patterns order like the values). Every probability is
-  // >= 0, so tau = -1 admits all when k > 64.
+  // tau from a bitwise search over the lane keys (probability bits + 1, 0 for a lane without experts; probabilities
+  // are in [0, 1], so their bit patterns order like the values and stay below 2^30). The search keeps the largest thr
+  // with at least k keys >= thr, deciding bits 29 .. 18 only: thr is then the k-th largest key with its low 18 bits
+  // cleared (within 2^-5 of it), still a lower bound, for 12 dependent ballots instead of 31 at the cost of a few
+  // more candidates. Every probability is >= 0, so tau = -1 admits all when k > 64.
   float tau = -1.0f;
   if (k <= kWave) {
     const std::uint32_t key = lm >= 0.0f ? __float_as_uint(lm) + 1u : 0u;
     std::uint32_t thr = 0;
-    for (int bit = 30; bit >= 0; --bit) {
+#pragma unroll
+    for (int bit = 29; bit >= 18; --bit) {
       const std::uint32_t cand = thr | (1u << bit);
       if (static_cast<std::uint32_t>(__builtin_popcountll(__ballot(key >= cand))) >= k) thr = cand;
     }
     tau = thr == 0 ? -1.0f : __uint_as_float(thr - 1u);
   }
-  // candidates p >= tau, compacted in (i, lane) order
+  // candidates p >= tau as 64-bit keys, probability bits above and ~id below: a larger key is an earlier slot (ties
+  // in probability to the lower id; ids are distinct, so keys are). Every lane stores, a non-candidate (or one past
+  // the scratch) into its own spare slot, so no store waits on an exec mask.
   std::uint32_t n = 0;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
@@ -259,39 +265,29 @@ __device__ void WaveTopK(const float* logits, std::uint32_t E, std::uint32_t k, 
     const bool f = e < E && p[i] >= tau;
     const std::uint64_t m = __ballot(f);
     const std::uint32_t pos = n + LanesBelow(m);
-    if (f && pos < kCandMax) {
-      sc.cp[pos] = p[i];
-      sc.ci[pos] = e;
-    }
+    sc.ck[f && pos < kCandMax ? pos : kCandMax + 8 + lane] =
+        (static_cast<std::uint64_t>(__float_as_uint(p[i])) << 32) | static_cast<std::uint32_t>(~e);
     n += static_cast<std::uint32_t>(__builtin_popcountll(m));
   }
+  if (lane < 8 && n <= kCandMax) sc.ck[n + lane] = 0;  // pad keys below every candidate: reads past n count nothing
   WaveSync();
-  if (n <= static_cast<std::uint32_t>(kWave)) {
-    // candidate c in lane c; its rank from the other candidates read across lanes (no LDS round trip per step)
-    const float pc = sc.cp[min(lane, n - 1)];
-    const std::uint32_t ic = sc.ci[min(lane, n - 1)];
-    std::uint32_t rank = 0;
-    for (std::uint32_t j = 0; j < n; ++j) {
-      const float pj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pc), j));
-      const std::uint32_t ij = static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ic), j));
-      rank += (pj > pc) || (pj == pc && ij < ic);
-    }
-    if (lane < n && rank < k) {
-      lds_ids[rank] = ic;
-      lds_w[rank] = pc;
-    }
-  } else if (n <= kCandMax) {
-    for (std::uint32_t c = lane; c < n; c += kWave) {
-      const float pc = sc.cp[c];
-      const std::uint32_t ic = sc.ci[c];
+  if (n <= kCandMax) {
+    // candidate c in lane c % 64: its rank = the number of larger keys, read 8 at a time (4 loads in flight)
+    for (std::uint32_t c0 = 0; c0 < n; c0 += kWave) {
+      const std::uint32_t c = c0 + lane;
+      const std::uint64_t key = sc.ck[min(c, n - 1)];
       std::uint32_t rank = 0;
-      for (std::uint32_t j = 0; j < n; ++j) {
-        const float pj = sc.cp[j];
-        rank += (pj > pc) || (pj == pc && sc.ci[j] < ic);
+      for (std::uint32_t j = 0; j < n; j += 8) {
+        const ulonglong2 k0 = *reinterpret_cast<const ulonglong2*>(&sc.ck[j]);
+        const ulonglong2 k1 = *reinterpret_cast<const ulonglong2*>(&sc.ck[j + 2]);
+        const ulonglong2 k2 = *reinterpret_cast<const ulonglong2*>(&sc.ck[j + 4]);
+        const ulonglong2 k3 = *reinterpret_cast<const ulonglong2*>(&sc.ck[j + 6]);
+        rank += ((k0.x > key) + (k0.y > key)) + ((k1.x > key) + (k1.y > key)) + ((k2.x > key) + (k2.y > key)) +
+                ((k3.x > key) + (k3.y > key));
       }
-      if (rank < k) {
-        lds_ids[rank] = ic;
-        lds_w[rank] = pc;
+      if (c < n && rank < k) {
+        lds_ids[rank] = ~static_cast<std::uint32_t>(key);
+        if (lds_w != nullptr) lds_w[rank] = __uint_as_float(static_cast<std::uint32_t>(key >> 32));
       }
     }
   } else {
@@ -318,11 +314,12 @@ __device__ void WaveTopK(const float* logits, std::uint32_t E, std::uint32_t k, 
       if (at % kWave == lane) taken |= 1u << (at / kWave);
       if (lane == 0) {
         lds_ids[s] = at;
-        lds_w[s] = v;
+        if (lds_w != nullptr) lds_w[s] = v;
       }
     }
   }
   WaveSync();
+  if (lds_w == nullptr) return;
   if (k <= static_cast<std::uint32_t>(kWave)) {
     // slot s in lane s; the sum in slot order, read across lanes
     const float ws = lds_w[min(lane, k - 1)];
@@ -503,7 +500,8 @@ extern "C" __global__ void __launch_bounds__(1024)
 // routed pairs, T * k + t for the shared expert).
 // kTopKPer > 0 (one token): the routing is done here, not by a halo_moe_topk launch before. Every routed block runs
 // WaveTopK from the logits in its first wave (the shared expert's blocks skip it) and block (0, 0) also writes ids /
-// weights for the down launch. At one token the redundant ranking (one wave per block) costs less than a launch.
+// weights for the down launch; the other blocks need only the ids and skip the renormalization. At one token the
+// redundant ranking (one wave per block) costs less than a launch.
 template <int kSteps, int kTopKPer = 0>
 __device__ __forceinline__ void MoeGateUp(
     const std::int8_t* __restrict__ gq, const std::uint16_t* __restrict__ gd, const std::int8_t* __restrict__ uq,
@@ -537,7 +535,8 @@ __device__ __forceinline__ void MoeGateUp(
     if constexpr (kTopKPer > 0) {
       if (wave == 0) {
         const bool first = blockIdx.x == 0 && blockIdx.y == 0;
-        WaveTopK<kTopKPer>(logits, E, k, first ? ids_out : nullptr, first ? w_out : nullptr, ids_l, w_l, tsc[0]);
+        WaveTopK<kTopKPer>(logits, E, k, first ? ids_out : nullptr, first ? w_out : nullptr, ids_l, first ? w_l : nullptr,
+                           tsc[0]);
       }
       __syncthreads();
       ids = ids_l;

@@ -140,10 +140,25 @@ def test_moe_decode_matches_oracle(dev, layer, small_layer, T, shape):
         assert int(np.argmax(got[t])) == int(np.argmax(acc_e2e))
 
 
+def _topk_cases(rng, E):
+    """Rows that reach every selection path of the one-wave top-k: exact ties among few values, about 100 equal
+    maxima (more candidates than lanes), all equal (more than the candidate scratch: the arg-max fallback), 40 equal
+    maxima among distinct values, and plain normal logits."""
+    rows = [(rng.integers(-6, 6, E) * 0.25) for _ in range(3)]
+    r = rng.normal(0, 1, E) - 10.0
+    r[rng.choice(E, 100, replace=False)] = 2.5
+    rows += [r, np.full(E, 0.75)]
+    r = rng.normal(0, 1, E)
+    r[rng.choice(E, 40, replace=False)] = 4.0
+    rows += [r, rng.normal(0, 1, E), rng.normal(0, 3, E)]
+    return np.stack(rows).astype(np.float32)
+
+
 def test_router_topk_reference_named(dev):
     rng = np.random.default_rng(5)
-    T, E, k = 3, 512, 10
-    logits = (rng.integers(-6, 6, (T, E)) * 0.25).astype(np.float32)  # exact ties
+    E, k = 512, 10
+    logits = _topk_cases(rng, E)
+    T = logits.shape[0]
     gl = dev.to_device(logits)
     gi, gw = dev.array((T, k), np.uint32), dev.array((T, k), np.float32)
     dev.launch("halo_router_topk_rows", (T,), (64,), [gl, gi, gw, ("u32", E), ("u32", k)])
@@ -153,6 +168,32 @@ def test_router_topk_reference_named(dev):
         O.oracle().or_route_topk(logits[t], E, k, oi, ow)
         assert ids[t].tolist() == oi.tolist()
         assert np.allclose(w[t], ow, rtol=1e-6)
+
+
+def test_gate_up_topk_one_token_selection_paths(dev, layer):
+    """The one-token gate/up launch with its routing folded in (halo_moe_gate_up_topk_q8_s2_e512) on crafted logits
+    that reach every selection path: block (0, 0)'s ids / weights equal the oracle's RouteTopK, and every h row
+    (the k routed slots and the shared expert) equals the plain gate/up launch given those ids, bitwise."""
+    L = layer
+    rng = np.random.default_rng(17)
+    E, k, F, H_ = L.E, L.k, L.F, L.H
+    x = rng.normal(0, 1, H_).astype(np.float32)
+    xq, xs = O.quantize(x[None, :])
+    gxq, gxs = dev.to_device(xq), dev.to_device(xs)
+    for row in _topk_cases(rng, E):
+        gl = dev.to_device(row)
+        ids, w = dev.array(k, np.uint32), dev.array(k, np.float32)
+        h1, h2 = dev.array((k + 1, F), np.float32), dev.array((k + 1, F), np.float32)
+        common = [L.gate.qs, L.gate.d, L.up.qs, L.up.d, L.sg.qs, L.sg.d, L.su.qs, L.su.d, gxq, gxs]
+        dev.launch("halo_moe_gate_up_topk_q8_s2_e512", (k + 1, F // 4), (256,),
+                   common + [gl, ids, w, h1, ("u32", E), ("u32", F), ("u32", F), ("u32", k), ("u32", F)])
+        oi, ow = np.zeros(k, np.uint32), np.zeros(k, np.float32)
+        O.oracle().or_route_topk(row, E, k, oi, ow)
+        assert ids.download().tolist() == oi.tolist()
+        assert np.allclose(w.download(), ow, rtol=1e-6, atol=0)
+        dev.launch("halo_moe_gate_up_q8_s2", (k + 1, F // 4), (256,),
+                   common + [dev.to_device(oi), h2, ("u32", 1), ("u32", F), ("u32", F), ("u32", k), ("u32", F)])
+        assert np.array_equal(h1.download().view(np.uint32), h2.download().view(np.uint32))
 
 
 @pytest.mark.parametrize("T", [1, 2, 4])

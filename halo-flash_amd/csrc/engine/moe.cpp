@@ -90,8 +90,9 @@ int MoeDecode(halo_engine* eng, const halo_moe_weights* w, const float* x, const
     const halo_arg a[] = {Ptr(w->router), Ptr(shared ? w->shared_gate : nullptr), Ptr(in->x), Ptr(in->delta),
                           Ptr(in->norm_w), Ptr(in->res_out), Ptr(v.logits), Ptr(v.shared_logit), Ptr(v.xq),
                           Ptr(v.xs), U32(E), U32(T), Val(in->eps)};
-    if (Launch(eng, H == 2048 ? "halo_moe_router_n_h2048" : "halo_moe_router_n_h4096", D3(CeilDiv(E + 1, 4)),
-               D3(256), a, err, errlen) != 0)
+    const char* rname = T == 1 ? (H == 2048 ? "halo_moe_router_n1_h2048" : "halo_moe_router_n1_h4096")
+                               : (H == 2048 ? "halo_moe_router_n_h2048" : "halo_moe_router_n_h4096");
+    if (Launch(eng, rname, D3(CeilDiv(E + 1, 4)), D3(256), a, err, errlen) != 0)
       return -1;
   } else {
     // 1. router logits + shared gate logit + x quantized

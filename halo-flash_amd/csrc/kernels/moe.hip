@@ -85,15 +85,15 @@ extern "C" __global__ void __launch_bounds__(256)
 // quantization xq / xs of x_t for the experts. Wave w of block b dots router row r = 4 b + w (r = E: the shared gate
 // row, skipped when null) with x_t from LDS.
 //   grid (ceil((E + 1) / 4)), block 256. router [E][H] fp32, logits [T][E], sgl [T].
-template <int KC>
+template <int KC, int kMaxT>
 __device__ __forceinline__ void MoeRouterN(const float* __restrict__ router, const float* __restrict__ sgate,
                                            const float* __restrict__ res, const float* __restrict__ delta,
                                            const float* __restrict__ norm_w, float* __restrict__ res_out,
                                            float* __restrict__ logits, float* __restrict__ sgl,
                                            std::int8_t* __restrict__ xq, float* __restrict__ xs, std::uint32_t E,
                                            std::uint32_t T, float eps) {
-  constexpr std::uint32_t H = KC * 2048, kMaxT = 4, kF4 = H / 256;  // float4 chunks of a row per lane
-  __shared__ __attribute__((aligned(16))) float xl[kMaxT * 2048];
+  constexpr std::uint32_t H = KC * 2048, kF4 = H / 256;  // float4 chunks of a row per lane
+  __shared__ __attribute__((aligned(16))) float xl[kMaxT * H < 8192 ? kMaxT * H : 8192];  // T * H <= 8192
   __shared__ float red[kMaxT][4];
   const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const std::uint32_t r = blockIdx.x * 4 + wave;
@@ -170,18 +170,19 @@ __device__ __forceinline__ void MoeRouterN(const float* __restrict__ router, con
   }
 }
 
-extern "C" __global__ void __launch_bounds__(256)
-    halo_moe_router_n_h2048(const float* router, const float* sgate, const float* res, const float* delta,
-                            const float* norm_w, float* res_out, float* logits, float* sgl, std::int8_t* xq,
-                            float* xs, std::uint32_t E, std::uint32_t T, float eps) {
-  MoeRouterN<1>(router, sgate, res, delta, norm_w, res_out, logits, sgl, xq, xs, E, T, eps);
-}
-extern "C" __global__ void __launch_bounds__(256)
-    halo_moe_router_n_h4096(const float* router, const float* sgate, const float* res, const float* delta,
-                            const float* norm_w, float* res_out, float* logits, float* sgl, std::int8_t* xq,
-                            float* xs, std::uint32_t E, std::uint32_t T, float eps) {
-  MoeRouterN<2>(router, sgate, res, delta, norm_w, res_out, logits, sgl, xq, xs, E, T, eps);
-}
+// _n: T <= 4; _n1: T = 1 (one residual row loaded, not four).
+#define HALO_MOE_ROUTER_N(NAME, KC, NT)                                                                            \
+  extern "C" __global__ void __launch_bounds__(256)                                                               \
+      NAME(const float* router, const float* sgate, const float* res, const float* delta, const float* norm_w,     \
+           float* res_out, float* logits, float* sgl, std::int8_t* xq, float* xs, std::uint32_t E, std::uint32_t T, \
+           float eps) {                                                                                            \
+    MoeRouterN<KC, NT>(router, sgate, res, delta, norm_w, res_out, logits, sgl, xq, xs, E, T, eps);               \
+  }
+HALO_MOE_ROUTER_N(halo_moe_router_n_h2048, 1, 4)
+HALO_MOE_ROUTER_N(halo_moe_router_n_h4096, 2, 4)
+HALO_MOE_ROUTER_N(halo_moe_router_n1_h2048, 1, 1)
+HALO_MOE_ROUTER_N(halo_moe_router_n1_h4096, 2, 1)
+#undef HALO_MOE_ROUTER_N
 
 namespace {
 // Softmax over E logits and top-k of the probabilities for one token, one wave (src/model/cpu_ops.cpp:187-207):

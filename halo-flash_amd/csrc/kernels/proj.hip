@@ -87,7 +87,8 @@ __device__ __forceinline__ void ProjQ8(const float* __restrict__ x, const float*
   const std::uint32_t task0 = blockIdx.x * (blockDim.x / kWave) * TPW + wave;
   // Order of issue: token 0's prologue inputs (L2 hits), then the weights of this wave's first two tasks (HBM),
   // so the prologue of token 0 waits only for its own loads while the weight stream is in flight.
-  constexpr int KC = kProjMaxCols / 2048;
+  // 2048-column chunks of the row per 256 threads: cols <= 64 LPR, so one chunk unless LPR = 64
+  constexpr int KC = LPR == 64 ? 2 : 1;
   halo::Row8<KC> row, aux;
   float w8[8];
   int4 xv = make_int4(0, 0, 0, 0);

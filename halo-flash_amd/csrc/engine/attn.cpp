@@ -74,6 +74,43 @@ int halo_op_attn_decode_q8(halo_engine* eng, const halo_paged_kv* kv, const floa
                 D3(256), a, err, errlen);
 }
 
+int halo_op_attn_decode_step_q8(halo_engine* eng, const halo_paged_kv* kv, const float* qg, const float* k,
+                                const float* v, const float* q_norm, const float* k_norm, uint32_t rot, float theta,
+                                float eps, float* o, int8_t* oq, float* os, uint32_t Hq, void* ws, size_t ws_bytes,
+                                char* err, size_t errlen) {
+  if (RequirePtrs(err, errlen, "attn_decode_step_q8",
+                  {{"kv", kv}, {"qg", qg}, {"k", k}, {"v", v}, {"q_norm", q_norm}, {"k_norm", k_norm}, {"ws", ws}}) != 0)
+    return -1;
+  if (Check(kv, Hq, err, errlen) != 0) return -1;
+  if (rot == 0 || rot % 2 != 0 || rot > 128)
+    return SetErr(err, errlen, "attn decode step: rotary dims %u must be even and <= 128", rot), -1;
+  if (o == nullptr && oq == nullptr) return SetErr(err, errlen, "attn decode step: no output"), -1;
+  if ((oq == nullptr) != (os == nullptr)) return SetErr(err, errlen, "attn decode step: oq and os go together"), -1;
+  const std::size_t need = halo_op_attn_decode_workspace_bytes(kv, Hq);
+  if (ws_bytes < need) return SetErr(err, errlen, "attn: workspace %zu < %zu", ws_bytes, need), -1;
+  std::uint32_t pc, sc;
+  Chunks(kv, &pc, &sc);
+  const std::uint32_t S = kv->sessions, Hkv = kv->kv_heads;
+  const std::size_t items = static_cast<std::size_t>(Hkv) * (pc + S * sc);
+  const std::size_t slots = S * (Hq / Hkv);
+  float* pm = static_cast<float*>(ws);
+  float* pl = pm + items * slots;
+  float* pacc = pl + items * slots;
+  {
+    const halo_arg a[] = {Ptr(qg), Ptr(k), Ptr(v), Ptr(q_norm), Ptr(k_norm), Ptr(kv->k_pool), Ptr(kv->v_pool),
+                          Ptr(kv->pages), Ptr(kv->nkv), Ptr(pm), Ptr(pl), Ptr(pacc), U32(S), U32(Hq), U32(Hkv),
+                          U32(kv->prefix), U32(kv->max_pages), U32(pc), U32(sc), U32(rot), Val(theta), Val(eps)};
+    const char* name = slots <= 8 ? "halo_attn_decode_partial_qk2" : "halo_attn_decode_partial_qk";
+    if (Launch(eng, name, D3(static_cast<std::uint32_t>(items)), D3(256), a, err, errlen) != 0)
+      return -1;
+  }
+  const halo_arg a[] = {Ptr(pm), Ptr(pl), Ptr(pacc), Ptr(qg + 256), Ptr(o), Ptr(oq), Ptr(os), U32(S), U32(Hq),
+                        U32(Hkv), U32(pc), U32(sc)};
+  const bool eighths = S * Hq * 4 < 256;
+  return Launch(eng, eighths ? "halo_attn_decode_combine8_qg" : "halo_attn_decode_combine_qg",
+                D3(S * Hq * (eighths ? 8 : 4)), D3(256), a, err, errlen);
+}
+
 int halo_op_attn_decode(halo_engine* eng, const halo_paged_kv* kv, const float* q, const float* gate, float* o,
                         uint32_t Hq, void* ws, size_t ws_bytes, char* err, size_t errlen) {
   if (RequirePtrs(err, errlen, "attn_decode", {{"kv", kv}, {"q", q}, {"o", o}, {"ws", ws}}) != 0) return -1;

@@ -276,17 +276,12 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
           save("k", HALO_TRACE_F32, m->ko.device, static_cast<std::size_t>(S) * Hkv * hd) != 0 ||
           save("v", HALO_TRACE_F32, m->vo.device, static_cast<std::size_t>(S) * Hkv * hd) != 0)
         return -1;
-      {
-        const halo_arg a[] = {Ptr(m->qgo.device), Ptr(m->ko.device), Ptr(m->vo.device), Ptr(L.q_norm.device),
-                              Ptr(L.k_norm.device), Ptr(m->q.device), Ptr(m->agate.device), Ptr(L.k_pool.device),
-                              Ptr(L.v_pool.device), Ptr(m->pages.device), Ptr(m->nkv.device), U32(Hq), U32(Hkv),
-                              U32(m->max_pages), U32(c.rotary_dim), Val(c.rope_theta), Val(eps), Ptr(nullptr),
-                              Ptr(nullptr)};
-        if (Launch(eng, "halo_attn_prep_decode", D3(S, Hq + 2 * Hkv), D3(64), a, err, errlen) != 0) return -1;
-      }
+      // q / k norms, rotation and the K / V append run inside the attention's partial launch
       const halo_paged_kv kv = KvDesc(m, L, S, prefix);
-      if (halo_op_attn_decode_q8(eng, &kv, P<float>(m->q), P<float>(m->agate), nullptr, P<int8_t>(m->oq),
-                                 P<float>(m->os), Hq, m->attn_ws.device, m->attn_ws_bytes, err, errlen) != 0)
+      if (halo_op_attn_decode_step_q8(eng, &kv, P<float>(m->qgo), P<float>(m->ko), P<float>(m->vo),
+                                      P<float>(L.q_norm), P<float>(L.k_norm), c.rotary_dim, c.rope_theta, eps, nullptr,
+                                      P<int8_t>(m->oq), P<float>(m->os), Hq, m->attn_ws.device, m->attn_ws_bytes, err,
+                                      errlen) != 0)
         return -1;
       if (save("oq", HALO_TRACE_I8, m->oq.device, static_cast<std::size_t>(S) * Hq * hd) != 0 ||
           save("os", HALO_TRACE_F32, m->os.device, static_cast<std::size_t>(S) * Hq * hd / 32) != 0)

@@ -31,11 +31,20 @@ constexpr int kMaxQ = 32;     // query vectors per block (sessions * G)
 // {4 (16 u + sub) .. +4 : u < 4} (each load instruction reads 256 contiguous bytes per row); the 16 partial dots
 // are summed with row DPP. V arrives as 16-byte loads and is staged through LDS (over the queries, once the scores
 // are done). Weighted V: thread = one of the 256 dims, all 32 tokens in registers.
-extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
-    const float* __restrict__ q, const float* __restrict__ kpool, const float* __restrict__ vpool,
+namespace {
+// The partial kernel's body. kFused: q arrives as the raw q | gate projection qg [S][Hq][2 * 256] and is RMSNormed
+// (wq) and rotated here at each session's position nkv[s] - 1, and the block whose chunk holds a session's newest
+// position (the last suffix chunk) forms that position's K (RMSNorm wk, rotation) and V from kin / vin [S][Hkv][256],
+// appends them to the pools and uses them for that row: the prologue launch before the attention disappears. The
+// arithmetic is halo_attn_prep_decode's (halo::NormRopeHead), so q, K and V carry the same bits.
+template <bool kFused, int kQW = 1>
+__device__ __forceinline__ void AttnDecodePartial(
+    const float* __restrict__ q, const float* __restrict__ kin, const float* __restrict__ vin,
+    const float* __restrict__ wq, const float* __restrict__ wk, float* __restrict__ kpool, float* __restrict__ vpool,
     const std::uint32_t* __restrict__ pages, const std::uint32_t* __restrict__ nkv, float* __restrict__ pm,
     float* __restrict__ pl, float* __restrict__ pacc, std::uint32_t S, std::uint32_t Hq, std::uint32_t Hkv,
-    std::uint32_t prefix, std::uint32_t max_pages, std::uint32_t prefix_chunks, std::uint32_t suffix_chunks) {
+    std::uint32_t prefix, std::uint32_t max_pages, std::uint32_t prefix_chunks, std::uint32_t suffix_chunks,
+    std::uint32_t rot, float theta, float eps) {
   __shared__ float qs[kMaxQ][kHd];       // 32 KB
   __shared__ __attribute__((aligned(16))) float sc[kMaxQ][kChunk + 4];  // rows 16-byte aligned: vector reads
   static_assert(kChunk == 32 && kPage == 16, "two pages per chunk, two tokens per 16-lane row");
@@ -68,6 +77,32 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
     return pool + ((static_cast<std::size_t>(pg) * Hkv + kvh) * kPage + tok % kPage) * kHd;
   };
   const std::uint32_t sub = t % 16, r = t / 16;
+  // Fused prologue inputs, all issued before the chunk's K / V (a load issued after them could only be waited for
+  // behind them): this wave's queries (kQW of them, slots past nq reload the last), their sessions' positions,
+  // the norm weights and the newest position's k / v (loaded by every block, used by the one that holds it).
+  static_assert(kQW >= 1 && kQW <= kMaxQ / 4, "queries per wave");
+  float xq[kQW][4], wqv[4], wkv[4], xk[4], xv[4];
+  std::uint32_t qpos[kQW];
+  const bool owner = kFused && !is_prefix && last - start < static_cast<std::uint32_t>(kChunk);
+  if constexpr (kFused) {
+#pragma unroll
+    for (int m = 0; m < kQW; ++m) {
+      const std::uint32_t qi = min(wave + 4u * m, nq - 1);
+      const std::uint32_t s = is_prefix ? qi / G : sess, g = is_prefix ? qi % G : qi;
+      const float* src = q + (static_cast<std::size_t>(s) * Hq + kvh * G + g) * 2 * kHd;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xq[m][i] = src[lane + 64 * i];
+      qpos[m] = nkv[s] - 1;
+    }
+    const std::size_t kv_src = (static_cast<std::size_t>(sess) * Hkv + kvh) * kHd;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      wqv[i] = wq[lane + 64 * i];
+      wkv[i] = wk[lane + 64 * i];
+      xk[i] = kin[kv_src + lane + 64 * i];
+      xv[i] = vin[kv_src + lane + 64 * i];
+    }
+  }
   float4 kf[2][4];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -88,13 +123,56 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
     for (int u = 0; u < 4; ++u) vq[h][u] = vp[u * 256 + t];
   }
   // queries of this kv head: slot i = session * G + g (prefix) or g (suffix)
-  for (std::uint32_t i = t; i < nq * (kHd / 4); i += blockDim.x) {
-    const std::uint32_t qi = i / (kHd / 4), d4 = i % (kHd / 4);
-    const std::uint32_t s = is_prefix ? qi / G : sess, g = is_prefix ? qi % G : qi;
-    const float4 v = reinterpret_cast<const float4*>(q + (static_cast<std::size_t>(s) * Hq + kvh * G + g) * kHd)[d4];
-    reinterpret_cast<float4*>(&qs[qi][0])[d4] = v;
+  __shared__ __attribute__((aligned(16))) float knew[kFused ? 2 : 1][kFused ? kHd : 4];
+  if constexpr (kFused) {
+    // wave w prepares queries w, w + 4, ... (the angles once per position)
+    std::uint32_t cur = 0xFFFFFFFFu;
+    halo::RopeCS cs{};
+    float out[4];
+#pragma unroll
+    for (int m = 0; m < kQW; ++m) {
+      const std::uint32_t qi = wave + 4u * m;
+      if (qi >= nq) break;
+      if (qpos[m] != cur) {
+        cur = qpos[m];
+        cs = halo::RopeAngles(cur, rot, theta);
+      }
+      halo::NormRopeHead(xq[m], wqv, cs, rot, eps, out);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qs[qi][lane + 64 * i] = out[i];
+    }
+    if (owner && wave == 3) {
+      // the newest position's K and V: to LDS for this block's scores and weighted sum, and to the pools (its page
+      // is one of the chunk's two)
+      if (cur != last) cs = halo::RopeAngles(last, rot, theta);
+      halo::NormRopeHead(xk, wkv, cs, rot, eps, out);
+      const std::size_t dst =
+          ((static_cast<std::size_t>(last - start < kPage ? pg0 : pg1) * Hkv + kvh) * kPage + last % kPage) * kHd;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        knew[0][lane + 64 * i] = out[i];
+        knew[1][lane + 64 * i] = xv[i];
+        kpool[dst + lane + 64 * i] = out[i];
+        vpool[dst + lane + 64 * i] = xv[i];
+      }
+    }
+  } else {
+    for (std::uint32_t i = t; i < nq * (kHd / 4); i += blockDim.x) {
+      const std::uint32_t qi = i / (kHd / 4), d4 = i % (kHd / 4);
+      const std::uint32_t s = is_prefix ? qi / G : sess, g = is_prefix ? qi % G : qi;
+      const float4 v = reinterpret_cast<const float4*>(q + (static_cast<std::size_t>(s) * Hq + kvh * G + g) * kHd)[d4];
+      reinterpret_cast<float4*>(&qs[qi][0])[d4] = v;
+    }
   }
   __syncthreads();
+  if (owner) {
+    // the newest row's K from LDS in place of the pool's (not yet written when the loads were issued)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if (start + r + 16 * h == last)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) kf[h][u] = reinterpret_cast<const float4*>(&knew[0][0])[16 * u + sub];
+  }
   const float scale = 1.0f / sqrtf(static_cast<float>(kHd));
   const bool live0 = start + r < limit, live1 = start + r + 16 < limit;
   // queries in groups of 8, the group's dot products and row reductions interleaved (independent chains; each
@@ -133,8 +211,9 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const std::uint32_t j = 16 * h + 4 * u + t / 64;
-      reinterpret_cast<float4*>(&qs[j][0])[t % 64] =
-          start + j < limit ? vq[h][u] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      float4 v = start + j < limit ? vq[h][u] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (owner && start + j == last) v = reinterpret_cast<const float4*>(&knew[1][0])[t % 64];
+      reinterpret_cast<float4*>(&qs[j][0])[t % 64] = v;
     }
   // softmax over the chunk per query: wave w takes queries w, w + 4, ...; lanes 0..31 are the tokens
   for (std::uint32_t i = wave; i < nq; i += 4) {
@@ -176,6 +255,38 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
       }
   }
 }
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
+    const float* __restrict__ q, const float* __restrict__ kpool, const float* __restrict__ vpool,
+    const std::uint32_t* __restrict__ pages, const std::uint32_t* __restrict__ nkv, float* __restrict__ pm,
+    float* __restrict__ pl, float* __restrict__ pacc, std::uint32_t S, std::uint32_t Hq, std::uint32_t Hkv,
+    std::uint32_t prefix, std::uint32_t max_pages, std::uint32_t prefix_chunks, std::uint32_t suffix_chunks) {
+  AttnDecodePartial<false>(q, nullptr, nullptr, nullptr, nullptr, const_cast<float*>(kpool), const_cast<float*>(vpool),
+                           pages, nkv, pm, pl, pacc, S, Hq, Hkv, prefix, max_pages, prefix_chunks, suffix_chunks, 0,
+                           0.0f, 0.0f);
+}
+
+// The partial launch with the attention prologue folded in (see AttnDecodePartial<true>): qg [S][Hq][2 * 256],
+// kin, vin [S][Hkv][256], wq, wk [256]; rot <= 128. Every session's newest position nkv[s] - 1 must lie past the
+// shared prefix (it is in that session's last suffix chunk). Same grid and partial outputs as
+// halo_attn_decode_partial; the gate for the combine is the second half of each qg head.
+// _qk: up to 32 query vectors per block (S * Hq / Hkv <= 32); _qk2: up to 8 (two per wave).
+#define HALO_ATTN_PARTIAL_QK(NAME, QW)                                                                           \
+  extern "C" __global__ void __launch_bounds__(256) NAME(                                                       \
+      const float* __restrict__ qg, const float* __restrict__ kin, const float* __restrict__ vin,               \
+      const float* __restrict__ wq, const float* __restrict__ wk, float* __restrict__ kpool,                    \
+      float* __restrict__ vpool, const std::uint32_t* __restrict__ pages, const std::uint32_t* __restrict__ nkv, \
+      float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ pacc, std::uint32_t S, std::uint32_t Hq, \
+      std::uint32_t Hkv, std::uint32_t prefix, std::uint32_t max_pages, std::uint32_t prefix_chunks,            \
+      std::uint32_t suffix_chunks, std::uint32_t rot, float theta, float eps) {                                 \
+    AttnDecodePartial<true, QW>(qg, kin, vin, wq, wk, kpool, vpool, pages, nkv, pm, pl, pacc, S, Hq, Hkv, prefix,  \
+                                max_pages, prefix_chunks, suffix_chunks, rot, theta, eps);                       \
+  }
+HALO_ATTN_PARTIAL_QK(halo_attn_decode_partial_qk, 8)
+HALO_ATTN_PARTIAL_QK(halo_attn_decode_partial_qk2, 2)
+#undef HALO_ATTN_PARTIAL_QK
+
 
 // grid (S * Hq * NS), block 256: block (s, h, slice) merges the partials of session s, head h over its prefix and
 // suffix chunks (log-sum-exp) for the slice's 256 / NS dims: o = acc / l, then o *= sigmoid(gate) when gate is
@@ -183,7 +294,7 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
 // os [S][Hq * 8]). At most 1024 items. Thread: float4 lane f of the slice, item group t / (lanes per slice), eight
 // loads in flight. NS = 8 doubles the blocks of small batches (more loads in flight over the chip).
 namespace {
-template <int NS>
+template <int NS, int kGS = 1>
 __device__ __forceinline__ void AttnDecodeCombine(
     const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ pacc,
     const float* __restrict__ gate, float* __restrict__ o, std::int8_t* __restrict__ oq, float* __restrict__ os,
@@ -255,7 +366,7 @@ __device__ __forceinline__ void AttnDecodeCombine(
   for (std::uint32_t k = 0; k < kG; ++k) sum += reinterpret_cast<const float*>(&part[k][0])[t];
   float r = sum / L;
   const std::size_t off = (static_cast<std::size_t>(s) * Hq + h) * kHd + quarter * kW + t;
-  if (gate != nullptr) r *= halo::Sigmoid(gate[off]);
+  if (gate != nullptr) r *= halo::Sigmoid(gate[(static_cast<std::size_t>(s) * Hq + h) * kGS * kHd + quarter * kW + t]);
   if (o != nullptr) o[off] = r;
   if (oq != nullptr) {
     // the row's Q8 quantization for the output projection: 32-value blocks are half waves
@@ -267,16 +378,19 @@ __device__ __forceinline__ void AttnDecodeCombine(
 }
 }  // namespace
 
-#define HALO_ATTN_COMBINE(NAME, NS)                                                                              \
+// _qg: gate rows with a head stride of 2 * 256 (the gate halves of the q | gate projection, gate = qg + 256).
+#define HALO_ATTN_COMBINE(NAME, NS, GS)                                                                          \
   extern "C" __global__ void __launch_bounds__(256) NAME(                                                       \
       const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ pacc,               \
       const float* __restrict__ gate, float* __restrict__ o, std::int8_t* __restrict__ oq, float* __restrict__ os, \
       std::uint32_t S, std::uint32_t Hq, std::uint32_t Hkv, std::uint32_t prefix_chunks,                         \
       std::uint32_t suffix_chunks) {                                                                             \
-    AttnDecodeCombine<NS>(pm, pl, pacc, gate, o, oq, os, S, Hq, Hkv, prefix_chunks, suffix_chunks);             \
+    AttnDecodeCombine<NS, GS>(pm, pl, pacc, gate, o, oq, os, S, Hq, Hkv, prefix_chunks, suffix_chunks);         \
   }
-HALO_ATTN_COMBINE(halo_attn_decode_combine, 4)
-HALO_ATTN_COMBINE(halo_attn_decode_combine8, 8)
+HALO_ATTN_COMBINE(halo_attn_decode_combine, 4, 1)
+HALO_ATTN_COMBINE(halo_attn_decode_combine8, 8, 1)
+HALO_ATTN_COMBINE(halo_attn_decode_combine_qg, 4, 2)
+HALO_ATTN_COMBINE(halo_attn_decode_combine8_qg, 8, 2)
 #undef HALO_ATTN_COMBINE
 
 // Appends one token's K and V per session at position nkv[s] - 1: k, v [S][Hkv][256] -> pools via page tables.

@@ -374,4 +374,60 @@ __device__ __forceinline__ bool LastBlock(std::uint32_t* counter, std::uint32_t 
   }
   return last;
 }
+
+// ---- attention head prologue (one wave per 256-dim head; lane l holds dims l + 64 i, i < 4) ------------------
+// NEOX rotary angles of the dims this lane holds among the first `rot` (rot <= 128: dims l and l + 64) at
+// position pos: freq = theta^(-2 j' / rot) with j' = j mod rot / 2. Not inlined: the precise powf / cosf / sinf are
+// long, and a caller that needs the angles of a few positions keeps one copy of them.
+struct RopeCS {
+  float c[2], s[2];
+};
+__device__ __noinline__ RopeCS RopeAngles(std::uint32_t pos, std::uint32_t rot, float theta) {
+  RopeCS r{{1.0f, 1.0f}, {0.0f, 0.0f}};
+  const std::uint32_t lane = threadIdx.x % kWave, half = rot / 2;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const std::uint32_t j = lane + 64 * i;
+    if (j < rot) {
+      const std::uint32_t jj = j < half ? j : j - half;
+      const float freq = powf(theta, -2.0f * static_cast<float>(jj) / static_cast<float>(rot));
+      const float ang = static_cast<float>(pos) * freq;
+      r.c[i] = cosf(ang);
+      r.s[i] = sinf(ang);
+    }
+  }
+  return r;
+}
+// x (this lane's 4 dims of one head, w the matching norm weights) -> RMSNorm(x) * w, then the NEOX rotation of the first rot dims: pairs
+// (j, j + rot / 2), y_j c - y_{j + rot/2} s and y_j s + y_{j + rot/2} c. The whole wave calls it.
+__device__ __forceinline__ void NormRopeHead(const float (&x)[4], const float (&w)[4], const RopeCS& cs,
+                                             std::uint32_t rot, float eps, float (&out)[4]) {
+  constexpr std::uint32_t d = 256;
+  const std::uint32_t lane = threadIdx.x % kWave;
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ss += x[i] * x[i];
+  ss = GroupSum(ss);
+  const float sc = 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
+  float y[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) y[i] = x[i] * sc * w[i];
+  const std::uint32_t half = rot / 2;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[i] = y[i];
+    const std::uint32_t j = lane + 64 * i;
+    if (i < 2 && j < rot) {
+      const std::uint32_t pj = j < half ? j + half : j - half;  // partner: element j + half or j - half
+      float partner = 0.0f;
+#pragma unroll
+      for (int i2 = 0; i2 < 4; ++i2) {
+        const float cand = __shfl(y[i2], pj % 64, kWave);
+        if (static_cast<std::uint32_t>(i2) == pj / 64) partner = cand;
+      }
+      out[i] = j < half ? y[i] * cs.c[i] - partner * cs.s[i] : partner * cs.s[i] + y[i] * cs.c[i];
+    }
+  }
+}
+
 }  // namespace halo

@@ -134,37 +134,10 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_prep_decode(
       for (int i = 0; i < 4; ++i) dst[lane + 64 * i] = x[i];
       return;
     }
-    float ss = 0.0f;
+    float out[4], wv[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ss += x[i] * x[i];
-    ss = halo::GroupSum(ss);
-    const float sc = 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
-    const float* wn = hh < Hq ? wq : wk;
-    float y[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) y[i] = x[i] * sc * wn[lane + 64 * i];
-    // NEOX rotation: pairs (j, j + rot / 2) for j < rot / 2 (rot <= 128 keeps both halves in y[0], y[1] lanes)
-    float out[4] = {y[0], y[1], y[2], y[3]};
-    const std::uint32_t half = rot / 2;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const std::uint32_t j = lane + 64 * i;
-      if (j < rot) {
-        const std::uint32_t jj = j < half ? j : j - half;
-        const float freq = powf(theta, -2.0f * static_cast<float>(jj) / static_cast<float>(rot));
-        const float ang = static_cast<float>(pos) * freq;
-        const float c = cosf(ang), sn = sinf(ang);
-        // partner value: element j + half or j - half
-        const std::uint32_t pj = j < half ? j + half : j - half;
-        float partner = 0.0f;
-#pragma unroll
-        for (int i2 = 0; i2 < 4; ++i2) {
-          const float cand = __shfl(y[i2], pj % 64, kWave);
-          if (static_cast<std::uint32_t>(i2) == pj / 64) partner = cand;
-        }
-        out[i] = j < half ? y[i] * c - partner * sn : partner * sn + y[i] * c;
-      }
-    }
+    for (int i = 0; i < 4; ++i) wv[i] = (hh < Hq ? wq : wk)[lane + 64 * i];
+    halo::NormRopeHead(x, wv, halo::RopeAngles(pos, rot, theta), rot, eps, out);
     if (hh < Hq) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {

@@ -386,6 +386,8 @@ _SIGS = {
     "halo_op_attn_decode_workspace_bytes": (_SZ, [C.POINTER(PagedKV), _U32], False),
     "halo_op_attn_decode": (C.c_int, [_VP, C.POINTER(PagedKV), _VP, _VP, _VP, _U32, _VP, _SZ], True),
     "halo_op_attn_decode_q8": (C.c_int, [_VP, C.POINTER(PagedKV), _VP, _VP, _VP, _VP, _VP, _U32, _VP, _SZ], True),
+    "halo_op_attn_decode_step_q8": (C.c_int, [_VP, C.POINTER(PagedKV), _VP, _VP, _VP, _VP, _VP, _U32, C.c_float,
+                                              C.c_float, _VP, _VP, _VP, _U32, _VP, _SZ], True),
     "halo_op_kv_append": (C.c_int, [_VP, C.POINTER(PagedKV), _VP, _VP], True),
     "halo_gdn_chunk_table": (_U32, [_VP, _U32, _VP, _VP], False),
     "halo_op_gdn_prefill_workspace_bytes": (_SZ, [_U32, _U32], False),

@@ -210,6 +210,17 @@ int halo_op_attn_decode(halo_engine* eng, const halo_paged_kv* kv, const float* 
 int halo_op_attn_decode_q8(halo_engine* eng, const halo_paged_kv* kv, const float* q, const float* gate, float* o,
                            int8_t* oq, float* os, uint32_t q_heads, void* ws, size_t ws_bytes, char* err,
                            size_t errlen);
+/* One decode step of the attention block from its input projections: every q head RMSNorm(q_norm) and rotated
+ * (NEOX, the first `rot` <= 128 dims) at its session's position nkv[s] - 1, that position's K (RMSNorm k_norm,
+ * rotated) and V appended to the pools, then the attention as above with gate = the second half of each qg head.
+ * Replaces the prologue of ReferenceModel::Attention (src/model/reference.cpp:368-416) plus halo_op_attn_decode_q8
+ * in two launches (the prologue runs inside the partial launch). qg [S][Hq][2 d] (per head: q | gate), k, v
+ * [S][Hkv][d]; every nkv[s] - 1 must lie at or past the shared prefix. Bitwise equal to halo_attn_prep_decode followed
+ * by halo_op_attn_decode_q8. */
+int halo_op_attn_decode_step_q8(halo_engine* eng, const halo_paged_kv* kv, const float* qg, const float* k,
+                                const float* v, const float* q_norm, const float* k_norm, uint32_t rot, float theta,
+                                float eps, float* o, int8_t* oq, float* os, uint32_t q_heads, void* ws,
+                                size_t ws_bytes, char* err, size_t errlen);
 /* A run of consecutive prompt positions of one session inside a prefill batch: tokens [first, first + length) of
  * the batch are positions [start, start + length) of session `session`. */
 typedef struct halo_prefill_segment {

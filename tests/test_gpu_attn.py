@@ -100,3 +100,52 @@ def test_kv_append(dev):
         kp[pg, :, pos % PAGE] = k[s]
         vp[pg, :, pos % PAGE] = v[s]
     assert np.array_equal(kp2, kp) and np.array_equal(vp2, vp)  # nothing else touched
+
+
+@pytest.mark.parametrize("S,prefix,suffixes,max_context", [
+    (4, 512, [37, 130, 1, 69], 512 + 256),
+    (1, 0, [300], 512),
+    (2, 64, [33, 32], 64 + 96),
+    (4, 8192, [256, 256, 256, 256], 8192 + 384),
+])
+def test_attn_decode_step_equals_prep_then_decode(dev, S, prefix, suffixes, max_context):
+    """halo_op_attn_decode_step_q8 (the q / k norms, rotation and K / V append inside the partial launch, the gate
+    read from the q | gate projection) against halo_attn_prep_decode followed by halo_op_attn_decode_q8 on a copy of
+    the same pools: o, its Q8 codes and scales, and both pools bitwise equal. The cases put the newest position at
+    the start, the end and the middle of a 32-token chunk, with and without a shared prefix."""
+    rng = np.random.default_rng(31 + S + prefix)
+    Hkv, Hq, rot, theta, eps = 2, 16, 64, 1e7, 1e-6
+    descA, gA, kp, vp, pages, nkv = build(dev, rng, S, Hkv, prefix, suffixes, max_context)
+    gB = dict(k=dev.to_device(kp), v=dev.to_device(vp), pages=gA["pages"], nkv=gA["nkv"])
+    descB = H.PagedKV(gB["k"].ptr, gB["v"].ptr, gB["pages"].ptr, gB["nkv"].ptr, S, Hkv, D, descA.max_pages, prefix,
+                      max_context)
+    qg = dev.to_device(rng.normal(0, 1, (S, Hq, 2 * D)).astype(np.float32))
+    kin = dev.to_device(rng.normal(0, 1, (S, Hkv, D)).astype(np.float32))
+    vin = dev.to_device(rng.normal(0, 1, (S, Hkv, D)).astype(np.float32))
+    wq = dev.to_device(rng.normal(1, 0.1, D).astype(np.float32))
+    wk = dev.to_device(rng.normal(1, 0.1, D).astype(np.float32))
+    nbytes = H.lib().halo_op_attn_decode_workspace_bytes(ctypes.byref(descA), Hq)
+    ws = dev.array(nbytes, np.uint8)
+    outs = []
+    for fused, desc, g in ((False, descA, gA), (True, descB, gB)):
+        o = dev.array((S, Hq, D), np.float32)
+        oq = dev.array((S, Hq * D), np.int8)
+        os_ = dev.array((S, Hq * D // 32), np.float32)
+        if fused:
+            dev.op("attn_decode_step_q8", ctypes.byref(desc), qg.ptr, kin.ptr, vin.ptr, wq.ptr, wk.ptr, rot, theta, eps,
+                   o.ptr, oq.ptr, os_.ptr, Hq, ws.ptr, ws.nbytes)
+        else:
+            q = dev.array((S, Hq, D), np.float32)
+            gate = dev.array((S, Hq, D), np.float32)
+            dev.launch("halo_attn_prep_decode", (S, Hq + 2 * Hkv), (64,),
+                       [qg, kin, vin, wq, wk, q, gate, g["k"], g["v"], g["pages"], g["nkv"], ("u32", Hq), ("u32", Hkv),
+                        ("u32", desc.max_pages), ("u32", rot), ("f32", theta), ("f32", eps), None, None])
+            dev.op("attn_decode_q8", ctypes.byref(desc), q.ptr, gate.ptr, o.ptr, oq.ptr, os_.ptr, Hq, ws.ptr, ws.nbytes)
+        outs.append([o.download(), oq.download(), os_.download(), g["k"].download(), g["v"].download()])
+    for name, a, b in zip(("o", "oq", "os", "k pool", "v pool"), outs[0], outs[1]):
+        assert np.array_equal(np.ascontiguousarray(a).view(np.uint8), np.ascontiguousarray(b).view(np.uint8)), name
+    # the appended rows really were written (not the pools' old contents)
+    last = nkv - 1
+    for s in range(S):
+        row = outs[1][4][pages[s, last[s] // PAGE], :, last[s] % PAGE]
+        assert np.array_equal(row, vin.download()[s])

@@ -113,9 +113,12 @@ int MoeDecode(halo_engine* eng, const halo_moe_weights* w, const float* x, const
     std::snprintf(name, sizeof name, "halo_moe_gate_up_topk_q8_s%u%s", H / 1024, E <= 512 ? "_e512" : "");
     if (Launch(eng, name, D3(k + 1, v.hstride / 4), D3(256), a, err, errlen) != 0) return -1;
   } else {
-    // 2. softmax / top-k, one block per token
+    // 2. softmax / top-k, one wave per token
     const halo_arg t[] = {Ptr(v.logits), Ptr(v.ids), Ptr(v.weights), U32(E), U32(k)};
-    if (Launch(eng, "halo_moe_topk", D3(T), D3(CeilDiv(E, 64) * 64), t, err, errlen) != 0) return -1;
+    const bool wave = E <= 1024 && k <= 64;
+    if (Launch(eng, !wave ? "halo_moe_topk" : E <= 512 ? "halo_moe_topk_w512" : "halo_moe_topk_w1024", D3(T),
+               D3(wave ? 64 : CeilDiv(E, 64) * 64), t, err, errlen) != 0)
+      return -1;
     // 3. gate/up over the union of experts + SwiGLU
     const halo_arg a[] = {Ptr(w->gate.qs), Ptr(w->gate.d), Ptr(w->up.qs), Ptr(w->up.d),
                           Ptr(shared ? w->shared_gate_proj.qs : nullptr), Ptr(shared ? w->shared_gate_proj.d : nullptr),

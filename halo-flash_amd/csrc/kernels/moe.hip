@@ -8,8 +8,9 @@
 // Launches (all take device buffers only, so one captured graph replays for any routing):
 //   1. halo_moe_router     logits[t][e] = W_r[e] . x[t] (fp32), shared-gate logit, x quantized per 32 (int8);
 //      or halo_moe_router_n_* (T <= 4), which also forms x = RMSNorm(res + delta) * w itself (the FFN norm).
-//   2. halo_moe_topk       one block per token: softmax, top-k (ties -> lower id), renormalized weights; at T = 1
-//                          folded into the gate/up launch instead (halo_moe_gate_up_topk_q8_*: 3 launches).
+//   2. halo_moe_topk_w*    one wave per token: softmax, top-k (ties -> lower id), renormalized weights (the block
+//                          kernel halo_moe_topk serves prefill batches); at T = 1 folded into the gate/up launch
+//                          instead (halo_moe_gate_up_topk_q8_*: 3 launches).
 //   3. halo_moe_gate_up_q8 block (routed pair, 4 ff rows): the first token that selected an expert computes it for
 //                          every token that selected it (the union of experts: weights streamed once), h =
 //                          SiLU(g) * u in fp32. One more block column is the shared expert.
@@ -491,6 +492,23 @@ extern "C" __global__ void __launch_bounds__(1024)
     weights[static_cast<std::size_t>(t) * k + e] = selp[e] / red[0];
   }
 }
+
+// The same routing with one wave per token (WaveTopK: kPer 8 for E <= 512, 16 for E <= 1024), k <= 64: grid (T),
+// block 64. Shorter than the block kernel above for decode batches (no block-wide reductions, no atomics).
+//   logits [T][E] -> ids [T][k], weights [T][k]
+#define HALO_MOE_TOPK_W(NAME, PER)                                                                                 \
+  extern "C" __global__ void __launch_bounds__(64) NAME(const float* __restrict__ logits,                          \
+                                                        std::uint32_t* __restrict__ ids, float* __restrict__ weights, \
+                                                        std::uint32_t E, std::uint32_t k) {                        \
+    __shared__ std::uint32_t lids[kWave];                                                                          \
+    __shared__ float lw[kWave];                                                                                    \
+    __shared__ TopKScratch sc;                                                                                     \
+    const std::size_t t = blockIdx.x;                                                                              \
+    WaveTopK<PER>(logits + t * E, E, k, ids + t * k, weights + t * k, lids, lw, sc);                               \
+  }
+HALO_MOE_TOPK_W(halo_moe_topk_w512, 8)
+HALO_MOE_TOPK_W(halo_moe_topk_w1024, 16)
+#undef HALO_MOE_TOPK_W
 
 // grid (T * k + 1, ceil(max(ff, sff) / 4)), block 256: wave w computes ff row j = 4 * blockIdx.y + w of gate and
 // up (two rows of H int8, kSteps = H / 1024 loads each per lane). Block x < T * k is routed pair x (token x / k,

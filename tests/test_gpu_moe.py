@@ -154,14 +154,17 @@ def _topk_cases(rng, E):
     return np.stack(rows).astype(np.float32)
 
 
-def test_router_topk_reference_named(dev):
+@pytest.mark.parametrize("kernel", ["halo_router_topk_rows", "halo_moe_topk_w512", "halo_moe_topk_w1024"])
+def test_router_topk_reference_named(dev, kernel):
+    """The one-wave top-k kernels (the reference-named rows launch and the decode-batch routing launches) on rows
+    that reach every selection path: ids equal to the oracle's RouteTopK, weights to 1e-6."""
     rng = np.random.default_rng(5)
     E, k = 512, 10
     logits = _topk_cases(rng, E)
     T = logits.shape[0]
     gl = dev.to_device(logits)
     gi, gw = dev.array((T, k), np.uint32), dev.array((T, k), np.float32)
-    dev.launch("halo_router_topk_rows", (T,), (64,), [gl, gi, gw, ("u32", E), ("u32", k)])
+    dev.launch(kernel, (T,), (64,), [gl, gi, gw, ("u32", E), ("u32", k)])
     ids, w = gi.download(), gw.download()
     for t in range(T):
         oi, ow = np.zeros(k, np.uint32), np.zeros(k, np.float32)

@@ -404,7 +404,9 @@ def run_proj(args, dev, H, res):
 def run_attn(args, dev, H, res):
     """C4's decode attention alone (16 q heads, 2 kv heads, head_dim 256, fp32 paged KV): 1 session at 8576
     visible positions, and 4 sessions sharing an 8192-token prefix with 384 suffix positions each. Eight KV pools
-    (> 256 MB) are rotated so K/V come from HBM. Bytes = K/V rows read (the shared prefix once)."""
+    (> 256 MB) are rotated so K/V come from HBM. Bytes = K/V rows read (the shared prefix once). `S*` times the
+    decode from normalized queries, `S*_step` the model's form from the projections (norms, rotation, K / V
+    append in the partial launch)."""
     import ctypes as C
 
     Hq, Hkv, D, PAGE, ncopy = 16, 2, 256, 16, 8
@@ -438,30 +440,41 @@ def run_attn(args, dev, H, res):
         ws = dev.array(wsb, np.uint8)
         call = lambda d: dev.op("attn_decode_q8", C.byref(d), q.ptr, gate.ptr, None, oq.ptr, os_.ptr, Hq, ws.ptr,
                                 wsb)
+        # the model's form: from the q | gate, k and v projections (norms, rotation and the K / V append inside)
+        qg = dev.array((S, Hq, 2 * D), np.float32)
+        kin, vin = dev.array((S, Hkv, D), np.float32), dev.array((S, Hkv, D), np.float32)
+        wq, wk = dev.array(D, np.float32), dev.array(D, np.float32)
+        for a, sd in ((qg, 9), (kin, 10), (vin, 11), (wq, 12), (wk, 13)):
+            dev.op("synth_f32", a.ptr, a.nbytes // 4, sd, 1.0)
+        step = lambda d: dev.op("attn_decode_step_q8", C.byref(d), qg.ptr, kin.ptr, vin.ptr, wq.ptr, wk.ptr, 64, 1e7,
+                                1e-6, None, oq.ptr, os_.ptr, Hq, ws.ptr, wsb)
         dev.sync()
         if args.eager:
             for _ in range(5):
                 for d in descs:
                     call(d)
+                for d in descs:
+                    step(d)
             dev.sync()
             continue
-        dev.begin_capture()
-        for d in descs:
-            call(d)
-        g = dev.end_capture()
-        dev.launch_graph(g)
-        dev.sync()
-        nrep = 100
-        dev.timer_start()
-        for _ in range(nrep):
-            dev.launch_graph(g)
-        us = dev.timer_stop() * 1e3 / (nrep * ncopy)
-        dev.free_graph(g)
         rows = (prefix + S * suffix) * Hkv
         nbytes = rows * D * 4 * 2
-        out[f"S{S}"] = {"us_per_layer": round(us, 2), "kv_MB": round(nbytes / 1e6, 1),
+        for key, fn in ((f"S{S}", call), (f"S{S}_step", step)):
+            dev.begin_capture()
+            for d in descs:
+                fn(d)
+            g = dev.end_capture()
+            dev.launch_graph(g)
+            dev.sync()
+            nrep = 100
+            dev.timer_start()
+            for _ in range(nrep):
+                dev.launch_graph(g)
+            us = dev.timer_stop() * 1e3 / (nrep * ncopy)
+            dev.free_graph(g)
+            out[key] = {"us_per_layer": round(us, 2), "kv_MB": round(nbytes / 1e6, 1),
                         "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
-        log(f"[bench] attn S={S}: {out[f'S{S}']}")
+            log(f"[bench] attn {key}: {out[key]}")
         del keep
     res["attn"] = out
     return res

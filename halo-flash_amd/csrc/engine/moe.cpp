@@ -133,7 +133,12 @@ int MoeDecode(halo_engine* eng, const halo_moe_weights* w, const float* x, const
     const halo_arg a[] = {Ptr(w->down.qs), Ptr(w->down.d), Ptr(shared ? w->shared_down.qs : nullptr),
                           Ptr(shared ? w->shared_down.d : nullptr), Ptr(v.h), Ptr(v.ids), Ptr(v.weights),
                           Ptr(v.shared_logit), Ptr(out), U32(T), U32(H), U32(F), U32(SF), U32(k), U32(v.hstride)};
-    if (Launch(eng, "halo_moe_down_q8", D3(CeilDiv(H, 8), T), D3(64 * (k + 1)), a, err, errlen) != 0) return -1;
+    // 8 output rows per block at one token, 16 for token batches (measured: T = 1 16.9 vs 17.9 us, T = 4 38.9 vs
+    // 37.5 us, T = 16 112.8 vs 107.7 us)
+    const std::uint32_t rows = T == 1 ? 8 : 16;
+    if (Launch(eng, T == 1 ? "halo_moe_down_q8" : "halo_moe_down_q8_r16", D3(CeilDiv(H, rows), T), D3(64 * (k + 1)),
+               a, err, errlen) != 0)
+      return -1;
   }
   return 0;
 }

@@ -662,17 +662,15 @@ HALO_MOE_GATE_UP_TOPK(2, halo_moe_gate_up_topk_q8_s2_e512, 8)
 HALO_MOE_GATE_UP_TOPK(4, halo_moe_gate_up_topk_q8_s4_e512, 8)
 #undef HALO_MOE_GATE_UP_TOPK
 
-namespace {
-constexpr int kDownRows = 8;  // output rows per block: 4 passes x 2 rows (a row is 32 lanes x 16 bytes)
-}
-
-// grid (ceil(H / 8), T), block 64 * (k + 1) (<= 1024): wave s < k streams 8 rows of expert ids[t][s]'s down matrix
-// (4 KB contiguous), wave k the shared expert's; each wave quantizes its h row per 32 values (amax / 127, round
+// grid (ceil(H / R), T), block 64 * (k + 1) (<= 1024), R = 8 (halo_moe_down_q8) or 16 (_r16): wave s < k streams
+// R rows of expert ids[t][s]'s down matrix (R / 2 KB contiguous; two rows per pass of 32 lanes x 16 bytes), wave k
+// the shared expert's; each wave quantizes its h row per 32 values (amax / 127, round
 // half to even; a 32-value block is two adjacent lanes) and the block combines in slot order through LDS:
 //   out[t][r] = sum over s < k, in order, of weights[t][s] * (W_d[ids[t][s]][r] . q8(h[t * k + s])),
 //               then + sigmoid(sgl[t]) * (W_sd[r] . q8(h[T * k + t])).
 // Down [E][H][ff] repacked (row stride ff), shared down [H][sff]; ff, sff <= 512.
-extern "C" __global__ void __launch_bounds__(1024) halo_moe_down_q8(
+template <int kDownRows>
+__device__ __forceinline__ void MoeDown(
     const std::int8_t* __restrict__ dq, const std::uint16_t* __restrict__ dd, const std::int8_t* __restrict__ sdq,
     const std::uint16_t* __restrict__ sdd, const float* __restrict__ h, const std::uint32_t* __restrict__ ids,
     const float* __restrict__ weights, const float* __restrict__ sgl, float* __restrict__ out, std::uint32_t T,
@@ -747,6 +745,19 @@ extern "C" __global__ void __launch_bounds__(1024) halo_moe_down_q8(
     out[static_cast<std::size_t>(t) * H + r0 + threadIdx.x] = acc;
   }
 }
+// 8 rows per block at one token (more blocks in flight); 16 for token batches, which halves the h rows each block
+// reads and quantizes again.
+#define HALO_MOE_DOWN(NAME, R)                                                                                     \
+  extern "C" __global__ void __launch_bounds__(1024) NAME(                                                        \
+      const std::int8_t* __restrict__ dq, const std::uint16_t* __restrict__ dd, const std::int8_t* __restrict__ sdq, \
+      const std::uint16_t* __restrict__ sdd, const float* __restrict__ h, const std::uint32_t* __restrict__ ids,   \
+      const float* __restrict__ weights, const float* __restrict__ sgl, float* __restrict__ out, std::uint32_t T,  \
+      std::uint32_t H, std::uint32_t ff, std::uint32_t sff, std::uint32_t k, std::uint32_t hstride) {             \
+    MoeDown<R>(dq, dd, sdq, sdd, h, ids, weights, sgl, out, T, H, ff, sff, k, hstride);                            \
+  }
+HALO_MOE_DOWN(halo_moe_down_q8, 8)
+HALO_MOE_DOWN(halo_moe_down_q8_r16, 16)
+#undef HALO_MOE_DOWN
 
 // Reference-named router top-k (src/kernels/core.hip:1110-1120): one token per block (grid 1 or T), the first
 // wave computes softmax/top-k of `n` logits; ids/weights receive k entries.

@@ -64,7 +64,7 @@ struct halo_model {
   // device sampling (halo_model_set_sampling): per-session parameters and penalty lists, the draws, workspace
   bool sampling = false;
   halo_buffer sample_params{}, sample_pen{}, sample_out{}, sample_ws{};
-  // prefill batch scratch, allocated at the first prefill for kPrefillCap tokens
+  // prefill batch scratch, allocated at the first prefill for the prefill batch cap tokens
   struct Prefill {
     bool ready = false;
     halo_buffer res{}, xn{}, xq{}, xs{}, qkv{}, zo{}, abo{}, qb{}, kb{}, vb{}, g{}, beta{}, o{}, oq{}, os{}, delta{};
@@ -143,6 +143,8 @@ int Check(const halo_model_config* c, char* err, std::size_t errlen) {
     return SetErr(err, errlen, "model: DeltaNet channels must be a multiple of 256"), -1;
   if (c->rotary_dim > 128 || c->rotary_dim % 64 != 0)
     return SetErr(err, errlen, "model: rotary dim must be 64 or 128"), -1;
+  if (c->prefill_batch != 0 && (c->prefill_batch < 64 || c->prefill_batch > 65536))
+    return SetErr(err, errlen, "model: prefill batch %u must be 0 (8192) or 64 ... 65536", c->prefill_batch), -1;
   return 0;
 }
 
@@ -364,20 +366,22 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
 }
 
 
-constexpr std::uint32_t kPrefillCap = 2048;  // tokens per prefill batch
+// Tokens per prefill batch: the config's prefill_batch, 8192 by default. Every expert's gate / up / down weights are
+// read once per batch, so larger batches amortize them over more rows of the grouped GEMMs.
+std::uint32_t PrefillCap(const halo_model_config& c) { return c.prefill_batch ? c.prefill_batch : 8192u; }
 
 int PrefillAlloc(halo_model* m, char* err, std::size_t errlen) {
   if (m->pf.ready) return 0;
   const halo_model_config& c = m->c;
-  const std::size_t T = kPrefillCap, H = c.hidden, Dv = static_cast<std::size_t>(c.gdn_v_heads) * c.gdn_head_dim;
+  const std::size_t T = PrefillCap(c), H = c.hidden, Dv = static_cast<std::size_t>(c.gdn_v_heads) * c.gdn_head_dim;
   const std::size_t Dk = static_cast<std::size_t>(c.gdn_k_heads) * c.gdn_head_dim, C = m->conv_ch;
   const std::size_t A = static_cast<std::size_t>(c.q_heads) * c.head_dim, KV = static_cast<std::size_t>(c.kv_heads) * c.head_dim;
   const std::size_t O = std::max(Dv, A);
   auto& p = m->pf;
-  const std::uint32_t max_chunks = kPrefillCap / 64 + c.max_sessions;
+  const std::uint32_t max_chunks = PrefillCap(c) / 64 + c.max_sessions;
   p.gdn_ws_bytes = halo_op_gdn_prefill_workspace_bytes(max_chunks, c.gdn_v_heads);
-  p.moe_ws_bytes = halo_op_moe_prefill_workspace_bytes(&m->layers[0].moe, kPrefillCap);
-  p.attn_ws_bytes = (kPrefillCap / 8 + c.max_sessions) * 4 * sizeof(std::uint32_t);
+  p.moe_ws_bytes = halo_op_moe_prefill_workspace_bytes(&m->layers[0].moe, PrefillCap(c));
+  p.attn_ws_bytes = (PrefillCap(c) / 8 + c.max_sessions) * 4 * sizeof(std::uint32_t);
   if (p.moe_ws_bytes == 0) return SetErr(err, errlen, "prefill: MoE shape unsupported by the batched path"), -1;
   struct B {
     halo_buffer* b;
@@ -401,7 +405,7 @@ int PrefillAlloc(halo_model* m, char* err, std::size_t errlen) {
 }
 
 // One prefill batch: segments with consecutive increasing sessions s0, s0 + 1, ..., positions already in the cache
-// below each segment's start. T = sum of lengths <= kPrefillCap.
+// below each segment's start. T = sum of lengths <= the prefill batch cap.
 int PrefillBatch(halo_model* m, const std::vector<halo_prefill_segment>& segs, char* err, std::size_t errlen,
                  Tracer* tr = nullptr) {
   const halo_model_config& c = m->c;
@@ -983,11 +987,11 @@ int halo_model_prefill(halo_model* m, const halo_prefill_segment* segs, uint32_t
       return SetErr(err, errlen, "prefill: segment %u (%u + %u) outside the context", i, g.start, g.length), -1;
   }
   if (PrefillAlloc(m, err, errlen) != 0) return -1;
-  // batches of at most kPrefillCap tokens; a long segment continues in the next batch
+  // batches of at most the prefill batch cap tokens; a long segment continues in the next batch
   std::vector<halo_prefill_segment> rest(segs, segs + nseg);
   while (!rest.empty()) {
     std::vector<halo_prefill_segment> batch, next;
-    std::uint32_t room = kPrefillCap;
+    std::uint32_t room = PrefillCap(m->c);
     for (auto& g : rest) {
       const std::uint32_t n = std::min(g.length, room);
       if (n > 0) batch.push_back(halo_prefill_segment{g.session, g.start, n, 0});
@@ -1028,7 +1032,8 @@ int halo_model_prefill_trace(halo_model* m, const halo_prefill_segment* segs, ui
       return SetErr(err, errlen, "prefill trace: segment %u invalid", i), -1;
     total += g.length;
   }
-  if (total > kPrefillCap) return SetErr(err, errlen, "prefill trace: %u tokens > one batch of %u", total, kPrefillCap), -1;
+  if (total > PrefillCap(m->c))
+    return SetErr(err, errlen, "prefill trace: %u tokens > one batch of %u", total, PrefillCap(m->c)), -1;
   if (m->c.shared_ff != m->c.expert_ff) return SetErr(err, errlen, "prefill trace: shared ff != expert ff"), -1;
   if (PrefillAlloc(m, err, errlen) != 0) return -1;
   Tracer tr;

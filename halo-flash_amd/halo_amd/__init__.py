@@ -107,7 +107,7 @@ class ModelConfig(C.Structure):
         "vocab", "hidden", "layers", "attn_interval", "gdn_k_heads", "gdn_v_heads", "gdn_head_dim", "conv_kernel",
         "q_heads", "kv_heads", "head_dim", "rotary_dim", "n_experts", "n_used", "expert_ff", "shared_ff")] + [
         ("rope_theta", C.c_float), ("rms_eps", C.c_float)] + [
-        (n, C.c_uint32) for n in ("max_sessions", "max_context", "prefix_tokens", "pad")]
+        (n, C.c_uint32) for n in ("max_sessions", "max_context", "prefix_tokens", "prefill_batch")]
 
 
 class SampleParams(C.Structure):

@@ -29,7 +29,7 @@ typedef struct halo_model_config {
   float rope_theta, rms_eps;
   uint32_t max_sessions, max_context; /* context per session, including the shared prefix */
   uint32_t prefix_tokens;             /* shared-prefix capacity (multiple of 64; 0: none) */
-  uint32_t pad;
+  uint32_t prefill_batch;             /* tokens per prefill batch (0: 8192; 64 ... 65536) */
 } halo_model_config;
 
 typedef struct halo_model halo_model;

@@ -18,12 +18,13 @@ from teacher import LayerChecker, PrefillChecker
 pytestmark = pytest.mark.gpu
 
 
-def twin(max_sessions=2, prefix=0, ctx=64):
+def twin(max_sessions=2, prefix=0, ctx=64, prefill_batch=0):
     """C4's attention grouping (8 query heads per kv head, the shape the prefill attention kernel is built for)."""
     return H.ModelConfig(vocab=2048, hidden=1024, layers=4, attn_interval=4, gdn_k_heads=4, gdn_v_heads=8,
                          gdn_head_dim=128, conv_kernel=4, q_heads=16, kv_heads=2, head_dim=256, rotary_dim=64,
                          n_experts=16, n_used=4, expert_ff=256, shared_ff=256, rope_theta=1e7, rms_eps=1e-6,
-                         max_sessions=max_sessions, max_context=ctx, prefix_tokens=prefix)
+                         max_sessions=max_sessions, max_context=ctx, prefix_tokens=prefix,
+                         prefill_batch=prefill_batch)
 
 
 def _flips_ok(rep):
@@ -95,10 +96,10 @@ def test_split_prefill_calls(dev):
 
 @pytest.mark.timeout(600)
 def test_prefill_longer_than_one_batch(dev):
-    """2,100 tokens: halo_model_prefill splits the call into batches of 2,048 and 52; the same two batches, traced,
-    are checked layer by layer (the second from the state, ring and cache the first left), and the one-call prefill
-    gives the same logits bit for bit."""
-    cfg = twin(max_sessions=1, ctx=2176)
+    """2,100 tokens with a prefill batch of 2,048: halo_model_prefill splits the call into batches of 2,048 and 52;
+    the same two batches, traced, are checked layer by layer (the second from the state, ring and cache the first
+    left), and the one-call prefill gives the same logits bit for bit."""
+    cfg = twin(max_sessions=1, ctx=2176, prefill_batch=2048)
     model = H.Model(dev, cfg, seed=8)
     try:
         rng = np.random.default_rng(6)

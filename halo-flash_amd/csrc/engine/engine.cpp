@@ -169,10 +169,13 @@ int halo_op_matvec_q8a8(halo_engine* eng, const halo_q8_matrix* w, const int8_t*
     return Launch(eng, wide ? "halo_gemm_q8a8_mfma_t4" : "halo_gemm_q8a8_mfma_t1",
                   D3(CeilDiv(w->rows, 16), CeilDiv(m, wide ? 64 : 16)), D3(256), a, err, errlen);
   }
-  // Up to 8 tokens, a dense output and rows of at most 2048 columns: the grouped projection kernel in its
-  // quantized-input mode (one task of rows per wave, activations staged in LDS once per block). Wider rows measure
-  // faster on the per-group GEMV below, whose 64 lanes per row read the activations straight from the caches.
-  if (m <= 8 && (m == 1 || ystride == w->rows) && w->qstride == w->cols && w->cols <= 2048) {
+  // Up to 8 tokens, a dense output and rows of at most 2048 columns (4096 from 3 tokens up): the grouped projection
+  // kernel in its quantized-input mode (one task of rows per wave, activations staged in LDS once per block). Wider
+  // rows at 1-2 tokens measure faster on the per-group GEMV below, whose 64 lanes per row read the activations
+  // straight from the caches; from 3 tokens on its per-lane activation loads cost more than the LDS staging
+  // (2048 x 4096 at 4 tokens: 7.4 -> 5.2 us).
+  if (m <= 8 && (m == 1 || ystride == w->rows) && w->qstride == w->cols &&
+      (w->cols <= 2048 || (m >= 3 && w->cols <= 4096))) {
     halo_proj_input in{};
     in.xq = xq;
     in.xs = xs;

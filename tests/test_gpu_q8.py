@@ -116,7 +116,7 @@ def test_c0_gemv_4096(dev):
 
 
 @pytest.mark.parametrize("rows,cols", [(4096, 2048), (512, 2048), (2048, 4096)])
-@pytest.mark.parametrize("m", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 16])
 def test_c1_projections(dev, rows, cols, m):
     rng = np.random.default_rng(rows * 31 + cols + m)
     w, xq, xs, want, mag = _gemv_case(dev, rng, rows, cols, m)

@@ -407,43 +407,122 @@ extern "C" __global__ void __launch_bounds__(64)
   reinterpret_cast<float4*>(vpool + dst)[threadIdx.x] = reinterpret_cast<const float4*>(v + src)[threadIdx.x];
 }
 
-// ---- causal GQA attention for a ragged batch of prefill tokens (fp32 MFMA) ------------------------------------------
+// ---- causal GQA attention for a ragged batch of prefill tokens (split-fp16 MFMA) -----------------------------------
 // Reference semantics: ReferenceModel::Attention (src/model/reference.cpp:368-416, 492-527) for every token of a
 // prompt: softmax(q . K[0..p]^T / sqrt(d)) V[0..p] * sigmoid(gate), K / V already appended at the tokens' positions.
 // tiles [n][4] = {first token index in the batch, tokens (<= 8), session, position of the first token}; a tile's
 // tokens are consecutive positions of one session. Block (tile, kv head): 64 queries = 8 tokens x G = 8 q heads,
-// wave w the tokens 2w, 2w + 1 (query row r = 8 (token - 2w) + g). Per 32-key chunk: scores with
-// v_mfma_f32_16x16x4f32 (A = q rows kept in registers, B = K chunk in LDS), online softmax per row in the MFMA
-// output layout (a row's 32 scores sit in one 16-lane DPP row, two tiles), P through LDS, P V with the same MFMA
-// (B = V chunk in LDS). Output o (fp32, may be null) and its Q8 quantization oq / os (may be null), per token
+// wave w the tokens 2w, 2w + 1 (query row r = 8 (token - 2w) + g). Per 32-key chunk: scores on
+// the matrix cores (A = q rows kept in registers, B = K chunk in LDS), online softmax per row in the MFMA output
+// layout (a row's 32 scores sit in one 16-lane DPP row, two tiles), P through LDS, P V with the same MFMA (B = V
+// chunk in LDS). Output o (fp32, may be null) and its Q8 quantization oq / os (may be null), per token
 // [Hq * 256], after o /= l and o *= sigmoid(gate). q, gate [T][Hq][256].
+//
+// Every fp32 operand x enters as a pair of halves, hi = fp16(x) and lo = fp16(x - hi) (|x - hi - lo| <= 2^-22 |x|
+// for normal values), and each product is formed as hi * hi + hi * lo + lo * hi on v_mfma_f32_16x16x32_f16
+// (products of halves are exact in the fp32 accumulator; the dropped lo * lo term is below 2^-22 of the product).
+// Three fp16 MFMAs cost 3/16 of the fp32 MFMA issue time of the same products, so the scores and P V run at about
+// five times the fp32 MFMA rate with fp32-level accuracy. Inputs must lie within the fp16 range (|x| < 65504); q and
+// k are RMS-normalized and the probabilities are at most 1.
+// (An fp32 version of this kernel on v_mfma_f32_16x16x4f32 ran the C4 prefix prefill's attention at 78.8 TFLOP/s.)
+// The K and V chunks are converted once per block while staged in LDS: K as kh / kl [key][256] (16-byte chunk c of row key at
+// c ^ (key & 15): the 16 lanes reading one column of keys hit 16 different bank groups), V transposed as vh / vl
+// [dim][32 keys] (chunk c at c ^ ((dim >> 2) & 3)), so each MFMA operand is one 16-byte LDS read. The next chunk's
+// K and V are loaded into registers while the current chunk computes.
 namespace {
-constexpr int kPfTok = 8;
-constexpr int kKvStride = kHd + 4;  // LDS row stride in floats (keeps 16-byte alignment, spreads banks)
 typedef float V4F __attribute__((ext_vector_type(4)));
+typedef _Float16 H8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ void SplitHalves(const float (&x)[8], H8& hi, H8& lo) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const _Float16 h = static_cast<_Float16>(x[e]);
+    hi[e] = h;
+    lo[e] = static_cast<_Float16>(x[e] - static_cast<float>(h));
+  }
+}
+
+__device__ __forceinline__ V4F Mfma3(const H8& ah, const H8& al, const H8& bh, const H8& bl, V4F c) {
+  c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, c, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, c, 0, 0, 0);
+}
 }  // namespace
 
-extern "C" __global__ void __launch_bounds__(256) halo_attn_prefill(
+extern "C" __global__ void __launch_bounds__(256, 2) halo_attn_prefill(
     const float* __restrict__ q, const float* __restrict__ gate, const float* __restrict__ kpool,
     const float* __restrict__ vpool, const std::uint32_t* __restrict__ pages, const std::uint32_t* __restrict__ tiles,
     float* __restrict__ o, std::int8_t* __restrict__ oq, float* __restrict__ os, std::uint32_t Hq, std::uint32_t Hkv,
     std::uint32_t max_pages) {
-  __shared__ __attribute__((aligned(16))) float kc[kChunk * kKvStride];
-  __shared__ __attribute__((aligned(16))) float vc[kChunk * kKvStride];
-  __shared__ float pw[4][16][kChunk + 1];
+  __shared__ __attribute__((aligned(16))) _Float16 kh[kChunk * kHd], kl[kChunk * kHd];
+  __shared__ __attribute__((aligned(16))) _Float16 vh[kHd * kChunk], vl[kHd * kChunk];
+  __shared__ __attribute__((aligned(16))) _Float16 ph[4][16 * kChunk], pl[4][16 * kChunk];
   const std::uint32_t G = Hq / Hkv;
   const std::uint32_t* tl = tiles + 4 * static_cast<std::size_t>(blockIdx.x);
   const std::uint32_t first = tl[0], ntok = tl[1], sess = tl[2], p0 = tl[3];
   const std::uint32_t kvh = blockIdx.y;
   const std::uint32_t t = threadIdx.x, wave = t / kWave, lane = t % kWave;
-  const std::uint32_t row = lane % 16, kq = lane / 16;  // A-operand row / k slot of this lane
-  // this lane's A-operand query: row r = lane % 16 -> token 2 wave + r / 8, head g = r % 8
+  const std::uint32_t row = lane % 16, kq = lane / 16;
+  const std::uint32_t last = p0 + ntok - 1;
+  const std::uint32_t nchunks = last / kChunk + 1;
+  const std::uint32_t* pt = pages + static_cast<std::size_t>(sess) * max_pages;
+  // staging roles: K rows key = t / 8, 32-byte pieces part + 8 j; V keys 8 (t / 64) + e at dims 4 (t % 64) ..
+  const std::uint32_t skey = t / 8, spart = t % 8, vdg = t % 64, vkg = t / 64;
+  float4 kreg[8], vreg[8];
+  auto load_chunk = [&](std::uint32_t k0) {
+    {
+      const std::uint32_t kp = min(k0 + skey, last);
+      const float4* ks = reinterpret_cast<const float4*>(
+          kpool + ((static_cast<std::size_t>(pt[kp / kPage]) * Hkv + kvh) * kPage + kp % kPage) * kHd);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        kreg[2 * j] = ks[2 * (spart + 8 * j)];
+        kreg[2 * j + 1] = ks[2 * (spart + 8 * j) + 1];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const std::uint32_t kp = min(k0 + 8 * vkg + e, last);
+      vreg[e] = reinterpret_cast<const float4*>(
+          vpool + ((static_cast<std::size_t>(pt[kp / kPage]) * Hkv + kvh) * kPage + kp % kPage) * kHd)[vdg];
+    }
+  };
+  auto stage_chunk = [&]() {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float x[8] = {kreg[2 * j].x,     kreg[2 * j].y,     kreg[2 * j].z,     kreg[2 * j].w,
+                          kreg[2 * j + 1].x, kreg[2 * j + 1].y, kreg[2 * j + 1].z, kreg[2 * j + 1].w};
+      H8 hi, lo;
+      SplitHalves(x, hi, lo);
+      const std::uint32_t off = skey * kHd + 8 * ((spart + 8 * j) ^ (skey & 15));
+      *reinterpret_cast<H8*>(&kh[off]) = hi;
+      *reinterpret_cast<H8*>(&kl[off]) = lo;
+    }
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = d == 0 ? vreg[e].x : d == 1 ? vreg[e].y : d == 2 ? vreg[e].z : vreg[e].w;
+      H8 hi, lo;
+      SplitHalves(x, hi, lo);
+      const std::uint32_t dim = 4 * vdg + d;
+      const std::uint32_t off = dim * kChunk + 8 * (vkg ^ ((dim >> 2) & 3));
+      *reinterpret_cast<H8*>(&vh[off]) = hi;
+      *reinterpret_cast<H8*>(&vl[off]) = lo;
+    }
+  };
+  load_chunk(0);
+  // this lane's A-operand query: row r -> token 2 wave + r / 8, head r % 8; dims 32 c + 8 kq .. + 7
   const std::uint32_t qtok = min(2 * wave + row / 8, ntok - 1), qg = row % 8;
   const float* qrow = q + ((static_cast<std::size_t>(first) + qtok) * Hq + kvh * G + qg) * kHd;
-  float qa[kHd / 4];
+  H8 qh[kHd / 32], ql[kHd / 32];
 #pragma unroll
-  for (int s = 0; s < kHd / 4; ++s) qa[s] = qrow[4 * s + kq];
-  // output-layout rows of this lane: 4 kq + i -> token 2 wave + (4 kq + i) / 8
+  for (int c = 0; c < kHd / 32; ++c) {
+    const float4 a = *reinterpret_cast<const float4*>(qrow + 32 * c + 8 * kq);
+    const float4 b = *reinterpret_cast<const float4*>(qrow + 32 * c + 8 * kq + 4);
+    const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    SplitHalves(x, qh[c], ql[c]);
+  }
   std::uint32_t qpos[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) qpos[i] = p0 + 2 * wave + (4 * kq + i) / 8;
@@ -456,41 +535,29 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_prefill(
   }
 #pragma unroll
   for (int c = 0; c < kHd / 16; ++c) acc[c] = V4F{0.0f, 0.0f, 0.0f, 0.0f};
-  const std::uint32_t last = p0 + ntok - 1;  // the tile's last position: keys beyond it are never needed
-  const std::uint32_t nchunks = last / kChunk + 1;
-  const std::uint32_t* pt = pages + static_cast<std::size_t>(sess) * max_pages;
   const float scale = 1.0f / sqrtf(static_cast<float>(kHd));
+  _Float16* pwh = &ph[wave][0];
+  _Float16* pwl = &pl[wave][0];
   for (std::uint32_t ch = 0; ch < nchunks; ++ch) {
     const std::uint32_t k0 = ch * kChunk;
-    // stage the K and V chunk: thread t -> key t / 8, float4 pieces (t % 8) + 8 j
-    {
-      const std::uint32_t key = t / 8, part = t % 8;
-      const std::uint32_t kp = min(k0 + key, last);
-      const std::size_t rowoff = ((static_cast<std::size_t>(pt[kp / kPage]) * Hkv + kvh) * kPage + kp % kPage) * kHd;
-      const float4* ks = reinterpret_cast<const float4*>(kpool + rowoff);
-      const float4* vs = reinterpret_cast<const float4*>(vpool + rowoff);
-      float4 kv[8], vv[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        kv[j] = ks[part + 8 * j];
-        vv[j] = vs[part + 8 * j];
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        *reinterpret_cast<float4*>(&kc[key * kKvStride + 4 * (part + 8 * j)]) = kv[j];
-        *reinterpret_cast<float4*>(&vc[key * kKvStride + 4 * (part + 8 * j)]) = vv[j];
-      }
-    }
+    __syncthreads();  // every wave is done with the previous chunk's LDS
+    stage_chunk();
     __syncthreads();
-    // scores: two 16 x 16 tiles (keys k0 .. k0 + 15, k0 + 16 .. k0 + 31)
+    if (ch + 1 < nchunks) load_chunk(k0 + kChunk);  // in flight while this chunk computes
+    // scores: two 16 x 16 tiles (keys k0 .. k0 + 15, k0 + 16 .. k0 + 31); B lane (key row, dims 32 c + 8 kq ..)
     V4F sc[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      V4F c = {0.0f, 0.0f, 0.0f, 0.0f};
-      const float* kb = &kc[(16 * h + row) * kKvStride + kq];
+      V4F c4 = {0.0f, 0.0f, 0.0f, 0.0f};
+      const std::uint32_t key = 16 * h + row;
 #pragma unroll
-      for (int s = 0; s < kHd / 4; ++s) c = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s], kb[4 * s], c, 0, 0, 0);
-      sc[h] = c;
+      for (int c = 0; c < kHd / 32; ++c) {
+        const std::uint32_t off = key * kHd + 8 * ((4 * c + kq) ^ (key & 15));
+        const H8 bh = *reinterpret_cast<const H8*>(&kh[off]);
+        const H8 bl = *reinterpret_cast<const H8*>(&kl[off]);
+        c4 = Mfma3(qh[c], ql[c], bh, bl, c4);
+      }
+      sc[h] = c4;
     }
     // online softmax per output row (lanes 16 kq .. 16 kq + 15 hold one row's 32 scores)
     float alpha[4];
@@ -507,8 +574,14 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_prefill(
       const float e0 = s0 == -INFINITY ? 0.0f : expf(s0 - mx), e1 = s1 == -INFINITY ? 0.0f : expf(s1 - mx);
       l[i] = l[i] * alpha[i] + halo::GroupSum<16>(e0 + e1);
       m[i] = mx;
-      pw[wave][4 * kq + i][row] = e0;
-      pw[wave][4 * kq + i][16 + row] = e1;
+      // P row 4 kq + i, keys row and 16 + row; 16-byte chunk c of a P row at c ^ (kq & 3) (row >> 2 == kq)
+      const std::uint32_t pr = (4 * kq + i) * kChunk;
+      const _Float16 h0 = static_cast<_Float16>(e0), h1 = static_cast<_Float16>(e1);
+      const std::uint32_t o0 = pr + 8 * ((row / 8) ^ kq) + row % 8, o1 = pr + 8 * ((2 + row / 8) ^ kq) + row % 8;
+      pwh[o0] = h0;
+      pwl[o0] = static_cast<_Float16>(e0 - static_cast<float>(h0));
+      pwh[o1] = h1;
+      pwl[o1] = static_cast<_Float16>(e1 - static_cast<float>(h1));
     }
 #pragma unroll
     for (int c = 0; c < kHd / 16; ++c)
@@ -517,15 +590,18 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_prefill(
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // P V: A = P (row = query, k = key), B = V chunk (k = key, col = dim)
+    // P V: A = P (row = query, k = keys 8 kq ..), B = V (k = keys 8 kq .., col = dim 16 c + row)
+    const std::uint32_t pa = row * kChunk + 8 * (kq ^ ((row >> 2) & 3));
+    const H8 pah = *reinterpret_cast<const H8*>(&pwh[pa]);
+    const H8 pal = *reinterpret_cast<const H8*>(&pwl[pa]);
 #pragma unroll
-    for (int s = 0; s < kChunk / 4; ++s) {
-      const float pa = pw[wave][row][4 * s + kq];
-      const float* vb = &vc[(4 * s + kq) * kKvStride + row];
-#pragma unroll
-      for (int c = 0; c < kHd / 16; ++c) acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, vb[16 * c], acc[c], 0, 0, 0);
+    for (int c = 0; c < kHd / 16; ++c) {
+      const std::uint32_t dim = 16 * c + row;
+      const std::uint32_t off = dim * kChunk + 8 * (kq ^ ((dim >> 2) & 3));
+      const H8 bh = *reinterpret_cast<const H8*>(&vh[off]);
+      const H8 bl = *reinterpret_cast<const H8*>(&vl[off]);
+      acc[c] = Mfma3(pah, pal, bh, bl, acc[c]);
     }
-    __syncthreads();
   }
   // epilogue: rows 4 kq + i, dims 16 c + row
 #pragma unroll
@@ -545,7 +621,6 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_prefill(
         o[base + d1] = v1;
       }
       if (oq != nullptr) {
-        // one Q8 block = dims 32 (c / 2) .. + 31: the 16 lanes of this row x tiles c, c + 1
         const float amax = halo::GroupMax<16>(fmaxf(fabsf(v0), fabsf(v1)));
         const float qs = amax / 127.0f;
         if (live) {

@@ -2,7 +2,8 @@
 2 kv heads, head_dim 256, 16-token pages, a prefix shared by the sessions).
 
 Each token (session s, position p) is compared with the oracle's dense softmax attention (reference.cpp:492-527)
-over its session's K/V rows 0..p, times sigmoid(gate): within 1e-5 relative to sum|p||v| (fp32 MFMA accumulation),
+over its session's K/V rows 0..p, times sigmoid(gate): within 1e-5 relative to sum|p||v| (fp16 matrix-core products of split
+hi / lo operands, fp32 accumulation),
 and the Q8 output equal to the quantization of the fp32 output it wrote.
 """
 import ctypes

@@ -483,9 +483,9 @@ int PrefillBatch(halo_model* m, const std::vector<halo_prefill_segment>& segs, c
       {
         const halo_arg a[] = {Ptr(p.qkv.device), Ptr(ring), Ptr(L.conv_w.device), Ptr(p.abo.device), Ptr(L.a.device),
                               Ptr(L.dt.device), Ptr(ts), Ptr(tp), Ptr(tstart), Ptr(p.qb.device), Ptr(p.kb.device),
-                              Ptr(p.vb.device), Ptr(p.g.device), Ptr(p.beta.device), U32(Hk), U32(Hv), U32(d),
+                              Ptr(p.vb.device), Ptr(p.g.device), Ptr(p.beta.device), U32(T), U32(Hk), U32(Hv),
                               U32(c.conv_kernel), Val(eps)};
-        if (Launch(eng, "halo_gdn_prep_prefill", D3(T, C / 256), D3(256), a, err, errlen) != 0) return -1;
+        if (Launch(eng, "halo_gdn_prep_prefill", D3(CeilDiv(T, 16), C / 256), D3(64), a, err, errlen) != 0) return -1;
       }
       if (save("gq", HALO_TRACE_F32, p.qb.device, static_cast<std::size_t>(T) * Hk * d) != 0 ||
           save("gk", HALO_TRACE_F32, p.kb.device, static_cast<std::size_t>(T) * Hk * d) != 0 ||

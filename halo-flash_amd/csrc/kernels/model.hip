@@ -285,52 +285,65 @@ extern "C" __global__ void __launch_bounds__(256)
     x[t * H + i] = halo::F16(d[tok * (H / 32) + i / 32]) * static_cast<float>(qs[tok * qstride + i]);
 }
 
-// grid (T, C / 256), block 256: the DeltaNet prologue of halo_gdn_prep_decode for every token of a prefill batch. The
-// conv taps at positions below the token's run come from the session's conv ring (slot p % K), inside the run from
-// the batch's own projection rows, below 0 they are zero. Outputs for the chunked recurrence: q, k [T][Hk][d] and
-// v [T][Hv][d], g, beta [T][Hv], all fp32 as the decode step computes them.
-extern "C" __global__ void __launch_bounds__(256) halo_gdn_prep_prefill(
+// grid (ceil(T / 16), C / 256), block 64: the DeltaNet prologue of halo_gdn_prep_decode for every token of a prefill
+// batch. The conv taps at positions below the token's run come from the session's conv ring (slot p % K), inside
+// the run from the batch's own projection rows, below 0 they are zero. Outputs for the chunked recurrence: q, k
+// [T][Hk][d] and v [T][Hv][d], g, beta [T][Hv], all fp32 as the decode step computes them. Lane l of block (b, c)
+// owns channels 256 c + 4 l .. + 3 (16-byte loads and stores) for the block's 16 consecutive batch tokens; a q / k
+// head of 128 channels is 32 lanes, its sum of squares one 32-lane reduction. The tap rows of a token are the rows
+// the block just loaded for the tokens before it (L1 / L2 hits). d = 128, C % 256 == 0, K <= 8.
+extern "C" __global__ void __launch_bounds__(64) halo_gdn_prep_prefill(
     const float* __restrict__ qkv, const float* __restrict__ ring, const float* __restrict__ conv_w,
     const float* __restrict__ ab, const float* __restrict__ a, const float* __restrict__ dt,
     const std::uint32_t* __restrict__ tok_sess, const std::uint32_t* __restrict__ tok_pos,
     const std::uint32_t* __restrict__ seg_start, float* __restrict__ q, float* __restrict__ k,
-    float* __restrict__ v, float* __restrict__ g, float* __restrict__ beta, std::uint32_t Hk, std::uint32_t Hv,
-    std::uint32_t d, std::uint32_t K, float eps) {
-  __shared__ float part[4];
-  const std::size_t t = blockIdx.x;
-  const std::uint32_t Dk = Hk * d, Dv = Hv * d, C = 2 * Dk + Dv;
-  const std::uint32_t ch = blockIdx.y * blockDim.x + threadIdx.x;
-  const std::uint32_t s = tok_sess[t], p = tok_pos[t], p0 = seg_start[t];
-  const float x = qkv[t * C + ch];
-  float acc = conv_w[static_cast<std::size_t>(ch) * K + K - 1] * x;
-  for (std::uint32_t j = 0; j + 1 < K; ++j) {
-    // tap j reads position p - (K - 1) + j
-    const std::int64_t pp = static_cast<std::int64_t>(p) - static_cast<std::int64_t>(K - 1) + j;
-    float xv = 0.0f;
-    if (pp >= static_cast<std::int64_t>(p0))
-      xv = qkv[(t - (p - static_cast<std::uint32_t>(pp))) * C + ch];
-    else if (pp >= 0)
-      xv = ring[(static_cast<std::size_t>(s) * K + static_cast<std::uint32_t>(pp) % K) * C + ch];
-    acc += conv_w[static_cast<std::size_t>(ch) * K + j] * xv;
-  }
-  const float y = halo::Silu(acc);
-  const std::uint32_t wave = threadIdx.x / kWave;
-  const float ss = halo::GroupSum(y * y);
-  if (threadIdx.x % kWave == 0) part[wave] = ss;
-  __syncthreads();
-  const std::uint32_t head = ch / d;
-  if (ch < 2 * Dk) {
-    const std::uint32_t w0 = (wave / 2) * 2;
-    const float sc = 1.0f / sqrtf(part[w0] + part[w0 + 1] + eps);
-    float* dst = head < Hk ? q + (t * Hk + head) * d : k + (t * Hk + head - Hk) * d;
-    dst[ch % d] = y * sc;
-  } else {
-    v[t * Dv + ch - 2 * Dk] = y;
-  }
-  if (blockIdx.y == 0 && threadIdx.x < Hv) {
-    const std::uint32_t h = threadIdx.x;
-    g[t * Hv + h] = a[h] * halo::Softplus(ab[t * 2 * Hv + h] + dt[h]);
-    beta[t * Hv + h] = halo::Sigmoid(ab[t * 2 * Hv + Hv + h]);
+    float* __restrict__ v, float* __restrict__ g, float* __restrict__ beta, std::uint32_t T, std::uint32_t Hk,
+    std::uint32_t Hv, std::uint32_t K, float eps) {
+  constexpr std::uint32_t kD = 128, kTok = 16, kMaxK = 8;
+  const std::uint32_t Dk = Hk * kD, Dv = Hv * kD, C = 2 * Dk + Dv;
+  const std::uint32_t lane = threadIdx.x, ch = blockIdx.y * 256 + 4 * lane;
+  const std::uint32_t t0 = blockIdx.x * kTok, t1 = min(t0 + kTok, T);
+  float w[4][kMaxK];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (std::uint32_t j = 0; j < kMaxK; ++j) w[c][j] = j < K ? conv_w[static_cast<std::size_t>(ch + c) * K + j] : 0.0f;
+  const bool is_qk = ch < 2 * Dk;
+  for (std::uint32_t t = t0; t < t1; ++t) {
+    const std::uint32_t s = tok_sess[t], p = tok_pos[t], p0 = seg_start[t];
+    const float4 x = *reinterpret_cast<const float4*>(qkv + static_cast<std::size_t>(t) * C + ch);
+    float acc[4] = {w[0][K - 1] * x.x, w[1][K - 1] * x.y, w[2][K - 1] * x.z, w[3][K - 1] * x.w};
+    for (std::uint32_t j = 0; j + 1 < K; ++j) {
+      // tap j reads position p - (K - 1) + j
+      const std::int64_t pp = static_cast<std::int64_t>(p) - static_cast<std::int64_t>(K - 1) + j;
+      float4 xv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (pp >= static_cast<std::int64_t>(p0))
+        xv = *reinterpret_cast<const float4*>(qkv + (static_cast<std::size_t>(t) - (p - static_cast<std::uint32_t>(pp))) * C + ch);
+      else if (pp >= 0)
+        xv = *reinterpret_cast<const float4*>(ring + (static_cast<std::size_t>(s) * K + static_cast<std::uint32_t>(pp) % K) * C + ch);
+      acc[0] += w[0][j] * xv.x;
+      acc[1] += w[1][j] * xv.y;
+      acc[2] += w[2][j] * xv.z;
+      acc[3] += w[3][j] * xv.w;
+    }
+    float y[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) y[c] = halo::Silu(acc[c]);
+    if (is_qk) {
+      const float ss = halo::GroupSum<32>((y[0] * y[0] + y[1] * y[1]) + (y[2] * y[2] + y[3] * y[3]));
+      const float sc = 1.0f / sqrtf(ss + eps);
+      const std::uint32_t head = ch / kD;
+      float* dst = head < Hk ? q + (static_cast<std::size_t>(t) * Hk + head) * kD
+                             : k + (static_cast<std::size_t>(t) * Hk + head - Hk) * kD;
+      *reinterpret_cast<float4*>(dst + ch % kD) = make_float4(y[0] * sc, y[1] * sc, y[2] * sc, y[3] * sc);
+    } else {
+      *reinterpret_cast<float4*>(v + static_cast<std::size_t>(t) * Dv + ch - 2 * Dk) = make_float4(y[0], y[1], y[2], y[3]);
+    }
+    if (blockIdx.y == 0)
+      for (std::uint32_t h = lane; h < Hv; h += 64) {
+        g[static_cast<std::size_t>(t) * Hv + h] = a[h] * halo::Softplus(ab[static_cast<std::size_t>(t) * 2 * Hv + h] + dt[h]);
+        beta[static_cast<std::size_t>(t) * Hv + h] = halo::Sigmoid(ab[static_cast<std::size_t>(t) * 2 * Hv + Hv + h]);
+      }
   }
 }
 

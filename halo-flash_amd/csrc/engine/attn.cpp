@@ -63,8 +63,9 @@ int halo_op_attn_decode_q8(halo_engine* eng, const halo_paged_kv* kv, const floa
   {
     const halo_arg a[] = {Ptr(q), Ptr(kv->k_pool), Ptr(kv->v_pool), Ptr(kv->pages), Ptr(kv->nkv), Ptr(pm), Ptr(pl),
                           Ptr(pacc), U32(S), U32(Hq), U32(Hkv), U32(kv->prefix), U32(kv->max_pages), U32(pc), U32(sc)};
-    if (Launch(eng, "halo_attn_decode_partial", D3(static_cast<std::uint32_t>(items)), D3(256), a, err, errlen) != 0)
-      return -1;
+    // the same arithmetic per query as the fused step launch of this batch size (halo_op_attn_decode_step_q8)
+    const char* name = slots <= 8 ? "halo_attn_decode_partial" : "halo_attn_decode_partial_mma";
+    if (Launch(eng, name, D3(static_cast<std::uint32_t>(items)), D3(256), a, err, errlen) != 0) return -1;
   }
   const halo_arg a[] = {Ptr(pm), Ptr(pl), Ptr(pacc), Ptr(gate), Ptr(o), Ptr(oq), Ptr(os), U32(S), U32(Hq), U32(Hkv),
                         U32(pc), U32(sc)};

@@ -20,6 +20,31 @@ constexpr int kChunk = 32;    // tokens per block
 constexpr int kMaxQ = 32;     // query vectors per block (sessions * G)
 }  // namespace
 
+// fp32 operands on fp16 matrix cores: x enters as the pair hi = fp16(x), lo = fp16(x - hi) (|x - hi - lo| <= 2^-22 |x|
+// for normal values) and each product as hi * hi + hi * lo + lo * hi on v_mfma_f32_16x16x32_f16 (products of halves
+// are exact in the fp32 accumulator; the dropped lo * lo term is below 2^-22 of the product). Three fp16 MFMAs take
+// 3/16 of the fp32 MFMA issue time of the same products. Operands must lie within the fp16 range (|x| < 65504).
+namespace {
+typedef float V4F __attribute__((ext_vector_type(4)));
+typedef _Float16 H8 __attribute__((ext_vector_type(8)));
+typedef _Float16 H4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void SplitHalves(const float (&x)[8], H8& hi, H8& lo) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const _Float16 h = static_cast<_Float16>(x[e]);
+    hi[e] = h;
+    lo[e] = static_cast<_Float16>(x[e] - static_cast<float>(h));
+  }
+}
+
+__device__ __forceinline__ V4F Mfma3(const H8& ah, const H8& al, const H8& bh, const H8& bl, V4F c) {
+  c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, c, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, c, 0, 0, 0);
+}
+}  // namespace
+
 // grid (Hkv * (prefix_chunks + S * suffix_chunks)), block 256.
 //   q [S][Hq][256]; kpool, vpool [pages][Hkv][16][256]; pages [S][max_pages]; nkv [S] visible positions;
 //   partial m, l [items][S * G], acc [items][S * G][256] (item = blockIdx.x).
@@ -37,7 +62,7 @@ namespace {
 // position (the last suffix chunk) forms that position's K (RMSNorm wk, rotation) and V from kin / vin [S][Hkv][256],
 // appends them to the pools and uses them for that row: the prologue launch before the attention disappears. The
 // arithmetic is halo_attn_prep_decode's (halo::NormRopeHead), so q, K and V carry the same bits.
-template <bool kFused, int kQW = 1>
+template <bool kFused, int kQW = 1, bool kMma = false>
 __device__ __forceinline__ void AttnDecodePartial(
     const float* __restrict__ q, const float* __restrict__ kin, const float* __restrict__ vin,
     const float* __restrict__ wq, const float* __restrict__ wk, float* __restrict__ kpool, float* __restrict__ vpool,
@@ -45,7 +70,8 @@ __device__ __forceinline__ void AttnDecodePartial(
     float* __restrict__ pl, float* __restrict__ pacc, std::uint32_t S, std::uint32_t Hq, std::uint32_t Hkv,
     std::uint32_t prefix, std::uint32_t max_pages, std::uint32_t prefix_chunks, std::uint32_t suffix_chunks,
     std::uint32_t rot, float theta, float eps) {
-  __shared__ float qs[kMaxQ][kHd];       // 32 KB
+  // 32 KB: the queries, then the K chunk as halves, then the V chunk as halves (38 KB in all: four blocks per CU)
+  __shared__ __attribute__((aligned(16))) float qs[kMaxQ][kHd];
   __shared__ __attribute__((aligned(16))) float sc[kMaxQ][kChunk + 4];  // rows 16-byte aligned: vector reads
   static_assert(kChunk == 32 && kPage == 16, "two pages per chunk, two tokens per 16-lane row");
   const std::uint32_t G = Hq / Hkv, x = blockIdx.x, kvh = x % Hkv, c = x / Hkv;
@@ -110,17 +136,29 @@ __device__ __forceinline__ void AttnDecodePartial(
 #pragma unroll
     for (int u = 0; u < 4; ++u) kf[h][u] = kr[16 * u + sub];
   }
+  float4 vq[2][4];
+  const std::uint32_t vdg = t % 64, vkg = t / 64;
+  float4 vreg[8];
+  if constexpr (!kMma) {
   // V as 16-byte loads of the two pages (each page's 16 rows are 16 KB contiguous; thread t takes float4 t of every
   // 4 KB part: row 4 part + t / 64, dims 4 (t % 64) ..): 4-byte loads of a column would take 32 instructions per
   // thread and run the chunk's V stream at half the rate. Staged through LDS below, so the weighted sum still reads
   // one dim of every row.
-  float4 vq[2][4];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const float4* vp = reinterpret_cast<const float4*>(vpool + (static_cast<std::size_t>(h ? pg1 : pg0) * Hkv + kvh) *
                                                                    kPage * kHd);
 #pragma unroll
     for (int u = 0; u < 4; ++u) vq[h][u] = vp[u * 256 + t];
+  }
+  } else {
+  // V: thread t takes keys 8 (t / 64) + e (e < 8, one page) at dims 4 (t % 64) ..: each load instruction reads one
+  // whole 1 KB row; staged transposed below (positions past the visible range are zeroed there)
+  {
+    const float* vp = vpool + ((static_cast<std::size_t>(vkg < 2 ? pg0 : pg1) * Hkv + kvh) * kPage) * kHd + 4 * vdg;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vreg[e] = *reinterpret_cast<const float4*>(vp + ((8 * vkg + e) % kPage) * kHd);
+  }
   }
   // queries of this kv head: slot i = session * G + g (prefix) or g (suffix)
   __shared__ __attribute__((aligned(16))) float knew[kFused ? 2 : 1][kFused ? kHd : 4];
@@ -164,6 +202,7 @@ __device__ __forceinline__ void AttnDecodePartial(
       reinterpret_cast<float4*>(&qs[qi][0])[d4] = v;
     }
   }
+  if constexpr (!kMma) {
   __syncthreads();
   if (owner) {
     // the newest row's K from LDS in place of the pool's (not yet written when the loads were issued)
@@ -254,25 +293,158 @@ __device__ __forceinline__ void AttnDecodePartial(
         a_out[static_cast<std::size_t>(slot) * kHd + t] = acc[k];
       }
   }
+  } else {
+  __syncthreads();
+  // Matrix-core tiles: nqt tiles of 16 query rows (rows past nq repeat the last query and are never stored); the
+  // scores are tiles (query tile w / 2, key tile w % 2) of waves w < 2 nqt; each query row's products, softmax and
+  // weighted sum depend only on that row, so a query gets the same bits whichever block and batch it is scored in.
+  const std::uint32_t nqt = (nq + 15) / 16, kq = lane / 16, lr = lane % 16;
+  const std::uint32_t qt = wave / 2, kt = wave % 2;
+  const bool score_wave = qt < nqt;
+  H8 qh[kHd / 32], ql[kHd / 32];
+  if (score_wave) {
+    const float* qr = &qs[min(16 * qt + lr, nq - 1)][0];
+#pragma unroll
+    for (int c = 0; c < kHd / 32; ++c) {
+      const float4 a0 = *reinterpret_cast<const float4*>(qr + 32 * c + 8 * kq);
+      const float4 a1 = *reinterpret_cast<const float4*>(qr + 32 * c + 8 * kq + 4);
+      const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      SplitHalves(x, qh[c], ql[c]);
+    }
+  }
+  __syncthreads();  // qs is free: the K chunk goes there as halves
+  // K halves kh / kl [32 keys][256]: 16-byte chunk c of key row j at c ^ (j & 15) (the 16 lanes of an operand read
+  // take 16 different bank groups); the newest row (owner) from LDS, not yet in the pool when it was loaded
+  _Float16* kh = reinterpret_cast<_Float16*>(&qs[0][0]);
+  _Float16* kl = kh + kChunk * kHd;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const std::uint32_t j = r + 16 * h;
+    const bool fresh = owner && start + j == last;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const std::uint32_t dim = 64 * u + 4 * sub;
+      const float4 kv = fresh ? *reinterpret_cast<const float4*>(&knew[0][dim]) : kf[h][u];
+      const float x[4] = {kv.x, kv.y, kv.z, kv.w};
+      const std::uint32_t off = j * kHd + 8 * ((dim / 8) ^ (j & 15)) + dim % 8;
+      H4 hi, lo;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        hi[e] = static_cast<_Float16>(x[e]);
+        lo[e] = static_cast<_Float16>(x[e] - static_cast<float>(hi[e]));
+      }
+      *reinterpret_cast<H4*>(&kh[off]) = hi;
+      *reinterpret_cast<H4*>(&kl[off]) = lo;
+    }
+  }
+  __syncthreads();
+  const float scale = 1.0f / sqrtf(static_cast<float>(kHd));
+  if (score_wave) {
+    V4F c4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    const std::uint32_t key = 16 * kt + lr;
+#pragma unroll
+    for (int c = 0; c < kHd / 32; ++c) {
+      const std::uint32_t off = key * kHd + 8 * ((4 * c + kq) ^ (key & 15));
+      c4 = Mfma3(qh[c], ql[c], *reinterpret_cast<const H8*>(&kh[off]), *reinterpret_cast<const H8*>(&kl[off]), c4);
+    }
+    // C tile: lane (key lr, kq) holds rows 16 qt + 4 kq + i
+    const bool live = start + key < limit;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const std::uint32_t qi = 16 * qt + 4 * kq + i;
+      if (qi < nq) sc[qi][key] = live ? c4[i] * scale : -INFINITY;
+    }
+  }
+  __syncthreads();
+  // the K chunk is done with: the V chunk goes to the same LDS as halves transposed, vh / vl [256 dims][32 keys]
+  // (chunk c of 8 keys of a dim row at c ^ ((dim >> 2) & 3))
+  _Float16* vh = kh;
+  _Float16* vl = kh + kHd * kChunk;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const std::uint32_t dim = 4 * vdg + d;
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const std::uint32_t j = 8 * vkg + e;
+      const float4 vv = vreg[e];
+      float val = d == 0 ? vv.x : d == 1 ? vv.y : d == 2 ? vv.z : vv.w;
+      if (owner && start + j == last) val = knew[kFused ? 1 : 0][dim];
+      x[e] = start + j < limit ? val : 0.0f;
+    }
+    H8 hi, lo;
+    SplitHalves(x, hi, lo);
+    const std::uint32_t off = dim * kChunk + 8 * (vkg ^ ((dim >> 2) & 3));
+    *reinterpret_cast<H8*>(&vh[off]) = hi;
+    *reinterpret_cast<H8*>(&vl[off]) = lo;
+  }
+  // softmax over the chunk per query: wave w takes queries w, w + 4, ...; lanes 0..31 are the tokens
+  for (std::uint32_t i = wave; i < nq; i += 4) {
+    const float s = lane < kChunk ? sc[i][lane] : -INFINITY;
+    const float m = halo::GroupMax(s);
+    const float p = s == -INFINITY ? 0.0f : expf(s - m);
+    const float l = halo::GroupSum(p);
+    if (lane < kChunk) sc[i][lane] = p;
+    if (lane == 0) {
+      const std::uint32_t slot = is_prefix ? i : sess * G + i;
+      m_out[slot] = m;
+      l_out[slot] = l;
+    }
+  }
+  __syncthreads();
+  // weighted V: output tiles (query tile, 16-dim tile); two query tiles: wave w takes tile w / 2, dim tiles
+  // 8 (w % 2) ..; one: dim tiles 4 w .. + 3
+  const std::uint32_t pqt = nqt == 2 ? wave / 2 : 0, ndt = nqt == 2 ? 8 : 4, dt0 = nqt == 2 ? 8 * (wave % 2) : 4 * wave;
+  H8 pah, pal;
+  {
+    const float* pr = &sc[min(16 * pqt + lr, nq - 1)][8 * kq];
+    const float4 a0 = *reinterpret_cast<const float4*>(pr), a1 = *reinterpret_cast<const float4*>(pr + 4);
+    const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    SplitHalves(x, pah, pal);
+  }
+#pragma unroll
+  for (std::uint32_t dc = 0; dc < 8; ++dc) {
+    if (dc >= ndt) break;
+    const std::uint32_t dim = 16 * (dt0 + dc) + lr;
+    const std::uint32_t off = dim * kChunk + 8 * (kq ^ ((dim >> 2) & 3));
+    const V4F acc = Mfma3(pah, pal, *reinterpret_cast<const H8*>(&vh[off]), *reinterpret_cast<const H8*>(&vl[off]),
+                          V4F{0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const std::uint32_t qi = 16 * pqt + 4 * kq + i;
+      if (qi < nq) {
+        const std::uint32_t slot = is_prefix ? qi : sess * G + qi;
+        a_out[static_cast<std::size_t>(slot) * kHd + dim] = acc[i];
+      }
+    }
+  }
+  }
 }
 }  // namespace
 
-extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
-    const float* __restrict__ q, const float* __restrict__ kpool, const float* __restrict__ vpool,
-    const std::uint32_t* __restrict__ pages, const std::uint32_t* __restrict__ nkv, float* __restrict__ pm,
-    float* __restrict__ pl, float* __restrict__ pacc, std::uint32_t S, std::uint32_t Hq, std::uint32_t Hkv,
-    std::uint32_t prefix, std::uint32_t max_pages, std::uint32_t prefix_chunks, std::uint32_t suffix_chunks) {
-  AttnDecodePartial<false>(q, nullptr, nullptr, nullptr, nullptr, const_cast<float*>(kpool), const_cast<float*>(vpool),
-                           pages, nkv, pm, pl, pacc, S, Hq, Hkv, prefix, max_pages, prefix_chunks, suffix_chunks, 0,
-                           0.0f, 0.0f);
-}
+#define HALO_ATTN_PARTIAL(NAME, MMA)                                                                                   \
+  extern "C" __global__ void __launch_bounds__(256) NAME(                                                             \
+      const float* __restrict__ q, const float* __restrict__ kpool, const float* __restrict__ vpool,                 \
+      const std::uint32_t* __restrict__ pages, const std::uint32_t* __restrict__ nkv, float* __restrict__ pm,        \
+      float* __restrict__ pl, float* __restrict__ pacc, std::uint32_t S, std::uint32_t Hq, std::uint32_t Hkv,      \
+      std::uint32_t prefix, std::uint32_t max_pages, std::uint32_t prefix_chunks, std::uint32_t suffix_chunks) {    \
+    AttnDecodePartial<false, 1, MMA>(q, nullptr, nullptr, nullptr, nullptr, const_cast<float*>(kpool),             \
+                                     const_cast<float*>(vpool), pages, nkv, pm, pl, pacc, S, Hq, Hkv, prefix,      \
+                                     max_pages, prefix_chunks, suffix_chunks, 0, 0.0f, 0.0f);                     \
+  }
+// fp32 VALU dot products (one session: eight queries per kv head, latency-bound) / split-fp16 matrix cores (several
+// sessions: up to 32 queries per block score a shared-prefix chunk)
+HALO_ATTN_PARTIAL(halo_attn_decode_partial, false)
+HALO_ATTN_PARTIAL(halo_attn_decode_partial_mma, true)
+#undef HALO_ATTN_PARTIAL
 
 // The partial launch with the attention prologue folded in (see AttnDecodePartial<true>): qg [S][Hq][2 * 256],
 // kin, vin [S][Hkv][256], wq, wk [256]; rot <= 128. Every session's newest position nkv[s] - 1 must lie past the
 // shared prefix (it is in that session's last suffix chunk). Same grid and partial outputs as
 // halo_attn_decode_partial; the gate for the combine is the second half of each qg head.
-// _qk: up to 32 query vectors per block (S * Hq / Hkv <= 32); _qk2: up to 8 (two per wave).
-#define HALO_ATTN_PARTIAL_QK(NAME, QW)                                                                           \
+// _qk: up to 32 query vectors per block (S * Hq / Hkv <= 32), split-fp16 matrix cores; _qk2: up to 8 (two per
+// wave), fp32 VALU.
+#define HALO_ATTN_PARTIAL_QK(NAME, QW, MMA)                                                                           \
   extern "C" __global__ void __launch_bounds__(256) NAME(                                                       \
       const float* __restrict__ qg, const float* __restrict__ kin, const float* __restrict__ vin,               \
       const float* __restrict__ wq, const float* __restrict__ wk, float* __restrict__ kpool,                    \
@@ -280,11 +452,11 @@ extern "C" __global__ void __launch_bounds__(256) halo_attn_decode_partial(
       float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ pacc, std::uint32_t S, std::uint32_t Hq, \
       std::uint32_t Hkv, std::uint32_t prefix, std::uint32_t max_pages, std::uint32_t prefix_chunks,            \
       std::uint32_t suffix_chunks, std::uint32_t rot, float theta, float eps) {                                 \
-    AttnDecodePartial<true, QW>(qg, kin, vin, wq, wk, kpool, vpool, pages, nkv, pm, pl, pacc, S, Hq, Hkv, prefix,  \
+    AttnDecodePartial<true, QW, MMA>(qg, kin, vin, wq, wk, kpool, vpool, pages, nkv, pm, pl, pacc, S, Hq, Hkv, prefix,  \
                                 max_pages, prefix_chunks, suffix_chunks, rot, theta, eps);                       \
   }
-HALO_ATTN_PARTIAL_QK(halo_attn_decode_partial_qk, 8)
-HALO_ATTN_PARTIAL_QK(halo_attn_decode_partial_qk2, 2)
+HALO_ATTN_PARTIAL_QK(halo_attn_decode_partial_qk, 8, true)
+HALO_ATTN_PARTIAL_QK(halo_attn_decode_partial_qk2, 2, false)
 #undef HALO_ATTN_PARTIAL_QK
 
 
@@ -429,25 +601,6 @@ extern "C" __global__ void __launch_bounds__(64)
 // c ^ (key & 15): the 16 lanes reading one column of keys hit 16 different bank groups), V transposed as vh / vl
 // [dim][32 keys] (chunk c at c ^ ((dim >> 2) & 3)), so each MFMA operand is one 16-byte LDS read. The next chunk's
 // K and V are loaded into registers while the current chunk computes.
-namespace {
-typedef float V4F __attribute__((ext_vector_type(4)));
-typedef _Float16 H8 __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ void SplitHalves(const float (&x)[8], H8& hi, H8& lo) {
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const _Float16 h = static_cast<_Float16>(x[e]);
-    hi[e] = h;
-    lo[e] = static_cast<_Float16>(x[e] - static_cast<float>(h));
-  }
-}
-
-__device__ __forceinline__ V4F Mfma3(const H8& ah, const H8& al, const H8& bh, const H8& bl, V4F c) {
-  c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, c, 0, 0, 0);
-  c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, c, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, c, 0, 0, 0);
-}
-}  // namespace
 
 extern "C" __global__ void __launch_bounds__(256, 2) halo_attn_prefill(
     const float* __restrict__ q, const float* __restrict__ gate, const float* __restrict__ kpool,

@@ -20,29 +20,16 @@ constexpr int kChunk = 32;    // tokens per block
 constexpr int kMaxQ = 32;     // query vectors per block (sessions * G)
 }  // namespace
 
-// fp32 operands on fp16 matrix cores: x enters as the pair hi = fp16(x), lo = fp16(x - hi) (|x - hi - lo| <= 2^-22 |x|
-// for normal values) and each product as hi * hi + hi * lo + lo * hi on v_mfma_f32_16x16x32_f16 (products of halves
-// are exact in the fp32 accumulator; the dropped lo * lo term is below 2^-22 of the product). Three fp16 MFMAs take
-// 3/16 of the fp32 MFMA issue time of the same products. Operands must lie within the fp16 range (|x| < 65504).
+using halo::H4;
+using halo::H8;
+using halo::Mfma3;
+using halo::SplitHalves;
+using halo::V4F;
 namespace {
-typedef float V4F __attribute__((ext_vector_type(4)));
-typedef _Float16 H8 __attribute__((ext_vector_type(8)));
-typedef _Float16 H4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ void SplitHalves(const float (&x)[8], H8& hi, H8& lo) {
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const _Float16 h = static_cast<_Float16>(x[e]);
-    hi[e] = h;
-    lo[e] = static_cast<_Float16>(x[e] - static_cast<float>(h));
-  }
-}
-
-__device__ __forceinline__ V4F Mfma3(const H8& ah, const H8& al, const H8& bh, const H8& bl, V4F c) {
-  c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, c, 0, 0, 0);
-  c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, c, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, c, 0, 0, 0);
-}
+// Operand scales of the split-fp16 paths (powers of two, undone on the results): q and k (RMS-normalized) and V by 2^8,
+// so values down to 2^-11 keep the full 22-bit split and |q|, |k|, |V| up to 255 stay in the fp16 range; the
+// probabilities (<= 1) by 2^14.
+constexpr float kSqk = 256.0f, kSvv = 256.0f, kSpp = 16384.0f;
 }  // namespace
 
 // grid (Hkv * (prefix_chunks + S * suffix_chunks)), block 256.
@@ -309,7 +296,7 @@ __device__ __forceinline__ void AttnDecodePartial(
       const float4 a0 = *reinterpret_cast<const float4*>(qr + 32 * c + 8 * kq);
       const float4 a1 = *reinterpret_cast<const float4*>(qr + 32 * c + 8 * kq + 4);
       const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-      SplitHalves(x, qh[c], ql[c]);
+      SplitHalves(x, qh[c], ql[c], kSqk);
     }
   }
   __syncthreads();  // qs is free: the K chunk goes there as halves
@@ -330,8 +317,9 @@ __device__ __forceinline__ void AttnDecodePartial(
       H4 hi, lo;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        hi[e] = static_cast<_Float16>(x[e]);
-        lo[e] = static_cast<_Float16>(x[e] - static_cast<float>(hi[e]));
+        const float xs = kSqk * x[e];
+        hi[e] = static_cast<_Float16>(xs);
+        lo[e] = static_cast<_Float16>(xs - static_cast<float>(hi[e]));
       }
       *reinterpret_cast<H4*>(&kh[off]) = hi;
       *reinterpret_cast<H4*>(&kl[off]) = lo;
@@ -352,7 +340,7 @@ __device__ __forceinline__ void AttnDecodePartial(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const std::uint32_t qi = 16 * qt + 4 * kq + i;
-      if (qi < nq) sc[qi][key] = live ? c4[i] * scale : -INFINITY;
+      if (qi < nq) sc[qi][key] = live ? c4[i] * (scale / (kSqk * kSqk)) : -INFINITY;
     }
   }
   __syncthreads();
@@ -373,7 +361,7 @@ __device__ __forceinline__ void AttnDecodePartial(
       x[e] = start + j < limit ? val : 0.0f;
     }
     H8 hi, lo;
-    SplitHalves(x, hi, lo);
+    SplitHalves(x, hi, lo, kSvv);
     const std::uint32_t off = dim * kChunk + 8 * (vkg ^ ((dim >> 2) & 3));
     *reinterpret_cast<H8*>(&vh[off]) = hi;
     *reinterpret_cast<H8*>(&vl[off]) = lo;
@@ -400,7 +388,7 @@ __device__ __forceinline__ void AttnDecodePartial(
     const float* pr = &sc[min(16 * pqt + lr, nq - 1)][8 * kq];
     const float4 a0 = *reinterpret_cast<const float4*>(pr), a1 = *reinterpret_cast<const float4*>(pr + 4);
     const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-    SplitHalves(x, pah, pal);
+    SplitHalves(x, pah, pal, kSpp);
   }
 #pragma unroll
   for (std::uint32_t dc = 0; dc < 8; ++dc) {
@@ -414,7 +402,7 @@ __device__ __forceinline__ void AttnDecodePartial(
       const std::uint32_t qi = 16 * pqt + 4 * kq + i;
       if (qi < nq) {
         const std::uint32_t slot = is_prefix ? qi : sess * G + qi;
-        a_out[static_cast<std::size_t>(slot) * kHd + dim] = acc[i];
+        a_out[static_cast<std::size_t>(slot) * kHd + dim] = acc[i] * (1.0f / (kSpp * kSvv));
       }
     }
   }
@@ -594,8 +582,8 @@ extern "C" __global__ void __launch_bounds__(64)
 // for normal values), and each product is formed as hi * hi + hi * lo + lo * hi on v_mfma_f32_16x16x32_f16
 // (products of halves are exact in the fp32 accumulator; the dropped lo * lo term is below 2^-22 of the product).
 // Three fp16 MFMAs cost 3/16 of the fp32 MFMA issue time of the same products, so the scores and P V run at about
-// five times the fp32 MFMA rate with fp32-level accuracy. Inputs must lie within the fp16 range (|x| < 65504); q and
-// k are RMS-normalized and the probabilities are at most 1.
+// five times the fp32 MFMA rate with fp32-level accuracy. q, k and V are scaled by 2^8 and the probabilities by 2^14
+// before the split (kSqk, kSvv, kSpp): |q|, |k|, |V| must stay below 255.
 // (An fp32 version of this kernel on v_mfma_f32_16x16x4f32 ran the C4 prefix prefill's attention at 78.8 TFLOP/s.)
 // The K and V chunks are converted once per block while staged in LDS: K as kh / kl [key][256] (16-byte chunk c of row key at
 // c ^ (key & 15): the 16 lanes reading one column of keys hit 16 different bank groups), V transposed as vh / vl
@@ -646,7 +634,7 @@ extern "C" __global__ void __launch_bounds__(256, 2) halo_attn_prefill(
       const float x[8] = {kreg[2 * j].x,     kreg[2 * j].y,     kreg[2 * j].z,     kreg[2 * j].w,
                           kreg[2 * j + 1].x, kreg[2 * j + 1].y, kreg[2 * j + 1].z, kreg[2 * j + 1].w};
       H8 hi, lo;
-      SplitHalves(x, hi, lo);
+      SplitHalves(x, hi, lo, kSqk);
       const std::uint32_t off = skey * kHd + 8 * ((spart + 8 * j) ^ (skey & 15));
       *reinterpret_cast<H8*>(&kh[off]) = hi;
       *reinterpret_cast<H8*>(&kl[off]) = lo;
@@ -657,7 +645,7 @@ extern "C" __global__ void __launch_bounds__(256, 2) halo_attn_prefill(
 #pragma unroll
       for (int e = 0; e < 8; ++e) x[e] = d == 0 ? vreg[e].x : d == 1 ? vreg[e].y : d == 2 ? vreg[e].z : vreg[e].w;
       H8 hi, lo;
-      SplitHalves(x, hi, lo);
+      SplitHalves(x, hi, lo, kSvv);
       const std::uint32_t dim = 4 * vdg + d;
       const std::uint32_t off = dim * kChunk + 8 * (vkg ^ ((dim >> 2) & 3));
       *reinterpret_cast<H8*>(&vh[off]) = hi;
@@ -674,7 +662,7 @@ extern "C" __global__ void __launch_bounds__(256, 2) halo_attn_prefill(
     const float4 a = *reinterpret_cast<const float4*>(qrow + 32 * c + 8 * kq);
     const float4 b = *reinterpret_cast<const float4*>(qrow + 32 * c + 8 * kq + 4);
     const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    SplitHalves(x, qh[c], ql[c]);
+    SplitHalves(x, qh[c], ql[c], kSqk);
   }
   std::uint32_t qpos[4];
 #pragma unroll
@@ -716,7 +704,7 @@ extern "C" __global__ void __launch_bounds__(256, 2) halo_attn_prefill(
     float alpha[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float s0 = sc[0][i] * scale, s1 = sc[1][i] * scale;
+      float s0 = sc[0][i] * (scale / (kSqk * kSqk)), s1 = sc[1][i] * (scale / (kSqk * kSqk));
       const std::uint32_t kp0 = k0 + row, kp1 = k0 + 16 + row;
       s0 = kp0 <= qpos[i] ? s0 : -INFINITY;
       s1 = kp1 <= qpos[i] ? s1 : -INFINITY;
@@ -729,12 +717,13 @@ extern "C" __global__ void __launch_bounds__(256, 2) halo_attn_prefill(
       m[i] = mx;
       // P row 4 kq + i, keys row and 16 + row; 16-byte chunk c of a P row at c ^ (kq & 3) (row >> 2 == kq)
       const std::uint32_t pr = (4 * kq + i) * kChunk;
-      const _Float16 h0 = static_cast<_Float16>(e0), h1 = static_cast<_Float16>(e1);
+      const float es0 = kSpp * e0, es1 = kSpp * e1;
+      const _Float16 h0 = static_cast<_Float16>(es0), h1 = static_cast<_Float16>(es1);
       const std::uint32_t o0 = pr + 8 * ((row / 8) ^ kq) + row % 8, o1 = pr + 8 * ((2 + row / 8) ^ kq) + row % 8;
       pwh[o0] = h0;
-      pwl[o0] = static_cast<_Float16>(e0 - static_cast<float>(h0));
+      pwl[o0] = static_cast<_Float16>(es0 - static_cast<float>(h0));
       pwh[o1] = h1;
-      pwl[o1] = static_cast<_Float16>(e1 - static_cast<float>(h1));
+      pwl[o1] = static_cast<_Float16>(es1 - static_cast<float>(h1));
     }
 #pragma unroll
     for (int c = 0; c < kHd / 16; ++c)
@@ -763,7 +752,7 @@ extern "C" __global__ void __launch_bounds__(256, 2) halo_attn_prefill(
     const std::uint32_t tok = 2 * wave + r / 8, g = r % 8;
     const bool live = tok < ntok;
     const std::size_t base = ((static_cast<std::size_t>(first) + min(tok, ntok - 1)) * Hq + kvh * G + g) * kHd;
-    const float inv = 1.0f / l[i];
+    const float inv = 1.0f / l[i] * (1.0f / (kSpp * kSvv));
 #pragma unroll
     for (int c = 0; c < kHd / 16; c += 2) {
       const std::uint32_t d0 = 16 * c + row, d1 = 16 * (c + 1) + row;

@@ -431,3 +431,31 @@ __device__ __forceinline__ void NormRopeHead(const float (&x)[4], const float (&
 }
 
 }  // namespace halo
+
+namespace halo {
+// fp32 operands on fp16 matrix cores: x enters as the pair hi = fp16(x), lo = fp16(x - hi) (|x - hi - lo| <= 2^-22 |x|
+// for normal values) and each product as hi * hi + hi * lo + lo * hi on v_mfma_f32_16x16x32_f16 (products of halves
+// are exact in the fp32 accumulator; the dropped lo * lo term is below 2^-22 of the product). Three fp16 MFMAs take
+// 3/16 of the fp32 MFMA issue time of the same products. Operands must lie within the fp16 range (|x| < 65504).
+typedef float V4F __attribute__((ext_vector_type(4)));
+typedef _Float16 H8 __attribute__((ext_vector_type(8)));
+typedef _Float16 H4 __attribute__((ext_vector_type(4)));
+
+// s: a power of two applied first (exact), so that the lo halves of the operand's typical values stay normal fp16
+// numbers: a subnormal lo keeps only an absolute precision of 2^-25.
+__device__ __forceinline__ void SplitHalves(const float (&x)[8], H8& hi, H8& lo, float s = 1.0f) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float v = s * x[e];
+    const _Float16 h = static_cast<_Float16>(v);
+    hi[e] = h;
+    lo[e] = static_cast<_Float16>(v - static_cast<float>(h));
+  }
+}
+
+__device__ __forceinline__ V4F Mfma3(const H8& ah, const H8& al, const H8& bh, const H8& bl, V4F c) {
+  c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, c, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, c, 0, 0, 0);
+}
+}  // namespace halo

@@ -17,7 +17,7 @@ pytestmark = pytest.mark.gpu
 D, PAGE = 256, 16
 
 
-def build(dev, rng, S, Hkv, prefix, suffixes, max_context):
+def build(dev, rng, S, Hkv, prefix, suffixes, max_context, kscale=1.0, vscale=1.0):
     max_pages = -(-max_context // PAGE)
     n_prefix_pages = prefix // PAGE
     total = n_prefix_pages + S * (max_pages - n_prefix_pages)
@@ -29,8 +29,8 @@ def build(dev, rng, S, Hkv, prefix, suffixes, max_context):
         for p in range(n_prefix_pages, max_pages):
             pages[s, p] = perm[nxt]
             nxt += 1
-    kp = rng.normal(0, 1, (total, Hkv, PAGE, D)).astype(np.float32)
-    vp = rng.normal(0, 1, (total, Hkv, PAGE, D)).astype(np.float32)
+    kp = (kscale * rng.normal(0, 1, (total, Hkv, PAGE, D))).astype(np.float32)
+    vp = (vscale * rng.normal(0, 1, (total, Hkv, PAGE, D))).astype(np.float32)
     nkv = np.array([prefix + x for x in suffixes], np.uint32)
     g = dict(k=dev.to_device(kp), v=dev.to_device(vp), pages=dev.to_device(pages), nkv=dev.to_device(nkv))
     desc = H.PagedKV(g["k"].ptr, g["v"].ptr, g["pages"].ptr, g["nkv"].ptr, S, Hkv, D, max_pages, prefix, max_context)
@@ -69,10 +69,23 @@ def oracle(q, gate, kp, vp, pages, nkv, Hkv):
     (4, 8192, [256, 256, 256, 256], 8192 + 384),
 ])
 def test_attn_decode(dev, S, prefix, suffixes, max_context):
+    decode_case(dev, S, prefix, suffixes, max_context)
+
+
+@pytest.mark.parametrize("S", [1, 4])
+@pytest.mark.parametrize("qk,v", [(0.1, 1e-3), (2.0, 50.0)])
+def test_attn_decode_operand_magnitudes(dev, S, qk, v):
+    """Small and large operands (q and K scaled by qk, V by v) through both partial kernels (one session: fp32
+    VALU; four sharing a prefix: split-fp16 matrix cores, whose operand scaling covers |V| from about 1e-4 to 255):
+    the 1e-5 bar relative to sum |p| |v| with no absolute slack."""
+    decode_case(dev, S, 128, [40] * S, 256, qk, v, abs_tol=0.0)
+
+
+def decode_case(dev, S, prefix, suffixes, max_context, qk=1.0, v=1.0, abs_tol=1e-6):
     Hq, Hkv = 16, 2
     rng = np.random.default_rng(S + prefix)
-    desc, g, kp, vp, pages, nkv = build(dev, rng, S, Hkv, prefix, suffixes, max_context)
-    q = rng.normal(0, 1, (S, Hq, D)).astype(np.float32)
+    desc, g, kp, vp, pages, nkv = build(dev, rng, S, Hkv, prefix, suffixes, max_context, qk, v)
+    q = (qk * rng.normal(0, 1, (S, Hq, D))).astype(np.float32)
     gate = rng.normal(0, 1, (S, Hq, D)).astype(np.float32)
     gq, gg, go = dev.to_device(q), dev.to_device(gate), dev.array((S, Hq, D), np.float32)
     nbytes = H.lib().halo_op_attn_decode_workspace_bytes(ctypes.byref(desc), Hq)
@@ -81,7 +94,7 @@ def test_attn_decode(dev, S, prefix, suffixes, max_context):
     dev.op("attn_decode", ctypes.byref(desc), gq.ptr, gg.ptr, go.ptr, Hq, ws.ptr, ws.nbytes)
     got = go.download()
     want, mag = oracle(q, gate, kp, vp, pages, nkv, Hkv)
-    assert np.all(np.abs(got - want) <= 1e-5 * mag + 1e-6), np.max(np.abs(got - want) - 1e-5 * mag)
+    assert np.all(np.abs(got - want) <= 1e-5 * mag + abs_tol), np.max(np.abs(got - want) - 1e-5 * mag)
 
 
 def test_kv_append(dev):

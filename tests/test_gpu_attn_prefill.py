@@ -25,9 +25,21 @@ D = 256
     (1, 0, [(0, 0, 64), (0, 64, 33)], 128),
 ])
 def test_attn_prefill(dev, S, prefix, segs, max_context):
+    run_case(dev, S, prefix, segs, max_context)
+
+
+@pytest.mark.parametrize("qk,v", [(0.1, 1e-3), (2.0, 50.0)])
+def test_attn_prefill_operand_magnitudes(dev, qk, v):
+    """Small and large operands (q and K scaled by qk, V by v): the split-fp16 products keep the 1e-5 bar relative
+    to sum |p| |v| with no absolute slack (V of 1e-3 is below the range whose lo halves an unscaled split keeps normal; the
+    split paths scale their operands by powers of two, which covers |V| from about 1e-4 to 255)."""
+    run_case(dev, 1, 0, [(0, 0, 70)], 128, qk, v, abs_tol=0.0)
+
+
+def run_case(dev, S, prefix, segs, max_context, qk=1.0, v=1.0, abs_tol=1e-6):
     Hq, Hkv = 16, 2
     rng = np.random.default_rng(S + prefix + len(segs))
-    desc, g, kp, vp, pages, _ = build(dev, rng, S, Hkv, prefix, [max_context - prefix] * S, max_context)
+    desc, g, kp, vp, pages, _ = build(dev, rng, S, Hkv, prefix, [max_context - prefix] * S, max_context, qk, v)
     seg_arr = (H.PrefillSegment * len(segs))()
     first = 0
     toks = []
@@ -36,7 +48,7 @@ def test_attn_prefill(dev, S, prefix, segs, max_context):
         toks += [(s, start + j) for j in range(n)]
         first += n
     T = len(toks)
-    q = rng.normal(0, 1, (T, Hq, D)).astype(np.float32)
+    q = (qk * rng.normal(0, 1, (T, Hq, D))).astype(np.float32)
     gate = rng.normal(0, 1, (T, Hq, D)).astype(np.float32)
     gq, gg = dev.to_device(q), dev.to_device(gate)
     go = dev.array((T, Hq, D), np.float32)
@@ -60,7 +72,7 @@ def test_attn_prefill(dev, S, prefix, segs, max_context):
             pr = np.exp(sc - sc.max())
             pr /= pr.sum()
             mag = (pr @ np.abs(V)) * sg
-            assert np.all(np.abs(got[ti, h] - oh * sg) <= 1e-5 * mag + 1e-6), f"token {ti} (s {s}, p {p}) head {h}"
+            assert np.all(np.abs(got[ti, h] - oh * sg) <= 1e-5 * mag + abs_tol), f"token {ti} (s {s}, p {p}) head {h}"
     xq, xs = O.quantize(got.reshape(T, Hq * D))
     assert np.array_equal(goq.download(), xq)
     assert np.array_equal(gos.download().view(np.uint32), xs.view(np.uint32))

@@ -200,6 +200,10 @@ typedef struct halo_paged_kv {
   uint32_t sessions, kv_heads, head_dim, max_pages, prefix, max_context;
 } halo_paged_kv;
 
+/* Arithmetic: one session runs fp32 dot products; two or more sessions (and the prefill below) run the products on
+ * split-fp16 matrix cores (each operand as hi + lo halves after a power-of-two scaling: q, k and V by 2^8, the
+ * probabilities by 2^14), within 2^-22 of each product for operands of magnitude about 1e-4 to 255; |q|, |k| or |V|
+ * of 255 or more overflow the halves. */
 /* Scratch for the partials of one decode attention call. */
 size_t halo_op_attn_decode_workspace_bytes(const halo_paged_kv* kv, uint32_t q_heads);
 /* o [S][Hq][d] = attention(q [S][Hq][d]) over each session's nkv positions; gate [S][Hq][d] or NULL. Two launches. */

@@ -196,7 +196,7 @@ int MoePrefillLayout(const halo_moe_weights* w, std::uint32_t T, void* ws, MoePr
   v->xs = reinterpret_cast<float*>(take(sizeof(float) * T * (H / 32)));
   v->ids = reinterpret_cast<std::uint32_t*>(take(sizeof(std::uint32_t) * P));
   v->weights = reinterpret_cast<float*>(take(sizeof(float) * P));
-  v->count = reinterpret_cast<std::uint32_t*>(take(sizeof(std::uint32_t) * (E + 1)));
+  v->count = reinterpret_cast<std::uint32_t*>(take(sizeof(std::uint32_t) * CeilDiv(P, 4096) * E));  // histograms
   v->start = reinterpret_cast<std::uint32_t*>(take(sizeof(std::uint32_t) * (E + 2)));
   v->max_tiles = static_cast<std::uint32_t>(CeilDiv(G, kPrefillTile) + E + 1);
   v->tiles = reinterpret_cast<std::uint32_t*>(take(sizeof(std::uint32_t) * 3 * v->max_tiles));
@@ -256,10 +256,11 @@ int halo_op_moe_prefill(halo_engine* eng, const halo_moe_weights* w, const float
   }
   // 4. group the pairs by expert (token order within an expert), tile table
   {
-    const halo_arg a[] = {Ptr(v.ids), Ptr(v.count), U32(T), U32(k)};
-    if (Launch(eng, "halo_moe_group_count", D3(E), D3(256), a, err, errlen) != 0) return -1;
+    const std::uint32_t nb = static_cast<std::uint32_t>(CeilDiv(static_cast<std::uint64_t>(T) * k, 4096));
+    const halo_arg a[] = {Ptr(v.ids), Ptr(v.count), U32(T), U32(k), U32(E)};
+    if (Launch(eng, "halo_moe_group_count", D3(nb), D3(256), a, err, errlen) != 0) return -1;
     const halo_arg b[] = {Ptr(v.count), Ptr(v.start), Ptr(v.tiles), Ptr(v.ntiles), U32(E), U32(T), U32(shared ? 1 : 0),
-                          U32(kPrefillTile)};
+                          U32(kPrefillTile), U32(nb)};
     if (Launch(eng, "halo_moe_group_scan", D3(1), D3(1024), b, err, errlen) != 0) return -1;
     const halo_arg c[] = {Ptr(v.ids), Ptr(v.start), Ptr(v.token), Ptr(v.pos), U32(T), U32(k), U32(E)};
     if (Launch(eng, "halo_moe_group_fill", D3(E + (shared ? 1 : 0)), D3(256), c, err, errlen) != 0) return -1;
@@ -289,7 +290,7 @@ int halo_op_moe_prefill(halo_engine* eng, const halo_moe_weights* w, const float
   // 8. slot-order combine + shared expert
   const halo_arg a[] = {Ptr(v.y), Ptr(v.pos), Ptr(v.weights), Ptr(v.sgl), Ptr(out), U32(T), U32(H), U32(k),
                         U32(shared ? 1 : 0)};
-  return Launch(eng, "halo_moe_prefill_combine", D3(CeilDiv(H, 256), T), D3(256), a, err, errlen);
+  return Launch(eng, "halo_moe_prefill_combine", D3(CeilDiv(H, 1024), T), D3(256), a, err, errlen);
 }
 
 }  // extern "C"

@@ -102,30 +102,33 @@ extern "C" __global__ void __launch_bounds__(256) halo_gemm_f32_nt(
 }
 
 // ---- grouping of (token, slot) pairs by expert --------------------------------------------------------------------
-// grid (E), block 256: count[e] = number of tokens whose top-k holds e (ids [T][k]).
+// grid (ceil(T k / 4096)), block 256: count[b][e] = how many of the pairs [4096 b, 4096 b + 4096) of ids [T][k]
+// select expert e (an LDS histogram per block: integer sums, so the result does not depend on the order of the
+// atomics). E <= 1024.
 extern "C" __global__ void __launch_bounds__(256)
     halo_moe_group_count(const std::uint32_t* __restrict__ ids, std::uint32_t* __restrict__ count, std::uint32_t T,
-                         std::uint32_t k) {
-  __shared__ std::uint32_t part[4];
-  const std::uint32_t e = blockIdx.x;
-  std::uint32_t n = 0;
-  for (std::uint32_t i = threadIdx.x; i < T * k; i += blockDim.x) n += ids[i] == e ? 1u : 0u;
-  n = static_cast<std::uint32_t>(halo::GroupSumI(static_cast<int>(n)));
-  if (threadIdx.x % kWave == 0) part[threadIdx.x / kWave] = n;
+                         std::uint32_t k, std::uint32_t E) {
+  __shared__ std::uint32_t hist[1024];
+  for (std::uint32_t e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
   __syncthreads();
-  if (threadIdx.x == 0) count[e] = part[0] + part[1] + part[2] + part[3];
+  const std::uint32_t p0 = blockIdx.x * 4096, p1 = min(p0 + 4096, T * k);
+  for (std::uint32_t i = p0 + threadIdx.x; i < p1; i += blockDim.x) atomicAdd(&hist[ids[i]], 1u);
+  __syncthreads();
+  for (std::uint32_t e = threadIdx.x; e < E; e += blockDim.x) count[static_cast<std::size_t>(blockIdx.x) * E + e] = hist[e];
 }
 
-// grid 1, block 1024: start[e] = exclusive prefix of count (e <= E, count[E] = T for the shared group when shared,
-// else 0), and the tile table: groups cut into tiles of `tile` pairs, tiles[i] = {group, first pair, pairs},
+// grid 1, block 1024: start[e] = exclusive prefix of the group sizes (group e < E: the sum of count[b][e] over the nb
+// partial histograms; group E: T for the shared expert when shared, else 0), and the tile table: groups cut into tiles of `tile` pairs, tiles[i] = {group, first pair, pairs},
 // ntiles[0] = the tile count. E + 1 <= 1024.
 extern "C" __global__ void __launch_bounds__(1024)
     halo_moe_group_scan(const std::uint32_t* __restrict__ count, std::uint32_t* __restrict__ start,
                         std::uint32_t* __restrict__ tiles, std::uint32_t* __restrict__ ntiles, std::uint32_t E,
-                        std::uint32_t T, std::uint32_t shared, std::uint32_t tile) {
+                        std::uint32_t T, std::uint32_t shared, std::uint32_t tile, std::uint32_t nb) {
   __shared__ std::uint32_t c[1024], tcount[1024];
   const std::uint32_t g = threadIdx.x;
-  const std::uint32_t n = g < E ? count[g] : (g == E && shared ? T : 0u);
+  std::uint32_t n = g == E && shared ? T : 0u;
+  if (g < E)
+    for (std::uint32_t b = 0; b < nb; ++b) n += count[static_cast<std::size_t>(b) * E + g];
   c[g] = n;
   tcount[g] = (n + tile - 1) / tile;
   __syncthreads();
@@ -233,18 +236,31 @@ extern "C" __global__ void __launch_bounds__(512) halo_moe_grouped_down_q8(
                                   blockIdx.x * 128, hq, hs, nullptr, p0, np, ff, y, p0, H);
 }
 
-// grid (ceil(H / 256), T), block 256: out[t][r] = sum over s < k, in order, of weights[t][s] * y[pos[t k + s]][r],
+// grid (ceil(H / 1024), T), block 256 (H % 4 == 0): out[t][r] = sum over s < k, in order, of weights[t][s] * y[pos[t k + s]][r],
 // then + sigmoid(sgl[t]) * y[P + t][r] when the shared expert is present (sgl: its gate logit).
 extern "C" __global__ void __launch_bounds__(256) halo_moe_prefill_combine(
     const float* __restrict__ y, const std::uint32_t* __restrict__ pos, const float* __restrict__ weights,
     const float* __restrict__ sgl, float* __restrict__ out, std::uint32_t T, std::uint32_t H, std::uint32_t k,
     std::uint32_t shared) {
-  const std::uint32_t t = blockIdx.y, r = blockIdx.x * blockDim.x + threadIdx.x;
+  // four consecutive outputs per thread (16-byte loads of each selected row), each summed in slot order
+  const std::uint32_t t = blockIdx.y, r = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
   if (r >= H) return;
-  float acc = 0.0f;
-  for (std::uint32_t s = 0; s < k; ++s)
-    acc += weights[static_cast<std::size_t>(t) * k + s] *
-           y[static_cast<std::size_t>(pos[static_cast<std::size_t>(t) * k + s]) * H + r];
-  if (shared) acc += halo::Sigmoid(sgl[t]) * y[(static_cast<std::size_t>(T) * k + t) * H + r];
-  out[static_cast<std::size_t>(t) * H + r] = acc;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (std::uint32_t s = 0; s < k; ++s) {
+    const float w = weights[static_cast<std::size_t>(t) * k + s];
+    const float4 v = *reinterpret_cast<const float4*>(y + static_cast<std::size_t>(pos[static_cast<std::size_t>(t) * k + s]) * H + r);
+    acc.x += w * v.x;
+    acc.y += w * v.y;
+    acc.z += w * v.z;
+    acc.w += w * v.w;
+  }
+  if (shared) {
+    const float g = halo::Sigmoid(sgl[t]);
+    const float4 v = *reinterpret_cast<const float4*>(y + (static_cast<std::size_t>(T) * k + t) * H + r);
+    acc.x += g * v.x;
+    acc.y += g * v.y;
+    acc.z += g * v.z;
+    acc.w += g * v.w;
+  }
+  *reinterpret_cast<float4*>(out + static_cast<std::size_t>(t) * H + r) = acc;
 }

@@ -82,3 +82,28 @@ def test_c4_full_shape_every_layer(dev):
         assert rep.loose <= max(64, rep.codes // 1000)
     finally:
         model.close()
+
+
+@pytest.mark.timeout(900)
+def test_c4_full_shape_prefill_every_layer(dev):
+    """The full C4 model's batched prefill: two sessions' prompts (19 and 12 tokens) in one ragged batch, traced through
+    all 48 layers (DeltaNet chunked recurrence, split-fp16 causal attention, grouped MoE over 512 experts) and the LM
+    head, each stage against the host restatement from the GPU's own inputs."""
+    from teacher import PrefillChecker
+
+    cfg = H.c4_config(max_sessions=2, prefix_tokens=0, max_context=64)
+    model = H.Model(dev, cfg, seed=6)
+    try:
+        rng = np.random.default_rng(12)
+        prompts = [rng.integers(0, cfg.vocab, 20).astype(np.uint32), rng.integers(0, cfg.vocab, 13).astype(np.uint32)]
+        model.reset()
+        for s, p in enumerate(prompts):
+            model.set_session(s, p)
+        pc = PrefillChecker(model, cfg)
+        pc.check_prefill([(0, 0, 19), (1, 0, 12)], prompts)
+        rep = pc.report
+        print(f"C4 prefill: {rep.flips} flips and {rep.loose} cancellation-bound codes in {rep.codes} codes; worst error / bar per stage {rep.worst}")
+        assert rep.flips <= max(8, rep.codes // 10000)
+        assert rep.loose <= max(64, rep.codes // 1000)
+    finally:
+        model.close()

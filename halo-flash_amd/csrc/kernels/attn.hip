@@ -315,12 +315,7 @@ __device__ __forceinline__ void AttnDecodePartial(
       const float x[4] = {kv.x, kv.y, kv.z, kv.w};
       const std::uint32_t off = j * kHd + 8 * ((dim / 8) ^ (j & 15)) + dim % 8;
       H4 hi, lo;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float xs = kSqk * x[e];
-        hi[e] = static_cast<_Float16>(xs);
-        lo[e] = static_cast<_Float16>(xs - static_cast<float>(hi[e]));
-      }
+      halo::SplitHalves4(x, hi, lo, kSqk);
       *reinterpret_cast<H4*>(&kh[off]) = hi;
       *reinterpret_cast<H4*>(&kl[off]) = lo;
     }

@@ -441,16 +441,33 @@ typedef float V4F __attribute__((ext_vector_type(4)));
 typedef _Float16 H8 __attribute__((ext_vector_type(8)));
 typedef _Float16 H4 __attribute__((ext_vector_type(4)));
 
+// hi / lo halves of s * a and s * b, packed two to a register (a in the low half): hi = fp16(s x), lo = fp16(s x -
+// hi), one v_fma_mix per value and half (the product and the difference are formed exactly inside the mixed-precision
+// FMA, so the result equals the convert / subtract / convert sequence bit for bit).
+__device__ __forceinline__ void SplitPair(float a, float b, float s, std::uint32_t& hi, std::uint32_t& lo) {
+  asm("v_fma_mixlo_f16 %0, %2, %4, 0\n\t"
+      "v_fma_mixhi_f16 %0, %3, %4, 0\n\t"
+      "v_fma_mixlo_f16 %1, %2, %4, -%0 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixhi_f16 %1, %3, %4, -%0 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+      : "=&v"(hi), "=&v"(lo)
+      : "v"(a), "v"(b), "v"(s));
+}
+
 // s: a power of two applied first (exact), so that the lo halves of the operand's typical values stay normal fp16
 // numbers: a subnormal lo keeps only an absolute precision of 2^-25.
 __device__ __forceinline__ void SplitHalves(const float (&x)[8], H8& hi, H8& lo, float s = 1.0f) {
+  std::uint32_t h[4], l[4];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float v = s * x[e];
-    const _Float16 h = static_cast<_Float16>(v);
-    hi[e] = h;
-    lo[e] = static_cast<_Float16>(v - static_cast<float>(h));
-  }
+  for (int e = 0; e < 4; ++e) SplitPair(x[2 * e], x[2 * e + 1], s, h[e], l[e]);
+  hi = __builtin_bit_cast(H8, h);
+  lo = __builtin_bit_cast(H8, l);
+}
+__device__ __forceinline__ void SplitHalves4(const float (&x)[4], H4& hi, H4& lo, float s = 1.0f) {
+  std::uint32_t h[2], l[2];
+  SplitPair(x[0], x[1], s, h[0], l[0]);
+  SplitPair(x[2], x[3], s, h[1], l[1]);
+  hi = __builtin_bit_cast(H4, h);
+  lo = __builtin_bit_cast(H4, l);
 }
 
 __device__ __forceinline__ V4F Mfma3(const H8& ah, const H8& al, const H8& bh, const H8& bl, V4F c) {

@@ -30,6 +30,7 @@ namespace {
 // so values down to 2^-11 keep the full 22-bit split and |q|, |k|, |V| up to 255 stay in the fp16 range; the
 // probabilities (<= 1) by 2^14.
 constexpr float kSqk = 256.0f, kSvv = 256.0f, kSpp = 16384.0f;
+constexpr float kLog2e = 1.4426950408889634f;
 }  // namespace
 
 // grid (Hkv * (prefix_chunks + S * suffix_chunks)), block 256.
@@ -697,33 +698,39 @@ extern "C" __global__ void __launch_bounds__(256, 2) halo_attn_prefill(
     }
     // online softmax per output row (lanes 16 kq .. 16 kq + 15 hold one row's 32 scores)
     float alpha[4];
+    // Scores and the running max in base-2 units (scale * log2(e) folded into the score scale), so each
+    // exponential is one v_exp_f32 and a masked score (-inf) needs no select.
+    bool rescale = false;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float s0 = sc[0][i] * (scale / (kSqk * kSqk)), s1 = sc[1][i] * (scale / (kSqk * kSqk));
+      float s0 = sc[0][i] * (scale * kLog2e / (kSqk * kSqk)), s1 = sc[1][i] * (scale * kLog2e / (kSqk * kSqk));
       const std::uint32_t kp0 = k0 + row, kp1 = k0 + 16 + row;
       s0 = kp0 <= qpos[i] ? s0 : -INFINITY;
       s1 = kp1 <= qpos[i] ? s1 : -INFINITY;
       const float cm = halo::GroupMax<16>(fmaxf(s0, s1));
       const float mx = fmaxf(m[i], cm);
       const bool none = mx == -INFINITY;
-      alpha[i] = none ? 1.0f : expf(m[i] - mx);
-      const float e0 = s0 == -INFINITY ? 0.0f : expf(s0 - mx), e1 = s1 == -INFINITY ? 0.0f : expf(s1 - mx);
+      alpha[i] = none ? 1.0f : __builtin_amdgcn_exp2f(m[i] - mx);
+      rescale |= alpha[i] != 1.0f;
+      const float e0 = __builtin_amdgcn_exp2f(s0 - mx), e1 = __builtin_amdgcn_exp2f(s1 - mx);
       l[i] = l[i] * alpha[i] + halo::GroupSum<16>(e0 + e1);
       m[i] = mx;
       // P row 4 kq + i, keys row and 16 + row; 16-byte chunk c of a P row at c ^ (kq & 3) (row >> 2 == kq)
       const std::uint32_t pr = (4 * kq + i) * kChunk;
-      const float es0 = kSpp * e0, es1 = kSpp * e1;
-      const _Float16 h0 = static_cast<_Float16>(es0), h1 = static_cast<_Float16>(es1);
+      std::uint32_t ph2, pl2;
+      halo::SplitPair(e0, e1, kSpp, ph2, pl2);
       const std::uint32_t o0 = pr + 8 * ((row / 8) ^ kq) + row % 8, o1 = pr + 8 * ((2 + row / 8) ^ kq) + row % 8;
-      pwh[o0] = h0;
-      pwl[o0] = static_cast<_Float16>(es0 - static_cast<float>(h0));
-      pwh[o1] = h1;
-      pwl[o1] = static_cast<_Float16>(es1 - static_cast<float>(h1));
+      pwh[o0] = __builtin_bit_cast(_Float16, static_cast<std::uint16_t>(ph2 & 0xFFFFu));
+      pwl[o0] = __builtin_bit_cast(_Float16, static_cast<std::uint16_t>(pl2 & 0xFFFFu));
+      pwh[o1] = __builtin_bit_cast(_Float16, static_cast<std::uint16_t>(ph2 >> 16));
+      pwl[o1] = __builtin_bit_cast(_Float16, static_cast<std::uint16_t>(pl2 >> 16));
     }
+    // the accumulators change only where some row's max moved (rare once the first chunks are in)
+    if (__any(rescale))
 #pragma unroll
-    for (int c = 0; c < kHd / 16; ++c)
+      for (int c = 0; c < kHd / 16; ++c)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[c][i] *= alpha[i];
+        for (int i = 0; i < 4; ++i) acc[c][i] *= alpha[i];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");

@@ -235,6 +235,8 @@ int halo_op_moe_prefill(halo_engine* eng, const halo_moe_weights* w, const float
   if (PrefillLayout(w, T, ws, &v, err, errlen) != 0) return -1;
   if (ws == nullptr || ws_bytes < v.bytes)
     return SetErr(err, errlen, "moe prefill: workspace of %zu bytes < %zu", ws_bytes, v.bytes), -1;
+  if (reinterpret_cast<std::uintptr_t>(out) % 16 != 0 || reinterpret_cast<std::uintptr_t>(ws) % 16 != 0)
+    return SetErr(err, errlen, "moe prefill: out and ws must be 16-byte aligned (the combine stores 16-byte rows)"), -1;
   const std::uint32_t E = w->n_experts, k = w->n_used, H = w->hidden, F = w->ff;
   const bool shared = w->shared_gate_proj.qs != nullptr;
   const std::uint32_t G = T * k + (shared ? T : 0);

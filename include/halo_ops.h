@@ -167,7 +167,7 @@ int halo_op_moe_decode_norm(halo_engine* eng, const halo_moe_weights* w, const h
  * ReferenceModel::Moe semantics, src/model/reference.cpp:530-578): fp32 router GEMM (+ shared gate logit), top-k per
  * token, pairs grouped by expert in token order, grouped int8 MFMA gate/up (SwiGLU) and down per expert group (the
  * shared expert is one more group), slot-order combine. x [T][hidden] fp32 (normalized), out [T][hidden]. Requires
- * shared_ff == ff when the shared expert is present, n_experts + 1 <= 1024. Workspace from
+ * shared_ff == ff when the shared expert is present, n_experts + 1 <= 1024; out and ws 16-byte aligned. Workspace from
  * halo_op_moe_prefill_workspace_bytes(w, T) (0: unsupported). The routing (ids / weights [T][k]) is at the start of
  * the workspace: ws + align(T * n_experts * 4) + align(T * 4) + align(T * hidden) + align(T * hidden / 8). */
 size_t halo_op_moe_prefill_workspace_bytes(const halo_moe_weights* w, uint32_t tokens);

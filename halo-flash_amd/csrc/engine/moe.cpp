@@ -162,7 +162,9 @@ int halo_op_moe_decode_norm(halo_engine* eng, const halo_moe_weights* w, const h
 }  // extern "C"
 
 namespace {
-constexpr std::uint32_t kPrefillTile = 64;
+// Pairs per grouped-GEMM tile: 128 once the groups average 96 pairs or more (a prefill batch of thousands of tokens:
+// twice the weight reuse per staged stage outweighs the emptier last tile of each group), else 64.
+std::uint32_t PrefillTile(std::uint64_t pairs, std::uint32_t E) { return pairs >= 96ull * E ? 128u : 64u; }
 }  // namespace
 
 namespace halo::engine {
@@ -198,7 +200,7 @@ int MoePrefillLayout(const halo_moe_weights* w, std::uint32_t T, void* ws, MoePr
   v->weights = reinterpret_cast<float*>(take(sizeof(float) * P));
   v->count = reinterpret_cast<std::uint32_t*>(take(sizeof(std::uint32_t) * CeilDiv(P, 4096) * E));  // histograms
   v->start = reinterpret_cast<std::uint32_t*>(take(sizeof(std::uint32_t) * (E + 2)));
-  v->max_tiles = static_cast<std::uint32_t>(CeilDiv(G, kPrefillTile) + E + 1);
+  v->max_tiles = static_cast<std::uint32_t>(CeilDiv(G, PrefillTile(P, E)) + E + 1);
   v->tiles = reinterpret_cast<std::uint32_t*>(take(sizeof(std::uint32_t) * 3 * v->max_tiles));
   v->ntiles = reinterpret_cast<std::uint32_t*>(take(sizeof(std::uint32_t)));
   v->token = reinterpret_cast<std::uint32_t*>(take(sizeof(std::uint32_t) * G));
@@ -259,10 +261,11 @@ int halo_op_moe_prefill(halo_engine* eng, const halo_moe_weights* w, const float
   // 4. group the pairs by expert (token order within an expert), tile table
   {
     const std::uint32_t nb = static_cast<std::uint32_t>(CeilDiv(static_cast<std::uint64_t>(T) * k, 4096));
+    const std::uint32_t tile = PrefillTile(static_cast<std::uint64_t>(T) * k, E);
     const halo_arg a[] = {Ptr(v.ids), Ptr(v.count), U32(T), U32(k), U32(E)};
     if (Launch(eng, "halo_moe_group_count", D3(nb), D3(256), a, err, errlen) != 0) return -1;
     const halo_arg b[] = {Ptr(v.count), Ptr(v.start), Ptr(v.tiles), Ptr(v.ntiles), U32(E), U32(T), U32(shared ? 1 : 0),
-                          U32(kPrefillTile), U32(nb)};
+                          U32(tile), U32(nb)};
     if (Launch(eng, "halo_moe_group_scan", D3(1), D3(1024), b, err, errlen) != 0) return -1;
     const halo_arg c[] = {Ptr(v.ids), Ptr(v.start), Ptr(v.token), Ptr(v.pos), U32(T), U32(k), U32(E)};
     if (Launch(eng, "halo_moe_group_fill", D3(E + (shared ? 1 : 0)), D3(256), c, err, errlen) != 0) return -1;
@@ -273,7 +276,9 @@ int halo_op_moe_prefill(halo_engine* eng, const halo_moe_weights* w, const float
                           Ptr(shared ? w->shared_gate_proj.qs : nullptr), Ptr(shared ? w->shared_gate_proj.d : nullptr),
                           Ptr(shared ? w->shared_up.qs : nullptr), Ptr(shared ? w->shared_up.d : nullptr), Ptr(v.xq),
                           Ptr(v.xs), Ptr(v.token), Ptr(v.tiles), Ptr(v.ntiles), Ptr(v.h), U32(F), U32(H), U32(E), U32(F)};
-    if (Launch(eng, "halo_moe_grouped_gate_up_q8", D3(CeilDiv(F, 64), v.max_tiles), D3(256), a, err, errlen) != 0)
+    const bool t128 = PrefillTile(static_cast<std::uint64_t>(T) * k, E) == 128;
+    if (Launch(eng, t128 ? "halo_moe_grouped_gate_up_q8_t128" : "halo_moe_grouped_gate_up_q8",
+               D3(CeilDiv(F, 64), v.max_tiles), D3(t128 ? 512 : 256), a, err, errlen) != 0)
       return -1;
   }
   // 6. h quantized per 32
@@ -286,7 +291,9 @@ int halo_op_moe_prefill(halo_engine* eng, const halo_moe_weights* w, const float
     const halo_arg a[] = {Ptr(w->down.qs), Ptr(w->down.d), Ptr(shared ? w->shared_down.qs : nullptr),
                           Ptr(shared ? w->shared_down.d : nullptr), Ptr(v.hq), Ptr(v.hs), Ptr(v.tiles), Ptr(v.ntiles),
                           Ptr(v.y), U32(H), U32(F), U32(E)};
-    if (Launch(eng, "halo_moe_grouped_down_q8", D3(CeilDiv(H, 128), v.max_tiles), D3(512), a, err, errlen) != 0)
+    const bool t128 = PrefillTile(static_cast<std::uint64_t>(T) * k, E) == 128;
+    if (Launch(eng, t128 ? "halo_moe_grouped_down_q8_t128" : "halo_moe_grouped_down_q8", D3(CeilDiv(H, 128), v.max_tiles),
+               D3(512), a, err, errlen) != 0)
       return -1;
   }
   // 8. slot-order combine + shared expert

@@ -201,40 +201,70 @@ extern "C" __global__ void __launch_bounds__(256)
 }
 
 // ---- grouped int8 MFMA over the pairs of each group ---------------------------------------------------------------
-// halo::GemmTileQ8Dma per (rows of group g's matrix, one tile of up to 64 pairs): group g < E reads rows g * rows + r
+// halo::GemmTileQ8Dma per (rows of group g's matrix, one tile of up to 64 (_t128: 128) pairs): group g < E reads rows g * rows + r
 // of the stacked expert tensors, group E the shared expert's. Pair p's activation row is xq[gather ? gather[p] : p].
 // The gate/up launch computes both matrices (64 rows of each per block, 4 waves) and writes h = SiLU(gate) * up; the
 // down launch (128 rows per block, 8 waves) writes the projection. grid (ceil(rows / 64) or ceil(rows / 128), max
-// tiles), block 256 / 512; blocks past ntiles[0] exit. y [pairs][ystride].
-extern "C" __global__ void __launch_bounds__(256) halo_moe_grouped_gate_up_q8(
-    const std::int8_t* gq, const std::uint16_t* gd, const std::int8_t* uq, const std::uint16_t* ud,
-    const std::int8_t* sgq, const std::uint16_t* sgd, const std::int8_t* suq, const std::uint16_t* sud,
-    const std::int8_t* xq, const float* xs, const std::uint32_t* gather, const std::uint32_t* tiles,
-    const std::uint32_t* ntiles, float* h, std::uint32_t ff, std::uint32_t H, std::uint32_t E, std::uint32_t hstride) {
+// tiles), block 256 / 512 (_t128: 512 / 512); blocks past ntiles[0] exit. y [pairs][ystride].
+namespace {
+// TOKS = 32 WT pairs per tile: WT = 2 (4 waves gate/up, 8 waves down with 128 rows) for groups of a few dozen pairs,
+// WT = 4 (8 waves each, 128-pair tiles, twice the weight reuse per stage) for groups of a hundred pairs and more.
+template <int WT>
+__device__ __forceinline__ void GroupedGateUp(const std::int8_t* gq, const std::uint16_t* gd, const std::int8_t* uq,
+                                              const std::uint16_t* ud, const std::int8_t* sgq, const std::uint16_t* sgd,
+                                              const std::int8_t* suq, const std::uint16_t* sud, const std::int8_t* xq,
+                                              const float* xs, const std::uint32_t* gather, const std::uint32_t* tiles,
+                                              const std::uint32_t* ntiles, float* h, std::uint32_t ff, std::uint32_t H,
+                                              std::uint32_t E, std::uint32_t hstride) {
   if (blockIdx.y >= ntiles[0]) return;
   const std::uint32_t* tt = tiles + 3 * static_cast<std::size_t>(blockIdx.y);
   const std::uint32_t g = tt[0], p0 = tt[1], np = tt[2];
   const bool sh = g == E;
   const std::size_t row0 = sh ? 0 : static_cast<std::size_t>(g) * ff;
   const std::uint32_t nblk = H / 32;
-  halo::GemmTileQ8Dma<2, 1, 2, 2, false, 1>((sh ? sgq : gq) + row0 * H, (sh ? sgd : gd) + row0 * nblk,
-                                            (sh ? suq : uq) + row0 * H, (sh ? sud : ud) + row0 * nblk, ff, H,
-                                            blockIdx.x * 64, xq, xs, gather + p0, 0, np, H, h, p0, hstride);
+  halo::GemmTileQ8Dma<2, 1, WT, 2, false, 1>((sh ? sgq : gq) + row0 * H, (sh ? sgd : gd) + row0 * nblk,
+                                             (sh ? suq : uq) + row0 * H, (sh ? sud : ud) + row0 * nblk, ff, H,
+                                             blockIdx.x * 64, xq, xs, gather + p0, 0, np, H, h, p0, hstride);
 }
-
-extern "C" __global__ void __launch_bounds__(512) halo_moe_grouped_down_q8(
-    const std::int8_t* dq, const std::uint16_t* dd, const std::int8_t* sdq, const std::uint16_t* sdd,
-    const std::int8_t* hq, const float* hs, const std::uint32_t* tiles, const std::uint32_t* ntiles, float* y,
-    std::uint32_t H, std::uint32_t ff, std::uint32_t E) {
+template <int WR, int MT, int WT>
+__device__ __forceinline__ void GroupedDown(const std::int8_t* dq, const std::uint16_t* dd, const std::int8_t* sdq,
+                                            const std::uint16_t* sdd, const std::int8_t* hq, const float* hs,
+                                            const std::uint32_t* tiles, const std::uint32_t* ntiles, float* y,
+                                            std::uint32_t H, std::uint32_t ff, std::uint32_t E) {
   if (blockIdx.y >= ntiles[0]) return;
   const std::uint32_t* tt = tiles + 3 * static_cast<std::size_t>(blockIdx.y);
   const std::uint32_t g = tt[0], p0 = tt[1], np = tt[2];
   const bool sh = g == E;
   const std::size_t row0 = sh ? 0 : static_cast<std::size_t>(g) * H;
   const std::uint32_t nblk = ff / 32;
-  halo::GemmTileQ8Dma<4, 1, 2, 1>((sh ? sdq : dq) + row0 * ff, (sh ? sdd : dd) + row0 * nblk, nullptr, nullptr, H, ff,
-                                  blockIdx.x * 128, hq, hs, nullptr, p0, np, ff, y, p0, H);
+  halo::GemmTileQ8Dma<WR, MT, WT, 1>((sh ? sdq : dq) + row0 * ff, (sh ? sdd : dd) + row0 * nblk, nullptr, nullptr, H,
+                                     ff, blockIdx.x * 128, hq, hs, nullptr, p0, np, ff, y, p0, H);
 }
+}  // namespace
+
+#define HALO_GROUPED_GATE_UP(NAME, WT, THREADS)                                                                    \
+  extern "C" __global__ void __launch_bounds__(THREADS) NAME(                                                      \
+      const std::int8_t* gq, const std::uint16_t* gd, const std::int8_t* uq, const std::uint16_t* ud,              \
+      const std::int8_t* sgq, const std::uint16_t* sgd, const std::int8_t* suq, const std::uint16_t* sud,          \
+      const std::int8_t* xq, const float* xs, const std::uint32_t* gather, const std::uint32_t* tiles,             \
+      const std::uint32_t* ntiles, float* h, std::uint32_t ff, std::uint32_t H, std::uint32_t E,                   \
+      std::uint32_t hstride) {                                                                                     \
+    GroupedGateUp<WT>(gq, gd, uq, ud, sgq, sgd, suq, sud, xq, xs, gather, tiles, ntiles, h, ff, H, E, hstride);    \
+  }
+HALO_GROUPED_GATE_UP(halo_moe_grouped_gate_up_q8, 2, 256)
+HALO_GROUPED_GATE_UP(halo_moe_grouped_gate_up_q8_t128, 4, 512)
+#undef HALO_GROUPED_GATE_UP
+
+#define HALO_GROUPED_DOWN(NAME, WR, MT, WT)                                                                        \
+  extern "C" __global__ void __launch_bounds__(512) NAME(                                                          \
+      const std::int8_t* dq, const std::uint16_t* dd, const std::int8_t* sdq, const std::uint16_t* sdd,            \
+      const std::int8_t* hq, const float* hs, const std::uint32_t* tiles, const std::uint32_t* ntiles, float* y,   \
+      std::uint32_t H, std::uint32_t ff, std::uint32_t E) {                                                        \
+    GroupedDown<WR, MT, WT>(dq, dd, sdq, sdd, hq, hs, tiles, ntiles, y, H, ff, E);                                \
+  }
+HALO_GROUPED_DOWN(halo_moe_grouped_down_q8, 4, 1, 2)
+HALO_GROUPED_DOWN(halo_moe_grouped_down_q8_t128, 2, 2, 4)
+#undef HALO_GROUPED_DOWN
 
 // grid (ceil(H / 1024), T), block 256 (H % 4 == 0): out[t][r] = sum over s < k, in order, of weights[t][s] * y[pos[t k + s]][r],
 // then + sigmoid(sgl[t]) * y[P + t][r] when the shared expert is present (sgl: its gate logit).

@@ -880,5 +880,27 @@ class MoeLayer:
         o_w = o_ids + al(T * k * 4)
         return o_logits, o_sgl, o_ids, o_w
 
+    def prefill_h_views(self, tokens: int):
+        """Byte offsets of pos [T k] (each routed pair's row in the grouped order; the shared expert's rows follow at
+        T k + t) and of the quantized h rows hq [G][ff] int8 / hs [G][ff / 32] fp32 in the prefill workspace (the
+        layout of MoePrefillLayout, csrc/engine/moe.cpp)."""
+        al = lambda b: (b + 255) // 256 * 256
+        T, E, H, k, F = tokens, self.E, self.H, self.k, self.F
+        P = T * k
+        G = P + T  # the shared expert is present in every MoeLayer
+        tile = 128 if P >= 96 * E else 64
+        max_tiles = -(-G // tile) + E + 1
+        o = self.prefill_views(T)[3] + al(P * 4)  # past the weights
+        o += al(-(-P // 4096) * E * 4)  # count histograms
+        o += al((E + 2) * 4)  # start
+        o += al(3 * max_tiles * 4) + al(4)  # tiles, ntiles
+        o += al(G * 4)  # token
+        o_pos = o
+        o += al(P * 4)
+        o += al(G * F * 4)  # h
+        o_hq = o
+        o_hs = o + al(G * F)
+        return o_pos, o_hq, o_hs
+
     def forward_prefill(self, x: DeviceArray, out: DeviceArray, tokens: int, ws: DeviceArray):
         self.dev.op("moe_prefill", C.byref(self.w), x.ptr, out.ptr, tokens, ws.ptr, ws.nbytes)

@@ -306,12 +306,19 @@ __device__ __forceinline__ void WyPrep(const In* __restrict__ q, const In* __res
 // 16-column tiles each; then wave w updates S rows 16 w .. + 16. The next chunk's operands are loaded into registers
 // during the current one; the block barriers inside the chunk loop synchronize LDS only, so those loads stay in
 // flight across them.
+// Column of token `tok` in row `key` of the K^T tile: 4-token groups xor-swizzled by (key / 8) & 15. With the 72-float
+// row stride, both the transposed 4-byte stores (64 lanes: 16 key rows x 4 tokens) and the 16-byte operand reads (16
+// key rows, one 4-token group) land on distinct banks of the 64-bank LDS.
+__device__ __forceinline__ std::uint32_t KtCol(std::uint32_t key, std::uint32_t tok) {
+  return 4 * ((tok / 4) ^ ((key / 8) & 15)) + tok % 4;
+}
+
 template <typename In, int kNC>
 __device__ __forceinline__ void WyScan(const In* __restrict__ k, const float* __restrict__ wy,
                                        const float* __restrict__ Gc, const std::uint32_t* __restrict__ chunks,
                                        const std::uint32_t* __restrict__ seqs, float* __restrict__ state,
                                        float* __restrict__ o, std::uint32_t Hv, std::uint32_t Hk) {
-  constexpr int kNB = kD / kNC, kNT = kNC / 16, kTL = kC + 4, kStL = kD + 4, kWL = kNC + 4;
+  constexpr int kNB = kD / kNC, kNT = kNC / 16, kTL = kC + 8, kStL = kD + 4, kWL = kNC + 4;
   constexpr int kUkF = kC * kCL, kKtF = kD * kTL, kAF = kUkF > kKtF ? kUkF : kKtF;
   __shared__ __attribute__((aligned(16))) float ua[kAF];       // Uk [64][kCL], then K^T [128][kTL]
   __shared__ __attribute__((aligned(16))) float qel[kC][kCL];
@@ -413,8 +420,8 @@ __device__ __forceinline__ void WyScan(const In* __restrict__ k, const float* __
     const std::uint32_t tk = tid / 16, pk = 8 * (tid % 16);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      kt[pk + e][tk] = tk < L ? Cv(rk0.v[e]) : 0.0f;
-      kt[pk + e][tk + 32] = tk + 32 < L ? Cv(rk1.v[e]) : 0.0f;
+      kt[pk + e][KtCol(pk + e, tk)] = tk < L ? Cv(rk0.v[e]) : 0.0f;
+      kt[pk + e][KtCol(pk + e, tk + 32)] = tk + 32 < L ? Cv(rk1.v[e]) : 0.0f;
     }
   };
   const float inv_sqrt_d = 1.0f / sqrtf(static_cast<float>(kD));
@@ -484,7 +491,7 @@ __device__ __forceinline__ void WyScan(const In* __restrict__ k, const float* __
 #pragma unroll
       for (int sb = 0; sb < 4; ++sb) {
         const std::uint32_t tk = 16 * fq + 4 * sb;
-        const float4 kv = *reinterpret_cast<const float4*>(&kt[r0 + fc][tk]);
+        const float4 kv = *reinterpret_cast<const float4*>(&kt[r0 + fc][KtCol(r0 + fc, tk)]);
         const float4 wv = *reinterpret_cast<const float4*>(&Wl[tk]);
         const float a0 = kv.x * wv.x, a1 = kv.y * wv.y, a2 = kv.z * wv.z, a3 = kv.w * wv.w;
 #pragma unroll

@@ -318,12 +318,12 @@ __device__ __forceinline__ void WyScan(const In* __restrict__ k, const float* __
                                        const float* __restrict__ Gc, const std::uint32_t* __restrict__ chunks,
                                        const std::uint32_t* __restrict__ seqs, float* __restrict__ state,
                                        float* __restrict__ o, std::uint32_t Hv, std::uint32_t Hk) {
-  constexpr int kNB = kD / kNC, kNT = kNC / 16, kTL = kC + 8, kStL = kD + 4, kWL = kNC + 4;
+  constexpr int kNB = kD / kNC, kNT = kNC / 16, kTL = kC + 8, kDL = kC + 4, kStL = kD + 4, kWL = kNC + 4;
   constexpr int kUkF = kC * kCL, kKtF = kD * kTL, kAF = kUkF > kKtF ? kUkF : kKtF;
   __shared__ __attribute__((aligned(16))) float ua[kAF];       // Uk [64][kCL], then K^T [128][kTL]
   __shared__ __attribute__((aligned(16))) float qel[kC][kCL];
   __shared__ __attribute__((aligned(16))) float st[kNC][kStL];  // S^T slice: [column][key]
-  __shared__ __attribute__((aligned(16))) float dt[kNC][kTL];   // Delta^T slice: [column][token]
+  __shared__ __attribute__((aligned(16))) float dt[kNC][kDL];   // Delta^T slice: [column][token]
   __shared__ __attribute__((aligned(16))) float wvl[kC][kWL];
   __shared__ __attribute__((aligned(16))) float ovl[kC][kWL];
   __shared__ __attribute__((aligned(16))) float Gl[kC], Wl[kC];

@@ -58,8 +58,9 @@ __device__ __forceinline__ void AttnDecodePartial(
     float* __restrict__ pl, float* __restrict__ pacc, std::uint32_t S, std::uint32_t Hq, std::uint32_t Hkv,
     std::uint32_t prefix, std::uint32_t max_pages, std::uint32_t prefix_chunks, std::uint32_t suffix_chunks,
     std::uint32_t rot, float theta, float eps) {
-  // 32 KB: the queries, then the K chunk as halves, then the V chunk as halves (38 KB in all: four blocks per CU)
-  __shared__ __attribute__((aligned(16))) float qs[kMaxQ][kHd];
+  // 32.5 KB: the queries, then the K chunk as halves, then the V chunk as halves (39 KB in all: four blocks per CU);
+  // query rows padded by 16 bytes so the 16 rows of a matrix-core operand read fall on different banks
+  __shared__ __attribute__((aligned(16))) float qs[kMaxQ][kHd + 4];
   __shared__ __attribute__((aligned(16))) float sc[kMaxQ][kChunk + 4];  // rows 16-byte aligned: vector reads
   static_assert(kChunk == 32 && kPage == 16, "two pages per chunk, two tokens per 16-lane row");
   const std::uint32_t G = Hq / Hkv, x = blockIdx.x, kvh = x % Hkv, c = x / Hkv;

@@ -54,7 +54,7 @@ int GdnPrefill(halo_engine* eng, bool f32, const void* q, const void* k, const v
   float* Gc = wy + static_cast<std::size_t>(n_chunks) * Hv * 4 * 64 * 128;
   {
     const halo_arg a[] = {Ptr(q), Ptr(k), Ptr(v), Ptr(g), Ptr(beta), Ptr(chunks), Ptr(wy), Ptr(Gc), U32(Hv), U32(Hk)};
-    if (Launch(eng, f32 ? "halo_gdn_wy_prep_f32" : "halo_gdn_wy_prep", D3(n_chunks, Hv), D3(256), a, err, errlen) != 0)
+    if (Launch(eng, f32 ? "halo_gdn_wy_prep_f32" : "halo_gdn_wy_prep", D3(n_chunks, Hv), D3(512), a, err, errlen) != 0)
       return -1;
   }
   const halo_arg a[] = {Ptr(k), Ptr(wy), Ptr(Gc), Ptr(chunks), Ptr(seqs), Ptr(state), Ptr(o), U32(Hv), U32(Hk)};

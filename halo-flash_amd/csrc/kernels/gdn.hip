@@ -134,11 +134,11 @@ __device__ __forceinline__ void Put8(float* dst, const Pack8<In>& x, bool on) {
 }
 }  // namespace
 
-// grid (n_chunks, Hv), block 256 (4 waves). MFMA v_mfma_f32_32x32x2f32: A lane l = A[l % 32][k], B lane l =
+// grid (n_chunks, Hv), block 512 (8 waves). MFMA v_mfma_f32_32x32x2f32: A lane l = A[l % 32][k], B lane l =
 // B[k][l % 32] with k split in halves (lanes 0-31 the first half of the K range, 32-63 the second), D lane l holds
-// column l % 32 and rows 8 (r / 4) + 4 (l / 32) + r % 4. Wave w owns the 32 x 32 tile (w / 2, w % 2) of K K^T and
-// of Q K^T, then two 32-column tiles of each 64 x 128 product. T = (I + A)^-1 by forward substitution in wave 0,
-// one column per lane, in registers.
+// column l % 32 and rows 8 (r / 4) + 4 (l / 32) + r % 4. Wave w owns the 32 x 32 tile ((w % 4) / 2, w % 2) of K K^T
+// (w < 4) or Q K^T (w >= 4), then the 32-column tile 2 (w % 2) + w / 4 of each 64 x 128 product. T = (I + A)^-1 by
+// forward substitution in wave 0, one column per lane, in registers.
 template <typename In>
 __device__ __forceinline__ void WyPrep(const In* __restrict__ q, const In* __restrict__ k, const In* __restrict__ v,
                                        const float* __restrict__ g, const float* __restrict__ beta,
@@ -177,22 +177,19 @@ __device__ __forceinline__ void WyPrep(const In* __restrict__ q, const In* __res
     Gm[tid] = expf(G[tid]);
     Bg[tid] = Bt[tid] * expf(G[tid]);
   }
-  // K K^T and Q K^T, tile (ti, tj) = (wave / 2, wave % 2), K range = 128 keys (step s: key s + 64 hh)
-  const std::uint32_t ti = wave / 2, tj = wave % 2;
-  V16F kk = {}, qk = {};
+  // K K^T (waves 0-3) and Q K^T (waves 4-7), tile (ti, tj) = ((wave % 4) / 2, wave % 2), K range = 128 keys
+  // (step s: key s + 64 hh); eight waves, two per SIMD, so one wave's MFMA chain overlaps another's loads and stores
+  const std::uint32_t w4 = wave % 4, ti = w4 / 2, tj = w4 % 2, half = wave / 4;
+  float(*xa)[kCL] = half ? ql : kl;
+  V16F kq = {};
 #pragma unroll 4
   for (int sb = 0; sb < 16; ++sb) {
-    const float4 ka = *reinterpret_cast<const float4*>(&kl[32 * ti + fr][4 * sb + 64 * hh]);
-    const float4 qa = *reinterpret_cast<const float4*>(&ql[32 * ti + fr][4 * sb + 64 * hh]);
+    const float4 xa4 = *reinterpret_cast<const float4*>(&xa[32 * ti + fr][4 * sb + 64 * hh]);
     const float4 kb = *reinterpret_cast<const float4*>(&kl[32 * tj + fr][4 * sb + 64 * hh]);
-    kk = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.x, kb.x, kk, 0, 0, 0);
-    qk = __builtin_amdgcn_mfma_f32_32x32x2f32(qa.x, kb.x, qk, 0, 0, 0);
-    kk = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.y, kb.y, kk, 0, 0, 0);
-    qk = __builtin_amdgcn_mfma_f32_32x32x2f32(qa.y, kb.y, qk, 0, 0, 0);
-    kk = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.z, kb.z, kk, 0, 0, 0);
-    qk = __builtin_amdgcn_mfma_f32_32x32x2f32(qa.z, kb.z, qk, 0, 0, 0);
-    kk = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.w, kb.w, kk, 0, 0, 0);
-    qk = __builtin_amdgcn_mfma_f32_32x32x2f32(qa.w, kb.w, qk, 0, 0, 0);
+    kq = __builtin_amdgcn_mfma_f32_32x32x2f32(xa4.x, kb.x, kq, 0, 0, 0);
+    kq = __builtin_amdgcn_mfma_f32_32x32x2f32(xa4.y, kb.y, kq, 0, 0, 0);
+    kq = __builtin_amdgcn_mfma_f32_32x32x2f32(xa4.z, kb.z, kq, 0, 0, 0);
+    kq = __builtin_amdgcn_mfma_f32_32x32x2f32(xa4.w, kb.w, kq, 0, 0, 0);
   }
   __syncthreads();  // Gm / Bg visible
 #pragma unroll
@@ -200,8 +197,10 @@ __device__ __forceinline__ void WyPrep(const In* __restrict__ q, const In* __res
     const std::uint32_t t = 32 * ti + 8 * (r / 4) + 4 * hh + r % 4, s = 32 * tj + fr;
     const bool low = s < t, leq = s <= t;
     const float dec = expf(leq ? G[t] - G[s] : 0.0f);
-    am[t][s] = low ? Bt[t] * dec * kk[r] : 0.0f;
-    pm[t][s] = leq ? dec * qk[r] : 0.0f;
+    if (half)
+      pm[t][s] = leq ? dec * kq[r] : 0.0f;
+    else
+      am[t][s] = low ? Bt[t] * dec * kq[r] : 0.0f;
   }
   __syncthreads();
   // T = (I + A)^-1: lane = column, rows in order; A rows are read as broadcasts, four partial sums per row
@@ -226,10 +225,11 @@ __device__ __forceinline__ void WyPrep(const In* __restrict__ q, const In* __res
     for (int t = 0; t < kC; ++t) am[t][lane] = T[t];
   }
   __syncthreads();
-  // Uk = T diag(beta gamma) K and Wv = T diag(beta) V: wave w owns rows 32 ti, columns 32 (2 (w % 2) + u), u < 2;
+  // Uk = T diag(beta gamma) K and Wv = T diag(beta) V: wave w owns rows 32 ti, columns 32 (2 (w % 2) + w / 4);
   // K range = 64 tokens (step s: token s + 32 hh)
   float* out = wy + (static_cast<std::size_t>(c) * Hv + h) * 4 * kC * kD;  // Uk, Qe, Wv, Ov
-  V16F uk[2] = {{}, {}}, wv[2] = {{}, {}};
+  const std::uint32_t col = 32 * (2 * tj + half) + fr;
+  V16F uk = {}, wv = {};
 #pragma unroll 2
   for (int sb = 0; sb < 8; ++sb) {
     const float4 ta = *reinterpret_cast<const float4*>(&am[32 * ti + fr][4 * sb + 32 * hh]);
@@ -237,36 +237,27 @@ __device__ __forceinline__ void WyPrep(const In* __restrict__ q, const In* __res
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const std::uint32_t tok = 4 * sb + e + 32 * hh;
-      const float bg = Bg[tok], bt = Bt[tok];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const std::uint32_t col = 32 * (2 * tj + u) + fr;
-        uk[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(tv[e], bg * kl[tok][col], uk[u], 0, 0, 0);
-        wv[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(tv[e], bt * vl[tok][col], wv[u], 0, 0, 0);
-      }
+      uk = __builtin_amdgcn_mfma_f32_32x32x2f32(tv[e], Bg[tok] * kl[tok][col], uk, 0, 0, 0);
+      wv = __builtin_amdgcn_mfma_f32_32x32x2f32(tv[e], Bt[tok] * vl[tok][col], wv, 0, 0, 0);
     }
   }
   __syncthreads();  // K and V are no longer read: Uk and Wv take their places
 #pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const std::uint32_t t = 32 * ti + 8 * (r / 4) + 4 * hh + r % 4, col = 32 * (2 * tj + u) + fr;
-      kl[t][col] = uk[u][r];
-      vl[t][col] = wv[u][r];
-      out[0 * kC * kD + t * kD + col] = uk[u][r];
-      out[2 * kC * kD + t * kD + col] = wv[u][r];
-    }
+  for (int r = 0; r < 16; ++r) {
+    const std::uint32_t t = 32 * ti + 8 * (r / 4) + 4 * hh + r % 4;
+    kl[t][col] = uk[r];
+    vl[t][col] = wv[r];
+    out[0 * kC * kD + t * kD + col] = uk[r];
+    out[2 * kC * kD + t * kD + col] = wv[r];
+  }
   __syncthreads();
   // Qe = diag(gamma) Q - P Uk and Ov = P Wv
-  V16F qe[2], ov[2] = {{}, {}};
+  V16F qe, ov = {};
 #pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const std::uint32_t t = 32 * ti + 8 * (r / 4) + 4 * hh + r % 4, col = 32 * (2 * tj + u) + fr;
-      qe[u][r] = Gm[t] * ql[t][col];
-    }
+  for (int r = 0; r < 16; ++r) {
+    const std::uint32_t t = 32 * ti + 8 * (r / 4) + 4 * hh + r % 4;
+    qe[r] = Gm[t] * ql[t][col];
+  }
 #pragma unroll 2
   for (int sb = 0; sb < 8; ++sb) {
     const float4 pa = *reinterpret_cast<const float4*>(&pm[32 * ti + fr][4 * sb + 32 * hh]);
@@ -274,22 +265,16 @@ __device__ __forceinline__ void WyPrep(const In* __restrict__ q, const In* __res
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const std::uint32_t tok = 4 * sb + e + 32 * hh;
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const std::uint32_t col = 32 * (2 * tj + u) + fr;
-        qe[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(-pv[e], kl[tok][col], qe[u], 0, 0, 0);
-        ov[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(pv[e], vl[tok][col], ov[u], 0, 0, 0);
-      }
+      qe = __builtin_amdgcn_mfma_f32_32x32x2f32(-pv[e], kl[tok][col], qe, 0, 0, 0);
+      ov = __builtin_amdgcn_mfma_f32_32x32x2f32(pv[e], vl[tok][col], ov, 0, 0, 0);
     }
   }
 #pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const std::uint32_t t = 32 * ti + 8 * (r / 4) + 4 * hh + r % 4, col = 32 * (2 * tj + u) + fr;
-      out[1 * kC * kD + t * kD + col] = qe[u][r];
-      out[3 * kC * kD + t * kD + col] = ov[u][r];
-    }
+  for (int r = 0; r < 16; ++r) {
+    const std::uint32_t t = 32 * ti + 8 * (r / 4) + 4 * hh + r % 4;
+    out[1 * kC * kD + t * kD + col] = qe[r];
+    out[3 * kC * kD + t * kD + col] = ov[r];
+  }
   if (tid < kC) Gc[(static_cast<std::size_t>(c) * Hv + h) * kC + tid] = G[tid];
 }
 
@@ -517,14 +502,14 @@ __device__ __forceinline__ void WyScan(const In* __restrict__ k, const float* __
   }
 }
 
-extern "C" __global__ void __launch_bounds__(256)
+extern "C" __global__ void __launch_bounds__(512)
     halo_gdn_wy_prep(const std::uint16_t* __restrict__ q, const std::uint16_t* __restrict__ k,
                      const std::uint16_t* __restrict__ v, const float* __restrict__ g, const float* __restrict__ beta,
                      const std::uint32_t* __restrict__ chunks, float* __restrict__ wy, float* __restrict__ Gc,
                      std::uint32_t Hv, std::uint32_t Hk) {
   WyPrep(q, k, v, g, beta, chunks, wy, Gc, Hv, Hk);
 }
-extern "C" __global__ void __launch_bounds__(256)
+extern "C" __global__ void __launch_bounds__(512)
     halo_gdn_wy_prep_f32(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
                          const float* __restrict__ g, const float* __restrict__ beta,
                          const std::uint32_t* __restrict__ chunks, float* __restrict__ wy, float* __restrict__ Gc,

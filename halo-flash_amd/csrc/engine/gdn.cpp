@@ -58,7 +58,12 @@ int GdnPrefill(halo_engine* eng, bool f32, const void* q, const void* k, const v
       return -1;
   }
   const halo_arg a[] = {Ptr(k), Ptr(wy), Ptr(Gc), Ptr(chunks), Ptr(seqs), Ptr(state), Ptr(o), U32(Hv), U32(Hk)};
-  return Launch(eng, f32 ? "halo_gdn_wy_scan_f32" : "halo_gdn_wy_scan", D3(n_seq * Hv * 4), D3(512), a, err, errlen);
+  // 32 value columns per block, or 16 when even then the blocks fit the 256 CUs once (one long prompt): the scan is
+  // chunk-serial, so idle CUs are better spent splitting each block's work
+  const bool n16 = static_cast<std::uint64_t>(n_seq) * Hv * 8 <= 256;
+  const char* name = f32 ? (n16 ? "halo_gdn_wy_scan_f32_n16" : "halo_gdn_wy_scan_f32")
+                         : (n16 ? "halo_gdn_wy_scan_n16" : "halo_gdn_wy_scan");
+  return Launch(eng, name, D3(n_seq * Hv * (n16 ? 8 : 4)), D3(512), a, err, errlen);
 }
 }  // namespace
 

@@ -170,8 +170,14 @@ __device__ __forceinline__ void WyPrep(const In* __restrict__ q, const In* __res
     Bt[tid] = on ? bv : 0.0f;
   }
   __syncthreads();
-  if (tid == 0)
-    for (int t = 1; t < kC; ++t) G[t] += G[t - 1];
+  if (tid == 0) {  // running sum in a register: the loads are independent, only the adds form a chain
+    float run = G[0];
+#pragma unroll
+    for (int t = 1; t < kC; ++t) {
+      run += G[t];
+      G[t] = run;
+    }
+  }
   __syncthreads();
   if (tid < kC) {
     Gm[tid] = expf(G[tid]);
@@ -356,7 +362,11 @@ __device__ __forceinline__ void WyScan(const In* __restrict__ k, const float* __
   // staged operands of one chunk, in registers: Uk, Qe (8192 floats each: 4 float4 per thread), the Wv and Ov slices
   // (64 x 64 each: rows tid / 16 and tid / 16 + 32, columns 4 (tid % 16)), G (threads < 64); K (8192 inputs: two
   // packs of 8) on its own, since it is stored later in the chunk
-  float4 ru0, ru1, ru2, ru3, rq0, rq1, rq2, rq3, rw[kNC / 32], ro[kNC / 32];
+  // Wv / Ov slices: 64 x kNC floats = 16 kNC float4, float4 e = tid + 512 i at row e / (kNC / 4), column 4 (e % (kNC / 4));
+  // with kNC = 16 the first 256 threads hold one each
+  constexpr int kWN = (kC * kNC / 4 + 511) / 512;
+  constexpr bool kWAll = kC * kNC / 4 >= 512;
+  float4 ru0, ru1, ru2, ru3, rq0, rq1, rq2, rq3, rw[kWN], ro[kWN];
   Pack8<In> rk0, rk1;
   float rg;
   auto load = [&](std::uint32_t ci) {
@@ -370,10 +380,11 @@ __device__ __forceinline__ void WyScan(const In* __restrict__ k, const float* __
     const float* bw = base + 2 * kC * kD + j0 + p;
     const float* bo = base + 3 * kC * kD + j0 + p;
 #pragma unroll
-    for (int i = 0; i < kNC / 32; ++i) {
-      rw[i] = *reinterpret_cast<const float4*>(bw + (t + (2048 / kNC) * i) * kD);
-      ro[i] = *reinterpret_cast<const float4*>(bo + (t + (2048 / kNC) * i) * kD);
-    }
+    for (int i = 0; i < kWN; ++i)
+      if (kWAll || tid < kC * kNC / 4) {
+        rw[i] = *reinterpret_cast<const float4*>(bw + (t + (2048 / kNC) * i) * kD);
+        ro[i] = *reinterpret_cast<const float4*>(bo + (t + (2048 / kNC) * i) * kD);
+      }
     rg = Gc[(static_cast<std::size_t>(c) * Hv + h) * kC + tid % kC];
   };
   auto load_k = [&](std::uint32_t ci) {
@@ -395,10 +406,11 @@ __device__ __forceinline__ void WyScan(const In* __restrict__ k, const float* __
     *reinterpret_cast<float4*>(&qel[t0 + 48][p4]) = rq3;
     const std::uint32_t t = tid / (kNC / 4), p = 4 * (tid % (kNC / 4));
 #pragma unroll
-    for (int i = 0; i < kNC / 32; ++i) {
-      *reinterpret_cast<float4*>(&wvl[t + (2048 / kNC) * i][p]) = rw[i];
-      *reinterpret_cast<float4*>(&ovl[t + (2048 / kNC) * i][p]) = ro[i];
-    }
+    for (int i = 0; i < kWN; ++i)
+      if (kWAll || tid < kC * kNC / 4) {
+        *reinterpret_cast<float4*>(&wvl[t + (2048 / kNC) * i][p]) = rw[i];
+        *reinterpret_cast<float4*>(&ovl[t + (2048 / kNC) * i][p]) = ro[i];
+      }
     if (tid < kC) Gl[tid] = rg;
   };
   auto store_k = [&](std::uint32_t L) {
@@ -527,6 +539,20 @@ extern "C" __global__ void __launch_bounds__(512)
                          const std::uint32_t* __restrict__ chunks, const std::uint32_t* __restrict__ seqs,
                          float* __restrict__ state, float* __restrict__ o, std::uint32_t Hv, std::uint32_t Hk) {
   WyScan<float, 32>(k, wy, Gc, chunks, seqs, state, o, Hv, Hk);
+}
+// 16 value columns per block (eight blocks per head): for batches with too few (sequence, head) pairs to fill the
+// CUs at 32 columns, halving each block's matrix work on the chunk-serial path
+extern "C" __global__ void __launch_bounds__(512)
+    halo_gdn_wy_scan_n16(const std::uint16_t* __restrict__ k, const float* __restrict__ wy, const float* __restrict__ Gc,
+                         const std::uint32_t* __restrict__ chunks, const std::uint32_t* __restrict__ seqs,
+                         float* __restrict__ state, float* __restrict__ o, std::uint32_t Hv, std::uint32_t Hk) {
+  WyScan<std::uint16_t, 16>(k, wy, Gc, chunks, seqs, state, o, Hv, Hk);
+}
+extern "C" __global__ void __launch_bounds__(512)
+    halo_gdn_wy_scan_f32_n16(const float* __restrict__ k, const float* __restrict__ wy, const float* __restrict__ Gc,
+                             const std::uint32_t* __restrict__ chunks, const std::uint32_t* __restrict__ seqs,
+                             float* __restrict__ state, float* __restrict__ o, std::uint32_t Hv, std::uint32_t Hk) {
+  WyScan<float, 16>(k, wy, Gc, chunks, seqs, state, o, Hv, Hk);
 }
 
 // ---- the whole DeltaNet token step of the decode graph, one block per (session, value head) -----------------

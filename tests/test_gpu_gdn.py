@@ -72,7 +72,7 @@ def from_bf16(b):
     return (b.astype(np.uint32) << 16).view(np.float32)
 
 
-def prefill_case(dev, rng, seqlens, Hv=32, Hk=16, zero_state=False):
+def prefill_inputs(rng, seqlens, Hv=32, Hk=16, zero_state=False):
     T = sum(seqlens)
     q = rng.normal(0, 1, (T, Hk, D)).astype(np.float32)
     k = rng.normal(0, 1, (T, Hk, D)).astype(np.float32)
@@ -81,24 +81,34 @@ def prefill_case(dev, rng, seqlens, Hv=32, Hk=16, zero_state=False):
     v = rng.normal(0, 1, (T, Hv, D)).astype(np.float32)
     g = (-np.log1p(np.exp(rng.normal(0, 1, (T, Hv))))).astype(np.float32)
     beta = (1 / (1 + np.exp(-rng.normal(0, 1, (T, Hv))))).astype(np.float32)
-    qb, kb, vb = to_bf16(q), to_bf16(k), to_bf16(v)
     nseq = len(seqlens)
     state = np.zeros((nseq, Hv, D, D), np.float32) if zero_state else \
         rng.normal(0, 0.05, (nseq, Hv, D, D)).astype(np.float32)
+    return to_bf16(q), to_bf16(k), to_bf16(v), g, beta, state
+
+
+def run_prefill(dev, seqlens, qb, kb, vb, g, beta, state, Hv=32, Hk=16):
+    T, nseq = sum(seqlens), len(seqlens)
     L = H.lib()
     sl = np.array(seqlens, np.uint32)
     nch = L.halo_gdn_chunk_table(sl.ctypes.data, nseq, None, None)
     chunks = np.zeros((nch, 3), np.uint32)
     seqs = np.zeros((nseq, 2), np.uint32)
     L.halo_gdn_chunk_table(sl.ctypes.data, nseq, chunks.ctypes.data, seqs.ctypes.data)
-    bufs = {n: dev.to_device(a) for n, a in dict(q=qb, k=kb, v=vb, g=g, beta=beta, chunks=chunks, seqs=seqs,
-                                                    state=state).items()}
+    bufs = {n: dev.to_device(np.ascontiguousarray(a)) for n, a in dict(
+        q=qb, k=kb, v=vb, g=g, beta=beta, chunks=chunks, seqs=seqs, state=state).items()}
     go = dev.array((T, Hv, D), np.float32)
     ws = dev.array(L.halo_op_gdn_prefill_workspace_bytes(nch, Hv), np.uint8)
     dev.op("gdn_prefill", bufs["q"].ptr, bufs["k"].ptr, bufs["v"].ptr, bufs["g"].ptr, bufs["beta"].ptr,
            bufs["chunks"].ptr, bufs["seqs"].ptr, nch, nseq, bufs["state"].ptr, go.ptr, Hv, Hk, D, ws.ptr, ws.nbytes)
+    return go.download(), bufs["state"].download()
+
+
+def prefill_case(dev, rng, seqlens, Hv=32, Hk=16, zero_state=False):
+    qb, kb, vb, g, beta, state = prefill_inputs(rng, seqlens, Hv, Hk, zero_state)
+    go, gs = run_prefill(dev, seqlens, qb, kb, vb, g, beta, state, Hv, Hk)
     inputs = (from_bf16(qb), from_bf16(kb), from_bf16(vb), g, beta)
-    return go.download(), bufs["state"].download(), state, inputs
+    return go, gs, state, inputs
 
 
 def oracle_prefill(seqlens, state0, inputs, heads, Hv=32, Hk=16):
@@ -149,3 +159,21 @@ def test_gdn_prefill_c3_full(dev):
     for h in (0, 17):
         _close(got_o[:, h], want_o[:, h], f"outputs head {h}")
         _close(got_s[:, h], want_s[:, h], f"final state head {h}")
+
+
+def test_gdn_prefill_single_sequence_slices(dev):
+    """One sequence of 32 heads takes the 16-column scan (8 blocks per head: 256 blocks), two sequences the
+    32-column one. Per state column the arithmetic is the same, so the first sequence's outputs and final state agree
+    bitwise between the two; the single run is also checked against stepping."""
+    seqlens = [300, 37]
+    rng = np.random.default_rng(11)
+    qb, kb, vb, g, beta, state = prefill_inputs(rng, seqlens)
+    both_o, both_s = run_prefill(dev, seqlens, qb, kb, vb, g, beta, state)
+    n = seqlens[0]
+    one_o, one_s = run_prefill(dev, [n], qb[:n], kb[:n], vb[:n], g[:n], beta[:n], state[:1])
+    assert np.array_equal(one_o, both_o[:n]), "outputs differ between 16- and 32-column scans"
+    assert np.array_equal(one_s[0], both_s[0]), "final state differs between 16- and 32-column scans"
+    want_o, want_s = oracle_prefill([n], state[:1], (from_bf16(qb[:n]), from_bf16(kb[:n]), from_bf16(vb[:n]),
+                                                     g[:n], beta[:n]), range(32))
+    _close(one_o, want_o, "outputs")
+    _close(one_s, want_s, "final state")

@@ -485,7 +485,8 @@ int PrefillBatch(halo_model* m, const std::vector<halo_prefill_segment>& segs, c
                               Ptr(L.dt.device), Ptr(ts), Ptr(tp), Ptr(tstart), Ptr(p.qb.device), Ptr(p.kb.device),
                               Ptr(p.vb.device), Ptr(p.g.device), Ptr(p.beta.device), U32(T), U32(Hk), U32(Hv),
                               U32(c.conv_kernel), Val(eps)};
-        if (Launch(eng, "halo_gdn_prep_prefill", D3(CeilDiv(T, 16), C / 256), D3(64), a, err, errlen) != 0) return -1;
+        const char* prep = c.conv_kernel == 4 ? "halo_gdn_prep_prefill_k4" : "halo_gdn_prep_prefill";
+        if (Launch(eng, prep, D3(CeilDiv(T, 16), C / 256), D3(64), a, err, errlen) != 0) return -1;
       }
       if (save("gq", HALO_TRACE_F32, p.qb.device, static_cast<std::size_t>(T) * Hk * d) != 0 ||
           save("gk", HALO_TRACE_F32, p.kb.device, static_cast<std::size_t>(T) * Hk * d) != 0 ||

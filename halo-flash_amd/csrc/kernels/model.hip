@@ -292,6 +292,34 @@ extern "C" __global__ void __launch_bounds__(256)
 // owns channels 256 c + 4 l .. + 3 (16-byte loads and stores) for the block's 16 consecutive batch tokens; a q / k
 // head of 128 channels is 32 lanes, its sum of squares one 32-lane reduction. The tap rows of a token are the rows
 // the block just loaded for the tokens before it (L1 / L2 hits). d = 128, C % 256 == 0, K <= 8.
+namespace {
+// The outputs of one token of the prefill prologue from its four conv results y (channels ch .. ch + 3 of lane
+// `lane`): q / k L2-normalized per 128-channel head, v as is; blocks of column 0 also write the token's g and beta.
+__device__ __forceinline__ void GdnPrepOut(const float (&y)[4], std::uint32_t t, std::uint32_t ch, std::uint32_t lane,
+                                           const float* __restrict__ ab, const float* __restrict__ a,
+                                           const float* __restrict__ dt, float* __restrict__ q, float* __restrict__ k,
+                                           float* __restrict__ v, float* __restrict__ g, float* __restrict__ beta,
+                                           std::uint32_t Hk, std::uint32_t Hv, float eps) {
+  constexpr std::uint32_t kD = 128;
+  const std::uint32_t Dk = Hk * kD, Dv = Hv * kD;
+  if (ch < 2 * Dk) {
+    const float ss = halo::GroupSum<32>((y[0] * y[0] + y[1] * y[1]) + (y[2] * y[2] + y[3] * y[3]));
+    const float sc = 1.0f / sqrtf(ss + eps);
+    const std::uint32_t head = ch / kD;
+    float* dst = head < Hk ? q + (static_cast<std::size_t>(t) * Hk + head) * kD
+                           : k + (static_cast<std::size_t>(t) * Hk + head - Hk) * kD;
+    *reinterpret_cast<float4*>(dst + ch % kD) = make_float4(y[0] * sc, y[1] * sc, y[2] * sc, y[3] * sc);
+  } else {
+    *reinterpret_cast<float4*>(v + static_cast<std::size_t>(t) * Dv + ch - 2 * Dk) = make_float4(y[0], y[1], y[2], y[3]);
+  }
+  if (blockIdx.y == 0)
+    for (std::uint32_t h = lane; h < Hv; h += 64) {
+      g[static_cast<std::size_t>(t) * Hv + h] = a[h] * halo::Softplus(ab[static_cast<std::size_t>(t) * 2 * Hv + h] + dt[h]);
+      beta[static_cast<std::size_t>(t) * Hv + h] = halo::Sigmoid(ab[static_cast<std::size_t>(t) * 2 * Hv + Hv + h]);
+    }
+}
+}  // namespace
+
 extern "C" __global__ void __launch_bounds__(64) halo_gdn_prep_prefill(
     const float* __restrict__ qkv, const float* __restrict__ ring, const float* __restrict__ conv_w,
     const float* __restrict__ ab, const float* __restrict__ a, const float* __restrict__ dt,
@@ -308,7 +336,6 @@ extern "C" __global__ void __launch_bounds__(64) halo_gdn_prep_prefill(
   for (int c = 0; c < 4; ++c)
 #pragma unroll
     for (std::uint32_t j = 0; j < kMaxK; ++j) w[c][j] = j < K ? conv_w[static_cast<std::size_t>(ch + c) * K + j] : 0.0f;
-  const bool is_qk = ch < 2 * Dk;
   for (std::uint32_t t = t0; t < t1; ++t) {
     const std::uint32_t s = tok_sess[t], p = tok_pos[t], p0 = seg_start[t];
     const float4 x = *reinterpret_cast<const float4*>(qkv + static_cast<std::size_t>(t) * C + ch);
@@ -329,21 +356,63 @@ extern "C" __global__ void __launch_bounds__(64) halo_gdn_prep_prefill(
     float y[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) y[c] = halo::Silu(acc[c]);
-    if (is_qk) {
-      const float ss = halo::GroupSum<32>((y[0] * y[0] + y[1] * y[1]) + (y[2] * y[2] + y[3] * y[3]));
-      const float sc = 1.0f / sqrtf(ss + eps);
-      const std::uint32_t head = ch / kD;
-      float* dst = head < Hk ? q + (static_cast<std::size_t>(t) * Hk + head) * kD
-                             : k + (static_cast<std::size_t>(t) * Hk + head - Hk) * kD;
-      *reinterpret_cast<float4*>(dst + ch % kD) = make_float4(y[0] * sc, y[1] * sc, y[2] * sc, y[3] * sc);
-    } else {
-      *reinterpret_cast<float4*>(v + static_cast<std::size_t>(t) * Dv + ch - 2 * Dk) = make_float4(y[0], y[1], y[2], y[3]);
+    GdnPrepOut(y, t, ch, lane, ab, a, dt, q, k, v, g, beta, Hk, Hv, eps);
+  }
+}
+
+// The same prologue for conv kernel K = 4 with the block's rows in registers: the 16 tokens' rows and the 3 before
+// them are loaded at once (19 independent 16-byte loads per lane), so the taps cost no further loads and no load
+// waits on the previous token's; ring rows (taps below a run's first position in this batch) are loaded where
+// needed. Same operations in the same order as halo_gdn_prep_prefill, so the results are bitwise equal.
+extern "C" __global__ void __launch_bounds__(64) halo_gdn_prep_prefill_k4(
+    const float* __restrict__ qkv, const float* __restrict__ ring, const float* __restrict__ conv_w,
+    const float* __restrict__ ab, const float* __restrict__ a, const float* __restrict__ dt,
+    const std::uint32_t* __restrict__ tok_sess, const std::uint32_t* __restrict__ tok_pos,
+    const std::uint32_t* __restrict__ seg_start, float* __restrict__ q, float* __restrict__ k,
+    float* __restrict__ v, float* __restrict__ g, float* __restrict__ beta, std::uint32_t T, std::uint32_t Hk,
+    std::uint32_t Hv, std::uint32_t K, float eps) {
+  constexpr std::uint32_t kD = 128, kTok = 16, kK = 4;
+  const std::uint32_t C = 2 * Hk * kD + Hv * kD;
+  const std::uint32_t lane = threadIdx.x, ch = blockIdx.y * 256 + 4 * lane;
+  const std::uint32_t t0 = blockIdx.x * kTok;
+  float w[4][kK];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (std::uint32_t j = 0; j < kK; ++j) w[c][j] = conv_w[static_cast<std::size_t>(ch + c) * K + j];
+  // xr[r] = row t0 - 3 + r (clamped into [0, T): rows outside are loaded but never used)
+  float4 xr[kTok + kK - 1];
+#pragma unroll
+  for (std::uint32_t r = 0; r < kTok + kK - 1; ++r) {
+    const std::int64_t row = static_cast<std::int64_t>(t0) - static_cast<std::int64_t>(kK - 1) + r;
+    const std::uint32_t rc = static_cast<std::uint32_t>(row < 0 ? 0 : (row >= T ? T - 1 : row));
+    xr[r] = *reinterpret_cast<const float4*>(qkv + static_cast<std::size_t>(rc) * C + ch);
+  }
+#pragma unroll
+  for (std::uint32_t i = 0; i < kTok; ++i) {
+    const std::uint32_t t = t0 + i;
+    if (t >= T) break;
+    const std::uint32_t s = tok_sess[t], p = tok_pos[t], p0 = seg_start[t];
+    const float4 x = xr[i + kK - 1];
+    float acc[4] = {w[0][kK - 1] * x.x, w[1][kK - 1] * x.y, w[2][kK - 1] * x.z, w[3][kK - 1] * x.w};
+#pragma unroll
+    for (std::uint32_t j = 0; j + 1 < kK; ++j) {
+      // tap j reads position p - 3 + j: row t - 3 + j when inside the run
+      const std::int64_t pp = static_cast<std::int64_t>(p) - static_cast<std::int64_t>(kK - 1) + j;
+      float4 xv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (pp >= static_cast<std::int64_t>(p0))
+        xv = xr[i + j];
+      else if (pp >= 0)
+        xv = *reinterpret_cast<const float4*>(ring + (static_cast<std::size_t>(s) * kK + static_cast<std::uint32_t>(pp) % kK) * C + ch);
+      acc[0] += w[0][j] * xv.x;
+      acc[1] += w[1][j] * xv.y;
+      acc[2] += w[2][j] * xv.z;
+      acc[3] += w[3][j] * xv.w;
     }
-    if (blockIdx.y == 0)
-      for (std::uint32_t h = lane; h < Hv; h += 64) {
-        g[static_cast<std::size_t>(t) * Hv + h] = a[h] * halo::Softplus(ab[static_cast<std::size_t>(t) * 2 * Hv + h] + dt[h]);
-        beta[static_cast<std::size_t>(t) * Hv + h] = halo::Sigmoid(ab[static_cast<std::size_t>(t) * 2 * Hv + Hv + h]);
-      }
+    float y[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) y[c] = halo::Silu(acc[c]);
+    GdnPrepOut(y, t, ch, lane, ab, a, dt, q, k, v, g, beta, Hk, Hv, eps);
   }
 }
 

@@ -18,10 +18,10 @@ from teacher import LayerChecker, PrefillChecker
 pytestmark = pytest.mark.gpu
 
 
-def twin(max_sessions=2, prefix=0, ctx=64, prefill_batch=0):
+def twin(max_sessions=2, prefix=0, ctx=64, prefill_batch=0, conv_kernel=4):
     """C4's attention grouping (8 query heads per kv head, the shape the prefill attention kernel is built for)."""
     return H.ModelConfig(vocab=2048, hidden=1024, layers=4, attn_interval=4, gdn_k_heads=4, gdn_v_heads=8,
-                         gdn_head_dim=128, conv_kernel=4, q_heads=16, kv_heads=2, head_dim=256, rotary_dim=64,
+                         gdn_head_dim=128, conv_kernel=conv_kernel, q_heads=16, kv_heads=2, head_dim=256, rotary_dim=64,
                          n_experts=16, n_used=4, expert_ff=256, shared_ff=256, rope_theta=1e7, rms_eps=1e-6,
                          max_sessions=max_sessions, max_context=ctx, prefix_tokens=prefix,
                          prefill_batch=prefill_batch)
@@ -33,8 +33,11 @@ def _flips_ok(rep):
     assert rep.loose <= max(64, rep.codes // 1000)
 
 
-def test_ragged_prefill_then_decode(dev):
-    cfg = twin()
+@pytest.mark.parametrize("conv_kernel", [4, 3])
+def test_ragged_prefill_then_decode(dev, conv_kernel):
+    """conv_kernel 4 takes the register-row prologue (halo_gdn_prep_prefill_k4), 3 the general one; the 16-token
+    prologue block spans both prompts."""
+    cfg = twin(conv_kernel=conv_kernel)
     model = H.Model(dev, cfg, seed=11)
     try:
         rng = np.random.default_rng(4)

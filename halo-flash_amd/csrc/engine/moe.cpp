@@ -250,8 +250,8 @@ int halo_op_moe_prefill(halo_engine* eng, const halo_moe_weights* w, const float
   }
   // 2. x quantized per 32
   {
-    const halo_arg a[] = {Ptr(x), Ptr(v.xq), Ptr(v.xs), U32(H)};
-    if (Launch(eng, "halo_quantize_q8_rows", D3(T), D3(256), a, err, errlen) != 0) return -1;
+    const halo_arg a[] = {Ptr(x), Ptr(v.xq), Ptr(v.xs), U32(H), U32(T)};
+    if (Launch(eng, "halo_quantize_q8_rows8", D3(CeilDiv(T, 8)), D3(256), a, err, errlen) != 0) return -1;
   }
   // 3. softmax / top-k per token
   {
@@ -283,8 +283,8 @@ int halo_op_moe_prefill(halo_engine* eng, const halo_moe_weights* w, const float
   }
   // 6. h quantized per 32
   {
-    const halo_arg a[] = {Ptr(v.h), Ptr(v.hq), Ptr(v.hs), U32(F)};
-    if (Launch(eng, "halo_quantize_q8_rows", D3(G), D3(256), a, err, errlen) != 0) return -1;
+    const halo_arg a[] = {Ptr(v.h), Ptr(v.hq), Ptr(v.hs), U32(F), U32(G)};
+    if (Launch(eng, "halo_quantize_q8_rows8", D3(CeilDiv(G, 8)), D3(256), a, err, errlen) != 0) return -1;
   }
   // 7. grouped down -> y [G][H]
   {

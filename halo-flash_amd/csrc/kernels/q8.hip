@@ -55,6 +55,23 @@ extern "C" __global__ void __launch_bounds__(256)
   }
 }
 
+// halo_quantize_q8_rows over 8 rows per block (grid ceil(T / 8)): the block's rows are one flat run of 16-byte
+// groups, so short rows (the MoE's 512-wide h) keep every lane busy and each lane has several loads in flight.
+// Q8_0 blocks and 8-lane groups line up as in the one-row form (cols % 32 == 0), so the codes are bitwise equal.
+extern "C" __global__ void __launch_bounds__(256)
+    halo_quantize_q8_rows8(const float* x, std::int8_t* xq, float* xd, std::uint32_t cols, std::uint32_t T) {
+  const std::size_t t0 = static_cast<std::size_t>(blockIdx.x) * 8;
+  const std::size_t rows = min(static_cast<std::size_t>(8), T - t0), n4 = rows * (cols / 4);
+  const float4* src = reinterpret_cast<const float4*>(x + t0 * cols);
+  std::uint32_t* codes = reinterpret_cast<std::uint32_t*>(xq + t0 * cols);
+  float* scales = xd + t0 * (cols / 32);
+  for (std::size_t g = threadIdx.x; g < n4; g += blockDim.x) {
+    float scale;
+    codes[g] = halo::QuantQuad(src[g], scale);
+    if (g % 8 == 0) scales[g / 8] = scale;
+  }
+}
+
 // reference src/kernels/batch_decode.hip:201-222. Grid (ceil(cols / 256), B), 256 threads: x column b at
 // x + b * xstride -> xq + b * cols, xs + b * cols / 32; with xq2 the residual x - q * s (product rounded before the
 // subtraction) is quantized again into xq2 / xs2. The block's 256 values go to its first wave, 4 values per lane

@@ -318,6 +318,27 @@ def test_quantize_kblocked_bit_exact(dev):
     assert gd.download().tobytes() == np.ascontiguousarray(wd.T).tobytes()
 
 
+@pytest.mark.parametrize("T,cols", [(1, 512), (13, 512), (21, 2048), (8, 96)])
+def test_quantize_rows8_bit_exact(dev, T, cols):
+    """halo_quantize_q8_rows8 (8 rows per block, ragged last block) against the oracle's quantizer and bytewise
+    against the one-row halo_quantize_q8_rows."""
+    rng = np.random.default_rng(T * cols)
+    x = rng.normal(0, 1, (T, cols)).astype(np.float32)
+    x[T // 2, :32] = 0.0  # an all-zero block: scale 0, q 0
+    gx = dev.to_device(x)
+    outs = []
+    for name, grid, extra in (("halo_quantize_q8_rows8", ((T + 7) // 8,), [("u32", T)]),
+                              ("halo_quantize_q8_rows", (T,), [])):
+        gq, gd = dev.array((T, cols), np.int8), dev.array((T, cols // 32), np.float32)
+        dev.launch(name, grid, (256,), [gx, gq, gd, ("u32", cols)] + extra)
+        outs.append((gq.download(), gd.download()))
+    wq, wd = np.zeros((T, cols), np.int8), np.zeros((T, cols // 32), np.float32)
+    for t in range(T):
+        O.oracle().or_quantize_q8_act(x[t], wq[t], wd[t], cols)
+    assert np.array_equal(outs[0][0], wq) and outs[0][1].tobytes() == wd.tobytes()
+    assert np.array_equal(outs[0][0], outs[1][0]) and outs[0][1].tobytes() == outs[1][1].tobytes()
+
+
 def test_router_topk_w(dev):
     rng = np.random.default_rng(46)
     for n, k in ((512, 10), (256, 8), (1024, 16), (64, 1)):

@@ -268,7 +268,7 @@ int halo_op_moe_prefill(halo_engine* eng, const halo_moe_weights* w, const float
                           U32(tile), U32(nb)};
     if (Launch(eng, "halo_moe_group_scan", D3(1), D3(1024), b, err, errlen) != 0) return -1;
     const halo_arg c[] = {Ptr(v.ids), Ptr(v.start), Ptr(v.token), Ptr(v.pos), U32(T), U32(k), U32(E)};
-    if (Launch(eng, "halo_moe_group_fill", D3(E + (shared ? 1 : 0)), D3(256), c, err, errlen) != 0) return -1;
+    if (Launch(eng, "halo_moe_group_fill", D3(E + (shared ? 1 : 0)), D3(1024), c, err, errlen) != 0) return -1;
   }
   // 5. grouped gate / up + SwiGLU -> h [G][F]
   {

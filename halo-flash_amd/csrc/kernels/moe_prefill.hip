@@ -158,14 +158,14 @@ extern "C" __global__ void __launch_bounds__(1024)
   }
 }
 
-// grid (E + shared), block 256: group e's pairs in token order: token[start[e] + j] = the j-th token selecting e
+// grid (E + shared), block 1024: group e's pairs in token order: token[start[e] + j] = the j-th token selecting e
 // (the shared group: every token), pos[t k + s] = that position for routed pairs. Compaction by ballot per chunk of
-// 256 tokens, chunks in order.
-extern "C" __global__ void __launch_bounds__(256)
+// 1024 tokens, chunks in order (16 waves per block: a quarter of the serial chunk steps of 256-token chunks).
+extern "C" __global__ void __launch_bounds__(1024)
     halo_moe_group_fill(const std::uint32_t* __restrict__ ids, const std::uint32_t* __restrict__ start,
                         std::uint32_t* __restrict__ token, std::uint32_t* __restrict__ pos, std::uint32_t T,
                         std::uint32_t k, std::uint32_t E) {
-  __shared__ std::uint32_t wcount[4];
+  __shared__ std::uint32_t wcount[16];
   __shared__ std::uint32_t base_s;
   const std::uint32_t e = blockIdx.x, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   if (threadIdx.x == 0) base_s = start[e];
@@ -177,6 +177,7 @@ extern "C" __global__ void __launch_bounds__(256)
       if (e == E) {
         slot = 0;
       } else {
+#pragma unroll 4
         for (std::uint32_t s = 0; s < k; ++s)
           if (ids[static_cast<std::size_t>(t) * k + s] == e) slot = s;
       }
@@ -195,7 +196,11 @@ extern "C" __global__ void __launch_bounds__(256)
       if (e < E) pos[static_cast<std::size_t>(t) * k + slot] = p;
     }
     __syncthreads();
-    if (threadIdx.x == 0) base_s += wcount[0] + wcount[1] + wcount[2] + wcount[3];
+    if (threadIdx.x == 0) {
+      std::uint32_t sum = 0;
+      for (std::uint32_t w = 0; w < blockDim.x / kWave; ++w) sum += wcount[w];
+      base_s += sum;
+    }
     __syncthreads();
   }
 }

@@ -901,17 +901,26 @@ def run_c0(args, dev, H, res):
         else:
             dev.op("matvec_q8a8_tiled", ctypes.byref(w.desc), x0q.ptr, x0s.ptr, y0.ptr, 1, 4096, *t)
 
-    def graph(t, n):  # n GEMVs cycling through the copies
+    def graph(t, n, first=0):  # n GEMVs cycling through the copies, starting at copy `first`
         dev.begin_capture()
         for i in range(n):
-            gemv(ws0[i % c0_copies], t)
+            gemv(ws0[(first + i) % c0_copies], t)
         return dev.end_capture()
 
-    def run_exact(t, steps):  # exactly `steps` GEMVs: whole rotations, then the remainder
+    def run_exact(t, steps, first=0):  # exactly `steps` GEMVs: whole rotations, then the remainder
         full, rest = divmod(steps, c0_copies)
-        gf = graph(t, c0_copies) if full else None
-        gr = graph(t, rest) if rest else None
+        gf = graph(t, c0_copies, first) if full else None
+        gr = graph(t, rest, (first + full * c0_copies) % c0_copies) if rest else None
         return gf, full, gr
+
+    # Cache flush between the untimed and the timed launches: one streaming read of 512 MB (twice the 256 MB MALL)
+    flush = dev.array(512 << 20, np.uint8)
+    sink = dev.array(4, np.int32)
+    stamps = dev.array(2, np.uint64)
+    khz = dev.wall_clock_khz()
+
+    def flush_caches():
+        dev.launch("halo_stream_read", (4096,), (256,), [("ptr", flush.ptr), ("u64", flush.nbytes // 16), sink])
 
     if args.eager:  # kernel durations under a profiler
         for i in range(args.steps):
@@ -919,25 +928,50 @@ def run_c0(args, dev, H, res):
         dev.sync()
         res.update(value=0.0, steps_timed=args.steps, ms_per_step=0.0, roofline=None)
         return res
+    # the stamps' own cost (two stamp launches back to back in one graph), subtracted from every timed region
+    dev.begin_capture()
+    dev.launch("halo_clock_stamp", (1,), (64,), [stamps, ("u32", 0)])
+    dev.launch("halo_clock_stamp", (1,), (64,), [stamps, ("u32", 1)])
+    g0 = dev.end_capture()
+    over = []
+    for _ in range(20):
+        dev.launch_graph(g0)
+        dev.sync()
+        st = stamps.download()
+        over.append(float(st[1] - st[0]) / khz)
+    dev.free_graph(g0)
+    stamp_ms = float(np.median(over))
     tilings = [None] + ([(64, 2, 4), (64, 1, 2), (64, 1, 1), (32, 1, 4), "nt"] if args.sweep else [])
     c0 = {}
     for t in tilings:
         steps = args.steps if t is None else 2000
-        gw, fw, rw = run_exact(t, args.warmup) if t is None and args.warmup else (None, 0, None)
+        warm = args.warmup if t is None else 0
+        # The timed region is one graph of exactly `steps` GEMVs, starting at copy `warm` (after the copies the
+        # warm-up reads), with the timer's start and stop marks recorded inside it as event nodes, so the graph
+        # launch's own latency is outside the region. The graph is launched once untimed first (its first launch
+        # pays the upload), then the caches are flushed, then the warm-up GEMVs run on copies 0 .. warm - 1: every
+        # timed GEMV reads weights that no launch touched since the flush.
+        dev.begin_capture()
+        dev.launch("halo_clock_stamp", (1,), (64,), [stamps, ("u32", 0)])
+        for i in range(steps):
+            gemv(ws0[(warm + i) % c0_copies], t)
+        dev.launch("halo_clock_stamp", (1,), (64,), [stamps, ("u32", 1)])
+        gt = dev.end_capture()
+        dev.launch_graph(gt)
+        flush_caches()
+        gw, fw, rw = run_exact(t, warm) if warm else (None, 0, None)
+        dev.sync()
+        # warm-up and timed launches queued back to back (no host wait between them, so the device does not idle
+        # and clock down before the timed region)
         for _ in range(fw):
             dev.launch_graph(gw)
         if rw is not None:
             dev.launch_graph(rw)
-        gf, full, gr = run_exact(t, steps)
+        dev.launch_graph(gt)
         dev.sync()
-        dev.timer_start()
-        for _ in range(full):
-            dev.launch_graph(gf)
-        if gr is not None:
-            dev.launch_graph(gr)
-        ms = dev.timer_stop()
-        dev.sync()
-        for g_ in (gw, rw, gf, gr):
+        st = stamps.download()
+        ms = float(st[1] - st[0]) / khz - stamp_ms
+        for g_ in (gw, rw, gt):
             if g_ is not None:
                 dev.free_graph(g_)
         us = ms * 1e3 / steps
@@ -963,7 +997,10 @@ def run_c0(args, dev, H, res):
         "traffic_source": "profiles/gemv_q8a8_c0_4096x4096.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)",
         "us_per_launch": best["us_per_gemv"],
         "algorithmic_bytes_per_launch": C0_BYTES,
-        "timing": "HIP events on the device stream around exactly `steps` back-to-back launches",
+        "timing": ("device wall clock (halo_clock_stamp nodes) at the start and end of one graph of exactly `steps` "
+                   "back-to-back launches, queued right after the warm-up launches, less the stamps' own time (two "
+                   "stamps back to back, median of 20)"),
+        "stamp_overhead_us": round(stamp_ms * 1e3, 3),
     }
     if args.sweep:
         res["c0_tilings"] = c0
@@ -979,6 +1016,16 @@ def _median_time(fn, budget_s, min_reps=10, max_reps=2000):
         fn()
         times.append(time.perf_counter() - t0)
     return float(np.median(times)), len(times)
+
+
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_baseline(budget_s: float):
@@ -1084,6 +1131,8 @@ def cpu_baseline(budget_s: float):
     except AttributeError:
         aff = os.cpu_count()
     head["available_cpus"] = aff
+    head["nproc"] = os.cpu_count()
+    head["cpu_model"] = _cpu_model()
     head["legs"] = legs
     return head
 
@@ -1091,8 +1140,8 @@ def cpu_baseline(budget_s: float):
 def main():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=6800)
-    p.add_argument("--warmup", type=int, default=680)
+    p.add_argument("--steps", type=int, default=2000)
+    p.add_argument("--warmup", type=int, default=200)
     p.add_argument("--sweep", action="store_true", help="also time alternative C0 GEMV tilings")
     p.add_argument("--cpu-seconds", type=float, default=20.0)
     p.add_argument("--no-cpu", action="store_true")

@@ -24,21 +24,26 @@ static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 std::mutex g_mu;
 std::array<void*, kMaxDevices> g_ptr{};  // scratch's device address per device, null until looked up
 
-// The current device's scratch address (looked up on the first call on that device).
-void* ScratchOfCurrentDevice(char* err, std::size_t errlen) {
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return halo::engine::SetErr(err, errlen, "hipGetDevice: %s", hipGetErrorString(e)), nullptr;
-  if (dev < 0 || dev >= kMaxDevices) return halo::engine::SetErr(err, errlen, "device %d out of range", dev), nullptr;
+// Device `ordinal`'s scratch address, looked up on the first call on that device with that device made current
+// (the calling thread's current device is restored afterwards).
+void* ScratchOfDevice(int ordinal, char* err, std::size_t errlen) {
+  if (ordinal < 0 || ordinal >= kMaxDevices)
+    return halo::engine::SetErr(err, errlen, "moe noalloc: device %d out of range", ordinal), nullptr;
   std::lock_guard<std::mutex> lock(g_mu);
-  if (g_ptr[dev] == nullptr) {
+  if (g_ptr[ordinal] == nullptr) {
+    int prev = -1;
+    hipError_t e = hipGetDevice(&prev);
+    if (e != hipSuccess) return halo::engine::SetErr(err, errlen, "hipGetDevice: %s", hipGetErrorString(e)), nullptr;
+    if (prev != ordinal && (e = hipSetDevice(ordinal)) != hipSuccess)
+      return halo::engine::SetErr(err, errlen, "hipSetDevice(%d): %s", ordinal, hipGetErrorString(e)), nullptr;
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (prev != ordinal) (void)hipSetDevice(prev);
     if (e != hipSuccess || p == nullptr)
       return halo::engine::SetErr(err, errlen, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e)), nullptr;
-    g_ptr[dev] = p;
+    g_ptr[ordinal] = p;
   }
-  return g_ptr[dev];
+  return g_ptr[ordinal];
 }
 
 }  // namespace
@@ -47,8 +52,8 @@ extern "C" {
 
 int halo_op_moe_decode_noalloc(halo_engine* eng, const halo_moe_weights* w, const float* x, float* out,
                                uint32_t tokens, char* err, size_t errlen) {
-  if (eng == nullptr || x == nullptr || out == nullptr)
-    return halo::engine::SetErr(err, errlen, "moe noalloc: null engine, input or output"), -1;
+  if (w == nullptr || x == nullptr || out == nullptr)
+    return halo::engine::SetErr(err, errlen, "moe noalloc: null weights, input or output"), -1;
   const std::size_t need = halo_op_moe_workspace_bytes(w, tokens);
   if (need == 0) {
     halo_moe_views v;  // reports why the layer is refused
@@ -60,7 +65,8 @@ int halo_op_moe_decode_noalloc(halo_engine* eng, const halo_moe_weights* w, cons
                                 "moe noalloc: %u tokens need %zu workspace bytes, more than the %zu-byte fixed scratch",
                                 tokens, need, kScratchBytes),
            -1;
-  void* ws = ScratchOfCurrentDevice(err, errlen);
+  if (eng == nullptr || eng->dev == nullptr) return halo::engine::SetErr(err, errlen, "moe noalloc: null engine"), -1;
+  void* ws = ScratchOfDevice(halo_device_ordinal(eng->dev), err, errlen);
   if (ws == nullptr) return -1;
   return halo_op_moe_decode(eng, w, x, out, tokens, ws, kScratchBytes, err, errlen);
 }

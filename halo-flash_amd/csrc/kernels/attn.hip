@@ -27,8 +27,9 @@ using halo::SplitHalves;
 using halo::V4F;
 namespace {
 // Operand scales of the split-fp16 paths (powers of two, undone on the results): q and k (RMS-normalized) and V by 2^8,
-// so values down to 2^-11 keep the full 22-bit split and |q|, |k|, |V| up to 255 stay in the fp16 range; the
-// probabilities (<= 1) by 2^14.
+// so values down to 2^-11 keep the full 22-bit split; a group (query row, K or V chunk) with a magnitude of 255.875 or
+// more takes a smaller power of two instead (halo::SplitScale), keeping it in the fp16 range. The probabilities (<= 1)
+// by 2^14.
 constexpr float kSqk = 256.0f, kSvv = 256.0f, kSpp = 16384.0f;
 constexpr float kLog2e = 1.4426950408889634f;
 }  // namespace
@@ -290,18 +291,62 @@ __device__ __forceinline__ void AttnDecodePartial(
   const std::uint32_t nqt = (nq + 15) / 16, kq = lane / 16, lr = lane % 16;
   const std::uint32_t qt = wave / 2, kt = wave % 2;
   const bool score_wave = qt < nqt;
+  // Operand scales (powers of two): per query row, and per block for the K and the V chunk (halo::SplitScale:
+  // kSqk / kSvv unless the group's largest magnitude would overflow the fp16 range)
+  __shared__ float qsc[kMaxQ], kvmax[2][4];
   H8 qh[kHd / 32], ql[kHd / 32];
   if (score_wave) {
     const float* qr = &qs[min(16 * qt + lr, nq - 1)][0];
+    float xr[kHd / 32][8];
+    float amax = 0.0f;
 #pragma unroll
     for (int c = 0; c < kHd / 32; ++c) {
       const float4 a0 = *reinterpret_cast<const float4*>(qr + 32 * c + 8 * kq);
       const float4 a1 = *reinterpret_cast<const float4*>(qr + 32 * c + 8 * kq + 4);
       const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-      SplitHalves(x, qh[c], ql[c], kSqk);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xr[c][e] = x[e];
+        amax = fmaxf(amax, fabsf(x[e]));
+      }
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    const float sq = halo::SplitScale(amax, kSqk);
+#pragma unroll
+    for (int c = 0; c < kHd / 32; ++c) SplitHalves(xr[c], qh[c], ql[c], sq);
+    if (kq == 0) qsc[16 * qt + lr] = sq;
+  }
+  {  // the block's K and V magnitudes (the newest row from LDS; V rows past the visible range are zeroed below)
+    float ka = 0.0f, va = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const std::uint32_t j = r + 16 * h;
+      const bool fresh = owner && start + j == last;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float4 kv = fresh ? *reinterpret_cast<const float4*>(&knew[0][64 * u + 4 * sub]) : kf[h][u];
+        ka = fmaxf(ka, fmaxf(fmaxf(fabsf(kv.x), fabsf(kv.y)), fmaxf(fabsf(kv.z), fabsf(kv.w))));
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const std::uint32_t j = 8 * vkg + e;
+      float4 vv = vreg[e];
+      if (owner && start + j == last) vv = *reinterpret_cast<const float4*>(&knew[kFused ? 1 : 0][4 * vdg]);
+      if (start + j < limit)
+        va = fmaxf(va, fmaxf(fmaxf(fabsf(vv.x), fabsf(vv.y)), fmaxf(fabsf(vv.z), fabsf(vv.w))));
+    }
+    ka = halo::GroupMax(ka);
+    va = halo::GroupMax(va);
+    if (lane == 0) {
+      kvmax[0][wave] = ka;
+      kvmax[1][wave] = va;
     }
   }
   __syncthreads();  // qs is free: the K chunk goes there as halves
+  const float sk = halo::SplitScale(fmaxf(fmaxf(kvmax[0][0], kvmax[0][1]), fmaxf(kvmax[0][2], kvmax[0][3])), kSqk);
+  const float sv = halo::SplitScale(fmaxf(fmaxf(kvmax[1][0], kvmax[1][1]), fmaxf(kvmax[1][2], kvmax[1][3])), kSvv);
   // K halves kh / kl [32 keys][256]: 16-byte chunk c of key row j at c ^ (j & 15) (the 16 lanes of an operand read
   // take 16 different bank groups); the newest row (owner) from LDS, not yet in the pool when it was loaded
   _Float16* kh = reinterpret_cast<_Float16*>(&qs[0][0]);
@@ -317,7 +362,7 @@ __device__ __forceinline__ void AttnDecodePartial(
       const float x[4] = {kv.x, kv.y, kv.z, kv.w};
       const std::uint32_t off = j * kHd + 8 * ((dim / 8) ^ (j & 15)) + dim % 8;
       H4 hi, lo;
-      halo::SplitHalves4(x, hi, lo, kSqk);
+      halo::SplitHalves4(x, hi, lo, sk);
       *reinterpret_cast<H4*>(&kh[off]) = hi;
       *reinterpret_cast<H4*>(&kl[off]) = lo;
     }
@@ -337,7 +382,7 @@ __device__ __forceinline__ void AttnDecodePartial(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const std::uint32_t qi = 16 * qt + 4 * kq + i;
-      if (qi < nq) sc[qi][key] = live ? c4[i] * (scale / (kSqk * kSqk)) : -INFINITY;
+      if (qi < nq) sc[qi][key] = live ? c4[i] * (scale / (qsc[qi] * sk)) : -INFINITY;
     }
   }
   __syncthreads();
@@ -358,7 +403,7 @@ __device__ __forceinline__ void AttnDecodePartial(
       x[e] = start + j < limit ? val : 0.0f;
     }
     H8 hi, lo;
-    SplitHalves(x, hi, lo, kSvv);
+    SplitHalves(x, hi, lo, sv);
     const std::uint32_t off = dim * kChunk + 8 * (vkg ^ ((dim >> 2) & 3));
     *reinterpret_cast<H8*>(&vh[off]) = hi;
     *reinterpret_cast<H8*>(&vl[off]) = lo;
@@ -399,7 +444,7 @@ __device__ __forceinline__ void AttnDecodePartial(
       const std::uint32_t qi = 16 * pqt + 4 * kq + i;
       if (qi < nq) {
         const std::uint32_t slot = is_prefix ? qi : sess * G + qi;
-        a_out[static_cast<std::size_t>(slot) * kHd + dim] = acc[i] * (1.0f / (kSpp * kSvv));
+        a_out[static_cast<std::size_t>(slot) * kHd + dim] = acc[i] * (1.0f / (kSpp * sv));
       }
     }
   }
@@ -580,7 +625,8 @@ extern "C" __global__ void __launch_bounds__(64)
 // (products of halves are exact in the fp32 accumulator; the dropped lo * lo term is below 2^-22 of the product).
 // Three fp16 MFMAs cost 3/16 of the fp32 MFMA issue time of the same products, so the scores and P V run at about
 // five times the fp32 MFMA rate with fp32-level accuracy. q, k and V are scaled by 2^8 and the probabilities by 2^14
-// before the split (kSqk, kSvv, kSpp): |q|, |k|, |V| must stay below 255.
+// before the split (kSqk, kSvv, kSpp); a query row, K chunk or V chunk whose magnitude would overflow fp16 at 2^8
+// takes a smaller power of two (halo::SplitScale), so any finite operand range is accepted.
 // (An fp32 version of this kernel on v_mfma_f32_16x16x4f32 ran the C4 prefix prefill's attention at 78.8 TFLOP/s.)
 // The K and V chunks are converted once per block while staged in LDS: K as kh / kl [key][256] (16-byte chunk c of row key at
 // c ^ (key & 15): the 16 lanes reading one column of keys hit 16 different bank groups), V transposed as vh / vl
@@ -625,13 +671,13 @@ extern "C" __global__ void __launch_bounds__(256, 2) halo_attn_prefill(
           vpool + ((static_cast<std::size_t>(pt[kp / kPage]) * Hkv + kvh) * kPage + kp % kPage) * kHd)[vdg];
     }
   };
-  auto stage_chunk = [&]() {
+  auto stage_chunk = [&](float sk, float sv) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float x[8] = {kreg[2 * j].x,     kreg[2 * j].y,     kreg[2 * j].z,     kreg[2 * j].w,
                           kreg[2 * j + 1].x, kreg[2 * j + 1].y, kreg[2 * j + 1].z, kreg[2 * j + 1].w};
       H8 hi, lo;
-      SplitHalves(x, hi, lo, kSqk);
+      SplitHalves(x, hi, lo, sk);
       const std::uint32_t off = skey * kHd + 8 * ((spart + 8 * j) ^ (skey & 15));
       *reinterpret_cast<H8*>(&kh[off]) = hi;
       *reinterpret_cast<H8*>(&kl[off]) = lo;
@@ -642,7 +688,7 @@ extern "C" __global__ void __launch_bounds__(256, 2) halo_attn_prefill(
 #pragma unroll
       for (int e = 0; e < 8; ++e) x[e] = d == 0 ? vreg[e].x : d == 1 ? vreg[e].y : d == 2 ? vreg[e].z : vreg[e].w;
       H8 hi, lo;
-      SplitHalves(x, hi, lo, kSvv);
+      SplitHalves(x, hi, lo, sv);
       const std::uint32_t dim = 4 * vdg + d;
       const std::uint32_t off = dim * kChunk + 8 * (vkg ^ ((dim >> 2) & 3));
       *reinterpret_cast<H8*>(&vh[off]) = hi;
@@ -653,14 +699,34 @@ extern "C" __global__ void __launch_bounds__(256, 2) halo_attn_prefill(
   // this lane's A-operand query: row r -> token 2 wave + r / 8, head r % 8; dims 32 c + 8 kq .. + 7
   const std::uint32_t qtok = min(2 * wave + row / 8, ntok - 1), qg = row % 8;
   const float* qrow = q + ((static_cast<std::size_t>(first) + qtok) * Hq + kvh * G + qg) * kHd;
+  // Operand scales (powers of two, halo::SplitScale): per query row, per chunk for K; V's scale is the smallest of
+  // the chunks so far (the accumulators are rescaled, exactly, when it drops)
   H8 qh[kHd / 32], ql[kHd / 32];
+  float sqc[4];
+  {
+    float xr[kHd / 32][8];
+    float amax = 0.0f;
 #pragma unroll
-  for (int c = 0; c < kHd / 32; ++c) {
-    const float4 a = *reinterpret_cast<const float4*>(qrow + 32 * c + 8 * kq);
-    const float4 b = *reinterpret_cast<const float4*>(qrow + 32 * c + 8 * kq + 4);
-    const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    SplitHalves(x, qh[c], ql[c], kSqk);
+    for (int c = 0; c < kHd / 32; ++c) {
+      const float4 a = *reinterpret_cast<const float4*>(qrow + 32 * c + 8 * kq);
+      const float4 b = *reinterpret_cast<const float4*>(qrow + 32 * c + 8 * kq + 4);
+      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xr[c][e] = x[e];
+        amax = fmaxf(amax, fabsf(x[e]));
+      }
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    const float sq = halo::SplitScale(amax, kSqk);
+#pragma unroll
+    for (int c = 0; c < kHd / 32; ++c) SplitHalves(xr[c], qh[c], ql[c], sq);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sqc[i] = __shfl(sq, 4 * kq + i);  // the scales of this lane's output rows
   }
+  __shared__ float kvmax[2][4];
+  float sv = kSvv;
   std::uint32_t qpos[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) qpos[i] = p0 + 2 * wave + (4 * kq + i) / 8;
@@ -678,8 +744,26 @@ extern "C" __global__ void __launch_bounds__(256, 2) halo_attn_prefill(
   _Float16* pwl = &pl[wave][0];
   for (std::uint32_t ch = 0; ch < nchunks; ++ch) {
     const std::uint32_t k0 = ch * kChunk;
+    {  // the chunk's K and V magnitudes
+      float ka = 0.0f, va = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        ka = fmaxf(ka, fmaxf(fmaxf(fabsf(kreg[e].x), fabsf(kreg[e].y)), fmaxf(fabsf(kreg[e].z), fabsf(kreg[e].w))));
+        va = fmaxf(va, fmaxf(fmaxf(fabsf(vreg[e].x), fabsf(vreg[e].y)), fmaxf(fabsf(vreg[e].z), fabsf(vreg[e].w))));
+      }
+      ka = halo::GroupMax(ka);
+      va = halo::GroupMax(va);
+      if (lane == 0) {
+        kvmax[0][wave] = ka;
+        kvmax[1][wave] = va;
+      }
+    }
     __syncthreads();  // every wave is done with the previous chunk's LDS
-    stage_chunk();
+    const float sk = halo::SplitScale(fmaxf(fmaxf(kvmax[0][0], kvmax[0][1]), fmaxf(kvmax[0][2], kvmax[0][3])), kSqk);
+    const float svc = halo::SplitScale(fmaxf(fmaxf(kvmax[1][0], kvmax[1][1]), fmaxf(kvmax[1][2], kvmax[1][3])), kSvv);
+    const float vfac = svc < sv ? svc / sv : 1.0f;  // exact: both are powers of two
+    sv = fminf(sv, svc);
+    stage_chunk(sk, sv);
     __syncthreads();
     if (ch + 1 < nchunks) load_chunk(k0 + kChunk);  // in flight while this chunk computes
     // scores: two 16 x 16 tiles (keys k0 .. k0 + 15, k0 + 16 .. k0 + 31); B lane (key row, dims 32 c + 8 kq ..)
@@ -704,7 +788,8 @@ extern "C" __global__ void __launch_bounds__(256, 2) halo_attn_prefill(
     bool rescale = false;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float s0 = sc[0][i] * (scale * kLog2e / (kSqk * kSqk)), s1 = sc[1][i] * (scale * kLog2e / (kSqk * kSqk));
+      const float f = scale * kLog2e / (sqc[i] * sk);
+      float s0 = sc[0][i] * f, s1 = sc[1][i] * f;
       const std::uint32_t kp0 = k0 + row, kp1 = k0 + 16 + row;
       s0 = kp0 <= qpos[i] ? s0 : -INFINITY;
       s1 = kp1 <= qpos[i] ? s1 : -INFINITY;
@@ -727,11 +812,11 @@ extern "C" __global__ void __launch_bounds__(256, 2) halo_attn_prefill(
       pwl[o1] = __builtin_bit_cast(_Float16, static_cast<std::uint16_t>(pl2 >> 16));
     }
     // the accumulators change only where some row's max moved (rare once the first chunks are in)
-    if (__any(rescale))
+    if (__any(rescale) || vfac != 1.0f)
 #pragma unroll
       for (int c = 0; c < kHd / 16; ++c)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[c][i] *= alpha[i];
+        for (int i = 0; i < 4; ++i) acc[c][i] *= alpha[i] * vfac;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -755,7 +840,7 @@ extern "C" __global__ void __launch_bounds__(256, 2) halo_attn_prefill(
     const std::uint32_t tok = 2 * wave + r / 8, g = r % 8;
     const bool live = tok < ntok;
     const std::size_t base = ((static_cast<std::size_t>(first) + min(tok, ntok - 1)) * Hq + kvh * G + g) * kHd;
-    const float inv = 1.0f / l[i] * (1.0f / (kSpp * kSvv));
+    const float inv = 1.0f / l[i] * (1.0f / (kSpp * sv));
 #pragma unroll
     for (int c = 0; c < kHd / 16; c += 2) {
       const std::uint32_t d0 = 16 * c + row, d1 = 16 * (c + 1) + row;

@@ -470,6 +470,16 @@ __device__ __forceinline__ void SplitHalves4(const float (&x)[4], H4& hi, H4& lo
   lo = __builtin_bit_cast(H4, l);
 }
 
+// The power-of-two operand scale for a group of values of absolute maximum amax: `base` (the scale that keeps small
+// values' lo halves normal) while amax * base stays below the fp16 maximum 65504, else 2^(15 - e) with amax < 2^e, so
+// every scaled value lies below 2^15. Groups within the base range keep the same scale (and bits) as a fixed one.
+__device__ __forceinline__ float SplitScale(float amax, float base) {
+  if (amax * base < 65504.0f) return base;
+  int e = 0;
+  (void)frexpf(amax, &e);
+  return ldexpf(1.0f, 15 - e);
+}
+
 __device__ __forceinline__ V4F Mfma3(const H8& ah, const H8& al, const H8& bh, const H8& bl, V4F c) {
   c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, c, 0, 0, 0);
   c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, c, 0, 0, 0);

@@ -556,6 +556,12 @@ extern "C" __global__ void __launch_bounds__(256)
   if (acc == 0x7F3A5C11) sink[0] = acc;  // keeps the loads; practically never taken
 }
 
+// grid (1), block 64: out[slot] = the device's constant wall clock (wall_clock64, halo_wall_clock_khz ticks per ms).
+// Graph nodes at the start and end of a timed region of back-to-back launches bracket it on the device itself.
+extern "C" __global__ void __launch_bounds__(64) halo_clock_stamp(std::uint64_t* __restrict__ out, std::uint32_t slot) {
+  if (threadIdx.x == 0) out[slot] = wall_clock64();
+}
+
 extern "C" __global__ void __launch_bounds__(256)
     halo_stream_copy(const int4* __restrict__ src, int4* __restrict__ dst, std::uint64_t n) {
   const std::uint64_t stride = static_cast<std::uint64_t>(gridDim.x) * blockDim.x;

@@ -26,6 +26,8 @@ struct halo_device {
   bool capturing = false;
   std::size_t captured = 0;          // launches recorded since BeginCapture
   std::vector<void*> deferred_free;  // Free() calls made while capturing, released at EndCapture
+  std::vector<std::pair<void*, std::size_t>> deferred_ranges;  // ReleaseRange() calls made while capturing
+  int ordinal = 0;                                               // the HIP device this stream belongs to
   // per-launch event timing of eager launches (halo_profile_begin / _end)
   bool profiling = false;
   struct Timed {
@@ -131,6 +133,8 @@ int halo_device_create(int backend, halo_device** out, char* err, size_t errlen)
   *out = dev;
   return 0;
 }
+
+int halo_device_ordinal(const halo_device* dev) { return dev ? dev->ordinal : -1; }
 
 void halo_device_destroy(halo_device* dev) {
   if (dev == nullptr) return;
@@ -325,6 +329,8 @@ int halo_end_capture(halo_device* dev, halo_graph* out, char* err, size_t errlen
   const hipError_t end = hipStreamEndCapture(dev->stream, &g);
   for (void* p : dev->deferred_free) (void)hipFree(p);
   dev->deferred_free.clear();
+  for (const auto& r : dev->deferred_ranges) (void)hipMemAddressFree(r.first, r.second);
+  dev->deferred_ranges.clear();
   if (!Ok(end, "hipStreamEndCapture", err, errlen)) return -1;
   hipGraphExec_t exec = nullptr;
   const bool ok = Ok(hipGraphInstantiate(&exec, g, nullptr, nullptr, 0), "hipGraphInstantiate", err, errlen);
@@ -366,6 +372,12 @@ int halo_reserve_range(halo_device* dev, size_t bytes, halo_buffer* out, char* e
 
 void halo_release_range(halo_device* dev, halo_buffer* range) {
   if (range == nullptr || range->device == nullptr) return;
+  if (dev != nullptr && dev->capturing) {
+    // no stream drain is possible mid-capture (it would invalidate the capture): the release waits for EndCapture
+    dev->deferred_ranges.emplace_back(range->device, range->bytes);
+    *range = halo_buffer{};
+    return;
+  }
   if (dev != nullptr) (void)hipStreamSynchronize(dev->stream);  // queued work may still address the range
   (void)hipMemAddressFree(range->device, range->bytes);
   if (dev != nullptr) VmmStamp(dev);
@@ -397,10 +409,11 @@ int halo_map_page(halo_device* dev, const halo_buffer* range, size_t offset, voi
   hipMemAccessDesc acc{};
   acc.location = dev->prop.location;
   acc.flags = hipMemAccessFlagsProtReadWrite;
-  const bool ok =
-      Ok(hipMemMap(at, dev->page_bytes, 0, reinterpret_cast<hipMemGenericAllocationHandle_t>(page), 0), "hipMemMap",
-         err, errlen) &&
-      Ok(hipMemSetAccess(at, dev->page_bytes, &acc, 1), "hipMemSetAccess", err, errlen);
+  if (!Ok(hipMemMap(at, dev->page_bytes, 0, reinterpret_cast<hipMemGenericAllocationHandle_t>(page), 0), "hipMemMap",
+          err, errlen))
+    return -1;
+  const bool ok = Ok(hipMemSetAccess(at, dev->page_bytes, &acc, 1), "hipMemSetAccess", err, errlen);
+  if (!ok) (void)hipMemUnmap(at, dev->page_bytes);  // a failed map leaves the range as it was
   VmmStamp(dev);
   return ok ? 0 : -1;
 }
@@ -463,6 +476,14 @@ int halo_timer_stop(halo_device* dev, float* ms, char* err, size_t errlen) {
       !Ok(hipEventSynchronize(dev->t1), "hipEventSynchronize", err, errlen))
     return -1;
   return Ok(hipEventElapsedTime(ms, dev->t0, dev->t1), "hipEventElapsedTime", err, errlen) ? 0 : -1;
+}
+
+int halo_wall_clock_khz(halo_device* dev, int* khz, char* err, size_t errlen) {
+  if (dev == nullptr || khz == nullptr) return SetErr(err, errlen, "null argument"), -1;
+  return Ok(hipDeviceGetAttribute(khz, hipDeviceAttributeWallClockRate, dev->ordinal), "hipDeviceGetAttribute", err,
+            errlen)
+             ? 0
+             : -1;
 }
 
 void* halo_device_stream(halo_device* dev) { return dev ? static_cast<void*>(dev->stream) : nullptr; }

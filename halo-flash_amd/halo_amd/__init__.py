@@ -328,6 +328,7 @@ _ERR = [C.c_char_p, _SZ]
 _SIGS = {
     "halo_device_create": (C.c_int, [C.c_int, C.POINTER(_VP)], True),
     "halo_device_destroy": (None, [_VP], False),
+    "halo_device_ordinal": (C.c_int, [_VP], False),
     "halo_alloc": (C.c_int, [_VP, _SZ, C.POINTER(Buffer)], True),
     "halo_free": (None, [_VP, C.POINTER(Buffer)], False),
     "halo_upload": (C.c_int, [_VP, C.POINTER(Buffer), _SZ, _VP, _SZ], True),
@@ -357,6 +358,7 @@ _SIGS = {
     "halo_read_global": (C.c_int, [_VP, C.c_char_p, _VP, _SZ], True),
     "halo_write_global": (C.c_int, [_VP, C.c_char_p, _VP, _SZ], True),
     "halo_timer_stop": (C.c_int, [_VP, C.POINTER(_F32)], True),
+    "halo_wall_clock_khz": (C.c_int, [_VP, C.POINTER(C.c_int)], True),
     "halo_device_stream": (_VP, [_VP], False),
     "halo_profile_begin": (C.c_int, [_VP], True),
     "halo_profile_end": (C.c_int, [_VP, _VP, _SZ], True),
@@ -616,6 +618,11 @@ class Device:
         ms = C.c_float()
         _call("halo_timer_stop", self.handle, C.byref(ms))
         return float(ms.value)
+
+    def wall_clock_khz(self) -> int:
+        khz = C.c_int()
+        _call("halo_wall_clock_khz", self.handle, C.byref(khz))
+        return int(khz.value)
 
     def profile_begin(self):
         _call("halo_profile_begin", self.handle)

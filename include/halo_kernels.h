@@ -96,6 +96,8 @@
  *       grid (ceil(T / BN), ceil(rows / BM)), block 256
  *   halo_synth_q8(qs, d, rows, cols, qstride, u64 seed, f32 sigma), halo_synth_f32(x, u64 n, u64 seed, f32 sigma)
  *                                                                                              new (synthetic data)
+ *   halo_stream_read(src, u64 n16, sink), halo_stream_copy(src, dst, u64 n16)   bandwidth yardsticks, new
+ *   halo_clock_stamp(u64* out, u32 slot)   grid (1), block 64: out[slot] = wall clock     new (timing)
  */
 #ifndef HALO_KERNELS_H_
 #define HALO_KERNELS_H_
@@ -134,6 +136,7 @@
   X(halo_gemm_q8r_wmma) X(halo_gemm_q8r_wmma_t) X(halo_gemm_q8a8_128x128) X(halo_gemm_q8a8_128x64)           \
   X(halo_gemm_q8a8_320x64) X(halo_gemm_q8a8_160x64) X(halo_gemm_q8a8_256x128)                                 \
   X(halo_synth_q8) X(halo_synth_f32) X(halo_code_object_info_copy)                                            \
+  X(halo_stream_read) X(halo_stream_copy) X(halo_clock_stamp)                                            \
   X(halo_gemv_q8r_r4_b1) X(halo_gemv_q8r_r4_b8_ps) X(halo_gemv_q8r_r2_b3_p) X(halo_gemv_q8r_r2_b5_s)              \
   X(halo_gemv_q8r_dual_b1) X(halo_gemv_q8r_dual_b8_ps)
 

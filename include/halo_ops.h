@@ -152,7 +152,8 @@ int halo_op_moe_decode(halo_engine* eng, const halo_moe_weights* w, const float*
  * this library (one per GPU, held until the process ends), located once per device on the first call. No reference
  * counterpart: for callers that cannot allocate device memory (code under stream capture, serving loops that forbid
  * hipMalloc). Layers whose halo_op_moe_workspace_bytes exceeds 512 KiB are refused with an error (the C2 layer at 16
- * tokens needs 422 KiB). Calls that overlap on one GPU (other streams or threads) race on the shared array. */
+ * tokens needs 422 KiB). Calls that overlap on one GPU (other streams or threads) race on the shared array. The array
+ * used is the one on the engine's device (halo_device_ordinal), whichever device is current in the calling thread. */
 int halo_op_moe_decode_noalloc(halo_engine* eng, const halo_moe_weights* w, const float* x, float* out,
                                uint32_t tokens, char* err, size_t errlen);
 /* The same layer with the FFN input norm folded into the router launch (the reference's post-attention
@@ -202,8 +203,9 @@ typedef struct halo_paged_kv {
 
 /* Arithmetic: one session runs fp32 dot products; two or more sessions (and the prefill below) run the products on
  * split-fp16 matrix cores (each operand as hi + lo halves after a power-of-two scaling: q, k and V by 2^8, the
- * probabilities by 2^14), within 2^-22 of each product for operands of magnitude about 1e-4 to 255; |q|, |k| or |V|
- * of 255 or more overflow the halves. */
+ * probabilities by 2^14), within 2^-22 of each product for operands of magnitude about 1e-4 to 255. A query row, K
+ * chunk or V chunk holding a magnitude of 255.875 or more takes a smaller power-of-two scale (largest value below
+ * 2^15), so no finite operand overflows; that group's small values then keep a coarser absolute precision. */
 /* Scratch for the partials of one decode attention call. */
 size_t halo_op_attn_decode_workspace_bytes(const halo_paged_kv* kv, uint32_t q_heads);
 /* o [S][Hq][d] = attention(q [S][Hq][d]) over each session's nkv positions; gate [S][Hq][d] or NULL. Two launches. */

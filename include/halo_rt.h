@@ -59,6 +59,9 @@ enum { HALO_BACKEND_HIP = 0 };
 /* Device::Create (src/rt/device.hpp:80). Uses HIP device 0 and one non-blocking stream. */
 int halo_device_create(int backend, halo_device** out, char* err, size_t errlen);
 void halo_device_destroy(halo_device* dev);
+/* The HIP device ordinal the device's stream belongs to (no counterpart in the reference, whose Device hides it);
+ * -1 for a null device. Code that resolves per-device addresses (hipGetSymbolAddress) selects this device first. */
+int halo_device_ordinal(const halo_device* dev);
 
 /* Device::Alloc / Free (src/rt/device.hpp:83-84). */
 int halo_alloc(halo_device* dev, size_t bytes, halo_buffer* out, char* err, size_t errlen);
@@ -89,7 +92,8 @@ size_t halo_available_bytes(halo_device* dev);
  * mapped into it; one page may be mapped into several ranges (offsets multiples of halo_page_bytes) and is read
  * and written through any of them. Unmapping and releasing a range drain the device stream first; the first launch
  * or copy after a mapping change waits out a 1 ms settle interval (as the reference's HIP backend does). Not
- * capturable. */
+ * capturable: map / unmap refuse during capture, and a range released during capture is freed at halo_end_capture.
+ * A map whose access grant fails is undone (the range is left unmapped at that offset). */
 size_t halo_page_bytes(halo_device* dev);
 int halo_reserve_range(halo_device* dev, size_t bytes, halo_buffer* out, char* err, size_t errlen);
 void halo_release_range(halo_device* dev, halo_buffer* range);
@@ -127,6 +131,9 @@ void halo_free_graph(halo_device* dev, halo_graph* graph);
  * halo_timer_stop records another, waits for it and returns the elapsed milliseconds. */
 int halo_timer_start(halo_device* dev, char* err, size_t errlen);
 int halo_timer_stop(halo_device* dev, float* ms, char* err, size_t errlen);
+/* Frequency of the device's constant wall clock (the counter kernels read with wall_clock64, e.g. halo_clock_stamp),
+ * in kHz. No counterpart in the reference. */
+int halo_wall_clock_khz(halo_device* dev, int* khz, char* err, size_t errlen);
 
 /* The raw HIP stream (hipStream_t) of the device, for callers that interoperate with other HIP code. */
 void* halo_device_stream(halo_device* dev);

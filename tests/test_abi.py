@@ -90,3 +90,29 @@ def test_device_layer_refuses_null_handles():
     assert L.halo_read_global(None, b"x", None, 4, err, 256) == -1
     assert L.halo_launch_graph(None, None, err, 256) == -1
     assert L.halo_page_bytes(None) == 0
+
+
+def test_moe_noalloc_refusals_on_the_host():
+    """halo_op_moe_decode_noalloc refuses, before touching any device, a workspace above its fixed scratch and a
+    missing engine (whose device selects which GPU's scratch array is used); the device ordinal of a null device is
+    -1. Tensor pointers are placeholders that are never dereferenced."""
+    import ctypes
+
+    L = H.lib()
+    err = ctypes.create_string_buffer(256)
+    w = H.MoeWeights()
+    E, k, Hd, F = 1024, 15, 4096, 512  # within the decode limits; 16 tokens need more than the 512 KiB scratch
+    fake = 1 << 40
+    w.router = fake
+    for name, rows, cols in (("gate", E * F, Hd), ("up", E * F, Hd), ("down", E * Hd, F)):
+        m = getattr(w, name)
+        m.qs, m.d, m.rows, m.cols, m.qstride = fake, fake, rows, cols, cols
+    w.n_experts, w.n_used, w.hidden, w.ff = E, k, Hd, F
+    assert L.halo_op_moe_workspace_bytes(ctypes.byref(w), 16) > (512 << 10)
+    rc = L.halo_op_moe_decode_noalloc(None, ctypes.byref(w), fake, fake, 16, err, 256)
+    assert rc == -1 and b"fixed scratch" in err.value, err.value
+    rc = L.halo_op_moe_decode_noalloc(None, ctypes.byref(w), fake, fake, 1, err, 256)
+    assert rc == -1 and b"null engine" in err.value, err.value
+    rc = L.halo_op_moe_decode_noalloc(None, ctypes.byref(w), None, fake, 1, err, 256)
+    assert rc == -1 and b"null" in err.value, err.value
+    assert L.halo_device_ordinal(None) == -1

@@ -17,7 +17,7 @@ pytestmark = pytest.mark.gpu
 D, PAGE = 256, 16
 
 
-def build(dev, rng, S, Hkv, prefix, suffixes, max_context, kscale=1.0, vscale=1.0):
+def build(dev, rng, S, Hkv, prefix, suffixes, max_context, kscale=1.0, vscale=1.0, tweak=None):
     max_pages = -(-max_context // PAGE)
     n_prefix_pages = prefix // PAGE
     total = n_prefix_pages + S * (max_pages - n_prefix_pages)
@@ -32,6 +32,8 @@ def build(dev, rng, S, Hkv, prefix, suffixes, max_context, kscale=1.0, vscale=1.
     kp = (kscale * rng.normal(0, 1, (total, Hkv, PAGE, D))).astype(np.float32)
     vp = (vscale * rng.normal(0, 1, (total, Hkv, PAGE, D))).astype(np.float32)
     nkv = np.array([prefix + x for x in suffixes], np.uint32)
+    if tweak is not None:
+        tweak(kp, vp, pages)
     g = dict(k=dev.to_device(kp), v=dev.to_device(vp), pages=dev.to_device(pages), nkv=dev.to_device(nkv))
     desc = H.PagedKV(g["k"].ptr, g["v"].ptr, g["pages"].ptr, g["nkv"].ptr, S, Hkv, D, max_pages, prefix, max_context)
     return desc, g, kp, vp, pages, nkv
@@ -81,11 +83,39 @@ def test_attn_decode_operand_magnitudes(dev, S, qk, v):
     decode_case(dev, S, 128, [40] * S, 256, qk, v, abs_tol=0.0)
 
 
-def decode_case(dev, S, prefix, suffixes, max_context, qk=1.0, v=1.0, abs_tol=1e-6):
+def outlier_kv(kp, vp, pages=None, v_pages=None):
+    """Outlier channels: K channel 9 ~ N(0, 400) (met by a q channel of 0.005), K channel 7 by 0.005 (met by a q
+    channel of 700), V channel 5 ~ N(0, 5000) on every page or only on the physical pages v_pages."""
+    kp[..., 9] *= 400.0
+    kp[..., 7] *= 0.005
+    if v_pages is None:
+        vp[..., 5] *= 5000.0
+    else:
+        for pg in v_pages:
+            vp[pg, ..., 5] *= 5000.0
+
+
+def outlier_q(q):
+    q[..., 7] *= 700.0
+    q[..., 9] *= 0.005
+
+
+@pytest.mark.parametrize("S", [1, 4])
+def test_attn_decode_outlier_channels(dev, S):
+    """|q|, |K| and |V| far above 255 in single channels (scores stay moderate): the split-fp16 partials (S = 4) pick
+    smaller power-of-two scales for those query rows and chunks instead of overflowing fp16; same 1e-5 bar."""
+    decode_case(dev, S, 128, [40] * S, 256, outliers=True)
+
+
+def decode_case(dev, S, prefix, suffixes, max_context, qk=1.0, v=1.0, abs_tol=1e-6, outliers=False):
     Hq, Hkv = 16, 2
     rng = np.random.default_rng(S + prefix)
-    desc, g, kp, vp, pages, nkv = build(dev, rng, S, Hkv, prefix, suffixes, max_context, qk, v)
+    desc, g, kp, vp, pages, nkv = build(dev, rng, S, Hkv, prefix, suffixes, max_context, qk, v,
+                                        tweak=(lambda k_, v_, p_: outlier_kv(k_, v_)) if outliers else None)
     q = (qk * rng.normal(0, 1, (S, Hq, D))).astype(np.float32)
+    if outliers:
+        outlier_q(q)
+        assert np.abs(q).max() > 256 and np.abs(kp).max() > 256 and np.abs(vp).max() > 256
     gate = rng.normal(0, 1, (S, Hq, D)).astype(np.float32)
     gq, gg, go = dev.to_device(q), dev.to_device(gate), dev.array((S, Hq, D), np.float32)
     nbytes = H.lib().halo_op_attn_decode_workspace_bytes(ctypes.byref(desc), Hq)
@@ -93,6 +123,7 @@ def decode_case(dev, S, prefix, suffixes, max_context, qk=1.0, v=1.0, abs_tol=1e
     ws = dev.array(nbytes, np.uint8)
     dev.op("attn_decode", ctypes.byref(desc), gq.ptr, gg.ptr, go.ptr, Hq, ws.ptr, ws.nbytes)
     got = go.download()
+    assert np.isfinite(got).all()
     want, mag = oracle(q, gate, kp, vp, pages, nkv, Hkv)
     assert np.all(np.abs(got - want) <= 1e-5 * mag + abs_tol), np.max(np.abs(got - want) - 1e-5 * mag)
 

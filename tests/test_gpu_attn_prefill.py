@@ -13,7 +13,7 @@ import pytest
 
 import halo_amd as H
 import oracle_py as O
-from test_gpu_attn import build, gather
+from test_gpu_attn import build, gather, outlier_kv, outlier_q
 
 pytestmark = pytest.mark.gpu
 D = 256
@@ -36,10 +36,19 @@ def test_attn_prefill_operand_magnitudes(dev, qk, v):
     run_case(dev, 1, 0, [(0, 0, 70)], 128, qk, v, abs_tol=0.0)
 
 
-def run_case(dev, S, prefix, segs, max_context, qk=1.0, v=1.0, abs_tol=1e-6):
+def test_attn_prefill_outlier_channels(dev):
+    """|q|, |K| and |V| far above 255 in single channels, the V outliers only on the page of positions 32-47 (the
+    second 32-key chunk): query rows and K chunks take smaller power-of-two scales, and the V scale drops at that chunk
+    (the accumulators of the rows that saw the first chunk are rescaled); same 1e-5 bar, outputs finite."""
+    run_case(dev, 1, 0, [(0, 0, 90)], 128, outliers=True)
+
+
+def run_case(dev, S, prefix, segs, max_context, qk=1.0, v=1.0, abs_tol=1e-6, outliers=False):
     Hq, Hkv = 16, 2
     rng = np.random.default_rng(S + prefix + len(segs))
-    desc, g, kp, vp, pages, _ = build(dev, rng, S, Hkv, prefix, [max_context - prefix] * S, max_context, qk, v)
+    tweak = (lambda k_, v_, p_: outlier_kv(k_, v_, v_pages=[int(p_[0, 2])])) if outliers else None
+    desc, g, kp, vp, pages, _ = build(dev, rng, S, Hkv, prefix, [max_context - prefix] * S, max_context, qk, v,
+                                      tweak=tweak)
     seg_arr = (H.PrefillSegment * len(segs))()
     first = 0
     toks = []
@@ -49,6 +58,8 @@ def run_case(dev, S, prefix, segs, max_context, qk=1.0, v=1.0, abs_tol=1e-6):
         first += n
     T = len(toks)
     q = (qk * rng.normal(0, 1, (T, Hq, D))).astype(np.float32)
+    if outliers:
+        outlier_q(q)
     gate = rng.normal(0, 1, (T, Hq, D)).astype(np.float32)
     gq, gg = dev.to_device(q), dev.to_device(gate)
     go = dev.array((T, Hq, D), np.float32)
@@ -58,6 +69,7 @@ def run_case(dev, S, prefix, segs, max_context, qk=1.0, v=1.0, abs_tol=1e-6):
     dev.op("attn_prefill", ctypes.byref(desc),
            seg_arr, len(segs), gq.ptr, gg.ptr, go.ptr, goq.ptr, gos.ptr, Hq, ws.ptr, nbytes)
     got = go.download()
+    assert np.isfinite(got).all()
     o = O.oracle()
     G = Hq // Hkv
     for ti, (s, p) in enumerate(toks):

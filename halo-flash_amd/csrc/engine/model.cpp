@@ -156,9 +156,11 @@ struct Tracer {
   std::size_t cap = 0, used = 0;
   halo_model_trace_entry* entries = nullptr;
   std::uint32_t max_entries = 0, n = 0;
+  std::uint64_t mask = ~std::uint64_t{0};  // bit l: layer l (l < 63); bit 63: the final norm
 
   int Save(const char* name, std::uint32_t layer, std::uint32_t dtype, const void* src, std::size_t bytes, char* err,
            std::size_t errlen) {
+    if (!((mask >> (layer < 63 ? layer : 63)) & 1u)) return 0;
     if (bytes % 4 != 0) return SetErr(err, errlen, "trace: %s has %zu bytes (not whole words)", name, bytes), -1;
     const std::size_t at = (used + 255) / 256 * 256;
     if (at + bytes > cap || n >= max_entries)
@@ -1023,6 +1025,14 @@ int halo_model_prefill(halo_model* m, const halo_prefill_segment* segs, uint32_t
 int halo_model_prefill_trace(halo_model* m, const halo_prefill_segment* segs, uint32_t nseg, void* trace,
                              size_t trace_bytes, halo_model_trace_entry* entries, uint32_t max_entries,
                              uint32_t* n_entries, char* err, size_t errlen) {
+  return halo_model_prefill_trace_layers(m, segs, nseg, ~std::uint64_t{0}, trace, trace_bytes, entries, max_entries,
+                                         n_entries, err, errlen);
+}
+
+int halo_model_prefill_trace_layers(halo_model* m, const halo_prefill_segment* segs, uint32_t nseg,
+                                    uint64_t layer_mask, void* trace, size_t trace_bytes,
+                                    halo_model_trace_entry* entries, uint32_t max_entries, uint32_t* n_entries,
+                                    char* err, size_t errlen) {
   if (m == nullptr || segs == nullptr || trace == nullptr || entries == nullptr || n_entries == nullptr ||
       nseg == 0 || nseg > m->c.max_sessions)
     return SetErr(err, errlen, "prefill trace: null argument or bad segment count"), -1;
@@ -1037,12 +1047,15 @@ int halo_model_prefill_trace(halo_model* m, const halo_prefill_segment* segs, ui
     return SetErr(err, errlen, "prefill trace: %u tokens > one batch of %u", total, PrefillCap(m->c)), -1;
   if (m->c.shared_ff != m->c.expert_ff) return SetErr(err, errlen, "prefill trace: shared ff != expert ff"), -1;
   if (PrefillAlloc(m, err, errlen) != 0) return -1;
+  if (m->c.layers > 63 && layer_mask != ~std::uint64_t{0})
+    return SetErr(err, errlen, "prefill trace: a layer mask needs at most 63 layers"), -1;
   Tracer tr;
   tr.eng = m->eng;
   tr.base = static_cast<char*>(trace);
   tr.cap = trace_bytes;
   tr.entries = entries;
   tr.max_entries = max_entries;
+  tr.mask = layer_mask;
   std::vector<halo_prefill_segment> batch(segs, segs + nseg);
   for (auto& g : batch) g.first = 0;
   const int rc = PrefillBatch(m, batch, err, errlen, &tr);

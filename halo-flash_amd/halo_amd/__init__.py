@@ -413,6 +413,8 @@ _SIGS = {
                                         C.POINTER(_U32)], True),
     "halo_model_prefill_trace": (C.c_int, [_VP, C.POINTER(PrefillSegment), _U32, _VP, _SZ, C.POINTER(TraceEntry),
                                            _U32, C.POINTER(_U32)], True),
+    "halo_model_prefill_trace_layers": (C.c_int, [_VP, C.POINTER(PrefillSegment), _U32, _U64, _VP, _SZ,
+                                                  C.POINTER(TraceEntry), _U32, C.POINTER(_U32)], True),
     "halo_model_prefill": (C.c_int, [_VP, C.POINTER(PrefillSegment), _U32], True),
     "halo_op_moe_workspace_bytes": (_SZ, [C.POINTER(MoeWeights), _U32], False),
     "halo_op_moe_views": (C.c_int, [C.POINTER(MoeWeights), _U32, _VP, C.POINTER(MoeViews)], True),
@@ -738,12 +740,12 @@ class Model:
         """One eager step with the teacher-forcing trace: {(layer, name): host array}; layer -1 is the head."""
         return self._trace("halo_model_step_trace", (S, prefix), S)
 
-    def _trace(self, fn, args, T: int) -> dict:
+    def _trace(self, fn, args, T: int, n_layers=None) -> dict:
         cfg = self.cfg
         per_layer = T * (16 * cfg.hidden + 12 * (2 * cfg.gdn_k_heads + 3 * cfg.gdn_v_heads) * cfg.gdn_head_dim +
                          12 * 2 * cfg.q_heads * cfg.head_dim + 4 * cfg.n_experts +
                          8 * (cfg.n_used + 1) * max(cfg.expert_ff, cfg.shared_ff) + 64 * cfg.n_used + 64) + 40 * 256
-        nbytes = (cfg.layers + 1) * per_layer
+        nbytes = ((cfg.layers if n_layers is None else n_layers) + 1) * per_layer
         buf = self.dev.array(nbytes, np.uint8)
         maxe = 40 * (cfg.layers + 1)
         ents = (TraceEntry * maxe)()
@@ -760,10 +762,18 @@ class Model:
             out[(layer, e.name.decode())] = blob[e.offset: e.offset + e.bytes].view(TRACE_DTYPES[e.dtype]).copy()
         return out
 
-    def prefill_trace(self, segments) -> dict:
-        """halo_model_prefill of (session, start, length) segments (one batch) with the teacher-forcing trace."""
+    def prefill_trace(self, segments, layers=None) -> dict:
+        """halo_model_prefill of (session, start, length) segments (one batch) with the teacher-forcing trace; with
+        `layers` (layer indices, -1 for the final norm) only those layers are traced."""
         arr = (PrefillSegment * len(segments))(*[PrefillSegment(s, a, n, 0) for s, a, n in segments])
-        return self._trace("halo_model_prefill_trace", (arr, len(segments)), sum(n for _, _, n in segments))
+        T = sum(n for _, _, n in segments)
+        if layers is None:
+            return self._trace("halo_model_prefill_trace", (arr, len(segments)), T)
+        mask = 0
+        for l in layers:
+            mask |= 1 << (63 if l < 0 else l)
+        return self._trace("halo_model_prefill_trace_layers", (arr, len(segments), mask), T,
+                           n_layers=len([l for l in layers if l >= 0]))
 
     def set_sampling(self, s: int, params: "SampleParams", penalties=None):
         """Device sampling for session s; penalties = (token, generated_count, repeated) arrays sorted by token."""

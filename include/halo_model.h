@@ -124,7 +124,7 @@ int halo_model_step_trace(halo_model* m, uint32_t S, uint32_t attn_prefix, void*
                           halo_model_trace_entry* entries, uint32_t max_entries, uint32_t* n_entries, char* err,
                           size_t errlen);
 
-/* The same trace for one batched prefill call (halo_model_prefill) whose segments fit one batch (<= 2048 tokens;
+/* The same trace for one batched prefill call (halo_model_prefill) whose segments fit one batch (<= the prefill batch;
  * shared_ff == expert_ff): entries per layer for all T tokens of the batch, [T][...] in batch order: res_in, xq,
  * xs; DeltaNet qkv, z, ab, gq / gk (the conv + L2 outputs [T][Hk d]), gv [T][Hv d], g / beta [T][Hv], o (the
  * recurrence output [T][Hv d]); attention qg, k, v, aq (normalised, rotated queries [T][Hq hd]); oq, os, delta;
@@ -134,6 +134,12 @@ int halo_model_step_trace(halo_model* m, uint32_t S, uint32_t attn_prefix, void*
 int halo_model_prefill_trace(halo_model* m, const halo_prefill_segment* segs, uint32_t nseg, void* trace,
                              size_t trace_bytes, halo_model_trace_entry* entries, uint32_t max_entries,
                              uint32_t* n_entries, char* err, size_t errlen);
+/* The prefill trace restricted to some layers: bit l of layer_mask (l < 63) selects layer l's entries, bit 63 the
+ * final norm's; the prefill itself runs every layer. Lets a long batch (thousands of tokens) be traced in a few
+ * layers within device memory. Models of more than 63 layers accept only the all-ones mask. */
+int halo_model_prefill_trace_layers(halo_model* m, const halo_prefill_segment* segs, uint32_t nseg, uint64_t layer_mask,
+                                    void* trace, size_t trace_bytes, halo_model_trace_entry* entries,
+                                    uint32_t max_entries, uint32_t* n_entries, char* err, size_t errlen);
 
 /* Host copy of session s's logits of the last step ([vocab] fp32). Not capturable. */
 int halo_model_logits(halo_model* m, uint32_t s, float* out, char* err, size_t errlen);

@@ -342,6 +342,44 @@ void or_gdn_sequence(float* S, uint32_t d, uint32_t T, const float* q, size_t qs
                 o + t * ostride);
 }
 
+/* Error bar of or_gdn_sequence (no reference counterpart: the magnitude of the terms each value sums): the same
+ * recurrence over absolute values, M <- decay M; u = M |k|; M[j][i] += (|v_j| + u_j) |beta| |k_i|; o_mag[j] =
+ * (M |q|)[j] / sqrt(d). M starts at |S0| (value-major, in place); per-token o_mag rows at ostride. A computed
+ * value's rounding error is a small multiple of its magnitude, whatever order its terms are summed in. */
+void or_gdn_sequence_mag(double* M, uint32_t d, uint32_t T, const float* q, size_t qstride, const float* k,
+                         size_t kstride, const float* v, size_t vstride, const float* g, const float* beta,
+                         size_t gstride, double* omag, size_t ostride) {
+  const double q_scale = 1.0 / sqrt((double)d);
+  double* u = (double*)malloc(sizeof(double) * d);
+  for (uint32_t t = 0; t < T; ++t) {
+    const float* qt = q + t * qstride;
+    const float* kt = k + t * kstride;
+    const float* vt = v + t * vstride;
+    const double decay = exp((double)g[t * gstride]);
+    const double b = fabs((double)beta[t * gstride]);
+    for (uint32_t j = 0; j < d; ++j) {
+      double* row = M + (size_t)j * d;
+      double acc = 0.0;
+      for (uint32_t i = 0; i < d; ++i) {
+        row[i] *= decay;
+        acc += row[i] * fabs((double)kt[i]);
+      }
+      u[j] = acc;
+    }
+    for (uint32_t j = 0; j < d; ++j) {
+      const double dm = (fabs((double)vt[j]) + u[j]) * b;
+      double* row = M + (size_t)j * d;
+      double acc = 0.0;
+      for (uint32_t i = 0; i < d; ++i) {
+        row[i] += dm * fabs((double)kt[i]);
+        acc += row[i] * fabs((double)qt[i]);
+      }
+      omag[t * ostride + j] = acc * q_scale;
+    }
+  }
+  free(u);
+}
+
 /* reference: src/model/reference.cpp:492-521 (dense branch: scores in double rounded to fp32, scaled by 1/sqrt(hd),
  * max-subtracted exp, double denominator, p = score/denom in fp32, o += p * v). */
 void or_attention_head(const float* q, const float* k, const float* v, uint32_t n, uint32_t hd, size_t kv_stride,

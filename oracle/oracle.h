@@ -75,6 +75,12 @@ void or_gdn_sequence(float* S, uint32_t d, uint32_t T, const float* q, size_t qs
                      const float* v, size_t vstride, const float* g, const float* beta, size_t gstride, float* o,
                      size_t ostride);
 
+/* The magnitude of the terms behind or_gdn_sequence's values (an error bar): M [d][d] value-major, starting at
+ * |S0|, in place; omag rows [T][d] at ostride. */
+void or_gdn_sequence_mag(double* M, uint32_t d, uint32_t T, const float* q, size_t qstride, const float* k,
+                         size_t kstride, const float* v, size_t vstride, const float* g, const float* beta,
+                         size_t gstride, double* omag, size_t ostride);
+
 /* ---- GQA decode attention ------------------------------------------------ */
 /* One query head over n positions: k, v rows of length hd at stride `kv_stride` floats;
  * o = softmax(q.k / sqrt(hd)) v. */

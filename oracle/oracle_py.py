@@ -48,6 +48,7 @@ _ORACLE_SIGS = {
     "or_route_topk": (None, [_PF, _U32, _U32, _PU32, _PF]),
     "or_gdn_step": (None, [_PF, _U32, _PF, _PF, _PF, _F32, _F32, _PF]),
     "or_gdn_sequence": (None, [_PF, _U32, _U32, _VP, _SZ, _VP, _SZ, _VP, _SZ, _VP, _VP, _SZ, _VP, _SZ]),
+    "or_gdn_sequence_mag": (None, [_VP, _U32, _U32, _VP, _SZ, _VP, _SZ, _VP, _SZ, _VP, _VP, _SZ, _VP, _SZ]),
     "or_attention_head": (None, [_PF, _PF, _PF, _U32, _U32, _SZ, _PF]),
     "or_next_random": (_U64, [C.POINTER(C.c_uint64)]),
     "or_sample": (_U32, [_PF, _U32, _F32, C.c_int32, _F32, _F32, _U32, _F32, _F32, _F32, _VP, _VP, _VP, _U32,

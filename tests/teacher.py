@@ -139,10 +139,13 @@ class LayerChecker:
             return qs[e * rows:(e + 1) * rows], d[e * rows:(e + 1) * rows]
         return self.m.tensor_rows(l, name, e * rows, rows)
 
-    def snapshot(self, S):
-        """The GPU's recurrent state before a step: per layer DeltaNet state / conv ring, or the KV pools."""
+    def snapshot(self, S, layers=None):
+        """The GPU's recurrent state before a step: per layer DeltaNet state / conv ring, or the KV pools (all layers,
+        or those in `layers`)."""
         snap = {"nkv": self.m.raw(-1, "nkv", np.uint32)[0, :S].copy(), "pages": self.m.raw(-1, "pages", np.uint32)}
         for l in range(self.c.layers):
+            if layers is not None and l not in layers:
+                continue
             if self.attn[l]:
                 snap[(l, "k_pool")] = self.m.raw(l, "k_pool")
                 snap[(l, "v_pool")] = self.m.raw(l, "v_pool")
@@ -159,8 +162,14 @@ class LayerChecker:
         xq = tr[(l, "xq")].reshape(S, H)
         xs = tr[(l, "xs")].reshape(S, H // 32)
         for s in range(S):
-            self.report.codes_match(f"norm codes@L{l}s{s}", xq[s], xs[s], _rmsnorm(res[s], norm_w, c.rms_eps))
+            if self._do(s):
+                self.report.codes_match(f"norm codes@L{l}s{s}", xq[s], xs[s], _rmsnorm(res[s], norm_w, c.rms_eps))
         return res, xq, xs
+
+    sample = None  # batch rows whose per-token stages a prefill check covers (None: all)
+
+    def _do(self, t):
+        return self.sample is None or t in self.sample
 
     def _deltanet(self, l, tr, S, snap, after):
         c, r = self.c, self.report
@@ -364,23 +373,32 @@ class PrefillChecker(LayerChecker):
     the GPU's state before it and the GPU's per-token q / k / v / decay / beta (the chunked WY form on the GPU sums in
     another order, so its outputs are held to 1e-5 of the terms' magnitudes carried through the recurrence)."""
 
-    def check_prefill(self, segments, prompts):
-        """segments: (session, start, length) in batch order; prompts[s]: session s's prompt (host tokens)."""
+    def check_prefill(self, segments, prompts, layers=None, sample=None):
+        """segments: (session, start, length) in batch order; prompts[s]: session s's prompt (host tokens).
+        layers: the layer indices to trace and check (-1: the final norm and LM head; None: all). sample: the batch
+        rows whose per-token stages are checked (None: all); the DeltaNet recurrence still runs over every token (the
+        state after the batch is checked whole), and whole-batch checks (pair positions, h codes) cover every row."""
         c = self.c
         S = max(s for s, _, _ in segments) + 1
-        snap = self.snapshot(S)
-        tr = self.m.prefill_trace(segments)
-        after = self.snapshot(S)
+        self.sample = None if sample is None else set(int(t) for t in sample)
+        sel = list(range(c.layers)) + [-1] if layers is None else sorted(set(layers))
+        snap = self.snapshot(S, layers=None if layers is None else set(sel))
+        tr = self.m.prefill_trace(segments, layers=None if layers is None else sel)
+        after = self.snapshot(S, layers=None if layers is None else set(sel))
+        self.after = after
         rows = []  # (session, position) of every batch row
         for s, a, n in segments:
             rows += [(s, a + j) for j in range(n)]
         T = len(rows)
-        emb_q, emb_d = self._w(-1, "embd")
-        want = np.stack([_f16(emb_d[int(prompts[s][p])]).repeat(32) * emb_q[int(prompts[s][p])].astype(np.float32)
-                         for s, p in rows])
-        assert np.array_equal(tr[(0, "res_in")].reshape(T, -1), want.astype(np.float32)), "embedding"
+        if 0 in sel:
+            emb_q, emb_d = self._w(-1, "embd")
+            want = np.stack([_f16(emb_d[int(prompts[s][p])]).repeat(32) * emb_q[int(prompts[s][p])].astype(np.float32)
+                             for s, p in rows])
+            assert np.array_equal(tr[(0, "res_in")].reshape(T, -1), want.astype(np.float32)), "embedding"
         for l in range(c.layers):
-            if l > 0:
+            if l not in sel:
+                continue
+            if l > 0 and l - 1 in sel:
                 prev = tr[(l - 1, "mres")].reshape(T, -1) + tr[(l - 1, "mout")].reshape(T, -1)
                 assert np.array_equal(tr[(l, "res_in")].reshape(T, -1), prev.astype(np.float32)), f"residual L{l}"
             if self.attn[l]:
@@ -388,11 +406,14 @@ class PrefillChecker(LayerChecker):
             else:
                 self._deltanet_prefill(l, tr, T, segments, snap, after)
             self._moe_prefill(l, tr, T)
+        if -1 not in sel:
+            return
         # final norm and the LM head on each segment's last token
         H = c.hidden
         res = tr[(-1, "res_in")].reshape(T, H)
-        lres = tr[(c.layers - 1, "mres")].reshape(T, H) + tr[(c.layers - 1, "mout")].reshape(T, H)
-        assert np.array_equal(res, lres.astype(np.float32)), "final residual add"
+        if c.layers - 1 in sel:
+            lres = tr[(c.layers - 1, "mres")].reshape(T, H) + tr[(c.layers - 1, "mout")].reshape(T, H)
+            assert np.array_equal(res, lres.astype(np.float32)), "final residual add"
         xq, xs = tr[(-1, "xq")].reshape(T, H), tr[(-1, "xs")].reshape(T, H // 32)
         head = self._w(-1, "head")
         on = self.m.tensor(-1, "out_norm")[0]
@@ -416,9 +437,10 @@ class PrefillChecker(LayerChecker):
         _, xq, xs = self._input(l, tr, T, self._w(l, "attn_norm")[0])
         qkv, z, ab = tr[(l, "qkv")].reshape(T, C), tr[(l, "z")].reshape(T, Dv), tr[(l, "ab")].reshape(T, 2 * Hv)
         for t in range(T):
-            gemv(r, f"qkv@L{l}t{t}", self._w(l, "qkv"), xq[t], xs[t], qkv[t])
-            gemv(r, f"z@L{l}t{t}", self._w(l, "z"), xq[t], xs[t], z[t])
-            gemv(r, f"ab@L{l}t{t}", self._w(l, "ab"), xq[t], xs[t], ab[t])
+            if self._do(t):
+                gemv(r, f"qkv@L{l}t{t}", self._w(l, "qkv"), xq[t], xs[t], qkv[t])
+                gemv(r, f"z@L{l}t{t}", self._w(l, "z"), xq[t], xs[t], z[t])
+                gemv(r, f"ab@L{l}t{t}", self._w(l, "ab"), xq[t], xs[t], ab[t])
         gq, gk = tr[(l, "gq")].reshape(T, Dk), tr[(l, "gk")].reshape(T, Dk)
         gv = tr[(l, "gv")].reshape(T, Dv)
         gg, gb = tr[(l, "g")].reshape(T, Hv), tr[(l, "beta")].reshape(T, Hv)
@@ -473,6 +495,8 @@ class PrefillChecker(LayerChecker):
                     oh = gdn_head(Sv[h], qh, kv_, vh, gg[t, h], gb[t, h])
                     r.close(f"recurrence o@L{l}t{t}", go[t, h * d:(h + 1) * d], oh,
                             (Sm[h] @ np.abs(qh)) / np.sqrt(d))
+                if not self._do(t):
+                    continue
                 # gated output norm from the GPU's o
                 on = np.concatenate([gated_head_norm(go[t, h * d:(h + 1) * d], nw, z[t, h * d:(h + 1) * d],
                                                      c.rms_eps) for h in range(Hv)])
@@ -499,6 +523,8 @@ class PrefillChecker(LayerChecker):
         pages = snap["pages"]
         qn, kn = self._w(l, "q_norm")[0], self._w(l, "k_norm")[0]
         for t, (s, p) in enumerate(rows):
+            if not self._do(t):
+                continue
             gemv(r, f"qg@L{l}t{t}", self._w(l, "qg"), xq[t], xs[t], qg[t])
             gemv(r, f"k@L{l}t{t}", self._w(l, "k"), xq[t], xs[t], kk[t])
             gemv(r, f"v@L{l}t{t}", self._w(l, "v"), xq[t], xs[t], vv[t])
@@ -546,6 +572,8 @@ class PrefillChecker(LayerChecker):
         assert np.array_equal(hq, wq) and hs.tobytes() == wsc.tobytes(), f"h codes L{l}"
         R, sg = self._w(l, "router"), self._w(l, "shared_gate")[0]
         for t in range(T):
+            if not self._do(t):
+                continue
             xn = _rmsnorm(mres[t], fnw, c.rms_eps)
             r.codes_match(f"moe input codes@L{l}t{t}", xq[t], xs[t], xn)
             x64 = xn.astype(np.float64)

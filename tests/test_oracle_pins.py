@@ -286,6 +286,46 @@ def test_gdn_step_invariants():
     assert np.allclose(S3, Sw, atol=1e-5) and np.allclose(out, ow, atol=1e-5)
 
 
+def test_gdn_sequence_mag_closed_form_and_bound():
+    """The DeltaNet error bar: from a zero state one token gives M = |beta| |v| |k|^T and o_mag = |beta| |v| (|k| .
+    |q|) / sqrt(d); with all inputs non-negative and a non-negative state (no cancellation) the bar equals |o| and
+    |S| exactly (up to fp32 rounding of the value path); over random signed sequences it bounds |o| and |S|."""
+    o = O.oracle()
+    rng = np.random.default_rng(21)
+    d, T = 16, 9
+    q = rng.normal(0, 1, (T, d)).astype(np.float32)
+    k = rng.normal(0, 1, (T, d)).astype(np.float32)
+    v = rng.normal(0, 1, (T, d)).astype(np.float32)
+    g = rng.normal(-0.3, 0.2, T).astype(np.float32)
+    b = rng.uniform(0.1, 0.9, T).astype(np.float32)
+    M = np.zeros((d, d), np.float64)
+    om = np.zeros((T, d), np.float64)
+    o.or_gdn_sequence_mag(M.ctypes.data, d, 1, q.ctypes.data, d, k.ctypes.data, d, v.ctypes.data, d, g.ctypes.data,
+                          b.ctypes.data, 1, om.ctypes.data, d)
+    v64, k64, q64, b64 = (x.astype(np.float64) for x in (v[0], k[0], q[0], b[0]))
+    assert np.allclose(M, b64 * np.outer(np.abs(v64), np.abs(k64)), rtol=1e-12)
+    assert np.allclose(om[0], b64 * np.abs(v64) * (np.abs(k64) @ np.abs(q64)) / np.sqrt(d), rtol=1e-12)
+    # signed sequence: a bound on the values
+    S0 = rng.normal(0, 0.5, (d, d)).astype(np.float32)
+    S = S0.copy()
+    M = np.abs(S0).astype(np.float64)
+    out = np.zeros((T, d), np.float32)
+    o.or_gdn_sequence(S, d, T, q.ctypes.data, d, k.ctypes.data, d, v.ctypes.data, d, g.ctypes.data, b.ctypes.data, 1,
+                      out.ctypes.data, d)
+    o.or_gdn_sequence_mag(M.ctypes.data, d, T, q.ctypes.data, d, k.ctypes.data, d, v.ctypes.data, d, g.ctypes.data,
+                          b.ctypes.data, 1, om.ctypes.data, d)
+    assert np.all(np.abs(out) <= om * (1 + 1e-5)) and np.all(np.abs(S) <= M * (1 + 1e-5))
+    # no cancellation (q, k >= 0, v >= 0, S0 >= 0, and decay S k never exceeds v: beta small, state small): equal
+    qp, kp, vp = np.abs(q), np.abs(k) * 0.01, np.abs(v) + 5.0
+    S = np.zeros((d, d), np.float32)
+    M = np.zeros((d, d), np.float64)
+    o.or_gdn_sequence(S, d, 1, qp.ctypes.data, d, kp.ctypes.data, d, vp.ctypes.data, d, g.ctypes.data,
+                      b.ctypes.data, 1, out.ctypes.data, d)
+    o.or_gdn_sequence_mag(M.ctypes.data, d, 1, qp.ctypes.data, d, kp.ctypes.data, d, vp.ctypes.data, d,
+                          g.ctypes.data, b.ctypes.data, 1, om.ctypes.data, d)
+    assert np.allclose(S, M, rtol=1e-6) and np.allclose(out[0], om[0], rtol=1e-6)
+
+
 def test_attention_head_closed_forms():
     o = O.oracle()
     rng = np.random.default_rng(13)

@@ -2,6 +2,7 @@
 #include "q8.hip"
 #include "moe.hip"
 #include "gdn.hip"
+#include "gdn_ref.hip"
 #include "attn.hip"
 #include "model.hip"
 #include "proj.hip"

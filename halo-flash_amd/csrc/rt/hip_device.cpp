@@ -228,6 +228,15 @@ size_t halo_available_bytes(halo_device* dev) {
   return free_b;
 }
 
+int halo_code_object_mach(const uint8_t* code, size_t bytes) {
+  // ELF64 little-endian header: magic, class 2, data 1; e_machine (offset 18) EM_AMDGPU = 224; e_flags at 48
+  if (code == nullptr || bytes < 64 || std::memcmp(code, "\x7f" "ELF", 4) != 0 || code[4] != 2 || code[5] != 1)
+    return -1;
+  const unsigned machine = code[18] | (code[19] << 8);
+  if (machine != 224) return -1;
+  return code[48];
+}
+
 int halo_load_module(halo_device* dev, const uint8_t* code, size_t bytes, char* err, size_t errlen) {
   if (dev == nullptr || code == nullptr || bytes == 0) return SetErr(err, errlen, "empty code object"), -1;
   if (dev->module) return SetErr(err, errlen, "a module is already loaded"), -1;

@@ -340,6 +340,7 @@ _SIGS = {
     "halo_available_bytes": (_SZ, [_VP], False),
     "halo_core_code_object": (C.POINTER(C.c_uint8), [C.POINTER(_SZ)], False),
     "halo_load_module": (C.c_int, [_VP, _VP, _SZ], True),
+    "halo_code_object_mach": (C.c_int, [_VP, _SZ], False),
     "halo_kernel": (_I32, [_VP, C.c_char_p], True),
     "halo_launch": (C.c_int, [_VP, _I32, Dim3, Dim3, C.POINTER(Arg), _SZ], True),
     "halo_synchronize": (C.c_int, [_VP], True),

@@ -1,8 +1,8 @@
 // The reference-side device adapter: an rt::Device (reference src/rt/device.hpp:77-137) that forwards every member
 // to this library's C ABI (include/halo_rt.h). A maintainer adds this file to the reference as
 // src/rt/amd_device.cpp, gives Device::Create (src/rt/device.cpp) a branch that calls CreateAmdDevice, and links
-// -lhalo_flash_amd; FlashNextGpu::Init's LoadModule(kernels::CoreHsaco()) (src/engine/flash_next_gpu.cpp:273) then
-// loads halo_core_code_object() instead. tests/test_integration_adapter.py compiles it against the reference's
+// -lhalo_flash_amd. FlashNextGpu::Init's LoadModule(kernels::CoreHsaco()) (src/engine/flash_next_gpu.cpp:273) needs no
+// edit: handed a code object for another target, LoadModule loads halo_core_code_object() instead. tests/test_integration_adapter.py compiles it against the reference's
 // device.hpp.
 #include <cstring>
 #include <memory>
@@ -104,7 +104,12 @@ class AmdDevice final : public Device {
 
   bool LoadModule(std::span<const std::uint8_t> code, std::string* error) override {
     char e[kErr];
-    return Check(halo_load_module(d_, code.data(), code.size(), e, kErr), e, error);
+    const std::uint8_t* data = code.data();
+    std::size_t bytes = code.size();
+    // another target's code object (the engine's gfx1151 CoreHsaco): the library's own gfx950 object, which holds
+    // the same kernel names and parameter lists, is loaded instead
+    if (halo_code_object_mach(data, bytes) != HALO_MACH_GFX950) data = halo_core_code_object(&bytes);
+    return Check(halo_load_module(d_, data, bytes, e, kErr), e, error);
   }
   KernelId Kernel(std::string_view name, std::string* error) override {
     char e[kErr];

@@ -75,6 +75,14 @@
  *     tokens) grid (ceil(T / 64), ceil(rows / 64)); halo_gemm_f32_rows(w, x, y, rows, cols) grid (ceil(rows / 8), T);
  *     halo_gemm_f32_narrow(same) grid (ceil(rows / 256), T), cols <= 8192; halo_gemm_f32_skinny(w, x, y, rows, cols,
  *     tokens) grid (ceil(T / 8)), rows <= 16; all block 256
+ *   reference-named fp32 DeltaNet prefill of one sequence (core.hip:5925, 6053, 6111; prefill_chunk.cpp:604-645),
+ *   same parameters and grids, chunked (16 tokens) on fp32 matrix cores:
+ *     halo_gdn_prefill_split(q, k, v, alpha, beta, a, dt, state, out, num_k_heads, tokens, qk_stride, v_stride,
+ *       o_stride)                                                       grid (2, heads), block 256
+ *     halo_gdn_chunk_prep(q, k, alpha, beta, a, dt, prep, num_k_heads, tokens, qk_stride)
+ *       grid (ceil(tokens / 16), heads), block 256; prep [heads][chunks][544] floats (the engine allocates 576)
+ *     halo_gdn_chunk_scan(q, k, v, prep, state, out, num_k_heads, tokens, qk_stride, v_stride, o_stride)
+ *                                                                       grid (2, heads), block 256
  *   halo_shexp_down_add(dq, dd, hin, sgate, out, rows, cols, qstride)  grid ceil(rows / 32)       core.hip:2938
  *   halo_router_topk_w_y(logits, ids, weights, n, k, lstride)          grid (1, B)       batch_decode.hip:1157
  *   halo_attention_select_b_y(q, tab, tstride, kslot, gate, visible, out, scores, params, num_heads, num_kv_heads,
@@ -136,7 +144,8 @@
   X(halo_gemm_q8r_wmma) X(halo_gemm_q8r_wmma_t) X(halo_gemm_q8a8_128x128) X(halo_gemm_q8a8_128x64)           \
   X(halo_gemm_q8a8_320x64) X(halo_gemm_q8a8_160x64) X(halo_gemm_q8a8_256x128)                                 \
   X(halo_synth_q8) X(halo_synth_f32) X(halo_code_object_info_copy)                                            \
-  X(halo_stream_read) X(halo_stream_copy) X(halo_clock_stamp)                                            \
+  X(halo_stream_read) X(halo_stream_copy) X(halo_clock_stamp)                                                 \
+  X(halo_gdn_prefill_split) X(halo_gdn_chunk_prep) X(halo_gdn_chunk_scan)                                            \
   X(halo_gemv_q8r_r4_b1) X(halo_gemv_q8r_r4_b8_ps) X(halo_gemv_q8r_r2_b3_p) X(halo_gemv_q8r_r2_b5_s)              \
   X(halo_gemv_q8r_dual_b1) X(halo_gemv_q8r_dual_b8_ps)
 

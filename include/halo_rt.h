@@ -109,6 +109,11 @@ int halo_write_global(halo_device* dev, const char* name, const void* src, size_
 
 /* kernels::CoreHsaco() (reference CMakeLists.txt:143-179): the embedded gfx950 code object. */
 const uint8_t* halo_core_code_object(size_t* bytes);
+/* The processor a code object targets: EF_AMDGPU_MACH of an AMDGPU ELF64 object (e_flags & 0xff; gfx950 is
+ * HALO_MACH_GFX950), -1 when the bytes are not one. Lets a loader that is handed another target's code object (the
+ * reference engine passes its gfx1151 CoreHsaco) load the embedded one instead. No counterpart in the reference. */
+enum { HALO_MACH_GFX950 = 0x4f };
+int halo_code_object_mach(const uint8_t* code, size_t bytes);
 
 /* Device::LoadModule / Kernel (src/rt/device.hpp:120-121). */
 int halo_load_module(halo_device* dev, const uint8_t* code, size_t bytes, char* err, size_t errlen);

@@ -116,3 +116,21 @@ def test_moe_noalloc_refusals_on_the_host():
     rc = L.halo_op_moe_decode_noalloc(None, ctypes.byref(w), None, fake, 1, err, 256)
     assert rc == -1 and b"null" in err.value, err.value
     assert L.halo_device_ordinal(None) == -1
+
+
+def test_code_object_mach():
+    """The embedded object is recognised as gfx950; another AMDGPU target's ELF header reports its own processor
+    (the adapter then loads the embedded object instead); bytes that are no AMDGPU ELF64 give -1."""
+    import ctypes
+
+    L = H.lib()
+    co = _code_object()
+    assert L.halo_code_object_mach(co, len(co)) == 0x4F
+    other = bytearray(co[:64])
+    other[48] = 0x4A  # another processor's EF_AMDGPU_MACH
+    assert L.halo_code_object_mach(bytes(other), 64) == 0x4A
+    x86 = bytearray(co[:64])
+    x86[18], x86[19] = 62, 0  # EM_X86_64
+    assert L.halo_code_object_mach(bytes(x86), 64) == -1
+    assert L.halo_code_object_mach(b"not an elf" * 8, 80) == -1
+    assert L.halo_code_object_mach(None, 0) == -1

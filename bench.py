@@ -78,6 +78,8 @@ def run_gpu(args):
             return run_pgemm(args, dev, H, res)
         if args.mode == "sample":
             return run_sample(args, dev, H, res)
+        if args.mode == "c1":
+            return run_c1(args, dev, H, res)
         run_c0(args, dev, H, res)
         if not args.quick:
             roof = res["roofline"]
@@ -115,11 +117,24 @@ def run_c1(args, dev, H, res):
     in_x = H.ProjInput(x=x.ptr, mode=H.PROJ_F)
     in_a = H.ProjInput(x=a.ptr, mode=H.PROJ_F)
 
-    def c1_pass(ws, m, fused=True):
-        if fused and m <= 8:
+    in_xq = H.ProjInput(xq=xq.ptr, xs=xs.ptr, mode=H.PROJ_Q)
+    in_aq = H.ProjInput(xq=aq.ptr, xs=as_.ptr, mode=H.PROJ_Q)
+
+    def c1_pass(ws, m, fused=True, mfma=False):
+        if fused and m == 1:
             # one launch per input row set: quantize prologue + (q|gate, kv), then quantize prologue + o
             H.proj_q8(dev, ws[:2], [yqg, ykv], in_x, m)
             H.proj_q8(dev, ws[2:], [yo], in_a, m)
+            return
+        if fused:
+            # as the model's batched step runs them: one quantize launch per input row set, then the grouped
+            # projection on the quantized rows (v_dot4 up to 8 tokens, int8 matrix cores beyond; `mfma`: the matrix
+            # cores at any token count)
+            t = (2, 2) if mfma else (0, 0)
+            dev.op("quantize_q8", x.ptr, xq.ptr, xs.ptr, m, 2048)
+            H.proj_q8(dev, ws[:2], [yqg, ykv], in_xq, m, *t)
+            dev.op("quantize_q8", a.ptr, aq.ptr, as_.ptr, m, 4096)
+            H.proj_q8(dev, ws[2:], [yo], in_aq, m, *t)
             return
         dev.op("quantize_q8", x.ptr, xq.ptr, xs.ptr, m, 2048)
         dev.op("matvec_q8a8", ctypes.byref(ws[0].desc), xq.ptr, xs.ptr, yqg.ptr, m, 4096)
@@ -147,10 +162,10 @@ def run_c1(args, dev, H, res):
         res["c1"] = None
         return res
 
-    def graph_for(m, fused=True):
+    def graph_for(m, fused=True, mfma=False):
         dev.begin_capture()
         for ws in sets:
-            c1_pass(ws, m, fused)
+            c1_pass(ws, m, fused, mfma)
         return dev.end_capture()
 
     sweep = {}
@@ -165,23 +180,26 @@ def run_c1(args, dev, H, res):
     sweep["1_unfused"] = {"us_per_pass": round(ms / (nrep * copies) * 1e3, 3),
                           "GBps": round(c1_pass_bytes(1) / (ms / (nrep * copies) * 1e-3) / 1e9, 1)}
     dev.free_graph(g)
-    for m in (1, 2, 4, 8, 16):
-        g = graph_for(m)
-        reps = 1 if m > 1 else max(1, args.warmup // copies)
+    for m in (1, 2, 3, 4, 8, 16, "2_mfma", "4_mfma", "8_mfma"):
+        g = graph_for(int(str(m).split("_")[0]), mfma=isinstance(m, str))
+        reps = 1 if m != 1 else max(1, args.warmup // copies)
         for _ in range(reps):
             dev.launch_graph(g)
         dev.sync()
-        nrep = max(1, -(-(2000 if m == 1 else 200) // copies))
+        nrep = max(1, -(-(2000 if m == 1 else 400) // copies))
         dev.timer_start()
         for _ in range(nrep):
             dev.launch_graph(g)
         ms = dev.timer_stop()
         steps = nrep * copies
+        mi = int(str(m).split("_")[0])
         sweep[str(m)] = {"us_per_pass": round(ms / steps * 1e3, 3),
-                         "GBps": round(c1_pass_bytes(m) / (ms / steps * 1e-3) / 1e9, 1)}
+                         "GBps": round(c1_pass_bytes(mi) / (ms / steps * 1e-3) / 1e9, 1)}
         dev.free_graph(g)
-    res["c1"] = {"workload": "C1 Q8_0 projections 2048->4096, 2048->512, 4096->2048, fp32 activations "
-                             "quantized in the prologue", "bytes_per_pass_m1": c1_pass_bytes(1),
+    res["c1"] = {"workload": "C1 Q8_0 projections 2048->4096, 2048->512, 4096->2048 from fp32 activations: at M = 1 "
+                             "quantized in the projection's prologue (2 launches), from M = 2 one quantize launch per "
+                             "input then the grouped projection on the quantized rows (4 launches: v_dot4 up to 8 "
+                             "tokens, int8 matrix cores at 16); *_mfma: the matrix-core kernel at that M", "bytes_per_pass_m1": c1_pass_bytes(1),
                  "GBps_m1": sweep["1"]["GBps"], "sweep": sweep}
     log(f"[bench] C1 sweep {sweep}")
     return res
@@ -1147,7 +1165,7 @@ def main():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--quick", action="store_true", help="only the C0 headline and its roofline")
     p.add_argument("--eager", action="store_true", help="launch without graphs (for profiling kernel durations)")
-    p.add_argument("--mode", choices=["all", "c0", "membw", "moe", "gdn", "c4", "pmc", "attn", "proj", "prefill",
+    p.add_argument("--mode", choices=["all", "c0", "c1", "membw", "moe", "gdn", "c4", "pmc", "attn", "proj", "prefill",
                                        "pgemm", "sample"],
                    default="all",
                    help="c0: only the C0 GEMV loop (for profiling one kernel shape)")
@@ -1157,9 +1175,9 @@ def main():
               "(the path runs on one GPU; a sharded version is not built)", file=sys.stderr)
         sys.exit(2)
     res = run_gpu(args)
-    if args.mode in ("c0", "membw", "moe", "gdn", "c4", "pmc", "attn", "proj", "prefill", "pgemm", "sample"):
-        print(json.dumps({k: res.get(k) for k in ("roofline", "c0_tilings", "membw", "moe", "gdn", "c4", "attn", "proj",
-                                                  "prefill", "sample")}),
+    if args.mode != "all":
+        print(json.dumps({k: res.get(k) for k in ("roofline", "c0_tilings", "c1", "membw", "moe", "gdn", "c4", "attn",
+                                                  "proj", "prefill", "sample")}),
               flush=True)
         return
     line = {

@@ -160,6 +160,15 @@ int halo_op_matvec_q8a8(halo_engine* eng, const halo_q8_matrix* w, const int8_t*
                           U32(w->qstride), U32(m), U32(ystride)};
     return Launch(eng, "halo_gemm_q8a8_mfma32", D3(CeilDiv(w->rows, 128), CeilDiv(m, 128)), D3(512), a, err, errlen);
   }
+  if (m >= 9 && m <= 16 && ystride == w->rows && w->qstride == w->cols &&
+      (w->cols == 1024 || w->cols == 2048 || w->cols == 4096)) {
+    // 9-16 token rows: the grouped projection's int8 matrix-core kernel (the weights streamed once, 16-byte loads)
+    halo_proj_input in{};
+    in.xq = xq;
+    in.xs = xs;
+    in.mode = HALO_PROJ_Q;
+    return halo_op_proj_q8(eng, w, &y, 1, &in, m, err, errlen);
+  }
   if (m >= 16) {
     // int8 MFMA tiles: 16 rows x 16 (or 64) tokens per block, one MFMA per Q8_0 block
     const std::uint32_t ys = m > 1 ? ystride : w->rows;

@@ -7,13 +7,57 @@
 
 using namespace halo::engine;
 
+namespace {
+
+// Fewest tokens for which the mode-Q projection runs on the int8 matrix cores (halo_proj_q8m_c*): beyond the v_dot4
+// kernel's 8. Up to 8 tokens the model's batched step keeps the v_dot4 kernels, whose per-token bits equal the
+// one-session step's (a batch gives the same tokens as its sessions run alone).
+constexpr std::uint32_t kProjMfmaMinTokens = 9;
+
+int ProjQ8Mfma(halo_engine* eng, const halo_q8_matrix* mats, float* const* ys, uint32_t n_mats,
+               const halo_proj_input* in, uint32_t tokens, char* err, size_t errlen) {
+  const std::uint32_t cols = mats[0].cols;
+  if (in->xq == nullptr || in->xs == nullptr) return SetErr(err, errlen, "proj: mode Q needs xq / xs"), -1;
+  for (std::uint32_t i = 0; i < n_mats; ++i) {
+    const halo_q8_matrix& w = mats[i];
+    if (w.qs == nullptr || w.d == nullptr || ys[i] == nullptr || w.rows == 0 || w.cols != cols || w.qstride != cols)
+      return SetErr(err, errlen, "proj: matrix %u (%u x %u, qstride %u) does not match cols %u", i, w.rows, w.cols,
+                    w.qstride, cols),
+             -1;
+  }
+  std::uint32_t off[5] = {0, 0, 0, 0, 0};
+  for (std::uint32_t i = 0; i < 4; ++i) off[i + 1] = off[i] + (i < n_mats ? CeilDiv(mats[i].rows, 16) : 0);
+  auto mat = [&](std::uint32_t i) { return i < n_mats ? mats[i] : mats[0]; };
+  auto out = [&](std::uint32_t i) { return i < n_mats ? ys[i] : ys[0]; };
+  auto rows = [&](std::uint32_t i) { return i < n_mats ? mats[i].rows : 0u; };
+  char name[32];
+  std::snprintf(name, sizeof name, "halo_proj_q8m_c%u", cols / 1024);
+  const halo_arg a[] = {Ptr(in->xq), Ptr(in->xs),
+                        Ptr(mat(0).qs), Ptr(mat(0).d), Ptr(out(0)), Ptr(mat(1).qs), Ptr(mat(1).d), Ptr(out(1)),
+                        Ptr(mat(2).qs), Ptr(mat(2).d), Ptr(out(2)), Ptr(mat(3).qs), Ptr(mat(3).d), Ptr(out(3)),
+                        U32(rows(0)), U32(rows(1)), U32(rows(2)), U32(rows(3)), U32(off[1]), U32(off[2]), U32(off[3]),
+                        U32(tokens)};
+  return Launch(eng, name, D3(off[4]), D3(512), a, err, errlen);
+}
+
+}  // namespace
+
 extern "C" int halo_op_proj_q8_grid(halo_engine* eng, const halo_q8_matrix* mats, float* const* ys,
                                     uint32_t n_mats, const halo_proj_input* in, uint32_t tokens, uint32_t grid_blocks,
                                     uint32_t lanes_per_row, char* err, size_t errlen) {
   if (mats == nullptr || ys == nullptr || in == nullptr || n_mats == 0 || n_mats > 4)
     return SetErr(err, errlen, "proj: 1..4 matrices with outputs and an input descriptor"), -1;
-  if (tokens == 0 || tokens > 8) return SetErr(err, errlen, "proj: tokens %u not in 1..8", tokens), -1;
+  if (tokens == 0 || tokens > 16) return SetErr(err, errlen, "proj: tokens %u not in 1..16", tokens), -1;
   const std::uint32_t cols = mats[0].cols;
+  // Quantized rows (mode Q) of more tokens than the VALU kernel takes on int8 matrix cores when the row length is one
+  // the MFMA kernel covers. Tuning overrides: tasks_per_wave = lanes_per_row = 1 selects the VALU kernel, = 2 the
+  // MFMA kernel, at any token count they support.
+  const bool force_valu = grid_blocks == 1 && lanes_per_row == 1, force_mfma = grid_blocks == 2 && lanes_per_row == 2;
+  if (in->mode == HALO_PROJ_Q && tokens <= 16 && (tokens >= kProjMfmaMinTokens || force_mfma) && !force_valu &&
+      (cols == 1024 || cols == 2048 || cols == 4096))
+    return ProjQ8Mfma(eng, mats, ys, n_mats, in, tokens, err, errlen);
+  if (force_valu || force_mfma) grid_blocks = lanes_per_row = 0;
+  if (tokens == 0 || tokens > 8) return SetErr(err, errlen, "proj: tokens %u not in 1..8", tokens), -1;
   if (cols == 0 || cols % 32 != 0 || cols > 4096) return SetErr(err, errlen, "proj: cols %u unsupported", cols), -1;
   for (std::uint32_t i = 0; i < n_mats; ++i) {
     const halo_q8_matrix& w = mats[i];

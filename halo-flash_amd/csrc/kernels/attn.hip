@@ -317,17 +317,19 @@ __device__ __forceinline__ void AttnDecodePartial(
     for (int c = 0; c < kHd / 32; ++c) SplitHalves(xr[c], qh[c], ql[c], sq);
     if (kq == 0) qsc[16 * qt + lr] = sq;
   }
-  {  // the block's K and V magnitudes (the newest row from LDS; V rows past the visible range are zeroed below)
+  {  // the block's K and V magnitudes over the visible rows (rows past them repeat the pool's row `last`, which for
+     // the owner block is not yet written: the newest row comes from LDS, and the masked rows' scores are dropped)
     float ka = 0.0f, va = 0.0f;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const std::uint32_t j = r + 16 * h;
       const bool fresh = owner && start + j == last;
+      if (start + j < limit)
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float4 kv = fresh ? *reinterpret_cast<const float4*>(&knew[0][64 * u + 4 * sub]) : kf[h][u];
-        ka = fmaxf(ka, fmaxf(fmaxf(fabsf(kv.x), fabsf(kv.y)), fmaxf(fabsf(kv.z), fabsf(kv.w))));
-      }
+        for (int u = 0; u < 4; ++u) {
+          const float4 kv = fresh ? *reinterpret_cast<const float4*>(&knew[0][64 * u + 4 * sub]) : kf[h][u];
+          ka = fmaxf(ka, fmaxf(fmaxf(fabsf(kv.x), fabsf(kv.y)), fmaxf(fabsf(kv.z), fabsf(kv.w))));
+        }
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {

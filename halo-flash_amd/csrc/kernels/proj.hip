@@ -208,3 +208,138 @@ HALO_PROJ_Q8_L(3, g)
 #undef HALO_PROJ_Q8_T
 #undef HALO_PROJ_Q8_NB
 #undef HALO_PROJ_Q8
+
+// ---- grouped projections of up to 16 quantized token rows on int8 matrix cores -------------------------------
+// The same products as halo_proj_q8q_* (mode q: xq [T][cols] int8, xs [T][cols / 32]) for T <= 16, where the VALU
+// form's dot4 chains grow with T (four v_dot4 and two FMAs per 16 weight bytes and token). A block of 8 waves owns
+// one task of 16 rows of one matrix; wave w the 64 S columns from 64 S w (S = cols / 512 steps of 64 columns, two
+// Q8_0 blocks each) on v_mfma_i32_16x16x64_i8: A = the 16 token rows, B = the 16 weight rows, lane l supplying the
+// 16 bytes at column 16 (l / 16) of the step for token / row l % 16, so each lane's weight load is one 16-byte piece
+// of its row. The step's two Q8_0 blocks need separate integer sums (each has its own scales): two MFMAs share the
+// weight operand, the activation operand holding only the first block's lanes (l / 16 < 2) in one and only the
+// second block's in the other. D lane l holds tokens 4 (l / 16) + i of row l % 16; its fp32 epilogue per block is
+// acc += d_w (s_x float(isum)), blocks in ascending order within the wave, then the 8 waves' partial sums are added
+// in wave order through LDS. Each token's outputs depend on its own row only, so they carry the same bits whatever
+// T. Small waves (8 per 16-row task, S <= 8 weight loads each, all issued first) keep the weight stream's requests in
+// flight across the chip; the activation scales sit in LDS transposed ([block][token]). (Measured on the C1 q|gate +
+// kv pair: 8 waves x 4 steps 7.5 us at 16 tokens, 16 x 2 8.3, 4 x 8 7.4; the int8 MFMAs themselves cost nothing
+// measurable, the weight-scale loads 0.7 us, the activation loads 1.4 us at 16 tokens.)
+namespace {
+typedef int V4I32p __attribute__((ext_vector_type(4)));
+constexpr std::uint32_t kMfmaWaves = 8;
+
+template <int S>  // 64-column steps per wave: cols = 512 S
+__device__ __forceinline__ void ProjQ8Mfma(const std::int8_t* __restrict__ xq, const float* __restrict__ xs,
+                                           const std::int8_t* qs0, const std::uint16_t* d0, float* y0,
+                                           const std::int8_t* qs1, const std::uint16_t* d1, float* y1,
+                                           const std::int8_t* qs2, const std::uint16_t* d2, float* y2,
+                                           const std::int8_t* qs3, const std::uint16_t* d3, float* y3,
+                                           std::uint32_t rows0, std::uint32_t rows1, std::uint32_t rows2,
+                                           std::uint32_t rows3, std::uint32_t o1, std::uint32_t o2, std::uint32_t o3,
+                                           std::uint32_t T) {
+  constexpr std::uint32_t cols = 64 * kMfmaWaves * S, nblk = cols / 32, kThreads = 64 * kMfmaWaves;
+  __shared__ __attribute__((aligned(16))) float sxt[nblk][16];
+  __shared__ __attribute__((aligned(16))) float red[kMfmaWaves - 1][64][4];
+  const std::uint32_t tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave, g = lane / 16, li = lane % 16;
+  const std::uint32_t task = blockIdx.x;
+  const std::uint32_t m = task < o1 ? 0 : task < o2 ? 1 : task < o3 ? 2 : 3;
+  const std::uint32_t lt = task - (m == 0 ? 0 : m == 1 ? o1 : m == 2 ? o2 : o3);
+  const std::int8_t* qs = m == 0 ? qs0 : m == 1 ? qs1 : m == 2 ? qs2 : qs3;
+  const std::uint16_t* d = m == 0 ? d0 : m == 1 ? d1 : m == 2 ? d2 : d3;
+  float* y = m == 0 ? y0 : m == 1 ? y1 : m == 2 ? y2 : y3;
+  const std::uint32_t rows = m == 0 ? rows0 : m == 1 ? rows1 : m == 2 ? rows2 : rows3;
+  const std::uint32_t row = min(lt * 16 + li, rows - 1), tok = min(li, T - 1);
+  const std::uint32_t c0 = wave * 64 * S;
+  // the activation scales first (vmcnt counts in order: their wait must not include the weight stream)
+  constexpr std::uint32_t kSx = (nblk * 16 + kThreads - 1) / kThreads;
+  float sxr[kSx];
+#pragma unroll
+  for (std::uint32_t j = 0; j < kSx; ++j) {
+    const std::uint32_t e = min(tid + kThreads * j, nblk * 16 - 1), b = e / 16, t = e % 16;
+    sxr[j] = xs[static_cast<std::size_t>(min(t, T - 1)) * nblk + b];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const std::int8_t* wp = qs + static_cast<std::size_t>(row) * cols + c0 + 16 * g;
+  const std::int8_t* xp = xq + static_cast<std::size_t>(tok) * cols + c0 + 16 * g;
+  const std::uint16_t* dp = d + static_cast<std::size_t>(row) * nblk + c0 / 32;
+  int4 w[S], x[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+    w[s] = __builtin_bit_cast(int4, __builtin_nontemporal_load(reinterpret_cast<const halo::V4i*>(wp + 64 * s)));
+  std::uint16_t dsv[2 * S];  // the wave's 2 S block scales of this row: 16-byte loads (8 bytes at S = 2)
+  if constexpr (S >= 4) {
+#pragma unroll
+    for (int j = 0; j < S / 4; ++j) {
+      const uint4 v = *reinterpret_cast<const uint4*>(dp + 8 * j);
+      __builtin_memcpy(dsv + 8 * j, &v, 16);
+    }
+  } else {
+    const uint2 v = *reinterpret_cast<const uint2*>(dp);
+    __builtin_memcpy(dsv, &v, 8);
+  }
+#pragma unroll
+  for (int s = 0; s < S; ++s) x[s] = *reinterpret_cast<const int4*>(xp + 64 * s);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (std::uint32_t j = 0; j < kSx; ++j) {
+    const std::uint32_t e = tid + kThreads * j, b = e / 16, t = e % 16;
+    if (e < nblk * 16) sxt[b][t] = t < T ? sxr[j] : 0.0f;
+  }
+  __syncthreads();
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const bool first_half = g < 2;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int4 xv = x[s];
+    const V4I32p xa = first_half ? V4I32p{xv.x, xv.y, xv.z, xv.w} : V4I32p{0, 0, 0, 0};
+    const V4I32p xb = first_half ? V4I32p{0, 0, 0, 0} : V4I32p{xv.x, xv.y, xv.z, xv.w};
+    const V4I32p wb = {w[s].x, w[s].y, w[s].z, w[s].w};
+    const V4I32p zero = {0, 0, 0, 0};
+    const V4I32p ia = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, wb, zero, 0, 0, 0);
+    const V4I32p ib = __builtin_amdgcn_mfma_i32_16x16x64_i8(xb, wb, zero, 0, 0, 0);
+    const std::uint32_t blk = c0 / 32 + 2 * s;
+    const float dwa = halo::F16(dsv[2 * s]), dwb = halo::F16(dsv[2 * s + 1]);
+    const float4 sa = *reinterpret_cast<const float4*>(&sxt[blk][4 * g]);
+    const float4 sb = *reinterpret_cast<const float4*>(&sxt[blk + 1][4 * g]);
+    const float sav[4] = {sa.x, sa.y, sa.z, sa.w}, sbv[4] = {sb.x, sb.y, sb.z, sb.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[i] += dwa * (sav[i] * static_cast<float>(ia[i]));
+      acc[i] += dwb * (sbv[i] * static_cast<float>(ib[i]));
+    }
+  }
+  if (wave > 0)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave - 1][lane][i] = acc[i];
+  __syncthreads();
+  if (wave == 0) {
+    const std::uint32_t r = lt * 16 + li;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = acc[i];
+#pragma unroll
+      for (std::uint32_t u = 0; u + 1 < kMfmaWaves; ++u) v += red[u][lane][i];
+      const std::uint32_t t = 4 * g + i;
+      if (r < rows && t < T) y[static_cast<std::size_t>(t) * rows + r] = v;
+    }
+  }
+}
+}  // namespace
+
+// grid (o_4) (one 16-row task per block), block 512. Matrix m owns tasks [o_m, o_{m+1}) (16 rows each, o_0 = 0);
+// y_m [T][rows_m]. cols = 512 S (the kernel name's c<cols / 1024>: 1024, 2048 or 4096), unpadded rows (qstride =
+// cols), 1 <= T <= 16.
+#define HALO_PROJ_Q8M(C, S)                                                                                        \
+  extern "C" __global__ void __launch_bounds__(512) halo_proj_q8m_c##C(                                           \
+      const std::int8_t* xq, const float* xs, const std::int8_t* qs0, const std::uint16_t* d0, float* y0,       \
+      const std::int8_t* qs1, const std::uint16_t* d1, float* y1, const std::int8_t* qs2, const std::uint16_t* d2, \
+      float* y2, const std::int8_t* qs3, const std::uint16_t* d3, float* y3, std::uint32_t rows0,                 \
+      std::uint32_t rows1, std::uint32_t rows2, std::uint32_t rows3, std::uint32_t o1, std::uint32_t o2,          \
+      std::uint32_t o3, std::uint32_t T) {                                                                        \
+    ProjQ8Mfma<S>(xq, xs, qs0, d0, y0, qs1, d1, y1, qs2, d2, y2, qs3, d3, y3, rows0, rows1, rows2, rows3, o1, o2, o3, \
+                  T);                                                                                             \
+  }
+HALO_PROJ_Q8M(1, 2)
+HALO_PROJ_Q8M(2, 4)
+HALO_PROJ_Q8M(4, 8)
+#undef HALO_PROJ_Q8M

@@ -51,12 +51,14 @@ int halo_op_quantize_q8(halo_engine* eng, const float* x, int8_t* xq, float* xs,
 /* Q8_0 x int8-activation projection for M tokens (FlashNextGpu::MatVec + the batched int8 GEMV,
  * src/engine/flash_next_gpu.cpp:212-254, src/kernels/batch_decode.hip:226-345):
  *   y[t * ystride + r] = sum_b d[r][b] * xs[t][b] * isum(r, b, t),   t < M.
- * M < 16 streams the weights once per launch with v_dot4 (in groups of up to 8 columns); M >= 16 runs int8 MFMA
- * tiles of 16 rows x 16 tokens (x 64 tokens from M = 64), one v_mfma_i32_16x16x32_i8 per Q8_0 block. */
+ * M <= 8 streams the weights with v_dot4 (in groups of up to 8 columns); 9 <= M <= 16 with dense rows of 1024,
+ * 2048 or 4096 columns runs the grouped projection's int8 matrix-core kernel (16 weight rows x 16 tokens per
+ * v_mfma_i32_16x16x64_i8, two Q8_0 blocks per step, one launch); M >= 16 otherwise runs int8 MFMA tiles of 16 rows
+ * x 16 tokens (x 64 tokens from M = 64), one v_mfma_i32_16x16x32_i8 per Q8_0 block. */
 int halo_op_matvec_q8a8(halo_engine* eng, const halo_q8_matrix* w, const int8_t* xq, const float* xs, float* y,
                         uint32_t m, uint32_t ystride, char* err, size_t errlen);
 /* Grouped projections with the activation prologue fused in: up to 4 Q8_0 matrices sharing the input row(s) of
- * `tokens` (<= 8) tokens, in ONE launch. Replaces the reference's sequence [RMSNorm] -> halo_quantize_q8_rows ->
+ * `tokens` (<= 8; <= 16 in mode Q with 1024, 2048 or 4096 columns) tokens, in ONE launch. Replaces the reference's sequence [RMSNorm] -> halo_quantize_q8_rows ->
  * one MatVec per matrix (src/engine/flash_next_gpu.cpp:212-254, src/kernels/core.hip:3089-3101) for the
  * projections that read the same activations (q|k|v + z + alpha|beta of a DeltaNet layer, q|gate + k + v of an
  * attention layer). ys[i] [tokens][mats[i].rows]. All matrices have cols = in cols (<= 4096, % 32 == 0) and
@@ -85,7 +87,9 @@ typedef struct halo_proj_input {
 int halo_op_proj_q8(halo_engine* eng, const halo_q8_matrix* mats, float* const* ys, uint32_t n_mats,
                     const halo_proj_input* in, uint32_t tokens, char* err, size_t errlen);
 /* The same with an explicit tiling for tuning: tasks per wave (1 / 2 / 4 rows groups per wave, so the prologue
- * runs once per 4 x that many groups) and lanes per row (16 / 32 / 64); 0 keeps the default of each. */
+ * runs once per 4 x that many groups) and lanes per row (16 / 32 / 64); 0 keeps the default of each. Mode Q with
+ * 9..16 tokens and 1024, 2048 or 4096 columns runs on int8 matrix cores (halo_proj_q8m_c*, 16-row tasks);
+ * tasks_per_wave = lanes_per_row = 2 selects that kernel from 1 token, = 1 the VALU kernel (8 tokens at most). */
 int halo_op_proj_q8_grid(halo_engine* eng, const halo_q8_matrix* mats, float* const* ys, uint32_t n_mats,
                          const halo_proj_input* in, uint32_t tokens, uint32_t tasks_per_wave, uint32_t lanes_per_row,
                          char* err, size_t errlen);

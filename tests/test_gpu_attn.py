@@ -160,6 +160,12 @@ def test_attn_decode_step_equals_prep_then_decode(dev, S, prefix, suffixes, max_
     rng = np.random.default_rng(31 + S + prefix)
     Hkv, Hq, rot, theta, eps = 2, 16, 64, 1e7, 1e-6
     descA, gA, kp, vp, pages, nkv = build(dev, rng, S, Hkv, prefix, suffixes, max_context)
+    # the slots the step appends to hold stale huge values (memory the pool never wrote): the fused kernel reads its
+    # chunk before it writes the newest row, and must neither use nor scale by those values
+    for s in range(S):
+        p_ = int(nkv[s]) - 1
+        kp[pages[s, p_ // PAGE], :, p_ % PAGE] = 1e30
+        vp[pages[s, p_ // PAGE], :, p_ % PAGE] = -1e30
     gB = dict(k=dev.to_device(kp), v=dev.to_device(vp), pages=gA["pages"], nkv=gA["nkv"])
     descB = H.PagedKV(gB["k"].ptr, gB["v"].ptr, gB["pages"].ptr, gB["nkv"].ptr, S, Hkv, D, descA.max_pages, prefix,
                       max_context)

@@ -58,12 +58,48 @@ def test_proj_mode_f_and_q(dev, tokens, shapes):
     for (qs, d), y in zip(host, got_f):
         want, mag = O.gemv_q8a8(qs, d, xq, xs)
         _check_y(y, want, mag)
-    # mode Q on the same activations: the same bits
+    # mode Q on the same activations through the same (v_dot4) kernel: the same bits
     outs_q = [dev.array((tokens, r), np.float32) for r, _ in shapes]
     inq = H.ProjInput(xq=xq_o.ptr, xs=xs_o.ptr, mode=H.PROJ_Q)
-    H.proj_q8(dev, ws, outs_q, inq, tokens)
+    H.proj_q8(dev, ws, outs_q, inq, tokens, 1, 1)
     for a, o in zip(got_f, outs_q):
         assert np.array_equal(a.view(np.uint32), o.download().view(np.uint32))
+
+
+@pytest.mark.parametrize("tokens", [1, 2, 3, 5, 8, 9, 12, 16])
+@pytest.mark.parametrize("shapes", [
+    [(4096, 2048), (512, 2048)],                        # C1 q|gate and kv
+    [(2048, 4096)],                                      # C1 o
+    [(300, 1024), (17, 1024), (1, 1024), (64, 1024)],   # ragged rows (partial 16-row tasks), four matrices
+])
+def test_proj_mode_q_matrix_cores(dev, tokens, shapes):
+    """halo_proj_q8m_c* (int8 MFMA, two Q8_0 blocks per step with separate integer sums; the default for mode Q at
+    9-16 tokens, forced here from 1): every output within 1e-5 * sum|term| of the oracle's GEMV on the same codes,
+    argmax equal; a zero block and an all-zero token row included; token 0's outputs carry the same bits as at one
+    token (each token's products and sums depend on its own row only)."""
+    rng = np.random.default_rng(tokens * 11 + len(shapes))
+    cols = shapes[0][1]
+    host, ws = _mats(dev, rng, shapes)
+    x = rng.normal(0, 1, (tokens, cols)).astype(np.float32)
+    x[0, 32:64] = 0.0
+    x[tokens - 1] = 0.0 if tokens > 2 else x[tokens - 1]
+    xq, xs = O.quantize(x)
+    gq, gs = dev.to_device(xq), dev.to_device(xs)
+    outs = [dev.array((tokens, r), np.float32) for r, _ in shapes]
+    H.proj_q8(dev, ws, outs, H.ProjInput(xq=gq.ptr, xs=gs.ptr, mode=H.PROJ_Q), tokens, 2, 2)
+    for (qs, d), o in zip(host, outs):
+        want, mag = O.gemv_q8a8(qs, d, xq, xs)
+        y = o.download()
+        err = np.abs(y.astype(np.float64) - want.astype(np.float64))
+        assert not np.any(err > TOL * mag + 1e-6), f"{np.count_nonzero(err > TOL * mag + 1e-6)} outputs off"
+        live = np.abs(want).max(-1) > 0
+        assert np.argmax(y[live], -1).tolist() == np.argmax(want[live], -1).tolist()
+        if tokens > 2:
+            assert not np.any(y[tokens - 1])
+    one = [dev.array((1, r), np.float32) for r, _ in shapes]
+    H.proj_q8(dev, ws, one, H.ProjInput(xq=gq.ptr, xs=gs.ptr, mode=H.PROJ_Q), 1, 2, 2)
+    for a, b in zip(outs, one):
+        assert a.download()[0].tobytes() == b.download()[0].tobytes()
 
 
 @pytest.mark.parametrize("tokens,cols,with_delta", [(1, 2048, True), (4, 2048, True), (3, 4096, False),

@@ -878,6 +878,9 @@ def run_membw(args, dev, H, res):
         res["membw"] = None
         res["roofline"] = None
         return res
+    # an independent ceiling: the runtime's device-to-device copy (hipMemcpyAsync), rotated over buffers beyond the
+    # MALL, HIP events on the device stream
+    out["memcpy_d2d"] = _memcpy_d2d(dev, [C0_BYTES, 512 << 20])
     xs = np.array(sizes, np.float64)
     ts = np.array([best[z][0] for z in sizes])
     A = np.stack([np.ones_like(xs), xs], 1)
@@ -889,6 +892,39 @@ def run_membw(args, dev, H, res):
     res["membw"] = out
     res["roofline"] = None
     return res
+
+
+def _memcpy_d2d(dev, sizes):
+    """hipMemcpyAsync device-to-device on the device's stream (the HIP runtime the library links), rotated over
+    buffers beyond the MALL, HIP events around the copies."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
+    hip.hipMemcpyAsync.restype = ctypes.c_int
+    stream = dev.stream()
+    out = {}
+    for size in sizes:
+        nbuf = max(2, -(-MIN_ROTATION_BYTES // size))
+        step = (size + 65535) // 65536 * 65536
+        pool = dev.array(2 * nbuf * step, np.uint8)
+        src = [pool.ptr + i * step for i in range(nbuf)]
+        dst = [pool.ptr + (nbuf + i) * step for i in range(nbuf)]
+        reps = max(nbuf, min(400, (4 << 30) // size))
+
+        def copy(i):
+            rc = hip.hipMemcpyAsync(dst[i % nbuf], src[i % nbuf], size, 3, stream)  # hipMemcpyDeviceToDevice
+            assert rc == 0, f"hipMemcpyAsync: {rc}"
+        for i in range(nbuf):
+            copy(i)
+        dev.sync()
+        dev.timer_start()
+        for i in range(reps):
+            copy(i)
+        us = dev.timer_stop() * 1e3 / reps
+        out[str(size)] = {"us": round(us, 3), "read_GBps": round(size / us / 1e3, 1),
+                          "read_plus_write_GBps": round(2 * size / us / 1e3, 1), "buffers": nbuf}
+        pool.free()
+    log(f"[bench] memcpy d2d {out}")
+    return out
 
 
 def run_c0(args, dev, H, res):

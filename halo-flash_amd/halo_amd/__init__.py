@@ -622,6 +622,10 @@ class Device:
         _call("halo_timer_stop", self.handle, C.byref(ms))
         return float(ms.value)
 
+    def stream(self) -> int:
+        """The device's HIP stream (hipStream_t) as an integer, for calls into the HIP runtime."""
+        return int(lib().halo_device_stream(self.handle) or 0)
+
     def wall_clock_khz(self) -> int:
         khz = C.c_int()
         _call("halo_wall_clock_khz", self.handle, C.byref(khz))

@@ -145,7 +145,8 @@
   X(halo_gemm_q8a8_320x64) X(halo_gemm_q8a8_160x64) X(halo_gemm_q8a8_256x128)                                 \
   X(halo_synth_q8) X(halo_synth_f32) X(halo_code_object_info_copy)                                            \
   X(halo_stream_read) X(halo_stream_copy) X(halo_clock_stamp)                                                 \
-  X(halo_gdn_prefill_split) X(halo_gdn_chunk_prep) X(halo_gdn_chunk_scan)                                            \
+  X(halo_gdn_prefill_split) X(halo_gdn_chunk_prep) X(halo_gdn_chunk_scan)                                    \
+  X(halo_proj_q8m_c1) X(halo_proj_q8m_c2) X(halo_proj_q8m_c4)                                            \
   X(halo_gemv_q8r_r4_b1) X(halo_gemv_q8r_r4_b8_ps) X(halo_gemv_q8r_r2_b3_p) X(halo_gemv_q8r_r2_b5_s)              \
   X(halo_gemv_q8r_dual_b1) X(halo_gemv_q8r_dual_b8_ps)
 

@@ -121,19 +121,17 @@ def run_c1(args, dev, H, res):
     in_aq = H.ProjInput(xq=aq.ptr, xs=as_.ptr, mode=H.PROJ_Q)
 
     def c1_pass(ws, m, fused=True, mfma=False):
-        if fused and m == 1:
+        if fused and m <= 2:
             # one launch per input row set: quantize prologue + (q|gate, kv), then quantize prologue + o
             H.proj_q8(dev, ws[:2], [yqg, ykv], in_x, m)
             H.proj_q8(dev, ws[2:], [yo], in_a, m)
             return
         if fused:
-            # as the model's batched step runs them: one quantize launch per input row set, then the grouped
-            # projection on the quantized rows (v_dot4 up to 8 tokens, int8 matrix cores beyond; `mfma`: the matrix
-            # cores at any token count)
+            # from 3 token rows: both inputs quantized by one launch, then the grouped projections on the quantized
+            # rows (v_dot4 up to 8 tokens, int8 matrix cores beyond; `mfma`: the matrix cores at any token count)
             t = (2, 2) if mfma else (0, 0)
-            dev.op("quantize_q8", x.ptr, xq.ptr, xs.ptr, m, 2048)
+            dev.op("quantize_q8_pair", x.ptr, xq.ptr, xs.ptr, 2048, a.ptr, aq.ptr, as_.ptr, 4096, m)
             H.proj_q8(dev, ws[:2], [yqg, ykv], in_xq, m, *t)
-            dev.op("quantize_q8", a.ptr, aq.ptr, as_.ptr, m, 4096)
             H.proj_q8(dev, ws[2:], [yo], in_aq, m, *t)
             return
         dev.op("quantize_q8", x.ptr, xq.ptr, xs.ptr, m, 2048)
@@ -154,11 +152,12 @@ def run_c1(args, dev, H, res):
     got = yo.download()[0]
     assert np.all(np.abs(got - want) <= 1e-5 * mag + 1e-6), "bench spot check failed"
 
-    if args.eager:  # kernel durations of the M = 1 pass under a tracer that cannot follow graph launches
-        for _ in range(max(1, args.steps // copies)):
-            for ws in sets:
-                c1_pass(ws, 1)
-        dev.sync()
+    if args.eager:  # kernel durations (and counters) of the M = 1, 4, 8, 16 passes, direct launches
+        for m in (1, 4, 8, 16):
+            for _ in range(3):
+                for ws in sets:
+                    c1_pass(ws, m)
+            dev.sync()
         res["c1"] = None
         return res
 
@@ -180,7 +179,7 @@ def run_c1(args, dev, H, res):
     sweep["1_unfused"] = {"us_per_pass": round(ms / (nrep * copies) * 1e3, 3),
                           "GBps": round(c1_pass_bytes(1) / (ms / (nrep * copies) * 1e-3) / 1e9, 1)}
     dev.free_graph(g)
-    for m in (1, 2, 3, 4, 8, 16, "2_mfma", "4_mfma", "8_mfma"):
+    for m in (1, 2, 3, 4, 8, 16, "4_mfma", "8_mfma"):
         g = graph_for(int(str(m).split("_")[0]), mfma=isinstance(m, str))
         reps = 1 if m != 1 else max(1, args.warmup // copies)
         for _ in range(reps):
@@ -197,9 +196,9 @@ def run_c1(args, dev, H, res):
                          "GBps": round(c1_pass_bytes(mi) / (ms / steps * 1e-3) / 1e9, 1)}
         dev.free_graph(g)
     res["c1"] = {"workload": "C1 Q8_0 projections 2048->4096, 2048->512, 4096->2048 from fp32 activations: at M = 1 "
-                             "quantized in the projection's prologue (2 launches), from M = 2 one quantize launch per "
-                             "input then the grouped projection on the quantized rows (4 launches: v_dot4 up to 8 "
-                             "tokens, int8 matrix cores at 16); *_mfma: the matrix-core kernel at that M", "bytes_per_pass_m1": c1_pass_bytes(1),
+                             "quantized in the projections' prologues at M <= 2 (2 launches); from M = 3 both inputs "
+                             "quantized by one launch, then the grouped projections on the quantized rows (3 launches: "
+                             "v_dot4 up to 8 tokens, int8 matrix cores at 16); *_mfma: the matrix-core kernel at that M", "bytes_per_pass_m1": c1_pass_bytes(1),
                  "GBps_m1": sweep["1"]["GBps"], "sweep": sweep}
     log(f"[bench] C1 sweep {sweep}")
     return res

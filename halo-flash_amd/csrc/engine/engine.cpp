@@ -123,6 +123,18 @@ int halo_op_quantize_q8(halo_engine* eng, const float* x, int8_t* xq, float* xs,
   return Launch(eng, "halo_quantize_q8_rows", D3(tokens), D3(256), a, err, errlen);
 }
 
+int halo_op_quantize_q8_pair(halo_engine* eng, const float* x0, int8_t* xq0, float* xs0, uint32_t cols0,
+                             const float* x1, int8_t* xq1, float* xs1, uint32_t cols1, uint32_t tokens, char* err,
+                             size_t errlen) {
+  if (RequirePtrs(err, errlen, "quantize_q8_pair",
+                  {{"x0", x0}, {"xq0", xq0}, {"xs0", xs0}, {"x1", x1}, {"xq1", xq1}, {"xs1", xs1}}) != 0)
+    return -1;
+  if (cols0 % 32 != 0 || cols1 % 32 != 0 || tokens == 0)
+    return SetErr(err, errlen, "quantize pair: cols %% 32 != 0 or no tokens"), -1;
+  const halo_arg a[] = {Ptr(x0), Ptr(xq0), Ptr(xs0), U32(cols0), Ptr(x1), Ptr(xq1), Ptr(xs1), U32(cols1), U32(tokens)};
+  return Launch(eng, "halo_quantize_q8_rows2", D3(2 * tokens), D3(256), a, err, errlen);
+}
+
 static int CheckMatrix(const halo_q8_matrix* w, char* err, size_t errlen) {
   if (w == nullptr || w->qs == nullptr || w->d == nullptr) return SetErr(err, errlen, "null matrix"), -1;
   if (w->rows == 0 || w->cols == 0 || w->cols % 32 != 0 || w->qstride < w->cols || w->qstride % 16 != 0)

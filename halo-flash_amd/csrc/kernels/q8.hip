@@ -55,6 +55,24 @@ extern "C" __global__ void __launch_bounds__(256)
   }
 }
 
+// Two independent inputs in one launch, grid (2 T): block t < T quantizes row t of x0 (cols0 wide), block T + t row t
+// of x1 (cols1 wide), each as halo_quantize_q8_rows (the same bytes).
+extern "C" __global__ void __launch_bounds__(256)
+    halo_quantize_q8_rows2(const float* x0, std::int8_t* xq0, float* xd0, std::uint32_t cols0, const float* x1,
+                           std::int8_t* xq1, float* xd1, std::uint32_t cols1, std::uint32_t T) {
+  const bool second = blockIdx.x >= T;
+  const std::size_t t = second ? blockIdx.x - T : blockIdx.x;
+  const std::uint32_t cols = second ? cols1 : cols0;
+  const float4* row = reinterpret_cast<const float4*>((second ? x1 : x0) + t * cols);
+  std::uint32_t* codes = reinterpret_cast<std::uint32_t*>((second ? xq1 : xq0) + t * cols);
+  float* xd = second ? xd1 : xd0;
+  for (std::uint32_t g = threadIdx.x; g < cols / 4; g += blockDim.x) {
+    float scale;
+    codes[g] = halo::QuantQuad(row[g], scale);
+    if (g % 8 == 0) xd[t * (cols / 32) + g / 8] = scale;
+  }
+}
+
 // halo_quantize_q8_rows over 8 rows per block (grid ceil(T / 8)): the block's rows are one flat run of 16-byte
 // groups, so short rows (the MoE's 512-wide h) keep every lane busy and each lane has several loads in flight.
 // Q8_0 blocks and 8-lane groups line up as in the one-row form (cols % 32 == 0), so the codes are bitwise equal.

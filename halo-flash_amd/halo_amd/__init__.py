@@ -369,6 +369,7 @@ _SIGS = {
     "halo_engine_launch": (C.c_int, [_VP, C.c_char_p, Dim3, Dim3, C.POINTER(Arg), _SZ], True),
     "halo_op_repack_q8_0": (C.c_int, [_VP, _VP, _VP, _VP, _U32, _U32, _U32], True),
     "halo_op_quantize_q8": (C.c_int, [_VP, _VP, _VP, _VP, _U32, _U32], True),
+    "halo_op_quantize_q8_pair": (C.c_int, [_VP, _VP, _VP, _VP, _U32, _VP, _VP, _VP, _U32, _U32], True),
     "halo_op_moe_prefill_workspace_bytes": (_SZ, [C.POINTER(MoeWeights), _U32], False),
     "halo_op_moe_prefill": (C.c_int, [_VP, C.POINTER(MoeWeights), _VP, _VP, _U32, _VP, _SZ], True),
     "halo_op_attn_prefill_workspace_bytes": (_SZ, [C.POINTER(PrefillSegment), _U32], False),

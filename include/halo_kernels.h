@@ -8,6 +8,7 @@
  *   halo_repack_q8_0(const u8* raw, i8* qs, u16* d, u32 rows, u32 cols, u32 qstride)         core.hip:2126
  *   halo_quantize_q8_rows(const f32* x, i8* xq, f32* xd, u32 cols)            grid (T)        core.hip:3089
  *   halo_quantize_q8_rows8(const f32* x, i8* xq, f32* xd, u32 cols, u32 T)    grid ceil(T / 8) (8 rows per block)
+ *   halo_quantize_q8_rows2(x0, xq0, xd0, cols0, x1, xq1, xd1, cols1, T)   grid (2 T): two inputs in one launch
  *   halo_q8x_cols(const f32* x, u32 xstride, u32 cols, i8* xq, f32* xs, i8* xq2, f32* xs2)   batch_decode.hip:201
  *   halo_gemv_q8r{,_r2,_r4}(const i8* qs, const u16* d, const f32* x, f32* y, u32 rows, u32 cols, u32 qstride)
  *                                                       grid ceil(rows / (8 R))              core.hip:2175,2429
@@ -113,7 +114,7 @@
 /* X(name) for every kernel the host layer launches; tests check each is present in the code object. */
 #define HALO_KERNEL_LIST(X)                                                                                  \
   X(halo_repack_q8_0)                                                                                        \
-  X(halo_quantize_q8_rows) X(halo_quantize_q8_rows8)                                                         \
+  X(halo_quantize_q8_rows) X(halo_quantize_q8_rows8) X(halo_quantize_q8_rows2)                                                         \
   X(halo_q8x_cols)                                                                                           \
   X(halo_gemv_q8r) X(halo_gemv_q8r_r2) X(halo_gemv_q8r_r4)                                                   \
   X(halo_gemv_q8r_i8_r1_b1) X(halo_gemv_q8r_i8_r2_b1) X(halo_gemv_q8r_i8_r4_b1)                              \

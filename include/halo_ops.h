@@ -47,6 +47,12 @@ int halo_op_repack_q8_0(halo_engine* eng, const void* raw, int8_t* qs, uint16_t*
  * xq [T][cols] int8, xs [T][cols/32] fp32. */
 int halo_op_quantize_q8(halo_engine* eng, const float* x, int8_t* xq, float* xs, uint32_t tokens, uint32_t cols,
                         char* err, size_t errlen);
+/* Two independent activation sets quantized in one launch (each exactly as halo_op_quantize_q8): x0 [tokens][cols0]
+ * and x1 [tokens][cols1]. For a step whose two inputs are ready together (the C1 pass's x and a); no counterpart
+ * in the reference. */
+int halo_op_quantize_q8_pair(halo_engine* eng, const float* x0, int8_t* xq0, float* xs0, uint32_t cols0,
+                             const float* x1, int8_t* xq1, float* xs1, uint32_t cols1, uint32_t tokens, char* err,
+                             size_t errlen);
 
 /* Q8_0 x int8-activation projection for M tokens (FlashNextGpu::MatVec + the batched int8 GEMV,
  * src/engine/flash_next_gpu.cpp:212-254, src/kernels/batch_decode.hip:226-345):

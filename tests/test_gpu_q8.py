@@ -58,6 +58,23 @@ def test_quantizer_bit_exact(dev, tokens, cols):
     assert np.array_equal(gq.download(), xq)
 
 
+@pytest.mark.parametrize("tokens", [1, 3, 16])
+def test_quantizer_pair_bit_exact(dev, tokens):
+    """Two inputs of different widths quantized by one launch: both equal the oracle's quantizer bit for bit."""
+    rng = np.random.default_rng(100 + tokens)
+    x0 = rng.normal(0, 1, (tokens, 2048)).astype(np.float32)
+    x1 = rng.normal(0, 3, (tokens, 4096)).astype(np.float32)
+    x1[0, :32] = 0.0
+    g0, g1 = dev.to_device(x0), dev.to_device(x1)
+    q0, s0 = dev.array((tokens, 2048), np.int8), dev.array((tokens, 64), np.float32)
+    q1, s1 = dev.array((tokens, 4096), np.int8), dev.array((tokens, 128), np.float32)
+    dev.op("quantize_q8_pair", g0.ptr, q0.ptr, s0.ptr, 2048, g1.ptr, q1.ptr, s1.ptr, 4096, tokens)
+    for x, q, sc in ((x0, q0, s0), (x1, q1, s1)):
+        xq, xs = O.quantize(x)
+        assert np.array_equal(q.download(), xq)
+        assert np.array_equal(sc.download().view(np.uint32), xs.view(np.uint32))
+
+
 def test_q8x_cols_two_level_bit_exact(dev):
     rng = np.random.default_rng(7)
     B, cols, xstride = 3, 2048, 2100

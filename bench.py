@@ -80,6 +80,8 @@ def run_gpu(args):
             return run_sample(args, dev, H, res)
         if args.mode == "c1":
             return run_c1(args, dev, H, res)
+        if args.mode == "phases":
+            return run_phases(args, dev, H, res)
         run_c0(args, dev, H, res)
         if not args.quick:
             roof = res["roofline"]
@@ -926,6 +928,111 @@ def _memcpy_d2d(dev, sizes):
     return out
 
 
+def _phases_read(dev, H, kind, nb):
+    """Per-block phase stamps of kernel family `kind` (0 DeltaNet step, 1 decode attention) of the last launch, in us
+    from the launch's first block start: [nb][8]."""
+    buf = np.zeros((2, 4096, 8), np.uint64)
+    err = ctypes.create_string_buffer(256)
+    if H.lib().halo_read_global(dev.handle, b"halo_phase_timing", buf.ctypes.data, buf.nbytes, err, 256) != 0:
+        raise RuntimeError("phase stamps need the timing build: make -C halo-flash_amd timing, then "
+                           "HALO_AMD_LIB=halo-flash_amd/libhalo_flash_amd_timing.so")
+    t = buf[kind, :nb].astype(np.int64)
+    return (t - t[:, 0].min()[None]) * 10 / 1000.0 if nb else t
+
+
+def _phases_summary(samples, names):
+    """Median over launches of (min, median, max over blocks) per stamp, and the median per-block phase lengths."""
+    out = {}
+    for i, nm in enumerate(names):
+        col = np.array([[r[:, i].min(), np.median(r[:, i]), r[:, i].max()] for r in samples])
+        out[nm] = {"min": round(float(np.median(col[:, 0])), 2), "median": round(float(np.median(col[:, 1])), 2),
+                   "max": round(float(np.median(col[:, 2])), 2)}
+    lens = {}
+    for i in range(1, len(names)):
+        d = np.array([np.median(r[:, i] - r[:, i - 1]) for r in samples])
+        lens[f"{names[i - 1]} -> {names[i]}"] = round(float(np.median(d)), 2)
+    return {"stamps_us": out, "phase_us_median_block": lens}
+
+
+def run_phases(args, dev, H, res):
+    """Phase breakdown of two decode kernels with the timing build (HALO_PHASE stamps, 10 ns resolution): the decode
+    attention partials at one session over 8576 positions (`halo_attn_decode_partial`, fp32) and at four sessions
+    sharing an 8192-token prefix with 384 positions each (`halo_attn_decode_partial_mma`, split-fp16), KV rotated over
+    8 pools; and the DeltaNet step of the C4 model (`halo_gdn_step_q8`, the last DeltaNet layer's launch of eager
+    steps at 1 and 4 sessions)."""
+    import ctypes as C
+
+    out = {}
+    Hq, Hkv, D, PAGE, ncopy = 16, 2, 256, 16, 8
+    for S, prefix, suffix in ((1, 0, 8576), (4, 8192, 384)):
+        max_context = prefix + suffix
+        max_pages = -(-max_context // PAGE)
+        total = prefix // PAGE + S * (max_pages - prefix // PAGE)
+        pages = np.zeros((S, max_pages), np.uint32)
+        nxt = prefix // PAGE
+        for s_ in range(S):
+            pages[s_, : prefix // PAGE] = np.arange(prefix // PAGE)
+            pages[s_, prefix // PAGE:] = np.arange(nxt, nxt + max_pages - prefix // PAGE)
+            nxt += max_pages - prefix // PAGE
+        gp, gn = dev.to_device(pages), dev.to_device(np.full(S, max_context, np.uint32))
+        keep, descs = [gp, gn], []
+        for i in range(ncopy):
+            k = dev.array((total, Hkv, PAGE, D), np.float32)
+            v = dev.array((total, Hkv, PAGE, D), np.float32)
+            dev.op("synth_f32", k.ptr, k.nbytes // 4, 100 + i, 1.0)
+            dev.op("synth_f32", v.ptr, v.nbytes // 4, 200 + i, 1.0)
+            keep += [k, v]
+            descs.append(H.PagedKV(k.ptr, v.ptr, gp.ptr, gn.ptr, S, Hkv, D, max_pages, prefix, max_context))
+        q, gate = dev.array((S, Hq, D), np.float32), dev.array((S, Hq, D), np.float32)
+        dev.op("synth_f32", q.ptr, S * Hq * D, 7, 1.0)
+        dev.op("synth_f32", gate.ptr, S * Hq * D, 8, 1.0)
+        oq, os_ = dev.array((S, Hq * D), np.int8), dev.array((S, Hq * D // 32), np.float32)
+        wsb = H.lib().halo_op_attn_decode_workspace_bytes(C.byref(descs[0]), Hq)
+        ws = dev.array(wsb, np.uint8)
+        nb = Hkv * (prefix // 32 + S * (-(-suffix // 32)))
+        samples = []
+        for rep in range(40):
+            dev.op("attn_decode_q8", C.byref(descs[rep % ncopy]), q.ptr, gate.ptr, None, oq.ptr, os_.ptr, Hq, ws.ptr,
+                   wsb)
+            dev.sync()
+            if rep >= 8:
+                samples.append(_phases_read(dev, H, 1, nb))
+        if S == 1:  # halo_attn_decode_partial (fp32 VALU)
+            names = ["start", "queries in LDS (K, V arrived)", "scores", "softmax", "end (weighted V stored)"]
+            cols = [0, 1, 2, 3, 4]
+        else:  # halo_attn_decode_partial_mma (split-fp16 matrix cores)
+            names = ["start", "queries in LDS", "K halves in LDS (K arrived)", "scores",
+                     "softmax + V halves in LDS", "end (weighted V stored)"]
+            cols = [0, 1, 2, 3, 5, 4]
+        out[f"attn_partial_S{S}"] = dict(blocks=nb, kernel="halo_attn_decode_partial" + ("" if S == 1 else "_mma"),
+                                         **_phases_summary([r_[:, cols] for r_ in samples], names))
+        del keep, ws
+    cfg = H.c4_config(max_sessions=4, prefix_tokens=0, max_context=64)
+    model = H.Model(dev, cfg, seed=5)
+    try:
+        rng = np.random.default_rng(0)
+        for S in (1, 4):
+            model.reset()
+            for s_ in range(S):
+                model.set_session(s_, rng.integers(0, cfg.vocab, 16).astype(np.uint32))
+            samples = []
+            for rep in range(12):
+                model.step_eager(S)
+                dev.sync()
+                if rep >= 2:
+                    samples.append(_phases_read(dev, H, 0, S * cfg.gdn_v_heads))
+            out[f"gdn_step_S{S}"] = dict(blocks=S * cfg.gdn_v_heads, **_phases_summary(
+                samples, ["start", "conv + gates (state, prologue arrived)", "q / k norms", "u = S^T k",
+                          "delta", "update + o (state stored)", "o norm", "end (codes stored)"]))
+    finally:
+        model.close()
+    for k_, v_ in out.items():
+        log(f"[bench] phases {k_}: {json.dumps(v_)}")
+    res["phases"] = out
+    res["roofline"] = None
+    return res
+
+
 def run_c0(args, dev, H, res):
     """C0, the headline: exactly args.steps GEMVs timed (after args.warmup untimed), weights rotated over copies."""
     c0_copies = max(2, -(-MIN_ROTATION_BYTES // q8_bytes(4096, 4096)))
@@ -1201,7 +1308,7 @@ def main():
     p.add_argument("--quick", action="store_true", help="only the C0 headline and its roofline")
     p.add_argument("--eager", action="store_true", help="launch without graphs (for profiling kernel durations)")
     p.add_argument("--mode", choices=["all", "c0", "c1", "membw", "moe", "gdn", "c4", "pmc", "attn", "proj", "prefill",
-                                       "pgemm", "sample"],
+                                       "pgemm", "sample", "phases"],
                    default="all",
                    help="c0: only the C0 GEMV loop (for profiling one kernel shape)")
     args = p.parse_args()
@@ -1212,7 +1319,7 @@ def main():
     res = run_gpu(args)
     if args.mode != "all":
         print(json.dumps({k: res.get(k) for k in ("roofline", "c0_tilings", "c1", "membw", "moe", "gdn", "c4", "attn",
-                                                  "proj", "prefill", "sample")}),
+                                                  "proj", "prefill", "sample", "phases")}),
               flush=True)
         return
     line = {

@@ -65,6 +65,7 @@ __device__ __forceinline__ void AttnDecodePartial(
   __shared__ __attribute__((aligned(16))) float sc[kMaxQ][kChunk + 4];  // rows 16-byte aligned: vector reads
   static_assert(kChunk == 32 && kPage == 16, "two pages per chunk, two tokens per 16-lane row");
   const std::uint32_t G = Hq / Hkv, x = blockIdx.x, kvh = x % Hkv, c = x / Hkv;
+  HALO_PHASE(1, 0);
   const std::uint32_t t = threadIdx.x, wave = t / kWave, lane = t % kWave;
   const bool is_prefix = c < prefix_chunks;
   const std::uint32_t sess = is_prefix ? 0 : (c - prefix_chunks) / suffix_chunks;
@@ -194,6 +195,7 @@ __device__ __forceinline__ void AttnDecodePartial(
   }
   if constexpr (!kMma) {
   __syncthreads();
+  HALO_PHASE(1, 1);
   if (owner) {
     // the newest row's K from LDS in place of the pool's (not yet written when the loads were issued)
 #pragma unroll
@@ -235,6 +237,7 @@ __device__ __forceinline__ void AttnDecodePartial(
         }
   }
   __syncthreads();  // the scores are in sc and qs is free: the V rows go there (rows past the visible range as 0)
+  HALO_PHASE(1, 2);
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -258,6 +261,7 @@ __device__ __forceinline__ void AttnDecodePartial(
     }
   }
   __syncthreads();
+  HALO_PHASE(1, 3);
   // weighted V, 8 queries' sums interleaved (each still adds its tokens in order j = 0 .. 31); V and the weights
   // are read from LDS four tokens at a time
   for (std::uint32_t i0 = 0; i0 < nq; i0 += kQG) {
@@ -283,8 +287,10 @@ __device__ __forceinline__ void AttnDecodePartial(
         a_out[static_cast<std::size_t>(slot) * kHd + t] = acc[k];
       }
   }
+  HALO_PHASE(1, 4);
   } else {
   __syncthreads();
+  HALO_PHASE(1, 1);
   // Matrix-core tiles: nqt tiles of 16 query rows (rows past nq repeat the last query and are never stored); the
   // scores are tiles (query tile w / 2, key tile w % 2) of waves w < 2 nqt; each query row's products, softmax and
   // weighted sum depend only on that row, so a query gets the same bits whichever block and batch it is scored in.
@@ -370,6 +376,7 @@ __device__ __forceinline__ void AttnDecodePartial(
     }
   }
   __syncthreads();
+  HALO_PHASE(1, 2);
   const float scale = 1.0f / sqrtf(static_cast<float>(kHd));
   if (score_wave) {
     V4F c4 = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -388,6 +395,7 @@ __device__ __forceinline__ void AttnDecodePartial(
     }
   }
   __syncthreads();
+  HALO_PHASE(1, 3);
   // the K chunk is done with: the V chunk goes to the same LDS as halves transposed, vh / vl [256 dims][32 keys]
   // (chunk c of 8 keys of a dim row at c ^ ((dim >> 2) & 3))
   _Float16* vh = kh;
@@ -424,6 +432,7 @@ __device__ __forceinline__ void AttnDecodePartial(
     }
   }
   __syncthreads();
+  HALO_PHASE(1, 5);
   // weighted V: output tiles (query tile, 16-dim tile); two query tiles: wave w takes tile w / 2, dim tiles
   // 8 (w % 2) ..; one: dim tiles 4 w .. + 3
   const std::uint32_t pqt = nqt == 2 ? wave / 2 : 0, ndt = nqt == 2 ? 8 : 4, dt0 = nqt == 2 ? 8 * (wave % 2) : 4 * wave;
@@ -450,6 +459,7 @@ __device__ __forceinline__ void AttnDecodePartial(
       }
     }
   }
+  HALO_PHASE(1, 4);
   }
 }
 }  // namespace

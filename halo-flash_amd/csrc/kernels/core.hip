@@ -10,6 +10,10 @@
 #include "sample.hip"
 #include "ref_named.hip"
 
+#ifdef HALO_PHASE_TIMING
+extern "C" __device__ unsigned long long halo_phase_timing[2][4096][8] = {};
+#endif
+
 // Module-scope variable read and written through halo_read_global / halo_write_global (the reference's
 // Device::ReadGlobal / WriteGlobal): the code object's identity {format version, wave size, target, spare}.
 extern "C" __device__ std::uint32_t halo_code_object_info[4] = {1u, 64u, 950u, 0u};

@@ -580,6 +580,7 @@ extern "C" __global__ void __launch_bounds__(512) halo_gdn_step_q8(
   const std::uint32_t cg = t % 32, rg = t / 32, j0 = 4 * cg, i0 = 8 * rg;
   const std::uint32_t Dk = Hk * kD, Dv = Hv * kD, C = 2 * Dk + Dv;
   float* St = state + (static_cast<std::size_t>(s) * Hv + h) * kD * kD;
+  HALO_PHASE(0, 0);
   // the head's state first (64 KB per block, eight 16-byte loads per thread)
   float4 row[8];
 #pragma unroll
@@ -622,6 +623,7 @@ extern "C" __global__ void __launch_bounds__(512) halo_gdn_step_q8(
     gates[1] = halo::Sigmoid(ab[static_cast<std::size_t>(s) * 2 * Hv + Hv + h]);
   }
   __syncthreads();
+  HALO_PHASE(0, 1);
   if (seg < 2) {
     const float sc = 1.0f / sqrtf(part[2 * seg] + part[2 * seg + 1] + eps);
     (seg == 0 ? sq : sk)[i] = y * sc;
@@ -629,6 +631,7 @@ extern "C" __global__ void __launch_bounds__(512) halo_gdn_step_q8(
     sv[i] = y;
   }
   __syncthreads();
+  HALO_PHASE(0, 2);
   // recurrence: u = (decay S)^T k, delta = (v - u) beta, S <- decay S + k delta^T, o = S^T q / sqrt(d)
   const float decay = expf(gates[0]), bt = gates[1];
   float u[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -647,6 +650,7 @@ extern "C" __global__ void __launch_bounds__(512) halo_gdn_step_q8(
 #pragma unroll
   for (int c = 0; c < 4; ++c) red[rg][j0 + c] = u[c];
   __syncthreads();
+  HALO_PHASE(0, 3);
   if (t < kD) {
     float acc = 0.0f;
 #pragma unroll
@@ -654,6 +658,7 @@ extern "C" __global__ void __launch_bounds__(512) halo_gdn_step_q8(
     dl[t] = (sv[t] - acc) * bt;
   }
   __syncthreads();
+  HALO_PHASE(0, 4);
   const float d0 = dl[j0], d1 = dl[j0 + 1], d2 = dl[j0 + 2], d3 = dl[j0 + 3];
   float oo[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -672,6 +677,7 @@ extern "C" __global__ void __launch_bounds__(512) halo_gdn_step_q8(
 #pragma unroll
   for (int c = 0; c < 4; ++c) red[rg][j0 + c] = oo[c];
   __syncthreads();
+  HALO_PHASE(0, 5);
   // output: RMSNorm over the head's 128 values * w * sigmoid(z), quantized per 32 (waves 0 and 1)
   float o = 0.0f;
   if (t < kD) {
@@ -682,6 +688,7 @@ extern "C" __global__ void __launch_bounds__(512) halo_gdn_step_q8(
   const float so = halo::GroupSum(o * o);
   if (lane == 0 && wave < 2) part[wave] = so;
   __syncthreads();
+  HALO_PHASE(0, 6);
   if (t < kD) {
     const float sc = 1.0f / sqrtf((part[0] + part[1]) / static_cast<float>(kD) + eps);
     const std::size_t off = static_cast<std::size_t>(s) * Dv + h * kD + t;
@@ -691,4 +698,5 @@ extern "C" __global__ void __launch_bounds__(512) halo_gdn_step_q8(
     oq[off] = static_cast<std::int8_t>(scale > 0.0f ? static_cast<int>(rintf(v / scale)) : 0);
     if (t % 32 == 0) os[off / 32] = scale;
   }
+  HALO_PHASE(0, 7);
 }

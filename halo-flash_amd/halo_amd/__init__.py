@@ -12,7 +12,8 @@ from pathlib import Path
 import numpy as np
 
 PKG_DIR = Path(__file__).resolve().parent.parent  # halo-flash_amd/
-LIB_PATH = PKG_DIR / "libhalo_flash_amd.so"
+# HALO_AMD_LIB selects another build of the library (the diagnostic `make timing` build)
+LIB_PATH = Path(os.environ["HALO_AMD_LIB"]) if os.environ.get("HALO_AMD_LIB") else PKG_DIR / "libhalo_flash_amd.so"
 
 
 class HaloError(RuntimeError):

@@ -929,15 +929,16 @@ def _memcpy_d2d(dev, sizes):
 
 
 def _phases_read(dev, H, kind, nb):
-    """Per-block phase stamps of kernel family `kind` (0 DeltaNet step, 1 decode attention) of the last launch, in us
-    from the launch's first block start: [nb][8]."""
-    buf = np.zeros((2, 4096, 8), np.uint64)
+    """Per-block phase stamps of kernel family `kind` (0 DeltaNet step, 1 decode attention, 2 RMSNorm-prologue
+    projection, 3 MoE gate/up with routing, 4 MoE router, 5 MoE down) of the last launch, in us from the launch's first
+    block start: [nb][8] (nb an int: blocks 0 .. nb - 1; else an index array of linear block ids)."""
+    buf = np.zeros((6, 4096, 8), np.uint64)
     err = ctypes.create_string_buffer(256)
     if H.lib().halo_read_global(dev.handle, b"halo_phase_timing", buf.ctypes.data, buf.nbytes, err, 256) != 0:
         raise RuntimeError("phase stamps need the timing build: make -C halo-flash_amd timing, then "
                            "HALO_AMD_LIB=halo-flash_amd/libhalo_flash_amd_timing.so")
-    t = buf[kind, :nb].astype(np.int64)
-    return (t - t[:, 0].min()[None]) * 10 / 1000.0 if nb else t
+    t = buf[kind, :nb].astype(np.int64) if isinstance(nb, int) else buf[kind, nb].astype(np.int64)
+    return (t - t[:, 0].min()[None]) * 10 / 1000.0 if len(t) else t
 
 
 def _phases_summary(samples, names):
@@ -1015,12 +1016,26 @@ def run_phases(args, dev, H, res):
             model.reset()
             for s_ in range(S):
                 model.set_session(s_, rng.integers(0, cfg.vocab, 16).astype(np.uint32))
-            samples = []
+            samples, extra = [], {2: [], 3: [], 4: []}
+            # the last layer (attention: q|gate + k + v = 9216 rows, 64 per block) input projection, and the last
+            # MoE layer's router (129 blocks) and gate/up blocks of the 10 routed slots (grid 11 x 128)
+            nbs = {2: 144, 3: np.array([x + 11 * y for y in range(128) for x in range(10)]), 4: 129}
             for rep in range(12):
                 model.step_eager(S)
                 dev.sync()
                 if rep >= 2:
                     samples.append(_phases_read(dev, H, 0, S * cfg.gdn_v_heads))
+                    if S == 1:
+                        for k_ in extra:
+                            extra[k_].append(_phases_read(dev, H, k_, nbs[k_]))
+            if S == 1:
+                out["proj_n_S1"] = dict(kernel="halo_proj_q8w_l32_t4", blocks=144, **_phases_summary(
+                    extra[2], ["start", "prologue (x arrived, norm, quantized to LDS)", "barrier (all weights issued)", "task 0 dot "
+                               "(its weights arrived)", "end (4 tasks stored)"]))
+                out["moe_gate_up_S1"] = dict(kernel="halo_moe_gate_up_topk_q8_s2_e512", blocks=1280, **_phases_summary(
+                    extra[3], ["start", "wave 0 ranked the logits", "barrier", "dot (weights arrived)", "end"]))
+                out["moe_router_S1"] = dict(kernel="halo_moe_router_n1_h2048", blocks=129, **_phases_summary(
+                    extra[4], ["start", "sums of squares (x and weights arrived)", "x in LDS", "end"]))
             out[f"gdn_step_S{S}"] = dict(blocks=S * cfg.gdn_v_heads, **_phases_summary(
                 samples, ["start", "conv + gates (state, prologue arrived)", "q / k norms", "u = S^T k",
                           "delta", "update + o (state stored)", "o norm", "end (codes stored)"]))

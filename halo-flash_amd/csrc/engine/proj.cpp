@@ -110,19 +110,25 @@ extern "C" int halo_op_proj_q8_grid(halo_engine* eng, const halo_q8_matrix* mats
   // for one task per wave, which keeps the most waves (and loads) in flight.
   std::uint32_t tpw = (in->mode == HALO_PROJ_N || in->mode == HALO_PROJ_G) ? 4 : 1;
   if (grid_blocks == 1 || grid_blocks == 2 || grid_blocks == 4) tpw = grid_blocks;  // tuning override
-  const std::uint32_t blocks = CeilDiv(off[4], 4 * tpw);
+  // One token in mode N with rows of at most 2048 columns: the 8-wave kernel (halo_proj_q8w_*), whose waves 4-7
+  // stream weights while waves 0-3 form the normalized row.
+  const bool wide = in->mode == HALO_PROJ_N && tokens == 1 && lpr <= 32;
+  const std::uint32_t blocks = CeilDiv(off[4], (wide ? 8 : 4) * tpw);
   auto mat = [&](std::uint32_t i) { return i < n_mats ? mats[i] : mats[0]; };
   auto out = [&](std::uint32_t i) { return i < n_mats ? ys[i] : ys[0]; };
   auto rows = [&](std::uint32_t i) { return i < n_mats ? mats[i].rows : 0u; };
   char name[64];
-  std::snprintf(name, sizeof name, "halo_proj_q8%s_l%u_b%u_t%u", letter, lpr, nb, tpw);
+  if (wide)
+    std::snprintf(name, sizeof name, "halo_proj_q8w_l%u_t%u", lpr, tpw);
+  else
+    std::snprintf(name, sizeof name, "halo_proj_q8%s_l%u_b%u_t%u", letter, lpr, nb, tpw);
   const halo_arg a[] = {Ptr(in->x), Ptr(in->delta), Ptr(in->norm_w), Ptr(in->res_out), Ptr(in->xq), Ptr(in->xs),
                         Ptr(in->xq_out), Ptr(in->xs_out),
                         Ptr(mat(0).qs), Ptr(mat(0).d), Ptr(out(0)), Ptr(mat(1).qs), Ptr(mat(1).d), Ptr(out(1)),
                         Ptr(mat(2).qs), Ptr(mat(2).d), Ptr(out(2)), Ptr(mat(3).qs), Ptr(mat(3).d), Ptr(out(3)),
                         U32(rows(0)), U32(rows(1)), U32(rows(2)), U32(rows(3)), U32(off[1]), U32(off[2]), U32(off[3]),
                         U32(off[4]), U32(tokens), U32(cols), Val(in->eps)};
-  return Launch(eng, name, D3(blocks), D3(256), a, err, errlen);
+  return Launch(eng, name, D3(blocks), D3(wide ? 512 : 256), a, err, errlen);
 }
 
 extern "C" int halo_op_proj_q8(halo_engine* eng, const halo_q8_matrix* mats, float* const* ys, uint32_t n_mats,

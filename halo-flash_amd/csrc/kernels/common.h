@@ -9,14 +9,16 @@
 #include <cstdint>
 
 // Phase timing (diagnostic builds only, `make timing`): HALO_PHASE(k, i) records the device wall clock (wall_clock64,
-// 100 MHz) at point i (< 8) of block blockIdx.x (< 4096) of kernel family k (0: the DeltaNet decode step, 1: the decode
-// attention partials) into the code object's halo_phase_timing[k], read back with halo_read_global. In the product
-// build it is empty.
+// 100 MHz) at point i (< 8) of block blockIdx.x + gridDim.x blockIdx.y (< 4096) of kernel family k (0: the DeltaNet
+// decode step, 1: the decode attention partials, 2: the RMSNorm-prologue projections, 3: the MoE gate/up launch with
+// the routing, 4: the MoE router with the FFN norm, 5: MoE down + combine) into the code object's
+// halo_phase_timing[k], read back with halo_read_global. In the product build it is empty.
 #ifdef HALO_PHASE_TIMING
-extern "C" __device__ unsigned long long halo_phase_timing[2][4096][8];
+extern "C" __device__ unsigned long long halo_phase_timing[6][4096][8];
 #define HALO_PHASE(k, i)                                                                                   \
   do {                                                                                                     \
-    if (threadIdx.x == 0 && blockIdx.x < 4096) halo_phase_timing[k][blockIdx.x][i] = wall_clock64();      \
+    const unsigned b_ = blockIdx.x + gridDim.x * blockIdx.y;                                             \
+    if (threadIdx.x == 0 && b_ < 4096) halo_phase_timing[k][b_][i] = wall_clock64();                     \
   } while (0)
 #else
 #define HALO_PHASE(k, i) \

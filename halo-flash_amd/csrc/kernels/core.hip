@@ -11,7 +11,7 @@
 #include "ref_named.hip"
 
 #ifdef HALO_PHASE_TIMING
-extern "C" __device__ unsigned long long halo_phase_timing[2][4096][8] = {};
+extern "C" __device__ unsigned long long halo_phase_timing[6][4096][8] = {};
 #endif
 
 // Module-scope variable read and written through halo_read_global / halo_write_global (the reference's

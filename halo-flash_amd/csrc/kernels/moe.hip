@@ -101,6 +101,7 @@ __device__ __forceinline__ void MoeRouterN(const float* __restrict__ router, con
   const float* row = r < E ? router + static_cast<std::size_t>(r) * H : sgate;
   const bool live = r < E || (r == E && sgate != nullptr);
   const float* rowc = live ? row : router;  // a valid address either way; the result is dropped
+  HALO_PHASE(4, 0);
   float4 w[kF4];
 #pragma unroll
   for (int i = 0; i < static_cast<int>(kF4); ++i) w[i] = reinterpret_cast<const float4*>(rowc)[lane + kWave * i];
@@ -127,6 +128,7 @@ __device__ __forceinline__ void MoeRouterN(const float* __restrict__ router, con
     if (lane == 0) red[t][wave] = ss;
   }
   __syncthreads();
+  HALO_PHASE(4, 1);
 #pragma unroll
   for (int t = 0; t < static_cast<int>(kMaxT); ++t) {
     const float ss = ((red[t][0] + red[t][1]) + red[t][2]) + red[t][3];
@@ -153,6 +155,7 @@ __device__ __forceinline__ void MoeRouterN(const float* __restrict__ router, con
       dst[1] = make_float4(x[t].v[k][4], x[t].v[k][5], x[t].v[k][6], x[t].v[k][7]);
     }
   __syncthreads();
+  HALO_PHASE(4, 2);
   if (!live) return;
   for (std::uint32_t t = 0; t < T; ++t) {
     float acc = 0.0f;
@@ -169,6 +172,7 @@ __device__ __forceinline__ void MoeRouterN(const float* __restrict__ router, con
         sgl[t] = acc;
     }
   }
+  HALO_PHASE(4, 3);
 }
 
 // _n: T <= 4; _n1: T = 1 (one residual row loaded, not four).
@@ -552,12 +556,15 @@ __device__ __forceinline__ void MoeGateUp(
   } else {
     if (blockIdx.y * (blockDim.x / kWave) >= ff) return;
     if constexpr (kTopKPer > 0) {
+      HALO_PHASE(3, 0);
       if (wave == 0) {
         const bool first = blockIdx.x == 0 && blockIdx.y == 0;
         WaveTopK<kTopKPer>(logits, E, k, first ? ids_out : nullptr, first ? w_out : nullptr, ids_l, first ? w_l : nullptr,
                            tsc[0]);
+        HALO_PHASE(3, 1);
       }
       __syncthreads();
+      HALO_PHASE(3, 2);
       ids = ids_l;
     }
     e = ids[px];
@@ -623,10 +630,12 @@ __device__ __forceinline__ void MoeGateUp(
       g += sw[0][st] * (sx * static_cast<float>(Dot16(w[0][st], xv)));
       u += sw[1][st] * (sx * static_cast<float>(Dot16(w[1][st], xv)));
     }
+    if constexpr (kTopKPer > 0) HALO_PHASE(3, 3);
     g = halo::GroupSum(g);
     u = halo::GroupSum(u);
     if (lane == 0) h[static_cast<std::size_t>(row) * hstride + j] = halo::Silu(g) * u;
   }
+  if constexpr (kTopKPer > 0) HALO_PHASE(3, 4);
 }
 
 #define HALO_MOE_GATE_UP(S)                                                                                        \

@@ -65,7 +65,52 @@ __device__ __forceinline__ void LoadTask(RowLoad<LPR>& w, std::uint32_t task, st
   }
 }
 
-template <int LPR, int NB, int kMode, int TPW>
+// The mode-n prologue of one row (n <= 2048) for waves 0-3 of a block without a block barrier: each wave loads
+// the whole residual row and forms the sum of squares of all four waves itself, with the arithmetic of
+// halo::LoadRow8 / RmsNormRow8W (lane l's partial j is thread l + 64 j's, GroupSum adds the same lanes in the same
+// tree, the four wave sums are added in order: the same bits), then normalizes and quantizes its own chunk as
+// thread threadIdx.x of the 256-thread layout. Block 0 writes res + delta to res_out and, with xq_out, the codes.
+__device__ __forceinline__ void WideNormRow(const float* __restrict__ x, const float* __restrict__ delta,
+                                            const float* __restrict__ nw, float* __restrict__ res_out,
+                                            std::int8_t* __restrict__ xq_out, float* __restrict__ xs_out,
+                                            std::uint32_t n, float eps, std::int8_t* lxq, float* lxs) {
+  const std::uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  float v[4][8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const std::uint32_t c = lane + 64u * j, cc = min(c, n / 8 - 1);
+    const float4 a = reinterpret_cast<const float4*>(x)[2 * cc], b = reinterpret_cast<const float4*>(x)[2 * cc + 1];
+    const float* dsrc = delta != nullptr ? delta : x;
+    const float on = delta != nullptr ? 1.0f : 0.0f;
+    const float4 e = reinterpret_cast<const float4*>(dsrc)[2 * cc], f = reinterpret_cast<const float4*>(dsrc)[2 * cc + 1];
+    const float xv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w}, dv[8] = {e.x, e.y, e.z, e.w, f.x, f.y, f.z, f.w};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[j][k] = c < n / 8 ? xv[k] + dv[k] * on : 0.0f;
+  }
+  halo::Row8<1> w8;
+  halo::LoadRow8(nw, nullptr, n, w8);
+  float ws[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(v[j][e], v[j][e], ss);
+    ws[j] = halo::GroupSum(ss);
+  }
+  const float ss = ((ws[0] + ws[1]) + ws[2]) + ws[3];
+  const float scale = 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
+  halo::Row8<1> row;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) row.v[0][e] = wave == 0 ? v[0][e] : wave == 1 ? v[1][e] : wave == 2 ? v[2][e] : v[3][e];
+  if (blockIdx.x == 0 && res_out != nullptr && delta != nullptr) halo::StoreRow8(res_out, n, row);
+  if (threadIdx.x < n / 8)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) row.v[0][e] = row.v[0][e] * scale * w8.v[0][e];
+  halo::QuantRow8(row, n, lxq, lxs);
+  if (blockIdx.x == 0 && xq_out != nullptr) halo::QuantRow8(row, n, xq_out, xs_out);
+}
+
+template <int LPR, int NB, int kMode, int TPW, bool kWide = false>
 __device__ __forceinline__ void ProjQ8(const float* __restrict__ x, const float* __restrict__ delta,
                                        const float* __restrict__ nw, float* __restrict__ res_out,
                                        const std::int8_t* __restrict__ xq_in, const float* __restrict__ xs_in,
@@ -83,12 +128,14 @@ __device__ __forceinline__ void ProjQ8(const float* __restrict__ x, const float*
   constexpr int P = kWave / LPR;  // rows per task
   constexpr std::uint32_t kStep = LPR * 16;
   const std::uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, nblk = cols / 32;
-  // TPW tasks per wave: block b covers tasks [4 TPW b, 4 TPW (b + 1)), wave w the tasks 4 TPW b + 4 i + w
-  const std::uint32_t task0 = blockIdx.x * (blockDim.x / kWave) * TPW + wave;
+  // TPW tasks per wave: block b covers tasks [W TPW b, W TPW (b + 1)), wave w the tasks W TPW b + W i + w (W waves)
+  constexpr std::uint32_t kWaves = kWide ? 8 : 4;
+  const std::uint32_t task0 = blockIdx.x * kWaves * TPW + wave;
   // Order of issue: token 0's prologue inputs (L2 hits), then the weights of this wave's first two tasks (HBM),
   // so the prologue of token 0 waits only for its own loads while the weight stream is in flight.
   // 2048-column chunks of the row per 256 threads: cols <= 64 LPR, so one chunk unless LPR = 64
   constexpr int KC = LPR == 64 ? 2 : 1;
+  static_assert(!kWide || (kMode == 2 && NB == 1 && KC == 1), "the 8-wave form: one token, RMSNorm prologue");
   halo::Row8<KC> row, aux;
   float w8[8];
   int4 xv = make_int4(0, 0, 0, 0);
@@ -129,24 +176,45 @@ __device__ __forceinline__ void ProjQ8(const float* __restrict__ x, const float*
     }
   };
   static_assert(kProjMaxCols / 16 <= 256, "one 16-byte piece of a quantized row per thread");
+  RowLoad<LPR> cur[TPW];
+  if constexpr (kMode == 2) HALO_PHASE(2, 0);
+  if constexpr (kWide) {
+    // 8 waves: waves 0-3 form the normalized, quantized row without a block barrier (WideNormRow) and only then
+    // issue their weight loads; waves 4-7 issue theirs at once. A wave's loads issue in order and stall while the
+    // weight stream is queued, so a prologue placed behind its own weight loads, or waiting at a barrier for waves
+    // that are, would finish only once most of the stream is in flight.
+    if (wave < 4) {
+      WideNormRow(x, delta, nw, res_out, xq_out, xs_out, cols, eps, &lxq[0][0], &lxs[0][0]);
+      HALO_PHASE(2, 1);
+    }
+#pragma unroll
+    for (int i = 0; i < TPW; ++i)
+      LoadTask<LPR>(cur[i], min(task0 + kWaves * i, o4 - 1), o1, o2, o3, qs0, d0, rows0, qs1, d1, rows1, qs2, d2, rows2,
+                    qs3, d3, rows3, cols);
+  } else {
   load_token(0);
   // The tasks' loads are unconditional (a load in a conditional block costs a vmcnt(0) wait at the join): a
   // wave past the end of the list reloads the last task and stores nothing.
-  RowLoad<LPR> cur[TPW];
 #pragma unroll
   for (int i = 0; i < TPW; ++i)
-    LoadTask<LPR>(cur[i], min(task0 + 4u * i, o4 - 1), o1, o2, o3, qs0, d0, rows0, qs1, d1, rows1, qs2, d2, rows2,
+    LoadTask<LPR>(cur[i], min(task0 + kWaves * i, o4 - 1), o1, o2, o3, qs0, d0, rows0, qs1, d1, rows1, qs2, d2, rows2,
                   qs3, d3, rows3, cols);
   finish_token(0);
+  if constexpr (kMode == 2) HALO_PHASE(2, 1);
   for (std::uint32_t b = 1; b < T; ++b) {
     load_token(b);
     finish_token(b);
   }
+  }
   __syncthreads();
+  if constexpr (kMode == 2) HALO_PHASE(2, 2);
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
-    const std::uint32_t task = task0 + 4u * i;
+    const std::uint32_t task = task0 + kWaves * i;
     if (task >= o4) break;
+    if constexpr (kMode == 2) {
+      if (i == 1) HALO_PHASE(2, 3);
+    }
     float acc[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = 0.0f;
@@ -174,6 +242,7 @@ __device__ __forceinline__ void ProjQ8(const float* __restrict__ x, const float*
       for (int b = 0; b < NB; ++b)
         if (b < static_cast<int>(T)) y[static_cast<std::size_t>(b) * rows + r] = acc[b];
   }
+  if constexpr (kMode == 2) HALO_PHASE(2, 4);
 }
 
 }  // namespace
@@ -200,6 +269,26 @@ __device__ __forceinline__ void ProjQ8(const float* __restrict__ x, const float*
   HALO_PROJ_Q8_T(MODE, LETTER, LPR, 8)
 #define HALO_PROJ_Q8_L(MODE, LETTER) \
   HALO_PROJ_Q8_NB(MODE, LETTER, 64) HALO_PROJ_Q8_NB(MODE, LETTER, 32) HALO_PROJ_Q8_NB(MODE, LETTER, 16)
+// grid (ceil(o_4 / (8 TPW))), block 512: the mode-n kernel of one token, waves 4-7 streaming weights while waves 0-3
+// form the normalized row (LPR <= 32, cols <= 2048); otherwise as above.
+#define HALO_PROJ_Q8W(LPR, TPW)                                                                                    \
+  extern "C" __global__ void __launch_bounds__(512) halo_proj_q8w_l##LPR##_t##TPW(                                \
+      const float* x, const float* delta, const float* nw, float* res_out, const std::int8_t* xq_in,           \
+      const float* xs_in, std::int8_t* xq_out, float* xs_out, const std::int8_t* qs0, const std::uint16_t* d0,   \
+      float* y0, const std::int8_t* qs1, const std::uint16_t* d1, float* y1, const std::int8_t* qs2,            \
+      const std::uint16_t* d2, float* y2, const std::int8_t* qs3, const std::uint16_t* d3, float* y3,           \
+      std::uint32_t rows0, std::uint32_t rows1, std::uint32_t rows2, std::uint32_t rows3, std::uint32_t o1,     \
+      std::uint32_t o2, std::uint32_t o3, std::uint32_t o4, std::uint32_t T, std::uint32_t cols, float eps) {   \
+    ProjQ8<LPR, 1, 2, TPW, true>(x, delta, nw, res_out, xq_in, xs_in, xq_out, xs_out, qs0, d0, y0, qs1, d1, y1, qs2, \
+                                 d2, y2, qs3, d3, y3, rows0, rows1, rows2, rows3, o1, o2, o3, o4, T, cols, eps); \
+  }
+HALO_PROJ_Q8W(32, 1)
+HALO_PROJ_Q8W(32, 2)
+HALO_PROJ_Q8W(32, 4)
+HALO_PROJ_Q8W(16, 1)
+HALO_PROJ_Q8W(16, 2)
+HALO_PROJ_Q8W(16, 4)
+#undef HALO_PROJ_Q8W
 HALO_PROJ_Q8_L(0, q)
 HALO_PROJ_Q8_L(1, f)
 HALO_PROJ_Q8_L(2, n)

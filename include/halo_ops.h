@@ -95,7 +95,9 @@ int halo_op_proj_q8(halo_engine* eng, const halo_q8_matrix* mats, float* const* 
 /* The same with an explicit tiling for tuning: tasks per wave (1 / 2 / 4 rows groups per wave, so the prologue
  * runs once per 4 x that many groups) and lanes per row (16 / 32 / 64); 0 keeps the default of each. Mode Q with
  * 9..16 tokens and 1024, 2048 or 4096 columns runs on int8 matrix cores (halo_proj_q8m_c*, 16-row tasks);
- * tasks_per_wave = lanes_per_row = 2 selects that kernel from 1 token, = 1 the VALU kernel (8 tokens at most). */
+ * tasks_per_wave = lanes_per_row = 2 selects that kernel from 1 token, = 1 the VALU kernel (8 tokens at most).
+ * Mode N at one token with 16 or 32 lanes per row runs the 8-wave form (halo_proj_q8w_*: waves 4-7 stream weights
+ * while waves 0-3 form the normalized row); its outputs equal the 4-wave kernel's bit for bit. */
 int halo_op_proj_q8_grid(halo_engine* eng, const halo_q8_matrix* mats, float* const* ys, uint32_t n_mats,
                          const halo_proj_input* in, uint32_t tokens, uint32_t tasks_per_wave, uint32_t lanes_per_row,
                          char* err, size_t errlen);

@@ -142,6 +142,42 @@ def test_proj_mode_n_matches_norm_kernel(dev, tokens, cols, with_delta):
         _check_y(y.download(), want, mag)
 
 
+@pytest.mark.parametrize("cols,with_delta", [(2048, True), (1024, False)])
+def test_proj_mode_n_one_token_every_tiling(dev, cols, with_delta):
+    """At one token the RMSNorm prologue runs in one wave (lanes playing the 256-thread layout); every tiling gives
+    the norm kernel's residual, codes and scales and the same outputs bit for bit."""
+    rng = np.random.default_rng(cols + 7)
+    shapes = [(1024, cols), (512, cols), (64, cols)]
+    host, ws = _mats(dev, rng, shapes)
+    res = rng.normal(0, 1, (1, cols)).astype(np.float32)
+    delta = rng.normal(0, 0.5, (1, cols)).astype(np.float32)
+    w = (1.0 + 0.1 * rng.normal(0, 1, cols)).astype(np.float32)
+    gres, gdel, gw = dev.to_device(res), dev.to_device(delta), dev.to_device(w)
+    r2 = dev.to_device(res)
+    xn2 = dev.array((1, cols), np.float32)
+    xq2, xs2 = dev.array((1, cols), np.int8), dev.array((1, cols // 32), np.float32)
+    dev.launch("halo_add_rmsnorm_q8", (1,), (256,),
+               [r2, gdel if with_delta else None, gw, xn2, xq2, xs2, ("u32", cols), ("f32", 1e-6)])
+    for lpr in (16, 32, 64):
+        if cols > 64 * lpr:
+            continue
+        for tpw in (1, 2, 4):
+            rout = dev.array((1, cols), np.float32)
+            xq_o, xs_o = dev.array((1, cols), np.int8), dev.array((1, cols // 32), np.float32)
+            outs = [dev.array((1, r), np.float32) for r, _ in shapes]
+            inp = H.ProjInput(x=gres.ptr, delta=gdel.ptr if with_delta else None, norm_w=gw.ptr, res_out=rout.ptr,
+                              xq_out=xq_o.ptr, xs_out=xs_o.ptr, eps=1e-6, mode=H.PROJ_N)
+            H.proj_q8(dev, ws, outs, inp, 1, tpw, lpr)
+            if with_delta:
+                assert np.array_equal(rout.download().view(np.uint32), (res + delta).view(np.uint32))
+            assert np.array_equal(xq_o.download(), xq2.download()), (lpr, tpw)
+            assert np.array_equal(xs_o.download().view(np.uint32), xs2.download().view(np.uint32)), (lpr, tpw)
+            xq, xs = xq2.download(), xs2.download()
+            for (qs, d), y in zip(host, outs):
+                want, mag = O.gemv_q8a8(qs, d, xq, xs)
+                _check_y(y.download(), want, mag)
+
+
 def test_proj_rejects_bad_shapes(dev):
     rng = np.random.default_rng(5)
     _, ws = _mats(dev, rng, [(64, 2048), (64, 1024)])

@@ -75,6 +75,54 @@ def test_quantizer_pair_bit_exact(dev, tokens):
         assert np.array_equal(sc.download().view(np.uint32), xs.view(np.uint32))
 
 
+def _near_tie_rows(rng, tokens, cols):
+    """Rows whose 32-value blocks hold an amax and 31 values within a few ulps of (k + 1/2) * scale: quotients at
+    half-integers, where any quotient other than the IEEE one (a reciprocal times v) can round the other way."""
+    nb = tokens * cols // 32
+    amax = (np.abs(rng.normal(0, 1, nb)) * 10.0 ** rng.integers(-6, 6, nb) + 1e-3).astype(np.float32)
+    scale = (amax / np.float32(127.0)).astype(np.float32)
+    k = rng.integers(-127, 127, (nb, 31)).astype(np.float32)
+    v = ((k + np.float32(0.5)) * scale[:, None]).astype(np.float32)
+    steps = rng.integers(-3, 4, v.shape)
+    for s_ in range(1, 4):
+        v = np.where(steps >= s_, np.nextafter(v, np.float32(np.inf)), v)
+        v = np.where(steps <= -s_, np.nextafter(v, np.float32(-np.inf)), v)
+    v = np.clip(v, -amax[:, None], amax[:, None])
+    blocks = np.concatenate([amax[:, None], v], 1).astype(np.float32)
+    blocks = np.take_along_axis(blocks, rng.permuted(np.tile(np.arange(32), (nb, 1)), axis=1), 1)
+    return blocks.reshape(tokens, cols)
+
+
+def test_quantizers_near_ties_bit_exact(dev):
+    """Every quantizer's codes equal the oracle's IEEE-quotient codes on values placed at half-integer quotients:
+    the standalone and pair quantizers (halo::QuantQuad) and a projection prologue's quantized copy of its input
+    (halo::QuantRow8)."""
+    rng = np.random.default_rng(2024)
+    x = _near_tie_rows(rng, 3, 2048)
+    xq, xs = O.quantize(x)
+    gx = dev.to_device(x)
+    gq, gs = dev.array((3, 2048), np.int8), dev.array((3, 64), np.float32)
+    dev.op("quantize_q8", gx.ptr, gq.ptr, gs.ptr, 3, 2048)
+    assert np.array_equal(gs.download().view(np.uint32), xs.view(np.uint32))
+    assert np.array_equal(gq.download(), xq)
+    x1 = _near_tie_rows(rng, 3, 4096)
+    g1 = dev.to_device(x1)
+    q0, s0 = dev.array((3, 2048), np.int8), dev.array((3, 64), np.float32)
+    q1, s1 = dev.array((3, 4096), np.int8), dev.array((3, 128), np.float32)
+    dev.op("quantize_q8_pair", gx.ptr, q0.ptr, s0.ptr, 2048, g1.ptr, q1.ptr, s1.ptr, 4096, 3)
+    assert np.array_equal(q0.download(), xq)
+    x1q, x1s = O.quantize(x1)
+    assert np.array_equal(q1.download(), x1q)
+    assert np.array_equal(s1.download().view(np.uint32), x1s.view(np.uint32))
+    for tokens in (1, 3):
+        ws = [H.Q8Weights(dev, 64, 2048).synth(dev, seed=3)]
+        ys = [dev.array((tokens, 64), np.float32)]
+        xo, so = dev.array((tokens, 2048), np.int8), dev.array((tokens, 64), np.float32)
+        H.proj_q8(dev, ws, ys, H.ProjInput(x=gx.ptr, xq_out=xo.ptr, xs_out=so.ptr, mode=H.PROJ_F), tokens)
+        assert np.array_equal(xo.download(), xq[:tokens])
+        assert np.array_equal(so.download().view(np.uint32), xs[:tokens].view(np.uint32))
+
+
 def test_q8x_cols_two_level_bit_exact(dev):
     rng = np.random.default_rng(7)
     B, cols, xstride = 3, 2048, 2100

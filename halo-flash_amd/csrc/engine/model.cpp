@@ -267,7 +267,9 @@ int Record(halo_model* m, std::uint32_t S, std::uint32_t prefix, char* err, std:
                               Ptr(L.conv_w.device), Ptr(L.a.device), Ptr(L.dt.device), Ptr(L.norm_w.device), Ptr(st),
                               Ptr(m->nkv.device), Ptr(m->oq.device), Ptr(m->os.device), U32(Hk), U32(Hv),
                               U32(c.conv_kernel), Val(eps)};
-        if (Launch(eng, "halo_gdn_step_q8", D3(S * Hv), D3(512), a, err, errlen) != 0) return -1;
+        if (Launch(eng, c.conv_kernel <= 4 ? "halo_gdn_step_q8" : "halo_gdn_step_q8_kn", D3(S * Hv), D3(512), a, err,
+                   errlen) != 0)
+          return -1;
       }
       if (save("oq", HALO_TRACE_I8, m->oq.device, static_cast<std::size_t>(S) * Dv) != 0 ||
           save("os", HALO_TRACE_F32, m->os.device, static_cast<std::size_t>(S) * Dv / 32) != 0)

@@ -565,7 +565,10 @@ extern "C" __global__ void __launch_bounds__(512)
 //   qkv [S][C] (C = 2 Hk d + Hv d), z [S][Hv d], ab [S][2 Hv] (alpha | beta logits), ring [S][K][C], conv_w [C][K],
 //   a, dt [Hv], norm_w [d], state [S][Hv][d][d] key-major fp32 (in place) -> oq [S][Hv d] int8, os [S][Hv d / 32].
 // grid (S * Hv), block 512: thread t owns state rows 8 (t / 32) .. + 8 and columns 4 (t % 32) .. + 4. d = 128.
-extern "C" __global__ void __launch_bounds__(512) halo_gdn_step_q8(
+// halo_gdn_step_q8 takes K <= 4 (the ring slots in registers, loaded before the state), _kn any K <= 8.
+namespace {
+template <bool kSmallK>
+__device__ __forceinline__ void GdnStepQ8(
     const float* __restrict__ qkv, const float* __restrict__ z, const float* __restrict__ ab, float* __restrict__ ring,
     const float* __restrict__ conv_w, const float* __restrict__ a, const float* __restrict__ dt,
     const float* __restrict__ norm_w, float* __restrict__ state, const std::uint32_t* __restrict__ nkv,
@@ -581,10 +584,6 @@ extern "C" __global__ void __launch_bounds__(512) halo_gdn_step_q8(
   const std::uint32_t Dk = Hk * kD, Dv = Hv * kD, C = 2 * Dk + Dv;
   float* St = state + (static_cast<std::size_t>(s) * Hv + h) * kD * kD;
   HALO_PHASE(0, 0);
-  // the head's state first (64 KB per block, eight 16-byte loads per thread)
-  float4 row[8];
-#pragma unroll
-  for (int r = 0; r < 8; ++r) row[r] = *reinterpret_cast<const float4*>(St + static_cast<std::size_t>(i0 + r) * kD + j0);
   // prologue: threads 0..383 take the q, k and v channels of this head (128 each: waves 0-1, 2-3, 4-5). With K <= 4
   // every ring slot is loaded before the position arrives, so the ring loads do not wait for nkv; the slots are
   // selected by position afterwards.
@@ -592,35 +591,49 @@ extern "C" __global__ void __launch_bounds__(512) halo_gdn_step_q8(
   const std::uint32_t ch = seg == 0 ? kh * kD + i : seg == 1 ? Dk + kh * kD + i : 2 * Dk + h * kD + min(i, kD - 1);
   float* rs = ring + static_cast<std::size_t>(s) * K * C;
   const std::uint32_t pos = nkv[s] - 1;
-  const float zg = t < kD ? z[static_cast<std::size_t>(s) * Dv + h * kD + t] : 0.0f;
+  const float zg = z[static_cast<std::size_t>(s) * Dv + h * kD + min(t, static_cast<std::uint32_t>(kD - 1))];  // t < kD
   float y = 0.0f;
+  // the prologue's loads are issued before the state's (64 KB per block, eight 16-byte loads per thread): loads
+  // complete in order, so the conv and norms below run while the state streams in
+  // (unconditional loads from clamped addresses, selected afterwards: a load under a branch would wait at the join
+  // for every load issued before it, the state's included)
+  const float x = qkv[static_cast<std::size_t>(s) * C + ch];
+  float slot[4], w[4];
+#pragma unroll
+  for (std::uint32_t j = 0; j < 4; ++j) {
+    const std::uint32_t jj = min(j, K - 1);
+    slot[j] = rs[static_cast<std::size_t>(jj) * C + ch];
+    w[j] = conv_w[static_cast<std::size_t>(ch) * K + jj];
+  }
+  const float ga = a[h], gdt = dt[h], galpha = ab[static_cast<std::size_t>(s) * 2 * Hv + h],
+              gbeta = ab[static_cast<std::size_t>(s) * 2 * Hv + Hv + h];
+  __builtin_amdgcn_sched_barrier(0);  // keep the issue order
+  float4 row[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) row[r] = *reinterpret_cast<const float4*>(St + static_cast<std::size_t>(i0 + r) * kD + j0);
+  __builtin_amdgcn_sched_barrier(0);
+  // the conv in every thread (waves 6-7 on a clamped channel, discarded), so the loads above stay where they are
+  float acc;
+  if constexpr (kSmallK) {
+    acc = w[K - 1] * x;
+#pragma unroll
+    for (std::uint32_t j = 0; j < 3; ++j)
+      if (j + 1 < K) acc += w[j] * slot[(pos + 1 + j) % K];
+  } else {
+    acc = conv_w[static_cast<std::size_t>(ch) * K + K - 1] * x;
+    for (std::uint32_t j = 0; j + 1 < K; ++j)
+      acc += conv_w[static_cast<std::size_t>(ch) * K + j] * rs[static_cast<std::size_t>((pos + 1 + j) % K) * C + ch];
+  }
   if (seg < 3) {
-    const float x = qkv[static_cast<std::size_t>(s) * C + ch];
-    float acc;
-    if (K <= 4) {
-      float slot[4], w[4];
-#pragma unroll
-      for (std::uint32_t j = 0; j < 4; ++j) {
-        slot[j] = j < K ? rs[static_cast<std::size_t>(j) * C + ch] : 0.0f;
-        w[j] = j < K ? conv_w[static_cast<std::size_t>(ch) * K + j] : 0.0f;
-      }
-      acc = w[K - 1] * x;
-#pragma unroll
-      for (std::uint32_t j = 0; j < 3; ++j)
-        if (j + 1 < K) acc += w[j] * slot[(pos + 1 + j) % K];
-    } else {
-      acc = conv_w[static_cast<std::size_t>(ch) * K + K - 1] * x;
-      for (std::uint32_t j = 0; j + 1 < K; ++j)
-        acc += conv_w[static_cast<std::size_t>(ch) * K + j] * rs[static_cast<std::size_t>((pos + 1 + j) % K) * C + ch];
-    }
     if (seg == 2 || h < Hk) rs[static_cast<std::size_t>(pos % K) * C + ch] = x;
     y = halo::Silu(acc);
   }
   const float ss = halo::GroupSum(y * y);
   if (lane == 0) part[wave] = ss;
+  const float g0 = ga * halo::Softplus(galpha + gdt), g1 = halo::Sigmoid(gbeta);
   if (t == 0) {
-    gates[0] = a[h] * halo::Softplus(ab[static_cast<std::size_t>(s) * 2 * Hv + h] + dt[h]);
-    gates[1] = halo::Sigmoid(ab[static_cast<std::size_t>(s) * 2 * Hv + Hv + h]);
+    gates[0] = g0;
+    gates[1] = g1;
   }
   __syncthreads();
   HALO_PHASE(0, 1);
@@ -699,4 +712,18 @@ extern "C" __global__ void __launch_bounds__(512) halo_gdn_step_q8(
     if (t % 32 == 0) os[off / 32] = scale;
   }
   HALO_PHASE(0, 7);
+}
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(512) halo_gdn_step_q8(
+    const float* qkv, const float* z, const float* ab, float* ring, const float* conv_w, const float* a,
+    const float* dt, const float* norm_w, float* state, const std::uint32_t* nkv, std::int8_t* oq, float* os,
+    std::uint32_t Hk, std::uint32_t Hv, std::uint32_t K, float eps) {
+  GdnStepQ8<true>(qkv, z, ab, ring, conv_w, a, dt, norm_w, state, nkv, oq, os, Hk, Hv, K, eps);
+}
+extern "C" __global__ void __launch_bounds__(512) halo_gdn_step_q8_kn(
+    const float* qkv, const float* z, const float* ab, float* ring, const float* conv_w, const float* a,
+    const float* dt, const float* norm_w, float* state, const std::uint32_t* nkv, std::int8_t* oq, float* os,
+    std::uint32_t Hk, std::uint32_t Hv, std::uint32_t K, float eps) {
+  GdnStepQ8<false>(qkv, z, ab, ring, conv_w, a, dt, norm_w, state, nkv, oq, os, Hk, Hv, K, eps);
 }

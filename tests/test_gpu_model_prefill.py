@@ -33,9 +33,10 @@ def _flips_ok(rep):
     assert rep.loose <= max(64, rep.codes // 1000)
 
 
-@pytest.mark.parametrize("conv_kernel", [4, 3])
+@pytest.mark.parametrize("conv_kernel", [4, 3, 6])
 def test_ragged_prefill_then_decode(dev, conv_kernel):
-    """conv_kernel 4 takes the register-row prologue (halo_gdn_prep_prefill_k4), 3 the general one; the 16-token
+    """conv_kernel 4 takes the register-row prologue (halo_gdn_prep_prefill_k4), 3 and 6 the general one (6: the
+    decode step with the ring slots read in a loop, halo_gdn_step_q8_kn); the 16-token
     prologue block spans both prompts."""
     cfg = twin(conv_kernel=conv_kernel)
     model = H.Model(dev, cfg, seed=11)

@@ -1033,7 +1033,9 @@ def run_phases(args, dev, H, res):
                     extra[2], ["start", "prologue (x arrived, norm, quantized to LDS)", "barrier (all weights issued)", "task 0 dot "
                                "(its weights arrived)", "end (4 tasks stored)"]))
                 out["moe_gate_up_S1"] = dict(kernel="halo_moe_gate_up_topk_q8_s2_e512", blocks=1280, **_phases_summary(
-                    extra[3], ["start", "wave 0 ranked the logits", "barrier", "dot (weights arrived)", "end"]))
+                    [r_[:, [0, 5, 6, 7, 1, 2, 3, 4]] for r_ in extra[3]],
+                    ["start", "softmax (logits arrived)", "threshold", "candidates in LDS", "wave 0 ranked the logits",
+                     "barrier", "dot (weights arrived)", "end"]))
                 out["moe_router_S1"] = dict(kernel="halo_moe_router_n1_h2048", blocks=129, **_phases_summary(
                     extra[4], ["start", "sums of squares (x and weights arrived)", "x in LDS", "end"]))
             out[f"gdn_step_S{S}"] = dict(blocks=S * cfg.gdn_v_heads, **_phases_summary(

@@ -217,7 +217,7 @@ __device__ __forceinline__ std::uint32_t LanesBelow(std::uint64_t mask) {
 }
 
 template <int kPer>
-__device__ void WaveTopK(const float* logits, std::uint32_t E, std::uint32_t k, std::uint32_t* ids, float* weights,
+__device__ __forceinline__ void WaveTopK(const float* logits, std::uint32_t E, std::uint32_t k, std::uint32_t* ids, float* weights,
                          std::uint32_t* lds_ids, float* lds_w, TopKScratch& sc) {
   const std::uint32_t lane = threadIdx.x % kWave;
   float p[kPer];
@@ -245,6 +245,7 @@ __device__ void WaveTopK(const float* logits, std::uint32_t E, std::uint32_t k, 
     p[i] = e < E ? p[i] / den : -1.0f;
     lm = fmaxf(lm, p[i]);
   }
+  HALO_PHASE(3, 5);
   // tau from a bitwise search over the lane keys (probability bits + 1, 0 for a lane without experts; probabilities
   // are in [0, 1], so their bit patterns order like the values and stay below 2^30). The search keeps the largest thr
   // with at least k keys >= thr, deciding bits 29 .. 18 only: thr is then the k-th largest key with its low 18 bits
@@ -261,6 +262,7 @@ __device__ void WaveTopK(const float* logits, std::uint32_t E, std::uint32_t k, 
     }
     tau = thr == 0 ? -1.0f : __uint_as_float(thr - 1u);
   }
+  HALO_PHASE(3, 6);
   // candidates p >= tau as 64-bit keys, probability bits above and ~id below: a larger key is an earlier slot (ties
   // in probability to the lower id; ids are distinct, so keys are). Every lane stores, a non-candidate (or one past
   // the scratch) into its own spare slot, so no store waits on an exec mask.
@@ -277,6 +279,7 @@ __device__ void WaveTopK(const float* logits, std::uint32_t E, std::uint32_t k, 
   }
   if (lane < 8 && n <= kCandMax) sc.ck[n + lane] = 0;  // pad keys below every candidate: reads past n count nothing
   WaveSync();
+  HALO_PHASE(3, 7);
   if (n <= kCandMax) {
     // candidate c in lane c % 64: its rank = the number of larger keys, read 8 at a time (4 loads in flight)
     for (std::uint32_t c0 = 0; c0 < n; c0 += kWave) {

@@ -249,16 +249,21 @@ __device__ __forceinline__ void WaveTopK(const float* logits, std::uint32_t E, s
   // tau from a bitwise search over the lane keys (probability bits + 1, 0 for a lane without experts; probabilities
   // are in [0, 1], so their bit patterns order like the values and stay below 2^30). The search keeps the largest thr
   // with at least k keys >= thr, deciding bits 29 .. 18 only: thr is then the k-th largest key with its low 18 bits
-  // cleared (within 2^-5 of it), still a lower bound, for 12 dependent ballots instead of 31 at the cost of a few
+  // cleared (within 2^-5 of it), still a lower bound, in 6 dependent steps instead of 31 at the cost of a few
   // more candidates. Every probability is >= 0, so tau = -1 admits all when k > 64.
   float tau = -1.0f;
   if (k <= kWave) {
     const std::uint32_t key = lm >= 0.0f ? __float_as_uint(lm) + 1u : 0u;
     std::uint32_t thr = 0;
+    // two bits per step (three independent ballots; the counts fall as the digit rises, so the largest digit
+    // whose count reaches k is the one two single-bit steps would pick): half the dependent ballot chain
 #pragma unroll
-    for (int bit = 29; bit >= 18; --bit) {
-      const std::uint32_t cand = thr | (1u << bit);
-      if (static_cast<std::uint32_t>(__builtin_popcountll(__ballot(key >= cand))) >= k) thr = cand;
+    for (int bit = 28; bit >= 18; bit -= 2) {
+      const std::uint32_t c1 = thr | (1u << bit), c2 = thr | (2u << bit), c3 = thr | (3u << bit);
+      const std::uint32_t n1 = static_cast<std::uint32_t>(__builtin_popcountll(__ballot(key >= c1)));
+      const std::uint32_t n2 = static_cast<std::uint32_t>(__builtin_popcountll(__ballot(key >= c2)));
+      const std::uint32_t n3 = static_cast<std::uint32_t>(__builtin_popcountll(__ballot(key >= c3)));
+      thr = n3 >= k ? c3 : n2 >= k ? c2 : n1 >= k ? c1 : thr;
     }
     tau = thr == 0 ? -1.0f : __uint_as_float(thr - 1u);
   }

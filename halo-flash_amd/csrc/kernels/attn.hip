@@ -526,49 +526,81 @@ __device__ __forceinline__ void AttnDecodeCombine(
     const std::uint32_t c = i < prefix_chunks ? i : prefix_chunks + s * suffix_chunks + (i - prefix_chunks);
     return static_cast<std::size_t>(c) * Hkv + kvh;
   };
+  // Every load is independent of the others, so all are issued first (unconditionally, from clamped items, then
+  // selected): the items' m and l (n <= 1024: four each per thread), this thread's first two groups of kU weighted
+  // partial sums and its gate value; the arithmetic then runs in the order it always had.
+  const std::uint32_t f = t % kF, ig = t / kF;
+  constexpr int kU = 8;
+  float mv[4], lv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const std::uint32_t i = min(t + 256u * j, n - 1);
+    mv[j] = pm[item(i) * slots + slot];
+    lv[j] = pl[item(i) * slots + slot];
+  }
+  float4 a[2][kU];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const std::uint32_t i = min(ig + kG * (kU * r + u), n - 1);
+      a[r][u] = reinterpret_cast<const float4*>(pacc + (item(i) * slots + slot) * kHd)[quarter * kF + f];
+    }
+  const std::size_t off = (static_cast<std::size_t>(s) * Hq + h) * kHd + quarter * kW + min(t, kW - 1);
+  const float gv = *(gate != nullptr ? gate + (static_cast<std::size_t>(s) * Hq + h) * kGS * kHd + quarter * kW +
+                                           min(t, kW - 1)
+                                     : pl);  // (any valid address without a gate; unused then)
   float M = -INFINITY;
-  for (std::uint32_t i = t; i < n; i += blockDim.x) {
-    const float m = pm[item(i) * slots + slot];
-    wts[i] = m;
-    M = fmaxf(M, m);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const std::uint32_t i = t + 256u * j;
+    if (i < n) {
+      wts[i] = mv[j];
+      M = fmaxf(M, mv[j]);
+    }
   }
   M = halo::GroupMax(M);
   if (t % kWave == 0) red[t / kWave] = M;
   __syncthreads();
   M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   float L = 0.0f;
-  for (std::uint32_t i = t; i < n; i += blockDim.x) {
-    const float m = wts[i];
-    const float w = m == -INFINITY ? 0.0f : expf(m - M);
-    wts[i] = w;
-    L += w * pl[item(i) * slots + slot];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const std::uint32_t i = t + 256u * j;
+    if (i < n) {
+      const float m = mv[j];
+      const float w = m == -INFINITY ? 0.0f : expf(m - M);
+      wts[i] = w;
+      L += w * lv[j];
+    }
   }
   L = halo::GroupSum(L);
   __syncthreads();
   if (t % kWave == 0) red[t / kWave] = L;
   __syncthreads();
   L = (red[0] + red[1]) + (red[2] + red[3]);
-  const std::uint32_t f = t % kF, ig = t / kF;
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  constexpr int kU = 8;
-  for (std::uint32_t i0 = ig; i0 < n; i0 += kG * kU) {
-    float4 a[kU];
+  for (std::uint32_t i0 = ig, r = 0; i0 < n; i0 += kG * kU, ++r) {
+    float4 b[kU];
     float w[kU];
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const std::uint32_t i = i0 + kG * u;
       const float wi = wts[min(i, n - 1)];
       w[u] = i < n ? wi : 0.0f;
-      // load unconditionally (clamped item), then select: an empty chunk's partial is never written
-      const float4 av = reinterpret_cast<const float4*>(pacc + (item(min(i, n - 1)) * slots + slot) * kHd)[quarter * kF + f];
-      a[u] = w[u] == 0.0f ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : av;
+      // past the two preloaded groups: load here (clamped item); an empty chunk's partial is never written
+      const float4 av = r == 0 ? a[0][u]
+                        : r == 1 ? a[1][u]
+                                 : reinterpret_cast<const float4*>(pacc + (item(min(i, n - 1)) * slots + slot) *
+                                                                              kHd)[quarter * kF + f];
+      b[u] = w[u] == 0.0f ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : av;
     }
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-      acc.x += w[u] * a[u].x;
-      acc.y += w[u] * a[u].y;
-      acc.z += w[u] * a[u].z;
-      acc.w += w[u] * a[u].w;
+      acc.x += w[u] * b[u].x;
+      acc.y += w[u] * b[u].y;
+      acc.z += w[u] * b[u].z;
+      acc.w += w[u] * b[u].w;
     }
   }
   part[ig][f] = acc;
@@ -579,8 +611,7 @@ __device__ __forceinline__ void AttnDecodeCombine(
 #pragma unroll
   for (std::uint32_t k = 0; k < kG; ++k) sum += reinterpret_cast<const float*>(&part[k][0])[t];
   float r = sum / L;
-  const std::size_t off = (static_cast<std::size_t>(s) * Hq + h) * kHd + quarter * kW + t;
-  if (gate != nullptr) r *= halo::Sigmoid(gate[(static_cast<std::size_t>(s) * Hq + h) * kGS * kHd + quarter * kW + t]);
+  if (gate != nullptr) r *= halo::Sigmoid(gv);
   if (o != nullptr) o[off] = r;
   if (oq != nullptr) {
     // the row's Q8 quantization for the output projection: 32-value blocks are half waves

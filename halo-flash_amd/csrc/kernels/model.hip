@@ -5,6 +5,8 @@
 // Reference semantics: cpu::RmsNorm / L2Norm / Rope / Silu / Softplus (src/model/cpu_ops.cpp:134-185),
 // ReferenceModel::LinearAttention conv + norms + gate (src/model/reference.cpp:278-366), ReferenceModel::Attention
 // q/gate split, q/k norm, NEOX rope (src/model/reference.cpp:368-416), HaloStepParam (src/kernels/step_params.h).
+#include <type_traits>
+
 #include "common.h"
 #include "halo_sample.h"
 
@@ -30,12 +32,28 @@ extern "C" __global__ void __launch_bounds__(256)
                         std::uint32_t H, float eps) {
   __shared__ float red[4];
   const std::size_t s = blockIdx.x;
-  halo::Row8<4> r;
-  halo::LoadRow8(res + s * H, delta != nullptr ? delta + s * H : nullptr, H, r);
-  if (delta != nullptr) halo::StoreRow8(res + s * H, H, r);
-  halo::RmsNormRow8(r, w, H, eps, red);
-  if (xn != nullptr) halo::StoreRow8(xn + s * H, H, r);
-  if (xq != nullptr) halo::QuantRow8(r, H, xq + s * H, xs + s * (H / 32));
+  // the row and the weights are loaded together (one round trip); rows of at most 2048 take one chunk per thread
+  auto body = [&](auto kc) {
+    constexpr int KC = decltype(kc)::value;
+    halo::Row8<KC> r, wr;
+    halo::LoadRow8(res + s * H, delta != nullptr ? delta + s * H : nullptr, H, r);
+    if (w != nullptr) {
+      halo::LoadRow8(w, nullptr, H, wr);
+    } else {
+#pragma unroll
+      for (int k = 0; k < KC; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) wr.v[k][e] = 1.0f;  // v * scale * 1 = v * scale
+    }
+    if (delta != nullptr) halo::StoreRow8(res + s * H, H, r);
+    halo::RmsNormRow8W(r, wr, H, eps, red);
+    if (xn != nullptr) halo::StoreRow8(xn + s * H, H, r);
+    if (xq != nullptr) halo::QuantRow8(r, H, xq + s * H, xs + s * (H / 32));
+  };
+  if (H <= 2048)
+    body(std::integral_constant<int, 1>{});
+  else
+    body(std::integral_constant<int, 4>{});
 }
 
 // grid (S, C / 256), block 256: the DeltaNet prologue for one token per session, one channel per thread.

@@ -694,22 +694,32 @@ __device__ __forceinline__ void MoeDown(
     std::uint32_t H, std::uint32_t ff, std::uint32_t sff, std::uint32_t k, std::uint32_t hstride) {
   __shared__ float part[33][kDownRows];
   __shared__ float wslot[33];
-  const std::uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, sub = lane / 32, l = lane % 32;
+  // (the wave index through readfirstlane: the compiler then keeps it, and the expert id load, scalar)
+  const std::uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave,
+                      sub = lane / 32, l = lane % 32;
   const std::uint32_t t = blockIdx.y, r0 = blockIdx.x * kDownRows;
   const bool shared = wave == k;
-  // the combine weights are read now, not after the barrier: one dependent round trip less at the end
-  if (threadIdx.x < k) wslot[threadIdx.x] = weights[t * k + threadIdx.x];
-  if (threadIdx.x == k) wslot[k] = sdq != nullptr ? halo::Sigmoid(sgl[t]) : 0.0f;
+  // the combine weights are loaded now (unconditionally, from clamped addresses: a load under a branch would wait
+  // at the join for its round trip before anything else is issued) and put in LDS after the dot products
+  const float wv = weights[t * k + min(threadIdx.x, k - 1)];
+  const float sgv = *(sgl != nullptr ? sgl + t : weights + t * k);
   if (wave < k || (shared && sdq != nullptr)) {
     const std::uint32_t f = shared ? sff : ff;
-    const std::size_t e = shared ? 0 : ids[t * k + wave];
     const std::uint32_t hrow = shared ? T * k + t : t * k + wave;
-    const std::int8_t* base = shared ? sdq : dq + e * H * f;
-    const std::uint16_t* dbase = shared ? sdd : dd + e * H * (f / 32);
     const std::uint32_t c = l * 16;
     const bool in = c < f;
     // loads from a clamped address, then a select: a load under a branch would cost a vmcnt(0) wait
     const std::uint32_t cc = in ? c : 0;
+    // h: lane (sub, l) loads and quantizes values c + 8 sub .. + 7 of the 16 its dot products cover (a 32-value
+    // block spans lanes 2i, 2i + 1 of both halves); the halves then swap their codes. Loads are unconditional, and
+    // issued before the expert id is even read: loads complete in order, so h is in registers, and quantized,
+    // while the weight rows stream in.
+    const float4* hp = reinterpret_cast<const float4*>(h + static_cast<std::size_t>(hrow) * hstride + cc + 8 * sub);
+    const float4 ha = hp[0], hb = hp[1];
+    __builtin_amdgcn_sched_barrier(0);
+    const std::size_t e = shared ? 0 : ids[t * k + wave];
+    const std::int8_t* base = shared ? sdq : dq + e * H * f;
+    const std::uint16_t* dbase = shared ? sdd : dd + e * H * (f / 32);
     int4 q[kDownRows / 2];
     float sw[kDownRows / 2];
 #pragma unroll
@@ -721,10 +731,7 @@ __device__ __forceinline__ void MoeDown(
       q[p] = in ? qv : make_int4(0, 0, 0, 0);
       sw[p] = in ? sv : 0.0f;
     }
-    // h: lane (sub, l) loads and quantizes values c + 8 sub .. + 7 of the 16 its dot products cover (a 32-value
-    // block spans lanes 2i, 2i + 1 of both halves); the halves then swap their codes. Loads are unconditional.
-    const float4* hp = reinterpret_cast<const float4*>(h + static_cast<std::size_t>(hrow) * hstride + cc + 8 * sub);
-    const float4 ha = hp[0], hb = hp[1];
+    __builtin_amdgcn_sched_barrier(0);
     float hv[8] = {ha.x, ha.y, ha.z, ha.w, hb.x, hb.y, hb.z, hb.w};
     float amax = 0.0f;
 #pragma unroll
@@ -754,6 +761,8 @@ __device__ __forceinline__ void MoeDown(
       if (l == 0) part[wave][2 * p + sub] = v;
     }
   }
+  if (threadIdx.x < k) wslot[threadIdx.x] = wv;
+  if (threadIdx.x == k) wslot[k] = sdq != nullptr ? halo::Sigmoid(sgv) : 0.0f;
   __syncthreads();
   if (threadIdx.x < kDownRows && r0 + threadIdx.x < H) {
     float acc = 0.0f;

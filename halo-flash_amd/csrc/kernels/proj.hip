@@ -191,6 +191,30 @@ __device__ __forceinline__ void ProjQ8(const float* __restrict__ x, const float*
     for (int i = 0; i < TPW; ++i)
       LoadTask<LPR>(cur[i], min(task0 + kWaves * i, o4 - 1), o1, o2, o3, qs0, d0, rows0, qs1, d1, rows1, qs2, d2, rows2,
                     qs3, d3, rows3, cols);
+  } else if constexpr (kMode == 0) {
+    // quantized rows: every token's 16 bytes and scale are loaded first (a clamped token past T reloads the last),
+    // then the weights; one round trip for all tokens instead of one per token
+    int4 xvs[NB];
+    float xss[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const std::uint32_t bb = min(static_cast<std::uint32_t>(b), T - 1);
+      xvs[b] = reinterpret_cast<const int4*>(xq_in + static_cast<std::size_t>(bb) * cols)[min(threadIdx.x, cols / 16 - 1)];
+      xss[b] = xs_in[static_cast<std::size_t>(bb) * nblk + min(threadIdx.x, nblk - 1)];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < TPW; ++i)
+      LoadTask<LPR>(cur[i], min(task0 + kWaves * i, o4 - 1), o1, o2, o3, qs0, d0, rows0, qs1, d1, rows1, qs2, d2, rows2,
+                    qs3, d3, rows3, cols);
+    __builtin_amdgcn_sched_barrier(0);
+    // unconditional stores (a thread past the row writes the clamped piece its neighbour writes, the same bytes;
+    // rows past T are never read), so the loads above are not sunk into a branch that waits on them one by one
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      reinterpret_cast<int4*>(&lxq[b][0])[min(threadIdx.x, cols / 16 - 1)] = xvs[b];
+      lxs[b][min(threadIdx.x, nblk - 1)] = xss[b];
+    }
   } else {
   load_token(0);
   // The tasks' loads are unconditional (a load in a conditional block costs a vmcnt(0) wait at the join): a

@@ -1007,6 +1007,22 @@ def run_phases(args, dev, H, res):
             cols = [0, 1, 2, 3, 5, 4]
         out[f"attn_partial_S{S}"] = dict(blocks=nb, kernel="halo_attn_decode_partial" + ("" if S == 1 else "_mma"),
                                          **_phases_summary([r_[:, cols] for r_ in samples], names))
+        # the model's form: from the q | gate, k and v projections (norms, rotation, K / V append in the prologue)
+        qg = dev.array((S, Hq, 2 * D), np.float32)
+        kin, vin = dev.array((S, Hkv, D), np.float32), dev.array((S, Hkv, D), np.float32)
+        wq, wk = dev.array(D, np.float32), dev.array(D, np.float32)
+        for a, sd in ((qg, 9), (kin, 10), (vin, 11), (wq, 12), (wk, 13)):
+            dev.op("synth_f32", a.ptr, a.nbytes // 4, sd, 1.0)
+        samples = []
+        for rep in range(40):
+            dev.op("attn_decode_step_q8", C.byref(descs[rep % ncopy]), qg.ptr, kin.ptr, vin.ptr, wq.ptr, wk.ptr, 64,
+                   1e7, 1e-6, None, oq.ptr, os_.ptr, Hq, ws.ptr, wsb)
+            dev.sync()
+            if rep >= 8:
+                samples.append(_phases_read(dev, H, 1, nb))
+        names[1] = "queries normed in LDS" + (" (K, V arrived)" if S == 1 else "")
+        out[f"attn_step_S{S}"] = dict(blocks=nb, kernel="halo_attn_decode_partial_qk" + ("2" if S == 1 else ""),
+                                      **_phases_summary([r_[:, cols] for r_ in samples], names))
         del keep, ws
     cfg = H.c4_config(max_sessions=4, prefix_tokens=0, max_context=64)
     model = H.Model(dev, cfg, seed=5)

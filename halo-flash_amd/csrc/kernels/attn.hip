@@ -127,9 +127,12 @@ __device__ __forceinline__ void AttnDecodePartial(
 #pragma unroll
     for (int u = 0; u < 4; ++u) kf[h][u] = kr[16 * u + sub];
   }
+  // The V chunk (fused prologue: issued only after the query prologue; a wave's loads issue in order and stall while
+  // the stream is queued, so V issued with K would hold that prologue back, and V is needed only after the scores)
   float4 vq[2][4];
   const std::uint32_t vdg = t % 64, vkg = t / 64;
   float4 vreg[8];
+  auto issue_v = [&]() {
   if constexpr (!kMma) {
   // V as 16-byte loads of the two pages (each page's 16 rows are 16 KB contiguous; thread t takes float4 t of every
   // 4 KB part: row 4 part + t / 64, dims 4 (t % 64) ..): 4-byte loads of a column would take 32 instructions per
@@ -151,6 +154,8 @@ __device__ __forceinline__ void AttnDecodePartial(
     for (int e = 0; e < 8; ++e) vreg[e] = *reinterpret_cast<const float4*>(vp + ((8 * vkg + e) % kPage) * kHd);
   }
   }
+  };
+  if constexpr (!kFused) issue_v();
   // queries of this kv head: slot i = session * G + g (prefix) or g (suffix)
   __shared__ __attribute__((aligned(16))) float knew[kFused ? 2 : 1][kFused ? kHd : 4];
   if constexpr (kFused) {
@@ -193,6 +198,7 @@ __device__ __forceinline__ void AttnDecodePartial(
       reinterpret_cast<float4*>(&qs[qi][0])[d4] = v;
     }
   }
+  if constexpr (kFused) issue_v();
   if constexpr (!kMma) {
   __syncthreads();
   HALO_PHASE(1, 1);
@@ -325,7 +331,7 @@ __device__ __forceinline__ void AttnDecodePartial(
   }
   {  // the block's K and V magnitudes over the visible rows (rows past them repeat the pool's row `last`, which for
      // the owner block is not yet written: the newest row comes from LDS, and the masked rows' scores are dropped)
-    float ka = 0.0f, va = 0.0f;
+    float ka = 0.0f;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const std::uint32_t j = r + 16 * h;
@@ -337,24 +343,11 @@ __device__ __forceinline__ void AttnDecodePartial(
           ka = fmaxf(ka, fmaxf(fmaxf(fabsf(kv.x), fabsf(kv.y)), fmaxf(fabsf(kv.z), fabsf(kv.w))));
         }
     }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const std::uint32_t j = 8 * vkg + e;
-      float4 vv = vreg[e];
-      if (owner && start + j == last) vv = *reinterpret_cast<const float4*>(&knew[kFused ? 1 : 0][4 * vdg]);
-      if (start + j < limit)
-        va = fmaxf(va, fmaxf(fmaxf(fabsf(vv.x), fabsf(vv.y)), fmaxf(fabsf(vv.z), fabsf(vv.w))));
-    }
     ka = halo::GroupMax(ka);
-    va = halo::GroupMax(va);
-    if (lane == 0) {
-      kvmax[0][wave] = ka;
-      kvmax[1][wave] = va;
-    }
+    if (lane == 0) kvmax[0][wave] = ka;
   }
   __syncthreads();  // qs is free: the K chunk goes there as halves
   const float sk = halo::SplitScale(fmaxf(fmaxf(kvmax[0][0], kvmax[0][1]), fmaxf(kvmax[0][2], kvmax[0][3])), kSqk);
-  const float sv = halo::SplitScale(fmaxf(fmaxf(kvmax[1][0], kvmax[1][1]), fmaxf(kvmax[1][2], kvmax[1][3])), kSvv);
   // K halves kh / kl [32 keys][256]: 16-byte chunk c of key row j at c ^ (j & 15) (the 16 lanes of an operand read
   // take 16 different bank groups); the newest row (owner) from LDS, not yet in the pool when it was loaded
   _Float16* kh = reinterpret_cast<_Float16*>(&qs[0][0]);
@@ -394,8 +387,22 @@ __device__ __forceinline__ void AttnDecodePartial(
       if (qi < nq) sc[qi][key] = live ? c4[i] * (scale / (qsc[qi] * sk)) : -INFINITY;
     }
   }
+  {  // the V chunk's magnitude over the visible rows (the newest row from LDS), only now that the scores are done
+    float va = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const std::uint32_t j = 8 * vkg + e;
+      float4 vv = vreg[e];
+      if (owner && start + j == last) vv = *reinterpret_cast<const float4*>(&knew[kFused ? 1 : 0][4 * vdg]);
+      if (start + j < limit)
+        va = fmaxf(va, fmaxf(fmaxf(fabsf(vv.x), fabsf(vv.y)), fmaxf(fabsf(vv.z), fabsf(vv.w))));
+    }
+    va = halo::GroupMax(va);
+    if (lane == 0) kvmax[1][wave] = va;
+  }
   __syncthreads();
   HALO_PHASE(1, 3);
+  const float sv = halo::SplitScale(fmaxf(fmaxf(kvmax[1][0], kvmax[1][1]), fmaxf(kvmax[1][2], kvmax[1][3])), kSvv);
   // the K chunk is done with: the V chunk goes to the same LDS as halves transposed, vh / vl [256 dims][32 keys]
   // (chunk c of 8 keys of a dim row at c ^ ((dim >> 2) & 3))
   _Float16* vh = kh;

@@ -122,17 +122,20 @@ def run_c1(args, dev, H, res):
     in_xq = H.ProjInput(xq=xq.ptr, xs=xs.ptr, mode=H.PROJ_Q)
     in_aq = H.ProjInput(xq=aq.ptr, xs=as_.ptr, mode=H.PROJ_Q)
 
-    def c1_pass(ws, m, fused=True, mfma=False):
-        if fused and m <= 2:
+    def c1_pass(ws, m, fused=True, mfma=False, pair=True):
+        if fused and (m == 1 or (m == 2 and not pair)):
             # one launch per input row set: quantize prologue + (q|gate, kv), then quantize prologue + o
             H.proj_q8(dev, ws[:2], [yqg, ykv], in_x, m)
             H.proj_q8(dev, ws[2:], [yo], in_a, m)
             return
         if fused:
-            # from 3 token rows: both inputs quantized by one launch, then the grouped projections on the quantized
+            # from 2 token rows: both inputs quantized by one launch, then the grouped projections on the quantized
             # rows (v_dot4 up to 8 tokens, int8 matrix cores beyond; `mfma`: the matrix cores at any token count)
             t = (2, 2) if mfma else (0, 0)
             dev.op("quantize_q8_pair", x.ptr, xq.ptr, xs.ptr, 2048, a.ptr, aq.ptr, as_.ptr, 4096, m)
+            if pair and not mfma and m <= 8:  # both projections in one launch (halo_proj_q8q2_l32x64_*)
+                H.proj_q8_pair(dev, ws, [yqg, ykv, yo], 2, in_xq, in_aq, m)
+                return
             H.proj_q8(dev, ws[:2], [yqg, ykv], in_xq, m, *t)
             H.proj_q8(dev, ws[2:], [yo], in_aq, m, *t)
             return
@@ -163,10 +166,10 @@ def run_c1(args, dev, H, res):
         res["c1"] = None
         return res
 
-    def graph_for(m, fused=True, mfma=False):
+    def graph_for(m, fused=True, mfma=False, pair=True):
         dev.begin_capture()
         for ws in sets:
-            c1_pass(ws, m, fused, mfma)
+            c1_pass(ws, m, fused, mfma, pair)
         return dev.end_capture()
 
     sweep = {}
@@ -181,8 +184,10 @@ def run_c1(args, dev, H, res):
     sweep["1_unfused"] = {"us_per_pass": round(ms / (nrep * copies) * 1e3, 3),
                           "GBps": round(c1_pass_bytes(1) / (ms / (nrep * copies) * 1e-3) / 1e9, 1)}
     dev.free_graph(g)
-    for m in (1, 2, 3, 4, 8, 16, "4_mfma", "8_mfma"):
-        g = graph_for(int(str(m).split("_")[0]), mfma=isinstance(m, str))
+    for m in (1, 2, 3, 4, 8, 16, "2_prologue", "4_two", "8_two", "4_mfma", "8_mfma"):
+        tag = str(m).split("_")[1] if isinstance(m, str) else ""
+        # 2_prologue: both launches quantizing in their prologues; *_two: quantize + two projection launches
+        g = graph_for(int(str(m).split("_")[0]), mfma=tag == "mfma", pair=tag not in ("two", "prologue"))
         reps = 1 if m != 1 else max(1, args.warmup // copies)
         for _ in range(reps):
             dev.launch_graph(g)
@@ -198,9 +203,11 @@ def run_c1(args, dev, H, res):
                          "GBps": round(c1_pass_bytes(mi) / (ms / steps * 1e-3) / 1e9, 1)}
         dev.free_graph(g)
     res["c1"] = {"workload": "C1 Q8_0 projections 2048->4096, 2048->512, 4096->2048 from fp32 activations: at M = 1 "
-                             "quantized in the projections' prologues at M <= 2 (2 launches); from M = 3 both inputs "
-                             "quantized by one launch, then the grouped projections on the quantized rows (3 launches: "
-                             "v_dot4 up to 8 tokens, int8 matrix cores at 16); *_mfma: the matrix-core kernel at that M", "bytes_per_pass_m1": c1_pass_bytes(1),
+                             "quantized in the projections' prologues (2 launches); from M = 2 both inputs quantized "
+                             "by one launch, then both projections on the quantized rows in one launch (v_dot4, "
+                             "halo_proj_q8q2_*) up to 8 tokens, two int8 matrix-core launches at 16; *_two: the two "
+                             "projections as two launches; 2_prologue: M = 2 as M = 1 runs; *_mfma: the matrix-core "
+                             "kernel at that M", "bytes_per_pass_m1": c1_pass_bytes(1),
                  "GBps_m1": sweep["1"]["GBps"], "sweep": sweep}
     log(f"[bench] C1 sweep {sweep}")
     return res

@@ -135,3 +135,45 @@ extern "C" int halo_op_proj_q8(halo_engine* eng, const halo_q8_matrix* mats, flo
                                const halo_proj_input* in, uint32_t tokens, char* err, size_t errlen) {
   return halo_op_proj_q8_grid(eng, mats, ys, n_mats, in, tokens, 0, 0, err, errlen);
 }
+
+extern "C" int halo_op_proj_q8_pair(halo_engine* eng, const halo_q8_matrix* mats, float* const* ys, uint32_t n_first,
+                                    const halo_proj_input* in, const halo_proj_input* in2, uint32_t tokens, char* err,
+                                    size_t errlen) {
+  if (mats == nullptr || ys == nullptr || in == nullptr || in2 == nullptr || n_first < 1 || n_first > 2)
+    return SetErr(err, errlen, "proj pair: 1 or 2 matrices on the first input, one on the second"), -1;
+  if (in->mode != HALO_PROJ_Q || in2->mode != HALO_PROJ_Q || in->xq == nullptr || in->xs == nullptr ||
+      in2->xq == nullptr || in2->xs == nullptr)
+    return SetErr(err, errlen, "proj pair: both inputs quantized (mode Q, xq and xs)"), -1;
+  if (tokens < 2 || tokens > 8) return SetErr(err, errlen, "proj pair: tokens %u not in 2..8", tokens), -1;
+  const std::uint32_t n = n_first + 1, cols = mats[0].cols, cols2 = mats[n_first].cols;
+  for (std::uint32_t i = 0; i < n; ++i) {
+    const halo_q8_matrix& w = mats[i];
+    const std::uint32_t c = i < n_first ? cols : cols2;
+    if (w.qs == nullptr || w.d == nullptr || ys[i] == nullptr || w.rows == 0 || w.cols != c || w.qstride != c)
+      return SetErr(err, errlen, "proj pair: matrix %u (%u x %u, qstride %u) does not match cols %u", i, w.rows,
+                    w.cols, w.qstride, c),
+             -1;
+  }
+  // lanes per row as the single-input kernel picks them; the pairs built are (32, 64), (32, 32) and (64, 64)
+  auto lanes = [](std::uint32_t c) { return c > 2048 ? 64u : (c > 1024 ? 32u : 16u); };
+  const std::uint32_t l1 = lanes(cols), l2 = lanes(cols2);
+  if (cols % 32 != 0 || cols2 % 32 != 0 || cols > 4096 || cols2 > 4096 || l1 == 16 || l2 == 16 ||
+      (l1 == 64 && l2 == 32))
+    return SetErr(err, errlen, "proj pair: cols %u / %u have no paired kernel", cols, cols2), -1;
+  const std::uint32_t nb = tokens == 2 ? 2 : tokens <= 4 ? 4 : 8;
+  if (nb == 2 && !(l1 == 32 && l2 == 64))
+    return SetErr(err, errlen, "proj pair: 2 tokens only with 32 x 64 lanes"), -1;
+  const std::uint32_t o1 = CeilDiv(mats[0].rows, 64 / l1);
+  const std::uint32_t o2 = o1 + (n_first == 2 ? CeilDiv(mats[1].rows, 64 / l1) : 0);
+  const std::uint32_t o3 = CeilDiv(mats[n_first].rows, 64 / l2);
+  const std::uint32_t nb1 = CeilDiv(o2, 4), blocks = nb1 + CeilDiv(o3, 4);
+  const halo_q8_matrix& m1 = n_first == 2 ? mats[1] : mats[0];
+  float* y1 = n_first == 2 ? ys[1] : ys[0];
+  char name[48];
+  std::snprintf(name, sizeof name, "halo_proj_q8q2_l%ux%u_b%u", l1, l2, nb);
+  const halo_arg a[] = {Ptr(in->xq), Ptr(in->xs), Ptr(mats[0].qs), Ptr(mats[0].d), Ptr(ys[0]), Ptr(m1.qs), Ptr(m1.d),
+                        Ptr(y1), U32(mats[0].rows), U32(n_first == 2 ? mats[1].rows : 0u), U32(o1), U32(o2),
+                        U32(cols), Ptr(in2->xq), Ptr(in2->xs), Ptr(mats[n_first].qs), Ptr(mats[n_first].d),
+                        Ptr(ys[n_first]), U32(mats[n_first].rows), U32(o3), U32(cols2), U32(nb1), U32(tokens)};
+  return Launch(eng, name, D3(blocks), D3(256), a, err, errlen);
+}

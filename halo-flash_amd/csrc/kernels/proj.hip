@@ -110,6 +110,19 @@ __device__ __forceinline__ void WideNormRow(const float* __restrict__ x, const f
   if (blockIdx.x == 0 && xq_out != nullptr) halo::QuantRow8(row, n, xq_out, xs_out);
 }
 
+// The staged activation rows, one allocation per token count whatever the lanes per row, so a launch that runs two
+// tilings (halo_proj_q8q2_*) holds one copy.
+template <int NB>
+__device__ __forceinline__ std::int8_t (&ProjLxq())[NB][kProjMaxCols] {
+  __shared__ __attribute__((aligned(16))) std::int8_t a[NB][kProjMaxCols];
+  return a;
+}
+template <int NB>
+__device__ __forceinline__ float (&ProjLxs())[NB][kProjMaxCols / 32] {
+  __shared__ float a[NB][kProjMaxCols / 32];
+  return a;
+}
+
 template <int LPR, int NB, int kMode, int TPW, bool kWide = false>
 __device__ __forceinline__ void ProjQ8(const float* __restrict__ x, const float* __restrict__ delta,
                                        const float* __restrict__ nw, float* __restrict__ res_out,
@@ -121,16 +134,16 @@ __device__ __forceinline__ void ProjQ8(const float* __restrict__ x, const float*
                                        const std::int8_t* qs3, const std::uint16_t* d3, float* y3, std::uint32_t rows0,
                                        std::uint32_t rows1, std::uint32_t rows2, std::uint32_t rows3, std::uint32_t o1,
                                        std::uint32_t o2, std::uint32_t o3, std::uint32_t o4, std::uint32_t T,
-                                       std::uint32_t cols, float eps) {
-  __shared__ __attribute__((aligned(16))) std::int8_t lxq[NB][kProjMaxCols];
-  __shared__ float lxs[NB][kProjMaxCols / 32];
+                                       std::uint32_t cols, float eps, std::uint32_t bid) {
+  auto& lxq = ProjLxq<NB>();
+  auto& lxs = ProjLxs<NB>();
   __shared__ float red[4];
   constexpr int P = kWave / LPR;  // rows per task
   constexpr std::uint32_t kStep = LPR * 16;
   const std::uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, nblk = cols / 32;
   // TPW tasks per wave: block b covers tasks [W TPW b, W TPW (b + 1)), wave w the tasks W TPW b + W i + w (W waves)
   constexpr std::uint32_t kWaves = kWide ? 8 : 4;
-  const std::uint32_t task0 = blockIdx.x * kWaves * TPW + wave;
+  const std::uint32_t task0 = bid * kWaves * TPW + wave;
   // Order of issue: token 0's prologue inputs (L2 hits), then the weights of this wave's first two tasks (HBM),
   // so the prologue of token 0 waits only for its own loads while the weight stream is in flight.
   // 2048-column chunks of the row per 256 threads: cols <= 64 LPR, so one chunk unless LPR = 64
@@ -167,12 +180,12 @@ __device__ __forceinline__ void ProjQ8(const float* __restrict__ x, const float*
       if (threadIdx.x < nblk) lxs[b][threadIdx.x] = xsv;
     } else {
       if constexpr (kMode == 2) {
-        if (blockIdx.x == 0 && res_out != nullptr && delta != nullptr) halo::StoreRow8(res_out + off, cols, row);
+        if (bid == 0 && res_out != nullptr && delta != nullptr) halo::StoreRow8(res_out + off, cols, row);
         halo::RmsNormRow8W(row, aux, cols, eps, red);
       }
       if constexpr (kMode == 3) halo::GatedNormRow8W(row, aux, w8, cols, eps);
       halo::QuantRow8(row, cols, &lxq[b][0], &lxs[b][0]);
-      if (blockIdx.x == 0 && xq_out != nullptr) halo::QuantRow8(row, cols, xq_out + off, xs_out + b * nblk);
+      if (bid == 0 && xq_out != nullptr) halo::QuantRow8(row, cols, xq_out + off, xs_out + b * nblk);
     }
   };
   static_assert(kProjMaxCols / 16 <= 256, "one 16-byte piece of a quantized row per thread");
@@ -284,7 +297,8 @@ __device__ __forceinline__ void ProjQ8(const float* __restrict__ x, const float*
       std::uint32_t rows0, std::uint32_t rows1, std::uint32_t rows2, std::uint32_t rows3, std::uint32_t o1,     \
       std::uint32_t o2, std::uint32_t o3, std::uint32_t o4, std::uint32_t T, std::uint32_t cols, float eps) {   \
     ProjQ8<LPR, NB, MODE, TPW>(x, delta, nw, res_out, xq_in, xs_in, xq_out, xs_out, qs0, d0, y0, qs1, d1, y1, qs2, \
-                               d2, y2, qs3, d3, y3, rows0, rows1, rows2, rows3, o1, o2, o3, o4, T, cols, eps);   \
+                               d2, y2, qs3, d3, y3, rows0, rows1, rows2, rows3, o1, o2, o3, o4, T, cols, eps,   \
+                               blockIdx.x);                                                                       \
   }
 #define HALO_PROJ_Q8_T(MODE, LETTER, LPR, NB) \
   HALO_PROJ_Q8(MODE, LETTER, LPR, NB, 1) HALO_PROJ_Q8(MODE, LETTER, LPR, NB, 2) HALO_PROJ_Q8(MODE, LETTER, LPR, NB, 4)
@@ -304,7 +318,8 @@ __device__ __forceinline__ void ProjQ8(const float* __restrict__ x, const float*
       std::uint32_t rows0, std::uint32_t rows1, std::uint32_t rows2, std::uint32_t rows3, std::uint32_t o1,     \
       std::uint32_t o2, std::uint32_t o3, std::uint32_t o4, std::uint32_t T, std::uint32_t cols, float eps) {   \
     ProjQ8<LPR, 1, 2, TPW, true>(x, delta, nw, res_out, xq_in, xs_in, xq_out, xs_out, qs0, d0, y0, qs1, d1, y1, qs2, \
-                                 d2, y2, qs3, d3, y3, rows0, rows1, rows2, rows3, o1, o2, o3, o4, T, cols, eps); \
+                                 d2, y2, qs3, d3, y3, rows0, rows1, rows2, rows3, o1, o2, o3, o4, T, cols, eps, \
+                                 blockIdx.x);                                                                     \
   }
 HALO_PROJ_Q8W(32, 1)
 HALO_PROJ_Q8W(32, 2)
@@ -313,6 +328,33 @@ HALO_PROJ_Q8W(16, 1)
 HALO_PROJ_Q8W(16, 2)
 HALO_PROJ_Q8W(16, 4)
 #undef HALO_PROJ_Q8W
+// grid (nb1 + ceil(o_3' / 4)), block 256: two grouped mode-q projections with their own quantized inputs in one
+// launch. Blocks b < nb1 = ceil(o_2 / 4) run matrices 0 and 1 on (xq, xs, cols) with LPR1 lanes per row (tasks
+// [0, o_2)); blocks b >= nb1 run matrix 2 on (xq2, xs2, cols2) with LPR2 (its own task list of o_3' tasks), each part
+// exactly as halo_proj_q8q_l<LPR>_b<NB>_t1 (the same bits).
+#define HALO_PROJ_Q8Q2(L1, L2, NB)                                                                                \
+  extern "C" __global__ void __launch_bounds__(256) halo_proj_q8q2_l##L1##x##L2##_b##NB(                          \
+      const std::int8_t* xq, const float* xs, const std::int8_t* qs0, const std::uint16_t* d0, float* y0,         \
+      const std::int8_t* qs1, const std::uint16_t* d1, float* y1, std::uint32_t rows0, std::uint32_t rows1,       \
+      std::uint32_t o1, std::uint32_t o2, std::uint32_t cols, const std::int8_t* xq2, const float* xs2,           \
+      const std::int8_t* qs2, const std::uint16_t* d2, float* y2, std::uint32_t rows2, std::uint32_t o3,          \
+      std::uint32_t cols2, std::uint32_t nb1, std::uint32_t T) {                                                  \
+    if (blockIdx.x < nb1)                                                                                         \
+      ProjQ8<L1, NB, 0, 1>(nullptr, nullptr, nullptr, nullptr, xq, xs, nullptr, nullptr, qs0, d0, y0, qs1, d1, y1,  \
+                           qs0, d0, y0, qs0, d0, y0, rows0, rows1, 0, 0, o1, o2, o2, o2, T, cols, 0.0f, blockIdx.x); \
+    else                                                                                                          \
+      ProjQ8<L2, NB, 0, 1>(nullptr, nullptr, nullptr, nullptr, xq2, xs2, nullptr, nullptr, qs2, d2, y2, qs2, d2, y2, \
+                           qs2, d2, y2, qs2, d2, y2, rows2, 0, 0, 0, o3, o3, o3, o3, T, cols2, 0.0f,               \
+                           blockIdx.x - nb1);                                                                     \
+  }
+HALO_PROJ_Q8Q2(32, 64, 2)
+HALO_PROJ_Q8Q2(32, 64, 4)
+HALO_PROJ_Q8Q2(32, 64, 8)
+HALO_PROJ_Q8Q2(32, 32, 4)
+HALO_PROJ_Q8Q2(32, 32, 8)
+HALO_PROJ_Q8Q2(64, 64, 4)
+HALO_PROJ_Q8Q2(64, 64, 8)
+#undef HALO_PROJ_Q8Q2
 HALO_PROJ_Q8_L(0, q)
 HALO_PROJ_Q8_L(1, f)
 HALO_PROJ_Q8_L(2, n)

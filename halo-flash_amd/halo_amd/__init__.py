@@ -70,6 +70,13 @@ def proj_q8(dev, weights, outs, inp: ProjInput, tokens: int, tasks_per_wave: int
     dev.op("proj_q8_grid", mats, ys, len(weights), C.byref(inp), tokens, tasks_per_wave, lanes_per_row)
 
 
+def proj_q8_pair(dev, weights, outs, n_first: int, inp: ProjInput, inp2: ProjInput, tokens: int):
+    """Two grouped mode-Q projections in one launch: weights[:n_first] read inp, weights[n_first] reads inp2."""
+    mats = (Q8Matrix * len(weights))(*[w.desc for w in weights])
+    ys = (C.c_void_p * len(outs))(*[o.ptr for o in outs])
+    dev.op("proj_q8_pair", mats, ys, n_first, C.byref(inp), C.byref(inp2), tokens)
+
+
 class MoeWeights(C.Structure):
     _fields_ = [
         ("router", C.c_void_p),
@@ -380,6 +387,8 @@ _SIGS = {
                         True),
     "halo_op_proj_q8_grid": (C.c_int, [_VP, C.POINTER(Q8Matrix), C.POINTER(C.c_void_p), _U32, C.POINTER(ProjInput),
                                        _U32, _U32, _U32], True),
+    "halo_op_proj_q8_pair": (C.c_int, [_VP, C.POINTER(Q8Matrix), C.POINTER(C.c_void_p), _U32, C.POINTER(ProjInput),
+                                       C.POINTER(ProjInput), _U32], True),
     "halo_op_matvec_q8a8": (C.c_int, [_VP, C.POINTER(Q8Matrix), _VP, _VP, _VP, _U32, _U32], True),
     "halo_op_matvec_q8a8_tiled": (
         C.c_int, [_VP, C.POINTER(Q8Matrix), _VP, _VP, _VP, _U32, _U32, _U32, _U32, _U32], True),

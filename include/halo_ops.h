@@ -102,6 +102,15 @@ int halo_op_proj_q8_grid(halo_engine* eng, const halo_q8_matrix* mats, float* co
                          const halo_proj_input* in, uint32_t tokens, uint32_t tasks_per_wave, uint32_t lanes_per_row,
                          char* err, size_t errlen);
 
+/* Two grouped mode-Q projections with different quantized inputs in one launch (halo_proj_q8q2_*): matrices
+ * [0, n_first) (n_first 1 or 2) read in, matrix n_first reads in2; 2..8 tokens; the same bits as two
+ * halo_op_proj_q8 calls. For a decode pass whose projections read two activation row sets that are both ready (the
+ * C1 q | gate + kv and o projections), one launch instead of two. No counterpart in the reference: it issues one
+ * FlashNextGpu::MatVec per matrix (src/engine/flash_next_gpu.cpp:212-254). */
+int halo_op_proj_q8_pair(halo_engine* eng, const halo_q8_matrix* mats, float* const* ys, uint32_t n_first,
+                         const halo_proj_input* in, const halo_proj_input* in2, uint32_t tokens, char* err,
+                         size_t errlen);
+
 /* The same with an explicit GEMV tiling (lanes per row 16/32/64, rows per lane group 1/2/4, waves per block) for
  * tuning sweeps; m <= 8. */
 int halo_op_matvec_q8a8_tiled(halo_engine* eng, const halo_q8_matrix* w, const int8_t* xq, const float* xs,

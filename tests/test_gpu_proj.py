@@ -231,3 +231,43 @@ def test_proj_mode_g_matches_gated_norm_kernel(dev, tokens):
     qs, dd = host[0]
     want_y, mag = O.gemv_q8a8(qs, dd, xq2.download(), xs2.download())
     _check_y(y.download(), want_y, mag)
+
+
+@pytest.mark.parametrize("tokens", [2, 3, 4, 8])
+def test_proj_pair_matches_two_launches(dev, tokens):
+    """The C1 pass's two projections with their own quantized inputs in one launch (q | gate + kv on x, o on a):
+    bit for bit the outputs of the two grouped launches, and within the bar of the oracle."""
+    rng = np.random.default_rng(300 + tokens)
+    host1, ws1 = _mats(dev, rng, [(4096, 2048), (512, 2048)])
+    host2, ws2 = _mats(dev, rng, [(2048, 4096)])
+    x = rng.normal(0, 1, (tokens, 2048)).astype(np.float32)
+    a = rng.normal(0, 1, (tokens, 4096)).astype(np.float32)
+    xq, xs = O.quantize(x)
+    aq, as_ = O.quantize(a)
+    gxq, gxs, gaq, gas = (dev.to_device(v) for v in (xq, xs, aq, as_))
+    in1 = H.ProjInput(xq=gxq.ptr, xs=gxs.ptr, mode=H.PROJ_Q)
+    in2 = H.ProjInput(xq=gaq.ptr, xs=gas.ptr, mode=H.PROJ_Q)
+    sep = [dev.array((tokens, r), np.float32) for r in (4096, 512, 2048)]
+    H.proj_q8(dev, ws1, sep[:2], in1, tokens)
+    H.proj_q8(dev, ws2, sep[2:], in2, tokens)
+    pair = [dev.array((tokens, r), np.float32) for r in (4096, 512, 2048)]
+    H.proj_q8_pair(dev, ws1 + ws2, pair, 2, in1, in2, tokens)
+    for s_, p_ in zip(sep, pair):
+        assert s_.download().tobytes() == p_.download().tobytes()
+    for (qs, d), y in zip(host1, pair[:2]):
+        want, mag = O.gemv_q8a8(qs, d, xq, xs)
+        _check_y(y.download(), want, mag)
+    want, mag = O.gemv_q8a8(host2[0][0], host2[0][1], aq, as_)
+    _check_y(pair[2].download(), want, mag)
+
+
+def test_proj_pair_rejects_bad_shapes(dev):
+    ws = [H.Q8Weights(dev, 64, 2048), H.Q8Weights(dev, 64, 1024)]
+    outs = [dev.array((4, 64), np.float32) for _ in ws]
+    q = dev.array((4, 2048), np.int8)
+    s = dev.array((4, 64), np.float32)
+    inp = H.ProjInput(xq=q.ptr, xs=s.ptr, mode=H.PROJ_Q)
+    with pytest.raises(RuntimeError, match="paired kernel"):
+        H.proj_q8_pair(dev, ws, outs, 1, inp, inp, 4)
+    with pytest.raises(RuntimeError, match="tokens"):
+        H.proj_q8_pair(dev, ws[:1] + ws[:1], outs, 1, inp, inp, 1)

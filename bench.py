@@ -133,7 +133,7 @@ def run_c1(args, dev, H, res):
             # rows (v_dot4 up to 8 tokens, int8 matrix cores beyond; `mfma`: the matrix cores at any token count)
             t = (2, 2) if mfma else (0, 0)
             dev.op("quantize_q8_pair", x.ptr, xq.ptr, xs.ptr, 2048, a.ptr, aq.ptr, as_.ptr, 4096, m)
-            if pair and not mfma and m <= 8:  # both projections in one launch (halo_proj_q8q2_l32x64_*)
+            if pair and (not mfma or m >= 9):  # both projections in one launch (halo_proj_q8q2_* / _q8m2_*)
                 H.proj_q8_pair(dev, ws, [yqg, ykv, yo], 2, in_xq, in_aq, m)
                 return
             H.proj_q8(dev, ws[:2], [yqg, ykv], in_xq, m, *t)
@@ -184,7 +184,7 @@ def run_c1(args, dev, H, res):
     sweep["1_unfused"] = {"us_per_pass": round(ms / (nrep * copies) * 1e3, 3),
                           "GBps": round(c1_pass_bytes(1) / (ms / (nrep * copies) * 1e-3) / 1e9, 1)}
     dev.free_graph(g)
-    for m in (1, 2, 3, 4, 8, 16, "2_prologue", "4_two", "8_two", "4_mfma", "8_mfma"):
+    for m in (1, 2, 3, 4, 8, 16, "2_prologue", "4_two", "8_two", "16_two", "4_mfma", "8_mfma"):
         tag = str(m).split("_")[1] if isinstance(m, str) else ""
         # 2_prologue: both launches quantizing in their prologues; *_two: quantize + two projection launches
         g = graph_for(int(str(m).split("_")[0]), mfma=tag == "mfma", pair=tag not in ("two", "prologue"))
@@ -205,7 +205,8 @@ def run_c1(args, dev, H, res):
     res["c1"] = {"workload": "C1 Q8_0 projections 2048->4096, 2048->512, 4096->2048 from fp32 activations: at M = 1 "
                              "quantized in the projections' prologues (2 launches); from M = 2 both inputs quantized "
                              "by one launch, then both projections on the quantized rows in one launch (v_dot4, "
-                             "halo_proj_q8q2_*) up to 8 tokens, two int8 matrix-core launches at 16; *_two: the two "
+                             "halo_proj_q8q2_*) up to 8 tokens, on int8 matrix cores (halo_proj_q8m2_c2x4) at 16; "
+                             "*_two: the two "
                              "projections as two launches; 2_prologue: M = 2 as M = 1 runs; *_mfma: the matrix-core "
                              "kernel at that M", "bytes_per_pass_m1": c1_pass_bytes(1),
                  "GBps_m1": sweep["1"]["GBps"], "sweep": sweep}

@@ -144,7 +144,7 @@ extern "C" int halo_op_proj_q8_pair(halo_engine* eng, const halo_q8_matrix* mats
   if (in->mode != HALO_PROJ_Q || in2->mode != HALO_PROJ_Q || in->xq == nullptr || in->xs == nullptr ||
       in2->xq == nullptr || in2->xs == nullptr)
     return SetErr(err, errlen, "proj pair: both inputs quantized (mode Q, xq and xs)"), -1;
-  if (tokens < 2 || tokens > 8) return SetErr(err, errlen, "proj pair: tokens %u not in 2..8", tokens), -1;
+  if (tokens < 2 || tokens > 16) return SetErr(err, errlen, "proj pair: tokens %u not in 2..16", tokens), -1;
   const std::uint32_t n = n_first + 1, cols = mats[0].cols, cols2 = mats[n_first].cols;
   for (std::uint32_t i = 0; i < n; ++i) {
     const halo_q8_matrix& w = mats[i];
@@ -153,6 +153,19 @@ extern "C" int halo_op_proj_q8_pair(halo_engine* eng, const halo_q8_matrix* mats
       return SetErr(err, errlen, "proj pair: matrix %u (%u x %u, qstride %u) does not match cols %u", i, w.rows,
                     w.cols, w.qstride, c),
              -1;
+  }
+  const halo_q8_matrix& m1 = n_first == 2 ? mats[1] : mats[0];
+  float* y1 = n_first == 2 ? ys[1] : ys[0];
+  if (tokens >= kProjMfmaMinTokens) {  // int8 matrix cores, 16-row tasks (halo_proj_q8m2_c2x4)
+    if (cols != 2048 || cols2 != 4096)
+      return SetErr(err, errlen, "proj pair: cols %u / %u have no paired kernel at %u tokens", cols, cols2, tokens),
+             -1;
+    const std::uint32_t o1 = CeilDiv(mats[0].rows, 16), o2 = o1 + (n_first == 2 ? CeilDiv(mats[1].rows, 16) : 0);
+    const halo_arg a[] = {Ptr(in->xq), Ptr(in->xs), Ptr(mats[0].qs), Ptr(mats[0].d), Ptr(ys[0]), Ptr(m1.qs),
+                          Ptr(m1.d), Ptr(y1), U32(mats[0].rows), U32(n_first == 2 ? mats[1].rows : 0u), U32(o1),
+                          U32(o2), Ptr(in2->xq), Ptr(in2->xs), Ptr(mats[n_first].qs), Ptr(mats[n_first].d),
+                          Ptr(ys[n_first]), U32(mats[n_first].rows), U32(tokens)};
+    return Launch(eng, "halo_proj_q8m2_c2x4", D3(o2 + CeilDiv(mats[n_first].rows, 16)), D3(512), a, err, errlen);
   }
   // lanes per row as the single-input kernel picks them; the pairs built are (32, 64), (32, 32) and (64, 64)
   auto lanes = [](std::uint32_t c) { return c > 2048 ? 64u : (c > 1024 ? 32u : 16u); };
@@ -167,8 +180,6 @@ extern "C" int halo_op_proj_q8_pair(halo_engine* eng, const halo_q8_matrix* mats
   const std::uint32_t o2 = o1 + (n_first == 2 ? CeilDiv(mats[1].rows, 64 / l1) : 0);
   const std::uint32_t o3 = CeilDiv(mats[n_first].rows, 64 / l2);
   const std::uint32_t nb1 = CeilDiv(o2, 4), blocks = nb1 + CeilDiv(o3, 4);
-  const halo_q8_matrix& m1 = n_first == 2 ? mats[1] : mats[0];
-  float* y1 = n_first == 2 ? ys[1] : ys[0];
   char name[48];
   std::snprintf(name, sizeof name, "halo_proj_q8q2_l%ux%u_b%u", l1, l2, nb);
   const halo_arg a[] = {Ptr(in->xq), Ptr(in->xs), Ptr(mats[0].qs), Ptr(mats[0].d), Ptr(ys[0]), Ptr(m1.qs), Ptr(m1.d),

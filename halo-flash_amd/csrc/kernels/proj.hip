@@ -391,12 +391,11 @@ __device__ __forceinline__ void ProjQ8Mfma(const std::int8_t* __restrict__ xq, c
                                            const std::int8_t* qs3, const std::uint16_t* d3, float* y3,
                                            std::uint32_t rows0, std::uint32_t rows1, std::uint32_t rows2,
                                            std::uint32_t rows3, std::uint32_t o1, std::uint32_t o2, std::uint32_t o3,
-                                           std::uint32_t T) {
+                                           std::uint32_t T, std::uint32_t task) {
   constexpr std::uint32_t cols = 64 * kMfmaWaves * S, nblk = cols / 32, kThreads = 64 * kMfmaWaves;
   __shared__ __attribute__((aligned(16))) float sxt[nblk][16];
   __shared__ __attribute__((aligned(16))) float red[kMfmaWaves - 1][64][4];
   const std::uint32_t tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave, g = lane / 16, li = lane % 16;
-  const std::uint32_t task = blockIdx.x;
   const std::uint32_t m = task < o1 ? 0 : task < o2 ? 1 : task < o3 ? 2 : 3;
   const std::uint32_t lt = task - (m == 0 ? 0 : m == 1 ? o1 : m == 2 ? o2 : o3);
   const std::int8_t* qs = m == 0 ? qs0 : m == 1 ? qs1 : m == 2 ? qs2 : qs3;
@@ -492,9 +491,25 @@ __device__ __forceinline__ void ProjQ8Mfma(const std::int8_t* __restrict__ xq, c
       std::uint32_t rows1, std::uint32_t rows2, std::uint32_t rows3, std::uint32_t o1, std::uint32_t o2,          \
       std::uint32_t o3, std::uint32_t T) {                                                                        \
     ProjQ8Mfma<S>(xq, xs, qs0, d0, y0, qs1, d1, y1, qs2, d2, y2, qs3, d3, y3, rows0, rows1, rows2, rows3, o1, o2, o3, \
-                  T);                                                                                             \
+                  T, blockIdx.x);                                                                                 \
   }
 HALO_PROJ_Q8M(1, 2)
 HALO_PROJ_Q8M(2, 4)
 HALO_PROJ_Q8M(4, 8)
 #undef HALO_PROJ_Q8M
+
+// grid (o_2 + o_3'), block 512: two of the above in one launch with their own quantized inputs: blocks b < o_2 run
+// matrices 0 and 1 (2048 columns) on (xq, xs), blocks b >= o_2 matrix 2 (4096 columns) on (xq2, xs2), each exactly
+// as halo_proj_q8m_c2 / _c4 (the same bits). 1 <= T <= 16.
+extern "C" __global__ void __launch_bounds__(512) halo_proj_q8m2_c2x4(
+    const std::int8_t* xq, const float* xs, const std::int8_t* qs0, const std::uint16_t* d0, float* y0,
+    const std::int8_t* qs1, const std::uint16_t* d1, float* y1, std::uint32_t rows0, std::uint32_t rows1,
+    std::uint32_t o1, std::uint32_t o2, const std::int8_t* xq2, const float* xs2, const std::int8_t* qs2,
+    const std::uint16_t* d2, float* y2, std::uint32_t rows2, std::uint32_t T) {
+  if (blockIdx.x < o2)
+    ProjQ8Mfma<4>(xq, xs, qs0, d0, y0, qs1, d1, y1, qs0, d0, y0, qs0, d0, y0, rows0, rows1, 0, 0, o1, o2, o2, T,
+                  blockIdx.x);
+  else
+    ProjQ8Mfma<8>(xq2, xs2, qs2, d2, y2, qs2, d2, y2, qs2, d2, y2, qs2, d2, y2, rows2, 0, 0, 0, 0xFFFFFFFFu,
+                  0xFFFFFFFFu, 0xFFFFFFFFu, T, blockIdx.x - o2);
+}

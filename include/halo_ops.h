@@ -103,8 +103,8 @@ int halo_op_proj_q8_grid(halo_engine* eng, const halo_q8_matrix* mats, float* co
                          char* err, size_t errlen);
 
 /* Two grouped mode-Q projections with different quantized inputs in one launch (halo_proj_q8q2_*): matrices
- * [0, n_first) (n_first 1 or 2) read in, matrix n_first reads in2; 2..8 tokens; the same bits as two
- * halo_op_proj_q8 calls. For a decode pass whose projections read two activation row sets that are both ready (the
+ * [0, n_first) (n_first 1 or 2) read in, matrix n_first reads in2; 2..16 tokens (9..16 on int8 matrix cores,
+ * halo_proj_q8m2_c2x4: 2048 then 4096 columns); the same bits as two halo_op_proj_q8 calls. For a decode pass whose projections read two activation row sets that are both ready (the
  * C1 q | gate + kv and o projections), one launch instead of two. No counterpart in the reference: it issues one
  * FlashNextGpu::MatVec per matrix (src/engine/flash_next_gpu.cpp:212-254). */
 int halo_op_proj_q8_pair(halo_engine* eng, const halo_q8_matrix* mats, float* const* ys, uint32_t n_first,

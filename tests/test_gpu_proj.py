@@ -233,10 +233,11 @@ def test_proj_mode_g_matches_gated_norm_kernel(dev, tokens):
     _check_y(y.download(), want_y, mag)
 
 
-@pytest.mark.parametrize("tokens", [2, 3, 4, 8])
+@pytest.mark.parametrize("tokens", [2, 3, 4, 8, 9, 16])
 def test_proj_pair_matches_two_launches(dev, tokens):
     """The C1 pass's two projections with their own quantized inputs in one launch (q | gate + kv on x, o on a):
-    bit for bit the outputs of the two grouped launches, and within the bar of the oracle."""
+    bit for bit the outputs of the two grouped launches (v_dot4 up to 8 tokens, int8 matrix cores from 9), and
+    within the bar of the oracle."""
     rng = np.random.default_rng(300 + tokens)
     host1, ws1 = _mats(dev, rng, [(4096, 2048), (512, 2048)])
     host2, ws2 = _mats(dev, rng, [(2048, 4096)])

@@ -593,8 +593,8 @@ __device__ __forceinline__ void GdnStepQ8(
   const std::uint32_t pos = nkv[s] - 1;
   const float zg = z[static_cast<std::size_t>(s) * Dv + h * kD + min(t, static_cast<std::uint32_t>(kD - 1))];  // t < kD
   float y = 0.0f;
-  // the prologue's loads are issued before the state's (64 KB per block, eight 16-byte loads per thread): loads
-  // complete in order, so the conv and norms below run while the state streams in
+  // the prologue's loads are issued before the state's (64 KB per block, eight 16-byte loads per thread), so the conv
+  // and norms below run while the state streams in
   // (unconditional loads from clamped addresses, selected afterwards: a load under a branch would wait at the join
   // for every load issued before it, the state's included)
   const float x = qkv[static_cast<std::size_t>(s) * C + ch];
@@ -608,6 +608,9 @@ __device__ __forceinline__ void GdnStepQ8(
   const float ga = a[h], gdt = dt[h], galpha = ab[static_cast<std::size_t>(s) * 2 * Hv + h],
               gbeta = ab[static_cast<std::size_t>(s) * 2 * Hv + Hv + h];
   __builtin_amdgcn_sched_barrier(0);  // keep the issue order
+  // Measured: the state issued only once the prologue's inputs have landed streams in ~2 us and leaves the conv and
+  // norms free to run; issued right behind them, the wave stalls on issuing it (until ~2.7 us) with the conv waiting.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   float4 row[8];
 #pragma unroll
   for (int r = 0; r < 8; ++r) row[r] = *reinterpret_cast<const float4*>(St + static_cast<std::size_t>(i0 + r) * kD + j0);

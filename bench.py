@@ -1040,10 +1040,10 @@ def run_phases(args, dev, H, res):
             model.reset()
             for s_ in range(S):
                 model.set_session(s_, rng.integers(0, cfg.vocab, 16).astype(np.uint32))
-            samples, extra = [], {2: [], 3: [], 4: []}
+            samples, extra = [], {2: [], 3: [], 4: [], 5: []}
             # the last layer (attention: q|gate + k + v = 9216 rows, 64 per block) input projection, and the last
             # MoE layer's router (129 blocks) and gate/up blocks of the 10 routed slots (grid 11 x 128)
-            nbs = {2: 144, 3: np.array([x + 11 * y for y in range(128) for x in range(10)]), 4: 129}
+            nbs = {2: 144, 3: np.array([x + 11 * y for y in range(128) for x in range(10)]), 4: 129, 5: 256}
             for rep in range(12):
                 model.step_eager(S)
                 dev.sync()
@@ -1060,6 +1060,9 @@ def run_phases(args, dev, H, res):
                     [r_[:, [0, 5, 6, 7, 1, 2, 3, 4]] for r_ in extra[3]],
                     ["start", "softmax (logits arrived)", "threshold", "candidates in LDS", "wave 0 ranked the logits",
                      "barrier", "dot (weights arrived)", "end"]))
+                out["moe_down_S1"] = dict(kernel="halo_moe_down_q8", blocks=256, **_phases_summary(
+                    extra[5], ["start", "h loaded, expert rows issued", "dots (rows arrived)", "barrier",
+                               "end (combined rows stored)"]))
                 out["moe_router_S1"] = dict(kernel="halo_moe_router_n1_h2048", blocks=129, **_phases_summary(
                     extra[4], ["start", "sums of squares (x and weights arrived)", "x in LDS", "end"]))
             out[f"gdn_step_S{S}"] = dict(blocks=S * cfg.gdn_v_heads, **_phases_summary(

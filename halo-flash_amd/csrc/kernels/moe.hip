@@ -699,6 +699,7 @@ __device__ __forceinline__ void MoeDown(
                       sub = lane / 32, l = lane % 32;
   const std::uint32_t t = blockIdx.y, r0 = blockIdx.x * kDownRows;
   const bool shared = wave == k;
+  HALO_PHASE(5, 0);
   // the combine weights are loaded now (unconditionally, from clamped addresses: a load under a branch would wait
   // at the join for its round trip before anything else is issued) and put in LDS after the dot products
   const float wv = weights[t * k + min(threadIdx.x, k - 1)];
@@ -732,6 +733,7 @@ __device__ __forceinline__ void MoeDown(
       sw[p] = in ? sv : 0.0f;
     }
     __builtin_amdgcn_sched_barrier(0);
+    HALO_PHASE(5, 1);
     float hv[8] = {ha.x, ha.y, ha.z, ha.w, hb.x, hb.y, hb.z, hb.w};
     float amax = 0.0f;
 #pragma unroll
@@ -761,15 +763,18 @@ __device__ __forceinline__ void MoeDown(
       if (l == 0) part[wave][2 * p + sub] = v;
     }
   }
+  HALO_PHASE(5, 2);
   if (threadIdx.x < k) wslot[threadIdx.x] = wv;
   if (threadIdx.x == k) wslot[k] = sdq != nullptr ? halo::Sigmoid(sgv) : 0.0f;
   __syncthreads();
+  HALO_PHASE(5, 3);
   if (threadIdx.x < kDownRows && r0 + threadIdx.x < H) {
     float acc = 0.0f;
     for (std::uint32_t s = 0; s < k; ++s) acc += wslot[s] * part[s][threadIdx.x];
     if (sdq != nullptr) acc += wslot[k] * part[k][threadIdx.x];
     out[static_cast<std::size_t>(t) * H + r0 + threadIdx.x] = acc;
   }
+  HALO_PHASE(5, 4);
 }
 // 8 rows per block at one token (more blocks in flight); 16 for token batches, which halves the h rows each block
 // reads and quantizes again.

@@ -533,38 +533,42 @@ __device__ __forceinline__ void AttnDecodeCombine(
     const std::uint32_t c = i < prefix_chunks ? i : prefix_chunks + s * suffix_chunks + (i - prefix_chunks);
     return static_cast<std::size_t>(c) * Hkv + kvh;
   };
-  // Every load is independent of the others, so all are issued first (unconditionally, from clamped items, then
-  // selected): the items' m and l (n <= 1024: four each per thread), this thread's first two groups of kU weighted
-  // partial sums and its gate value; the arithmetic then runs in the order it always had.
+  // The loads that do not depend on each other are issued together (unconditionally, from clamped items, then
+  // selected): the items' m and l for n <= 512 (two each per thread), this thread's first group of kU partial sums
+  // and its gate value; further items (n > 512, groups past the first) are loaded where they are used. The
+  // arithmetic runs in the order it always had.
   const std::uint32_t f = t % kF, ig = t / kF;
   constexpr int kU = 8;
-  float mv[4], lv[4];
+  float mv[2], lv[2];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < 2; ++j) {
     const std::uint32_t i = min(t + 256u * j, n - 1);
     mv[j] = pm[item(i) * slots + slot];
     lv[j] = pl[item(i) * slots + slot];
   }
-  float4 a[2][kU];
+  float4 a0[kU];
 #pragma unroll
-  for (int r = 0; r < 2; ++r)
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const std::uint32_t i = min(ig + kG * (kU * r + u), n - 1);
-      a[r][u] = reinterpret_cast<const float4*>(pacc + (item(i) * slots + slot) * kHd)[quarter * kF + f];
-    }
-  const std::size_t off = (static_cast<std::size_t>(s) * Hq + h) * kHd + quarter * kW + min(t, kW - 1);
+  for (int u = 0; u < kU; ++u) {
+    const std::uint32_t i = min(ig + kG * u, n - 1);
+    a0[u] = reinterpret_cast<const float4*>(pacc + (item(i) * slots + slot) * kHd)[quarter * kF + f];
+  }
   const float gv = *(gate != nullptr ? gate + (static_cast<std::size_t>(s) * Hq + h) * kGS * kHd + quarter * kW +
                                            min(t, kW - 1)
                                      : pl);  // (any valid address without a gate; unused then)
+  const std::size_t off = (static_cast<std::size_t>(s) * Hq + h) * kHd + quarter * kW + min(t, kW - 1);
   float M = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < 2; ++j) {
     const std::uint32_t i = t + 256u * j;
     if (i < n) {
       wts[i] = mv[j];
       M = fmaxf(M, mv[j]);
     }
+  }
+  for (std::uint32_t i = t + 512; i < n; i += blockDim.x) {
+    const float m = pm[item(i) * slots + slot];
+    wts[i] = m;
+    M = fmaxf(M, m);
   }
   M = halo::GroupMax(M);
   if (t % kWave == 0) red[t / kWave] = M;
@@ -572,7 +576,7 @@ __device__ __forceinline__ void AttnDecodeCombine(
   M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   float L = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < 2; ++j) {
     const std::uint32_t i = t + 256u * j;
     if (i < n) {
       const float m = mv[j];
@@ -580,6 +584,12 @@ __device__ __forceinline__ void AttnDecodeCombine(
       wts[i] = w;
       L += w * lv[j];
     }
+  }
+  for (std::uint32_t i = t + 512; i < n; i += blockDim.x) {
+    const float m = wts[i];
+    const float w = m == -INFINITY ? 0.0f : expf(m - M);
+    wts[i] = w;
+    L += w * pl[item(i) * slots + slot];
   }
   L = halo::GroupSum(L);
   __syncthreads();
@@ -595,11 +605,10 @@ __device__ __forceinline__ void AttnDecodeCombine(
       const std::uint32_t i = i0 + kG * u;
       const float wi = wts[min(i, n - 1)];
       w[u] = i < n ? wi : 0.0f;
-      // past the two preloaded groups: load here (clamped item); an empty chunk's partial is never written
-      const float4 av = r == 0 ? a[0][u]
-                        : r == 1 ? a[1][u]
-                                 : reinterpret_cast<const float4*>(pacc + (item(min(i, n - 1)) * slots + slot) *
-                                                                              kHd)[quarter * kF + f];
+      // past the preloaded group: load here (clamped item); an empty chunk's partial is never written
+      const float4 av = r == 0 ? a0[u]
+                               : reinterpret_cast<const float4*>(pacc + (item(min(i, n - 1)) * slots + slot) *
+                                                                           kHd)[quarter * kF + f];
       b[u] = w[u] == 0.0f ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : av;
     }
 #pragma unroll

@@ -523,7 +523,7 @@ __device__ __forceinline__ void AttnDecodeCombine(
     std::uint32_t suffix_chunks) {
   constexpr std::uint32_t kW = kHd / NS, kF = kW / 4, kG = 256 / kF;  // slice dims, float4 lanes, item groups
   __shared__ float wts[1024];
-  __shared__ float red[4];
+  __shared__ float red[4], redl[4];
   __shared__ float4 part[kG][kF];
   const std::uint32_t quarter = blockIdx.x % NS, sh = blockIdx.x / NS;
   const std::uint32_t G = Hq / Hkv, s = sh / Hq, h = sh % Hq, kvh = h / G, g = h % G;
@@ -592,10 +592,9 @@ __device__ __forceinline__ void AttnDecodeCombine(
     L += w * pl[item(i) * slots + slot];
   }
   L = halo::GroupSum(L);
+  if (t % kWave == 0) redl[t / kWave] = L;  // (its own array: red may still be read for M)
   __syncthreads();
-  if (t % kWave == 0) red[t / kWave] = L;
-  __syncthreads();
-  L = (red[0] + red[1]) + (red[2] + red[3]);
+  L = (redl[0] + redl[1]) + (redl[2] + redl[3]);
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   for (std::uint32_t i0 = ig, r = 0; i0 < n; i0 += kG * kU, ++r) {
     float4 b[kU];

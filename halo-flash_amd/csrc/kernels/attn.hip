@@ -308,25 +308,27 @@ __device__ __forceinline__ void AttnDecodePartial(
   __shared__ float qsc[kMaxQ], kvmax[2][4];
   H8 qh[kHd / 32], ql[kHd / 32];
   if (score_wave) {
+    // two passes over the query row in LDS (its magnitude, then the split), so the row is never held in registers
+    // next to its halves (that took the kernel to 180 VGPRs: two blocks per CU instead of three)
     const float* qr = &qs[min(16 * qt + lr, nq - 1)][0];
-    float xr[kHd / 32][8];
     float amax = 0.0f;
 #pragma unroll
     for (int c = 0; c < kHd / 32; ++c) {
       const float4 a0 = *reinterpret_cast<const float4*>(qr + 32 * c + 8 * kq);
       const float4 a1 = *reinterpret_cast<const float4*>(qr + 32 * c + 8 * kq + 4);
-      const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        xr[c][e] = x[e];
-        amax = fmaxf(amax, fabsf(x[e]));
-      }
+      amax = fmaxf(amax, fmaxf(fmaxf(fmaxf(fabsf(a0.x), fabsf(a0.y)), fmaxf(fabsf(a0.z), fabsf(a0.w))),
+                               fmaxf(fmaxf(fabsf(a1.x), fabsf(a1.y)), fmaxf(fabsf(a1.z), fabsf(a1.w)))));
     }
     amax = fmaxf(amax, __shfl_xor(amax, 16));
     amax = fmaxf(amax, __shfl_xor(amax, 32));
     const float sq = halo::SplitScale(amax, kSqk);
 #pragma unroll
-    for (int c = 0; c < kHd / 32; ++c) SplitHalves(xr[c], qh[c], ql[c], sq);
+    for (int c = 0; c < kHd / 32; ++c) {
+      const float4 a0 = *reinterpret_cast<const float4*>(qr + 32 * c + 8 * kq);
+      const float4 a1 = *reinterpret_cast<const float4*>(qr + 32 * c + 8 * kq + 4);
+      const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      SplitHalves(x, qh[c], ql[c], sq);
+    }
     if (kq == 0) qsc[16 * qt + lr] = sq;
   }
   {  // the block's K and V magnitudes over the visible rows (rows past them repeat the pool's row `last`, which for
@@ -471,8 +473,10 @@ __device__ __forceinline__ void AttnDecodePartial(
 }
 }  // namespace
 
+// (the matrix-core forms ask for 3 waves per SIMD, i.e. at most 168 VGPRs: three 4-wave blocks per CU; at 180 the
+// 608 blocks of the 4-session C4 step ran in two rounds)
 #define HALO_ATTN_PARTIAL(NAME, MMA)                                                                                   \
-  extern "C" __global__ void __launch_bounds__(256) NAME(                                                             \
+  extern "C" __global__ void __launch_bounds__(256, MMA ? 3 : 1) NAME(                                                \
       const float* __restrict__ q, const float* __restrict__ kpool, const float* __restrict__ vpool,                 \
       const std::uint32_t* __restrict__ pages, const std::uint32_t* __restrict__ nkv, float* __restrict__ pm,        \
       float* __restrict__ pl, float* __restrict__ pacc, std::uint32_t S, std::uint32_t Hq, std::uint32_t Hkv,      \
@@ -494,7 +498,7 @@ HALO_ATTN_PARTIAL(halo_attn_decode_partial_mma, true)
 // _qk: up to 32 query vectors per block (S * Hq / Hkv <= 32), split-fp16 matrix cores; _qk2: up to 8 (two per
 // wave), fp32 VALU.
 #define HALO_ATTN_PARTIAL_QK(NAME, QW, MMA)                                                                           \
-  extern "C" __global__ void __launch_bounds__(256) NAME(                                                       \
+  extern "C" __global__ void __launch_bounds__(256, MMA ? 3 : 1) NAME(                                          \
       const float* __restrict__ qg, const float* __restrict__ kin, const float* __restrict__ vin,               \
       const float* __restrict__ wq, const float* __restrict__ wk, float* __restrict__ kpool,                    \
       float* __restrict__ vpool, const std::uint32_t* __restrict__ pages, const std::uint32_t* __restrict__ nkv, \

@@ -151,6 +151,17 @@ def _topk_cases(rng, E):
     r = rng.normal(0, 1, E)
     r[rng.choice(E, 40, replace=False)] = 4.0
     rows += [r, rng.normal(0, 1, E), rng.normal(0, 3, E)]
+    # 30 logits a few ulp apart at the top (probabilities that round together); one large logit over 100 near-zero
+    # ones that all round to the same l - max (more than 64 candidates, ranked in two passes); a spread so wide that
+    # selected probabilities are below 2^-100 or zero
+    r = rng.normal(0, 1, E).astype(np.float32)
+    r[rng.choice(E, 30, replace=False)] = np.float32(3.0) + rng.integers(0, 6, 30) * np.spacing(np.float32(3.0))
+    rows.append(r)
+    r = np.full(E, -5.0, np.float32)
+    r[rng.choice(E, 100, replace=False)] = (rng.normal(0, 1, 100) * 1e-7).astype(np.float32)
+    r[7] = 30.0
+    rows.append(r)
+    rows.append(rng.normal(0, 1, E) * 300.0)
     return np.stack(rows).astype(np.float32)
 
 

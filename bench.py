@@ -7,7 +7,7 @@ metric's "Q8_0 GEMV achieved HBM GB/s". Weights are seeded on the device and rot
 (graph replays of the rotation plus one graph of the remainder), after --warmup untimed ones.
 
 value    = algorithmic bytes of a GEMV (17,858,560: weights + x + y) / measured time per GEMV, in GB/s.
-roofline = the same kernel (halo_gemv_q8a8_l64_r1_b1) against 8 TB/s, with the calibrated PMC traffic from the
+roofline = the same kernel (halo_gemv_q8a8s_l64_r1_b1) against 8 TB/s, with the calibrated PMC traffic from the
            committed profile; moe.T1.roofline likewise for the MoE layer at one token.
 cpu_baseline = the reference's cpu::MatVec (built from its sources into oracle/_ref) on the same GEMV, all hardware
            threads, plus legs: 1 thread, the C1 projections, the C2 MoE layer at T=1 and the C3 recurrence at S=4.
@@ -1152,7 +1152,7 @@ def run_c0(args, dev, H, res):
         warm = args.warmup if t is None else 0
         # The timed region is one graph of exactly `steps` GEMVs, starting at copy `warm` (after the copies the
         # warm-up reads), with the timer's start and stop marks recorded inside it as event nodes, so the graph
-        # launch's own latency is outside the region. The graph is launched once untimed first (its first launch
+        # launch's own latency is outside the region. The graphs are launched once untimed first (a first launch
         # pays the upload), then the caches are flushed, then the warm-up GEMVs run on copies 0 .. warm - 1: every
         # timed GEMV reads weights that no launch touched since the flush.
         dev.begin_capture()
@@ -1161,12 +1161,14 @@ def run_c0(args, dev, H, res):
             gemv(ws0[(warm + i) % c0_copies], t)
         dev.launch("halo_clock_stamp", (1,), (64,), [stamps, ("u32", 1)])
         gt = dev.end_capture()
-        dev.launch_graph(gt)
-        flush_caches()
         gw, fw, rw = run_exact(t, warm) if warm else (None, 0, None)
+        for g_ in (gw, rw, gt):  # first launches (uploads) before the flush
+            if g_ is not None:
+                dev.launch_graph(g_)
         dev.sync()
-        # warm-up and timed launches queued back to back (no host wait between them, so the device does not idle
-        # and clock down before the timed region)
+        # cache flush, warm-up and timed launches queued back to back (no host wait between them, so the device does
+        # not idle and clock down before the timed region)
+        flush_caches()
         for _ in range(fw):
             dev.launch_graph(gw)
         if rw is not None:
@@ -1192,7 +1194,7 @@ def run_c0(args, dev, H, res):
                 traffic = int(line.split(":")[1])
     res["roofline"] = {
         "bound": "hbm",
-        "kernel": "halo_gemv_q8a8_l64_r1_b1 (C0 4096x4096 Q8_0 GEMV)",
+        "kernel": "halo_gemv_q8a8s_l64_r1_b1 (C0 4096x4096 Q8_0 GEMV)",
         "achieved": best["GBps"],
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",

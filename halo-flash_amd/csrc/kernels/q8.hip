@@ -1164,3 +1164,54 @@ extern "C" __global__ void __launch_bounds__(256) halo_zero16(int4* __restrict__
        i += static_cast<std::uint64_t>(gridDim.x) * blockDim.x)
     dst[i] = make_int4(0, 0, 0, 0);
 }
+
+// The batch-1 int8 GEMV with the activation row staged in LDS once per block (one row per wave, 4 waves): the
+// block's threads copy xq (16 bytes each) and xs into LDS by DMA before issuing their weight loads, then wait for
+// those two loads only (the weights stay in flight) and read the row from LDS: a wave issues 8 vector-memory loads
+// instead of 16, and the 4 KB row is read from L2 once per block instead of once per wave. Arithmetic and order are
+// those of halo_gemv_q8a8_l64_r1_b1 (bitwise the same y). cols 2048 or 4096, block 256, grid ceil(rows / 4).
+// (Copying each wave's row of weight scales by DMA as well, and 8- or 16-wave blocks, measured slower.)
+extern "C" __global__ void __launch_bounds__(256) halo_gemv_q8a8s_l64_r1_b1(
+    const std::int8_t* __restrict__ qs, const std::uint16_t* __restrict__ d, const std::int8_t* __restrict__ xq,
+    const float* __restrict__ xs, float* __restrict__ y, std::uint32_t rows, std::uint32_t cols,
+    std::uint32_t qstride, std::uint32_t ystride) {
+  __shared__ __attribute__((aligned(16))) std::int8_t xl[4096];
+  __shared__ __attribute__((aligned(16))) float sl[128];
+  const std::uint32_t tid = threadIdx.x, lane = tid % kWave, nblk = cols / 32;
+  const std::uint32_t wv = tid / kWave;
+  const std::uint32_t row = blockIdx.x * (blockDim.x / kWave) + wv;
+  const std::uint32_t lx = static_cast<std::uint32_t>(reinterpret_cast<std::uintptr_t>(xl));
+  const std::uint32_t ls = static_cast<std::uint32_t>(reinterpret_cast<std::uintptr_t>(sl));
+  // staging (a DMA load writes lane l's element at the wave-uniform LDS base + 4 l or 16 l): wave w copies the 64
+  // row pieces and the 64 scales from min(64 w, count - 64); a wave past the end repeats the last 64 (same bytes)
+  const std::uint32_t bx = min(64 * wv, cols / 16 - 64), bs = min(64 * wv, nblk - 64);
+  DmaRow16(xq, (bx + lane) * 16, lx + bx * 16);
+  DmaDword(xs + bs + lane, ls + bs * 4);
+  const std::uint32_t r = min(row, rows - 1);
+  const std::int8_t* rowp = qs + static_cast<std::size_t>(r) * qstride;
+  const std::uint16_t* dp = d + static_cast<std::size_t>(r) * nblk;
+  int4 q[4];
+  float s[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const std::uint32_t c = lane * 16 + u * 1024;
+    const std::uint32_t cc = c < cols ? c : lane * 16;
+    q[u] = __builtin_bit_cast(int4, __builtin_nontemporal_load(reinterpret_cast<const halo::V4i*>(rowp + cc)));
+    s[u] = F16(dp[cc / 32]);
+  }
+  WaitVmem<8>();  // the two staging loads (issued first) have landed; the 8 weight and scale loads stay in flight
+  __syncthreads();
+  float acc = 0.0f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const bool ok = lane * 16 + u * 1024 < cols;
+    const std::uint32_t cc = ok ? lane * 16 + u * 1024 : lane * 16;
+    const int4 xv = *reinterpret_cast<const int4*>(xl + cc);
+    const float sx = sl[cc / 32];
+    const float part = sx * static_cast<float>(Dot16(q[u], xv));
+    acc += (ok ? s[u] : 0.0f) * part;
+  }
+  acc = halo::GroupSum(acc);
+  if (lane == 0 && row < rows) y[row] = acc;
+  (void)ystride;
+}

@@ -120,7 +120,7 @@
   X(halo_gemv_q8r_i8_r1_b1) X(halo_gemv_q8r_i8_r2_b1) X(halo_gemv_q8r_i8_r4_b1)                              \
   X(halo_gemv_q8r_i8_r4_b4) X(halo_gemv_q8r_i8x_r4_b4) X(halo_gemv_q8r_i8_r4_b8)                             \
   X(halo_gemv_q8r_i8_dual_r4_b1) X(halo_gemv_q8r_i8x_dual_r4_b4) X(halo_gemv_q8r_dual)                        \
-  X(halo_gemv_q8a8_l64_r1_b1) X(halo_gemv_q8a8_l32_r1_b1) X(halo_gemv_q8a8_l16_r1_b1)                        \
+  X(halo_gemv_q8a8_l64_r1_b1) X(halo_gemv_q8a8s_l64_r1_b1) X(halo_gemv_q8a8_l32_r1_b1) X(halo_gemv_q8a8_l16_r1_b1) \
   X(halo_gemv_q8a8_l64_r2_b4) X(halo_gemv_q8a8_l64_r2_b8)                                                    \
   X(halo_q8_half_dots)                                                                                       \
   X(halo_rmsnorm) X(halo_l2norm) X(halo_rope_neox) X(halo_rope_neox_rows) X(halo_rope_neox_p)               \

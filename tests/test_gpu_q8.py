@@ -180,6 +180,24 @@ def test_c0_gemv_4096(dev):
     _check_y(gy.download(), want, mag)
 
 
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (1001, 4096), (998, 2048)])
+def test_gemv_lds_staged_bitwise(dev, rows, cols):
+    """halo_gemv_q8a8s_l64_r1_b1 (the activation row staged in LDS by DMA once per block) gives the bits of
+    halo_gemv_q8a8_l64_r1_b1 (the same per-wave arithmetic, activations read per wave), and both meet the oracle."""
+    rng = np.random.default_rng(rows + cols)
+    w, xq, xs, want, mag = _gemv_case(dev, rng, rows, cols, 1)
+    gq, gs = dev.to_device(xq), dev.to_device(xs)
+    ys = []
+    for name in ("halo_gemv_q8a8_l64_r1_b1", "halo_gemv_q8a8s_l64_r1_b1"):
+        gy = dev.array(rows, np.float32)
+        dev.launch(name, ((rows + 3) // 4,), (256,), [w.qs, w.d, gq, gs, gy, ("u32", rows),
+                                                      ("u32", cols), ("u32", w.qstride), ("u32", rows)])
+        ys.append(gy.download())
+    for y_ in ys[1:]:
+        assert np.array_equal(ys[0].view(np.uint32), y_.view(np.uint32))
+    _check_y(ys[1][None, :], want, mag)
+
+
 @pytest.mark.parametrize("rows,cols", [(4096, 2048), (512, 2048), (2048, 4096)])
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 16])
 def test_c1_projections(dev, rows, cols, m):

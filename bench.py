@@ -3,8 +3,8 @@
 
 Headline workload (C0, batch 1): one Q8_0 GEMV, W [4096 x 4096] x Q8_0-quantized x, the
 metric's "Q8_0 GEMV achieved HBM GB/s". Weights are seeded on the device and rotated over enough distinct copies
-(>= 600 MB) that no launch reads weights from the 256 MB MALL. A step is one GEMV; exactly --steps GEMVs are timed
-(graph replays of the rotation plus one graph of the remainder), after --warmup untimed ones.
+(>= 600 MB) that no launch reads weights from the 256 MB MALL. A step is one GEMV; exactly --steps GEMVs are timed,
+after --warmup untimed ones in the same graph, between two device wall-clock stamps.
 
 value    = algorithmic bytes of a GEMV (17,858,560: weights + x + y) / measured time per GEMV, in GB/s.
 roofline = the same kernel (halo_gemv_q8a8s_l64_r1_b1) against 8 TB/s, with the calibrated PMC traffic from the
@@ -1224,9 +1224,9 @@ def run_c0(args, dev, H, res):
         "traffic_source": "profiles/gemv_q8a8_c0_4096x4096.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)",
         "us_per_launch": best["us_per_gemv"],
         "algorithmic_bytes_per_launch": C0_BYTES,
-        "timing": ("device wall clock (halo_clock_stamp nodes) at the start and end of one graph of exactly `steps` "
-                   "back-to-back launches, queued right after the warm-up launches, less the stamps' own time (two "
-                   "stamps back to back, median of 20)"),
+        "timing": ("device wall clock (halo_clock_stamp nodes) around exactly `steps` back-to-back launches, inside "
+                   "one graph after the warm-up launches and right after a 512 MB cache flush, less the stamps' own "
+                   "time (two stamps back to back, median of 20)"),
         "stamp_overhead_us": round(stamp_ms * 1e3, 3),
     }
     if args.sweep:

@@ -1199,7 +1199,9 @@ extern "C" __global__ void __launch_bounds__(256) halo_gemv_q8a8s_l64_r1_b1(
     q[u] = __builtin_bit_cast(int4, __builtin_nontemporal_load(reinterpret_cast<const halo::V4i*>(rowp + cc)));
     s[u] = F16(dp[cc / 32]);
   }
-  WaitVmem<8>();  // the two staging loads (issued first) have landed; the 8 weight and scale loads stay in flight
+  // the two staging loads (issued first) have landed; the 8 weight and scale loads stay in flight (loads complete in
+  // issue order; the count of loads the compiler emits between the DMAs and this wait is checked on the built code)
+  WaitVmem<8>();
   __syncthreads();
   float acc = 0.0f;
 #pragma unroll

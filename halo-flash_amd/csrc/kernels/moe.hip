@@ -557,6 +557,19 @@ __device__ __forceinline__ void MoeGateUp(
   std::uint32_t np, f;
   std::size_t e = 0;
   const std::uint32_t* ids = ids_in;
+  // the activation pieces of the block's first row (its pair's token; token 0 for the shared expert) do not depend
+  // on the routing: loaded first, they land while the routing and the ownership check run
+  int4 x0[kSteps];
+  float s0[kSteps];
+  {
+    const std::uint32_t tok0 = shared ? 0u : px / k;
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) {
+      const std::uint32_t c = st * kWave * 16 + lane * 16;
+      x0[st] = *reinterpret_cast<const int4*>(xq + static_cast<std::size_t>(tok0) * H + c);
+      s0[st] = xs[static_cast<std::size_t>(tok0) * nblk + c / 32];
+    }
+  }
   if (shared) {
     if (sgq == nullptr || blockIdx.y * (blockDim.x / kWave) >= sff) return;
     np = T;
@@ -633,8 +646,9 @@ __device__ __forceinline__ void MoeGateUp(
 #pragma unroll
     for (int st = 0; st < kSteps; ++st) {
       const std::uint32_t c = st * kWave * 16 + lane * 16;
-      const int4 xv = *reinterpret_cast<const int4*>(xt + c);
-      const float sx = st_[c / 32];
+      // the first row's pieces were loaded at the start (lp = 0 is the pair's own token, or token 0 shared)
+      const int4 xv = lp == 0 ? x0[st] : *reinterpret_cast<const int4*>(xt + c);
+      const float sx = lp == 0 ? s0[st] : st_[c / 32];
       g += sw[0][st] * (sx * static_cast<float>(Dot16(w[0][st], xv)));
       u += sw[1][st] * (sx * static_cast<float>(Dot16(w[1][st], xv)));
     }

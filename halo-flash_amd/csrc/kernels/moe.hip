@@ -561,6 +561,9 @@ __device__ __forceinline__ void MoeGateUp(
   // on the routing: loaded first, they land while the routing and the ownership check run
   int4 x0[kSteps];
   float s0[kSteps];
+  // likewise this thread's entry of the pair ids (several tokens: the ownership check reads them all)
+  std::uint32_t idpre = 0;
+  if constexpr (kTopKPer == 0) idpre = ids_in[min(static_cast<std::uint32_t>(threadIdx.x), T * k - 1)];
   {
     const std::uint32_t tok0 = shared ? 0u : px / k;
 #pragma unroll
@@ -624,7 +627,7 @@ __device__ __forceinline__ void MoeGateUp(
     }
     __syncthreads();
     for (std::uint32_t i = threadIdx.x; i < T * k; i += blockDim.x)
-      if (ids[i] == e) {
+      if ((i == threadIdx.x ? idpre : ids[i]) == e) {
         if (i / k < t) owner = 0;
         atomicOr(&tokmask, 1u << (i / k));
       }
@@ -633,7 +636,7 @@ __device__ __forceinline__ void MoeGateUp(
     const std::uint32_t m = tokmask;
     np = static_cast<std::uint32_t>(__builtin_popcount(m));
     for (std::uint32_t i = threadIdx.x; i < T * k; i += blockDim.x)
-      if (ids[i] == e) rows_s[__builtin_popcount(m & ((1u << (i / k)) - 1u))] = i;
+      if ((i == threadIdx.x ? idpre : ids[i]) == e) rows_s[__builtin_popcount(m & ((1u << (i / k)) - 1u))] = i;
   }
   if (T > 1) __syncthreads();
   if (j >= f) return;

@@ -198,7 +198,7 @@ __device__ __forceinline__ void AttnDecodePartial(
       reinterpret_cast<float4*>(&qs[qi][0])[d4] = v;
     }
   }
-  if constexpr (kFused) issue_v();
+  if constexpr (kFused && !kMma) issue_v();
   if constexpr (!kMma) {
   __syncthreads();
   HALO_PHASE(1, 1);
@@ -372,6 +372,9 @@ __device__ __forceinline__ void AttnDecodePartial(
   }
   __syncthreads();
   HALO_PHASE(1, 2);
+  // fused: the V chunk issued only now that the K fragments are in LDS (its 32 destination registers and the K
+  // fragments are never live together)
+  if constexpr (kFused) issue_v();
   const float scale = 1.0f / sqrtf(static_cast<float>(kHd));
   if (score_wave) {
     V4F c4 = {0.0f, 0.0f, 0.0f, 0.0f};

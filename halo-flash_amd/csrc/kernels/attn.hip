@@ -155,7 +155,7 @@ __device__ __forceinline__ void AttnDecodePartial(
   }
   }
   };
-  if constexpr (!kFused) issue_v();
+  if constexpr (!kFused && !kMma) issue_v();
   // queries of this kv head: slot i = session * G + g (prefix) or g (suffix)
   __shared__ __attribute__((aligned(16))) float knew[kFused ? 2 : 1][kFused ? kHd : 4];
   if constexpr (kFused) {
@@ -372,9 +372,9 @@ __device__ __forceinline__ void AttnDecodePartial(
   }
   __syncthreads();
   HALO_PHASE(1, 2);
-  // fused: the V chunk issued only now that the K fragments are in LDS (its 32 destination registers and the K
-  // fragments are never live together)
-  if constexpr (kFused) issue_v();
+  // the V chunk issued only now that the K fragments are in LDS (its 32 destination registers and the K fragments
+  // are never live together: held together they spilled, and the spill's reloads waited for V before the K phase)
+  issue_v();
   const float scale = 1.0f / sqrtf(static_cast<float>(kHd));
   if (score_wave) {
     V4F c4 = {0.0f, 0.0f, 0.0f, 0.0f};

@@ -434,12 +434,17 @@ __device__ __forceinline__ void ProjQ8Mfma(const std::int8_t* __restrict__ xq, c
 #pragma unroll
   for (int s = 0; s < S; ++s) x[s] = *reinterpret_cast<const int4*>(xp + 64 * s);
   __builtin_amdgcn_sched_barrier(0);
+  // unconditional stores (a thread past the table rewrites its last entry with the value it loaded for it): a
+  // store under `e < nblk * 16` let the compiler sink that load into the branch, where it waited for the weights
 #pragma unroll
   for (std::uint32_t j = 0; j < kSx; ++j) {
-    const std::uint32_t e = tid + kThreads * j, b = e / 16, t = e % 16;
-    if (e < nblk * 16) sxt[b][t] = t < T ? sxr[j] : 0.0f;
+    const std::uint32_t e = min(tid + kThreads * j, nblk * 16 - 1), b = e / 16, t = e % 16;
+    sxt[b][t] = t < T ? sxr[j] : 0.0f;
   }
+  // nothing of the products moves above the barrier (a product hoisted there waits for the weights first)
+  __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   const bool first_half = g < 2;
 #pragma unroll

@@ -503,4 +503,17 @@ __device__ __forceinline__ V4F Mfma3(const H8& ah, const H8& al, const H8& bh, c
   c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, c, 0, 0, 0);
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, c, 0, 0, 0);
 }
+
+// Global -> LDS loads that bypass registers (wave-uniform LDS base in M0; lane l's element lands at base + 16 l or
+// base + 4 l) and a wait on the vector-memory counter by count (loads complete in issue order).
+__device__ __forceinline__ void DmaRow16(const void* sbase, std::uint32_t voff, std::uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void DmaDword(const void* addr, std::uint32_t lds) {
+  asm volatile("global_load_lds_dword %0, off" ::"v"(addr), "{m0}"(lds) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void WaitVmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 }  // namespace halo

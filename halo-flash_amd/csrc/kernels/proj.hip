@@ -205,29 +205,29 @@ __device__ __forceinline__ void ProjQ8(const float* __restrict__ x, const float*
       LoadTask<LPR>(cur[i], min(task0 + kWaves * i, o4 - 1), o1, o2, o3, qs0, d0, rows0, qs1, d1, rows1, qs2, d2, rows2,
                     qs3, d3, rows3, cols);
   } else if constexpr (kMode == 0) {
-    // quantized rows: every token's 16 bytes and scale are loaded first (a clamped token past T reloads the last),
-    // then the weights; one round trip for all tokens instead of one per token
-    int4 xvs[NB];
-    float xss[NB];
+    // quantized rows straight into LDS, issued before the weights: every token's row (wave w its 16-byte pieces
+    // 64 w .. 64 w + 63, from clamped addresses; pieces past the row land in the row's unused tail) and, by waves 0
+    // and 1, its scales (128 slots, those past nblk unused); a clamped token past T reloads the last. Register
+    // staging let the compiler sink the row loads behind the weights, so the block waited for its weights before
+    // its barrier.
+    const std::uint32_t lx = static_cast<std::uint32_t>(reinterpret_cast<std::uintptr_t>(&lxq[0][0]));
+    const std::uint32_t ls = static_cast<std::uint32_t>(reinterpret_cast<std::uintptr_t>(&lxs[0][0]));
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const std::uint32_t bb = min(static_cast<std::uint32_t>(b), T - 1);
-      xvs[b] = reinterpret_cast<const int4*>(xq_in + static_cast<std::size_t>(bb) * cols)[min(threadIdx.x, cols / 16 - 1)];
-      xss[b] = xs_in[static_cast<std::size_t>(bb) * nblk + min(threadIdx.x, nblk - 1)];
+      halo::DmaRow16(xq_in + static_cast<std::size_t>(bb) * cols, min(64 * wave + lane, cols / 16 - 1) * 16,
+                     lx + b * kProjMaxCols + 64 * wave * 16);
+      if (wave < 2)
+        halo::DmaDword(xs_in + static_cast<std::size_t>(bb) * nblk + min(64 * wave + lane, nblk - 1),
+                       ls + (b * (kProjMaxCols / 32) + 64 * wave) * 4);
     }
-    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < TPW; ++i)
       LoadTask<LPR>(cur[i], min(task0 + kWaves * i, o4 - 1), o1, o2, o3, qs0, d0, rows0, qs1, d1, rows1, qs2, d2, rows2,
                     qs3, d3, rows3, cols);
-    __builtin_amdgcn_sched_barrier(0);
-    // unconditional stores (a thread past the row writes the clamped piece its neighbour writes, the same bytes;
-    // rows past T are never read), so the loads above are not sunk into a branch that waits on them one by one
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      reinterpret_cast<int4*>(&lxq[b][0])[min(threadIdx.x, cols / 16 - 1)] = xvs[b];
-      lxs[b][min(threadIdx.x, nblk - 1)] = xss[b];
-    }
+    // the rows and scales have landed; the weights (8 loads a task) stay in flight (the count of loads between the
+    // DMAs and this wait is checked on the built code)
+    halo::WaitVmem<8 * TPW>();
   } else {
   load_token(0);
   // The tasks' loads are unconditional (a load in a conditional block costs a vmcnt(0) wait at the join): a

@@ -915,17 +915,10 @@ __device__ __forceinline__ void GemmTileQ8(const std::int8_t* __restrict__ A0, c
 // address is a per-lane constant plus an immediate. The scale MFMA is the two-block rank-1 v_mfma_f32_32x32x1_2b,
 // covering two tiles (NMAT * MT even) or both blocks of the stage (a single tile).
 // Limits: cols % 64 == 0; every weight offset (rows * qstride) and activation offset fits in 32 bits.
+using halo::DmaDword;
+using halo::DmaRow16;
+using halo::WaitVmem;
 namespace {
-__device__ __forceinline__ void DmaRow16(const void* sbase, std::uint32_t voff, std::uint32_t lds) {
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
-}
-__device__ __forceinline__ void DmaDword(const void* addr, std::uint32_t lds) {
-  asm volatile("global_load_lds_dword %0, off" ::"v"(addr), "{m0}"(lds) : "memory");
-}
-template <int N>
-__device__ __forceinline__ void WaitVmem() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
 __device__ __forceinline__ std::uint32_t ChunkSwz(std::uint32_t r) { return (r >> 2) & 3u; }
 // An empty asm that reads and writes the 16 values: everything computing them is done before this point.
 __device__ __forceinline__ void PinVgprs(float (&a)[16]) {

@@ -39,7 +39,7 @@ constexpr double kFix = 1099511627776.0;  // 2^40
 constexpr std::uint64_t kNoBound = ~0ull;
 
 struct Lds {
-  union {
+  union alignas(16) {
     std::uint32_t bitmap[HALO_SAMPLE_MAX_VOCAB / 32];
     double w[kCap];
   } a;
@@ -327,58 +327,93 @@ __device__ RowMax ReduceParts(const Ws& w, std::uint32_t row, std::uint32_t nb, 
   return RowMax{k, tk, nf};
 }
 
-// Sequential double chains in list order on one lane (they must stay left-to-right to round as the CPU does).
-// Each chunk of 16 runs its adds back to back without branches (the LDS loads issued ahead) and tests the 16
-// partial results afterwards, so an element costs about one add latency.
+// Sequential double chains in list order on one lane (they must stay left-to-right to round as the CPU does), over
+// the on-chip candidate list w[kCap] (n <= kCap). Chunks of 16 are read whole as 8 double2 (in bounds: a chunk starts
+// below n <= kCap, a multiple of 16); full chunks add without per-entry bounds tests, the last one selects entries
+// past n to +0.0 (adding +0.0 to a sum of non-negative weights leaves it unchanged), and a chunk's tests are folded
+// into a bit mask off the add chain, so an element costs about one add latency.
+struct SeqChunk {
+  double v[16];
+};
+__device__ __forceinline__ SeqChunk SeqLoad(const double* w, std::uint32_t k0, std::uint32_t n) {
+  const double2* p = reinterpret_cast<const double2*>(w + k0);
+  SeqChunk c;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const double2 d = p[j];
+    c.v[2 * j] = d.x;
+    c.v[2 * j + 1] = d.y;
+  }
+  if (k0 + 16 > n) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) c.v[j] = k0 + j < n ? c.v[j] : 0.0;
+  }
+  return c;
+}
 __device__ double SeqSum(const double* w, std::uint32_t n) {
   double sum = 0.0;
   for (std::uint32_t k0 = 0; k0 < n; k0 += 16) {
-    double v[16];
+    const SeqChunk c = SeqLoad(w, k0, n);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = k0 + j < n ? w[k0 + j] : 0.0;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) sum += v[j];  // adding +0.0 past the end leaves the sum unchanged
+    for (int j = 0; j < 16; ++j) sum += c.v[j];
   }
   return sum;
 }
+// Entry j of a chunk's 16 values (a select chain, not a dynamic register index).
+__device__ __forceinline__ double SeqPick(const double (&c)[16], std::uint32_t j) {
+  double v = c[0];
+#pragma unroll
+  for (std::uint32_t i = 1; i < 16; ++i) v = i == j ? c[i] : v;
+  return v;
+}
 // The first k (1-based) with k >= minimum and w[0] + ... + w[k-1] >= target, scanning at most n entries; n + 1
-// when the scan ends first.
-__device__ std::uint32_t SeqCut(const double* w, std::uint32_t n, std::uint32_t minimum, double target) {
+// when the scan ends first. The weights are >= 0, so the rounded running sum never decreases: a chunk holds the
+// first crossing exactly when its last sum crosses, so only that sum is tested per chunk (the chain costs one add
+// per element) and the crossing chunk's sums are searched once. *at_cut receives w[0] + ... + w[k-1] when k is the
+// crossing itself (the same adds in the same order as SeqSum over k entries), else -1.
+__device__ std::uint32_t SeqCut(const double* w, std::uint32_t n, std::uint32_t minimum, double target,
+                                double* at_cut) {
+  *at_cut = -1.0;
   double cum = 0.0;
   for (std::uint32_t k0 = 0; k0 < n; k0 += 16) {
-    double v[16], c[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = k0 + j < n ? w[k0 + j] : 0.0;
+    const SeqChunk c = SeqLoad(w, k0, n);
+    double cs[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      cum += v[j];
-      c[j] = cum;
+      cum += c.v[j];
+      cs[j] = cum;
     }
-    std::uint32_t hit = 16;
+    if (cum >= target) {  // entries past n add +0.0, so the crossing lies below n
+      std::uint32_t hit = 0;
 #pragma unroll
-    for (int j = 15; j >= 0; --j)
-      if (k0 + j < n && k0 + j + 1 >= minimum && c[j] >= target) hit = j;
-    if (hit < 16) return k0 + hit + 1;
+      for (int j = 0; j < 16; ++j) hit |= static_cast<std::uint32_t>(cs[j] >= target) << j;
+      const std::uint32_t j = __builtin_ctz(hit), k = k0 + j + 1;
+      if (k >= minimum) {
+        *at_cut = SeqPick(cs, j);
+        return k;
+      }
+      return minimum <= n ? minimum : n + 1;  // the sums only grow: the first k >= minimum crosses too
+    }
   }
   return n + 1;
 }
-// The first i with u - p[0] - ... - p[i] < 0, or n when none.
+// The first i with u - p[0] - ... - p[i] < 0, or n when none (the remainder never grows: p >= 0).
 __device__ std::uint32_t SeqWalk(const double* pr, std::uint32_t n, double u) {
   double r = u;
   for (std::uint32_t k0 = 0; k0 < n; k0 += 16) {
-    double v[16], c[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = k0 + j < n ? pr[k0 + j] : 0.0;
+    const SeqChunk c = SeqLoad(pr, k0, n);
+    double rs[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      r -= v[j];
-      c[j] = r;
+      r -= c.v[j];
+      rs[j] = r;
     }
-    std::uint32_t hit = 16;
+    if (r < 0.0) {
+      std::uint32_t hit = 0;
 #pragma unroll
-    for (int j = 15; j >= 0; --j)
-      if (k0 + j < n && c[j] < 0.0) hit = j;
-    if (hit < 16) return k0 + hit;
+      for (int j = 0; j < 16; ++j) hit |= static_cast<std::uint32_t>(rs[j] < 0.0) << j;
+      return k0 + __builtin_ctz(hit);
+    }
   }
   return n;
 }
@@ -797,16 +832,28 @@ extern "C" __global__ void __launch_bounds__(1024)
     std::uint32_t mt = 0;
     BlockMinPair(mk, mt, s);
     if (static_cast<std::uint32_t>(~mk) <= 512) {
-      for (std::uint32_t i = t; i < n; i += kThreads) {
-        const std::uint64_t k = w.ckey[static_cast<std::size_t>(row) * kCap + i];
-        const std::uint32_t bin = Bin(M, KeyValue(k));
-        const std::uint32_t at = s.b.hist[bin] + atomicAdd(&s.a.bitmap[bin], 1u);
-        s.key[at] = k;
-        s.tok[at] = w.ctok[static_cast<std::size_t>(row) * kCap + i];
+      // n <= kCap: every candidate's reads issued before the first scatter
+      constexpr std::uint32_t kPerE = kCap / kThreads;
+      std::uint64_t gk[kPerE];
+      std::uint32_t gt[kPerE];
+#pragma unroll
+      for (std::uint32_t j = 0; j < kPerE; ++j) {
+        const std::uint32_t i = t + kThreads * j;
+        if (i < n) {
+          gk[j] = w.ckey[static_cast<std::size_t>(row) * kCap + i];
+          gt[j] = w.ctok[static_cast<std::size_t>(row) * kCap + i];
+        }
       }
+#pragma unroll
+      for (std::uint32_t j = 0; j < kPerE; ++j)
+        if (t + kThreads * j < n) {
+          const std::uint32_t bin = Bin(M, KeyValue(gk[j]));
+          const std::uint32_t at = s.b.hist[bin] + atomicAdd(&s.a.bitmap[bin], 1u);
+          s.key[at] = gk[j];
+          s.tok[at] = gt[j];
+        }
       __syncthreads();
       // rank within the bin by (key, token), then move every element to start + rank
-      constexpr std::uint32_t kPerE = kCap / kThreads;
       std::uint64_t ek[kPerE];
       std::uint32_t et[kPerE], pos[kPerE];
 #pragma unroll
@@ -819,9 +866,19 @@ extern "C" __global__ void __launch_bounds__(1024)
           const std::uint32_t bin = Bin(M, KeyValue(ek[j]));
           const std::uint32_t b0 = s.b.hist[bin], cnt = s.a.bitmap[bin];
           std::uint32_t r = 0;
-          for (std::uint32_t q = b0; q < b0 + cnt; ++q) {
-            const std::uint64_t kq = s.key[q];
-            r += kq < ek[j] || (kq == ek[j] && s.tok[q] < et[j]);
+          for (std::uint32_t q0 = b0; q0 < b0 + cnt; q0 += 4) {  // four reads in flight per step
+            std::uint64_t kq[4];
+            std::uint32_t tq[4];
+#pragma unroll
+            for (std::uint32_t u = 0; u < 4; ++u) {
+              const std::uint32_t q = min(q0 + u, kCap - 1);
+              kq[u] = s.key[q];
+              tq[u] = s.tok[q];
+            }
+#pragma unroll
+            for (std::uint32_t u = 0; u < 4; ++u)  // bitwise, not short-circuit: no branches
+              r += static_cast<std::uint32_t>((q0 + u < b0 + cnt) &
+                                              ((kq[u] < ek[j]) | ((kq[u] == ek[j]) & (tq[u] < et[j]))));
           }
           pos[j] = b0 + r;
         }
@@ -896,6 +953,7 @@ extern "C" __global__ void __launch_bounds__(1024)
   if (t == 0) {
     std::uint32_t keep = K0;
     bool large = false;
+    double cut_sum = -1.0;  // the sum over the kept prefix when the top-p cut produced it
     if (p.top_p < 1.0f && K0 > 1) {
       double sum = full_sum;
       if (!has_full) {
@@ -903,20 +961,26 @@ extern "C" __global__ void __launch_bounds__(1024)
         else sum = SeqSum(s.a.w, K0);
       }
       if (!large) {
-        const std::uint32_t k = SeqCut(s.a.w, min(K0, Rc), minimum, static_cast<double>(p.top_p) * sum);
+        double at_cut;
+        const std::uint32_t k =
+            SeqCut(s.a.w, min(K0, Rc), minimum, static_cast<double>(p.top_p) * sum, &at_cut);
         if (k > min(K0, Rc)) {
           if (Rc < K0) large = true;  // the cut lies past the sorted candidates
           else keep = K0;
         } else {
           keep = k;
+          cut_sum = at_cut;
         }
       }
     }
     s.bu[5] = keep;
     s.bu[6] = large;
+    s.bd[2] = cut_sum;
   }
   __syncthreads();
-  std::uint32_t keep = s.bu[5];
+  const std::uint32_t keep_top_p = s.bu[5];
+  const double cut_sum = s.bd[2];
+  std::uint32_t keep = keep_top_p;
   bool large = s.bu[6] != 0;
   __syncthreads();
   if (!large && p.min_p > 0.0f && keep > 1) {
@@ -931,7 +995,8 @@ extern "C" __global__ void __launch_bounds__(1024)
   }
   if (!large && keep > Rc) large = true;
   if (!large) {
-    if (t == 0) s.bd[0] = SeqSum(s.a.w, keep);
+    // the cut's own running sum when min-p kept the whole top-p prefix (bitwise SeqSum over it)
+    if (t == 0) s.bd[0] = keep == keep_top_p && cut_sum >= 0.0 ? cut_sum : SeqSum(s.a.w, keep);
     __syncthreads();
     const double total = s.bd[0];
     std::uint32_t nz = 0, last = 0;

@@ -807,21 +807,49 @@ extern "C" __global__ void __launch_bounds__(1024)
   std::uint32_t n;
   bool sorted = false;
   if (collected) {
-    // The candidates are every token in bins 0..cut, so the histogram gives each bin's place in the sorted list:
-    // scatter them to their bin's range and sort within bins (one lane per bin), unless a bin is too full for that.
+    // The candidates are every token in bins 0..cut: values within (cut + 1) / 64 of the maximum. They are counted
+    // again on chip over kBins finer bins spanning that range (the coarse bins themselves when the last one, which is
+    // open-ended, is in), a scan of the counts gives each bin's place in the sorted list, and the candidates are
+    // scattered to their bin's range and ranked within it (a few per bin, so the rank loop is short), unless a bin
+    // is too full for that. The bin is a non-decreasing function of max - value, so bin order is list order.
     n = w.cn[row];
-    const std::uint32_t* gh = w.hist + static_cast<std::size_t>(row) * kBins;
+    constexpr std::uint32_t kPerE = kCap / kThreads;  // n <= kCap
     constexpr std::uint32_t kPerT = kBins / kThreads;
+    std::uint64_t gk[kPerE];
+    std::uint32_t gt[kPerE], gb[kPerE];
+#pragma unroll
+    for (std::uint32_t j = 0; j < kPerE; ++j) {
+      const std::uint32_t i = t + kThreads * j;
+      if (i < n) {
+        gk[j] = w.ckey[static_cast<std::size_t>(row) * kCap + i];
+        gt[j] = w.ctok[static_cast<std::size_t>(row) * kCap + i];
+      }
+    }
+    // (max - value) * 64 is exact, so scale 64 reproduces the coarse bins
+    const double scale = cut < kBins - 1 ? static_cast<double>(kBins) * 64.0 / static_cast<double>(cut + 1) : 64.0;
+    const auto bin_of = [&](std::uint64_t k) -> std::uint32_t {
+      const double d = (M - KeyValue(k)) * scale;
+      return d < static_cast<double>(kBins) ? static_cast<std::uint32_t>(d) : kBins - 1;
+    };
+#pragma unroll
+    for (std::uint32_t j = 0; j < kPerT; ++j) s.b.hist[t * kPerT + j] = 0;
+    __syncthreads();
+#pragma unroll
+    for (std::uint32_t j = 0; j < kPerE; ++j)
+      if (t + kThreads * j < n) {
+        gb[j] = bin_of(gk[j]);
+        atomicAdd(&s.b.hist[gb[j]], 1u);
+      }
+    __syncthreads();
     std::uint32_t c[kPerT], c4 = 0, cmax = 0;
 #pragma unroll
     for (std::uint32_t j = 0; j < kPerT; ++j) {
-      const std::uint32_t bin = t * kPerT + j;
-      c[j] = bin <= cut ? gh[bin] : 0;
+      c[j] = s.b.hist[t * kPerT + j];
       c4 += c[j];
       cmax = max(cmax, c[j]);
     }
     std::uint32_t tot;
-    std::uint32_t start = BlockExclScan(c4, s.ru, &tot);
+    std::uint32_t start = BlockExclScan(c4, s.ru, &tot);  // its barriers order the reads above before the writes
 #pragma unroll
     for (std::uint32_t j = 0; j < kPerT; ++j) {
       s.b.hist[t * kPerT + j] = start;  // bin start
@@ -832,23 +860,10 @@ extern "C" __global__ void __launch_bounds__(1024)
     std::uint32_t mt = 0;
     BlockMinPair(mk, mt, s);
     if (static_cast<std::uint32_t>(~mk) <= 512) {
-      // n <= kCap: every candidate's reads issued before the first scatter
-      constexpr std::uint32_t kPerE = kCap / kThreads;
-      std::uint64_t gk[kPerE];
-      std::uint32_t gt[kPerE];
-#pragma unroll
-      for (std::uint32_t j = 0; j < kPerE; ++j) {
-        const std::uint32_t i = t + kThreads * j;
-        if (i < n) {
-          gk[j] = w.ckey[static_cast<std::size_t>(row) * kCap + i];
-          gt[j] = w.ctok[static_cast<std::size_t>(row) * kCap + i];
-        }
-      }
 #pragma unroll
       for (std::uint32_t j = 0; j < kPerE; ++j)
         if (t + kThreads * j < n) {
-          const std::uint32_t bin = Bin(M, KeyValue(gk[j]));
-          const std::uint32_t at = s.b.hist[bin] + atomicAdd(&s.a.bitmap[bin], 1u);
+          const std::uint32_t at = s.b.hist[gb[j]] + atomicAdd(&s.a.bitmap[gb[j]], 1u);
           s.key[at] = gk[j];
           s.tok[at] = gt[j];
         }
@@ -863,7 +878,7 @@ extern "C" __global__ void __launch_bounds__(1024)
         if (i < n) {
           ek[j] = s.key[i];
           et[j] = s.tok[i];
-          const std::uint32_t bin = Bin(M, KeyValue(ek[j]));
+          const std::uint32_t bin = bin_of(ek[j]);
           const std::uint32_t b0 = s.b.hist[bin], cnt = s.a.bitmap[bin];
           std::uint32_t r = 0;
           for (std::uint32_t q0 = b0; q0 < b0 + cnt; q0 += 4) {  // four reads in flight per step
@@ -892,10 +907,12 @@ extern "C" __global__ void __launch_bounds__(1024)
         }
       sorted = true;
     } else {
-      for (std::uint32_t i = t; i < n; i += kThreads) {
-        s.key[i] = w.ckey[static_cast<std::size_t>(row) * kCap + i];
-        s.tok[i] = w.ctok[static_cast<std::size_t>(row) * kCap + i];
-      }
+#pragma unroll
+      for (std::uint32_t j = 0; j < kPerE; ++j)
+        if (t + kThreads * j < n) {
+          s.key[t + kThreads * j] = gk[j];
+          s.tok[t + kThreads * j] = gt[j];
+        }
     }
     Rc = min(n, K0);
   } else {

@@ -424,9 +424,13 @@ __device__ std::uint32_t SeqWalk(const double* pr, std::uint32_t n, double u) {
 // without top-k takes the bins before it (still a full prefix of the sorted order), unless that is empty.
 __device__ bool HistCut(const std::uint32_t* hist, std::uint32_t Rc, bool topk, std::uint32_t* cut,
                         std::uint32_t* red, std::uint32_t* out2) {
-  const std::uint32_t per = kBins / blockDim.x;
-  std::uint32_t c = 0;
-  for (std::uint32_t j = 0; j < per; ++j) c += hist[threadIdx.x * per + j];
+  constexpr std::uint32_t per = kBins / kThreads;  // both callers run kThreads threads
+  std::uint32_t h[per], c = 0;
+#pragma unroll
+  for (std::uint32_t j = 0; j < per; ++j) {
+    h[j] = hist[threadIdx.x * per + j];  // read once, kept for the crossing search
+    c += h[j];
+  }
   std::uint32_t tot;
   std::uint32_t base = BlockExclScan(c, red, &tot);
   if (threadIdx.x == 0) {
@@ -434,14 +438,15 @@ __device__ bool HistCut(const std::uint32_t* hist, std::uint32_t Rc, bool topk, 
     out2[1] = 0;
   }
   __syncthreads();
+#pragma unroll
   for (std::uint32_t j = 0; j < per; ++j) {
-    const std::uint32_t bin = threadIdx.x * per + j, h = hist[bin];
-    if (base < Rc && base + h >= Rc) {
+    const std::uint32_t bin = threadIdx.x * per + j;
+    if (base < Rc && base + h[j] >= Rc) {
       out2[0] = bin;
       out2[1] = base;  // count before the crossing bin
-      out2[2] = base + h;
+      out2[2] = base + h[j];
     }
-    base += h;
+    base += h[j];
   }
   __syncthreads();
   const std::uint32_t bc = out2[0], before = out2[1], through = out2[2];

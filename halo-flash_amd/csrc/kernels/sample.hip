@@ -35,6 +35,8 @@ constexpr std::uint32_t kThreads = 1024;
 constexpr std::uint32_t kWaves = kThreads / kWave;
 constexpr std::uint32_t kCap = kSampleCap;   // candidates sorted on chip
 constexpr std::uint32_t kBins = kSampleBins;  // histogram of max - v, bins 1/64 wide, the last one open-ended
+static_assert((HALO_SAMPLE_MAX_VOCAB + kSampleSlice - 1) / kSampleSlice <= kWave,
+              "one wave holds every slice's partials");
 constexpr double kFix = 1099511627776.0;  // 2^40
 constexpr std::uint64_t kNoBound = ~0ull;
 
@@ -53,6 +55,9 @@ struct Lds {
   std::uint64_t key[kCap];
   std::uint32_t tok[kCap];
   double rd[kWaves];
+  double xd;  // wave-0 reductions of the per-slice partials, broadcast
+  std::uint32_t xu;
+  unsigned long long xq[2];
   std::uint32_t ru[kWaves];
   unsigned long long rq[kWaves];
   std::uint64_t bq[4];
@@ -96,8 +101,24 @@ __device__ __forceinline__ double Penalize(double l, const HaloSampleParams& p, 
 
 // ---- block-wide reductions in a fixed order (every thread calls; every thread gets the result) --------------
 template <typename T>
-__device__ T BlockSum(T v, T* red) {
+__device__ T WaveSum(T v) {
   for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+// Smallest (key, token) pair over the wave.
+__device__ void WaveMinPair(std::uint64_t& k, std::uint32_t& t) {
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    const std::uint64_t ok = __shfl_xor(k, o, kWave);
+    const std::uint32_t ot = __shfl_xor(t, o, kWave);
+    if (ok < k || (ok == k && ot < t)) {
+      k = ok;
+      t = ot;
+    }
+  }
+}
+template <typename T>
+__device__ T BlockSum(T v, T* red) {
+  v = WaveSum(v);
   if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = v;
   __syncthreads();
   T r = 0;
@@ -132,14 +153,7 @@ __device__ T BlockExclScan(T v, T* wave_tot, T* total) {
 }
 // Smallest (key, token) pair over the block (the best candidate when keys are DescKeys).
 __device__ void BlockMinPair(std::uint64_t& k, std::uint32_t& t, unsigned long long* rk, std::uint32_t* rt) {
-  for (int o = kWave / 2; o > 0; o >>= 1) {
-    const std::uint64_t ok = __shfl_xor(k, o, kWave);
-    const std::uint32_t ot = __shfl_xor(t, o, kWave);
-    if (ok < k || (ok == k && ot < t)) {
-      k = ok;
-      t = ot;
-    }
-  }
+  WaveMinPair(k, t);
   if (threadIdx.x % kWave == 0) {
     rk[threadIdx.x / kWave] = k;
     rt[threadIdx.x / kWave] = t;
@@ -308,23 +322,32 @@ struct RowMax {
   std::uint64_t key;
   std::uint32_t tok, nf;
 };
+// nb <= kWave (vocabularies up to 64 slices): wave 0 holds every slice's partials and reduces them with the block
+// reductions' shuffle trees (the other waves would add only zeros and neutral pairs, so the results are those of the
+// block forms), then one broadcast through LDS.
 __device__ RowMax ReduceParts(const Ws& w, std::uint32_t row, std::uint32_t nb, unsigned long long* rk,
                               std::uint32_t* rt, std::uint32_t* ru) {
-  std::uint64_t k = kNoBound;
-  std::uint32_t tk = 0xFFFFFFFFu, nf = 0;
-  for (std::uint32_t b = threadIdx.x; b < nb; b += blockDim.x) {
-    const std::size_t o = static_cast<std::size_t>(row) * nb + b;
-    const std::uint64_t kb = w.pkey[o];
-    const std::uint32_t tb = w.ptok[o];
-    if (kb < k || (kb == k && tb < tk)) {
-      k = kb;
-      tk = tb;
+  if (threadIdx.x < kWave) {
+    std::uint64_t k = kNoBound;
+    std::uint32_t tk = 0xFFFFFFFFu, nf = 0;
+    if (threadIdx.x < nb) {
+      const std::size_t o = static_cast<std::size_t>(row) * nb + threadIdx.x;
+      k = w.pkey[o];
+      tk = w.ptok[o];
+      nf = w.pnf[o];
     }
-    nf += w.pnf[o];
+    nf = WaveSum(nf);
+    WaveMinPair(k, tk);
+    if (threadIdx.x == 0) {
+      rk[0] = k;
+      rt[0] = tk;
+      ru[1] = nf;  // callers may pass one array as rt and ru
+    }
   }
-  nf = BlockSum(nf, ru);
-  BlockMinPair(k, tk, rk, rt);
-  return RowMax{k, tk, nf};
+  __syncthreads();
+  const RowMax m{rk[0], rt[0], ru[1]};
+  __syncthreads();
+  return m;
 }
 
 // Sequential double chains in list order on one lane (they must stay left-to-right to round as the CPU does), over
@@ -728,15 +751,28 @@ extern "C" __global__ void __launch_bounds__(1024)
       pl = w.plast[po + t];
       if (pz) mw = w.pminw[po + t];
     }
-    const double total = BlockSumD(ps, s);
-    std::uint32_t live = BlockSumU(pz, s);
-    std::uint64_t lk = ~static_cast<std::uint64_t>(pl);
-    std::uint32_t lt = 0;
-    BlockMinPair(lk, lt, s);
-    std::uint32_t last = static_cast<std::uint32_t>(~lk);
-    std::uint64_t mk = static_cast<std::uint64_t>(__double_as_longlong(mw));  // positive doubles order as bits
-    std::uint32_t mt = 0;
-    BlockMinPair(mk, mt, s);
+    // wave 0 holds them all: its shuffle trees give the block reductions' results, one broadcast
+    if (t < kWave) {  // ps stays this thread's slice sum (the slice search below reads it)
+      const double sum = WaveSum(ps);
+      const std::uint32_t nz = WaveSum(pz);
+      std::uint64_t lk = ~static_cast<std::uint64_t>(pl);
+      std::uint32_t lt = 0;
+      WaveMinPair(lk, lt);
+      std::uint64_t mk = static_cast<std::uint64_t>(__double_as_longlong(mw));  // positive doubles order as bits
+      std::uint32_t mt = 0;
+      WaveMinPair(mk, mt);
+      if (t == 0) {
+        s.xd = sum;
+        s.xu = nz;
+        s.xq[0] = lk;
+        s.xq[1] = mk;
+      }
+    }
+    __syncthreads();
+    const double total = s.xd;
+    std::uint32_t live = s.xu;
+    std::uint32_t last = static_cast<std::uint32_t>(~s.xq[0]);
+    const std::uint64_t mk = s.xq[1];
     const bool exact_count = __longlong_as_double(static_cast<long long>(mk)) / total != 0.0;
     if (!exact_count) {  // weights near the underflow of w / total: count the way the CPU drops them
       std::uint32_t nz = 0, lst = 0;

@@ -563,13 +563,30 @@ extern "C" __global__ void __launch_bounds__(1024)
     }
     val[i] = a;
   }
-  nf = BlockSum(nf, ru);
-  BlockMinPair(best_k, best_t, rk, rt);
+  // only thread 0 needs the block's results: wave reductions, one barrier, thread 0 combines the waves in
+  // BlockSum / BlockMinPair order
+  nf = WaveSum(nf);
+  WaveMinPair(best_k, best_t);
+  if (t % kWave == 0) {
+    ru[t / kWave] = nf;
+    rk[t / kWave] = best_k;
+    rt[t / kWave] = best_t;
+  }
+  __syncthreads();
   if (t == 0) {
+    std::uint32_t n = 0, tk = rt[0];
+    std::uint64_t k = rk[0];
+    for (std::uint32_t i = 0; i < kWaves; ++i) {
+      n += ru[i];
+      if (rk[i] < k || (rk[i] == k && rt[i] < tk)) {
+        k = rk[i];
+        tk = rt[i];
+      }
+    }
     const std::size_t o = static_cast<std::size_t>(row) * nb + b;
-    w.pkey[o] = best_k;
-    w.ptok[o] = best_t;
-    w.pnf[o] = nf;
+    w.pkey[o] = k;
+    w.ptok[o] = tk;
+    w.pnf[o] = n;
   }
 }
 
@@ -581,7 +598,7 @@ extern "C" __global__ void __launch_bounds__(1024)
   using namespace halo::sample;
   __shared__ double rd[kWaves];
   __shared__ std::uint32_t ru[kWaves];
-  __shared__ unsigned long long rk[kWaves];
+  __shared__ unsigned long long rk[kWaves], rm[kWaves];
   __shared__ std::uint32_t rt[kWaves];
   __shared__ std::uint32_t lh[kBins];
   const std::uint32_t row = blockIdx.y, b = blockIdx.x, t = threadIdx.x, nb = gridDim.x;
@@ -619,19 +636,37 @@ extern "C" __global__ void __launch_bounds__(1024)
         minw = fmin(minw, wt);
       }
     }
-    sum = BlockSum(sum, rd);
-    nz = BlockSum(nz, ru);
+    // only thread 0 needs the block's results: wave reductions, one barrier, thread 0 adds the wave sums in
+    // BlockSum order (the minima are order-free)
+    sum = WaveSum(sum);
+    nz = WaveSum(nz);
     std::uint64_t lk = ~static_cast<std::uint64_t>(last);
     std::uint32_t lt = 0;
-    BlockMinPair(lk, lt, rk, rt);
+    WaveMinPair(lk, lt);
     std::uint64_t mk = static_cast<std::uint64_t>(__double_as_longlong(minw));  // positive doubles order as bits
     std::uint32_t mt = 0;
-    BlockMinPair(mk, mt, rk, rt);
+    WaveMinPair(mk, mt);
+    if (t % kWave == 0) {
+      rd[t / kWave] = sum;
+      ru[t / kWave] = nz;
+      rk[t / kWave] = lk;
+      rm[t / kWave] = mk;
+    }
+    __syncthreads();
     if (t == 0) {
-      w.psum[o] = sum;
-      w.pnz[o] = nz;
-      w.plast[o] = static_cast<std::uint32_t>(~lk);
-      w.pminw[o] = __longlong_as_double(static_cast<long long>(mk));
+      double s0 = 0.0;
+      std::uint32_t z = 0;
+      std::uint64_t l = rk[0], m = rm[0];
+      for (std::uint32_t i = 0; i < kWaves; ++i) {
+        s0 += rd[i];
+        z += ru[i];
+        l = min(l, static_cast<std::uint64_t>(rk[i]));
+        m = min(m, static_cast<std::uint64_t>(rm[i]));
+      }
+      w.psum[o] = s0;
+      w.pnz[o] = z;
+      w.plast[o] = static_cast<std::uint32_t>(~l);
+      w.pminw[o] = __longlong_as_double(static_cast<long long>(m));
     }
     return;
   }

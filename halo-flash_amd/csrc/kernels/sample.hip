@@ -16,12 +16,15 @@
 //   3. collect (sorted path): the bins that hold the best min(candidates, 4096) tokens, or the full bins before
 //      them, are cut from the histogram and their tokens appended to a candidate list;
 //   4. final: temperature 0 takes the argmax; the linear path finds the slice, then the 4-token range, holding the
-//      uniform and walks it in token order; the sorted path bitonic-sorts the candidates by (value descending,
-//      token ascending) in LDS (an exact radix select over (value, token) replaces the histogram cut when ties
-//      overflow it) and runs top-p, min-p, the weight sum, the zero drop and the draw over that list in list order
-//      on one lane, as the CPU runs them; when the kept set reaches past the sorted candidates (a flat row with a
-//      loose top-p or a min-p floor), the cut and the draw are radix selects over the whole row on 2^-40
-//      fixed-point weights (integer sums, so runs agree bit for bit) and the nonzero count stays exact in double.
+//      uniform and walks it in token order; the sorted path orders the candidates by (value descending, token
+//      ascending) in LDS: counted again over 4096 fine bins spanning the collected range, scattered to their bin's
+//      place and ranked within it (a bitonic sort when a bin overflows; an exact radix select over (value, token)
+//      replaces the histogram cut when ties overflow it), and runs top-p, min-p, the weight sum, the zero drop and
+//      the draw over that list in list order on one lane, as the CPU runs them (one add per element: the running
+//      sums are monotone, so only a chunk's last sum is tested); when the kept set reaches past the sorted
+//      candidates (a flat row with a loose top-p or a min-p floor), the cut and the draw are radix selects over the
+//      whole row on 2^-40 fixed-point weights (integer sums, so runs agree bit for bit) and the nonzero count
+//      stays exact in double.
 // Only sums formed across slices or threads (the linear path's total, the full top-p sum, the fixed-point path)
 // differ from the CPU's sequential sums, by rounding; they move a draw only when the uniform falls within rounding
 // of a CDF boundary. Every reduction runs in a fixed order, so a row's result never depends on timing.

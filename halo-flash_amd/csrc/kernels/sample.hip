@@ -912,20 +912,25 @@ extern "C" __global__ void __launch_bounds__(1024)
     };
 #pragma unroll
     for (std::uint32_t j = 0; j < kPerT; ++j) s.b.hist[t * kPerT + j] = 0;
+    if (t == 0) s.bu[7] = 0;
     __syncthreads();
+    // the largest bin count is the largest count any increment returns: a wave maximum, one LDS maximum
+    std::uint32_t cm = 0;
 #pragma unroll
     for (std::uint32_t j = 0; j < kPerE; ++j)
       if (t + kThreads * j < n) {
         gb[j] = bin_of(gk[j]);
-        atomicAdd(&s.b.hist[gb[j]], 1u);
+        cm = max(cm, atomicAdd(&s.b.hist[gb[j]], 1u) + 1);
       }
+    for (int o = kWave / 2; o > 0; o >>= 1) cm = max(cm, static_cast<std::uint32_t>(__shfl_xor(cm, o, kWave)));
+    if (t % kWave == 0 && cm) atomicMax(&s.bu[7], cm);
     __syncthreads();
-    std::uint32_t c[kPerT], c4 = 0, cmax = 0;
+    const std::uint32_t cmax = s.bu[7];
+    std::uint32_t c[kPerT], c4 = 0;
 #pragma unroll
     for (std::uint32_t j = 0; j < kPerT; ++j) {
       c[j] = s.b.hist[t * kPerT + j];
       c4 += c[j];
-      cmax = max(cmax, c[j]);
     }
     std::uint32_t tot;
     std::uint32_t start = BlockExclScan(c4, s.ru, &tot);  // its barriers order the reads above before the writes
@@ -935,10 +940,8 @@ extern "C" __global__ void __launch_bounds__(1024)
       s.a.bitmap[t * kPerT + j] = 0;    // bin fill counter
       start += c[j];
     }
-    std::uint64_t mk = ~static_cast<std::uint64_t>(cmax);
-    std::uint32_t mt = 0;
-    BlockMinPair(mk, mt, s);
-    if (static_cast<std::uint32_t>(~mk) <= 512) {
+    __syncthreads();  // starts and cleared counters before any scatter
+    if (cmax <= 512) {
 #pragma unroll
       for (std::uint32_t j = 0; j < kPerE; ++j)
         if (t + kThreads * j < n) {
@@ -1104,12 +1107,24 @@ extern "C" __global__ void __launch_bounds__(1024)
         last = max(last, i + 1);
       }
     }
-    const std::uint32_t live = BlockSumU(nz, s);
+    // only thread 0 draws: wave reductions, one barrier, thread 0 combines the waves
+    nz = WaveSum(nz);
     std::uint64_t lk = ~static_cast<std::uint64_t>(last);
     std::uint32_t lt = 0;
-    BlockMinPair(lk, lt, s);
-    const std::uint32_t last_nz = static_cast<std::uint32_t>(~lk) - 1;
+    WaveMinPair(lk, lt);
+    if (t % kWave == 0) {
+      s.ru[t / kWave] = nz;
+      s.rq[t / kWave] = lk;
+    }
+    __syncthreads();
     if (t == 0) {
+      std::uint32_t live = 0;
+      std::uint64_t l = s.rq[0];
+      for (std::uint32_t i = 0; i < kWaves; ++i) {
+        live += s.ru[i];
+        l = min(l, static_cast<std::uint64_t>(s.rq[i]));
+      }
+      const std::uint32_t last_nz = static_cast<std::uint32_t>(~l) - 1;
       std::uint32_t token = s.tok[last_nz];
       if (live > 1) {
         const std::uint32_t i = SeqWalk(s.a.w, keep, Uniform(&rng));
